@@ -1,0 +1,126 @@
+"""ctypes binding of libgrws.so (the C ABI declared in include/grws.h).
+
+The library is the only compute path: if it is missing or fails to load,
+every op raises (there is no CPU or PyTorch fallback).  torch is imported
+first so that libgrws.so binds to the HIP runtime torch already loaded.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must precede loading libgrws.so)
+
+_PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.environ.get("GRWS_LIB", os.path.join(_PKG, "libgrws.so"))
+
+GRWS_F32, GRWS_F16, GRWS_BF16 = 0, 1, 2
+GRWS_OK = 0
+
+_c_i64p = ctypes.POINTER(ctypes.c_int64)
+_vp = ctypes.c_void_p
+
+
+class BcsrView(ctypes.Structure):
+    """grws_bcsr (include/grws.h)."""
+    _fields_ = [("window_offset", _vp), ("col_indices", _vp), ("values", _vp),
+                ("num_windows", ctypes.c_int64), ("num_tiles", ctypes.c_int64),
+                ("tile_rows", ctypes.c_int32), ("tile_cols", ctypes.c_int32),
+                ("values_dtype", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+class SpmmPlanView(ctypes.Structure):
+    """grws_spmm_plan (include/grws.h)."""
+    _fields_ = [("items", _vp), ("split", _vp), ("num_items", ctypes.c_int64),
+                ("num_split", ctypes.c_int64), ("num_slots", ctypes.c_int64),
+                ("slabs_per_item", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+# name -> (restype, argtypes)
+_PROTOS = {
+    "grws_last_error": (ctypes.c_char_p, []),
+    "grws_abi_version": (ctypes.c_int, []),
+    "grws_spmm_plan_capacity": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+                                               ctypes.c_int32, _c_i64p, _c_i64p]),
+    "grws_spmm_default_slabs": (ctypes.c_int32, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+                                                 ctypes.c_int64]),
+    "grws_spmm_plan_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "grws_spmm_plan_build": (ctypes.c_int, [_vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+                                            ctypes.c_int32, _vp, ctypes.c_int64, _vp,
+                                            ctypes.c_int64, _vp, ctypes.c_size_t, _c_i64p, _vp]),
+    "grws_spmm_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(SpmmPlanView), ctypes.c_int64]),
+    "grws_spmm": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.POINTER(SpmmPlanView), _vp,
+                                 ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                 _vp, ctypes.c_int32, ctypes.c_int64, _vp, ctypes.c_size_t, _vp]),
+    "grws_csr_to_bcsr_host_count": (ctypes.c_int, [ctypes.c_int64, _vp, _vp, ctypes.c_int32,
+                                                   ctypes.c_int32, _vp, _c_i64p, ctypes.c_int32]),
+    "grws_csr_to_bcsr_host_fill": (ctypes.c_int, [ctypes.c_int64, _vp, _vp, _vp, ctypes.c_int32,
+                                                  ctypes.c_int32, _vp, _vp, _vp, ctypes.c_int32]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load():
+    """Loads libgrws.so and declares every prototype; raises if missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"libgrws.so not found at {LIB_PATH}; build it with "
+                "`python -m graph_rws_amd.csrc.build` (there is no fallback path)")
+        L = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+        for name, (res, args) in _PROTOS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return list(_PROTOS)
+
+
+class GrwsError(RuntimeError):
+    """A libgrws call returned a non-zero status."""
+
+    def __init__(self, fn: str, status: int, msg: str):
+        super().__init__(f"{fn} failed ({status}): {msg}")
+        self.status = status
+
+
+def check(fn: str, status: int) -> None:
+    if status != GRWS_OK:
+        msg = load().grws_last_error()
+        raise GrwsError(fn, int(status), msg.decode() if msg else "")
+
+
+def call(fn: str, *args):
+    st = getattr(load(), fn)(*args)
+    check(fn, st)
+    return st
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return GRWS_F32
+    if dt == torch.float16:
+        return GRWS_F16
+    if dt == torch.bfloat16:
+        return GRWS_BF16
+    raise TypeError(f"unsupported dtype {dt} (float32, float16, bfloat16)")
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)

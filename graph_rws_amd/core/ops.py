@@ -1,0 +1,206 @@
+"""Reference-named ops over libgrws.so.
+
+Each function keeps the name, argument meaning and return shape of the
+reference's pybind11 op it replaces (core/wrapper/bind.cpp:99-159) and runs
+the hand-written gfx950 kernels through the C ABI.  Outputs and workspaces are
+allocated here with torch's caching allocator; the library allocates nothing.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import weakref
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib as L
+
+# spmm_tc timing (the reference returns the kernel ms measured with a host
+# sync per call, timer.h:22-52).  Off by default: ms is reported as 0.0 and
+# no synchronisation happens.  Set to True to time each call with events.
+TIMING = False
+
+
+# ---------------------------------------------------------------------------
+# SpMM plan
+# ---------------------------------------------------------------------------
+class SpmmPlan:
+    """Device work schedule of one BCSR graph (see grws_spmm_plan in
+    include/grws.h).  Built once per graph and reused by every SpMM call."""
+
+    def __init__(self, items: torch.Tensor, split: torch.Tensor, counts, slabs: int):
+        self.items = items
+        self.split = split
+        self.num_items, self.num_split, self.num_slots = (int(c) for c in counts)
+        self.slabs_per_item = int(slabs)
+
+    def view(self) -> L.SpmmPlanView:
+        return L.SpmmPlanView(L.ptr(self.items), L.ptr(self.split), self.num_items,
+                              self.num_split, self.num_slots, self.slabs_per_item, 0)
+
+
+def default_slabs(num_windows: int, num_tiles: int, tile_cols: int, n_cols: int) -> int:
+    return int(L.load().grws_spmm_default_slabs(num_windows, num_tiles, tile_cols, n_cols))
+
+
+def build_spmm_plan(window_offset: torch.Tensor, num_tiles: int, tile_cols: int,
+                    slabs_per_item: int) -> SpmmPlan:
+    """Builds the SpMM schedule on the device (one stream sync)."""
+    lib = L.load()
+    dev = window_offset.device
+    W = window_offset.numel() - 1
+    mi = ctypes.c_int64()
+    ms = ctypes.c_int64()
+    L.call("grws_spmm_plan_capacity", W, num_tiles, tile_cols, slabs_per_item,
+           ctypes.byref(mi), ctypes.byref(ms))
+    items = torch.empty(max(1, mi.value) * 4, dtype=torch.int32, device=dev)
+    split = torch.empty(max(1, ms.value) * 3, dtype=torch.int32, device=dev)
+    wsb = int(lib.grws_spmm_plan_workspace_bytes(W))
+    ws = torch.empty(max(1, wsb), dtype=torch.uint8, device=dev)
+    counts = (ctypes.c_int64 * 3)()
+    L.call("grws_spmm_plan_build", L.ptr(window_offset), W, num_tiles, tile_cols, slabs_per_item,
+           L.ptr(items), mi.value, L.ptr(split), ms.value, L.ptr(ws), wsb,
+           ctypes.cast(counts, ctypes.POINTER(ctypes.c_int64)), L.stream_of(dev))
+    return SpmmPlan(items, split, list(counts), slabs_per_item)
+
+
+# plans for raw-tensor calls (spmm_tc), keyed weakly on the window_offset tensor
+_plan_cache: "weakref.WeakKeyDictionary[torch.Tensor, dict]" = weakref.WeakKeyDictionary()
+
+
+def _cached_plan(window_offset: torch.Tensor, col_indices: torch.Tensor, tile_cols: int,
+                 n_cols: int) -> SpmmPlan:
+    num_tiles = col_indices.numel() // tile_cols
+    W = window_offset.numel() - 1
+    slabs = default_slabs(W, num_tiles, tile_cols, n_cols)
+    key = (window_offset._version, col_indices.data_ptr(), col_indices.numel(), tile_cols, slabs)
+    d = _plan_cache.get(window_offset)
+    if d is None:
+        d = {}
+        _plan_cache[window_offset] = d
+    p = d.get(key)
+    if p is None:
+        d.clear()
+        p = build_spmm_plan(window_offset, num_tiles, tile_cols, slabs)
+        d[key] = p
+    return p
+
+
+# ---------------------------------------------------------------------------
+# SpMM forward
+# ---------------------------------------------------------------------------
+def _check_graph(window_offset, col_indices, values, tile_cols):
+    if not (window_offset.is_contiguous() and col_indices.is_contiguous() and values.is_contiguous()):
+        raise RuntimeError("window_offset, original_col_indices and values_condensed must be contiguous")
+    if window_offset.dtype != torch.int64:
+        raise TypeError("window_offset must be int64")
+    if col_indices.dtype != torch.int32:
+        raise TypeError("original_col_indices must be int32")
+    if tile_cols not in (8, 16):
+        raise ValueError(f"tile_cols must be 8 or 16 (got {tile_cols})")
+    if col_indices.numel() % tile_cols != 0:
+        raise ValueError("original_col_indices length is not a multiple of tile_cols")
+    if values.numel() != col_indices.numel() * 16:
+        raise ValueError("values_condensed must hold 16*tile_cols values per tile")
+
+
+def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.Tensor,
+         x: torch.Tensor, tile_cols: int, plan: Optional[SpmmPlan] = None,
+         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Y[16W, N] = A X on the device (H1 kernel).  x: [x_rows, N] (row stride
+    may exceed N); out dtype = x dtype."""
+    _check_graph(window_offset, col_indices, values, tile_cols)
+    if not x.is_cuda:
+        raise RuntimeError("input_B must be a CUDA tensor")
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise RuntimeError("input_B must be 2-D with unit column stride (contiguous rows)")
+    for t in (window_offset, col_indices, values):
+        if t.device != x.device:
+            raise RuntimeError("graph arrays and input_B must be on the same device")
+    W = window_offset.numel() - 1
+    N = x.shape[1]
+    if out is None:
+        out = torch.empty((W * 16, N), dtype=x.dtype, device=x.device)
+    elif out.shape != (W * 16, N) or out.dtype != x.dtype or out.stride(1) != 1:
+        raise ValueError("out must be [16W, N] with x's dtype and unit column stride")
+    if W == 0 or N == 0:
+        return out
+    view = L.BcsrView(L.ptr(window_offset), L.ptr(col_indices), L.ptr(values), W,
+                      col_indices.numel() // tile_cols, 16, tile_cols, L.dtype_code(values.dtype), 0)
+    pv = None
+    ws = None
+    wsb = 0
+    if plan is not None:
+        pv = plan.view()
+        wsb = int(L.load().grws_spmm_workspace_bytes(ctypes.byref(pv), N))
+        if wsb:
+            ws = torch.empty(wsb, dtype=torch.uint8, device=x.device)
+    L.call("grws_spmm", ctypes.byref(view), ctypes.byref(pv) if pv is not None else None,
+           L.ptr(x), L.dtype_code(x.dtype), x.shape[0], x.stride(0), N, L.ptr(out),
+           L.dtype_code(out.dtype), out.stride(0), L.ptr(ws), wsb, L.stream_of(x.device))
+    return out
+
+
+def spmm_tc(window_offset: torch.Tensor, original_col_indices: torch.Tensor,
+            values_condensed: torch.Tensor, input_B: torch.Tensor, warps_per_block: int = 8,
+            tile_cols: int = 8) -> Tuple[torch.Tensor, float]:
+    """Drop-in for core_lib.spmm_tc (bind.cpp:124-130, spmm_wrapper.cu:33-95).
+
+    Returns (C[16W, N], ms).  `warps_per_block` is accepted for API
+    compatibility and ignored (the gfx950 kernel picks its own shape).
+    `tile_cols` defaults to the reference's fixed 8 (config.h:17).  ms is 0.0
+    unless ``graph_rws_amd.core.ops.TIMING`` is set.
+    """
+    plan = _cached_plan(window_offset, original_col_indices, tile_cols, input_B.shape[1])
+    if not TIMING:
+        return spmm(window_offset, original_col_indices, values_condensed, input_B, tile_cols,
+                    plan=plan), 0.0
+    s = torch.cuda.current_stream(input_B.device)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    y = spmm(window_offset, original_col_indices, values_condensed, input_B, tile_cols, plan=plan)
+    e1.record(s)
+    e1.synchronize()
+    return y, float(e0.elapsed_time(e1))
+
+
+# ---------------------------------------------------------------------------
+# CSR -> BCSR on host cores
+# ---------------------------------------------------------------------------
+def host_threads() -> int:
+    """Host worker threads: OMP_NUM_THREADS when set (the share of the
+    machine this process may use), else the visible core count."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return os.cpu_count() or 1
+
+
+def csr_to_bcsr_cpu(num_rows: int, row_ptr: torch.Tensor, col_idx: torch.Tensor,
+                    values: torch.Tensor, tile_rows: int, tile_cols: int,
+                    num_threads: int = 0):
+    """Drop-in for core_lib.csr_to_bcsr_cpu (bind.cpp:143-150,
+    convert_wrapper.cpp:27-180).  CPU tensors in, CPU tensors out:
+    (window_offset int64[W+1], original_col_indices int32, values_condensed f32)."""
+    if row_ptr.device.type != "cpu":
+        raise RuntimeError("row_ptr must be on CPU")
+    if num_threads <= 0:
+        num_threads = host_threads()
+    rp = row_ptr.to(torch.int64).contiguous()
+    ci = col_idx.to("cpu", torch.int32).contiguous()
+    va = values.to("cpu", torch.float32).contiguous()
+    num_rows = int(num_rows)
+    if rp.numel() != num_rows + 1:
+        raise ValueError("row_ptr must have num_rows + 1 entries")
+    W = (num_rows + tile_rows - 1) // tile_rows
+    win = torch.empty(W + 1, dtype=torch.int64)
+    T = ctypes.c_int64()
+    L.call("grws_csr_to_bcsr_host_count", num_rows, L.ptr(rp), L.ptr(ci), tile_rows, tile_cols,
+           L.ptr(win), ctypes.byref(T), num_threads)
+    cols = torch.empty(T.value * tile_cols, dtype=torch.int32)
+    vals = torch.empty(T.value * tile_rows * tile_cols, dtype=torch.float32)
+    L.call("grws_csr_to_bcsr_host_fill", num_rows, L.ptr(rp), L.ptr(ci), L.ptr(va), tile_rows,
+           tile_cols, L.ptr(win), L.ptr(cols), L.ptr(vals), num_threads)
+    return win, cols, vals

@@ -1,0 +1,599 @@
+// BCSR row-window SpMM  Y[16W x N] = A * X  for gfx950 (MI355X).
+//
+// Replaces the reference's tcspmm_base_kernel (core/include/spmm_tc.cuh:40-195,
+// launched by core/wrapper/spmm_wrapper.cu:33-95).  Design:
+//   * one wave64 work-group per (work item, N-chunk); a work item is a window
+//     or, for heavy windows, a contiguous range of its slabs (16 column slots);
+//   * the 16 X rows a slab references are gathered with 16-byte loads
+//     (coalesced row segments), staged in LDS, and fed to CDNA4 MFMA:
+//     v_mfma_f32_16x16x16_{f16,bf16} for 16-bit inputs, v_mfma_f32_16x16x4_f32
+//     for fp32; fp32 accumulation in registers;
+//   * the next slab's gathers are issued before the current slab is consumed
+//     (register double buffer), so HBM latency overlaps the MFMA work;
+//   * -1 padding (and any column outside [0, x_rows)) is masked at the load:
+//     no memory traffic, zero contribution;
+//   * heavy windows are split over several items whose fp32 partial sums are
+//     added in a fixed order by a second kernel: deterministic, no atomics;
+//   * work-group ids are remapped so each XCD (work-groups are dealt to the 8
+//     XCDs round-robin) walks a contiguous range of (chunk, window) pairs,
+//     keeping a community's X rows resident in that XCD's L2.
+#include "grws_internal.h"
+
+namespace grws {
+namespace {
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+template <int XT>
+struct XTraits;
+template <>
+struct XTraits<GRWS_F32> {
+    using S = float;
+    static constexpr int SZ = 4;
+};
+template <>
+struct XTraits<GRWS_F16> {
+    using S = _Float16;
+    static constexpr int SZ = 2;
+};
+template <>
+struct XTraits<GRWS_BF16> {
+    using S = uint16_t;  // raw bf16 bits
+    static constexpr int SZ = 2;
+};
+
+// Raw load unit for a given byte width.
+template <int BYTES>
+struct RawT;
+template <>
+struct RawT<16> { using T = u32x4_t; };
+template <>
+struct RawT<8> { using T = u32x2_t; };
+template <>
+struct RawT<4> { using T = uint32_t; };
+template <>
+struct RawT<2> { using T = uint16_t; };
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+struct SpmmArgs {
+    const int64_t* win_off;
+    const int32_t* cols;
+    const void* vals;
+    const int32_t* items;  // null: one item per window
+    int64_t num_items;
+    int64_t num_tiles;
+    const void* x;
+    int64_t x_rows;
+    int64_t ldx;
+    int64_t n_cols;
+    void* y;
+    int64_t ldy;
+    float* partials;
+    int32_t nchunks;
+};
+
+// Output conversion for the three element types.
+template <int XT>
+__device__ __forceinline__ void store_out(void* y, int64_t idx, float v) {
+    if constexpr (XT == GRWS_F32) {
+        static_cast<float*>(y)[idx] = v;
+    } else if constexpr (XT == GRWS_F16) {
+        static_cast<_Float16*>(y)[idx] = (_Float16)v;
+    } else {
+        static_cast<uint16_t*>(y)[idx] = f32_to_bf16_bits(v);
+    }
+}
+
+template <int XT, bool AF32, int TC, int NBLK, bool VECT>
+__global__ __launch_bounds__(64) void spmm_fwd_kernel(SpmmArgs a) {
+    using S = typename XTraits<XT>::S;
+    constexpr int SZ = XTraits<XT>::SZ;
+    constexpr int NC = NBLK * 16;                  // output columns per work-group
+    constexpr int VEC = VECT ? 16 / SZ : 1;        // elements per lane load
+    constexpr int LDB = VEC * SZ;                  // bytes per lane load
+    using LoadT = typename RawT<LDB>::T;
+    constexpr int PITCH = NC + (SZ == 2 ? 8 : 4);  // LDS row pitch (elements), 16-B aligned rows
+    constexpr int NLD = (16 * NC + 64 * VEC - 1) / (64 * VEC);  // lane loads per slab
+    static_assert(TC == 8 || TC == 16, "tile_cols must be 8 or 16");
+
+    __shared__ __attribute__((aligned(16))) S stage[16 * PITCH];
+
+    const int lane = threadIdx.x;
+    const int64_t total = a.num_items * a.nchunks;
+    const int64_t per_xcd = (total + 7) >> 3;
+    const int64_t logical = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (logical >= total) return;
+    const int64_t item = logical % a.num_items;
+    const int chunk = (int)(logical / a.num_items);
+
+    int64_t w, sb, se;
+    int slot;
+    if (a.items) {
+        const int32_t* it = a.items + 4 * item;
+        w = it[0];
+        sb = it[1];
+        se = it[2];
+        slot = it[3];
+    } else {
+        w = item;
+        sb = 0;
+        se = INT64_MAX;
+        slot = -1;
+    }
+    int64_t t1 = a.win_off[w + 1];
+    int64_t t0 = a.win_off[w];
+    // malformed offsets must never read outside the tile arrays
+    t1 = t1 < 0 ? 0 : (t1 > a.num_tiles ? a.num_tiles : t1);
+    t0 = t0 < 0 ? 0 : (t0 > t1 ? t1 : t0);
+    const int64_t nslots = (t1 - t0) * TC;
+    const int64_t nslabs = (nslots + 15) >> 4;
+    if (se > nslabs) se = nslabs;
+    if (sb > se) sb = se;
+
+    const int64_t n0 = (int64_t)chunk * NC;
+    const int64_t N = a.n_cols;
+    const uint32_t xr = (uint32_t)a.x_rows;
+    const S* __restrict__ X = static_cast<const S*>(a.x);
+    const int32_t* __restrict__ colp = a.cols + t0 * TC;
+
+    // per-lane load geometry (compile-time per lane position)
+    int ld_row[NLD], ld_col[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        int e = (i * 64 + lane) * VEC;
+        ld_row[i] = e / NC;
+        ld_col[i] = e % NC;
+    }
+
+    auto load_cols = [&](int64_t s) -> int {
+        int64_t sl = s * 16 + (lane & 15);
+        return (s < se && sl < nslots) ? colp[sl] : -1;
+    };
+    auto load_x = [&](int cv, LoadT* regs) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            int r = ld_row[i];
+            int c = __shfl(cv, r & 15, 64);
+            bool ok = (r < 16) && ((uint32_t)c < xr) && (n0 + ld_col[i] < N);
+            LoadT v = {};
+            if (ok) v = *reinterpret_cast<const LoadT*>(X + (int64_t)c * a.ldx + n0 + ld_col[i]);
+            regs[i] = v;
+        }
+    };
+
+    // A fragment: row r = lane%16, slots 16s + 4g .. 16s + 4g + 3 (g = lane/16)
+    const int ar = lane & 15;
+    const int ag = lane >> 4;
+    using AVec = typename std::conditional<AF32, float4_t, typename std::conditional<XT == GRWS_F32, float4_t, u32x2_t>::type>::type;
+    auto load_a = [&](int64_t s) -> AVec {
+        AVec v = {};
+        int64_t sl = s * 16 + 4 * ag;
+        if (s < se && sl < nslots) {
+            int64_t tile = t0 + sl / TC;
+            int c = (int)(sl % TC);
+            int64_t off = (tile * 16 + ar) * TC + c;
+            if constexpr (AF32 || XT == GRWS_F32) {
+                v = *reinterpret_cast<const float4_t*>(static_cast<const float*>(a.vals) + off);
+            } else {
+                v = *reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(a.vals) + off);
+            }
+        }
+        return v;
+    };
+
+    float4_t acc[NBLK];
+#pragma unroll
+    for (int b = 0; b < NBLK; ++b) acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    LoadT cur[NLD], nxt[NLD];
+    AVec a_cur = {}, a_nxt = {};
+    int c_nxt = -1;
+    if (sb < se) {
+        int c0 = load_cols(sb);
+        load_x(c0, cur);
+        a_cur = load_a(sb);
+        c_nxt = load_cols(sb + 1);
+    }
+    const int bn = lane & 15;
+    for (int64_t s = sb; s < se; ++s) {
+        if (s + 1 < se) {
+            load_x(c_nxt, nxt);
+            a_nxt = load_a(s + 1);
+            c_nxt = load_cols(s + 2);
+        }
+        // stage slab s
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            if (ld_row[i] < 16)
+                *reinterpret_cast<LoadT*>(&stage[ld_row[i] * PITCH + ld_col[i]]) = cur[i];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        if constexpr (XT == GRWS_F32) {
+            float4_t af = a_cur;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int k = 4 * ag + q;
+#pragma unroll
+                for (int b = 0; b < NBLK; ++b) {
+                    float bv = stage[k * PITCH + b * 16 + bn];
+                    acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[q], bv, acc[b], 0, 0, 0);
+                }
+            }
+        } else if constexpr (XT == GRWS_F16) {
+            half4_t af;
+            if constexpr (AF32) {
+                af = half4_t{(_Float16)a_cur[0], (_Float16)a_cur[1], (_Float16)a_cur[2], (_Float16)a_cur[3]};
+            } else {
+                af = __builtin_bit_cast(half4_t, a_cur);
+            }
+#pragma unroll
+            for (int b = 0; b < NBLK; ++b) {
+                const S* p = stage + (4 * ag) * PITCH + b * 16 + bn;
+                half4_t bf = half4_t{p[0], p[PITCH], p[2 * PITCH], p[3 * PITCH]};
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(af, bf, acc[b], 0, 0, 0);
+            }
+        } else {
+            short4_t af;
+            if constexpr (AF32) {
+                af = short4_t{(short)f32_to_bf16_bits(a_cur[0]), (short)f32_to_bf16_bits(a_cur[1]),
+                              (short)f32_to_bf16_bits(a_cur[2]), (short)f32_to_bf16_bits(a_cur[3])};
+            } else {
+                af = __builtin_bit_cast(short4_t, a_cur);
+            }
+#pragma unroll
+            for (int b = 0; b < NBLK; ++b) {
+                const S* p = stage + (4 * ag) * PITCH + b * 16 + bn;
+                short4_t bf = short4_t{(short)p[0], (short)p[PITCH], (short)p[2 * PITCH], (short)p[3 * PITCH]};
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(af, bf, acc[b], 0, 0, 0);
+            }
+        }
+        // the next iteration overwrites the stage
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) cur[i] = nxt[i];
+        a_cur = a_nxt;
+    }
+
+    // D layout of the 16x16 MFMA family: lane l, element i -> row 4*(l/16)+i, col l%16
+    if (slot < 0) {
+        const int64_t row0 = w * 16;
+#pragma unroll
+        for (int b = 0; b < NBLK; ++b) {
+            const int64_t col = n0 + b * 16 + bn;
+            if (col < N) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) store_out<XT>(a.y, (row0 + 4 * ag + i) * a.ldy + col, acc[b][i]);
+            }
+        }
+    } else {
+        float* P = a.partials + ((int64_t)slot * a.nchunks + chunk) * (16 * NC);
+#pragma unroll
+        for (int b = 0; b < NBLK; ++b) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) P[(4 * ag + i) * NC + b * 16 + bn] = acc[b][i];
+        }
+    }
+}
+
+// Sums the partial slots of each split window in slot order (deterministic).
+template <int XT, int NBLK>
+__global__ __launch_bounds__(256) void spmm_fixup_kernel(const int32_t* __restrict__ split, int64_t num_split,
+                                                         const float* __restrict__ partials, int32_t nchunks,
+                                                         void* y, int64_t ldy, int64_t N) {
+    constexpr int NC = NBLK * 16;
+    const int64_t si = blockIdx.x / nchunks;
+    const int chunk = (int)(blockIdx.x % nchunks);
+    if (si >= num_split) return;
+    const int64_t w = split[3 * si];
+    const int64_t first = split[3 * si + 1];
+    const int cnt = split[3 * si + 2];
+    const int64_t n0 = (int64_t)chunk * NC;
+    for (int e = threadIdx.x; e < 16 * NC; e += 256) {
+        const int r = e / NC, c = e % NC;
+        if (n0 + c >= N) continue;
+        float s = 0.f;
+        for (int k = 0; k < cnt; ++k) s += partials[((first + k) * nchunks + chunk) * (16 * NC) + e];
+        store_out<XT>(y, (w * 16 + r) * ldy + n0 + c, s);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// plan construction
+// ---------------------------------------------------------------------------
+__global__ void plan_count_kernel(const int64_t* __restrict__ win_off, int64_t W, int64_t num_tiles, int TC,
+                                  int S, int32_t* __restrict__ nitems, int32_t* __restrict__ nsplit,
+                                  int32_t* __restrict__ nslot) {
+    int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (w >= W) return;
+    int64_t t1 = win_off[w + 1], t0 = win_off[w];
+    t1 = t1 < 0 ? 0 : (t1 > num_tiles ? num_tiles : t1);
+    t0 = t0 < 0 ? 0 : (t0 > t1 ? t1 : t0);
+    int64_t slabs = ((t1 - t0) * TC + 15) / 16;
+    int64_t ni = slabs <= S ? 1 : (slabs + S - 1) / S;
+    nitems[w] = (int32_t)ni;
+    nsplit[w] = ni > 1 ? 1 : 0;
+    nslot[w] = ni > 1 ? (int32_t)ni : 0;
+}
+
+__global__ void plan_fill_kernel(const int64_t* __restrict__ win_off, int64_t W, int64_t num_tiles, int TC, int S,
+                                 const int64_t* __restrict__ item_off, const int64_t* __restrict__ split_off,
+                                 const int64_t* __restrict__ slot_off, int32_t* __restrict__ items,
+                                 int32_t* __restrict__ split) {
+    int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (w >= W) return;
+    int64_t t1 = win_off[w + 1], t0 = win_off[w];
+    t1 = t1 < 0 ? 0 : (t1 > num_tiles ? num_tiles : t1);
+    t0 = t0 < 0 ? 0 : (t0 > t1 ? t1 : t0);
+    int64_t slabs = ((t1 - t0) * TC + 15) / 16;
+    int64_t ni = item_off[w + 1] - item_off[w];
+    for (int64_t k = 0; k < ni; ++k) {
+        int32_t* it = items + 4 * (item_off[w] + k);
+        int64_t b = k * S, e = (k + 1) * S;
+        it[0] = (int32_t)w;
+        it[1] = (int32_t)b;
+        it[2] = (int32_t)(e < slabs ? e : slabs);
+        it[3] = ni > 1 ? (int32_t)(slot_off[w] + k) : -1;
+    }
+    if (ni > 1) {
+        int32_t* sp = split + 3 * split_off[w];
+        sp[0] = (int32_t)w;
+        sp[1] = (int32_t)slot_off[w];
+        sp[2] = (int32_t)ni;
+    }
+}
+
+int nblk_for(int64_t N) { return N <= 16 ? 1 : (N <= 32 ? 2 : (N <= 64 ? 4 : 8)); }
+
+template <int XT, bool AF32, int TC, int NBLK, bool VECT>
+int launch_fwd(const SpmmArgs& a, hipStream_t stream) {
+    int64_t total = a.num_items * a.nchunks;
+    int64_t grid = ((total + 7) / 8) * 8;
+    if (grid > INT32_MAX) return set_error(GRWS_E_INVALID, "spmm: too many work items (%lld)", (long long)total);
+    hipLaunchKernelGGL((spmm_fwd_kernel<XT, AF32, TC, NBLK, VECT>), dim3((unsigned)grid), dim3(64), 0, stream, a);
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
+template <int XT, bool AF32, int TC, int NBLK>
+int dispatch_vec(const SpmmArgs& a, bool vect, hipStream_t stream) {
+    return vect ? launch_fwd<XT, AF32, TC, NBLK, true>(a, stream) : launch_fwd<XT, AF32, TC, NBLK, false>(a, stream);
+}
+
+template <int XT, bool AF32, int TC>
+int dispatch_nblk(const SpmmArgs& a, int nblk, bool vect, hipStream_t stream) {
+    switch (nblk) {
+        case 1: return dispatch_vec<XT, AF32, TC, 1>(a, vect, stream);
+        case 2: return dispatch_vec<XT, AF32, TC, 2>(a, vect, stream);
+        case 4: return dispatch_vec<XT, AF32, TC, 4>(a, vect, stream);
+        default: return dispatch_vec<XT, AF32, TC, 8>(a, vect, stream);
+    }
+}
+
+template <int XT, bool AF32>
+int dispatch_tc(const SpmmArgs& a, int tc, int nblk, bool vect, hipStream_t stream) {
+    return tc == 8 ? dispatch_nblk<XT, AF32, 8>(a, nblk, vect, stream)
+                   : dispatch_nblk<XT, AF32, 16>(a, nblk, vect, stream);
+}
+
+template <int XT>
+int launch_fixup(const grws_spmm_plan* plan, const SpmmArgs& a, int nblk, hipStream_t stream) {
+    int64_t grid = plan->num_split * a.nchunks;
+    if (grid <= 0) return GRWS_OK;
+    switch (nblk) {
+        case 1:
+            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 1>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols);
+            break;
+        case 2:
+            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 2>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols);
+            break;
+        case 4:
+            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 4>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols);
+            break;
+        default:
+            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 8>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols);
+            break;
+    }
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
+}  // namespace
+}  // namespace grws
+
+using namespace grws;
+
+extern "C" int grws_spmm_plan_capacity(int64_t num_windows, int64_t num_tiles, int32_t tile_cols,
+                                       int32_t slabs_per_item, int64_t* max_items, int64_t* max_split) {
+    clear_error();
+    GRWS_CHECK_ARG(num_windows >= 0 && num_tiles >= 0, "plan_capacity: negative size");
+    GRWS_CHECK_ARG(tile_cols == 8 || tile_cols == 16, "plan_capacity: tile_cols must be 8 or 16");
+    GRWS_CHECK_ARG(slabs_per_item >= 1, "plan_capacity: slabs_per_item must be >= 1");
+    GRWS_CHECK_ARG(max_items && max_split, "plan_capacity: null output");
+    // sum_w ceil(slabs_w / S) <= W + sum_w slabs_w / S, and slabs_w <= T_w*tc/16 + 1
+    int64_t slab_bound = (num_tiles * tile_cols) / 16 + num_windows;
+    *max_items = num_windows + slab_bound / slabs_per_item + 1;
+    int64_t ms = slab_bound / (int64_t)(slabs_per_item + 1) + 1;
+    *max_split = ms < num_windows ? ms : num_windows;
+    return GRWS_OK;
+}
+
+extern "C" int32_t grws_spmm_default_slabs(int64_t num_windows, int64_t num_tiles, int32_t tile_cols,
+                                           int64_t n_cols) {
+    int64_t nblk = nblk_for(n_cols > 0 ? n_cols : 1);
+    int64_t nchunks = (n_cols + nblk * 16 - 1) / (nblk * 16);
+    if (nchunks < 1) nchunks = 1;
+    int64_t slabs = (num_tiles * (tile_cols > 0 ? tile_cols : 16) + 15) / 16;
+    // a fair share for one of ~2048 resident waves (256 CUs x 8)
+    int64_t share = slabs * nchunks / 2048;
+    int64_t s = 16;
+    while (s * 2 <= share && s < (1 << 20)) s *= 2;
+    (void)num_windows;
+    return (int32_t)s;
+}
+
+extern "C" size_t grws_spmm_plan_workspace_bytes(int64_t num_windows) {
+    Sizer s;
+    for (int i = 0; i < 3; ++i) s.take<int32_t>((size_t)num_windows + 1);
+    for (int i = 0; i < 3; ++i) s.take<int64_t>((size_t)num_windows + 2);
+    s.used += scan_workspace_bytes(num_windows) + 256;
+    return s.used;
+}
+
+extern "C" int grws_spmm_plan_build(const int64_t* window_offset, int64_t num_windows, int64_t num_tiles,
+                                    int32_t tile_cols, int32_t slabs_per_item, int32_t* items, int64_t max_items,
+                                    int32_t* split, int64_t max_split, void* workspace, size_t workspace_bytes,
+                                    int64_t* counts_out, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(window_offset && items && counts_out, "plan_build: null pointer");
+    GRWS_CHECK_ARG(num_windows >= 0 && num_tiles >= 0, "plan_build: negative size");
+    GRWS_CHECK_ARG(tile_cols == 8 || tile_cols == 16, "plan_build: tile_cols must be 8 or 16");
+    GRWS_CHECK_ARG(slabs_per_item >= 1, "plan_build: slabs_per_item must be >= 1");
+    int64_t cap_items = 0, cap_split = 0;
+    GRWS_TRY(grws_spmm_plan_capacity(num_windows, num_tiles, tile_cols, slabs_per_item, &cap_items, &cap_split));
+    if (max_items < cap_items || max_split < cap_split || (cap_split > 0 && !split))
+        return set_error(GRWS_E_CAPACITY, "plan_build: plan buffers too small (items %lld < %lld or split %lld < %lld)",
+                         (long long)max_items, (long long)cap_items, (long long)max_split, (long long)cap_split);
+    if (num_windows == 0) {
+        counts_out[0] = counts_out[1] = counts_out[2] = 0;
+        return GRWS_OK;
+    }
+    Carver cv(workspace, workspace_bytes);
+    int32_t* nitems = cv.take<int32_t>(num_windows + 1);
+    int32_t* nsplit = cv.take<int32_t>(num_windows + 1);
+    int32_t* nslot = cv.take<int32_t>(num_windows + 1);
+    int64_t* item_off = cv.take<int64_t>(num_windows + 2);
+    int64_t* split_off = cv.take<int64_t>(num_windows + 2);
+    int64_t* slot_off = cv.take<int64_t>(num_windows + 2);
+    size_t scan_bytes = scan_workspace_bytes(num_windows);
+    char* scan_ws = cv.take<char>(scan_bytes);
+    if (!cv.ok) return set_error(GRWS_E_CAPACITY, "plan_build: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+    unsigned blocks = (unsigned)((num_windows + 255) / 256);
+    hipLaunchKernelGGL(plan_count_kernel, dim3(blocks), dim3(256), 0, stream, window_offset, num_windows, num_tiles,
+                       (int)tile_cols, (int)slabs_per_item, nitems, nsplit, nslot);
+    GRWS_LAUNCH_CHECK();
+    GRWS_TRY(scan_i32_to_i64(nitems, item_off, num_windows, false, scan_ws, scan_bytes, stream));
+    GRWS_TRY(scan_i32_to_i64(nsplit, split_off, num_windows, false, scan_ws, scan_bytes, stream));
+    GRWS_TRY(scan_i32_to_i64(nslot, slot_off, num_windows, false, scan_ws, scan_bytes, stream));
+    hipLaunchKernelGGL(plan_fill_kernel, dim3(blocks), dim3(256), 0, stream, window_offset, num_windows, num_tiles,
+                       (int)tile_cols, (int)slabs_per_item, item_off, split_off, slot_off, items, split);
+    GRWS_LAUNCH_CHECK();
+    int64_t h[3];
+    GRWS_HIP(hipMemcpyAsync(&h[0], item_off + num_windows, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipMemcpyAsync(&h[1], split_off + num_windows, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipMemcpyAsync(&h[2], slot_off + num_windows, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipStreamSynchronize(stream));
+    counts_out[0] = h[0];
+    counts_out[1] = h[1];
+    counts_out[2] = h[2];
+    return GRWS_OK;
+}
+
+extern "C" size_t grws_spmm_workspace_bytes(const grws_spmm_plan* plan, int64_t n_cols) {
+    if (!plan || plan->num_slots <= 0 || n_cols <= 0) return 0;
+    int64_t nblk = nblk_for(n_cols);
+    int64_t nc = nblk * 16;
+    int64_t nchunks = (n_cols + nc - 1) / nc;
+    return (size_t)plan->num_slots * (size_t)nchunks * 16 * (size_t)nc * sizeof(float);
+}
+
+extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const void* x, int32_t x_dtype,
+                         int64_t x_rows, int64_t ldx, int64_t n_cols, void* y, int32_t y_dtype, int64_t ldy,
+                         void* workspace, size_t workspace_bytes, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(A != nullptr, "spmm: null graph");
+    GRWS_CHECK_ARG(A->tile_rows == 16, "spmm: tile_rows must be 16 (got %d)", A->tile_rows);
+    GRWS_CHECK_ARG(A->tile_cols == 8 || A->tile_cols == 16, "spmm: tile_cols must be 8 or 16 (got %d)", A->tile_cols);
+    GRWS_CHECK_ARG(A->num_windows >= 0 && A->num_tiles >= 0, "spmm: negative graph size");
+    GRWS_CHECK_ARG(n_cols >= 0 && x_rows >= 0, "spmm: negative size");
+    GRWS_CHECK_ARG(x_rows <= INT32_MAX, "spmm: x_rows exceeds int32 column range");
+    if (x_dtype != GRWS_F32 && x_dtype != GRWS_F16 && x_dtype != GRWS_BF16)
+        return set_error(GRWS_E_DTYPE, "spmm: unsupported x dtype %d", x_dtype);
+    if (y_dtype != x_dtype) return set_error(GRWS_E_DTYPE, "spmm: y dtype must equal x dtype");
+    if (A->values_dtype != GRWS_F32 && A->values_dtype != x_dtype)
+        return set_error(GRWS_E_DTYPE, "spmm: values dtype must be F32 or the x dtype");
+    if (A->num_windows == 0 || n_cols == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(A->window_offset && y, "spmm: null pointer");
+    GRWS_CHECK_ARG(ldy >= n_cols, "spmm: ldy < n_cols");
+    if (x_rows > 0) GRWS_CHECK_ARG(x != nullptr && ldx >= n_cols, "spmm: bad x (null or ldx < n_cols)");
+    if (A->num_tiles > 0) GRWS_CHECK_ARG(A->col_indices && A->values, "spmm: null tile arrays");
+
+    const int nblk = nblk_for(n_cols);
+    const int64_t nc = nblk * 16;
+    SpmmArgs a{};
+    a.win_off = A->window_offset;
+    a.cols = A->col_indices;
+    a.vals = A->values;
+    a.num_tiles = A->num_tiles;
+    a.x = x;
+    a.x_rows = x_rows;
+    a.ldx = ldx;
+    a.n_cols = n_cols;
+    a.y = y;
+    a.ldy = ldy;
+    a.nchunks = (int32_t)((n_cols + nc - 1) / nc);
+    if (plan) {
+        GRWS_CHECK_ARG(plan->items != nullptr || plan->num_items == 0, "spmm: plan without items");
+        a.items = plan->items;
+        a.num_items = plan->num_items;
+        if (plan->num_slots > 0) {
+            size_t need = grws_spmm_workspace_bytes(plan, n_cols);
+            if (!workspace || workspace_bytes < need)
+                return set_error(GRWS_E_CAPACITY, "spmm: workspace too small (%zu < %zu)", workspace_bytes, need);
+            a.partials = static_cast<float*>(workspace);
+        }
+    } else {
+        a.items = nullptr;
+        a.num_items = A->num_windows;
+    }
+    if (a.num_items == 0) return GRWS_OK;
+
+    const size_t esz = dtype_size(x_dtype);
+    const int64_t vec = (int64_t)(16 / esz);
+    const bool vect = (n_cols % vec == 0) && (ldx % vec == 0) && ((reinterpret_cast<uintptr_t>(x) % 16) == 0);
+    const bool af32 = A->values_dtype == GRWS_F32;
+    const int tc = A->tile_cols;
+    int st;
+    switch (x_dtype) {
+        case GRWS_F32: st = dispatch_tc<GRWS_F32, true>(a, tc, nblk, vect, stream); break;
+        case GRWS_F16:
+            st = af32 ? dispatch_tc<GRWS_F16, true>(a, tc, nblk, vect, stream)
+                      : dispatch_tc<GRWS_F16, false>(a, tc, nblk, vect, stream);
+            break;
+        default:
+            st = af32 ? dispatch_tc<GRWS_BF16, true>(a, tc, nblk, vect, stream)
+                      : dispatch_tc<GRWS_BF16, false>(a, tc, nblk, vect, stream);
+            break;
+    }
+    if (st != GRWS_OK) return st;
+    if (plan && plan->num_split > 0) {
+        switch (x_dtype) {
+            case GRWS_F32: return launch_fixup<GRWS_F32>(plan, a, nblk, stream);
+            case GRWS_F16: return launch_fixup<GRWS_F16>(plan, a, nblk, stream);
+            default: return launch_fixup<GRWS_BF16>(plan, a, nblk, stream);
+        }
+    }
+    return GRWS_OK;
+}

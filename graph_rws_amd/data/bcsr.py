@@ -1,0 +1,249 @@
+"""BCSRGraph: the reference's BCSR container (data/bcsr.py:23-306) on MI355X.
+
+Layout (unchanged, data/bcsr.py:24-33):
+  window_offset        int64 [W+1]      prefix sum of tiles per 16-row window
+  original_col_indices int32 [T*tc]     ascending unique global columns per
+                                        window, -1 padding in the last tile
+  values_condensed     [T*16*tc]        row-major [tile][row][col]
+
+Differences from the reference, all opt-in or invisible to its callers:
+  * `values_dtype` keyword: float32 (the reference's forced type, :50) by
+    default; float16/bfloat16 halve the value bytes the SpMM streams;
+  * graphs on a CUDA device are built by the gfx950 device builder when the
+    library provides it, otherwise by the host converter (as the reference);
+  * `spmm_plan()` caches the SpMM schedule, `transpose()` caches A^T (used
+    by the backward pass instead of an atomic scatter).
+"""
+from __future__ import annotations
+
+from typing import Any, Dict, Optional
+
+import numpy as np
+import torch
+
+from ..core import csr_to_bcsr_cpu, build_spmm_plan, default_slabs
+
+
+class BCSRGraph:
+    """BCSR graph (data/bcsr.py:23-62)."""
+
+    def __init__(self,
+                 num_nodes: int,
+                 num_edges: int,
+                 tile_rows: int,
+                 tile_cols: int,
+                 window_offset: torch.Tensor,
+                 original_col_indices: torch.Tensor,
+                 values_condensed: torch.Tensor,
+                 device: Optional[torch.device] = None,
+                 num_rows: Optional[int] = None,
+                 num_cols: Optional[int] = None,
+                 values_dtype: Optional[torch.dtype] = None) -> None:
+        self.device = device
+        vdt = torch.float32 if values_dtype is None else values_dtype
+        self.window_offset = window_offset.to(device, non_blocking=True).to(torch.int64)
+        self.original_col_indices = original_col_indices.to(device, non_blocking=True).to(torch.int32)
+        self.values_condensed = values_condensed.to(device, non_blocking=True).to(vdt)
+        self.num_rows = int(num_rows) if num_rows is not None else int(num_nodes)
+        self.num_cols = int(num_cols) if num_cols is not None else int(num_nodes)
+        self.num_nodes = int(num_nodes)
+        self.num_edges = int(num_edges)
+        self.tile_rows = int(tile_rows)
+        self.tile_cols = int(tile_cols)
+        if self.tile_rows != 16:
+            raise ValueError("tile_rows must be 16 (one row window)")
+        self.num_windows = int(self.window_offset.shape[0] - 1)
+        # set from the array sizes (the reference leaves it None, :62)
+        self.num_tiles = int(self.original_col_indices.numel() // self.tile_cols)
+        self._plans: Dict[int, Any] = {}
+        self._transpose: Optional["BCSRGraph"] = None
+
+    # ---------------- constructors (data/bcsr.py:65-159) ----------------
+    @classmethod
+    def from_dgl(cls, g: Any, tile_rows: int = 16, tile_cols: int = 8,
+                 values_dtype: Optional[torch.dtype] = None) -> "BCSRGraph":
+        """From a DGLGraph-like object (num_nodes(), edges(), edata, device)."""
+        device = g.device
+        num_nodes = g.num_nodes()
+        src, dst = g.edges()
+        edge_weights = g.edata.get("weight", None)
+        num_edges, row_ptr, col_idx, values = cls._coo_to_csr(num_nodes, src, dst, edge_weights,
+                                                              device, num_cols=num_nodes)
+        return cls._from_csr(num_rows=num_nodes, row_ptr=row_ptr, col_idx=col_idx,
+                             edge_values=values, tile_rows=tile_rows, tile_cols=tile_cols,
+                             device=device, num_cols=num_nodes, values_dtype=values_dtype)
+
+    @classmethod
+    def from_mtx(cls, filepath: str, index_base: int = 0, undirected: bool = False,
+                 tile_rows: int = 16, tile_cols: int = 8, device: Optional[torch.device] = None,
+                 values_dtype: Optional[torch.dtype] = None) -> "BCSRGraph":
+        """From a Matrix Market file (data/bcsr.py:90-131): all-ones values,
+        square, duplicates summed by scipy's CSR constructor."""
+        import scipy.io as sio
+        import scipy.sparse as sps
+        if device is None:
+            device = torch.device("cuda" if torch.cuda.is_available() else "cpu")
+        coo = sio.mmread(filepath).tocoo()
+        rows = coo.row.astype(np.int64)
+        cols = coo.col.astype(np.int64)
+        if index_base == 1:
+            rows -= 1
+            cols -= 1
+        if undirected:
+            rows, cols = np.concatenate([rows, cols]), np.concatenate([cols, rows])
+        num_rows = int(max(rows.max(), cols.max()) + 1)
+        data = np.ones_like(rows, dtype=np.float32)
+        csr = sps.csr_matrix((data, (rows, cols)), shape=(num_rows, num_rows))
+        return cls._from_csr(num_rows=num_rows,
+                             row_ptr=torch.from_numpy(csr.indptr.astype(np.int64)),
+                             col_idx=torch.from_numpy(csr.indices.astype(np.int32)),
+                             edge_values=torch.from_numpy(csr.data.astype(np.float32)),
+                             tile_rows=tile_rows, tile_cols=tile_cols, device=device,
+                             num_cols=num_rows, values_dtype=values_dtype)
+
+    @classmethod
+    def from_components(cls, window_offset: torch.Tensor, original_col_indices: torch.Tensor,
+                        values_condensed: torch.Tensor, num_rows: int, num_cols: int,
+                        tile_rows: int, tile_cols: int, device: Optional[torch.device] = None,
+                        values_dtype: Optional[torch.dtype] = None) -> "BCSRGraph":
+        """From kernel outputs (data/bcsr.py:134-159).  num_edges is the
+        count of non-zero values, as in the reference (:147)."""
+        if device is None:
+            device = window_offset.device
+        nnz = int(torch.count_nonzero(values_condensed).item()) if values_condensed.numel() > 0 else 0
+        return cls(num_nodes=int(num_rows), num_edges=nnz, tile_rows=tile_rows, tile_cols=tile_cols,
+                   window_offset=window_offset, original_col_indices=original_col_indices,
+                   values_condensed=values_condensed, device=device, num_rows=int(num_rows),
+                   num_cols=int(num_cols),
+                   values_dtype=values_dtype if values_dtype is not None else
+                   (values_condensed.dtype if values_condensed.is_floating_point() else None))
+
+    @classmethod
+    def from_csr(cls, row_ptr: torch.Tensor, col_idx: torch.Tensor, values: Optional[torch.Tensor],
+                 num_rows: int, num_cols: Optional[int] = None, tile_rows: int = 16,
+                 tile_cols: int = 16, device: Optional[torch.device] = None,
+                 values_dtype: Optional[torch.dtype] = None) -> "BCSRGraph":
+        """From a CSR matrix (row_ptr int64 [n+1], col_idx int32, values)."""
+        if device is None:
+            device = row_ptr.device
+        if values is None:
+            values = torch.ones(col_idx.numel(), dtype=torch.float32, device=row_ptr.device)
+        return cls._from_csr(num_rows=num_rows, row_ptr=row_ptr, col_idx=col_idx,
+                             edge_values=values, tile_rows=tile_rows, tile_cols=tile_cols,
+                             device=device, num_cols=num_cols, values_dtype=values_dtype)
+
+    # ---------------- conversions (data/bcsr.py:162-234) ----------------
+    @classmethod
+    def _coo_to_csr(cls, num_rows: int, src: torch.Tensor, dst: torch.Tensor,
+                    edge_weights: Optional[torch.Tensor], device: torch.device,
+                    num_cols: Optional[int] = None):
+        """COO -> CSR with torch ops (data/bcsr.py:163-187).  The sort key is
+        row * num_cols + col (the reference multiplies by num_rows, :170,
+        which misorders rectangular blocks); the sort is stable so duplicate
+        edges keep their input order."""
+        ncols = max(1, int(num_cols) if num_cols is not None else int(num_rows))
+        sort_key = src.to(torch.long) * ncols + dst.to(torch.long)
+        perm = torch.sort(sort_key, stable=True).indices
+        src = src[perm]
+        dst = dst[perm]
+        num_edges = int(src.numel())
+        if edge_weights is not None:
+            values = edge_weights[perm].to(device).to(torch.float32)
+        else:
+            values = torch.ones(num_edges, dtype=torch.float32, device=device)
+        row_counts = torch.bincount(src.to(torch.long), minlength=num_rows).to(torch.int64)
+        row_ptr = torch.zeros(num_rows + 1, dtype=torch.int64, device=device)
+        torch.cumsum(row_counts, dim=0, out=row_ptr[1:])
+        col_idx = dst.to(torch.int32)
+        return num_edges, row_ptr, col_idx, values
+
+    @classmethod
+    def _from_csr(cls, num_rows: int, row_ptr: torch.Tensor, col_idx: torch.Tensor,
+                  edge_values: torch.Tensor, tile_rows: int, tile_cols: int, device: torch.device,
+                  num_cols: Optional[int] = None,
+                  values_dtype: Optional[torch.dtype] = None) -> "BCSRGraph":
+        """CSR -> BCSR (data/bcsr.py:190-234)."""
+        if num_cols is None:
+            num_cols = num_rows
+        device = torch.device(device) if device is not None else row_ptr.device
+        from .. import builder
+        if device.type == "cuda" and builder.available():
+            win, cols, vals = builder.csr_to_bcsr_device(
+                int(num_rows), int(num_cols), row_ptr.to(device), col_idx.to(device),
+                edge_values.to(device), tile_cols=tile_cols,
+                values_dtype=values_dtype or torch.float32)
+        else:
+            win, cols, vals = csr_to_bcsr_cpu(int(num_rows), row_ptr.to("cpu", torch.int64),
+                                              col_idx.to("cpu", torch.int32),
+                                              edge_values.to("cpu", torch.float32),
+                                              int(tile_rows), int(tile_cols))
+        return cls(num_nodes=int(num_rows), num_edges=int(col_idx.numel()), tile_rows=tile_rows,
+                   tile_cols=tile_cols, window_offset=win.to(device),
+                   original_col_indices=cols.to(device), values_condensed=vals.to(device),
+                   device=device, num_rows=int(num_rows), num_cols=int(num_cols),
+                   values_dtype=values_dtype)
+
+    # ---------------- utilities ----------------
+    def to(self, device: torch.device, non_blocking: bool = False) -> "BCSRGraph":
+        """Move to a device, keeping the rectangular shape (data/bcsr.py:238-258)."""
+        if device == self.device:
+            return self
+        return BCSRGraph(num_nodes=self.num_rows, num_edges=self.num_edges,
+                         tile_rows=self.tile_rows, tile_cols=self.tile_cols,
+                         window_offset=self.window_offset.to(device, non_blocking=non_blocking),
+                         original_col_indices=self.original_col_indices.to(device, non_blocking=non_blocking),
+                         values_condensed=self.values_condensed.to(device, non_blocking=non_blocking),
+                         device=device, num_rows=self.num_rows, num_cols=self.num_cols,
+                         values_dtype=self.values_condensed.dtype)
+
+    def with_values_dtype(self, dtype: torch.dtype) -> "BCSRGraph":
+        """Same structure, values cast to `dtype` (round to nearest even)."""
+        return BCSRGraph(num_nodes=self.num_rows, num_edges=self.num_edges,
+                         tile_rows=self.tile_rows, tile_cols=self.tile_cols,
+                         window_offset=self.window_offset,
+                         original_col_indices=self.original_col_indices,
+                         values_condensed=self.values_condensed, device=self.device,
+                         num_rows=self.num_rows, num_cols=self.num_cols, values_dtype=dtype)
+
+    def __repr__(self) -> str:
+        return (f"BCSRGraph(rows={self.num_rows}, cols={self.num_cols}, windows={self.num_windows}, "
+                f"tiles={self.num_tiles}, tile={self.tile_rows}x{self.tile_cols}, "
+                f"values={self.values_condensed.dtype}, device={self.device})")
+
+    @classmethod
+    def from_dgl_block(cls, block: Any, tile_rows: int = 16, tile_cols: int = 8,
+                       values_dtype: Optional[torch.dtype] = None) -> "BCSRGraph":
+        """A DGL message-flow block (dst rows x src cols, data/bcsr.py:266-306)."""
+        device = block.device
+        num_rows = block.num_dst_nodes()
+        num_cols = block.num_src_nodes()
+        src, dst = block.edges()
+        edge_weights = block.edata.get("weight", None) if "weight" in block.edata else None
+        num_edges, row_ptr, col_idx, values = cls._coo_to_csr(num_rows, dst, src, edge_weights,
+                                                              device, num_cols=num_cols)
+        return cls._from_csr(num_rows=num_rows, row_ptr=row_ptr, col_idx=col_idx,
+                             edge_values=values, tile_rows=tile_rows, tile_cols=tile_cols,
+                             device=device, num_cols=num_cols, values_dtype=values_dtype)
+
+    # ---------------- MI355X additions ----------------
+    def spmm_plan(self, n_cols: int):
+        """Cached SpMM schedule for outputs of width n_cols."""
+        slabs = default_slabs(self.num_windows, self.num_tiles, self.tile_cols, n_cols)
+        p = self._plans.get(slabs)
+        if p is None:
+            p = build_spmm_plan(self.window_offset, self.num_tiles, self.tile_cols, slabs)
+            self._plans[slabs] = p
+        return p
+
+    def spmm(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Y[16W, N] = A x on the device."""
+        from ..core import spmm as _spmm
+        return _spmm(self.window_offset, self.original_col_indices, self.values_condensed, x,
+                     self.tile_cols, plan=self.spmm_plan(x.shape[1]), out=out)
+
+    def transpose(self) -> "BCSRGraph":
+        """Cached BCSR of A^T (num_cols x num_rows), built on the device."""
+        if self._transpose is None:
+            from .. import builder
+            self._transpose = builder.transpose(self)
+        return self._transpose

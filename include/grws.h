@@ -1,0 +1,157 @@
+/*
+ * grws.h -- C ABI of the MI355X-native Graph_RWS hot path (libgrws.so).
+ *
+ * This is the drop-in boundary that replaces the reference's pybind11 module
+ * `core_lib` (core/wrapper/bind.cpp:78-161, re-exported by core/__init__.py).
+ * Plain C types only: device pointers, sizes, dtype codes and a hipStream_t
+ * passed as `void*`.  No torch types cross this boundary.
+ *
+ * Conventions (every entry point):
+ *   - returns GRWS_OK (0) or a negative GRWS_E_* code; the message of the
+ *     last failure on the calling thread is returned by grws_last_error();
+ *   - never allocates device memory: outputs and workspaces are provided by
+ *     the caller, sized by the matching *_bytes / *_capacity query;
+ *   - all device work is enqueued on `stream`; entry points that must return
+ *     a data-dependent size to the host say so and synchronise that stream;
+ *   - no global mutable state: calls on different streams and threads are
+ *     independent (re-entrant).
+ *
+ * Tile geometry: tile_rows is 16 (one row window); tile_cols is 8 (the
+ * reference default, config.h:16-18) or 16 (MFMA-native).
+ */
+#ifndef GRWS_H
+#define GRWS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GRWS_ABI_VERSION 1
+
+/* element types */
+enum {
+    GRWS_F32 = 0,
+    GRWS_F16 = 1,
+    GRWS_BF16 = 2
+};
+
+/* status codes */
+enum {
+    GRWS_OK = 0,
+    GRWS_E_INVALID = -1,  /* bad argument: null pointer, negative size, bad tile shape */
+    GRWS_E_DTYPE = -2,    /* unsupported element type or combination */
+    GRWS_E_CAPACITY = -3, /* caller buffer or workspace too small */
+    GRWS_E_HIP = -4,      /* HIP runtime / launch failure */
+    GRWS_E_RANGE = -5     /* index data out of range */
+};
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* grws_last_error(void);
+
+/* GRWS_ABI_VERSION of the loaded library. */
+int grws_abi_version(void);
+
+/*
+ * A BCSR graph as stored by BCSRGraph (data/bcsr.py:23-62):
+ *   window_offset [num_windows+1] int64 prefix sum of tiles per window,
+ *   col_indices   [num_tiles*tile_cols] int32 global column per tile slot,
+ *                 ascending and unique per window, -1 padding,
+ *   values        [num_tiles*tile_rows*tile_cols], row-major per tile.
+ */
+typedef struct grws_bcsr {
+    const int64_t* window_offset;
+    const int32_t* col_indices;
+    const void* values;
+    int64_t num_windows;
+    int64_t num_tiles;
+    int32_t tile_rows;    /* must be 16 */
+    int32_t tile_cols;    /* 8 or 16 */
+    int32_t values_dtype; /* GRWS_F32 / GRWS_F16 / GRWS_BF16 */
+    int32_t reserved;
+} grws_bcsr;
+
+/*
+ * SpMM work schedule (built once per graph by grws_spmm_plan_build).
+ * A "slab" is 16 consecutive column slots of a window (one tile at
+ * tile_cols=16, two at tile_cols=8).  Windows with more than slabs_per_item
+ * slabs are split over several items whose partial sums are combined in a
+ * fixed order (deterministic, no atomics).
+ */
+typedef struct grws_spmm_plan {
+    const int32_t* items; /* [num_items][4] = window, slab_begin, slab_end, partial slot or -1 */
+    const int32_t* split; /* [num_split][3] = window, first slot, number of slots */
+    int64_t num_items;
+    int64_t num_split;
+    int64_t num_slots;
+    int32_t slabs_per_item;
+    int32_t reserved;
+} grws_spmm_plan;
+
+/* ------------------------------------------------------------------------ */
+/* SpMM forward  Y[16W x N] = A * X                                          */
+/* Replaces core_lib.spmm_tc (bind.cpp:124-130 -> spmm_wrapper.cu:33-95,     */
+/* kernel spmm_tc.cuh:40-195).  Unlike the reference it computes every one   */
+/* of the N output columns and writes every row (no memset needed).          */
+/* ------------------------------------------------------------------------ */
+
+/* Upper bounds of the plan arrays for a graph (host arithmetic only). */
+int grws_spmm_plan_capacity(int64_t num_windows, int64_t num_tiles, int32_t tile_cols,
+                            int32_t slabs_per_item, int64_t* max_items, int64_t* max_split);
+
+/* Default slabs_per_item for a graph and output width (host heuristic). */
+int32_t grws_spmm_default_slabs(int64_t num_windows, int64_t num_tiles, int32_t tile_cols,
+                                int64_t n_cols);
+
+/* Workspace bytes needed by grws_spmm_plan_build. */
+size_t grws_spmm_plan_workspace_bytes(int64_t num_windows);
+
+/* Builds the plan on the device.  items: int32 [max_items*4], split: int32
+ * [max_split*3] (device).  Synchronises `stream` and writes the host array
+ * counts_out[3] = {num_items, num_split, num_slots}. */
+int grws_spmm_plan_build(const int64_t* window_offset, int64_t num_windows, int64_t num_tiles,
+                         int32_t tile_cols, int32_t slabs_per_item, int32_t* items,
+                         int64_t max_items, int32_t* split, int64_t max_split, void* workspace,
+                         size_t workspace_bytes, int64_t* counts_out, void* stream);
+
+/* Workspace bytes grws_spmm needs (0 when the plan has no split windows or
+ * plan is NULL). */
+size_t grws_spmm_workspace_bytes(const grws_spmm_plan* plan, int64_t n_cols);
+
+/*
+ * Y = A X.  x: [x_rows, ldx] row-major, first n_cols columns used; y:
+ * [16*num_windows, ldy].  x_dtype == y_dtype; A's values may be F32 or
+ * x_dtype.  F16/BF16 use MFMA with fp32 accumulation; F32 uses fp32 MFMA.
+ * Column slots of -1, or outside [0, x_rows), contribute nothing.
+ * plan may be NULL (one work item per window, no splitting).
+ */
+int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const void* x, int32_t x_dtype,
+              int64_t x_rows, int64_t ldx, int64_t n_cols, void* y, int32_t y_dtype, int64_t ldy,
+              void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* CSR -> BCSR on host cores.  Replaces core_lib.csr_to_bcsr_cpu             */
+/* (bind.cpp:143-150 -> convert_wrapper.cpp:27-180): same layout, same       */
+/* "last duplicate in CSR order wins" rule.  Host pointers.                  */
+/* ------------------------------------------------------------------------ */
+
+/* Pass 1: tiles per window, written as the prefix sum window_offset
+ * [num_windows+1]; *num_tiles_out = total tiles. */
+int grws_csr_to_bcsr_host_count(int64_t num_rows, const int64_t* row_ptr, const int32_t* col_idx,
+                                int32_t tile_rows, int32_t tile_cols, int64_t* window_offset,
+                                int64_t* num_tiles_out, int32_t num_threads);
+
+/* Pass 2: fills col_indices [num_tiles*tile_cols] and values
+ * [num_tiles*tile_rows*tile_cols] (float32). */
+int grws_csr_to_bcsr_host_fill(int64_t num_rows, const int64_t* row_ptr, const int32_t* col_idx,
+                               const float* values, int32_t tile_rows, int32_t tile_cols,
+                               const int64_t* window_offset, int32_t* col_indices,
+                               float* out_values, int32_t num_threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GRWS_H */

@@ -1,0 +1,310 @@
+"""CPU oracle for the Graph_RWS hot path -- TEST INFRASTRUCTURE ONLY.
+
+This package is the parity checker for the HIP library in ``graph_rws_amd``.
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import it, and only as the checker (or as the timed CPU
+baseline).  The product path never imports, links or calls anything here.
+
+The arithmetic lives in ``grws_oracle.c`` (plain C, built into
+``liboracle.so`` by ``oracle/Makefile``); this module is a thin numpy/ctypes
+front end.  Each function names the reference file:line it restates.
+
+Pinning (how each function is checked against something other than itself):
+  * csr_to_bcsr        -- against the reference's own converter compiled from
+                          /root/reference (oracle/_ref, see build_ref.py), and
+                          against BCSR->dense == CSR->dense.
+  * bcsr_spmm          -- against scipy.sparse CSR @ X (an independent
+                          library routine) on the CSR the BCSR came from, and
+                          closed forms (identity, linearity).
+  * bcsr_spmm_t        -- against scipy.sparse (A^T) @ G.
+  * reindex_prune      -- hand-built cases with known answers (C truncation of
+                          negative columns included).
+  * philox4x32_10      -- against vectors produced by ATen's independent
+                          PhiloxRNGEngine.h (tests/golden/philox_aten.npz,
+                          generator script alongside).
+  * sample_hop/relabel -- invariants (distinct, min(deg,k) per node, sorted,
+                          in range, bijective relabel, frontier prefix) and a
+                          brute-force Floyd restatement in pure Python.
+"""
+from __future__ import annotations
+
+import ctypes
+import importlib.util
+import os
+from typing import Optional, Tuple
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(HERE, "liboracle.so")
+_lib = None
+
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_f32p = ctypes.POINTER(ctypes.c_float)
+
+
+def build() -> str:
+    """Compile liboracle.so with the committed Makefile (gcc, OpenMP)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", HERE, "liboracle.so"], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {_LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(_LIB_PATH)
+        L.orc_csr_to_bcsr_count.restype = ctypes.c_int64
+        L.orc_csr_to_bcsr_count.argtypes = [ctypes.c_int64, _i64p, _i32p, ctypes.c_int64,
+                                            ctypes.c_int64, _i64p]
+        L.orc_csr_to_bcsr_fill.restype = None
+        L.orc_csr_to_bcsr_fill.argtypes = [ctypes.c_int64, _i64p, _i32p, _f64p, ctypes.c_int64,
+                                           ctypes.c_int64, _i64p, _i32p, _f64p]
+        L.orc_bcsr_spmm_f64.restype = None
+        L.orc_bcsr_spmm_f64.argtypes = [ctypes.c_int64, _i64p, _i32p, _f64p, ctypes.c_int64,
+                                        ctypes.c_int64, _f64p, ctypes.c_int64, ctypes.c_int64,
+                                        ctypes.c_int64, _f64p, _f64p]
+        L.orc_bcsr_spmm_f32.restype = None
+        L.orc_bcsr_spmm_f32.argtypes = [ctypes.c_int64, ctypes.c_int64, _i64p, _i32p, _f32p,
+                                        ctypes.c_int64, ctypes.c_int64, _f32p, ctypes.c_int64,
+                                        ctypes.c_int64, ctypes.c_int64, _f32p]
+        L.orc_bcsr_spmm_t_f64.restype = None
+        L.orc_bcsr_spmm_t_f64.argtypes = [ctypes.c_int64, _i64p, _i32p, _f64p, ctypes.c_int64,
+                                          ctypes.c_int64, _f64p, ctypes.c_int64, ctypes.c_int64,
+                                          ctypes.c_int64, _f64p, _f64p]
+        L.orc_reindex_prune.restype = None
+        L.orc_reindex_prune.argtypes = [_i32p, ctypes.c_int64, _f32p, _i32p, ctypes.c_int64,
+                                        ctypes.c_int32, ctypes.c_int32, _i32p]
+        L.orc_philox4x32_10.restype = None
+        L.orc_philox4x32_10.argtypes = [_u32p, _u32p, _u32p]
+        L.orc_philox_draws.restype = None
+        L.orc_philox_draws.argtypes = [ctypes.c_uint64, _i64p, _u32p, ctypes.c_int64, _u32p]
+        L.orc_sample_hop.restype = ctypes.c_int64
+        L.orc_sample_hop.argtypes = [_i64p, _i32p, ctypes.c_uint64, _i64p, ctypes.c_int64,
+                                     ctypes.c_int, _i32p, _i64p]
+        L.orc_relabel.restype = ctypes.c_int64
+        L.orc_relabel.argtypes = [_i64p, ctypes.c_int64, _i64p, ctypes.c_int64, _i32p, _i64p]
+        L.orc_num_threads.restype = ctypes.c_int
+        L.orc_set_num_threads.argtypes = [ctypes.c_int]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray, t):
+    return a.ctypes.data_as(t)
+
+
+def _c(a, dtype) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a), dtype=dtype)
+
+
+# ----------------------------------------------------------------------------
+# CSR -> BCSR  (convert_wrapper.cpp:27-180)
+# ----------------------------------------------------------------------------
+def csr_to_bcsr(num_rows: int, row_ptr, col_idx, values, tile_rows: int = 16,
+                tile_cols: int = 8) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Restates csr_to_bcsr_cpu (convert_wrapper.cpp:27-180).  Values are
+    carried in float64 (exact for any f16/bf16/f32 input)."""
+    rp = _c(row_ptr, np.int64)
+    ci = _c(col_idx, np.int32)
+    va = _c(values, np.float64)
+    W = (num_rows + tile_rows - 1) // tile_rows
+    win = np.zeros(W + 1, np.int64)
+    T = lib().orc_csr_to_bcsr_count(num_rows, _p(rp, _i64p), _p(ci, _i32p), tile_rows,
+                                    tile_cols, _p(win, _i64p))
+    cols = np.empty(T * tile_cols, np.int32)
+    vals = np.empty(T * tile_rows * tile_cols, np.float64)
+    lib().orc_csr_to_bcsr_fill(num_rows, _p(rp, _i64p), _p(ci, _i32p), _p(va, _f64p),
+                               tile_rows, tile_cols, _p(win, _i64p), _p(cols, _i32p),
+                               _p(vals, _f64p))
+    return win, cols, vals
+
+
+def ref_csr_to_bcsr(num_rows: int, row_ptr, col_idx, values, tile_rows: int = 16,
+                    tile_cols: int = 8):
+    """The reference's own converter (oracle/_ref, compiled from
+    /root/reference/core/wrapper/convert_wrapper.cpp).  None if not built."""
+    mod = _ref_module()
+    if mod is None:
+        return None
+    import torch
+    out = mod.csr_to_bcsr_cpu(int(num_rows), torch.as_tensor(_c(row_ptr, np.int64)),
+                              torch.as_tensor(_c(col_idx, np.int32)),
+                              torch.as_tensor(_c(values, np.float32)), int(tile_rows),
+                              int(tile_cols))
+    return tuple(t.numpy() for t in out)
+
+
+_ref_mod = None
+
+
+def _ref_module():
+    global _ref_mod
+    if _ref_mod is not None:
+        return _ref_mod
+    d = os.path.join(HERE, "_ref")
+    if not os.path.isdir(d):
+        return None
+    so = [f for f in os.listdir(d) if f.startswith("ref_convert") and f.endswith(".so")]
+    if not so:
+        return None
+    import torch  # noqa: F401  (the module links libtorch)
+    spec = importlib.util.spec_from_file_location("ref_convert", os.path.join(d, so[0]))
+    m = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(m)
+    _ref_mod = m
+    return m
+
+
+def bcsr_to_dense(win, cols, vals, tile_rows: int, tile_cols: int, num_cols: int) -> np.ndarray:
+    """Dense [16W x num_cols] float64 matrix of a BCSR graph (duplicates cannot
+    occur: columns are unique per window)."""
+    win = np.asarray(win); cols = np.asarray(cols); vals = np.asarray(vals, np.float64)
+    W = len(win) - 1
+    D = np.zeros((W * tile_rows, num_cols), np.float64)
+    for w in range(W):
+        for t in range(win[w], win[w + 1]):
+            for c in range(tile_cols):
+                col = cols[t * tile_cols + c]
+                if col < 0 or col >= num_cols:
+                    continue
+                D[w * tile_rows:(w + 1) * tile_rows, col] = \
+                    vals[t * tile_rows * tile_cols + c:(t + 1) * tile_rows * tile_cols:tile_cols]
+    return D
+
+
+# ----------------------------------------------------------------------------
+# SpMM forward / transpose
+# ----------------------------------------------------------------------------
+def bcsr_spmm(win, cols, vals, tile_rows: int, tile_cols: int, X) -> Tuple[np.ndarray, np.ndarray]:
+    """Y = A X and |A||X| in float64 (spmm_tc.cuh:113-193 semantics, all N
+    columns).  X may be any float dtype; it is widened exactly."""
+    win = _c(win, np.int64); cols = _c(cols, np.int32); vals = _c(vals, np.float64)
+    X = _c(X, np.float64)
+    if X.ndim != 2:
+        raise ValueError("X must be 2-D")
+    W = len(win) - 1
+    N = X.shape[1]
+    Y = np.empty((W * tile_rows, N), np.float64)
+    Ya = np.empty_like(Y)
+    lib().orc_bcsr_spmm_f64(W, _p(win, _i64p), _p(cols, _i32p), _p(vals, _f64p), tile_rows,
+                            tile_cols, _p(X, _f64p), X.shape[0], N, N, _p(Y, _f64p),
+                            _p(Ya, _f64p))
+    return Y, Ya
+
+
+def bcsr_spmm_t(win, cols, vals, tile_rows: int, tile_cols: int, G, num_cols: int):
+    """G_in = A^T G and |A|^T|G| in float64 (spmm_tc.cuh:211-270 semantics
+    without the 1e-9 skip / int32 / D>1024 quirks)."""
+    win = _c(win, np.int64); cols = _c(cols, np.int32); vals = _c(vals, np.float64)
+    G = _c(G, np.float64)
+    W = len(win) - 1
+    D = G.shape[1]
+    if G.shape[0] < W * tile_rows:
+        raise ValueError("G must have at least 16W rows")
+    out = np.empty((num_cols, D), np.float64)
+    outa = np.empty_like(out)
+    lib().orc_bcsr_spmm_t_f64(W, _p(win, _i64p), _p(cols, _i32p), _p(vals, _f64p), tile_rows,
+                              tile_cols, _p(G, _f64p), D, D, num_cols, _p(out, _f64p),
+                              _p(outa, _f64p))
+    return out, outa
+
+
+def bcsr_spmm_f32_timed(win, cols, vals_f32, tile_rows: int, tile_cols: int, X_f32,
+                        w_begin: int, w_end: int) -> np.ndarray:
+    """fp32 CPU SpMM over windows [w_begin, w_end) (the timed CPU baseline)."""
+    N = X_f32.shape[1]
+    Y = np.empty(((w_end - w_begin) * tile_rows, N), np.float32)
+    lib().orc_bcsr_spmm_f32(w_begin, w_end, _p(win, _i64p), _p(cols, _i32p),
+                            _p(vals_f32, _f32p), tile_rows, tile_cols, _p(X_f32, _f32p),
+                            X_f32.shape[0], X_f32.shape[1], N, _p(Y, _f32p))
+    return Y
+
+
+def num_threads() -> int:
+    return int(lib().orc_num_threads())
+
+
+def set_num_threads(n: int) -> None:
+    lib().orc_set_num_threads(int(n))
+
+
+# ----------------------------------------------------------------------------
+# reindex (reindex.cuh:33-102)
+# ----------------------------------------------------------------------------
+def reindex_prune(in_cols, values, active_windows, tile_rows: int = 16, tile_cols: int = 8):
+    """Returns (out_cols, values_after).  `values` is not modified; a pruned
+    copy is returned (the reference prunes in place)."""
+    ic = _c(in_cols, np.int32)
+    va = _c(values, np.float32).copy()
+    aw = _c(active_windows, np.int32)
+    out = np.empty_like(ic)
+    lib().orc_reindex_prune(_p(ic, _i32p), ic.size, _p(va, _f32p), _p(aw, _i32p), aw.size,
+                            tile_rows, tile_cols, _p(out, _i32p))
+    return out, va
+
+
+# ----------------------------------------------------------------------------
+# Philox + node-wise sampler + relabel (no reference counterpart)
+# ----------------------------------------------------------------------------
+def philox4x32_10(counter, key) -> np.ndarray:
+    c = _c(counter, np.uint32)
+    k = _c(key, np.uint32)
+    o = np.empty(4, np.uint32)
+    lib().orc_philox4x32_10(_p(c, _u32p), _p(k, _u32p), _p(o, _u32p))
+    return o
+
+
+def philox_draws(seed: int, nodes, draws) -> np.ndarray:
+    n = _c(nodes, np.int64)
+    d = _c(draws, np.uint32)
+    o = np.empty(n.size, np.uint32)
+    lib().orc_philox_draws(seed, _p(n, _i64p), _p(d, _u32p), n.size, _p(o, _u32p))
+    return o
+
+
+def sample_hop(indptr, indices, seed: int, frontier, k: int):
+    """Floyd sampling of min(deg,k) neighbours per frontier node.  Returns
+    (edge_dst_local int32[E], edge_src_global int64[E])."""
+    ip = _c(indptr, np.int64)
+    ix = _c(indices, np.int32)
+    fr = _c(frontier, np.int64)
+    if k < 1 or k > 64:
+        raise ValueError("k must be in [1, 64]")
+    cap = max(1, fr.size * k)
+    dst = np.empty(cap, np.int32)
+    src = np.empty(cap, np.int64)
+    E = lib().orc_sample_hop(_p(ip, _i64p), _p(ix, _i32p), seed, _p(fr, _i64p), fr.size, k,
+                             _p(dst, _i32p), _p(src, _i64p))
+    return dst[:E].copy(), src[:E].copy()
+
+
+def relabel(frontier, edge_src):
+    """Returns (src_local int32[E], next_frontier int64[n_src])."""
+    fr = _c(frontier, np.int64)
+    es = _c(edge_src, np.int64)
+    sl = np.empty(max(1, es.size), np.int32)
+    nf = np.empty(max(1, fr.size + es.size), np.int64)
+    n = lib().orc_relabel(_p(fr, _i64p), fr.size, _p(es, _i64p), es.size, _p(sl, _i32p),
+                          _p(nf, _i64p))
+    return sl[:es.size].copy(), nf[:n].copy()
+
+
+# ----------------------------------------------------------------------------
+# quantisation helpers (the same rounding the device applies)
+# ----------------------------------------------------------------------------
+def round_to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 (round to nearest even), returned as float32."""
+    x = np.ascontiguousarray(x, np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    lsb = (u >> 16) & 1
+    r = ((u + 0x7FFF + lsb) >> 16) << 16
+    nan = np.isnan(x)
+    out = r.astype(np.uint32).view(np.float32).copy()
+    out[nan] = np.nan
+    return out

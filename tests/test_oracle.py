@@ -1,0 +1,241 @@
+"""Pins the CPU oracle (oracle/) against things other than itself:
+the reference's own converter compiled from /root/reference (when built),
+scipy.sparse, closed forms, ATen's independent Philox engine, and invariants.
+CPU only."""
+import os
+
+import numpy as np
+import pytest
+import scipy.sparse as sps
+
+import oracle
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _csr(n_rows, n_cols, nnz, seed, dup=False, empty_rows=()):
+    rng = np.random.default_rng(seed)
+    r = rng.integers(0, n_rows, nnz)
+    c = rng.integers(0, n_cols, nnz)
+    keep = ~np.isin(r, np.array(list(empty_rows), dtype=np.int64))
+    r, c = r[keep], c[keep]
+    v = rng.standard_normal(r.size).astype(np.float32)
+    if not dup:
+        key = r * n_cols + c
+        _, first = np.unique(key, return_index=True)
+        r, c, v = r[first], c[first], v[first]
+    order = np.argsort(r * n_cols + c, kind="stable")
+    r, c, v = r[order], c[order], v[order]
+    rp = np.zeros(n_rows + 1, np.int64)
+    np.add.at(rp, r + 1, 1)
+    rp = np.cumsum(rp)
+    return rp, c.astype(np.int32), v
+
+
+CASES = [
+    # n_rows, n_cols, nnz, seed, dup, empty rows
+    (1, 1, 1, 0, False, ()),
+    (15, 15, 30, 1, False, ()),
+    (33, 50, 200, 2, False, (0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15)),  # empty window 0
+    (100, 100, 900, 3, True, (40,)),        # duplicate edges
+    (64, 1000, 3000, 4, False, ()),         # rectangular, wide
+    (257, 31, 2000, 5, True, ()),           # dense-ish, duplicates
+]
+
+
+@pytest.mark.parametrize("tc", [8, 16])
+@pytest.mark.parametrize("case", CASES)
+def test_csr_to_bcsr_matches_reference_converter(case, tc):
+    n, m, nnz, seed, dup, empty = case
+    rp, ci, va = _csr(n, m, nnz, seed, dup, empty)
+    win, cols, vals = oracle.csr_to_bcsr(n, rp, ci, va, 16, tc)
+    ref = oracle.ref_csr_to_bcsr(n, rp, ci, va, 16, tc)
+    if ref is None:
+        pytest.skip("oracle/_ref not built (needs /root/reference); run make -C oracle ref")
+    rw, rc, rv = ref
+    np.testing.assert_array_equal(win, rw)
+    np.testing.assert_array_equal(cols, rc)
+    np.testing.assert_array_equal(vals.astype(np.float32), rv)
+
+
+@pytest.mark.parametrize("tc", [8, 16])
+@pytest.mark.parametrize("case", [c for c in CASES if not c[4]])
+def test_csr_to_bcsr_dense_equivalence_and_invariants(case, tc):
+    n, m, nnz, seed, dup, empty = case
+    rp, ci, va = _csr(n, m, nnz, seed, dup, empty)
+    win, cols, vals = oracle.csr_to_bcsr(n, rp, ci, va, 16, tc)
+    W = (n + 15) // 16
+    assert win.shape == (W + 1,) and win[0] == 0 and np.all(np.diff(win) >= 0)
+    dense = oracle.bcsr_to_dense(win, cols, vals, 16, tc, m)[:n]
+    ref = sps.csr_matrix((va.astype(np.float64), ci, rp), shape=(n, m)).toarray()
+    np.testing.assert_array_equal(dense, ref)
+    for w in range(W):
+        c = cols[win[w] * tc:win[w + 1] * tc]
+        valid = c[c >= 0]
+        assert np.all(np.diff(valid) > 0)                 # ascending unique
+        k = valid.size
+        assert np.all(c[k:] == -1)                        # -1 only as the tail
+        assert len(c) - k < tc                            # padding < one tile
+        t = vals[win[w] * 16 * tc:win[w + 1] * 16 * tc].reshape(-1, 16, tc)
+        pad = (c == -1).reshape(-1, tc)
+        assert np.all(t[np.broadcast_to(pad[:, None, :], t.shape)] == 0)
+    assert np.count_nonzero(vals) == np.count_nonzero(va)
+
+
+def test_csr_to_bcsr_duplicate_last_wins():
+    # row 0 has column 3 twice: the later entry in CSR order wins
+    rp = np.array([0, 3], np.int64)
+    ci = np.array([3, 1, 3], np.int32)
+    va = np.array([1.0, 2.0, 5.0], np.float32)
+    win, cols, vals = oracle.csr_to_bcsr(1, rp, ci, va, 16, 8)
+    assert list(cols[:2]) == [1, 3]
+    assert vals[0] == 2.0 and vals[1] == 5.0
+
+
+@pytest.mark.parametrize("tc", [8, 16])
+def test_spmm_oracle_matches_scipy(tc):
+    n, m = 130, 90
+    rp, ci, va = _csr(n, m, 1500, 7)
+    win, cols, vals = oracle.csr_to_bcsr(n, rp, ci, va, 16, tc)
+    X = np.random.default_rng(8).standard_normal((m, 37))
+    Y, Ya = oracle.bcsr_spmm(win, cols, vals, 16, tc, X)
+    A = sps.csr_matrix((va.astype(np.float64), ci, rp), shape=(n, m))
+    np.testing.assert_allclose(Y[:n], A @ X, rtol=1e-12, atol=1e-12)
+    assert np.all(Y[n:] == 0)
+    np.testing.assert_allclose(Ya[:n], abs(A) @ abs(X), rtol=1e-12, atol=1e-12)
+
+
+def test_spmm_oracle_identity_and_linearity():
+    n = 70
+    rp = np.arange(n + 1, dtype=np.int64)
+    ci = np.arange(n, dtype=np.int32)
+    va = np.ones(n, np.float32)
+    win, cols, vals = oracle.csr_to_bcsr(n, rp, ci, va, 16, 16)
+    X = np.random.default_rng(0).standard_normal((n, 5))
+    Y, _ = oracle.bcsr_spmm(win, cols, vals, 16, 16, X)
+    np.testing.assert_array_equal(Y[:n], X)
+    rp, ci, va = _csr(n, n, 400, 9)
+    win, cols, vals = oracle.csr_to_bcsr(n, rp, ci, va, 16, 8)
+    X2 = np.random.default_rng(1).standard_normal((n, 5))
+    Ya, _ = oracle.bcsr_spmm(win, cols, vals, 16, 8, X)
+    Yb, _ = oracle.bcsr_spmm(win, cols, vals, 16, 8, X2)
+    Yc, _ = oracle.bcsr_spmm(win, cols, vals, 16, 8, 2.0 * X - 3.0 * X2)
+    np.testing.assert_allclose(Yc, 2.0 * Ya - 3.0 * Yb, rtol=1e-12, atol=1e-12)
+
+
+def test_spmm_oracle_skips_padding_and_out_of_range():
+    # column -1 and column >= x_rows contribute nothing, even with NaN rows
+    win = np.array([0, 1], np.int64)
+    cols = np.array([0, 5, -1, -1, -1, -1, -1, -1], np.int32)
+    vals = np.zeros(128)
+    vals[0 * 8 + 0] = 2.0
+    vals[0 * 8 + 1] = 3.0    # column 5 is outside x_rows=4
+    X = np.array([[1.0], [np.nan], [np.nan], [np.nan]])
+    Y, _ = oracle.bcsr_spmm(win, cols, vals, 16, 8, X)
+    assert Y[0, 0] == 2.0 and np.all(Y[1:] == 0)
+
+
+@pytest.mark.parametrize("tc", [8, 16])
+def test_spmm_t_oracle_matches_scipy(tc):
+    n, m = 97, 61
+    rp, ci, va = _csr(n, m, 900, 11)
+    win, cols, vals = oracle.csr_to_bcsr(n, rp, ci, va, 16, tc)
+    W = len(win) - 1
+    G = np.random.default_rng(12).standard_normal((16 * W, 19))
+    out, outa = oracle.bcsr_spmm_t(win, cols, vals, 16, tc, G, m)
+    A = sps.csr_matrix((va.astype(np.float64), ci, rp), shape=(n, m))
+    np.testing.assert_allclose(out, A.T @ G[:n], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(outa, abs(A).T @ abs(G[:n]), rtol=1e-12, atol=1e-12)
+
+
+def test_spmm_f32_baseline_close_to_f64():
+    n = 200
+    rp, ci, va = _csr(n, n, 3000, 13)
+    win, cols, vals = oracle.csr_to_bcsr(n, rp, ci, va, 16, 16)
+    X = np.random.default_rng(14).standard_normal((n, 33)).astype(np.float32)
+    Y64, Ya = oracle.bcsr_spmm(win, cols, vals, 16, 16, X)
+    W = len(win) - 1
+    Y32 = oracle.bcsr_spmm_f32_timed(win, cols, vals.astype(np.float32), 16, 16, X, 0, W)
+    assert np.all(np.abs(Y32 - Y64) <= 1e-5 * Ya + 1e-30)
+
+
+def test_reindex_prune_known_answers():
+    # active windows 0, 3, 7 -> local windows 0, 1, 2
+    act = np.array([0, 3, 7], np.int32)
+    cols = np.array([-1, 5, 49, 113, 20, -17, 48, 127], np.int32)  # one 16x8 tile
+    vals = np.arange(1, 129, dtype=np.float32)
+    out, v2 = oracle.reindex_prune(cols, vals, act, 16, 8)
+    # -1 -> window 0 (C truncation), offset -1 -> -1;  20 -> window 1 missing;
+    # -17 -> window -1 missing
+    assert list(out) == [-1, 5, 17, 33, 0, 0, 16, 47]
+    v = vals.reshape(16, 8).copy()
+    v[:, 4] = 0
+    v[:, 5] = 0
+    np.testing.assert_array_equal(v2.reshape(16, 8), v)
+    # without window 0 the -1 padding is pruned to column 0
+    out2, v3 = oracle.reindex_prune(cols, vals, np.array([3, 7], np.int32), 16, 8)
+    assert out2[0] == 0 and np.all(v3.reshape(16, 8)[:, 0] == 0)
+
+
+def test_philox_matches_aten_engine():
+    z = np.load(os.path.join(HERE, "golden", "philox_aten.npz"))
+    for s, n, d, w in zip(z["seed"], z["node"], z["draw"], z["words"]):
+        s, n, d = int(s), int(n), int(d)
+        out = oracle.philox4x32_10([n & 0xFFFFFFFF, n >> 32, d & 0xFFFFFFFF, d >> 32],
+                                   [s & 0xFFFFFFFF, s >> 32])
+        np.testing.assert_array_equal(out, w)
+    # the sampler's draw = word 0 with counter (node, draw, 0) and key seed
+    sel = (z["seed"] == 42) & (z["draw"] < 2**32) & (z["node"] < 2**62)
+    nodes = z["node"][sel].astype(np.int64)
+    draws = z["draw"][sel].astype(np.uint32)
+    np.testing.assert_array_equal(oracle.philox_draws(42, nodes, draws), z["words"][sel][:, 0])
+
+
+def _toy_csr(degs, seed=0):
+    rng = np.random.default_rng(seed)
+    indptr = np.concatenate([[0], np.cumsum(degs)]).astype(np.int64)
+    indices = rng.integers(0, 10_000, int(indptr[-1])).astype(np.int32)
+    return indptr, indices
+
+
+def test_floyd_sampler_invariants():
+    degs = [0, 1, 3, 5, 6, 15, 16, 40, 1000, 64, 65]
+    indptr, indices = _toy_csr(degs)
+    for k in (1, 5, 15, 64):
+        dst, src = oracle.sample_hop(indptr, indices, 42, np.arange(len(degs)), k)
+        for i, d in enumerate(degs):
+            sel = dst == i
+            assert sel.sum() == min(d, k)
+    # positions: distinct, sorted by CSR position -> compare to the neighbour list
+    dst, src = oracle.sample_hop(indptr, indices, 42, np.arange(len(degs)), 15)
+    for i, d in enumerate(degs):
+        nb = indices[indptr[i]:indptr[i + 1]]
+        got = src[dst == i]
+        if d <= 15:
+            np.testing.assert_array_equal(got, nb)
+
+
+def test_floyd_sampler_is_uniform():
+    # every subset position equally likely: frequency of each position ~ k/deg
+    deg, k, nodes = 12, 4, 60000
+    indptr = np.arange(0, (nodes + 1) * deg, deg, dtype=np.int64)
+    indices = np.tile(np.arange(deg, dtype=np.int32), nodes)
+    dst, src = oracle.sample_hop(indptr, indices, 42, np.arange(nodes), k)
+    counts = np.bincount(src, minlength=deg)
+    expect = nodes * k / deg
+    chi2 = ((counts - expect) ** 2 / expect).sum()
+    assert chi2 < 40.0  # 11 dof, p ~ 1e-4
+
+
+def test_relabel_invariants():
+    rng = np.random.default_rng(3)
+    frontier = rng.choice(5000, 300, replace=False).astype(np.int64)
+    src = rng.integers(0, 5000, 4000).astype(np.int64)
+    src[:50] = frontier[rng.integers(0, 300, 50)]
+    local, nxt = oracle.relabel(frontier, src)
+    np.testing.assert_array_equal(nxt[:300], frontier)           # frontier prefix kept
+    new = nxt[300:]
+    assert np.all(np.diff(new) > 0)                              # ascending, unique
+    assert not np.isin(new, frontier).any()
+    np.testing.assert_array_equal(nxt[local], src)               # bijective relabel
+    assert set(np.unique(np.concatenate([frontier, src]))) == set(nxt)

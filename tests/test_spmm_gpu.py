@@ -1,0 +1,162 @@
+"""BCSR SpMM forward (H1) on the GPU against the float64 oracle.
+
+Tolerance (north_star): |Y - Y_ref| <= rtol * (|A| |X|) elementwise, computed
+in float64 on the same quantised inputs, with rtol = 1e-2 for float16 /
+bfloat16 inputs and 1e-5 for float32.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from graph_rws_amd import core, synth
+from graph_rws_amd.data import BCSRGraph
+
+pytestmark = pytest.mark.gpu
+
+RTOL = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 1e-2}
+
+
+def _bcsr(g, tc, dev, vdt=torch.float32):
+    win, cols, vals = core.csr_to_bcsr_cpu(g.num_nodes, g.row_ptr, g.col_idx, g.values, 16, tc)
+    return BCSRGraph(g.num_nodes, g.nnz, 16, tc, win, cols, vals, device=dev,
+                     num_cols=g.num_nodes, values_dtype=vdt)
+
+
+def _check(G, X, Y, xdt):
+    """Compare the device result with the oracle on the quantised inputs."""
+    vq = G.values_condensed.to(xdt).double().cpu().numpy() if G.values_condensed.dtype != xdt \
+        else G.values_condensed.double().cpu().numpy()
+    Yr, Ya = oracle.bcsr_spmm(G.window_offset.cpu().numpy(), G.original_col_indices.cpu().numpy(),
+                              vq, 16, G.tile_cols, X.double().cpu().numpy())
+    Yd = Y.double().cpu().numpy()
+    err = np.abs(Yd - Yr)
+    bound = RTOL[xdt] * Ya
+    bad = err > bound
+    assert not bad.any(), (f"{bad.sum()} of {bad.size} elements out of tolerance; "
+                           f"worst excess {float((err - bound).max()):.3e}")
+    return Yr
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("tc", [8, 16])
+@pytest.mark.parametrize("N", [1, 7, 16, 17, 41, 64, 128, 200])
+def test_spmm_parity_random(cuda_device, xdt, tc, N):
+    print(f"case random xdt={xdt} tc={tc} N={N}", flush=True)
+    g = synth.random_graph(333, 9.0, seed=N + tc)
+    G = _bcsr(g, tc, cuda_device)
+    X = synth.features(g.num_nodes, N, seed=N, device=cuda_device).to(xdt)
+    Y = G.spmm(X)
+    torch.cuda.synchronize()
+    assert Y.shape == (16 * G.num_windows, N) and Y.dtype == xdt
+    _check(G, X, Y, xdt)
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("tc", [8, 16])
+def test_spmm_parity_low_precision_values(cuda_device, xdt, tc):
+    """values stored in the 16-bit type (no in-kernel conversion)."""
+    print(f"case lowprec-values xdt={xdt} tc={tc}", flush=True)
+    g = synth.random_graph(500, 12.0, seed=3)
+    G = _bcsr(g, tc, cuda_device, vdt=xdt)
+    X = synth.features(g.num_nodes, 96, seed=4, device=cuda_device).to(xdt)
+    Y = G.spmm(X)
+    torch.cuda.synchronize()
+    _check(G, X, Y, xdt)
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16])
+@pytest.mark.parametrize("slabs", [1, 2, 3, 16])
+def test_spmm_split_windows(cuda_device, xdt, slabs):
+    """Power-law graph with hub windows, forced splitting over work items."""
+    print(f"case split xdt={xdt} slabs={slabs}", flush=True)
+    g = synth.chung_lu(3000, 40000, 2.1, seed=11)
+    G = _bcsr(g, 16, cuda_device)
+    plan = core.build_spmm_plan(G.window_offset, G.num_tiles, 16, slabs)
+    assert plan.num_split > 0
+    X = synth.features(g.num_nodes, 80, seed=5, device=cuda_device).to(xdt)
+    Y = core.spmm(G.window_offset, G.original_col_indices, G.values_condensed, X, 16, plan=plan)
+    Y0 = core.spmm(G.window_offset, G.original_col_indices, G.values_condensed, X, 16, plan=None)
+    torch.cuda.synchronize()
+    _check(G, X, Y, xdt)
+    _check(G, X, Y0, xdt)
+
+
+def test_spmm_deterministic(cuda_device):
+    print("case determinism", flush=True)
+    g = synth.chung_lu(4000, 60000, 2.1, seed=12)
+    G = _bcsr(g, 16, cuda_device)
+    plan = core.build_spmm_plan(G.window_offset, G.num_tiles, 16, 2)
+    X = synth.features(g.num_nodes, 128, seed=6, device=cuda_device).to(torch.float16)
+    a = core.spmm(G.window_offset, G.original_col_indices, G.values_condensed, X, 16, plan=plan)
+    b = core.spmm(G.window_offset, G.original_col_indices, G.values_condensed, X, 16, plan=plan)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_spmm_padding_never_reads_x(cuda_device):
+    """NaN in every X row no column references must not reach Y: -1 slots and
+    out-of-range columns are masked at the load."""
+    print("case nan-poison", flush=True)
+    n = 400
+    rng = np.random.default_rng(7)
+    rows = rng.integers(0, n, 3000)
+    cols = rng.integers(0, n // 2, 3000)          # only the first half is referenced
+    key = np.unique(rows * n + cols)
+    rows, cols = key // n, key % n
+    rp = np.zeros(n + 1, np.int64)
+    np.add.at(rp, rows + 1, 1)
+    rp = np.cumsum(rp)
+    g = synth.CSRGraph(n, torch.from_numpy(rp), torch.from_numpy(cols.astype(np.int32)),
+                       torch.from_numpy(rng.standard_normal(cols.size).astype(np.float32)))
+    for tc in (8, 16):
+        G = _bcsr(g, tc, cuda_device)
+        X = synth.features(n, 48, seed=1, device=cuda_device)
+        X[n // 2:] = float("nan")
+        Y = G.spmm(X)
+        torch.cuda.synchronize()
+        assert torch.isfinite(Y).all()
+        _check(G, X[: n // 2].contiguous(), Y, torch.float32)
+
+
+def test_spmm_empty_windows_and_short_x(cuda_device):
+    """Windows without tiles produce zero rows; columns >= x_rows contribute
+    nothing (x shorter than num_cols)."""
+    print("case empty-windows", flush=True)
+    n = 100
+    rp = np.zeros(n + 1, np.int64)
+    rp[50:] = 3                                    # only row 49 has edges
+    cols = np.array([2, 60, 99], np.int32)
+    vals = np.array([1.0, 2.0, 4.0], np.float32)
+    g = synth.CSRGraph(n, torch.from_numpy(rp), torch.from_numpy(cols), torch.from_numpy(vals))
+    G = _bcsr(g, 8, cuda_device)
+    X = torch.ones(70, 16, device=cuda_device)      # rows 70.. do not exist
+    Y = G.spmm(X)
+    torch.cuda.synchronize()
+    expect = torch.zeros(112, 16)
+    expect[49] = 3.0
+    assert torch.equal(Y.cpu(), expect)
+
+
+def test_spmm_tc_dropin_signature(cuda_device):
+    """core.spmm_tc keeps the reference's (C, ms) return (bind.cpp:124-130)."""
+    print("case spmm_tc", flush=True)
+    g = synth.random_graph(257, 6.0, seed=21)
+    G = _bcsr(g, 8, cuda_device)
+    X = synth.features(g.num_nodes, 64, seed=2, device=cuda_device)
+    C, ms = core.spmm_tc(G.window_offset, G.original_col_indices, G.values_condensed, X, 8)
+    torch.cuda.synchronize()
+    assert isinstance(ms, float) and C.shape == (16 * G.num_windows, 64)
+    _check(G, X, C, torch.float32)
+
+
+def test_spmm_c2_full_size(cuda_device):
+    """BASELINE config c2 (169,343 nodes, ~2.33M nnz, N=128, f16 and bf16)."""
+    print("case c2 full", flush=True)
+    g = synth.config_graph("c2")
+    G = _bcsr(g, 16, cuda_device)
+    for xdt in (torch.float16, torch.bfloat16):
+        X = synth.features(g.num_nodes, 128, seed=2, device=cuda_device).to(xdt)
+        Y = G.spmm(X)
+        torch.cuda.synchronize()
+        _check(G, X, Y, xdt)
