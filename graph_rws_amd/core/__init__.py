@@ -9,8 +9,10 @@ from .ops import (  # noqa: F401
     build_spmm_plan,
     csr_to_bcsr_cpu,
     default_slabs,
+    reindex_bcsr,
     spmm,
     spmm_tc,
+    spmm_transpose,
 )
 
 
@@ -25,6 +27,8 @@ class SamplingConfig:
 
 __all__ = [
     "spmm_tc",
+    "spmm_transpose",
+    "reindex_bcsr",
     "csr_to_bcsr_cpu",
     "SamplingConfig",
     "spmm",

@@ -57,6 +57,25 @@ _PROTOS = {
                                                    ctypes.c_int32, _vp, _c_i64p, ctypes.c_int32]),
     "grws_csr_to_bcsr_host_fill": (ctypes.c_int, [ctypes.c_int64, _vp, _vp, _vp, ctypes.c_int32,
                                                   ctypes.c_int32, _vp, _vp, _vp, ctypes.c_int32]),
+    "grws_bcsr_build_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64,
+                                                          ctypes.c_int64, ctypes.c_int32]),
+    "grws_bcsr_build_count": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64,
+                                             ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _vp,
+                                             _vp, ctypes.c_size_t, _c_i64p, _vp]),
+    "grws_bcsr_build_fill": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                            ctypes.c_int32, ctypes.c_int32, _vp, ctypes.c_int64,
+                                            _vp, _vp, ctypes.c_int32, _vp, ctypes.c_size_t, _vp]),
+    "grws_bcsr_to_coo_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "grws_bcsr_to_coo_count": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.c_int64, _vp,
+                                              ctypes.c_size_t, _c_i64p, _vp]),
+    "grws_bcsr_to_coo_fill": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.c_int64, _vp, _vp,
+                                             _vp, _vp, ctypes.c_size_t, _vp]),
+    "grws_coo_to_csr_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64,
+                                                          ctypes.c_int64]),
+    "grws_coo_to_csr": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64,
+                                       ctypes.c_int64, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "grws_reindex_prune": (ctypes.c_int, [_vp, ctypes.c_int64, _vp, ctypes.c_int32, _vp,
+                                          ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _vp, _vp]),
 }
 
 _lib = None

@@ -9,7 +9,6 @@ from __future__ import annotations
 
 import ctypes
 import os
-import weakref
 from typing import Optional, Tuple
 
 import torch
@@ -65,8 +64,15 @@ def build_spmm_plan(window_offset: torch.Tensor, num_tiles: int, tile_cols: int,
     return SpmmPlan(items, split, list(counts), slabs_per_item)
 
 
-# plans for raw-tensor calls (spmm_tc), keyed weakly on the window_offset tensor
-_plan_cache: "weakref.WeakKeyDictionary[torch.Tensor, dict]" = weakref.WeakKeyDictionary()
+def _tensor_cache(t: torch.Tensor) -> dict:
+    """Per-tensor cache for raw-tensor calls (spmm_tc, spmm_transpose): a
+    dict stored on the window_offset tensor object, so it lives exactly as
+    long as the graph arrays do."""
+    d = getattr(t, "_grws_cache", None)
+    if d is None:
+        d = {}
+        t._grws_cache = d
+    return d
 
 
 def _cached_plan(window_offset: torch.Tensor, col_indices: torch.Tensor, tile_cols: int,
@@ -74,17 +80,13 @@ def _cached_plan(window_offset: torch.Tensor, col_indices: torch.Tensor, tile_co
     num_tiles = col_indices.numel() // tile_cols
     W = window_offset.numel() - 1
     slabs = default_slabs(W, num_tiles, tile_cols, n_cols)
-    key = (window_offset._version, col_indices.data_ptr(), col_indices.numel(), tile_cols, slabs)
-    d = _plan_cache.get(window_offset)
-    if d is None:
-        d = {}
-        _plan_cache[window_offset] = d
-    p = d.get(key)
-    if p is None:
-        d.clear()
-        p = build_spmm_plan(window_offset, num_tiles, tile_cols, slabs)
-        d[key] = p
-    return p
+    key = (window_offset._version, col_indices.numel(), tile_cols, slabs)
+    d = _tensor_cache(window_offset)
+    hit = d.get("plan")
+    if hit is None or hit[0] != key:
+        hit = (key, build_spmm_plan(window_offset, num_tiles, tile_cols, slabs))
+        d["plan"] = hit
+    return hit[1]
 
 
 # ---------------------------------------------------------------------------
@@ -164,6 +166,75 @@ def spmm_tc(window_offset: torch.Tensor, original_col_indices: torch.Tensor,
     e1.record(s)
     e1.synchronize()
     return y, float(e0.elapsed_time(e1))
+
+
+# ---------------------------------------------------------------------------
+# SpMM transpose (backward)
+# ---------------------------------------------------------------------------
+def _cached_transpose(window_offset, col_indices, values, tile_cols: int, num_cols: int):
+    key = (window_offset._version, col_indices.data_ptr(), col_indices._version,
+           values.data_ptr(), values._version, int(num_cols), int(tile_cols))
+    d = _tensor_cache(window_offset)
+    hit = d.get("T")
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    from ..data.bcsr import BCSRGraph
+    W = window_offset.numel() - 1
+    g = BCSRGraph(num_nodes=16 * W, num_edges=0, tile_rows=16, tile_cols=tile_cols,
+                  window_offset=window_offset, original_col_indices=col_indices,
+                  values_condensed=values, device=window_offset.device, num_rows=16 * W,
+                  num_cols=int(num_cols), values_dtype=values.dtype)
+    AT = g.transpose()
+    d["T"] = (key, AT)
+    return AT
+
+
+def spmm_transpose(window_offset: torch.Tensor, original_col_indices: torch.Tensor,
+                   values_condensed: torch.Tensor, grad_out: torch.Tensor, num_cols: int,
+                   tile_cols: int = 8) -> torch.Tensor:
+    """Drop-in for core_lib.spmm_transpose (bind.cpp:133-140,
+    spmm_wrapper.cu:109-152): grad_in[num_cols, D] = A^T grad_out.
+
+    The reference scatters with fp32 atomics (spmm_tc.cuh:211-270); here the
+    BCSR of A^T is built once on the device (cached per graph) and the
+    forward kernel runs over it, so the result is deterministic, exact in
+    int64 index math, and covers every D (no 1e-9 skip, no D > 1024 cut)."""
+    _check_graph(window_offset, original_col_indices, values_condensed, tile_cols)
+    if not grad_out.is_cuda:
+        raise RuntimeError("grad_out must be a CUDA tensor")
+    AT = _cached_transpose(window_offset, original_col_indices, values_condensed, tile_cols,
+                           num_cols)
+    Y = AT.spmm(grad_out.contiguous())
+    n = int(num_cols)
+    if Y.shape[0] >= n:
+        return Y[:n]
+    return torch.nn.functional.pad(Y, (0, 0, 0, n - Y.shape[0]))
+
+
+# ---------------------------------------------------------------------------
+# reindex (model.py:126-141 -> reindex.cuh:33-102)
+# ---------------------------------------------------------------------------
+def reindex_bcsr(col_indices: torch.Tensor, values_condensed: torch.Tensor,
+                 active_windows: torch.Tensor, tile_rows: int = 16,
+                 tile_cols: int = 8) -> torch.Tensor:
+    """Drop-in for core_lib.reindex_bcsr (bind.cpp:153-159): returns the
+    local column ids (new int32 tensor) and prunes `values_condensed` in
+    place where a column's window is not among `active_windows` (sorted)."""
+    if not (col_indices.is_cuda and values_condensed.is_cuda and active_windows.is_cuda):
+        raise RuntimeError("reindex_bcsr: all tensors must be CUDA tensors")
+    if col_indices.dtype != torch.int32 or active_windows.dtype != torch.int32:
+        raise TypeError("reindex_bcsr: col_indices and active_windows must be int32")
+    if not (col_indices.is_contiguous() and values_condensed.is_contiguous()
+            and active_windows.is_contiguous()):
+        raise RuntimeError("reindex_bcsr: tensors must be contiguous")
+    n = col_indices.numel()
+    if n % tile_cols != 0 or values_condensed.numel() != n * tile_rows:
+        raise ValueError("reindex_bcsr: values_condensed must hold tile_rows values per column slot")
+    out = torch.empty_like(col_indices)
+    L.call("grws_reindex_prune", L.ptr(col_indices), n, L.ptr(values_condensed),
+           L.dtype_code(values_condensed.dtype), L.ptr(active_windows), active_windows.numel(),
+           int(tile_rows), int(tile_cols), L.ptr(out), L.stream_of(col_indices.device))
+    return out
 
 
 # ---------------------------------------------------------------------------

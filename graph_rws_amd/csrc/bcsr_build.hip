@@ -1,0 +1,624 @@
+// On-device COO / CSR -> BCSR construction, BCSR -> COO, COO -> CSR (gfx950).
+//
+// Replaces the host-core converter the reference runs on every graph
+// (core/wrapper/convert_wrapper.cpp:27-180, reached from data/bcsr.py:190-234)
+// and the torch COO -> CSR of data/bcsr.py:162-187, and adds the transposed
+// build that the backward pass uses in place of the reference's atomic
+// scatter (core/include/spmm_tc.cuh:211-270).
+//
+// BCSR build, one sort for the whole graph:
+//   key = (window << (cbits + 4)) | (column << 4) | row-in-window, with the
+//   edge value as payload, sorted by the stable LSD radix sort (sort.hip) over
+//   exactly the bits the graph needs.  After the sort every window's edges
+//   are contiguous and column-ascending, so
+//     unique-column flag  = key>>4 differs from the previous key's,
+//     column position     = exclusive scan of those flags,
+//     tiles per window    = ceil(unique columns / tile_cols) -> scan,
+//   and one scatter writes every column slot and value.  Duplicate (row,
+//   column) edges keep input order through the stable sort; the last one
+//   wins, as in the reference's plain store (convert_wrapper.cpp:174).
+// The transposed build swaps the roles of rows and columns in the key.
+#include "grws_internal.h"
+
+namespace grws {
+namespace {
+
+constexpr int kBlk = 256;
+
+enum : int32_t { kErrRow = 1, kErrCol = 2, kErrRowPtr = 4 };
+
+// Bits needed to hold every value in [0, x).
+inline int bits_for(int64_t x) {
+    int b = 0;
+    while (b < 63 && ((int64_t)1 << b) < x) ++b;
+    return b;
+}
+
+inline unsigned grid_for(int64_t n, int64_t per_block = kBlk) {
+    int64_t g = (n + per_block - 1) / per_block;
+    return (unsigned)(g < 1 ? 1 : g);
+}
+
+// Shape of one build, derived identically by the count and fill phases.
+struct BuildShape {
+    int64_t n, R, C, W;  // edges; rows / columns of the built matrix; windows
+    int cbits, wbits, bits;
+};
+
+BuildShape build_shape(int64_t nnz, int64_t num_rows, int64_t num_cols, int32_t transpose) {
+    BuildShape s;
+    s.n = nnz;
+    s.R = transpose ? num_cols : num_rows;
+    s.C = transpose ? num_rows : num_cols;
+    s.W = (s.R + 15) / 16;
+    s.cbits = bits_for(s.C);
+    s.wbits = bits_for(s.W);
+    s.bits = s.wbits + s.cbits + 4;
+    return s;
+}
+
+// Workspace of a build (the fill phase re-derives the same pointers).
+struct BuildWs {
+    uint64_t *ka, *kb;
+    uint32_t *va, *vb;
+    int32_t* uflag;
+    int64_t* uidx;
+    int64_t *wstart, *wend;
+    int32_t* wtiles;
+    int32_t* err;
+    char* sort_ws;
+    size_t sort_bytes;
+    char* scan_ws;
+    size_t scan_bytes;
+};
+
+template <typename C>
+void carve_build(C& cv, const BuildShape& s, BuildWs* w) {
+    const int64_t n = s.n > 0 ? s.n : 1;
+    w->ka = cv.template take<uint64_t>(n);
+    w->kb = cv.template take<uint64_t>(n);
+    w->va = cv.template take<uint32_t>(n);
+    w->vb = cv.template take<uint32_t>(n);
+    w->uflag = cv.template take<int32_t>(n);
+    w->uidx = cv.template take<int64_t>(n + 1);
+    w->wstart = cv.template take<int64_t>(s.W + 1);
+    w->wend = cv.template take<int64_t>(s.W + 1);
+    w->wtiles = cv.template take<int32_t>(s.W + 1);
+    w->err = cv.template take<int32_t>(64);
+    w->sort_bytes = radix_sort_workspace_bytes(n);
+    w->sort_ws = cv.template take<char>(w->sort_bytes);
+    int64_t m = n > s.W ? n : s.W;
+    w->scan_bytes = scan_workspace_bytes(m);
+    w->scan_ws = cv.template take<char>(w->scan_bytes);
+}
+
+struct NullCarver {
+    Sizer s;
+    template <typename T>
+    T* take(size_t k) {
+        s.take<T>(k);
+        return nullptr;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// kernels
+// ---------------------------------------------------------------------------
+__global__ void check_row_ptr_kernel(const int64_t* __restrict__ row_ptr, int64_t num_rows, int64_t nnz,
+                                     int32_t* __restrict__ err) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r > num_rows) return;
+    bool bad = false;
+    if (r == 0) bad = row_ptr[0] != 0;
+    if (r == num_rows) bad = bad || row_ptr[num_rows] != nnz;
+    if (r < num_rows) bad = bad || row_ptr[r + 1] < row_ptr[r];
+    if (bad) atomicOr(err, kErrRowPtr);
+}
+
+// Row of edge e in a CSR: the largest r with row_ptr[r] <= e.
+__device__ __forceinline__ int64_t csr_row_of(const int64_t* __restrict__ row_ptr, int64_t num_rows, int64_t e) {
+    int64_t lo = 0, hi = num_rows - 1;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (row_ptr[mid] <= e) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+__global__ void build_keys_kernel(const int64_t* __restrict__ row_ptr, const int32_t* __restrict__ rows,
+                                  const int32_t* __restrict__ cols, const float* __restrict__ vals, int64_t n,
+                                  int64_t num_rows, int64_t num_cols, int transpose, int cbits,
+                                  uint64_t* __restrict__ keys, uint32_t* __restrict__ pay, int32_t* __restrict__ err) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t r = rows ? (int64_t)rows[i] : csr_row_of(row_ptr, num_rows, i);
+    int64_t c = cols[i];
+    int32_t e = 0;
+    if (r < 0 || r >= num_rows) { e |= kErrRow; r = 0; }
+    if (c < 0 || c >= num_cols) { e |= kErrCol; c = 0; }
+    if (e) atomicOr(err, e);
+    const int64_t wr = transpose ? c : r;
+    const int64_t cc = transpose ? r : c;
+    keys[i] = ((uint64_t)(wr >> 4) << (cbits + 4)) | ((uint64_t)cc << 4) | (uint64_t)(wr & 15);
+    pay[i] = vals ? __float_as_uint(vals[i]) : 0x3f800000u;  // 1.0f when no values are given
+}
+
+__global__ void unique_flag_kernel(const uint64_t* __restrict__ keys, int64_t n, int32_t* __restrict__ uflag) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uflag[i] = (i == 0 || (keys[i] >> 4) != (keys[i - 1] >> 4)) ? 1 : 0;
+}
+
+__global__ void window_bounds_kernel(const uint64_t* __restrict__ keys, int64_t n, int wshift,
+                                     const int32_t* __restrict__ uflag, const int64_t* __restrict__ uidx,
+                                     int64_t* __restrict__ wstart, int64_t* __restrict__ wend) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t w = keys[i] >> wshift;
+    if (i == 0 || (keys[i - 1] >> wshift) != w) wstart[w] = uidx[i];
+    if (i == n - 1 || (keys[i + 1] >> wshift) != w) wend[w] = uidx[i] + uflag[i];
+}
+
+__global__ void window_tiles_kernel(const int64_t* __restrict__ wstart, const int64_t* __restrict__ wend, int64_t W,
+                                    int tc, int32_t* __restrict__ wtiles) {
+    const int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (w >= W) return;
+    const int64_t u = wend[w] - wstart[w];
+    wtiles[w] = (int32_t)((u + tc - 1) / tc);
+}
+
+template <typename VT>
+__device__ __forceinline__ void store_value(void* vals, int64_t idx, float v);
+template <>
+__device__ __forceinline__ void store_value<float>(void* vals, int64_t idx, float v) {
+    static_cast<float*>(vals)[idx] = v;
+}
+template <>
+__device__ __forceinline__ void store_value<_Float16>(void* vals, int64_t idx, float v) {
+    static_cast<_Float16*>(vals)[idx] = (_Float16)v;
+}
+template <>
+__device__ __forceinline__ void store_value<__hip_bfloat16>(void* vals, int64_t idx, float v) {
+    static_cast<__hip_bfloat16*>(vals)[idx] = __float2bfloat16(v);
+}
+
+template <typename VT>
+__global__ void build_scatter_kernel(const uint64_t* __restrict__ keys, const uint32_t* __restrict__ pay, int64_t n,
+                                     int cbits, const int32_t* __restrict__ uflag, const int64_t* __restrict__ uidx,
+                                     const int64_t* __restrict__ wstart, const int64_t* __restrict__ win_off,
+                                     int tc, int32_t* __restrict__ out_cols, void* __restrict__ out_vals) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t k = keys[i];
+    const int wshift = cbits + 4;
+    const int64_t w = (int64_t)(k >> wshift);
+    const int64_t col = (int64_t)((k >> 4) & ((1ull << cbits) - 1ull));
+    const int r = (int)(k & 15u);
+    const int32_t f = uflag[i];
+    const int64_t p = uidx[i] + f - 1 - wstart[w];
+    const int64_t tile = win_off[w] + p / tc;
+    const int c = (int)(p % tc);
+    if (f) out_cols[tile * tc + c] = (int32_t)col;
+    if (i == n - 1 || keys[i + 1] != k) store_value<VT>(out_vals, (tile * 16 + r) * tc + c, __uint_as_float(pay[i]));
+}
+
+// --- BCSR -> COO ---------------------------------------------------------
+template <typename VT>
+__device__ __forceinline__ float load_value(const void* v, int64_t idx);
+template <>
+__device__ __forceinline__ float load_value<float>(const void* v, int64_t idx) {
+    return static_cast<const float*>(v)[idx];
+}
+template <>
+__device__ __forceinline__ float load_value<_Float16>(const void* v, int64_t idx) {
+    return (float)static_cast<const _Float16*>(v)[idx];
+}
+template <>
+__device__ __forceinline__ float load_value<__hip_bfloat16>(const void* v, int64_t idx) {
+    return __bfloat162float(static_cast<const __hip_bfloat16*>(v)[idx]);
+}
+
+// One wave per tile; slot s = lane + 64 j is (row s / tc, column s % tc).
+template <typename VT>
+__global__ __launch_bounds__(256) void tile_nnz_kernel(const int32_t* __restrict__ cols, const void* __restrict__ vals,
+                                                       int64_t T, int tc, int64_t num_cols,
+                                                       int32_t* __restrict__ cnt) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+    if (t >= T) return;
+    const int lane = lane_id();
+    const int per = 16 * tc / kWave;
+    int total = 0;
+    for (int j = 0; j < per; ++j) {
+        const int s = lane + kWave * j;
+        const int c = s % tc;
+        const int64_t col = cols[t * tc + c];
+        const bool v = col >= 0 && col < num_cols && load_value<VT>(vals, t * 16 * tc + s) != 0.0f;
+        total += __popcll(__ballot(v));
+    }
+    if (lane == 0) cnt[t] = total;
+}
+
+template <typename VT>
+__global__ __launch_bounds__(256) void tile_to_coo_kernel(const int64_t* __restrict__ win_off, int64_t W,
+                                                          const int32_t* __restrict__ cols,
+                                                          const void* __restrict__ vals, int64_t T, int tc,
+                                                          int64_t num_cols, const int64_t* __restrict__ toff,
+                                                          int32_t* __restrict__ out_rows,
+                                                          int32_t* __restrict__ out_cols,
+                                                          float* __restrict__ out_vals) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+    if (t >= T) return;
+    const int lane = lane_id();
+    // window of tile t: largest w with win_off[w] <= t
+    int64_t lo = 0, hi = W - 1;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (win_off[mid] <= t) lo = mid;
+        else hi = mid - 1;
+    }
+    const int64_t row0 = lo * 16;
+    const int per = 16 * tc / kWave;
+    int64_t pos = toff[t];
+    for (int j = 0; j < per; ++j) {
+        const int s = lane + kWave * j;
+        const int c = s % tc;
+        const int64_t col = cols[t * tc + c];
+        const float x = load_value<VT>(vals, t * 16 * tc + s);
+        const bool v = col >= 0 && col < num_cols && x != 0.0f;
+        const uint64_t m = __ballot(v);
+        if (v) {
+            const int64_t o = pos + __popcll(m & lanemask_lt());
+            out_rows[o] = (int32_t)(row0 + s / tc);
+            out_cols[o] = (int32_t)col;
+            out_vals[o] = x;
+        }
+        pos += __popcll(m);
+    }
+}
+
+// --- COO -> CSR ------------------------------------------------------------
+__global__ void coo_keys_kernel(const int32_t* __restrict__ src, const int32_t* __restrict__ dst, int64_t n,
+                                int64_t num_rows, int64_t num_cols, int cbits, uint64_t* __restrict__ keys,
+                                uint32_t* __restrict__ pay, int32_t* __restrict__ err) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t r = src[i], c = dst[i];
+    int32_t e = 0;
+    if (r < 0 || r >= num_rows) { e |= kErrRow; r = 0; }
+    if (c < 0 || c >= num_cols) { e |= kErrCol; c = 0; }
+    if (e) atomicOr(err, e);
+    keys[i] = ((uint64_t)r << cbits) | (uint64_t)c;
+    pay[i] = (uint32_t)i;
+}
+
+__global__ void coo_emit_kernel(const uint64_t* __restrict__ keys, const uint32_t* __restrict__ perm, int64_t n,
+                                int cbits, const float* __restrict__ w, int32_t* __restrict__ col_idx,
+                                float* __restrict__ values) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    col_idx[i] = (int32_t)(keys[i] & ((1ull << cbits) - 1ull));
+    values[i] = w ? w[perm[i]] : 1.0f;
+}
+
+// row_ptr[r] = first sorted position whose row is >= r.
+__global__ void coo_row_ptr_kernel(const uint64_t* __restrict__ keys, int64_t n, int cbits, int64_t num_rows,
+                                   int64_t* __restrict__ row_ptr) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r > num_rows) return;
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if ((int64_t)(keys[mid] >> cbits) < r) lo = mid + 1;
+        else hi = mid;
+    }
+    row_ptr[r] = lo;
+}
+
+int read_error_flag(const int32_t* err_dev, hipStream_t stream, int32_t* out) {
+    GRWS_HIP(hipMemcpyAsync(out, err_dev, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+    return GRWS_OK;
+}
+
+int report_input_error(int32_t e, const char* who) {
+    if (e & kErrRowPtr) return set_error(GRWS_E_RANGE, "%s: row_ptr is not a valid CSR row pointer", who);
+    if (e & kErrRow) return set_error(GRWS_E_RANGE, "%s: a row index is out of range", who);
+    if (e & kErrCol) return set_error(GRWS_E_RANGE, "%s: a column index is out of range", who);
+    return GRWS_OK;
+}
+
+}  // namespace
+}  // namespace grws
+
+using namespace grws;
+
+// ---------------------------------------------------------------------------
+// COO / CSR -> BCSR
+// ---------------------------------------------------------------------------
+extern "C" size_t grws_bcsr_build_workspace_bytes(int64_t nnz, int64_t num_rows, int64_t num_cols,
+                                                  int32_t transpose) {
+    if (nnz < 0 || num_rows < 0 || num_cols < 0) return 0;
+    BuildShape s = build_shape(nnz, num_rows, num_cols, transpose);
+    NullCarver nc;
+    BuildWs w;
+    carve_build(nc, s, &w);
+    return nc.s.used + 256;
+}
+
+extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows, const int32_t* cols,
+                                     const float* values, int64_t nnz, int64_t num_rows, int64_t num_cols,
+                                     int32_t tile_cols, int32_t transpose, int64_t* window_offset, void* workspace,
+                                     size_t workspace_bytes, int64_t* num_tiles_out, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(nnz >= 0 && num_rows >= 0 && num_cols >= 0, "bcsr_build: negative size");
+    GRWS_CHECK_ARG(num_rows <= INT32_MAX && num_cols <= INT32_MAX, "bcsr_build: dimensions exceed int32 ids");
+    GRWS_CHECK_ARG(nnz <= (int64_t)UINT32_MAX, "bcsr_build: more than 2^32-1 edges");
+    GRWS_CHECK_ARG(tile_cols == 8 || tile_cols == 16, "bcsr_build: tile_cols must be 8 or 16 (got %d)", tile_cols);
+    GRWS_CHECK_ARG(window_offset && num_tiles_out, "bcsr_build: null output");
+    GRWS_CHECK_ARG((row_ptr != nullptr) != (rows != nullptr), "bcsr_build: pass exactly one of row_ptr and rows");
+    if (nnz > 0) GRWS_CHECK_ARG(cols != nullptr, "bcsr_build: null cols");
+    if (row_ptr) GRWS_CHECK_ARG(num_rows > 0 || nnz == 0, "bcsr_build: edges without rows");
+    BuildShape s = build_shape(nnz, num_rows, num_cols, transpose);
+    Carver cv(workspace, workspace_bytes);
+    BuildWs w;
+    carve_build(cv, s, &w);
+    if (!cv.ok) return set_error(GRWS_E_CAPACITY, "bcsr_build: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+
+    GRWS_TRY(fill_i32(w.err, 1, 0, stream));
+    if (s.W == 0) {
+        GRWS_TRY(fill_i64(window_offset, 1, 0, stream));
+        GRWS_HIP(hipStreamSynchronize(stream));
+        *num_tiles_out = 0;
+        return nnz == 0 ? GRWS_OK : set_error(GRWS_E_RANGE, "bcsr_build: edges in an empty matrix");
+    }
+    GRWS_TRY(fill_i64(w.wstart, s.W, 0, stream));
+    GRWS_TRY(fill_i64(w.wend, s.W, 0, stream));
+    if (row_ptr) {
+        hipLaunchKernelGGL(check_row_ptr_kernel, dim3(grid_for(num_rows + 1)), dim3(kBlk), 0, stream, row_ptr,
+                           num_rows, nnz, w.err);
+        GRWS_LAUNCH_CHECK();
+    }
+    bool alt = false;
+    if (nnz > 0) {
+        hipLaunchKernelGGL(build_keys_kernel, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, row_ptr, rows, cols, values,
+                           nnz, num_rows, num_cols, (int)transpose, s.cbits, w.ka, w.va, w.err);
+        GRWS_LAUNCH_CHECK();
+        GRWS_TRY(radix_sort_pairs(w.ka, w.va, w.kb, w.vb, nnz, s.bits, w.sort_ws, w.sort_bytes, stream, &alt));
+        const uint64_t* k = alt ? w.kb : w.ka;
+        hipLaunchKernelGGL(unique_flag_kernel, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, nnz, w.uflag);
+        GRWS_LAUNCH_CHECK();
+        GRWS_TRY(scan_i32_to_i64(w.uflag, w.uidx, nnz, false, w.scan_ws, w.scan_bytes, stream));
+        hipLaunchKernelGGL(window_bounds_kernel, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, nnz, s.cbits + 4,
+                           w.uflag, w.uidx, w.wstart, w.wend);
+        GRWS_LAUNCH_CHECK();
+    }
+    hipLaunchKernelGGL(window_tiles_kernel, dim3(grid_for(s.W)), dim3(kBlk), 0, stream, w.wstart, w.wend, s.W,
+                       (int)tile_cols, w.wtiles);
+    GRWS_LAUNCH_CHECK();
+    GRWS_TRY(scan_i32_to_i64(w.wtiles, window_offset, s.W, false, w.scan_ws, w.scan_bytes, stream));
+    int64_t T = 0;
+    int32_t e = 0;
+    GRWS_HIP(hipMemcpyAsync(&T, window_offset + s.W, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    GRWS_TRY(read_error_flag(w.err, stream, &e));
+    GRWS_HIP(hipStreamSynchronize(stream));
+    GRWS_TRY(report_input_error(e, "bcsr_build"));
+    *num_tiles_out = T;
+    return GRWS_OK;
+}
+
+extern "C" int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_cols, int32_t tile_cols,
+                                    int32_t transpose, const int64_t* window_offset, int64_t num_tiles,
+                                    int32_t* col_indices, void* values, int32_t values_dtype, void* workspace,
+                                    size_t workspace_bytes, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(nnz >= 0 && num_rows >= 0 && num_cols >= 0 && num_tiles >= 0, "bcsr_build: negative size");
+    GRWS_CHECK_ARG(tile_cols == 8 || tile_cols == 16, "bcsr_build: tile_cols must be 8 or 16 (got %d)", tile_cols);
+    if (values_dtype != GRWS_F32 && values_dtype != GRWS_F16 && values_dtype != GRWS_BF16)
+        return set_error(GRWS_E_DTYPE, "bcsr_build: unsupported values dtype %d", values_dtype);
+    if (num_tiles == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(window_offset && col_indices && values, "bcsr_build: null output");
+    BuildShape s = build_shape(nnz, num_rows, num_cols, transpose);
+    Carver cv(workspace, workspace_bytes);
+    BuildWs w;
+    carve_build(cv, s, &w);
+    if (!cv.ok) return set_error(GRWS_E_CAPACITY, "bcsr_build: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+    const int passes = (s.bits + 7) / 8;
+    const bool alt = nnz > 1 && (passes & 1);
+    const uint64_t* k = alt ? w.kb : w.ka;
+    const uint32_t* v = alt ? w.vb : w.va;
+    GRWS_TRY(fill_i32(col_indices, num_tiles * tile_cols, -1, stream));
+    GRWS_TRY(fill_bytes_zero(values, (size_t)num_tiles * 16 * tile_cols * dtype_size(values_dtype), stream));
+    if (nnz == 0) return GRWS_OK;
+    switch (values_dtype) {
+        case GRWS_F32:
+            hipLaunchKernelGGL(build_scatter_kernel<float>, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, v, nnz,
+                               s.cbits, w.uflag, w.uidx, w.wstart, window_offset, (int)tile_cols, col_indices, values);
+            break;
+        case GRWS_F16:
+            hipLaunchKernelGGL(build_scatter_kernel<_Float16>, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, v, nnz,
+                               s.cbits, w.uflag, w.uidx, w.wstart, window_offset, (int)tile_cols, col_indices, values);
+            break;
+        default:
+            hipLaunchKernelGGL(build_scatter_kernel<__hip_bfloat16>, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, v,
+                               nnz, s.cbits, w.uflag, w.uidx, w.wstart, window_offset, (int)tile_cols, col_indices,
+                               values);
+            break;
+    }
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// BCSR -> COO
+// ---------------------------------------------------------------------------
+extern "C" size_t grws_bcsr_to_coo_workspace_bytes(int64_t num_tiles) {
+    if (num_tiles < 0) return 0;
+    Sizer s;
+    s.take<int32_t>((size_t)num_tiles + 1);
+    s.take<int64_t>((size_t)num_tiles + 2);
+    s.used += scan_workspace_bytes(num_tiles) + 256;
+    return s.used;
+}
+
+static int coo_ws(void* workspace, size_t workspace_bytes, int64_t T, int32_t** cnt, int64_t** toff, char** scan_ws,
+                  size_t* scan_bytes) {
+    Carver cv(workspace, workspace_bytes);
+    *cnt = cv.take<int32_t>(T + 1);
+    *toff = cv.take<int64_t>(T + 2);
+    *scan_bytes = scan_workspace_bytes(T);
+    *scan_ws = cv.take<char>(*scan_bytes);
+    if (!cv.ok) return set_error(GRWS_E_CAPACITY, "bcsr_to_coo: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+    return GRWS_OK;
+}
+
+static int check_bcsr(const grws_bcsr* A, const char* who) {
+    GRWS_CHECK_ARG(A != nullptr, "%s: null graph", who);
+    GRWS_CHECK_ARG(A->tile_rows == 16, "%s: tile_rows must be 16", who);
+    GRWS_CHECK_ARG(A->tile_cols == 8 || A->tile_cols == 16, "%s: tile_cols must be 8 or 16", who);
+    GRWS_CHECK_ARG(A->num_windows >= 0 && A->num_tiles >= 0, "%s: negative size", who);
+    if (A->values_dtype != GRWS_F32 && A->values_dtype != GRWS_F16 && A->values_dtype != GRWS_BF16)
+        return set_error(GRWS_E_DTYPE, "%s: unsupported values dtype %d", who, A->values_dtype);
+    if (A->num_tiles > 0) GRWS_CHECK_ARG(A->window_offset && A->col_indices && A->values, "%s: null arrays", who);
+    GRWS_CHECK_ARG(A->num_windows * 16 <= INT32_MAX, "%s: rows exceed int32 ids", who);
+    return GRWS_OK;
+}
+
+extern "C" int grws_bcsr_to_coo_count(const grws_bcsr* A, int64_t num_cols, void* workspace, size_t workspace_bytes,
+                                      int64_t* nnz_out, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_TRY(check_bcsr(A, "bcsr_to_coo"));
+    GRWS_CHECK_ARG(nnz_out != nullptr && num_cols >= 0, "bcsr_to_coo: bad argument");
+    const int64_t T = A->num_tiles;
+    if (T == 0) {
+        *nnz_out = 0;
+        return GRWS_OK;
+    }
+    int32_t* cnt;
+    int64_t* toff;
+    char* sws;
+    size_t sb;
+    GRWS_TRY(coo_ws(workspace, workspace_bytes, T, &cnt, &toff, &sws, &sb));
+    const unsigned grid = (unsigned)((T + 3) / 4);
+    switch (A->values_dtype) {
+        case GRWS_F32:
+            hipLaunchKernelGGL(tile_nnz_kernel<float>, dim3(grid), dim3(256), 0, stream, A->col_indices, A->values, T,
+                               A->tile_cols, num_cols, cnt);
+            break;
+        case GRWS_F16:
+            hipLaunchKernelGGL(tile_nnz_kernel<_Float16>, dim3(grid), dim3(256), 0, stream, A->col_indices, A->values,
+                               T, A->tile_cols, num_cols, cnt);
+            break;
+        default:
+            hipLaunchKernelGGL(tile_nnz_kernel<__hip_bfloat16>, dim3(grid), dim3(256), 0, stream, A->col_indices,
+                               A->values, T, A->tile_cols, num_cols, cnt);
+            break;
+    }
+    GRWS_LAUNCH_CHECK();
+    GRWS_TRY(scan_i32_to_i64(cnt, toff, T, false, sws, sb, stream));
+    int64_t nnz = 0;
+    GRWS_HIP(hipMemcpyAsync(&nnz, toff + T, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipStreamSynchronize(stream));
+    *nnz_out = nnz;
+    return GRWS_OK;
+}
+
+extern "C" int grws_bcsr_to_coo_fill(const grws_bcsr* A, int64_t num_cols, int32_t* rows, int32_t* cols,
+                                     float* values, void* workspace, size_t workspace_bytes, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_TRY(check_bcsr(A, "bcsr_to_coo"));
+    GRWS_CHECK_ARG(num_cols >= 0, "bcsr_to_coo: negative num_cols");
+    const int64_t T = A->num_tiles;
+    if (T == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(rows && cols && values, "bcsr_to_coo: null output");
+    int32_t* cnt;
+    int64_t* toff;
+    char* sws;
+    size_t sb;
+    GRWS_TRY(coo_ws(workspace, workspace_bytes, T, &cnt, &toff, &sws, &sb));
+    const unsigned grid = (unsigned)((T + 3) / 4);
+    switch (A->values_dtype) {
+        case GRWS_F32:
+            hipLaunchKernelGGL(tile_to_coo_kernel<float>, dim3(grid), dim3(256), 0, stream, A->window_offset,
+                               A->num_windows, A->col_indices, A->values, T, A->tile_cols, num_cols, toff, rows, cols,
+                               values);
+            break;
+        case GRWS_F16:
+            hipLaunchKernelGGL(tile_to_coo_kernel<_Float16>, dim3(grid), dim3(256), 0, stream, A->window_offset,
+                               A->num_windows, A->col_indices, A->values, T, A->tile_cols, num_cols, toff, rows, cols,
+                               values);
+            break;
+        default:
+            hipLaunchKernelGGL(tile_to_coo_kernel<__hip_bfloat16>, dim3(grid), dim3(256), 0, stream, A->window_offset,
+                               A->num_windows, A->col_indices, A->values, T, A->tile_cols, num_cols, toff, rows, cols,
+                               values);
+            break;
+    }
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// COO -> CSR  (data/bcsr.py:162-187)
+// ---------------------------------------------------------------------------
+extern "C" size_t grws_coo_to_csr_workspace_bytes(int64_t nnz, int64_t num_rows, int64_t num_cols) {
+    if (nnz < 0 || num_rows < 0 || num_cols < 0) return 0;
+    const int64_t n = nnz > 0 ? nnz : 1;
+    Sizer s;
+    s.take<uint64_t>(n);
+    s.take<uint64_t>(n);
+    s.take<uint32_t>(n);
+    s.take<uint32_t>(n);
+    s.take<int32_t>(64);
+    s.used += radix_sort_workspace_bytes(n) + 256;
+    return s.used;
+}
+
+extern "C" int grws_coo_to_csr(const int32_t* src, const int32_t* dst, const float* weights, int64_t nnz,
+                               int64_t num_rows, int64_t num_cols, int64_t* row_ptr, int32_t* col_idx, float* values,
+                               void* workspace, size_t workspace_bytes, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(nnz >= 0 && num_rows >= 0 && num_cols >= 0, "coo_to_csr: negative size");
+    GRWS_CHECK_ARG(num_rows <= INT32_MAX && num_cols <= INT32_MAX, "coo_to_csr: dimensions exceed int32 ids");
+    GRWS_CHECK_ARG(nnz <= (int64_t)UINT32_MAX, "coo_to_csr: more than 2^32-1 edges");
+    GRWS_CHECK_ARG(row_ptr != nullptr, "coo_to_csr: null row_ptr");
+    if (nnz > 0) GRWS_CHECK_ARG(src && dst && col_idx && values, "coo_to_csr: null array");
+    const int64_t n = nnz > 0 ? nnz : 1;
+    Carver cv(workspace, workspace_bytes);
+    uint64_t* ka = cv.take<uint64_t>(n);
+    uint64_t* kb = cv.take<uint64_t>(n);
+    uint32_t* va = cv.take<uint32_t>(n);
+    uint32_t* vb = cv.take<uint32_t>(n);
+    int32_t* err = cv.take<int32_t>(64);
+    const size_t sort_bytes = radix_sort_workspace_bytes(n);
+    char* sort_ws = cv.take<char>(sort_bytes);
+    if (!cv.ok) return set_error(GRWS_E_CAPACITY, "coo_to_csr: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+    const int cbits = bits_for(num_cols);
+    const int bits = bits_for(num_rows) + cbits;
+    GRWS_TRY(fill_i32(err, 1, 0, stream));
+    const uint64_t* k = ka;
+    const uint32_t* p = va;
+    if (nnz > 0) {
+        hipLaunchKernelGGL(coo_keys_kernel, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, src, dst, nnz, num_rows,
+                           num_cols, cbits, ka, va, err);
+        GRWS_LAUNCH_CHECK();
+        bool alt = false;
+        GRWS_TRY(radix_sort_pairs(ka, va, kb, vb, nnz, bits, sort_ws, sort_bytes, stream, &alt));
+        k = alt ? kb : ka;
+        p = alt ? vb : va;
+        hipLaunchKernelGGL(coo_emit_kernel, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, p, nnz, cbits, weights,
+                           col_idx, values);
+        GRWS_LAUNCH_CHECK();
+    }
+    hipLaunchKernelGGL(coo_row_ptr_kernel, dim3(grid_for(num_rows + 1)), dim3(kBlk), 0, stream, k, nnz, cbits,
+                       num_rows, row_ptr);
+    GRWS_LAUNCH_CHECK();
+    int32_t e = 0;
+    GRWS_TRY(read_error_flag(err, stream, &e));
+    GRWS_HIP(hipStreamSynchronize(stream));
+    return report_input_error(e, "coo_to_csr");
+}

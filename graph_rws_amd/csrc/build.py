@@ -25,7 +25,10 @@ OBJ_DIR = os.path.join(HERE, "_build")
 SOURCES = [
     "abi.cpp",
     "scan.hip",
+    "sort.hip",
     "spmm.hip",
+    "bcsr_build.hip",
+    "reindex.hip",
 ]
 
 ARCH = os.environ.get("GRWS_OFFLOAD_ARCH", "gfx950")

@@ -168,6 +168,13 @@ int scan_i32_to_i64(const int32_t* in, int64_t* out, int64_t n, bool inclusive, 
 int scan_i64_to_i64(const int64_t* in, int64_t* out, int64_t n, bool inclusive, void* ws,
                     size_t ws_bytes, hipStream_t stream);
 
+// Stable LSD radix sort of (u64 key, u32 payload) pairs over the low `bits`
+// key bits (sort.hip).  The result lands in keys/vals or, when
+// *result_in_alt, in keys_alt/vals_alt.
+size_t radix_sort_workspace_bytes(int64_t n);
+int radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt, int64_t n, int bits,
+                     void* ws, size_t ws_bytes, hipStream_t stream, bool* result_in_alt);
+
 // Fill helpers (plain kernels: safe under graph capture, unlike memset nodes).
 int fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream);
 int fill_i64(int64_t* p, int64_t n, int64_t v, hipStream_t stream);

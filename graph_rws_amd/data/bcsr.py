@@ -55,8 +55,9 @@ class BCSRGraph:
         self.num_windows = int(self.window_offset.shape[0] - 1)
         # set from the array sizes (the reference leaves it None, :62)
         self.num_tiles = int(self.original_col_indices.numel() // self.tile_cols)
-        self._plans: Dict[int, Any] = {}
-        self._transpose: Optional["BCSRGraph"] = None
+        # SpMM plans and the transpose, shared by shallow copies (the model
+        # copies the graph once per layer per forward, model.py:88-96)
+        self._cache: Dict[Any, Any] = {}
 
     # ---------------- constructors (data/bcsr.py:65-159) ----------------
     @classmethod
@@ -142,6 +143,11 @@ class BCSRGraph:
         which misorders rectangular blocks); the sort is stable so duplicate
         edges keep their input order."""
         ncols = max(1, int(num_cols) if num_cols is not None else int(num_rows))
+        from .. import builder
+        if src.is_cuda and builder.available():
+            num_edges, row_ptr, col_idx, values = builder.coo_to_csr_device(
+                int(num_rows), ncols, src, dst, edge_weights)
+            return num_edges, row_ptr.to(device), col_idx.to(device), values.to(device)
         sort_key = src.to(torch.long) * ncols + dst.to(torch.long)
         perm = torch.sort(sort_key, stable=True).indices
         src = src[perm]
@@ -229,21 +235,38 @@ class BCSRGraph:
     def spmm_plan(self, n_cols: int):
         """Cached SpMM schedule for outputs of width n_cols."""
         slabs = default_slabs(self.num_windows, self.num_tiles, self.tile_cols, n_cols)
-        p = self._plans.get(slabs)
+        key = ("plan", slabs, self.window_offset.data_ptr())
+        p = self._cache.get(key)
         if p is None:
             p = build_spmm_plan(self.window_offset, self.num_tiles, self.tile_cols, slabs)
-            self._plans[slabs] = p
+            self._cache[key] = p
         return p
 
     def spmm(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """Y[16W, N] = A x on the device."""
+        """Y[16W, N] = A x on the device (columns >= x.shape[0] contribute nothing)."""
         from ..core import spmm as _spmm
         return _spmm(self.window_offset, self.original_col_indices, self.values_condensed, x,
                      self.tile_cols, plan=self.spmm_plan(x.shape[1]), out=out)
 
     def transpose(self) -> "BCSRGraph":
-        """Cached BCSR of A^T (num_cols x num_rows), built on the device."""
-        if self._transpose is None:
+        """Cached BCSR of A^T (num_cols x 16W), built on the device.  Rebuilt
+        when the column or value arrays are replaced or modified in place."""
+        key = ("T", self.original_col_indices.data_ptr(), self.original_col_indices._version,
+               self.values_condensed.data_ptr(), self.values_condensed._version, self.num_cols)
+        t = self._cache.get("T")
+        if t is None or t[0] != key:
             from .. import builder
-            self._transpose = builder.transpose(self)
-        return self._transpose
+            t = (key, builder.transpose(self))
+            self._cache["T"] = t
+        return t[1]
+
+    def spmm_transpose(self, grad_out: torch.Tensor, num_cols: Optional[int] = None) -> torch.Tensor:
+        """A^T grad_out, [num_cols, D] (core_lib.spmm_transpose semantics,
+        spmm_wrapper.cu:109-152), as a forward SpMM over the cached A^T:
+        deterministic, no atomics.  grad_out: [16W, D]."""
+        n = self.num_cols if num_cols is None else int(num_cols)
+        AT = self.transpose()
+        Y = AT.spmm(grad_out)
+        if Y.shape[0] >= n:
+            return Y[:n]
+        return torch.nn.functional.pad(Y, (0, 0, 0, n - Y.shape[0]))

@@ -1,0 +1,101 @@
+"""BCSR graph convolution with autograd (layers/layer.py:28-191 of the reference).
+
+Same classes, signatures and arithmetic as the reference:
+  forward   H = A (X W)                         (layer.py:38-59)
+  backward  G_agg = A^T dH, dX = G_agg W^T, dW = X^T G_agg   (layer.py:61-92)
+  conv      out = trim(A (X W_neigh)) + X_target W_self      (layer.py:118-191)
+The SpMM runs on the gfx950 kernel (H1); A^T dH runs the same kernel over the
+cached device-built transpose of A instead of the reference's atomic scatter.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.autograd import Function
+
+from ..core import ops as _ops
+from ..helper.timer import record_spmm_time
+
+
+def _spmm_timed(graph, x: torch.Tensor):
+    """graph.spmm with the reference's (output, ms) convention (bind.cpp:124-130)."""
+    if not _ops.TIMING:
+        return graph.spmm(x), 0.0
+    s = torch.cuda.current_stream(x.device)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    y = graph.spmm(x)
+    e1.record(s)
+    e1.synchronize()
+    return y, float(e0.elapsed_time(e1))
+
+
+class BCSRSPMMFunction(Function):
+    """output = A @ (X @ W) with A a BCSRGraph (layer.py:28-92).  Under
+    torch.autocast the backward runs in the forward's autocast state, so a
+    float16/bfloat16 forward has a float16/bfloat16 backward SpMM."""
+
+    @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda")
+    def forward(ctx, graph, features, weight, warps_per_block):
+        x_mult_w = torch.matmul(features, weight)
+        output, timing = _spmm_timed(graph, x_mult_w)
+        record_spmm_time(timing)
+        ctx.save_for_backward(features, weight)
+        ctx.graph = graph
+        ctx.warps_per_block = warps_per_block
+        return output
+
+    @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
+    def backward(ctx, grad_output):
+        features, weight = ctx.saved_tensors
+        graph = ctx.graph
+        num_input_nodes = features.shape[0]
+        grad_input_aggr = graph.spmm_transpose(grad_output.contiguous(), num_input_nodes)
+        grad_features = None
+        grad_weight = None
+        if ctx.needs_input_grad[1]:
+            grad_features = torch.matmul(grad_input_aggr, weight.t())
+        if ctx.needs_input_grad[2]:
+            grad_weight = torch.matmul(features.t(), grad_input_aggr)
+        return None, grad_features, grad_weight, None
+
+
+class BCSRGraphConv(nn.Module):
+    """GraphSAGE-style convolution: neighbour aggregation plus self transform
+    (layer.py:95-191).  `warps_per_block` is kept for API compatibility; the
+    gfx950 kernel chooses its own launch shape."""
+
+    def __init__(self, in_feats: int, out_feats: int, dropout: float = 0.5,
+                 warps_per_block: int = 8):
+        super().__init__()
+        self.in_feats = in_feats
+        self.out_feats = out_feats
+        self.warps_per_block = warps_per_block
+        self.weight_neigh = nn.Parameter(torch.empty(in_feats, out_feats))
+        self.weight_self = nn.Parameter(torch.empty(in_feats, out_feats))
+        self.reset_parameters()
+
+    def reset_parameters(self):
+        nn.init.xavier_uniform_(self.weight_neigh)
+        nn.init.xavier_uniform_(self.weight_self)
+
+    def forward(self, graph, features: torch.Tensor,
+                features_target: torch.Tensor = None) -> torch.Tensor:
+        h_neigh = BCSRSPMMFunction.apply(graph, features, self.weight_neigh, self.warps_per_block)
+        target_rows = h_neigh.shape[0]
+        if features_target is not None:
+            h_in_self = features_target
+        elif features.shape[0] >= target_rows:
+            h_in_self = features[:target_rows]
+        else:
+            h_in_self = F.pad(features, (0, 0, 0, target_rows - features.shape[0]))
+        h_self = torch.matmul(h_in_self, self.weight_self)
+        if h_neigh.shape[0] > h_self.shape[0]:
+            h_neigh = h_neigh[:h_self.shape[0]]
+        elif h_neigh.shape[0] < h_self.shape[0]:
+            h_neigh = F.pad(h_neigh, (0, 0, 0, h_self.shape[0] - h_neigh.shape[0]))
+        return h_neigh + h_self

@@ -1,0 +1,189 @@
+"""GCN_BCSR: the reference's model (models/model.py:13-285) over the gfx950 ops.
+
+L BCSRGraphConv layers (GraphSAGE-style neighbour + self weights), then per
+hidden layer: optional residual, activation, LayerNorm, dropout
+(model.py:212-266).  Graph preparation follows the reference:
+  * layer 0 keeps global column ids and masks -1 / out-of-range columns to
+    column 0 with value 0 (model.py:118-125);
+  * layers > 0 of a sampled stack remap global columns to local ones with
+    reindex_bcsr over the previous layer's active windows (model.py:126-141);
+  * the self path gathers/slices the target rows (_get_residual,
+    model.py:145-210).
+The one change: the layer-0 masking is applied once per graph state instead
+of on every forward (it is idempotent), so the cached SpMM transpose of the
+graph survives from epoch to epoch.
+"""
+from __future__ import annotations
+
+import copy
+from typing import List, Union
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.utils.checkpoint import checkpoint
+
+from ..data import BCSRGraph
+from ..layers import BCSRGraphConv
+
+
+class GCN_BCSR(nn.Module):
+    def __init__(self, in_feats: int, hidden_size: int, num_classes: int, num_layers: int,
+                 dropout: float = 0.5, activation: str = "relu", residual: bool = False,
+                 warps_per_block: int = 8, use_checkpoint: bool = True):
+        super().__init__()
+        if num_layers < 2:
+            raise ValueError("num_layers must be >= 2")
+        self.in_feats = in_feats
+        self.hidden_size = hidden_size
+        self.num_classes = num_classes
+        self.num_layers = num_layers
+        self.dropout = dropout
+        self.residual = residual
+        self.warps_per_block = warps_per_block
+        self.use_checkpoint = use_checkpoint
+        acts = {"relu": F.relu, "elu": F.elu, "gelu": F.gelu}
+        if activation not in acts:
+            raise ValueError(f"Unsupported activation: {activation}")
+        self.activation = acts[activation]
+        dims = [in_feats] + [hidden_size] * (num_layers - 1) + [num_classes]
+        self.layers = nn.ModuleList(
+            BCSRGraphConv(dims[i], dims[i + 1], warps_per_block=warps_per_block)
+            for i in range(num_layers))
+        self.dropout_layer = nn.Dropout(dropout) if dropout > 0 else None
+        self.norms = nn.ModuleList(nn.LayerNorm(hidden_size) for _ in range(num_layers - 1))
+        if residual:
+            self.residual_projs = nn.ModuleList()
+            for i in range(num_layers - 1):
+                d_in = in_feats if i == 0 else hidden_size
+                self.residual_projs.append(
+                    nn.Linear(d_in, hidden_size, bias=False) if d_in != hidden_size else None)
+        else:
+            self.residual_projs = None
+        self._init_parameters()
+
+    def _init_parameters(self):
+        for layer in self.layers:
+            layer.reset_parameters()
+        if self.residual_projs is not None:
+            for proj in self.residual_projs:
+                if proj is not None:
+                    nn.init.kaiming_uniform_(proj.weight, nonlinearity="relu")
+        for norm in self.norms:
+            norm.reset_parameters()
+
+    # ---------------- graph preparation (model.py:88-143) ----------------
+    def _ensure_graph_list(self, graphs: Union[BCSRGraph, List[BCSRGraph]]) -> List[BCSRGraph]:
+        if isinstance(graphs, BCSRGraph):
+            return [copy.copy(graphs) for _ in range(len(self.layers))]
+        if isinstance(graphs, list):
+            if len(graphs) != len(self.layers):
+                raise ValueError("need one graph per layer")
+            return graphs
+        raise TypeError(f"graphs must be BCSRGraph or List[BCSRGraph], got {type(graphs)}")
+
+    @staticmethod
+    def _mask_global_columns(g, num_in: int) -> None:
+        """-1 and columns >= num_in become column 0 with value 0, in place
+        (model.py:118-125).  Skipped when this graph state was masked already."""
+        cols, vals = g.original_col_indices, g.values_condensed
+        key = (cols.data_ptr(), cols._version, vals.data_ptr(), vals._version, int(num_in))
+        if g._cache.get("masked") == key:
+            return
+        bad = (cols == -1) | (cols >= num_in)
+        cols.masked_fill_(bad, 0)
+        mask = bad.view(-1, g.tile_cols).unsqueeze(1).expand(-1, g.tile_rows, -1).reshape(-1)
+        vals.view(-1).masked_fill_(mask, 0.0)
+        g._cache["masked"] = (cols.data_ptr(), cols._version, vals.data_ptr(), vals._version,
+                              int(num_in))
+
+    def _sanitize_and_reindex(self, layer_idx, curr_g, prev_g, h_in_shape):
+        if getattr(curr_g, "is_local_input", False):
+            curr_g.num_cols = h_in_shape[0]
+            return
+        fwd_g = getattr(curr_g, "fwd", curr_g)
+        if layer_idx == 0:
+            self._mask_global_columns(fwd_g, h_in_shape[0])
+        else:
+            if getattr(prev_g, "active_windows", None) is not None:
+                from ..core import reindex_bcsr
+                fwd_g.original_col_indices = reindex_bcsr(
+                    fwd_g.original_col_indices, fwd_g.values_condensed, prev_g.active_windows,
+                    fwd_g.tile_rows, fwd_g.tile_cols)
+            fwd_g.num_cols = h_in_shape[0]
+
+    def _get_residual(self, layer_idx, curr_g, prev_g, h_in, target_rows):
+        """Rows of h_in aligned with the current layer's output rows
+        (model.py:145-210)."""
+        if h_in.shape[0] == target_rows:
+            return h_in
+        device = h_in.device
+        aw = getattr(curr_g, "active_windows", None)
+        if layer_idx == 0:
+            if getattr(curr_g, "is_local_input", False):
+                return torch.zeros((target_rows, h_in.shape[1]), device=device, dtype=h_in.dtype)
+            if aw is None:
+                if target_rows > h_in.shape[0]:
+                    return F.pad(h_in, (0, 0, 0, target_rows - h_in.shape[0]))
+                return h_in[:target_rows]
+            t = curr_g.tile_rows
+            idx = (aw.unsqueeze(1).long() * t + torch.arange(t, device=device).unsqueeze(0)).view(-1)
+            valid = idx < h_in.shape[0]
+            res = h_in[torch.where(valid, idx, torch.zeros_like(idx))]
+            return res.masked_fill((~valid).unsqueeze(1), 0.0)
+        if aw is not None:
+            t = curr_g.tile_rows
+            prev_w = prev_g.active_windows
+            wi = torch.searchsorted(prev_w, aw).clamp(0, max(0, prev_w.numel() - 1))
+            idx = (wi.unsqueeze(1) * t + torch.arange(t, device=device).unsqueeze(0)).view(-1)
+            return h_in[idx]
+        if target_rows > h_in.shape[0]:
+            return F.pad(h_in, (0, 0, 0, target_rows - h_in.shape[0]))
+        return h_in[:target_rows]
+
+    # ---------------- forward (model.py:212-266) ----------------
+    def forward(self, graphs: Union[BCSRGraph, List[BCSRGraph]], features: torch.Tensor) -> torch.Tensor:
+        if features.device.type != "cuda":
+            features = features.to("cuda", non_blocking=True)
+        graph_list = self._ensure_graph_list(graphs)
+        h = features
+        for l, (layer, g) in enumerate(zip(self.layers, graph_list)):
+            prev_g = graph_list[l - 1] if l > 0 else None
+            self._sanitize_and_reindex(l, g, prev_g, h.shape)
+            h_target = self._get_residual(l, g, prev_g, h, g.num_rows)
+
+            def run(h_curr, layer=layer, g=g, h_tgt=h_target):
+                return layer(g, h_curr, features_target=h_tgt)
+
+            if self.use_checkpoint and self.training and h.requires_grad:
+                h_out = checkpoint(run, h, use_reentrant=False)
+            else:
+                h_out = run(h)
+            if self.residual and l < len(self.layers) - 1:
+                h_res = h
+                proj = self.residual_projs[l] if self.residual_projs is not None else None
+                if proj is not None:
+                    h_res = proj(h_res)
+                h_out = h_out + self._get_residual(l, g, prev_g, h_res, h_out.shape[0])
+            h = h_out
+            if l < len(self.layers) - 1:
+                h = self.activation(h)
+                h = self.norms[l](h)
+                if self.dropout_layer is not None:
+                    h = self.dropout_layer(h)
+        return h
+
+    @torch.no_grad()
+    def inference(self, graph: BCSRGraph, features: torch.Tensor, batch_size: int = 0) -> torch.Tensor:
+        """Full-graph inference (model.py:268-285)."""
+        if features.device.type != "cuda":
+            features = features.to("cuda", non_blocking=True)
+        h = features
+        g = copy.copy(graph)
+        self._sanitize_and_reindex(0, g, None, h.shape)
+        for l, layer in enumerate(self.layers):
+            h = layer(g, h)
+            if l < len(self.layers) - 1:
+                h = self.activation(h)
+                h = self.norms[l](h)
+        return h

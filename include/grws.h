@@ -150,6 +150,73 @@ int grws_csr_to_bcsr_host_fill(int64_t num_rows, const int64_t* row_ptr, const i
                                const int64_t* window_offset, int32_t* col_indices,
                                float* out_values, int32_t num_threads);
 
+/* ------------------------------------------------------------------------ */
+/* On-device BCSR build.  Replaces core_lib.csr_to_bcsr_cpu on device        */
+/* graphs (bind.cpp:143-150 -> convert_wrapper.cpp:27-180, called from       */
+/* data/bcsr.py:190-234): identical window_offset / col_indices / values,    */
+/* identical "last duplicate in input order wins" rule.  With transpose != 0 */
+/* it builds the BCSR of A^T instead (windows over A's columns), the cached  */
+/* transpose the backward pass runs on in place of the reference's atomic    */
+/* scatter (spmm_tc.cuh:211-270).  Device pointers.                          */
+/* ------------------------------------------------------------------------ */
+
+/* Workspace bytes of one build (count + fill share it). */
+size_t grws_bcsr_build_workspace_bytes(int64_t nnz, int64_t num_rows, int64_t num_cols,
+                                       int32_t transpose);
+
+/*
+ * Phase 1.  Edges of A [num_rows x num_cols] given either as CSR (row_ptr
+ * [num_rows+1], rows NULL) or as COO (rows [nnz], row_ptr NULL); cols [nnz];
+ * values [nnz] float32 or NULL (all ones).  Writes window_offset
+ * [ceil(R/16)+1] (R = num_rows, or num_cols when transposed), synchronises
+ * `stream` and returns the tile count in *num_tiles_out.  GRWS_E_RANGE when a
+ * row or column is out of range or row_ptr is not a CSR row pointer.
+ */
+int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows, const int32_t* cols,
+                          const float* values, int64_t nnz, int64_t num_rows, int64_t num_cols,
+                          int32_t tile_cols, int32_t transpose, int64_t* window_offset,
+                          void* workspace, size_t workspace_bytes, int64_t* num_tiles_out,
+                          void* stream);
+
+/* Phase 2.  Same sizes and the workspace phase 1 left (unmodified); fills
+ * col_indices [num_tiles*tile_cols] (-1 padding) and values
+ * [num_tiles*16*tile_cols] of values_dtype (round to nearest even). */
+int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_cols, int32_t tile_cols,
+                         int32_t transpose, const int64_t* window_offset, int64_t num_tiles,
+                         int32_t* col_indices, void* values, int32_t values_dtype,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* BCSR -> COO: every slot with a column in [0, num_cols) and a non-zero
+ * value becomes one edge (row = 16*window + row in tile).  Feeds the
+ * transposed build of a graph that exists only as BCSR (sampled subgraphs,
+ * from_components).  count synchronises `stream`. */
+size_t grws_bcsr_to_coo_workspace_bytes(int64_t num_tiles);
+int grws_bcsr_to_coo_count(const grws_bcsr* A, int64_t num_cols, void* workspace,
+                           size_t workspace_bytes, int64_t* nnz_out, void* stream);
+int grws_bcsr_to_coo_fill(const grws_bcsr* A, int64_t num_cols, int32_t* rows, int32_t* cols,
+                          float* values, void* workspace, size_t workspace_bytes, void* stream);
+
+/* COO -> CSR, replacing BCSRGraph._coo_to_csr (data/bcsr.py:162-187):
+ * stable sort by (src, dst) (the reference sorts on src*num_rows+dst with a
+ * non-stable argsort, :170-171), row_ptr int64 [num_rows+1], col_idx = dst,
+ * values = weights in sorted order or ones.  Synchronises `stream`. */
+size_t grws_coo_to_csr_workspace_bytes(int64_t nnz, int64_t num_rows, int64_t num_cols);
+int grws_coo_to_csr(const int32_t* src, const int32_t* dst, const float* weights, int64_t nnz,
+                    int64_t num_rows, int64_t num_cols, int64_t* row_ptr, int32_t* col_idx,
+                    float* values, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Reindex + prune.  Replaces core_lib.reindex_bcsr (bind.cpp:153-159 ->     */
+/* reindex_wrapper.cu:27-68, kernel reindex.cuh:33-102): out_cols[i] =       */
+/* pos * tile_rows + g % tile_rows where pos is the index of window          */
+/* g / tile_rows (C division) in the sorted active_windows; a slot whose     */
+/* window is absent gets column 0 and its tile_rows values are zeroed IN     */
+/* PLACE in `values` ([num_indices / tile_cols][tile_rows][tile_cols]).      */
+/* ------------------------------------------------------------------------ */
+int grws_reindex_prune(const int32_t* in_cols, int64_t num_indices, void* values,
+                       int32_t values_dtype, const int32_t* active_windows, int64_t num_active,
+                       int32_t tile_rows, int32_t tile_cols, int32_t* out_cols, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,207 @@
+"""Device BCSR build (COO/CSR -> BCSR, transpose, COO -> CSR) and reindex on
+the GPU.  Integer and index results must be bit-exact against the oracle /
+host converter; float32 values are moved, never computed, so they are
+bit-exact too; float16/bfloat16 values equal torch's round-to-nearest-even
+cast of the float32 values."""
+import numpy as np
+import pytest
+import scipy.sparse as sps
+import torch
+
+import oracle
+from graph_rws_amd import builder, core, synth
+from graph_rws_amd.core._lib import GrwsError
+
+pytestmark = pytest.mark.gpu
+
+
+def _host(g, tc):
+    return core.csr_to_bcsr_cpu(g.num_nodes, g.row_ptr, g.col_idx, g.values, 16, tc)
+
+
+def _eq(a, b):
+    assert torch.equal(a.cpu(), b.cpu())
+
+
+GRAPHS = {
+    "random": lambda: synth.random_graph(777, 11.0, seed=3),
+    "powerlaw": lambda: synth.chung_lu(5000, 80000, 2.1, seed=4),
+    "tiny": lambda: synth.random_graph(5, 2.0, seed=1),
+}
+
+
+@pytest.mark.parametrize("name", list(GRAPHS))
+@pytest.mark.parametrize("tc", [8, 16])
+@pytest.mark.parametrize("vdt", [torch.float32, torch.float16, torch.bfloat16])
+def test_csr_build_matches_host_converter(cuda_device, name, tc, vdt):
+    print(f"case build {name} tc={tc} {vdt}", flush=True)
+    g = GRAPHS[name]()
+    hw, hc, hv = _host(g, tc)
+    dw, dc, dv = builder.csr_to_bcsr_device(g.num_nodes, g.num_nodes, g.row_ptr.to(cuda_device),
+                                            g.col_idx.to(cuda_device), g.values.to(cuda_device),
+                                            tile_cols=tc, values_dtype=vdt)
+    torch.cuda.synchronize()
+    _eq(dw, hw)
+    _eq(dc, hc)
+    assert dv.dtype == vdt
+    _eq(dv, hv.to(vdt))
+
+
+def test_coo_build_duplicates_last_wins(cuda_device):
+    """Duplicate (row, col) edges: the last in input order wins
+    (convert_wrapper.cpp:174), as in the oracle's restatement."""
+    print("case duplicates", flush=True)
+    rng = np.random.default_rng(11)
+    n = 300
+    rows = rng.integers(0, n, 6000).astype(np.int32)
+    cols = rng.integers(0, n, 6000).astype(np.int32)
+    vals = rng.standard_normal(6000).astype(np.float32)
+    # CSR in input order within each row (stable by row) = the oracle's CSR order
+    order = np.argsort(rows, kind="stable")
+    rp = np.zeros(n + 1, np.int64)
+    np.add.at(rp, rows + 1, 1)
+    rp = np.cumsum(rp)
+    ow, oc, ov = oracle.csr_to_bcsr(n, rp, cols[order], vals[order], 16, 16)
+    dw, dc, dv = builder.coo_to_bcsr_device(n, n, torch.from_numpy(rows).to(cuda_device),
+                                            torch.from_numpy(cols).to(cuda_device),
+                                            torch.from_numpy(vals).to(cuda_device), tile_cols=16)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dw.cpu().numpy(), ow)
+    np.testing.assert_array_equal(dc.cpu().numpy(), oc)
+    np.testing.assert_array_equal(dv.cpu().numpy(), ov.astype(np.float32))
+
+
+def test_rectangular_and_empty(cuda_device):
+    print("case rectangular", flush=True)
+    # 37 rows x 1000 cols, rows 0..15 empty
+    rng = np.random.default_rng(2)
+    rows = rng.integers(16, 37, 400).astype(np.int32)
+    cols = rng.integers(0, 1000, 400).astype(np.int32)
+    vals = np.ones(400, np.float32)
+    order = np.argsort(rows, kind="stable")
+    rp = np.zeros(38, np.int64)
+    np.add.at(rp, rows + 1, 1)
+    rp = np.cumsum(rp)
+    ow, oc, ov = oracle.csr_to_bcsr(37, rp, cols[order], vals[order], 16, 8)
+    dw, dc, dv = builder.csr_to_bcsr_device(37, 1000, torch.from_numpy(rp).to(cuda_device),
+                                            torch.from_numpy(cols[order]).to(cuda_device),
+                                            torch.from_numpy(vals[order]).to(cuda_device), tile_cols=8)
+    np.testing.assert_array_equal(dw.cpu().numpy(), ow)
+    np.testing.assert_array_equal(dc.cpu().numpy(), oc)
+    assert ow[1] == 0  # first window empty
+    # no edges at all
+    rp0 = torch.zeros(21, dtype=torch.int64, device=cuda_device)
+    ew, ec, ev = builder.csr_to_bcsr_device(20, 20, rp0, torch.empty(0, dtype=torch.int32, device=cuda_device),
+                                            None, tile_cols=16)
+    assert ew.cpu().tolist() == [0, 0, 0] and ec.numel() == 0 and ev.numel() == 0
+
+
+def test_build_rejects_out_of_range(cuda_device):
+    print("case build errors", flush=True)
+    rp = torch.tensor([0, 2, 3], dtype=torch.int64, device=cuda_device)
+    ci = torch.tensor([0, 5, 1], dtype=torch.int32, device=cuda_device)
+    with pytest.raises(GrwsError, match="column index is out of range"):
+        builder.csr_to_bcsr_device(2, 4, rp, ci, None, tile_cols=8)
+    bad = torch.tensor([0, 3, 2], dtype=torch.int64, device=cuda_device)
+    with pytest.raises(GrwsError, match="row_ptr"):
+        builder.csr_to_bcsr_device(2, 4, bad, ci.clamp(max=3), None, tile_cols=8)
+
+
+def test_coo_to_csr_matches_stable_sort(cuda_device):
+    print("case coo_to_csr", flush=True)
+    rng = np.random.default_rng(5)
+    n_r, n_c, m = 500, 900, 20000
+    src = rng.integers(0, n_r, m).astype(np.int32)
+    dst = rng.integers(0, n_c, m).astype(np.int32)
+    w = rng.standard_normal(m).astype(np.float32)
+    E, rp, ci, va = builder.coo_to_csr_device(n_r, n_c, torch.from_numpy(src).to(cuda_device),
+                                              torch.from_numpy(dst).to(cuda_device),
+                                              torch.from_numpy(w).to(cuda_device))
+    order = np.lexsort((dst, src))  # stable: by src, then dst, ties in input order
+    exp_rp = np.concatenate([[0], np.cumsum(np.bincount(src, minlength=n_r))])
+    assert E == m
+    np.testing.assert_array_equal(rp.cpu().numpy(), exp_rp)
+    np.testing.assert_array_equal(ci.cpu().numpy(), dst[order])
+    np.testing.assert_array_equal(va.cpu().numpy(), w[order])
+
+
+@pytest.mark.parametrize("tc", [8, 16])
+def test_transpose_matches_host_build_of_transpose(cuda_device, tc):
+    """BCSR(A^T) built from BCSR(A) on the device equals the host converter
+    run on scipy's CSR transpose."""
+    print(f"case transpose tc={tc}", flush=True)
+    g = synth.chung_lu(3000, 50000, 2.1, seed=8)
+    n = g.num_nodes
+    hw, hc, hv = _host(g, tc)
+    tw, tcol, tv = builder.transpose_arrays(hw.to(cuda_device), hc.to(cuda_device),
+                                            hv.to(cuda_device), tc, n)
+    W = hw.numel() - 1
+    A = sps.csr_matrix((g.values.numpy(), g.col_idx.numpy(), g.row_ptr.numpy()), shape=(n, n))
+    AT = A.T.tocsr()
+    AT.sort_indices()
+    ew, ec, ev = core.csr_to_bcsr_cpu(n, torch.from_numpy(AT.indptr.astype(np.int64)),
+                                      torch.from_numpy(AT.indices.astype(np.int32)),
+                                      torch.from_numpy(AT.data.astype(np.float32)), 16, tc)
+    _eq(tw, ew)
+    _eq(tcol, ec)
+    _eq(tv, ev)
+    assert W * 16 >= n
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+def test_spmm_transpose_parity(cuda_device, xdt):
+    """A^T G through the cached transpose against the float64 oracle
+    (spmm_tc.cuh:238-269 semantics), rtol 1e-5 (f32) / 1e-2 (f16, bf16)."""
+    print(f"case spmm_transpose {xdt}", flush=True)
+    rtol = 1e-5 if xdt == torch.float32 else 1e-2
+    g = synth.chung_lu(2000, 30000, 2.1, seed=9)
+    for tc in (8, 16):
+        w, c, v = _host(g, tc)
+        w, c = w.to(cuda_device), c.to(cuda_device)
+        v = v.to(cuda_device).to(xdt)
+        W = w.numel() - 1
+        G = synth.features(16 * W, 72, seed=3, device=cuda_device).to(xdt)
+        out = core.spmm_transpose(w, c, v, G, g.num_nodes, tile_cols=tc)
+        out2 = core.spmm_transpose(w, c, v, G, g.num_nodes, tile_cols=tc)
+        torch.cuda.synchronize()
+        assert out.shape == (g.num_nodes, 72)
+        assert torch.equal(out.view(-1).view(torch.int16 if xdt != torch.float32 else torch.int32),
+                           out2.view(-1).view(torch.int16 if xdt != torch.float32 else torch.int32))
+        ref, refa = oracle.bcsr_spmm_t(w.cpu().numpy(), c.cpu().numpy(), v.double().cpu().numpy(),
+                                       16, tc, G.double().cpu().numpy(), g.num_nodes)
+        err = np.abs(out.double().cpu().numpy() - ref)
+        assert np.all(err <= rtol * refa), f"max excess {(err - rtol * refa).max():.3e}"
+
+
+@pytest.mark.parametrize("vdt", [torch.float32, torch.float16])
+def test_reindex_matches_oracle(cuda_device, vdt):
+    print(f"case reindex {vdt}", flush=True)
+    rng = np.random.default_rng(13)
+    tc, ntiles = 8, 500
+    cols = rng.integers(-1, 4000, ntiles * tc).astype(np.int32)
+    cols[::17] = -1
+    vals = rng.standard_normal(ntiles * 16 * tc).astype(np.float32)
+    vals = torch.from_numpy(vals).to(vdt).float().numpy()  # representable in vdt
+    for active in (np.unique(rng.integers(0, 250, 90)).astype(np.int32),
+                   np.unique(np.concatenate([[0], rng.integers(1, 250, 60)])).astype(np.int32),
+                   np.zeros(0, np.int32)):
+        oc, ov = oracle.reindex_prune(cols, vals, active, 16, tc)
+        dv = torch.from_numpy(vals).to(cuda_device).to(vdt)
+        out = core.reindex_bcsr(torch.from_numpy(cols).to(cuda_device), dv,
+                                torch.from_numpy(active).to(cuda_device), 16, tc)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy(), oc)
+        np.testing.assert_array_equal(dv.float().cpu().numpy(), ov)
+
+
+def test_build_c2_full_size(cuda_device):
+    """BASELINE config c2 through the device builder equals the host converter."""
+    print("case c2 build", flush=True)
+    g = synth.config_graph("c2")
+    hw, hc, hv = _host(g, 16)
+    dw, dc, dv = builder.csr_to_bcsr_device(g.num_nodes, g.num_nodes, g.row_ptr.to(cuda_device),
+                                            g.col_idx.to(cuda_device), g.values.to(cuda_device),
+                                            tile_cols=16)
+    _eq(dw, hw)
+    _eq(dc, hc)
+    _eq(dv, hv)
