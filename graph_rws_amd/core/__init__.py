@@ -10,6 +10,8 @@ from .ops import (  # noqa: F401
     csr_to_bcsr_cpu,
     default_slabs,
     reindex_bcsr,
+    relabel,
+    sample_hop,
     spmm,
     spmm_tc,
     spmm_transpose,
@@ -34,4 +36,6 @@ __all__ = [
     "spmm",
     "build_spmm_plan",
     "SpmmPlan",
+    "sample_hop",
+    "relabel",
 ]

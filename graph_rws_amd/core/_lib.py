@@ -76,6 +76,14 @@ _PROTOS = {
                                        ctypes.c_int64, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "grws_reindex_prune": (ctypes.c_int, [_vp, ctypes.c_int64, _vp, ctypes.c_int32, _vp,
                                           ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _vp, _vp]),
+    "grws_sample_hop_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "grws_sample_hop": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp,
+                                       ctypes.c_int64, ctypes.c_int32, ctypes.c_uint64, _vp, _vp,
+                                       _vp, ctypes.c_int64, _vp, ctypes.c_size_t, _c_i64p, _vp]),
+    "grws_relabel_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
+    "grws_relabel": (ctypes.c_int, [_vp, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int64,
+                                    _vp, _vp, ctypes.c_int64, _vp, ctypes.c_size_t, _c_i64p,
+                                    _vp]),
 }
 
 _lib = None

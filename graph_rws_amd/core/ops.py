@@ -275,3 +275,59 @@ def csr_to_bcsr_cpu(num_rows: int, row_ptr: torch.Tensor, col_idx: torch.Tensor,
     L.call("grws_csr_to_bcsr_host_fill", num_rows, L.ptr(rp), L.ptr(ci), L.ptr(va), tile_rows,
            tile_cols, L.ptr(win), L.ptr(cols), L.ptr(vals), num_threads)
     return win, cols, vals
+
+
+# ---------------------------------------------------------------------------
+# node-wise fanout sampling + relabel (csrc/sample.hip)
+# ---------------------------------------------------------------------------
+def _csr_arrays(indptr: torch.Tensor, indices: torch.Tensor):
+    if not (indptr.is_cuda and indices.is_cuda):
+        raise RuntimeError("indptr and indices must be CUDA tensors")
+    if indptr.dtype != torch.int64 or indices.dtype != torch.int32:
+        raise TypeError("indptr must be int64 and indices int32")
+    if not (indptr.is_contiguous() and indices.is_contiguous()):
+        raise RuntimeError("indptr and indices must be contiguous")
+    return indptr.numel() - 1, indices.numel()
+
+
+def sample_hop(indptr: torch.Tensor, indices: torch.Tensor, frontier: torch.Tensor, fanout: int,
+               seed: int = 42, with_values: bool = True):
+    """One hop of node-wise sampling without replacement (Floyd over a
+    Philox4x32-10 stream keyed by (seed, node, draw)).  Returns
+    (edge_dst int32 [E] frontier positions, edge_src int64 [E] global ids,
+    edge_val float32 [E] GCN weights or None), in frontier order then
+    ascending CSR position.  One stream sync (the edge count)."""
+    n, nnz = _csr_arrays(indptr, indices)
+    dev = indptr.device
+    fr = frontier.to(dev, torch.int64).contiguous()
+    F = fr.numel()
+    cap = max(1, F * int(fanout))
+    dst = torch.empty(cap, dtype=torch.int32, device=dev)
+    src = torch.empty(cap, dtype=torch.int64, device=dev)
+    val = torch.empty(cap, dtype=torch.float32, device=dev) if with_values else None
+    wsb = int(L.load().grws_sample_hop_workspace_bytes(F))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    E = ctypes.c_int64()
+    L.call("grws_sample_hop", L.ptr(indptr), L.ptr(indices), n, nnz, L.ptr(fr), F, int(fanout),
+           ctypes.c_uint64(int(seed) & 0xFFFFFFFFFFFFFFFF), L.ptr(dst), L.ptr(src), L.ptr(val), cap,
+           L.ptr(ws), wsb, ctypes.byref(E), L.stream_of(dev))
+    E = E.value
+    return dst[:E], src[:E], (val[:E] if val is not None else None)
+
+
+def relabel(frontier: torch.Tensor, edge_src: torch.Tensor, num_nodes: int):
+    """Unique + relabel: frontier ids keep local ids [0, F); new source ids
+    follow in ascending global id.  Returns (src_local int32 [E],
+    next_frontier int64 [num_src]).  One stream sync."""
+    dev = edge_src.device
+    fr = frontier.to(dev, torch.int64).contiguous()
+    es = edge_src.to(torch.int64).contiguous()
+    F, E = fr.numel(), es.numel()
+    src_local = torch.empty(max(E, 1), dtype=torch.int32, device=dev)
+    nxt = torch.empty(max(F + E, 1), dtype=torch.int64, device=dev)
+    wsb = int(L.load().grws_relabel_workspace_bytes(F, E))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    ns = ctypes.c_int64()
+    L.call("grws_relabel", L.ptr(fr), F, L.ptr(es), E, int(num_nodes), L.ptr(src_local),
+           L.ptr(nxt), max(F + E, 1), L.ptr(ws), wsb, ctypes.byref(ns), L.stream_of(dev))
+    return src_local[:E], nxt[:ns.value]

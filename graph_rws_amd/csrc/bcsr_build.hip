@@ -356,7 +356,8 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
     GRWS_CHECK_ARG(nnz <= (int64_t)UINT32_MAX, "bcsr_build: more than 2^32-1 edges");
     GRWS_CHECK_ARG(tile_cols == 8 || tile_cols == 16, "bcsr_build: tile_cols must be 8 or 16 (got %d)", tile_cols);
     GRWS_CHECK_ARG(window_offset && num_tiles_out, "bcsr_build: null output");
-    GRWS_CHECK_ARG((row_ptr != nullptr) != (rows != nullptr), "bcsr_build: pass exactly one of row_ptr and rows");
+    GRWS_CHECK_ARG(row_ptr == nullptr || rows == nullptr, "bcsr_build: pass only one of row_ptr and rows");
+    if (nnz > 0) GRWS_CHECK_ARG(row_ptr != nullptr || rows != nullptr, "bcsr_build: pass row_ptr or rows");
     if (nnz > 0) GRWS_CHECK_ARG(cols != nullptr, "bcsr_build: null cols");
     if (row_ptr) GRWS_CHECK_ARG(num_rows > 0 || nnz == 0, "bcsr_build: edges without rows");
     BuildShape s = build_shape(nnz, num_rows, num_cols, transpose);

@@ -29,6 +29,7 @@ SOURCES = [
     "spmm.hip",
     "bcsr_build.hip",
     "reindex.hip",
+    "sample.hip",
 ]
 
 ARCH = os.environ.get("GRWS_OFFLOAD_ARCH", "gfx950")

@@ -1,0 +1,106 @@
+"""Node-wise fanout sampler on MI355X: Philox draws, unique + relabel, and a
+BCSR block per hop.
+
+Returns the same ``List[BCSRGraph]`` the reference's
+``BCSRSampler.sample_layers`` returns (sampler/sampler.py:186-279): one
+graph per model layer, input side first, hop 0 (from the seeds) drawn with
+the LAST fanout as the reference does (``reversed(fanouts)``,
+sampler.py:204).  Each graph is a message-flow block in the layout of
+``BCSRGraph.from_dgl_block`` (data/bcsr.py:266-306): rows are the hop's
+destination nodes, columns its source nodes, and the destination nodes are
+the first columns ("target-top", layers/layer.py:159-161), so a layer's
+self path is ``features[:num_rows]``.
+
+Per hop, on the device (csrc/sample.hip, csrc/bcsr_build.hip):
+  1. grws_sample_hop  -- min(deg, k) distinct neighbours per frontier node,
+                         Floyd over Philox4x32-10(seed, node, draw);
+  2. grws_relabel     -- frontier keeps [0, F), new sources appended in
+                         ascending global id; the next frontier;
+  3. BCSR build       -- rows = destination positions, columns = source
+                         local ids, values 1/sqrt((deg_u+1)(deg_v+1)) from
+                         full-graph out-degrees.
+"""
+from __future__ import annotations
+
+import time
+from typing import List, Optional, Sequence
+
+import torch
+
+from ..core import relabel, sample_hop
+from ..data import BCSRGraph
+
+
+class NeighborSampler:
+    """Fixed-fanout node-wise sampler over a CSR graph resident in HBM.
+
+    Args:
+        fanouts: neighbours per node for each model layer, input side first
+            (as the reference's ``BCSRSampler(fanouts=...)``); each in [1, 64].
+        seed: Philox key (the stream is counter = (node, draw)).
+        tile_cols: 16 (MFMA-native) or 8 (the reference's tile).
+        values_dtype: dtype of the blocks' values_condensed.
+    """
+
+    def __init__(self, fanouts: Sequence[int], seed: int = 42, tile_rows: int = 16,
+                 tile_cols: int = 16, values_dtype: torch.dtype = torch.float32,
+                 verbose: bool = False):
+        if tile_rows != 16:
+            raise ValueError("tile_rows must be 16")
+        if tile_cols not in (8, 16):
+            raise ValueError("tile_cols must be 8 or 16")
+        for f in fanouts:
+            if not 1 <= int(f) <= 64:
+                raise ValueError(f"fanout {f} outside [1, 64]")
+        self.fanouts = [int(f) for f in fanouts]
+        self.seed = int(seed)
+        self.tile_rows = 16
+        self.tile_cols = int(tile_cols)
+        self.values_dtype = values_dtype
+        self.verbose = verbose
+        self.last_stats: dict = {}
+
+    def sample_layers(self, indptr: torch.Tensor, indices: torch.Tensor,
+                      seed_nodes: torch.Tensor) -> List[BCSRGraph]:
+        """Samples len(fanouts) hops from `seed_nodes` (distinct global ids).
+
+        Every returned block carries ``src_nodes`` (int64 global ids of its
+        columns, destination nodes first), ``num_sampled_edges`` and
+        ``fanout``.  ``layers[0].src_nodes`` are the input nodes whose
+        features the first layer reads."""
+        from .. import builder
+        dev = indptr.device
+        num_nodes = indptr.numel() - 1
+        frontier = seed_nodes.to(dev, torch.int64).contiguous()
+        blocks: List[BCSRGraph] = []
+        t0 = time.perf_counter()
+        edges = 0
+        for k in reversed(self.fanouts):
+            dst, src, val = sample_hop(indptr, indices, frontier, k, seed=self.seed)
+            src_local, nxt = relabel(frontier, src, num_nodes)
+            F, S = frontier.numel(), nxt.numel()
+            win, cols, vals = builder.coo_to_bcsr_device(
+                F, S, dst, src_local, val, tile_cols=self.tile_cols,
+                values_dtype=self.values_dtype)
+            g = BCSRGraph(num_nodes=F, num_edges=int(dst.numel()), tile_rows=16,
+                          tile_cols=self.tile_cols, window_offset=win, original_col_indices=cols,
+                          values_condensed=vals, device=dev, num_rows=F, num_cols=S,
+                          values_dtype=self.values_dtype)
+            g.src_nodes = nxt
+            g.dst_nodes = frontier
+            g.num_sampled_edges = int(dst.numel())
+            g.fanout = k
+            blocks.insert(0, g)
+            edges += g.num_sampled_edges
+            frontier = nxt
+        self.last_stats = {"edges": edges, "seconds": time.perf_counter() - t0,
+                           "input_nodes": int(frontier.numel())}
+        if self.verbose:
+            s = self.last_stats
+            print(f"[NeighborSampler] {len(self.fanouts)} hops, {s['edges']} edges, "
+                  f"{s['input_nodes']} input nodes, {1e3 * s['seconds']:.3f} ms")
+        return blocks
+
+    def __repr__(self) -> str:
+        return (f"NeighborSampler(fanouts={self.fanouts}, seed={self.seed}, "
+                f"tile={self.tile_rows}x{self.tile_cols}, values={self.values_dtype})")

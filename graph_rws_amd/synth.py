@@ -186,3 +186,78 @@ def config_graph(name: str, device="cpu", scale: float = 1.0) -> CSRGraph:
         return sbm(n, c["communities"], c["intra"], e, seed=c["seed"], device=device)
     return chung_lu(n, e, c["gamma"], seed=c["seed"], max_degree=c.get("max_degree"),
                     device=device)
+
+
+def powerlaw_csr(n: int, num_edges: int, gamma: float = 2.1, max_degree: int = 100_000,
+                 seed: int = 5, device="cpu", chunk: int = 1 << 27) -> CSRGraph:
+    """Directed power-law graph as CSR, generated directly (no symmetrise or
+    dedup pass, so it scales to billions of edges in HBM).
+
+    Out-degrees: the Chung-Lu expectation w_r = c (r+1)^(-1/(gamma-1)) for
+    degree rank r, capped at `max_degree` and rescaled to `num_edges`,
+    rounded stochastically.  Neighbours: i.i.d. endpoint ranks drawn from
+    the continuous inverse CDF of the same power law.  Node ids are a
+    seeded permutation of ranks, so hubs are spread over the id range.
+    Neighbour lists are in draw order and may repeat a node.  values are
+    empty (the sampler derives GCN weights from the degrees)."""
+    device = torch.device(device)
+    g = _gen(seed, device)
+    a = 1.0 / (gamma - 1.0)
+    r = torch.arange(n, device=device, dtype=torch.float64)
+    w = (r + 1.0).pow(-a)
+    w = w * (num_edges / w.sum())
+    for _ in range(6):
+        w = w.clamp(max=float(max_degree))
+        w = w * (num_edges / w.sum())
+    w = w.clamp(max=float(max_degree))
+    fl = torch.floor(w)
+    deg = (fl + (torch.rand(n, generator=g, device=device, dtype=torch.float64) < (w - fl))).to(torch.int64)
+    del w, fl, r
+    perm = torch.randperm(n, generator=g, device=device)  # rank -> node id
+    deg_by_id = torch.empty_like(deg)
+    deg_by_id[perm] = deg
+    del deg
+    indptr = torch.zeros(n + 1, dtype=torch.int64, device=device)
+    torch.cumsum(deg_by_id, 0, out=indptr[1:])
+    del deg_by_id
+    nnz = int(indptr[-1].item())
+    indices = torch.empty(nnz, dtype=torch.int32, device=device)
+    b = 1.0 - a
+    top = float((n + 1.0) ** b - 1.0)
+    for s in range(0, nnz, chunk):
+        e = min(nnz, s + chunk)
+        u = torch.rand(e - s, generator=g, device=device, dtype=torch.float64)
+        x = (1.0 + u * top).pow(1.0 / b).sub_(1.0).floor_().clamp_(0, n - 1).to(torch.int64)
+        indices[s:e] = perm[x].to(torch.int32)
+        del u, x
+    return CSRGraph(n, indptr, indices, torch.empty(0, dtype=torch.float32, device=device))
+
+
+def distinct_seeds(n: int, count: int, seed: int = 42, device="cpu") -> torch.Tensor:
+    """`count` distinct node ids drawn uniformly from [0, n) (int64)."""
+    device = torch.device(device)
+    g = _gen(seed, device)
+    have = torch.empty(0, dtype=torch.int64, device=device)
+    while have.numel() < count:
+        draw = torch.randint(0, n, (2 * count,), generator=g, device=device)
+        cat = torch.cat([have, draw])
+        u, idx = torch.unique(cat, return_inverse=True)
+        # keep first occurrences in draw order
+        first = torch.full((u.numel(),), cat.numel(), dtype=torch.int64, device=device)
+        first.scatter_reduce_(0, idx, torch.arange(cat.numel(), device=device), reduce="amin")
+        have = cat[torch.sort(first).values]
+    return have[:count].contiguous()
+
+
+# c5: mini-batch sampling at web scale (BASELINE.json configs[4])
+C5 = dict(n=111_000_000, edges=1_600_000_000, gamma=2.1, max_degree=100_000, seed=5,
+          batch=1024, fanouts=[15, 10, 5], philox_seed=42, feat=128, classes=172)
+
+
+def c5_graph(device="cpu", scale: float = 1.0) -> CSRGraph:
+    """The c5 CSR (111M nodes, ~1.6B edges, int64 indptr, int32 indices);
+    `scale` < 1 shrinks nodes and edges proportionally."""
+    n = max(64, int(C5["n"] * scale))
+    e = max(256, int(C5["edges"] * scale))
+    return powerlaw_csr(n, e, gamma=C5["gamma"], max_degree=C5["max_degree"], seed=C5["seed"],
+                        device=device)

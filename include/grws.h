@@ -217,6 +217,51 @@ int grws_reindex_prune(const int32_t* in_cols, int64_t num_indices, void* values
                        int32_t values_dtype, const int32_t* active_windows, int64_t num_active,
                        int32_t tile_rows, int32_t tile_cols, int32_t* out_cols, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Node-wise fanout sampling, one hop.  Takes the place of the per-hop       */
+/* column-sampling phase of core_lib.sample_all_layers (bind.cpp:99-121 ->   */
+/* sampling_wrapper.cu:365-438, phase 1 = sampling.cuh:65-448) for the       */
+/* mini-batch path that draws a fixed fanout per node (BCSRSampler's         */
+/* sample_layers, sampler/sampler.py:186-279, calls it once per hop, hop 0   */
+/* from the seeds with the last fanout, sampler.py:204).                     */
+/*                                                                          */
+/* For every frontier node v (CSR indptr int64 [num_nodes+1], indices int32  */
+/* [nnz]): deg <= fanout takes every neighbour, otherwise Floyd's algorithm  */
+/* picks fanout distinct CSR positions with draws                            */
+/*   u = word 0 of Philox4x32-10(counter (v_lo, v_hi, d, 0), key (seed_lo,   */
+/*       seed_hi)),  t = (u64(u) * (j+1)) >> 32,  j = deg-fanout+d.          */
+/* Edges are written in frontier order, then ascending CSR position:        */
+/* edge_dst = frontier position (int32), edge_src = neighbour id (int64),   */
+/* edge_val (optional, may be NULL) = 1/sqrt((deg(v)+1)(deg(src)+1)) from    */
+/* out-degrees.  fanout in [1, 64]; edge_capacity >= num_frontier * fanout.  */
+/* Synchronises `stream`; *num_edges_out = edges written.  GRWS_E_RANGE for  */
+/* an id outside [0, num_nodes) or an invalid indptr.                        */
+/* ------------------------------------------------------------------------ */
+size_t grws_sample_hop_workspace_bytes(int64_t num_frontier);
+int grws_sample_hop(const int64_t* indptr, const int32_t* indices, int64_t num_nodes, int64_t nnz,
+                    const int64_t* frontier, int64_t num_frontier, int32_t fanout, uint64_t seed,
+                    int32_t* edge_dst, int64_t* edge_src, float* edge_val, int64_t edge_capacity,
+                    void* workspace, size_t workspace_bytes, int64_t* num_edges_out, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Unique + relabel of one hop's sources.  Takes the place of the reference's */
+/* next-seed extraction and active-window bookkeeping                       */
+/* (sampling_wrapper.cu:283-347 prepare_windows_and_masks, :421-433) and of  */
+/* the global -> local mapping its layers apply afterwards (reindex.cuh:33-  */
+/* 102): frontier nodes keep local ids [0, F) in frontier order (the         */
+/* "destination nodes first" block layout of data/bcsr.py:266-306 and       */
+/* layers/layer.py:159-161); sources outside the frontier are appended in    */
+/* ascending global id.  Writes src_local [num_edges] int32 and              */
+/* next_frontier [num_src] int64 (the frontier followed by the new ids;      */
+/* next_capacity >= num_frontier + num_edges).  Frontier ids must be         */
+/* distinct (GRWS_E_INVALID otherwise).  Synchronises `stream`.              */
+/* ------------------------------------------------------------------------ */
+size_t grws_relabel_workspace_bytes(int64_t num_frontier, int64_t num_edges);
+int grws_relabel(const int64_t* frontier, int64_t num_frontier, const int64_t* edge_src,
+                 int64_t num_edges, int64_t num_nodes, int32_t* src_local, int64_t* next_frontier,
+                 int64_t next_capacity, void* workspace, size_t workspace_bytes,
+                 int64_t* num_src_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -308,3 +308,46 @@ def round_to_bf16(x: np.ndarray) -> np.ndarray:
     out = r.astype(np.uint32).view(np.float32).copy()
     out[nan] = np.nan
     return out
+
+
+def gcn_weight(deg_dst, deg_src) -> np.ndarray:
+    """1/sqrt((deg_dst+1)(deg_src+1)) in float64 (exact product, correctly
+    rounded sqrt and division), rounded once to float32."""
+    p = (np.asarray(deg_dst, np.int64) + 1).astype(np.float64) * \
+        (np.asarray(deg_src, np.int64) + 1).astype(np.float64)
+    return (1.0 / np.sqrt(p)).astype(np.float32)
+
+
+def coo_to_bcsr(num_rows: int, rows, cols, vals, tile_cols: int):
+    """COO (duplicates: last in input order wins) -> BCSR through a stable
+    (row, col) ordering and csr_to_bcsr (convert_wrapper.cpp:27-180)."""
+    rows = np.asarray(rows, np.int64)
+    cols = np.asarray(cols, np.int64)
+    vals = np.asarray(vals, np.float64)
+    order = np.lexsort((cols, rows))  # stable: ties keep input order
+    r, c, v = rows[order], cols[order], vals[order]
+    rp = np.zeros(num_rows + 1, np.int64)
+    np.cumsum(np.bincount(r, minlength=num_rows), out=rp[1:])
+    return csr_to_bcsr(num_rows, rp, c.astype(np.int32), v, 16, tile_cols)
+
+
+def sample_blocks(indptr, indices, seeds, fanouts, seed: int = 42, tile_cols: int = 16):
+    """Host restatement of the node-wise sampler's batch: hop 0 from the
+    seeds with fanouts[-1] (sampler.py:204 order), Floyd + relabel per hop,
+    a BCSR block per hop with GCN weights from out-degrees.  Returns a list
+    (input side first) of dicts with dst, src, val, src_local, src_nodes and
+    the BCSR arrays (win, cols, vals as float32)."""
+    ip = np.asarray(indptr, np.int64)
+    deg = ip[1:] - ip[:-1]
+    frontier = np.asarray(seeds, np.int64)
+    out = []
+    for k in reversed(list(fanouts)):
+        dst, src = sample_hop(ip, indices, seed, frontier, k)
+        val = gcn_weight(deg[frontier[dst]], deg[src])
+        local, nxt = relabel(frontier, src)
+        win, cols, vals = coo_to_bcsr(frontier.size, dst, local, val, tile_cols)
+        out.insert(0, dict(dst=dst, src=src, val=val, src_local=local, src_nodes=nxt,
+                           num_rows=frontier.size, num_cols=nxt.size, win=win, cols=cols,
+                           vals=vals.astype(np.float32)))
+        frontier = nxt
+    return out

@@ -239,3 +239,71 @@ def test_relabel_invariants():
     assert not np.isin(new, frontier).any()
     np.testing.assert_array_equal(nxt[local], src)               # bijective relabel
     assert set(np.unique(np.concatenate([frontier, src]))) == set(nxt)
+
+
+def _floyd_py(seed, node, deg, k):
+    """Floyd's algorithm spelled out in Python over the ATen-pinned draws."""
+    if deg <= k:
+        return list(range(deg))
+    chosen = []
+    for j in range(deg - k, deg):
+        u = int(oracle.philox_draws(seed, [node], [j - (deg - k)])[0])
+        t = (u * (j + 1)) >> 32
+        chosen.append(j if t in chosen else t)
+    return sorted(chosen)
+
+
+def test_floyd_sampler_matches_python_restatement():
+    degs = [0, 2, 5, 7, 16, 33, 64, 65, 200, 5000]
+    indptr, _ = _toy_csr(degs, seed=9)
+    indices = np.arange(indptr[-1], dtype=np.int32)  # neighbour id == CSR position
+    nodes = np.arange(len(degs), dtype=np.int64)
+    for k in (1, 5, 15, 64):
+        dst, src = oracle.sample_hop(indptr, indices, 1234, nodes, k)
+        for i, d in enumerate(degs):
+            got = (src[dst == i] - indptr[i]).tolist()
+            assert got == _floyd_py(1234, i, d, k), (k, d)
+
+
+def test_gcn_weight_closed_forms():
+    w = oracle.gcn_weight([0, 3, 0, 15, 8, 99], [0, 3, 3, 63, 8, 0])
+    np.testing.assert_array_equal(w, np.float32([1.0, 0.25, 0.5, 1.0 / 32, 1.0 / 9, 0.1]))
+    rng = np.random.default_rng(0)
+    a, b = rng.integers(0, 10 ** 6, 1000), rng.integers(0, 10 ** 6, 1000)
+    np.testing.assert_array_equal(oracle.gcn_weight(a, b), oracle.gcn_weight(b, a))
+    ref = np.float32([1.0 / np.sqrt(np.longdouble(x + 1) * np.longdouble(y + 1)) for x, y in zip(a, b)])
+    np.testing.assert_array_equal(oracle.gcn_weight(a, b), ref)
+
+
+def test_coo_to_bcsr_dense_and_last_wins():
+    rng = np.random.default_rng(5)
+    rows = rng.integers(0, 40, 600)
+    cols = rng.integers(0, 70, 600)
+    vals = rng.standard_normal(600)
+    for tc in (8, 16):
+        win, c, v = oracle.coo_to_bcsr(40, rows, cols, vals, tc)
+        D = oracle.bcsr_to_dense(win, c, v, 16, tc, 70)[:40]
+        last = {}
+        for r, cc, x in zip(rows, cols, vals):
+            last[(r, cc)] = x
+        E = np.zeros((40, 70))
+        for (r, cc), x in last.items():
+            E[r, cc] = x
+        np.testing.assert_array_equal(D, E)
+
+
+def test_sample_blocks_structure():
+    degs = np.random.default_rng(2).integers(0, 40, 3000)
+    indptr, indices = _toy_csr(degs.tolist(), seed=4)
+    indices = indices % 3000
+    seeds = np.random.default_rng(8).choice(3000, 50, replace=False)
+    blocks = oracle.sample_blocks(indptr, indices, seeds, [15, 10, 5], seed=42, tile_cols=16)
+    assert [b["num_rows"] for b in blocks][-1] == 50
+    for i, b in enumerate(blocks):
+        np.testing.assert_array_equal(b["src_nodes"][b["src_local"]], b["src"])
+        if i + 1 < len(blocks):  # a layer's destinations are the next layer's sources
+            assert b["num_rows"] == blocks[i + 1]["num_cols"]
+        D = oracle.bcsr_to_dense(b["win"], b["cols"], b["vals"], 16, 16, b["num_cols"])
+        E = np.zeros_like(D)
+        E[b["dst"], b["src_local"]] = b["val"]
+        np.testing.assert_array_equal(D, E)
