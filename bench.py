@@ -25,6 +25,15 @@ import torch
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16
 
+# HBM bytes per SpMM launch measured with rocprofv3 --pmc (FETCH_SIZE x2.0 and
+# WRITE_SIZE x1.0, both scaled by a 1 GiB device copy); bench.py cannot read
+# counters itself, so the figure of the profiled workload is recorded here and
+# reported only for that exact workload.  Source: profiles/spmm_fwd_c3_n608_f16.md
+MEASURED_TRAFFIC = {
+    # (config, N, x dtype, tile cols): (bytes per launch, profile file)
+    ("c3", 608, "f16", 16): (49.75e9, "profiles/spmm_fwd_c3_n608_f16.md"),
+}
+
 
 def _cpu_model() -> str:
     try:
@@ -181,6 +190,9 @@ def main():
     ap.add_argument("--tile-cols", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sampling", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="only run 5 device-to-device copies of BYTES (the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     ap.add_argument("--sampling-batches", type=int, default=20)
     args = ap.parse_args()
 
@@ -193,6 +205,18 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda", 0)
+    if args.calibrate_copy > 0:
+        a = torch.ones(args.calibrate_copy, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize(dev)
+        ms = (time.perf_counter() - t0) * 200.0
+        print(json.dumps({"copy_bytes": args.calibrate_copy, "copies": 5, "ms_per_copy": round(ms, 4),
+                          "gbps_read_plus_write": round(2 * args.calibrate_copy / ms / 1e6, 1)}))
+        return
     from graph_rws_amd.core import _lib
     _lib.load()
 
@@ -265,7 +289,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC.get((cfg, N, dname, G.tile_cols), (None, None))[0],
+            "traffic_source": MEASURED_TRAFFIC.get((cfg, N, dname, G.tile_cols), (None, None))[1],
             "kernel_ms_avg": round(ms_avg, 4),
             "mfma_issued_tflops": round(issued / (ms_avg / 1e3) / 1e12, 2),
             "mfma_frac": round(issued / (ms_avg / 1e3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
