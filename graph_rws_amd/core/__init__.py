@@ -9,8 +9,11 @@ from .ops import (  # noqa: F401
     build_spmm_plan,
     csr_to_bcsr_cpu,
     default_slabs,
+    SamplingTimingResult,
     reindex_bcsr,
     relabel,
+    sample_all_layers,
+    window_seeds,
     sample_hop,
     spmm,
     spmm_tc,
@@ -38,4 +41,7 @@ __all__ = [
     "SpmmPlan",
     "sample_hop",
     "relabel",
+    "sample_all_layers",
+    "SamplingTimingResult",
+    "window_seeds",
 ]

@@ -37,6 +37,16 @@ class SpmmPlanView(ctypes.Structure):
                 ("slabs_per_item", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
+class HacsView(ctypes.Structure):
+    """grws_hacs (include/grws.h)."""
+    _fields_ = [("static_scores", _vp), ("window_part_ids", _vp), ("part_starts", _vp),
+                ("part_ends", _vp), ("num_static_scores", ctypes.c_int64),
+                ("num_window_part_ids", ctypes.c_int64), ("num_parts", ctypes.c_int64),
+                ("alpha", ctypes.c_float), ("beta", ctypes.c_float), ("delta", ctypes.c_float),
+                ("gamma_bonus", ctypes.c_float), ("score_scale", ctypes.c_float),
+                ("use_hacs", ctypes.c_int32), ("locality_enabled", ctypes.c_int32)]
+
+
 # name -> (restype, argtypes)
 _PROTOS = {
     "grws_last_error": (ctypes.c_char_p, []),
@@ -80,6 +90,18 @@ _PROTOS = {
     "grws_sample_hop": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp,
                                        ctypes.c_int64, ctypes.c_int32, ctypes.c_uint64, _vp, _vp,
                                        _vp, ctypes.c_int64, _vp, ctypes.c_size_t, _c_i64p, _vp]),
+    "grws_window_sample_num": (ctypes.c_int32, [ctypes.c_int32]),
+    "grws_window_seeds_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "grws_window_seeds": (ctypes.c_int, [_vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+                                         ctypes.c_int32, _vp, _vp, _vp, ctypes.c_size_t, _c_i64p,
+                                         _vp]),
+    "grws_window_topk_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "grws_window_topk": (ctypes.c_int, [ctypes.POINTER(BcsrView), _vp, ctypes.c_int64,
+                                        ctypes.c_int32, ctypes.POINTER(HacsView), _vp, _vp, _vp,
+                                        _vp, ctypes.c_size_t, _c_i64p, _vp]),
+    "grws_window_recompress": (ctypes.c_int, [ctypes.POINTER(BcsrView), _vp, ctypes.c_int64,
+                                              ctypes.c_int32, _vp, _vp, _vp, ctypes.c_int64, _vp,
+                                              _vp, _vp]),
     "grws_relabel_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
     "grws_relabel": (ctypes.c_int, [_vp, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int64,
                                     _vp, _vp, ctypes.c_int64, _vp, ctypes.c_size_t, _c_i64p,

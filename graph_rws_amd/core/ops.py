@@ -331,3 +331,147 @@ def relabel(frontier: torch.Tensor, edge_src: torch.Tensor, num_nodes: int):
     L.call("grws_relabel", L.ptr(fr), F, L.ptr(es), E, int(num_nodes), L.ptr(src_local),
            L.ptr(nxt), max(F + E, 1), L.ptr(ws), wsb, ctypes.byref(ns), L.stream_of(dev))
     return src_local[:E], nxt[:ns.value]
+
+
+# ---------------------------------------------------------------------------
+# window top-K sampling (csrc/window_sample.hip): core_lib.sample_all_layers
+# ---------------------------------------------------------------------------
+class SamplingTimingResult:
+    """Per-layer timing of sample_all_layers (bind.cpp:81-96): milliseconds
+    of the column selection (phase 1, which here also records each column's
+    source slot), the mapping (phase 2, folded into phase 1: 0.0), the
+    recompression (phase 3) and the whole layer."""
+
+    __slots__ = ("phase1_sampling_time", "phase2_mapping_time", "phase3_recompression_time",
+                 "total_time")
+
+    def __init__(self, p1: float = 0.0, p2: float = 0.0, p3: float = 0.0, total: float = 0.0):
+        self.phase1_sampling_time = float(p1)
+        self.phase2_mapping_time = float(p2)
+        self.phase3_recompression_time = float(p3)
+        self.total_time = float(total)
+
+    def to_dict(self) -> dict:
+        return {k: getattr(self, k) for k in self.__slots__}
+
+    def __repr__(self) -> str:
+        return ("SamplingTimingResult(phase1={:.3f}ms, phase2={:.3f}ms, phase3={:.3f}ms, "
+                "total={:.3f}ms)".format(self.phase1_sampling_time, self.phase2_mapping_time,
+                                         self.phase3_recompression_time, self.total_time))
+
+
+def _window_seeds(ids: torch.Tensor, num_nodes: int, drop: bool):
+    dev = ids.device
+    ids = ids.to(torch.int32).contiguous()
+    n = ids.numel()
+    act = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    msk = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    wsb = int(L.load().grws_window_seeds_workspace_bytes(n))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    na = ctypes.c_int64()
+    L.call("grws_window_seeds", L.ptr(ids), n, int(num_nodes), 16, 1 if drop else 0, L.ptr(act),
+           L.ptr(msk), L.ptr(ws), wsb, ctypes.byref(na), L.stream_of(dev))
+    return act[:na.value], msk[:na.value]
+
+
+def window_seeds(seeds: torch.Tensor, num_nodes: int, drop_out_of_range: bool = False):
+    """prepare_windows_and_masks (sampling_wrapper.cu:283-347): seed ids ->
+    (sorted unique active windows int32, OR-ed row masks int32)."""
+    return _window_seeds(seeds, num_nodes, drop_out_of_range)
+
+
+def _hacs_view(dev, static_scores, window_part_ids, part_starts, part_ends, alpha, beta, delta,
+               gamma_bonus, score_scale, use_hacs, locality_enabled, keep: list):
+    if not use_hacs:
+        return None
+    def prep(t, dt):
+        if t is None:
+            return None
+        t = torch.as_tensor(t).to(dev, dt).contiguous()
+        keep.append(t)
+        return t
+    ss = prep(static_scores, torch.float32)
+    if ss is None:
+        raise RuntimeError("use_hacs needs static_scores")
+    wp = ps = pe = None
+    if locality_enabled:
+        wp = prep(window_part_ids, torch.int32)
+        ps = prep(part_starts, torch.int32)
+        pe = prep(part_ends, torch.int32)
+        if wp is None or ps is None or pe is None:
+            raise RuntimeError("locality_enabled needs window_part_ids, part_starts and part_ends")
+    return L.HacsView(L.ptr(ss), L.ptr(wp), L.ptr(ps), L.ptr(pe), ss.numel(),
+                      0 if wp is None else wp.numel(), 0 if ps is None else min(ps.numel(), pe.numel()),
+                      float(alpha), float(beta), float(delta), float(gamma_bonus), float(score_scale),
+                      1, 1 if locality_enabled else 0)
+
+
+def sample_all_layers(window_offset: torch.Tensor, original_col_indices: torch.Tensor,
+                      values_condensed: torch.Tensor, initial_seeds: torch.Tensor, fanouts,
+                      num_global_nodes: int, static_scores: Optional[torch.Tensor] = None,
+                      window_part_ids: Optional[torch.Tensor] = None,
+                      part_starts: Optional[torch.Tensor] = None,
+                      part_ends: Optional[torch.Tensor] = None, alpha: float = 1.0,
+                      beta: float = 10.0, delta: float = 0.0, gamma_bonus: float = 0.0,
+                      score_scale: float = 100.0, use_hacs: int = 0, locality_enabled: int = 0,
+                      tile_rows: int = 16, tile_cols: int = 8, warps_per_block: int = 8):
+    """Drop-in for core_lib.sample_all_layers (bind.cpp:99-121 ->
+    sampling_wrapper.cu:365-438).  Returns (layers, timings): per fanout, in
+    the order given, [out_window_offset int64, out_col_indices int32 (global
+    ids), out_values, active_windows int32, masks int32], and one
+    SamplingTimingResult.  Output arrays are sized exactly (no -1 tail);
+    values keep values_condensed's dtype.  warps_per_block is validated as
+    the reference does (4 or 8) and has no effect on the result."""
+    if tile_rows != 16 or tile_cols not in (8, 16):
+        raise RuntimeError("sample_all_layers supports 16x8 tiles (the reference's) and 16x16")
+    if warps_per_block not in (4, 8):
+        raise RuntimeError(f"Unsupported warps_per_block: {warps_per_block}. Only 4 and 8 allowed.")
+    _check_graph(window_offset, original_col_indices, values_condensed, tile_cols)
+    if not window_offset.is_cuda:
+        raise RuntimeError("window_offset must be a CUDA tensor")
+    dev = window_offset.device
+    W = window_offset.numel() - 1
+    n_nodes = int(num_global_nodes) if int(num_global_nodes) > 0 else 16 * W
+    keep: list = []
+    hv = _hacs_view(dev, static_scores, window_part_ids, part_starts, part_ends, alpha, beta,
+                    delta, gamma_bonus, score_scale, use_hacs, locality_enabled, keep)
+    view = L.BcsrView(L.ptr(window_offset), L.ptr(original_col_indices), L.ptr(values_condensed),
+                      W, original_col_indices.numel() // tile_cols, 16, tile_cols,
+                      L.dtype_code(values_condensed.dtype), 0)
+    stream = torch.cuda.current_stream(dev)
+    seeds = initial_seeds.to(dev)
+    active, masks = _window_seeds(seeds, n_nodes, drop=False)
+    layers, timings = [], []
+    fanouts = [int(f) for f in fanouts]
+    for i, f in enumerate(fanouts):
+        S = int(L.load().grws_window_sample_num(f))
+        if not 1 <= f <= 256:
+            raise RuntimeError("Fanout > 256 not supported (fanout must be in [1, 256])")
+        A = active.numel()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev[0].record(stream)
+        scols = torch.empty(max(A * S, 1), dtype=torch.int32, device=dev)
+        sslot = torch.empty(max(A * S, 1), dtype=torch.int32, device=dev)
+        out_off = torch.empty(A + 1, dtype=torch.int64, device=dev)
+        wsb = int(L.load().grws_window_topk_workspace_bytes(A))
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        T = ctypes.c_int64()
+        L.call("grws_window_topk", ctypes.byref(view), L.ptr(active), A, f,
+               ctypes.byref(hv) if hv is not None else None, L.ptr(scols), L.ptr(sslot),
+               L.ptr(out_off), L.ptr(ws), wsb, ctypes.byref(T), L.stream_of(dev))
+        T = T.value
+        ev[1].record(stream)
+        out_cols = torch.empty(T * tile_cols, dtype=torch.int32, device=dev)
+        out_vals = torch.empty(T * 16 * tile_cols, dtype=values_condensed.dtype, device=dev)
+        L.call("grws_window_recompress", ctypes.byref(view), L.ptr(active), A, f, L.ptr(scols),
+               L.ptr(sslot), L.ptr(out_off), T, L.ptr(out_cols), L.ptr(out_vals),
+               L.stream_of(dev))
+        ev[2].record(stream)
+        layers.append([out_off, out_cols, out_vals, active, masks])
+        if i + 1 < len(fanouts):
+            active, masks = _window_seeds(out_cols, n_nodes, drop=True)
+        ev[2].synchronize()
+        p1 = ev[0].elapsed_time(ev[1])
+        p3 = ev[1].elapsed_time(ev[2])
+        timings.append(SamplingTimingResult(p1, 0.0, p3, p1 + p3))
+    return layers, timings

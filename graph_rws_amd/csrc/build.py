@@ -30,6 +30,7 @@ SOURCES = [
     "bcsr_build.hip",
     "reindex.hip",
     "sample.hip",
+    "window_sample.hip",
 ]
 
 ARCH = os.environ.get("GRWS_OFFLOAD_ARCH", "gfx950")

@@ -1,0 +1,606 @@
+// Window top-K sampling of a BCSR graph (gfx950): the reference-compatible
+// mode of core_lib.sample_all_layers.
+//
+// Replaces, with the same results:
+//   prepare_windows_and_masks          sampling_wrapper.cu:283-347
+//   warp_centric_find_top_k_kernel     sampling.cuh:65-448
+//   build_col_to_val_map_kernel + scan sampling.cuh:707-773, sampling_wrapper.cu:160-204
+//   recompress_sampled_bcsr_kernel     sampling.cuh:471-579
+//
+// Semantics (per active window, all of it determined by the reference):
+//   * every column slot c != -1 of the window scores each of its tile_rows
+//     values v:  non-HACS  s = trunc(fma(10, |v|, 1) * 1000)
+//                HACS      s = trunc((fma(beta, |v|, alpha) * q[col]
+//                                     [+ delta if col in the window's part])
+//                                    * scale)
+//     (sampling.cuh:251-275); a value with s <= 0 does not count (:277), a
+//     column none of whose values count is not a candidate; the seed mask is
+//     not applied (:246-248);
+//   * a candidate's total is the wrapping int32 sum of its counted scores,
+//     plus trunc(gamma_bonus * scale) under HACS with gamma_bonus > 0 (:332);
+//   * the CAP candidates first in (total desc, column asc) are kept (the
+//     per-batch truncation of :390-393 equals a global top-CAP because columns
+//     are unique per window), CAP = 32, 128 or 256 for S = roundup32(fanout)
+//     <= 32, <= 128, <= 256 (macros.h DISPATCH_SAMPLING);
+//   * the kept columns are sorted ascending and the first min(kept, S) are
+//     the window's sample (:396-447) -- for 32 < S < CAP this is the S
+//     smallest column ids of the top-CAP, not the top-S;
+//   * tiles = ceil(sample / tile_cols); the output tile's slot j holds sample
+//     column j (or -1) and its tile_rows values are that column's values in
+//     the input window (or 0), :520-578.
+//
+// Design: one 256-thread work-group per active window.  The 64-bit key
+// (~total << 32 | column) orders candidates exactly as the reference's
+// comparator; an MSB-first 8-bit radix select over the window's slots (keys
+// recomputed from the values on every pass; the window stays in L2) finds the
+// CAP-th key, the selected (column, slot) pairs are compacted into LDS and
+// bitonic-sorted by column.  The slot index replaces the reference's linear
+// column search when the tiles are rebuilt.
+#include "grws_internal.h"
+
+namespace grws {
+namespace {
+
+constexpr int kBlk = 256;
+constexpr int kMaxCap = 256;
+
+enum : int32_t { kErrWindow = 1, kErrSeed = 2, kErrHacs = 4 };
+
+inline int bits_for(int64_t x) {
+    int b = 0;
+    while (b < 63 && ((int64_t)1 << b) < x) ++b;
+    return b;
+}
+
+inline unsigned grid_for(int64_t n, int64_t per_block = kBlk) {
+    int64_t g = (n + per_block - 1) / per_block;
+    return (unsigned)(g < 1 ? 1 : g);
+}
+
+// C's (int) of a float as the GPU converts it: truncation toward zero,
+// saturating at the int32 range, NaN -> 0.
+__device__ __forceinline__ int32_t f2i_sat(float x) {
+    if (x != x) return 0;
+    if (x >= 2147483648.0f) return INT32_MAX;
+    if (x <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)x;
+}
+
+struct ScoreParams {
+    const float* static_scores;
+    const int32_t* window_part_ids;
+    const int32_t* part_starts;
+    const int32_t* part_ends;
+    int64_t num_static_scores;
+    int64_t num_parts;
+    float alpha, beta, delta, scale;
+    int32_t gamma_int;
+    int32_t use_hacs;
+    int32_t locality;
+};
+
+template <typename VT>
+__device__ __forceinline__ float ld_val(const void* v, int64_t i) {
+    return to_float(static_cast<const VT*>(v)[i]);
+}
+
+// Key of one column slot of a window (sampling.cuh:222-345 restated per
+// column): ~(total as order-preserving u32) << 32 | column.  Returns false
+// when the slot is not a candidate.
+template <typename VT>
+__device__ __forceinline__ bool slot_key(const int32_t* __restrict__ cols, const void* __restrict__ vals,
+                                         int64_t tile0, int tc, int64_t s, int32_t window, int32_t part_lo,
+                                         int32_t part_hi, bool in_part_known, const ScoreParams& p,
+                                         uint64_t* key) {
+    // separate roundings where the reference's source writes separate
+    // operations (only its 1 + 10|v| and alpha + beta|v| are fused)
+#pragma clang fp contract(off)
+    const int64_t t = tile0 + s / tc;
+    const int c = (int)(s % tc);
+    const int32_t col = cols[t * tc + c];
+    if (col == -1) return false;
+    float q = 1.0f;
+    bool in_part = false;
+    if (p.use_hacs) {
+        if (col < 0 || (int64_t)col >= p.num_static_scores) return false;  // flagged by the caller
+        q = p.static_scores[col];
+        in_part = in_part_known && col >= part_lo && col < part_hi;
+    }
+    uint32_t total = 0;
+    bool any = false;
+    const int64_t vbase = t * 16 * tc + c;
+#pragma unroll 4
+    for (int r = 0; r < 16; ++r) {
+        const float v = fabsf(ld_val<VT>(vals, vbase + (int64_t)r * tc));
+        int32_t sc;
+        if (p.use_hacs) {
+            float f = __builtin_fmaf(p.beta, v, p.alpha) * q;
+            if (in_part) f += p.delta;
+            sc = f2i_sat(f * p.scale);
+        } else {
+            sc = f2i_sat(__builtin_fmaf(10.0f, v, 1.0f) * 1000.0f);
+        }
+        if (sc > 0) {
+            total += (uint32_t)sc;
+            any = true;
+        }
+    }
+    if (!any) return false;
+    total += (uint32_t)p.gamma_int;
+    const uint32_t ord = total ^ 0x80000000u;  // int32 order -> u32 order
+    *key = ((uint64_t)(~ord) << 32) | (uint32_t)col;
+    (void)window;
+    return true;
+}
+
+template <typename VT>
+__global__ __launch_bounds__(kBlk) void window_topk_kernel(const int64_t* __restrict__ win_off, int64_t num_windows,
+                                                           const int32_t* __restrict__ cols,
+                                                           const void* __restrict__ vals, int tc,
+                                                           const int32_t* __restrict__ active, int64_t num_active,
+                                                           ScoreParams p, int cap, int S,
+                                                           int32_t* __restrict__ out_cols,
+                                                           int32_t* __restrict__ out_slots,
+                                                           int32_t* __restrict__ out_tiles,
+                                                           int32_t* __restrict__ err) {
+    __shared__ int32_t hist[256];
+    __shared__ int32_t s_cnt;
+    __shared__ uint64_t s_prefix;
+    __shared__ int32_t s_shift;
+    __shared__ int32_t s_k;
+    __shared__ int32_t s_col[kMaxCap];
+    __shared__ int32_t s_slot[kMaxCap];
+
+    const int64_t b = blockIdx.x;
+    if (b >= num_active) return;
+    const int tid = threadIdx.x;
+    const int32_t w = active[b];
+    int32_t* oc = out_cols + b * (int64_t)S;
+    int32_t* os = out_slots + b * (int64_t)S;
+    if (w < 0 || (int64_t)w >= num_windows) {
+        if (tid == 0) {
+            atomicOr(err, kErrWindow);
+            out_tiles[b] = 0;
+        }
+        for (int i = tid; i < S; i += kBlk) {
+            oc[i] = -1;
+            os[i] = -1;
+        }
+        return;
+    }
+    const int64_t t0 = win_off[w];
+    const int64_t nslots = (win_off[w + 1] - t0) * tc;
+    int32_t part_lo = 0, part_hi = 0;
+    bool in_part_known = false;
+    if (p.use_hacs && p.locality && p.window_part_ids && p.part_starts && p.part_ends) {
+        const int32_t pid = p.window_part_ids[w];
+        if ((int64_t)pid >= p.num_parts) {
+            if (tid == 0) atomicOr(err, kErrHacs);
+        } else if (pid >= 0) {
+            part_lo = p.part_starts[pid];
+            part_hi = p.part_ends[pid];
+            in_part_known = true;
+        }
+    }
+
+    // candidates
+    if (tid == 0) s_cnt = 0;
+    __syncthreads();
+    {
+        int local = 0;
+        for (int64_t s = tid; s < nslots; s += kBlk) {
+            uint64_t k;
+            local += slot_key<VT>(cols, vals, t0, tc, s, w, part_lo, part_hi, in_part_known, p, &k) ? 1 : 0;
+            if (p.use_hacs) {
+                const int32_t col = cols[(t0 + s / tc) * tc + s % tc];
+                if (col != -1 && (col < 0 || (int64_t)col >= p.num_static_scores)) atomicOr(err, kErrHacs);
+            }
+        }
+        if (local) atomicAdd(&s_cnt, local);
+    }
+    __syncthreads();
+    const int32_t count = s_cnt;
+
+    // radix select of the cap-th smallest key (keys are distinct)
+    uint64_t prefix = 0;
+    int shift = 64;  // selected: key >> shift <= prefix >> shift (shift 64: all)
+    if (count > cap) {
+        if (tid == 0) {
+            s_k = cap;
+            s_prefix = 0;
+        }
+        for (int sh = 56; sh >= 0; sh -= 8) {
+            hist[tid] = 0;
+            __syncthreads();
+            const uint64_t pre = s_prefix;
+            for (int64_t s = tid; s < nslots; s += kBlk) {
+                uint64_t k;
+                if (!slot_key<VT>(cols, vals, t0, tc, s, w, part_lo, part_hi, in_part_known, p, &k)) continue;
+                if (sh < 56 && (k >> (sh + 8)) != (pre >> (sh + 8))) continue;
+                atomicAdd(&hist[(k >> sh) & 255u], 1);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                int kk = s_k, below = 0, d = 0;
+                for (; d < 255; ++d) {
+                    if (below + hist[d] >= kk) break;
+                    below += hist[d];
+                }
+                s_prefix = pre | ((uint64_t)d << sh);
+                s_k = kk - below;
+                // the whole bucket is taken: no need to resolve lower digits
+                s_shift = (below + hist[d] == kk) ? sh : -1;
+            }
+            __syncthreads();
+            if (s_shift >= 0) break;
+        }
+        prefix = s_prefix;
+        shift = s_shift >= 0 ? s_shift : 0;
+    }
+
+    // compact the selected (column, slot) pairs
+    if (tid == 0) s_cnt = 0;
+    for (int i = tid; i < kMaxCap; i += kBlk) {
+        s_col[i] = INT32_MAX;
+        s_slot[i] = -1;
+    }
+    __syncthreads();
+    for (int64_t s = tid; s < nslots; s += kBlk) {
+        uint64_t k;
+        if (!slot_key<VT>(cols, vals, t0, tc, s, w, part_lo, part_hi, in_part_known, p, &k)) continue;
+        if (shift < 64 && (k >> shift) > (prefix >> shift)) continue;
+        const int i = atomicAdd(&s_cnt, 1);
+        if (i < kMaxCap) {
+            s_col[i] = (int32_t)(uint32_t)k;
+            s_slot[i] = (int32_t)s;
+        }
+    }
+    __syncthreads();
+    const int nsel = s_cnt < cap ? s_cnt : cap;
+
+    // bitonic sort of the 256 LDS entries by column (padding INT32_MAX last)
+    for (int size = 2; size <= kMaxCap; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const int j = tid ^ stride;
+            if (j > tid) {
+                const bool up = (tid & size) == 0;
+                const int32_t a = s_col[tid], c = s_col[j];
+                if ((a > c) == up) {
+                    s_col[tid] = c;
+                    s_col[j] = a;
+                    const int32_t t = s_slot[tid];
+                    s_slot[tid] = s_slot[j];
+                    s_slot[j] = t;
+                }
+            }
+            __syncthreads();
+        }
+    }
+
+    const int nout = nsel < S ? nsel : S;
+    for (int i = tid; i < S; i += kBlk) {
+        oc[i] = i < nout ? s_col[i] : -1;
+        os[i] = i < nout ? s_slot[i] : -1;
+    }
+    if (tid == 0) out_tiles[b] = (nout + tc - 1) / tc;
+}
+
+// Output tile t of window b holds sample columns t*tc .. t*tc+tc-1.
+template <typename VT>
+__global__ __launch_bounds__(kBlk) void window_recompress_kernel(const int64_t* __restrict__ win_off,
+                                                                 int64_t num_windows,
+                                                                 const void* __restrict__ vals, int tc,
+                                                                 const int32_t* __restrict__ active,
+                                                                 int64_t num_active, int S,
+                                                                 const int32_t* __restrict__ samp_cols,
+                                                                 const int32_t* __restrict__ samp_slots,
+                                                                 const int64_t* __restrict__ out_off,
+                                                                 int32_t* __restrict__ out_cols,
+                                                                 VT* __restrict__ out_vals) {
+    const int64_t b = blockIdx.x;
+    if (b >= num_active) return;
+    const int64_t o0 = out_off[b];
+    const int64_t ntile = out_off[b + 1] - o0;
+    const int per_tile = 16 * tc;
+    const int64_t total = ntile * per_tile;
+    const int32_t w = active[b];
+    const bool w_ok = w >= 0 && (int64_t)w < num_windows;
+    const int64_t t0 = w_ok ? win_off[w] : 0;
+    const int64_t nslots = w_ok ? (win_off[w + 1] - t0) * tc : 0;
+    for (int64_t e = threadIdx.x; e < total; e += kBlk) {
+        const int64_t t = e / per_tile;
+        const int r = (int)((e % per_tile) / tc);
+        const int c = (int)(e % tc);
+        const int64_t j = t * tc + c;
+        int32_t col = -1, slot = -1;
+        if (j < S) {
+            col = samp_cols[b * (int64_t)S + j];
+            slot = samp_slots[b * (int64_t)S + j];
+        }
+        if (r == 0) out_cols[(o0 + t) * tc + c] = col;
+        VT v = VT(0.0f);
+        if (col != -1 && slot >= 0 && slot < nslots) {
+            const int64_t it = t0 + slot / tc;
+            v = static_cast<const VT*>(vals)[(it * 16 + r) * tc + slot % tc];
+        }
+        out_vals[(o0 + t) * per_tile + (int64_t)r * tc + c] = v;
+    }
+}
+
+// --- seeds -> active windows + masks (sampling_wrapper.cu:283-347) ------
+__global__ void seed_keys_kernel(const int32_t* __restrict__ ids, int64_t n, int64_t num_nodes, int tile_rows,
+                                 int drop_out_of_range, uint64_t sentinel, uint64_t* __restrict__ keys,
+                                 uint32_t* __restrict__ bits, int32_t* __restrict__ err) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int32_t v = ids[i];
+    uint64_t k = sentinel;
+    uint32_t m = 0;
+    if (v >= 0 && (int64_t)v < num_nodes) {
+        k = (uint64_t)(v / tile_rows);
+        m = 1u << (v % tile_rows);
+    } else if (v != -1 && !drop_out_of_range) {
+        atomicOr(err, kErrSeed);
+    }
+    keys[i] = k;
+    bits[i] = m;
+}
+
+__global__ void seed_heads_kernel(const uint64_t* __restrict__ keys, int64_t n, uint64_t sentinel,
+                                  int32_t* __restrict__ head) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    head[i] = (keys[i] != sentinel && (i == 0 || keys[i - 1] != keys[i])) ? 1 : 0;
+}
+
+__global__ void seed_emit_kernel(const uint64_t* __restrict__ keys, const uint32_t* __restrict__ bits, int64_t n,
+                                 uint64_t sentinel, const int32_t* __restrict__ head,
+                                 const int64_t* __restrict__ rank, int32_t* __restrict__ windows,
+                                 int32_t* __restrict__ masks) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    if (keys[i] == sentinel) return;
+    const int64_t idx = rank[i] + head[i] - 1;  // inclusive rank of this run
+    if (head[i]) windows[idx] = (int32_t)keys[i];
+    atomicOr(reinterpret_cast<uint32_t*>(masks) + idx, bits[i]);
+}
+
+struct SeedWs {
+    uint64_t *k, *k2;
+    uint32_t *m, *m2;
+    int32_t *head, *err;
+    int64_t* rank;
+    char* sort_ws;
+    size_t sort_bytes;
+    char* scan_ws;
+    size_t scan_bytes;
+};
+
+template <typename C>
+void carve_seed(C& cv, int64_t n, SeedWs* w) {
+    const int64_t m = n > 0 ? n : 1;
+    w->k = cv.template take<uint64_t>(m);
+    w->k2 = cv.template take<uint64_t>(m);
+    w->m = cv.template take<uint32_t>(m);
+    w->m2 = cv.template take<uint32_t>(m);
+    w->head = cv.template take<int32_t>(m);
+    w->rank = cv.template take<int64_t>(m + 1);
+    w->err = cv.template take<int32_t>(64);
+    w->sort_bytes = radix_sort_workspace_bytes(m);
+    w->sort_ws = cv.template take<char>(w->sort_bytes);
+    w->scan_bytes = scan_workspace_bytes(m);
+    w->scan_ws = cv.template take<char>(w->scan_bytes);
+}
+
+struct NullCarver {
+    Sizer s;
+    template <typename T>
+    T* take(size_t k) {
+        s.take<T>(k);
+        return nullptr;
+    }
+};
+
+int check_graph(const grws_bcsr* A, const char* who) {
+    GRWS_CHECK_ARG(A != nullptr, "%s: null graph", who);
+    GRWS_CHECK_ARG(A->tile_rows == 16, "%s: tile_rows must be 16", who);
+    GRWS_CHECK_ARG(A->tile_cols == 8 || A->tile_cols == 16, "%s: tile_cols must be 8 or 16", who);
+    GRWS_CHECK_ARG(A->num_windows >= 0 && A->num_tiles >= 0, "%s: negative size", who);
+    if (A->values_dtype != GRWS_F32 && A->values_dtype != GRWS_F16 && A->values_dtype != GRWS_BF16)
+        return set_error(GRWS_E_DTYPE, "%s: unsupported values dtype %d", who, A->values_dtype);
+    GRWS_CHECK_ARG(A->window_offset != nullptr, "%s: null window_offset", who);
+    if (A->num_tiles > 0) GRWS_CHECK_ARG(A->col_indices && A->values, "%s: null arrays", who);
+    return GRWS_OK;
+}
+
+}  // namespace
+}  // namespace grws
+
+using namespace grws;
+
+extern "C" int32_t grws_window_sample_num(int32_t fanout) {
+    if (fanout < 1) return 0;
+    return ((fanout + 31) / 32) * 32;
+}
+
+extern "C" size_t grws_window_seeds_workspace_bytes(int64_t num_ids) {
+    if (num_ids < 0) return 0;
+    NullCarver nc;
+    SeedWs w;
+    carve_seed(nc, num_ids, &w);
+    return nc.s.used + 256;
+}
+
+extern "C" int grws_window_seeds(const int32_t* ids, int64_t num_ids, int64_t num_nodes, int32_t tile_rows,
+                                 int32_t drop_out_of_range, int32_t* active_windows, int32_t* masks,
+                                 void* workspace, size_t workspace_bytes, int64_t* num_active_out, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(num_ids >= 0 && num_nodes >= 0, "window_seeds: negative size");
+    GRWS_CHECK_ARG(tile_rows >= 1 && tile_rows <= 32, "window_seeds: tile_rows must be in [1, 32]");
+    GRWS_CHECK_ARG(num_ids <= (int64_t)UINT32_MAX, "window_seeds: too many ids");
+    GRWS_CHECK_ARG(num_active_out != nullptr, "window_seeds: null num_active_out");
+    *num_active_out = 0;
+    if (num_ids == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(ids && active_windows && masks, "window_seeds: null pointer");
+    Carver cv(workspace, workspace_bytes);
+    SeedWs w;
+    carve_seed(cv, num_ids, &w);
+    if (!cv.ok) return set_error(GRWS_E_CAPACITY, "window_seeds: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+    const int64_t W = (num_nodes + tile_rows - 1) / tile_rows;
+    const uint64_t sentinel = (uint64_t)W;
+    const int bits = bits_for(W + 1);
+    GRWS_TRY(fill_i32(w.err, 1, 0, stream));
+    GRWS_TRY(fill_i32(masks, num_ids, 0, stream));
+    hipLaunchKernelGGL(seed_keys_kernel, dim3(grid_for(num_ids)), dim3(kBlk), 0, stream, ids, num_ids, num_nodes,
+                       (int)tile_rows, (int)drop_out_of_range, sentinel, w.k, w.m, w.err);
+    GRWS_LAUNCH_CHECK();
+    bool alt = false;
+    GRWS_TRY(radix_sort_pairs(w.k, w.m, w.k2, w.m2, num_ids, bits, w.sort_ws, w.sort_bytes, stream, &alt));
+    const uint64_t* k = alt ? w.k2 : w.k;
+    const uint32_t* m = alt ? w.m2 : w.m;
+    hipLaunchKernelGGL(seed_heads_kernel, dim3(grid_for(num_ids)), dim3(kBlk), 0, stream, k, num_ids, sentinel, w.head);
+    GRWS_LAUNCH_CHECK();
+    GRWS_TRY(scan_i32_to_i64(w.head, w.rank, num_ids, false, w.scan_ws, w.scan_bytes, stream));
+    hipLaunchKernelGGL(seed_emit_kernel, dim3(grid_for(num_ids)), dim3(kBlk), 0, stream, k, m, num_ids, sentinel,
+                       w.head, w.rank, active_windows, masks);
+    GRWS_LAUNCH_CHECK();
+    int64_t na = 0;
+    int32_t e = 0;
+    GRWS_HIP(hipMemcpyAsync(&na, w.rank + num_ids, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipMemcpyAsync(&e, w.err, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipStreamSynchronize(stream));
+    if (e & kErrSeed) return set_error(GRWS_E_RANGE, "window_seeds: a seed id is outside [0, num_nodes) and not -1");
+    *num_active_out = na;
+    return GRWS_OK;
+}
+
+extern "C" size_t grws_window_topk_workspace_bytes(int64_t num_active) {
+    if (num_active < 0) return 0;
+    Sizer s;
+    s.take<int32_t>((size_t)num_active + 1);
+    s.take<int32_t>(64);
+    s.used += scan_workspace_bytes(num_active) + 256;
+    return s.used;
+}
+
+extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
+                                int32_t fanout, const grws_hacs* hacs, int32_t* sampled_cols,
+                                int32_t* sampled_slots, int64_t* out_window_offset, void* workspace,
+                                size_t workspace_bytes, int64_t* num_tiles_out, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_TRY(check_graph(A, "window_topk"));
+    GRWS_CHECK_ARG(num_active >= 0, "window_topk: negative num_active");
+    GRWS_CHECK_ARG(num_active <= INT32_MAX, "window_topk: too many active windows");
+    GRWS_CHECK_ARG(num_tiles_out && out_window_offset, "window_topk: null output");
+    const int S = grws_window_sample_num(fanout);
+    GRWS_CHECK_ARG(S >= 32 && S <= kMaxCap, "window_topk: fanout must be in [1, 256] (got %d)", fanout);
+    const int cap = S <= 32 ? 32 : (S <= 128 ? 128 : 256);
+    *num_tiles_out = 0;
+    if (num_active == 0) return fill_i64(out_window_offset, 1, 0, stream);
+    GRWS_CHECK_ARG(active_windows && sampled_cols && sampled_slots, "window_topk: null pointer");
+    ScoreParams p{};
+    p.alpha = 1.0f;
+    p.beta = 10.0f;
+    p.scale = 100.0f;
+    if (hacs && hacs->use_hacs) {
+        p.use_hacs = 1;
+        p.static_scores = hacs->static_scores;
+        p.num_static_scores = hacs->num_static_scores;
+        p.num_parts = hacs->num_parts;
+        p.alpha = hacs->alpha;
+        p.beta = hacs->beta;
+        p.delta = hacs->delta;
+        p.scale = hacs->score_scale;
+        p.gamma_int = hacs->gamma_bonus > 0.0f ? (int32_t)(hacs->gamma_bonus * hacs->score_scale) : 0;
+        p.locality = hacs->locality_enabled ? 1 : 0;
+        p.window_part_ids = hacs->window_part_ids;
+        p.part_starts = hacs->part_starts;
+        p.part_ends = hacs->part_ends;
+        GRWS_CHECK_ARG(p.static_scores != nullptr, "window_topk: HACS needs static_scores");
+        if (p.locality) {
+            GRWS_CHECK_ARG(p.window_part_ids && p.part_starts && p.part_ends,
+                           "window_topk: locality needs window_part_ids, part_starts and part_ends");
+            GRWS_CHECK_ARG(hacs->num_window_part_ids >= A->num_windows,
+                           "window_topk: window_part_ids has fewer entries than the graph has windows");
+        }
+    }
+    Carver cv(workspace, workspace_bytes);
+    int32_t* tiles = cv.take<int32_t>(num_active + 1);
+    int32_t* err = cv.take<int32_t>(64);
+    const size_t scan_bytes = scan_workspace_bytes(num_active);
+    char* scan_ws = cv.take<char>(scan_bytes);
+    if (!cv.ok) return set_error(GRWS_E_CAPACITY, "window_topk: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+    GRWS_TRY(fill_i32(err, 1, 0, stream));
+    switch (A->values_dtype) {
+        case GRWS_F32:
+            hipLaunchKernelGGL(window_topk_kernel<float>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
+                               A->window_offset, A->num_windows, A->col_indices, A->values, (int)A->tile_cols,
+                               active_windows, num_active, p, cap, S, sampled_cols, sampled_slots, tiles, err);
+            break;
+        case GRWS_F16:
+            hipLaunchKernelGGL(window_topk_kernel<_Float16>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
+                               A->window_offset, A->num_windows, A->col_indices, A->values, (int)A->tile_cols,
+                               active_windows, num_active, p, cap, S, sampled_cols, sampled_slots, tiles, err);
+            break;
+        default:
+            hipLaunchKernelGGL(window_topk_kernel<__hip_bfloat16>, dim3((unsigned)num_active), dim3(kBlk), 0,
+                               stream, A->window_offset, A->num_windows, A->col_indices, A->values,
+                               (int)A->tile_cols, active_windows, num_active, p, cap, S, sampled_cols, sampled_slots,
+                               tiles, err);
+            break;
+    }
+    GRWS_LAUNCH_CHECK();
+    GRWS_TRY(scan_i32_to_i64(tiles, out_window_offset, num_active, false, scan_ws, scan_bytes, stream));
+    int64_t T = 0;
+    int32_t e = 0;
+    GRWS_HIP(hipMemcpyAsync(&T, out_window_offset + num_active, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipMemcpyAsync(&e, err, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipStreamSynchronize(stream));
+    if (e & kErrWindow) return set_error(GRWS_E_RANGE, "window_topk: an active window is outside the graph");
+    if (e & kErrHacs)
+        return set_error(GRWS_E_RANGE, "window_topk: a column has no static score or a part id has no range");
+    *num_tiles_out = T;
+    return GRWS_OK;
+}
+
+extern "C" int grws_window_recompress(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
+                                      int32_t fanout, const int32_t* sampled_cols, const int32_t* sampled_slots,
+                                      const int64_t* out_window_offset, int64_t num_tiles, int32_t* out_cols,
+                                      void* out_values, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_TRY(check_graph(A, "window_recompress"));
+    GRWS_CHECK_ARG(num_active >= 0 && num_tiles >= 0, "window_recompress: negative size");
+    const int S = grws_window_sample_num(fanout);
+    GRWS_CHECK_ARG(S >= 32 && S <= kMaxCap, "window_recompress: fanout must be in [1, 256] (got %d)", fanout);
+    if (num_active == 0 || num_tiles == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(active_windows && sampled_cols && sampled_slots && out_window_offset && out_cols && out_values,
+                   "window_recompress: null pointer");
+    switch (A->values_dtype) {
+        case GRWS_F32:
+            hipLaunchKernelGGL(window_recompress_kernel<float>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
+                               A->window_offset, A->num_windows, A->values, (int)A->tile_cols, active_windows,
+                               num_active, S,
+                               sampled_cols, sampled_slots, out_window_offset, out_cols,
+                               static_cast<float*>(out_values));
+            break;
+        case GRWS_F16:
+            hipLaunchKernelGGL(window_recompress_kernel<_Float16>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
+                               A->window_offset, A->num_windows, A->values, (int)A->tile_cols, active_windows,
+                               num_active, S,
+                               sampled_cols, sampled_slots, out_window_offset, out_cols,
+                               static_cast<_Float16*>(out_values));
+            break;
+        default:
+            hipLaunchKernelGGL(window_recompress_kernel<uint16_t>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
+                               A->window_offset, A->num_windows, A->values, (int)A->tile_cols, active_windows,
+                               num_active, S,
+                               sampled_cols, sampled_slots, out_window_offset, out_cols,
+                               static_cast<uint16_t*>(out_values));
+            break;
+    }
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}

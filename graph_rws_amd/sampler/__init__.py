@@ -1,3 +1,4 @@
 from .neighbor import NeighborSampler  # noqa: F401
+from .sampler import BCSRSampler  # noqa: F401
 
-__all__ = ["NeighborSampler"]
+__all__ = ["BCSRSampler", "NeighborSampler"]

@@ -1,0 +1,112 @@
+"""BCSRSampler: the reference's window top-K multi-layer sampler
+(sampler/sampler.py:31-307) over the gfx950 kernels of
+csrc/window_sample.hip.
+
+Same constructor arguments, same ``sample_layers(g, seed_nodes)`` contract:
+one BCSRGraph per model layer, input side first.  Hop 0 runs from the seeds
+with the LAST fanout (``reversed(fanouts)``, sampler.py:204).  Each layer
+has ``num_rows = 16 * len(active_windows)`` and ``num_cols = g.num_cols``,
+and carries ``active_windows`` / ``active_masks``, which the model's reindex
+uses (models/model.py:126-143).  Column ids are global.
+"""
+from __future__ import annotations
+
+from typing import List
+
+import torch
+
+from ..core import sample_all_layers
+from ..data import BCSRGraph
+
+
+class BCSRSampler:
+    def __init__(self, fanouts: List[int], tile_rows: int = 16, tile_cols: int = 8,
+                 warps_per_block: int = 8, partition_book: list = None, verbose: bool = True,
+                 static_scores: torch.Tensor = None, window_part_ids: torch.Tensor = None,
+                 part_ranges: torch.Tensor = None, hacs_enabled: bool = False,
+                 alpha: float = 1.0, beta: float = 10.0, delta: float = 0.0,
+                 gamma_bonus: float = 0.0, score_scale: float = 100.0,
+                 locality_enabled: bool = False):
+        self.fanouts = list(fanouts)
+        self.tile_rows = tile_rows
+        self.tile_cols = tile_cols
+        self.warps_per_block = warps_per_block
+        self.partition_book = partition_book
+        self.verbose = verbose
+        self.time_tracker = {}
+        self.static_scores = static_scores
+        self.window_part_ids = window_part_ids
+        self.part_ranges = part_ranges
+        self.hacs_enabled = bool(hacs_enabled)
+        self.locality_enabled = bool(locality_enabled)
+        self.alpha = float(alpha)
+        self.beta = float(beta)
+        self.delta = float(delta)
+        self.gamma_bonus = float(gamma_bonus)
+        self.score_scale = float(score_scale)
+
+    def _hacs_args(self, device):
+        """(static_scores, window_part_ids, part_starts, part_ends, use_hacs,
+        locality) as the reference prepares them (sampler.py:101-151)."""
+        use_hacs = self.hacs_enabled and self.static_scores is not None
+        if not use_hacs:
+            return None, None, None, None, 0, 0
+        ss = torch.as_tensor(self.static_scores).to(device, torch.float32).contiguous()
+        loc = int(self.locality_enabled and self.window_part_ids is not None
+                  and self.part_ranges is not None)
+        if not loc:
+            return ss, None, None, None, 1, 0
+        wp = torch.as_tensor(self.window_part_ids).to(device, torch.int32).contiguous()
+        pr = torch.as_tensor(self.part_ranges).to(device, torch.int32)
+        return ss, wp, pr[:, 0].contiguous(), pr[:, 1].contiguous(), 1, 1
+
+    def sample_layers(self, g: BCSRGraph, seed_nodes: torch.Tensor) -> List[BCSRGraph]:
+        """Samples len(fanouts) layers from `seed_nodes` (global node ids)."""
+        device = g.window_offset.device if g.window_offset.is_cuda else torch.device("cuda")
+        seeds = torch.as_tensor(seed_nodes).to(device, torch.int32).contiguous()
+        ss, wp, ps, pe, use_hacs, loc = self._hacs_args(device)
+        layers_data, timings = sample_all_layers(
+            g.window_offset, g.original_col_indices, g.values_condensed, seeds,
+            list(reversed(self.fanouts)), int(g.num_nodes), ss, wp, ps, pe, self.alpha, self.beta,
+            self.delta, self.gamma_bonus, self.score_scale, use_hacs, loc, self.tile_rows,
+            self.tile_cols, self.warps_per_block)
+        if self.verbose:
+            n = len(self.fanouts)
+            for i, t in enumerate(timings):
+                st = self.time_tracker.setdefault(n - 1 - i, {"count": 0, "p1_sample": 0.0,
+                                                              "p2_map": 0.0, "p3_recomp": 0.0,
+                                                              "total": 0.0})
+                st["count"] += 1
+                st["p1_sample"] += t.phase1_sampling_time
+                st["p2_map"] += t.phase2_mapping_time
+                st["p3_recomp"] += t.phase3_recompression_time
+                st["total"] += t.total_time
+        layers: List[BCSRGraph] = []
+        for win, cols, vals, act, msk in layers_data:
+            sub = BCSRGraph.from_components(window_offset=win, original_col_indices=cols,
+                                            values_condensed=vals,
+                                            num_rows=int(act.numel()) * self.tile_rows,
+                                            num_cols=g.num_cols, tile_rows=self.tile_rows,
+                                            tile_cols=self.tile_cols, device=win.device)
+            sub.active_windows = act
+            sub.active_masks = msk
+            layers.insert(0, sub)
+        return layers
+
+    def print_avg_timing(self):
+        print("\n" + "-" * 60)
+        print(" [Average Sampling Performance Summary (All Epochs)]")
+        print("-" * 60)
+        for layer_id in sorted(self.time_tracker):
+            st = self.time_tracker[layer_id]
+            c = st["count"]
+            if c == 0:
+                continue
+            print(f"  [Layer {layer_id}] select {st['p1_sample'] / c:8.3f} ms | "
+                  f"map {st['p2_map'] / c:8.3f} ms | recompress {st['p3_recomp'] / c:8.3f} ms | "
+                  f"total {st['total'] / c:8.3f} ms")
+
+    def __repr__(self):
+        # the reference reads a missing self._bcsr_cache here (sampler.py:281-284)
+        return (f"BCSRSampler(fanouts={self.fanouts}, tile={self.tile_rows}x{self.tile_cols}, "
+                f"warps_per_block={self.warps_per_block})")

@@ -256,6 +256,67 @@ int grws_sample_hop(const int64_t* indptr, const int32_t* indices, int64_t num_n
 /* next_capacity >= num_frontier + num_edges).  Frontier ids must be         */
 /* distinct (GRWS_E_INVALID otherwise).  Synchronises `stream`.              */
 /* ------------------------------------------------------------------------ */
+/* ------------------------------------------------------------------------ */
+/* Window top-K sampling: the reference-compatible core_lib.sample_all_layers */
+/* (bind.cpp:99-121 -> sampling_wrapper.cu:365-438), one call per phase.     */
+/* ------------------------------------------------------------------------ */
+
+/* HACS scoring parameters (sampler/sampler.py:101-151, sampling.cuh:251-    */
+/* 270).  Pass NULL or use_hacs = 0 for the default score                   */
+/* trunc((1 + 10|v|) * 1000).  Device arrays; the counts bound every lookup. */
+typedef struct grws_hacs {
+    const float* static_scores;     /* [num_static_scores], indexed by column */
+    const int32_t* window_part_ids; /* [num_window_part_ids] part of each window or -1 */
+    const int32_t* part_starts;     /* [num_parts] first column of each part */
+    const int32_t* part_ends;       /* [num_parts] one past its last column */
+    int64_t num_static_scores;
+    int64_t num_window_part_ids;
+    int64_t num_parts;
+    float alpha, beta, delta, gamma_bonus, score_scale;
+    int32_t use_hacs;
+    int32_t locality_enabled;
+} grws_hacs;
+
+/* S = roundup32(fanout), the reference's per-window output stride         */
+/* (sampling_wrapper.cu:88).                                                 */
+int32_t grws_window_sample_num(int32_t fanout);
+
+/* Seeds -> sorted unique active windows and OR-ed row masks, replacing     */
+/* prepare_windows_and_masks (sampling_wrapper.cu:283-347): id -> (id / tile_rows, */
+/* 1 << id % tile_rows); -1 is skipped.  Other ids outside [0, num_nodes)    */
+/* are skipped when drop_out_of_range != 0 (the inter-hop filter of         */
+/* sampling_wrapper.cu:424-429) and are GRWS_E_RANGE otherwise.  Outputs    */
+/* hold num_ids entries; *num_active_out = windows written.  Synchronises.  */
+size_t grws_window_seeds_workspace_bytes(int64_t num_ids);
+int grws_window_seeds(const int32_t* ids, int64_t num_ids, int64_t num_nodes, int32_t tile_rows,
+                      int32_t drop_out_of_range, int32_t* active_windows, int32_t* masks,
+                      void* workspace, size_t workspace_bytes, int64_t* num_active_out,
+                      void* stream);
+
+/* Phase 1 + 2, replacing warp_centric_find_top_k_kernel (sampling.cuh:65-  */
+/* 448) and the tile-count scan (sampling_wrapper.cu:160-177): per active    */
+/* window, the columns ranked by the reference's score, top-CAP by (total    */
+/* desc, column asc) with CAP = 32/128/256 for S <= 32/128/256, re-sorted    */
+/* ascending, first min(kept, S) kept.  Writes sampled_cols [num_active * S] */
+/* (-1 padded), sampled_slots [num_active * S] (the column's slot index in   */
+/* its input window), out_window_offset [num_active+1] int64; synchronises   */
+/* and returns the output tile count.  fanout in [1, 256].                   */
+size_t grws_window_topk_workspace_bytes(int64_t num_active);
+int grws_window_topk(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
+                     int32_t fanout, const grws_hacs* hacs, int32_t* sampled_cols,
+                     int32_t* sampled_slots, int64_t* out_window_offset, void* workspace,
+                     size_t workspace_bytes, int64_t* num_tiles_out, void* stream);
+
+/* Phase 3, replacing build_col_to_val_map_kernel + recompress_sampled_bcsr */
+/* _kernel (sampling.cuh:471-579, 707-773): out_cols [num_tiles*tile_cols]   */
+/* and out_values [num_tiles*16*tile_cols] in A's values dtype, sized        */
+/* exactly (the reference over-allocates and pre-fills -1 / -1.0,           */
+/* sampling_wrapper.cu:215-218).                                             */
+int grws_window_recompress(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
+                           int32_t fanout, const int32_t* sampled_cols,
+                           const int32_t* sampled_slots, const int64_t* out_window_offset,
+                           int64_t num_tiles, int32_t* out_cols, void* out_values, void* stream);
+
 size_t grws_relabel_workspace_bytes(int64_t num_frontier, int64_t num_edges);
 int grws_relabel(const int64_t* frontier, int64_t num_frontier, const int64_t* edge_src,
                  int64_t num_edges, int64_t num_nodes, int32_t* src_local, int64_t* next_frontier,

@@ -351,3 +351,95 @@ def sample_blocks(indptr, indices, seeds, fanouts, seed: int = 42, tile_cols: in
                            vals=vals.astype(np.float32)))
         frontier = nxt
     return out
+
+
+# ----------------------------------------------------------------------------
+# window top-K sampling (sampling.cuh:65-579, sampling_wrapper.cu:58-438)
+# ----------------------------------------------------------------------------
+class _Hacs(ctypes.Structure):
+    _fields_ = [("static_scores", ctypes.c_void_p), ("window_part_ids", ctypes.c_void_p),
+                ("part_starts", ctypes.c_void_p), ("part_ends", ctypes.c_void_p),
+                ("alpha", ctypes.c_float), ("beta", ctypes.c_float), ("delta", ctypes.c_float),
+                ("gamma_bonus", ctypes.c_float), ("score_scale", ctypes.c_float),
+                ("use_hacs", ctypes.c_int32), ("locality_enabled", ctypes.c_int32)]
+
+
+def _window_lib():
+    L = lib()
+    if not getattr(L, "_window_protos", False):
+        L.orc_window_topk.restype = None
+        L.orc_window_topk.argtypes = [_i64p, _i32p, _f32p, ctypes.c_int32, _i32p, ctypes.c_int64,
+                                      ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, _i32p, _i32p]
+        L.orc_window_recompress.restype = None
+        L.orc_window_recompress.argtypes = [_i64p, _i32p, _f32p, ctypes.c_int64, ctypes.c_int32,
+                                            _i32p, ctypes.c_int64, ctypes.c_int32, _i32p, _i64p,
+                                            _i32p, _f32p]
+        L.orc_prepare_windows.restype = ctypes.c_int64
+        L.orc_prepare_windows.argtypes = [_i32p, ctypes.c_int64, ctypes.c_int32, _i32p, _i32p]
+        L._window_protos = True
+    return L
+
+
+def prepare_windows(seeds, tile_rows: int = 16):
+    """(active_windows int32, masks int32) of seed ids (sampling_wrapper.cu:283-347)."""
+    s = _c(seeds, np.int32)
+    w = np.empty(max(1, s.size), np.int32)
+    m = np.empty(max(1, s.size), np.int32)
+    n = _window_lib().orc_prepare_windows(_p(s, _i32p), s.size, tile_rows, _p(w, _i32p), _p(m, _i32p))
+    return w[:n].copy(), m[:n].copy()
+
+
+def window_sample_layer(win, cols, vals, active, fanout: int, tile_cols: int = 8,
+                        warps_per_block: int = 8, hacs: Optional[dict] = None):
+    """One layer of the reference's window sampler.  Returns (out_win int64,
+    out_cols int32, out_vals float32), sized exactly."""
+    win = _c(win, np.int64); cols = _c(cols, np.int32); vals = _c(vals, np.float32)
+    act = _c(active, np.int32)
+    A = act.size
+    S = ((fanout + 31) // 32) * 32
+    sampled = np.empty(max(1, A * S), np.int32)
+    tiles = np.empty(max(1, A), np.int32)
+    keep = []
+    hp = None
+    if hacs is not None:
+        arrs = {k: (None if hacs.get(k) is None else
+                    _c(hacs[k], np.float32 if k == "static_scores" else np.int32))
+                for k in ("static_scores", "window_part_ids", "part_starts", "part_ends")}
+        keep = [a for a in arrs.values() if a is not None]
+        h = _Hacs(*(None if arrs[k] is None else arrs[k].ctypes.data
+                    for k in ("static_scores", "window_part_ids", "part_starts", "part_ends")),
+                  hacs.get("alpha", 1.0), hacs.get("beta", 10.0), hacs.get("delta", 0.0),
+                  hacs.get("gamma_bonus", 0.0), hacs.get("score_scale", 100.0),
+                  int(hacs.get("use_hacs", 1)), int(hacs.get("locality_enabled", 0)))
+        hp = ctypes.byref(h)
+    _window_lib().orc_window_topk(_p(win, _i64p), _p(cols, _i32p), _p(vals, _f32p), tile_cols,
+                                  _p(act, _i32p), A, fanout, warps_per_block, hp,
+                                  _p(sampled, _i32p), _p(tiles, _i32p))
+    del keep
+    out_win = np.zeros(A + 1, np.int64)
+    out_win[1:] = np.cumsum(tiles[:A])
+    T = int(out_win[-1])
+    oc = np.empty(max(1, T * tile_cols), np.int32)
+    ov = np.empty(max(1, T * 16 * tile_cols), np.float32)
+    _window_lib().orc_window_recompress(_p(win, _i64p), _p(cols, _i32p), _p(vals, _f32p), vals.size,
+                                        tile_cols, _p(act, _i32p), A, fanout, _p(sampled, _i32p),
+                                        _p(out_win, _i64p), _p(oc, _i32p), _p(ov, _f32p))
+    return out_win, oc[:T * tile_cols].copy(), ov[:T * 16 * tile_cols].copy(), sampled[:A * S].reshape(A, S)
+
+
+def window_sample_all_layers(win, cols, vals, seeds, fanouts, num_global_nodes: int,
+                             tile_cols: int = 8, warps_per_block: int = 8,
+                             hacs: Optional[dict] = None):
+    """bcsr_sample_all_layers_wrapper (sampling_wrapper.cu:365-438): layers in
+    sampling order, each [out_win, out_cols, out_vals, active, masks]."""
+    active, masks = prepare_windows(seeds)
+    out = []
+    for i, f in enumerate(fanouts):
+        ow, oc, ov, _ = window_sample_layer(win, cols, vals, active, f, tile_cols,
+                                            warps_per_block, hacs)
+        out.append([ow, oc, ov, active, masks])
+        if i + 1 < len(fanouts):
+            nxt = oc.copy()
+            nxt[(nxt < 0) | (nxt >= num_global_nodes)] = -1
+            active, masks = prepare_windows(nxt)
+    return out

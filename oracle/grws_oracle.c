@@ -388,6 +388,206 @@ ORC_API int64_t orc_relabel(const int64_t* frontier, int64_t F, const int64_t* e
     return n;
 }
 
+/* ------------------------------------------------------------------------ */
+/* Window top-K sampling  (sampling.cuh:65-579, 707-773;                    */
+/* sampling_wrapper.cu:58-347), restated step by step as the reference      */
+/* executes it: per batch of warps_per_block tiles, per-tile candidate lists */
+/* in element order, a single-threaded merge into the window list, a sort   */
+/* by (total desc, column asc) with (INT_MAX, 0) padding, truncation to     */
+/* CAP; finally an ascending sort by column and the first min(cnt, S).      */
+/* ------------------------------------------------------------------------ */
+
+/* C's (int) of a float as a GPU converts it (cvt.rzi.s32.f32 /             */
+/* v_cvt_i32_f32): toward zero, saturating, NaN -> 0.                        */
+static int32_t f2i_sat(float x) {
+    if (x != x) return 0;
+    if (x >= 2147483648.0f) return INT32_MAX;
+    if (x <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)x;
+}
+
+typedef struct { int32_t col; int32_t freq; } orc_cand;
+
+/* ColumnCandidateComparator (sampling_helper.h:28-34) */
+static int cmp_cand(const void* a, const void* b) {
+    const orc_cand* x = (const orc_cand*)a;
+    const orc_cand* y = (const orc_cand*)b;
+    if (x->freq != y->freq) return x->freq > y->freq ? -1 : 1;
+    return (x->col > y->col) - (x->col < y->col);
+}
+
+static int32_t wrap_add(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+
+typedef struct {
+    const float* static_scores;
+    const int32_t* window_part_ids;
+    const int32_t* part_starts;
+    const int32_t* part_ends;
+    float alpha, beta, delta, gamma_bonus, score_scale;
+    int32_t use_hacs, locality_enabled;
+} orc_hacs;
+
+/* Score of one element (sampling.cuh:251-275). */
+static int32_t elem_score(const orc_hacs* h, int32_t window, int32_t col, float v) {
+    if (h && h->use_hacs) {
+        float q = h->static_scores ? h->static_scores[col] : 1.0f;
+        float f = fmaf(h->beta, fabsf(v), h->alpha) * q;
+        if (h->locality_enabled && h->window_part_ids && h->part_starts && h->part_ends) {
+            int32_t pid = h->window_part_ids[window];
+            if (pid >= 0 && col >= h->part_starts[pid] && col < h->part_ends[pid]) f += h->delta;
+        }
+        return f2i_sat(f * h->score_scale);
+    }
+    return f2i_sat(fmaf(10.0f, fabsf(v), 1.0f) * 1000.0f);
+}
+
+ORC_API int32_t orc_window_cap(int32_t S) { return S <= 32 ? 32 : (S <= 128 ? 128 : 256); }
+
+/* Candidate buffer size of the reference kernel (sampling.cuh:128-139). */
+static int32_t global_buffer(int32_t cap, int32_t warps, int32_t tile_cols) {
+    int32_t block = warps * 32;
+    int32_t max_items = cap + warps * 16 * tile_cols;
+    int32_t raw = (max_items + block - 1) / block;
+    int32_t ipt = raw <= 1 ? 1 : raw <= 2 ? 2 : raw <= 4 ? 4 : raw <= 8 ? 8 : 16;
+    return ipt * block;
+}
+
+/* Phase 1 for every active window.  sampled [A*S] (-1 padded), tiles [A]. */
+ORC_API void orc_window_topk(const int64_t* win_off, const int32_t* cols, const float* vals,
+                             int32_t tile_cols, const int32_t* active, int64_t A, int32_t fanout,
+                             int32_t warps, const orc_hacs* h, int32_t* sampled, int32_t* tiles) {
+    const int32_t S = ((fanout + 31) / 32) * 32;
+    const int32_t cap = orc_window_cap(S);
+    const int32_t G = global_buffer(cap, warps, tile_cols);
+    const int32_t per_tile = 16 * tile_cols;
+    const int32_t gamma_int = (h && h->use_hacs && h->gamma_bonus > 0.0f)
+                                  ? (int32_t)(h->gamma_bonus * h->score_scale) : 0;
+    orc_cand* glob = (orc_cand*)malloc(sizeof(orc_cand) * (size_t)G);
+    orc_cand* wl = (orc_cand*)malloc(sizeof(orc_cand) * (size_t)warps * per_tile);
+    int32_t* wcnt = (int32_t*)malloc(sizeof(int32_t) * (size_t)warps);
+    int32_t* keys = (int32_t*)malloc(sizeof(int32_t) * (size_t)G);
+    for (int64_t b = 0; b < A; ++b) {
+        const int32_t w = active[b];
+        const int64_t t0 = win_off[w], total = win_off[w + 1] - t0;
+        int32_t* out = sampled + b * S;
+        if (total == 0) {
+            for (int32_t i = 0; i < S; ++i) out[i] = -1;
+            tiles[b] = 0;
+            continue;
+        }
+        int32_t gcnt = 0;
+        for (int64_t bs = 0; bs < total; bs += warps) {
+            int32_t bt = (int32_t)(total - bs < warps ? total - bs : warps);
+            for (int32_t j = 0; j < bt; ++j) {
+                const int64_t tile = t0 + bs + j;
+                orc_cand* L = wl + (size_t)j * per_tile;
+                wcnt[j] = 0;
+                for (int32_t off = 0; off < per_tile; ++off) { /* lanes in order, elements in order */
+                    const int32_t r = off / tile_cols, c = off % tile_cols;
+                    const int32_t col = cols[tile * tile_cols + c];
+                    if (col == -1) continue;
+                    const int32_t sc = elem_score(h, w, col, vals[tile * per_tile + r * tile_cols + c]);
+                    if (sc <= 0) continue;
+                    int32_t i = 0;
+                    for (; i < wcnt[j]; ++i) if (L[i].col == col) { L[i].freq = wrap_add(L[i].freq, sc); break; }
+                    if (i == wcnt[j] && wcnt[j] < per_tile) { L[wcnt[j]].col = col; L[wcnt[j]].freq = sc; wcnt[j]++; }
+                }
+            }
+            /* single-threaded merge (sampling.cuh:306-344) */
+            for (int32_t j = 0; j < bt && gcnt < G; ++j) {
+                const orc_cand* L = wl + (size_t)j * per_tile;
+                for (int32_t i = 0; i < wcnt[j]; ++i) {
+                    if (gcnt >= G) break;
+                    int32_t k = 0;
+                    for (; k < gcnt; ++k) if (glob[k].col == L[i].col) { glob[k].freq = wrap_add(glob[k].freq, L[i].freq); break; }
+                    if (k == gcnt && gcnt < G) {
+                        glob[gcnt].col = L[i].col;
+                        glob[gcnt].freq = wrap_add(L[i].freq, gamma_int);
+                        gcnt++;
+                    }
+                }
+            }
+            if (gcnt > 1) { /* sort with (INT_MAX, 0) padding over the block's G slots */
+                for (int32_t k = gcnt; k < G; ++k) { glob[k].col = INT32_MAX; glob[k].freq = 0; }
+                qsort(glob, (size_t)G, sizeof(orc_cand), cmp_cand);
+            }
+            if (gcnt > cap) gcnt = cap;
+        }
+        if (gcnt > 1) {
+            for (int32_t k = 0; k < gcnt; ++k) keys[k] = glob[k].col;
+            qsort(keys, (size_t)gcnt, sizeof(int32_t), cmp_i32);
+            for (int32_t k = 0; k < gcnt; ++k) glob[k].col = keys[k];
+        }
+        const int32_t valid = gcnt < S ? gcnt : S;
+        tiles[b] = (valid + tile_cols - 1) / tile_cols;
+        for (int32_t i = 0; i < S; ++i) out[i] = i < valid ? glob[i].col : -1;
+    }
+    free(glob); free(wl); free(wcnt); free(keys);
+}
+
+/* Phases 2-3: values of the sampled columns (build_col_to_val_map_kernel's */
+/* linear search, sampling.cuh:707-773; recompress_sampled_bcsr_kernel,    */
+/* :471-579).  out_off [A+1] is the prefix sum of tiles; out_cols / out_vals */
+/* are written for every output tile. */
+ORC_API void orc_window_recompress(const int64_t* win_off, const int32_t* cols, const float* vals,
+                                   int64_t num_entries, int32_t tile_cols, const int32_t* active,
+                                   int64_t A, int32_t fanout, const int32_t* sampled,
+                                   const int64_t* out_off, int32_t* out_cols, float* out_vals) {
+    const int32_t S = ((fanout + 31) / 32) * 32;
+    const int32_t per_tile = 16 * tile_cols;
+    for (int64_t b = 0; b < A; ++b) {
+        const int32_t w = active[b];
+        const int64_t t0 = win_off[w], t1 = win_off[w + 1];
+        for (int64_t t = 0; t < out_off[b + 1] - out_off[b]; ++t) {
+            const int64_t ot = out_off[b] + t;
+            for (int32_t c = 0; c < tile_cols; ++c) {
+                const int64_t j = t * tile_cols + c;
+                const int32_t col = j < S ? sampled[b * S + j] : -1;
+                out_cols[ot * tile_cols + c] = col;
+                int64_t map_tile = -1; int32_t map_c = -1;
+                if (col != -1) {
+                    for (int64_t it = t0; it < t1 && map_tile < 0; ++it)
+                        for (int32_t cc = 0; cc < tile_cols; ++cc)
+                            if (cols[it * tile_cols + cc] == col) { map_tile = it - t0; map_c = cc; break; }
+                }
+                for (int32_t r = 0; r < 16; ++r) {
+                    float v = 0.0f;
+                    if (map_tile >= 0) {
+                        int64_t idx = (t0 + map_tile) * per_tile + (int64_t)r * tile_cols + map_c;
+                        if (idx < num_entries) v = vals[idx];
+                    }
+                    out_vals[ot * per_tile + (int64_t)r * tile_cols + c] = v;
+                }
+            }
+        }
+    }
+}
+
+/* prepare_windows_and_masks (sampling_wrapper.cu:283-347): seeds -> sorted */
+/* unique windows with OR-ed masks; -1 dropped.  Returns the window count.   */
+typedef struct { int32_t w; uint32_t m; } orc_wm;
+static int cmp_wm(const void* a, const void* b) {
+    int32_t x = ((const orc_wm*)a)->w, y = ((const orc_wm*)b)->w;
+    return (x > y) - (x < y);
+}
+ORC_API int64_t orc_prepare_windows(const int32_t* seeds, int64_t n, int32_t tile_rows,
+                                    int32_t* windows, int32_t* masks) {
+    orc_wm* t = (orc_wm*)malloc(sizeof(orc_wm) * (size_t)(n > 0 ? n : 1));
+    for (int64_t i = 0; i < n; ++i) {
+        if (seeds[i] == -1) { t[i].w = INT32_MAX; t[i].m = 0; }
+        else { t[i].w = seeds[i] / tile_rows; t[i].m = 1u << (seeds[i] % tile_rows); }
+    }
+    qsort(t, (size_t)n, sizeof(orc_wm), cmp_wm);
+    int64_t na = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        if (na > 0 && windows[na - 1] == t[i].w) { masks[na - 1] = (int32_t)((uint32_t)masks[na - 1] | t[i].m); continue; }
+        windows[na] = t[i].w; masks[na] = (int32_t)t[i].m; na++;
+    }
+    if (na > 0 && windows[na - 1] == INT32_MAX) na--;
+    free(t);
+    return na;
+}
+
 ORC_API int orc_num_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

@@ -307,3 +307,136 @@ def test_sample_blocks_structure():
         E = np.zeros_like(D)
         E[b["dst"], b["src_local"]] = b["val"]
         np.testing.assert_array_equal(D, E)
+
+
+# --- window top-K sampling (sampling.cuh:65-579) ------------------------------
+def _window_graph(col_lists, vals_per_col, tc=8):
+    """BCSR with one window per entry of col_lists: each column's 16 values
+    given by vals_per_col[col] (scalar -> all rows)."""
+    win = [0]
+    cols, vals = [], []
+    for cl in col_lists:
+        cl = sorted(cl)
+        nt = (len(cl) + tc - 1) // tc
+        for t in range(nt):
+            cc = cl[t * tc:(t + 1) * tc] + [-1] * (tc - len(cl[t * tc:(t + 1) * tc]))
+            cols += cc
+            tile = np.zeros((16, tc), np.float32)
+            for c, col in enumerate(cc):
+                if col >= 0:
+                    tile[:, c] = vals_per_col[col]
+            vals += tile.ravel().tolist()
+        win.append(win[-1] + nt)
+    return np.array(win, np.int64), np.array(cols, np.int32), np.array(vals, np.float32)
+
+
+def _exact_score(v):  # (1 + 10|v|) * 1000 for v = k/16: exact in float
+    return int(round((1 + 10 * abs(v)) * 1000))
+
+
+def test_window_topk_known_answer_cap32():
+    # 40 candidates, fanout 10 -> S = 32 = CAP: the 8 lowest totals drop out
+    cols = list(range(100, 140))
+    v = {c: ((c * 7) % 40) / 16.0 for c in cols}   # distinct k/16 per column
+    v[105] = v[106]                                   # one tie: lower column wins
+    win, ci, va = _window_graph([cols], v)
+    out_win, oc, ov, sampled = oracle.window_sample_layer(win, ci, va, [0], 10)
+    total = {c: 16 * _exact_score(v[c]) for c in cols}
+    top = sorted(cols, key=lambda c: (-total[c], c))[:32]
+    assert sampled[0].tolist() == sorted(top)
+    assert out_win.tolist() == [0, 4]
+    # values of an output column are that column's values in the input
+    for t in range(4):
+        for c in range(8):
+            col = oc[t * 8 + c]
+            np.testing.assert_array_equal(ov[t * 128 + c:(t + 1) * 128:8],
+                                          np.full(16, v[col], np.float32))
+
+
+def test_window_topk_capacity_quirk():
+    # fanout 40 -> S = 64, CAP = 128: the output is the 64 SMALLEST column ids
+    # of the top-128 by total, not the top-64 (sampling.cuh:396-447)
+    cols = list(range(150))
+    v = {c: (0.0 if c < 22 else (c % 30 + 1) / 16.0) for c in cols}
+    win, ci, va = _window_graph([cols], v)
+    _, _, _, sampled = oracle.window_sample_layer(win, ci, va, [0], 40)
+    total = {c: 16 * _exact_score(v[c]) for c in cols}
+    top128 = sorted(cols, key=lambda c: (-total[c], c))[:128]
+    assert set(range(22)).isdisjoint(top128)
+    assert sampled[0].tolist() == sorted(top128)[:64] == list(range(22, 86))
+
+
+def test_window_topk_zero_values_score_and_empty_window():
+    # zero entries still score 1000 each (sampling.cuh:273-274)
+    win, ci, va = _window_graph([[3, 9], [], [1]], {3: 0.0, 9: 0.0, 1: 0.5})
+    out_win, oc, ov, sampled = oracle.window_sample_layer(win, ci, va, [0, 1, 2], 3)
+    assert sampled[0][:3].tolist() == [3, 9, -1]
+    assert (sampled[1] == -1).all()
+    assert out_win.tolist() == [0, 1, 1, 2]
+
+
+def test_window_topk_hacs_and_locality():
+    cols = [4, 5, 6, 7, 20, 21]
+    v = {c: 0.5 for c in cols}
+    q = np.zeros(32, np.float32)
+    q[[4, 5, 6, 20, 21]] = [0.25, 0.5, 1.0, 0.25, 0.75]      # column 7: q = 0, outside the part
+    win, ci, va = _window_graph([cols], v)
+    hacs = dict(static_scores=q, window_part_ids=np.array([0], np.int32),
+                part_starts=np.array([0], np.int32), part_ends=np.array([7], np.int32),
+                alpha=1.0, beta=2.0, delta=0.5, gamma_bonus=0.37, score_scale=100.0,
+                use_hacs=1, locality_enabled=1)
+    _, _, _, sampled = oracle.window_sample_layer(win, ci, va, [0], 3, hacs=hacs)
+    f32 = np.float32
+    gamma = int(f32(0.37) * f32(100.0))
+    def tot(c):
+        f = (f32(1.0) + f32(2.0) * f32(0.5)) * q[c]          # fma of exact values
+        if c < 7:                                              # in the window's part
+            f = f32(f + f32(0.5))
+        s = int(f32(f * f32(100.0)))
+        return 16 * s + gamma if s > 0 else None
+    cand = [c for c in cols if tot(c) is not None]
+    assert 7 not in cand
+    top = sorted(cand, key=lambda c: (-tot(c), c))[:32]
+    assert sampled[0][:len(top)].tolist() == sorted(top)
+
+
+def test_window_topk_batches_equal_global_topk():
+    """The reference truncates per batch of warps_per_block tiles; with unique
+    columns per window that equals one global top-CAP.  Random windows,
+    random values: the oracle's batch-wise restatement (warps 4 and 8) ==
+    a plain global selection written here."""
+    rng = np.random.default_rng(11)
+    col_lists, v = [], {}
+    for w in range(12):
+        n = int(rng.integers(0, 400))
+        cl = sorted(rng.choice(5000, n, replace=False).tolist())
+        col_lists.append(cl)
+    win, ci, va = _window_graph(col_lists, {c: 0.0 for c in range(5000)})
+    va = (rng.integers(-64, 64, va.size) / 16.0).astype(np.float32) * (va == 0)
+    va[np.repeat(ci, 16).reshape(-1, 8, 16).transpose(0, 2, 1).ravel() < 0] = 0
+    for fanout in (5, 32, 40, 100, 128, 129, 256):
+        S = ((fanout + 31) // 32) * 32
+        cap = 32 if S <= 32 else (128 if S <= 128 else 256)
+        r8 = oracle.window_sample_layer(win, ci, va, np.arange(12), fanout, warps_per_block=8)[3]
+        r4 = oracle.window_sample_layer(win, ci, va, np.arange(12), fanout, warps_per_block=4)[3]
+        np.testing.assert_array_equal(r8, r4)
+        for w in range(12):
+            t0, t1 = win[w], win[w + 1]
+            tot = {}
+            for t in range(t0, t1):
+                for c in range(8):
+                    col = ci[t * 8 + c]
+                    if col < 0:
+                        continue
+                    s = [_exact_score(x) for x in va[t * 128 + c:(t + 1) * 128:8]]
+                    tot[col] = sum(s)
+            top = sorted(sorted(tot, key=lambda c: (-tot[c], c))[:cap])[:S]
+            assert r8[w].tolist() == top + [-1] * (S - len(top)), (fanout, w)
+
+
+def test_prepare_windows_known_answer():
+    w, m = oracle.prepare_windows([5, 17, 3, -1, 40, 18, 5])
+    assert w.tolist() == [0, 1, 2]
+    assert m.tolist() == [(1 << 5) | (1 << 3), (1 << 1) | (1 << 2), 1 << 8]
+    w, m = oracle.prepare_windows([-1, -1])
+    assert w.size == 0

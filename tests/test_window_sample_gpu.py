@@ -1,0 +1,156 @@
+"""Window top-K sampler on the GPU (csrc/window_sample.hip) against the CPU
+restatement of the reference's sampling kernels, bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from graph_rws_amd import synth
+from graph_rws_amd.core import sample_all_layers, window_seeds
+from graph_rws_amd.core._lib import GrwsError
+from graph_rws_amd.data import BCSRGraph
+from graph_rws_amd.sampler import BCSRSampler
+
+pytestmark = pytest.mark.gpu
+
+
+def _graph(name, dev, tc=8, scale=1.0, vdt=torch.float32):
+    g = synth.config_graph(name, scale=scale)
+    G = BCSRGraph.from_csr(g.row_ptr, g.col_idx, g.values, g.num_nodes, g.num_nodes,
+                           tile_cols=tc, device=dev, values_dtype=vdt)
+    return g, G
+
+
+def _compare(layers, ref, vdt=torch.float32):
+    assert len(layers) == len(ref)
+    for got, want in zip(layers, ref):
+        ow, oc, ov, act, msk = got
+        rw, rc, rv, ract, rmsk = want
+        np.testing.assert_array_equal(act.cpu().numpy(), ract)
+        np.testing.assert_array_equal(msk.cpu().numpy(), rmsk)
+        np.testing.assert_array_equal(ow.cpu().numpy(), rw)
+        np.testing.assert_array_equal(oc.cpu().numpy(), rc)
+        assert torch.equal(ov.cpu(), torch.from_numpy(rv).to(vdt))
+
+
+@pytest.mark.parametrize("fanouts", [[5], [10, 10], [15, 10, 5], [32, 40], [100, 129], [256]])
+def test_sample_all_layers_c1_bit_exact(cuda_device, fanouts):
+    g, G = _graph("c1", cuda_device)
+    seeds = np.random.default_rng(len(fanouts)).choice(g.num_nodes, 300, replace=False)
+    layers, timings = sample_all_layers(G.window_offset, G.original_col_indices,
+                                        G.values_condensed, torch.from_numpy(seeds).to(cuda_device),
+                                        fanouts, g.num_nodes, None, None, None, None)
+    ref = oracle.window_sample_all_layers(G.window_offset.cpu().numpy(),
+                                          G.original_col_indices.cpu().numpy(),
+                                          G.values_condensed.cpu().numpy(), seeds, fanouts,
+                                          g.num_nodes)
+    _compare(layers, ref)
+    assert len(timings) == len(fanouts) and all(t.total_time >= 0 for t in timings)
+
+
+def test_sample_all_layers_c2_full_size(cuda_device):
+    """1,024 seeds over the full c2 graph (169k nodes), fanouts [15,10,5] in
+    the reference's sampling order (5 first)."""
+    g, G = _graph("c2", cuda_device)
+    seeds = synth.distinct_seeds(g.num_nodes, 1024, seed=3).numpy()
+    layers, _ = sample_all_layers(G.window_offset, G.original_col_indices, G.values_condensed,
+                                  torch.from_numpy(seeds).to(cuda_device), [5, 10, 15],
+                                  g.num_nodes)
+    ref = oracle.window_sample_all_layers(G.window_offset.cpu().numpy(),
+                                          G.original_col_indices.cpu().numpy(),
+                                          G.values_condensed.cpu().numpy(), seeds, [5, 10, 15],
+                                          g.num_nodes)
+    _compare(layers, ref)
+
+
+def test_sample_all_layers_c3_dense_windows(cuda_device):
+    """Dense community windows (thousands of candidate columns per window):
+    the radix select resolves many equal totals by column."""
+    g, G = _graph("c3", cuda_device, scale=0.02)
+    seeds = synth.distinct_seeds(g.num_nodes, 256, seed=5).numpy()
+    for fanouts in ([10, 25], [100], [200]):
+        layers, _ = sample_all_layers(G.window_offset, G.original_col_indices,
+                                      G.values_condensed, torch.from_numpy(seeds).to(cuda_device),
+                                      fanouts, g.num_nodes)
+        ref = oracle.window_sample_all_layers(G.window_offset.cpu().numpy(),
+                                              G.original_col_indices.cpu().numpy(),
+                                              G.values_condensed.cpu().numpy(), seeds, fanouts,
+                                              g.num_nodes)
+        _compare(layers, ref)
+
+
+@pytest.mark.parametrize("vdt", [torch.float16, torch.bfloat16])
+def test_sample_all_layers_low_precision_values(cuda_device, vdt):
+    g, G = _graph("c1", cuda_device, vdt=vdt)
+    seeds = np.arange(0, g.num_nodes, 5)
+    layers, _ = sample_all_layers(G.window_offset, G.original_col_indices, G.values_condensed,
+                                  torch.from_numpy(seeds).to(cuda_device), [20, 7], g.num_nodes)
+    ref = oracle.window_sample_all_layers(G.window_offset.cpu().numpy(),
+                                          G.original_col_indices.cpu().numpy(),
+                                          G.values_condensed.float().cpu().numpy(), seeds,
+                                          [20, 7], g.num_nodes)
+    _compare(layers, ref, vdt)
+
+
+def test_sample_all_layers_hacs_locality(cuda_device):
+    g, G = _graph("c1", cuda_device)
+    rng = np.random.default_rng(4)
+    q = rng.random(g.num_nodes).astype(np.float32)
+    q[rng.random(g.num_nodes) < 0.1] = 0.0
+    W = G.num_windows
+    parts = np.array([[0, 900], [900, 1800], [1800, 2708]], np.int32)
+    wpart = rng.integers(-1, 3, W).astype(np.int32)
+    seeds = np.arange(3, g.num_nodes, 9)
+    kw = dict(alpha=0.5, beta=3.0, delta=0.25, gamma_bonus=0.37, score_scale=250.0)
+    layers, _ = sample_all_layers(
+        G.window_offset, G.original_col_indices, G.values_condensed,
+        torch.from_numpy(seeds).to(cuda_device), [12, 40], g.num_nodes,
+        torch.from_numpy(q).to(cuda_device), torch.from_numpy(wpart).to(cuda_device),
+        torch.from_numpy(parts[:, 0].copy()).to(cuda_device),
+        torch.from_numpy(parts[:, 1].copy()).to(cuda_device), use_hacs=1, locality_enabled=1, **kw)
+    hacs = dict(static_scores=q, window_part_ids=wpart, part_starts=parts[:, 0],
+                part_ends=parts[:, 1], use_hacs=1, locality_enabled=1, **kw)
+    ref = oracle.window_sample_all_layers(G.window_offset.cpu().numpy(),
+                                          G.original_col_indices.cpu().numpy(),
+                                          G.values_condensed.cpu().numpy(), seeds, [12, 40],
+                                          g.num_nodes, hacs=hacs)
+    _compare(layers, ref)
+
+
+def test_window_seeds_matches_oracle(cuda_device):
+    rng = np.random.default_rng(9)
+    ids = rng.integers(-1, 5000, 20000).astype(np.int32)
+    act, msk = window_seeds(torch.from_numpy(ids).to(cuda_device), 5000)
+    ra, rm = oracle.prepare_windows(ids)
+    np.testing.assert_array_equal(act.cpu().numpy(), ra)
+    np.testing.assert_array_equal(msk.cpu().numpy(), rm)
+
+
+def test_sample_all_layers_rejects_bad_input(cuda_device):
+    g, G = _graph("c1", cuda_device)
+    args = (G.window_offset, G.original_col_indices, G.values_condensed)
+    with pytest.raises(GrwsError, match="outside"):
+        sample_all_layers(*args, torch.tensor([5, g.num_nodes + 40], device=cuda_device), [5],
+                          g.num_nodes)
+    with pytest.raises(RuntimeError, match="256"):
+        sample_all_layers(*args, torch.tensor([5], device=cuda_device), [257], g.num_nodes)
+    with pytest.raises(RuntimeError, match="warps_per_block"):
+        sample_all_layers(*args, torch.tensor([5], device=cuda_device), [5], g.num_nodes,
+                          warps_per_block=16)
+
+
+def test_bcsr_sampler_layers(cuda_device):
+    g, G = _graph("c1", cuda_device)
+    s = BCSRSampler(fanouts=[10, 5], verbose=True)
+    seeds = torch.arange(0, g.num_nodes, 11)
+    layers = s.sample_layers(G, seeds)
+    assert len(layers) == 2
+    # layers[-1] is the hop from the seeds (drawn with fanouts[-1] = 5)
+    act0 = layers[-1].active_windows.cpu().numpy()
+    np.testing.assert_array_equal(act0, np.unique(seeds.numpy() // 16))
+    for L in layers:
+        assert L.num_rows == 16 * L.active_windows.numel()
+        assert L.num_cols == g.num_nodes
+        assert L.num_tiles == L.window_offset[-1].item()
+    assert set(s.time_tracker) == {0, 1}
+    assert "BCSRSampler" in repr(s)
