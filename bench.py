@@ -180,6 +180,181 @@ def bench_sampling(dev, batches: int, warmup: int, cpu: bool) -> dict:
     return out
 
 
+# ---------------------------------------------------------------------------
+# GCN step / epoch (models/model.py:212-266, helper/engine.py:44-83)
+# ---------------------------------------------------------------------------
+GCN_CONFIGS = {
+    # config: (feature dim, padded dim, feature kind, hidden, classes, layers, dtype name)
+    "c1": (1433, 1433, "binary", 16, 7, 2, "f32"),
+    "c3": (602, 608, "normal", 256, 41, 3, "f16"),
+    "c4": (100, 112, "normal", 256, 47, 3, "bf16"),
+}
+
+
+class _CpuSpmm(torch.autograd.Function):
+    """A @ X on host cores with torch.sparse CSR and a precomputed CSR of A^T
+    for the backward (the same cached-transpose scheme as the GPU path)."""
+
+    @staticmethod
+    def forward(ctx, A, AT, x):
+        ctx.AT = AT
+        return A @ x
+
+    @staticmethod
+    def backward(ctx, g):
+        return None, None, ctx.AT @ g
+
+
+class _CpuGCN(torch.nn.Module):
+    """GCN_BCSR's arithmetic (layer.py:95-191, model.py:212-266) on torch
+    CPU tensors in float32: h = A (h Wn) + h Ws, then ReLU, LayerNorm and
+    dropout between layers."""
+
+    def __init__(self, dims, dropout):
+        super().__init__()
+        self.wn = torch.nn.ParameterList(torch.nn.Parameter(torch.empty(a, b)) for a, b in zip(dims, dims[1:]))
+        self.ws = torch.nn.ParameterList(torch.nn.Parameter(torch.empty(a, b)) for a, b in zip(dims, dims[1:]))
+        for p in list(self.wn) + list(self.ws):
+            torch.nn.init.xavier_uniform_(p)
+        self.norms = torch.nn.ModuleList(torch.nn.LayerNorm(d) for d in dims[1:-1])
+        self.dropout = torch.nn.Dropout(dropout)
+
+    def forward(self, A, AT, x):
+        h = x
+        for l in range(len(self.wn)):
+            h = _CpuSpmm.apply(A, AT, h @ self.wn[l]) + h @ self.ws[l]
+            if l < len(self.wn) - 1:
+                h = self.dropout(self.norms[l](torch.relu(h)))
+        return h
+
+
+def cpu_gcn_epoch(g, X, labels, train_idx, dims, dropout: float) -> float:
+    """Seconds of one CPU training epoch (forward, CE loss, backward,
+    clip_grad_norm_(1.0), Adam) on the same graph and features."""
+    import numpy as np
+    import scipy.sparse as sps
+    n = g.num_nodes
+    rp, ci, va = g.row_ptr.cpu(), g.col_idx.cpu(), g.values.cpu()
+    A = torch.sparse_csr_tensor(rp, ci.long(), va, size=(n, n))
+    At = sps.csr_matrix((va.numpy(), ci.numpy(), rp.numpy()), shape=(n, n)).T.tocsr()
+    AT = torch.sparse_csr_tensor(torch.from_numpy(At.indptr.astype(np.int64)),
+                                 torch.from_numpy(At.indices.astype(np.int64)),
+                                 torch.from_numpy(At.data), size=(n, n))
+    model = _CpuGCN(dims, dropout)
+    opt = torch.optim.Adam(model.parameters(), lr=0.01)
+    x = X.float().cpu()
+    lab, idx = labels.cpu(), train_idx.cpu()
+    t0 = time.perf_counter()
+    opt.zero_grad()
+    out = model(A, AT, x)
+    loss = torch.nn.functional.cross_entropy(out[idx], lab[idx])
+    loss.backward()
+    torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+    opt.step()
+    return time.perf_counter() - t0
+
+
+def bench_gcn(cfg: str, dev, epochs: int, warmup: int, cpu: bool) -> dict:
+    """Full-graph training epochs of GCN_BCSR on config `cfg` (c1: the tiny
+    fp32 step; c3, c4: 3 layers, hidden 256, autocast to the config dtype,
+    BCSR values in that dtype, 16x16 tiles).  Epoch = forward + loss +
+    backward + clip + Adam, synchronised at its end."""
+    from graph_rws_amd import synth
+    from graph_rws_amd.data import BCSRGraph
+    from graph_rws_amd.helper import train_epoch_full
+    from graph_rws_amd.models import GCN_BCSR
+    d_raw, d_pad, kind, hidden, classes, layers, dname = GCN_CONFIGS[cfg]
+    dt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dname]
+    g = synth.config_graph(cfg, device=dev)
+    G = BCSRGraph.from_csr(g.row_ptr, g.col_idx, g.values, g.num_nodes, g.num_nodes,
+                           tile_cols=16, device=dev, values_dtype=dt)
+    X = synth.features(g.num_nodes, d_raw, pad_to=d_pad, kind=kind, seed=11, device=dev).to(dt)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(12)
+    labels = torch.randint(0, classes, (g.num_nodes,), generator=gen, device=dev)
+    train_idx = torch.nonzero(torch.rand(g.num_nodes, generator=gen, device=dev) < 0.66).view(-1)
+    torch.manual_seed(13)
+    model = GCN_BCSR(d_pad, hidden, classes, layers, dropout=0.5, use_checkpoint=False).to(dev)
+    opt = torch.optim.Adam(model.parameters(), lr=0.01)
+
+    def epoch():
+        if dt == torch.float32:
+            return train_epoch_full(model, G, X, labels, train_idx, opt, dev, sync=False)
+        with torch.autocast("cuda", dtype=dt):
+            return train_epoch_full(model, G, X, labels, train_idx, opt, dev, sync=False)
+
+    for _ in range(warmup):
+        epoch()
+    torch.cuda.synchronize(dev)
+    times = []
+    for _ in range(epochs):
+        t0 = time.perf_counter()
+        loss, _ = epoch()
+        torch.cuda.synchronize(dev)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    out = {"workload": f"{cfg} full-graph GCN_BCSR epoch (fwd+bwd+clip+Adam)",
+           "nodes": g.num_nodes, "nnz": g.nnz, "features": d_pad, "hidden": hidden,
+           "classes": classes, "layers": layers, "dtype": dname, "tile": "16x16",
+           "epochs": epochs, "epoch_ms": round(1e3 * times[len(times) // 2], 3),
+           "epoch_ms_min": round(1e3 * times[0], 3), "final_loss": round(float(loss), 4)}
+    if cpu:
+        torch.set_num_threads(os.cpu_count() or 1)
+        dims = [d_pad] + [hidden] * (layers - 1) + [classes]
+        if cfg == "c1":
+            cpu_gcn_epoch(g, X, labels, train_idx, dims, 0.5)  # warm-up
+            ts = sorted(cpu_gcn_epoch(g, X, labels, train_idx, dims, 0.5) for _ in range(3))
+            t_cpu, note = ts[1], "median of 3 after 1 warm-up"
+        else:
+            t_cpu, note = cpu_gcn_epoch(g, X, labels, train_idx, dims, 0.5), "one epoch"
+        out["cpu_baseline"] = {"value": round(1e3 * t_cpu, 2), "unit": "ms per epoch",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"{note}: the same model arithmetic in fp32 on "
+                                         "torch.sparse CSR (A and a precomputed A^T) over the "
+                                         "whole graph"}
+    del G, X, model, opt, g
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_spmm_c2(dev, reps: int = 20) -> dict:
+    """c2 SpMM microbenchmark: forward A X and backward A^T G (G like X),
+    X [169,343 x 128] in bf16 and f16, 16x16 tiles."""
+    from graph_rws_amd import synth
+    from graph_rws_amd.data import BCSRGraph
+    g = synth.config_graph("c2", device=dev)
+    res = {"workload": "c2 SpMM forward A*X and backward A^T*G", "nodes": g.num_nodes,
+           "nnz": g.nnz, "N": 128}
+    for dname, dt in (("bf16", torch.bfloat16), ("f16", torch.float16)):
+        G = BCSRGraph.from_csr(g.row_ptr, g.col_idx, g.values, g.num_nodes, g.num_nodes,
+                               tile_cols=16, device=dev, values_dtype=dt)
+        X = synth.features(g.num_nodes, 128, seed=21, device=dev).to(dt)
+        Gr = synth.features(16 * G.num_windows, 128, seed=22, device=dev).to(dt)
+        AT = G.transpose()
+        r = {}
+        for name, M, inp in (("fwd", G, X), ("bwd", AT, Gr)):
+            out = torch.empty((16 * M.num_windows, 128), dtype=dt, device=dev)
+            for _ in range(3):
+                M.spmm(inp, out=out)
+            s = torch.cuda.current_stream(dev)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(reps):
+                M.spmm(inp, out=out)
+            e1.record(s)
+            e1.synchronize()
+            ms = e0.elapsed_time(e1) / reps
+            B = alg_bytes(M, 128, 2, 2)
+            r[name] = {"ms": round(ms, 4), "gflops": round(2.0 * g.nnz * 128 / ms / 1e6, 1),
+                       "alg_gbps": round(B["total"] / ms / 1e6, 1),
+                       "pct_hbm_peak": round(100.0 * B["total"] / ms / 1e6 / HBM_PEAK_GBS, 2),
+                       "alg_bytes": B["total"]}
+        res[dname] = r
+        del G, X, Gr, AT
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -194,6 +369,9 @@ def main():
                     help="only run 5 device-to-device copies of BYTES (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     ap.add_argument("--sampling-batches", type=int, default=20)
+    ap.add_argument("--no-gcn", action="store_true")
+    ap.add_argument("--gcn-epochs", type=int, default=5)
+    ap.add_argument("--gcn-configs", default="c1,c3,c4")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -303,6 +481,10 @@ def main():
         del G, X, Y, g, plan
         torch.cuda.empty_cache()
         out["sampling"] = bench_sampling(dev, args.sampling_batches, 3, not args.no_cpu_baseline)
+    if not args.no_gcn:
+        out["spmm_c2"] = bench_spmm_c2(dev)
+        out["gcn"] = {c: bench_gcn(c, dev, args.gcn_epochs, 2, not args.no_cpu_baseline)
+                      for c in args.gcn_configs.split(",") if c}
     print(json.dumps(out), flush=True)
 
 
