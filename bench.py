@@ -317,6 +317,58 @@ def bench_gcn(cfg: str, dev, epochs: int, warmup: int, cpu: bool) -> dict:
     return out
 
 
+def bench_minibatch(dev, batches: int, warmup: int) -> dict:
+    """c5 mini-batch training: per batch, 1,024 seeds, NeighborSampler
+    ([15,10,5], Philox seed 42), the input features gathered from the
+    111M x 128 fp16 matrix in HBM, then a 3-layer GCN_BCSR step (hidden 256,
+    172 classes, fp16 autocast, CE loss, clip, Adam), sampling pipelined one
+    batch ahead on a side stream (train_epoch_node_sampling)."""
+    from graph_rws_amd import synth
+    from graph_rws_amd.helper import EpochTimer, train_epoch_node_sampling
+    from graph_rws_amd.models import GCN_BCSR
+    from graph_rws_amd.sampler import NeighborSampler
+    c = synth.C5
+    t0 = time.time()
+    g = synth.c5_graph(device=dev)
+    X = synth.features(g.num_nodes, c["feat"], dtype=torch.float16, seed=31, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(32)
+    labels = torch.randint(0, c["classes"], (g.num_nodes,), generator=gen, device=dev)
+    torch.cuda.synchronize(dev)
+    t_gen = time.time() - t0
+    torch.manual_seed(33)
+    model = GCN_BCSR(c["feat"], 256, c["classes"], 3, dropout=0.5, use_checkpoint=False).to(dev)
+    opt = torch.optim.Adam(model.parameters(), lr=0.003)
+    sampler = NeighborSampler(c["fanouts"], seed=c["philox_seed"], tile_cols=16,
+                              values_dtype=torch.float16)
+
+    def run(nb, seed):
+        idx = synth.distinct_seeds(g.num_nodes, c["batch"] * nb, seed=seed, device=dev).cpu()
+        timer = EpochTimer()
+        e0, b0 = sampler.total_edges, sampler.total_batches
+        torch.cuda.synchronize(dev)
+        t = time.perf_counter()
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss, _ = train_epoch_node_sampling(model, g, X, labels, idx, opt, dev, sampler,
+                                                batch_size=c["batch"], timer=timer, pipeline=True)
+        torch.cuda.synchronize(dev)
+        return (time.perf_counter() - t, sampler.total_edges - e0, sampler.total_batches - b0,
+                loss, timer.get_epoch_stats())
+
+    run(warmup, 40)
+    wall, edges, nb, loss, stats = run(batches, 41)
+    out = {"workload": "c5 mini-batch GCN step (sample + feature gather + fwd/bwd/Adam), pipelined",
+           "graph": {"nodes": g.num_nodes, "edges": g.nnz}, "features": [g.num_nodes, c["feat"], "f16"],
+           "batches": nb, "batch_ms": round(1e3 * wall / nb, 3),
+           "sampled_edges_per_s_in_training": round(edges / wall, 1),
+           "edges_per_batch": round(edges / nb, 1), "final_loss": round(float(loss), 4),
+           "stage_ms_per_batch": {k: round(v, 3) for k, v in stats.items()},
+           "generate_s": round(t_gen, 2)}
+    del g, X, labels, model, opt
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_spmm_c2(dev, reps: int = 20) -> dict:
     """c2 SpMM microbenchmark: forward A X and backward A^T G (G like X),
     X [169,343 x 128] in bf16 and f16, 16x16 tiles."""
@@ -370,6 +422,8 @@ def main():
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     ap.add_argument("--sampling-batches", type=int, default=20)
     ap.add_argument("--no-gcn", action="store_true")
+    ap.add_argument("--no-minibatch", action="store_true")
+    ap.add_argument("--minibatch-batches", type=int, default=20)
     ap.add_argument("--gcn-epochs", type=int, default=5)
     ap.add_argument("--gcn-configs", default="c1,c3,c4")
     args = ap.parse_args()
@@ -485,6 +539,8 @@ def main():
         out["spmm_c2"] = bench_spmm_c2(dev)
         out["gcn"] = {c: bench_gcn(c, dev, args.gcn_epochs, 2, not args.no_cpu_baseline)
                       for c in args.gcn_configs.split(",") if c}
+    if not args.no_minibatch:
+        out["minibatch"] = bench_minibatch(dev, args.minibatch_batches, 3)
     print(json.dumps(out), flush=True)
 
 

@@ -1,3 +1,4 @@
 from .bcsr import BCSRGraph  # noqa: F401
+from .loader import WindowWiseDataLoader  # noqa: F401
 
-__all__ = ["BCSRGraph"]
+__all__ = ["BCSRGraph", "WindowWiseDataLoader"]

@@ -1,2 +1,14 @@
-from .timer import record_spmm_time, get_spmm_time, reset_spmm_time  # noqa: F401
-from .engine import train_epoch_full, evaluate, compute_loss_and_metrics  # noqa: F401
+from .timer import (  # noqa: F401
+    EpochTimer,
+    get_avg_spmm_time,
+    get_spmm_time,
+    record_spmm_time,
+    reset_spmm_time,
+    reset_spmm_timings,
+)
+from .engine import (  # noqa: F401
+    compute_loss_and_metrics,
+    evaluate,
+    train_epoch_full,
+    train_epoch_node_sampling,
+)

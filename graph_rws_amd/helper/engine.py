@@ -51,3 +51,168 @@ def evaluate(model, bcsr_full, features: torch.Tensor, labels: torch.Tensor,
     logits = model.inference(bcsr_full, features)
     _, correct, n = compute_loss_and_metrics(logits[eval_idx].float(), labels[eval_idx])
     return (correct / n).item() if n > 0 else 0.0
+
+
+# ---------------------------------------------------------------------------
+# mini-batch training (helper/engine.py:86-256)
+# ---------------------------------------------------------------------------
+def _adopt(tensors, stream) -> None:
+    """Tensors made on the sampling stream are used on `stream`: tell the
+    caching allocator, so their memory is not reused before that work ends."""
+    for t in tensors:
+        if isinstance(t, torch.Tensor) and t.is_cuda:
+            t.record_stream(stream)
+
+
+def _graph_tensors(g):
+    out = [g.window_offset, g.original_col_indices, g.values_condensed]
+    for name in ("active_windows", "active_masks", "src_nodes", "dst_nodes"):
+        t = getattr(g, name, None)
+        if t is not None:
+            out.append(t)
+    return out
+
+
+def _sample_batch(sampler, graph, seeds, features, device):
+    """(subgraphs, batch_features or None, rows of the seeds in the logits).
+
+    NeighborSampler: graph is a CSR (row_ptr, col_idx); blocks come back
+    destination-first, the input features are gathered for
+    blocks[0].src_nodes and the seeds are the first rows of the output.
+    BCSRSampler: graph is the full BCSRGraph; the model reads the full
+    feature matrix by global column id and the seed rows are located through
+    the last layer's active windows (engine.py:170-181)."""
+    from ..sampler import NeighborSampler
+    if isinstance(sampler, NeighborSampler):
+        blocks = sampler.sample_layers(graph.row_ptr, graph.col_idx, seeds)
+        inp = blocks[0].src_nodes
+        if features.is_cuda:
+            feats = features.index_select(0, inp)
+        else:  # host-resident features: gather on the host, copy over
+            feats = features.index_select(0, inp.cpu()).pin_memory().to(device, non_blocking=True)
+        return blocks, feats, None
+    subgraphs = sampler.sample_layers(graph, seeds)
+    feats = None
+    if not features.is_cuda:  # UVA-style mode of engine.py:128-141
+        g0 = subgraphs[0]
+        inp = g0.original_col_indices
+        feats = features[inp.cpu().clamp(min=0).long()].to(device, non_blocking=True)
+        g0.original_col_indices = torch.arange(inp.numel(), device=device, dtype=torch.int32)
+        g0.is_local_input = True
+    return subgraphs, feats, None
+
+
+def _seed_rows(sampler, subgraphs, seeds, logits, tile_rows):
+    from ..sampler import NeighborSampler
+    if isinstance(sampler, NeighborSampler):
+        return torch.arange(seeds.numel(), device=logits.device)
+    act = subgraphs[-1].active_windows.long()
+    sw = torch.div(seeds, tile_rows, rounding_mode="floor")
+    sa, perm = torch.sort(act)
+    wi = perm[torch.searchsorted(sa, sw)]
+    rows = wi * tile_rows + seeds % tile_rows
+    return torch.clamp(rows, max=logits.shape[0] - 1)
+
+
+def train_epoch_node_sampling(model, graphs_for_model, features: torch.Tensor,
+                              labels: torch.Tensor, train_idx: torch.Tensor,
+                              optimizer: torch.optim.Optimizer, device, sampler,
+                              batch_size: int = 1024, tile_rows: int = 16, timer=None,
+                              pipeline: bool = True, max_batches: int = 0):
+    """One epoch of mini-batch training (engine.py:86-256).  Returns
+    (average loss, accuracy).
+
+    pipeline=True: a producer thread samples (and gathers features) on its
+    own stream, one batch ahead of the training loop on the current stream
+    (engine.py:112-203).  Streams keep the default priority.
+    `sampler` is a BCSRSampler (window top-K, the reference's) with the full
+    BCSRGraph, or a NeighborSampler (Philox fanout) with the CSR graph
+    (an object with row_ptr / col_idx).  max_batches > 0 stops early."""
+    import queue
+    import threading
+    from ..data import WindowWiseDataLoader
+    from .timer import EpochTimer
+
+    model.train()
+    timer = timer or EpochTimer()
+    timer.reset()
+    total_loss = torch.zeros(1, device=device)
+    total_correct = torch.zeros(1, device=device)
+    total_samples = 0
+    num_batches = 0
+    graph = graphs_for_model[0] if isinstance(graphs_for_model, list) else graphs_for_model
+    loader = WindowWiseDataLoader(train_idx.cpu(), batch_size=batch_size, tile_rows=tile_rows)
+    main = torch.cuda.current_stream(device)
+
+    def step(seeds, subgraphs, feats):
+        nonlocal total_samples, num_batches
+        optimizer.zero_grad()
+        logits = model(subgraphs, feats if feats is not None else features)
+        timer.record("Fwd")
+        rows = _seed_rows(sampler, subgraphs, seeds, logits, tile_rows)
+        loss, correct, n = compute_loss_and_metrics(logits[rows].float(), labels[seeds])
+        loss.backward()
+        timer.record("Bwd")
+        torch.nn.utils.clip_grad_norm_(model.parameters(), max_norm=1.0)
+        optimizer.step()
+        timer.record("Step")
+        with torch.no_grad():
+            total_loss.add_(loss.detach())
+            total_correct.add_(correct)
+        total_samples += n
+        num_batches += 1
+        timer.end_batch()
+
+    if pipeline:
+        side = torch.cuda.Stream(device)
+        q: "queue.Queue" = queue.Queue(maxsize=1)
+        failure = []
+
+        def producer():
+            try:
+                with torch.cuda.stream(side):
+                    for b, seeds in enumerate(loader):
+                        if max_batches and b >= max_batches:
+                            break
+                        seeds = torch.sort(seeds.to(device, non_blocking=True)).values
+                        subgraphs, feats, _ = _sample_batch(sampler, graph, seeds, features, device)
+                        ev = torch.cuda.Event()
+                        ev.record(side)
+                        q.put((seeds, subgraphs, feats, ev))
+            except BaseException as e:  # surfaced in the training thread
+                failure.append(e)
+            finally:
+                q.put(None)
+
+        worker = threading.Thread(target=producer, daemon=True)
+        worker.start()
+        while True:
+            timer.start_batch()
+            item = q.get()
+            timer.record("Data")
+            if item is None:
+                break
+            seeds, subgraphs, feats, ev = item
+            main.wait_event(ev)
+            for g in subgraphs:
+                _adopt(_graph_tensors(g), main)
+            _adopt([seeds, feats], main)
+            timer.record("Sample")
+            step(seeds, subgraphs, feats)
+        worker.join()
+        if failure:
+            raise failure[0]
+    else:
+        for b, seeds in enumerate(loader):
+            if max_batches and b >= max_batches:
+                break
+            timer.start_batch()
+            seeds = torch.sort(seeds.to(device)).values
+            timer.record("Data")
+            subgraphs, feats, _ = _sample_batch(sampler, graph, seeds, features, device)
+            timer.record("Sample")
+            step(seeds, subgraphs, feats)
+
+    if num_batches == 0:
+        return 0.0, 0.0
+    return total_loss.item() / num_batches, total_correct.item() / max(total_samples, 1)

@@ -59,6 +59,8 @@ class NeighborSampler:
         self.values_dtype = values_dtype
         self.verbose = verbose
         self.last_stats: dict = {}
+        self.total_edges = 0
+        self.total_batches = 0
 
     def sample_layers(self, indptr: torch.Tensor, indices: torch.Tensor,
                       seed_nodes: torch.Tensor) -> List[BCSRGraph]:
@@ -95,6 +97,8 @@ class NeighborSampler:
             frontier = nxt
         self.last_stats = {"edges": edges, "seconds": time.perf_counter() - t0,
                            "input_nodes": int(frontier.numel())}
+        self.total_edges += edges
+        self.total_batches += 1
         if self.verbose:
             s = self.last_stats
             print(f"[NeighborSampler] {len(self.fanouts)} hops, {s['edges']} edges, "

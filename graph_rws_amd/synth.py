@@ -154,6 +154,8 @@ def features(n: int, d: int, pad_to: Optional[int] = None, dtype=torch.float32, 
     """Node features [n, pad_to or d]: N(0,1) or Bernoulli(p) ('binary');
     padding columns are zero."""
     device = torch.device(device)
+    if dtype != torch.float32 and n * (pad_to or d) > (1 << 28):
+        return _features_chunked(n, d, pad_to, dtype, seed, device, kind, p)
     g = _gen(seed, device)
     if kind == "binary":
         x = (torch.rand(n, d, generator=g, device=device) < p).to(torch.float32)
@@ -162,6 +164,21 @@ def features(n: int, d: int, pad_to: Optional[int] = None, dtype=torch.float32, 
     if pad_to is not None and pad_to > d:
         x = torch.nn.functional.pad(x, (0, pad_to - d))
     return x.to(dtype)
+
+
+def _features_chunked(n, d, pad_to, dtype, seed, device, kind, p, rows: int = 1 << 20):
+    """features() for matrices too large to stage in float32: generated in
+    row chunks straight into the target dtype."""
+    g = _gen(seed, device)
+    out = torch.zeros(n, pad_to or d, dtype=dtype, device=device)
+    for s in range(0, n, rows):
+        e = min(n, s + rows)
+        if kind == "binary":
+            x = (torch.rand(e - s, d, generator=g, device=device) < p).to(dtype)
+        else:
+            x = torch.randn(e - s, d, generator=g, device=device, dtype=torch.float32).to(dtype)
+        out[s:e, :d] = x
+    return out
 
 
 # ---------------------------------------------------------------------------
