@@ -93,3 +93,59 @@ def test_synthetic_config_shapes():
     assert np.all(A.diagonal() > 0)
     deg = np.diff(g.row_ptr.numpy())
     np.testing.assert_allclose(A.diagonal(), 1.0 / deg, rtol=1e-6)
+
+
+def test_python_shim_keeps_reference_signatures():
+    """The shim's ops take the reference's pybind11 argument names, in order,
+    with the same defaults (core/wrapper/bind.cpp:99-159)."""
+    import inspect
+    import graph_rws_amd.core as core
+    want = {
+        "sample_all_layers": ["window_offset", "original_col_indices", "values_condensed",
+                              "initial_seeds", "fanouts", "num_global_nodes", "static_scores",
+                              "window_part_ids", "part_starts", "part_ends", "alpha", "beta",
+                              "delta", "gamma_bonus", "score_scale", "use_hacs",
+                              "locality_enabled", "tile_rows", "tile_cols", "warps_per_block"],
+        "spmm_tc": ["window_offset", "original_col_indices", "values_condensed", "input_B",
+                    "warps_per_block"],
+        "spmm_transpose": ["window_offset", "original_col_indices", "values_condensed",
+                           "grad_out", "num_cols"],
+        "csr_to_bcsr_cpu": ["num_rows", "row_ptr", "col_idx", "values", "tile_rows", "tile_cols"],
+        "reindex_bcsr": ["col_indices", "values_condensed", "active_windows", "tile_rows",
+                         "tile_cols"],
+    }
+    defaults = {"sample_all_layers": dict(alpha=1.0, beta=10.0, delta=0.0, gamma_bonus=0.0,
+                                          score_scale=100.0, use_hacs=0, locality_enabled=0,
+                                          tile_rows=16, tile_cols=8, warps_per_block=8),
+                "spmm_tc": dict(warps_per_block=8), "reindex_bcsr": dict(tile_rows=16, tile_cols=8)}
+    for name, args in want.items():
+        params = list(inspect.signature(getattr(core, name)).parameters.values())
+        assert [p.name for p in params[:len(args)]] == args, name
+        for k, v in defaults.get(name, {}).items():
+            assert inspect.signature(getattr(core, name)).parameters[k].default == v, (name, k)
+    t = core.SamplingTimingResult(1.0, 2.0, 3.0, 6.0)
+    assert t.to_dict() == {"phase1_sampling_time": 1.0, "phase2_mapping_time": 2.0,
+                           "phase3_recompression_time": 3.0, "total_time": 6.0}
+    assert "SamplingTimingResult" in repr(t)
+
+
+def test_window_sampler_host_checks_without_gpu():
+    lib = L.load()
+    assert lib.grws_window_sample_num(1) == 32 and lib.grws_window_sample_num(33) == 64
+    assert lib.grws_window_sample_num(256) == 256
+    n = ctypes.c_int64(-1)
+    # empty inputs return before touching the device
+    assert lib.grws_window_seeds(None, 0, 10, 16, 0, None, None, None, 0, ctypes.byref(n), None) == 0
+    assert n.value == 0
+    win = np.zeros(5, np.int64)  # never read: the fanout check comes first
+    view = L.BcsrView(win.ctypes.data, None, None, 4, 0, 16, 8, 0, 0)
+    T = ctypes.c_int64()
+    st = lib.grws_window_topk(ctypes.byref(view), None, 0, 300, None, None, None, None, None, 0,
+                              ctypes.byref(T), None)
+    assert st == -1 and b"fanout" in lib.grws_last_error()
+    st = lib.grws_sample_hop(None, None, 10, 0, None, 5, 65, 42, None, None, None, 0, None, 0,
+                             ctypes.byref(T), None)
+    assert st == -1 and b"fanout" in lib.grws_last_error()
+    st = lib.grws_sample_hop(None, None, 10, 0, None, 5, 8, 42, None, None, None, 39, None, 0,
+                             ctypes.byref(T), None)
+    assert st == -1 and b"edge_capacity" in lib.grws_last_error()
