@@ -140,8 +140,9 @@ def test_window_sampler_host_checks_without_gpu():
     win = np.zeros(5, np.int64)  # never read: the fanout check comes first
     view = L.BcsrView(win.ctypes.data, None, None, 4, 0, 16, 8, 0, 0)
     T = ctypes.c_int64()
-    st = lib.grws_window_topk(ctypes.byref(view), None, 0, 300, None, None, None, None, None, 0,
-                              ctypes.byref(T), None)
+    off = np.zeros(1, np.int64)  # never written: the fanout check comes first
+    st = lib.grws_window_topk(ctypes.byref(view), None, 0, 300, None, None, None,
+                              off.ctypes.data, None, 0, ctypes.byref(T), None)
     assert st == -1 and b"fanout" in lib.grws_last_error()
     st = lib.grws_sample_hop(None, None, 10, 0, None, 5, 65, 42, None, None, None, 0, None, 0,
                              ctypes.byref(T), None)
