@@ -31,7 +31,7 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16
 # reported only for that exact workload.  Source: profiles/spmm_fwd_c3_n608_f16.md
 MEASURED_TRAFFIC = {
     # (config, N, x dtype, tile cols): (bytes per launch, profile file)
-    ("c3", 608, "f16", 16): (49.75e9, "profiles/spmm_fwd_c3_n608_f16.md"),
+    ("c3", 608, "f16", 16): (44.26e9, "profiles/spmm_fwd_c3_n608_f16.md"),
 }
 
 
@@ -460,7 +460,10 @@ def main():
 
     g, G, t_gen, t_build = build_graph(cfg, args.tile_cols, xdt, dev)
     from graph_rws_amd import synth
-    X = synth.features(g.num_nodes, d_raw, pad_to=N, seed=7, device=dev).to(xdt)
+    from graph_rws_amd.data import aligned_rows
+    # rows stored at a 128-byte multiple pitch (608 fp16 -> 640): same values,
+    # every gathered row segment starts on a cache line
+    X = aligned_rows(synth.features(g.num_nodes, d_raw, pad_to=N, seed=7, device=dev).to(xdt))
     plan = G.spmm_plan(N)
     Y = torch.empty((16 * G.num_windows, N), dtype=xdt, device=dev)
     stream = torch.cuda.current_stream(dev)
@@ -506,7 +509,7 @@ def main():
             "workload": f"{cfg} BCSR SpMM forward Y=A*X",
             "graph": synth.CONFIGS[cfg]["kind"],
             "nodes": g.num_nodes, "nnz": nnz, "windows": G.num_windows, "tiles": G.num_tiles,
-            "tile": f"16x{G.tile_cols}", "N": N, "x_dtype": dname,
+            "tile": f"16x{G.tile_cols}", "N": N, "x_dtype": dname, "x_row_pitch": X.stride(0),
             "values_dtype": str(G.values_condensed.dtype).replace("torch.", ""),
             "plan": {"items": plan.num_items, "split_windows": plan.num_split,
                      "slabs_per_item": plan.slabs_per_item},

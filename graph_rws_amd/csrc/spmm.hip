@@ -2,22 +2,29 @@
 //
 // Replaces the reference's tcspmm_base_kernel (core/include/spmm_tc.cuh:40-195,
 // launched by core/wrapper/spmm_wrapper.cu:33-95).  Design:
-//   * one wave64 work-group per (work item, N-chunk); a work item is a window
-//     or, for heavy windows, a contiguous range of its slabs (16 column slots);
+//   * one work-group per (work item, N-chunk of up to 128 columns); a work
+//     item is a window or, for heavy windows, a contiguous range of its slabs
+//     (16 column slots); one or two wave64s share it, splitting its slabs;
 //   * the 16 X rows a slab references are gathered with 16-byte loads
 //     (coalesced row segments), staged in LDS, and fed to CDNA4 MFMA:
 //     v_mfma_f32_16x16x16_{f16,bf16} for 16-bit inputs, v_mfma_f32_16x16x4_f32
 //     for fp32; fp32 accumulation in registers;
-//   * the next slab's gathers are issued before the current slab is consumed
-//     (register double buffer), so HBM latency overlaps the MFMA work;
-//   * -1 padding (and any column outside [0, x_rows)) is masked at the load:
-//     no memory traffic, zero contribution;
+//   * a ring of register buffers keeps the next slab's gathers, A values and
+//     the column indices beyond them in flight while a slab is multiplied;
+//     loads are branch-free (clamped address, result masked when consumed)
+//     so the wait before each slab covers that slab's loads only;
+//   * A (columns and values) is streamed with non-temporal loads so it does
+//     not evict the X rows that neighbouring windows re-read from L2;
+//   * -1 padding (and any column outside [0, x_rows)) contributes zero;
 //   * heavy windows are split over several items whose fp32 partial sums are
 //     added in a fixed order by a second kernel: deterministic, no atomics;
 //   * work-group ids are remapped so each XCD (work-groups are dealt to the 8
-//     XCDs round-robin) walks a contiguous range of (chunk, window) pairs,
-//     keeping a community's X rows resident in that XCD's L2.
+//     XCDs round-robin) walks a contiguous range of windows of one chunk,
+//     keeping a community's X rows (one chunk wide) in that XCD's L2.
+// Tuning overrides for benchmarking: GRWS_SPMM_WAVES (1|2), GRWS_SPMM_PF (1|2).
 #include "grws_internal.h"
+
+#include <cstdlib>
 
 namespace grws {
 namespace {
@@ -96,8 +103,16 @@ __device__ __forceinline__ void store_out(void* y, int64_t idx, float v) {
     }
 }
 
-template <int XT, bool AF32, int TC, int NBLK, bool VECT>
-__global__ __launch_bounds__(64) void spmm_fwd_kernel(SpmmArgs a) {
+// One work-group per (work item, N-chunk); WPB waves split the item's slabs
+// (wave w takes slabs sb + w, sb + w + WPB, ...) and add their partials in
+// LDS in a fixed order.  Each wave runs a software pipeline over a ring of
+// PF + 1 register buffers: while slab s is staged and multiplied, the X rows
+// and A values of the next PF slabs are in flight, and the column indices of
+// the slab after those.  Every load is unconditional (an invalid slot loads
+// a clamped, valid address and its result is replaced by zero), so the
+// compiler can count outstanding loads and wait only for the slab it needs.
+template <int XT, bool AF32, int TC, int NBLK, bool VECT, int WPB, int PF>
+__global__ __launch_bounds__(64 * WPB) void spmm_fwd_kernel(SpmmArgs a) {
     using S = typename XTraits<XT>::S;
     constexpr int SZ = XTraits<XT>::SZ;
     constexpr int NC = NBLK * 16;                  // output columns per work-group
@@ -106,15 +121,23 @@ __global__ __launch_bounds__(64) void spmm_fwd_kernel(SpmmArgs a) {
     using LoadT = typename RawT<LDB>::T;
     constexpr int PITCH = NC + (SZ == 2 ? 8 : 4);  // LDS row pitch (elements), 16-B aligned rows
     constexpr int NLD = (16 * NC + 64 * VEC - 1) / (64 * VEC);  // lane loads per slab
+    constexpr int R = PF + 1;                      // pipeline ring size
     static_assert(TC == 8 || TC == 16, "tile_cols must be 8 or 16");
+    static_assert(PF >= 1 && PF <= 2, "prefetch depth 1..2");
+    // the waves' stage buffers double as the fp32 reduction buffer
+    static_assert(WPB == 1 || WPB * 16 * PITCH * SZ >= 16 * NC * 4, "stage too small to reduce in");
 
-    __shared__ __attribute__((aligned(16))) S stage[16 * PITCH];
+    __shared__ __attribute__((aligned(16))) S stage_all[WPB * 16 * PITCH];
 
-    const int lane = threadIdx.x;
+    const int wave = WPB > 1 ? (int)(threadIdx.x >> 6) : 0;
+    const int lane = threadIdx.x & 63;
+    S* stage = stage_all + wave * (16 * PITCH);
     const int64_t total = a.num_items * a.nchunks;
     const int64_t per_xcd = (total + 7) >> 3;
     const int64_t logical = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (logical >= total) return;
+    if (logical >= total) return;  // uniform over the work-group
+    // chunk-major: consecutive work-groups of an XCD walk consecutive items
+    // of one chunk, so a window range's X rows (one chunk wide) stay in L2
     const int64_t item = logical % a.num_items;
     const int chunk = (int)(logical / a.num_items);
 
@@ -157,72 +180,63 @@ __global__ __launch_bounds__(64) void spmm_fwd_kernel(SpmmArgs a) {
         ld_col[i] = e % NC;
     }
 
+    // A (column indices and values) is read once per chunk and not again
+    // soon: non-temporal loads keep it from evicting the X rows L2 reuses
     auto load_cols = [&](int64_t s) -> int {
-        int64_t sl = s * 16 + (lane & 15);
-        return (s < se && sl < nslots) ? colp[sl] : -1;
+        const int64_t sl = s * 16 + (lane & 15);
+        const bool ok = s < se && sl < nslots;
+        const int v = __builtin_nontemporal_load(colp + (ok ? sl : 0));
+        return ok ? v : -1;
     };
-    auto load_x = [&](int cv, LoadT* regs) {
+    // Returns the validity bits of the NLD loads; invalid lanes load a
+    // clamped address and are zeroed only when the slab is consumed, so no
+    // select waits on a load that was just issued.
+    auto load_x = [&](int cv, LoadT* regs) -> uint32_t {
+        uint32_t okm = 0;
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
-            int r = ld_row[i];
-            int c = __shfl(cv, r & 15, 64);
-            bool ok = (r < 16) && ((uint32_t)c < xr) && (n0 + ld_col[i] < N);
-            LoadT v = {};
-            if (ok) v = *reinterpret_cast<const LoadT*>(X + (int64_t)c * a.ldx + n0 + ld_col[i]);
-            regs[i] = v;
+            const int r = ld_row[i];
+            const int c = __shfl(cv, r & 15, 64);
+            const bool ok = (r < 16) && ((uint32_t)c < xr) && (n0 + ld_col[i] < N);
+            regs[i] = *reinterpret_cast<const LoadT*>(X + (ok ? (int64_t)c * a.ldx + n0 + ld_col[i] : 0));
+            okm |= (ok ? 1u : 0u) << i;
         }
+        return okm;
     };
 
     // A fragment: row r = lane%16, slots 16s + 4g .. 16s + 4g + 3 (g = lane/16)
     const int ar = lane & 15;
     const int ag = lane >> 4;
     using AVec = typename std::conditional<AF32, float4_t, typename std::conditional<XT == GRWS_F32, float4_t, u32x2_t>::type>::type;
+    // the A fragment of an invalid slab is zeroed at consumption as well
+    auto a_valid = [&](int64_t s) -> bool { return s < se && s * 16 + 4 * ag < nslots; };
     auto load_a = [&](int64_t s) -> AVec {
-        AVec v = {};
-        int64_t sl = s * 16 + 4 * ag;
-        if (s < se && sl < nslots) {
-            int64_t tile = t0 + sl / TC;
-            int c = (int)(sl % TC);
-            int64_t off = (tile * 16 + ar) * TC + c;
-            if constexpr (AF32 || XT == GRWS_F32) {
-                v = *reinterpret_cast<const float4_t*>(static_cast<const float*>(a.vals) + off);
-            } else {
-                v = *reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(a.vals) + off);
-            }
+        const int64_t sl = s * 16 + 4 * ag;
+        const bool ok = s < se && sl < nslots;
+        const int64_t slc = ok ? sl : 0;
+        const int64_t off = ok ? ((t0 + slc / TC) * 16 + ar) * TC + (slc % TC) : 0;
+        if constexpr (AF32 || XT == GRWS_F32) {
+            return __builtin_nontemporal_load(reinterpret_cast<const float4_t*>(static_cast<const float*>(a.vals) + off));
+        } else {
+            return __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(a.vals) + off));
         }
-        return v;
     };
 
     float4_t acc[NBLK];
 #pragma unroll
     for (int b = 0; b < NBLK; ++b) acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    LoadT cur[NLD], nxt[NLD];
-    AVec a_cur = {}, a_nxt = {};
-    int c_nxt = -1;
-    if (sb < se) {
-        int c0 = load_cols(sb);
-        load_x(c0, cur);
-        a_cur = load_a(sb);
-        c_nxt = load_cols(sb + 1);
-    }
     const int bn = lane & 15;
-    for (int64_t s = sb; s < se; ++s) {
-        if (s + 1 < se) {
-            load_x(c_nxt, nxt);
-            a_nxt = load_a(s + 1);
-            c_nxt = load_cols(s + 2);
-        }
-        // stage slab s
+    auto consume = [&](const LoadT* xb, const uint32_t okm, const AVec a_raw, const bool a_ok) {
+        const AVec a_cur = a_ok ? a_raw : AVec{};
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
             if (ld_row[i] < 16)
-                *reinterpret_cast<LoadT*>(&stage[ld_row[i] * PITCH + ld_col[i]]) = cur[i];
+                *reinterpret_cast<LoadT*>(&stage[ld_row[i] * PITCH + ld_col[i]]) = ((okm >> i) & 1u) ? xb[i] : LoadT{};
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
         if constexpr (XT == GRWS_F32) {
             float4_t af = a_cur;
 #pragma unroll
@@ -262,16 +276,84 @@ __global__ __launch_bounds__(64) void spmm_fwd_kernel(SpmmArgs a) {
                 acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(af, bf, acc[b], 0, 0, 0);
             }
         }
-        // the next iteration overwrites the stage
+        // the next slab overwrites the stage
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+
+    const int64_t s0 = sb + wave;
+    if (s0 < se && xr > 0) {  // uniform per wave; every load below is in bounds
+        LoadT buf[R][NLD];
+        AVec abuf[R];
+        uint32_t okx[R];
+        int cring[R];
 #pragma unroll
-        for (int i = 0; i < NLD; ++i) cur[i] = nxt[i];
-        a_cur = a_nxt;
+        for (int k = 0; k < R; ++k) cring[k] = load_cols(s0 + (int64_t)k * WPB);
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+            okx[k] = load_x(cring[k], buf[k]);
+            abuf[k] = load_a(s0 + (int64_t)k * WPB);
+        }
+        // one pipeline step for slab s in ring slot u
+        auto step = [&](const int u, const int64_t s) {
+            const int ps = (u + PF) % R;  // ring slot of slab s + PF*WPB
+            // columns of slab s + R*WPB into the slot slab s no longer needs
+            cring[u] = load_cols(s + (int64_t)R * WPB);
+            okx[ps] = load_x(cring[ps], buf[ps]);
+            abuf[ps] = load_a(s + (int64_t)PF * WPB);
+            consume(buf[u], okx[u], abuf[u], a_valid(s));
+        };
+        // whole ring turns without exits (uniform load counts), then the rest
+        const int64_t nsteps = (se - s0 + WPB - 1) / WPB;
+        const int64_t nturns = nsteps / R;
+        int64_t s = s0;
+        for (int64_t t = 0; t < nturns; ++t) {
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                step(u, s);
+                s += WPB;
+            }
+        }
+        const int rest = (int)(nsteps - nturns * R);
+#pragma unroll
+        for (int u = 0; u < R - 1; ++u) {
+            if (u < rest) step(u, s);
+            s += WPB;
+        }
     }
 
     // D layout of the 16x16 MFMA family: lane l, element i -> row 4*(l/16)+i, col l%16
+    if constexpr (WPB > 1) {
+        // fixed-order sum of the waves' partials in LDS (deterministic)
+        float* red = reinterpret_cast<float*>(stage_all);
+        __syncthreads();
+#pragma unroll 1
+        for (int k = 0; k < WPB; ++k) {
+            if (wave == k) {
+#pragma unroll
+                for (int b = 0; b < NBLK; ++b) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int e = (4 * ag + i) * NC + b * 16 + bn;
+                        red[e] = k == 0 ? acc[b][i] : red[e] + acc[b][i];
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        if (slot < 0) {
+            const int64_t row0 = w * 16;
+            for (int e = threadIdx.x; e < 16 * NC; e += 64 * WPB) {
+                const int r = e / NC, c = e % NC;
+                if (n0 + c < N) store_out<XT>(a.y, (row0 + r) * a.ldy + n0 + c, red[e]);
+            }
+        } else {
+            float* P = a.partials + ((int64_t)slot * a.nchunks + chunk) * (16 * NC);
+            for (int e = threadIdx.x; e < 16 * NC; e += 64 * WPB) P[e] = red[e];
+        }
+        return;
+    }
     if (slot < 0) {
         const int64_t row0 = w * 16;
 #pragma unroll
@@ -361,19 +443,44 @@ __global__ void plan_fill_kernel(const int64_t* __restrict__ win_off, int64_t W,
 
 int nblk_for(int64_t N) { return N <= 16 ? 1 : (N <= 32 ? 2 : (N <= 64 ? 4 : 8)); }
 
-template <int XT, bool AF32, int TC, int NBLK, bool VECT>
+template <int XT, bool AF32, int TC, int NBLK, bool VECT, int WPB>
 int launch_fwd(const SpmmArgs& a, hipStream_t stream) {
-    int64_t total = a.num_items * a.nchunks;
-    int64_t grid = ((total + 7) / 8) * 8;
+    const int64_t total = a.num_items * a.nchunks;
+    const int64_t grid = ((total + 7) / 8) * 8;
     if (grid > INT32_MAX) return set_error(GRWS_E_INVALID, "spmm: too many work items (%lld)", (long long)total);
-    hipLaunchKernelGGL((spmm_fwd_kernel<XT, AF32, TC, NBLK, VECT>), dim3((unsigned)grid), dim3(64), 0, stream, a);
+    int pf = 1;
+    if (const char* e = getenv("GRWS_SPMM_PF")) pf = atoi(e) == 2 ? 2 : 1;  // tuning override
+    if (pf == 2)
+        hipLaunchKernelGGL((spmm_fwd_kernel<XT, AF32, TC, NBLK, VECT, WPB, 2>), dim3((unsigned)grid),
+                           dim3(64 * WPB), 0, stream, a);
+    else
+        hipLaunchKernelGGL((spmm_fwd_kernel<XT, AF32, TC, NBLK, VECT, WPB, 1>), dim3((unsigned)grid),
+                           dim3(64 * WPB), 0, stream, a);
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }
 
+// Waves per work-group.  Two waves share an (item, chunk) when the launch has
+// plenty of work-groups (irregular graphs with many windows gain from it);
+// small launches keep one wave per work-group so the chip still fills.
+int waves_for(const SpmmArgs& a, int nblk) {
+    (void)nblk;
+    if (const char* e = getenv("GRWS_SPMM_WAVES")) {  // tuning override
+        const int v = atoi(e);
+        if (v == 1 || v == 2) return v;
+    }
+    return a.num_items * a.nchunks >= 65536 ? 2 : 1;
+}
+
 template <int XT, bool AF32, int TC, int NBLK>
 int dispatch_vec(const SpmmArgs& a, bool vect, hipStream_t stream) {
-    return vect ? launch_fwd<XT, AF32, TC, NBLK, true>(a, stream) : launch_fwd<XT, AF32, TC, NBLK, false>(a, stream);
+    const int wpb = waves_for(a, NBLK);
+    if (vect) {
+        if (wpb == 2) return launch_fwd<XT, AF32, TC, NBLK, true, 2>(a, stream);
+        return launch_fwd<XT, AF32, TC, NBLK, true, 1>(a, stream);
+    }
+    if (wpb == 2) return launch_fwd<XT, AF32, TC, NBLK, false, 2>(a, stream);
+    return launch_fwd<XT, AF32, TC, NBLK, false, 1>(a, stream);
 }
 
 template <int XT, bool AF32, int TC>

@@ -150,3 +150,12 @@ def test_window_sampler_host_checks_without_gpu():
     st = lib.grws_sample_hop(None, None, 10, 0, None, 5, 8, 42, None, None, None, 39, None, 0,
                              ctypes.byref(T), None)
     assert st == -1 and b"edge_capacity" in lib.grws_last_error()
+
+
+def test_aligned_rows_keeps_values_and_pads_pitch():
+    from graph_rws_amd.data import aligned_rows
+    x = torch.randn(7, 608).half()
+    y = aligned_rows(x)
+    assert y.stride() == (640, 1) and y.shape == x.shape and torch.equal(x, y)
+    z = torch.randn(3, 256)  # 1024 B rows: already aligned, returned as is
+    assert aligned_rows(z) is z
