@@ -102,6 +102,16 @@ _PROTOS = {
     "grws_window_recompress": (ctypes.c_int, [ctypes.POINTER(BcsrView), _vp, ctypes.c_int64,
                                               ctypes.c_int32, _vp, _vp, _vp, ctypes.c_int64, _vp,
                                               _vp, _vp]),
+    "grws_sample_state_init": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, _vp]),
+    "grws_sample_block_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int32,
+                                                            ctypes.c_int64]),
+    "grws_sample_block_capacity": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                                  _c_i64p, _c_i64p]),
+    "grws_sample_block": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp,
+                                         ctypes.c_int64, ctypes.c_int32, ctypes.c_uint64, _vp, _vp,
+                                         ctypes.c_int32, ctypes.c_int32, _vp, ctypes.c_int64, _vp,
+                                         _vp, _vp, ctypes.c_int64, _vp, ctypes.c_size_t, _c_i64p,
+                                         _vp]),
     "grws_relabel_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
     "grws_relabel": (ctypes.c_int, [_vp, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int64,
                                     _vp, _vp, ctypes.c_int64, _vp, ctypes.c_size_t, _c_i64p,

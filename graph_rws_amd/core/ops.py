@@ -475,3 +475,49 @@ def sample_all_layers(window_offset: torch.Tensor, original_col_indices: torch.T
         p3 = ev[1].elapsed_time(ev[2])
         timings.append(SamplingTimingResult(p1, 0.0, p3, p1 + p3))
     return layers, timings
+
+
+class SampleState:
+    """Per-graph scratch of the fused sampler: a node -> local id map (int32,
+    all -1 between calls) and a new-source bitmap (uint32, all 0 between
+    calls).  Every grws_sample_block call leaves both as it found them.  One
+    state serves one stream at a time."""
+
+    def __init__(self, num_nodes: int, device):
+        self.num_nodes = int(num_nodes)
+        self.node_map = torch.empty(max(1, self.num_nodes), dtype=torch.int32, device=device)
+        self.bitmap = torch.empty(max(1, (self.num_nodes + 31) // 32), dtype=torch.int32, device=device)
+        L.call("grws_sample_state_init", L.ptr(self.node_map), L.ptr(self.bitmap), self.num_nodes,
+               L.stream_of(torch.device(device)))
+
+
+def sample_block(indptr: torch.Tensor, indices: torch.Tensor, frontier: torch.Tensor, fanout: int,
+                 state: SampleState, seed: int = 42, tile_cols: int = 16,
+                 values_dtype: torch.dtype = torch.float32):
+    """One hop in one call: fanout sampling, relabel and the hop's BCSR block
+    (rows = frontier positions, columns = local source ids).  Returns
+    (window_offset int64 [W+1], col_indices int32, values, next_frontier
+    int64 [num_src], num_edges).  One stream sync."""
+    n, nnz = _csr_arrays(indptr, indices)
+    dev = indptr.device
+    fr = frontier.to(dev, torch.int64).contiguous()
+    F = fr.numel()
+    lib = L.load()
+    ms, mt = ctypes.c_int64(), ctypes.c_int64()
+    L.call("grws_sample_block_capacity", F, int(fanout), int(tile_cols), ctypes.byref(ms),
+           ctypes.byref(mt))
+    W = (F + 15) // 16
+    nxt = torch.empty(max(1, ms.value), dtype=torch.int64, device=dev)
+    win = torch.empty(W + 1, dtype=torch.int64, device=dev)
+    cols = torch.empty(max(1, mt.value * tile_cols), dtype=torch.int32, device=dev)
+    vals = torch.empty(max(1, mt.value * 16 * tile_cols), dtype=values_dtype, device=dev)
+    wsb = int(lib.grws_sample_block_workspace_bytes(F, int(fanout), n))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    counts = (ctypes.c_int64 * 3)()
+    L.call("grws_sample_block", L.ptr(indptr), L.ptr(indices), n, nnz, L.ptr(fr), F, int(fanout),
+           ctypes.c_uint64(int(seed) & 0xFFFFFFFFFFFFFFFF), L.ptr(state.node_map), L.ptr(state.bitmap),
+           int(tile_cols), L.dtype_code(values_dtype), L.ptr(nxt), ms.value, L.ptr(win), L.ptr(cols),
+           L.ptr(vals), mt.value, L.ptr(ws), wsb, ctypes.cast(counts, ctypes.POINTER(ctypes.c_int64)),
+           L.stream_of(dev))
+    E, S, T = (int(c) for c in counts)
+    return win, cols[:T * tile_cols], vals[:T * 16 * tile_cols], nxt[:S], E

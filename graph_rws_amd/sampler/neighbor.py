@@ -28,6 +28,7 @@ from typing import List, Optional, Sequence
 import torch
 
 from ..core import relabel, sample_hop
+from ..core.ops import SampleState, sample_block
 from ..data import BCSRGraph
 
 
@@ -44,7 +45,7 @@ class NeighborSampler:
 
     def __init__(self, fanouts: Sequence[int], seed: int = 42, tile_rows: int = 16,
                  tile_cols: int = 16, values_dtype: torch.dtype = torch.float32,
-                 verbose: bool = False):
+                 verbose: bool = False, fused: bool = True):
         if tile_rows != 16:
             raise ValueError("tile_rows must be 16")
         if tile_cols not in (8, 16):
@@ -61,6 +62,10 @@ class NeighborSampler:
         self.last_stats: dict = {}
         self.total_edges = 0
         self.total_batches = 0
+        # fused: one grws_sample_block call per hop (dense relabel state kept
+        # per graph); otherwise sample_hop + relabel + COO build
+        self.fused = bool(fused)
+        self._state = None
 
     def sample_layers(self, indptr: torch.Tensor, indices: torch.Tensor,
                       seed_nodes: torch.Tensor) -> List[BCSRGraph]:
@@ -77,20 +82,29 @@ class NeighborSampler:
         blocks: List[BCSRGraph] = []
         t0 = time.perf_counter()
         edges = 0
+        if self.fused and (self._state is None or self._state.num_nodes != num_nodes
+                           or self._state.node_map.device != dev):
+            self._state = SampleState(num_nodes, dev)
         for k in reversed(self.fanouts):
-            dst, src, val = sample_hop(indptr, indices, frontier, k, seed=self.seed)
-            src_local, nxt = relabel(frontier, src, num_nodes)
+            if self.fused:
+                win, cols, vals, nxt, E = sample_block(indptr, indices, frontier, k, self._state,
+                                                       seed=self.seed, tile_cols=self.tile_cols,
+                                                       values_dtype=self.values_dtype)
+            else:
+                dst, src, val = sample_hop(indptr, indices, frontier, k, seed=self.seed)
+                src_local, nxt = relabel(frontier, src, num_nodes)
+                win, cols, vals = builder.coo_to_bcsr_device(
+                    frontier.numel(), nxt.numel(), dst, src_local, val, tile_cols=self.tile_cols,
+                    values_dtype=self.values_dtype)
+                E = int(dst.numel())
             F, S = frontier.numel(), nxt.numel()
-            win, cols, vals = builder.coo_to_bcsr_device(
-                F, S, dst, src_local, val, tile_cols=self.tile_cols,
-                values_dtype=self.values_dtype)
-            g = BCSRGraph(num_nodes=F, num_edges=int(dst.numel()), tile_rows=16,
+            g = BCSRGraph(num_nodes=F, num_edges=E, tile_rows=16,
                           tile_cols=self.tile_cols, window_offset=win, original_col_indices=cols,
                           values_condensed=vals, device=dev, num_rows=F, num_cols=S,
                           values_dtype=self.values_dtype)
             g.src_nodes = nxt
             g.dst_nodes = frontier
-            g.num_sampled_edges = int(dst.numel())
+            g.num_sampled_edges = E
             g.fanout = k
             blocks.insert(0, g)
             edges += g.num_sampled_edges

@@ -257,6 +257,34 @@ int grws_sample_hop(const int64_t* indptr, const int32_t* indices, int64_t num_n
 /* distinct (GRWS_E_INVALID otherwise).  Synchronises `stream`.              */
 /* ------------------------------------------------------------------------ */
 /* ------------------------------------------------------------------------ */
+/* One hop in one call: grws_sample_hop + relabel + the hop's BCSR block     */
+/* (what BCSRGraph.from_dgl_block builds from a sampled block,               */
+/* data/bcsr.py:266-306), with a single synchronisation.  Same results as    */
+/* the three separate calls.                                                 */
+/*                                                                          */
+/* The relabel uses caller-owned state instead of sorting: node_map int32    */
+/* [num_nodes], all -1, and bitmap uint32 [ceil(num_nodes/32)], all 0; every */
+/* call leaves them so (grws_sample_state_init sets them up).  Calls sharing */
+/* one state must not overlap.                                               */
+/*                                                                          */
+/* Outputs: next_frontier int64 [max_src] (frontier, then new sources in     */
+/* ascending id), window_offset int64 [ceil(F/16)+1], col_indices int32 and  */
+/* values (values_dtype) for up to max_tiles tiles; the bounds come from     */
+/* grws_sample_block_capacity.  counts_out[3] = {edges, sources, tiles}.     */
+/* Synchronises `stream`.                                                    */
+/* ------------------------------------------------------------------------ */
+int grws_sample_state_init(int32_t* node_map, uint32_t* bitmap, int64_t num_nodes, void* stream);
+size_t grws_sample_block_workspace_bytes(int64_t num_frontier, int32_t fanout, int64_t num_nodes);
+int grws_sample_block_capacity(int64_t num_frontier, int32_t fanout, int32_t tile_cols,
+                               int64_t* max_src, int64_t* max_tiles);
+int grws_sample_block(const int64_t* indptr, const int32_t* indices, int64_t num_nodes, int64_t nnz,
+                      const int64_t* frontier, int64_t num_frontier, int32_t fanout, uint64_t seed,
+                      int32_t* node_map, uint32_t* bitmap, int32_t tile_cols, int32_t values_dtype,
+                      int64_t* next_frontier, int64_t max_src, int64_t* window_offset,
+                      int32_t* col_indices, void* values, int64_t max_tiles, void* workspace,
+                      size_t workspace_bytes, int64_t* counts_out, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Window top-K sampling: the reference-compatible core_lib.sample_all_layers */
 /* (bind.cpp:99-121 -> sampling_wrapper.cu:365-438), one call per phase.     */
 /* ------------------------------------------------------------------------ */

@@ -107,16 +107,40 @@ def _check_blocks(blocks, ref, vdt):
         assert torch.equal(b.values_condensed.cpu(), want)
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("tc,vdt", [(16, torch.float32), (8, torch.float32), (16, torch.float16),
                                     (16, torch.bfloat16)])
-def test_neighbor_sampler_blocks_bit_exact(cuda_device, tc, vdt):
+def test_neighbor_sampler_blocks_bit_exact(cuda_device, tc, vdt, fused):
     g = synth.c5_graph(device=cuda_device, scale=2e-4)  # 22k nodes, 320k edges
     seeds = synth.distinct_seeds(g.num_nodes, 256, seed=7, device=cuda_device)
-    s = NeighborSampler([15, 10, 5], seed=42, tile_cols=tc, values_dtype=vdt)
+    s = NeighborSampler([15, 10, 5], seed=42, tile_cols=tc, values_dtype=vdt, fused=fused)
     blocks = s.sample_layers(g.row_ptr, g.col_idx, seeds)
     ref = oracle.sample_blocks(g.row_ptr.cpu().numpy(), g.col_idx.cpu().numpy(),
                                seeds.cpu().numpy(), [15, 10, 5], seed=42, tile_cols=tc)
     _check_blocks(blocks, ref, vdt)
+
+
+def test_fused_block_state_restored_and_fanout_64(cuda_device):
+    """The dense relabel state is all -1 / all 0 after every call, also
+    after a call that fails (duplicate frontier ids); fanout 64 (windows of
+    up to 1,024 edges) matches the oracle."""
+    from graph_rws_amd.core.ops import SampleState, sample_block
+    degs = np.random.default_rng(6).integers(0, 300, 5000)
+    ip, ix, ipd, ixd = _csr(degs, 5000, 7, cuda_device)
+    st = SampleState(5000, cuda_device)
+    fr = np.random.default_rng(8).choice(5000, 700, replace=False).astype(np.int64)
+    win, cols, vals, nxt, E = sample_block(ipd, ixd, torch.from_numpy(fr).to(cuda_device), 64, st)
+    ref = oracle.sample_blocks(ip, ix, fr, [64], seed=42, tile_cols=16)[0]
+    np.testing.assert_array_equal(nxt.cpu().numpy(), ref["src_nodes"])
+    np.testing.assert_array_equal(win.cpu().numpy(), ref["win"])
+    np.testing.assert_array_equal(cols.cpu().numpy(), ref["cols"])
+    np.testing.assert_array_equal(vals.cpu().numpy(), ref["vals"])
+    assert E == ref["dst"].size
+    assert bool((st.node_map == -1).all()) and bool((st.bitmap == 0).all())
+    bad = torch.tensor([3, 9, 3], device=cuda_device)
+    with pytest.raises(GrwsError, match="twice"):
+        sample_block(ipd, ixd, bad, 5, st)
+    assert bool((st.node_map == -1).all()) and bool((st.bitmap == 0).all())
 
 
 def test_neighbor_sampler_c5_batch_shape(cuda_device):
