@@ -521,3 +521,33 @@ def sample_block(indptr: torch.Tensor, indices: torch.Tensor, frontier: torch.Te
            L.stream_of(dev))
     E, S, T = (int(c) for c in counts)
     return win, cols[:T * tile_cols], vals[:T * 16 * tile_cols], nxt[:S], E
+
+
+# ---------------------------------------------------------------------------
+# weight gradient A^T B (csrc/gemm_tn.hip)
+# ---------------------------------------------------------------------------
+def gemm_tn_supported(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Whether gemm_tn takes these operands (F16/BF16 on the GPU, widths and
+    row strides multiples of 8, 16-byte aligned, unit column stride)."""
+    return (a.is_cuda and b.is_cuda and a.dim() == 2 and b.dim() == 2
+            and a.dtype == b.dtype and a.dtype in (torch.float16, torch.bfloat16)
+            and a.shape[0] == b.shape[0] and a.stride(1) == 1 and b.stride(1) == 1
+            and a.shape[1] % 8 == 0 and b.shape[1] % 8 == 0
+            and a.stride(0) % 8 == 0 and b.stride(0) % 8 == 0
+            and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0)
+
+
+def gemm_tn(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """a^T @ b for a [K, M], b [K, N] (split over K, fp32 accumulation,
+    deterministic); returns [M, N] in out_dtype (float32 or the inputs')."""
+    if not gemm_tn_supported(a, b):
+        raise ValueError("gemm_tn: unsupported operands (see gemm_tn_supported)")
+    K, M = a.shape
+    N = b.shape[1]
+    out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    wsb = int(L.load().grws_gemm_tn_workspace_bytes(K, M, N))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=a.device)
+    L.call("grws_gemm_tn", L.ptr(a), a.stride(0), L.ptr(b), b.stride(0), L.dtype_code(a.dtype), K, M,
+           N, L.ptr(out), out.stride(0), L.dtype_code(out_dtype), L.ptr(ws), wsb,
+           L.stream_of(a.device))
+    return out

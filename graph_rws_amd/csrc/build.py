@@ -31,6 +31,7 @@ SOURCES = [
     "reindex.hip",
     "sample.hip",
     "window_sample.hip",
+    "gemm_tn.hip",
 ]
 
 ARCH = os.environ.get("GRWS_OFFLOAD_ARCH", "gfx950")

@@ -1,0 +1,209 @@
+// Weight gradient C[M x N] = A^T B for tall, skinny operands (gfx950).
+//
+// The backward of the reference's graph convolution computes
+// grad_weight = features^T @ grad_input_aggr (layers/layer.py:61-92) and,
+// through autograd, the self path's weight gradient the same way
+// (layer.py:171-175): K = the node count (10^5..10^6), M and N = the layer
+// widths (<= a few hundred).  A library GEMM tiles the small M x N output
+// into a handful of work-groups, so most of the chip idles while each
+// streams all of K.  Here K is split instead:
+//   * work-group (M-tile of 128, N-tile of 128, K-chunk): 4 wave64s, each a
+//     64 x 64 block of the output as 4 x 4 v_mfma_f32_16x16x16 tiles;
+//   * per step, 32 rows of A and B (128 columns each) are loaded with
+//     16-byte coalesced loads and staged in LDS; the MFMA fragments are read
+//     from LDS (A^T needs A's columns, 4 consecutive k per lane);
+//   * every chunk writes an fp32 partial; a second kernel adds the chunks
+//     in order (deterministic, no atomics) and writes C.
+// A and B are each read once per N-tile / M-tile of the other operand.
+#include "grws_internal.h"
+
+namespace grws {
+namespace {
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kT = 128;       // output tile edge
+constexpr int kStep = 32;     // K rows per LDS stage
+constexpr int kPitch = kT + 8;  // LDS row pitch (elements)
+constexpr int kMaxChunks = 512;
+constexpr int64_t kMinChunkRows = 1024;
+
+template <int DT>
+__global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const uint16_t* __restrict__ A, int64_t lda,
+                                                              const uint16_t* __restrict__ B, int64_t ldb,
+                                                              int64_t K, int M, int N, int64_t kc,
+                                                              float* __restrict__ partials) {
+    __shared__ __attribute__((aligned(16))) uint16_t sA[kStep * kPitch];
+    __shared__ __attribute__((aligned(16))) uint16_t sB[kStep * kPitch];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int i0 = blockIdx.x * kT;
+    const int j0 = blockIdx.y * kT;
+    const int64_t chunk = blockIdx.z;
+    const int64_t kb = chunk * kc;
+    const int64_t ke = kb + kc < K ? kb + kc : K;
+    const int wm = (wave & 1) * 64;
+    const int wn = (wave >> 1) * 64;
+    const int fr = lane & 15;      // fragment row / column within a 16 x 16 tile
+    const int fk = (lane >> 4) * 4;  // first of the lane's 4 consecutive k
+
+    float4_t acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // staging geometry: 32 rows x 128 columns = 512 loads of 8 elements,
+    // two per thread for each operand
+    for (int64_t k0 = kb; k0 < ke; k0 += kStep) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int e = (tid + 256 * q) * 8;
+            const int r = e / kT, c = e % kT;
+            const int64_t k = k0 + r;
+            const bool okr = k < ke;
+            u32x4_t va = {0u, 0u, 0u, 0u}, vb = {0u, 0u, 0u, 0u};
+            if (okr && i0 + c < M) va = *reinterpret_cast<const u32x4_t*>(A + k * lda + i0 + c);
+            if (okr && j0 + c < N) vb = *reinterpret_cast<const u32x4_t*>(B + k * ldb + j0 + c);
+            *reinterpret_cast<u32x4_t*>(&sA[r * kPitch + c]) = va;
+            *reinterpret_cast<u32x4_t*>(&sB[r * kPitch + c]) = vb;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < kStep; ks += 16) {
+            short4_t af[4], bf[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint16_t* pa = &sA[(ks + fk) * kPitch + wm + 16 * t + fr];
+                const uint16_t* pb = &sB[(ks + fk) * kPitch + wn + 16 * t + fr];
+                af[t] = short4_t{(short)pa[0], (short)pa[kPitch], (short)pa[2 * kPitch], (short)pa[3 * kPitch]};
+                bf[t] = short4_t{(short)pb[0], (short)pb[kPitch], (short)pb[2 * kPitch], (short)pb[3 * kPitch]};
+            }
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    if constexpr (DT == GRWS_F16)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, af[a]),
+                                                                          __builtin_bit_cast(half4_t, bf[b]),
+                                                                          acc[a][b], 0, 0, 0);
+                    else
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(af[a], bf[b], acc[a][b], 0, 0, 0);
+                }
+        }
+        __syncthreads();
+    }
+    // D layout: lane l, element e -> row 4*(l/16)+e, column l%16 of the tile
+    float* P = partials + chunk * (int64_t)M * N;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int j = j0 + wn + 16 * b + fr;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = i0 + wm + 16 * a + fk + e;
+                if (i < M && j < N) P[(int64_t)i * N + j] = acc[a][b][e];
+            }
+        }
+}
+
+// C[i][j] = sum over chunks, in chunk order.
+template <int OT>
+__global__ void gemm_tn_reduce_kernel(const float* __restrict__ partials, int64_t nchunks, int M, int N, void* c,
+                                      int64_t ldc) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)M * N) return;
+    const int64_t mn = (int64_t)M * N;
+    float s = 0.f;
+    for (int64_t ch = 0; ch < nchunks; ++ch) s += partials[ch * mn + idx];
+    const int64_t i = idx / N, j = idx % N;
+    if constexpr (OT == GRWS_F32) {
+        static_cast<float*>(c)[i * ldc + j] = s;
+    } else if constexpr (OT == GRWS_F16) {
+        static_cast<_Float16*>(c)[i * ldc + j] = (_Float16)s;
+    } else {
+        static_cast<__hip_bfloat16*>(c)[i * ldc + j] = __float2bfloat16(s);
+    }
+}
+
+int64_t chunks_for(int64_t K) {
+    int64_t n = (K + kMinChunkRows - 1) / kMinChunkRows;
+    if (n > kMaxChunks) n = kMaxChunks;
+    return n < 1 ? 1 : n;
+}
+
+}  // namespace
+}  // namespace grws
+
+using namespace grws;
+
+extern "C" size_t grws_gemm_tn_workspace_bytes(int64_t K, int64_t M, int64_t N) {
+    if (K < 0 || M < 0 || N < 0) return 0;
+    return (size_t)chunks_for(K) * (size_t)M * (size_t)N * sizeof(float);
+}
+
+extern "C" int grws_gemm_tn(const void* a, int64_t lda, const void* b, int64_t ldb, int32_t in_dtype, int64_t K,
+                            int64_t M, int64_t N, void* c, int64_t ldc, int32_t out_dtype, void* workspace,
+                            size_t workspace_bytes, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(K >= 0 && M >= 0 && N >= 0, "gemm_tn: negative size");
+    GRWS_CHECK_ARG(M <= 65536 && N <= 65536, "gemm_tn: M and N must be at most 65536");
+    if (in_dtype != GRWS_F16 && in_dtype != GRWS_BF16)
+        return set_error(GRWS_E_DTYPE, "gemm_tn: inputs must be F16 or BF16 (got %d)", in_dtype);
+    if (out_dtype != GRWS_F32 && out_dtype != in_dtype)
+        return set_error(GRWS_E_DTYPE, "gemm_tn: output must be F32 or the input dtype");
+    GRWS_CHECK_ARG(M % 8 == 0 && N % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0,
+                   "gemm_tn: M, N, lda and ldb must be multiples of 8");
+    GRWS_CHECK_ARG(lda >= M && ldb >= N && ldc >= N, "gemm_tn: leading dimensions too small");
+    if (M == 0 || N == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(c != nullptr, "gemm_tn: null output");
+    if (K > 0) {
+        GRWS_CHECK_ARG(a && b, "gemm_tn: null input");
+        GRWS_CHECK_ARG((reinterpret_cast<uintptr_t>(a) % 16) == 0 && (reinterpret_cast<uintptr_t>(b) % 16) == 0,
+                       "gemm_tn: inputs must be 16-byte aligned");
+    }
+    const int64_t nch = K > 0 ? chunks_for(K) : 0;
+    const size_t need = (size_t)nch * (size_t)M * (size_t)N * sizeof(float);
+    if (nch > 0 && (!workspace || workspace_bytes < need))
+        return set_error(GRWS_E_CAPACITY, "gemm_tn: workspace too small (%zu < %zu)", workspace_bytes, need);
+    int64_t chunks = 0;  // K == 0: the reduction over no chunks writes zeros
+    if (nch > 0) {
+        const int64_t kc = ((K + nch - 1) / nch + kStep - 1) / kStep * kStep;
+        chunks = (K + kc - 1) / kc;
+        dim3 grid((unsigned)((M + kT - 1) / kT), (unsigned)((N + kT - 1) / kT), (unsigned)chunks);
+        if (in_dtype == GRWS_F16)
+            hipLaunchKernelGGL(gemm_tn_partial_kernel<GRWS_F16>, grid, dim3(256), 0, stream,
+                               static_cast<const uint16_t*>(a), lda, static_cast<const uint16_t*>(b), ldb, K,
+                               (int)M, (int)N, kc, static_cast<float*>(workspace));
+        else
+            hipLaunchKernelGGL(gemm_tn_partial_kernel<GRWS_BF16>, grid, dim3(256), 0, stream,
+                               static_cast<const uint16_t*>(a), lda, static_cast<const uint16_t*>(b), ldb, K,
+                               (int)M, (int)N, kc, static_cast<float*>(workspace));
+        GRWS_LAUNCH_CHECK();
+    }
+    {
+        const unsigned rg = (unsigned)((M * N + 255) / 256);
+        switch (out_dtype) {
+            case GRWS_F32:
+                hipLaunchKernelGGL(gemm_tn_reduce_kernel<GRWS_F32>, dim3(rg), dim3(256), 0, stream,
+                                   static_cast<const float*>(workspace), chunks, (int)M, (int)N, c, ldc);
+                break;
+            case GRWS_F16:
+                hipLaunchKernelGGL(gemm_tn_reduce_kernel<GRWS_F16>, dim3(rg), dim3(256), 0, stream,
+                                   static_cast<const float*>(workspace), chunks, (int)M, (int)N, c, ldc);
+                break;
+            default:
+                hipLaunchKernelGGL(gemm_tn_reduce_kernel<GRWS_BF16>, dim3(rg), dim3(256), 0, stream,
+                                   static_cast<const float*>(workspace), chunks, (int)M, (int)N, c, ldc);
+                break;
+        }
+        GRWS_LAUNCH_CHECK();
+    }
+    return GRWS_OK;
+}

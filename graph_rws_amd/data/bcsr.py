@@ -233,8 +233,14 @@ class BCSRGraph:
 
     # ---------------- MI355X additions ----------------
     def spmm_plan(self, n_cols: int):
-        """Cached SpMM schedule for outputs of width n_cols."""
+        """Cached SpMM schedule for outputs of width n_cols, or None when no
+        window can exceed the per-item slab budget (``max_window_slabs``
+        known, e.g. for sampled blocks): then one work item per window is the
+        schedule and no plan needs building."""
         slabs = default_slabs(self.num_windows, self.num_tiles, self.tile_cols, n_cols)
+        mws = getattr(self, "max_window_slabs", None)
+        if mws is not None and mws <= slabs:
+            return None
         key = ("plan", slabs, self.window_offset.data_ptr())
         p = self._cache.get(key)
         if p is None:

@@ -66,6 +66,10 @@ def _adopt(tensors, stream) -> None:
 
 def _graph_tensors(g):
     out = [g.window_offset, g.original_col_indices, g.values_condensed]
+    cached = getattr(g, "_cache", {}).get("T")
+    if cached is not None:  # a transpose built on the sampling stream
+        AT = cached[1]
+        out += [AT.window_offset, AT.original_col_indices, AT.values_condensed]
     for name in ("active_windows", "active_masks", "src_nodes", "dst_nodes"):
         t = getattr(g, name, None)
         if t is not None:
@@ -85,6 +89,11 @@ def _sample_batch(sampler, graph, seeds, features, device):
     from ..sampler import NeighborSampler
     if isinstance(sampler, NeighborSampler):
         blocks = sampler.sample_layers(graph.row_ptr, graph.col_idx, seeds)
+        if torch.is_grad_enabled():
+            # build the backward's A^T here, on the sampling stream, off the
+            # training critical path (blocks are not modified afterwards)
+            for b in blocks:
+                b.transpose()
         inp = blocks[0].src_nodes
         if features.is_cuda:
             feats = features.index_select(0, inp)

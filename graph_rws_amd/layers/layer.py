@@ -32,18 +32,38 @@ def _spmm_timed(graph, x: torch.Tensor):
     return y, float(e0.elapsed_time(e1))
 
 
+def _autocast_operand(x: torch.Tensor) -> torch.Tensor:
+    """x in the dtype autocast would multiply it in (x itself otherwise)."""
+    if x.is_cuda and torch.is_autocast_enabled("cuda"):
+        dt = torch.get_autocast_dtype("cuda")
+        if x.dtype != dt and x.is_floating_point():
+            return x.to(dt)
+    return x
+
+
+def _weight_grad(x: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+    """x^T @ g: the split-K gfx950 kernel for tall f16/bf16 operands (the
+    library GEMM leaves most of the chip idle on this shape), torch
+    otherwise.  float32 result from the kernel."""
+    if x.shape[0] >= 4096 and _ops.gemm_tn_supported(x, g):
+        return _ops.gemm_tn(x, g, out_dtype=torch.float32)
+    return torch.matmul(x.t(), g)
+
+
 class BCSRSPMMFunction(Function):
     """output = A @ (X @ W) with A a BCSRGraph (layer.py:28-92).  Under
     torch.autocast the backward runs in the forward's autocast state, so a
-    float16/bfloat16 forward has a float16/bfloat16 backward SpMM."""
+    float16/bfloat16 forward has a float16/bfloat16 backward SpMM; the
+    features are kept in the autocast dtype for the weight gradient."""
 
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
     def forward(ctx, graph, features, weight, warps_per_block):
-        x_mult_w = torch.matmul(features, weight)
+        xh = _autocast_operand(features)
+        x_mult_w = torch.matmul(xh, weight)
         output, timing = _spmm_timed(graph, x_mult_w)
         record_spmm_time(timing)
-        ctx.save_for_backward(features, weight)
+        ctx.save_for_backward(xh, weight)
         ctx.graph = graph
         ctx.warps_per_block = warps_per_block
         return output
@@ -60,8 +80,28 @@ class BCSRSPMMFunction(Function):
         if ctx.needs_input_grad[1]:
             grad_features = torch.matmul(grad_input_aggr, weight.t())
         if ctx.needs_input_grad[2]:
-            grad_weight = torch.matmul(features.t(), grad_input_aggr)
+            grad_weight = _weight_grad(features, grad_input_aggr)
         return None, grad_features, grad_weight, None
+
+
+class _SelfLinear(Function):
+    """x @ W for the self path (layer.py:171-175) with the weight gradient on
+    the split-K kernel; the same arithmetic as torch.matmul under autocast."""
+
+    @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda")
+    def forward(ctx, x, weight):
+        xh = _autocast_operand(x)
+        ctx.save_for_backward(xh, weight)
+        return torch.matmul(xh, weight)
+
+    @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
+    def backward(ctx, grad):
+        xh, weight = ctx.saved_tensors
+        gx = torch.matmul(grad, weight.t()) if ctx.needs_input_grad[0] else None
+        gw = _weight_grad(xh, grad.contiguous()) if ctx.needs_input_grad[1] else None
+        return gx, gw
 
 
 class BCSRGraphConv(nn.Module):
@@ -93,7 +133,7 @@ class BCSRGraphConv(nn.Module):
             h_in_self = features[:target_rows]
         else:
             h_in_self = F.pad(features, (0, 0, 0, target_rows - features.shape[0]))
-        h_self = torch.matmul(h_in_self, self.weight_self)
+        h_self = _SelfLinear.apply(h_in_self, self.weight_self)
         if h_neigh.shape[0] > h_self.shape[0]:
             h_neigh = h_neigh[:h_self.shape[0]]
         elif h_neigh.shape[0] < h_self.shape[0]:

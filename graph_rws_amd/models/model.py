@@ -98,7 +98,10 @@ class GCN_BCSR(nn.Module):
                               int(num_in))
 
     def _sanitize_and_reindex(self, layer_idx, curr_g, prev_g, h_in_shape):
-        if getattr(curr_g, "is_local_input", False):
+        # is_local_input (the reference's UVA mode) and columns_local (blocks
+        # of the node-wise sampler) hold local columns already; the SpMM
+        # skips -1 padding, so they need no masking or reindex
+        if getattr(curr_g, "is_local_input", False) or getattr(curr_g, "columns_local", False):
             curr_g.num_cols = h_in_shape[0]
             return
         fwd_g = getattr(curr_g, "fwd", curr_g)

@@ -105,6 +105,11 @@ class NeighborSampler:
             g.src_nodes = nxt
             g.dst_nodes = frontier
             g.num_sampled_edges = E
+            # columns are local ids into the layer input (-1 only as padding):
+            # the model needs no masking or reindex for this block
+            g.columns_local = True
+            # at most 16 x fanout distinct columns per window
+            g.max_window_slabs = (16 * k + 15) // 16
             g.fanout = k
             blocks.insert(0, g)
             edges += g.num_sampled_edges

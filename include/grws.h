@@ -351,6 +351,20 @@ int grws_relabel(const int64_t* frontier, int64_t num_frontier, const int64_t* e
                  int64_t next_capacity, void* workspace, size_t workspace_bytes,
                  int64_t* num_src_out, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Weight gradient C[M x N] = A^T B, A [K x M] and B [K x N] row-major       */
+/* F16/BF16, fp32 accumulation, C in F32 or the input dtype.  The backward   */
+/* of the graph convolution (layers/layer.py:61-92: grad_weight =            */
+/* features^T @ grad_input_aggr, and the self path's weight through          */
+/* autograd, layer.py:171-175) has K = node count and M, N = layer widths;  */
+/* K is split over work-groups and the fp32 partials added in a fixed order  */
+/* (deterministic).  M, N, lda, ldb multiples of 8; A and B 16-byte aligned. */
+/* ------------------------------------------------------------------------ */
+size_t grws_gemm_tn_workspace_bytes(int64_t K, int64_t M, int64_t N);
+int grws_gemm_tn(const void* a, int64_t lda, const void* b, int64_t ldb, int32_t in_dtype, int64_t K,
+                 int64_t M, int64_t N, void* c, int64_t ldc, int32_t out_dtype, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
