@@ -89,6 +89,26 @@ def _cached_plan(window_offset: torch.Tensor, col_indices: torch.Tensor, tile_co
     return hit[1]
 
 
+def _widen(t: torch.Tensor, vec: int) -> torch.Tensor:
+    """t [R, C] as [R, C'] with C' = C rounded up to a multiple of vec,
+    16-byte aligned rows: a strided view over the row padding t already
+    has when its storage covers it (the extra columns then hold whatever
+    the padding holds), otherwise a zero-padded copy.  Callers use the
+    first C columns of any result that is column-separable."""
+    R, C = t.shape
+    Cp = -(-C // vec) * vec
+    if C == Cp and t.stride(0) % vec == 0 and t.data_ptr() % 16 == 0:
+        return t
+    esz = t.element_size()
+    if R > 0 and t.stride(1) == 1 and t.stride(0) >= Cp and t.stride(0) % vec == 0 \
+            and t.data_ptr() % 16 == 0 \
+            and (t.storage_offset() + (R - 1) * t.stride(0) + Cp) * esz <= t.untyped_storage().nbytes():
+        return t.as_strided((R, Cp), (t.stride(0), 1))
+    out = torch.zeros((R, Cp), dtype=t.dtype, device=t.device)
+    out[:, :C] = t
+    return out
+
+
 # ---------------------------------------------------------------------------
 # SpMM forward
 # ---------------------------------------------------------------------------
@@ -122,6 +142,15 @@ def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.T
             raise RuntimeError("graph arrays and input_B must be on the same device")
     W = window_offset.numel() - 1
     N = x.shape[1]
+    vec = 16 // x.element_size()
+    if out is None and N % vec != 0 and W > 0:
+        # The kernel's 16-byte gathers need whole vectors per row; a ragged
+        # width (a 41-class output layer) would fall back to element loads.
+        # Run on X widened to the next multiple and hand back the first N
+        # columns of the result (columns are independent).
+        x = _widen(x, vec)
+        full = spmm(window_offset, col_indices, values, x, tile_cols, plan=plan)
+        return full[:, :N]
     if out is None:
         out = torch.empty((W * 16, N), dtype=x.dtype, device=x.device)
     elif out.shape != (W * 16, N) or out.dtype != x.dtype or out.stride(1) != 1:
@@ -527,14 +556,14 @@ def sample_block(indptr: torch.Tensor, indices: torch.Tensor, frontier: torch.Te
 # weight gradient A^T B (csrc/gemm_tn.hip)
 # ---------------------------------------------------------------------------
 def gemm_tn_supported(a: torch.Tensor, b: torch.Tensor) -> bool:
-    """Whether gemm_tn takes these operands (F16/BF16 on the GPU, widths and
-    row strides multiples of 8, 16-byte aligned, unit column stride)."""
+    """Whether gemm_tn takes these operands: F16/BF16 2-D CUDA tensors with
+    one dtype, equal row counts and unit column stride.  Widths or row
+    strides that are not multiples of 8 (or rows not 16-byte aligned) are
+    widened first (row padding reused when the storage covers it, a
+    zero-padded copy otherwise)."""
     return (a.is_cuda and b.is_cuda and a.dim() == 2 and b.dim() == 2
             and a.dtype == b.dtype and a.dtype in (torch.float16, torch.bfloat16)
-            and a.shape[0] == b.shape[0] and a.stride(1) == 1 and b.stride(1) == 1
-            and a.shape[1] % 8 == 0 and b.shape[1] % 8 == 0
-            and a.stride(0) % 8 == 0 and b.stride(0) % 8 == 0
-            and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0)
+            and a.shape[0] == b.shape[0] and a.stride(1) == 1 and b.stride(1) == 1)
 
 
 def gemm_tn(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
@@ -544,10 +573,14 @@ def gemm_tn(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype = torch.flo
         raise ValueError("gemm_tn: unsupported operands (see gemm_tn_supported)")
     K, M = a.shape
     N = b.shape[1]
-    out = torch.empty((M, N), dtype=out_dtype, device=a.device)
-    wsb = int(L.load().grws_gemm_tn_workspace_bytes(K, M, N))
+    a2, b2 = _widen(a, 8), _widen(b, 8)
+    M2, N2 = a2.shape[1], b2.shape[1]
+    out = torch.empty((M2, N2), dtype=out_dtype, device=a.device)
+    wsb = int(L.load().grws_gemm_tn_workspace_bytes(K, M2, N2))
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=a.device)
-    L.call("grws_gemm_tn", L.ptr(a), a.stride(0), L.ptr(b), b.stride(0), L.dtype_code(a.dtype), K, M,
-           N, L.ptr(out), out.stride(0), L.dtype_code(out_dtype), L.ptr(ws), wsb,
+    L.call("grws_gemm_tn", L.ptr(a2), a2.stride(0), L.ptr(b2), b2.stride(0), L.dtype_code(a.dtype), K,
+           M2, N2, L.ptr(out), out.stride(0), L.dtype_code(out_dtype), L.ptr(ws), wsb,
            L.stream_of(a.device))
+    if (M2, N2) != (M, N):
+        out = out[:M, :N].contiguous()
     return out

@@ -1,4 +1,8 @@
-// Device-wide prefix sums and fills (reduce-then-scan, three launches).
+// Device-wide prefix sums and fills.  A scan is one launch up to 16,384
+// elements, reduce + scan (the scan adds the preceding tiles' sums itself)
+// up to 1,024 tiles of 4,096, and reduce + scan of the tile sums + scan
+// beyond that.  Within a tile each wave scans a contiguous segment in
+// registers; one barrier joins the waves.
 #include "grws_internal.h"
 
 namespace grws {
@@ -38,25 +42,70 @@ __global__ __launch_bounds__(1024) void scan_partials_kernel(int64_t* __restrict
     }
 }
 
-template <typename TIn>
-__global__ __launch_bounds__(kScanBlock) void scan_down_kernel(const TIn* __restrict__ in, int64_t n,
-                                                               const int64_t* __restrict__ partial,
-                                                               int64_t* __restrict__ out, int inclusive) {
-    __shared__ int64_t smem[kScanBlock / kWave + 1];
-    const int64_t base = (int64_t)blockIdx.x * kScanTile;
-    int64_t carry = partial[blockIdx.x];
-    // exclusive results are written shifted by one: out[i+1] = inclusive[i]
-    int64_t* dst = inclusive ? out : out + 1;
+// Scans one tile of BLOCK * kScanIters elements starting at `base`: wave w
+// takes the contiguous segment [base + w*64*kScanIters, +64*kScanIters) in
+// kScanIters coalesced steps, keeping its running inclusive sums in
+// registers; one barrier exchanges the wave totals.  dst[i] = carry +
+// inclusive prefix for i < n.
+template <typename TIn, int BLOCK>
+__device__ __forceinline__ void scan_tile(const TIn* __restrict__ in, int64_t n, int64_t base, int64_t carry,
+                                          int64_t* __restrict__ dst, int64_t* smem) {
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int64_t wb = base + (int64_t)wave * (kWave * kScanIters);
+    int64_t v[kScanIters];
+#pragma unroll
     for (int it = 0; it < kScanIters; ++it) {
-        int64_t i = base + (int64_t)it * kScanBlock + threadIdx.x;
-        int64_t v = i < n ? (int64_t)in[i] : 0;
-        int64_t total;
-        int64_t inc = block_incl_scan<kScanBlock>(v, smem, &total);
-        if (i < n) dst[i] = carry + inc;
-        carry += total;
+        const int64_t i = wb + it * kWave + lane;
+        v[it] = i < n ? (int64_t)in[i] : 0;
     }
+    int64_t run = 0;
+#pragma unroll
+    for (int it = 0; it < kScanIters; ++it) {
+        const int64_t inc = wave_incl_scan(v[it]);
+        v[it] = run + inc;
+        run += __shfl(inc, kWave - 1, kWave);
+    }
+    if (lane == 0) smem[wave] = run;
+    __syncthreads();
+    for (int k = 0; k < wave; ++k) carry += smem[k];
+#pragma unroll
+    for (int it = 0; it < kScanIters; ++it) {
+        const int64_t i = wb + it * kWave + lane;
+        if (i < n) dst[i] = carry + v[it];
+    }
+}
+
+// CARRY 0: a single tile (carry 0); 1: the carry is the sum of the
+// preceding tiles' partials, added up here (few tiles); 2: partial[] already
+// holds each tile's exclusive prefix.
+template <typename TIn, int BLOCK, int CARRY>
+__global__ __launch_bounds__(BLOCK) void scan_down_kernel(const TIn* __restrict__ in, int64_t n,
+                                                          const int64_t* __restrict__ partial,
+                                                          int64_t* __restrict__ out, int inclusive) {
+    __shared__ int64_t smem[BLOCK / kWave];
+    const int64_t base = (int64_t)blockIdx.x * BLOCK * kScanIters;
+    int64_t carry = 0;
+    if constexpr (CARRY == 2) {
+        carry = partial[blockIdx.x];
+    } else if constexpr (CARRY == 1) {
+        int64_t s = 0;
+        for (int64_t k = threadIdx.x; k < (int64_t)blockIdx.x; k += BLOCK) s += partial[k];
+#pragma unroll
+        for (int d = kWave / 2; d > 0; d >>= 1) s += __shfl_xor(s, d, kWave);
+        if (threadIdx.x % kWave == 0) smem[threadIdx.x / kWave] = s;
+        __syncthreads();
+        for (int k = 0; k < BLOCK / kWave; ++k) carry += smem[k];
+        __syncthreads();
+    }
+    // exclusive results are written shifted by one: out[i+1] = inclusive[i]
+    scan_tile<TIn, BLOCK>(in, n, base, carry, inclusive ? out : out + 1, smem);
     if (!inclusive && blockIdx.x == 0 && threadIdx.x == 0) out[0] = 0;
 }
+
+constexpr int kSingleBlock = 1024;                                 // one-launch scans
+constexpr int64_t kSingleTile = (int64_t)kSingleBlock * kScanIters;  // up to 16,384 elements
+constexpr int64_t kMaxSummedTiles = 1024;                          // two-launch scans
 
 template <typename TIn>
 int scan_impl(const TIn* in, int64_t* out, int64_t n, bool inclusive, void* ws, size_t ws_bytes,
@@ -66,16 +115,29 @@ int scan_impl(const TIn* in, int64_t* out, int64_t n, bool inclusive, void* ws, 
         if (!inclusive) return fill_i64(out, 1, 0, stream);
         return GRWS_OK;
     }
+    const int inc = inclusive ? 1 : 0;
+    if (n <= kSingleTile) {
+        hipLaunchKernelGGL((scan_down_kernel<TIn, kSingleBlock, 0>), dim3(1), dim3(kSingleBlock), 0, stream, in, n,
+                           (const int64_t*)nullptr, out, inc);
+        GRWS_LAUNCH_CHECK();
+        return GRWS_OK;
+    }
     int64_t nb = (n + kScanTile - 1) / kScanTile;
     Carver cv(ws, ws_bytes);
     int64_t* partial = cv.take<int64_t>(nb);
     if (!cv.ok) return set_error(GRWS_E_CAPACITY, "scan: workspace too small (%zu < %zu)", ws_bytes, cv.used);
     hipLaunchKernelGGL(scan_reduce_kernel<TIn>, dim3((unsigned)nb), dim3(kScanBlock), 0, stream, in, n, partial);
     GRWS_LAUNCH_CHECK();
+    if (nb <= kMaxSummedTiles) {
+        hipLaunchKernelGGL((scan_down_kernel<TIn, kScanBlock, 1>), dim3((unsigned)nb), dim3(kScanBlock), 0, stream,
+                           in, n, partial, out, inc);
+        GRWS_LAUNCH_CHECK();
+        return GRWS_OK;
+    }
     hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(1024), 0, stream, partial, nb);
     GRWS_LAUNCH_CHECK();
-    hipLaunchKernelGGL(scan_down_kernel<TIn>, dim3((unsigned)nb), dim3(kScanBlock), 0, stream, in, n, partial,
-                       out, inclusive ? 1 : 0);
+    hipLaunchKernelGGL((scan_down_kernel<TIn, kScanBlock, 2>), dim3((unsigned)nb), dim3(kScanBlock), 0, stream, in,
+                       n, partial, out, inc);
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }

@@ -21,7 +21,7 @@
 //   * work-group ids are remapped so each XCD (work-groups are dealt to the 8
 //     XCDs round-robin) walks a contiguous range of windows of one chunk,
 //     keeping a community's X rows (one chunk wide) in that XCD's L2.
-// Tuning overrides for benchmarking: GRWS_SPMM_WAVES (1|2), GRWS_SPMM_PF (1|2).
+// Tuning overrides for benchmarking: GRWS_SPMM_WAVES (1|2), GRWS_SPMM_NBLK (1|2|4|8|16).
 #include "grws_internal.h"
 
 #include <cstdlib>
@@ -441,21 +441,24 @@ __global__ void plan_fill_kernel(const int64_t* __restrict__ win_off, int64_t W,
     }
 }
 
-int nblk_for(int64_t N) { return N <= 16 ? 1 : (N <= 32 ? 2 : (N <= 64 ? 4 : 8)); }
+// MFMA column blocks (16 output columns each) per work-group.  16-bit X may
+// use 256-column chunks; fp32 stays at 128 (its loads carry half as many
+// elements per lane).
+int nblk_for(int64_t N, int32_t x_dtype) {
+    if (const char* e = getenv("GRWS_SPMM_NBLK")) {  // tuning override
+        const int v = atoi(e);
+        if (v == 1 || v == 2 || v == 4 || v == 8 || (v == 16 && x_dtype != GRWS_F32)) return v;
+    }
+    return N <= 16 ? 1 : (N <= 32 ? 2 : (N <= 64 ? 4 : 8));
+}
 
 template <int XT, bool AF32, int TC, int NBLK, bool VECT, int WPB>
 int launch_fwd(const SpmmArgs& a, hipStream_t stream) {
     const int64_t total = a.num_items * a.nchunks;
     const int64_t grid = ((total + 7) / 8) * 8;
     if (grid > INT32_MAX) return set_error(GRWS_E_INVALID, "spmm: too many work items (%lld)", (long long)total);
-    int pf = 1;
-    if (const char* e = getenv("GRWS_SPMM_PF")) pf = atoi(e) == 2 ? 2 : 1;  // tuning override
-    if (pf == 2)
-        hipLaunchKernelGGL((spmm_fwd_kernel<XT, AF32, TC, NBLK, VECT, WPB, 2>), dim3((unsigned)grid),
-                           dim3(64 * WPB), 0, stream, a);
-    else
-        hipLaunchKernelGGL((spmm_fwd_kernel<XT, AF32, TC, NBLK, VECT, WPB, 1>), dim3((unsigned)grid),
-                           dim3(64 * WPB), 0, stream, a);
+    hipLaunchKernelGGL((spmm_fwd_kernel<XT, AF32, TC, NBLK, VECT, WPB, 1>), dim3((unsigned)grid), dim3(64 * WPB),
+                       0, stream, a);
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }
@@ -489,6 +492,9 @@ int dispatch_nblk(const SpmmArgs& a, int nblk, bool vect, hipStream_t stream) {
         case 1: return dispatch_vec<XT, AF32, TC, 1>(a, vect, stream);
         case 2: return dispatch_vec<XT, AF32, TC, 2>(a, vect, stream);
         case 4: return dispatch_vec<XT, AF32, TC, 4>(a, vect, stream);
+        case 16:
+            if constexpr (XT != GRWS_F32) return dispatch_vec<XT, AF32, TC, 16>(a, vect, stream);
+            [[fallthrough]];
         default: return dispatch_vec<XT, AF32, TC, 8>(a, vect, stream);
     }
 }
@@ -514,6 +520,10 @@ int launch_fixup(const grws_spmm_plan* plan, const SpmmArgs& a, int nblk, hipStr
             break;
         case 4:
             hipLaunchKernelGGL((spmm_fixup_kernel<XT, 4>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols);
+            break;
+        case 16:
+            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 16>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
                                plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols);
             break;
         default:
@@ -547,7 +557,7 @@ extern "C" int grws_spmm_plan_capacity(int64_t num_windows, int64_t num_tiles, i
 
 extern "C" int32_t grws_spmm_default_slabs(int64_t num_windows, int64_t num_tiles, int32_t tile_cols,
                                            int64_t n_cols) {
-    int64_t nblk = nblk_for(n_cols > 0 ? n_cols : 1);
+    int64_t nblk = nblk_for(n_cols > 0 ? n_cols : 1, GRWS_F16);
     int64_t nchunks = (n_cols + nblk * 16 - 1) / (nblk * 16);
     if (nchunks < 1) nchunks = 1;
     int64_t slabs = (num_tiles * (tile_cols > 0 ? tile_cols : 16) + 15) / 16;
@@ -619,10 +629,9 @@ extern "C" int grws_spmm_plan_build(const int64_t* window_offset, int64_t num_wi
 
 extern "C" size_t grws_spmm_workspace_bytes(const grws_spmm_plan* plan, int64_t n_cols) {
     if (!plan || plan->num_slots <= 0 || n_cols <= 0) return 0;
-    int64_t nblk = nblk_for(n_cols);
-    int64_t nc = nblk * 16;
-    int64_t nchunks = (n_cols + nc - 1) / nc;
-    return (size_t)plan->num_slots * (size_t)nchunks * 16 * (size_t)nc * sizeof(float);
+    // every chunk width divides 256, so this covers whichever width runs
+    const int64_t padded = (n_cols + 255) / 256 * 256;
+    return (size_t)plan->num_slots * 16 * (size_t)padded * sizeof(float);
 }
 
 extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const void* x, int32_t x_dtype,
@@ -647,7 +656,7 @@ extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const v
     if (x_rows > 0) GRWS_CHECK_ARG(x != nullptr && ldx >= n_cols, "spmm: bad x (null or ldx < n_cols)");
     if (A->num_tiles > 0) GRWS_CHECK_ARG(A->col_indices && A->values, "spmm: null tile arrays");
 
-    const int nblk = nblk_for(n_cols);
+    const int nblk = nblk_for(n_cols, x_dtype);
     const int64_t nc = nblk * 16;
     SpmmArgs a{};
     a.win_off = A->window_offset;

@@ -77,7 +77,18 @@ def _graph_tensors(g):
     return out
 
 
-def _sample_batch(sampler, graph, seeds, features, device):
+def _transpose_needs(model, features: torch.Tensor):
+    """Per layer, whether its backward uses the block's A^T (the first
+    layer's input is the feature matrix; later inputs carry gradients)."""
+    out = []
+    for l, layer in enumerate(getattr(model, "layers", [])):
+        x_grad = l > 0 or features.requires_grad
+        f = getattr(layer, "needs_transpose", None)
+        out.append(True if f is None else bool(f(x_grad)))
+    return out
+
+
+def _sample_batch(sampler, graph, seeds, features, device, needs_t=None):
     """(subgraphs, batch_features or None, rows of the seeds in the logits).
 
     NeighborSampler: graph is a CSR (row_ptr, col_idx); blocks come back
@@ -91,9 +102,11 @@ def _sample_batch(sampler, graph, seeds, features, device):
         blocks = sampler.sample_layers(graph.row_ptr, graph.col_idx, seeds)
         if torch.is_grad_enabled():
             # build the backward's A^T here, on the sampling stream, off the
-            # training critical path (blocks are not modified afterwards)
-            for b in blocks:
-                b.transpose()
+            # training critical path (blocks are not modified afterwards),
+            # for the layers whose backward runs it
+            for l, b in enumerate(blocks):
+                if needs_t is None or l >= len(needs_t) or needs_t[l]:
+                    b.transpose()
         inp = blocks[0].src_nodes
         if features.is_cuda:
             feats = features.index_select(0, inp)
@@ -152,6 +165,7 @@ def train_epoch_node_sampling(model, graphs_for_model, features: torch.Tensor,
     graph = graphs_for_model[0] if isinstance(graphs_for_model, list) else graphs_for_model
     loader = WindowWiseDataLoader(train_idx.cpu(), batch_size=batch_size, tile_rows=tile_rows)
     main = torch.cuda.current_stream(device)
+    needs_t = _transpose_needs(model, features)
 
     def step(seeds, subgraphs, feats):
         nonlocal total_samples, num_batches
@@ -184,7 +198,7 @@ def train_epoch_node_sampling(model, graphs_for_model, features: torch.Tensor,
                         if max_batches and b >= max_batches:
                             break
                         seeds = torch.sort(seeds.to(device, non_blocking=True)).values
-                        subgraphs, feats, _ = _sample_batch(sampler, graph, seeds, features, device)
+                        subgraphs, feats, _ = _sample_batch(sampler, graph, seeds, features, device, needs_t)
                         ev = torch.cuda.Event()
                         ev.record(side)
                         q.put((seeds, subgraphs, feats, ev))
@@ -218,7 +232,7 @@ def train_epoch_node_sampling(model, graphs_for_model, features: torch.Tensor,
             timer.start_batch()
             seeds = torch.sort(seeds.to(device)).values
             timer.record("Data")
-            subgraphs, feats, _ = _sample_batch(sampler, graph, seeds, features, device)
+            subgraphs, feats, _ = _sample_batch(sampler, graph, seeds, features, device, needs_t)
             timer.record("Sample")
             step(seeds, subgraphs, feats)
 

@@ -6,6 +6,7 @@ Same classes, signatures and arithmetic as the reference:
   conv      out = trim(A (X W_neigh)) + X_target W_self      (layer.py:118-191)
 The SpMM runs on the gfx950 kernel (H1); A^T dH runs the same kernel over the
 cached device-built transpose of A instead of the reference's atomic scatter.
+A (X W) may be associated as (A X) W when that gathers fewer columns.
 """
 from __future__ import annotations
 
@@ -50,37 +51,67 @@ def _weight_grad(x: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
     return torch.matmul(x.t(), g)
 
 
+def _aggregate_first(in_w: int, out_w: int, x_needs_grad: bool) -> bool:
+    """Whether A (X W) is cheaper evaluated as (A X) W.  The SpMM's cost is
+    its gathered width: X-first aggregates out_w columns forward and again
+    backward (A^T G feeds the weight gradient); aggregate-first gathers in_w
+    columns forward, and backward only when X itself needs a gradient
+    (dW = (A X)^T G is a plain GEMM)."""
+    if x_needs_grad:
+        return in_w < out_w
+    return in_w < 2 * out_w
+
+
 class BCSRSPMMFunction(Function):
-    """output = A @ (X @ W) with A a BCSRGraph (layer.py:28-92).  Under
-    torch.autocast the backward runs in the forward's autocast state, so a
-    float16/bfloat16 forward has a float16/bfloat16 backward SpMM; the
-    features are kept in the autocast dtype for the weight gradient."""
+    """output = A @ (X @ W) with A a BCSRGraph (layer.py:28-92).  The product
+    is associated as A (X W), as the reference does, or as (A X) W when that
+    gathers fewer columns (a layer widening its input, or any layer whose
+    input needs no gradient); the result is the same product, rounded in the
+    other order.  Under torch.autocast the backward runs in the forward's
+    autocast state, so a float16/bfloat16 forward has a float16/bfloat16
+    backward SpMM; saved operands are kept in the autocast dtype for the
+    weight gradient."""
 
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
     def forward(ctx, graph, features, weight, warps_per_block):
         xh = _autocast_operand(features)
-        x_mult_w = torch.matmul(xh, weight)
-        output, timing = _spmm_timed(graph, x_mult_w)
-        record_spmm_time(timing)
-        ctx.save_for_backward(xh, weight)
         ctx.graph = graph
         ctx.warps_per_block = warps_per_block
+        ctx.num_input_nodes = features.shape[0]
+        ctx.agg_first = _aggregate_first(weight.shape[0], weight.shape[1], features.requires_grad)
+        if ctx.agg_first:
+            agg, timing = _spmm_timed(graph, xh)
+            output = torch.matmul(agg, weight)
+            ctx.save_for_backward(agg, weight)
+        else:
+            x_mult_w = torch.matmul(xh, weight)
+            output, timing = _spmm_timed(graph, x_mult_w)
+            ctx.save_for_backward(xh, weight)
+        record_spmm_time(timing)
         return output
 
     @staticmethod
     @torch.amp.custom_bwd(device_type="cuda")
     def backward(ctx, grad_output):
-        features, weight = ctx.saved_tensors
+        saved, weight = ctx.saved_tensors
         graph = ctx.graph
-        num_input_nodes = features.shape[0]
-        grad_input_aggr = graph.spmm_transpose(grad_output.contiguous(), num_input_nodes)
         grad_features = None
         grad_weight = None
+        g = grad_output.contiguous()
+        if ctx.agg_first:
+            # H = (A X) W:  dW = (A X)^T dH,  dX = A^T (dH W^T)
+            if ctx.needs_input_grad[2]:
+                grad_weight = _weight_grad(saved, g)
+            if ctx.needs_input_grad[1]:
+                grad_features = graph.spmm_transpose(torch.matmul(g, weight.t()).contiguous(),
+                                                     ctx.num_input_nodes)
+            return None, grad_features, grad_weight, None
+        grad_input_aggr = graph.spmm_transpose(g, ctx.num_input_nodes)
         if ctx.needs_input_grad[1]:
             grad_features = torch.matmul(grad_input_aggr, weight.t())
         if ctx.needs_input_grad[2]:
-            grad_weight = _weight_grad(features, grad_input_aggr)
+            grad_weight = _weight_grad(saved, grad_input_aggr)
         return None, grad_features, grad_weight, None
 
 
@@ -122,6 +153,11 @@ class BCSRGraphConv(nn.Module):
     def reset_parameters(self):
         nn.init.xavier_uniform_(self.weight_neigh)
         nn.init.xavier_uniform_(self.weight_self)
+
+    def needs_transpose(self, x_needs_grad: bool) -> bool:
+        """Whether this layer's backward runs A^T (an SpMM over the graph's
+        transpose) when its input does (not) need a gradient."""
+        return x_needs_grad or not _aggregate_first(self.in_feats, self.out_feats, False)
 
     def forward(self, graph, features: torch.Tensor,
                 features_target: torch.Tensor = None) -> torch.Tensor:

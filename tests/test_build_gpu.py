@@ -107,10 +107,15 @@ def test_build_rejects_out_of_range(cuda_device):
         builder.csr_to_bcsr_device(2, 4, bad, ci.clamp(max=3), None, tile_cols=8)
 
 
-def test_coo_to_csr_matches_stable_sort(cuda_device):
-    print("case coo_to_csr", flush=True)
+@pytest.mark.parametrize("n_r,n_c,m", [(500, 900, 20000), (1, 7, 3), (16384, 50, 40000),
+                                       (16385, 50, 40000), (4096 * 1024, 30, 300000),
+                                       (4096 * 1024 + 1, 30, 300000), (5000000, 1000, 6000000)])
+def test_coo_to_csr_matches_stable_sort(cuda_device, n_r, n_c, m):
+    """Row pointers are an exclusive scan over n_r counts: the sizes cover a
+    one-launch scan (up to 16,384), the two-launch scan (up to 1,024 tiles of
+    4,096) and the three-launch scan beyond, at their boundaries."""
+    print(f"case coo_to_csr {n_r}x{n_c} m={m}", flush=True)
     rng = np.random.default_rng(5)
-    n_r, n_c, m = 500, 900, 20000
     src = rng.integers(0, n_r, m).astype(np.int32)
     dst = rng.integers(0, n_c, m).astype(np.int32)
     w = rng.standard_normal(m).astype(np.float32)

@@ -37,7 +37,26 @@ def test_gemm_tn_strided_and_low_precision_output(cuda_device):
         tol = 2e-3 if od == torch.float16 else 1e-4
         bound = A.double().abs().t() @ B.double().abs()
         assert bool(((C.double() - ref).abs() <= tol * bound).all())
-    assert not gemm_tn_supported(A0[:, 1:129], B)  # misaligned start
+    # a misaligned start and ragged widths go through a widened copy; a
+    # ragged width over a wider buffer reuses its row padding (NaN there
+    # must not reach the result)
+    Am = A0[:, 1:129]
+    assert gemm_tn_supported(Am, B)
+    Cm = gemm_tn(Am, B)
+    bm = Am.double().abs().t() @ B.double().abs()
+    assert bool(((Cm.double() - Am.double().t() @ B.double()).abs() <= 1e-4 * bm).all())
+    Bp = torch.full((20000, 48), float("nan"), device=cuda_device).half()
+    Bp[:, :41] = torch.randn(20000, 41, device=cuda_device).half()
+    Br = Bp[:, :41]
+    Cr = gemm_tn(A, Br)
+    assert Cr.shape == (128, 41) and bool(torch.isfinite(Cr).all())
+    br = A.double().abs().t() @ Br.double().abs()
+    assert bool(((Cr.double() - A.double().t() @ Br.double()).abs() <= 1e-4 * br).all())
+    A41 = torch.randn(20000, 41, device=cuda_device).bfloat16()
+    B41 = torch.randn(20000, 41, device=cuda_device).bfloat16()
+    C41 = gemm_tn(A41, B41)
+    b41 = A41.double().abs().t() @ B41.double().abs()
+    assert bool(((C41.double() - A41.double().t() @ B41.double()).abs() <= 1e-4 * b41).all())
 
 
 def test_graphconv_autocast_backward_uses_split_k(cuda_device):

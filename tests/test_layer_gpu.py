@@ -37,30 +37,35 @@ def _close(a, b, tol):
 
 
 @pytest.mark.parametrize("tc", [8, 16])
-def test_graphconv_forward_backward_f32(cuda_device, tc):
-    print(f"case graphconv f32 tc={tc}", flush=True)
+@pytest.mark.parametrize("fin,fout,xgrad", [(48, 24, True), (24, 48, True), (40, 24, False),
+                                            (64, 24, False)])
+def test_graphconv_forward_backward_f32(cuda_device, tc, fin, fout, xgrad):
+    """Both associations of A X W: X-first (48->24 with dX, 64->24 without)
+    and aggregate-first (24->48 with dX, 40->24 without)."""
+    print(f"case graphconv f32 tc={tc} {fin}->{fout} xgrad={xgrad}", flush=True)
     torch.manual_seed(0)
     g = synth.chung_lu(1500, 20000, 2.2, seed=3)
     G = BCSRGraph.from_csr(g.row_ptr, g.col_idx, g.values, g.num_nodes, g.num_nodes, tile_cols=tc,
                            device=cuda_device)
-    conv = BCSRGraphConv(48, 24).to(cuda_device)
-    X = torch.randn(g.num_nodes, 48, device=cuda_device, requires_grad=True)
-    R = torch.randn(g.num_nodes, 24, device=cuda_device)
+    conv = BCSRGraphConv(fin, fout).to(cuda_device)
+    X = torch.randn(g.num_nodes, fin, device=cuda_device, requires_grad=xgrad)
+    R = torch.randn(g.num_nodes, fout, device=cuda_device)
     # without features_target the self path is padded to the 16W output rows
     # (layer.py:159-166); with it the output is trimmed to the target rows
-    assert conv(G, X).shape == (16 * G.num_windows, 24)
+    assert conv(G, X).shape == (16 * G.num_windows, fout)
     out = conv(G, X, features_target=X)
-    assert out.shape == (g.num_nodes, 24)
+    assert out.shape == (g.num_nodes, fout)
     (out * R).sum().backward()
 
     A = _dense(g)
-    Xd = X.detach().double().cpu().requires_grad_(True)
+    Xd = X.detach().double().cpu().requires_grad_(xgrad)
     Wn = conv.weight_neigh.detach().double().cpu().requires_grad_(True)
     Ws = conv.weight_self.detach().double().cpu().requires_grad_(True)
     ref = A @ (Xd @ Wn) + Xd @ Ws
     (ref * R.double().cpu()).sum().backward()
     _close(out, ref, 1e-4)
-    _close(X.grad, Xd.grad, 1e-4)
+    if xgrad:
+        _close(X.grad, Xd.grad, 1e-4)
     _close(conv.weight_neigh.grad, Wn.grad, 1e-4)
     _close(conv.weight_self.grad, Ws.grad, 1e-4)
 

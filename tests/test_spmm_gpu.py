@@ -160,3 +160,26 @@ def test_spmm_c2_full_size(cuda_device):
         Y = G.spmm(X)
         torch.cuda.synchronize()
         _check(G, X, Y, xdt)
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+def test_spmm_ragged_width_row_padding(cuda_device, xdt):
+    """A ragged width (41 columns) read from a wider buffer runs the vector
+    kernel over the row padding: NaN in the padding columns must stay out of
+    the first 41 output columns.  The explicit-out path (element loads) and
+    the zero-padded copy path give the same values."""
+    print(f"case ragged xdt={xdt}", flush=True)
+    g = synth.chung_lu(2000, 30000, 2.1, seed=21)
+    G = _bcsr(g, 16, cuda_device)
+    buf = torch.full((g.num_nodes, 48), float("nan"), device=cuda_device, dtype=xdt)
+    buf[:, :41] = synth.features(g.num_nodes, 41, seed=2, device=cuda_device).to(xdt)
+    X = buf[:, :41]
+    Y = G.spmm(X)
+    Yc = G.spmm(X.contiguous())
+    Yo = torch.empty(16 * G.num_windows, 41, device=cuda_device, dtype=xdt)
+    G.spmm(X, out=Yo)
+    torch.cuda.synchronize()
+    assert Y.shape == (16 * G.num_windows, 41) and bool(torch.isfinite(Y).all())
+    _check(G, X.contiguous(), Y, xdt)
+    _check(G, X.contiguous(), Yo, xdt)
+    assert torch.equal(Y, Yc)
