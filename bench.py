@@ -28,10 +28,10 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16
 # HBM bytes per SpMM launch measured with rocprofv3 --pmc (FETCH_SIZE x2.0 and
 # WRITE_SIZE x1.0, both scaled by a 1 GiB device copy); bench.py cannot read
 # counters itself, so the figure of the profiled workload is recorded here and
-# reported only for that exact workload.  Source: profiles/spmm_fwd_c3_n608_f16.md
+# reported only for that exact workload.  Source: profiles/spmm_buf_c3_n608_f16.md
 MEASURED_TRAFFIC = {
     # (config, N, x dtype, tile cols): (bytes per launch, profile file)
-    ("c3", 608, "f16", 16): (44.26e9, "profiles/spmm_fwd_c3_n608_f16.md"),
+    ("c3", 608, "f16", 16): (44.995e9, "profiles/spmm_buf_c3_n608_f16.md"),
 }
 
 
@@ -519,13 +519,16 @@ def main():
         "alg_bytes": B,
         "roofline": {
             "bound": "hbm",
-            "kernel": "spmm_fwd_kernel",
+            # 16-bit X runs the buffer-load kernel, fp32 X the element-masked one
+            "kernel": "spmm_buf_kernel" if dname in ("f16", "bf16") else "spmm_fwd_kernel",
             "achieved": round(kernel_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
             "traffic": MEASURED_TRAFFIC.get((cfg, N, dname, G.tile_cols), (None, None))[0],
             "traffic_source": MEASURED_TRAFFIC.get((cfg, N, dname, G.tile_cols), (None, None))[1],
+            "traffic_gbs": (round(MEASURED_TRAFFIC[(cfg, N, dname, G.tile_cols)][0] / (ms_avg / 1e3) / 1e9, 1)
+                            if (cfg, N, dname, G.tile_cols) in MEASURED_TRAFFIC else None),
             "kernel_ms_avg": round(ms_avg, 4),
             "mfma_issued_tflops": round(issued / (ms_avg / 1e3) / 1e12, 2),
             "mfma_frac": round(issued / (ms_avg / 1e3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),

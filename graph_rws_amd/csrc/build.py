@@ -4,8 +4,10 @@
 
 Every translation unit is compiled with
   --offload-arch=gfx950 -O3 -fPIC -std=c++17
-  -Xclang -target-feature -Xclang -packed-fp32-ops
-(the last pair keeps the compiler from emitting packed fp32 VALU ops), then
+  -Xclang -target-feature -Xclang -packed-fp32-ops -mllvm -amdgpu-mfma-vgpr-form
+(the feature pair keeps the compiler from emitting packed fp32 VALU ops; the
+last option keeps MFMA accumulators in ordinary VGPRs, which avoids copies
+between accumulator registers in the pipelined loops), then
 linked into one shared library that exports the C ABI of include/grws.h.
 """
 from __future__ import annotations
@@ -48,6 +50,7 @@ def _flags():
     return [f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall",
             "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-result",
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            "-mllvm", "-amdgpu-mfma-vgpr-form",
             f"-I{os.path.join(ROOT, 'include')}"]
 
 

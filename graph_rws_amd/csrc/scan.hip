@@ -1,8 +1,8 @@
 // Device-wide prefix sums and fills.  A scan is one launch up to 16,384
 // elements, reduce + scan (the scan adds the preceding tiles' sums itself)
 // up to 1,024 tiles of 4,096, and reduce + scan of the tile sums + scan
-// beyond that.  Within a tile each wave scans a contiguous segment in
-// registers; one barrier joins the waves.
+// beyond that.  Within a tile each thread scans 16 consecutive elements in
+// registers; one wave scan and one barrier join the threads.
 #include "grws_internal.h"
 
 namespace grws {
@@ -42,37 +42,43 @@ __global__ __launch_bounds__(1024) void scan_partials_kernel(int64_t* __restrict
     }
 }
 
-// Scans one tile of BLOCK * kScanIters elements starting at `base`: wave w
-// takes the contiguous segment [base + w*64*kScanIters, +64*kScanIters) in
-// kScanIters coalesced steps, keeping its running inclusive sums in
-// registers; one barrier exchanges the wave totals.  dst[i] = carry +
-// inclusive prefix for i < n.
+// Scans one tile of BLOCK * kScanIters elements starting at `base`: thread
+// t owns the kScanIters consecutive elements at base + t * kScanIters and
+// scans them serially in registers; one wave scan of the thread totals and
+// one barrier for the wave totals give each thread its prefix.  dst[i] =
+// carry + inclusive prefix for i < n.
 template <typename TIn, int BLOCK>
 __device__ __forceinline__ void scan_tile(const TIn* __restrict__ in, int64_t n, int64_t base, int64_t carry,
                                           int64_t* __restrict__ dst, int64_t* smem) {
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
-    const int64_t wb = base + (int64_t)wave * (kWave * kScanIters);
+    const int64_t t0 = base + (int64_t)threadIdx.x * kScanIters;
     int64_t v[kScanIters];
+    if (t0 + kScanIters <= n) {
 #pragma unroll
-    for (int it = 0; it < kScanIters; ++it) {
-        const int64_t i = wb + it * kWave + lane;
-        v[it] = i < n ? (int64_t)in[i] : 0;
+        for (int j = 0; j < kScanIters; ++j) v[j] = (int64_t)in[t0 + j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < kScanIters; ++j) v[j] = t0 + j < n ? (int64_t)in[t0 + j] : 0;
     }
     int64_t run = 0;
 #pragma unroll
-    for (int it = 0; it < kScanIters; ++it) {
-        const int64_t inc = wave_incl_scan(v[it]);
-        v[it] = run + inc;
-        run += __shfl(inc, kWave - 1, kWave);
+    for (int j = 0; j < kScanIters; ++j) {
+        run += v[j];
+        v[j] = run;
     }
-    if (lane == 0) smem[wave] = run;
+    const int64_t inc = wave_incl_scan(run);
+    if (lane == kWave - 1) smem[wave] = inc;
     __syncthreads();
+    carry += inc - run;
     for (int k = 0; k < wave; ++k) carry += smem[k];
+    if (t0 + kScanIters <= n) {
 #pragma unroll
-    for (int it = 0; it < kScanIters; ++it) {
-        const int64_t i = wb + it * kWave + lane;
-        if (i < n) dst[i] = carry + v[it];
+        for (int j = 0; j < kScanIters; ++j) dst[t0 + j] = carry + v[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < kScanIters; ++j)
+            if (t0 + j < n) dst[t0 + j] = carry + v[j];
     }
 }
 

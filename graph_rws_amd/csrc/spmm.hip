@@ -34,6 +34,14 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+typedef int32_t i32x8_t __attribute__((ext_vector_type(8)));
+typedef int32_t i32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 tr_v4f16_t;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 tr_v4bf16_t;
+typedef __attribute__((address_space(3))) tr_v4f16_t lds_v4f16_t;
+typedef __attribute__((address_space(3))) tr_v4bf16_t lds_v4bf16_t;
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 template <int XT>
 struct XTraits;
@@ -89,6 +97,7 @@ struct SpmmArgs {
     int64_t ldy;
     float* partials;
     int32_t nchunks;
+    uint32_t x_bytes;  // buffer path: readable bytes of x (last row: n_cols elements)
 };
 
 // Output conversion for the three element types.
@@ -100,6 +109,67 @@ __device__ __forceinline__ void store_out(void* y, int64_t idx, float v) {
         static_cast<_Float16*>(y)[idx] = (_Float16)v;
     } else {
         static_cast<uint16_t*>(y)[idx] = f32_to_bf16_bits(v);
+    }
+}
+
+// Writes a work-group's 16 x NC result: to Y (converted), or as an fp32
+// partial for a split window.  With WPB > 1 the waves' accumulators are
+// first added in LDS in wave order (deterministic); `stage_all` must hold
+// 16 * NC floats.
+template <int XT, int NBLK, int WPB, typename S>
+__device__ __forceinline__ void spmm_epilogue(const SpmmArgs& a, const float4_t* acc, S* stage_all, int wave,
+                                              int lane, int64_t w, int slot, int chunk, int64_t n0) {
+    constexpr int NC = NBLK * 16;
+    const int ag = lane >> 4;
+    const int bn = lane & 15;
+    const int64_t N = a.n_cols;
+    // D layout of the 16x16 MFMA family: lane l, element i -> row 4*(l/16)+i, col l%16
+    if constexpr (WPB > 1) {
+        float* red = reinterpret_cast<float*>(stage_all);
+        __syncthreads();
+#pragma unroll 1
+        for (int k = 0; k < WPB; ++k) {
+            if (wave == k) {
+#pragma unroll
+                for (int b = 0; b < NBLK; ++b) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int e = (4 * ag + i) * NC + b * 16 + bn;
+                        red[e] = k == 0 ? acc[b][i] : red[e] + acc[b][i];
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        if (slot < 0) {
+            const int64_t row0 = w * 16;
+            for (int e = threadIdx.x; e < 16 * NC; e += 64 * WPB) {
+                const int r = e / NC, c = e % NC;
+                if (n0 + c < N) store_out<XT>(a.y, (row0 + r) * a.ldy + n0 + c, red[e]);
+            }
+        } else {
+            float* P = a.partials + ((int64_t)slot * a.nchunks + chunk) * (16 * NC);
+            for (int e = threadIdx.x; e < 16 * NC; e += 64 * WPB) P[e] = red[e];
+        }
+        return;
+    }
+    if (slot < 0) {
+        const int64_t row0 = w * 16;
+#pragma unroll
+        for (int b = 0; b < NBLK; ++b) {
+            const int64_t col = n0 + b * 16 + bn;
+            if (col < N) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) store_out<XT>(a.y, (row0 + 4 * ag + i) * a.ldy + col, acc[b][i]);
+            }
+        }
+    } else {
+        float* P = a.partials + ((int64_t)slot * a.nchunks + chunk) * (16 * NC);
+#pragma unroll
+        for (int b = 0; b < NBLK; ++b) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) P[(4 * ag + i) * NC + b * 16 + bn] = acc[b][i];
+        }
     }
 }
 
@@ -323,55 +393,225 @@ __global__ __launch_bounds__(64 * WPB) void spmm_fwd_kernel(SpmmArgs a) {
         }
     }
 
-    // D layout of the 16x16 MFMA family: lane l, element i -> row 4*(l/16)+i, col l%16
-    if constexpr (WPB > 1) {
-        // fixed-order sum of the waves' partials in LDS (deterministic)
-        float* red = reinterpret_cast<float*>(stage_all);
-        __syncthreads();
-#pragma unroll 1
-        for (int k = 0; k < WPB; ++k) {
-            if (wave == k) {
-#pragma unroll
-                for (int b = 0; b < NBLK; ++b) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int e = (4 * ag + i) * NC + b * 16 + bn;
-                        red[e] = k == 0 ? acc[b][i] : red[e] + acc[b][i];
-                    }
-                }
-            }
-            __syncthreads();
+    spmm_epilogue<XT, NBLK, WPB>(a, acc, stage_all, wave, lane, w, slot, chunk, n0);
+}
+
+// Buffer-load variant for 16-bit X (the common case).  Same work mapping,
+// ring pipeline and arithmetic as spmm_fwd_kernel, with the per-slab
+// instruction count cut down:
+//   * X, A and the column indices are read with raw buffer loads whose
+//     range check returns zero past the end of the resource: an invalid
+//     column is redirected to row x_rows (out of range), A and the column
+//     indices use one resource per work item, so no load needs a mask or a
+//     select when consumed and row offsets are 32-bit (24 x 24 multiply);
+//   * lane l gathers NLD consecutive rows of the slab, so its column
+//     indices come from one vector load instead of cross-lane shuffles;
+//   * the B operand of each MFMA is one ds_read_b64_tr_b16 (gfx950's LDS
+//     transpose read): lane k of each 16-lane group reads 4 halves of stage
+//     row 4*(l/16) + k/4 at column 16*b + 4*(k%4), and the group's 64 halves
+//     come back transposed so lane i holds column i of rows 4g..4g+3.
+// Requires (checked on the host): x_rows < 2^24, row pitch < 2^24 bytes,
+// 2 * (x_rows + 1) rows of X addressable in 32 bits, and every work item's
+// A within 2^31 bytes.
+template <int XT, bool AF32, int TC, int NBLK, int WPB, int PF>
+__global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
+    static_assert(XT == GRWS_F16 || XT == GRWS_BF16, "16-bit X only");
+    static_assert(TC == 8 || TC == 16, "tile_cols must be 8 or 16");
+    static_assert(PF >= 1 && PF <= 2, "prefetch depth 1..2");
+    using S = typename XTraits<XT>::S;
+    constexpr int SZ = 2;
+    constexpr int SZA = AF32 ? 4 : 2;
+    constexpr int NC = NBLK * 16;               // output columns per work-group
+    constexpr int VEC = 8;                      // elements per 16-byte load
+    constexpr int LPR = NC / VEC;               // lanes per staged row
+    constexpr int NLD = (16 * LPR + 63) / 64;   // rows (loads) per lane per slab
+    constexpr int PITCH = NC + 16;              // LDS row pitch (elements)
+    constexpr int R = PF + 1;
+    static_assert(NLD == 1 || NLD == 2 || NLD == 4 || NLD == 8, "rows per lane");
+    static_assert(WPB == 1 || WPB * 16 * PITCH * SZ >= 16 * NC * 4, "stage too small to reduce in");
+    using ColV = typename std::conditional<
+        NLD == 8, i32x8_t,
+        typename std::conditional<NLD == 4, i32x4_t,
+                                  typename std::conditional<NLD == 2, i32x2_t, int32_t>::type>::type>::type;
+    using AVec = typename std::conditional<AF32, float4_t, u32x2_t>::type;
+
+    __shared__ __attribute__((aligned(16))) S stage_all[WPB * 16 * PITCH];
+
+    const int wave = WPB > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;
+    const int lane = threadIdx.x & 63;
+    S* stage = stage_all + wave * (16 * PITCH);
+    const int64_t total = a.num_items * a.nchunks;
+    const int64_t per_xcd = (total + 7) >> 3;
+    const int64_t logical = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (logical >= total) return;  // uniform over the work-group
+    const int64_t item = logical % a.num_items;
+    const int chunk = (int)(logical / a.num_items);
+
+    int64_t w, sb, se;
+    int slot;
+    if (a.items) {
+        const int32_t* it = a.items + 4 * item;
+        w = it[0];
+        sb = it[1];
+        se = it[2];
+        slot = it[3];
+    } else {
+        w = item;
+        sb = 0;
+        se = INT64_MAX;
+        slot = -1;
+    }
+    int64_t t1 = a.win_off[w + 1];
+    int64_t t0 = a.win_off[w];
+    t1 = t1 < 0 ? 0 : (t1 > a.num_tiles ? a.num_tiles : t1);
+    t0 = t0 < 0 ? 0 : (t0 > t1 ? t1 : t0);
+    const int64_t nslots = (t1 - t0) * TC;
+    const int64_t nslabs = (nslots + 15) >> 4;
+    if (se > nslabs) se = nslabs;
+    if (sb > se) sb = se;
+    const int64_t n0 = (int64_t)chunk * NC;
+
+    // one resource per work item for A and the column indices, starting at
+    // slab sb; reads beyond the window return zero
+    const int64_t a_bytes = nslots * 16 * SZA - sb * 256 * SZA;
+    const int64_t c_bytes = (nslots - sb * 16) * 4;
+    const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(static_cast<const char*>(a.vals) + (t0 * 16 * TC + sb * 256) * SZA), (short)0,
+        (int)(a_bytes > 0x7fffffff ? 0x7fffffff : (a_bytes < 0 ? 0 : a_bytes)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsC = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.cols + t0 * TC + sb * 16), (short)0, (int)(c_bytes < 0 ? 0 : c_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsX =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.x), (short)0, (int)a.x_bytes, 0x00020000);
+
+    const int rbase = NLD * (lane / LPR);  // first of the lane's slab rows
+    const bool lrow = rbase < 16;          // NBLK == 1: lanes 32..63 stage nothing
+    // a lane whose 8 columns lie past n_cols (the last chunk) reads nothing:
+    // its offset starts at (x_rows + 1) rows, past the resource whatever the row
+    const uint32_t colb = n0 + (lane % LPR) * VEC < a.n_cols ? (uint32_t)((n0 + (lane % LPR) * VEC) * SZ)
+                                                              : (uint32_t)((a.x_rows + 1) * a.ldx * SZ);
+    const uint32_t ldxb = (uint32_t)(a.ldx * SZ);
+    const uint32_t xr = (uint32_t)a.x_rows;
+    const int ag = lane >> 4;
+    const int ar = lane & 15;
+    // A fragment: row ar, slots 4ag..4ag+3 of the slab (values are [tile][row][col])
+    const uint32_t a_lane = (uint32_t)((((4 * ag) / TC) * 16 + ar) * TC + (4 * ag) % TC) * SZA;
+    // transpose-read address of this lane within a 16-column block
+    const int tr_off = (4 * ag + ((lane & 15) >> 2)) * PITCH + 4 * (lane & 3);
+
+    auto load_cols = [&](int64_t s) -> ColV {
+        const uint32_t off = (uint32_t)((s - sb) * 64) + (uint32_t)rbase * 4;
+        if constexpr (NLD == 8) {
+            const u32x4_t lo = __builtin_amdgcn_raw_buffer_load_b128(rsC, (int)off, 0, 2);
+            const u32x4_t hi = __builtin_amdgcn_raw_buffer_load_b128(rsC, (int)(off + 16), 0, 2);
+            return ColV{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        } else if constexpr (NLD == 4) {
+            return __builtin_bit_cast(ColV, __builtin_amdgcn_raw_buffer_load_b128(rsC, (int)off, 0, 2));
+        } else if constexpr (NLD == 2) {
+            return __builtin_bit_cast(ColV, __builtin_amdgcn_raw_buffer_load_b64(rsC, (int)off, 0, 2));
+        } else {
+            return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rsC, (int)off, 0, 2);
         }
-        if (slot < 0) {
-            const int64_t row0 = w * 16;
-            for (int e = threadIdx.x; e < 16 * NC; e += 64 * WPB) {
-                const int r = e / NC, c = e % NC;
-                if (n0 + c < N) store_out<XT>(a.y, (row0 + r) * a.ldy + n0 + c, red[e]);
+    };
+    auto load_x = [&](const ColV cv, int64_t s, u32x4_t* regs) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            int32_t c;
+            if constexpr (NLD == 1) c = cv; else c = cv[i];
+            bool ok = lrow && (uint32_t)c < xr;
+            if constexpr (TC == 8) ok = ok && (s * 16 + rbase + i < nslots);  // half-empty last slab
+            const uint32_t row = ok ? (uint32_t)c : xr;  // row x_rows lies past the resource
+            regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rsX, (int)(__umul24(row, ldxb) + colb), 0, 0);
+        }
+    };
+    auto load_a = [&](int64_t s) -> AVec {
+        const uint32_t off = (uint32_t)((s - sb) * 256 * SZA) + a_lane;
+        if constexpr (AF32) {
+            return __builtin_bit_cast(AVec, __builtin_amdgcn_raw_buffer_load_b128(rsA, (int)off, 0, 2));
+        } else {
+            return __builtin_bit_cast(AVec, __builtin_amdgcn_raw_buffer_load_b64(rsA, (int)off, 0, 2));
+        }
+    };
+
+    float4_t acc[NBLK];
+#pragma unroll
+    for (int b = 0; b < NBLK; ++b) acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto consume = [&](const u32x4_t* xb, const AVec a_cur) {
+        if (lrow) {
+#pragma unroll
+            for (int i = 0; i < NLD; ++i)
+                *reinterpret_cast<u32x4_t*>(&stage[(rbase + i) * PITCH + (lane % LPR) * VEC]) = xb[i];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        short4_t af;
+        if constexpr (AF32) {
+            if constexpr (XT == GRWS_F16) {
+                af = __builtin_bit_cast(short4_t, half4_t{(_Float16)a_cur[0], (_Float16)a_cur[1], (_Float16)a_cur[2],
+                                                          (_Float16)a_cur[3]});
+            } else {
+                af = short4_t{(short)f32_to_bf16_bits(a_cur[0]), (short)f32_to_bf16_bits(a_cur[1]),
+                              (short)f32_to_bf16_bits(a_cur[2]), (short)f32_to_bf16_bits(a_cur[3])};
             }
         } else {
-            float* P = a.partials + ((int64_t)slot * a.nchunks + chunk) * (16 * NC);
-            for (int e = threadIdx.x; e < 16 * NC; e += 64 * WPB) P[e] = red[e];
+            af = __builtin_bit_cast(short4_t, a_cur);
         }
-        return;
-    }
-    if (slot < 0) {
-        const int64_t row0 = w * 16;
 #pragma unroll
         for (int b = 0; b < NBLK; ++b) {
-            const int64_t col = n0 + b * 16 + bn;
-            if (col < N) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) store_out<XT>(a.y, (row0 + 4 * ag + i) * a.ldy + col, acc[b][i]);
+            lds_ptr_t p = (lds_ptr_t)(stage + tr_off + 16 * b);
+            if constexpr (XT == GRWS_F16) {
+                const half4_t bf = __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                                                   (lds_v4f16_t*)p));
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, af), bf, acc[b], 0, 0, 0);
+            } else {
+                const short4_t bf = __builtin_bit_cast(short4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                                                                     (lds_v4bf16_t*)p));
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(af, bf, acc[b], 0, 0, 0);
             }
         }
-    } else {
-        float* P = a.partials + ((int64_t)slot * a.nchunks + chunk) * (16 * NC);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+
+    const int64_t s0 = sb + wave;
+    if (s0 < se && xr > 0) {  // uniform per wave
+        u32x4_t buf[R][NLD];
+        AVec abuf[R];
+        ColV cring[R];
 #pragma unroll
-        for (int b = 0; b < NBLK; ++b) {
+        for (int k = 0; k < R; ++k) cring[k] = load_cols(s0 + (int64_t)k * WPB);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) P[(4 * ag + i) * NC + b * 16 + bn] = acc[b][i];
+        for (int k = 0; k < PF; ++k) {
+            load_x(cring[k], s0 + (int64_t)k * WPB, buf[k]);
+            abuf[k] = load_a(s0 + (int64_t)k * WPB);
+        }
+        auto step = [&](const int u, const int64_t s) {
+            const int ps = (u + PF) % R;
+            cring[u] = load_cols(s + (int64_t)R * WPB);
+            load_x(cring[ps], s + (int64_t)PF * WPB, buf[ps]);
+            abuf[ps] = load_a(s + (int64_t)PF * WPB);
+            consume(buf[u], abuf[u]);
+        };
+        const int64_t nsteps = (se - s0 + WPB - 1) / WPB;
+        const int64_t nturns = nsteps / R;
+        int64_t s = s0;
+        for (int64_t t = 0; t < nturns; ++t) {
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                step(u, s);
+                s += WPB;
+            }
+        }
+        const int rest = (int)(nsteps - nturns * R);
+#pragma unroll
+        for (int u = 0; u < R - 1; ++u) {
+            if (u < rest) step(u, s);
+            s += WPB;
         }
     }
+    spmm_epilogue<XT, NBLK, WPB>(a, acc, stage_all, wave, lane, w, slot, chunk, n0);
 }
 
 // Sums the partial slots of each split window in slot order (deterministic).
@@ -441,14 +681,17 @@ __global__ void plan_fill_kernel(const int64_t* __restrict__ win_off, int64_t W,
     }
 }
 
-// MFMA column blocks (16 output columns each) per work-group.  16-bit X may
-// use 256-column chunks; fp32 stays at 128 (its loads carry half as many
+// MFMA column blocks (16 output columns each) per work-group: 128-column
+// chunks, or 256 on the buffer-load path when N is a multiple of 256 (A is
+// then streamed once per 256 columns; measured faster on community graphs,
+// equal on random ones).  fp32 X stays at 128 (its loads carry half as many
 // elements per lane).
-int nblk_for(int64_t N, int32_t x_dtype) {
+int nblk_for(int64_t N, int32_t x_dtype, bool buffer_path) {
     if (const char* e = getenv("GRWS_SPMM_NBLK")) {  // tuning override
         const int v = atoi(e);
         if (v == 1 || v == 2 || v == 4 || v == 8 || (v == 16 && x_dtype != GRWS_F32)) return v;
     }
+    if (buffer_path && x_dtype != GRWS_F32 && N >= 256 && N % 256 == 0) return 16;
     return N <= 16 ? 1 : (N <= 32 ? 2 : (N <= 64 ? 4 : 8));
 }
 
@@ -505,6 +748,51 @@ int dispatch_tc(const SpmmArgs& a, int tc, int nblk, bool vect, hipStream_t stre
                    : dispatch_nblk<XT, AF32, 16>(a, nblk, vect, stream);
 }
 
+template <int XT, bool AF32, int TC, int NBLK, int WPB>
+int launch_buf(const SpmmArgs& a, hipStream_t stream) {
+    const int64_t total = a.num_items * a.nchunks;
+    const int64_t grid = ((total + 7) / 8) * 8;
+    if (grid > INT32_MAX) return set_error(GRWS_E_INVALID, "spmm: too many work items (%lld)", (long long)total);
+    hipLaunchKernelGGL((spmm_buf_kernel<XT, AF32, TC, NBLK, WPB, 1>), dim3((unsigned)grid), dim3(64 * WPB), 0, stream,
+                       a);
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
+template <int XT, bool AF32, int TC>
+int dispatch_buf(const SpmmArgs& a, int nblk, hipStream_t stream) {
+    const bool two = waves_for(a, nblk) == 2;
+    switch (nblk) {
+        case 1: return two ? launch_buf<XT, AF32, TC, 1, 2>(a, stream) : launch_buf<XT, AF32, TC, 1, 1>(a, stream);
+        case 2: return two ? launch_buf<XT, AF32, TC, 2, 2>(a, stream) : launch_buf<XT, AF32, TC, 2, 1>(a, stream);
+        case 4: return two ? launch_buf<XT, AF32, TC, 4, 2>(a, stream) : launch_buf<XT, AF32, TC, 4, 1>(a, stream);
+        case 16: return two ? launch_buf<XT, AF32, TC, 16, 2>(a, stream) : launch_buf<XT, AF32, TC, 16, 1>(a, stream);
+        default: return two ? launch_buf<XT, AF32, TC, 8, 2>(a, stream) : launch_buf<XT, AF32, TC, 8, 1>(a, stream);
+    }
+}
+
+template <int XT, bool AF32>
+int dispatch_buf_tc(const SpmmArgs& a, int tc, int nblk, hipStream_t stream) {
+    return tc == 8 ? dispatch_buf<XT, AF32, 8>(a, nblk, stream) : dispatch_buf<XT, AF32, 16>(a, nblk, stream);
+}
+
+// Whether the buffer-load kernel's 32-bit offsets cover this call: rows and
+// row pitch below 2^24 (24-bit multiply), 2 (x_rows + 1) rows below 2^32 bytes,
+// and every work item's A below 2^31 bytes (an item spans at most the
+// plan's slabs_per_item slabs, or a whole window without a plan).
+bool buffer_path_fits(const grws_bcsr* A, const grws_spmm_plan* plan, int64_t x_rows, int64_t ldx, int64_t nc,
+                      size_t esz) {
+    if (const char* e = getenv("GRWS_SPMM_KERNEL"))  // tuning override: 1 = element-masked kernel
+        if (atoi(e) == 1) return false;
+    const int64_t ldxb = ldx * (int64_t)esz;
+    if (x_rows <= 0 || x_rows >= (1 << 24) || ldxb >= (1 << 24)) return false;
+    if (2 * (x_rows + 1) * ldxb + nc * (int64_t)esz >= ((int64_t)1 << 32)) return false;
+    const int64_t sza = A->values_dtype == GRWS_F32 ? 4 : 2;
+    const int64_t slabs = plan && plan->items ? (int64_t)plan->slabs_per_item
+                                              : (A->num_tiles * A->tile_cols + 15) / 16 + 1;
+    return (slabs + 4) * 256 * sza < ((int64_t)1 << 31);
+}
+
 template <int XT>
 int launch_fixup(const grws_spmm_plan* plan, const SpmmArgs& a, int nblk, hipStream_t stream) {
     int64_t grid = plan->num_split * a.nchunks;
@@ -557,7 +845,7 @@ extern "C" int grws_spmm_plan_capacity(int64_t num_windows, int64_t num_tiles, i
 
 extern "C" int32_t grws_spmm_default_slabs(int64_t num_windows, int64_t num_tiles, int32_t tile_cols,
                                            int64_t n_cols) {
-    int64_t nblk = nblk_for(n_cols > 0 ? n_cols : 1, GRWS_F16);
+    int64_t nblk = nblk_for(n_cols > 0 ? n_cols : 1, GRWS_F16, true);
     int64_t nchunks = (n_cols + nblk * 16 - 1) / (nblk * 16);
     if (nchunks < 1) nchunks = 1;
     int64_t slabs = (num_tiles * (tile_cols > 0 ? tile_cols : 16) + 15) / 16;
@@ -656,7 +944,11 @@ extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const v
     if (x_rows > 0) GRWS_CHECK_ARG(x != nullptr && ldx >= n_cols, "spmm: bad x (null or ldx < n_cols)");
     if (A->num_tiles > 0) GRWS_CHECK_ARG(A->col_indices && A->values, "spmm: null tile arrays");
 
-    const int nblk = nblk_for(n_cols, x_dtype);
+    const size_t esz = dtype_size(x_dtype);
+    const int64_t vec = (int64_t)(16 / esz);
+    const bool vect = (n_cols % vec == 0) && (ldx % vec == 0) && ((reinterpret_cast<uintptr_t>(x) % 16) == 0);
+    const bool use_buf = x_dtype != GRWS_F32 && vect && buffer_path_fits(A, plan, x_rows, ldx, 256, esz);
+    const int nblk = nblk_for(n_cols, x_dtype, use_buf);
     const int64_t nc = nblk * 16;
     SpmmArgs a{};
     a.win_off = A->window_offset;
@@ -686,13 +978,18 @@ extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const v
     }
     if (a.num_items == 0) return GRWS_OK;
 
-    const size_t esz = dtype_size(x_dtype);
-    const int64_t vec = (int64_t)(16 / esz);
-    const bool vect = (n_cols % vec == 0) && (ldx % vec == 0) && ((reinterpret_cast<uintptr_t>(x) % 16) == 0);
     const bool af32 = A->values_dtype == GRWS_F32;
     const int tc = A->tile_cols;
     int st;
-    switch (x_dtype) {
+    if (use_buf) {
+        a.x_bytes = (uint32_t)((x_rows - 1) * ldx * (int64_t)esz + n_cols * (int64_t)esz);
+        if (x_dtype == GRWS_F16)
+            st = af32 ? dispatch_buf_tc<GRWS_F16, true>(a, tc, nblk, stream)
+                      : dispatch_buf_tc<GRWS_F16, false>(a, tc, nblk, stream);
+        else
+            st = af32 ? dispatch_buf_tc<GRWS_BF16, true>(a, tc, nblk, stream)
+                      : dispatch_buf_tc<GRWS_BF16, false>(a, tc, nblk, stream);
+    } else switch (x_dtype) {
         case GRWS_F32: st = dispatch_tc<GRWS_F32, true>(a, tc, nblk, vect, stream); break;
         case GRWS_F16:
             st = af32 ? dispatch_tc<GRWS_F16, true>(a, tc, nblk, vect, stream)
