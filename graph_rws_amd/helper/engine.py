@@ -77,6 +77,23 @@ def _graph_tensors(g):
     return out
 
 
+_SAMPLING_STREAMS = {}
+
+
+def _sampling_stream(device) -> torch.cuda.Stream:
+    """The producer's stream, one per device for the life of the process
+    (default priority).  The caching allocator keeps freed blocks per
+    stream, so a new stream per epoch would allocate fresh device memory
+    every epoch; reusing one keeps the producer's pool warm."""
+    dev = torch.device(device)
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    s = _SAMPLING_STREAMS.get(key)
+    if s is None:
+        s = torch.cuda.Stream(torch.device("cuda", key))
+        _SAMPLING_STREAMS[key] = s
+    return s
+
+
 def _transpose_needs(model, features: torch.Tensor):
     """Per layer, whether its backward uses the block's A^T (the first
     layer's input is the feature matrix; later inputs carry gradients)."""
@@ -187,7 +204,7 @@ def train_epoch_node_sampling(model, graphs_for_model, features: torch.Tensor,
         timer.end_batch()
 
     if pipeline:
-        side = torch.cuda.Stream(device)
+        side = _sampling_stream(device)
         q: "queue.Queue" = queue.Queue(maxsize=1)
         failure = []
 
