@@ -117,6 +117,15 @@ _PROTOS = {
     "grws_gemm_tn": (ctypes.c_int, [_vp, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int32,
                                     ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _vp,
                                     ctypes.c_int64, ctypes.c_int32, _vp, ctypes.c_size_t, _vp]),
+    "grws_repack_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
+    "grws_repack_prepare": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.c_int64, _vp, ctypes.c_int64,
+                                           _vp, _vp, ctypes.POINTER(ctypes.c_int64), _vp,
+                                           ctypes.c_size_t, _vp]),
+    "grws_repack_externals": (ctypes.c_int, [_vp, ctypes.c_int64, _vp, _vp, ctypes.c_size_t, _vp]),
+    "grws_repack_finish": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.c_int64, _vp, ctypes.c_int64,
+                                          _vp, ctypes.c_int64, _vp, ctypes.c_int64, _vp, _vp, _vp, _vp,
+                                          _vp, _vp, _vp, ctypes.POINTER(ctypes.c_int32), _vp,
+                                          ctypes.c_size_t, _vp]),
     "grws_relabel_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
     "grws_relabel": (ctypes.c_int, [_vp, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int64,
                                     _vp, _vp, ctypes.c_int64, _vp, ctypes.c_size_t, _c_i64p,

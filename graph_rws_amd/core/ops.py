@@ -516,8 +516,12 @@ class SampleState:
         self.num_nodes = int(num_nodes)
         self.node_map = torch.empty(max(1, self.num_nodes), dtype=torch.int32, device=device)
         self.bitmap = torch.empty(max(1, (self.num_nodes + 31) // 32), dtype=torch.int32, device=device)
+        self.reset()
+
+    def reset(self) -> None:
+        """Back to all -1 / all 0 (on the current stream)."""
         L.call("grws_sample_state_init", L.ptr(self.node_map), L.ptr(self.bitmap), self.num_nodes,
-               L.stream_of(torch.device(device)))
+               L.stream_of(self.node_map.device))
 
 
 def sample_block(indptr: torch.Tensor, indices: torch.Tensor, frontier: torch.Tensor, fanout: int,
@@ -584,3 +588,83 @@ def gemm_tn(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype = torch.flo
     if (M2, N2) != (M, N):
         out = out[:M, :N].contiguous()
     return out
+
+
+# ---------------------------------------------------------------------------
+# halo-aware subgraph repack (sampler/sampler.py:420-690)
+# ---------------------------------------------------------------------------
+class RepackResult:
+    """Device outputs of one repack: the new window offsets, the input nodes
+    (internal first, then the kept externals ascending), the halo and inner
+    column / value arrays, the internal node count, and whether a halo value
+    is NaN."""
+
+    def __init__(self, window_offset, input_nodes, num_internal, halo_cols, halo_values, inner_cols,
+                 inner_values, any_nan):
+        self.window_offset = window_offset
+        self.input_nodes = input_nodes
+        self.num_internal = int(num_internal)
+        self.halo_cols = halo_cols
+        self.halo_values = halo_values
+        self.inner_cols = inner_cols
+        self.inner_values = inner_values
+        self.any_nan = bool(any_nan)
+
+
+def repack(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.Tensor, tile_cols: int,
+           num_nodes: int, window_ids: torch.Tensor, max_external_ratio: float, state: "SampleState",
+           generator: Optional[torch.Generator] = None) -> RepackResult:
+    """Repack of the selected windows on the device (csrc/repack.hip).
+
+    window_ids: int64, strictly ascending, in [0, num_windows).  The external
+    candidates are kept whole when they fit int(num_internal * ratio);
+    otherwise a random subset of that size is kept, drawn as the reference
+    draws it (one torch.randperm over the ascending candidates on the
+    device, then sorted).  `state` is the graph's SampleState; it is left as
+    found, also when a call fails."""
+    _check_graph(window_offset, col_indices, values, tile_cols)
+    dev = window_offset.device
+    for t in (col_indices, values, window_ids, state.node_map):
+        if t.device != dev:
+            raise RuntimeError("repack: graph, window ids and state must be on one device")
+    if state.num_nodes < int(num_nodes):
+        raise ValueError("repack: state is smaller than the graph")
+    ids = window_ids.to(torch.int64).contiguous()
+    n_sel = ids.numel()
+    W = window_offset.numel() - 1
+    view = L.BcsrView(L.ptr(window_offset), L.ptr(col_indices), L.ptr(values), W,
+                      col_indices.numel() // tile_cols, 16, tile_cols, L.dtype_code(values.dtype), 0)
+    lib = L.load()
+    wsb = int(lib.grws_repack_workspace_bytes(n_sel, int(num_nodes)))
+    ws = torch.empty(max(1, wsb), dtype=torch.uint8, device=dev)
+    new_off = torch.empty(n_sel + 1, dtype=torch.int64, device=dev)
+    counts = (ctypes.c_int64 * 3)()
+    stream = L.stream_of(dev)
+    L.call("grws_repack_prepare", ctypes.byref(view), int(num_nodes), L.ptr(ids), n_sel, L.ptr(state.bitmap),
+           L.ptr(new_off), ctypes.cast(counts, ctypes.POINTER(ctypes.c_int64)), L.ptr(ws), wsb, stream)
+    T, n_int, n_cand = (int(c) for c in counts)
+    try:
+        budget = int(n_int * max_external_ratio)
+        kept = None
+        n_kept = n_cand
+        if n_cand > budget:
+            ext = torch.empty(n_cand, dtype=torch.int64, device=dev)
+            L.call("grws_repack_externals", L.ptr(state.bitmap), int(num_nodes), L.ptr(ext), L.ptr(ws), wsb, stream)
+            perm = torch.randperm(n_cand, device=dev, generator=generator)
+            kept = torch.sort(ext[perm[:budget]]).values.contiguous()
+            n_kept = kept.numel()
+        input_nodes = torch.empty(max(1, n_int + n_kept), dtype=torch.int64, device=dev)
+        halo_cols = torch.empty(T * tile_cols, dtype=torch.int32, device=dev)
+        inner_cols = torch.empty_like(halo_cols)
+        halo_vals = torch.empty(T * 16 * tile_cols, dtype=values.dtype, device=dev)
+        inner_vals = torch.empty_like(halo_vals)
+        flags = (ctypes.c_int32 * 1)()
+        L.call("grws_repack_finish", ctypes.byref(view), int(num_nodes), L.ptr(ids), n_sel, L.ptr(new_off), n_int,
+               L.ptr(kept) if kept is not None else None, n_kept, L.ptr(state.node_map), L.ptr(state.bitmap),
+               L.ptr(input_nodes), L.ptr(halo_cols), L.ptr(halo_vals), L.ptr(inner_cols), L.ptr(inner_vals),
+               ctypes.cast(flags, ctypes.POINTER(ctypes.c_int32)), L.ptr(ws), wsb, stream)
+    except BaseException:
+        state.reset()
+        raise
+    return RepackResult(new_off, input_nodes[: n_int + n_kept], n_int, halo_cols, halo_vals, inner_cols,
+                        inner_vals, flags[0])

@@ -34,6 +34,7 @@ SOURCES = [
     "sample.hip",
     "window_sample.hip",
     "gemm_tn.hip",
+    "repack.hip",
 ]
 
 ARCH = os.environ.get("GRWS_OFFLOAD_ARCH", "gfx950")

@@ -8,6 +8,9 @@ with the LAST fanout (``reversed(fanouts)``, sampler.py:204).  Each layer
 has ``num_rows = 16 * len(active_windows)`` and ``num_cols = g.num_cols``,
 and carries ``active_windows`` / ``active_masks``, which the model's reindex
 uses (models/model.py:126-143).  Column ids are global.
+
+``repack_subgraph`` (sampler.py:420-690) repacks a window set into a halo
+graph on the device (csrc/repack.hip).
 """
 from __future__ import annotations
 
@@ -16,6 +19,7 @@ from typing import List
 import torch
 
 from ..core import sample_all_layers
+from ..core.ops import SampleState, repack
 from ..data import BCSRGraph
 
 
@@ -92,6 +96,92 @@ class BCSRSampler:
             sub.active_masks = msk
             layers.insert(0, sub)
         return layers
+
+    # ------------------------------------------------------------------
+    # halo-aware repack of a window set (sampler.py:420-690)
+    # ------------------------------------------------------------------
+    def _repack_state(self, num_nodes: int, device) -> SampleState:
+        st = getattr(self, "_repack_state_cache", None)
+        if st is None or st.num_nodes < num_nodes or st.node_map.device != torch.device(device):
+            st = SampleState(num_nodes, device)
+            self._repack_state_cache = st
+        return st
+
+    def repack_subgraph(self, g: BCSRGraph, window_ids: torch.Tensor, max_external_ratio: float = 5.0,
+                        dry_run: bool = False, generator: torch.Generator = None):
+        """The selected windows of ``g`` as a halo graph (sampler.py:420-690).
+
+        Rows: the windows' nodes (``num_internal_nodes``, window order).
+        Columns: those nodes first, then the external neighbours (halo) in
+        ascending id -- all of them, or, when there are more than
+        ``int(num_internal_nodes * max_external_ratio)``, a random subset of
+        that size drawn as the reference draws it (one ``torch.randperm``
+        on the device; ``generator`` defaults to the device's default
+        generator).  Edges to dropped or invalid columns become -1 with zero
+        values; if a value is NaN, every value goes through
+        ``nan_to_num_(0.0)`` (after ``num_edges`` was counted), as in the
+        reference.  ``subgraph.inner_graph`` masks every halo column too
+        (``num_cols = num_internal_nodes``).  Attributes as in the reference:
+        ``original_node_ids``, ``original_window_ids``, ``is_local_input``,
+        ``num_internal_nodes``.  Column arrays are stored flat (the reference
+        keeps a ``[tiles, tile_cols]`` view of the same values).
+
+        Runs on the device kernels of csrc/repack.hip; ``g`` must be resident
+        on ``window_ids``' device.  Duplicate window ids are an error (the
+        reference's result is ill-defined for them)."""
+        from types import SimpleNamespace
+        device = window_ids.device
+        window_ids, _ = torch.sort(window_ids)
+        if window_ids.numel() > 0:
+            valid = (window_ids >= 0) & (window_ids < g.num_windows)
+            window_ids = window_ids[valid]
+        num_windows = window_ids.size(0)
+        if dry_run:
+            off = g.window_offset
+            ids = window_ids.to(off.device, torch.int64)
+            lengths = off[ids + 1] - off[ids]
+            total_tiles = int(lengths.sum().item()) if lengths.numel() > 0 else 0
+            stub = SimpleNamespace()
+            stub.original_window_ids = window_ids
+            stub.num_internal_nodes = num_windows * self.tile_rows
+            stub.total_tiles = total_tiles
+            stub.approx_values = total_tiles * self.tile_rows * self.tile_cols
+            stub.approx_cols = total_tiles * self.tile_cols
+            stub.values_condensed = None
+            stub.original_col_indices = None
+            return stub
+        if g.tile_rows != self.tile_rows or g.tile_cols != self.tile_cols:
+            raise ValueError(f"repack_subgraph: graph tiles {g.tile_rows}x{g.tile_cols} differ from the "
+                             f"sampler's {self.tile_rows}x{self.tile_cols}")
+        if g.window_offset.device != device:
+            raise RuntimeError("repack_subgraph: the graph must be resident on the window ids' device")
+        if num_windows > 1 and bool((window_ids[1:] == window_ids[:-1]).any()):
+            raise ValueError("repack_subgraph: duplicate window ids")
+        st = self._repack_state(g.num_nodes, device)
+        r = repack(g.window_offset, g.original_col_indices, g.values_condensed, g.tile_cols, g.num_nodes,
+                   window_ids, max_external_ratio, st, generator=generator)
+        n_in = r.input_nodes.numel()
+        subgraph = BCSRGraph.from_components(
+            window_offset=r.window_offset, original_col_indices=r.halo_cols, values_condensed=r.halo_values,
+            num_rows=r.num_internal, num_cols=n_in, tile_rows=self.tile_rows, tile_cols=self.tile_cols,
+            device=device)
+        subgraph.original_node_ids = r.input_nodes
+        subgraph.original_window_ids = window_ids
+        subgraph.is_local_input = True
+        subgraph.num_internal_nodes = r.num_internal
+        inner_vals = r.inner_values
+        if r.any_nan:
+            # in place: the halo graph holds the same tensor
+            subgraph.values_condensed.nan_to_num_(0.0)
+            inner_vals = subgraph.values_condensed.clone()
+            T = r.inner_cols.numel() // self.tile_cols
+            m = (r.inner_cols == -1).view(T, 1, self.tile_cols).expand(-1, self.tile_rows, -1)
+            inner_vals.view(T, self.tile_rows, self.tile_cols).masked_fill_(m, 0.0)
+        subgraph.inner_graph = BCSRGraph.from_components(
+            window_offset=r.window_offset, original_col_indices=r.inner_cols, values_condensed=inner_vals,
+            num_rows=r.num_internal, num_cols=r.num_internal, tile_rows=self.tile_rows,
+            tile_cols=self.tile_cols, device=device)
+        return subgraph
 
     def print_avg_timing(self):
         print("\n" + "-" * 60)

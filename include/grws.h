@@ -365,6 +365,38 @@ int grws_gemm_tn(const void* a, int64_t lda, const void* b, int64_t ldb, int32_t
                  int64_t M, int64_t N, void* c, int64_t ldc, int32_t out_dtype, void* workspace,
                  size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Halo-aware subgraph repack: the device part of BCSRSampler.repack_subgraph */
+/* (sampler/sampler.py:420-690).  window_ids: int64, strictly ascending, in  */
+/* [0, num_windows).  State: the sampler's bitmap (uint32 [ceil(n/32)], all  */
+/* 0) and node map (int32 [n], all -1), n = num_nodes; every successful call */
+/* sequence prepare -> [externals] -> finish leaves both as found (prepare   */
+/* leaves the candidate marks in the bitmap for the next two calls; a failed */
+/* prepare clears them).                                                     */
+/*   prepare: new_offsets int64 [num_selected+1] (device); synchronises and  */
+/*     writes counts_out[3] = {tiles, internal nodes, external candidates}.  */
+/*   externals: the candidates ascending into int64 [candidates] (device).   */
+/*   finish: kept_external (ascending, device) or NULL to keep every         */
+/*     candidate (num_kept must then equal the candidate count); outputs:    */
+/*     input_nodes int64 [internal + kept] (internal nodes window by window, */
+/*     then the kept externals), halo/inner cols int32 [tiles*tc] and values */
+/*     [tiles*16*tc] in the graph's values dtype (masked columns -1 with     */
+/*     zero values; inner also masks columns >= internal).  Synchronises and */
+/*     writes flags_out[0] = 1 when a halo value is NaN.                     */
+/* ------------------------------------------------------------------------ */
+size_t grws_repack_workspace_bytes(int64_t num_selected, int64_t num_nodes);
+int grws_repack_prepare(const grws_bcsr* g, int64_t num_nodes, const int64_t* window_ids,
+                        int64_t num_selected, uint32_t* bitmap, int64_t* new_offsets,
+                        int64_t* counts_out, void* workspace, size_t workspace_bytes, void* stream);
+int grws_repack_externals(const uint32_t* bitmap, int64_t num_nodes, int64_t* external_out,
+                          void* workspace, size_t workspace_bytes, void* stream);
+int grws_repack_finish(const grws_bcsr* g, int64_t num_nodes, const int64_t* window_ids,
+                       int64_t num_selected, const int64_t* new_offsets, int64_t num_internal,
+                       const int64_t* kept_external, int64_t num_kept, int32_t* node_map,
+                       uint32_t* bitmap, int64_t* input_nodes, int32_t* halo_cols, void* halo_values,
+                       int32_t* inner_cols, void* inner_values, int32_t* flags_out, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

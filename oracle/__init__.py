@@ -25,6 +25,9 @@ Pinning (how each function is checked against something other than itself):
   * sample_hop/relabel -- invariants (distinct, min(deg,k) per node, sorted,
                           in range, bijective relabel, frontier prefix) and a
                           brute-force Floyd restatement in pure Python.
+  * repack_subgraph    -- a hand-built known answer, and edge-set equality
+                          against the dense matrix of the original graph
+                          restricted to the kept rows and columns.
 """
 from __future__ import annotations
 
@@ -443,3 +446,67 @@ def window_sample_all_layers(win, cols, vals, seeds, fanouts, num_global_nodes: 
             nxt[(nxt < 0) | (nxt >= num_global_nodes)] = -1
             active, masks = prepare_windows(nxt)
     return out
+
+
+def repack_subgraph(win, cols, vals, num_nodes: int, tile_cols: int, window_ids, ratio: float,
+                    perm=None, tile_rows: int = 16) -> dict:
+    """numpy restatement of BCSRSampler.repack_subgraph (sampler/sampler.py:
+    420-690), steps as in the reference: sort and filter the window ids
+    (:433-436); gather the windows' tiles (:466-487); internal nodes, window
+    then row order, below num_nodes (:492-497); valid neighbour columns,
+    unique, minus internal (:503-524); the budget int(internal * ratio)
+    with ``perm`` standing for the reference's torch.randperm draw
+    (:529-538); input nodes internal + kept (:543); relabel, dropped and
+    invalid columns -1 (:551-579); zero the values of -1 columns (:582-604);
+    nan_to_num when a NaN is left, after the halo graph counted its edges
+    (:607-639); the inner copy masking columns >= internal (:647-688).
+    Returns the arrays of both graphs."""
+    win = np.asarray(win, np.int64)
+    cols = np.asarray(cols, np.int64)
+    vals = np.asarray(vals)
+    W = win.size - 1
+    wid = np.sort(np.asarray(window_ids, np.int64))
+    wid = wid[(wid >= 0) & (wid < W)]
+    starts, ends = win[wid], win[wid + 1]
+    lengths = ends - starts
+    new_off = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    tiles = (np.concatenate([np.arange(a, b) for a, b in zip(starts, ends)]).astype(np.int64)
+             if wid.size else np.zeros(0, np.int64))
+    raw_cols = cols.reshape(-1, tile_cols)[tiles].reshape(-1).copy()
+    raw_vals = vals.reshape(-1, tile_rows, tile_cols)[tiles].reshape(-1).copy()
+    internal = (np.repeat(wid, tile_rows) * tile_rows + np.tile(np.arange(tile_rows), wid.size)).astype(np.int64)
+    internal = internal[internal < num_nodes]
+    n_int = int(internal.size)
+    valid = (raw_cols >= 0) & (raw_cols < num_nodes)
+    raw_cols[~valid] = -1
+    uniq = np.unique(raw_cols[valid])
+    is_int = np.zeros(W * tile_rows, bool)
+    is_int[internal] = True
+    ext = uniq[~is_int[uniq]]
+    budget = int(n_int * ratio)
+    if ext.size > budget:
+        if perm is None:
+            raise ValueError("over budget: pass the permutation the reference would draw")
+        kept = np.sort(ext[np.asarray(perm, np.int64)[:budget]])
+    else:
+        kept = ext
+    final = np.concatenate([internal, kept]).astype(np.int64)
+    g2l = np.full(max(num_nodes, 1), -1, np.int64)
+    g2l[final] = np.arange(final.size)
+    new_cols = np.full(raw_cols.shape, -1, np.int64)
+    new_cols[valid] = g2l[raw_cols[valid]]
+    T = tiles.size
+    v3 = raw_vals.reshape(T, tile_rows, tile_cols)
+    v3[np.broadcast_to((new_cols.reshape(T, tile_cols) == -1)[:, None, :], v3.shape)] = 0
+    nnz_halo = int(np.count_nonzero(raw_vals))
+    if np.isnan(raw_vals).any():
+        raw_vals = np.nan_to_num(raw_vals, nan=0.0)
+    inner_cols = new_cols.copy()
+    inner_cols[inner_cols >= n_int] = -1
+    inner_vals = raw_vals.copy()
+    iv3 = inner_vals.reshape(T, tile_rows, tile_cols)
+    iv3[np.broadcast_to((inner_cols.reshape(T, tile_cols) == -1)[:, None, :], iv3.shape)] = 0
+    return {"window_ids": wid, "window_offset": new_off, "input_nodes": final, "num_internal": n_int,
+            "halo_cols": new_cols.astype(np.int32), "halo_values": raw_vals, "halo_nnz": nnz_halo,
+            "inner_cols": inner_cols.astype(np.int32), "inner_values": inner_vals,
+            "inner_nnz": int(np.count_nonzero(inner_vals)), "num_external": int(ext.size)}
