@@ -372,6 +372,80 @@ def bench_minibatch(dev, batches: int, warmup: int) -> dict:
     return out
 
 
+def bench_dps(dev, cpu: bool, reps: int = 10) -> dict:
+    """The next-row extensions: the halo repack of BCSRSampler.repack_subgraph
+    (sampler.py:420-690) on c3 (a batch of 256 random windows = 4,096 seed
+    rows, external budget 5x, the reference's default), and loading a BCSR
+    cache in the reference's on-disk layout (data_loader.py:282-406) into
+    HBM, on c2 (page cache warm: host-memory-to-HBM rate, not the disk)."""
+    import tempfile
+
+    import numpy as np
+    from graph_rws_amd import synth
+    from graph_rws_amd.data import BCSRGraph, load_bcsr_bins, save_bcsr_bins
+    from graph_rws_amd.sampler import BCSRSampler
+    out = {}
+    g = synth.config_graph("c3", device=dev)
+    G = BCSRGraph.from_csr(g.row_ptr, g.col_idx, g.values, g.num_nodes, g.num_nodes, tile_cols=16,
+                           device=dev, values_dtype=torch.float16)
+    del g
+    s = BCSRSampler([5, 5], tile_cols=16)
+    gen = torch.Generator(device="cpu").manual_seed(77)
+    wids = torch.randperm(G.num_windows, generator=gen)[:256].to(dev)
+    torch.manual_seed(78)
+    sub = s.repack_subgraph(G, wids)  # warm-up
+    torch.cuda.synchronize(dev)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        sub = s.repack_subgraph(G, wids)
+        torch.cuda.synchronize(dev)
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    T = int(sub.window_offset[-1])
+    moved = T * 16 * 4 + T * 256 * 2 * 3 + T * 16 * 4 * 2  # cols read; values read + 2 writes; cols 2 writes
+    r = {"workload": "c3 repack_subgraph: 256 random windows (4,096 rows), max_external_ratio 5.0, f16 values",
+         "ms": round(1e3 * ts[len(ts) // 2], 3), "tiles": T, "internal_nodes": sub.num_internal_nodes,
+         "input_nodes": int(sub.original_node_ids.numel()), "tile_gb_moved": round(moved / 1e9, 4),
+         "note": "median of %d; includes the host syncs and torch.randperm of the over-budget draw" % reps}
+    if cpu:
+        import oracle
+        win = G.window_offset.cpu().numpy()
+        cols = G.original_col_indices.cpu().numpy()
+        vals = G.values_condensed.float().cpu().numpy()
+        ref0 = oracle.repack_subgraph(win, cols, vals, G.num_nodes, 16, wids.cpu().numpy(), 1e18)
+        perm = np.random.default_rng(0).permutation(ref0["num_external"])
+        t0 = time.perf_counter()
+        oracle.repack_subgraph(win, cols, vals, G.num_nodes, 16, wids.cpu().numpy(), 5.0, perm=perm)
+        t_cpu = time.perf_counter() - t0
+        r["cpu_baseline"] = {"value": round(1e3 * t_cpu, 2), "unit": "ms per repack", "cores": 1, "kind": "port",
+                             "sample": "the same batch through oracle.repack_subgraph (numpy, one thread, "
+                                       "graph arrays already in host memory)"}
+    out["repack"] = r
+    del G, sub
+    torch.cuda.empty_cache()
+    g = synth.config_graph("c2", device=dev)
+    G2 = BCSRGraph.from_csr(g.row_ptr, g.col_idx, g.values, g.num_nodes, g.num_nodes, tile_cols=16,
+                            device=dev)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "c2.pt")
+        save_bcsr_bins(G2, path)
+        load_bcsr_bins(path, device=dev, values_dtype=torch.float16)  # warm the page cache
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        H, _ = load_bcsr_bins(path, device=dev, values_dtype=torch.float16)
+        torch.cuda.synchronize(dev)
+        t_load = time.perf_counter() - t0
+        nbytes = 8 * H.window_offset.numel() + 4 * H.original_col_indices.numel() + 4 * H.values_condensed.numel()
+        same = bool(torch.equal(H.values_condensed, G2.values_condensed.half()))
+    out["bcsr_load"] = {"workload": "c2 BCSR cache (reference layout, f32 values) -> HBM, values to f16 on "
+                                    "the device", "file_bytes": nbytes, "ms": round(1e3 * t_load, 2),
+                        "gb_per_s": round(nbytes / t_load / 1e9, 2), "round_trip_equal": same}
+    del G2, H, g
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_spmm_c2(dev, reps: int = 20) -> dict:
     """c2 SpMM microbenchmark: forward A X and backward A^T G (G like X),
     X [169,343 x 128] in bf16 and f16, 16x16 tiles."""
@@ -426,6 +500,7 @@ def main():
     ap.add_argument("--sampling-batches", type=int, default=20)
     ap.add_argument("--no-gcn", action="store_true")
     ap.add_argument("--no-minibatch", action="store_true")
+    ap.add_argument("--no-dps", action="store_true", help="skip the repack / BCSR-cache leg")
     ap.add_argument("--minibatch-batches", type=int, default=40)
     ap.add_argument("--gcn-epochs", type=int, default=5)
     ap.add_argument("--gcn-configs", default="c1,c3,c4")
@@ -548,6 +623,8 @@ def main():
         out["spmm_c2"] = bench_spmm_c2(dev)
         out["gcn"] = {c: bench_gcn(c, dev, args.gcn_epochs, 2, not args.no_cpu_baseline)
                       for c in args.gcn_configs.split(",") if c}
+    if not args.no_dps:
+        out["dps"] = bench_dps(dev, not args.no_cpu_baseline)
     if not args.no_minibatch:
         out["minibatch"] = bench_minibatch(dev, args.minibatch_batches, 20)
     print(json.dumps(out), flush=True)
