@@ -668,3 +668,82 @@ def repack(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch
         raise
     return RepackResult(new_off, input_nodes[: n_int + n_kept], n_int, halo_cols, halo_vals, inner_cols,
                         inner_vals, flags[0])
+
+
+# ---------------------------------------------------------------------------
+# fused per-row epilogues (models/model.py:259-264, helper/engine.py:22-41)
+# ---------------------------------------------------------------------------
+def _rowwise_ok(t: torch.Tensor) -> bool:
+    return (t.is_cuda and t.dim() == 2 and t.stride(1) == 1 and t.stride(0) % 4 == 0
+            and t.data_ptr() % 8 == 0 and t.dtype in (torch.float32, torch.float16, torch.bfloat16))
+
+
+def act_norm_dropout_supported(z: torch.Tensor) -> bool:
+    """Whether the fused activation / LayerNorm / dropout kernel takes z."""
+    return _rowwise_ok(z) and 4 <= z.shape[1] <= 1024 and z.shape[1] % 4 == 0
+
+
+def act_norm_dropout_fwd(z: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float, p: float,
+                         act: int, seed: int, out_dtype: torch.dtype, save_stats: bool):
+    """out = dropout_p(LayerNorm(act(z))) (csrc/fused.hip); returns (out,
+    mean, rstd) with mean/rstd None unless save_stats."""
+    rows, dim = z.shape
+    out = torch.empty((rows, dim), dtype=out_dtype, device=z.device)
+    w = weight.detach().float().contiguous()
+    b = bias.detach().float().contiguous()
+    mean = rstd = None
+    if save_stats:
+        mean = torch.empty(max(1, rows), dtype=torch.float32, device=z.device)
+        rstd = torch.empty_like(mean)
+    L.call("grws_act_norm_dropout_fwd", L.ptr(z), L.dtype_code(z.dtype), z.stride(0), rows, dim, int(act),
+           L.ptr(w), L.ptr(b), float(eps), float(p), int(seed) & ((1 << 64) - 1), L.ptr(out),
+           L.dtype_code(out_dtype), out.stride(0), L.ptr(mean), L.ptr(rstd), L.stream_of(z.device))
+    return out, mean, rstd
+
+
+def act_norm_dropout_bwd(dout: torch.Tensor, z: torch.Tensor, mean: torch.Tensor, rstd: torch.Tensor,
+                         weight: torch.Tensor, p: float, act: int, seed: int):
+    """(dz, dgamma, dbeta) of act_norm_dropout_fwd."""
+    rows, dim = z.shape
+    if not _rowwise_ok(dout):
+        dout = dout.contiguous()
+    dz = torch.empty_like(z, memory_format=torch.contiguous_format)
+    dg = torch.empty(dim, dtype=torch.float32, device=z.device)
+    db = torch.empty_like(dg)
+    w = weight.detach().float().contiguous()
+    wsb = int(L.load().grws_act_norm_dropout_bwd_workspace_bytes(rows, dim))
+    ws = torch.empty(max(1, wsb), dtype=torch.uint8, device=z.device)
+    L.call("grws_act_norm_dropout_bwd", L.ptr(dout), L.dtype_code(dout.dtype), dout.stride(0), L.ptr(z),
+           L.dtype_code(z.dtype), z.stride(0), rows, dim, int(act), L.ptr(mean), L.ptr(rstd), L.ptr(w),
+           float(p), int(seed) & ((1 << 64) - 1), L.ptr(dz), dz.stride(0), L.ptr(dg), L.ptr(db), L.ptr(ws), wsb,
+           L.stream_of(z.device))
+    return dz, dg, db
+
+
+def cross_entropy_fwd(logits: torch.Tensor, rows: Optional[torch.Tensor], labels: torch.Tensor):
+    """(loss f32 scalar, counts int64 [3] = {argmax hits, counted rows, bad},
+    lse f32 [n]) of cross-entropy over logits[rows] (csrc/fused.hip); no
+    host sync."""
+    n = labels.numel()
+    dev = logits.device
+    lse = torch.empty(max(1, n), dtype=torch.float32, device=dev)
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    counts = torch.empty(3, dtype=torch.int64, device=dev)
+    wsb = int(L.load().grws_cross_entropy_workspace_bytes(n))
+    ws = torch.empty(max(1, wsb), dtype=torch.uint8, device=dev)
+    L.call("grws_cross_entropy_fwd", L.ptr(logits), L.dtype_code(logits.dtype), logits.stride(0),
+           logits.shape[0], logits.shape[1], L.ptr(rows) if rows is not None else None, L.ptr(labels), n,
+           L.ptr(lse), L.ptr(loss), L.ptr(counts), L.ptr(ws), wsb, L.stream_of(dev))
+    return loss, counts, lse
+
+
+def cross_entropy_bwd(logits: torch.Tensor, rows: Optional[torch.Tensor], labels: torch.Tensor,
+                      lse: torch.Tensor, dloss: torch.Tensor, counts: torch.Tensor) -> torch.Tensor:
+    """Gradient of cross_entropy_fwd's loss w.r.t. logits (zero outside rows)."""
+    grad = torch.zeros(logits.shape, dtype=logits.dtype, device=logits.device)
+    dl = dloss.detach().float().reshape(1).contiguous()
+    L.call("grws_cross_entropy_bwd", L.ptr(logits), L.dtype_code(logits.dtype), logits.stride(0),
+           logits.shape[0], logits.shape[1], L.ptr(rows) if rows is not None else None, L.ptr(labels),
+           labels.numel(), L.ptr(lse), L.ptr(dl), L.ptr(counts), L.ptr(grad), L.dtype_code(grad.dtype),
+           grad.stride(0), L.stream_of(logits.device))
+    return grad

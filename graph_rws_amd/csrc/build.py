@@ -35,6 +35,7 @@ SOURCES = [
     "window_sample.hip",
     "gemm_tn.hip",
     "repack.hip",
+    "fused.hip",
 ]
 
 ARCH = os.environ.get("GRWS_OFFLOAD_ARCH", "gfx950")

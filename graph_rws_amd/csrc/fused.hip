@@ -1,0 +1,582 @@
+// Fused per-row epilogues of the GCN model (gfx950).
+//
+// 1. Activation -> LayerNorm -> dropout, the per-hidden-layer tail of the
+//    reference model (models/model.py:259-264: act, self.norms[l], dropout),
+//    forward and backward.  The unfused torch path makes ~6 passes over the
+//    [rows x dim] activations forward (cast, ReLU, LayerNorm, dropout, cast)
+//    and ~8 backward; here each direction is one pass: one wave64 per row,
+//    4 consecutive elements per lane per 256 columns, statistics in fp32.
+//    The dropout mask is a pure function of (seed, row, column) -- Philox4x32-10
+//    (Salmon et al., SC'11), counter (row_lo, row_hi, column/4, 0), one
+//    4-word block per 4 columns, element kept when its word >= p * 2^32 --
+//    so the backward recomputes it instead of storing it.  dgamma / dbeta are
+//    summed per work-group in registers and LDS, then over work-groups in a
+//    fixed order (deterministic).
+// 2. Cross-entropy over a row subset (helper/engine.py:22-41 on
+//    logits[train_idx]): log-sum-exp, the label's term, mean over the rows
+//    whose label is not ignore_index, and the argmax hit count, in one pass
+//    over the selected rows; the backward writes softmax - onehot scaled by
+//    the incoming gradient straight into the selected rows of a
+//    [rows x classes] gradient.
+#include "grws_internal.h"
+
+namespace grws {
+namespace {
+
+constexpr int kBlk = 256;
+constexpr int kRowsPerBlock = kBlk / kWave;
+constexpr int kMaxSteps = 4;  // dim <= 4 * 256
+
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+struct Philox4 {
+    uint32_t w[4];
+};
+
+__device__ __forceinline__ Philox4 philox4(uint64_t seed, uint64_t row, uint32_t block) {
+    uint32_t c0 = (uint32_t)row, c1 = (uint32_t)(row >> 32), c2 = block, c3 = 0u;
+    uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        const uint32_t hi0 = __umulhi(0xD2511F53u, c0);
+        const uint32_t lo0 = 0xD2511F53u * c0;
+        const uint32_t hi1 = __umulhi(0xCD9E8D57u, c2);
+        const uint32_t lo1 = 0xCD9E8D57u * c2;
+        const uint32_t n0 = hi1 ^ c1 ^ k0;
+        const uint32_t n2 = hi0 ^ c3 ^ k1;
+        c0 = n0;
+        c1 = lo1;
+        c2 = n2;
+        c3 = lo0;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    return Philox4{{c0, c1, c2, c3}};
+}
+
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, float* v) {
+    if constexpr (std::is_same<T, float>::value) {
+        const float4_t x = *reinterpret_cast<const float4_t*>(p);
+        v[0] = x[0], v[1] = x[1], v[2] = x[2], v[3] = x[3];
+    } else {
+        const uint2 x = *reinterpret_cast<const uint2*>(p);
+        const T* h = reinterpret_cast<const T*>(&x);
+        v[0] = to_float(h[0]), v[1] = to_float(h[1]), v[2] = to_float(h[2]), v[3] = to_float(h[3]);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const float* v) {
+    if constexpr (std::is_same<T, float>::value) {
+        *reinterpret_cast<float4_t*>(p) = float4_t{v[0], v[1], v[2], v[3]};
+    } else {
+        T h[4] = {from_float<T>(v[0]), from_float<T>(v[1]), from_float<T>(v[2]), from_float<T>(v[3])};
+        *reinterpret_cast<uint2*>(p) = *reinterpret_cast<const uint2*>(h);
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t keep_threshold(float p) {
+    const double t = (double)p * 4294967296.0;
+    return t >= 4294967295.0 ? 0xFFFFFFFFu : (uint32_t)t;
+}
+
+// out = dropout(LayerNorm(act(z))), one wave per row.
+template <typename ZT, typename OT>
+__global__ __launch_bounds__(kBlk) void act_norm_dropout_fwd_kernel(
+    const ZT* __restrict__ z, int64_t ldz, int64_t rows, int dim, int act, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, float p, uint64_t seed, OT* __restrict__ out, int64_t ldo,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out) {
+    const int lane = threadIdx.x & 63;
+    const int steps = (dim + 255) / 256;
+    const uint32_t thr = keep_threshold(p);
+    const float scale = p > 0.f ? 1.0f / (1.0f - p) : 1.0f;
+    for (int64_t r = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6); r < rows;
+         r += (int64_t)gridDim.x * kRowsPerBlock) {
+        float x[kMaxSteps][4];
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < kMaxSteps; ++k) {
+            const int c = 256 * k + 4 * lane;
+            if (k < steps && c < dim) {
+                load4(z + r * ldz + c, x[k]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (act == 1) x[k][j] = x[k][j] < 0.f ? 0.f : x[k][j];  // NaN passes, as torch.relu
+                    s += x[k][j];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) x[k][j] = 0.f;
+            }
+        }
+        const float mean = wave_sum(s) / (float)dim;
+        float q = 0.f;
+#pragma unroll
+        for (int k = 0; k < kMaxSteps; ++k) {
+            const int c = 256 * k + 4 * lane;
+            if (k < steps && c < dim) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float d = x[k][j] - mean;
+                    q += d * d;
+                }
+            }
+        }
+        const float rstd = 1.0f / sqrtf(wave_sum(q) / (float)dim + eps);
+#pragma unroll
+        for (int k = 0; k < kMaxSteps; ++k) {
+            const int c = 256 * k + 4 * lane;
+            if (k < steps && c < dim) {
+                float y[4];
+                Philox4 u{{0u, 0u, 0u, 0u}};
+                if (p > 0.f) u = philox4(seed, (uint64_t)r, (uint32_t)(c >> 2));
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    y[j] = (x[k][j] - mean) * rstd * gamma[c + j] + beta[c + j];
+                    if (p > 0.f) y[j] = u.w[j] >= thr ? y[j] * scale : 0.f;
+                }
+                store4(out + r * ldo + c, y);
+            }
+        }
+        if (lane == 0 && mean_out) {
+            mean_out[r] = mean;
+            rstd_out[r] = rstd;
+        }
+    }
+}
+
+// dz from dout (see the header); per-work-group dgamma / dbeta partials.
+template <typename GT, typename ZT>
+__global__ __launch_bounds__(kBlk) void act_norm_dropout_bwd_kernel(
+    const GT* __restrict__ g, int64_t ldg, const ZT* __restrict__ z, int64_t ldz, int64_t rows, int dim, int act,
+    const float* __restrict__ mean_in, const float* __restrict__ rstd_in, const float* __restrict__ gamma, float p,
+    uint64_t seed, ZT* __restrict__ dz, int64_t lddz, float* __restrict__ part_g, float* __restrict__ part_b) {
+    __shared__ float red[2][kRowsPerBlock][1024];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int steps = (dim + 255) / 256;
+    const uint32_t thr = keep_threshold(p);
+    const float scale = p > 0.f ? 1.0f / (1.0f - p) : 1.0f;
+    float ag[kMaxSteps][4], ab[kMaxSteps][4];
+#pragma unroll
+    for (int k = 0; k < kMaxSteps; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ag[k][j] = ab[k][j] = 0.f;
+    for (int64_t r = (int64_t)blockIdx.x * kRowsPerBlock + wave; r < rows; r += (int64_t)gridDim.x * kRowsPerBlock) {
+        const float mean = mean_in[r], rstd = rstd_in[r];
+        float xh[kMaxSteps][4], dxh[kMaxSteps][4], zz[kMaxSteps][4];
+        float sa = 0.f, sb = 0.f;
+#pragma unroll
+        for (int k = 0; k < kMaxSteps; ++k) {
+            const int c = 256 * k + 4 * lane;
+            if (k < steps && c < dim) {
+                float gv[4];
+                load4(g + r * ldg + c, gv);
+                load4(z + r * ldz + c, zz[k]);
+                Philox4 u{{0u, 0u, 0u, 0u}};
+                if (p > 0.f) u = philox4(seed, (uint64_t)r, (uint32_t)(c >> 2));
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float x = zz[k][j];
+                    if (act == 1) x = x < 0.f ? 0.f : x;
+                    xh[k][j] = (x - mean) * rstd;
+                    float g1 = gv[j];
+                    if (p > 0.f) g1 = u.w[j] >= thr ? g1 * scale : 0.f;
+                    ag[k][j] += g1 * xh[k][j];
+                    ab[k][j] += g1;
+                    dxh[k][j] = g1 * gamma[c + j];
+                    sa += dxh[k][j];
+                    sb += dxh[k][j] * xh[k][j];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xh[k][j] = dxh[k][j] = zz[k][j] = 0.f;
+            }
+        }
+        const float a = wave_sum(sa) / (float)dim;
+        const float b = wave_sum(sb) / (float)dim;
+#pragma unroll
+        for (int k = 0; k < kMaxSteps; ++k) {
+            const int c = 256 * k + 4 * lane;
+            if (k < steps && c < dim) {
+                float d[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    d[j] = rstd * (dxh[k][j] - a - xh[k][j] * b);
+                    if (act == 1 && zz[k][j] <= 0.f) d[j] = 0.f;  // threshold_backward on the result
+                }
+                store4(dz + r * lddz + c, d);
+            }
+        }
+    }
+    // fixed-order reduction of the 4 waves, then one partial row per work-group
+#pragma unroll
+    for (int k = 0; k < kMaxSteps; ++k) {
+        const int c = 256 * k + 4 * lane;
+        if (k < steps && c < dim) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                red[0][wave][c + j] = ag[k][j];
+                red[1][wave][c + j] = ab[k][j];
+            }
+        }
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < dim; c += kBlk) {
+        float sg = 0.f, sbeta = 0.f;
+#pragma unroll
+        for (int w = 0; w < kRowsPerBlock; ++w) {
+            sg += red[0][w][c];
+            sbeta += red[1][w][c];
+        }
+        part_g[(int64_t)blockIdx.x * dim + c] = sg;
+        part_b[(int64_t)blockIdx.x * dim + c] = sbeta;
+    }
+}
+
+__global__ void column_sum_kernel(const float* __restrict__ part, int64_t nparts, int dim, float* __restrict__ out) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= dim) return;
+    float s = 0.f;
+    for (int64_t k = 0; k < nparts; ++k) s += part[k * dim + c];
+    out[c] = s;
+}
+
+int64_t bwd_blocks(int64_t rows) {
+    int64_t b = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    if (b > 2048) b = 2048;
+    return b < 1 ? 1 : b;
+}
+
+// ---------------------------------------------------------------------------
+// cross-entropy
+// ---------------------------------------------------------------------------
+constexpr int64_t kIgnore = -100;
+
+struct CeAcc {
+    double loss;
+    long long correct;
+    long long valid;
+    int bad;
+};
+
+// Whether (v, i) replaces the running (m, a) of an argmax: torch.argmax
+// treats NaN as the maximum and returns the first index among equal maxima.
+__device__ __forceinline__ bool argmax_better(float v, int i, float m, int a) {
+    const bool vn = v != v, mn = m != m;
+    if (vn) return !mn || i < a;
+    if (mn) return false;
+    return v > m || (v == m && i < a);
+}
+
+// One wave per selected row: lse, the label term, argmax (first index of the
+// maximum, as torch.argmax).  Block partials of (loss, hits, valid rows).
+template <typename T>
+__global__ __launch_bounds__(kBlk) void ce_fwd_kernel(const T* __restrict__ logits, int64_t ld, int64_t total_rows,
+                                                      int classes, const int64_t* __restrict__ rows,
+                                                      const int64_t* __restrict__ labels, int64_t n,
+                                                      float* __restrict__ lse_out, double* __restrict__ part_loss,
+                                                      long long* __restrict__ part_cnt) {
+    __shared__ double sl[kRowsPerBlock];
+    __shared__ long long sc[kRowsPerBlock], sv[kRowsPerBlock], sbad[kRowsPerBlock];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    double wl = 0.0;
+    long long wc = 0, wv = 0, wbad = 0;
+    for (int64_t i = (int64_t)blockIdx.x * kRowsPerBlock + wave; i < n; i += (int64_t)gridDim.x * kRowsPerBlock) {
+        const int64_t row = rows ? rows[i] : i;
+        const int64_t lab = labels[i];
+        if (row < 0 || row >= total_rows) {
+            if (lane == 0) wbad = 1;
+            continue;
+        }
+        const T* x = logits + row * ld;
+        float m = -INFINITY;
+        int arg = 0x7fffffff;
+        for (int c = lane; c < classes; c += kWave) {
+            const float v = to_float(x[c]);
+            if (argmax_better(v, c, m, arg)) {
+                m = v;
+                arg = c;
+            }
+        }
+#pragma unroll
+        for (int d = kWave / 2; d > 0; d >>= 1) {
+            const float om = __shfl_xor(m, d, kWave);
+            const int oa = __shfl_xor(arg, d, kWave);
+            if (argmax_better(om, oa, m, arg)) {
+                m = om;
+                arg = oa;
+            }
+        }
+        float s = 0.f;
+        for (int c = lane; c < classes; c += kWave) s += expf(to_float(x[c]) - m);
+        s = wave_sum(s);
+        const float lse = m + logf(s);
+        if (lane == 0) {
+            lse_out[i] = lse;
+            if (lab != kIgnore) {
+                if (lab < 0 || lab >= classes) {
+                    wbad = 1;
+                } else {
+                    wl += (double)(lse - to_float(x[lab]));
+                    wv += 1;
+                    wc += (arg == lab) ? 1 : 0;
+                }
+            }
+        }
+    }
+    if (lane == 0) {
+        sl[wave] = wl;
+        sc[wave] = wc;
+        sv[wave] = wv;
+        sbad[wave] = wbad;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double L = 0.0;
+        long long C = 0, V = 0, B = 0;
+        for (int w = 0; w < kRowsPerBlock; ++w) {
+            L += sl[w];
+            C += sc[w];
+            V += sv[w];
+            B |= sbad[w];
+        }
+        part_loss[blockIdx.x] = L;
+        part_cnt[3 * blockIdx.x] = C;
+        part_cnt[3 * blockIdx.x + 1] = V;
+        part_cnt[3 * blockIdx.x + 2] = B;
+    }
+}
+
+// loss = sum / valid (NaN when no row counts or a label is out of range:
+// torch asserts there), correct = hits, valid = counted rows.
+__global__ void ce_finish_kernel(const double* __restrict__ part_loss, const long long* __restrict__ part_cnt,
+                                 int64_t nparts, float* __restrict__ loss, int64_t* __restrict__ counts) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    double L = 0.0;
+    long long C = 0, V = 0, B = 0;
+    for (int64_t k = 0; k < nparts; ++k) {
+        L += part_loss[k];
+        C += part_cnt[3 * k];
+        V += part_cnt[3 * k + 1];
+        B |= part_cnt[3 * k + 2];
+    }
+    loss[0] = (B || V == 0) ? __int_as_float(0x7fc00000) : (float)(L / (double)V);
+    counts[0] = C;
+    counts[1] = V;
+    counts[2] = B;
+}
+
+// grad[row][c] = (softmax - onehot) * dloss / valid for counted rows, 0 for
+// ignored ones; other rows of grad are left alone (the caller zero-fills).
+template <typename T, typename GT>
+__global__ __launch_bounds__(kBlk) void ce_bwd_kernel(const T* __restrict__ logits, int64_t ld, int64_t total_rows,
+                                                      int classes, const int64_t* __restrict__ rows,
+                                                      const int64_t* __restrict__ labels, int64_t n,
+                                                      const float* __restrict__ lse, const float* __restrict__ dloss,
+                                                      const int64_t* __restrict__ counts, GT* __restrict__ grad,
+                                                      int64_t ldg) {
+    const int lane = threadIdx.x & 63;
+    const int64_t valid = counts[1];
+    const float scale = valid > 0 ? dloss[0] / (float)valid : 0.f;
+    for (int64_t i = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6); i < n;
+         i += (int64_t)gridDim.x * kRowsPerBlock) {
+        const int64_t row = rows ? rows[i] : i;
+        if (row < 0 || row >= total_rows) continue;
+        const int64_t lab = labels[i];
+        const bool counted = lab != kIgnore && lab >= 0 && lab < classes;
+        const float l = lse[i];
+        for (int c = lane; c < classes; c += kWave) {
+            float v = 0.f;
+            if (counted) v = (expf(to_float(logits[row * ld + c]) - l) - (c == lab ? 1.f : 0.f)) * scale;
+            grad[row * ldg + c] = from_float<GT>(v);
+        }
+    }
+}
+
+int64_t ce_blocks(int64_t n) {
+    int64_t b = (n + kRowsPerBlock - 1) / kRowsPerBlock;
+    if (b > 4096) b = 4096;
+    return b < 1 ? 1 : b;
+}
+
+}  // namespace
+}  // namespace grws
+
+using namespace grws;
+
+extern "C" size_t grws_act_norm_dropout_bwd_workspace_bytes(int64_t rows, int64_t dim) {
+    if (rows < 0 || dim < 0) return 0;
+    Sizer s;
+    s.take<float>((size_t)bwd_blocks(rows) * (size_t)dim);
+    s.take<float>((size_t)bwd_blocks(rows) * (size_t)dim);
+    return s.used;
+}
+
+#define GRWS_DISPATCH2(DT_A, DT_B, MACRO)                                                          \
+    do {                                                                                           \
+        if ((DT_A) == GRWS_F32) {                                                                  \
+            if ((DT_B) == GRWS_F32) MACRO(float, float);                                           \
+            else if ((DT_B) == GRWS_F16) MACRO(float, _Float16);                                   \
+            else MACRO(float, __hip_bfloat16);                                                     \
+        } else if ((DT_A) == GRWS_F16) {                                                           \
+            if ((DT_B) == GRWS_F32) MACRO(_Float16, float);                                        \
+            else if ((DT_B) == GRWS_F16) MACRO(_Float16, _Float16);                                \
+            else MACRO(_Float16, __hip_bfloat16);                                                  \
+        } else {                                                                                   \
+            if ((DT_B) == GRWS_F32) MACRO(__hip_bfloat16, float);                                  \
+            else if ((DT_B) == GRWS_F16) MACRO(__hip_bfloat16, _Float16);                          \
+            else MACRO(__hip_bfloat16, __hip_bfloat16);                                            \
+        }                                                                                          \
+    } while (0)
+
+static int check_rowwise(int32_t a_dt, int32_t b_dt, int64_t rows, int64_t dim, int64_t lda, int64_t ldb,
+                         const void* a, const void* b) {
+    for (int32_t dt : {a_dt, b_dt})
+        if (dt != GRWS_F32 && dt != GRWS_F16 && dt != GRWS_BF16)
+            return set_error(GRWS_E_DTYPE, "act_norm_dropout: unsupported dtype %d", dt);
+    GRWS_CHECK_ARG(rows >= 0, "act_norm_dropout: negative rows");
+    GRWS_CHECK_ARG(dim > 0 && dim <= 1024 && dim % 4 == 0, "act_norm_dropout: dim must be 4..1024, a multiple of 4");
+    GRWS_CHECK_ARG(lda >= dim && ldb >= dim && lda % 4 == 0 && ldb % 4 == 0,
+                   "act_norm_dropout: leading dimensions must be >= dim and multiples of 4");
+    GRWS_CHECK_ARG((reinterpret_cast<uintptr_t>(a) % 8) == 0 && (reinterpret_cast<uintptr_t>(b) % 8) == 0,
+                   "act_norm_dropout: rows must be 8-byte aligned");
+    return GRWS_OK;
+}
+
+extern "C" int grws_act_norm_dropout_fwd(const void* z, int32_t z_dtype, int64_t ldz, int64_t rows, int64_t dim,
+                                         int32_t act, const float* gamma, const float* beta, float eps, float p,
+                                         uint64_t seed, void* out, int32_t out_dtype, int64_t ldo, float* mean,
+                                         float* rstd, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(act == 0 || act == 1, "act_norm_dropout: act must be 0 (none) or 1 (relu)");
+    GRWS_CHECK_ARG(p >= 0.f && p < 1.f, "act_norm_dropout: p must be in [0, 1)");
+    GRWS_CHECK_ARG((mean == nullptr) == (rstd == nullptr), "act_norm_dropout: mean and rstd go together");
+    if (rows == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(z && out && gamma && beta, "act_norm_dropout: null pointer");
+    GRWS_TRY(check_rowwise(z_dtype, out_dtype, rows, dim, ldz, ldo, z, out));
+    int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    if (blocks > 65536) blocks = 65536;
+#define GRWS_ANDF(ZT, OT)                                                                                     \
+    hipLaunchKernelGGL((act_norm_dropout_fwd_kernel<ZT, OT>), dim3((unsigned)blocks), dim3(kBlk), 0, stream,  \
+                       static_cast<const ZT*>(z), ldz, rows, (int)dim, (int)act, gamma, beta, eps, p, seed,    \
+                       static_cast<OT*>(out), ldo, mean, rstd)
+    GRWS_DISPATCH2(z_dtype, out_dtype, GRWS_ANDF);
+#undef GRWS_ANDF
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
+extern "C" int grws_act_norm_dropout_bwd(const void* dout, int32_t dout_dtype, int64_t ldg, const void* z,
+                                         int32_t z_dtype, int64_t ldz, int64_t rows, int64_t dim, int32_t act,
+                                         const float* mean, const float* rstd, const float* gamma, float p,
+                                         uint64_t seed, void* dz, int64_t lddz, float* dgamma, float* dbeta,
+                                         void* workspace, size_t workspace_bytes, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(act == 0 || act == 1, "act_norm_dropout: act must be 0 (none) or 1 (relu)");
+    GRWS_CHECK_ARG(p >= 0.f && p < 1.f, "act_norm_dropout: p must be in [0, 1)");
+    GRWS_CHECK_ARG(dgamma && dbeta, "act_norm_dropout: null dgamma/dbeta");
+    GRWS_CHECK_ARG(dim > 0 && dim <= 1024 && dim % 4 == 0, "act_norm_dropout: dim must be 4..1024, a multiple of 4");
+    if (rows == 0) {
+        GRWS_TRY(fill_bytes_zero(dgamma, (size_t)dim * 4, stream));
+        GRWS_TRY(fill_bytes_zero(dbeta, (size_t)dim * 4, stream));
+        return GRWS_OK;
+    }
+    GRWS_CHECK_ARG(dout && z && mean && rstd && gamma && dz, "act_norm_dropout: null pointer");
+    GRWS_TRY(check_rowwise(dout_dtype, z_dtype, rows, dim, ldg, ldz, dout, z));
+    GRWS_CHECK_ARG(lddz >= dim && lddz % 4 == 0 && (reinterpret_cast<uintptr_t>(dz) % 8) == 0,
+                   "act_norm_dropout: bad dz layout");
+    const int64_t blocks = bwd_blocks(rows);
+    Carver cv(workspace, workspace_bytes);
+    float* pg = cv.take<float>((size_t)blocks * (size_t)dim);
+    float* pb = cv.take<float>((size_t)blocks * (size_t)dim);
+    if (!cv.ok)
+        return set_error(GRWS_E_CAPACITY, "act_norm_dropout: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+#define GRWS_ANDB(GT, ZT)                                                                                     \
+    hipLaunchKernelGGL((act_norm_dropout_bwd_kernel<GT, ZT>), dim3((unsigned)blocks), dim3(kBlk), 0, stream,  \
+                       static_cast<const GT*>(dout), ldg, static_cast<const ZT*>(z), ldz, rows, (int)dim,      \
+                       (int)act, mean, rstd, gamma, p, seed, static_cast<ZT*>(dz), lddz, pg, pb)
+    GRWS_DISPATCH2(dout_dtype, z_dtype, GRWS_ANDB);
+#undef GRWS_ANDB
+    GRWS_LAUNCH_CHECK();
+    const unsigned cb = (unsigned)((dim + 255) / 256);
+    hipLaunchKernelGGL(column_sum_kernel, dim3(cb), dim3(256), 0, stream, pg, blocks, (int)dim, dgamma);
+    GRWS_LAUNCH_CHECK();
+    hipLaunchKernelGGL(column_sum_kernel, dim3(cb), dim3(256), 0, stream, pb, blocks, (int)dim, dbeta);
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
+extern "C" size_t grws_cross_entropy_workspace_bytes(int64_t n) {
+    if (n < 0) return 0;
+    Sizer s;
+    s.take<double>((size_t)ce_blocks(n));
+    s.take<long long>(3 * (size_t)ce_blocks(n));
+    return s.used;
+}
+
+extern "C" int grws_cross_entropy_fwd(const void* logits, int32_t dtype, int64_t ld, int64_t total_rows,
+                                      int64_t classes, const int64_t* rows, const int64_t* labels, int64_t n,
+                                      float* lse_out, float* loss_out, int64_t* counts_out, void* workspace,
+                                      size_t workspace_bytes, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    if (dtype != GRWS_F32 && dtype != GRWS_F16 && dtype != GRWS_BF16)
+        return set_error(GRWS_E_DTYPE, "cross_entropy: unsupported dtype %d", dtype);
+    GRWS_CHECK_ARG(classes > 0 && classes <= INT32_MAX && ld >= classes && n >= 0 && total_rows >= 0,
+                   "cross_entropy: bad sizes");
+    GRWS_CHECK_ARG(loss_out && counts_out, "cross_entropy: null output");
+    if (n > 0) GRWS_CHECK_ARG(logits && labels && lse_out, "cross_entropy: null pointer");
+    const int64_t blocks = ce_blocks(n);
+    Carver cv(workspace, workspace_bytes);
+    double* pl = cv.take<double>((size_t)blocks);
+    long long* pc = cv.take<long long>(3 * (size_t)blocks);
+    if (!cv.ok)
+        return set_error(GRWS_E_CAPACITY, "cross_entropy: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+#define GRWS_CEF(T)                                                                                            \
+    hipLaunchKernelGGL(ce_fwd_kernel<T>, dim3((unsigned)blocks), dim3(kBlk), 0, stream,                        \
+                       static_cast<const T*>(logits), ld, total_rows, (int)classes, rows, labels, n, lse_out, pl, pc)
+    if (dtype == GRWS_F32) GRWS_CEF(float);
+    else if (dtype == GRWS_F16) GRWS_CEF(_Float16);
+    else GRWS_CEF(__hip_bfloat16);
+#undef GRWS_CEF
+    GRWS_LAUNCH_CHECK();
+    hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(64), 0, stream, pl, pc, blocks, loss_out, counts_out);
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
+extern "C" int grws_cross_entropy_bwd(const void* logits, int32_t dtype, int64_t ld, int64_t total_rows,
+                                      int64_t classes, const int64_t* rows, const int64_t* labels, int64_t n,
+                                      const float* lse, const float* dloss, const int64_t* counts, void* grad,
+                                      int32_t grad_dtype, int64_t ldg, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    if (dtype != GRWS_F32 && dtype != GRWS_F16 && dtype != GRWS_BF16)
+        return set_error(GRWS_E_DTYPE, "cross_entropy: unsupported dtype %d", dtype);
+    if (grad_dtype != GRWS_F32 && grad_dtype != GRWS_F16 && grad_dtype != GRWS_BF16)
+        return set_error(GRWS_E_DTYPE, "cross_entropy: unsupported grad dtype %d", grad_dtype);
+    GRWS_CHECK_ARG(classes > 0 && classes <= INT32_MAX && ld >= classes && ldg >= classes && n >= 0,
+                   "cross_entropy: bad sizes");
+    if (n == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(logits && labels && lse && dloss && counts && grad, "cross_entropy: null pointer");
+    const int64_t blocks = ce_blocks(n);
+#define GRWS_CEB(T, GT)                                                                                        \
+    hipLaunchKernelGGL((ce_bwd_kernel<T, GT>), dim3((unsigned)blocks), dim3(kBlk), 0, stream,                  \
+                       static_cast<const T*>(logits), ld, total_rows, (int)classes, rows, labels, n, lse, dloss,  \
+                       counts, static_cast<GT*>(grad), ldg)
+    GRWS_DISPATCH2(dtype, grad_dtype, GRWS_CEB);
+#undef GRWS_CEB
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}

@@ -21,6 +21,28 @@ def compute_loss_and_metrics(logits, labels):
     return loss, correct, labels.size(0)
 
 
+def loss_and_metrics_rows(logits, rows, labels, check_rows: bool = True):
+    """compute_loss_and_metrics(logits[rows].float(), labels) with the
+    single-label cross-entropy on the fused kernel (no gather, no cast) when
+    rows are strictly ascending (train_idx from a mask is; checked once per
+    tensor, or not at all with check_rows=False, which then takes the torch
+    path for any rows given); the reference's torch ops otherwise.  rows
+    None = the first labels.numel() rows."""
+    from ..layers.fused import cross_entropy_rows, cross_entropy_supported, rows_distinct
+    if (FUSED_LOSS and labels.dim() == 1 and cross_entropy_supported(logits, labels)
+            and (rows is None or (check_rows and rows.dtype == torch.int64 and rows.is_cuda
+                                  and rows.dim() == 1 and rows_distinct(rows)))):
+        loss, counts = cross_entropy_rows(logits, rows, labels)
+        return loss, counts[0], labels.numel()
+    sel = logits[rows] if rows is not None else logits[: labels.shape[0]]
+    return compute_loss_and_metrics(sel.float(), labels)
+
+
+# Cross-entropy on the fused kernel where it applies; False restores the
+# reference's torch ops.
+FUSED_LOSS = True
+
+
 def train_epoch_full(model, graphs_for_model, features: torch.Tensor, labels: torch.Tensor,
                      train_idx: torch.Tensor, optimizer: torch.optim.Optimizer, device,
                      timer=None, sync: bool = True):
@@ -33,7 +55,7 @@ def train_epoch_full(model, graphs_for_model, features: torch.Tensor, labels: to
         features = features.to(device)
     optimizer.zero_grad()
     logits = model(graphs_for_model, features)
-    loss, correct, n = compute_loss_and_metrics(logits[train_idx].float(), labels[train_idx])
+    loss, correct, n = loss_and_metrics_rows(logits, train_idx, labels[train_idx])
     acc = correct / n if n > 0 else 0.0
     loss.backward()
     torch.nn.utils.clip_grad_norm_(model.parameters(), max_norm=1.0)
@@ -144,7 +166,7 @@ def _sample_batch(sampler, graph, seeds, features, device, needs_t=None):
 def _seed_rows(sampler, subgraphs, seeds, logits, tile_rows):
     from ..sampler import NeighborSampler
     if isinstance(sampler, NeighborSampler):
-        return torch.arange(seeds.numel(), device=logits.device)
+        return None  # the seeds are the first rows of the output
     act = subgraphs[-1].active_windows.long()
     sw = torch.div(seeds, tile_rows, rounding_mode="floor")
     sa, perm = torch.sort(act)
@@ -190,7 +212,7 @@ def train_epoch_node_sampling(model, graphs_for_model, features: torch.Tensor,
         logits = model(subgraphs, feats if feats is not None else features)
         timer.record("Fwd")
         rows = _seed_rows(sampler, subgraphs, seeds, logits, tile_rows)
-        loss, correct, n = compute_loss_and_metrics(logits[rows].float(), labels[seeds])
+        loss, correct, n = loss_and_metrics_rows(logits, rows, labels[seeds], check_rows=False)
         loss.backward()
         timer.record("Bwd")
         torch.nn.utils.clip_grad_norm_(model.parameters(), max_norm=1.0)

@@ -9,9 +9,10 @@ hidden layer: optional residual, activation, LayerNorm, dropout
     reindex_bcsr over the previous layer's active windows (model.py:126-141);
   * the self path gathers/slices the target rows (_get_residual,
     model.py:145-210).
-The one change: the layer-0 masking is applied once per graph state instead
-of on every forward (it is idempotent), so the cached SpMM transpose of the
-graph survives from epoch to epoch.
+Two changes: the layer-0 masking is applied once per graph state instead of
+on every forward (it is idempotent), so the cached SpMM transpose of the
+graph survives from epoch to epoch; and the hidden-layer tail (ReLU,
+LayerNorm, dropout) runs as one fused kernel each way (layers/fused.py).
 """
 from __future__ import annotations
 
@@ -25,6 +26,11 @@ from torch.utils.checkpoint import checkpoint
 
 from ..data import BCSRGraph
 from ..layers import BCSRGraphConv
+from ..layers.fused import act_norm_dropout, fusable_norm
+
+# Run the hidden-layer tail (ReLU, LayerNorm, dropout) on the fused kernel
+# where it applies; False restores torch's separate ops.
+FUSED_EPILOGUE = True
 
 
 class GCN_BCSR(nn.Module):
@@ -170,10 +176,21 @@ class GCN_BCSR(nn.Module):
                 h_out = h_out + self._get_residual(l, g, prev_g, h_res, h_out.shape[0])
             h = h_out
             if l < len(self.layers) - 1:
-                h = self.activation(h)
-                h = self.norms[l](h)
-                if self.dropout_layer is not None:
-                    h = self.dropout_layer(h)
+                h = self._hidden_tail(l, h, self.training)
+        return h
+
+    def _hidden_tail(self, l: int, h: torch.Tensor, training: bool) -> torch.Tensor:
+        """activation -> norms[l] -> dropout (model.py:259-264): one fused
+        kernel each way for ReLU (or no activation) + LayerNorm + dropout,
+        torch ops otherwise."""
+        p = self.dropout if (training and self.dropout_layer is not None) else 0.0
+        relu = self.activation is F.relu
+        if FUSED_EPILOGUE and relu and h.is_cuda and fusable_norm(self.norms[l], h):
+            return act_norm_dropout(h, self.norms[l], p, relu=True)
+        h = self.activation(h)
+        h = self.norms[l](h)
+        if training and self.dropout_layer is not None:
+            h = self.dropout_layer(h)
         return h
 
     @torch.no_grad()
@@ -187,6 +204,5 @@ class GCN_BCSR(nn.Module):
         for l, layer in enumerate(self.layers):
             h = layer(g, h)
             if l < len(self.layers) - 1:
-                h = self.activation(h)
-                h = self.norms[l](h)
+                h = self._hidden_tail(l, h, False)
         return h

@@ -397,6 +397,51 @@ int grws_repack_finish(const grws_bcsr* g, int64_t num_nodes, const int64_t* win
                        int32_t* inner_cols, void* inner_values, int32_t* flags_out, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Fused hidden-layer tail: out = dropout(LayerNorm(act(z))) per row, the   */
+/* sequence of models/model.py:259-264 (act, self.norms[l], dropout).  act  */
+/* 0 = identity, 1 = ReLU; LayerNorm over dim (biased variance, eps) with   */
+/* fp32 gamma/beta; dropout with probability p, scale 1/(1-p), mask from    */
+/* Philox4x32-10 keyed by seed (counter = row, column/4), recomputed by the */
+/* backward.  z/out/dout/dz in F32/F16/BF16; dim a multiple of 4, <= 1024;  */
+/* rows and leading dimensions multiples of 4 elements, 8-byte aligned.     */
+/* mean/rstd: fp32 [rows] saved for the backward (both NULL to skip).       */
+/* The backward writes dz (z's dtype) and fp32 dgamma/dbeta [dim], summed   */
+/* in a fixed order.                                                        */
+/* ------------------------------------------------------------------------ */
+int grws_act_norm_dropout_fwd(const void* z, int32_t z_dtype, int64_t ldz, int64_t rows, int64_t dim,
+                              int32_t act, const float* gamma, const float* beta, float eps, float p,
+                              uint64_t seed, void* out, int32_t out_dtype, int64_t ldo, float* mean,
+                              float* rstd, void* stream);
+size_t grws_act_norm_dropout_bwd_workspace_bytes(int64_t rows, int64_t dim);
+int grws_act_norm_dropout_bwd(const void* dout, int32_t dout_dtype, int64_t ldg, const void* z,
+                              int32_t z_dtype, int64_t ldz, int64_t rows, int64_t dim, int32_t act,
+                              const float* mean, const float* rstd, const float* gamma, float p,
+                              uint64_t seed, void* dz, int64_t lddz, float* dgamma, float* dbeta,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Cross-entropy over a subset of the rows of logits [total_rows x ld]      */
+/* (helper/engine.py:22-41: F.cross_entropy(logits[idx], labels[idx]) and   */
+/* the argmax hit count).  rows: int64 [n] row ids (NULL = rows 0..n-1),    */
+/* labels: int64 [n]; label -100 is ignored (torch's ignore_index).         */
+/* Forward, no sync: lse_out fp32 [n], loss_out fp32 device scalar (mean    */
+/* over counted rows; NaN when none counts or a label is out of range,      */
+/* where torch asserts), counts_out int64 [3] device = {argmax hits,        */
+/* counted rows, bad input flag}.  Backward: grad rows of `rows` get        */
+/* (softmax - onehot) * dloss / counted (0 for ignored rows); other rows of */
+/* grad are left as they are (zero them first).  rows must be distinct.     */
+/* ------------------------------------------------------------------------ */
+size_t grws_cross_entropy_workspace_bytes(int64_t n);
+int grws_cross_entropy_fwd(const void* logits, int32_t dtype, int64_t ld, int64_t total_rows,
+                           int64_t classes, const int64_t* rows, const int64_t* labels, int64_t n,
+                           float* lse_out, float* loss_out, int64_t* counts_out, void* workspace,
+                           size_t workspace_bytes, void* stream);
+int grws_cross_entropy_bwd(const void* logits, int32_t dtype, int64_t ld, int64_t total_rows,
+                           int64_t classes, const int64_t* rows, const int64_t* labels, int64_t n,
+                           const float* lse, const float* dloss, const int64_t* counts, void* grad,
+                           int32_t grad_dtype, int64_t ldg, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
