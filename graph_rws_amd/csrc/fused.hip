@@ -25,7 +25,6 @@ namespace {
 
 constexpr int kBlk = 256;
 constexpr int kRowsPerBlock = kBlk / kWave;
-constexpr int kMaxSteps = 4;  // dim <= 4 * 256
 
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
@@ -87,145 +86,175 @@ __device__ __forceinline__ uint32_t keep_threshold(float p) {
     return t >= 4294967295.0 ? 0xFFFFFFFFu : (uint32_t)t;
 }
 
-// out = dropout(LayerNorm(act(z))), one wave per row.
-template <typename ZT, typename OT>
+// out = dropout(LayerNorm(act(z))).  One wave per row, ROWS rows in flight
+// per wave (their loads are issued together), STEPS = ceil(dim / 256).
+template <typename ZT, typename OT, int STEPS, int ROWS>
 __global__ __launch_bounds__(kBlk) void act_norm_dropout_fwd_kernel(
     const ZT* __restrict__ z, int64_t ldz, int64_t rows, int dim, int act, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, float p, uint64_t seed, OT* __restrict__ out, int64_t ldo,
     float* __restrict__ mean_out, float* __restrict__ rstd_out) {
     const int lane = threadIdx.x & 63;
-    const int steps = (dim + 255) / 256;
     const uint32_t thr = keep_threshold(p);
     const float scale = p > 0.f ? 1.0f / (1.0f - p) : 1.0f;
-    for (int64_t r = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6); r < rows;
-         r += (int64_t)gridDim.x * kRowsPerBlock) {
-        float x[kMaxSteps][4];
-        float s = 0.f;
+    const int64_t stride = (int64_t)gridDim.x * kRowsPerBlock * ROWS;
+    for (int64_t r0 = ((int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) * ROWS; r0 < rows; r0 += stride) {
+        float x[ROWS][STEPS][4];
 #pragma unroll
-        for (int k = 0; k < kMaxSteps; ++k) {
-            const int c = 256 * k + 4 * lane;
-            if (k < steps && c < dim) {
-                load4(z + r * ldz + c, x[k]);
+        for (int i = 0; i < ROWS; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (act == 1) x[k][j] = x[k][j] < 0.f ? 0.f : x[k][j];  // NaN passes, as torch.relu
-                    s += x[k][j];
-                }
-            } else {
+            for (int k = 0; k < STEPS; ++k) {
+                const int c = 256 * k + 4 * lane;
+                if (r0 + i < rows && c < dim) {
+                    load4(z + (r0 + i) * ldz + c, x[i][k]);
+                } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) x[k][j] = 0.f;
-            }
-        }
-        const float mean = wave_sum(s) / (float)dim;
-        float q = 0.f;
-#pragma unroll
-        for (int k = 0; k < kMaxSteps; ++k) {
-            const int c = 256 * k + 4 * lane;
-            if (k < steps && c < dim) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float d = x[k][j] - mean;
-                    q += d * d;
+                    for (int j = 0; j < 4; ++j) x[i][k][j] = 0.f;
                 }
             }
-        }
-        const float rstd = 1.0f / sqrtf(wave_sum(q) / (float)dim + eps);
+        float mean[ROWS], rstd[ROWS];
 #pragma unroll
-        for (int k = 0; k < kMaxSteps; ++k) {
-            const int c = 256 * k + 4 * lane;
-            if (k < steps && c < dim) {
-                float y[4];
-                Philox4 u{{0u, 0u, 0u, 0u}};
-                if (p > 0.f) u = philox4(seed, (uint64_t)r, (uint32_t)(c >> 2));
+        for (int i = 0; i < ROWS; ++i) {
+            float sum = 0.f;
+#pragma unroll
+            for (int k = 0; k < STEPS; ++k)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    y[j] = (x[k][j] - mean) * rstd * gamma[c + j] + beta[c + j];
-                    if (p > 0.f) y[j] = u.w[j] >= thr ? y[j] * scale : 0.f;
+                    if (act == 1) x[i][k][j] = x[i][k][j] < 0.f ? 0.f : x[i][k][j];  // NaN passes, as torch.relu
+                    sum += x[i][k][j];
                 }
-                store4(out + r * ldo + c, y);
-            }
+            mean[i] = wave_sum(sum) / (float)dim;
         }
-        if (lane == 0 && mean_out) {
-            mean_out[r] = mean;
-            rstd_out[r] = rstd;
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i) {
+            float q = 0.f;
+#pragma unroll
+            for (int k = 0; k < STEPS; ++k) {
+                const int c = 256 * k + 4 * lane;
+                if (c < dim) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float d = x[i][k][j] - mean[i];
+                        q += d * d;
+                    }
+                }
+            }
+            rstd[i] = 1.0f / sqrtf(wave_sum(q) / (float)dim + eps);
+        }
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i) {
+            const int64_t r = r0 + i;
+            if (r >= rows) break;
+#pragma unroll
+            for (int k = 0; k < STEPS; ++k) {
+                const int c = 256 * k + 4 * lane;
+                if (c < dim) {
+                    float y[4];
+                    Philox4 u{{0u, 0u, 0u, 0u}};
+                    if (p > 0.f) u = philox4(seed, (uint64_t)r, (uint32_t)(c >> 2));
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        y[j] = (x[i][k][j] - mean[i]) * rstd[i] * gamma[c + j] + beta[c + j];
+                        if (p > 0.f) y[j] = u.w[j] >= thr ? y[j] * scale : 0.f;
+                    }
+                    store4(out + r * ldo + c, y);
+                }
+            }
+            if (lane == 0 && mean_out) {
+                mean_out[r] = mean[i];
+                rstd_out[r] = rstd[i];
+            }
         }
     }
 }
 
 // dz from dout (see the header); per-work-group dgamma / dbeta partials.
-template <typename GT, typename ZT>
+// ROWS rows in flight per wave, as in the forward.
+template <typename GT, typename ZT, int STEPS, int ROWS>
 __global__ __launch_bounds__(kBlk) void act_norm_dropout_bwd_kernel(
     const GT* __restrict__ g, int64_t ldg, const ZT* __restrict__ z, int64_t ldz, int64_t rows, int dim, int act,
     const float* __restrict__ mean_in, const float* __restrict__ rstd_in, const float* __restrict__ gamma, float p,
     uint64_t seed, ZT* __restrict__ dz, int64_t lddz, float* __restrict__ part_g, float* __restrict__ part_b) {
-    __shared__ float red[2][kRowsPerBlock][1024];
+    __shared__ float red[2][kRowsPerBlock][STEPS * 256];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int steps = (dim + 255) / 256;
     const uint32_t thr = keep_threshold(p);
     const float scale = p > 0.f ? 1.0f / (1.0f - p) : 1.0f;
-    float ag[kMaxSteps][4], ab[kMaxSteps][4];
+    float ag[STEPS][4], ab[STEPS][4], gm[STEPS][4];
 #pragma unroll
-    for (int k = 0; k < kMaxSteps; ++k)
+    for (int k = 0; k < STEPS; ++k)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ag[k][j] = ab[k][j] = 0.f;
-    for (int64_t r = (int64_t)blockIdx.x * kRowsPerBlock + wave; r < rows; r += (int64_t)gridDim.x * kRowsPerBlock) {
-        const float mean = mean_in[r], rstd = rstd_in[r];
-        float xh[kMaxSteps][4], dxh[kMaxSteps][4], zz[kMaxSteps][4];
-        float sa = 0.f, sb = 0.f;
+        for (int j = 0; j < 4; ++j) {
+            ag[k][j] = ab[k][j] = 0.f;
+            const int c = 256 * k + 4 * lane + j;
+            gm[k][j] = c < dim ? gamma[c] : 0.f;
+        }
+    const int64_t stride = (int64_t)gridDim.x * kRowsPerBlock * ROWS;
+    for (int64_t r0 = ((int64_t)blockIdx.x * kRowsPerBlock + wave) * ROWS; r0 < rows; r0 += stride) {
+        float gv[ROWS][STEPS][4], zz[ROWS][STEPS][4];
 #pragma unroll
-        for (int k = 0; k < kMaxSteps; ++k) {
-            const int c = 256 * k + 4 * lane;
-            if (k < steps && c < dim) {
-                float gv[4];
-                load4(g + r * ldg + c, gv);
-                load4(z + r * ldz + c, zz[k]);
+        for (int i = 0; i < ROWS; ++i)
+#pragma unroll
+            for (int k = 0; k < STEPS; ++k) {
+                const int c = 256 * k + 4 * lane;
+                if (r0 + i < rows && c < dim) {
+                    load4(g + (r0 + i) * ldg + c, gv[i][k]);
+                    load4(z + (r0 + i) * ldz + c, zz[i][k]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) gv[i][k][j] = zz[i][k][j] = 0.f;
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i) {
+            const int64_t r = r0 + i;
+            if (r >= rows) break;
+            const float mean = mean_in[r], rstd = rstd_in[r];
+            float xh[STEPS][4], dxh[STEPS][4];
+            float sa = 0.f, sb = 0.f;
+#pragma unroll
+            for (int k = 0; k < STEPS; ++k) {
+                const int c = 256 * k + 4 * lane;
                 Philox4 u{{0u, 0u, 0u, 0u}};
-                if (p > 0.f) u = philox4(seed, (uint64_t)r, (uint32_t)(c >> 2));
+                if (p > 0.f && c < dim) u = philox4(seed, (uint64_t)r, (uint32_t)(c >> 2));
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    float x = zz[k][j];
+                    float x = zz[i][k][j];
                     if (act == 1) x = x < 0.f ? 0.f : x;
-                    xh[k][j] = (x - mean) * rstd;
-                    float g1 = gv[j];
+                    xh[k][j] = c < dim ? (x - mean) * rstd : 0.f;
+                    float g1 = gv[i][k][j];
                     if (p > 0.f) g1 = u.w[j] >= thr ? g1 * scale : 0.f;
                     ag[k][j] += g1 * xh[k][j];
                     ab[k][j] += g1;
-                    dxh[k][j] = g1 * gamma[c + j];
+                    dxh[k][j] = g1 * gm[k][j];
                     sa += dxh[k][j];
                     sb += dxh[k][j] * xh[k][j];
                 }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) xh[k][j] = dxh[k][j] = zz[k][j] = 0.f;
             }
-        }
-        const float a = wave_sum(sa) / (float)dim;
-        const float b = wave_sum(sb) / (float)dim;
+            const float a = wave_sum(sa) / (float)dim;
+            const float b = wave_sum(sb) / (float)dim;
 #pragma unroll
-        for (int k = 0; k < kMaxSteps; ++k) {
-            const int c = 256 * k + 4 * lane;
-            if (k < steps && c < dim) {
-                float d[4];
+            for (int k = 0; k < STEPS; ++k) {
+                const int c = 256 * k + 4 * lane;
+                if (c < dim) {
+                    float d[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    d[j] = rstd * (dxh[k][j] - a - xh[k][j] * b);
-                    if (act == 1 && zz[k][j] <= 0.f) d[j] = 0.f;  // threshold_backward on the result
+                    for (int j = 0; j < 4; ++j) {
+                        d[j] = rstd * (dxh[k][j] - a - xh[k][j] * b);
+                        if (act == 1 && zz[i][k][j] <= 0.f) d[j] = 0.f;  // threshold_backward on the result
+                    }
+                    store4(dz + r * lddz + c, d);
                 }
-                store4(dz + r * lddz + c, d);
             }
         }
     }
     // fixed-order reduction of the 4 waves, then one partial row per work-group
 #pragma unroll
-    for (int k = 0; k < kMaxSteps; ++k) {
+    for (int k = 0; k < STEPS; ++k) {
         const int c = 256 * k + 4 * lane;
-        if (k < steps && c < dim) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                red[0][wave][c + j] = ag[k][j];
-                red[1][wave][c + j] = ab[k][j];
-            }
+        for (int j = 0; j < 4; ++j) {
+            red[0][wave][c + j] = ag[k][j];
+            red[1][wave][c + j] = ab[k][j];
         }
     }
     __syncthreads();
@@ -241,12 +270,25 @@ __global__ __launch_bounds__(kBlk) void act_norm_dropout_bwd_kernel(
     }
 }
 
-__global__ void column_sum_kernel(const float* __restrict__ part, int64_t nparts, int dim, float* __restrict__ out) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= dim) return;
+// out[c] = sum over parts of part[k][c]: 16 waves per 64 columns, wave w
+// adding parts w, w+16, ... in order, then the 16 wave sums in order.
+__global__ __launch_bounds__(1024) void column_sum_kernel(const float* __restrict__ part, int64_t nparts, int dim,
+                                                          float* __restrict__ out) {
+    __shared__ float red[16][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + lane;
     float s = 0.f;
-    for (int64_t k = 0; k < nparts; ++k) s += part[k * dim + c];
-    out[c] = s;
+    if (c < dim)
+        for (int64_t k = wave; k < nparts; k += 16) s += part[k * dim + c];
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && c < dim) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) t += red[w][lane];
+        out[c] = t;
+    }
 }
 
 int64_t bwd_blocks(int64_t rows) {
@@ -276,39 +318,58 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float m, int a) {
     return v > m || (v == m && i < a);
 }
 
-// One wave per selected row: lse, the label term, argmax (first index of the
-// maximum, as torch.argmax).  Block partials of (loss, hits, valid rows).
-template <typename T>
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int d = LPR / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
+    return v;
+}
+
+template <int LPR>
+__device__ __forceinline__ double group_sum_d(double v) {
+#pragma unroll
+    for (int d = LPR / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
+    return v;
+}
+
+// LPR lanes per selected row (16 for up to 64 classes: 4 rows per wave;
+// 64 otherwise): lse, the label term, argmax (first index of the maximum,
+// as torch.argmax).  Block partials of (loss, hits, valid rows, bad input).
+template <typename T, int LPR>
 __global__ __launch_bounds__(kBlk) void ce_fwd_kernel(const T* __restrict__ logits, int64_t ld, int64_t total_rows,
                                                       int classes, const int64_t* __restrict__ rows,
                                                       const int64_t* __restrict__ labels, int64_t n,
                                                       float* __restrict__ lse_out, double* __restrict__ part_loss,
                                                       long long* __restrict__ part_cnt) {
+    constexpr int GPW = kWave / LPR;  // rows per wave
     __shared__ double sl[kRowsPerBlock];
     __shared__ long long sc[kRowsPerBlock], sv[kRowsPerBlock], sbad[kRowsPerBlock];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    const int sub = lane % LPR;
+    const int grp = lane / LPR;
     double wl = 0.0;
     long long wc = 0, wv = 0, wbad = 0;
-    for (int64_t i = (int64_t)blockIdx.x * kRowsPerBlock + wave; i < n; i += (int64_t)gridDim.x * kRowsPerBlock) {
-        const int64_t row = rows ? rows[i] : i;
-        const int64_t lab = labels[i];
-        if (row < 0 || row >= total_rows) {
-            if (lane == 0) wbad = 1;
-            continue;
-        }
-        const T* x = logits + row * ld;
+    const int64_t stride = (int64_t)gridDim.x * kRowsPerBlock * GPW;
+    for (int64_t i0 = ((int64_t)blockIdx.x * kRowsPerBlock + wave) * GPW; i0 < n; i0 += stride) {
+        const int64_t i = i0 + grp;
+        const bool live = i < n;
+        const int64_t row = live ? (rows ? rows[i] : i) : 0;
+        const int64_t lab = live ? labels[i] : kIgnore;
+        const bool row_ok = live && row >= 0 && row < total_rows;
+        const T* x = logits + (row_ok ? row : 0) * ld;
         float m = -INFINITY;
         int arg = 0x7fffffff;
-        for (int c = lane; c < classes; c += kWave) {
-            const float v = to_float(x[c]);
-            if (argmax_better(v, c, m, arg)) {
-                m = v;
-                arg = c;
+        if (row_ok)
+            for (int c = sub; c < classes; c += LPR) {
+                const float v = to_float(x[c]);
+                if (argmax_better(v, c, m, arg)) {
+                    m = v;
+                    arg = c;
+                }
             }
-        }
 #pragma unroll
-        for (int d = kWave / 2; d > 0; d >>= 1) {
+        for (int d = LPR / 2; d > 0; d >>= 1) {
             const float om = __shfl_xor(m, d, kWave);
             const int oa = __shfl_xor(arg, d, kWave);
             if (argmax_better(om, oa, m, arg)) {
@@ -317,27 +378,37 @@ __global__ __launch_bounds__(kBlk) void ce_fwd_kernel(const T* __restrict__ logi
             }
         }
         float s = 0.f;
-        for (int c = lane; c < classes; c += kWave) s += expf(to_float(x[c]) - m);
-        s = wave_sum(s);
+        if (row_ok)
+            for (int c = sub; c < classes; c += LPR) s += expf(to_float(x[c]) - m);
+        s = group_sum<LPR>(s);
         const float lse = m + logf(s);
-        if (lane == 0) {
-            lse_out[i] = lse;
-            if (lab != kIgnore) {
-                if (lab < 0 || lab >= classes) {
-                    wbad = 1;
-                } else {
-                    wl += (double)(lse - to_float(x[lab]));
-                    wv += 1;
-                    wc += (arg == lab) ? 1 : 0;
+        if (sub == 0 && live) {
+            if (!row_ok) {
+                wbad = 1;
+            } else {
+                lse_out[i] = lse;
+                if (lab != kIgnore) {
+                    if (lab < 0 || lab >= classes) {
+                        wbad = 1;
+                    } else {
+                        wl += (double)(lse - to_float(x[lab]));
+                        wv += 1;
+                        wc += (arg == lab) ? 1 : 0;
+                    }
                 }
             }
         }
     }
+    // the group leaders' sums, added over the wave (fixed order of the xor tree)
+    wl = group_sum_d<kWave>(wl);
+    wc = (long long)group_sum_d<kWave>((double)wc);
+    wv = (long long)group_sum_d<kWave>((double)wv);
+    wbad = (long long)group_sum_d<kWave>((double)wbad);
     if (lane == 0) {
         sl[wave] = wl;
         sc[wave] = wc;
         sv[wave] = wv;
-        sbad[wave] = wbad;
+        sbad[wave] = wbad ? 1 : 0;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -357,17 +428,35 @@ __global__ __launch_bounds__(kBlk) void ce_fwd_kernel(const T* __restrict__ logi
 }
 
 // loss = sum / valid (NaN when no row counts or a label is out of range:
-// torch asserts there), correct = hits, valid = counted rows.
-__global__ void ce_finish_kernel(const double* __restrict__ part_loss, const long long* __restrict__ part_cnt,
-                                 int64_t nparts, float* __restrict__ loss, int64_t* __restrict__ counts) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// torch asserts there), correct = hits, valid = counted rows.  One
+// work-group: thread t adds parts t, t+256, ... in order, then thread 0 the
+// 256 sums in order (deterministic).
+__global__ __launch_bounds__(256) void ce_finish_kernel(const double* __restrict__ part_loss,
+                                                        const long long* __restrict__ part_cnt, int64_t nparts,
+                                                        float* __restrict__ loss, int64_t* __restrict__ counts) {
+    __shared__ double sl[256];
+    __shared__ long long sc[256], sv[256], sb[256];
     double L = 0.0;
     long long C = 0, V = 0, B = 0;
-    for (int64_t k = 0; k < nparts; ++k) {
+    for (int64_t k = threadIdx.x; k < nparts; k += 256) {
         L += part_loss[k];
         C += part_cnt[3 * k];
         V += part_cnt[3 * k + 1];
         B |= part_cnt[3 * k + 2];
+    }
+    sl[threadIdx.x] = L;
+    sc[threadIdx.x] = C;
+    sv[threadIdx.x] = V;
+    sb[threadIdx.x] = B;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    L = 0.0;
+    C = V = B = 0;
+    for (int t = 0; t < 256; ++t) {
+        L += sl[t];
+        C += sc[t];
+        V += sv[t];
+        B |= sb[t];
     }
     loss[0] = (B || V == 0) ? __int_as_float(0x7fc00000) : (float)(L / (double)V);
     counts[0] = C;
@@ -377,24 +466,27 @@ __global__ void ce_finish_kernel(const double* __restrict__ part_loss, const lon
 
 // grad[row][c] = (softmax - onehot) * dloss / valid for counted rows, 0 for
 // ignored ones; other rows of grad are left alone (the caller zero-fills).
-template <typename T, typename GT>
+template <typename T, typename GT, int LPR>
 __global__ __launch_bounds__(kBlk) void ce_bwd_kernel(const T* __restrict__ logits, int64_t ld, int64_t total_rows,
                                                       int classes, const int64_t* __restrict__ rows,
                                                       const int64_t* __restrict__ labels, int64_t n,
                                                       const float* __restrict__ lse, const float* __restrict__ dloss,
                                                       const int64_t* __restrict__ counts, GT* __restrict__ grad,
                                                       int64_t ldg) {
+    constexpr int GPW = kWave / LPR;
     const int lane = threadIdx.x & 63;
+    const int sub = lane % LPR;
     const int64_t valid = counts[1];
     const float scale = valid > 0 ? dloss[0] / (float)valid : 0.f;
-    for (int64_t i = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6); i < n;
-         i += (int64_t)gridDim.x * kRowsPerBlock) {
+    const int64_t stride = (int64_t)gridDim.x * kRowsPerBlock * GPW;
+    for (int64_t i = ((int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) * GPW + lane / LPR; i < n;
+         i += stride) {
         const int64_t row = rows ? rows[i] : i;
         if (row < 0 || row >= total_rows) continue;
         const int64_t lab = labels[i];
         const bool counted = lab != kIgnore && lab >= 0 && lab < classes;
         const float l = lse[i];
-        for (int c = lane; c < classes; c += kWave) {
+        for (int c = sub; c < classes; c += LPR) {
             float v = 0.f;
             if (counted) v = (expf(to_float(logits[row * ld + c]) - l) - (c == lab ? 1.f : 0.f)) * scale;
             grad[row * ldg + c] = from_float<GT>(v);
@@ -464,14 +556,24 @@ extern "C" int grws_act_norm_dropout_fwd(const void* z, int32_t z_dtype, int64_t
     if (rows == 0) return GRWS_OK;
     GRWS_CHECK_ARG(z && out && gamma && beta, "act_norm_dropout: null pointer");
     GRWS_TRY(check_rowwise(z_dtype, out_dtype, rows, dim, ldz, ldo, z, out));
-    int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    const int steps = (int)((dim + 255) / 256);
+    const int rpw = steps == 1 ? 4 : (steps == 2 ? 2 : 1);  // rows in flight per wave
+    int64_t blocks = (rows + kRowsPerBlock * rpw - 1) / (kRowsPerBlock * rpw);
     if (blocks > 65536) blocks = 65536;
-#define GRWS_ANDF(ZT, OT)                                                                                     \
-    hipLaunchKernelGGL((act_norm_dropout_fwd_kernel<ZT, OT>), dim3((unsigned)blocks), dim3(kBlk), 0, stream,  \
-                       static_cast<const ZT*>(z), ldz, rows, (int)dim, (int)act, gamma, beta, eps, p, seed,    \
+#define GRWS_ANDF_SR(ZT, OT, S, R)                                                                              \
+    hipLaunchKernelGGL((act_norm_dropout_fwd_kernel<ZT, OT, S, R>), dim3((unsigned)blocks), dim3(kBlk), 0, stream, \
+                       static_cast<const ZT*>(z), ldz, rows, (int)dim, (int)act, gamma, beta, eps, p, seed,       \
                        static_cast<OT*>(out), ldo, mean, rstd)
+#define GRWS_ANDF(ZT, OT)                              \
+    do {                                               \
+        if (steps == 1) GRWS_ANDF_SR(ZT, OT, 1, 4);    \
+        else if (steps == 2) GRWS_ANDF_SR(ZT, OT, 2, 2); \
+        else if (steps == 3) GRWS_ANDF_SR(ZT, OT, 3, 1); \
+        else GRWS_ANDF_SR(ZT, OT, 4, 1);               \
+    } while (0)
     GRWS_DISPATCH2(z_dtype, out_dtype, GRWS_ANDF);
 #undef GRWS_ANDF
+#undef GRWS_ANDF_SR
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }
@@ -502,17 +604,26 @@ extern "C" int grws_act_norm_dropout_bwd(const void* dout, int32_t dout_dtype, i
     float* pb = cv.take<float>((size_t)blocks * (size_t)dim);
     if (!cv.ok)
         return set_error(GRWS_E_CAPACITY, "act_norm_dropout: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
-#define GRWS_ANDB(GT, ZT)                                                                                     \
-    hipLaunchKernelGGL((act_norm_dropout_bwd_kernel<GT, ZT>), dim3((unsigned)blocks), dim3(kBlk), 0, stream,  \
-                       static_cast<const GT*>(dout), ldg, static_cast<const ZT*>(z), ldz, rows, (int)dim,      \
+    const int steps = (int)((dim + 255) / 256);
+#define GRWS_ANDB_SR(GT, ZT, S, R)                                                                              \
+    hipLaunchKernelGGL((act_norm_dropout_bwd_kernel<GT, ZT, S, R>), dim3((unsigned)blocks), dim3(kBlk), 0, stream, \
+                       static_cast<const GT*>(dout), ldg, static_cast<const ZT*>(z), ldz, rows, (int)dim,          \
                        (int)act, mean, rstd, gamma, p, seed, static_cast<ZT*>(dz), lddz, pg, pb)
+#define GRWS_ANDB(GT, ZT)                              \
+    do {                                               \
+        if (steps == 1) GRWS_ANDB_SR(GT, ZT, 1, 4);    \
+        else if (steps == 2) GRWS_ANDB_SR(GT, ZT, 2, 2); \
+        else if (steps == 3) GRWS_ANDB_SR(GT, ZT, 3, 1); \
+        else GRWS_ANDB_SR(GT, ZT, 4, 1);               \
+    } while (0)
     GRWS_DISPATCH2(dout_dtype, z_dtype, GRWS_ANDB);
 #undef GRWS_ANDB
+#undef GRWS_ANDB_SR
     GRWS_LAUNCH_CHECK();
-    const unsigned cb = (unsigned)((dim + 255) / 256);
-    hipLaunchKernelGGL(column_sum_kernel, dim3(cb), dim3(256), 0, stream, pg, blocks, (int)dim, dgamma);
+    const unsigned cb = (unsigned)((dim + 63) / 64);
+    hipLaunchKernelGGL(column_sum_kernel, dim3(cb), dim3(1024), 0, stream, pg, blocks, (int)dim, dgamma);
     GRWS_LAUNCH_CHECK();
-    hipLaunchKernelGGL(column_sum_kernel, dim3(cb), dim3(256), 0, stream, pb, blocks, (int)dim, dbeta);
+    hipLaunchKernelGGL(column_sum_kernel, dim3(cb), dim3(1024), 0, stream, pb, blocks, (int)dim, dbeta);
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }
@@ -543,15 +654,22 @@ extern "C" int grws_cross_entropy_fwd(const void* logits, int32_t dtype, int64_t
     long long* pc = cv.take<long long>(3 * (size_t)blocks);
     if (!cv.ok)
         return set_error(GRWS_E_CAPACITY, "cross_entropy: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
-#define GRWS_CEF(T)                                                                                            \
-    hipLaunchKernelGGL(ce_fwd_kernel<T>, dim3((unsigned)blocks), dim3(kBlk), 0, stream,                        \
+    const bool narrow = classes <= 64;
+#define GRWS_CEF_L(T, L)                                                                                       \
+    hipLaunchKernelGGL((ce_fwd_kernel<T, L>), dim3((unsigned)blocks), dim3(kBlk), 0, stream,                   \
                        static_cast<const T*>(logits), ld, total_rows, (int)classes, rows, labels, n, lse_out, pl, pc)
+#define GRWS_CEF(T)                                \
+    do {                                           \
+        if (narrow) GRWS_CEF_L(T, 16);             \
+        else GRWS_CEF_L(T, 64);                    \
+    } while (0)
     if (dtype == GRWS_F32) GRWS_CEF(float);
     else if (dtype == GRWS_F16) GRWS_CEF(_Float16);
     else GRWS_CEF(__hip_bfloat16);
 #undef GRWS_CEF
+#undef GRWS_CEF_L
     GRWS_LAUNCH_CHECK();
-    hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(64), 0, stream, pl, pc, blocks, loss_out, counts_out);
+    hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(256), 0, stream, pl, pc, blocks, loss_out, counts_out);
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }
@@ -571,12 +689,19 @@ extern "C" int grws_cross_entropy_bwd(const void* logits, int32_t dtype, int64_t
     if (n == 0) return GRWS_OK;
     GRWS_CHECK_ARG(logits && labels && lse && dloss && counts && grad, "cross_entropy: null pointer");
     const int64_t blocks = ce_blocks(n);
-#define GRWS_CEB(T, GT)                                                                                        \
-    hipLaunchKernelGGL((ce_bwd_kernel<T, GT>), dim3((unsigned)blocks), dim3(kBlk), 0, stream,                  \
+    const bool narrow = classes <= 64;
+#define GRWS_CEB_L(T, GT, L)                                                                                   \
+    hipLaunchKernelGGL((ce_bwd_kernel<T, GT, L>), dim3((unsigned)blocks), dim3(kBlk), 0, stream,               \
                        static_cast<const T*>(logits), ld, total_rows, (int)classes, rows, labels, n, lse, dloss,  \
                        counts, static_cast<GT*>(grad), ldg)
+#define GRWS_CEB(T, GT)                            \
+    do {                                           \
+        if (narrow) GRWS_CEB_L(T, GT, 16);         \
+        else GRWS_CEB_L(T, GT, 64);                \
+    } while (0)
     GRWS_DISPATCH2(dtype, grad_dtype, GRWS_CEB);
 #undef GRWS_CEB
+#undef GRWS_CEB_L
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }

@@ -7,6 +7,10 @@ Same classes, signatures and arithmetic as the reference:
 The SpMM runs on the gfx950 kernel (H1); A^T dH runs the same kernel over the
 cached device-built transpose of A instead of the reference's atomic scatter.
 A (X W) may be associated as (A X) W when that gathers fewer columns.
+BCSRGraphConv runs as one autograd node (_GraphConvFunction): the self
+product is added by a beta=1 GEMM, and a target that is a prefix of X gets
+its gradient added into dX in place.  BCSRSPMMFunction keeps the reference's
+A (X W) node for callers that use it directly.
 """
 from __future__ import annotations
 
@@ -115,24 +119,85 @@ class BCSRSPMMFunction(Function):
         return None, grad_features, grad_weight, None
 
 
-class _SelfLinear(Function):
-    """x @ W for the self path (layer.py:171-175) with the weight gradient on
-    the split-K kernel; the same arithmetic as torch.matmul under autocast."""
+def _is_prefix_view(t: torch.Tensor, base: torch.Tensor) -> bool:
+    """Whether t is base[:t.shape[0]] (same storage, offset and strides)."""
+    return (t.dim() == 2 and base.dim() == 2 and t.shape[1] == base.shape[1] and t.shape[0] <= base.shape[0]
+            and t.untyped_storage().data_ptr() == base.untyped_storage().data_ptr()
+            and t.storage_offset() == base.storage_offset() and t.stride() == base.stride())
+
+
+class _GraphConvFunction(Function):
+    """out[T] = A (X W_n) [:T] + X_tgt W_s (layer.py:118-191) as one autograd
+    node.  The self product is added into the SpMM output by a beta=1 GEMM
+    instead of a separate add; when X_tgt is a prefix of X (the full-graph
+    and node-wise block cases) its gradient is added into dX in place, and
+    the backward SpMM reads the T gradient rows directly (rows of A beyond T
+    contribute nothing), so no padded gradient is materialised.  The product
+    is associated as A (X W_n) or (A X) W_n by _aggregate_first."""
 
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
-    def forward(ctx, x, weight):
+    def forward(ctx, graph, x, x_tgt, w_n, w_s, prefix_rows):
         xh = _autocast_operand(x)
-        ctx.save_for_backward(xh, weight)
-        return torch.matmul(xh, weight)
+        if x_tgt is None:
+            xt = xh[:prefix_rows]
+        else:
+            xt = _autocast_operand(x_tgt)
+        T = xt.shape[0]
+        ctx.graph = graph
+        ctx.num_input_nodes = x.shape[0]
+        ctx.prefix = x_tgt is None
+        ctx.agg_first = _aggregate_first(w_n.shape[0], w_n.shape[1], x.requires_grad)
+
+        def rows_T(y):
+            if y.shape[0] >= T:
+                return y[:T]
+            return F.pad(y, (0, 0, 0, T - y.shape[0]))
+
+        if ctx.agg_first:
+            y, ms = _spmm_timed(graph, xh)
+            yt = rows_T(y)
+            out = torch.addmm(torch.matmul(xt, w_s), yt, w_n)
+            ctx.save_for_backward(yt, xt, w_n, w_s)
+        else:
+            y, ms = _spmm_timed(graph, torch.matmul(xh, w_n))
+            yt = rows_T(y)
+            out = torch.addmm(yt, xt, w_s)
+            ctx.save_for_backward(xh, xt, w_n, w_s)
+        record_spmm_time(ms)
+        return out
 
     @staticmethod
     @torch.amp.custom_bwd(device_type="cuda")
     def backward(ctx, grad):
-        xh, weight = ctx.saved_tensors
-        gx = torch.matmul(grad, weight.t()) if ctx.needs_input_grad[0] else None
-        gw = _weight_grad(xh, grad.contiguous()) if ctx.needs_input_grad[1] else None
-        return gx, gw
+        saved, xt, w_n, w_s = ctx.saved_tensors
+        graph = ctx.graph
+        g = grad.contiguous()
+        need_x, need_xt, need_wn, need_ws = (ctx.needs_input_grad[1], ctx.needs_input_grad[2],
+                                             ctx.needs_input_grad[3], ctx.needs_input_grad[4])
+        dx = dxt = dwn = dws = None
+        if need_ws:
+            dws = _weight_grad(xt, g)
+        if ctx.agg_first:
+            # out = (A X)[:T] W_n + X_tgt W_s
+            if need_wn:
+                dwn = _weight_grad(saved, g)
+            if need_x:
+                dx = graph.spmm_transpose(torch.matmul(g, w_n.t()).contiguous(), ctx.num_input_nodes)
+        else:
+            g_agg = graph.spmm_transpose(g, ctx.num_input_nodes)
+            if need_wn:
+                dwn = _weight_grad(saved, g_agg)
+            if need_x:
+                dx = torch.matmul(g_agg, w_n.t())
+        if ctx.prefix:
+            if need_x:
+                if not dx.is_contiguous():
+                    dx = dx.contiguous()
+                dx[: g.shape[0]].addmm_(g, w_s.t().to(g.dtype))
+        elif need_xt:
+            dxt = torch.matmul(g, w_s.t())
+        return None, dx, dxt, dwn, dws, None
 
 
 class BCSRGraphConv(nn.Module):
@@ -161,17 +226,16 @@ class BCSRGraphConv(nn.Module):
 
     def forward(self, graph, features: torch.Tensor,
                 features_target: torch.Tensor = None) -> torch.Tensor:
-        h_neigh = BCSRSPMMFunction.apply(graph, features, self.weight_neigh, self.warps_per_block)
-        target_rows = h_neigh.shape[0]
-        if features_target is not None:
-            h_in_self = features_target
-        elif features.shape[0] >= target_rows:
-            h_in_self = features[:target_rows]
-        else:
-            h_in_self = F.pad(features, (0, 0, 0, target_rows - features.shape[0]))
-        h_self = _SelfLinear.apply(h_in_self, self.weight_self)
-        if h_neigh.shape[0] > h_self.shape[0]:
-            h_neigh = h_neigh[:h_self.shape[0]]
-        elif h_neigh.shape[0] < h_self.shape[0]:
-            h_neigh = F.pad(h_neigh, (0, 0, 0, h_self.shape[0] - h_neigh.shape[0]))
-        return h_neigh + h_self
+        """A (X W_neigh) + X_target W_self, trimmed or zero-padded to the
+        target rows (layer.py:118-191): features_target, or the graph's 16W
+        rows (features sliced or zero-padded to them) when it is None."""
+        target_rows = 16 * graph.num_windows
+        if features_target is None:
+            if features.shape[0] >= target_rows:
+                features_target = features[:target_rows]
+            else:
+                features_target = F.pad(features, (0, 0, 0, target_rows - features.shape[0]))
+        if _is_prefix_view(features_target, features):
+            return _GraphConvFunction.apply(graph, features, None, self.weight_neigh, self.weight_self,
+                                            features_target.shape[0])
+        return _GraphConvFunction.apply(graph, features, features_target, self.weight_neigh, self.weight_self, 0)
