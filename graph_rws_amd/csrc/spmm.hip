@@ -98,6 +98,7 @@ struct SpmmArgs {
     float* partials;
     int32_t nchunks;
     uint32_t x_bytes;  // buffer path: readable bytes of x (last row: n_cols elements)
+    int64_t col_base;  // first output column of chunk 0 (a launch may cover part of N)
 };
 
 // Output conversion for the three element types.
@@ -210,6 +211,7 @@ __global__ __launch_bounds__(64 * WPB) void spmm_fwd_kernel(SpmmArgs a) {
     // of one chunk, so a window range's X rows (one chunk wide) stay in L2
     const int64_t item = logical % a.num_items;
     const int chunk = (int)(logical / a.num_items);
+    const int64_t col_base = a.col_base;
 
     int64_t w, sb, se;
     int slot;
@@ -235,7 +237,7 @@ __global__ __launch_bounds__(64 * WPB) void spmm_fwd_kernel(SpmmArgs a) {
     if (se > nslabs) se = nslabs;
     if (sb > se) sb = se;
 
-    const int64_t n0 = (int64_t)chunk * NC;
+    const int64_t n0 = col_base + (int64_t)chunk * NC;
     const int64_t N = a.n_cols;
     const uint32_t xr = (uint32_t)a.x_rows;
     const S* __restrict__ X = static_cast<const S*>(a.x);
@@ -446,6 +448,7 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
     if (logical >= total) return;  // uniform over the work-group
     const int64_t item = logical % a.num_items;
     const int chunk = (int)(logical / a.num_items);
+    const int64_t col_base = a.col_base;
 
     int64_t w, sb, se;
     int slot;
@@ -469,7 +472,7 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
     const int64_t nslabs = (nslots + 15) >> 4;
     if (se > nslabs) se = nslabs;
     if (sb > se) sb = se;
-    const int64_t n0 = (int64_t)chunk * NC;
+    const int64_t n0 = col_base + (int64_t)chunk * NC;
 
     // one resource per work item for A and the column indices, starting at
     // slab sb; reads beyond the window return zero
@@ -618,7 +621,7 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
 template <int XT, int NBLK>
 __global__ __launch_bounds__(256) void spmm_fixup_kernel(const int32_t* __restrict__ split, int64_t num_split,
                                                          const float* __restrict__ partials, int32_t nchunks,
-                                                         void* y, int64_t ldy, int64_t N) {
+                                                         void* y, int64_t ldy, int64_t N, int64_t col_base) {
     constexpr int NC = NBLK * 16;
     const int64_t si = blockIdx.x / nchunks;
     const int chunk = (int)(blockIdx.x % nchunks);
@@ -626,7 +629,7 @@ __global__ __launch_bounds__(256) void spmm_fixup_kernel(const int32_t* __restri
     const int64_t w = split[3 * si];
     const int64_t first = split[3 * si + 1];
     const int cnt = split[3 * si + 2];
-    const int64_t n0 = (int64_t)chunk * NC;
+    const int64_t n0 = col_base + (int64_t)chunk * NC;
     for (int e = threadIdx.x; e < 16 * NC; e += 256) {
         const int r = e / NC, c = e % NC;
         if (n0 + c >= N) continue;
@@ -800,23 +803,23 @@ int launch_fixup(const grws_spmm_plan* plan, const SpmmArgs& a, int nblk, hipStr
     switch (nblk) {
         case 1:
             hipLaunchKernelGGL((spmm_fixup_kernel<XT, 1>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
-                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols);
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
             break;
         case 2:
             hipLaunchKernelGGL((spmm_fixup_kernel<XT, 2>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
-                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols);
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
             break;
         case 4:
             hipLaunchKernelGGL((spmm_fixup_kernel<XT, 4>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
-                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols);
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
             break;
         case 16:
             hipLaunchKernelGGL((spmm_fixup_kernel<XT, 16>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
-                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols);
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
             break;
         default:
             hipLaunchKernelGGL((spmm_fixup_kernel<XT, 8>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
-                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols);
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
             break;
     }
     GRWS_LAUNCH_CHECK();
@@ -983,12 +986,32 @@ extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const v
     int st;
     if (use_buf) {
         a.x_bytes = (uint32_t)((x_rows - 1) * ldx * (int64_t)esz + n_cols * (int64_t)esz);
-        if (x_dtype == GRWS_F16)
-            st = af32 ? dispatch_buf_tc<GRWS_F16, true>(a, tc, nblk, stream)
-                      : dispatch_buf_tc<GRWS_F16, false>(a, tc, nblk, stream);
-        else
-            st = af32 ? dispatch_buf_tc<GRWS_BF16, true>(a, tc, nblk, stream)
-                      : dispatch_buf_tc<GRWS_BF16, false>(a, tc, nblk, stream);
+        // N above 256 and not a multiple of it: 256-column chunks over the
+        // whole multiples, then one narrower launch for the rest, so A is
+        // streamed once per 256 columns and no chunk is mostly empty
+        const bool forced = getenv("GRWS_SPMM_NBLK") != nullptr;
+        const int64_t head = (!forced && n_cols > 256 && n_cols % 256 != 0) ? n_cols / 256 * 256 : 0;
+        const int64_t parts[2][2] = {{0, head > 0 ? head : n_cols}, {head, n_cols}};
+        for (int pi = 0; pi < (head > 0 ? 2 : 1); ++pi) {
+            const int64_t c0 = parts[pi][0], c1 = parts[pi][1];
+            const int pnblk = head > 0 ? (pi == 0 ? 16 : nblk_for(c1 - c0, x_dtype, false)) : nblk;
+            const int64_t pnc = pnblk * 16;
+            a.col_base = c0;
+            a.nchunks = (int32_t)((c1 - c0 + pnc - 1) / pnc);
+            if (x_dtype == GRWS_F16)
+                st = af32 ? dispatch_buf_tc<GRWS_F16, true>(a, tc, pnblk, stream)
+                          : dispatch_buf_tc<GRWS_F16, false>(a, tc, pnblk, stream);
+            else
+                st = af32 ? dispatch_buf_tc<GRWS_BF16, true>(a, tc, pnblk, stream)
+                          : dispatch_buf_tc<GRWS_BF16, false>(a, tc, pnblk, stream);
+            if (st != GRWS_OK) return st;
+            if (plan && plan->num_split > 0) {
+                st = x_dtype == GRWS_F16 ? launch_fixup<GRWS_F16>(plan, a, pnblk, stream)
+                                         : launch_fixup<GRWS_BF16>(plan, a, pnblk, stream);
+                if (st != GRWS_OK) return st;
+            }
+        }
+        return GRWS_OK;
     } else switch (x_dtype) {
         case GRWS_F32: st = dispatch_tc<GRWS_F32, true>(a, tc, nblk, vect, stream); break;
         case GRWS_F16:

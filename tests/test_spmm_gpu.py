@@ -183,3 +183,24 @@ def test_spmm_ragged_width_row_padding(cuda_device, xdt):
     _check(G, X.contiguous(), Y, xdt)
     _check(G, X.contiguous(), Yo, xdt)
     assert torch.equal(Y, Yc)
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N", [300, 608, 520])
+@pytest.mark.parametrize("slabs", [None, 2])
+def test_spmm_wide_split_launches(cuda_device, xdt, N, slabs):
+    """Widths above 256 that are not multiples of it run as 256-column
+    chunks plus a narrower launch for the rest (and, with split windows,
+    two partial fixups at different column offsets)."""
+    print(f"case wide xdt={xdt} N={N} slabs={slabs}", flush=True)
+    g = synth.chung_lu(2500, 40000, 2.1, seed=N)
+    G = _bcsr(g, 16, cuda_device, vdt=xdt)
+    X = synth.features(g.num_nodes, N, seed=N + 1, device=cuda_device).to(xdt)
+    if slabs is None:
+        Y = G.spmm(X)
+    else:
+        plan = core.build_spmm_plan(G.window_offset, G.num_tiles, 16, slabs)
+        assert plan.num_split > 0
+        Y = core.spmm(G.window_offset, G.original_col_indices, G.values_condensed, X, 16, plan=plan)
+    torch.cuda.synchronize()
+    _check(G, X, Y, xdt)
