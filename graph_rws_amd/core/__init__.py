@@ -5,6 +5,8 @@ reference, a missing library is an error, not a silent `None`.
 """
 from ._lib import load as _load  # noqa: F401
 from .ops import (  # noqa: F401
+    PackedTiles,
+    pack_tiles,
     SpmmPlan,
     build_spmm_plan,
     csr_to_bcsr_cpu,
@@ -39,6 +41,8 @@ __all__ = [
     "spmm",
     "build_spmm_plan",
     "SpmmPlan",
+    "PackedTiles",
+    "pack_tiles",
     "sample_hop",
     "relabel",
     "sample_all_layers",

@@ -17,6 +17,7 @@ LIB_PATH = os.environ.get("GRWS_LIB", os.path.join(_PKG, "libgrws.so"))
 
 GRWS_F32, GRWS_F16, GRWS_BF16 = 0, 1, 2
 GRWS_OK = 0
+GRWS_E_INVALID, GRWS_E_DTYPE, GRWS_E_CAPACITY, GRWS_E_HIP, GRWS_E_RANGE = -1, -2, -3, -4, -5
 
 _c_i64p = ctypes.POINTER(ctypes.c_int64)
 _vp = ctypes.c_void_p
@@ -28,6 +29,11 @@ class BcsrView(ctypes.Structure):
                 ("num_windows", ctypes.c_int64), ("num_tiles", ctypes.c_int64),
                 ("tile_rows", ctypes.c_int32), ("tile_cols", ctypes.c_int32),
                 ("values_dtype", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+class PackedTilesView(ctypes.Structure):
+    """grws_packed_tiles (include/grws.h)."""
+    _fields_ = [("header", _vp), ("values", _vp), ("num_values", ctypes.c_int64)]
 
 
 class SpmmPlanView(ctypes.Structure):
@@ -63,6 +69,15 @@ _PROTOS = {
     "grws_spmm": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.POINTER(SpmmPlanView), _vp,
                                  ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
                                  _vp, ctypes.c_int32, ctypes.c_int64, _vp, ctypes.c_size_t, _vp]),
+    "grws_spmm_packed": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.POINTER(PackedTilesView),
+                                        ctypes.POINTER(SpmmPlanView), _vp, ctypes.c_int32, ctypes.c_int64,
+                                        ctypes.c_int64, ctypes.c_int64, _vp, ctypes.c_int32, ctypes.c_int64,
+                                        _vp, ctypes.c_size_t, _vp]),
+    "grws_pack_tiles_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "grws_pack_tiles_count": (ctypes.c_int, [ctypes.POINTER(BcsrView), _vp, ctypes.c_size_t,
+                                             ctypes.POINTER(ctypes.c_int64), _vp]),
+    "grws_pack_tiles_fill": (ctypes.c_int, [ctypes.POINTER(BcsrView), _vp, _vp, ctypes.c_int64, _vp,
+                                            ctypes.c_size_t, _vp]),
     "grws_csr_to_bcsr_host_count": (ctypes.c_int, [ctypes.c_int64, _vp, _vp, ctypes.c_int32,
                                                    ctypes.c_int32, _vp, _c_i64p, ctypes.c_int32]),
     "grws_csr_to_bcsr_host_fill": (ctypes.c_int, [ctypes.c_int64, _vp, _vp, _vp, ctypes.c_int32,

@@ -20,6 +20,10 @@ from . import _lib as L
 # no synchronisation happens.  Set to True to time each call with events.
 TIMING = False
 
+# Graphs multiplied more than once read their values from packed tiles
+# (BCSRGraph.packed_tiles); False keeps every SpMM on the dense tiles.
+PACK_TILES = True
+
 
 # ---------------------------------------------------------------------------
 # SpMM plan
@@ -110,6 +114,61 @@ def _widen(t: torch.Tensor, vec: int) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
+# packed tiles
+# ---------------------------------------------------------------------------
+class PackedTiles:
+    """Compact copy of a 16x16-tile graph's values (grws_packed_tiles in
+    include/grws.h): per tile 4 row groups of {mask_lo, mask_hi, start} and
+    the nonzero values.  grws_spmm_packed reads it instead of the dense
+    tiles and returns the same bits."""
+
+    def __init__(self, header: torch.Tensor, values: torch.Tensor, num_values: int):
+        self.header = header
+        self.values = values
+        self.num_values = int(num_values)
+
+    def view(self) -> L.PackedTilesView:
+        return L.PackedTilesView(L.ptr(self.header), L.ptr(self.values), self.num_values)
+
+    def nbytes(self) -> int:
+        return self.header.numel() * 4 + self.values.numel() * self.values.element_size()
+
+
+def pack_tiles_supported(col_indices: torch.Tensor, values: torch.Tensor, tile_cols: int) -> bool:
+    return (tile_cols == 16 and values.dtype in (torch.float16, torch.bfloat16) and values.is_cuda
+            and values.is_contiguous() and values.data_ptr() % 8 == 0)
+
+
+def pack_tiles(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.Tensor,
+               tile_cols: int) -> Optional[PackedTiles]:
+    """Builds the packed tiles on the device (one stream sync), or returns
+    None when the graph cannot be packed (tile shape, dtype, or more than
+    2^30 - 16 nonzero values)."""
+    if not pack_tiles_supported(col_indices, values, tile_cols):
+        return None
+    _check_graph(window_offset, col_indices, values, tile_cols)
+    lib = L.load()
+    dev = values.device
+    W = window_offset.numel() - 1
+    T = col_indices.numel() // tile_cols
+    view = L.BcsrView(L.ptr(window_offset), L.ptr(col_indices), L.ptr(values), W, T, 16, tile_cols,
+                      L.dtype_code(values.dtype), 0)
+    wsb = int(lib.grws_pack_tiles_workspace_bytes(T))
+    ws = torch.empty(max(1, wsb), dtype=torch.uint8, device=dev)
+    nv = ctypes.c_int64()
+    st = lib.grws_pack_tiles_count(ctypes.byref(view), L.ptr(ws), wsb, ctypes.byref(nv), L.stream_of(dev))
+    if st == L.GRWS_E_CAPACITY:
+        return None
+    L.check("grws_pack_tiles_count", st)
+    header = torch.empty(max(1, T * 12), dtype=torch.int32, device=dev)
+    # 8 elements of padding the SpMM may read past the last value
+    pvals = torch.zeros(nv.value + 8, dtype=values.dtype, device=dev)
+    L.call("grws_pack_tiles_fill", ctypes.byref(view), L.ptr(header), L.ptr(pvals), nv.value, L.ptr(ws), wsb,
+           L.stream_of(dev))
+    return PackedTiles(header, pvals, nv.value)
+
+
+# ---------------------------------------------------------------------------
 # SpMM forward
 # ---------------------------------------------------------------------------
 def _check_graph(window_offset, col_indices, values, tile_cols):
@@ -129,9 +188,10 @@ def _check_graph(window_offset, col_indices, values, tile_cols):
 
 def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.Tensor,
          x: torch.Tensor, tile_cols: int, plan: Optional[SpmmPlan] = None,
-         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+         out: Optional[torch.Tensor] = None, packed: Optional[PackedTiles] = None) -> torch.Tensor:
     """Y[16W, N] = A X on the device (H1 kernel).  x: [x_rows, N] (row stride
-    may exceed N); out dtype = x dtype."""
+    may exceed N); out dtype = x dtype.  packed: the graph's packed tiles
+    (read instead of the dense values when x has the values' dtype)."""
     _check_graph(window_offset, col_indices, values, tile_cols)
     if not x.is_cuda:
         raise RuntimeError("input_B must be a CUDA tensor")
@@ -149,7 +209,7 @@ def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.T
         # Run on X widened to the next multiple and hand back the first N
         # columns of the result (columns are independent).
         x = _widen(x, vec)
-        full = spmm(window_offset, col_indices, values, x, tile_cols, plan=plan)
+        full = spmm(window_offset, col_indices, values, x, tile_cols, plan=plan, packed=packed)
         return full[:, :N]
     if out is None:
         out = torch.empty((W * 16, N), dtype=x.dtype, device=x.device)
@@ -167,10 +227,36 @@ def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.T
         wsb = int(L.load().grws_spmm_workspace_bytes(ctypes.byref(pv), N))
         if wsb:
             ws = torch.empty(wsb, dtype=torch.uint8, device=x.device)
+    if packed is not None and x.dtype == values.dtype:
+        pk = packed.view()
+        L.call("grws_spmm_packed", ctypes.byref(view), ctypes.byref(pk),
+               ctypes.byref(pv) if pv is not None else None,
+               L.ptr(x), L.dtype_code(x.dtype), x.shape[0], x.stride(0), N, L.ptr(out),
+               L.dtype_code(out.dtype), out.stride(0), L.ptr(ws), wsb, L.stream_of(x.device))
+        return out
     L.call("grws_spmm", ctypes.byref(view), ctypes.byref(pv) if pv is not None else None,
            L.ptr(x), L.dtype_code(x.dtype), x.shape[0], x.stride(0), N, L.ptr(out),
            L.dtype_code(out.dtype), out.stride(0), L.ptr(ws), wsb, L.stream_of(x.device))
     return out
+
+
+def _cached_packed(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.Tensor,
+                   tile_cols: int) -> Optional[PackedTiles]:
+    """Packed tiles for raw-tensor calls, with BCSRGraph.packed_tiles' rule:
+    built on the second product of the same, unmodified arrays."""
+    if not PACK_TILES or not pack_tiles_supported(col_indices, values, tile_cols):
+        return None
+    key = (values.data_ptr(), values._version, col_indices.data_ptr(), col_indices._version)
+    d = _tensor_cache(window_offset)
+    ent = d.get("packed")
+    if ent is None or ent[0] != key:
+        d["packed"] = (key, 1, None)
+        return None
+    _, calls, p = ent
+    if p is None and calls == 1:
+        p = pack_tiles(window_offset, col_indices, values, tile_cols) or False
+        d["packed"] = (key, 2, p)
+    return p or None
 
 
 def spmm_tc(window_offset: torch.Tensor, original_col_indices: torch.Tensor,
@@ -184,14 +270,18 @@ def spmm_tc(window_offset: torch.Tensor, original_col_indices: torch.Tensor,
     unless ``graph_rws_amd.core.ops.TIMING`` is set.
     """
     plan = _cached_plan(window_offset, original_col_indices, tile_cols, input_B.shape[1])
+    packed = None
+    if input_B.dtype == values_condensed.dtype and input_B.is_cuda:
+        packed = _cached_packed(window_offset, original_col_indices, values_condensed, tile_cols)
     if not TIMING:
         return spmm(window_offset, original_col_indices, values_condensed, input_B, tile_cols,
-                    plan=plan), 0.0
+                    plan=plan, packed=packed), 0.0
     s = torch.cuda.current_stream(input_B.device)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(s)
-    y = spmm(window_offset, original_col_indices, values_condensed, input_B, tile_cols, plan=plan)
+    y = spmm(window_offset, original_col_indices, values_condensed, input_B, tile_cols, plan=plan,
+             packed=packed)
     e1.record(s)
     e1.synchronize()
     return y, float(e0.elapsed_time(e1))

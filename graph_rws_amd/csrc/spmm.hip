@@ -33,6 +33,7 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 typedef int32_t i32x8_t __attribute__((ext_vector_type(8)));
@@ -99,6 +100,11 @@ struct SpmmArgs {
     int32_t nchunks;
     uint32_t x_bytes;  // buffer path: readable bytes of x (last row: n_cols elements)
     int64_t col_base;  // first output column of chunk 0 (a launch may cover part of N)
+    // packed tiles (16x16 tiles, 16-bit values): per tile 4 row groups of
+    // {mask_lo, mask_hi, start}, and the nonzero values they index
+    const uint32_t* hdr;
+    const void* pvals;
+    uint32_t pv_bytes;
 };
 
 // Output conversion for the three element types.
@@ -415,11 +421,24 @@ __global__ __launch_bounds__(64 * WPB) void spmm_fwd_kernel(SpmmArgs a) {
 // Requires (checked on the host): x_rows < 2^24, row pitch < 2^24 bytes,
 // 2 * (x_rows + 1) rows of X addressable in 32 bits, and every work item's
 // A within 2^31 bytes.
-template <int XT, bool AF32, int TC, int NBLK, int WPB, int PF>
+//
+// PK: A comes from packed tiles instead of the dense 16x16 values.  A tile's
+// 256 slots (row-major) form 4 groups of 4 rows; group q has a 64-bit mask
+// (bit (r%4)*16 + c set iff slot (r, c) holds a value whose bits are not
+// zero) and the index of its first value in the packed array, where the
+// nonzero values follow in slot order.  Lane (ag, ar) needs slots
+// ar*16 + 4ag .. +3: its mask nibble, and the popcount of the mask bits
+// below it added to the group start locate its values; a 12-byte load and
+// a byte permute rebuild the 4 halves with zeros in the empty slots, so
+// the MFMA sees exactly the dense tile's operand (bit-identical results).
+// The header rides in the column-index ring, loaded a step before the
+// dependent value read, which so adds no wait of its own.
+template <int XT, bool AF32, int TC, int NBLK, int WPB, int PF, bool PK = false>
 __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
     static_assert(XT == GRWS_F16 || XT == GRWS_BF16, "16-bit X only");
     static_assert(TC == 8 || TC == 16, "tile_cols must be 8 or 16");
     static_assert(PF >= 1 && PF <= 2, "prefetch depth 1..2");
+    static_assert(!PK || (TC == 16 && !AF32), "packed tiles: 16x16 tiles of 16-bit values");
     using S = typename XTraits<XT>::S;
     constexpr int SZ = 2;
     constexpr int SZA = AF32 ? 4 : 2;
@@ -428,14 +447,16 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
     constexpr int LPR = NC / VEC;               // lanes per staged row
     constexpr int NLD = (16 * LPR + 63) / 64;   // rows (loads) per lane per slab
     constexpr int PITCH = NC + 16;              // LDS row pitch (elements)
-    constexpr int R = PF + 1;
     static_assert(NLD == 1 || NLD == 2 || NLD == 4 || NLD == 8, "rows per lane");
+    constexpr int R = PF + 1;
     static_assert(WPB == 1 || WPB * 16 * PITCH * SZ >= 16 * NC * 4, "stage too small to reduce in");
     using ColV = typename std::conditional<
         NLD == 8, i32x8_t,
         typename std::conditional<NLD == 4, i32x4_t,
                                   typename std::conditional<NLD == 2, i32x2_t, int32_t>::type>::type>::type;
-    using AVec = typename std::conditional<AF32, float4_t, u32x2_t>::type;
+    using AVec = typename std::conditional<PK, u32x4_t,
+                                           typename std::conditional<AF32, float4_t, u32x2_t>::type>::type;
+    using HdrV = typename std::conditional<PK, u32x3_t, int>::type;
 
     __shared__ __attribute__((aligned(16))) S stage_all[WPB * 16 * PITCH];
 
@@ -485,6 +506,20 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
         (void*)(a.cols + t0 * TC + sb * 16), (short)0, (int)(c_bytes < 0 ? 0 : c_bytes), 0x00020000);
     const __amdgpu_buffer_rsrc_t rsX =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.x), (short)0, (int)a.x_bytes, 0x00020000);
+    // packed tiles: headers of the item's tiles from slab sb (slab = tile at
+    // tile_cols 16), and all packed values; reads past either return zero
+    auto make_h = [&]() {
+        if constexpr (PK) {
+            const int64_t h_bytes = (nslabs - sb) * 48;
+            return __builtin_amdgcn_make_buffer_rsrc((void*)(a.hdr + (t0 + sb) * 12), (short)0,
+                                                     (int)(h_bytes > 0x7fffffff ? 0x7fffffff : h_bytes), 0x00020000);
+        } else {
+            return __builtin_amdgcn_make_buffer_rsrc(nullptr, (short)0, 0, 0x00020000);
+        }
+    };
+    const __amdgpu_buffer_rsrc_t rsH = make_h();
+    const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(PK ? a.pvals : nullptr),
+                                                                         (short)0, PK ? (int)a.pv_bytes : 0, 0x00020000);
 
     const int rbase = NLD * (lane / LPR);  // first of the lane's slab rows
     const bool lrow = rbase < 16;          // NBLK == 1: lanes 32..63 stage nothing
@@ -500,6 +535,9 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
     const uint32_t a_lane = (uint32_t)((((4 * ag) / TC) * 16 + ar) * TC + (4 * ag) % TC) * SZA;
     // transpose-read address of this lane within a 16-column block
     const int tr_off = (4 * ag + ((lane & 15) >> 2)) * PITCH + 4 * (lane & 3);
+    // packed tiles: this lane's row group header and its first mask bit
+    const uint32_t h_lane = (uint32_t)(ar >> 2) * 12;
+    const uint32_t bitoff = (uint32_t)((ar & 3) * 16 + 4 * ag);
 
     auto load_cols = [&](int64_t s) -> ColV {
         const uint32_t off = (uint32_t)((s - sb) * 64) + (uint32_t)rbase * 4;
@@ -526,12 +564,32 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
             regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rsX, (int)(__umul24(row, ldxb) + colb), 0, 0);
         }
     };
-    auto load_a = [&](int64_t s) -> AVec {
-        const uint32_t off = (uint32_t)((s - sb) * 256 * SZA) + a_lane;
-        if constexpr (AF32) {
-            return __builtin_bit_cast(AVec, __builtin_amdgcn_raw_buffer_load_b128(rsA, (int)off, 0, 2));
+    auto load_hdr = [&](int64_t s) -> HdrV {
+        if constexpr (PK) {
+            return __builtin_amdgcn_raw_buffer_load_b96(rsH, (int)((uint32_t)((s - sb) * 48) + h_lane), 0, 2);
         } else {
-            return __builtin_bit_cast(AVec, __builtin_amdgcn_raw_buffer_load_b64(rsA, (int)off, 0, 2));
+            return 0;
+        }
+    };
+    auto load_a = [&](int64_t s, const HdrV h) -> AVec {
+        if constexpr (PK) {
+            // {d0, d1, d2} hold the lane's run of up to 4 values starting
+            // at the low half of d0, or at its high half when info bit 4 is set
+            const uint64_t m = ((uint64_t)h[1] << 32) | h[0];
+            const uint32_t below = (uint32_t)__builtin_popcountll(m & ((1ull << bitoff) - 1));
+            const uint32_t nib = (uint32_t)(m >> bitoff) & 15u;
+            const uint32_t hidx = h[2] + below;
+            const uint32_t off = nib ? (hidx & ~1u) * 2u : 0x80000000u;  // empty: no read
+            const u32x3_t d = __builtin_amdgcn_raw_buffer_load_b96(rsV, (int)off, 0, 2);
+            return u32x4_t{d[0], d[1], d[2], nib | ((hidx & 1u) << 4)};
+        } else {
+            (void)h;
+            const uint32_t off = (uint32_t)((s - sb) * 256 * SZA) + a_lane;
+            if constexpr (AF32) {
+                return __builtin_bit_cast(AVec, __builtin_amdgcn_raw_buffer_load_b128(rsA, (int)off, 0, 2));
+            } else {
+                return __builtin_bit_cast(AVec, __builtin_amdgcn_raw_buffer_load_b64(rsA, (int)off, 0, 2));
+            }
         }
     };
 
@@ -549,7 +607,21 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         short4_t af;
-        if constexpr (AF32) {
+        if constexpr (PK) {
+            const uint32_t info = a_cur[3];
+            const uint32_t sh = (info >> 4) * 16u;
+            const uint32_t r0 = __builtin_amdgcn_alignbit(a_cur[1], a_cur[0], sh);
+            const uint32_t r1 = __builtin_amdgcn_alignbit(a_cur[2], a_cur[1], sh);
+            // selector of slot j: bytes of run value rank_j, or 0x0c (zero byte)
+            const uint32_t b0 = info & 1u, b1 = (info >> 1) & 1u, b2 = (info >> 2) & 1u, b3 = (info >> 3) & 1u;
+            const uint32_t k2 = b0 + b1, k3 = k2 + b2;
+            const uint32_t s0 = b0 ? 0x0100u : 0x0c0cu;
+            const uint32_t s1 = b1 ? 0x0100u + 0x0202u * b0 : 0x0c0cu;
+            const uint32_t s2 = b2 ? 0x0100u + 0x0202u * k2 : 0x0c0cu;
+            const uint32_t s3 = b3 ? 0x0100u + 0x0202u * k3 : 0x0c0cu;
+            af = __builtin_bit_cast(short4_t, u32x2_t{__builtin_amdgcn_perm(r1, r0, s0 | (s1 << 16)),
+                                                      __builtin_amdgcn_perm(r1, r0, s2 | (s3 << 16))});
+        } else if constexpr (AF32) {
             if constexpr (XT == GRWS_F16) {
                 af = __builtin_bit_cast(short4_t, half4_t{(_Float16)a_cur[0], (_Float16)a_cur[1], (_Float16)a_cur[2],
                                                           (_Float16)a_cur[3]});
@@ -580,21 +652,29 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
 
     const int64_t s0 = sb + wave;
     if (s0 < se && xr > 0) {  // uniform per wave
+        // Ring of R = PF + 1 slots: each step issues the column indices R
+        // slabs ahead (and, for packed tiles, their headers), the X rows and
+        // A values PF slabs ahead, then multiplies the current slab.
         u32x4_t buf[R][NLD];
         AVec abuf[R];
         ColV cring[R];
+        HdrV hring[R];
 #pragma unroll
-        for (int k = 0; k < R; ++k) cring[k] = load_cols(s0 + (int64_t)k * WPB);
+        for (int k = 0; k < R; ++k) {
+            cring[k] = load_cols(s0 + (int64_t)k * WPB);
+            hring[k] = load_hdr(s0 + (int64_t)k * WPB);
+        }
 #pragma unroll
         for (int k = 0; k < PF; ++k) {
             load_x(cring[k], s0 + (int64_t)k * WPB, buf[k]);
-            abuf[k] = load_a(s0 + (int64_t)k * WPB);
+            abuf[k] = load_a(s0 + (int64_t)k * WPB, hring[k]);
         }
         auto step = [&](const int u, const int64_t s) {
             const int ps = (u + PF) % R;
             cring[u] = load_cols(s + (int64_t)R * WPB);
+            hring[u] = load_hdr(s + (int64_t)R * WPB);
             load_x(cring[ps], s + (int64_t)PF * WPB, buf[ps]);
-            abuf[ps] = load_a(s + (int64_t)PF * WPB);
+            abuf[ps] = load_a(s + (int64_t)PF * WPB, hring[ps]);
             consume(buf[u], abuf[u]);
         };
         const int64_t nsteps = (se - s0 + WPB - 1) / WPB;
@@ -751,32 +831,44 @@ int dispatch_tc(const SpmmArgs& a, int tc, int nblk, bool vect, hipStream_t stre
                    : dispatch_nblk<XT, AF32, 16>(a, nblk, vect, stream);
 }
 
-template <int XT, bool AF32, int TC, int NBLK, int WPB>
+template <int XT, bool AF32, int TC, int NBLK, int WPB, bool PK>
 int launch_buf(const SpmmArgs& a, hipStream_t stream) {
     const int64_t total = a.num_items * a.nchunks;
     const int64_t grid = ((total + 7) / 8) * 8;
     if (grid > INT32_MAX) return set_error(GRWS_E_INVALID, "spmm: too many work items (%lld)", (long long)total);
-    hipLaunchKernelGGL((spmm_buf_kernel<XT, AF32, TC, NBLK, WPB, 1>), dim3((unsigned)grid), dim3(64 * WPB), 0, stream,
-                       a);
+    hipLaunchKernelGGL((spmm_buf_kernel<XT, AF32, TC, NBLK, WPB, 1, PK>), dim3((unsigned)grid), dim3(64 * WPB), 0,
+                       stream, a);
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }
 
-template <int XT, bool AF32, int TC>
+template <int XT, bool AF32, int TC, bool PK>
 int dispatch_buf(const SpmmArgs& a, int nblk, hipStream_t stream) {
     const bool two = waves_for(a, nblk) == 2;
     switch (nblk) {
-        case 1: return two ? launch_buf<XT, AF32, TC, 1, 2>(a, stream) : launch_buf<XT, AF32, TC, 1, 1>(a, stream);
-        case 2: return two ? launch_buf<XT, AF32, TC, 2, 2>(a, stream) : launch_buf<XT, AF32, TC, 2, 1>(a, stream);
-        case 4: return two ? launch_buf<XT, AF32, TC, 4, 2>(a, stream) : launch_buf<XT, AF32, TC, 4, 1>(a, stream);
-        case 16: return two ? launch_buf<XT, AF32, TC, 16, 2>(a, stream) : launch_buf<XT, AF32, TC, 16, 1>(a, stream);
-        default: return two ? launch_buf<XT, AF32, TC, 8, 2>(a, stream) : launch_buf<XT, AF32, TC, 8, 1>(a, stream);
+        case 1:
+            return two ? launch_buf<XT, AF32, TC, 1, 2, PK>(a, stream) : launch_buf<XT, AF32, TC, 1, 1, PK>(a, stream);
+        case 2:
+            return two ? launch_buf<XT, AF32, TC, 2, 2, PK>(a, stream) : launch_buf<XT, AF32, TC, 2, 1, PK>(a, stream);
+        case 4:
+            return two ? launch_buf<XT, AF32, TC, 4, 2, PK>(a, stream) : launch_buf<XT, AF32, TC, 4, 1, PK>(a, stream);
+        case 16:
+            return two ? launch_buf<XT, AF32, TC, 16, 2, PK>(a, stream)
+                       : launch_buf<XT, AF32, TC, 16, 1, PK>(a, stream);
+        default:
+            return two ? launch_buf<XT, AF32, TC, 8, 2, PK>(a, stream) : launch_buf<XT, AF32, TC, 8, 1, PK>(a, stream);
     }
 }
 
+// a.hdr set (packed tiles; the host checked 16x16 tiles of x-dtype values)
+// selects the packed variant.
 template <int XT, bool AF32>
 int dispatch_buf_tc(const SpmmArgs& a, int tc, int nblk, hipStream_t stream) {
-    return tc == 8 ? dispatch_buf<XT, AF32, 8>(a, nblk, stream) : dispatch_buf<XT, AF32, 16>(a, nblk, stream);
+    if constexpr (!AF32) {
+        if (a.hdr) return dispatch_buf<XT, false, 16, true>(a, nblk, stream);
+    }
+    return tc == 8 ? dispatch_buf<XT, AF32, 8, false>(a, nblk, stream)
+                   : dispatch_buf<XT, AF32, 16, false>(a, nblk, stream);
 }
 
 // Whether the buffer-load kernel's 32-bit offsets cover this call: rows and
@@ -824,6 +916,76 @@ int launch_fixup(const grws_spmm_plan* plan, const SpmmArgs& a, int nblk, hipStr
     }
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// packed tiles
+// ---------------------------------------------------------------------------
+// One wave per 16x16 tile of 16-bit values; lane l holds slots 4l..4l+3
+// (row l/4, columns 4(l%4)..+3).  nib = which of them are nonzero bit
+// patterns; counts per lane are at most 4, so three ballots give every
+// lane's exclusive prefix and the tile total.
+struct PackLane {
+    uint32_t v0, v1, nib, pre, total;
+};
+
+__device__ __forceinline__ PackLane pack_lane(const uint16_t* __restrict__ vals, int64_t t, int lane) {
+    const u32x2_t v = *reinterpret_cast<const u32x2_t*>(vals + t * 256 + 4 * lane);
+    PackLane p;
+    p.v0 = v[0];
+    p.v1 = v[1];
+    p.nib = ((v[0] & 0xffffu) ? 1u : 0u) | ((v[0] >> 16) ? 2u : 0u) | ((v[1] & 0xffffu) ? 4u : 0u) |
+            ((v[1] >> 16) ? 8u : 0u);
+    const uint32_t cnt = (uint32_t)__builtin_popcount(p.nib);
+    const uint64_t q1 = __ballot(cnt & 1u), q2 = __ballot(cnt & 2u), q4 = __ballot(cnt & 4u);
+    auto below = [](uint64_t m) {
+        return (uint32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    };
+    p.pre = below(q1) + 2u * below(q2) + 4u * below(q4);
+    p.total = (uint32_t)(__builtin_popcountll(q1) + 2 * __builtin_popcountll(q2) + 4 * __builtin_popcountll(q4));
+    return p;
+}
+
+__global__ __launch_bounds__(256) void pack_count_kernel(const uint16_t* __restrict__ vals, int64_t num_tiles,
+                                                         int32_t* __restrict__ counts) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= num_tiles) return;  // uniform per wave
+    const int lane = threadIdx.x & 63;
+    const PackLane p = pack_lane(vals, t, lane);
+    if (lane == 0) counts[t] = (int32_t)p.total;
+}
+
+// off: exclusive prefix of the counts (int64, num_tiles + 1 entries).
+// Writes past num_values (a caller that passed a smaller count than
+// grws_pack_tiles_count returned) are dropped.
+__global__ __launch_bounds__(256) void pack_fill_kernel(const uint16_t* __restrict__ vals, int64_t num_tiles,
+                                                        const int64_t* __restrict__ off, uint32_t* __restrict__ hdr,
+                                                        uint16_t* __restrict__ pvals, int64_t num_values) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= num_tiles) return;  // uniform per wave
+    const int lane = threadIdx.x & 63;
+    const PackLane p = pack_lane(vals, t, lane);
+    const uint32_t base = (uint32_t)off[t] + p.pre;
+    const uint16_t h[4] = {(uint16_t)(p.v0 & 0xffffu), (uint16_t)(p.v0 >> 16), (uint16_t)(p.v1 & 0xffffu),
+                           (uint16_t)(p.v1 >> 16)};
+    uint32_t k = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if ((p.nib >> j) & 1u) {
+            if ((int64_t)base + k < num_values) pvals[base + k] = h[j];
+            ++k;
+        }
+    }
+    // the 16 lanes of row group q contribute 4 mask bits each, in slot order
+    uint64_t m = (uint64_t)p.nib << (4 * (lane & 15));
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) m |= __shfl_xor(m, d, 64);
+    if ((lane & 15) == 0) {
+        uint32_t* o = hdr + t * 12 + (lane >> 4) * 3;
+        o[0] = (uint32_t)m;
+        o[1] = (uint32_t)(m >> 32);
+        o[2] = base;
+    }
 }
 
 }  // namespace
@@ -925,9 +1087,17 @@ extern "C" size_t grws_spmm_workspace_bytes(const grws_spmm_plan* plan, int64_t 
     return (size_t)plan->num_slots * 16 * (size_t)padded * sizeof(float);
 }
 
-extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const void* x, int32_t x_dtype,
-                         int64_t x_rows, int64_t ldx, int64_t n_cols, void* y, int32_t y_dtype, int64_t ldy,
-                         void* workspace, size_t workspace_bytes, void* stream_) {
+namespace {
+// Packed values addressable by the kernel's 32-bit byte offsets (with the
+// 12-byte reads past the last value inside the range check).
+constexpr int64_t kPackMaxValues = ((int64_t)1 << 30) - 16;
+// Elements of readable padding after the packed values (a lane's 12-byte
+// read starts at most 1 element before its first value and spans 6).
+constexpr int64_t kPackPad = 8;
+
+int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_plan* plan, const void* x,
+              int32_t x_dtype, int64_t x_rows, int64_t ldx, int64_t n_cols, void* y, int32_t y_dtype, int64_t ldy,
+              void* workspace, size_t workspace_bytes, void* stream_) {
     clear_error();
     hipStream_t stream = as_stream(stream_);
     GRWS_CHECK_ARG(A != nullptr, "spmm: null graph");
@@ -946,6 +1116,15 @@ extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const v
     GRWS_CHECK_ARG(ldy >= n_cols, "spmm: ldy < n_cols");
     if (x_rows > 0) GRWS_CHECK_ARG(x != nullptr && ldx >= n_cols, "spmm: bad x (null or ldx < n_cols)");
     if (A->num_tiles > 0) GRWS_CHECK_ARG(A->col_indices && A->values, "spmm: null tile arrays");
+    if (P) {
+        GRWS_CHECK_ARG(A->tile_cols == 16 && x_dtype != GRWS_F32 && A->values_dtype == x_dtype,
+                       "spmm_packed: packed tiles need 16x16 tiles whose values have the x dtype");
+        GRWS_CHECK_ARG(P->num_values >= 0 && P->num_values <= kPackMaxValues, "spmm_packed: bad num_values %lld",
+                       (long long)P->num_values);
+        GRWS_CHECK_ARG(A->num_tiles == 0 || (P->header && (P->values || P->num_values == 0)),
+                       "spmm_packed: null packed arrays");
+        GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(P->header) % 4 == 0, "spmm_packed: header not 4-byte aligned");
+    }
 
     const size_t esz = dtype_size(x_dtype);
     const int64_t vec = (int64_t)(16 / esz);
@@ -986,6 +1165,13 @@ extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const v
     int st;
     if (use_buf) {
         a.x_bytes = (uint32_t)((x_rows - 1) * ldx * (int64_t)esz + n_cols * (int64_t)esz);
+        if (P && A->num_tiles > 0) {  // the element-masked kernel below reads the dense values
+            a.hdr = P->header;
+            a.pvals = P->values;
+            // a 12-byte read that runs past the end of the resource returns
+            // zero as a whole, so the range covers the padding as well
+            a.pv_bytes = (uint32_t)((P->num_values + kPackPad) * 2);
+        }
         // N above 256 and not a multiple of it: 256-column chunks over the
         // whole multiples, then one narrower launch for the rest, so A is
         // streamed once per 256 columns and no chunk is mostly empty
@@ -1033,3 +1219,113 @@ extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const v
     }
     return GRWS_OK;
 }
+}  // namespace
+
+extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const void* x, int32_t x_dtype,
+                         int64_t x_rows, int64_t ldx, int64_t n_cols, void* y, int32_t y_dtype, int64_t ldy,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    return spmm_impl(A, nullptr, plan, x, x_dtype, x_rows, ldx, n_cols, y, y_dtype, ldy, workspace, workspace_bytes,
+                     stream);
+}
+
+extern "C" int grws_spmm_packed(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_plan* plan,
+                                const void* x, int32_t x_dtype, int64_t x_rows, int64_t ldx, int64_t n_cols, void* y,
+                                int32_t y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+    return spmm_impl(A, P, plan, x, x_dtype, x_rows, ldx, n_cols, y, y_dtype, ldy, workspace, workspace_bytes,
+                     stream);
+}
+
+namespace {
+int check_pack_graph(const grws_bcsr* A) {
+    GRWS_CHECK_ARG(A != nullptr, "pack_tiles: null graph");
+    GRWS_CHECK_ARG(A->tile_rows == 16 && A->tile_cols == 16, "pack_tiles: tiles must be 16x16 (got %dx%d)",
+                   A->tile_rows, A->tile_cols);
+    if (A->values_dtype != GRWS_F16 && A->values_dtype != GRWS_BF16)
+        return set_error(GRWS_E_DTYPE, "pack_tiles: values must be F16 or BF16");
+    GRWS_CHECK_ARG(A->num_tiles >= 0, "pack_tiles: negative tile count");
+    if (A->num_tiles > 0) {
+        GRWS_CHECK_ARG(A->values != nullptr, "pack_tiles: null values");
+        GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(A->values) % 8 == 0, "pack_tiles: values not 8-byte aligned");
+    }
+    return GRWS_OK;
+}
+
+struct PackWs {
+    int32_t* counts;
+    int64_t* off;
+    char* scan;
+    size_t scan_bytes;
+    bool ok;
+    size_t used;
+};
+
+PackWs carve_pack(void* ws, size_t wsb, int64_t num_tiles) {
+    Carver cv(ws, wsb);
+    PackWs w;
+    w.counts = cv.take<int32_t>(num_tiles + 1);
+    w.off = cv.take<int64_t>(num_tiles + 2);
+    w.scan_bytes = scan_workspace_bytes(num_tiles);
+    w.scan = cv.take<char>(w.scan_bytes);
+    w.ok = cv.ok;
+    w.used = cv.used;
+    return w;
+}
+}  // namespace
+
+extern "C" size_t grws_pack_tiles_workspace_bytes(int64_t num_tiles) {
+    if (num_tiles < 0) return 0;
+    Sizer s;
+    s.take<int32_t>((size_t)num_tiles + 1);
+    s.take<int64_t>((size_t)num_tiles + 2);
+    s.used += scan_workspace_bytes(num_tiles) + 256;
+    return s.used;
+}
+
+extern "C" int grws_pack_tiles_count(const grws_bcsr* A, void* workspace, size_t workspace_bytes,
+                                     int64_t* num_values, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_TRY(check_pack_graph(A));
+    GRWS_CHECK_ARG(num_values != nullptr, "pack_tiles_count: null output");
+    *num_values = 0;
+    if (A->num_tiles == 0) return GRWS_OK;
+    PackWs w = carve_pack(workspace, workspace_bytes, A->num_tiles);
+    if (!w.ok)
+        return set_error(GRWS_E_CAPACITY, "pack_tiles_count: workspace too small (%zu < %zu)", workspace_bytes, w.used);
+    const int64_t blocks = (A->num_tiles + 3) / 4;
+    if (blocks > INT32_MAX) return set_error(GRWS_E_INVALID, "pack_tiles_count: too many tiles");
+    hipLaunchKernelGGL(pack_count_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(A->values), A->num_tiles, w.counts);
+    GRWS_LAUNCH_CHECK();
+    GRWS_TRY(scan_i32_to_i64(w.counts, w.off, A->num_tiles, false, w.scan, w.scan_bytes, stream));
+    int64_t total = 0;
+    GRWS_HIP(hipMemcpyAsync(&total, w.off + A->num_tiles, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipStreamSynchronize(stream));
+    *num_values = total;
+    if (total > kPackMaxValues)
+        return set_error(GRWS_E_CAPACITY, "pack_tiles_count: %lld nonzero values exceed the packed limit %lld",
+                         (long long)total, (long long)kPackMaxValues);
+    return GRWS_OK;
+}
+
+extern "C" int grws_pack_tiles_fill(const grws_bcsr* A, uint32_t* header, void* values, int64_t num_values,
+                                    void* workspace, size_t workspace_bytes, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_TRY(check_pack_graph(A));
+    GRWS_CHECK_ARG(num_values >= 0 && num_values <= kPackMaxValues, "pack_tiles_fill: bad num_values %lld",
+                   (long long)num_values);
+    if (A->num_tiles == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(header != nullptr && (values != nullptr || num_values == 0), "pack_tiles_fill: null output");
+    GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(header) % 4 == 0, "pack_tiles_fill: header not 4-byte aligned");
+    PackWs w = carve_pack(workspace, workspace_bytes, A->num_tiles);
+    if (!w.ok)
+        return set_error(GRWS_E_CAPACITY, "pack_tiles_fill: workspace too small (%zu < %zu)", workspace_bytes, w.used);
+    const int64_t blocks = (A->num_tiles + 3) / 4;
+    hipLaunchKernelGGL(pack_fill_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(A->values), A->num_tiles, w.off, header,
+                       static_cast<uint16_t*>(values), num_values);
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+

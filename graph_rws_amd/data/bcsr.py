@@ -248,11 +248,34 @@ class BCSRGraph:
             self._cache[key] = p
         return p
 
+    def packed_tiles(self):
+        """The packed copy of the values the SpMM reads instead of the dense
+        tiles (16x16 tiles of f16/bf16 values), built on this graph's second
+        SpMM and kept while the value and column arrays are unchanged.  A
+        graph multiplied once (a sampled block) is never packed: packing reads
+        the dense values twice, so it pays only from the second product on.
+        None when packing is off or does not apply."""
+        from ..core import ops as _ops
+        if not _ops.PACK_TILES or self.tile_cols != 16:
+            return None
+        v, c = self.values_condensed, self.original_col_indices
+        key = (v.data_ptr(), v._version, c.data_ptr(), c._version)
+        ent = self._cache.get("packed")
+        if ent is None or ent[0] != key:
+            self._cache["packed"] = (key, 1, None)
+            return None
+        _, calls, p = ent
+        if p is None and calls == 1:
+            p = _ops.pack_tiles(self.window_offset, c, v, self.tile_cols) or False
+            self._cache["packed"] = (key, 2, p)
+        return p or None
+
     def spmm(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Y[16W, N] = A x on the device (columns >= x.shape[0] contribute nothing)."""
         from ..core import spmm as _spmm
         return _spmm(self.window_offset, self.original_col_indices, self.values_condensed, x,
-                     self.tile_cols, plan=self.spmm_plan(x.shape[1]), out=out)
+                     self.tile_cols, plan=self.spmm_plan(x.shape[1]), out=out,
+                     packed=self.packed_tiles() if x.dtype == self.values_condensed.dtype else None)
 
     def transpose(self) -> "BCSRGraph":
         """Cached BCSR of A^T (num_cols x 16W), built on the device.  Rebuilt

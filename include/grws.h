@@ -132,6 +132,52 @@ int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const void* x, int
               void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Packed tiles: a compact copy of A's values for graphs that are multiplied */
+/* many times (full-graph training).  No counterpart in the reference, which */
+/* streams the dense 16x16 tiles (spmm_tc.cuh:113-193) on every call; the    */
+/* dense arrays stay the graph of record and grws_spmm_packed gives          */
+/* bit-identical results to grws_spmm.                                       */
+/*                                                                           */
+/* Layout (16x16 tiles of F16/BF16 values only): header[num_tiles][4][3]     */
+/* uint32 -- for row group q (rows 4q..4q+3) {mask_lo, mask_hi, start}, mask */
+/* bit (r%4)*16 + c set iff slot (r, c) holds a value whose bit pattern is   */
+/* not zero, start = index of the group's first such value in values[];     */
+/* values[num_values] = those values in tile, then slot, order.  At most     */
+/* 2^30 - 16 values.                                                         */
+/* ------------------------------------------------------------------------ */
+typedef struct grws_packed_tiles {
+    const uint32_t* header;
+    const void* values;
+    int64_t num_values;
+} grws_packed_tiles;
+
+/* Workspace bytes for both packing calls. */
+size_t grws_pack_tiles_workspace_bytes(int64_t num_tiles);
+
+/* Pass 1: counts the nonzero values per tile into the workspace and writes
+ * the host *num_values (synchronises `stream`).  GRWS_E_CAPACITY past the
+ * 2^30 - 16 limit. */
+int grws_pack_tiles_count(const grws_bcsr* A, void* workspace, size_t workspace_bytes,
+                          int64_t* num_values, void* stream);
+
+/* Pass 2: writes header [num_tiles*12] uint32 and values (A's dtype),
+ * reading the counts pass 1 left in the same, unchanged, workspace.  The
+ * values buffer holds num_values + 8 elements: grws_spmm_packed may read
+ * the 8 after the last value (their contents do not matter). */
+int grws_pack_tiles_fill(const grws_bcsr* A, uint32_t* header, void* values, int64_t num_values,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* grws_spmm with A's values read from packed tiles P (P NULL: grws_spmm).
+ * Needs 16x16 tiles whose values have the x dtype (F16/BF16).  The same
+ * result, bit for bit, as grws_spmm on the dense arrays (which are still
+ * read when the call runs on the element-masked kernel, e.g. X rows not
+ * 16-byte aligned). */
+int grws_spmm_packed(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_plan* plan,
+                     const void* x, int32_t x_dtype, int64_t x_rows, int64_t ldx, int64_t n_cols,
+                     void* y, int32_t y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* CSR -> BCSR on host cores.  Replaces core_lib.csr_to_bcsr_cpu             */
 /* (bind.cpp:143-150 -> convert_wrapper.cpp:27-180): same layout, same       */
 /* "last duplicate in CSR order wins" rule.  Host pointers.                  */

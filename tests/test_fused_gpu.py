@@ -90,6 +90,39 @@ def test_dropout_mask_statistics_and_backward(cuda_device):
     _close(z.grad, zr.grad, 1e-4)
 
 
+@pytest.mark.parametrize("dim,p", [(300, 0.3), (64, 0.9), (1000, 0.05)])
+def test_dropout_mask_is_the_oracle_philox(cuda_device, dim, p):
+    """Element (r, c) is kept iff word c%4 of Philox4x32-10 at counter
+    (r_lo, r_hi, c/4, 0), key = the 64-bit seed, is >= p * 2^32.  The
+    oracle's Philox is pinned against ATen's vectors, so this pins the
+    counter layout and threshold of the kernel's mask."""
+    import numpy as np
+    import oracle
+    print(f"case mask dim={dim} p={p}", flush=True)
+    rows = 23
+    torch.manual_seed(dim)
+    z = torch.randn(rows, dim, device=cuda_device)
+    norm = torch.nn.LayerNorm(dim).to(cuda_device)
+    with torch.no_grad():
+        norm.bias.fill_(1.0)  # no output is exactly zero before dropout
+    y = act_norm_dropout(z, norm, 0.0, relu=True)
+    torch.manual_seed(77)
+    seed = int(torch.randint(0, 2 ** 62, (1,)).item())  # the draw the wrapper makes
+    torch.manual_seed(77)
+    out = act_norm_dropout(z, norm, p, relu=True)
+    thr = min(int(float(np.float32(p)) * 2.0 ** 32), 0xFFFFFFFF)  # p reaches the kernel as fp32
+    key = [seed & 0xFFFFFFFF, seed >> 32]
+    want = np.zeros((rows, dim), bool)
+    for r in range(rows):
+        for b in range((dim + 3) // 4):
+            w = oracle.philox4x32_10([r, 0, b, 0], key)
+            for j in range(min(4, dim - 4 * b)):
+                want[r, 4 * b + j] = int(w[j]) >= thr
+    got = (out != 0).cpu().numpy()
+    assert (got == want).all(), f"{int((got != want).sum())} mask elements differ"
+    _close(out[out != 0], y[out != 0] / (1.0 - p), 1e-5)
+
+
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("classes", [7, 47, 172])
 def test_cross_entropy_matches_torch(cuda_device, dt, classes):
