@@ -37,10 +37,12 @@ __device__ __forceinline__ Philox4 philox4(uint64_t seed, uint64_t row, uint32_t
     uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
 #pragma unroll
     for (int r = 0; r < 10; ++r) {
-        const uint32_t hi0 = __umulhi(0xD2511F53u, c0);
-        const uint32_t lo0 = 0xD2511F53u * c0;
-        const uint32_t hi1 = __umulhi(0xCD9E8D57u, c2);
-        const uint32_t lo1 = 0xCD9E8D57u * c2;
+        // one 32x32->64 multiply each (v_mad_u64_u32) instead of separate
+        // high and low multiplies
+        const uint64_t m0 = (uint64_t)0xD2511F53u * c0;
+        const uint64_t m1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t hi0 = (uint32_t)(m0 >> 32), lo0 = (uint32_t)m0;
+        const uint32_t hi1 = (uint32_t)(m1 >> 32), lo1 = (uint32_t)m1;
         const uint32_t n0 = hi1 ^ c1 ^ k0;
         const uint32_t n2 = hi0 ^ c3 ^ k1;
         c0 = n0;
@@ -51,6 +53,32 @@ __device__ __forceinline__ Philox4 philox4(uint64_t seed, uint64_t row, uint32_t
         k1 += 0xBB67AE85u;
     }
     return Philox4{{c0, c1, c2, c3}};
+}
+
+// Four consecutive elements as loaded (converted later, so a load can be
+// issued an iteration ahead of its use).
+template <typename T>
+struct Raw4 {
+    using V = uint2;
+};
+template <>
+struct Raw4<float> {
+    using V = float4_t;
+};
+
+template <typename T>
+__device__ __forceinline__ typename Raw4<T>::V load_raw4(const T* p) {
+    return *reinterpret_cast<const typename Raw4<T>::V*>(p);
+}
+
+template <typename T>
+__device__ __forceinline__ void cvt4(const typename Raw4<T>::V& x, float* v) {
+    if constexpr (std::is_same<T, float>::value) {
+        v[0] = x[0], v[1] = x[1], v[2] = x[2], v[3] = x[3];
+    } else {
+        const T* h = reinterpret_cast<const T*>(&x);
+        v[0] = to_float(h[0]), v[1] = to_float(h[1]), v[2] = to_float(h[2]), v[3] = to_float(h[3]);
+    }
 }
 
 template <typename T>
@@ -75,10 +103,24 @@ __device__ __forceinline__ void store4(T* p, const float* v) {
     }
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 64 lanes, the same value in every lane, in a fixed order:
+// within each row of 16 lanes by DPP (xor 1, xor 2 quad permutes, then
+// rotations by 4 and 8), then the 4 row sums in row order.  No LDS traffic.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
-    return v;
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x124>(v);  // row_ror:4
+    v += dpp_f<0x128>(v);  // row_ror:8
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return ((r0 + r1) + r2) + r3;
 }
 
 __device__ __forceinline__ uint32_t keep_threshold(float p) {
@@ -87,30 +129,51 @@ __device__ __forceinline__ uint32_t keep_threshold(float p) {
 }
 
 // out = dropout(LayerNorm(act(z))).  One wave per row, ROWS rows in flight
-// per wave (their loads are issued together), STEPS = ceil(dim / 256).
+// per wave (their loads are issued together, an iteration ahead), STEPS =
+// ceil(dim / 256).
 template <typename ZT, typename OT, int STEPS, int ROWS>
 __global__ __launch_bounds__(kBlk) void act_norm_dropout_fwd_kernel(
     const ZT* __restrict__ z, int64_t ldz, int64_t rows, int dim, int act, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, float p, uint64_t seed, OT* __restrict__ out, int64_t ldo,
     float* __restrict__ mean_out, float* __restrict__ rstd_out) {
     const int lane = threadIdx.x & 63;
+    // wave-uniform row index: per-row scalars then go through scalar loads
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const uint32_t thr = keep_threshold(p);
     const float scale = p > 0.f ? 1.0f / (1.0f - p) : 1.0f;
+    const float inv_dim = 1.0f / (float)dim;
+    // this lane's gamma / beta, loaded once for all its rows
+    float gm[STEPS][4], bt[STEPS][4];
+#pragma unroll
+    for (int k = 0; k < STEPS; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = 256 * k + 4 * lane + j;
+            gm[k][j] = c < dim ? gamma[c] : 0.f;
+            bt[k][j] = c < dim ? beta[c] : 0.f;
+        }
     const int64_t stride = (int64_t)gridDim.x * kRowsPerBlock * ROWS;
-    for (int64_t r0 = ((int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) * ROWS; r0 < rows; r0 += stride) {
-        float x[ROWS][STEPS][4];
+    // the next iteration's rows are loaded while this one is computed
+    typename Raw4<ZT>::V raw[ROWS][STEPS];
+    auto fetch = [&](int64_t rb) {
 #pragma unroll
         for (int i = 0; i < ROWS; ++i)
 #pragma unroll
             for (int k = 0; k < STEPS; ++k) {
                 const int c = 256 * k + 4 * lane;
-                if (r0 + i < rows && c < dim) {
-                    load4(z + (r0 + i) * ldz + c, x[i][k]);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) x[i][k][j] = 0.f;
-                }
+                if (rb + i < rows && c < dim) raw[i][k] = load_raw4(z + (rb + i) * ldz + c);
+                else raw[i][k] = typename Raw4<ZT>::V{};
             }
+    };
+    int64_t r0 = ((int64_t)blockIdx.x * kRowsPerBlock + wave) * ROWS;
+    if (r0 < rows) fetch(r0);
+    for (; r0 < rows; r0 += stride) {
+        float x[ROWS][STEPS][4];
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i)
+#pragma unroll
+            for (int k = 0; k < STEPS; ++k) cvt4<ZT>(raw[i][k], x[i][k]);
+        if (r0 + stride < rows) fetch(r0 + stride);
         float mean[ROWS], rstd[ROWS];
 #pragma unroll
         for (int i = 0; i < ROWS; ++i) {
@@ -122,7 +185,7 @@ __global__ __launch_bounds__(kBlk) void act_norm_dropout_fwd_kernel(
                     if (act == 1) x[i][k][j] = x[i][k][j] < 0.f ? 0.f : x[i][k][j];  // NaN passes, as torch.relu
                     sum += x[i][k][j];
                 }
-            mean[i] = wave_sum(sum) / (float)dim;
+            mean[i] = wave_sum(sum) * inv_dim;
         }
 #pragma unroll
         for (int i = 0; i < ROWS; ++i) {
@@ -138,7 +201,7 @@ __global__ __launch_bounds__(kBlk) void act_norm_dropout_fwd_kernel(
                     }
                 }
             }
-            rstd[i] = 1.0f / sqrtf(wave_sum(q) / (float)dim + eps);
+            rstd[i] = __builtin_amdgcn_rsqf(wave_sum(q) * inv_dim + eps);
         }
 #pragma unroll
         for (int i = 0; i < ROWS; ++i) {
@@ -153,7 +216,7 @@ __global__ __launch_bounds__(kBlk) void act_norm_dropout_fwd_kernel(
                     if (p > 0.f) u = philox4(seed, (uint64_t)r, (uint32_t)(c >> 2));
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        y[j] = (x[i][k][j] - mean[i]) * rstd[i] * gamma[c + j] + beta[c + j];
+                        y[j] = (x[i][k][j] - mean[i]) * rstd[i] * gm[k][j] + bt[k][j];
                         if (p > 0.f) y[j] = u.w[j] >= thr ? y[j] * scale : 0.f;
                     }
                     store4(out + r * ldo + c, y);
@@ -168,7 +231,9 @@ __global__ __launch_bounds__(kBlk) void act_norm_dropout_fwd_kernel(
 }
 
 // dz from dout (see the header); per-work-group dgamma / dbeta partials.
-// ROWS rows in flight per wave, as in the forward.
+// ROWS rows in flight per wave, as in the forward.  The dropout mask is
+// recomputed from Philox: as fast here as reading a stored bit mask, which
+// would cost the forward its stores.
 template <typename GT, typename ZT, int STEPS, int ROWS>
 __global__ __launch_bounds__(kBlk) void act_norm_dropout_bwd_kernel(
     const GT* __restrict__ g, int64_t ldg, const ZT* __restrict__ z, int64_t ldz, int64_t rows, int dim, int act,
@@ -176,9 +241,11 @@ __global__ __launch_bounds__(kBlk) void act_norm_dropout_bwd_kernel(
     uint64_t seed, ZT* __restrict__ dz, int64_t lddz, float* __restrict__ part_g, float* __restrict__ part_b) {
     __shared__ float red[2][kRowsPerBlock][STEPS * 256];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform row index: mean, rstd and the mask words go through scalar loads
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const uint32_t thr = keep_threshold(p);
     const float scale = p > 0.f ? 1.0f / (1.0f - p) : 1.0f;
+    const float inv_dim = 1.0f / (float)dim;
     float ag[STEPS][4], ab[STEPS][4], gm[STEPS][4];
 #pragma unroll
     for (int k = 0; k < STEPS; ++k)
@@ -189,21 +256,36 @@ __global__ __launch_bounds__(kBlk) void act_norm_dropout_bwd_kernel(
             gm[k][j] = c < dim ? gamma[c] : 0.f;
         }
     const int64_t stride = (int64_t)gridDim.x * kRowsPerBlock * ROWS;
-    for (int64_t r0 = ((int64_t)blockIdx.x * kRowsPerBlock + wave) * ROWS; r0 < rows; r0 += stride) {
-        float gv[ROWS][STEPS][4], zz[ROWS][STEPS][4];
+    // the next iteration's rows are loaded while this one is computed
+    typename Raw4<GT>::V rg[ROWS][STEPS];
+    typename Raw4<ZT>::V rz[ROWS][STEPS];
+    auto fetch = [&](int64_t rb) {
 #pragma unroll
         for (int i = 0; i < ROWS; ++i)
 #pragma unroll
             for (int k = 0; k < STEPS; ++k) {
                 const int c = 256 * k + 4 * lane;
-                if (r0 + i < rows && c < dim) {
-                    load4(g + (r0 + i) * ldg + c, gv[i][k]);
-                    load4(z + (r0 + i) * ldz + c, zz[i][k]);
+                if (rb + i < rows && c < dim) {
+                    rg[i][k] = load_raw4(g + (rb + i) * ldg + c);
+                    rz[i][k] = load_raw4(z + (rb + i) * ldz + c);
                 } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) gv[i][k][j] = zz[i][k][j] = 0.f;
+                    rg[i][k] = typename Raw4<GT>::V{};
+                    rz[i][k] = typename Raw4<ZT>::V{};
                 }
             }
+    };
+    int64_t r0 = ((int64_t)blockIdx.x * kRowsPerBlock + wave) * ROWS;
+    if (r0 < rows) fetch(r0);
+    for (; r0 < rows; r0 += stride) {
+        float gv[ROWS][STEPS][4], zz[ROWS][STEPS][4];
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i)
+#pragma unroll
+            for (int k = 0; k < STEPS; ++k) {
+                cvt4<GT>(rg[i][k], gv[i][k]);
+                cvt4<ZT>(rz[i][k], zz[i][k]);
+            }
+        if (r0 + stride < rows) fetch(r0 + stride);
 #pragma unroll
         for (int i = 0; i < ROWS; ++i) {
             const int64_t r = r0 + i;
@@ -214,15 +296,20 @@ __global__ __launch_bounds__(kBlk) void act_norm_dropout_bwd_kernel(
 #pragma unroll
             for (int k = 0; k < STEPS; ++k) {
                 const int c = 256 * k + 4 * lane;
-                Philox4 u{{0u, 0u, 0u, 0u}};
-                if (p > 0.f && c < dim) u = philox4(seed, (uint64_t)r, (uint32_t)(c >> 2));
+                bool keep[4] = {true, true, true, true};
+                if (p > 0.f) {
+                    Philox4 u{{0u, 0u, 0u, 0u}};
+                    if (c < dim) u = philox4(seed, (uint64_t)r, (uint32_t)(c >> 2));
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) keep[j] = u.w[j] >= thr;
+                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     float x = zz[i][k][j];
                     if (act == 1) x = x < 0.f ? 0.f : x;
                     xh[k][j] = c < dim ? (x - mean) * rstd : 0.f;
                     float g1 = gv[i][k][j];
-                    if (p > 0.f) g1 = u.w[j] >= thr ? g1 * scale : 0.f;
+                    if (p > 0.f) g1 = keep[j] ? g1 * scale : 0.f;
                     ag[k][j] += g1 * xh[k][j];
                     ab[k][j] += g1;
                     dxh[k][j] = g1 * gm[k][j];
@@ -230,8 +317,8 @@ __global__ __launch_bounds__(kBlk) void act_norm_dropout_bwd_kernel(
                     sb += dxh[k][j] * xh[k][j];
                 }
             }
-            const float a = wave_sum(sa) / (float)dim;
-            const float b = wave_sum(sb) / (float)dim;
+            const float a = wave_sum(sa) * inv_dim;
+            const float b = wave_sum(sb) * inv_dim;
 #pragma unroll
             for (int k = 0; k < STEPS; ++k) {
                 const int c = 256 * k + 4 * lane;
@@ -291,10 +378,25 @@ __global__ __launch_bounds__(1024) void column_sum_kernel(const float* __restric
     }
 }
 
+// Upper bound of the backward's work-groups (and of its partial rows).
+constexpr int64_t kMaxBwdBlocks = 4096;
 int64_t bwd_blocks(int64_t rows) {
     int64_t b = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-    if (b > 2048) b = 2048;
+    if (b > kMaxBwdBlocks) b = kMaxBwdBlocks;
     return b < 1 ? 1 : b;
+}
+
+// Work-groups of `kernel` that fit on the device at once (all resident,
+// equal shares of the rows, no second round of a few groups), at most cap.
+template <typename K>
+int64_t resident_blocks(K kernel, int64_t cap) {
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, kBlk, 0) != hipSuccess || cus <= 0 || per <= 0)
+        return cap;
+    const int64_t r = (int64_t)cus * per;
+    return r < cap ? r : cap;
 }
 
 // ---------------------------------------------------------------------------
@@ -558,6 +660,8 @@ extern "C" int grws_act_norm_dropout_fwd(const void* z, int32_t z_dtype, int64_t
     GRWS_TRY(check_rowwise(z_dtype, out_dtype, rows, dim, ldz, ldo, z, out));
     const int steps = (int)((dim + 255) / 256);
     const int rpw = steps == 1 ? 4 : (steps == 2 ? 2 : 1);  // rows in flight per wave
+    // a few passes per wave (its next rows load during the current ones):
+    // measured faster than one pass per wave or a resident-only grid
     int64_t blocks = (rows + kRowsPerBlock * rpw - 1) / (kRowsPerBlock * rpw);
     if (blocks > 65536) blocks = 65536;
 #define GRWS_ANDF_SR(ZT, OT, S, R)                                                                              \
@@ -599,6 +703,7 @@ extern "C" int grws_act_norm_dropout_bwd(const void* dout, int32_t dout_dtype, i
     GRWS_CHECK_ARG(lddz >= dim && lddz % 4 == 0 && (reinterpret_cast<uintptr_t>(dz) % 8) == 0,
                    "act_norm_dropout: bad dz layout");
     const int64_t blocks = bwd_blocks(rows);
+    int64_t nb = blocks;  // launched work-groups: the resident count, at most `blocks`
     Carver cv(workspace, workspace_bytes);
     float* pg = cv.take<float>((size_t)blocks * (size_t)dim);
     float* pb = cv.take<float>((size_t)blocks * (size_t)dim);
@@ -606,9 +711,12 @@ extern "C" int grws_act_norm_dropout_bwd(const void* dout, int32_t dout_dtype, i
         return set_error(GRWS_E_CAPACITY, "act_norm_dropout: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
     const int steps = (int)((dim + 255) / 256);
 #define GRWS_ANDB_SR(GT, ZT, S, R)                                                                              \
-    hipLaunchKernelGGL((act_norm_dropout_bwd_kernel<GT, ZT, S, R>), dim3((unsigned)blocks), dim3(kBlk), 0, stream, \
-                       static_cast<const GT*>(dout), ldg, static_cast<const ZT*>(z), ldz, rows, (int)dim,          \
-                       (int)act, mean, rstd, gamma, p, seed, static_cast<ZT*>(dz), lddz, pg, pb)
+    do {                                                                                                         \
+        nb = resident_blocks(act_norm_dropout_bwd_kernel<GT, ZT, S, R>, blocks);                                 \
+        hipLaunchKernelGGL((act_norm_dropout_bwd_kernel<GT, ZT, S, R>), dim3((unsigned)nb), dim3(kBlk), 0, stream, \
+                           static_cast<const GT*>(dout), ldg, static_cast<const ZT*>(z), ldz, rows, (int)dim,      \
+                           (int)act, mean, rstd, gamma, p, seed, static_cast<ZT*>(dz), lddz, pg, pb);              \
+    } while (0)
 #define GRWS_ANDB(GT, ZT)                              \
     do {                                               \
         if (steps == 1) GRWS_ANDB_SR(GT, ZT, 1, 4);    \
@@ -621,9 +729,9 @@ extern "C" int grws_act_norm_dropout_bwd(const void* dout, int32_t dout_dtype, i
 #undef GRWS_ANDB_SR
     GRWS_LAUNCH_CHECK();
     const unsigned cb = (unsigned)((dim + 63) / 64);
-    hipLaunchKernelGGL(column_sum_kernel, dim3(cb), dim3(1024), 0, stream, pg, blocks, (int)dim, dgamma);
+    hipLaunchKernelGGL(column_sum_kernel, dim3(cb), dim3(1024), 0, stream, pg, nb, (int)dim, dgamma);
     GRWS_LAUNCH_CHECK();
-    hipLaunchKernelGGL(column_sum_kernel, dim3(cb), dim3(1024), 0, stream, pb, blocks, (int)dim, dbeta);
+    hipLaunchKernelGGL(column_sum_kernel, dim3(cb), dim3(1024), 0, stream, pb, nb, (int)dim, dbeta);
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }

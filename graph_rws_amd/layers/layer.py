@@ -154,15 +154,19 @@ class _GraphConvFunction(Function):
                 return y[:T]
             return F.pad(y, (0, 0, 0, T - y.shape[0]))
 
+        # the beta=1 GEMMs accumulate in place into a tensor this function
+        # made (no copy of it into a new output); in-place ops are not
+        # autocast, so the weights take the operands' dtype explicitly
         if ctx.agg_first:
             y, ms = _spmm_timed(graph, xh)
             yt = rows_T(y)
-            out = torch.addmm(torch.matmul(xt, w_s), yt, w_n)
+            out = torch.matmul(xt, w_s)
+            out.addmm_(yt, w_n.to(out.dtype))
             ctx.save_for_backward(yt, xt, w_n, w_s)
         else:
             y, ms = _spmm_timed(graph, torch.matmul(xh, w_n))
             yt = rows_T(y)
-            out = torch.addmm(yt, xt, w_s)
+            out = yt.addmm_(xt, w_s.to(yt.dtype))
             ctx.save_for_backward(xh, xt, w_n, w_s)
         record_spmm_time(ms)
         return out

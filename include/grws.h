@@ -447,13 +447,15 @@ int grws_repack_finish(const grws_bcsr* g, int64_t num_nodes, const int64_t* win
 /* Fused hidden-layer tail: out = dropout(LayerNorm(act(z))) per row, the   */
 /* sequence of models/model.py:259-264 (act, self.norms[l], dropout).  act  */
 /* 0 = identity, 1 = ReLU; LayerNorm over dim (biased variance, eps) with   */
-/* fp32 gamma/beta; dropout with probability p, scale 1/(1-p), mask from    */
-/* Philox4x32-10 keyed by seed (counter = row, column/4), recomputed by the */
-/* backward.  z/out/dout/dz in F32/F16/BF16; dim a multiple of 4, <= 1024;  */
-/* rows and leading dimensions multiples of 4 elements, 8-byte aligned.     */
-/* mean/rstd: fp32 [rows] saved for the backward (both NULL to skip).       */
-/* The backward writes dz (z's dtype) and fp32 dgamma/dbeta [dim], summed   */
-/* in a fixed order.                                                        */
+/* fp32 gamma/beta; dropout with probability p, scale 1/(1-p), element     */
+/* (r, c) kept iff word c%4 of Philox4x32-10 at counter (r_lo, r_hi, c/4,  */
+/* 0), key seed, is >= p * 2^32; the backward recomputes it.  z/out/dout/dz */
+/* in F32/F16/BF16; dim a multiple of 4, <= 1024; rows and leading          */
+/* dimensions multiples of 4 elements, 8-byte aligned.  mean/rstd: fp32     */
+/* [rows] saved for the backward (both NULL to skip).  The backward writes  */
+/* dz (z's dtype) and fp32 dgamma/dbeta [dim], summed in a fixed order for  */
+/* a given device (the number of partial sums is the device's resident      */
+/* work-group count).                                                       */
 /* ------------------------------------------------------------------------ */
 int grws_act_norm_dropout_fwd(const void* z, int32_t z_dtype, int64_t ldz, int64_t rows, int64_t dim,
                               int32_t act, const float* gamma, const float* beta, float eps, float p,
