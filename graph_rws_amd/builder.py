@@ -141,8 +141,13 @@ def transpose(graph):
     from .data.bcsr import BCSRGraph
     win, cols, vals = transpose_arrays(graph.window_offset, graph.original_col_indices,
                                        graph.values_condensed, graph.tile_cols, graph.num_cols)
-    return BCSRGraph(num_nodes=graph.num_cols, num_edges=graph.num_edges, tile_rows=16,
-                     tile_cols=graph.tile_cols, window_offset=win, original_col_indices=cols,
-                     values_condensed=vals, device=graph.window_offset.device,
-                     num_rows=graph.num_cols, num_cols=16 * graph.num_windows,
-                     values_dtype=graph.values_condensed.dtype)
+    AT = BCSRGraph(num_nodes=graph.num_cols, num_edges=graph.num_edges, tile_rows=16,
+                   tile_cols=graph.tile_cols, window_offset=win, original_col_indices=cols,
+                   values_condensed=vals, device=graph.window_offset.device,
+                   num_rows=graph.num_cols, num_cols=16 * graph.num_windows,
+                   values_dtype=graph.values_condensed.dtype)
+    # the longest window (one sync, here rather than at the first product):
+    # lets a small transpose (a sampled block's) skip the SpMM work plan
+    if win.numel() > 1:
+        AT.max_window_slabs = (int((win[1:] - win[:-1]).max().item()) * graph.tile_cols + 15) // 16
+    return AT

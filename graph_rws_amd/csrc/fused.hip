@@ -366,8 +366,10 @@ __global__ __launch_bounds__(1024) void column_sum_kernel(const float* __restric
     const int wave = threadIdx.x >> 6;
     const int c = blockIdx.x * 64 + lane;
     float s = 0.f;
-    if (c < dim)
+    if (c < dim) {
+#pragma unroll 8
         for (int64_t k = wave; k < nparts; k += 16) s += part[k * dim + c];
+    }
     red[wave][lane] = s;
     __syncthreads();
     if (wave == 0 && c < dim) {
