@@ -28,7 +28,7 @@ class BcsrView(ctypes.Structure):
     _fields_ = [("window_offset", _vp), ("col_indices", _vp), ("values", _vp),
                 ("num_windows", ctypes.c_int64), ("num_tiles", ctypes.c_int64),
                 ("tile_rows", ctypes.c_int32), ("tile_cols", ctypes.c_int32),
-                ("values_dtype", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("values_dtype", ctypes.c_int32), ("max_window_slabs", ctypes.c_int32)]
 
 
 class PackedTilesView(ctypes.Structure):

@@ -188,10 +188,13 @@ def _check_graph(window_offset, col_indices, values, tile_cols):
 
 def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.Tensor,
          x: torch.Tensor, tile_cols: int, plan: Optional[SpmmPlan] = None,
-         out: Optional[torch.Tensor] = None, packed: Optional[PackedTiles] = None) -> torch.Tensor:
+         out: Optional[torch.Tensor] = None, packed: Optional[PackedTiles] = None,
+         max_window_slabs: int = 0) -> torch.Tensor:
     """Y[16W, N] = A X on the device (H1 kernel).  x: [x_rows, N] (row stride
     may exceed N); out dtype = x dtype.  packed: the graph's packed tiles
-    (read instead of the dense values when x has the values' dtype)."""
+    (read instead of the dense values when x has the values' dtype).
+    max_window_slabs: an upper bound of every window's slabs when known
+    (0 = unknown); lets a call without a plan use the buffer-load kernel."""
     _check_graph(window_offset, col_indices, values, tile_cols)
     if not x.is_cuda:
         raise RuntimeError("input_B must be a CUDA tensor")
@@ -209,7 +212,8 @@ def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.T
         # Run on X widened to the next multiple and hand back the first N
         # columns of the result (columns are independent).
         x = _widen(x, vec)
-        full = spmm(window_offset, col_indices, values, x, tile_cols, plan=plan, packed=packed)
+        full = spmm(window_offset, col_indices, values, x, tile_cols, plan=plan, packed=packed,
+                    max_window_slabs=max_window_slabs)
         return full[:, :N]
     if out is None:
         out = torch.empty((W * 16, N), dtype=x.dtype, device=x.device)
@@ -218,7 +222,8 @@ def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.T
     if W == 0 or N == 0:
         return out
     view = L.BcsrView(L.ptr(window_offset), L.ptr(col_indices), L.ptr(values), W,
-                      col_indices.numel() // tile_cols, 16, tile_cols, L.dtype_code(values.dtype), 0)
+                      col_indices.numel() // tile_cols, 16, tile_cols, L.dtype_code(values.dtype),
+                      int(min(max(0, max_window_slabs), 2**31 - 1)))
     pv = None
     ws = None
     wsb = 0

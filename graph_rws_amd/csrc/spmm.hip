@@ -874,7 +874,8 @@ int dispatch_buf_tc(const SpmmArgs& a, int tc, int nblk, hipStream_t stream) {
 // Whether the buffer-load kernel's 32-bit offsets cover this call: rows and
 // row pitch below 2^24 (24-bit multiply), 2 (x_rows + 1) rows below 2^32 bytes,
 // and every work item's A below 2^31 bytes (an item spans at most the
-// plan's slabs_per_item slabs, or a whole window without a plan).
+// plan's slabs_per_item slabs, or without a plan a whole window: at most
+// A->max_window_slabs when the caller knows it, else the whole graph).
 bool buffer_path_fits(const grws_bcsr* A, const grws_spmm_plan* plan, int64_t x_rows, int64_t ldx, int64_t nc,
                       size_t esz) {
     if (const char* e = getenv("GRWS_SPMM_KERNEL"))  // tuning override: 1 = element-masked kernel
@@ -883,8 +884,9 @@ bool buffer_path_fits(const grws_bcsr* A, const grws_spmm_plan* plan, int64_t x_
     if (x_rows <= 0 || x_rows >= (1 << 24) || ldxb >= (1 << 24)) return false;
     if (2 * (x_rows + 1) * ldxb + nc * (int64_t)esz >= ((int64_t)1 << 32)) return false;
     const int64_t sza = A->values_dtype == GRWS_F32 ? 4 : 2;
-    const int64_t slabs = plan && plan->items ? (int64_t)plan->slabs_per_item
-                                              : (A->num_tiles * A->tile_cols + 15) / 16 + 1;
+    const int64_t slabs = plan && plan->items      ? (int64_t)plan->slabs_per_item
+                          : A->max_window_slabs > 0 ? (int64_t)A->max_window_slabs
+                                                   : (A->num_tiles * A->tile_cols + 15) / 16 + 1;
     return (slabs + 4) * 256 * sza < ((int64_t)1 << 31);
 }
 

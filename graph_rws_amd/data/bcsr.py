@@ -275,7 +275,8 @@ class BCSRGraph:
         from ..core import spmm as _spmm
         return _spmm(self.window_offset, self.original_col_indices, self.values_condensed, x,
                      self.tile_cols, plan=self.spmm_plan(x.shape[1]), out=out,
-                     packed=self.packed_tiles() if x.dtype == self.values_condensed.dtype else None)
+                     packed=self.packed_tiles() if x.dtype == self.values_condensed.dtype else None,
+                     max_window_slabs=getattr(self, "max_window_slabs", None) or 0)
 
     def transpose(self) -> "BCSRGraph":
         """Cached BCSR of A^T (num_cols x 16W), built on the device.  Rebuilt

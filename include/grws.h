@@ -70,7 +70,9 @@ typedef struct grws_bcsr {
     int32_t tile_rows;    /* must be 16 */
     int32_t tile_cols;    /* 8 or 16 */
     int32_t values_dtype; /* GRWS_F32 / GRWS_F16 / GRWS_BF16 */
-    int32_t reserved;
+    int32_t max_window_slabs; /* 0 = unknown; else an upper bound of every window's
+                                 slabs (16 column slots), used by a plan-less grws_spmm to
+                                 size its 32-bit offsets.  A wrong bound gives wrong sums. */
 } grws_bcsr;
 
 /*
