@@ -10,8 +10,12 @@
 //   * work-group (M-tile of 128, N-tile of 128, K-chunk): 4 wave64s, each a
 //     64 x 64 block of the output as 4 x 4 v_mfma_f32_16x16x16 tiles;
 //   * per step, 32 rows of A and B (128 columns each) are loaded with
-//     16-byte coalesced loads and staged in LDS; the MFMA fragments are read
-//     from LDS (A^T needs A's columns, 4 consecutive k per lane);
+//     16-byte coalesced loads into two alternating LDS stages; the next
+//     step's rows are loaded into registers while the current stage is
+//     multiplied;
+//   * both MFMA operands are columns of the staged rows (A^T needs A's
+//     columns, 4 consecutive k per lane), read with gfx950's transposing
+//     LDS read: one ds_read_b64_tr_b16 per operand per 16 k;
 //   * every chunk writes an fp32 partial; a second kernel adds the chunks
 //     in order (deterministic, no atomics) and writes C.
 // A and B are each read once per N-tile / M-tile of the other operand.
@@ -24,6 +28,10 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 tr_v4f16_t;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 tr_v4bf16_t;
+typedef __attribute__((address_space(3))) tr_v4f16_t lds_v4f16_t;
+typedef __attribute__((address_space(3))) tr_v4bf16_t lds_v4bf16_t;
 
 constexpr int kT = 128;       // output tile edge
 constexpr int kStep = 32;     // K rows per LDS stage
@@ -31,13 +39,30 @@ constexpr int kPitch = kT + 8;  // LDS row pitch (elements)
 constexpr int kMaxChunks = 512;
 constexpr int64_t kMinChunkRows = 1024;
 
+// Column block of 16 (columns c0..c0+15) of rows k..k+15 of a staged
+// operand as the MFMA's 16x16x16 operand: lane (g, i) gets rows 4g..4g+3 of
+// column c0 + i.  The 16 lanes of a group read 4 halves each at row
+// 4g + (lane%16)/4, column c0 + 4 (lane%4); the transposing read hands
+// lane i column i of the group's 4 rows.
+template <int DT>
+__device__ __forceinline__ short4_t lds_col_frag(const uint16_t* stage, int k, int c0, int lane) {
+    const uint16_t* p = stage + (k + 4 * (lane >> 4) + ((lane & 15) >> 2)) * kPitch + c0 + 4 * (lane & 3);
+    if constexpr (DT == GRWS_F16) {
+        return __builtin_bit_cast(short4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                                (lds_v4f16_t*)(__attribute__((address_space(3))) void*)p));
+    } else {
+        return __builtin_bit_cast(short4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                                                (lds_v4bf16_t*)(__attribute__((address_space(3))) void*)p));
+    }
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                               const uint16_t* __restrict__ B, int64_t ldb,
                                                               int64_t K, int M, int N, int64_t kc,
                                                               float* __restrict__ partials) {
-    __shared__ __attribute__((aligned(16))) uint16_t sA[kStep * kPitch];
-    __shared__ __attribute__((aligned(16))) uint16_t sB[kStep * kPitch];
+    __shared__ __attribute__((aligned(16))) uint16_t sA[2][kStep * kPitch];
+    __shared__ __attribute__((aligned(16))) uint16_t sB[2][kStep * kPitch];
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
@@ -48,8 +73,8 @@ __global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const uint16_t* __
     const int64_t ke = kb + kc < K ? kb + kc : K;
     const int wm = (wave & 1) * 64;
     const int wn = (wave >> 1) * 64;
-    const int fr = lane & 15;      // fragment row / column within a 16 x 16 tile
-    const int fk = (lane >> 4) * 4;  // first of the lane's 4 consecutive k
+    const int fr = lane & 15;        // output column within a 16 x 16 tile
+    const int fk = (lane >> 4) * 4;  // first output row of the lane within a tile
 
     float4_t acc[4][4];
 #pragma unroll
@@ -59,29 +84,39 @@ __global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const uint16_t* __
 
     // staging geometry: 32 rows x 128 columns = 512 loads of 8 elements,
     // two per thread for each operand
-    for (int64_t k0 = kb; k0 < ke; k0 += kStep) {
+    u32x4_t ra[2], rb[2];
+    auto fetch = [&](int64_t k0) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int e = (tid + 256 * q) * 8;
             const int r = e / kT, c = e % kT;
             const int64_t k = k0 + r;
             const bool okr = k < ke;
-            u32x4_t va = {0u, 0u, 0u, 0u}, vb = {0u, 0u, 0u, 0u};
-            if (okr && i0 + c < M) va = *reinterpret_cast<const u32x4_t*>(A + k * lda + i0 + c);
-            if (okr && j0 + c < N) vb = *reinterpret_cast<const u32x4_t*>(B + k * ldb + j0 + c);
-            *reinterpret_cast<u32x4_t*>(&sA[r * kPitch + c]) = va;
-            *reinterpret_cast<u32x4_t*>(&sB[r * kPitch + c]) = vb;
+            ra[q] = u32x4_t{0u, 0u, 0u, 0u};
+            rb[q] = u32x4_t{0u, 0u, 0u, 0u};
+            if (okr && i0 + c < M) ra[q] = *reinterpret_cast<const u32x4_t*>(A + k * lda + i0 + c);
+            if (okr && j0 + c < N) rb[q] = *reinterpret_cast<const u32x4_t*>(B + k * ldb + j0 + c);
         }
-        __syncthreads();
+    };
+    int buf = 0;
+    if (kb < ke) fetch(kb);
+    for (int64_t k0 = kb; k0 < ke; k0 += kStep) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int e = (tid + 256 * q) * 8;
+            const int r = e / kT, c = e % kT;
+            *reinterpret_cast<u32x4_t*>(&sA[buf][r * kPitch + c]) = ra[q];
+            *reinterpret_cast<u32x4_t*>(&sB[buf][r * kPitch + c]) = rb[q];
+        }
+        __syncthreads();  // the stage is written; the other stage's readers are done
+        if (k0 + kStep < ke) fetch(k0 + kStep);
 #pragma unroll
         for (int ks = 0; ks < kStep; ks += 16) {
             short4_t af[4], bf[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const uint16_t* pa = &sA[(ks + fk) * kPitch + wm + 16 * t + fr];
-                const uint16_t* pb = &sB[(ks + fk) * kPitch + wn + 16 * t + fr];
-                af[t] = short4_t{(short)pa[0], (short)pa[kPitch], (short)pa[2 * kPitch], (short)pa[3 * kPitch]};
-                bf[t] = short4_t{(short)pb[0], (short)pb[kPitch], (short)pb[2 * kPitch], (short)pb[3 * kPitch]};
+                af[t] = lds_col_frag<DT>(sA[buf], ks, wm + 16 * t, lane);
+                bf[t] = lds_col_frag<DT>(sB[buf], ks, wn + 16 * t, lane);
             }
 #pragma unroll
             for (int a = 0; a < 4; ++a)
@@ -95,7 +130,7 @@ __global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const uint16_t* __
                         acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(af[a], bf[b], acc[a][b], 0, 0, 0);
                 }
         }
-        __syncthreads();
+        buf ^= 1;
     }
     // D layout: lane l, element e -> row 4*(l/16)+e, column l%16 of the tile
     float* P = partials + chunk * (int64_t)M * N;
@@ -112,22 +147,36 @@ __global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const uint16_t* __
         }
 }
 
-// C[i][j] = sum over chunks, in chunk order.
+// C[i][j] = sum over chunks.  A work-group of 16 waves covers 64
+// consecutive outputs; wave w adds chunks w, w+16, ... in order (coalesced
+// 256-byte rows), then wave 0 adds the 16 wave sums in order: a fixed order
+// (deterministic), with 16 waves' loads in flight per output group.
 template <int OT>
-__global__ void gemm_tn_reduce_kernel(const float* __restrict__ partials, int64_t nchunks, int M, int N, void* c,
-                                      int64_t ldc) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (int64_t)M * N) return;
+__global__ __launch_bounds__(1024) void gemm_tn_reduce_kernel(const float* __restrict__ partials, int64_t nchunks,
+                                                              int M, int N, void* c, int64_t ldc) {
+    __shared__ float red[16][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int64_t mn = (int64_t)M * N;
+    const int64_t idx = (int64_t)blockIdx.x * 64 + lane;
     float s = 0.f;
-    for (int64_t ch = 0; ch < nchunks; ++ch) s += partials[ch * mn + idx];
+    if (idx < mn) {
+#pragma unroll 8
+        for (int64_t ch = wave; ch < nchunks; ch += 16) s += partials[ch * mn + idx];
+    }
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave != 0 || idx >= mn) return;
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) t += red[w][lane];
     const int64_t i = idx / N, j = idx % N;
     if constexpr (OT == GRWS_F32) {
-        static_cast<float*>(c)[i * ldc + j] = s;
+        static_cast<float*>(c)[i * ldc + j] = t;
     } else if constexpr (OT == GRWS_F16) {
-        static_cast<_Float16*>(c)[i * ldc + j] = (_Float16)s;
+        static_cast<_Float16*>(c)[i * ldc + j] = (_Float16)t;
     } else {
-        static_cast<__hip_bfloat16*>(c)[i * ldc + j] = __float2bfloat16(s);
+        static_cast<__hip_bfloat16*>(c)[i * ldc + j] = __float2bfloat16(t);
     }
 }
 
@@ -188,18 +237,18 @@ extern "C" int grws_gemm_tn(const void* a, int64_t lda, const void* b, int64_t l
         GRWS_LAUNCH_CHECK();
     }
     {
-        const unsigned rg = (unsigned)((M * N + 255) / 256);
+        const unsigned rg = (unsigned)((M * N + 63) / 64);
         switch (out_dtype) {
             case GRWS_F32:
-                hipLaunchKernelGGL(gemm_tn_reduce_kernel<GRWS_F32>, dim3(rg), dim3(256), 0, stream,
+                hipLaunchKernelGGL(gemm_tn_reduce_kernel<GRWS_F32>, dim3(rg), dim3(1024), 0, stream,
                                    static_cast<const float*>(workspace), chunks, (int)M, (int)N, c, ldc);
                 break;
             case GRWS_F16:
-                hipLaunchKernelGGL(gemm_tn_reduce_kernel<GRWS_F16>, dim3(rg), dim3(256), 0, stream,
+                hipLaunchKernelGGL(gemm_tn_reduce_kernel<GRWS_F16>, dim3(rg), dim3(1024), 0, stream,
                                    static_cast<const float*>(workspace), chunks, (int)M, (int)N, c, ldc);
                 break;
             default:
-                hipLaunchKernelGGL(gemm_tn_reduce_kernel<GRWS_BF16>, dim3(rg), dim3(256), 0, stream,
+                hipLaunchKernelGGL(gemm_tn_reduce_kernel<GRWS_BF16>, dim3(rg), dim3(1024), 0, stream,
                                    static_cast<const float*>(workspace), chunks, (int)M, (int)N, c, ldc);
                 break;
         }
