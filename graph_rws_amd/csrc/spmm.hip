@@ -1113,11 +1113,6 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
     if (y_dtype != x_dtype) return set_error(GRWS_E_DTYPE, "spmm: y dtype must equal x dtype");
     if (A->values_dtype != GRWS_F32 && A->values_dtype != x_dtype)
         return set_error(GRWS_E_DTYPE, "spmm: values dtype must be F32 or the x dtype");
-    if (A->num_windows == 0 || n_cols == 0) return GRWS_OK;
-    GRWS_CHECK_ARG(A->window_offset && y, "spmm: null pointer");
-    GRWS_CHECK_ARG(ldy >= n_cols, "spmm: ldy < n_cols");
-    if (x_rows > 0) GRWS_CHECK_ARG(x != nullptr && ldx >= n_cols, "spmm: bad x (null or ldx < n_cols)");
-    if (A->num_tiles > 0) GRWS_CHECK_ARG(A->col_indices && A->values, "spmm: null tile arrays");
     if (P) {
         GRWS_CHECK_ARG(A->tile_cols == 16 && x_dtype != GRWS_F32 && A->values_dtype == x_dtype,
                        "spmm_packed: packed tiles need 16x16 tiles whose values have the x dtype");
@@ -1127,6 +1122,11 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
                        "spmm_packed: null packed arrays");
         GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(P->header) % 4 == 0, "spmm_packed: header not 4-byte aligned");
     }
+    if (A->num_windows == 0 || n_cols == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(A->window_offset && y, "spmm: null pointer");
+    GRWS_CHECK_ARG(ldy >= n_cols, "spmm: ldy < n_cols");
+    if (x_rows > 0) GRWS_CHECK_ARG(x != nullptr && ldx >= n_cols, "spmm: bad x (null or ldx < n_cols)");
+    if (A->num_tiles > 0) GRWS_CHECK_ARG(A->col_indices && A->values, "spmm: null tile arrays");
 
     const size_t esz = dtype_size(x_dtype);
     const int64_t vec = (int64_t)(16 / esz);

@@ -159,3 +159,36 @@ def test_aligned_rows_keeps_values_and_pads_pitch():
     assert y.stride() == (640, 1) and y.shape == x.shape and torch.equal(x, y)
     z = torch.randn(3, 256)  # 1024 B rows: already aligned, returned as is
     assert aligned_rows(z) is z
+
+
+def test_packed_tiles_reject_bad_arguments_without_launching():
+    """Packing needs 16x16 tiles of 16-bit values; grws_spmm_packed needs
+    values of the x dtype and a sane value count.  All refused on the host."""
+    lib = L.load()
+    n = ctypes.c_int64()
+    st = lib.grws_pack_tiles_count(None, None, 0, ctypes.byref(n), None)
+    assert st == -1 and b"null graph" in lib.grws_last_error()
+    view = L.BcsrView(None, None, None, 4, 10, 16, 8, L.GRWS_F16, 0)
+    st = lib.grws_pack_tiles_count(ctypes.byref(view), None, 0, ctypes.byref(n), None)
+    assert st == -1 and b"16x16" in lib.grws_last_error()
+    view = L.BcsrView(None, None, None, 4, 10, 16, 16, L.GRWS_F32, 0)
+    st = lib.grws_pack_tiles_count(ctypes.byref(view), None, 0, ctypes.byref(n), None)
+    assert st == -2
+    view = L.BcsrView(None, None, None, 4, 0, 16, 16, L.GRWS_F16, 0)  # no tiles: nothing to count
+    assert lib.grws_pack_tiles_count(ctypes.byref(view), None, 0, ctypes.byref(n), None) == 0
+    assert n.value == 0
+    st = lib.grws_pack_tiles_fill(ctypes.byref(view), None, None, -1, None, 0, None)
+    assert st == -1 and b"num_values" in lib.grws_last_error()
+    assert lib.grws_pack_tiles_workspace_bytes(-1) == 0
+    assert lib.grws_pack_tiles_workspace_bytes(1000) > 1000 * 12
+    # grws_spmm_packed: f32 values with packed tiles, and a negative value count
+    pk = L.PackedTilesView(None, None, 0)
+    view = L.BcsrView(None, None, None, 4, 10, 16, 16, L.GRWS_F32, 0)
+    st = lib.grws_spmm_packed(ctypes.byref(view), ctypes.byref(pk), None, None, L.GRWS_F16, 0, 8, 8, None,
+                              L.GRWS_F16, 8, None, 0, None)
+    assert st == -1 and b"packed tiles need" in lib.grws_last_error()
+    pk = L.PackedTilesView(None, None, -5)
+    view = L.BcsrView(None, None, None, 4, 10, 16, 16, L.GRWS_F16, 0)
+    st = lib.grws_spmm_packed(ctypes.byref(view), ctypes.byref(pk), None, None, L.GRWS_F16, 0, 8, 8, None,
+                              L.GRWS_F16, 8, None, 0, None)
+    assert st == -1 and b"num_values" in lib.grws_last_error()
