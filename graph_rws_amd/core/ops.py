@@ -97,7 +97,9 @@ def _widen(t: torch.Tensor, vec: int) -> torch.Tensor:
     """t [R, C] as [R, C'] with C' = C rounded up to a multiple of vec,
     16-byte aligned rows: a strided view over the row padding t already
     has when its storage covers it (the extra columns then hold whatever
-    the padding holds), otherwise a zero-padded copy.  Callers use the
+    the padding holds), otherwise a zero-padded copy whose rows start on
+    128-byte lines (a 96-byte row at a 96-byte pitch straddles lines: the
+    SpMM's gathers of such rows ran up to 26% slower).  Callers use the
     first C columns of any result that is column-separable."""
     R, C = t.shape
     Cp = -(-C // vec) * vec
@@ -108,9 +110,11 @@ def _widen(t: torch.Tensor, vec: int) -> torch.Tensor:
             and t.data_ptr() % 16 == 0 \
             and (t.storage_offset() + (R - 1) * t.stride(0) + Cp) * esz <= t.untyped_storage().nbytes():
         return t.as_strided((R, Cp), (t.stride(0), 1))
-    out = torch.zeros((R, Cp), dtype=t.dtype, device=t.device)
+    per = 128 // esz
+    pitch = -(-Cp // per) * per
+    out = torch.zeros((R, pitch), dtype=t.dtype, device=t.device)
     out[:, :C] = t
-    return out
+    return out[:, :Cp]
 
 
 # ---------------------------------------------------------------------------

@@ -204,3 +204,45 @@ def test_spmm_wide_split_launches(cuda_device, xdt, N, slabs):
         Y = core.spmm(G.window_offset, G.original_col_indices, G.values_condensed, X, 16, plan=plan)
     torch.cuda.synchronize()
     _check(G, X, Y, xdt)
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+def test_gather_input_aligned_copy(cuda_device, xdt):
+    """A graph that gathers each row many times multiplies X through a copy
+    whose rows start on 128-byte lines when X's pitch is not a multiple of
+    128 bytes (112 columns here): same bits as the product on X itself, the
+    copy is kept while X is alive and unmodified, and redone after an
+    in-place change."""
+    print(f"case aligned-copy xdt={xdt}", flush=True)
+    g = synth.chung_lu(3000, 200000, 2.1, seed=4)
+    G = _bcsr(g, 16, cuda_device, vdt=xdt)
+    assert G.num_tiles * 16 >= 8 * g.num_nodes
+    X = synth.features(g.num_nodes, 112, seed=8, device=cuda_device).to(xdt)
+    assert X.stride(0) * X.element_size() % 128 != 0
+    args = (G.window_offset, G.original_col_indices, G.values_condensed)
+    ref = core.spmm(*args, X, 16, plan=G.spmm_plan(112))       # the kernel on the 224-byte pitch
+    Y = G.spmm(X)
+    xa = G._cache["aligned_x"][2]
+    assert xa.stride(0) * xa.element_size() % 128 == 0 and torch.equal(xa, X)
+    Y2 = G.spmm(X)
+    assert G._cache["aligned_x"][2] is xa                       # reused
+    torch.cuda.synchronize()
+    assert torch.equal(Y.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(Y2.view(torch.int16), ref.view(torch.int16))
+    with torch.no_grad():
+        X.mul_(2)
+    Y3 = G.spmm(X)
+    assert G._cache["aligned_x"][2] is not xa
+    ref3 = core.spmm(*args, X, 16, plan=G.spmm_plan(112))
+    torch.cuda.synchronize()
+    assert torch.equal(Y3.view(torch.int16), ref3.view(torch.int16))
+
+
+def test_ragged_width_copy_is_line_aligned(cuda_device):
+    """A ragged width widened by copy gets 128-byte row pitch (41 -> 48
+    columns at a 64-element pitch)."""
+    from graph_rws_amd.core.ops import _widen
+    x = torch.randn(1000, 41, device=cuda_device).half()
+    w = _widen(x, 8)
+    assert w.shape == (1000, 48) and w.stride(0) == 64
+    assert torch.equal(w[:, :41], x) and not bool(w[:, 41:].any())
