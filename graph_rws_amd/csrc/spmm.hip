@@ -435,18 +435,22 @@ __global__ __launch_bounds__(64 * WPB) void spmm_fwd_kernel(SpmmArgs a) {
 // dependent value read, which so adds no wait of its own.
 template <int XT, bool AF32, int TC, int NBLK, int WPB, int PF, bool PK = false>
 __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
-    static_assert(XT == GRWS_F16 || XT == GRWS_BF16, "16-bit X only");
+    static_assert(XT == GRWS_F16 || XT == GRWS_BF16 || (XT == GRWS_F32 && AF32 && !PK),
+                  "16-bit X, or fp32 X with fp32 values");
     static_assert(TC == 8 || TC == 16, "tile_cols must be 8 or 16");
     static_assert(PF >= 1 && PF <= 2, "prefetch depth 1..2");
     static_assert(!PK || (TC == 16 && !AF32), "packed tiles: 16x16 tiles of 16-bit values");
     using S = typename XTraits<XT>::S;
-    constexpr int SZ = 2;
+    constexpr bool XF32 = XT == GRWS_F32;
+    constexpr int SZ = XTraits<XT>::SZ;
     constexpr int SZA = AF32 ? 4 : 2;
     constexpr int NC = NBLK * 16;               // output columns per work-group
-    constexpr int VEC = 8;                      // elements per 16-byte load
+    constexpr int VEC = 16 / SZ;                // elements per 16-byte load
     constexpr int LPR = NC / VEC;               // lanes per staged row
     constexpr int NLD = (16 * LPR + 63) / 64;   // rows (loads) per lane per slab
-    constexpr int PITCH = NC + 16;              // LDS row pitch (elements)
+    // LDS row pitch (elements).  fp32: the 4 k-groups of a B read (rows
+    // 4g + q, g = 0..3) then start 16 banks apart (no conflict)
+    constexpr int PITCH = XF32 ? NC + 4 : NC + 16;
     static_assert(NLD == 1 || NLD == 2 || NLD == 4 || NLD == 8, "rows per lane");
     constexpr int R = PF + 1;
     static_assert(WPB == 1 || WPB * 16 * PITCH * SZ >= 16 * NC * 4, "stage too small to reduce in");
@@ -606,6 +610,18 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if constexpr (XF32) {
+            // v_mfma_f32_16x16x4f32: lane (ag, ar) holds A[ar][4ag + q] for the
+            // q-th of 4 MFMAs, and reads B[4ag + q][16b + ar] from the stage
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+#pragma unroll
+                for (int b = 0; b < NBLK; ++b) {
+                    const float bv = stage[(4 * ag + q) * PITCH + b * 16 + ar];
+                    acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a_cur[q], bv, acc[b], 0, 0, 0);
+                }
+            }
+        } else {
         short4_t af;
         if constexpr (PK) {
             const uint32_t info = a_cur[3];
@@ -644,6 +660,7 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
                                                                      (lds_v4bf16_t*)p));
                 acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(af, bf, acc[b], 0, 0, 0);
             }
+        }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -853,8 +870,10 @@ int dispatch_buf(const SpmmArgs& a, int nblk, hipStream_t stream) {
         case 4:
             return two ? launch_buf<XT, AF32, TC, 4, 2, PK>(a, stream) : launch_buf<XT, AF32, TC, 4, 1, PK>(a, stream);
         case 16:
-            return two ? launch_buf<XT, AF32, TC, 16, 2, PK>(a, stream)
-                       : launch_buf<XT, AF32, TC, 16, 1, PK>(a, stream);
+            if constexpr (XT != GRWS_F32)  // fp32 chunks stop at 128 columns
+                return two ? launch_buf<XT, AF32, TC, 16, 2, PK>(a, stream)
+                           : launch_buf<XT, AF32, TC, 16, 1, PK>(a, stream);
+            [[fallthrough]];
         default:
             return two ? launch_buf<XT, AF32, TC, 8, 2, PK>(a, stream) : launch_buf<XT, AF32, TC, 8, 1, PK>(a, stream);
     }
@@ -1131,7 +1150,7 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
     const size_t esz = dtype_size(x_dtype);
     const int64_t vec = (int64_t)(16 / esz);
     const bool vect = (n_cols % vec == 0) && (ldx % vec == 0) && ((reinterpret_cast<uintptr_t>(x) % 16) == 0);
-    const bool use_buf = x_dtype != GRWS_F32 && vect && buffer_path_fits(A, plan, x_rows, ldx, 256, esz);
+    const bool use_buf = vect && buffer_path_fits(A, plan, x_rows, ldx, 256, esz);
     const int nblk = nblk_for(n_cols, x_dtype, use_buf);
     const int64_t nc = nblk * 16;
     SpmmArgs a{};
@@ -1178,7 +1197,8 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
         // whole multiples, then one narrower launch for the rest, so A is
         // streamed once per 256 columns and no chunk is mostly empty
         const bool forced = getenv("GRWS_SPMM_NBLK") != nullptr;
-        const int64_t head = (!forced && n_cols > 256 && n_cols % 256 != 0) ? n_cols / 256 * 256 : 0;
+        const int64_t head =
+            (!forced && x_dtype != GRWS_F32 && n_cols > 256 && n_cols % 256 != 0) ? n_cols / 256 * 256 : 0;
         const int64_t parts[2][2] = {{0, head > 0 ? head : n_cols}, {head, n_cols}};
         for (int pi = 0; pi < (head > 0 ? 2 : 1); ++pi) {
             const int64_t c0 = parts[pi][0], c1 = parts[pi][1];
@@ -1186,7 +1206,9 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
             const int64_t pnc = pnblk * 16;
             a.col_base = c0;
             a.nchunks = (int32_t)((c1 - c0 + pnc - 1) / pnc);
-            if (x_dtype == GRWS_F16)
+            if (x_dtype == GRWS_F32)  // fp32 X: fp32 values (checked above)
+                st = dispatch_buf_tc<GRWS_F32, true>(a, tc, pnblk, stream);
+            else if (x_dtype == GRWS_F16)
                 st = af32 ? dispatch_buf_tc<GRWS_F16, true>(a, tc, pnblk, stream)
                           : dispatch_buf_tc<GRWS_F16, false>(a, tc, pnblk, stream);
             else
@@ -1194,8 +1216,9 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
                           : dispatch_buf_tc<GRWS_BF16, false>(a, tc, pnblk, stream);
             if (st != GRWS_OK) return st;
             if (plan && plan->num_split > 0) {
-                st = x_dtype == GRWS_F16 ? launch_fixup<GRWS_F16>(plan, a, pnblk, stream)
-                                         : launch_fixup<GRWS_BF16>(plan, a, pnblk, stream);
+                st = x_dtype == GRWS_F32   ? launch_fixup<GRWS_F32>(plan, a, pnblk, stream)
+                     : x_dtype == GRWS_F16 ? launch_fixup<GRWS_F16>(plan, a, pnblk, stream)
+                                           : launch_fixup<GRWS_BF16>(plan, a, pnblk, stream);
                 if (st != GRWS_OK) return st;
             }
         }

@@ -246,3 +246,32 @@ def test_ragged_width_copy_is_line_aligned(cuda_device):
     w = _widen(x, 8)
     assert w.shape == (1000, 48) and w.stride(0) == 64
     assert torch.equal(w[:, :41], x) and not bool(w[:, 41:].any())
+
+
+@pytest.mark.parametrize("tc", [8, 16])
+@pytest.mark.parametrize("N", [4, 16, 64, 128, 200])
+@pytest.mark.parametrize("slabs", [None, 2])
+def test_fp32_buffer_kernel_equals_element_masked(cuda_device, tc, N, slabs):
+    """fp32 X runs the buffer-load kernel (v_mfma_f32_16x16x4f32, the same
+    MFMA sequence as the element-masked kernel): the same bits as the
+    element-masked kernel, forced with GRWS_SPMM_KERNEL=1."""
+    import os
+    print(f"case fp32 buf tc={tc} N={N} slabs={slabs}", flush=True)
+    g = synth.chung_lu(2500, 30000, 2.1, seed=N + tc)
+    G = _bcsr(g, tc, cuda_device)
+    plan = None if slabs is None else core.build_spmm_plan(G.window_offset, G.num_tiles, tc, slabs)
+    X = synth.features(g.num_nodes, N, seed=N, device=cuda_device)
+    args = (G.window_offset, G.original_col_indices, G.values_condensed, X, tc)
+    Yb = core.spmm(*args, plan=plan)
+    old = os.environ.get("GRWS_SPMM_KERNEL")
+    os.environ["GRWS_SPMM_KERNEL"] = "1"
+    try:
+        Ye = core.spmm(*args, plan=plan)
+        torch.cuda.synchronize()
+    finally:
+        if old is None:
+            del os.environ["GRWS_SPMM_KERNEL"]
+        else:
+            os.environ["GRWS_SPMM_KERNEL"] = old
+    assert torch.equal(Yb.view(torch.int32), Ye.view(torch.int32))
+    _check(G, X, Yb, torch.float32)
