@@ -8,6 +8,7 @@ allocated here with torch's caching allocator; the library allocates nothing.
 from __future__ import annotations
 
 import ctypes
+import weakref
 import os
 from typing import Optional, Tuple
 
@@ -66,6 +67,24 @@ def build_spmm_plan(window_offset: torch.Tensor, num_tiles: int, tile_cols: int,
            L.ptr(items), mi.value, L.ptr(split), ms.value, L.ptr(ws), wsb,
            ctypes.cast(counts, ctypes.POINTER(ctypes.c_int64)), L.stream_of(dev))
     return SpmmPlan(items, split, list(counts), slabs_per_item)
+
+
+class TensorKey:
+    """Cache key over tensors: valid while they are the same objects, not
+    modified in place since (weak references, so a cache keeps nothing
+    alive; an address reused by a new tensor does not match), plus plain
+    values."""
+
+    __slots__ = ("refs", "versions", "extra")
+
+    def __init__(self, tensors, extra=()):
+        self.refs = tuple(weakref.ref(t) for t in tensors)
+        self.versions = tuple(t._version for t in tensors)
+        self.extra = tuple(extra)
+
+    def matches(self, tensors, extra=()) -> bool:
+        return (len(tensors) == len(self.refs) and all(r() is t for r, t in zip(self.refs, tensors))
+                and self.versions == tuple(t._version for t in tensors) and self.extra == tuple(extra))
 
 
 def _tensor_cache(t: torch.Tensor) -> dict:
@@ -255,13 +274,12 @@ def _cached_packed(window_offset: torch.Tensor, col_indices: torch.Tensor, value
     built on the second product of the same, unmodified arrays."""
     if not PACK_TILES or not pack_tiles_supported(col_indices, values, tile_cols):
         return None
-    key = (values.data_ptr(), values._version, col_indices.data_ptr(), col_indices._version)
     d = _tensor_cache(window_offset)
     ent = d.get("packed")
-    if ent is None or ent[0] != key:
-        d["packed"] = (key, 1, None)
+    if ent is None or not ent[0].matches((values, col_indices)):
+        d["packed"] = (TensorKey((values, col_indices)), 1, None)
         return None
-    _, calls, p = ent
+    key, calls, p = ent
     if p is None and calls == 1:
         p = pack_tiles(window_offset, col_indices, values, tile_cols) or False
         d["packed"] = (key, 2, p)
@@ -300,12 +318,12 @@ def spmm_tc(window_offset: torch.Tensor, original_col_indices: torch.Tensor,
 # SpMM transpose (backward)
 # ---------------------------------------------------------------------------
 def _cached_transpose(window_offset, col_indices, values, tile_cols: int, num_cols: int):
-    key = (window_offset._version, col_indices.data_ptr(), col_indices._version,
-           values.data_ptr(), values._version, int(num_cols), int(tile_cols))
+    extra = (int(num_cols), int(tile_cols))
     d = _tensor_cache(window_offset)
     hit = d.get("T")
-    if hit is not None and hit[0] == key:
+    if hit is not None and hit[0].matches((window_offset, col_indices, values), extra):
         return hit[1]
+    key = TensorKey((window_offset, col_indices, values), extra)
     from ..data.bcsr import BCSRGraph
     W = window_offset.numel() - 1
     g = BCSRGraph(num_nodes=16 * W, num_edges=0, tile_rows=16, tile_cols=tile_cols,

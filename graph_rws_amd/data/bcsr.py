@@ -243,12 +243,13 @@ class BCSRGraph:
         mws = getattr(self, "max_window_slabs", None)
         if mws is not None and mws <= slabs:
             return None
-        key = ("plan", slabs, self.window_offset.data_ptr())
-        p = self._cache.get(key)
-        if p is None:
+        from ..core.ops import TensorKey
+        ent = self._cache.get(("plan", slabs))
+        if ent is None or not ent[0].matches((self.window_offset,), (self.num_tiles, self.tile_cols)):
             p = build_spmm_plan(self.window_offset, self.num_tiles, self.tile_cols, slabs)
-            self._cache[key] = p
-        return p
+            ent = (TensorKey((self.window_offset,), (self.num_tiles, self.tile_cols)), p)
+            self._cache[("plan", slabs)] = ent
+        return ent[1]
 
     def packed_tiles(self):
         """The packed copy of the values the SpMM reads instead of the dense
@@ -260,13 +261,13 @@ class BCSRGraph:
         from ..core import ops as _ops
         if not _ops.PACK_TILES or self.tile_cols != 16:
             return None
+        from ..core.ops import TensorKey
         v, c = self.values_condensed, self.original_col_indices
-        key = (v.data_ptr(), v._version, c.data_ptr(), c._version)
         ent = self._cache.get("packed")
-        if ent is None or ent[0] != key:
-            self._cache["packed"] = (key, 1, None)
+        if ent is None or not ent[0].matches((v, c)):
+            self._cache["packed"] = (TensorKey((v, c)), 1, None)
             return None
-        _, calls, p = ent
+        key, calls, p = ent
         if p is None and calls == 1:
             p = _ops.pack_tiles(self.window_offset, c, v, self.tile_cols) or False
             self._cache["packed"] = (key, 2, p)
@@ -304,10 +305,11 @@ class BCSRGraph:
     def transpose(self) -> "BCSRGraph":
         """Cached BCSR of A^T (num_cols x 16W), built on the device.  Rebuilt
         when the column or value arrays are replaced or modified in place."""
-        key = ("T", self.original_col_indices.data_ptr(), self.original_col_indices._version,
-               self.values_condensed.data_ptr(), self.values_condensed._version, self.num_cols)
+        from ..core.ops import TensorKey
+        arrays = (self.window_offset, self.original_col_indices, self.values_condensed)
         t = self._cache.get("T")
-        if t is None or t[0] != key:
+        if t is None or not t[0].matches(arrays, (self.num_cols,)):
+            key = TensorKey(arrays, (self.num_cols,))
             from .. import builder
             t = (key, builder.transpose(self))
             self._cache["T"] = t

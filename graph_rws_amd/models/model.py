@@ -92,16 +92,16 @@ class GCN_BCSR(nn.Module):
     def _mask_global_columns(g, num_in: int) -> None:
         """-1 and columns >= num_in become column 0 with value 0, in place
         (model.py:118-125).  Skipped when this graph state was masked already."""
+        from ..core.ops import TensorKey
         cols, vals = g.original_col_indices, g.values_condensed
-        key = (cols.data_ptr(), cols._version, vals.data_ptr(), vals._version, int(num_in))
-        if g._cache.get("masked") == key:
+        ent = g._cache.get("masked")
+        if ent is not None and ent.matches((cols, vals), (int(num_in),)):
             return
         bad = (cols == -1) | (cols >= num_in)
         cols.masked_fill_(bad, 0)
         mask = bad.view(-1, g.tile_cols).unsqueeze(1).expand(-1, g.tile_rows, -1).reshape(-1)
         vals.view(-1).masked_fill_(mask, 0.0)
-        g._cache["masked"] = (cols.data_ptr(), cols._version, vals.data_ptr(), vals._version,
-                              int(num_in))
+        g._cache["masked"] = TensorKey((cols, vals), (int(num_in),))
 
     def _sanitize_and_reindex(self, layer_idx, curr_g, prev_g, h_in_shape):
         # is_local_input (the reference's UVA mode) and columns_local (blocks
