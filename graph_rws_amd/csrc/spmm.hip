@@ -715,25 +715,44 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
 }
 
 // Sums the partial slots of each split window in slot order (deterministic).
+// One wave per 256 floats of a (split window, chunk) block: NBLK waves per
+// block, lane l owns 4 consecutive floats (one row, 4 columns).  A hub
+// window split into hundreds of slots would otherwise serialise one load
+// latency per slot; here the loads of 8 slots are in flight at once and are
+// added in slot order afterwards (same order, same result).
 template <int XT, int NBLK>
-__global__ __launch_bounds__(256) void spmm_fixup_kernel(const int32_t* __restrict__ split, int64_t num_split,
-                                                         const float* __restrict__ partials, int32_t nchunks,
-                                                         void* y, int64_t ldy, int64_t N, int64_t col_base) {
+__global__ __launch_bounds__(64) void spmm_fixup_kernel(const int32_t* __restrict__ split, int64_t num_split,
+                                                        const float* __restrict__ partials, int32_t nchunks,
+                                                        void* y, int64_t ldy, int64_t N, int64_t col_base) {
     constexpr int NC = NBLK * 16;
-    const int64_t si = blockIdx.x / nchunks;
-    const int chunk = (int)(blockIdx.x % nchunks);
+    constexpr int U = 8;
+    const int64_t blk = blockIdx.x / NBLK;  // (split window, chunk)
+    const int sub = (int)(blockIdx.x % NBLK);
+    const int64_t si = blk / nchunks;
+    const int chunk = (int)(blk % nchunks);
     if (si >= num_split) return;
     const int64_t w = split[3 * si];
     const int64_t first = split[3 * si + 1];
     const int cnt = split[3 * si + 2];
+    const int e = 4 * (sub * 64 + (int)threadIdx.x);  // first of the lane's 4 floats in the 16 x NC block
+    const int r = e / NC, c = e % NC;
     const int64_t n0 = col_base + (int64_t)chunk * NC;
-    for (int e = threadIdx.x; e < 16 * NC; e += 256) {
-        const int r = e / NC, c = e % NC;
-        if (n0 + c >= N) continue;
-        float s = 0.f;
-        for (int k = 0; k < cnt; ++k) s += partials[((first + k) * nchunks + chunk) * (16 * NC) + e];
-        store_out<XT>(y, (w * 16 + r) * ldy + n0 + c, s);
+    const float4_t* p = reinterpret_cast<const float4_t*>(partials + (first * nchunks + chunk) * (16 * NC) + e);
+    const int64_t stride = (int64_t)nchunks * (16 * NC) / 4;  // float4s between consecutive slots
+    float4_t s = float4_t{0.f, 0.f, 0.f, 0.f};
+    int k = 0;
+    for (; k + U <= cnt; k += U) {
+        float4_t t[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) t[j] = __builtin_nontemporal_load(p + (k + j) * stride);
+#pragma unroll
+        for (int j = 0; j < U; ++j) s += t[j];
     }
+    for (; k < cnt; ++k) s += __builtin_nontemporal_load(p + k * stride);
+    const int64_t o = (w * 16 + r) * ldy + n0 + c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (n0 + c + i < N) store_out<XT>(y, o + i, s[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -911,27 +930,29 @@ bool buffer_path_fits(const grws_bcsr* A, const grws_spmm_plan* plan, int64_t x_
 
 template <int XT>
 int launch_fixup(const grws_spmm_plan* plan, const SpmmArgs& a, int nblk, hipStream_t stream) {
-    int64_t grid = plan->num_split * a.nchunks;
+    const int64_t grid = plan->num_split * a.nchunks * nblk;
     if (grid <= 0) return GRWS_OK;
+    if (grid > INT32_MAX) return set_error(GRWS_E_INVALID, "spmm: too many split windows (%lld)",
+                                           (long long)plan->num_split);
     switch (nblk) {
         case 1:
-            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 1>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
+            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 1>), dim3((unsigned)grid), dim3(64), 0, stream, plan->split,
                                plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
             break;
         case 2:
-            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 2>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
+            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 2>), dim3((unsigned)grid), dim3(64), 0, stream, plan->split,
                                plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
             break;
         case 4:
-            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 4>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
+            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 4>), dim3((unsigned)grid), dim3(64), 0, stream, plan->split,
                                plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
             break;
         case 16:
-            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 16>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
+            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 16>), dim3((unsigned)grid), dim3(64), 0, stream, plan->split,
                                plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
             break;
         default:
-            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 8>), dim3((unsigned)grid), dim3(256), 0, stream, plan->split,
+            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 8>), dim3((unsigned)grid), dim3(64), 0, stream, plan->split,
                                plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
             break;
     }
@@ -1173,6 +1194,7 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
             size_t need = grws_spmm_workspace_bytes(plan, n_cols);
             if (!workspace || workspace_bytes < need)
                 return set_error(GRWS_E_CAPACITY, "spmm: workspace too small (%zu < %zu)", workspace_bytes, need);
+            GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "spmm: workspace not 16-byte aligned");
             a.partials = static_cast<float*>(workspace);
         }
     } else {

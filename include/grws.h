@@ -127,7 +127,8 @@ size_t grws_spmm_workspace_bytes(const grws_spmm_plan* plan, int64_t n_cols);
  * [16*num_windows, ldy].  x_dtype == y_dtype; A's values may be F32 or
  * x_dtype.  F16/BF16 use MFMA with fp32 accumulation; F32 uses fp32 MFMA.
  * Column slots of -1, or outside [0, x_rows), contribute nothing.
- * plan may be NULL (one work item per window, no splitting).
+ * plan may be NULL (one work item per window, no splitting).  workspace
+ * (grws_spmm_workspace_bytes) must be 16-byte aligned.
  */
 int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const void* x, int32_t x_dtype,
               int64_t x_rows, int64_t ldx, int64_t n_cols, void* y, int32_t y_dtype, int64_t ldy,
