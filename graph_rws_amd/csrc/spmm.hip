@@ -1056,8 +1056,12 @@ extern "C" int32_t grws_spmm_default_slabs(int64_t num_windows, int64_t num_tile
     int64_t nchunks = (n_cols + nblk * 16 - 1) / (nblk * 16);
     if (nchunks < 1) nchunks = 1;
     int64_t slabs = (num_tiles * (tile_cols > 0 ? tile_cols : 16) + 15) / 16;
-    // a fair share for one of ~2048 resident waves (256 CUs x 8)
-    int64_t share = slabs * nchunks / 2048;
+    // a fair share for one of ~4096 resident waves (256 CUs x 16).  Split
+    // windows cost a partial write and a fixup read, so items stay long
+    // enough that only hub windows split (measured: c2 best at 32 slabs,
+    // c4 within 1% of its best at 512-1024, c3 slower once its ~320-tile
+    // windows split)
+    int64_t share = slabs * nchunks / 4096;
     int64_t s = 16;
     while (s * 2 <= share && s < (1 << 20)) s *= 2;
     (void)num_windows;
