@@ -21,7 +21,9 @@
 //   * work-group ids are remapped so each XCD (work-groups are dealt to the 8
 //     XCDs round-robin) walks a contiguous range of windows of one chunk,
 //     keeping a community's X rows (one chunk wide) in that XCD's L2.
-// Tuning overrides for benchmarking: GRWS_SPMM_WAVES (1|2), GRWS_SPMM_NBLK (1|2|4|8|16).
+// Tuning overrides for benchmarking: GRWS_SPMM_WAVES (1|2), GRWS_SPMM_NBLK (1|2|4|8|16),
+// GRWS_SPMM_ORDER (1: chunk-major work order, the default; 0: XCD shares of
+// the (chunk, window) pairs).
 #include "grws_internal.h"
 
 #include <cstdlib>
@@ -105,6 +107,10 @@ struct SpmmArgs {
     const uint32_t* hdr;
     const void* pvals;
     uint32_t pv_bytes;
+    // buffer path: all XCDs walk chunk 0, then chunk 1, ... (each XCD on its
+    // own window range), instead of each XCD walking its own share of the
+    // (chunk, window) pairs
+    int32_t chunk_major;
 };
 
 // Output conversion for the three element types.
@@ -467,12 +473,22 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
     const int wave = WPB > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;
     const int lane = threadIdx.x & 63;
     S* stage = stage_all + wave * (16 * PITCH);
-    const int64_t total = a.num_items * a.nchunks;
-    const int64_t per_xcd = (total + 7) >> 3;
-    const int64_t logical = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (logical >= total) return;  // uniform over the work-group
-    const int64_t item = logical % a.num_items;
-    const int chunk = (int)(logical / a.num_items);
+    int64_t item;
+    int chunk;
+    if (a.chunk_major) {
+        const int64_t ipc = (a.num_items + 7) & ~(int64_t)7;  // work-groups per chunk
+        chunk = (int)(blockIdx.x / ipc);
+        const int64_t r = (int64_t)blockIdx.x - (int64_t)chunk * ipc;
+        item = (r & 7) * (ipc >> 3) + (r >> 3);
+        if (chunk >= a.nchunks || item >= a.num_items) return;  // uniform over the work-group
+    } else {
+        const int64_t total = a.num_items * a.nchunks;
+        const int64_t per_xcd = (total + 7) >> 3;
+        const int64_t logical = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+        if (logical >= total) return;  // uniform over the work-group
+        item = logical % a.num_items;
+        chunk = (int)(logical / a.num_items);
+    }
     const int64_t col_base = a.col_base;
 
     int64_t w, sb, se;
@@ -800,17 +816,27 @@ __global__ void plan_fill_kernel(const int64_t* __restrict__ win_off, int64_t W,
     }
 }
 
+// Whether 256-column chunks pay: A is then streamed once per 256 columns
+// instead of per 128, but a wave holds twice the accumulators and X
+// registers (3 waves per SIMD instead of 4).  That wins while a 256-column
+// slice of X stays in the 256 MB Infinity Cache (c3, 233k rows: 2.61 ms
+// against 2.79 at N=256); when it cannot (c4, 2.45M rows of random ids) the
+// gathers go to HBM and the extra resident waves hide more of their latency
+// (7.31 ms against 7.72).
+bool wide_chunks(int64_t x_rows, int32_t x_dtype) {
+    return x_dtype != GRWS_F32 && x_rows * 256 * (int64_t)dtype_size(x_dtype) <= ((int64_t)256 << 20);
+}
+
 // MFMA column blocks (16 output columns each) per work-group: 128-column
-// chunks, or 256 on the buffer-load path when N is a multiple of 256 (A is
-// then streamed once per 256 columns; measured faster on community graphs,
-// equal on random ones).  fp32 X stays at 128 (its loads carry half as many
+// chunks, or 256 on the buffer-load path when N is a multiple of 256 and
+// wide_chunks holds.  fp32 X stays at 128 (its loads carry half as many
 // elements per lane).
-int nblk_for(int64_t N, int32_t x_dtype, bool buffer_path) {
+int nblk_for(int64_t N, int32_t x_dtype, bool buffer_path, int64_t x_rows) {
     if (const char* e = getenv("GRWS_SPMM_NBLK")) {  // tuning override
         const int v = atoi(e);
         if (v == 1 || v == 2 || v == 4 || v == 8 || (v == 16 && x_dtype != GRWS_F32)) return v;
     }
-    if (buffer_path && x_dtype != GRWS_F32 && N >= 256 && N % 256 == 0) return 16;
+    if (buffer_path && wide_chunks(x_rows, x_dtype) && N >= 256 && N % 256 == 0) return 16;
     return N <= 16 ? 1 : (N <= 32 ? 2 : (N <= 64 ? 4 : 8));
 }
 
@@ -870,7 +896,7 @@ int dispatch_tc(const SpmmArgs& a, int tc, int nblk, bool vect, hipStream_t stre
 template <int XT, bool AF32, int TC, int NBLK, int WPB, bool PK>
 int launch_buf(const SpmmArgs& a, hipStream_t stream) {
     const int64_t total = a.num_items * a.nchunks;
-    const int64_t grid = ((total + 7) / 8) * 8;
+    const int64_t grid = a.chunk_major ? ((a.num_items + 7) / 8) * 8 * a.nchunks : ((total + 7) / 8) * 8;
     if (grid > INT32_MAX) return set_error(GRWS_E_INVALID, "spmm: too many work items (%lld)", (long long)total);
     hipLaunchKernelGGL((spmm_buf_kernel<XT, AF32, TC, NBLK, WPB, 1, PK>), dim3((unsigned)grid), dim3(64 * WPB), 0,
                        stream, a);
@@ -1052,7 +1078,7 @@ extern "C" int grws_spmm_plan_capacity(int64_t num_windows, int64_t num_tiles, i
 
 extern "C" int32_t grws_spmm_default_slabs(int64_t num_windows, int64_t num_tiles, int32_t tile_cols,
                                            int64_t n_cols) {
-    int64_t nblk = nblk_for(n_cols > 0 ? n_cols : 1, GRWS_F16, true);
+    int64_t nblk = nblk_for(n_cols > 0 ? n_cols : 1, GRWS_F16, true, 0);
     int64_t nchunks = (n_cols + nblk * 16 - 1) / (nblk * 16);
     if (nchunks < 1) nchunks = 1;
     int64_t slabs = (num_tiles * (tile_cols > 0 ? tile_cols : 16) + 15) / 16;
@@ -1176,7 +1202,7 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
     const int64_t vec = (int64_t)(16 / esz);
     const bool vect = (n_cols % vec == 0) && (ldx % vec == 0) && ((reinterpret_cast<uintptr_t>(x) % 16) == 0);
     const bool use_buf = vect && buffer_path_fits(A, plan, x_rows, ldx, 256, esz);
-    const int nblk = nblk_for(n_cols, x_dtype, use_buf);
+    const int nblk = nblk_for(n_cols, x_dtype, use_buf, x_rows);
     const int64_t nc = nblk * 16;
     SpmmArgs a{};
     a.win_off = A->window_offset;
@@ -1212,6 +1238,8 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
     int st;
     if (use_buf) {
         a.x_bytes = (uint32_t)((x_rows - 1) * ldx * (int64_t)esz + n_cols * (int64_t)esz);
+        a.chunk_major = 1;
+        if (const char* e = getenv("GRWS_SPMM_ORDER")) a.chunk_major = atoi(e) == 1;  // tuning override
         if (P && A->num_tiles > 0) {  // the element-masked kernel below reads the dense values
             a.hdr = P->header;
             a.pvals = P->values;
@@ -1224,11 +1252,11 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
         // streamed once per 256 columns and no chunk is mostly empty
         const bool forced = getenv("GRWS_SPMM_NBLK") != nullptr;
         const int64_t head =
-            (!forced && x_dtype != GRWS_F32 && n_cols > 256 && n_cols % 256 != 0) ? n_cols / 256 * 256 : 0;
+            (!forced && wide_chunks(x_rows, x_dtype) && n_cols > 256 && n_cols % 256 != 0) ? n_cols / 256 * 256 : 0;
         const int64_t parts[2][2] = {{0, head > 0 ? head : n_cols}, {head, n_cols}};
         for (int pi = 0; pi < (head > 0 ? 2 : 1); ++pi) {
             const int64_t c0 = parts[pi][0], c1 = parts[pi][1];
-            const int pnblk = head > 0 ? (pi == 0 ? 16 : nblk_for(c1 - c0, x_dtype, false)) : nblk;
+            const int pnblk = head > 0 ? (pi == 0 ? 16 : nblk_for(c1 - c0, x_dtype, false, x_rows)) : nblk;
             const int64_t pnc = pnblk * 16;
             a.col_base = c0;
             a.nchunks = (int32_t)((c1 - c0 + pnc - 1) / pnc);

@@ -275,3 +275,46 @@ def test_fp32_buffer_kernel_equals_element_masked(cuda_device, tc, N, slabs):
             os.environ["GRWS_SPMM_KERNEL"] = old
     assert torch.equal(Yb.view(torch.int32), Ye.view(torch.int32))
     _check(G, X, Yb, torch.float32)
+
+
+def _with_env(env, fn):
+    import os
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return fn()
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("slabs", [None, 3])
+@pytest.mark.parametrize("big_x", [False, True])
+def test_chunk_widths_and_work_orders_agree(cuda_device, xdt, slabs, big_x):
+    """The chunk width (16..256 columns per work-group) and the work order
+    (chunk-major or per-XCD shares of the (chunk, window) pairs) change only
+    which work-group computes an output column, not the order of its sum:
+    every variant gives the same bits.  big_x: X has 600k rows, past the
+    256 MB a 256-column slice may take before the library picks 128-column
+    chunks by itself."""
+    print(f"case chunk-orders xdt={xdt} slabs={slabs} big_x={big_x}", flush=True)
+    g = synth.chung_lu(3000, 50000, 2.1, seed=11)
+    G = _bcsr(g, 16, cuda_device, vdt=xdt)
+    N = 512
+    rows = 600_000 if big_x else g.num_nodes
+    X = synth.features(rows, N, seed=12, device=cuda_device).to(xdt)
+    plan = None if slabs is None else core.build_spmm_plan(G.window_offset, G.num_tiles, 16, slabs)
+    args = (G.window_offset, G.original_col_indices, G.values_condensed, X, 16)
+    ref = core.spmm(*args, plan=plan)
+    torch.cuda.synchronize()
+    for env in ({"GRWS_SPMM_ORDER": "0"}, {"GRWS_SPMM_NBLK": "8", "GRWS_SPMM_ORDER": "0"},
+                {"GRWS_SPMM_NBLK": "8", "GRWS_SPMM_ORDER": "1"}, {"GRWS_SPMM_NBLK": "16", "GRWS_SPMM_ORDER": "1"},
+                {"GRWS_SPMM_NBLK": "2", "GRWS_SPMM_ORDER": "1"}):
+        Y = _with_env(env, lambda: core.spmm(*args, plan=plan))
+        torch.cuda.synchronize()
+        assert torch.equal(Y.view(torch.int16), ref.view(torch.int16)), env
+    _check(G, X[: g.num_nodes], ref, xdt)
