@@ -447,7 +447,31 @@ def bench_dps(dev, cpu: bool, reps: int = 10) -> dict:
     return out
 
 
-def bench_spmm_c2(dev, reps: int = 20) -> dict:
+def cpu_spmm_c2(g, reps: int = 5) -> dict:
+    """torch.sparse CSR fp32 A X and A^T G (N=128) on the host cores, the CPU
+    path beside the c2 microbenchmark: median of `reps` after one warm-up."""
+    torch.set_num_threads(os.cpu_count() or 1)
+    n = g.num_nodes
+    A = torch.sparse_csr_tensor(g.row_ptr.cpu(), g.col_idx.cpu().long(), g.values.cpu().float(),
+                                size=(n, n))
+    AT = A.t().to_sparse_csr()
+    X = torch.randn(n, 128, generator=torch.Generator().manual_seed(23))
+    out = {}
+    for name, M in (("fwd", A), ("bwd", AT)):
+        M @ X
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            M @ X
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        out[name] = {"ms": round(1e3 * ts[len(ts) // 2], 3),
+                     "gflops": round(2.0 * g.nnz * 128 / ts[len(ts) // 2] / 1e9, 2)}
+    return {"value": out, "unit": "ms per product", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"whole graph, fp32, torch.sparse CSR (A and a precomputed A^T), median of {reps}"}
+
+
+def bench_spmm_c2(dev, reps: int = 20, cpu: bool = False) -> dict:
     """c2 SpMM microbenchmark: forward A X and backward A^T G (G like X),
     X [169,343 x 128] in bf16 and f16, 16x16 tiles."""
     from graph_rws_amd import synth
@@ -482,6 +506,8 @@ def bench_spmm_c2(dev, reps: int = 20) -> dict:
         res[dname] = r
         del G, X, Gr, AT
     torch.cuda.empty_cache()
+    if cpu:
+        res["cpu_baseline"] = cpu_spmm_c2(g)
     return res
 
 
@@ -634,7 +660,7 @@ def main():
         torch.cuda.empty_cache()
         out["sampling"] = bench_sampling(dev, args.sampling_batches, 3, not args.no_cpu_baseline)
     if not args.no_gcn:
-        out["spmm_c2"] = bench_spmm_c2(dev)
+        out["spmm_c2"] = bench_spmm_c2(dev, cpu=not args.no_cpu_baseline)
         out["gcn"] = {c: bench_gcn(c, dev, args.gcn_epochs, 2, not args.no_cpu_baseline)
                       for c in args.gcn_configs.split(",") if c}
     if not args.no_dps:
