@@ -76,6 +76,9 @@ def alg_bytes(G, N: int, s_x: int, s_y: int) -> dict:
     }
     parts["total"] = sum(parts.values())
     parts["U"] = U
+    # compulsory lower bound: the same, with every X row read once
+    parts["compulsory"] = (parts["win_off"] + parts["cols"] + parts["vals"] + s_x * G.num_cols * N
+                           + parts["y"])
     return parts
 
 
