@@ -265,7 +265,7 @@ def bench_gcn(cfg: str, dev, epochs: int, warmup: int, cpu: bool) -> dict:
     backward + clip + Adam, synchronised at its end."""
     from graph_rws_amd import synth
     from graph_rws_amd.data import BCSRGraph
-    from graph_rws_amd.helper import train_epoch_full
+    from graph_rws_amd.helper import GraphedFullStep, train_epoch_full
     from graph_rws_amd.models import GCN_BCSR
     d_raw, d_pad, kind, hidden, classes, layers, dname = GCN_CONFIGS[cfg]
     dt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dname]
@@ -302,6 +302,27 @@ def bench_gcn(cfg: str, dev, epochs: int, warmup: int, cpu: bool) -> dict:
            "classes": classes, "layers": layers, "dtype": dname, "tile": "16x16",
            "epochs": epochs, "epoch_ms": round(1e3 * times[len(times) // 2], 3),
            "epoch_ms_min": round(1e3 * times[0], 3), "final_loss": round(float(loss), 4)}
+    # the same step captured once on a HIP graph and replayed (GraphedFullStep):
+    # a fresh model of the same init, Adam with capturable=True
+    torch.manual_seed(13)
+    model_g = GCN_BCSR(d_pad, hidden, classes, layers, dropout=0.5, use_checkpoint=False).to(dev)
+    opt_g = torch.optim.Adam(model_g.parameters(), lr=0.01, capturable=True)
+    step = GraphedFullStep(model_g, G, X, labels, train_idx, opt_g, dev, warmup=max(2, warmup),
+                           autocast_dtype=None if dt == torch.float32 else dt)
+    n_g = max(epochs, 20)
+    step()
+    torch.cuda.synchronize(dev)
+    tg = []
+    for _ in range(n_g):
+        t0 = time.perf_counter()
+        loss_g, _ = step()
+        torch.cuda.synchronize(dev)
+        tg.append(time.perf_counter() - t0)
+    tg.sort()
+    out["graphed"] = {"epoch_ms": round(1e3 * tg[len(tg) // 2], 3), "epoch_ms_min": round(1e3 * tg[0], 3),
+                      "epochs": n_g, "final_loss": round(float(loss_g), 4),
+                      "how": "the same step captured once on a HIP graph (torch.cuda.graph) and replayed"}
+    del step, model_g, opt_g
     if cpu:
         torch.set_num_threads(os.cpu_count() or 1)
         dims = [d_pad] + [hidden] * (layers - 1) + [classes]

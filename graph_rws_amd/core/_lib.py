@@ -143,12 +143,12 @@ _PROTOS = {
                                           ctypes.c_size_t, _vp]),
     "grws_act_norm_dropout_fwd": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64,
                                                  ctypes.c_int64, ctypes.c_int32, _vp, _vp, ctypes.c_float,
-                                                 ctypes.c_float, ctypes.c_uint64, _vp, ctypes.c_int32,
+                                                 ctypes.c_float, ctypes.c_uint64, _vp, _vp, ctypes.c_int32,
                                                  ctypes.c_int64, _vp, _vp, _vp]),
     "grws_act_norm_dropout_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
     "grws_act_norm_dropout_bwd": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int64, _vp, ctypes.c_int32,
                                                  ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
-                                                 _vp, _vp, _vp, ctypes.c_float, ctypes.c_uint64, _vp,
+                                                 _vp, _vp, _vp, ctypes.c_float, ctypes.c_uint64, _vp, _vp,
                                                  ctypes.c_int64, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "grws_cross_entropy_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
     "grws_cross_entropy_fwd": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64,

@@ -800,10 +800,20 @@ def act_norm_dropout_supported(z: torch.Tensor) -> bool:
     return _rowwise_ok(z) and 4 <= z.shape[1] <= 1024 and z.shape[1] % 4 == 0
 
 
+def _seed_dev(seed_dev: Optional[torch.Tensor], dev: torch.device):
+    if seed_dev is None:
+        return None
+    if not (seed_dev.is_cuda and seed_dev.device == dev and seed_dev.dtype == torch.int64 and seed_dev.numel() >= 1):
+        raise ValueError("seed_dev must be an int64 tensor with one element on the device of z")
+    return L.ptr(seed_dev)
+
+
 def act_norm_dropout_fwd(z: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float, p: float,
-                         act: int, seed: int, out_dtype: torch.dtype, save_stats: bool):
+                         act: int, seed: int, out_dtype: torch.dtype, save_stats: bool,
+                         seed_dev: Optional[torch.Tensor] = None):
     """out = dropout_p(LayerNorm(act(z))) (csrc/fused.hip); returns (out,
-    mean, rstd) with mean/rstd None unless save_stats."""
+    mean, rstd) with mean/rstd None unless save_stats.  seed_dev: an int64
+    device tensor whose first element the kernel reads in place of seed."""
     rows, dim = z.shape
     out = torch.empty((rows, dim), dtype=out_dtype, device=z.device)
     w = weight.detach().float().contiguous()
@@ -813,13 +823,14 @@ def act_norm_dropout_fwd(z: torch.Tensor, weight: torch.Tensor, bias: torch.Tens
         mean = torch.empty(max(1, rows), dtype=torch.float32, device=z.device)
         rstd = torch.empty_like(mean)
     L.call("grws_act_norm_dropout_fwd", L.ptr(z), L.dtype_code(z.dtype), z.stride(0), rows, dim, int(act),
-           L.ptr(w), L.ptr(b), float(eps), float(p), int(seed) & ((1 << 64) - 1), L.ptr(out),
-           L.dtype_code(out_dtype), out.stride(0), L.ptr(mean), L.ptr(rstd), L.stream_of(z.device))
+           L.ptr(w), L.ptr(b), float(eps), float(p), int(seed) & ((1 << 64) - 1), _seed_dev(seed_dev, z.device),
+           L.ptr(out), L.dtype_code(out_dtype), out.stride(0), L.ptr(mean), L.ptr(rstd), L.stream_of(z.device))
     return out, mean, rstd
 
 
 def act_norm_dropout_bwd(dout: torch.Tensor, z: torch.Tensor, mean: torch.Tensor, rstd: torch.Tensor,
-                         weight: torch.Tensor, p: float, act: int, seed: int):
+                         weight: torch.Tensor, p: float, act: int, seed: int,
+                         seed_dev: Optional[torch.Tensor] = None):
     """(dz, dgamma, dbeta) of act_norm_dropout_fwd."""
     rows, dim = z.shape
     if not _rowwise_ok(dout):
@@ -832,8 +843,8 @@ def act_norm_dropout_bwd(dout: torch.Tensor, z: torch.Tensor, mean: torch.Tensor
     ws = torch.empty(max(1, wsb), dtype=torch.uint8, device=z.device)
     L.call("grws_act_norm_dropout_bwd", L.ptr(dout), L.dtype_code(dout.dtype), dout.stride(0), L.ptr(z),
            L.dtype_code(z.dtype), z.stride(0), rows, dim, int(act), L.ptr(mean), L.ptr(rstd), L.ptr(w),
-           float(p), int(seed) & ((1 << 64) - 1), L.ptr(dz), dz.stride(0), L.ptr(dg), L.ptr(db), L.ptr(ws), wsb,
-           L.stream_of(z.device))
+           float(p), int(seed) & ((1 << 64) - 1), _seed_dev(seed_dev, z.device), L.ptr(dz), dz.stride(0),
+           L.ptr(dg), L.ptr(db), L.ptr(ws), wsb, L.stream_of(z.device))
     return dz, dg, db
 
 

@@ -134,8 +134,9 @@ __device__ __forceinline__ uint32_t keep_threshold(float p) {
 template <typename ZT, typename OT, int STEPS, int ROWS>
 __global__ __launch_bounds__(kBlk) void act_norm_dropout_fwd_kernel(
     const ZT* __restrict__ z, int64_t ldz, int64_t rows, int dim, int act, const float* __restrict__ gamma,
-    const float* __restrict__ beta, float eps, float p, uint64_t seed, OT* __restrict__ out, int64_t ldo,
-    float* __restrict__ mean_out, float* __restrict__ rstd_out) {
+    const float* __restrict__ beta, float eps, float p, uint64_t seed, const uint64_t* __restrict__ seed_dev,
+    OT* __restrict__ out, int64_t ldo, float* __restrict__ mean_out, float* __restrict__ rstd_out) {
+    if (seed_dev) seed = *seed_dev;  // a seed drawn on the device (graph-captured callers)
     const int lane = threadIdx.x & 63;
     // wave-uniform row index: per-row scalars then go through scalar loads
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -238,8 +239,10 @@ template <typename GT, typename ZT, int STEPS, int ROWS>
 __global__ __launch_bounds__(kBlk) void act_norm_dropout_bwd_kernel(
     const GT* __restrict__ g, int64_t ldg, const ZT* __restrict__ z, int64_t ldz, int64_t rows, int dim, int act,
     const float* __restrict__ mean_in, const float* __restrict__ rstd_in, const float* __restrict__ gamma, float p,
-    uint64_t seed, ZT* __restrict__ dz, int64_t lddz, float* __restrict__ part_g, float* __restrict__ part_b) {
+    uint64_t seed, const uint64_t* __restrict__ seed_dev, ZT* __restrict__ dz, int64_t lddz,
+    float* __restrict__ part_g, float* __restrict__ part_b) {
     __shared__ float red[2][kRowsPerBlock][STEPS * 256];
+    if (seed_dev) seed = *seed_dev;
     const int lane = threadIdx.x & 63;
     // wave-uniform row index: mean, rstd and the mask words go through scalar loads
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -650,8 +653,8 @@ static int check_rowwise(int32_t a_dt, int32_t b_dt, int64_t rows, int64_t dim, 
 
 extern "C" int grws_act_norm_dropout_fwd(const void* z, int32_t z_dtype, int64_t ldz, int64_t rows, int64_t dim,
                                          int32_t act, const float* gamma, const float* beta, float eps, float p,
-                                         uint64_t seed, void* out, int32_t out_dtype, int64_t ldo, float* mean,
-                                         float* rstd, void* stream_) {
+                                         uint64_t seed, const uint64_t* seed_dev, void* out, int32_t out_dtype,
+                                         int64_t ldo, float* mean, float* rstd, void* stream_) {
     clear_error();
     hipStream_t stream = as_stream(stream_);
     GRWS_CHECK_ARG(act == 0 || act == 1, "act_norm_dropout: act must be 0 (none) or 1 (relu)");
@@ -669,7 +672,7 @@ extern "C" int grws_act_norm_dropout_fwd(const void* z, int32_t z_dtype, int64_t
 #define GRWS_ANDF_SR(ZT, OT, S, R)                                                                              \
     hipLaunchKernelGGL((act_norm_dropout_fwd_kernel<ZT, OT, S, R>), dim3((unsigned)blocks), dim3(kBlk), 0, stream, \
                        static_cast<const ZT*>(z), ldz, rows, (int)dim, (int)act, gamma, beta, eps, p, seed,       \
-                       static_cast<OT*>(out), ldo, mean, rstd)
+                       seed_dev, static_cast<OT*>(out), ldo, mean, rstd)
 #define GRWS_ANDF(ZT, OT)                              \
     do {                                               \
         if (steps == 1) GRWS_ANDF_SR(ZT, OT, 1, 4);    \
@@ -687,7 +690,8 @@ extern "C" int grws_act_norm_dropout_fwd(const void* z, int32_t z_dtype, int64_t
 extern "C" int grws_act_norm_dropout_bwd(const void* dout, int32_t dout_dtype, int64_t ldg, const void* z,
                                          int32_t z_dtype, int64_t ldz, int64_t rows, int64_t dim, int32_t act,
                                          const float* mean, const float* rstd, const float* gamma, float p,
-                                         uint64_t seed, void* dz, int64_t lddz, float* dgamma, float* dbeta,
+                                         uint64_t seed, const uint64_t* seed_dev, void* dz, int64_t lddz,
+                                         float* dgamma, float* dbeta,
                                          void* workspace, size_t workspace_bytes, void* stream_) {
     clear_error();
     hipStream_t stream = as_stream(stream_);
@@ -717,7 +721,7 @@ extern "C" int grws_act_norm_dropout_bwd(const void* dout, int32_t dout_dtype, i
         nb = resident_blocks(act_norm_dropout_bwd_kernel<GT, ZT, S, R>, blocks);                                 \
         hipLaunchKernelGGL((act_norm_dropout_bwd_kernel<GT, ZT, S, R>), dim3((unsigned)nb), dim3(kBlk), 0, stream, \
                            static_cast<const GT*>(dout), ldg, static_cast<const ZT*>(z), ldz, rows, (int)dim,      \
-                           (int)act, mean, rstd, gamma, p, seed, static_cast<ZT*>(dz), lddz, pg, pb);              \
+                           (int)act, mean, rstd, gamma, p, seed, seed_dev, static_cast<ZT*>(dz), lddz, pg, pb);              \
     } while (0)
 #define GRWS_ANDB(GT, ZT)                              \
     do {                                               \

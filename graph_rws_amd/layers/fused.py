@@ -8,7 +8,10 @@ unfused path produces fp32 there (LayerNorm runs in fp32) and the next
 layer's product casts it to that dtype, so the next layer sees the same
 values.  The dropout mask comes from Philox keyed by a seed drawn from
 torch's CPU generator (reproducible under torch.manual_seed; not the same
-mask torch's dropout would draw).
+mask torch's dropout would draw).  While the stream is being captured into
+a graph the seed is drawn on the device instead (torch's CUDA generator,
+whose draws advance on every replay) and the kernels read it from there, so
+each replay of a captured training step draws a new mask.
 
 ``cross_entropy_rows`` is ``F.cross_entropy(logits[rows], labels)`` plus the
 argmax hit count of helper/engine.py:22-41, in one kernel each way.
@@ -30,18 +33,23 @@ def _seed() -> int:
 class _ActNormDropout(Function):
     @staticmethod
     def forward(ctx, z, weight, bias, eps, p, act, out_dtype):
-        seed = _seed() if p > 0 else 0
+        seed, seed_dev = 0, None
+        if p > 0:
+            if torch.cuda.is_current_stream_capturing():
+                seed_dev = torch.randint(0, 2 ** 62, (1,), dtype=torch.int64, device=z.device)
+            else:
+                seed = _seed()
         need = any(ctx.needs_input_grad[:3])
-        out, mean, rstd = _ops.act_norm_dropout_fwd(z, weight, bias, eps, p, act, seed, out_dtype, need)
+        out, mean, rstd = _ops.act_norm_dropout_fwd(z, weight, bias, eps, p, act, seed, out_dtype, need, seed_dev)
         if need:
             ctx.save_for_backward(z, weight, mean, rstd)
-        ctx.p, ctx.act, ctx.seed = p, act, seed
+        ctx.p, ctx.act, ctx.seed, ctx.seed_dev = p, act, seed, seed_dev
         return out
 
     @staticmethod
     def backward(ctx, dout):
         z, weight, mean, rstd = ctx.saved_tensors
-        dz, dg, db = _ops.act_norm_dropout_bwd(dout, z, mean, rstd, weight, ctx.p, ctx.act, ctx.seed)
+        dz, dg, db = _ops.act_norm_dropout_bwd(dout, z, mean, rstd, weight, ctx.p, ctx.act, ctx.seed, ctx.seed_dev)
         return (dz if ctx.needs_input_grad[0] else None, dg.to(weight.dtype) if ctx.needs_input_grad[1] else None,
                 db if ctx.needs_input_grad[2] else None, None, None, None, None)
 

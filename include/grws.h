@@ -452,7 +452,10 @@ int grws_repack_finish(const grws_bcsr* g, int64_t num_nodes, const int64_t* win
 /* 0 = identity, 1 = ReLU; LayerNorm over dim (biased variance, eps) with   */
 /* fp32 gamma/beta; dropout with probability p, scale 1/(1-p), element     */
 /* (r, c) kept iff word c%4 of Philox4x32-10 at counter (r_lo, r_hi, c/4,  */
-/* 0), key seed, is >= p * 2^32; the backward recomputes it.  z/out/dout/dz */
+/* 0), key seed, is >= p * 2^32; the backward recomputes it.  seed_dev,     */
+/* when not NULL, points to a device uint64 read in place of seed (a seed   */
+/* drawn on the device, so a captured graph draws a new mask per replay).   */
+/* z/out/dout/dz                                                            */
 /* in F32/F16/BF16; dim a multiple of 4, <= 1024; rows and leading          */
 /* dimensions multiples of 4 elements, 8-byte aligned.  mean/rstd: fp32     */
 /* [rows] saved for the backward (both NULL to skip).  The backward writes  */
@@ -462,14 +465,15 @@ int grws_repack_finish(const grws_bcsr* g, int64_t num_nodes, const int64_t* win
 /* ------------------------------------------------------------------------ */
 int grws_act_norm_dropout_fwd(const void* z, int32_t z_dtype, int64_t ldz, int64_t rows, int64_t dim,
                               int32_t act, const float* gamma, const float* beta, float eps, float p,
-                              uint64_t seed, void* out, int32_t out_dtype, int64_t ldo, float* mean,
-                              float* rstd, void* stream);
+                              uint64_t seed, const uint64_t* seed_dev, void* out, int32_t out_dtype,
+                              int64_t ldo, float* mean, float* rstd, void* stream);
 size_t grws_act_norm_dropout_bwd_workspace_bytes(int64_t rows, int64_t dim);
 int grws_act_norm_dropout_bwd(const void* dout, int32_t dout_dtype, int64_t ldg, const void* z,
                               int32_t z_dtype, int64_t ldz, int64_t rows, int64_t dim, int32_t act,
                               const float* mean, const float* rstd, const float* gamma, float p,
-                              uint64_t seed, void* dz, int64_t lddz, float* dgamma, float* dbeta,
-                              void* workspace, size_t workspace_bytes, void* stream);
+                              uint64_t seed, const uint64_t* seed_dev, void* dz, int64_t lddz,
+                              float* dgamma, float* dbeta, void* workspace, size_t workspace_bytes,
+                              void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Cross-entropy over a subset of the rows of logits [total_rows x ld]      */
