@@ -278,19 +278,27 @@ class BCSRGraph:
         is not a multiple of 128 bytes and this graph gathers every row many
         times (at least 8 column slots per row of x): a 224-byte row at a
         224-byte pitch straddles lines, and the SpMM gathering such rows ran
-        19% slower (c4, 112 columns).  The copy of the last input is kept
-        while that input is alive and unmodified (the layer-0 features of
-        full-graph training are copied once)."""
+        19% slower (c4, 112 columns).  Each input's copy is kept while that
+        input is alive and unmodified, and dropped when it dies: the layer-0
+        features of full-graph training are copied once, although the same
+        graph multiplies other (short-lived) inputs in between."""
         esz = x.element_size()
         if (x.dim() != 2 or x.stride(1) != 1 or (x.stride(0) * esz) % 128 == 0
                 or x.shape[1] * esz < 64 or self.num_tiles * self.tile_cols < 8 * x.shape[0]):
             return x
-        ent = self._cache.get("aligned_x")
+        copies = self._cache.setdefault("aligned_x", {})
+        key = id(x)
+        ent = copies.get(key)
         if ent is not None and ent[0]() is x and ent[1] == x._version:
             return ent[2]
         from .layout import aligned_rows
         xa = aligned_rows(x.detach())
-        self._cache["aligned_x"] = (weakref.ref(x), x._version, xa)
+
+        def _drop(ref, copies=copies, key=key):
+            if copies.get(key, (None,))[0] is ref:
+                del copies[key]
+
+        copies[key] = (weakref.ref(x, _drop), x._version, xa)
         return xa
 
     def spmm(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:

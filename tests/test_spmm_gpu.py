@@ -222,17 +222,28 @@ def test_gather_input_aligned_copy(cuda_device, xdt):
     args = (G.window_offset, G.original_col_indices, G.values_condensed)
     ref = core.spmm(*args, X, 16, plan=G.spmm_plan(112))       # the kernel on the 224-byte pitch
     Y = G.spmm(X)
-    xa = G._cache["aligned_x"][2]
+    xa = G._cache["aligned_x"][id(X)][2]
     assert xa.stride(0) * xa.element_size() % 128 == 0 and torch.equal(xa, X)
+    # another, short-lived input in between (a later layer's product on the
+    # same graph): it gets its own copy, dropped with it, and X's stays
+    T = synth.features(g.num_nodes, 47, seed=9, device=cuda_device).to(xdt)
+    refT = core.spmm(*args, T, 16, plan=G.spmm_plan(47))
+    YT = G.spmm(T)
+    assert id(T) in G._cache["aligned_x"]
+    torch.cuda.synchronize()
+    assert torch.equal(YT.view(torch.int16), refT.view(torch.int16))
+    tid = id(T)
+    del T
+    assert tid not in G._cache["aligned_x"]
     Y2 = G.spmm(X)
-    assert G._cache["aligned_x"][2] is xa                       # reused
+    assert G._cache["aligned_x"][id(X)][2] is xa                # reused
     torch.cuda.synchronize()
     assert torch.equal(Y.view(torch.int16), ref.view(torch.int16))
     assert torch.equal(Y2.view(torch.int16), ref.view(torch.int16))
     with torch.no_grad():
         X.mul_(2)
     Y3 = G.spmm(X)
-    assert G._cache["aligned_x"][2] is not xa
+    assert G._cache["aligned_x"][id(X)][2] is not xa
     ref3 = core.spmm(*args, X, 16, plan=G.spmm_plan(112))
     torch.cuda.synchronize()
     assert torch.equal(Y3.view(torch.int16), ref3.view(torch.int16))
