@@ -112,6 +112,31 @@ def _cached_plan(window_offset: torch.Tensor, col_indices: torch.Tensor, tile_co
     return hit[1]
 
 
+def line_pitched_empty(rows: int, cols: int, dtype: torch.dtype, device, zero: bool = False) -> torch.Tensor:
+    """A [rows, cols] view of a new buffer whose rows start on 128-byte
+    lines (the row pitch rounded up to a multiple of 128 bytes).  Ragged
+    widths (41 or 47 classes) made this way are gathered by the SpMM and
+    widened to a multiple of 8 columns without a copy.  zero: the padding
+    columns (and the values) start at zero; otherwise they are left as
+    allocated."""
+    esz = torch.empty(0, dtype=dtype).element_size()
+    per = max(1, 128 // esz)
+    pitch = (cols + per - 1) // per * per
+    make = torch.zeros if zero else torch.empty
+    return make((rows, pitch), dtype=dtype, device=device)[:, :cols]
+
+
+def mm_line_pitched(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """a @ w (w cast to a's dtype) into a line-pitched output when the
+    output width does not fill whole 128-byte lines (torch's GEMM writes
+    the row-strided view directly); a plain matmul otherwise."""
+    n = w.shape[1]
+    if a.dim() != 2 or (n * a.element_size()) % 128 == 0:
+        return torch.matmul(a, w)
+    out = line_pitched_empty(a.shape[0], n, a.dtype, a.device)
+    return torch.mm(a, w.to(a.dtype), out=out)
+
+
 def _widen(t: torch.Tensor, vec: int) -> torch.Tensor:
     """t [R, C] as [R, C'] with C' = C rounded up to a multiple of vec,
     16-byte aligned rows: a strided view over the row padding t already
@@ -867,8 +892,10 @@ def cross_entropy_fwd(logits: torch.Tensor, rows: Optional[torch.Tensor], labels
 
 def cross_entropy_bwd(logits: torch.Tensor, rows: Optional[torch.Tensor], labels: torch.Tensor,
                       lse: torch.Tensor, dloss: torch.Tensor, counts: torch.Tensor) -> torch.Tensor:
-    """Gradient of cross_entropy_fwd's loss w.r.t. logits (zero outside rows)."""
-    grad = torch.zeros(logits.shape, dtype=logits.dtype, device=logits.device)
+    """Gradient of cross_entropy_fwd's loss w.r.t. logits (zero outside rows),
+    written into a line-pitched buffer (the backward SpMM and the weight
+    gradient then read it without a widening copy)."""
+    grad = line_pitched_empty(logits.shape[0], logits.shape[1], logits.dtype, logits.device, zero=True)
     dl = dloss.detach().float().reshape(1).contiguous()
     L.call("grws_cross_entropy_bwd", L.ptr(logits), L.dtype_code(logits.dtype), logits.stride(0),
            logits.shape[0], logits.shape[1], L.ptr(rows) if rows is not None else None, L.ptr(labels),

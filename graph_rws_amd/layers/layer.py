@@ -164,7 +164,7 @@ class _GraphConvFunction(Function):
             out.addmm_(yt, w_n.to(out.dtype))
             ctx.save_for_backward(yt, xt, w_n, w_s)
         else:
-            y, ms = _spmm_timed(graph, torch.matmul(xh, w_n))
+            y, ms = _spmm_timed(graph, _ops.mm_line_pitched(xh, w_n))
             yt = rows_T(y)
             out = yt.addmm_(xt, w_s.to(yt.dtype))
             ctx.save_for_backward(xh, xt, w_n, w_s)
@@ -176,7 +176,10 @@ class _GraphConvFunction(Function):
     def backward(ctx, grad):
         saved, xt, w_n, w_s = ctx.saved_tensors
         graph = ctx.graph
-        g = grad.contiguous()
+        # row-strided gradients (a line-pitched loss gradient) are used as
+        # they are: every consumer below takes a row stride
+        row_strided = grad.dim() == 2 and grad.stride(1) == 1 and grad.stride(0) >= grad.shape[1]
+        g = grad if row_strided else grad.contiguous()
         need_x, need_xt, need_wn, need_ws = (ctx.needs_input_grad[1], ctx.needs_input_grad[2],
                                              ctx.needs_input_grad[3], ctx.needs_input_grad[4])
         dx = dxt = dwn = dws = None
