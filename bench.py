@@ -258,14 +258,41 @@ def cpu_gcn_epoch(g, X, labels, train_idx, dims, dropout: float) -> float:
     return time.perf_counter() - t0
 
 
-def bench_gcn(cfg: str, dev, epochs: int, warmup: int, cpu: bool) -> dict:
+def bench_gcn_graphed(G, X, labels, train_idx, d_pad, hidden, classes, layers, dt, dev, epochs: int,
+                      warmup: int) -> dict:
+    """The same step captured once on a HIP graph and replayed
+    (GraphedFullStep): a fresh model of the same init, Adam with
+    capturable=True; median over at least 20 replays."""
+    from graph_rws_amd.helper import GraphedFullStep
+    from graph_rws_amd.models import GCN_BCSR
+    torch.manual_seed(13)
+    model_g = GCN_BCSR(d_pad, hidden, classes, layers, dropout=0.5, use_checkpoint=False).to(dev)
+    opt_g = torch.optim.Adam(model_g.parameters(), lr=0.01, capturable=True)
+    step = GraphedFullStep(model_g, G, X, labels, train_idx, opt_g, dev, warmup=max(2, warmup),
+                           autocast_dtype=None if dt == torch.float32 else dt)
+    n_g = max(epochs, 20)
+    step()
+    torch.cuda.synchronize(dev)
+    tg = []
+    for _ in range(n_g):
+        t0 = time.perf_counter()
+        loss_g, _ = step()
+        torch.cuda.synchronize(dev)
+        tg.append(time.perf_counter() - t0)
+    tg.sort()
+    return {"epoch_ms": round(1e3 * tg[len(tg) // 2], 3), "epoch_ms_min": round(1e3 * tg[0], 3),
+            "epochs": n_g, "final_loss": round(float(loss_g), 4),
+            "how": "the same step captured once on a HIP graph (torch.cuda.graph) and replayed"}
+
+
+def bench_gcn(cfg: str, dev, epochs: int, warmup: int, cpu: bool, graphed: bool = True) -> dict:
     """Full-graph training epochs of GCN_BCSR on config `cfg` (c1: the tiny
     fp32 step; c3, c4: 3 layers, hidden 256, autocast to the config dtype,
     BCSR values in that dtype, 16x16 tiles).  Epoch = forward + loss +
     backward + clip + Adam, synchronised at its end."""
     from graph_rws_amd import synth
     from graph_rws_amd.data import BCSRGraph
-    from graph_rws_amd.helper import GraphedFullStep, train_epoch_full
+    from graph_rws_amd.helper import train_epoch_full
     from graph_rws_amd.models import GCN_BCSR
     d_raw, d_pad, kind, hidden, classes, layers, dname = GCN_CONFIGS[cfg]
     dt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dname]
@@ -302,27 +329,9 @@ def bench_gcn(cfg: str, dev, epochs: int, warmup: int, cpu: bool) -> dict:
            "classes": classes, "layers": layers, "dtype": dname, "tile": "16x16",
            "epochs": epochs, "epoch_ms": round(1e3 * times[len(times) // 2], 3),
            "epoch_ms_min": round(1e3 * times[0], 3), "final_loss": round(float(loss), 4)}
-    # the same step captured once on a HIP graph and replayed (GraphedFullStep):
-    # a fresh model of the same init, Adam with capturable=True
-    torch.manual_seed(13)
-    model_g = GCN_BCSR(d_pad, hidden, classes, layers, dropout=0.5, use_checkpoint=False).to(dev)
-    opt_g = torch.optim.Adam(model_g.parameters(), lr=0.01, capturable=True)
-    step = GraphedFullStep(model_g, G, X, labels, train_idx, opt_g, dev, warmup=max(2, warmup),
-                           autocast_dtype=None if dt == torch.float32 else dt)
-    n_g = max(epochs, 20)
-    step()
-    torch.cuda.synchronize(dev)
-    tg = []
-    for _ in range(n_g):
-        t0 = time.perf_counter()
-        loss_g, _ = step()
-        torch.cuda.synchronize(dev)
-        tg.append(time.perf_counter() - t0)
-    tg.sort()
-    out["graphed"] = {"epoch_ms": round(1e3 * tg[len(tg) // 2], 3), "epoch_ms_min": round(1e3 * tg[0], 3),
-                      "epochs": n_g, "final_loss": round(float(loss_g), 4),
-                      "how": "the same step captured once on a HIP graph (torch.cuda.graph) and replayed"}
-    del step, model_g, opt_g
+    if graphed:
+        out["graphed"] = bench_gcn_graphed(G, X, labels, train_idx, d_pad, hidden, classes, layers, dt,
+                                           dev, epochs, warmup)
     if cpu:
         torch.set_num_threads(os.cpu_count() or 1)
         dims = [d_pad] + [hidden] * (layers - 1) + [classes]
@@ -555,6 +564,8 @@ def main():
     ap.add_argument("--minibatch-batches", type=int, default=40)
     ap.add_argument("--gcn-epochs", type=int, default=5)
     ap.add_argument("--gcn-configs", default="c1,c3,c4")
+    ap.add_argument("--no-gcn-graphed", action="store_true",
+                    help="skip the GCN legs' captured-graph replays")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -685,7 +696,8 @@ def main():
         out["sampling"] = bench_sampling(dev, args.sampling_batches, 3, not args.no_cpu_baseline)
     if not args.no_gcn:
         out["spmm_c2"] = bench_spmm_c2(dev, cpu=not args.no_cpu_baseline)
-        out["gcn"] = {c: bench_gcn(c, dev, args.gcn_epochs, 2, not args.no_cpu_baseline)
+        out["gcn"] = {c: bench_gcn(c, dev, args.gcn_epochs, 2, not args.no_cpu_baseline,
+                                   graphed=not args.no_gcn_graphed)
                       for c in args.gcn_configs.split(",") if c}
     if not args.no_dps:
         out["dps"] = bench_dps(dev, not args.no_cpu_baseline)

@@ -18,7 +18,10 @@
 //     LDS read: one ds_read_b64_tr_b16 per operand per 16 k;
 //   * every chunk writes an fp32 partial; a second kernel adds the chunks
 //     in order (deterministic, no atomics) and writes C.
-// A and B are each read once per N-tile / M-tile of the other operand.
+// A and B are each read once per N-tile / M-tile of the other operand; the
+// work-groups of one K-chunk (all its output tiles) are dealt to the same
+// XCD one after another, so the second read of a chunk's rows hits that
+// XCD's L2 instead of going out to memory again.
 #include "grws_internal.h"
 
 namespace grws {
@@ -60,15 +63,24 @@ template <int DT>
 __global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                               const uint16_t* __restrict__ B, int64_t ldb,
                                                               int64_t K, int M, int N, int64_t kc,
-                                                              float* __restrict__ partials) {
+                                                              int64_t nchunks, float* __restrict__ partials) {
     __shared__ __attribute__((aligned(16))) uint16_t sA[2][kStep * kPitch];
     __shared__ __attribute__((aligned(16))) uint16_t sB[2][kStep * kPitch];
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
-    const int i0 = blockIdx.x * kT;
-    const int j0 = blockIdx.y * kT;
-    const int64_t chunk = blockIdx.z;
+    // work-groups are dealt round-robin to the 8 XCDs: block b runs on XCD
+    // b % 8.  Slot b / 8 of an XCD walks the output tiles of chunk
+    // (slot / tiles) * 8 + xcd, so a chunk's tiles share one L2.
+    const int tiles_m = (M + kT - 1) / kT;
+    const int tiles = tiles_m * ((N + kT - 1) / kT);
+    const int64_t blk = blockIdx.x;
+    const int64_t slot = blk >> 3;
+    const int t = (int)(slot % tiles);
+    const int64_t chunk = (slot / tiles) * 8 + (blk & 7);
+    if (chunk >= nchunks) return;  // uniform over the work-group
+    const int i0 = (t % tiles_m) * kT;
+    const int j0 = (t / tiles_m) * kT;
     const int64_t kb = chunk * kc;
     const int64_t ke = kb + kc < K ? kb + kc : K;
     const int wm = (wave & 1) * 64;
@@ -225,15 +237,17 @@ extern "C" int grws_gemm_tn(const void* a, int64_t lda, const void* b, int64_t l
     if (nch > 0) {
         const int64_t kc = ((K + nch - 1) / nch + kStep - 1) / kStep * kStep;
         chunks = (K + kc - 1) / kc;
-        dim3 grid((unsigned)((M + kT - 1) / kT), (unsigned)((N + kT - 1) / kT), (unsigned)chunks);
+        const int64_t tiles = ((M + kT - 1) / kT) * ((N + kT - 1) / kT);
+        const int64_t blocks = (chunks + 7) / 8 * 8 * tiles;  // chunks padded to whole XCD rounds
+        GRWS_CHECK_ARG(blocks <= INT32_MAX, "gemm_tn: too many work-groups");
         if (in_dtype == GRWS_F16)
-            hipLaunchKernelGGL(gemm_tn_partial_kernel<GRWS_F16>, grid, dim3(256), 0, stream,
+            hipLaunchKernelGGL(gemm_tn_partial_kernel<GRWS_F16>, dim3((unsigned)blocks), dim3(256), 0, stream,
                                static_cast<const uint16_t*>(a), lda, static_cast<const uint16_t*>(b), ldb, K,
-                               (int)M, (int)N, kc, static_cast<float*>(workspace));
+                               (int)M, (int)N, kc, chunks, static_cast<float*>(workspace));
         else
-            hipLaunchKernelGGL(gemm_tn_partial_kernel<GRWS_BF16>, grid, dim3(256), 0, stream,
+            hipLaunchKernelGGL(gemm_tn_partial_kernel<GRWS_BF16>, dim3((unsigned)blocks), dim3(256), 0, stream,
                                static_cast<const uint16_t*>(a), lda, static_cast<const uint16_t*>(b), ldb, K,
-                               (int)M, (int)N, kc, static_cast<float*>(workspace));
+                               (int)M, (int)N, kc, chunks, static_cast<float*>(workspace));
         GRWS_LAUNCH_CHECK();
     }
     {
