@@ -137,6 +137,42 @@ def mm_line_pitched(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return torch.mm(a, w.to(a.dtype), out=out)
 
 
+def pair_pitch(n: int, esz: int) -> int:
+    """Row pitch (elements) of mm_pair_line_pitched's output: two products
+    of width n, each padded to whole 128-byte lines."""
+    per = max(1, 128 // esz)
+    return 2 * ((n + per - 1) // per * per)
+
+
+def fuse_self_pays(rows: int, n: int, esz: int) -> bool:
+    """Whether to make X W_n and X W_s with one GEMM and add the self term in
+    the SpMM's epilogue (measured on c3/c4): it saves the second pass over X
+    and the separate add, but the SpMM then gathers rows of the paired
+    output (twice the pitch) and reads the self term.  That pays for narrow
+    outputs (the class layer: c4 3.19 -> 2.54 ms) and while the paired
+    output stays within the 256 MB Infinity Cache (c3 hidden layers, even);
+    a wide output past it lost (c4 hidden layer: 8.89 -> 9.05 ms)."""
+    pitch_bytes = pair_pitch(n, esz) * esz
+    return pitch_bytes <= 512 or rows * pitch_bytes <= (256 << 20)
+
+
+def mm_pair_line_pitched(a: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor):
+    """(a @ w1, a @ w2) from one GEMM over the weights side by side (cast to
+    a's dtype): a [M, K], w1 and w2 [K, N].  Each product starts on a
+    128-byte line of the shared output rows (N is padded with zero weight
+    columns to whole lines), so both are line-pitched [M, N] views."""
+    K, N = w1.shape
+    npad = pair_pitch(N, a.element_size()) // 2
+    if npad == N:
+        w = torch.cat([w1, w2], 1).to(a.dtype)
+    else:
+        w = torch.zeros((K, 2 * npad), dtype=a.dtype, device=a.device)
+        w[:, :N] = w1
+        w[:, npad:npad + N] = w2
+    ts = torch.matmul(a, w)
+    return ts[:, :N], ts[:, npad:npad + N]
+
+
 def _widen(t: torch.Tensor, vec: int) -> torch.Tensor:
     """t [R, C] as [R, C'] with C' = C rounded up to a multiple of vec,
     16-byte aligned rows: a strided view over the row padding t already
@@ -237,13 +273,19 @@ def _check_graph(window_offset, col_indices, values, tile_cols):
 def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.Tensor,
          x: torch.Tensor, tile_cols: int, plan: Optional[SpmmPlan] = None,
          out: Optional[torch.Tensor] = None, packed: Optional[PackedTiles] = None,
-         max_window_slabs: int = 0) -> torch.Tensor:
+         max_window_slabs: int = 0, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Y[16W, N] = A X on the device (H1 kernel).  x: [x_rows, N] (row stride
     may exceed N); out dtype = x dtype.  packed: the graph's packed tiles
     (read instead of the dense values when x has the values' dtype).
     max_window_slabs: an upper bound of every window's slabs when known
-    (0 = unknown); lets a call without a plan use the buffer-load kernel."""
+    (0 = unknown); lets a call without a plan use the buffer-load kernel.
+    residual: R [r_rows, N] in x's dtype, added to the first r_rows rows of
+    the product before rounding (Y = A X + R there)."""
     _check_graph(window_offset, col_indices, values, tile_cols)
+    if residual is not None:
+        if (residual.dim() != 2 or residual.shape[1] != x.shape[1] or residual.dtype != x.dtype
+                or residual.stride(1) != 1 or residual.device != x.device):
+            raise ValueError("residual must be [rows, N] with x's dtype and device and unit column stride")
     if not x.is_cuda:
         raise RuntimeError("input_B must be a CUDA tensor")
     if x.dim() != 2 or x.stride(1) != 1:
@@ -261,7 +303,8 @@ def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.T
         # columns of the result (columns are independent).
         x = _widen(x, vec)
         full = spmm(window_offset, col_indices, values, x, tile_cols, plan=plan, packed=packed,
-                    max_window_slabs=max_window_slabs)
+                    max_window_slabs=max_window_slabs,
+                    residual=None if residual is None else _widen(residual, vec))
         return full[:, :N]
     if out is None:
         out = torch.empty((W * 16, N), dtype=x.dtype, device=x.device)
@@ -280,6 +323,14 @@ def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.T
         wsb = int(L.load().grws_spmm_workspace_bytes(ctypes.byref(pv), N))
         if wsb:
             ws = torch.empty(wsb, dtype=torch.uint8, device=x.device)
+    if residual is not None:
+        pk = packed.view() if packed is not None and x.dtype == values.dtype else None
+        L.call("grws_spmm_residual", ctypes.byref(view), ctypes.byref(pk) if pk is not None else None,
+               ctypes.byref(pv) if pv is not None else None,
+               L.ptr(x), L.dtype_code(x.dtype), x.shape[0], x.stride(0), N,
+               L.ptr(residual), residual.stride(0), residual.shape[0], L.ptr(out),
+               L.dtype_code(out.dtype), out.stride(0), L.ptr(ws), wsb, L.stream_of(x.device))
+        return out
     if packed is not None and x.dtype == values.dtype:
         pk = packed.view()
         L.call("grws_spmm_packed", ctypes.byref(view), ctypes.byref(pk),

@@ -111,6 +111,10 @@ struct SpmmArgs {
     // own window range), instead of each XCD walking its own share of the
     // (chunk, window) pairs
     int32_t chunk_major;
+    // optional residual R (the y dtype): Y = A X + R on rows < res_rows
+    const void* res;
+    int64_t ldr;
+    int64_t res_rows;
 };
 
 // Output conversion for the three element types.
@@ -125,8 +129,20 @@ __device__ __forceinline__ void store_out(void* y, int64_t idx, float v) {
     }
 }
 
-// Writes a work-group's 16 x NC result: to Y (converted), or as an fp32
-// partial for a split window.  With WPB > 1 the waves' accumulators are
+// Residual element as fp32 (R has the output's element type).
+template <int XT>
+__device__ __forceinline__ float load_res(const void* r, int64_t idx) {
+    if constexpr (XT == GRWS_F32) {
+        return static_cast<const float*>(r)[idx];
+    } else if constexpr (XT == GRWS_F16) {
+        return (float)static_cast<const _Float16*>(r)[idx];
+    } else {
+        return __uint_as_float((uint32_t)static_cast<const uint16_t*>(r)[idx] << 16);
+    }
+}
+
+// Writes a work-group's 16 x NC result: to Y (converted, after adding the
+// residual when there is one), or as an fp32 partial for a split window.  With WPB > 1 the waves' accumulators are
 // first added in LDS in wave order (deterministic); `stage_all` must hold
 // 16 * NC floats.
 template <int XT, int NBLK, int WPB, typename S>
@@ -158,7 +174,11 @@ __device__ __forceinline__ void spmm_epilogue(const SpmmArgs& a, const float4_t*
             const int64_t row0 = w * 16;
             for (int e = threadIdx.x; e < 16 * NC; e += 64 * WPB) {
                 const int r = e / NC, c = e % NC;
-                if (n0 + c < N) store_out<XT>(a.y, (row0 + r) * a.ldy + n0 + c, red[e]);
+                if (n0 + c < N) {
+                    float v = red[e];
+                    if (a.res && row0 + r < a.res_rows) v += load_res<XT>(a.res, (row0 + r) * a.ldr + n0 + c);
+                    store_out<XT>(a.y, (row0 + r) * a.ldy + n0 + c, v);
+                }
             }
         } else {
             float* P = a.partials + ((int64_t)slot * a.nchunks + chunk) * (16 * NC);
@@ -173,7 +193,12 @@ __device__ __forceinline__ void spmm_epilogue(const SpmmArgs& a, const float4_t*
             const int64_t col = n0 + b * 16 + bn;
             if (col < N) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) store_out<XT>(a.y, (row0 + 4 * ag + i) * a.ldy + col, acc[b][i]);
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t row = row0 + 4 * ag + i;
+                    float v = acc[b][i];
+                    if (a.res && row < a.res_rows) v += load_res<XT>(a.res, row * a.ldr + col);
+                    store_out<XT>(a.y, row * a.ldy + col, v);
+                }
             }
         }
     } else {
@@ -425,7 +450,7 @@ __global__ __launch_bounds__(64 * WPB) void spmm_fwd_kernel(SpmmArgs a) {
 //     row 4*(l/16) + k/4 at column 16*b + 4*(k%4), and the group's 64 halves
 //     come back transposed so lane i holds column i of rows 4g..4g+3.
 // Requires (checked on the host): x_rows < 2^24, row pitch < 2^24 bytes,
-// 2 * (x_rows + 1) rows of X addressable in 32 bits, and every work item's
+// x_rows + 1 rows of X addressable in 32 bits, and every work item's
 // A within 2^31 bytes.
 //
 // PK: A comes from packed tiles instead of the dense 16x16 values.  A tile's
@@ -543,10 +568,11 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
 
     const int rbase = NLD * (lane / LPR);  // first of the lane's slab rows
     const bool lrow = rbase < 16;          // NBLK == 1: lanes 32..63 stage nothing
-    // a lane whose 8 columns lie past n_cols (the last chunk) reads nothing:
-    // its offset starts at (x_rows + 1) rows, past the resource whatever the row
-    const uint32_t colb = n0 + (lane % LPR) * VEC < a.n_cols ? (uint32_t)((n0 + (lane % LPR) * VEC) * SZ)
-                                                              : (uint32_t)((a.x_rows + 1) * a.ldx * SZ);
+    // a lane whose columns lie past n_cols (the last chunk) reads nothing:
+    // it always takes row x_rows, which lies past the resource (so every
+    // offset stays below (x_rows + 1) rows)
+    const bool lcol = n0 + (lane % LPR) * VEC < a.n_cols;
+    const uint32_t colb = lcol ? (uint32_t)((n0 + (lane % LPR) * VEC) * SZ) : 0u;
     const uint32_t ldxb = (uint32_t)(a.ldx * SZ);
     const uint32_t xr = (uint32_t)a.x_rows;
     const int ag = lane >> 4;
@@ -578,7 +604,7 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
         for (int i = 0; i < NLD; ++i) {
             int32_t c;
             if constexpr (NLD == 1) c = cv; else c = cv[i];
-            bool ok = lrow && (uint32_t)c < xr;
+            bool ok = lrow && lcol && (uint32_t)c < xr;
             if constexpr (TC == 8) ok = ok && (s * 16 + rbase + i < nslots);  // half-empty last slab
             const uint32_t row = ok ? (uint32_t)c : xr;  // row x_rows lies past the resource
             regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rsX, (int)(__umul24(row, ldxb) + colb), 0, 0);
@@ -739,7 +765,8 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
 template <int XT, int NBLK>
 __global__ __launch_bounds__(64) void spmm_fixup_kernel(const int32_t* __restrict__ split, int64_t num_split,
                                                         const float* __restrict__ partials, int32_t nchunks,
-                                                        void* y, int64_t ldy, int64_t N, int64_t col_base) {
+                                                        void* y, int64_t ldy, int64_t N, int64_t col_base,
+                                                        const void* res, int64_t ldr, int64_t res_rows) {
     constexpr int NC = NBLK * 16;
     constexpr int U = 8;
     const int64_t blk = blockIdx.x / NBLK;  // (split window, chunk)
@@ -765,10 +792,12 @@ __global__ __launch_bounds__(64) void spmm_fixup_kernel(const int32_t* __restric
         for (int j = 0; j < U; ++j) s += t[j];
     }
     for (; k < cnt; ++k) s += __builtin_nontemporal_load(p + k * stride);
-    const int64_t o = (w * 16 + r) * ldy + n0 + c;
+    const int64_t row = w * 16 + r;
+    const int64_t o = row * ldy + n0 + c;
+    const bool add = res && row < res_rows;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        if (n0 + c + i < N) store_out<XT>(y, o + i, s[i]);
+        if (n0 + c + i < N) store_out<XT>(y, o + i, add ? s[i] + load_res<XT>(res, row * ldr + n0 + c + i) : s[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -946,7 +975,7 @@ bool buffer_path_fits(const grws_bcsr* A, const grws_spmm_plan* plan, int64_t x_
         if (atoi(e) == 1) return false;
     const int64_t ldxb = ldx * (int64_t)esz;
     if (x_rows <= 0 || x_rows >= (1 << 24) || ldxb >= (1 << 24)) return false;
-    if (2 * (x_rows + 1) * ldxb + nc * (int64_t)esz >= ((int64_t)1 << 32)) return false;
+    if ((x_rows + 1) * ldxb + nc * (int64_t)esz >= ((int64_t)1 << 32)) return false;
     const int64_t sza = A->values_dtype == GRWS_F32 ? 4 : 2;
     const int64_t slabs = plan && plan->items      ? (int64_t)plan->slabs_per_item
                           : A->max_window_slabs > 0 ? (int64_t)A->max_window_slabs
@@ -963,23 +992,28 @@ int launch_fixup(const grws_spmm_plan* plan, const SpmmArgs& a, int nblk, hipStr
     switch (nblk) {
         case 1:
             hipLaunchKernelGGL((spmm_fixup_kernel<XT, 1>), dim3((unsigned)grid), dim3(64), 0, stream, plan->split,
-                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base,
+                               a.res, a.ldr, a.res_rows);
             break;
         case 2:
             hipLaunchKernelGGL((spmm_fixup_kernel<XT, 2>), dim3((unsigned)grid), dim3(64), 0, stream, plan->split,
-                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base,
+                               a.res, a.ldr, a.res_rows);
             break;
         case 4:
             hipLaunchKernelGGL((spmm_fixup_kernel<XT, 4>), dim3((unsigned)grid), dim3(64), 0, stream, plan->split,
-                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base,
+                               a.res, a.ldr, a.res_rows);
             break;
         case 16:
             hipLaunchKernelGGL((spmm_fixup_kernel<XT, 16>), dim3((unsigned)grid), dim3(64), 0, stream, plan->split,
-                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base,
+                               a.res, a.ldr, a.res_rows);
             break;
         default:
             hipLaunchKernelGGL((spmm_fixup_kernel<XT, 8>), dim3((unsigned)grid), dim3(64), 0, stream, plan->split,
-                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base);
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base,
+                               a.res, a.ldr, a.res_rows);
             break;
     }
     GRWS_LAUNCH_CHECK();
@@ -1168,8 +1202,9 @@ constexpr int64_t kPackMaxValues = ((int64_t)1 << 30) - 16;
 constexpr int64_t kPackPad = 8;
 
 int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_plan* plan, const void* x,
-              int32_t x_dtype, int64_t x_rows, int64_t ldx, int64_t n_cols, void* y, int32_t y_dtype, int64_t ldy,
-              void* workspace, size_t workspace_bytes, void* stream_) {
+              int32_t x_dtype, int64_t x_rows, int64_t ldx, int64_t n_cols, const void* res, int64_t ldr,
+              int64_t res_rows, void* y, int32_t y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes,
+              void* stream_) {
     clear_error();
     hipStream_t stream = as_stream(stream_);
     GRWS_CHECK_ARG(A != nullptr, "spmm: null graph");
@@ -1191,6 +1226,11 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
         GRWS_CHECK_ARG(A->num_tiles == 0 || (P->header && (P->values || P->num_values == 0)),
                        "spmm_packed: null packed arrays");
         GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(P->header) % 4 == 0, "spmm_packed: header not 4-byte aligned");
+    }
+    if (res) {
+        GRWS_CHECK_ARG(ldr >= n_cols && res_rows >= 0, "spmm_residual: ldr < n_cols or negative r_rows");
+        GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(res) % dtype_size(x_dtype) == 0,
+                       "spmm_residual: residual not aligned to its element size");
     }
     if (A->num_windows == 0 || n_cols == 0) return GRWS_OK;
     GRWS_CHECK_ARG(A->window_offset && y, "spmm: null pointer");
@@ -1216,6 +1256,9 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
     a.y = y;
     a.ldy = ldy;
     a.nchunks = (int32_t)((n_cols + nc - 1) / nc);
+    a.res = res;
+    a.ldr = ldr;
+    a.res_rows = res ? res_rows : 0;
     if (plan) {
         GRWS_CHECK_ARG(plan->items != nullptr || plan->num_items == 0, "spmm: plan without items");
         a.items = plan->items;
@@ -1303,15 +1346,23 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
 extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const void* x, int32_t x_dtype,
                          int64_t x_rows, int64_t ldx, int64_t n_cols, void* y, int32_t y_dtype, int64_t ldy,
                          void* workspace, size_t workspace_bytes, void* stream) {
-    return spmm_impl(A, nullptr, plan, x, x_dtype, x_rows, ldx, n_cols, y, y_dtype, ldy, workspace, workspace_bytes,
-                     stream);
+    return spmm_impl(A, nullptr, plan, x, x_dtype, x_rows, ldx, n_cols, nullptr, 0, 0, y, y_dtype, ldy, workspace,
+                     workspace_bytes, stream);
 }
 
 extern "C" int grws_spmm_packed(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_plan* plan,
                                 const void* x, int32_t x_dtype, int64_t x_rows, int64_t ldx, int64_t n_cols, void* y,
                                 int32_t y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
-    return spmm_impl(A, P, plan, x, x_dtype, x_rows, ldx, n_cols, y, y_dtype, ldy, workspace, workspace_bytes,
-                     stream);
+    return spmm_impl(A, P, plan, x, x_dtype, x_rows, ldx, n_cols, nullptr, 0, 0, y, y_dtype, ldy, workspace,
+                     workspace_bytes, stream);
+}
+
+extern "C" int grws_spmm_residual(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_plan* plan,
+                                  const void* x, int32_t x_dtype, int64_t x_rows, int64_t ldx, int64_t n_cols,
+                                  const void* r, int64_t ldr, int64_t r_rows, void* y, int32_t y_dtype, int64_t ldy,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+    return spmm_impl(A, P, plan, x, x_dtype, x_rows, ldx, n_cols, r, ldr, r_rows, y, y_dtype, ldy, workspace,
+                     workspace_bytes, stream);
 }
 
 namespace {

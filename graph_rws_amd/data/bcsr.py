@@ -301,14 +301,16 @@ class BCSRGraph:
         copies[key] = (weakref.ref(x, _drop), x._version, xa)
         return xa
 
-    def spmm(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """Y[16W, N] = A x on the device (columns >= x.shape[0] contribute nothing)."""
+    def spmm(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+             residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Y[16W, N] = A x on the device (columns >= x.shape[0] contribute
+        nothing); plus residual on its rows when given (Y = A x + R there)."""
         from ..core import spmm as _spmm
         x = self._gather_input(x)
         return _spmm(self.window_offset, self.original_col_indices, self.values_condensed, x,
                      self.tile_cols, plan=self.spmm_plan(x.shape[1]), out=out,
                      packed=self.packed_tiles() if x.dtype == self.values_condensed.dtype else None,
-                     max_window_slabs=getattr(self, "max_window_slabs", None) or 0)
+                     max_window_slabs=getattr(self, "max_window_slabs", None) or 0, residual=residual)
 
     def transpose(self) -> "BCSRGraph":
         """Cached BCSR of A^T (num_cols x 16W), built on the device.  Rebuilt

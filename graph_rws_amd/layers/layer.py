@@ -23,15 +23,21 @@ from ..core import ops as _ops
 from ..helper.timer import record_spmm_time
 
 
-def _spmm_timed(graph, x: torch.Tensor):
+# Add the self path's product inside the SpMM's epilogue (one GEMM makes
+# both X W_n and X W_s) when the targets are (nearly) all of X's rows;
+# False restores the separate beta=1 GEMM.
+FUSED_SELF = True
+
+
+def _spmm_timed(graph, x: torch.Tensor, residual: torch.Tensor = None):
     """graph.spmm with the reference's (output, ms) convention (bind.cpp:124-130)."""
     if not _ops.TIMING:
-        return graph.spmm(x), 0.0
+        return graph.spmm(x, residual=residual), 0.0
     s = torch.cuda.current_stream(x.device)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(s)
-    y = graph.spmm(x)
+    y = graph.spmm(x, residual=residual)
     e1.record(s)
     e1.synchronize()
     return y, float(e0.elapsed_time(e1))
@@ -163,6 +169,14 @@ class _GraphConvFunction(Function):
             out = torch.matmul(xt, w_s)
             out.addmm_(yt, w_n.to(out.dtype))
             ctx.save_for_backward(yt, xt, w_n, w_s)
+        elif (FUSED_SELF and x_tgt is None and T <= 16 * graph.num_windows and 10 * T >= 9 * xh.shape[0]
+              and xh.is_cuda and _ops.fuse_self_pays(xh.shape[0], w_n.shape[1], xh.element_size())):
+            # out = A (X W_n)[:T] + X[:T] W_s: both products from one GEMM,
+            # the self term added by the SpMM before it rounds Y
+            t_n, t_s = _ops.mm_pair_line_pitched(xh, w_n, w_s)
+            y, ms = _spmm_timed(graph, t_n, residual=t_s[:T])
+            out = y[:T]
+            ctx.save_for_backward(xh, xt, w_n, w_s)
         else:
             y, ms = _spmm_timed(graph, _ops.mm_line_pitched(xh, w_n))
             yt = rows_T(y)

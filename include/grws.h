@@ -180,6 +180,18 @@ int grws_spmm_packed(const grws_bcsr* A, const grws_packed_tiles* P, const grws_
                      void* y, int32_t y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/* Y = A X + R: as grws_spmm_packed (P may be NULL for the dense tiles),
+ * with R [r_rows x ldr] in the y dtype added to rows < r_rows of the
+ * product in fp32 before Y is rounded; rows >= r_rows get A X alone.  R may
+ * be Y itself (each element is read before it is written).  No counterpart
+ * in the reference, which adds the self path's product with a separate
+ * tensor add after the SpMM (layers/layer.py:150-191); the graph
+ * convolution fuses that add here. */
+int grws_spmm_residual(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_plan* plan,
+                       const void* x, int32_t x_dtype, int64_t x_rows, int64_t ldx, int64_t n_cols,
+                       const void* r, int64_t ldr, int64_t r_rows, void* y, int32_t y_dtype, int64_t ldy,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* CSR -> BCSR on host cores.  Replaces core_lib.csr_to_bcsr_cpu             */
 /* (bind.cpp:143-150 -> convert_wrapper.cpp:27-180): same layout, same       */

@@ -192,3 +192,18 @@ def test_packed_tiles_reject_bad_arguments_without_launching():
     st = lib.grws_spmm_packed(ctypes.byref(view), ctypes.byref(pk), None, None, L.GRWS_F16, 0, 8, 8, None,
                               L.GRWS_F16, 8, None, 0, None)
     assert st == -1 and b"num_values" in lib.grws_last_error()
+
+
+def test_spmm_residual_rejects_bad_arguments_without_launching():
+    """grws_spmm_residual checks the residual's leading dimension and row
+    count before anything touches the device."""
+    lib = L.load()
+    view = L.BcsrView(None, None, None, 1, 0, 16, 16, L.GRWS_F16, 0)
+    r = ctypes.c_void_p(16)
+    st = lib.grws_spmm_residual(ctypes.byref(view), None, None, None, L.GRWS_F16, 0, 8, 8, r, 4, 16, None,
+                                L.GRWS_F16, 8, None, 0, None)
+    assert st == L.GRWS_E_INVALID and b"ldr" in lib.grws_last_error()
+    st = lib.grws_spmm_residual(ctypes.byref(view), None, None, None, L.GRWS_F16, 0, 8, 8, r, 8, -1, None,
+                                L.GRWS_F16, 8, None, 0, None)
+    assert st == L.GRWS_E_INVALID
+

@@ -167,3 +167,40 @@ def test_gcn_loss_decreases(cuda_device):
     opt = torch.optim.Adam(model.parameters(), lr=0.01)
     losses = [train_epoch_full(model, G, X, labels, idx, opt, cuda_device)[0] for _ in range(30)]
     assert losses[-1] < 0.8 * losses[0], losses
+
+
+@pytest.mark.parametrize("dt", [None, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("fout", [16, 47, 256])
+def test_fused_self_path_matches_separate_add(cuda_device, dt, fout):
+    """The convolution's self product added in the SpMM epilogue (one GEMM
+    for X W_n and X W_s) against the separate beta=1 GEMM: outputs within
+    the rounding of the sum, and the same gradients (the backward is the
+    same computation)."""
+    from graph_rws_amd.layers import layer as layer_mod
+    print(f"case fused-self dt={dt} fout={fout}", flush=True)
+    g = synth.chung_lu(3000, 60000, 2.1, seed=fout)
+    G = BCSRGraph.from_csr(g.row_ptr.to(cuda_device), g.col_idx.to(cuda_device), g.values.to(cuda_device),
+                           g.num_nodes, g.num_nodes, tile_cols=16, device=cuda_device,
+                           values_dtype=torch.float32 if dt is None else dt)
+    torch.manual_seed(fout)
+    conv = BCSRGraphConv(96, fout).to(cuda_device)
+    X0 = synth.features(g.num_nodes, 96, seed=3, device=cuda_device)
+    outs, grads = [], []
+    for fused in (True, False):
+        layer_mod.FUSED_SELF = fused
+        try:
+            X = X0.clone().requires_grad_(True)
+            conv.zero_grad()
+            with torch.autocast("cuda", dtype=dt or torch.float16, enabled=dt is not None):
+                y = conv(G, X, features_target=X)           # the model's full-graph call
+            y.float().square().sum().backward()
+            outs.append(y.detach().float())
+            grads.append([X.grad.clone(), conv.weight_neigh.grad.clone(), conv.weight_self.grad.clone()])
+        finally:
+            layer_mod.FUSED_SELF = True
+    torch.cuda.synchronize()
+    tol = 1e-5 if dt is None else 2e-2
+    scale = float(outs[1].abs().max())
+    assert float((outs[0] - outs[1]).abs().max()) <= tol * scale
+    for a, b in zip(grads[0], grads[1]):
+        assert float((a - b).abs().max()) <= tol * float(b.abs().max()) + 1e-6

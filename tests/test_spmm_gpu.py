@@ -329,3 +329,63 @@ def test_chunk_widths_and_work_orders_agree(cuda_device, xdt, slabs, big_x):
         torch.cuda.synchronize()
         assert torch.equal(Y.view(torch.int16), ref.view(torch.int16)), env
     _check(G, X[: g.num_nodes], ref, xdt)
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N", [16, 47, 128, 256, 300])
+@pytest.mark.parametrize("variant", ["plain", "split", "packed", "two_waves", "element_masked"])
+def test_spmm_residual_parity(cuda_device, xdt, N, variant):
+    """Y = A X + R on the first r_rows rows (grws_spmm_residual): against the
+    float64 oracle plus R, with the oracle's bound widened by |R| for the
+    one rounding of the sum; rows past r_rows equal the plain product."""
+    import os
+    print(f"case residual xdt={xdt} N={N} {variant}", flush=True)
+    if variant == "packed" and xdt == torch.float32:
+        pytest.skip("packed tiles hold 16-bit values")
+    g = synth.chung_lu(2500, 40000, 2.1, seed=N + 3)
+    G = _bcsr(g, 16, cuda_device, vdt=torch.float32 if xdt == torch.float32 else xdt)
+    X = synth.features(g.num_nodes, N, seed=N, device=cuda_device).to(xdt)
+    rows = 16 * G.num_windows
+    r_rows = rows - 37
+    R = (synth.features(r_rows, N, seed=N + 9, device=cuda_device) * 4).to(xdt)
+    args = (G.window_offset, G.original_col_indices, G.values_condensed, X, 16)
+    plan = core.build_spmm_plan(G.window_offset, G.num_tiles, 16, 2) if variant == "split" else None
+    packed = core.pack_tiles(G.window_offset, G.original_col_indices, G.values_condensed, 16) \
+        if variant == "packed" else None
+    env = {"two_waves": {"GRWS_SPMM_WAVES": "2"}, "element_masked": {"GRWS_SPMM_KERNEL": "1"}}.get(variant, {})
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        Y = core.spmm(*args, plan=plan, packed=packed, residual=R)
+        Y0 = core.spmm(*args, plan=plan, packed=packed)
+        torch.cuda.synchronize()
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    vq = G.values_condensed.double().cpu().numpy()
+    Yr, Ya = oracle.bcsr_spmm(G.window_offset.cpu().numpy(), G.original_col_indices.cpu().numpy(), vq, 16, 16,
+                              X.double().cpu().numpy())
+    Rn = R.double().cpu().numpy()
+    Yr[:r_rows] += Rn
+    Ya[:r_rows] += np.abs(Rn)
+    err = np.abs(Y.double().cpu().numpy() - Yr)
+    assert (err <= RTOL[xdt] * Ya).all()
+    assert torch.equal(Y[r_rows:], Y0[r_rows:])
+
+
+def test_spmm_residual_in_place(cuda_device):
+    """R may be the output itself: Y = A X + Y."""
+    print("case residual in place", flush=True)
+    g = synth.chung_lu(2000, 30000, 2.1, seed=5)
+    G = _bcsr(g, 16, cuda_device, vdt=torch.float16)
+    X = synth.features(g.num_nodes, 64, seed=6, device=cuda_device).half()
+    args = (G.window_offset, G.original_col_indices, G.values_condensed, X, 16)
+    Y = synth.features(16 * G.num_windows, 64, seed=7, device=cuda_device).half()
+    R = Y.clone()
+    ref = core.spmm(*args, residual=R)
+    core.spmm(*args, out=Y, residual=Y)
+    torch.cuda.synchronize()
+    assert torch.equal(Y.view(torch.int16), ref.view(torch.int16))
