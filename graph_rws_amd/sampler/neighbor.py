@@ -23,7 +23,7 @@ Per hop, on the device (csrc/sample.hip, csrc/bcsr_build.hip):
 from __future__ import annotations
 
 import time
-from typing import List, Optional, Sequence
+from typing import List, Sequence
 
 import torch
 

@@ -10,7 +10,6 @@ deterministic for a given (seed, device type).
 """
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass
 from typing import Optional
 
