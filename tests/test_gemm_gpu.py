@@ -78,7 +78,6 @@ def test_graphconv_autocast_backward_uses_split_k(cuda_device):
         loss = (out.float() * R).sum()
     loss.backward()
     import scipy.sparse as sps
-    import numpy as np
     vals16 = torch.from_numpy(g.values.numpy()).half().double().numpy()
     A = torch.from_numpy(sps.csr_matrix((vals16, g.col_idx.numpy(), g.row_ptr.numpy()),
                                         shape=(g.num_nodes, g.num_nodes)).toarray())
