@@ -33,6 +33,8 @@ MEASURED_TRAFFIC = {
     # (config, N, x dtype, tile cols, A format): (bytes per SpMM, profile file)
     ("c3", 608, "f16", 16, "dense tiles"): (38.127e9, "profiles/spmm_buf_c3_n608_f16.md"),
     ("c3", 608, "f16", 16, "packed tiles"): (34.487e9, "profiles/spmm_buf_c3_n608_f16.md"),
+    # SpMM kernel (373.1 MB read, 54.7 MB written) plus the split-window fixup (14.6 MB)
+    ("c2", 128, "f16", 16, "packed tiles"): (442.4e6, "profiles/spmm_buf_c2_n128_f16.md"),
 }
 
 
@@ -536,6 +538,11 @@ def bench_spmm_c2(dev, reps: int = 20, cpu: bool = False) -> dict:
                        "alg_gbps": round(B["total"] / ms / 1e6, 1),
                        "pct_hbm_peak": round(100.0 * B["total"] / ms / 1e6 / HBM_PEAK_GBS, 2),
                        "alg_bytes": B["total"]}
+            tk = ("c2", 128, dname, 16, "packed tiles")
+            if name == "fwd" and tk in MEASURED_TRAFFIC:
+                r[name]["traffic"] = MEASURED_TRAFFIC[tk][0]
+                r[name]["traffic_gbs"] = round(MEASURED_TRAFFIC[tk][0] / ms / 1e6, 1)
+                r[name]["traffic_source"] = MEASURED_TRAFFIC[tk][1]
         res[dname] = r
         del G, X, Gr, AT
     torch.cuda.empty_cache()
