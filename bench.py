@@ -35,6 +35,7 @@ MEASURED_TRAFFIC = {
     ("c3", 608, "f16", 16, "packed tiles"): (34.487e9, "profiles/spmm_buf_c3_n608_f16.md"),
     # SpMM kernel (373.1 MB read, 54.7 MB written) plus the split-window fixup (14.6 MB)
     ("c2", 128, "f16", 16, "packed tiles"): (442.4e6, "profiles/spmm_buf_c2_n128_f16.md"),
+    ("c4", 112, "bf16", 16, "packed tiles"): (26.571e9, "profiles/spmm_buf_c4_n112_bf16.md"),
 }
 
 
