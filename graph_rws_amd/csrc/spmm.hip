@@ -142,9 +142,9 @@ __device__ __forceinline__ float load_res(const void* r, int64_t idx) {
 }
 
 // Writes a work-group's 16 x NC result: to Y (converted, after adding the
-// residual when there is one), or as an fp32 partial for a split window.  With WPB > 1 the waves' accumulators are
-// first added in LDS in wave order (deterministic); `stage_all` must hold
-// 16 * NC floats.
+// residual when there is one), or as an fp32 partial for a split window.
+// With WPB > 1 the waves' accumulators are first added in LDS in wave order
+// (deterministic); `stage_all` must hold 16 * NC floats.
 template <int XT, int NBLK, int WPB, typename S>
 __device__ __forceinline__ void spmm_epilogue(const SpmmArgs& a, const float4_t* acc, S* stage_all, int wave,
                                               int lane, int64_t w, int slot, int chunk, int64_t n0) {
