@@ -301,6 +301,16 @@ class BCSRGraph:
         copies[key] = (weakref.ref(x, _drop), x._version, xa)
         return xa
 
+    def padded_input(self, x: torch.Tensor) -> Optional[torch.Tensor]:
+        """The line-aligned copy this graph gathers x through, with its
+        zero padding columns ([rows, pitch], pitch a multiple of 128 bytes),
+        or None when x is gathered as it is.  Products over the padded
+        width equal those over x plus exact zeros."""
+        xa = self._gather_input(x)
+        if xa is x or xa.stride(0) <= xa.shape[1]:
+            return None
+        return xa.as_strided((xa.shape[0], xa.stride(0)), (xa.stride(0), 1))
+
     def spmm(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
              residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Y[16W, N] = A x on the device (columns >= x.shape[0] contribute

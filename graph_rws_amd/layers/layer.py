@@ -28,6 +28,14 @@ from ..helper.timer import record_spmm_time
 # False restores the separate beta=1 GEMM.
 FUSED_SELF = True
 
+# Aggregate-first layers whose input the graph gathers through a zero-padded,
+# line-aligned copy (112 features on a 128-element pitch) run both GEMMs on
+# that padded width: the padding columns and zero weight rows add exact zeros,
+# and the library GEMM is faster at K=128 than at K=112 (c4: 0.45 against
+# 0.62 ms, and 0.58 against 0.71 ms for the accumulating one).  False keeps
+# the unpadded width.
+PAD_AGGREGATE = True
+
 
 def _spmm_timed(graph, x: torch.Tensor, residual: torch.Tensor = None):
     """graph.spmm with the reference's (output, ms) convention (bind.cpp:124-130)."""
@@ -163,7 +171,21 @@ class _GraphConvFunction(Function):
         # the beta=1 GEMMs accumulate in place into a tensor this function
         # made (no copy of it into a new output); in-place ops are not
         # autocast, so the weights take the operands' dtype explicitly
-        if ctx.agg_first:
+        ctx.kpad = 0
+        padded = getattr(graph, "padded_input", None)
+        xp = (padded(xh) if (PAD_AGGREGATE and padded is not None and ctx.agg_first and x_tgt is None
+                             and xh.is_cuda) else None)
+        if xp is not None:
+            # (A Xp) Wn_p + Xp[:T] Ws_p over the zero-padded width
+            k, kp = xh.shape[1], xp.shape[1]
+            y, ms = _spmm_timed(graph, xp)
+            yt = rows_T(y)
+            xtp = xp[:T]
+            out = torch.matmul(xtp, F.pad(w_s, (0, 0, 0, kp - k)).to(xtp.dtype))
+            out.addmm_(yt, F.pad(w_n, (0, 0, 0, kp - k)).to(out.dtype))
+            ctx.save_for_backward(yt, xtp, w_n, w_s)
+            ctx.kpad = k
+        elif ctx.agg_first:
             y, ms = _spmm_timed(graph, xh)
             yt = rows_T(y)
             out = torch.matmul(xt, w_s)
@@ -199,10 +221,14 @@ class _GraphConvFunction(Function):
         dx = dxt = dwn = dws = None
         if need_ws:
             dws = _weight_grad(xt, g)
+            if ctx.kpad:
+                dws = dws[: ctx.kpad]  # the padded width's extra rows are zero
         if ctx.agg_first:
             # out = (A X)[:T] W_n + X_tgt W_s
             if need_wn:
                 dwn = _weight_grad(saved, g)
+                if ctx.kpad:
+                    dwn = dwn[: ctx.kpad]
             if need_x:
                 dx = graph.spmm_transpose(torch.matmul(g, w_n.t()).contiguous(), ctx.num_input_nodes)
         else:

@@ -204,3 +204,42 @@ def test_fused_self_path_matches_separate_add(cuda_device, dt, fout):
     assert float((outs[0] - outs[1]).abs().max()) <= tol * scale
     for a, b in zip(grads[0], grads[1]):
         assert float((a - b).abs().max()) <= tol * float(b.abs().max()) + 1e-6
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("xgrad", [False, True])
+def test_aggregate_first_on_padded_width(cuda_device, dt, xgrad):
+    """An aggregate-first layer (112 -> 256) whose input the graph gathers
+    through a zero-padded 128-element copy runs its GEMMs over the padded
+    width: same output (within the rounding of the GEMMs) and the same
+    gradients as over the 112 columns, weight gradients of the weights'
+    own shape."""
+    from graph_rws_amd.layers import layer as layer_mod
+    print(f"case padded-aggregate dt={dt} xgrad={xgrad}", flush=True)
+    g = synth.chung_lu(3000, 200000, 2.1, seed=21)
+    G = BCSRGraph.from_csr(g.row_ptr.to(cuda_device), g.col_idx.to(cuda_device), g.values.to(cuda_device),
+                           g.num_nodes, g.num_nodes, tile_cols=16, device=cuda_device, values_dtype=dt)
+    assert G.num_tiles * 16 >= 8 * g.num_nodes                  # the graph gathers through a copy
+    torch.manual_seed(5)
+    conv = BCSRGraphConv(112, 256).to(cuda_device)
+    X0 = synth.features(g.num_nodes, 112, seed=4, device=cuda_device).to(dt)
+    assert G.padded_input(X0) is not None and G.padded_input(X0).shape[1] == 128
+    outs, grads = [], []
+    for pad in (True, False):
+        layer_mod.PAD_AGGREGATE = pad
+        try:
+            X = X0.clone().requires_grad_(xgrad)
+            conv.zero_grad()
+            with torch.autocast("cuda", dtype=dt):
+                y = conv(G, X, features_target=X)
+            y.float().square().sum().backward()
+            outs.append(y.detach().float())
+            grads.append([conv.weight_neigh.grad.clone(), conv.weight_self.grad.clone()]
+                         + ([X.grad.clone()] if xgrad else []))
+        finally:
+            layer_mod.PAD_AGGREGATE = True
+    torch.cuda.synchronize()
+    assert float((outs[0] - outs[1]).abs().max()) <= 2e-2 * float(outs[1].abs().max())
+    for a, b in zip(grads[0], grads[1]):
+        assert a.shape == b.shape
+        assert float((a - b).abs().max()) <= 2e-2 * float(b.abs().max()) + 1e-6
