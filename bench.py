@@ -14,6 +14,7 @@ fp32 BCSR SpMM on host cores over a bounded sample of the same windows).
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import platform
@@ -63,12 +64,23 @@ def build_graph(cfg: str, tc: int, vdt: torch.dtype, dev: torch.device):
     return g, G, t1 - t0, t2 - t1
 
 
-def alg_bytes(G, N: int, s_x: int, s_y: int) -> dict:
-    """B_alg = 8(W+1) + 4 T tc + s_a T 16 tc + s_x U N + s_y 16 W N: every
-    stored A array read once, each referenced X row read once per window that
-    references it, Y written once."""
+def alg_bytes(G, N: int, s_x: int, s_y: int, packed=None, plan=None) -> dict:
+    """Bytes one SpMM must move, two ways.
+
+    compulsory: every array the kernel reads, read once, in the format it
+    actually reads (packed tiles when the product uses them), every
+    referenced X row read once, Y written once.  This is the roofline's
+    numerator: a kernel cannot move less.
+
+    gather model: B = 8(W+1) + 4 T tc + s_a T 16 tc + s_x U N + s_y 16 W N,
+    each referenced X row counted once per window that references it (no
+    reuse across windows).  The caches serve those re-references, so this
+    count is modelled L2-side traffic, not a bound on DRAM bytes."""
     W, T, tc = G.num_windows, G.num_tiles, G.tile_cols
-    U = int(torch.count_nonzero(G.original_col_indices >= 0).item())
+    cols = G.original_col_indices
+    valid = cols[cols >= 0]
+    U = int(valid.numel())
+    rows_ref = int(torch.unique(valid[valid < G.num_cols]).numel()) if U else 0
     s_a = G.values_condensed.element_size()
     parts = {
         "win_off": 8 * (W + 1),
@@ -79,15 +91,46 @@ def alg_bytes(G, N: int, s_x: int, s_y: int) -> dict:
     }
     parts["total"] = sum(parts.values())
     parts["U"] = U
-    # compulsory lower bound: the same, with every X row read once
-    parts["compulsory"] = (parts["win_off"] + parts["cols"] + parts["vals"] + s_x * G.num_cols * N
-                           + parts["y"])
+    a_read = (48 * T + s_a * packed.num_values) if packed is not None else parts["vals"]
+    items = 16 * plan.num_items if plan is not None else 0
+    parts["compulsory"] = (parts["win_off"] + parts["cols"] + a_read + s_x * rows_ref * N + parts["y"]
+                           + items)
+    parts["compulsory_detail"] = {"a_values": a_read, "a_format": "packed" if packed is not None else "dense",
+                                  "x_rows_referenced": rows_ref, "x_once": s_x * rows_ref * N,
+                                  "plan_items": items}
     return parts
 
 
-def cpu_baseline(g, G, X: torch.Tensor, budget_s: float = 12.0) -> dict:
-    """oracle fp32 BCSR SpMM on host cores over the first windows of the
-    same graph, until ~budget_s of CPU work; GFLOP/s on the sample's nnz."""
+def copy_peak(dev, nbytes: int = 1 << 30, reps: int = 5) -> float:
+    """Read+write GB/s of a device-to-device copy of nbytes (torch's copy
+    kernel), median of reps after one warm-up, HIP events on the stream."""
+    a = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    s = torch.cuda.current_stream(dev)
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        b.copy_(a)
+        e1.record(s)
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    ts.sort()
+    del a, b
+    torch.cuda.empty_cache()
+    return 2 * nbytes / ts[len(ts) // 2] / 1e6
+
+
+def cpu_baseline(g, G, X: torch.Tensor, Y: torch.Tensor, rtol: float, budget_s: float = 12.0) -> dict:
+    """The CPU path beside the headline, and the check of the timed Y.
+
+    Timed: the oracle's fp32 BCSR SpMM (the reference kernel's arithmetic on
+    host cores) over the first windows until ~budget_s, and torch.sparse CSR
+    fp32 A @ X over the whole graph.  Untimed: every timed window of the
+    GPU's Y against the fp32 oracle, |Y - Y_cpu| <= (rtol + 2e-4) |A||X| (the
+    fp32 sum's own error is far below 2e-4 here), and a projection of every
+    row onto a seeded r in float64, |Y r - A (X r)| <= rtol |A| (|X| |r|)."""
     import numpy as np
     import oracle
     from graph_rws_amd.core.ops import host_threads
@@ -95,28 +138,70 @@ def cpu_baseline(g, G, X: torch.Tensor, budget_s: float = 12.0) -> dict:
     win = G.window_offset.cpu().numpy()
     cols = G.original_col_indices.cpu().numpy()
     vals = G.values_condensed.float().cpu().numpy()
+    vabs = np.abs(vals)
     Xh = X.float().cpu().numpy()
+    Xabs = np.abs(Xh)
+    Yd = Y.float().cpu().numpy()
     rp = g.row_ptr.cpu().numpy()
     W = G.num_windows
     N = Xh.shape[1]
     done, t_total, nnz = 0, 0.0, 0
+    worst = 0.0
     step = 64
     oracle.bcsr_spmm_f32_timed(win, cols, vals, 16, G.tile_cols, Xh, 0, min(W, 4))  # warm
     while done < W and t_total < budget_s:
         e = min(W, done + step)
         t0 = time.perf_counter()
-        oracle.bcsr_spmm_f32_timed(win, cols, vals, 16, G.tile_cols, Xh, done, e)
+        Yc = oracle.bcsr_spmm_f32_timed(win, cols, vals, 16, G.tile_cols, Xh, done, e)
         t_total += time.perf_counter() - t0
+        Ya = oracle.bcsr_spmm_f32_timed(win, cols, vabs, 16, G.tile_cols, Xabs, done, e)
+        err = np.abs(Yd[16 * done:16 * e] - Yc)
+        worst = max(worst, float(np.max(err / np.maximum((rtol + 2e-4) * Ya, 1e-30))))
         nnz += int(rp[min(e * 16, g.num_nodes)] - rp[min(done * 16, g.num_nodes)])
         done = e
         step = min(step * 2, 4096)
     gflops = 2.0 * nnz * N / t_total / 1e9
+    # projection of every row, float64
+    r = np.random.default_rng(17).standard_normal(N)
+    v = Xh.astype(np.float64) @ r
+    va = Xabs.astype(np.float64) @ np.abs(r)
+    z, za = oracle.bcsr_spmv(win, cols, vals, "f32", G.tile_cols, v, va, Xh.shape[0])
+    yr = Yd.astype(np.float64) @ r
+    proj = float(np.max(np.abs(yr - z) / np.maximum(rtol * za, 1e-300)))
+    parity = {"pass": bool(worst <= 1.0 and proj <= 1.0),
+              "elementwise": f"windows 0..{done} of {W} against the fp32 oracle, bound (rtol + 2e-4) |A||X|, "
+                             f"rtol {rtol}",
+              "elementwise_worst_err_over_bound": round(worst, 5),
+              "projection": f"all {16 * W} rows: Y r against A (X r) in float64, bound rtol |A| (|X| |r|)",
+              "projection_worst_err_over_bound": round(proj, 5)}
+    del vals, vabs, Xabs, Yd
+    # torch.sparse CSR fp32 over the whole graph (the CPU SpMM BASELINE.md names)
+    torch.set_num_threads(host_threads())
+    A = torch.sparse_csr_tensor(g.row_ptr.cpu(), g.col_idx.cpu().long(), g.values.cpu().float(),
+                                size=(g.num_nodes, g.num_nodes))
+    Xt = torch.from_numpy(Xh)
+    t0 = time.perf_counter()
+    A @ Xt
+    t_first = time.perf_counter() - t0
+    ts = [t_first]
+    if t_first < 10.0:
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            A @ Xt
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+    t_sp = ts[len(ts) // 2]
     return {"value": round(gflops, 3), "unit": "GFLOP/s", "cores": int(oracle.num_threads()),
             "kind": "port",
             "sample": f"windows 0..{done} of {W} ({nnz} nnz, {100.0 * done / W:.1f}% of the graph), "
                       f"fp32, {t_total:.1f} s; oracle/grws_oracle.c orc_bcsr_spmm_f32",
+            "torch_sparse_csr": {"value": round(2.0 * g.nnz * N / t_sp / 1e9, 3), "unit": "GFLOP/s",
+                                 "ms": round(1e3 * t_sp, 1), "threads": torch.get_num_threads(),
+                                 "sample": "whole graph, fp32 A @ X, "
+                                           + ("median of 3 after 1 warm-up" if len(ts) == 3 else "one run")},
             "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
-            "torch_threads": torch.get_num_threads()}
+            "torch_threads": torch.get_num_threads(), "parity": parity}
 
 
 def bench_sampling(dev, batches: int, warmup: int, cpu: bool) -> dict:
@@ -524,21 +609,35 @@ def bench_spmm_c2(dev, reps: int = 20, cpu: bool = False) -> dict:
         r = {}
         for name, M, inp in (("fwd", G, X), ("bwd", AT, Gr)):
             out = torch.empty((16 * M.num_windows, 128), dtype=dt, device=dev)
-            for _ in range(3):
+            for _ in range(3):  # builds the plan, then the packed tiles
                 M.spmm(inp, out=out)
+            torch.cuda.synchronize(dev)
+            # every per-graph cache must exist before timing: a build inside
+            # the timed loop would be a host sync and a pass over the graph
+            plan = M.spmm_plan(128)
+            packed = M.packed_tiles()
+            assert packed is not None, f"c2 {dname} {name}: packed tiles not built in the warm-up"
             s = torch.cuda.current_stream(dev)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(s)
-            for _ in range(reps):
+            gc.collect()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(reps)]
+            for e0, e1 in ev:
+                e0.record(s)
                 M.spmm(inp, out=out)
-            e1.record(s)
-            e1.synchronize()
-            ms = e0.elapsed_time(e1) / reps
-            B = alg_bytes(M, 128, 2, 2)
-            r[name] = {"ms": round(ms, 4), "gflops": round(2.0 * g.nnz * 128 / ms / 1e6, 1),
-                       "alg_gbps": round(B["total"] / ms / 1e6, 1),
-                       "pct_hbm_peak": round(100.0 * B["total"] / ms / 1e6 / HBM_PEAK_GBS, 2),
-                       "alg_bytes": B["total"]}
+                e1.record(s)
+            torch.cuda.synchronize(dev)
+            per = sorted(e0.elapsed_time(e1) for e0, e1 in ev)
+            ms = per[len(per) // 2]
+            B = alg_bytes(M, 128, 2, 2, packed=packed, plan=plan)
+            r[name] = {"ms": round(ms, 4), "ms_min": round(per[0], 4), "ms_max": round(per[-1], 4),
+                       "reps": reps, "gflops": round(2.0 * g.nnz * 128 / ms / 1e6, 1),
+                       "compulsory_bytes": B["compulsory"],
+                       "compulsory_gbps": round(B["compulsory"] / ms / 1e6, 1),
+                       "frac_hbm_peak": round(B["compulsory"] / ms / 1e6 / HBM_PEAK_GBS, 4),
+                       "gather_model_bytes": B["total"],
+                       "gather_model_gbps": round(B["total"] / ms / 1e6, 1),
+                       "plan": {"items": plan.num_items if plan is not None else M.num_windows,
+                                "split_windows": plan.num_split if plan is not None else 0}}
             tk = ("c2", 128, dname, 16, "packed tiles")
             if name == "fwd" and tk in MEASURED_TRAFFIC:
                 r[name]["traffic"] = MEASURED_TRAFFIC[tk][0]
@@ -599,6 +698,7 @@ def main():
         return
     from graph_rws_amd.core import _lib
     _lib.load()
+    copy_gbs = copy_peak(dev)
 
     cfg = args.config
     spec = {"c2": (128, 128, "f16"), "c3": (602, 608, "f16"), "c4": (100, 112, "bf16")}[cfg]
@@ -629,6 +729,7 @@ def main():
         G.spmm(X, out=Y)
     torch.cuda.synchronize(dev)
     a_format = "packed tiles" if G.packed_tiles() is not None else "dense tiles"
+    gc.collect()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.steps)]
     torch.cuda.synchronize(dev)
@@ -646,10 +747,13 @@ def main():
     nnz = g.nnz
     flops = 2.0 * nnz * N
     gflops = flops / (ms_step / 1e3) / 1e9
-    B = alg_bytes(G, N, X.element_size(), Y.element_size())
-    kernel_gbs = B["total"] / (ms_avg / 1e3) / 1e9
+    packed = G.packed_tiles()
+    B = alg_bytes(G, N, X.element_size(), Y.element_size(), packed=packed, plan=plan)
+    comp_gbs = B["compulsory"] / (ms_avg / 1e3) / 1e9
+    gather_gbs = B["total"] / (ms_avg / 1e3) / 1e9
     issued = 2.0 * G.num_tiles * 16 * G.tile_cols * N
     tkey = (cfg, N, dname, G.tile_cols, a_format)
+    traffic = MEASURED_TRAFFIC.get(tkey, (None, None))
 
     out = {
         "metric": "BCSR SpMM GFLOP/s + HBM GB/s (% peak); GCN epoch ms; sampled edges/s",
@@ -674,22 +778,31 @@ def main():
             "plan": {"items": plan.num_items, "split_windows": plan.num_split,
                      "slabs_per_item": plan.slabs_per_item},
         },
-        "hbm_gbps_effective": round(kernel_gbs, 1),
-        "pct_hbm_peak": round(100.0 * kernel_gbs / HBM_PEAK_GBS, 2),
         "alg_bytes": B,
         "roofline": {
             "bound": "hbm",
             # 16-bit X runs the buffer-load kernel, fp32 X the element-masked one
             "kernel": "spmm_buf_kernel" if dname in ("f16", "bf16") else "spmm_fwd_kernel",
-            "achieved": round(kernel_gbs, 1),
+            # compulsory bytes (A in the format read, X and Y once) per product
+            # over the product's kernel time (HIP events on the launch stream)
+            "achieved": round(comp_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
-            "traffic": MEASURED_TRAFFIC.get(tkey, (None, None))[0],
-            "traffic_source": MEASURED_TRAFFIC.get(tkey, (None, None))[1],
-            "traffic_gbs": (round(MEASURED_TRAFFIC[tkey][0] / (ms_avg / 1e3) / 1e9, 1)
-                            if tkey in MEASURED_TRAFFIC else None),
+            "frac": round(comp_gbs / HBM_PEAK_GBS, 4),
+            "bytes": B["compulsory"],
+            "peak_measured_copy": round(copy_gbs, 1),
+            "frac_of_measured_copy": round(comp_gbs / copy_gbs, 4),
+            "traffic": traffic[0],
+            "traffic_source": traffic[1],
+            "traffic_over_compulsory": round(traffic[0] / B["compulsory"], 2) if traffic[0] else None,
+            "traffic_gbs": round(traffic[0] / (ms_avg / 1e3) / 1e9, 1) if traffic[0] else None,
+            "gather_model": {"bytes": B["total"], "gbs": round(gather_gbs, 1),
+                             "note": "modelled L2-side bytes: each gathered X row counted once per "
+                                     "window that references it; the caches serve re-references, so "
+                                     "this rate can exceed the DRAM peak"},
             "kernel_ms_avg": round(ms_avg, 4),
+            "kernel_ms_min": round(min(ms), 4),
+            "kernel_ms_max": round(max(ms), 4),
             "mfma_issued_tflops": round(issued / (ms_avg / 1e3) / 1e12, 2),
             "mfma_frac": round(issued / (ms_avg / 1e3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
         },
@@ -697,7 +810,11 @@ def main():
                     "pack_tiles": round(t_pack, 4)},
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(g, G, X)
+        cb = cpu_baseline(g, G, X, Y, 1e-2 if dname != "f32" else 1e-5)
+        out["parity"] = cb.pop("parity")
+        out["cpu_baseline"] = cb
+    else:
+        out["parity"] = {"pass": None, "note": "not checked (--no-cpu-baseline)"}
     if not args.no_sampling:
         del G, X, Y, g, plan
         torch.cuda.empty_cache()

@@ -441,7 +441,8 @@ def reindex_bcsr(col_indices: torch.Tensor, values_condensed: torch.Tensor,
                  tile_cols: int = 8) -> torch.Tensor:
     """Drop-in for core_lib.reindex_bcsr (bind.cpp:153-159): returns the
     local column ids (new int32 tensor) and prunes `values_condensed` in
-    place where a column's window is not among `active_windows` (sorted)."""
+    place where a column's window is not among `active_windows` (sorted);
+    its version counter is bumped as by any in-place op."""
     if not (col_indices.is_cuda and values_condensed.is_cuda and active_windows.is_cuda):
         raise RuntimeError("reindex_bcsr: all tensors must be CUDA tensors")
     if col_indices.dtype != torch.int32 or active_windows.dtype != torch.int32:
@@ -456,6 +457,9 @@ def reindex_bcsr(col_indices: torch.Tensor, values_condensed: torch.Tensor,
     L.call("grws_reindex_prune", L.ptr(col_indices), n, L.ptr(values_condensed),
            L.dtype_code(values_condensed.dtype), L.ptr(active_windows), active_windows.numel(),
            int(tile_rows), int(tile_cols), L.ptr(out), L.stream_of(col_indices.device))
+    # the prune wrote through a raw pointer: bump the version so caches keyed
+    # on it (packed tiles, the transpose) see the change
+    torch.autograd.graph.increment_version(values_condensed)
     return out
 
 

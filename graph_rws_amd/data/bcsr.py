@@ -281,11 +281,19 @@ class BCSRGraph:
         19% slower (c4, 112 columns).  Each input's copy is kept while that
         input is alive and unmodified, and dropped when it dies: the layer-0
         features of full-graph training are copied once, although the same
-        graph multiplies other (short-lived) inputs in between."""
+        graph multiplies other (short-lived) inputs in between.
+
+        While the current stream is being captured the cache is bypassed:
+        the copy is made afresh, so its kernel is recorded in the graph and
+        every replay re-reads x (a replay after ``x.copy_(new)`` multiplies
+        the new values, not the copy made before the capture)."""
         esz = x.element_size()
         if (x.dim() != 2 or x.stride(1) != 1 or (x.stride(0) * esz) % 128 == 0
                 or x.shape[1] * esz < 64 or self.num_tiles * self.tile_cols < 8 * x.shape[0]):
             return x
+        if x.is_cuda and torch.cuda.is_current_stream_capturing():
+            from .layout import aligned_rows
+            return aligned_rows(x.detach())
         copies = self._cache.setdefault("aligned_x", {})
         key = id(x)
         ent = copies.get(key)

@@ -13,14 +13,21 @@ Conditions, checked or established at construction:
   built with ``capturable=True`` (torch's Adam / AdamW);
 * the warm-up steps (on a side stream, default priority) build everything
   the graph keeps between calls: SpMM plans, packed tiles, the transpose, the
-  masked layer-0 columns, the features' line-aligned copy.  The captured
-  step then issues no host sync and allocates only from the graph's pool;
+  masked layer-0 columns.  The captured step then issues no host sync and
+  allocates only from the graph's pool.  The features' line-aligned copy
+  (made when their row pitch straddles cache lines) is not taken from the
+  cache under capture: its copy kernel is recorded, so every replay reads
+  the features as they are then;
 * dropout draws its seed on the device while the stream is captured, so each
   replay trains with a new mask.
 
 A replay reads the tensors given at construction: update features, labels
 or the training rows in place (``copy_``) to train on new values; new
-tensors, new shapes or a modified graph need a new capture.  Parameters and
+tensors, new shapes or a modified graph need a new capture.  Training rows
+updated in place must stay strictly ascending: the fused loss that the
+capture recorded was chosen for distinct rows, and it writes (does not add)
+each row's gradient, so a repeated row would get the gradient of one
+occurrence only.  Parameters and
 optimizer state are updated in place by every replay, as by the eager step.
 """
 from __future__ import annotations
@@ -51,6 +58,7 @@ class GraphedFullStep:
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self.loss, self.acc = self._step()
+        self._idx_version = train_idx._version
 
     def _step(self):
         model, graphs, x, y, idx, opt, dev = self._args
@@ -61,6 +69,15 @@ class GraphedFullStep:
 
     def __call__(self):
         """One training step; returns (loss, accuracy) as device tensors that
-        the next replay overwrites."""
+        the next replay overwrites.  Training rows changed in place since the
+        last call are checked first (one device reduction and one sync per
+        change): they must still be strictly ascending."""
+        idx = self._args[4]
+        if idx._version != self._idx_version:
+            from ..layers.fused import rows_distinct
+            if not rows_distinct(idx):
+                raise ValueError("GraphedFullStep: the training rows were updated in place to values that are "
+                                 "not strictly ascending; the captured loss needs distinct rows (capture anew)")
+            self._idx_version = idx._version
         self.graph.replay()
         return self.loss, self.acc

@@ -17,6 +17,11 @@ Pinning (how each function is checked against something other than itself):
                           library routine) on the CSR the BCSR came from, and
                           closed forms (identity, linearity).
   * bcsr_spmm_t        -- against scipy.sparse (A^T) @ G.
+  * bcsr_spmm_windows, bcsr_spmv, bcsr_spmv_t, bcsr_spmm_t_rows
+                       -- the same products on the stored 16-bit types, for
+                          full-size checks: against scipy.sparse on the CSR
+                          the BCSR came from, with values and features
+                          quantised by numpy/torch (tests/test_oracle.py).
   * reindex_prune      -- hand-built cases with known answers (C truncation of
                           negative columns included).
   * philox4x32_10      -- against vectors produced by ATen's independent
@@ -80,6 +85,25 @@ def lib():
         L.orc_bcsr_spmm_t_f64.argtypes = [ctypes.c_int64, _i64p, _i32p, _f64p, ctypes.c_int64,
                                           ctypes.c_int64, _f64p, ctypes.c_int64, ctypes.c_int64,
                                           ctypes.c_int64, _f64p, _f64p]
+        L.orc_bcsr_spmm_windows_f64.restype = None
+        L.orc_bcsr_spmm_windows_f64.argtypes = [ctypes.c_int64, _i64p, _i64p, _i32p, ctypes.c_void_p,
+                                                ctypes.c_int32, ctypes.c_int64, ctypes.c_int64,
+                                                ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
+                                                ctypes.c_int64, ctypes.c_int64, _f64p, _f64p]
+        L.orc_bcsr_spmv_f64.restype = None
+        L.orc_bcsr_spmv_f64.argtypes = [ctypes.c_int64, _i64p, _i32p, ctypes.c_void_p, ctypes.c_int32,
+                                        ctypes.c_int64, ctypes.c_int64, _f64p, _f64p, ctypes.c_int64,
+                                        _f64p, _f64p]
+        L.orc_bcsr_spmv_t_f64.restype = None
+        L.orc_bcsr_spmv_t_f64.argtypes = [ctypes.c_int64, _i64p, _i32p, ctypes.c_void_p, ctypes.c_int32,
+                                          ctypes.c_int64, ctypes.c_int64, _f64p, _f64p, ctypes.c_int64,
+                                          _f64p, _f64p]
+        L.orc_bcsr_spmm_t_rows_f64.restype = None
+        L.orc_bcsr_spmm_t_rows_f64.argtypes = [ctypes.c_int64, _i64p, _i32p, ctypes.c_void_p,
+                                               ctypes.c_int32, ctypes.c_int64, ctypes.c_int64,
+                                               ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
+                                               ctypes.c_int64, ctypes.c_int64, _i32p, ctypes.c_int64,
+                                               _f64p, _f64p]
         L.orc_reindex_prune.restype = None
         L.orc_reindex_prune.argtypes = [_i32p, ctypes.c_int64, _f32p, _i32p, ctypes.c_int64,
                                         ctypes.c_int32, ctypes.c_int32, _i32p]
@@ -227,6 +251,93 @@ def bcsr_spmm_f32_timed(win, cols, vals_f32, tile_rows: int, tile_cols: int, X_f
                             _p(vals_f32, _f32p), tile_rows, tile_cols, _p(X_f32, _f32p),
                             X_f32.shape[0], X_f32.shape[1], N, _p(Y, _f32p))
     return Y
+
+
+# ----------------------------------------------------------------------------
+# Full-size checks on the stored element types (no float64 copy of A)
+# ----------------------------------------------------------------------------
+_DT = {"f32": (0, np.float32), "f16": (1, np.float16), "bf16": (2, np.uint16)}
+
+
+def _typed(a, dt: str) -> np.ndarray:
+    """a as a contiguous array of the element type dt ("f32", "f16", or
+    "bf16" given as its raw uint16 bits)."""
+    code, npt = _DT[dt]
+    a = np.asarray(a)
+    if dt == "bf16" and a.dtype == np.int16:
+        a = a.view(np.uint16)
+    if a.dtype != npt:
+        raise TypeError(f"expected {npt.__name__} data for {dt}, got {a.dtype}")
+    return np.ascontiguousarray(a)
+
+
+def bcsr_spmm_windows(win, cols, vals, vdt: str, tile_cols: int, X, xdt: str, sel):
+    """Rows of Y = A X and |A||X| (float64) for the windows in sel: output
+    rows 16k..16k+15 belong to window sel[k] (spmm_tc.cuh:113-193 semantics,
+    as bcsr_spmm).  vals and X keep their stored element type."""
+    win = _c(win, np.int64); cols = _c(cols, np.int32); sel = _c(sel, np.int64)
+    vals = _typed(vals, vdt)
+    X = _typed(X, xdt)
+    if X.ndim != 2:
+        raise ValueError("X must be 2-D")
+    N = X.shape[1]
+    Y = np.empty((sel.size * 16, N), np.float64)
+    Ya = np.empty_like(Y)
+    lib().orc_bcsr_spmm_windows_f64(sel.size, _p(sel, _i64p), _p(win, _i64p), _p(cols, _i32p),
+                                    vals.ctypes.data, _DT[vdt][0], 16, tile_cols, X.ctypes.data,
+                                    _DT[xdt][0], X.shape[0], N, N, _p(Y, _f64p), _p(Ya, _f64p))
+    return Y, Ya
+
+
+def bcsr_spmv(win, cols, vals, vdt: str, tile_cols: int, v, v_abs, x_rows: int):
+    """z = A v and |A| v_abs over all 16W rows (float64)."""
+    win = _c(win, np.int64); cols = _c(cols, np.int32)
+    vals = _typed(vals, vdt)
+    v = _c(v, np.float64); v_abs = _c(v_abs, np.float64)
+    W = len(win) - 1
+    z = np.empty(W * 16, np.float64)
+    za = np.empty_like(z)
+    lib().orc_bcsr_spmv_f64(W, _p(win, _i64p), _p(cols, _i32p), vals.ctypes.data, _DT[vdt][0], 16,
+                            tile_cols, _p(v, _f64p), _p(v_abs, _f64p), min(x_rows, v.size),
+                            _p(z, _f64p), _p(za, _f64p))
+    return z, za
+
+
+def bcsr_spmv_t(win, cols, vals, vdt: str, tile_cols: int, u, u_abs, num_cols: int):
+    """z = A^T u and |A|^T u_abs over num_cols outputs (float64); u has 16W
+    entries."""
+    win = _c(win, np.int64); cols = _c(cols, np.int32)
+    vals = _typed(vals, vdt)
+    u = _c(u, np.float64); u_abs = _c(u_abs, np.float64)
+    W = len(win) - 1
+    if u.size < 16 * W:
+        raise ValueError("u must have 16W entries")
+    z = np.empty(num_cols, np.float64)
+    za = np.empty_like(z)
+    lib().orc_bcsr_spmv_t_f64(W, _p(win, _i64p), _p(cols, _i32p), vals.ctypes.data, _DT[vdt][0], 16,
+                              tile_cols, _p(u, _f64p), _p(u_abs, _f64p), num_cols, _p(z, _f64p),
+                              _p(za, _f64p))
+    return z, za
+
+
+def bcsr_spmm_t_rows(win, cols, vals, vdt: str, tile_cols: int, G, gdt: str, num_cols: int, rows):
+    """Rows `rows` (distinct column ids of A) of A^T G and |A|^T |G| in
+    float64; G is [16W, D] of type gdt (spmm_tc.cuh:238-269 semantics)."""
+    win = _c(win, np.int64); cols = _c(cols, np.int32); rows = _c(rows, np.int64)
+    vals = _typed(vals, vdt)
+    G = _typed(G, gdt)
+    W = len(win) - 1
+    if G.ndim != 2 or G.shape[0] < 16 * W:
+        raise ValueError("G must be [>=16W, D]")
+    D = G.shape[1]
+    m = np.full(num_cols, -1, np.int32)
+    m[rows] = np.arange(rows.size, dtype=np.int32)
+    out = np.empty((rows.size, D), np.float64)
+    outa = np.empty_like(out)
+    lib().orc_bcsr_spmm_t_rows_f64(W, _p(win, _i64p), _p(cols, _i32p), vals.ctypes.data, _DT[vdt][0], 16,
+                                   tile_cols, G.ctypes.data, _DT[gdt][0], D, D, num_cols, _p(m, _i32p),
+                                   rows.size, _p(out, _f64p), _p(outa, _f64p))
+    return out, outa
 
 
 def num_threads() -> int:

@@ -180,6 +180,203 @@ ORC_API void orc_bcsr_spmm_f32(int64_t w_begin, int64_t w_end, const int64_t* wi
 }
 
 /* ------------------------------------------------------------------------ */
+/* Full-size checks: the same products on the stored element types, over a  */
+/* subset of windows or projected onto one vector, so graphs whose values    */
+/* would not fit in memory as float64 (c3: 1.2G slots) can be checked.       */
+/* Element types: 0 = float32, 1 = float16, 2 = bfloat16 (raw bits).         */
+/* ------------------------------------------------------------------------ */
+
+/* IEEE binary16 bits -> double, exactly (normals, subnormals, inf, NaN). */
+static double half_bits_to_double(uint16_t h) {
+    const int s = h >> 15, e = (h >> 10) & 31, m = h & 1023;
+    double v;
+    if (e == 0) v = ldexp((double)m, -24);
+    else if (e == 31) v = m ? NAN : INFINITY;
+    else v = ldexp((double)(m | 1024), e - 25);
+    return s ? -v : v;
+}
+
+/* bfloat16 bits -> double, exactly (the high half of a float32). */
+static double bf16_bits_to_double(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return (double)f;
+}
+
+/* Table of the 65536 values of a 16-bit type (dt 1 or 2), or NULL for f32. */
+static double* elem_table(int32_t dt) {
+    if (dt != 1 && dt != 2) return NULL;
+    double* t = (double*)malloc(65536 * sizeof(double));
+    for (uint32_t i = 0; i < 65536; ++i)
+        t[i] = dt == 1 ? half_bits_to_double((uint16_t)i) : bf16_bits_to_double((uint16_t)i);
+    return t;
+}
+
+static inline double elem_at(const void* p, const double* tab, int64_t i) {
+    if (tab) return tab[((const uint16_t*)p)[i]];
+    return (double)((const float*)p)[i];
+}
+
+/* Rows of Y = A X (and |A||X|) for the windows sel[0..nsel), in float64 on
+ * the stored values and features: output row 16k + r is row r of window
+ * sel[k] (spmm_tc.cuh:113-193 semantics as orc_bcsr_spmm_f64: -1 and
+ * columns outside [0, x_rows) contribute nothing). */
+ORC_API void orc_bcsr_spmm_windows_f64(int64_t nsel, const int64_t* sel, const int64_t* win_off,
+                                       const int32_t* cols, const void* vals, int32_t vdt,
+                                       int64_t tile_rows, int64_t tile_cols, const void* X,
+                                       int32_t xdt, int64_t x_rows, int64_t ldx, int64_t N,
+                                       double* Y, double* AX_abs) {
+    double* vt = elem_table(vdt);
+    double* xt = elem_table(xdt);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t k = 0; k < nsel; ++k) {
+        const int64_t w = sel[k];
+        double* yw = Y + k * tile_rows * N;
+        double* aw = AX_abs + k * tile_rows * N;
+        for (int64_t i = 0; i < tile_rows * N; ++i) { yw[i] = 0.0; aw[i] = 0.0; }
+        for (int64_t t = win_off[w]; t < win_off[w + 1]; ++t) {
+            for (int64_t c = 0; c < tile_cols; ++c) {
+                const int32_t col = cols[t * tile_cols + c];
+                if (col < 0 || col >= x_rows) continue;
+                for (int64_t r = 0; r < tile_rows; ++r) {
+                    const double a = elem_at(vals, vt, (t * tile_rows + r) * tile_cols + c);
+                    if (a == 0.0) continue;
+                    double* y = yw + r * N;
+                    double* ya = aw + r * N;
+                    const int64_t xo = (int64_t)col * ldx;
+                    for (int64_t n = 0; n < N; ++n) {
+                        const double x = elem_at(X, xt, xo + n);
+                        y[n] += a * x;
+                        ya[n] += fabs(a) * fabs(x);
+                    }
+                }
+            }
+        }
+    }
+    free(vt);
+    free(xt);
+}
+
+/* z = A v and z_abs = |A| v_abs over all 16W rows, in float64 on the stored
+ * values (v = X r projects the product onto r: (A X) r = A (X r)). */
+ORC_API void orc_bcsr_spmv_f64(int64_t W, const int64_t* win_off, const int32_t* cols,
+                               const void* vals, int32_t vdt, int64_t tile_rows, int64_t tile_cols,
+                               const double* v, const double* v_abs, int64_t x_rows, double* z,
+                               double* z_abs) {
+    double* vt = elem_table(vdt);
+#pragma omp parallel for schedule(dynamic, 64)
+    for (int64_t w = 0; w < W; ++w) {
+        double acc[64], acca[64];
+        for (int64_t r = 0; r < tile_rows; ++r) { acc[r] = 0.0; acca[r] = 0.0; }
+        for (int64_t t = win_off[w]; t < win_off[w + 1]; ++t) {
+            for (int64_t c = 0; c < tile_cols; ++c) {
+                const int32_t col = cols[t * tile_cols + c];
+                if (col < 0 || col >= x_rows) continue;
+                for (int64_t r = 0; r < tile_rows; ++r) {
+                    const double a = elem_at(vals, vt, (t * tile_rows + r) * tile_cols + c);
+                    acc[r] += a * v[col];
+                    acca[r] += fabs(a) * v_abs[col];
+                }
+            }
+        }
+        for (int64_t r = 0; r < tile_rows; ++r) {
+            z[w * tile_rows + r] = acc[r];
+            z_abs[w * tile_rows + r] = acca[r];
+        }
+    }
+    free(vt);
+}
+
+/* z = A^T u and z_abs = |A|^T u_abs over num_cols outputs (u has 16W rows):
+ * the projection of A^T G onto r when u = G r (spmm_tc.cuh:238-269
+ * semantics).  Per-thread partial vectors, added afterwards. */
+ORC_API void orc_bcsr_spmv_t_f64(int64_t W, const int64_t* win_off, const int32_t* cols,
+                                 const void* vals, int32_t vdt, int64_t tile_rows,
+                                 int64_t tile_cols, const double* u, const double* u_abs,
+                                 int64_t num_cols, double* z, double* z_abs) {
+    double* vt = elem_table(vdt);
+    for (int64_t i = 0; i < num_cols; ++i) { z[i] = 0.0; z_abs[i] = 0.0; }
+#pragma omp parallel
+    {
+        double* pz = (double*)calloc((size_t)num_cols, sizeof(double));
+        double* pa = (double*)calloc((size_t)num_cols, sizeof(double));
+#pragma omp for schedule(dynamic, 64)
+        for (int64_t w = 0; w < W; ++w) {
+            for (int64_t t = win_off[w]; t < win_off[w + 1]; ++t) {
+                for (int64_t c = 0; c < tile_cols; ++c) {
+                    const int32_t col = cols[t * tile_cols + c];
+                    if (col < 0 || col >= num_cols) continue;
+                    double s = 0.0, sa = 0.0;
+                    for (int64_t r = 0; r < tile_rows; ++r) {
+                        const double a = elem_at(vals, vt, (t * tile_rows + r) * tile_cols + c);
+                        s += a * u[w * tile_rows + r];
+                        sa += fabs(a) * u_abs[w * tile_rows + r];
+                    }
+                    pz[col] += s;
+                    pa[col] += sa;
+                }
+            }
+        }
+#pragma omp critical
+        {
+            for (int64_t i = 0; i < num_cols; ++i) { z[i] += pz[i]; z_abs[i] += pa[i]; }
+        }
+        free(pz);
+        free(pa);
+    }
+    free(vt);
+}
+
+/* Selected rows of A^T G: out row map[col] (>= 0) receives sum_r A[r][col]
+ * G[r] over every stored slot of that column, out_abs the same with
+ * absolute values; columns with map[col] < 0 are skipped.  G is [16W, ldg]
+ * of type gdt.  Per-thread partial outputs, added afterwards. */
+ORC_API void orc_bcsr_spmm_t_rows_f64(int64_t W, const int64_t* win_off, const int32_t* cols,
+                                      const void* vals, int32_t vdt, int64_t tile_rows,
+                                      int64_t tile_cols, const void* G, int32_t gdt, int64_t ldg,
+                                      int64_t D, int64_t num_cols, const int32_t* map,
+                                      int64_t nout, double* out, double* out_abs) {
+    double* vt = elem_table(vdt);
+    double* gt = elem_table(gdt);
+    for (int64_t i = 0; i < nout * D; ++i) { out[i] = 0.0; out_abs[i] = 0.0; }
+#pragma omp parallel
+    {
+        double* po = (double*)calloc((size_t)(nout * D), sizeof(double));
+        double* pa = (double*)calloc((size_t)(nout * D), sizeof(double));
+#pragma omp for schedule(dynamic, 64)
+        for (int64_t w = 0; w < W; ++w) {
+            for (int64_t t = win_off[w]; t < win_off[w + 1]; ++t) {
+                for (int64_t c = 0; c < tile_cols; ++c) {
+                    const int32_t col = cols[t * tile_cols + c];
+                    if (col < 0 || col >= num_cols || map[col] < 0) continue;
+                    double* o = po + (int64_t)map[col] * D;
+                    double* oa = pa + (int64_t)map[col] * D;
+                    for (int64_t r = 0; r < tile_rows; ++r) {
+                        const double a = elem_at(vals, vt, (t * tile_rows + r) * tile_cols + c);
+                        if (a == 0.0) continue;
+                        const int64_t go = (w * tile_rows + r) * ldg;
+                        for (int64_t f = 0; f < D; ++f) {
+                            const double g = elem_at(G, gt, go + f);
+                            o[f] += a * g;
+                            oa[f] += fabs(a) * fabs(g);
+                        }
+                    }
+                }
+            }
+        }
+#pragma omp critical
+        {
+            for (int64_t i = 0; i < nout * D; ++i) { out[i] += po[i]; out_abs[i] += pa[i]; }
+        }
+        free(po);
+        free(pa);
+    }
+    free(vt);
+    free(gt);
+}
+
+/* ------------------------------------------------------------------------ */
 /* BCSR SpMM transpose  (spmm_tc.cuh:211-270 semantics)                      */
 /* ------------------------------------------------------------------------ */
 

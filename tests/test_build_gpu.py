@@ -23,6 +23,13 @@ def _eq(a, b):
     assert torch.equal(a.cpu(), b.cpu())
 
 
+def _oracle_bcsr(g, tc):
+    """The oracle's restatement of convert_wrapper.cpp:27-180 (itself pinned
+    to the reference's compiled converter in tests/test_oracle.py)."""
+    ow, oc, ov = oracle.csr_to_bcsr(g.num_nodes, g.row_ptr.numpy(), g.col_idx.numpy(), g.values.numpy(), 16, tc)
+    return torch.from_numpy(ow), torch.from_numpy(oc), torch.from_numpy(ov.astype(np.float32))
+
+
 GRAPHS = {
     "random": lambda: synth.random_graph(777, 11.0, seed=3),
     "powerlaw": lambda: synth.chung_lu(5000, 80000, 2.1, seed=4),
@@ -33,18 +40,23 @@ GRAPHS = {
 @pytest.mark.parametrize("name", list(GRAPHS))
 @pytest.mark.parametrize("tc", [8, 16])
 @pytest.mark.parametrize("vdt", [torch.float32, torch.float16, torch.bfloat16])
-def test_csr_build_matches_host_converter(cuda_device, name, tc, vdt):
+def test_csr_build_matches_oracle(cuda_device, name, tc, vdt):
+    """The device build equals the oracle's converter and the host one."""
     print(f"case build {name} tc={tc} {vdt}", flush=True)
     g = GRAPHS[name]()
+    ow, oc, ov = _oracle_bcsr(g, tc)
     hw, hc, hv = _host(g, tc)
     dw, dc, dv = builder.csr_to_bcsr_device(g.num_nodes, g.num_nodes, g.row_ptr.to(cuda_device),
                                             g.col_idx.to(cuda_device), g.values.to(cuda_device),
                                             tile_cols=tc, values_dtype=vdt)
     torch.cuda.synchronize()
-    _eq(dw, hw)
-    _eq(dc, hc)
+    _eq(dw, ow)
+    _eq(dc, oc)
     assert dv.dtype == vdt
-    _eq(dv, hv.to(vdt))
+    _eq(dv, ov.to(vdt))
+    _eq(hw, ow)
+    _eq(hc, oc)
+    _eq(hv, ov)
 
 
 def test_coo_build_duplicates_last_wins(cuda_device):
@@ -192,21 +204,28 @@ def test_reindex_matches_oracle(cuda_device, vdt):
                    np.zeros(0, np.int32)):
         oc, ov = oracle.reindex_prune(cols, vals, active, 16, tc)
         dv = torch.from_numpy(vals).to(cuda_device).to(vdt)
+        v0 = dv._version
         out = core.reindex_bcsr(torch.from_numpy(cols).to(cuda_device), dv,
                                 torch.from_numpy(active).to(cuda_device), 16, tc)
         torch.cuda.synchronize()
+        assert dv._version > v0, "the in-place prune must bump the version caches key on"
         np.testing.assert_array_equal(out.cpu().numpy(), oc)
         np.testing.assert_array_equal(dv.float().cpu().numpy(), ov)
 
 
 def test_build_c2_full_size(cuda_device):
-    """BASELINE config c2 through the device builder equals the host converter."""
+    """BASELINE config c2 through the device builder equals the oracle's
+    converter and the host converter."""
     print("case c2 build", flush=True)
     g = synth.config_graph("c2")
+    ow, oc, ov = _oracle_bcsr(g, 16)
     hw, hc, hv = _host(g, 16)
     dw, dc, dv = builder.csr_to_bcsr_device(g.num_nodes, g.num_nodes, g.row_ptr.to(cuda_device),
                                             g.col_idx.to(cuda_device), g.values.to(cuda_device),
                                             tile_cols=16)
-    _eq(dw, hw)
-    _eq(dc, hc)
-    _eq(dv, hv)
+    _eq(dw, ow)
+    _eq(dc, oc)
+    _eq(dv, ov)
+    _eq(hw, ow)
+    _eq(hc, oc)
+    _eq(hv, ov)

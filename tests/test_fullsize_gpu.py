@@ -1,0 +1,166 @@
+"""The benchmarked workloads at their full BASELINE sizes against the float64
+oracle (tests/_fullsize.py: a fixed window set elementwise, and a projection
+over every row), through the same calls bench.py times.
+
+* c3 (232,965 nodes, 114.6M nnz, f16): the headline N=608 product on X at a
+  640-element pitch, default plan, chunk-major order, the dense-tile first
+  product and the packed-tile second product (bit-identical); the epoch
+  widths N=256 and N=41 (ragged); A^T G at N=256.
+* c4 (2,449,029 nodes, 123.7M nnz, bf16): N=112 at a 128-element pitch,
+  N=256 (two 128-column chunks), N=47 (ragged); A^T G at N=256.
+* c2 (169,343 nodes, 2.33M nnz): A^T G at N=128 in f16 and bf16 through the
+  cached transpose, as the bench's backward leg.
+* c5 (111M nodes, 1.6B edges): one full-size sampling batch bit-exact
+  against the host sampler driven by the same Philox draws.
+
+Tolerance (north_star): rtol 1e-2 for f16/bf16 inputs against |A| |X|.
+The forward semantics follow /root/reference/core/include/spmm_tc.cuh:113-193
+(every output column computed, -1 slots skipped), the transpose :238-269
+without its atomics and 1e-9 skip, the sampling hop order
+/root/reference/sampler/sampler.py:186-279.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _fullsize import HostGraph, check_forward, check_transpose
+from graph_rws_amd import synth
+from graph_rws_amd.data import BCSRGraph, aligned_rows
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-2
+
+
+def _graph(cfg, dev, vdt):
+    g = synth.config_graph(cfg, device=dev)
+    G = BCSRGraph.from_csr(g.row_ptr, g.col_idx, g.values, g.num_nodes, g.num_nodes, tile_cols=16,
+                           device=dev, values_dtype=vdt)
+    torch.cuda.synchronize()
+    return g, G
+
+
+@pytest.fixture(scope="module")
+def c3(cuda_device):
+    print("fixture c3 full size (f16)", flush=True)
+    g, G = _graph("c3", cuda_device, torch.float16)
+    return g, G, HostGraph(G)
+
+
+@pytest.fixture(scope="module")
+def c4(cuda_device):
+    print("fixture c4 full size (bf16)", flush=True)
+    g, G = _graph("c4", cuda_device, torch.bfloat16)
+    return g, G, HostGraph(G)
+
+
+def test_c3_headline_n608_bench_path(c3, cuda_device):
+    """bench.py's timed call: X [n, 608] f16 at a 640 pitch, Y preallocated,
+    G.spmm(X, out=Y); the second product reads the packed tiles."""
+    print("case c3 N=608 f16 bench path", flush=True)
+    g, G, hg = c3
+    X = aligned_rows(synth.features(g.num_nodes, 602, pad_to=608, seed=7, device=cuda_device).half())
+    assert X.stride(0) == 640
+    plan = G.spmm_plan(608)
+    Y1 = torch.empty((16 * G.num_windows, 608), dtype=torch.float16, device=cuda_device)
+    Y2 = torch.empty_like(Y1)
+    G.spmm(X, out=Y1)
+    G.spmm(X, out=Y2)
+    torch.cuda.synchronize()
+    assert G.packed_tiles() is not None, "the second product must have packed the tiles"
+    assert torch.equal(Y1.view(torch.int16), Y2.view(torch.int16)), "packed and dense tiles differ"
+    print(check_forward(hg, X, Y2, RTOL, plan=plan, seed=3), flush=True)
+
+
+@pytest.mark.parametrize("N", [256, 41])
+def test_c3_epoch_widths(c3, cuda_device, N):
+    print(f"case c3 N={N} f16", flush=True)
+    g, G, hg = c3
+    X = synth.features(g.num_nodes, N, seed=N, device=cuda_device).half()
+    Y = G.spmm(X)
+    torch.cuda.synchronize()
+    assert Y.shape == (16 * G.num_windows, N)
+    print(check_forward(hg, X, Y, RTOL, plan=G.spmm_plan(N), seed=N), flush=True)
+
+
+def test_c3_transpose_n256(c3, cuda_device):
+    print("case c3 A^T G N=256 f16", flush=True)
+    g, G, hg = c3
+    Gout = synth.features(16 * G.num_windows, 256, seed=31, device=cuda_device).half()
+    out = G.spmm_transpose(Gout)
+    torch.cuda.synchronize()
+    AT = G.transpose()
+    print(check_transpose(hg, HostGraph(AT), Gout, out, RTOL, planT=AT.spmm_plan(256), seed=5), flush=True)
+
+
+def test_c4_bench_path_n112(c4, cuda_device):
+    """X [n, 112] bf16 at a 128-element (256-byte) pitch, as bench.py
+    --config c4 and the aggregate-first layer 0 gather it."""
+    print("case c4 N=112 bf16", flush=True)
+    g, G, hg = c4
+    X = aligned_rows(synth.features(g.num_nodes, 100, pad_to=112, seed=7, device=cuda_device).to(torch.bfloat16))
+    assert X.stride(0) == 128
+    Y1 = G.spmm(X)
+    Y2 = G.spmm(X)
+    torch.cuda.synchronize()
+    assert torch.equal(Y1.view(torch.int16), Y2.view(torch.int16))
+    print(check_forward(hg, X, Y2, RTOL, plan=G.spmm_plan(112), seed=7), flush=True)
+
+
+@pytest.mark.parametrize("N", [256, 47])
+def test_c4_epoch_widths(c4, cuda_device, N):
+    print(f"case c4 N={N} bf16", flush=True)
+    g, G, hg = c4
+    X = synth.features(g.num_nodes, N, seed=N, device=cuda_device).to(torch.bfloat16)
+    Y = G.spmm(X)
+    torch.cuda.synchronize()
+    print(check_forward(hg, X, Y, RTOL, plan=G.spmm_plan(N), seed=N), flush=True)
+
+
+def test_c4_transpose_n256(c4, cuda_device):
+    print("case c4 A^T G N=256 bf16", flush=True)
+    g, G, hg = c4
+    Gout = synth.features(16 * G.num_windows, 256, seed=41, device=cuda_device).to(torch.bfloat16)
+    out = G.spmm_transpose(Gout)
+    torch.cuda.synchronize()
+    AT = G.transpose()
+    print(check_transpose(hg, HostGraph(AT), Gout, out, RTOL, planT=AT.spmm_plan(256), seed=9), flush=True)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_c2_transpose_bench_leg(cuda_device, dt):
+    """bench.py's c2 backward leg: AT = G.transpose(); AT.spmm(G_r, out=)."""
+    print(f"case c2 A^T G N=128 {dt}", flush=True)
+    g, G = _graph("c2", cuda_device, dt)
+    Gr = synth.features(16 * G.num_windows, 128, seed=22, device=cuda_device).to(dt)
+    AT = G.transpose()
+    out = torch.empty((16 * AT.num_windows, 128), dtype=dt, device=cuda_device)
+    for _ in range(3):  # plan, then packed tiles, then the packed product
+        AT.spmm(Gr, out=out)
+    torch.cuda.synchronize()
+    print(check_transpose(HostGraph(G), HostGraph(AT), Gr, out[: g.num_nodes], RTOL,
+                          planT=AT.spmm_plan(128), seed=2), flush=True)
+
+
+def test_c5_full_size_batch_bit_exact(cuda_device):
+    """One c5 batch (1,024 seeds, fanouts [15, 10, 5], Philox seed 42) on the
+    111M-node graph: every per-hop block equal, bit for bit, to the host
+    sampler's."""
+    print("case c5 full-size batch", flush=True)
+    from graph_rws_amd.sampler import NeighborSampler
+    c = synth.C5
+    g = synth.c5_graph(device=cuda_device)
+    s = NeighborSampler(c["fanouts"], seed=c["philox_seed"], tile_cols=16)
+    seeds = synth.distinct_seeds(g.num_nodes, c["batch"], seed=1000, device=cuda_device)
+    blocks = s.sample_layers(g.row_ptr, g.col_idx, seeds)
+    torch.cuda.synchronize()
+    ref = oracle.sample_blocks(g.row_ptr.cpu().numpy(), g.col_idx.cpu().numpy(), seeds.cpu().numpy(),
+                               c["fanouts"], seed=c["philox_seed"], tile_cols=16)
+    assert len(blocks) == len(ref) == 3
+    for i, (b, r) in enumerate(zip(blocks, ref)):
+        np.testing.assert_array_equal(b.src_nodes.cpu().numpy(), r["src_nodes"], err_msg=f"hop {i} src")
+        np.testing.assert_array_equal(b.window_offset.cpu().numpy(), r["win"], err_msg=f"hop {i} win")
+        np.testing.assert_array_equal(b.original_col_indices.cpu().numpy(), r["cols"], err_msg=f"hop {i} cols")
+        np.testing.assert_array_equal(b.values_condensed.cpu().numpy(), r["vals"], err_msg=f"hop {i} vals")
+    assert sum(int(r["dst"].size) for r in ref) > 300_000

@@ -100,3 +100,43 @@ def test_graphed_dropout_draws_new_mask_each_replay(cuda_device):
         masks.append(kept.clone())
         torch.randn(1000, device=dev).sum()                  # eager work between replays
     assert not torch.equal(masks[0], masks[1]) and not torch.equal(masks[1], masks[2])
+
+
+def test_graphed_step_reads_features_updated_in_place(cuda_device):
+    """c4's layer 0 gathers its 112 bf16 features through a line-aligned,
+    zero-padded copy.  Under capture that copy must be made inside the graph,
+    so a replay after features.copy_(new) trains on the new values: each
+    replay is checked against an eager twin fed the same features."""
+    print("case graphed features copy_ (c4 shape, 1%, bf16)", flush=True)
+    dev = cuda_device
+    g = synth.config_graph("c4", device=dev, scale=0.01)
+    G = BCSRGraph.from_csr(g.row_ptr, g.col_idx, g.values, g.num_nodes, g.num_nodes, tile_cols=16,
+                           device=dev, values_dtype=torch.bfloat16)
+    X = synth.features(g.num_nodes, 112, seed=5, device=dev).to(torch.bfloat16)
+    assert G.padded_input(X) is not None, "the case must gather through the aligned copy"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(6)
+    labels = torch.randint(0, 47, (g.num_nodes,), generator=gen, device=dev)
+    train_idx = torch.nonzero(torch.rand(g.num_nodes, generator=gen, device=dev) < 0.5).view(-1)
+    torch.manual_seed(7)
+    m_e = GCN_BCSR(112, 64, 47, 3, dropout=0.0, use_checkpoint=False).to(dev)
+    m_g = copy.deepcopy(m_e)
+    o_e = torch.optim.Adam(m_e.parameters(), lr=0.01, capturable=True)
+    o_g = torch.optim.Adam(m_g.parameters(), lr=0.01, capturable=True)
+
+    def eager():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            return train_epoch_full(m_e, G, X, labels, train_idx, o_e, dev, sync=False)
+
+    warm = 3
+    step = GraphedFullStep(m_g, G, X, labels, train_idx, o_g, dev, warmup=warm, autocast_dtype=torch.bfloat16)
+    for _ in range(warm):
+        eager()
+    for r in range(3):
+        X.copy_(synth.features(g.num_nodes, 112, seed=100 + r, device=dev).to(torch.bfloat16))
+        loss_g, _ = step()
+        loss_e, _ = eager()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(loss_g, loss_e, rtol=1e-5, atol=1e-6, msg=f"replay {r}: loss")
+        for (n, p), (_, q) in zip(m_g.named_parameters(), m_e.named_parameters()):
+            torch.testing.assert_close(p, q, rtol=1e-5, atol=1e-6, msg=f"replay {r}: {n}")

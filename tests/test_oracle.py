@@ -148,6 +148,90 @@ def test_spmm_t_oracle_matches_scipy(tc):
     np.testing.assert_allclose(outa, abs(A).T @ abs(G[:n]), rtol=1e-12, atol=1e-12)
 
 
+def _quantise(a, dt):
+    """float array -> (stored array of type dt, its exact float64 values)."""
+    import torch
+    a32 = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+    if dt == "f32":
+        return a32.numpy(), a32.double().numpy()
+    if dt == "f16":
+        q = a32.to(torch.float16)
+        return q.numpy(), q.double().numpy()
+    q = a32.to(torch.bfloat16)
+    return q.view(torch.int16).numpy().view(np.uint16), q.double().numpy()
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+def test_element_decoders_cover_every_bit_pattern(dt):
+    """A one-slot graph with A[0][0] = 1 copies X's row through the oracle's
+    element decoder: every 16-bit pattern (subnormals, +-0, +-inf) comes back
+    as numpy's / torch's widening of it; NaN patterns stay NaN."""
+    import torch
+    win = np.array([0, 1], np.int64)
+    cols = np.array([0] + [-1] * 15, np.int32)
+    v = np.zeros(256, np.float32)
+    v[0] = 1.0
+    vq, _ = _quantise(v, dt)
+    if dt == "f32":
+        X = np.random.default_rng(1).standard_normal((1, 4096)).astype(np.float32)
+        ref = X.astype(np.float64)
+    else:
+        bits = np.arange(65536, dtype=np.uint32).astype(np.uint16).reshape(1, -1)
+        if dt == "f16":
+            X, ref = bits.view(np.float16), bits.view(np.float16).astype(np.float64)
+        else:
+            X = bits
+            ref = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).double().numpy()
+    Y, _ = oracle.bcsr_spmm_windows(win, cols, vq, dt, 16, X, dt, [0])
+    nan = np.isnan(ref[0])
+    assert np.array_equal(np.isnan(Y[0]), nan)
+    assert np.array_equal(Y[0][~nan], ref[0][~nan])
+    assert np.all(Y[1:] == 0)
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("tc", [8, 16])
+def test_fullsize_checkers_match_scipy(dt, tc):
+    """The window-subset product, both projections and the selected rows of
+    A^T G equal scipy.sparse on the quantised CSR the BCSR came from."""
+    n, m = 150, 170
+    rp, ci, va = _csr(n, m, 2500, 21)
+    win, cols, vals = oracle.csr_to_bcsr(n, rp, ci, va, 16, tc)
+    vq, vd = _quantise(vals, dt)
+    _, vad = _quantise(va, dt)
+    A = sps.csr_matrix((vad, ci, rp), shape=(n, m))
+    rng = np.random.default_rng(22)
+    Xq, Xd = _quantise(rng.standard_normal((m, 29)), dt)
+    W = len(win) - 1
+    sel = np.array([0, 3, W - 1], np.int64)
+    Y, Ya = oracle.bcsr_spmm_windows(win, cols, vq, dt, tc, Xq, dt, sel)
+    ref = np.zeros((16 * W, 29))
+    ref[:n] = A @ Xd
+    refa = np.zeros((16 * W, 29))
+    refa[:n] = abs(A) @ abs(Xd)
+    rows = np.concatenate([np.arange(16 * w, 16 * w + 16) for w in sel])
+    np.testing.assert_allclose(Y, ref[rows], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(Ya, refa[rows], rtol=1e-12, atol=1e-12)
+    # projection A (X r)
+    r = rng.standard_normal(29)
+    v, va_ = Xd @ r, abs(Xd) @ abs(r)
+    z, za = oracle.bcsr_spmv(win, cols, vq, dt, tc, v, va_, m)
+    np.testing.assert_allclose(z[:n], A @ v, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(za[:n], abs(A) @ va_, rtol=1e-12, atol=1e-12)
+    assert np.all(z[n:] == 0)
+    # projection A^T (G r) and selected rows of A^T G
+    Gq, Gd = _quantise(rng.standard_normal((16 * W, 23)), dt)
+    r2 = rng.standard_normal(23)
+    u, ua = Gd @ r2, abs(Gd) @ abs(r2)
+    zt, zta = oracle.bcsr_spmv_t(win, cols, vq, dt, tc, u, ua, m)
+    np.testing.assert_allclose(zt, A.T @ u[:n], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(zta, abs(A).T @ ua[:n], rtol=1e-12, atol=1e-12)
+    pick = np.array([0, 5, 77, m - 1], np.int64)
+    o, oa = oracle.bcsr_spmm_t_rows(win, cols, vq, dt, tc, Gq, dt, m, pick)
+    np.testing.assert_allclose(o, (A.T @ Gd[:n])[pick], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(oa, (abs(A).T @ abs(Gd[:n]))[pick], rtol=1e-12, atol=1e-12)
+
+
 def test_spmm_f32_baseline_close_to_f64():
     n = 200
     rp, ci, va = _csr(n, n, 3000, 13)
