@@ -77,6 +77,10 @@ _PROTOS = {
                                           ctypes.POINTER(SpmmPlanView), _vp, ctypes.c_int32, ctypes.c_int64,
                                           ctypes.c_int64, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int64,
                                           _vp, ctypes.c_int32, ctypes.c_int64, _vp, ctypes.c_size_t, _vp]),
+    "grws_spmm_noalloc": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.POINTER(PackedTilesView),
+                                         ctypes.POINTER(SpmmPlanView), _vp, ctypes.c_int32, ctypes.c_int64,
+                                         ctypes.c_int64, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int64,
+                                         _vp, ctypes.c_int32, ctypes.c_int64, _vp]),
     "grws_pack_tiles_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
     "grws_pack_tiles_count": (ctypes.c_int, [ctypes.POINTER(BcsrView), _vp, ctypes.c_size_t,
                                              ctypes.POINTER(ctypes.c_int64), _vp]),

@@ -27,6 +27,7 @@
 #include "grws_internal.h"
 
 #include <cstdlib>
+#include <mutex>
 
 namespace grws {
 namespace {
@@ -1363,6 +1364,58 @@ extern "C" int grws_spmm_residual(const grws_bcsr* A, const grws_packed_tiles* P
                                   void* workspace, size_t workspace_bytes, void* stream) {
     return spmm_impl(A, P, plan, x, x_dtype, x_rows, ldx, n_cols, r, ldr, r_rows, y, y_dtype, ldy, workspace,
                      workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// allocation-free SpMM: the split-window partials live in a library-owned
+// device array instead of a caller workspace
+// ---------------------------------------------------------------------------
+namespace {
+// Every GPU the library runs on holds one copy of this array until the
+// process ends.  Host code never passes its name to a kernel (on the host it
+// is only a stand-in for the symbol): the device address of each GPU's copy
+// is looked up once per device and kept in scratch_ptr.
+static __device__ __align__(256) unsigned char scratch[GRWS_SPMM_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch (looked up on the first
+// call on that device, with it current).
+int scratch_for_current_device(void** out) {
+    int dev = -1;
+    GRWS_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return set_error(GRWS_E_INVALID, "spmm_noalloc: device %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        GRWS_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return set_error(GRWS_E_HIP, "spmm_noalloc: no device address for the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return GRWS_OK;
+}
+}  // namespace
+
+extern "C" int grws_spmm_noalloc(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_plan* plan,
+                                 const void* x, int32_t x_dtype, int64_t x_rows, int64_t ldx, int64_t n_cols,
+                                 const void* r, int64_t ldr, int64_t r_rows, void* y, int32_t y_dtype, int64_t ldy,
+                                 void* stream) {
+    clear_error();
+    const size_t need = grws_spmm_workspace_bytes(plan, n_cols);
+    if (need > (size_t)GRWS_SPMM_NOALLOC_SCRATCH_BYTES)
+        return set_error(GRWS_E_CAPACITY,
+                         "spmm_noalloc: the split windows need %zu bytes of partials, above the %zu-byte scratch "
+                         "(use grws_spmm_residual with a workspace, or a plan with more slabs per item)",
+                         need, (size_t)GRWS_SPMM_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if (need > 0) GRWS_TRY(scratch_for_current_device(&ws));
+    // every partial a launch reads was written by the same launch's items
+    // first, so the scratch needs no clearing between calls
+    return spmm_impl(A, P, plan, x, x_dtype, x_rows, ldx, n_cols, r, ldr, r_rows, y, y_dtype,
+                     ldy, ws, need, stream);
 }
 
 namespace {

@@ -192,6 +192,24 @@ int grws_spmm_residual(const grws_bcsr* A, const grws_packed_tiles* P, const grw
                        const void* r, int64_t ldr, int64_t r_rows, void* y, int32_t y_dtype, int64_t ldy,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * grws_spmm_residual without a workspace argument; it allocates nothing.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The partial sums of split windows go to
+ * a device array the library owns, GRWS_SPMM_NOALLOC_SCRATCH_BYTES on every
+ * GPU it runs on, held until the process ends; a call whose plan needs more
+ * (grws_spmm_workspace_bytes(plan, n_cols)) returns GRWS_E_CAPACITY.  All
+ * calls on one GPU share that array: calls that overlap in time on one GPU
+ * (different streams or threads) race and give wrong results.  The stream
+ * must belong to the current device.  r may be NULL (Y = A X).
+ */
+#define GRWS_SPMM_NOALLOC_SCRATCH_BYTES (16u << 20)
+int grws_spmm_noalloc(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_plan* plan,
+                      const void* x, int32_t x_dtype, int64_t x_rows, int64_t ldx, int64_t n_cols,
+                      const void* r, int64_t ldr, int64_t r_rows, void* y, int32_t y_dtype, int64_t ldy,
+                      void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* CSR -> BCSR on host cores.  Replaces core_lib.csr_to_bcsr_cpu             */
 /* (bind.cpp:143-150 -> convert_wrapper.cpp:27-180): same layout, same       */
