@@ -204,6 +204,15 @@ def cpu_baseline(g, G, X: torch.Tensor, Y: torch.Tensor, rtol: float, budget_s: 
             "torch_threads": torch.get_num_threads(), "parity": parity}
 
 
+def sampling_bytes(blk) -> int:
+    """Algorithmic bytes of one sampled hop: 16 F + 36 E plus its BCSR block
+    (window offsets, column slots, values)."""
+    F, E, T, tc = blk.num_rows, blk.num_sampled_edges, blk.num_tiles, blk.tile_cols
+    W = (F + 15) // 16
+    return (16 * F + 36 * E + 8 * (W + 1) + 4 * T * tc
+            + blk.values_condensed.element_size() * T * 16 * tc)
+
+
 def bench_sampling(dev, batches: int, warmup: int, cpu: bool) -> dict:
     """c5: one batch = 1,024 distinct uniform seeds, 3 hops with fanouts
     [15, 10, 5] (hop 0 from the seeds draws 5), Philox seed 42, unique +
@@ -224,13 +233,17 @@ def bench_sampling(dev, batches: int, warmup: int, cpu: bool) -> dict:
         s.sample_layers(g.row_ptr, g.col_idx, seed_sets[b])
     torch.cuda.synchronize(dev)
     edges, times, blocks = 0, [], None
+    b_alg = 0
+    gc.collect()
     for b in range(warmup, warmup + batches):
         t1 = time.perf_counter()
         blocks = s.sample_layers(g.row_ptr, g.col_idx, seed_sets[b])
         torch.cuda.synchronize(dev)
         times.append(time.perf_counter() - t1)
         edges += sum(x.num_sampled_edges for x in blocks)
+        b_alg += sum(sampling_bytes(x) for x in blocks)
     total = sum(times)
+    sgbs = b_alg / total / 1e9
     out = {
         "workload": "c5 mini-batch sampling (Philox fanout [15,10,5], unique+relabel, per-hop BCSR)",
         "graph": {"nodes": g.num_nodes, "edges": g.nnz, "indptr": "int64", "indices": "int32"},
@@ -241,6 +254,15 @@ def bench_sampling(dev, batches: int, warmup: int, cpu: bool) -> dict:
         "hop_edges_last_batch": [x.num_sampled_edges for x in blocks],
         "input_nodes_last_batch": int(blocks[0].num_cols),
         "generate_s": round(t_gen, 2),
+        "dispatches_per_batch": 7 * len(c["fanouts"]) + 2,
+        "host_syncs_per_batch": 1,
+        "roofline": {"bound": "hbm (random 8-64 B reads: latency bound in practice)",
+                     "achieved": round(sgbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(sgbs / HBM_PEAK_GBS, 5),
+                     "bytes_per_batch": round(b_alg / batches),
+                     "bytes": "per hop 16 F + 36 E (indptr pair and frontier id per node; per edge the "
+                              "index, the source's degree, three relabel passes of 8 B) plus the block "
+                              "written"},
     }
     if cpu:
         import numpy as np

@@ -704,20 +704,23 @@ def sample_all_layers(window_offset: torch.Tensor, original_col_indices: torch.T
 
 
 class SampleState:
-    """Per-graph scratch of the fused sampler: a node -> local id map (int32,
-    all -1 between calls) and a new-source bitmap (uint32, all 0 between
-    calls).  Every grws_sample_block call leaves both as it found them.  One
-    state serves one stream at a time."""
+    """Per-graph scratch of the fused samplers: a node -> local id map (int32,
+    all -1 between calls) and the state words of grws_sample_blocks (uint32,
+    all 0 between calls): the new-source bitmap (its first ceil(n/32) words,
+    which grws_sample_block and the repack take), per-1024-id counts and the
+    batch counters.  Every call leaves both as it found them.  One state
+    serves one stream at a time."""
 
     def __init__(self, num_nodes: int, device):
         self.num_nodes = int(num_nodes)
         self.node_map = torch.empty(max(1, self.num_nodes), dtype=torch.int32, device=device)
-        self.bitmap = torch.empty(max(1, (self.num_nodes + 31) // 32), dtype=torch.int32, device=device)
+        words = int(L.load().grws_sample_blocks_state_words(self.num_nodes))
+        self.bitmap = torch.empty(max(4, words), dtype=torch.int32, device=device)
         self.reset()
 
     def reset(self) -> None:
         """Back to all -1 / all 0 (on the current stream)."""
-        L.call("grws_sample_state_init", L.ptr(self.node_map), L.ptr(self.bitmap), self.num_nodes,
+        L.call("grws_sample_blocks_state_init", L.ptr(self.node_map), L.ptr(self.bitmap), self.num_nodes,
                L.stream_of(self.node_map.device))
 
 
@@ -751,6 +754,81 @@ def sample_block(indptr: torch.Tensor, indices: torch.Tensor, frontier: torch.Te
            L.stream_of(dev))
     E, S, T = (int(c) for c in counts)
     return win, cols[:T * tile_cols], vals[:T * 16 * tile_cols], nxt[:S], E
+
+
+_BLOCKS_SIZES: dict = {}
+
+
+def _sample_blocks_sizes(F0: int, fanouts, tile_cols: int, n: int):
+    """Capacities and workspace of a batch shape (host arithmetic, cached)."""
+    key = (F0, tuple(fanouts), tile_cols, n)
+    hit = _BLOCKS_SIZES.get(key)
+    if hit is None:
+        H = len(fanouts)
+        fo = (ctypes.c_int32 * H)(*[int(k) for k in fanouts])
+        ms = (ctypes.c_int64 * H)()
+        mt = (ctypes.c_int64 * H)()
+        L.call("grws_sample_blocks_capacity", F0, fo, H, int(tile_cols), n,
+               ctypes.cast(ms, ctypes.POINTER(ctypes.c_int64)), ctypes.cast(mt, ctypes.POINTER(ctypes.c_int64)))
+        wsb = int(L.load().grws_sample_blocks_workspace_bytes(F0, fo, H, int(tile_cols), n))
+        fcap = [F0] + [int(ms[h]) for h in range(H - 1)]
+        hit = (fo, [int(x) for x in ms], [int(x) for x in mt], fcap, wsb)
+        if len(_BLOCKS_SIZES) > 64:
+            _BLOCKS_SIZES.clear()
+        _BLOCKS_SIZES[key] = hit
+    return hit
+
+
+def sample_blocks(indptr: torch.Tensor, indices: torch.Tensor, seeds: torch.Tensor, fanouts,
+                  state: SampleState, seed: int = 42, tile_cols: int = 16,
+                  values_dtype: torch.dtype = torch.float32):
+    """Every hop of a mini-batch in one call (fanouts in hop order, hop 0 from
+    the seeds): per hop (window_offset, col_indices, values, next_frontier,
+    num_edges) as sample_block returns them.  One stream sync for the whole
+    batch; outputs are views of buffers sized by the hops' capacities."""
+    n, nnz = _csr_arrays(indptr, indices)
+    dev = indptr.device
+    sd = seeds.to(dev, torch.int64).contiguous()
+    F0 = sd.numel()
+    H = len(fanouts)
+    fo, ms, mt, fcap, wsb = _sample_blocks_sizes(F0, fanouts, int(tile_cols), n)
+    # one buffer per element type, carved per hop on 256-byte boundaries
+    def layout(sizes, esz):
+        offs, o = [], 0
+        for k in sizes:
+            offs.append(o)
+            o += -(-max(1, k) * esz // 256) * 256 // esz
+        return offs, o
+    i64_sizes = [ms[h] for h in range(H)] + [(fcap[h] + 15) // 16 + 1 for h in range(H)]
+    i64_offs, i64_total = layout(i64_sizes, 8)
+    c_offs, c_total = layout([mt[h] * tile_cols for h in range(H)], 4)
+    esz = torch.empty(0, dtype=values_dtype).element_size()
+    v_offs, v_total = layout([mt[h] * 16 * tile_cols for h in range(H)], esz)
+    b64 = torch.empty(i64_total, dtype=torch.int64, device=dev)
+    bc = torch.empty(c_total, dtype=torch.int32, device=dev)
+    bv = torch.empty(v_total, dtype=values_dtype, device=dev)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    nxt = [b64[i64_offs[h]:i64_offs[h] + max(1, ms[h])] for h in range(H)]
+    win = [b64[i64_offs[H + h]:i64_offs[H + h] + i64_sizes[H + h]] for h in range(H)]
+    cols = [bc[c_offs[h]:c_offs[h] + max(1, mt[h] * tile_cols)] for h in range(H)]
+    vals = [bv[v_offs[h]:v_offs[h] + max(1, mt[h] * 16 * tile_cols)] for h in range(H)]
+
+    def parr(ts):
+        return (ctypes.c_void_p * H)(*[t.data_ptr() for t in ts])
+
+    counts = (ctypes.c_int64 * (3 * H))()
+    L.call("grws_sample_blocks", L.ptr(indptr), L.ptr(indices), n, nnz, L.ptr(sd), F0, fo, H,
+           ctypes.c_uint64(int(seed) & 0xFFFFFFFFFFFFFFFF), L.ptr(state.node_map), L.ptr(state.bitmap),
+           int(tile_cols), L.dtype_code(values_dtype), parr(nxt), parr(win), parr(cols), parr(vals), L.ptr(ws),
+           wsb, ctypes.cast(counts, ctypes.POINTER(ctypes.c_int64)), L.stream_of(dev))
+    out = []
+    F = F0
+    for h in range(H):
+        E, S, T = int(counts[3 * h]), int(counts[3 * h + 1]), int(counts[3 * h + 2])
+        W = (F + 15) // 16
+        out.append((win[h][:W + 1], cols[h][:T * tile_cols], vals[h][:T * 16 * tile_cols], nxt[h][:S], E))
+        F = S
+    return out
 
 
 # ---------------------------------------------------------------------------

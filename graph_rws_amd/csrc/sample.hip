@@ -35,6 +35,8 @@ namespace {
 constexpr int kBlk = 256;
 constexpr int kWavesPerBlock = kBlk / kWave;
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 enum : int32_t { kErrNode = 1, kErrIndptr = 2, kErrIndex = 4, kErrDup = 8, kErrDegree = 16 };
 
 inline int bits_for(int64_t x) {
@@ -531,6 +533,427 @@ void carve_block(C& cv, int64_t F, int32_t k, int64_t num_nodes, BlockWs* w) {
     w->scan_ws = cv.template take<char>(w->scan_bytes);
 }
 
+// ---------------------------------------------------------------------------
+// whole batch (grws_sample_blocks): every hop on the device, one sync
+// ---------------------------------------------------------------------------
+// Sizes stay on the device: each hop's frontier, edge and tile counts live in
+// BatchCtr (in the caller's state buffer, all zero between calls), and every
+// kernel is launched over the hop's host-side capacity, its surplus threads
+// leaving at once.  Edges are stored in fixed slots: frontier node i owns
+// slots [i k, i k + k), min(deg, k) of them filled in ascending CSR position
+// and the rest -1, so no offset scan is needed.  The relabel ranks a new
+// source by the count of new sources in earlier 1024-id groups (one scan
+// over the group counts the marking kept) plus the set bits before it in its
+// own group: work proportional to the batch and to num_nodes / 1024, not to
+// the whole bitmap.
+constexpr int kMaxHops = 8;
+constexpr int kGroupShift = 10;  // 1024 ids (32 bitmap words) per group
+
+struct BatchCtr {
+    int64_t F[kMaxHops + 1];  // frontier size of each hop (F[h+1] = sources of hop h)
+    int64_t E[kMaxHops];      // sampled edges of each hop
+    int64_t T[kMaxHops];      // tiles of each hop's block
+    int32_t err;
+    uint32_t done;            // work-groups of the group scan that have finished
+};
+constexpr int64_t kCtrWords = (sizeof(BatchCtr) + 3) / 4;
+
+inline int64_t bitmap_words(int64_t n) { return (n + 31) / 32; }
+inline int64_t group_count(int64_t n) { return (n + (1 << kGroupShift) - 1) >> kGroupShift; }
+
+__device__ __forceinline__ int64_t hop_frontier(const BatchCtr* c, int h, int64_t F0) { return h == 0 ? F0 : c->F[h]; }
+
+// Per frontier node: min(deg, k) and the node map entry; edge total per hop.
+__global__ __launch_bounds__(kBlk) void mh_count_kernel(const int64_t* __restrict__ indptr, int64_t nnz,
+                                                        int64_t num_nodes, const int64_t* __restrict__ frontier,
+                                                        int64_t F0, int h, int k, int32_t* __restrict__ node_map,
+                                                        BatchCtr* __restrict__ ctr) {
+    const int64_t F = hop_frontier(ctr, h, F0);
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (h == 0 && i == 0) ctr->F[0] = F0;
+    int64_t c = 0;
+    if (i < F) {
+        const int64_t v = frontier[i];
+        const NodeRange r = node_range(indptr, nnz, num_nodes, v);
+        if (r.err) {
+            atomicOr(&ctr->err, r.err);
+        } else if (atomicExch(&node_map[v], (int32_t)i) != -1) {
+            atomicOr(&ctr->err, kErrDup);
+        }
+        c = r.deg < k ? r.deg : k;
+    }
+    // one atomic per wave
+    for (int d = 32; d > 0; d >>= 1) c += __shfl_xor(c, d, kWave);
+    if (lane_id() == 0 && c) atomicAdd((unsigned long long*)&ctr->E[h], (unsigned long long)c);
+}
+
+// One wave per frontier node: the hop_sample_kernel draw into fixed slots,
+// then the new sources' bits and group counts.
+__global__ __launch_bounds__(kBlk) void mh_sample_kernel(const int64_t* __restrict__ indptr,
+                                                         const int32_t* __restrict__ indices, int64_t nnz,
+                                                         int64_t num_nodes, const int64_t* __restrict__ frontier,
+                                                         int64_t F0, int h, int k, uint64_t seed,
+                                                         const int32_t* __restrict__ node_map,
+                                                         uint32_t* __restrict__ bitmap, int32_t* __restrict__ grpcnt,
+                                                         int64_t* __restrict__ edge_src, float* __restrict__ edge_val,
+                                                         BatchCtr* __restrict__ ctr) {
+    const int64_t F = hop_frontier(ctr, h, F0);
+    const int64_t i = (int64_t)blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+    if (i >= F) return;  // wave-uniform
+    const int lane = lane_id();
+    const int64_t v = frontier[i];
+    const NodeRange r = node_range(indptr, nnz, num_nodes, v);
+    const int64_t deg = r.err ? 0 : r.deg;
+    int64_t x = lane;
+    int rank = lane;
+    int n;
+    if (deg <= k) {
+        n = (int)deg;
+    } else {
+        n = k;
+        const int64_t j0 = deg - k;
+        int64_t t = 0;
+        if (lane < k) {
+            const uint32_t u = philox_word0(seed, (uint64_t)v, (uint32_t)lane);
+            t = (int64_t)(((uint64_t)u * (uint64_t)(j0 + lane + 1)) >> 32);
+        }
+        x = -1;
+        for (int d = 0; d < k; ++d) {
+            const int64_t td = readlane64(t, d);
+            const bool taken = __ballot(lane < d && x == td) != 0ull;
+            if (lane == d) x = taken ? j0 + d : td;
+        }
+        rank = 0;
+        for (int e = 0; e < k; ++e) rank += readlane64(x, e) < x ? 1 : 0;
+    }
+    const int64_t slot0 = i * (int64_t)k;
+    if (lane < n) {
+        const int32_t s = indices[r.start + x];
+        const int64_t o = slot0 + rank;
+        edge_src[o] = (int64_t)s;
+        float w = 0.0f;
+        if (s >= 0 && (int64_t)s < num_nodes) {
+            w = gcn_weight(deg, indptr[(int64_t)s + 1] - indptr[s]);
+            if (node_map[s] < 0) {
+                const uint32_t bit = 1u << (s & 31);
+                if (!(atomicOr(&bitmap[s >> 5], bit) & bit)) atomicAdd(&grpcnt[s >> kGroupShift], 1);
+            }
+        } else {
+            atomicOr(&ctr->err, kErrIndex);
+        }
+        edge_val[o] = w;
+    } else if (lane < k) {
+        edge_src[slot0 + lane] = -1;  // empty slot
+    }
+}
+
+// Exclusive scan of the group counts: one work-group of 256 threads per
+// slice of 1024 groups (lane t of the slice takes 4 consecutive counts)
+// writes the in-slice prefixes and the slice total; the last work-group to
+// finish (a ticket, no waiting) turns the slice totals into slice offsets and
+// sets F[h+1] = F[h] + the number of new sources.
+constexpr int kSliceGroups = 1024;
+__global__ __launch_bounds__(kBlk) void mh_group_scan_kernel(const int32_t* __restrict__ grpcnt, int64_t ng,
+                                                             int32_t* __restrict__ grpoff, int32_t* slicesum,
+                                                             int32_t* __restrict__ sliceoff, int64_t nslices,
+                                                             int64_t F0, int h, BatchCtr* __restrict__ ctr) {
+    __shared__ int64_t tmp[kBlk / kWave + 1];
+    __shared__ bool last;
+    const int64_t base = (int64_t)blockIdx.x * kSliceGroups + 4 * threadIdx.x;
+    int32_t v[4];
+    int64_t t = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        v[q] = base + q < ng ? grpcnt[base + q] : 0;
+        t += v[q];
+    }
+    int64_t total;
+    const int64_t incl = block_incl_scan<kBlk>(t, tmp, &total);
+    int64_t x = incl - t;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (base + q < ng) grpoff[base + q] = (int32_t)x;
+        x += v[q];
+    }
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(&slicesum[blockIdx.x], (int32_t)total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __threadfence();
+        last = atomicAdd(&ctr->done, 1u) == (uint32_t)(nslices - 1);
+    }
+    __syncthreads();
+    if (!last) return;
+    // every slice total is visible: exclusive scan of the nslices totals
+    __threadfence();
+    const int64_t per = (nslices + kBlk - 1) / kBlk;
+    const int64_t b = threadIdx.x * per;
+    const int64_t e = b + per < nslices ? b + per : nslices;
+    int64_t sum = 0;
+    for (int64_t k = b; k < e; ++k) sum += __hip_atomic_load(&slicesum[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int64_t inc2 = block_incl_scan<kBlk>(sum, tmp, &total);
+    int64_t run = inc2 - sum;
+    for (int64_t k = b; k < e; ++k) {
+        sliceoff[k] = (int32_t)run;
+        run += __hip_atomic_load(&slicesum[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (threadIdx.x == 0) {
+        ctr->F[h + 1] = hop_frontier(ctr, h, F0) + total;
+        ctr->done = 0u;
+    }
+}
+
+// Local id of every filled slot's source (-1 for an empty slot, 0 for an
+// invalid id, which the sampler flagged), the next frontier's new ids, and
+// (threads below F) its first F entries.
+__global__ __launch_bounds__(kBlk) void mh_assign_kernel(const int64_t* __restrict__ frontier, int64_t F0, int h,
+                                                         int k, int64_t num_nodes,
+                                                         const int64_t* __restrict__ edge_src,
+                                                         const int32_t* __restrict__ node_map,
+                                                         const uint32_t* __restrict__ bitmap,
+                                                         const int32_t* __restrict__ grpoff,
+                                                         const int32_t* __restrict__ sliceoff,
+                                                         int32_t* __restrict__ src_local,
+                                                         int64_t* __restrict__ next_frontier,
+                                                         const BatchCtr* __restrict__ ctr) {
+    const int64_t F = hop_frontier(ctr, h, F0);
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < F) next_frontier[e] = frontier[e];
+    if (e >= F * (int64_t)k) return;
+    const int64_t s = edge_src[e];
+    if (s < 0) {
+        src_local[e] = -1;
+        return;
+    }
+    if (s >= num_nodes) {
+        src_local[e] = 0;
+        return;
+    }
+    const int32_t l = node_map[s];
+    if (l >= 0) {
+        src_local[e] = l;
+        return;
+    }
+    // new source: sources of earlier groups, then the set bits before it in
+    // its group (the group's 32 words are one 128-byte line)
+    const int64_t g = s >> kGroupShift;
+    const int wi = (int)((s >> 5) & 31);
+    const u32x4_t* gw = reinterpret_cast<const u32x4_t*>(bitmap + (g << 5));
+    int below = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const u32x4_t v = gw[q];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) below += (4 * q + j < wi) ? __popc(v[j]) : 0;
+    }
+    below += __popc(bitmap[s >> 5] & ((1u << (s & 31)) - 1u));
+    const int64_t local = F + sliceoff[g / kSliceGroups] + grpoff[g] + below;
+    src_local[e] = (int32_t)local;
+    next_frontier[local] = s;  // every slot of this source writes the same value
+}
+
+// One work-group per 16-row window of the hop's block, slots
+// [16 w k, min(16 w + 16, F) k): sorted in LDS by (column, row, slot), the
+// distinct columns numbered; count pass: tiles per window, and the window's
+// share of the state restored (its rows' node map entries, its sources' bitmap
+// words and group counts); fill pass: the tiles.  Same rules as
+// block_window_kernel (the last of duplicate (row, column) slots wins).
+template <typename VT>
+__global__ __launch_bounds__(256) void mh_window_kernel(int fill, const int64_t* __restrict__ frontier, int64_t F0,
+                                                        int h, int k, const int32_t* __restrict__ src_local,
+                                                        const int64_t* __restrict__ edge_src,
+                                                        const float* __restrict__ edge_val, int tc,
+                                                        int32_t* __restrict__ wtiles, int64_t wcap,
+                                                        const int64_t* __restrict__ window_offset,
+                                                        int32_t* __restrict__ out_cols, VT* __restrict__ out_vals,
+                                                        int64_t num_nodes, int32_t* __restrict__ node_map,
+                                                        uint32_t* __restrict__ bitmap, int32_t* __restrict__ grpcnt,
+                                                        BatchCtr* __restrict__ ctr) {
+    __shared__ uint64_t key[kWinEdges];
+    __shared__ int32_t pos[kWinEdges];
+    __shared__ int64_t scan_tmp[kBlk / kWave + 1];
+    const int tid = threadIdx.x;
+    const int64_t F = hop_frontier(ctr, h, F0);
+    const int64_t W = (F + 15) / 16;
+    const int64_t w = blockIdx.x;
+    if (fill && w == 0 && tid == 0) ctr->T[h] = window_offset[wcap];
+    if (w >= W) {
+        if (!fill && tid == 0) wtiles[w] = 0;
+        return;
+    }
+    const int64_t r0 = w * 16;
+    const int rows = (int)(F - r0 < 16 ? F - r0 : 16);
+    const int64_t s0 = r0 * k;
+    const int ns = rows * k;  // <= kWinEdges
+    int P = 1;
+    while (P < ns) P <<= 1;
+    for (int i = tid; i < P; i += kBlk) {
+        uint64_t kk = ~0ull;
+        if (i < ns) {
+            const int32_t c = src_local[s0 + i];
+            if (c >= 0) kk = ((uint64_t)(uint32_t)c << 14) | ((uint64_t)(i / k) << 10) | (uint64_t)i;
+        }
+        key[i] = kk;
+    }
+    if (!fill) {
+        // restore the state this hop changed: node map of the window's rows,
+        // bitmap words and group counts of its sources (the relabel is done)
+        if (tid < rows) {
+            const int64_t v = frontier[r0 + tid];
+            if (v >= 0 && v < num_nodes) node_map[v] = -1;
+        }
+        for (int i = tid; i < ns; i += kBlk) {
+            const int64_t s = edge_src[s0 + i];
+            if (s >= 0 && s < num_nodes) {
+                bitmap[s >> 5] = 0u;
+                grpcnt[s >> kGroupShift] = 0;
+            }
+        }
+    }
+    __syncthreads();
+    for (int size = 2; size <= P; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < P; i += kBlk) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool up = (i & size) == 0;
+                    const uint64_t a = key[i], b = key[j];
+                    if ((a > b) == up) {
+                        key[i] = b;
+                        key[j] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    int flags = 0, cnt = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int i = tid * 4 + q;
+        const bool f = i < P && key[i] != ~0ull && (i == 0 || (key[i] >> 14) != (key[i - 1] >> 14));
+        flags |= (f ? 1 : 0) << q;
+        cnt += f ? 1 : 0;
+    }
+    int64_t total;
+    const int64_t incl = block_incl_scan<kBlk>(cnt, scan_tmp, &total);
+    int run = (int)(incl - cnt);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int i = tid * 4 + q;
+        if (i < P) {
+            run += (flags >> q) & 1;
+            pos[i] = run - 1;
+        }
+    }
+    const int64_t tiles = (total + tc - 1) / tc;
+    if (!fill) {
+        if (tid == 0) wtiles[w] = (int32_t)tiles;
+        return;
+    }
+    __syncthreads();
+    const int64_t wo = window_offset[w];
+    for (int64_t i = tid; i < tiles * tc; i += kBlk) out_cols[wo * tc + i] = -1;
+    for (int64_t i = tid; i < tiles * 16 * tc; i += kBlk) out_vals[wo * 16 * tc + i] = cvt_value<VT>(0.0f);
+    __syncthreads();
+    for (int i = tid; i < P; i += kBlk) {
+        const uint64_t kk = key[i];
+        if (kk == ~0ull) continue;
+        const int p = pos[i];
+        const int64_t tile = wo + p / tc;
+        const int c = p % tc;
+        if (i == 0 || (key[i - 1] >> 14) != (kk >> 14)) out_cols[tile * tc + c] = (int32_t)(kk >> 14);
+        if (i + 1 >= P || (key[i + 1] >> 10) != (kk >> 10)) {
+            const int r = (int)((kk >> 10) & 15u);
+            out_vals[(tile * 16 + r) * tc + c] = cvt_value<VT>(edge_val[s0 + (int64_t)(kk & 1023u)]);
+        }
+    }
+}
+
+// Copies the batch counters out and clears them for the next call.
+__global__ void mh_finish_kernel(BatchCtr* __restrict__ ctr, int64_t* __restrict__ out, int H) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    for (int h = 0; h <= H; ++h) out[h] = ctr->F[h];
+    for (int h = 0; h < H; ++h) {
+        out[H + 1 + h] = ctr->E[h];
+        out[2 * H + 1 + h] = ctr->T[h];
+    }
+    out[3 * H + 1] = ctr->err;
+    for (int h = 0; h <= kMaxHops; ++h) ctr->F[h] = 0;
+    for (int h = 0; h < kMaxHops; ++h) ctr->E[h] = ctr->T[h] = 0;
+    ctr->err = 0;
+}
+
+// Host-side capacities of a batch: frontier, edge slots, windows and tiles
+// of each hop.
+struct HopCaps {
+    int64_t F[kMaxHops + 1], E[kMaxHops], W[kMaxHops], T[kMaxHops];
+};
+
+HopCaps hop_caps(int64_t num_seeds, const int32_t* fanouts, int H, int tc, int64_t num_nodes) {
+    HopCaps c{};
+    c.F[0] = num_seeds;
+    for (int h = 0; h < H; ++h) {
+        const int64_t k = fanouts[h];
+        c.E[h] = c.F[h] * k;
+        c.W[h] = (c.F[h] + 15) / 16;
+        c.T[h] = c.W[h] * ((16 * k + tc - 1) / tc);
+        // the next frontier is this one plus at most min(edges, num_nodes)
+        // new sources
+        const int64_t nf = c.F[h] * (1 + k);
+        const int64_t lim = c.F[h] + num_nodes;
+        c.F[h + 1] = nf < lim ? nf : lim;
+    }
+    return c;
+}
+
+struct BatchWs {
+    int64_t* edge_src;
+    float* edge_val;
+    int32_t* src_local;
+    int32_t* grpoff;
+    int32_t* slicesum;
+    int32_t* sliceoff;
+    int32_t* wtiles;
+    int64_t* out;
+    char* scan_ws;
+    size_t scan_bytes;
+};
+
+template <typename C>
+void carve_batch(C& cv, const HopCaps& c, int H, int64_t num_nodes, BatchWs* w) {
+    int64_t emax = 1, wmax = 1;
+    for (int h = 0; h < H; ++h) {
+        emax = c.E[h] > emax ? c.E[h] : emax;
+        wmax = c.W[h] > wmax ? c.W[h] : wmax;
+    }
+    w->edge_src = cv.template take<int64_t>(emax);
+    w->edge_val = cv.template take<float>(emax);
+    w->src_local = cv.template take<int32_t>(emax);
+    w->grpoff = cv.template take<int32_t>(group_count(num_nodes) + 1);
+    w->slicesum = cv.template take<int32_t>(group_count(num_nodes) / kSliceGroups + 2);
+    w->sliceoff = cv.template take<int32_t>(group_count(num_nodes) / kSliceGroups + 2);
+    w->wtiles = cv.template take<int32_t>(wmax + 1);
+    w->out = cv.template take<int64_t>(3 * kMaxHops + 4);
+    w->scan_bytes = scan_workspace_bytes(wmax);
+    w->scan_ws = cv.template take<char>(w->scan_bytes);
+}
+
+// State buffer of grws_sample_blocks (uint32 words): the new-source bitmap
+// (padded to whole groups), the group counts, then BatchCtr on an 8-byte
+// boundary.  Its first ceil(num_nodes / 32) words are the bitmap that
+// grws_sample_block and grws_repack_* use.
+struct StateLayout {
+    int64_t groups, grp_off, ctr_off, words;
+};
+
+StateLayout state_layout(int64_t num_nodes) {
+    StateLayout l;
+    l.groups = group_count(num_nodes > 0 ? num_nodes : 1);
+    l.grp_off = l.groups * 32;
+    l.ctr_off = (l.grp_off + l.groups + 1) & ~(int64_t)1;
+    l.words = l.ctr_off + kCtrWords;
+    return l;
+}
+
 }  // namespace
 }  // namespace grws
 
@@ -800,5 +1223,153 @@ extern "C" int grws_sample_block(const int64_t* indptr, const int32_t* indices, 
     counts_out[0] = h[0];
     counts_out[1] = F + h[1];
     counts_out[2] = h[2];
+    return GRWS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// whole batch: every hop, one synchronisation
+// ---------------------------------------------------------------------------
+extern "C" size_t grws_sample_blocks_state_words(int64_t num_nodes) {
+    if (num_nodes < 0) return 0;
+    return (size_t)state_layout(num_nodes).words;
+}
+
+extern "C" int grws_sample_blocks_state_init(int32_t* node_map, uint32_t* state, int64_t num_nodes, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(num_nodes >= 0, "sample_blocks_state_init: negative num_nodes");
+    GRWS_CHECK_ARG(state != nullptr && (node_map != nullptr || num_nodes == 0),
+                   "sample_blocks_state_init: null pointer");
+    GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(state) % 16 == 0, "sample_blocks_state_init: state not 16-byte aligned");
+    const StateLayout l = state_layout(num_nodes);
+    int64_t blocks = ((num_nodes > l.words ? num_nodes : l.words) + kBlk - 1) / kBlk;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(fill_state_kernel, dim3((unsigned)blocks), dim3(kBlk), 0, stream, node_map, num_nodes, state,
+                       l.words);
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
+extern "C" int grws_sample_blocks_capacity(int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
+                                           int32_t tile_cols, int64_t num_nodes, int64_t* max_src,
+                                           int64_t* max_tiles) {
+    clear_error();
+    GRWS_CHECK_ARG(num_seeds >= 0 && num_nodes >= 0, "sample_blocks_capacity: negative size");
+    GRWS_CHECK_ARG(num_hops >= 1 && num_hops <= kMaxHops, "sample_blocks_capacity: num_hops must be in [1, %d]",
+                   kMaxHops);
+    GRWS_CHECK_ARG(fanouts && max_src && max_tiles, "sample_blocks_capacity: null pointer");
+    GRWS_CHECK_ARG(tile_cols == 8 || tile_cols == 16, "sample_blocks_capacity: tile_cols must be 8 or 16");
+    for (int h = 0; h < num_hops; ++h)
+        GRWS_CHECK_ARG(fanouts[h] >= 1 && fanouts[h] <= kWave, "sample_blocks_capacity: fanout %d outside [1, 64]",
+                       fanouts[h]);
+    const HopCaps c = hop_caps(num_seeds, fanouts, num_hops, tile_cols, num_nodes);
+    for (int h = 0; h < num_hops; ++h) {
+        max_src[h] = c.F[h + 1];
+        max_tiles[h] = c.T[h];
+    }
+    return GRWS_OK;
+}
+
+extern "C" size_t grws_sample_blocks_workspace_bytes(int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
+                                                     int32_t tile_cols, int64_t num_nodes) {
+    if (num_seeds < 0 || num_nodes < 0 || !fanouts || num_hops < 1 || num_hops > kMaxHops) return 0;
+    for (int h = 0; h < num_hops; ++h)
+        if (fanouts[h] < 1 || fanouts[h] > kWave) return 0;
+    const HopCaps c = hop_caps(num_seeds, fanouts, num_hops, tile_cols == 8 ? 8 : 16, num_nodes);
+    NullCarver nc;
+    BatchWs w;
+    carve_batch(nc, c, num_hops, num_nodes, &w);
+    return nc.s.used + 256;
+}
+
+extern "C" int grws_sample_blocks(const int64_t* indptr, const int32_t* indices, int64_t num_nodes, int64_t nnz,
+                                  const int64_t* seeds, int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
+                                  uint64_t seed, int32_t* node_map, uint32_t* state, int32_t tile_cols,
+                                  int32_t values_dtype, int64_t* const* next_frontier,
+                                  int64_t* const* window_offset, int32_t* const* col_indices,
+                                  void* const* values, void* workspace, size_t workspace_bytes, int64_t* counts_out,
+                                  void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    const int H = num_hops;
+    GRWS_CHECK_ARG(num_nodes >= 0 && nnz >= 0 && num_seeds >= 0, "sample_blocks: negative size");
+    GRWS_CHECK_ARG(num_nodes <= INT32_MAX, "sample_blocks: ids exceed int32 local ids");
+    GRWS_CHECK_ARG(H >= 1 && H <= kMaxHops, "sample_blocks: num_hops must be in [1, %d]", kMaxHops);
+    GRWS_CHECK_ARG(fanouts && counts_out, "sample_blocks: null pointer");
+    GRWS_CHECK_ARG(tile_cols == 8 || tile_cols == 16, "sample_blocks: tile_cols must be 8 or 16");
+    if (values_dtype != GRWS_F32 && values_dtype != GRWS_F16 && values_dtype != GRWS_BF16)
+        return set_error(GRWS_E_DTYPE, "sample_blocks: unsupported values dtype %d", values_dtype);
+    for (int h = 0; h < H; ++h)
+        GRWS_CHECK_ARG(fanouts[h] >= 1 && fanouts[h] <= kWave, "sample_blocks: fanout %d outside [1, 64]", fanouts[h]);
+    const HopCaps c = hop_caps(num_seeds, fanouts, H, tile_cols, num_nodes);
+    GRWS_CHECK_ARG(c.F[H] <= INT32_MAX, "sample_blocks: a hop could exceed int32 local ids");
+    for (int h = 0; h < 3 * H; ++h) counts_out[h] = 0;
+    if (num_seeds == 0) {
+        for (int h = 0; h < H; ++h) GRWS_TRY(fill_i64(window_offset[h], 1, 0, stream));
+        return GRWS_OK;
+    }
+    GRWS_CHECK_ARG(indptr && seeds && node_map && state && next_frontier && window_offset && col_indices && values,
+                   "sample_blocks: null pointer");
+    for (int h = 0; h < H; ++h)
+        GRWS_CHECK_ARG(next_frontier[h] && window_offset[h] && col_indices[h] && values[h],
+                       "sample_blocks: null output of hop %d", h);
+    if (nnz > 0) GRWS_CHECK_ARG(indices != nullptr, "sample_blocks: null indices");
+    GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(state) % 16 == 0, "sample_blocks: state not 16-byte aligned");
+    Carver cv(workspace, workspace_bytes);
+    BatchWs w;
+    carve_batch(cv, c, H, num_nodes, &w);
+    if (!cv.ok) return set_error(GRWS_E_CAPACITY, "sample_blocks: workspace too small (%zu < %zu)", workspace_bytes,
+                                 cv.used);
+    const StateLayout l = state_layout(num_nodes);
+    uint32_t* bitmap = state;
+    int32_t* grpcnt = reinterpret_cast<int32_t*>(state + l.grp_off);
+    BatchCtr* ctr = reinterpret_cast<BatchCtr*>(state + l.ctr_off);
+    const int tc = tile_cols;
+    for (int h = 0; h < H; ++h) {
+        const int k = fanouts[h];
+        const int64_t Fc = c.F[h], Wc = c.W[h];
+        const int64_t* fr = h == 0 ? seeds : next_frontier[h - 1];
+        hipLaunchKernelGGL(mh_count_kernel, dim3(grid_for(Fc)), dim3(kBlk), 0, stream, indptr, nnz, num_nodes, fr,
+                           num_seeds, h, k, node_map, ctr);
+        GRWS_LAUNCH_CHECK();
+        hipLaunchKernelGGL(mh_sample_kernel, dim3(grid_for(Fc, kWavesPerBlock)), dim3(kBlk), 0, stream, indptr,
+                           indices, nnz, num_nodes, fr, num_seeds, h, k, seed, node_map, bitmap, grpcnt, w.edge_src,
+                           w.edge_val, ctr);
+        GRWS_LAUNCH_CHECK();
+        const int64_t nslices = (l.groups + kSliceGroups - 1) / kSliceGroups;
+        hipLaunchKernelGGL(mh_group_scan_kernel, dim3((unsigned)nslices), dim3(kBlk), 0, stream, grpcnt, l.groups,
+                           w.grpoff, w.slicesum, w.sliceoff, nslices, num_seeds, h, ctr);
+        GRWS_LAUNCH_CHECK();
+        hipLaunchKernelGGL(mh_assign_kernel, dim3(grid_for(c.E[h])), dim3(kBlk), 0, stream, fr, num_seeds, h, k,
+                           num_nodes, w.edge_src, node_map, bitmap, w.grpoff, w.sliceoff, w.src_local,
+                           next_frontier[h], ctr);
+        GRWS_LAUNCH_CHECK();
+#define GRWS_MH_WINDOWS(FILL, VT)                                                                                  \
+    hipLaunchKernelGGL(mh_window_kernel<VT>, dim3((unsigned)Wc), dim3(kBlk), 0, stream, FILL, fr, num_seeds, h, k,    \
+                       w.src_local, w.edge_src, w.edge_val, tc, w.wtiles, Wc, window_offset[h], col_indices[h],       \
+                       static_cast<VT*>(values[h]), num_nodes, node_map, bitmap, grpcnt, ctr)
+        if (values_dtype == GRWS_F32) GRWS_MH_WINDOWS(0, float);
+        else if (values_dtype == GRWS_F16) GRWS_MH_WINDOWS(0, _Float16);
+        else GRWS_MH_WINDOWS(0, __hip_bfloat16);
+        GRWS_LAUNCH_CHECK();
+        GRWS_TRY(scan_i32_to_i64(w.wtiles, window_offset[h], Wc, false, w.scan_ws, w.scan_bytes, stream));
+        if (values_dtype == GRWS_F32) GRWS_MH_WINDOWS(1, float);
+        else if (values_dtype == GRWS_F16) GRWS_MH_WINDOWS(1, _Float16);
+        else GRWS_MH_WINDOWS(1, __hip_bfloat16);
+#undef GRWS_MH_WINDOWS
+        GRWS_LAUNCH_CHECK();
+    }
+    hipLaunchKernelGGL(mh_finish_kernel, dim3(1), dim3(64), 0, stream, ctr, w.out, H);
+    GRWS_LAUNCH_CHECK();
+    int64_t h_out[3 * kMaxHops + 4];
+    GRWS_HIP(hipMemcpyAsync(h_out, w.out, sizeof(int64_t) * (3 * H + 2), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipStreamSynchronize(stream));
+    GRWS_TRY(report((int32_t)h_out[3 * H + 1], "sample_blocks"));
+    for (int h = 0; h < H; ++h) {
+        counts_out[3 * h + 0] = h_out[H + 1 + h];  // edges
+        counts_out[3 * h + 1] = h_out[h + 1];      // sources (next frontier size)
+        counts_out[3 * h + 2] = h_out[2 * H + 1 + h];  // tiles
+    }
     return GRWS_OK;
 }

@@ -12,13 +12,16 @@ the first columns ("target-top", layers/layer.py:159-161), so a layer's
 self path is ``features[:num_rows]``.
 
 Per hop, on the device (csrc/sample.hip, csrc/bcsr_build.hip):
-  1. grws_sample_hop  -- min(deg, k) distinct neighbours per frontier node,
-                         Floyd over Philox4x32-10(seed, node, draw);
-  2. grws_relabel     -- frontier keeps [0, F), new sources appended in
-                         ascending global id; the next frontier;
-  3. BCSR build       -- rows = destination positions, columns = source
-                         local ids, values 1/sqrt((deg_u+1)(deg_v+1)) from
-                         full-graph out-degrees.
+  1. sampling  -- min(deg, k) distinct neighbours per frontier node, Floyd
+                  over Philox4x32-10(seed, node, draw);
+  2. relabel   -- frontier keeps [0, F), new sources appended in ascending
+                  global id; the next frontier;
+  3. BCSR      -- rows = destination positions, columns = source local ids,
+                  values 1/sqrt((deg_u+1)(deg_v+1)) from full-graph
+                  out-degrees.
+The fused path runs every hop of the batch in one grws_sample_blocks call
+with one stream sync; fused=False runs grws_sample_hop, grws_relabel and the
+COO build per hop.
 """
 from __future__ import annotations
 
@@ -28,7 +31,7 @@ from typing import List, Sequence
 import torch
 
 from ..core import relabel, sample_hop
-from ..core.ops import SampleState, sample_block
+from ..core.ops import SampleState, sample_blocks
 from ..data import BCSRGraph
 
 
@@ -62,8 +65,9 @@ class NeighborSampler:
         self.last_stats: dict = {}
         self.total_edges = 0
         self.total_batches = 0
-        # fused: one grws_sample_block call per hop (dense relabel state kept
-        # per graph); otherwise sample_hop + relabel + COO build
+        # fused: the whole batch in one grws_sample_blocks call (dense relabel
+        # state kept per graph, one sync); otherwise sample_hop + relabel +
+        # COO build per hop
         self.fused = bool(fused)
         self._state = None
 
@@ -85,11 +89,13 @@ class NeighborSampler:
         if self.fused and (self._state is None or self._state.num_nodes != num_nodes
                            or self._state.node_map.device != dev):
             self._state = SampleState(num_nodes, dev)
-        for k in reversed(self.fanouts):
+        hop_fanouts = list(reversed(self.fanouts))
+        batch = (sample_blocks(indptr, indices, frontier, hop_fanouts, self._state, seed=self.seed,
+                               tile_cols=self.tile_cols, values_dtype=self.values_dtype)
+                 if self.fused else None)
+        for h, k in enumerate(hop_fanouts):
             if self.fused:
-                win, cols, vals, nxt, E = sample_block(indptr, indices, frontier, k, self._state,
-                                                       seed=self.seed, tile_cols=self.tile_cols,
-                                                       values_dtype=self.values_dtype)
+                win, cols, vals, nxt, E = batch[h]
             else:
                 dst, src, val = sample_hop(indptr, indices, frontier, k, seed=self.seed)
                 src_local, nxt = relabel(frontier, src, num_nodes)

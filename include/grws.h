@@ -352,6 +352,43 @@ int grws_sample_hop(const int64_t* indptr, const int32_t* indices, int64_t num_n
 /* grws_sample_block_capacity.  counts_out[3] = {edges, sources, tiles}.     */
 /* Synchronises `stream`.                                                    */
 /* ------------------------------------------------------------------------ */
+/* ------------------------------------------------------------------------ */
+/* A whole mini-batch in one call: every hop of grws_sample_block, hop h      */
+/* from the previous hop's sources, with a single synchronisation at the     */
+/* end.  Takes the place of the reference's per-hop loop with a host sync    */
+/* per hop (sampling_wrapper.cu:365-438, the sync at :340-344) for the       */
+/* node-wise path; BCSRSampler.sample_layers (sampler/sampler.py:186-279)    */
+/* passes the fanouts in hop order (reversed, sampler.py:204).  Results are   */
+/* those of num_hops grws_sample_block calls, bit for bit.                   */
+/*                                                                          */
+/* State: node_map int32 [num_nodes] (all -1) and state uint32               */
+/* [grws_sample_blocks_state_words(num_nodes)] (all 0), both set up by       */
+/* grws_sample_blocks_state_init and left so by every call; the first        */
+/* ceil(num_nodes/32) words of state are the bitmap grws_sample_block and    */
+/* grws_repack_* take.  Calls sharing one state must not overlap.            */
+/*                                                                          */
+/* Outputs per hop h (device pointers in host arrays of num_hops entries):   */
+/* next_frontier[h] int64 [max_src[h]], window_offset[h] int64              */
+/* [ceil(F_h/16)+1 <= ceil(cap/16)+1, see below], col_indices[h] int32       */
+/* [max_tiles[h]*tile_cols], values[h] [max_tiles[h]*16*tile_cols], with     */
+/* max_src/max_tiles from grws_sample_blocks_capacity; window_offset[h]      */
+/* needs ceil(F_cap_h/16)+1 entries where F_cap_0 = num_seeds and            */
+/* F_cap_h = max_src[h-1].  counts_out[3*h .. 3*h+2] = {edges, sources,      */
+/* tiles} of hop h.  num_hops in [1, 8], fanouts in [1, 64].                 */
+/* ------------------------------------------------------------------------ */
+size_t grws_sample_blocks_state_words(int64_t num_nodes);
+int grws_sample_blocks_state_init(int32_t* node_map, uint32_t* state, int64_t num_nodes, void* stream);
+int grws_sample_blocks_capacity(int64_t num_seeds, const int32_t* fanouts, int32_t num_hops, int32_t tile_cols,
+                                int64_t num_nodes, int64_t* max_src, int64_t* max_tiles);
+size_t grws_sample_blocks_workspace_bytes(int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
+                                          int32_t tile_cols, int64_t num_nodes);
+int grws_sample_blocks(const int64_t* indptr, const int32_t* indices, int64_t num_nodes, int64_t nnz,
+                       const int64_t* seeds, int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
+                       uint64_t seed, int32_t* node_map, uint32_t* state, int32_t tile_cols, int32_t values_dtype,
+                       int64_t* const* next_frontier, int64_t* const* window_offset, int32_t* const* col_indices,
+                       void* const* values, void* workspace, size_t workspace_bytes, int64_t* counts_out,
+                       void* stream);
+
 int grws_sample_state_init(int32_t* node_map, uint32_t* bitmap, int64_t num_nodes, void* stream);
 size_t grws_sample_block_workspace_bytes(int64_t num_frontier, int32_t fanout, int64_t num_nodes);
 int grws_sample_block_capacity(int64_t num_frontier, int32_t fanout, int32_t tile_cols,

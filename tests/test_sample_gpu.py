@@ -161,3 +161,57 @@ def test_neighbor_sampler_c5_batch_shape(cuda_device):
         assert got.sum() == b.num_tiles
         want = np.minimum(deg[dnodes], b.fanout).sum()
         assert b.num_sampled_edges == want
+
+
+@pytest.mark.parametrize("hops,tc", [([5, 10, 15], 16), ([5, 10, 15], 8), ([64, 1], 16), ([2] * 8, 16),
+                                     ([1], 16)])
+def test_sample_blocks_one_call_bit_exact(cuda_device, hops, tc):
+    """grws_sample_blocks (every hop of the batch in one call, fanouts in hop
+    order): each hop equal, bit for bit, to the oracle's; the dense state is
+    all -1 / all 0 afterwards; zero-degree and hub nodes included."""
+    from graph_rws_amd.core.ops import SampleState, sample_blocks
+    degs = np.random.default_rng(16).integers(0, 40, 6000)
+    degs[::97] = 0
+    degs[5] = 3000
+    ip, ix, ipd, ixd = _csr(degs, 6000, 17, cuda_device)
+    st = SampleState(6000, cuda_device)
+    seeds = np.random.default_rng(18).choice(6000, 300, replace=False).astype(np.int64)
+    seeds[0] = 5
+    out = sample_blocks(ipd, ixd, torch.from_numpy(seeds).to(cuda_device), hops, st, seed=42, tile_cols=tc)
+    ref = oracle.sample_blocks(ip, ix, seeds, list(reversed(hops)), seed=42, tile_cols=tc)[::-1]
+    assert len(out) == len(ref) == len(hops)
+    for h, ((win, cols, vals, nxt, E), r) in enumerate(zip(out, ref)):
+        np.testing.assert_array_equal(nxt.cpu().numpy(), r["src_nodes"], err_msg=f"hop {h}")
+        np.testing.assert_array_equal(win.cpu().numpy(), r["win"], err_msg=f"hop {h}")
+        np.testing.assert_array_equal(cols.cpu().numpy(), r["cols"], err_msg=f"hop {h}")
+        np.testing.assert_array_equal(vals.cpu().numpy(), r["vals"], err_msg=f"hop {h}")
+        assert E == r["dst"].size
+    assert bool((st.node_map == -1).all()) and bool((st.bitmap == 0).all())
+    # the same state serves the next batch (and the per-hop entry point)
+    out2 = sample_blocks(ipd, ixd, torch.from_numpy(seeds[::-1].copy()).to(cuda_device), hops, st, tile_cols=tc)
+    ref2 = oracle.sample_blocks(ip, ix, seeds[::-1].copy(), list(reversed(hops)), tile_cols=tc)[::-1]
+    for (win, cols, vals, nxt, E), r in zip(out2, ref2):
+        np.testing.assert_array_equal(cols.cpu().numpy(), r["cols"])
+        np.testing.assert_array_equal(nxt.cpu().numpy(), r["src_nodes"])
+
+
+def test_sample_blocks_errors_leave_state_clean(cuda_device):
+    """Duplicate or out-of-range seeds are reported after the batch (the
+    kernels skip them); the state is restored, and the empty batch is a
+    no-op."""
+    from graph_rws_amd.core.ops import SampleState, sample_blocks
+    ip, ix, ipd, ixd = _csr([3, 4, 0, 2, 5], 5, 0, cuda_device)
+    st = SampleState(5, cuda_device)
+    with pytest.raises(GrwsError, match="twice"):
+        sample_blocks(ipd, ixd, torch.tensor([1, 3, 1], device=cuda_device), [2, 2], st)
+    assert bool((st.node_map == -1).all()) and bool((st.bitmap == 0).all())
+    with pytest.raises(GrwsError, match="outside"):
+        sample_blocks(ipd, ixd, torch.tensor([0, 11], device=cuda_device), [3], st)
+    assert bool((st.node_map == -1).all()) and bool((st.bitmap == 0).all())
+    out = sample_blocks(ipd, ixd, torch.empty(0, dtype=torch.int64, device=cuda_device), [3, 3], st)
+    for win, cols, vals, nxt, E in out:
+        assert E == 0 and nxt.numel() == 0 and win.cpu().tolist() == [0]
+    bad_ix = torch.tensor([0, 1, 9, 0, 1, 1, 0, 2, 2, 3, 3, 4, 4, 0], dtype=torch.int32, device=cuda_device)
+    with pytest.raises(GrwsError, match="neighbour index"):
+        sample_blocks(ipd, bad_ix, torch.tensor([0, 1], device=cuda_device), [5], st)
+    assert bool((st.node_map == -1).all()) and bool((st.bitmap == 0).all())
