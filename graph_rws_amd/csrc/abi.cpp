@@ -6,7 +6,7 @@
 #include <thread>
 #include <vector>
 
-#include "grws_internal.h"
+#include "grws_host.h"
 
 namespace grws {
 

@@ -5,26 +5,11 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_bf16.h>
 
-#include <cstdint>
-#include <cstdio>
-#include <cstdarg>
-#include <string>
 #include <type_traits>
 
-#include "../../include/grws.h"
+#include "grws_host.h"
 
 namespace grws {
-
-// ---------------------------------------------------------------------------
-// errors
-// ---------------------------------------------------------------------------
-int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-void clear_error();
-
-#define GRWS_CHECK_ARG(cond, ...)                                   \
-    do {                                                            \
-        if (!(cond)) return ::grws::set_error(GRWS_E_INVALID, __VA_ARGS__); \
-    } while (0)
 
 #define GRWS_HIP(call)                                                                   \
     do {                                                                                 \
@@ -40,12 +25,6 @@ void clear_error();
         if (e_ != hipSuccess)                                                            \
             return ::grws::set_error(GRWS_E_HIP, "%s:%d kernel launch: %s", __FILE__, __LINE__, \
                                      hipGetErrorString(e_));                             \
-    } while (0)
-
-#define GRWS_TRY(call)              \
-    do {                            \
-        int s_ = (call);            \
-        if (s_ != GRWS_OK) return s_; \
     } while (0)
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

@@ -44,7 +44,9 @@ from typing import Optional, Tuple
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(HERE, "liboracle.so")
+# GRWS_ORACLE_LIB: another build of grws_oracle.c (the sanitizer build of
+# tests/sanitize/ runs the oracle tests against it)
+_LIB_PATH = os.environ.get("GRWS_ORACLE_LIB", os.path.join(HERE, "liboracle.so"))
 _lib = None
 
 _i64p = ctypes.POINTER(ctypes.c_int64)
