@@ -116,6 +116,9 @@ struct SpmmArgs {
     const void* res;
     int64_t ldr;
     int64_t res_rows;
+    // buffer path, 16-bit X and values, chunks of 64+ columns: gather
+    // 128-byte segments of 8 rows per instruction
+    int32_t narrow;
 };
 
 // Output conversion for the three element types.
@@ -465,8 +468,9 @@ __global__ __launch_bounds__(64 * WPB) void spmm_fwd_kernel(SpmmArgs a) {
 // the MFMA sees exactly the dense tile's operand (bit-identical results).
 // The header rides in the column-index ring, loaded a step before the
 // dependent value read, which so adds no wait of its own.
-template <int XT, bool AF32, int TC, int NBLK, int WPB, int PF, bool PK = false>
-__global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
+template <int XT, bool AF32, int TC, int NBLK, int WPB, int PF, bool PK = false, bool NR = false>
+__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(NBLK == 20 ? 3 : 1, 8))) void spmm_buf_kernel(
+    SpmmArgs a) {
     static_assert(XT == GRWS_F16 || XT == GRWS_BF16 || (XT == GRWS_F32 && AF32 && !PK),
                   "16-bit X, or fp32 X with fp32 values");
     static_assert(TC == 8 || TC == 16, "tile_cols must be 8 or 16");
@@ -483,13 +487,20 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
     // LDS row pitch (elements).  fp32: the 4 k-groups of a B read (rows
     // 4g + q, g = 0..3) then start 16 banks apart (no conflict)
     constexpr int PITCH = XF32 ? NC + 4 : NC + 16;
-    static_assert(NLD == 1 || NLD == 2 || NLD == 4 || NLD == 8, "rows per lane");
+    static_assert(NR || NLD == 1 || NLD == 2 || NLD == 4 || NLD == 8, "rows per lane");
+    // NR: every gather instruction reads 128-byte segments of 8 slab rows (8
+    // lanes per segment) instead of NC*SZ-byte runs of 64/LPR rows; the same
+    // NLD loads per lane, each lane on 2 rows (rsub, 8 + rsub)
+    static_assert(!NR || (!XF32 && NC % 64 == 0), "narrow segments: 16-bit X, NC a multiple of 64");
+    constexpr int SEGS = NR ? NC / 64 : 1;  // 128-byte segments per staged row
     constexpr int R = PF + 1;
     static_assert(WPB == 1 || WPB * 16 * PITCH * SZ >= 16 * NC * 4, "stage too small to reduce in");
     using ColV = typename std::conditional<
-        NLD == 8, i32x8_t,
-        typename std::conditional<NLD == 4, i32x4_t,
-                                  typename std::conditional<NLD == 2, i32x2_t, int32_t>::type>::type>::type;
+        NR, i32x2_t,
+        typename std::conditional<
+            NLD == 8, i32x8_t,
+            typename std::conditional<NLD == 4, i32x4_t,
+                                      typename std::conditional<NLD == 2, i32x2_t, int32_t>::type>::type>::type>::type;
     using AVec = typename std::conditional<PK, u32x4_t,
                                            typename std::conditional<AF32, float4_t, u32x2_t>::type>::type;
     using HdrV = typename std::conditional<PK, u32x3_t, int>::type;
@@ -567,13 +578,23 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
     const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(PK ? a.pvals : nullptr),
                                                                          (short)0, PK ? (int)a.pv_bytes : 0, 0x00020000);
 
-    const int rbase = NLD * (lane / LPR);  // first of the lane's slab rows
-    const bool lrow = rbase < 16;          // NBLK == 1: lanes 32..63 stage nothing
+    const int rbase = NR ? (lane >> 3) : NLD * (lane / LPR);  // the lane's first slab row
+    const bool lrow = NR || rbase < 16;   // NBLK == 1: lanes 32..63 stage nothing
     // a lane whose columns lie past n_cols (the last chunk) reads nothing:
     // it always takes row x_rows, which lies past the resource (so every
-    // offset stays below (x_rows + 1) rows)
-    const bool lcol = n0 + (lane % LPR) * VEC < a.n_cols;
-    const uint32_t colb = lcol ? (uint32_t)((n0 + (lane % LPR) * VEC) * SZ) : 0u;
+    // offset stays below (x_rows + 1) rows).  Column element of load i:
+    // (lane % LPR) * VEC, or with NR 64 (i % SEGS) + 8 (lane % 8)
+    int lce[SEGS];
+    bool lcol[SEGS];
+    uint32_t colb[SEGS];
+#pragma unroll
+    for (int g = 0; g < SEGS; ++g) {
+        lce[g] = NR ? 64 * g + 8 * (lane & 7) : (lane % LPR) * VEC;
+        lcol[g] = n0 + lce[g] < a.n_cols;
+        colb[g] = lcol[g] ? (uint32_t)((n0 + lce[g]) * SZ) : 0u;
+    }
+    // slab row of the lane's load i
+    auto row_of = [&](int i) { return NR ? 8 * (i / SEGS) + rbase : rbase + i; };
     const uint32_t ldxb = (uint32_t)(a.ldx * SZ);
     const uint32_t xr = (uint32_t)a.x_rows;
     const int ag = lane >> 4;
@@ -588,7 +609,10 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
 
     auto load_cols = [&](int64_t s) -> ColV {
         const uint32_t off = (uint32_t)((s - sb) * 64) + (uint32_t)rbase * 4;
-        if constexpr (NLD == 8) {
+        if constexpr (NR) {
+            return ColV{(int32_t)__builtin_amdgcn_raw_buffer_load_b32(rsC, (int)off, 0, 2),
+                        (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rsC, (int)(off + 32), 0, 2)};
+        } else if constexpr (NLD == 8) {
             const u32x4_t lo = __builtin_amdgcn_raw_buffer_load_b128(rsC, (int)off, 0, 2);
             const u32x4_t hi = __builtin_amdgcn_raw_buffer_load_b128(rsC, (int)(off + 16), 0, 2);
             return ColV{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
@@ -604,11 +628,11 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
             int32_t c;
-            if constexpr (NLD == 1) c = cv; else c = cv[i];
-            bool ok = lrow && lcol && (uint32_t)c < xr;
-            if constexpr (TC == 8) ok = ok && (s * 16 + rbase + i < nslots);  // half-empty last slab
+            if constexpr (NR) c = cv[i / SEGS]; else if constexpr (NLD == 1) c = cv; else c = cv[i];
+            bool ok = lrow && lcol[i % SEGS] && (uint32_t)c < xr;
+            if constexpr (TC == 8) ok = ok && (s * 16 + row_of(i) < nslots);  // half-empty last slab
             const uint32_t row = ok ? (uint32_t)c : xr;  // row x_rows lies past the resource
-            regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rsX, (int)(__umul24(row, ldxb) + colb), 0, 0);
+            regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rsX, (int)(__umul24(row, ldxb) + colb[i % SEGS]), 0, 0);
         }
     };
     auto load_hdr = [&](int64_t s) -> HdrV {
@@ -648,7 +672,7 @@ __global__ __launch_bounds__(64 * WPB) void spmm_buf_kernel(SpmmArgs a) {
         if (lrow) {
 #pragma unroll
             for (int i = 0; i < NLD; ++i)
-                *reinterpret_cast<u32x4_t*>(&stage[(rbase + i) * PITCH + (lane % LPR) * VEC]) = xb[i];
+                *reinterpret_cast<u32x4_t*>(&stage[row_of(i) * PITCH + lce[i % SEGS]]) = xb[i];
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -928,10 +952,22 @@ int launch_buf(const SpmmArgs& a, hipStream_t stream) {
     const int64_t total = a.num_items * a.nchunks;
     const int64_t grid = a.chunk_major ? ((a.num_items + 7) / 8) * 8 * a.nchunks : ((total + 7) / 8) * 8;
     if (grid > INT32_MAX) return set_error(GRWS_E_INVALID, "spmm: too many work items (%lld)", (long long)total);
-    hipLaunchKernelGGL((spmm_buf_kernel<XT, AF32, TC, NBLK, WPB, 1, PK>), dim3((unsigned)grid), dim3(64 * WPB), 0,
-                       stream, a);
-    GRWS_LAUNCH_CHECK();
-    return GRWS_OK;
+    if constexpr (XT != GRWS_F32 && !AF32 && NBLK >= 4) {
+        if (a.narrow || NBLK == 20) {
+            hipLaunchKernelGGL((spmm_buf_kernel<XT, AF32, TC, NBLK, WPB, 1, PK, true>), dim3((unsigned)grid),
+                               dim3(64 * WPB), 0, stream, a);
+            GRWS_LAUNCH_CHECK();
+            return GRWS_OK;
+        }
+    }
+    if constexpr (NBLK == 20) {  // 320-column chunks exist on the narrow path only
+        return set_error(GRWS_E_INVALID, "spmm: 320-column chunks need 16-bit X and values");
+    } else {
+        hipLaunchKernelGGL((spmm_buf_kernel<XT, AF32, TC, NBLK, WPB, 1, PK>), dim3((unsigned)grid), dim3(64 * WPB),
+                           0, stream, a);
+        GRWS_LAUNCH_CHECK();
+        return GRWS_OK;
+    }
 }
 
 template <int XT, bool AF32, int TC, bool PK>
@@ -944,6 +980,11 @@ int dispatch_buf(const SpmmArgs& a, int nblk, hipStream_t stream) {
             return two ? launch_buf<XT, AF32, TC, 2, 2, PK>(a, stream) : launch_buf<XT, AF32, TC, 2, 1, PK>(a, stream);
         case 4:
             return two ? launch_buf<XT, AF32, TC, 4, 2, PK>(a, stream) : launch_buf<XT, AF32, TC, 4, 1, PK>(a, stream);
+        case 20:
+            if constexpr (XT != GRWS_F32 && !AF32)
+                return two ? launch_buf<XT, AF32, TC, 20, 2, PK>(a, stream)
+                           : launch_buf<XT, AF32, TC, 20, 1, PK>(a, stream);
+            return set_error(GRWS_E_INVALID, "spmm: 320-column chunks need 16-bit X and values");
         case 16:
             if constexpr (XT != GRWS_F32)  // fp32 chunks stop at 128 columns
                 return two ? launch_buf<XT, AF32, TC, 16, 2, PK>(a, stream)
@@ -1008,6 +1049,11 @@ int launch_fixup(const grws_spmm_plan* plan, const SpmmArgs& a, int nblk, hipStr
             break;
         case 16:
             hipLaunchKernelGGL((spmm_fixup_kernel<XT, 16>), dim3((unsigned)grid), dim3(64), 0, stream, plan->split,
+                               plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base,
+                               a.res, a.ldr, a.res_rows);
+            break;
+        case 20:
+            hipLaunchKernelGGL((spmm_fixup_kernel<XT, 20>), dim3((unsigned)grid), dim3(64), 0, stream, plan->split,
                                plan->num_split, a.partials, a.nchunks, a.y, a.ldy, a.n_cols, a.col_base,
                                a.res, a.ldr, a.res_rows);
             break;
@@ -1189,8 +1235,9 @@ extern "C" int grws_spmm_plan_build(const int64_t* window_offset, int64_t num_wi
 
 extern "C" size_t grws_spmm_workspace_bytes(const grws_spmm_plan* plan, int64_t n_cols) {
     if (!plan || plan->num_slots <= 0 || n_cols <= 0) return 0;
-    // every chunk width divides 256, so this covers whichever width runs
-    const int64_t padded = (n_cols + 255) / 256 * 256;
+    // chunk widths divide 256 or are 320: this covers whichever runs
+    const int64_t p256 = (n_cols + 255) / 256 * 256, p320 = (n_cols + 319) / 320 * 320;
+    const int64_t padded = p256 > p320 ? p256 : p320;
     return (size_t)plan->num_slots * 16 * (size_t)padded * sizeof(float);
 }
 
@@ -1284,6 +1331,8 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
         a.x_bytes = (uint32_t)((x_rows - 1) * ldx * (int64_t)esz + n_cols * (int64_t)esz);
         a.chunk_major = 1;
         if (const char* e = getenv("GRWS_SPMM_ORDER")) a.chunk_major = atoi(e) == 1;  // tuning override
+        a.narrow = 1;  // 128-byte segments of 8 rows per gather where the kernel has them
+        if (const char* e = getenv("GRWS_SPMM_NARROW")) a.narrow = atoi(e) == 1;      // tuning override
         if (P && A->num_tiles > 0) {  // the element-masked kernel below reads the dense values
             a.hdr = P->header;
             a.pvals = P->values;
@@ -1295,6 +1344,21 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
         // whole multiples, then one narrower launch for the rest, so A is
         // streamed once per 256 columns and no chunk is mostly empty
         const bool forced = getenv("GRWS_SPMM_NBLK") != nullptr;
+        // 320-column chunks (narrow path) when they stream A fewer times than
+        // 256-column chunks plus a narrower rest (N = 608: 2 passes, not 3)
+        if (!forced && !af32 && x_dtype != GRWS_F32 && n_cols > 256 && n_cols % 256 != 0 &&
+            x_rows * 320 * (int64_t)esz <= ((int64_t)256 << 20) && (n_cols + 319) / 320 < (n_cols + 255) / 256 &&
+            (x_rows + 1) * ldx * (int64_t)esz + 320 * (int64_t)esz < ((int64_t)1 << 32) &&
+            !(getenv("GRWS_SPMM_C320") && atoi(getenv("GRWS_SPMM_C320")) == 0)) {
+            a.col_base = 0;
+            a.nchunks = (int32_t)((n_cols + 319) / 320);
+            st = x_dtype == GRWS_F16 ? dispatch_buf_tc<GRWS_F16, false>(a, tc, 20, stream)
+                                     : dispatch_buf_tc<GRWS_BF16, false>(a, tc, 20, stream);
+            if (st == GRWS_OK && plan && plan->num_split > 0)
+                st = x_dtype == GRWS_F16 ? launch_fixup<GRWS_F16>(plan, a, 20, stream)
+                                         : launch_fixup<GRWS_BF16>(plan, a, 20, stream);
+            return st;
+        }
         const int64_t head =
             (!forced && wide_chunks(x_rows, x_dtype) && n_cols > 256 && n_cols % 256 != 0) ? n_cols / 256 * 256 : 0;
         const int64_t parts[2][2] = {{0, head > 0 ? head : n_cols}, {head, n_cols}};
