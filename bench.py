@@ -467,9 +467,13 @@ def bench_minibatch(dev, batches: int, warmup: int) -> dict:
     ([15,10,5], Philox seed 42), the input features gathered from the
     111M x 128 fp16 matrix in HBM, then a 3-layer GCN_BCSR step (hidden 256,
     172 classes, fp16 autocast, CE loss, clip, Adam), sampling pipelined one
-    batch ahead on a side stream (train_epoch_node_sampling)."""
+    batch ahead on a side stream (train_epoch_node_sampling).  Timed twice
+    on the same seeds: the eager step, and the step replayed from HIP graphs
+    captured per bucket of batch shapes (GraphedBlockStep).  A third,
+    untimed pass times each forward SpMM with events (the SpMM column)."""
     from graph_rws_amd import synth
-    from graph_rws_amd.helper import EpochTimer, train_epoch_node_sampling
+    from graph_rws_amd.core import ops as _ops
+    from graph_rws_amd.helper import EpochTimer, GraphedBlockStep, train_epoch_node_sampling
     from graph_rws_amd.models import GCN_BCSR
     from graph_rws_amd.sampler import NeighborSampler
     c = synth.C5
@@ -483,11 +487,12 @@ def bench_minibatch(dev, batches: int, warmup: int) -> dict:
     t_gen = time.time() - t0
     torch.manual_seed(33)
     model = GCN_BCSR(c["feat"], 256, c["classes"], 3, dropout=0.5, use_checkpoint=False).to(dev)
-    opt = torch.optim.Adam(model.parameters(), lr=0.003)
+    opt = torch.optim.Adam(model.parameters(), lr=0.003, capturable=True)
     sampler = NeighborSampler(c["fanouts"], seed=c["philox_seed"], tile_cols=16,
                               values_dtype=torch.float16)
+    graphed = GraphedBlockStep(model, opt, dev, autocast_dtype=torch.float16)
 
-    def run(nb, seed):
+    def run(nb, seed, step=None):
         idx = synth.distinct_seeds(g.num_nodes, c["batch"] * nb, seed=seed, device=dev).cpu()
         timer = EpochTimer()
         e0, b0 = sampler.total_edges, sampler.total_batches
@@ -495,24 +500,45 @@ def bench_minibatch(dev, batches: int, warmup: int) -> dict:
         t = time.perf_counter()
         with torch.autocast("cuda", dtype=torch.float16):
             loss, _ = train_epoch_node_sampling(model, g, X, labels, idx, opt, dev, sampler,
-                                                batch_size=c["batch"], timer=timer, pipeline=True)
+                                                batch_size=c["batch"], timer=timer, pipeline=True,
+                                                graphed=step)
         torch.cuda.synchronize(dev)
         return (time.perf_counter() - t, sampler.total_edges - e0, sampler.total_batches - b0,
                 loss, timer.get_epoch_stats())
 
     # warm-up epochs on other seed sets: GEMM kernels for the batch shapes
-    # seen load lazily (a one-off stall of tens of ms on first use)
+    # seen load lazily (a one-off stall of tens of ms on first use), and the
+    # graphed step captures the buckets these shapes fall in
     for e in range(2):
         run(warmup, 40 + e)
     wall, edges, nb, loss, stats = run(batches, 42)
+    for e in range(3):
+        run(warmup, 50 + e, graphed)
+    cap0 = graphed.captures
+    g_wall, g_edges, g_nb, g_loss, g_stats = run(batches, 42, graphed)
+    g_caps = graphed.captures - cap0
+    # the SpMM column: each forward SpMM timed with events (a sync per call)
+    _ops.TIMING = True
+    try:
+        _, _, _, _, t_stats = run(min(batches, 10), 43)
+    finally:
+        _ops.TIMING = False
     out = {"workload": "c5 mini-batch GCN step (sample + feature gather + fwd/bwd/Adam), pipelined",
            "graph": {"nodes": g.num_nodes, "edges": g.nnz}, "features": [g.num_nodes, c["feat"], "f16"],
-           "batches": nb, "warmup": f"2 epochs x {warmup} batches", "batch_ms": round(1e3 * wall / nb, 3),
-           "sampled_edges_per_s_in_training": round(edges / wall, 1),
-           "edges_per_batch": round(edges / nb, 1), "final_loss": round(float(loss), 4),
-           "stage_ms_per_batch": {k: round(v, 3) for k, v in stats.items()},
+           "batches": g_nb, "warmup": f"2 eager + 3 graphed epochs x {warmup} batches",
+           "batch_ms": round(1e3 * g_wall / g_nb, 3), "step": "replayed from HIP graphs (GraphedBlockStep)",
+           "sampled_edges_per_s_in_training": round(g_edges / g_wall, 1),
+           "edges_per_batch": round(g_edges / g_nb, 1), "final_loss": round(float(g_loss), 4),
+           "stage_ms_per_batch": {k: round(v, 3) for k, v in g_stats.items() if k != "SpMM"},
+           "buckets_captured": graphed.captures, "captures_in_timed_epoch": g_caps,
+           "eager": {"batch_ms": round(1e3 * wall / nb, 3), "final_loss": round(float(loss), 4),
+                     "sampled_edges_per_s_in_training": round(edges / wall, 1),
+                     "stage_ms_per_batch": {k: round(v, 3) for k, v in stats.items() if k != "SpMM"}},
+           "spmm_fwd_ms_per_call": round(t_stats["SpMM"], 4),
+           "spmm_note": "SpMM: mean event-timed ms of one forward block SpMM, from a separate eager pass "
+                        "of 10 batches with a sync per call (3 per batch); the timed epochs do not sync",
            "generate_s": round(t_gen, 2)}
-    del g, X, labels, model, opt
+    del g, X, labels, model, opt, graphed
     torch.cuda.empty_cache()
     return out
 

@@ -238,7 +238,12 @@ class BCSRGraph:
         """Cached SpMM schedule for outputs of width n_cols, or None when no
         window can exceed the per-item slab budget (``max_window_slabs``
         known, e.g. for sampled blocks): then one work item per window is the
-        schedule and no plan needs building."""
+        schedule and no plan needs building.  A graph whose arrays are
+        refilled in place between replays of a captured step
+        (``refilled = True``) never takes a plan: its windows change under
+        the plan."""
+        if getattr(self, "refilled", False):
+            return None
         slabs = default_slabs(self.num_windows, self.num_tiles, self.tile_cols, n_cols)
         mws = getattr(self, "max_window_slabs", None)
         if mws is not None and mws <= slabs:
@@ -259,7 +264,7 @@ class BCSRGraph:
         the dense values twice, so it pays only from the second product on.
         None when packing is off or does not apply."""
         from ..core import ops as _ops
-        if not _ops.PACK_TILES or self.tile_cols != 16:
+        if not _ops.PACK_TILES or self.tile_cols != 16 or getattr(self, "refilled", False):
             return None
         from ..core.ops import TensorKey
         v, c = self.values_condensed, self.original_col_indices

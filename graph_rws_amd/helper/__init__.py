@@ -12,4 +12,4 @@ from .engine import (  # noqa: F401
     train_epoch_full,
     train_epoch_node_sampling,
 )
-from .graphed import GraphedFullStep  # noqa: F401
+from .graphed import GraphedBlockStep, GraphedFullStep, bucket_rows  # noqa: F401

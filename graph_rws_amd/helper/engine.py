@@ -179,7 +179,7 @@ def train_epoch_node_sampling(model, graphs_for_model, features: torch.Tensor,
                               labels: torch.Tensor, train_idx: torch.Tensor,
                               optimizer: torch.optim.Optimizer, device, sampler,
                               batch_size: int = 1024, tile_rows: int = 16, timer=None,
-                              pipeline: bool = True, max_batches: int = 0):
+                              pipeline: bool = True, max_batches: int = 0, graphed=None):
     """One epoch of mini-batch training (engine.py:86-256).  Returns
     (average loss, accuracy).
 
@@ -188,7 +188,11 @@ def train_epoch_node_sampling(model, graphs_for_model, features: torch.Tensor,
     (engine.py:112-203).  Streams keep the default priority.
     `sampler` is a BCSRSampler (window top-K, the reference's) with the full
     BCSRGraph, or a NeighborSampler (Philox fanout) with the CSR graph
-    (an object with row_ptr / col_idx).  max_batches > 0 stops early."""
+    (an object with row_ptr / col_idx).  max_batches > 0 stops early.
+    graphed: a GraphedBlockStep over the same model and optimizer, which
+    replays each batch's step from a HIP graph captured per bucket of batch
+    shapes (NeighborSampler blocks only); the timer then records the whole
+    step under "Step"."""
     import queue
     import threading
     from ..data import WindowWiseDataLoader
@@ -206,8 +210,23 @@ def train_epoch_node_sampling(model, graphs_for_model, features: torch.Tensor,
     main = torch.cuda.current_stream(device)
     needs_t = _transpose_needs(model, features)
 
+    if graphed is not None:
+        from ..sampler import NeighborSampler
+        if not isinstance(sampler, NeighborSampler):
+            raise ValueError("graphed steps take the node-wise sampler's blocks (NeighborSampler)")
+
     def step(seeds, subgraphs, feats):
         nonlocal total_samples, num_batches
+        if graphed is not None:
+            loss, correct = graphed(subgraphs, feats, labels[seeds])
+            timer.record("Step")
+            with torch.no_grad():
+                total_loss.add_(loss)
+                total_correct.add_(correct)
+            total_samples += seeds.numel()
+            num_batches += 1
+            timer.end_batch()
+            return
         optimizer.zero_grad()
         logits = model(subgraphs, feats if feats is not None else features)
         timer.record("Fwd")
