@@ -145,6 +145,14 @@ _PROTOS = {
                                           _vp, ctypes.c_int32, ctypes.c_uint64, _vp, _vp, ctypes.c_int32,
                                           ctypes.c_int32, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _c_i64p,
                                           _vp]),
+    "grws_sample_blocks_transposed_capacity": (ctypes.c_int, [ctypes.c_int64, _vp, ctypes.c_int32,
+                                                              ctypes.c_int32, ctypes.c_int64, _c_i64p, _c_i64p]),
+    "grws_sample_blocks_transposed_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, _vp, ctypes.c_int32,
+                                                                        ctypes.c_int32, ctypes.c_int64, _vp]),
+    "grws_sample_blocks_transposed": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp,
+                                                     ctypes.c_int64, _vp, ctypes.c_int32, ctypes.c_uint64, _vp,
+                                                     _vp, ctypes.c_int32, ctypes.c_int32, _vp, _vp, _vp, _vp,
+                                                     _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _c_i64p, _vp]),
     "grws_gemm_tn_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64,
                                                        ctypes.c_int64]),
     "grws_gemm_tn": (ctypes.c_int, [_vp, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int32,

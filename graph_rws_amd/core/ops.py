@@ -779,19 +779,59 @@ def _sample_blocks_sizes(F0: int, fanouts, tile_cols: int, n: int):
     return hit
 
 
+_BLOCKS_T_SIZES: dict = {}
+
+
+def _sample_blocks_t_sizes(F0: int, fanouts, tile_cols: int, n: int, thops):
+    """Transposed-block capacities and the workspace of a batch shape."""
+    key = (F0, tuple(fanouts), tile_cols, n, tuple(thops))
+    hit = _BLOCKS_T_SIZES.get(key)
+    if hit is None:
+        H = len(fanouts)
+        fo = (ctypes.c_int32 * H)(*[int(k) for k in fanouts])
+        th = (ctypes.c_int32 * H)(*[1 if t else 0 for t in thops])
+        mw = (ctypes.c_int64 * H)()
+        mt = (ctypes.c_int64 * H)()
+        L.call("grws_sample_blocks_transposed_capacity", F0, fo, H, int(tile_cols), n,
+               ctypes.cast(mw, ctypes.POINTER(ctypes.c_int64)), ctypes.cast(mt, ctypes.POINTER(ctypes.c_int64)))
+        wsb = int(L.load().grws_sample_blocks_transposed_workspace_bytes(F0, fo, H, int(tile_cols), n, th))
+        hit = (th, [int(x) for x in mw], [int(x) for x in mt], wsb)
+        if len(_BLOCKS_T_SIZES) > 64:
+            _BLOCKS_T_SIZES.clear()
+        _BLOCKS_T_SIZES[key] = hit
+    return hit
+
+
 def sample_blocks(indptr: torch.Tensor, indices: torch.Tensor, seeds: torch.Tensor, fanouts,
                   state: SampleState, seed: int = 42, tile_cols: int = 16,
-                  values_dtype: torch.dtype = torch.float32):
+                  values_dtype: torch.dtype = torch.float32, transposes=None):
     """Every hop of a mini-batch in one call (fanouts in hop order, hop 0 from
     the seeds): per hop (window_offset, col_indices, values, next_frontier,
     num_edges) as sample_block returns them.  One stream sync for the whole
-    batch; outputs are views of buffers sized by the hops' capacities."""
+    batch; outputs are views of buffers sized by the hops' capacities.
+
+    transposes: per hop, whether to build the transpose of its block in the
+    same call (grws_sample_blocks_transposed); each hop's tuple then has a
+    sixth entry, (t_window_offset, t_col_indices, t_values, most tiles in
+    one window) for a transposed hop and None for another."""
     n, nnz = _csr_arrays(indptr, indices)
     dev = indptr.device
     sd = seeds.to(dev, torch.int64).contiguous()
     F0 = sd.numel()
     H = len(fanouts)
     fo, ms, mt, fcap, wsb = _sample_blocks_sizes(F0, fanouts, int(tile_cols), n)
+    thops = None
+    if transposes is not None:
+        if len(transposes) != H:
+            raise ValueError("sample_blocks: one transposes flag per hop")
+        thops = [bool(t) for t in transposes]
+    any_t = bool(thops) and any(thops)
+    tw = tt = [0] * H
+    if any_t:
+        th, tw, tt, wsb = _sample_blocks_t_sizes(F0, fanouts, int(tile_cols), n, thops)
+    tw = [tw[h] if any_t and thops[h] else 0 for h in range(H)]
+    tt = [tt[h] if any_t and thops[h] else 0 for h in range(H)]
+
     # one buffer per element type, carved per hop on 256-byte boundaries
     def layout(sizes, esz):
         offs, o = [], 0
@@ -799,11 +839,13 @@ def sample_blocks(indptr: torch.Tensor, indices: torch.Tensor, seeds: torch.Tens
             offs.append(o)
             o += -(-max(1, k) * esz // 256) * 256 // esz
         return offs, o
-    i64_sizes = [ms[h] for h in range(H)] + [(fcap[h] + 15) // 16 + 1 for h in range(H)]
+    i64_sizes = ([ms[h] for h in range(H)] + [(fcap[h] + 15) // 16 + 1 for h in range(H)]
+                 + [tw[h] + 1 for h in range(H)])
     i64_offs, i64_total = layout(i64_sizes, 8)
-    c_offs, c_total = layout([mt[h] * tile_cols for h in range(H)], 4)
+    c_offs, c_total = layout([mt[h] * tile_cols for h in range(H)] + [tt[h] * tile_cols for h in range(H)], 4)
     esz = torch.empty(0, dtype=values_dtype).element_size()
-    v_offs, v_total = layout([mt[h] * 16 * tile_cols for h in range(H)], esz)
+    v_offs, v_total = layout([mt[h] * 16 * tile_cols for h in range(H)]
+                             + [tt[h] * 16 * tile_cols for h in range(H)], esz)
     b64 = torch.empty(i64_total, dtype=torch.int64, device=dev)
     bc = torch.empty(c_total, dtype=torch.int32, device=dev)
     bv = torch.empty(v_total, dtype=values_dtype, device=dev)
@@ -812,21 +854,38 @@ def sample_blocks(indptr: torch.Tensor, indices: torch.Tensor, seeds: torch.Tens
     win = [b64[i64_offs[H + h]:i64_offs[H + h] + i64_sizes[H + h]] for h in range(H)]
     cols = [bc[c_offs[h]:c_offs[h] + max(1, mt[h] * tile_cols)] for h in range(H)]
     vals = [bv[v_offs[h]:v_offs[h] + max(1, mt[h] * 16 * tile_cols)] for h in range(H)]
+    twin = [b64[i64_offs[2 * H + h]:i64_offs[2 * H + h] + tw[h] + 1] for h in range(H)]
+    tcols = [bc[c_offs[H + h]:c_offs[H + h] + max(1, tt[h] * tile_cols)] for h in range(H)]
+    tvals = [bv[v_offs[H + h]:v_offs[H + h] + max(1, tt[h] * 16 * tile_cols)] for h in range(H)]
 
     def parr(ts):
         return (ctypes.c_void_p * H)(*[t.data_ptr() for t in ts])
 
-    counts = (ctypes.c_int64 * (3 * H))()
-    L.call("grws_sample_blocks", L.ptr(indptr), L.ptr(indices), n, nnz, L.ptr(sd), F0, fo, H,
-           ctypes.c_uint64(int(seed) & 0xFFFFFFFFFFFFFFFF), L.ptr(state.node_map), L.ptr(state.bitmap),
-           int(tile_cols), L.dtype_code(values_dtype), parr(nxt), parr(win), parr(cols), parr(vals), L.ptr(ws),
-           wsb, ctypes.cast(counts, ctypes.POINTER(ctypes.c_int64)), L.stream_of(dev))
+    per = 5 if any_t else 3
+    counts = (ctypes.c_int64 * (per * H))()
+    common = (L.ptr(indptr), L.ptr(indices), n, nnz, L.ptr(sd), F0, fo, H,
+              ctypes.c_uint64(int(seed) & 0xFFFFFFFFFFFFFFFF), L.ptr(state.node_map), L.ptr(state.bitmap),
+              int(tile_cols), L.dtype_code(values_dtype), parr(nxt), parr(win), parr(cols), parr(vals))
+    if any_t:
+        L.call("grws_sample_blocks_transposed", *common, th, parr(twin), parr(tcols), parr(tvals), L.ptr(ws),
+               wsb, ctypes.cast(counts, ctypes.POINTER(ctypes.c_int64)), L.stream_of(dev))
+    else:
+        L.call("grws_sample_blocks", *common, L.ptr(ws), wsb, ctypes.cast(counts, ctypes.POINTER(ctypes.c_int64)),
+               L.stream_of(dev))
     out = []
     F = F0
     for h in range(H):
-        E, S, T = int(counts[3 * h]), int(counts[3 * h + 1]), int(counts[3 * h + 2])
+        E, S, T = int(counts[per * h]), int(counts[per * h + 1]), int(counts[per * h + 2])
         W = (F + 15) // 16
-        out.append((win[h][:W + 1], cols[h][:T * tile_cols], vals[h][:T * 16 * tile_cols], nxt[h][:S], E))
+        hop = (win[h][:W + 1], cols[h][:T * tile_cols], vals[h][:T * 16 * tile_cols], nxt[h][:S], E)
+        if thops is not None:
+            t = None
+            if thops[h]:
+                TT, TM = int(counts[per * h + 3]), int(counts[per * h + 4])
+                Wt = (S + 15) // 16
+                t = (twin[h][:Wt + 1], tcols[h][:TT * tile_cols], tvals[h][:TT * 16 * tile_cols], TM)
+            hop = hop + (t,)
+        out.append(hop)
         F = S
     return out
 

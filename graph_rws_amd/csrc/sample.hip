@@ -553,6 +553,8 @@ struct BatchCtr {
     int64_t F[kMaxHops + 1];  // frontier size of each hop (F[h+1] = sources of hop h)
     int64_t E[kMaxHops];      // sampled edges of each hop
     int64_t T[kMaxHops];      // tiles of each hop's block
+    int64_t TT[kMaxHops];     // tiles of each hop's transposed block
+    int32_t TM[kMaxHops];     // most tiles in one window of the transposed block
     int32_t err;
     uint32_t done;            // work-groups of the group scan that have finished
 };
@@ -868,17 +870,145 @@ __global__ __launch_bounds__(256) void mh_window_kernel(int fill, const int64_t*
     }
 }
 
-// Copies the batch counters out and clears them for the next call.
+// --- transposed blocks -----------------------------------------------------
+// A^T of hop h's block: windows of 16 sources, columns = the hop's frontier
+// rows, the BCSR that a build of the block's transpose makes (every cell of
+// the block with a nonzero value, in a window's distinct rows ascending).
+// Built from the hop's slots without a host sync: a stable radix sort by
+// source window keeps slot order inside a window, so a window's slots come
+// out ordered by frontier row (slot / k) and, within a row, by slot.
+
+__device__ __forceinline__ bool value_nonzero(float v) { return v != 0.0f; }
+__device__ __forceinline__ bool value_nonzero(_Float16 v) { return (float)v != 0.0f; }
+__device__ __forceinline__ bool value_nonzero(__hip_bfloat16 v) { return __bfloat162float(v) != 0.0f; }
+
+// Key of every slot: its source's window, or wcap (after every window) for an
+// empty slot, a slot past the hop's edges, or a value that is zero in VT.
+template <typename VT>
+__global__ __launch_bounds__(kBlk) void mh_tkeys_kernel(int64_t F0, int h, int k, const int32_t* __restrict__ src_local,
+                                                        const float* __restrict__ edge_val, int64_t ecap, int64_t wcap,
+                                                        uint64_t* __restrict__ keys, uint32_t* __restrict__ pay,
+                                                        const BatchCtr* __restrict__ ctr) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= ecap) return;
+    const int64_t F = hop_frontier(ctr, h, F0);
+    uint64_t kk = (uint64_t)wcap;
+    if (e < F * (int64_t)k) {
+        const int32_t c = src_local[e];
+        if (c >= 0 && value_nonzero(cvt_value<VT>(edge_val[e]))) kk = (uint64_t)(c >> 4);
+    }
+    keys[e] = kk;
+    pay[e] = (uint32_t)e;
+}
+
+// First position of a sorted key array holding a key >= x.
+__device__ __forceinline__ int64_t lower_bound_u64(const uint64_t* __restrict__ a, int64_t n, uint64_t x) {
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (a[mid] < x) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// One work-group per transposed window: its distinct frontier rows -> tiles.
+__global__ __launch_bounds__(kBlk) void mh_tcount_kernel(int h, int k, const uint64_t* __restrict__ keys,
+                                                         const uint32_t* __restrict__ pay, int64_t ecap, int tc,
+                                                         int32_t* __restrict__ wtiles, BatchCtr* __restrict__ ctr) {
+    __shared__ int64_t tmp[kBlk / kWave + 1];
+    const int64_t w = blockIdx.x;
+    const int64_t lo = lower_bound_u64(keys, ecap, (uint64_t)w);
+    const int64_t hi = lower_bound_u64(keys, ecap, (uint64_t)w + 1);
+    int64_t distinct = 0;
+    for (int64_t b = lo; b < hi; b += kBlk) {  // uniform over the work-group
+        const int64_t i = b + threadIdx.x;
+        const int f = i < hi && (i == lo || pay[i - 1] / (uint32_t)k != pay[i] / (uint32_t)k) ? 1 : 0;
+        int64_t tot;
+        block_incl_scan<kBlk>(f, tmp, &tot);
+        distinct += tot;
+    }
+    if (threadIdx.x == 0) {
+        const int32_t t = (int32_t)((distinct + tc - 1) / tc);
+        wtiles[w] = t;
+        if (t > 0) atomicMax(&ctr->TM[h], t);
+    }
+}
+
+// One work-group per transposed window: column = frontier row, value at the
+// source's row of the window; of slots repeating a (row, source) pair the
+// last one's value is stored, as in the block.
+template <typename VT>
+__global__ __launch_bounds__(kBlk) void mh_tfill_kernel(int h, int k, const uint64_t* __restrict__ keys,
+                                                        const uint32_t* __restrict__ pay, int64_t ecap, int64_t wcap,
+                                                        int tc, const int32_t* __restrict__ src_local,
+                                                        const float* __restrict__ edge_val,
+                                                        const int64_t* __restrict__ t_win, int32_t* __restrict__ out_cols,
+                                                        void* __restrict__ out_vals_, BatchCtr* __restrict__ ctr) {
+    __shared__ int64_t tmp[kBlk / kWave + 1];
+    VT* __restrict__ out_vals = static_cast<VT*>(out_vals_);
+    const int tid = threadIdx.x;
+    const int64_t w = blockIdx.x;
+    if (w == 0 && tid == 0) ctr->TT[h] = t_win[wcap];
+    const int64_t wo = t_win[w];
+    const int64_t tiles = t_win[w + 1] - wo;
+    if (tiles <= 0) return;  // uniform over the work-group
+    for (int64_t i = tid; i < tiles * tc; i += kBlk) out_cols[wo * tc + i] = -1;
+    for (int64_t i = tid; i < tiles * 16 * tc; i += kBlk) out_vals[wo * 16 * tc + i] = cvt_value<VT>(0.0f);
+    __syncthreads();
+    const int64_t lo = lower_bound_u64(keys, ecap, (uint64_t)w);
+    const int64_t hi = lower_bound_u64(keys, ecap, (uint64_t)w + 1);
+    int64_t run = 0;
+    for (int64_t b = lo; b < hi; b += kBlk) {  // uniform over the work-group
+        const int64_t i = b + tid;
+        const bool v = i < hi;
+        uint32_t e = 0, d = 0;
+        int f = 0;
+        if (v) {
+            e = pay[i];
+            d = e / (uint32_t)k;
+            f = (i == lo || pay[i - 1] / (uint32_t)k != d) ? 1 : 0;
+        }
+        int64_t tot;
+        const int64_t inc = block_incl_scan<kBlk>(f, tmp, &tot);
+        if (v) {
+            const int64_t p = run + inc - 1;  // the row's position among the window's distinct rows
+            const int64_t tile = wo + p / tc;
+            const int col = (int)(p % tc);
+            if (f) out_cols[tile * tc + col] = (int32_t)d;
+            const int32_t c = src_local[e];
+            bool last = true;
+            for (int64_t j = i + 1; j < hi; ++j) {  // the row's later slots in this window (at most k)
+                const uint32_t ej = pay[j];
+                if (ej / (uint32_t)k != d) break;
+                if (src_local[ej] == c) {
+                    last = false;
+                    break;
+                }
+            }
+            if (last) out_vals[(tile * 16 + (c & 15)) * tc + col] = cvt_value<VT>(edge_val[e]);
+        }
+        run += tot;
+    }
+}
+
+// Copies the batch counters out and clears them for the next call:
+// out = F[0..H], E[H], T[H], TT[H], TM[H], err.
 __global__ void mh_finish_kernel(BatchCtr* __restrict__ ctr, int64_t* __restrict__ out, int H) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     for (int h = 0; h <= H; ++h) out[h] = ctr->F[h];
     for (int h = 0; h < H; ++h) {
         out[H + 1 + h] = ctr->E[h];
         out[2 * H + 1 + h] = ctr->T[h];
+        out[3 * H + 1 + h] = ctr->TT[h];
+        out[4 * H + 1 + h] = ctr->TM[h];
     }
-    out[3 * H + 1] = ctr->err;
+    out[5 * H + 1] = ctr->err;
     for (int h = 0; h <= kMaxHops; ++h) ctr->F[h] = 0;
-    for (int h = 0; h < kMaxHops; ++h) ctr->E[h] = ctr->T[h] = 0;
+    for (int h = 0; h < kMaxHops; ++h) {
+        ctr->E[h] = ctr->T[h] = ctr->TT[h] = 0;
+        ctr->TM[h] = 0;
+    }
     ctr->err = 0;
 }
 
@@ -886,6 +1016,7 @@ __global__ void mh_finish_kernel(BatchCtr* __restrict__ ctr, int64_t* __restrict
 // of each hop.
 struct HopCaps {
     int64_t F[kMaxHops + 1], E[kMaxHops], W[kMaxHops], T[kMaxHops];
+    int64_t WT[kMaxHops], TT[kMaxHops];  // transposed block: windows, tiles
 };
 
 HopCaps hop_caps(int64_t num_seeds, const int32_t* fanouts, int H, int tc, int64_t num_nodes) {
@@ -901,6 +1032,10 @@ HopCaps hop_caps(int64_t num_seeds, const int32_t* fanouts, int H, int tc, int64
         const int64_t nf = c.F[h] * (1 + k);
         const int64_t lim = c.F[h] + num_nodes;
         c.F[h + 1] = nf < lim ? nf : lim;
+        // windows of 16 sources; a window's tiles are at most one partial
+        // tile more than its edges fill
+        c.WT[h] = (c.F[h + 1] + 15) / 16;
+        c.TT[h] = c.WT[h] + (c.E[h] + tc - 1) / tc;
     }
     return c;
 }
@@ -916,14 +1051,23 @@ struct BatchWs {
     int64_t* out;
     char* scan_ws;
     size_t scan_bytes;
+    // transposed blocks (carved only when a hop asks for one)
+    uint64_t *tka, *tkb;
+    uint32_t *tpa, *tpb;
+    char* sort_ws;
+    size_t sort_bytes;
 };
 
 template <typename C>
-void carve_batch(C& cv, const HopCaps& c, int H, int64_t num_nodes, BatchWs* w) {
-    int64_t emax = 1, wmax = 1;
+void carve_batch(C& cv, const HopCaps& c, int H, int64_t num_nodes, const int32_t* thops, BatchWs* w) {
+    int64_t emax = 1, wmax = 1, etmax = 0;
     for (int h = 0; h < H; ++h) {
         emax = c.E[h] > emax ? c.E[h] : emax;
         wmax = c.W[h] > wmax ? c.W[h] : wmax;
+        if (thops && thops[h]) {
+            etmax = c.E[h] > etmax ? c.E[h] : etmax;
+            wmax = c.WT[h] > wmax ? c.WT[h] : wmax;
+        }
     }
     w->edge_src = cv.template take<int64_t>(emax);
     w->edge_val = cv.template take<float>(emax);
@@ -932,9 +1076,21 @@ void carve_batch(C& cv, const HopCaps& c, int H, int64_t num_nodes, BatchWs* w) 
     w->slicesum = cv.template take<int32_t>(group_count(num_nodes) / kSliceGroups + 2);
     w->sliceoff = cv.template take<int32_t>(group_count(num_nodes) / kSliceGroups + 2);
     w->wtiles = cv.template take<int32_t>(wmax + 1);
-    w->out = cv.template take<int64_t>(3 * kMaxHops + 4);
+    w->out = cv.template take<int64_t>(5 * kMaxHops + 4);
     w->scan_bytes = scan_workspace_bytes(wmax);
     w->scan_ws = cv.template take<char>(w->scan_bytes);
+    w->tka = w->tkb = nullptr;
+    w->tpa = w->tpb = nullptr;
+    w->sort_ws = nullptr;
+    w->sort_bytes = 0;
+    if (etmax > 0) {
+        w->tka = cv.template take<uint64_t>(etmax);
+        w->tkb = cv.template take<uint64_t>(etmax);
+        w->tpa = cv.template take<uint32_t>(etmax);
+        w->tpb = cv.template take<uint32_t>(etmax);
+        w->sort_bytes = radix_sort_workspace_bytes(etmax);
+        w->sort_ws = cv.template take<char>(w->sort_bytes);
+    }
 }
 
 // State buffer of grws_sample_blocks (uint32 words): the new-source bitmap
@@ -1271,27 +1427,57 @@ extern "C" int grws_sample_blocks_capacity(int64_t num_seeds, const int32_t* fan
     return GRWS_OK;
 }
 
-extern "C" size_t grws_sample_blocks_workspace_bytes(int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
-                                                     int32_t tile_cols, int64_t num_nodes) {
+static size_t blocks_workspace_bytes(int64_t num_seeds, const int32_t* fanouts, int32_t num_hops, int32_t tile_cols,
+                                     int64_t num_nodes, const int32_t* thops) {
     if (num_seeds < 0 || num_nodes < 0 || !fanouts || num_hops < 1 || num_hops > kMaxHops) return 0;
     for (int h = 0; h < num_hops; ++h)
         if (fanouts[h] < 1 || fanouts[h] > kWave) return 0;
     const HopCaps c = hop_caps(num_seeds, fanouts, num_hops, tile_cols == 8 ? 8 : 16, num_nodes);
     NullCarver nc;
     BatchWs w;
-    carve_batch(nc, c, num_hops, num_nodes, &w);
+    carve_batch(nc, c, num_hops, num_nodes, thops, &w);
     return nc.s.used + 256;
 }
 
-extern "C" int grws_sample_blocks(const int64_t* indptr, const int32_t* indices, int64_t num_nodes, int64_t nnz,
-                                  const int64_t* seeds, int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
-                                  uint64_t seed, int32_t* node_map, uint32_t* state, int32_t tile_cols,
-                                  int32_t values_dtype, int64_t* const* next_frontier,
-                                  int64_t* const* window_offset, int32_t* const* col_indices,
-                                  void* const* values, void* workspace, size_t workspace_bytes, int64_t* counts_out,
-                                  void* stream_) {
+extern "C" size_t grws_sample_blocks_workspace_bytes(int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
+                                                     int32_t tile_cols, int64_t num_nodes) {
+    return blocks_workspace_bytes(num_seeds, fanouts, num_hops, tile_cols, num_nodes, nullptr);
+}
+
+extern "C" size_t grws_sample_blocks_transposed_workspace_bytes(int64_t num_seeds, const int32_t* fanouts,
+                                                                int32_t num_hops, int32_t tile_cols, int64_t num_nodes,
+                                                                const int32_t* transpose_hops) {
+    return blocks_workspace_bytes(num_seeds, fanouts, num_hops, tile_cols, num_nodes, transpose_hops);
+}
+
+extern "C" int grws_sample_blocks_transposed_capacity(int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
+                                                      int32_t tile_cols, int64_t num_nodes, int64_t* max_t_windows,
+                                                      int64_t* max_t_tiles) {
     clear_error();
-    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(num_seeds >= 0 && num_nodes >= 0, "sample_blocks_transposed_capacity: negative size");
+    GRWS_CHECK_ARG(num_hops >= 1 && num_hops <= kMaxHops,
+                   "sample_blocks_transposed_capacity: num_hops must be in [1, %d]", kMaxHops);
+    GRWS_CHECK_ARG(fanouts && max_t_windows && max_t_tiles, "sample_blocks_transposed_capacity: null pointer");
+    GRWS_CHECK_ARG(tile_cols == 8 || tile_cols == 16, "sample_blocks_transposed_capacity: tile_cols must be 8 or 16");
+    for (int h = 0; h < num_hops; ++h)
+        GRWS_CHECK_ARG(fanouts[h] >= 1 && fanouts[h] <= kWave,
+                       "sample_blocks_transposed_capacity: fanout %d outside [1, 64]", fanouts[h]);
+    const HopCaps c = hop_caps(num_seeds, fanouts, num_hops, tile_cols, num_nodes);
+    for (int h = 0; h < num_hops; ++h) {
+        max_t_windows[h] = c.WT[h];
+        max_t_tiles[h] = c.TT[h];
+    }
+    return GRWS_OK;
+}
+
+static int sample_blocks_impl(const int64_t* indptr, const int32_t* indices, int64_t num_nodes, int64_t nnz,
+                              const int64_t* seeds, int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
+                              uint64_t seed, int32_t* node_map, uint32_t* state, int32_t tile_cols,
+                              int32_t values_dtype, int64_t* const* next_frontier, int64_t* const* window_offset,
+                              int32_t* const* col_indices, void* const* values, const int32_t* thops,
+                              int64_t* const* t_window_offset, int32_t* const* t_col_indices, void* const* t_values,
+                              void* workspace, size_t workspace_bytes, int64_t* counts_out, int per_hop,
+                              hipStream_t stream) {
     const int H = num_hops;
     GRWS_CHECK_ARG(num_nodes >= 0 && nnz >= 0 && num_seeds >= 0, "sample_blocks: negative size");
     GRWS_CHECK_ARG(num_nodes <= INT32_MAX, "sample_blocks: ids exceed int32 local ids");
@@ -1304,9 +1490,22 @@ extern "C" int grws_sample_blocks(const int64_t* indptr, const int32_t* indices,
         GRWS_CHECK_ARG(fanouts[h] >= 1 && fanouts[h] <= kWave, "sample_blocks: fanout %d outside [1, 64]", fanouts[h]);
     const HopCaps c = hop_caps(num_seeds, fanouts, H, tile_cols, num_nodes);
     GRWS_CHECK_ARG(c.F[H] <= INT32_MAX, "sample_blocks: a hop could exceed int32 local ids");
-    for (int h = 0; h < 3 * H; ++h) counts_out[h] = 0;
+    for (int h = 0; h < per_hop * H; ++h) counts_out[h] = 0;
+    bool any_t = false;
+    for (int h = 0; h < H; ++h) any_t = any_t || (thops && thops[h]);
+    if (any_t) {
+        GRWS_CHECK_ARG(t_window_offset && t_col_indices && t_values, "sample_blocks: null transposed outputs");
+        for (int h = 0; h < H; ++h)
+            if (thops[h]) {
+                GRWS_CHECK_ARG(t_window_offset[h] && t_col_indices[h] && t_values[h],
+                               "sample_blocks: null transposed output of hop %d", h);
+                GRWS_CHECK_ARG(c.E[h] <= (int64_t)UINT32_MAX, "sample_blocks: hop %d has too many edge slots", h);
+            }
+    }
     if (num_seeds == 0) {
         for (int h = 0; h < H; ++h) GRWS_TRY(fill_i64(window_offset[h], 1, 0, stream));
+        for (int h = 0; h < H; ++h)
+            if (any_t && thops[h]) GRWS_TRY(fill_i64(t_window_offset[h], 1, 0, stream));
         return GRWS_OK;
     }
     GRWS_CHECK_ARG(indptr && seeds && node_map && state && next_frontier && window_offset && col_indices && values,
@@ -1318,7 +1517,7 @@ extern "C" int grws_sample_blocks(const int64_t* indptr, const int32_t* indices,
     GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(state) % 16 == 0, "sample_blocks: state not 16-byte aligned");
     Carver cv(workspace, workspace_bytes);
     BatchWs w;
-    carve_batch(cv, c, H, num_nodes, &w);
+    carve_batch(cv, c, H, num_nodes, any_t ? thops : nullptr, &w);
     if (!cv.ok) return set_error(GRWS_E_CAPACITY, "sample_blocks: workspace too small (%zu < %zu)", workspace_bytes,
                                  cv.used);
     const StateLayout l = state_layout(num_nodes);
@@ -1359,17 +1558,80 @@ extern "C" int grws_sample_blocks(const int64_t* indptr, const int32_t* indices,
         else GRWS_MH_WINDOWS(1, __hip_bfloat16);
 #undef GRWS_MH_WINDOWS
         GRWS_LAUNCH_CHECK();
+        if (any_t && thops[h]) {
+            // the hop's slots are still in the workspace: its transposed block
+            const int64_t ecap = c.E[h], wcap = c.WT[h];
+#define GRWS_MH_T(KERNEL, VT, ...) hipLaunchKernelGGL(KERNEL<VT>, __VA_ARGS__)
+#define GRWS_MH_TDISPATCH(KERNEL, ...)                                                  \
+    if (values_dtype == GRWS_F32) GRWS_MH_T(KERNEL, float, __VA_ARGS__);                \
+    else if (values_dtype == GRWS_F16) GRWS_MH_T(KERNEL, _Float16, __VA_ARGS__);        \
+    else GRWS_MH_T(KERNEL, __hip_bfloat16, __VA_ARGS__)
+            GRWS_MH_TDISPATCH(mh_tkeys_kernel, dim3(grid_for(ecap)), dim3(kBlk), 0, stream, num_seeds, h, k,
+                              w.src_local, w.edge_val, ecap, wcap, w.tka, w.tpa, ctr);
+            GRWS_LAUNCH_CHECK();
+            bool alt = false;
+            GRWS_TRY(radix_sort_pairs(w.tka, w.tpa, w.tkb, w.tpb, ecap, bits_for(wcap + 1), w.sort_ws, w.sort_bytes,
+                                      stream, &alt));
+            const uint64_t* sk = alt ? w.tkb : w.tka;
+            const uint32_t* sp = alt ? w.tpb : w.tpa;
+            hipLaunchKernelGGL(mh_tcount_kernel, dim3((unsigned)wcap), dim3(kBlk), 0, stream, h, k, sk, sp, ecap, tc,
+                               w.wtiles, ctr);
+            GRWS_LAUNCH_CHECK();
+            GRWS_TRY(scan_i32_to_i64(w.wtiles, t_window_offset[h], wcap, false, w.scan_ws, w.scan_bytes, stream));
+            GRWS_MH_TDISPATCH(mh_tfill_kernel, dim3((unsigned)wcap), dim3(kBlk), 0, stream, h, k, sk, sp, ecap, wcap,
+                              tc, w.src_local, w.edge_val, t_window_offset[h], t_col_indices[h], t_values[h],
+                              ctr);
+#undef GRWS_MH_TDISPATCH
+#undef GRWS_MH_T
+            GRWS_LAUNCH_CHECK();
+        }
     }
     hipLaunchKernelGGL(mh_finish_kernel, dim3(1), dim3(64), 0, stream, ctr, w.out, H);
     GRWS_LAUNCH_CHECK();
-    int64_t h_out[3 * kMaxHops + 4];
-    GRWS_HIP(hipMemcpyAsync(h_out, w.out, sizeof(int64_t) * (3 * H + 2), hipMemcpyDeviceToHost, stream));
+    int64_t h_out[5 * kMaxHops + 4];
+    GRWS_HIP(hipMemcpyAsync(h_out, w.out, sizeof(int64_t) * (5 * H + 2), hipMemcpyDeviceToHost, stream));
     GRWS_HIP(hipStreamSynchronize(stream));
-    GRWS_TRY(report((int32_t)h_out[3 * H + 1], "sample_blocks"));
+    GRWS_TRY(report((int32_t)h_out[5 * H + 1], "sample_blocks"));
     for (int h = 0; h < H; ++h) {
-        counts_out[3 * h + 0] = h_out[H + 1 + h];  // edges
-        counts_out[3 * h + 1] = h_out[h + 1];      // sources (next frontier size)
-        counts_out[3 * h + 2] = h_out[2 * H + 1 + h];  // tiles
+        counts_out[per_hop * h + 0] = h_out[H + 1 + h];      // edges
+        counts_out[per_hop * h + 1] = h_out[h + 1];          // sources (next frontier size)
+        counts_out[per_hop * h + 2] = h_out[2 * H + 1 + h];  // tiles
+        if (per_hop == 5) {
+            counts_out[per_hop * h + 3] = h_out[3 * H + 1 + h];  // tiles of the transposed block
+            counts_out[per_hop * h + 4] = h_out[4 * H + 1 + h];  // most tiles in one of its windows
+        }
     }
     return GRWS_OK;
+}
+
+extern "C" int grws_sample_blocks(const int64_t* indptr, const int32_t* indices, int64_t num_nodes, int64_t nnz,
+                                  const int64_t* seeds, int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
+                                  uint64_t seed, int32_t* node_map, uint32_t* state, int32_t tile_cols,
+                                  int32_t values_dtype, int64_t* const* next_frontier,
+                                  int64_t* const* window_offset, int32_t* const* col_indices,
+                                  void* const* values, void* workspace, size_t workspace_bytes, int64_t* counts_out,
+                                  void* stream_) {
+    clear_error();
+    return sample_blocks_impl(indptr, indices, num_nodes, nnz, seeds, num_seeds, fanouts, num_hops, seed, node_map,
+                              state, tile_cols, values_dtype, next_frontier, window_offset, col_indices, values,
+                              nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes, counts_out, 3,
+                              as_stream(stream_));
+}
+
+extern "C" int grws_sample_blocks_transposed(const int64_t* indptr, const int32_t* indices, int64_t num_nodes,
+                                             int64_t nnz, const int64_t* seeds, int64_t num_seeds,
+                                             const int32_t* fanouts, int32_t num_hops, uint64_t seed,
+                                             int32_t* node_map, uint32_t* state, int32_t tile_cols,
+                                             int32_t values_dtype, int64_t* const* next_frontier,
+                                             int64_t* const* window_offset, int32_t* const* col_indices,
+                                             void* const* values, const int32_t* transpose_hops,
+                                             int64_t* const* t_window_offset, int32_t* const* t_col_indices,
+                                             void* const* t_values, void* workspace, size_t workspace_bytes,
+                                             int64_t* counts_out, void* stream_) {
+    clear_error();
+    GRWS_CHECK_ARG(transpose_hops != nullptr, "sample_blocks_transposed: null transpose_hops");
+    return sample_blocks_impl(indptr, indices, num_nodes, nnz, seeds, num_seeds, fanouts, num_hops, seed, node_map,
+                              state, tile_cols, values_dtype, next_frontier, window_offset, col_indices, values,
+                              transpose_hops, t_window_offset, t_col_indices, t_values, workspace, workspace_bytes,
+                              counts_out, 5, as_stream(stream_));
 }

@@ -138,14 +138,17 @@ def _sample_batch(sampler, graph, seeds, features, device, needs_t=None):
     the last layer's active windows (engine.py:170-181)."""
     from ..sampler import NeighborSampler
     if isinstance(sampler, NeighborSampler):
-        blocks = sampler.sample_layers(graph.row_ptr, graph.col_idx, seeds)
+        want = None
         if torch.is_grad_enabled():
-            # build the backward's A^T here, on the sampling stream, off the
-            # training critical path (blocks are not modified afterwards),
-            # for the layers whose backward runs it
+            # the backward's A^T, for the layers whose backward runs it: built
+            # by the sampler's own call (no further sync), on the sampling
+            # stream, off the training critical path
+            want = [needs_t is None or l >= len(needs_t) or bool(needs_t[l]) for l in range(len(sampler.fanouts))]
+        blocks = sampler.sample_layers(graph.row_ptr, graph.col_idx, seeds, transposes=want)
+        if want is not None:
             for l, b in enumerate(blocks):
-                if needs_t is None or l >= len(needs_t) or needs_t[l]:
-                    b.transpose()
+                if want[l]:
+                    b.transpose()  # found in the block's cache (built here when the sampler did not)
         inp = blocks[0].src_nodes
         if features.is_cuda:
             feats = features.index_select(0, inp)

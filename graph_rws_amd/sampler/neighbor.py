@@ -72,8 +72,12 @@ class NeighborSampler:
         self._state = None
 
     def sample_layers(self, indptr: torch.Tensor, indices: torch.Tensor,
-                      seed_nodes: torch.Tensor) -> List[BCSRGraph]:
+                      seed_nodes: torch.Tensor, transposes=None) -> List[BCSRGraph]:
         """Samples len(fanouts) hops from `seed_nodes` (distinct global ids).
+
+        transposes: per layer (input side first), whether to build the
+        block's transpose as well, in the same device call (fused path): the
+        block's ``transpose()`` then returns it without a build.
 
         Every returned block carries ``src_nodes`` (int64 global ids of its
         columns, destination nodes first), ``num_sampled_edges`` and
@@ -90,12 +94,22 @@ class NeighborSampler:
                            or self._state.node_map.device != dev):
             self._state = SampleState(num_nodes, dev)
         hop_fanouts = list(reversed(self.fanouts))
+        hop_t = None
+        if transposes is not None and self.fused:
+            if len(transposes) != len(self.fanouts):
+                raise ValueError("sample_layers: one transposes flag per layer")
+            hop_t = [bool(t) for t in reversed(list(transposes))]
+            if not any(hop_t):
+                hop_t = None
         batch = (sample_blocks(indptr, indices, frontier, hop_fanouts, self._state, seed=self.seed,
-                               tile_cols=self.tile_cols, values_dtype=self.values_dtype)
+                               tile_cols=self.tile_cols, values_dtype=self.values_dtype, transposes=hop_t)
                  if self.fused else None)
         for h, k in enumerate(hop_fanouts):
+            tr = None
             if self.fused:
-                win, cols, vals, nxt, E = batch[h]
+                win, cols, vals, nxt, E = batch[h][:5]
+                if hop_t is not None:
+                    tr = batch[h][5]
             else:
                 dst, src, val = sample_hop(indptr, indices, frontier, k, seed=self.seed)
                 src_local, nxt = relabel(frontier, src, num_nodes)
@@ -117,6 +131,15 @@ class NeighborSampler:
             # at most 16 x fanout distinct columns per window
             g.max_window_slabs = (16 * k + 15) // 16
             g.fanout = k
+            if tr is not None:
+                from ..core.ops import TensorKey
+                twin, tcols, tvals, tmax = tr
+                AT = BCSRGraph(num_nodes=S, num_edges=E, tile_rows=16, tile_cols=self.tile_cols,
+                               window_offset=twin, original_col_indices=tcols, values_condensed=tvals,
+                               device=dev, num_rows=S, num_cols=16 * g.num_windows, values_dtype=self.values_dtype)
+                AT.max_window_slabs = (tmax * self.tile_cols + 15) // 16
+                g._cache["T"] = (TensorKey((g.window_offset, g.original_col_indices, g.values_condensed),
+                                           (g.num_cols,)), AT)
             blocks.insert(0, g)
             edges += g.num_sampled_edges
             frontier = nxt

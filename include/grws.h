@@ -389,6 +389,35 @@ int grws_sample_blocks(const int64_t* indptr, const int32_t* indices, int64_t nu
                        void* const* values, void* workspace, size_t workspace_bytes, int64_t* counts_out,
                        void* stream);
 
+/* grws_sample_blocks plus, for each hop h with transpose_hops[h] != 0, the  */
+/* BCSR of that hop's block transposed (windows of 16 sources, columns = the */
+/* hop's frontier rows 0 .. 16 ceil(F_h/16) - 1), built in the same call     */
+/* with no further sync.  It is the matrix the backward SpMM over the block  */
+/* multiplies by (the reference's spmm_transpose, spmm_wrapper.cu:109-152,   */
+/* reached from layers/layer.py:66-79), bit for bit the BCSR a device build */
+/* of the block's transpose makes: every cell with a nonzero value, a       */
+/* window's distinct rows ascending.  Outputs per such hop:                  */
+/* t_window_offset[h] int64 [max_t_windows[h]+1] (windows past               */
+/* ceil(sources/16) hold no tiles), t_col_indices[h] int32                   */
+/* [max_t_tiles[h]*tile_cols], t_values[h] [max_t_tiles[h]*16*tile_cols],    */
+/* capacities from grws_sample_blocks_transposed_capacity; entries of hops   */
+/* not transposed are ignored.  counts_out[5*h .. 5*h+4] = {edges, sources,  */
+/* tiles, transposed tiles, most tiles in one transposed window}.            */
+int grws_sample_blocks_transposed_capacity(int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
+                                           int32_t tile_cols, int64_t num_nodes, int64_t* max_t_windows,
+                                           int64_t* max_t_tiles);
+size_t grws_sample_blocks_transposed_workspace_bytes(int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
+                                                     int32_t tile_cols, int64_t num_nodes,
+                                                     const int32_t* transpose_hops);
+int grws_sample_blocks_transposed(const int64_t* indptr, const int32_t* indices, int64_t num_nodes, int64_t nnz,
+                                  const int64_t* seeds, int64_t num_seeds, const int32_t* fanouts, int32_t num_hops,
+                                  uint64_t seed, int32_t* node_map, uint32_t* state, int32_t tile_cols,
+                                  int32_t values_dtype, int64_t* const* next_frontier,
+                                  int64_t* const* window_offset, int32_t* const* col_indices, void* const* values,
+                                  const int32_t* transpose_hops, int64_t* const* t_window_offset,
+                                  int32_t* const* t_col_indices, void* const* t_values, void* workspace,
+                                  size_t workspace_bytes, int64_t* counts_out, void* stream);
+
 int grws_sample_state_init(int32_t* node_map, uint32_t* bitmap, int64_t num_nodes, void* stream);
 size_t grws_sample_block_workspace_bytes(int64_t num_frontier, int32_t fanout, int64_t num_nodes);
 int grws_sample_block_capacity(int64_t num_frontier, int32_t fanout, int32_t tile_cols,

@@ -215,3 +215,96 @@ def test_sample_blocks_errors_leave_state_clean(cuda_device):
     with pytest.raises(GrwsError, match="neighbour index"):
         sample_blocks(ipd, bad_ix, torch.tensor([0, 1], device=cuda_device), [5], st)
     assert bool((st.node_map == -1).all()) and bool((st.bitmap == 0).all())
+
+
+def _vdt_cast(vals: np.ndarray, vdt) -> np.ndarray:
+    if vdt == torch.float16:
+        return vals.astype(np.float16)
+    if vdt == torch.bfloat16:
+        return oracle.round_to_bf16(vals.astype(np.float32))
+    return vals.astype(np.float32)
+
+
+def _tensor_np(t: torch.Tensor) -> np.ndarray:
+    if t.dtype == torch.bfloat16:
+        return t.float().cpu().numpy()
+    return t.cpu().numpy()
+
+
+@pytest.mark.parametrize("hops,tc,vdt,mask", [([5, 10, 15], 16, torch.float32, None),
+                                              ([5, 10, 15], 8, torch.float16, None),
+                                              ([5, 10, 15], 16, torch.bfloat16, [True, False, True]),
+                                              ([64, 1], 16, torch.float32, None),
+                                              ([2] * 8, 16, torch.float16, None)])
+def test_sample_blocks_transposed_bit_exact(cuda_device, hops, tc, vdt, mask):
+    """grws_sample_blocks_transposed: the blocks are those of the plain call,
+    and each transposed block equals, bit for bit, the oracle's BCSR of the
+    hop's edges with rows and columns swapped (sources as rows, the
+    frontier rows as columns: the reference converter's layout), and the
+    device build of the block's transpose (builder.transpose).  Hub and
+    zero-degree nodes included; a repeated (row, source) pair keeps one
+    entry."""
+    from graph_rws_amd import builder
+    from graph_rws_amd.core.ops import SampleState, sample_blocks
+    from graph_rws_amd.data import BCSRGraph
+    degs = np.random.default_rng(16).integers(0, 40, 6000)
+    degs[::97] = 0
+    degs[5] = 3000
+    ip, ix, ipd, ixd = _csr(degs, 6000, 17, cuda_device)
+    st = SampleState(6000, cuda_device)
+    seeds = np.random.default_rng(18).choice(6000, 300, replace=False).astype(np.int64)
+    seeds[0] = 5
+    sd = torch.from_numpy(seeds).to(cuda_device)
+    mask = mask or [True] * len(hops)
+    out = sample_blocks(ipd, ixd, sd, hops, st, seed=42, tile_cols=tc, values_dtype=vdt, transposes=mask)
+    plain = sample_blocks(ipd, ixd, sd, hops, st, seed=42, tile_cols=tc, values_dtype=vdt)
+    ref = oracle.sample_blocks(ip, ix, seeds, list(reversed(hops)), seed=42, tile_cols=tc)[::-1]
+    for h, (o, p, r) in enumerate(zip(out, plain, ref)):
+        for a, b in zip(o[:4], p[:4]):
+            np.testing.assert_array_equal(_tensor_np(a), _tensor_np(b), err_msg=f"hop {h}")
+        assert o[4] == p[4]
+        if not mask[h]:
+            assert o[5] is None
+            continue
+        twin, tcols, tvals, tmax = o[5]
+        S = r["num_cols"]
+        ow, oc, ov = oracle.coo_to_bcsr(S, r["src_local"], r["dst"], r["val"], tc)
+        np.testing.assert_array_equal(twin.cpu().numpy(), ow, err_msg=f"hop {h}: t_window_offset")
+        np.testing.assert_array_equal(tcols.cpu().numpy(), oc, err_msg=f"hop {h}: t_col_indices")
+        np.testing.assert_array_equal(_tensor_np(tvals), _vdt_cast(ov, vdt).astype(np.float32)
+                                      if vdt == torch.bfloat16 else _vdt_cast(ov, vdt), err_msg=f"hop {h}: t_values")
+        assert tmax == int(np.diff(ow).max(initial=0))
+        # the device build of the block's transpose gives the same arrays
+        win, cols, vals = o[0], o[1], o[2]
+        F = r["num_rows"]
+        g = BCSRGraph(num_nodes=F, num_edges=o[4], tile_rows=16, tile_cols=tc, window_offset=win,
+                      original_col_indices=cols, values_condensed=vals, device=cuda_device, num_rows=F,
+                      num_cols=S, values_dtype=vdt)
+        AT = builder.transpose(g)
+        np.testing.assert_array_equal(AT.window_offset.cpu().numpy(), twin.cpu().numpy())
+        np.testing.assert_array_equal(AT.original_col_indices.cpu().numpy(), tcols.cpu().numpy())
+        np.testing.assert_array_equal(_tensor_np(AT.values_condensed), _tensor_np(tvals))
+    assert bool((st.node_map == -1).all()) and bool((st.bitmap == 0).all())
+
+
+def test_neighbor_sampler_blocks_carry_their_transposes(cuda_device):
+    """sample_layers(transposes=...) attaches each built transpose to its
+    block: transpose() returns it without a build, and the backward SpMM
+    over it equals the one over a fresh device build."""
+    g = synth.c5_graph(device=cuda_device, scale=1e-4)
+    seeds = synth.distinct_seeds(g.num_nodes, 200, seed=3, device=cuda_device)
+    s = NeighborSampler([6, 4, 3], tile_cols=16, values_dtype=torch.float16)
+    blocks = s.sample_layers(g.row_ptr, g.col_idx, seeds, transposes=[False, True, True])
+    assert blocks[0]._cache.get("T") is None
+    from graph_rws_amd import builder
+    for b in blocks[1:]:
+        AT = b.transpose()
+        assert AT is b._cache["T"][1]
+        fresh = builder.transpose(b)
+        np.testing.assert_array_equal(AT.window_offset.cpu().numpy(), fresh.window_offset.cpu().numpy())
+        np.testing.assert_array_equal(AT.original_col_indices.cpu().numpy(),
+                                      fresh.original_col_indices.cpu().numpy())
+        np.testing.assert_array_equal(AT.values_condensed.cpu().numpy(), fresh.values_condensed.cpu().numpy())
+        assert AT.max_window_slabs == fresh.max_window_slabs
+        G = torch.randn(16 * b.num_windows, 32, device=cuda_device).half()
+        torch.testing.assert_close(AT.spmm(G), fresh.spmm(G), rtol=0, atol=0)
