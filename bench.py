@@ -65,7 +65,7 @@ def build_graph(cfg: str, tc: int, vdt: torch.dtype, dev: torch.device):
     return g, G, t1 - t0, t2 - t1
 
 
-def alg_bytes(G, N: int, s_x: int, s_y: int, packed=None, plan=None) -> dict:
+def alg_bytes(G, N: int, s_x: int, s_y: int, packed=None, plan=None, grouped=None) -> dict:
     """Bytes one SpMM must move, two ways.
 
     compulsory: every array the kernel reads, read once, in the format it
@@ -92,6 +92,13 @@ def alg_bytes(G, N: int, s_x: int, s_y: int, packed=None, plan=None) -> dict:
     }
     parts["total"] = sum(parts.values())
     parts["U"] = U
+    if grouped is not None:
+        # group offsets, union columns, sub-tile headers and values: all the kernel reads of A
+        a_read = grouped.nbytes()
+        parts["compulsory"] = a_read + s_x * rows_ref * N + parts["y"]
+        parts["compulsory_detail"] = {"a_grouped": a_read, "a_format": f"grouped ({grouped.group_size} windows)",
+                                      "x_rows_referenced": rows_ref, "x_once": s_x * rows_ref * N}
+        return parts
     a_read = (48 * T + s_a * packed.num_values) if packed is not None else parts["vals"]
     items = 16 * plan.num_items if plan is not None else 0
     parts["compulsory"] = (parts["win_off"] + parts["cols"] + a_read + s_x * rows_ref * N + parts["y"]
@@ -508,6 +515,11 @@ def bench_minibatch(dev, batches: int, warmup: int) -> dict:
         return (time.perf_counter() - t, sampler.total_edges - e0, sampler.total_batches - b0,
                 loss, timer.get_epoch_stats())
 
+    # the objects earlier legs left are moved out of the collector's reach
+    # (gc.freeze): a full collection over them inside a timed epoch cost
+    # ~0.5 ms per batch
+    gc.collect()
+    gc.freeze()
     # warm-up epochs on other seed sets: GEMM kernels for the batch shapes
     # seen load lazily (a one-off stall of tens of ms on first use), and the
     # graphed step captures the buckets these shapes fall in
@@ -545,6 +557,7 @@ def bench_minibatch(dev, batches: int, warmup: int) -> dict:
                         "of 10 batches with a sync per call (3 per batch); the timed epochs do not sync",
            "generate_s": round(t_gen, 2)}
     del g, X, labels, model, opt, graphed
+    gc.unfreeze()
     torch.cuda.empty_cache()
     return out
 
@@ -783,7 +796,20 @@ def main():
     for _ in range(max(2, args.warmup)):
         G.spmm(X, out=Y)
     torch.cuda.synchronize(dev)
-    a_format = "packed tiles" if G.packed_tiles() is not None else "dense tiles"
+    grouped = G.grouped_tiles(X.shape[0]) if N >= _ops.GROUP_MIN_N else None
+    if grouped is not None:
+        a_format = f"grouped tiles ({grouped.group_size} windows)"
+    else:
+        a_format = "packed tiles" if G.packed_tiles() is not None else "dense tiles"
+    t_group = None
+    if grouped is not None:  # its build, timed once on its own for the record
+        torch.cuda.synchronize(dev)
+        tq = time.perf_counter()
+        _gq = _ops.group_tiles(G.window_offset, G.original_col_indices, G.values_condensed, G.tile_cols,
+                               X.shape[0])
+        torch.cuda.synchronize(dev)
+        t_group = time.perf_counter() - tq
+        del _gq
     gc.collect()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.steps)]
@@ -802,11 +828,12 @@ def main():
     nnz = g.nnz
     flops = 2.0 * nnz * N
     gflops = flops / (ms_step / 1e3) / 1e9
-    packed = G.packed_tiles()
-    B = alg_bytes(G, N, X.element_size(), Y.element_size(), packed=packed, plan=plan)
+    packed = G.packed_tiles() if grouped is None else None
+    B = alg_bytes(G, N, X.element_size(), Y.element_size(), packed=packed, plan=plan, grouped=grouped)
     comp_gbs = B["compulsory"] / (ms_avg / 1e3) / 1e9
     gather_gbs = B["total"] / (ms_avg / 1e3) / 1e9
-    issued = 2.0 * G.num_tiles * 16 * G.tile_cols * N
+    issued = (2.0 * grouped.num_slabs * grouped.group_size * 256 * N if grouped is not None
+              else 2.0 * G.num_tiles * 16 * G.tile_cols * N)
     tkey = (cfg, N, dname, G.tile_cols, a_format)
     traffic = MEASURED_TRAFFIC.get(tkey, (None, None))
 
@@ -830,14 +857,18 @@ def main():
             "tile": f"16x{G.tile_cols}", "N": N, "x_dtype": dname, "x_row_pitch": X.stride(0),
             "values_dtype": str(G.values_condensed.dtype).replace("torch.", ""),
             "a_format": a_format,
-            "plan": {"items": plan.num_items, "split_windows": plan.num_split,
-                     "slabs_per_item": plan.slabs_per_item},
+            "plan": ({"groups": grouped.num_groups, "union_slabs": grouped.num_slabs,
+                      "union_over_window_slots": round(grouped.slot_ratio, 4),
+                      "longest_group_slabs": grouped.max_group_slabs} if grouped is not None else
+                     {"items": plan.num_items, "split_windows": plan.num_split,
+                      "slabs_per_item": plan.slabs_per_item}),
         },
         "alg_bytes": B,
         "roofline": {
             "bound": "hbm",
             # 16-bit X runs the buffer-load kernel, fp32 X the element-masked one
-            "kernel": "spmm_buf_kernel" if dname in ("f16", "bf16") else "spmm_fwd_kernel",
+            "kernel": ("spmm_grp_kernel" if grouped is not None else
+                       "spmm_buf_kernel" if dname in ("f16", "bf16") else "spmm_fwd_kernel"),
             # compulsory bytes (A in the format read, X and Y once) per product
             # over the product's kernel time (HIP events on the launch stream)
             "achieved": round(comp_gbs, 1),
@@ -862,7 +893,8 @@ def main():
             "mfma_frac": round(issued / (ms_avg / 1e3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
         },
         "setup_s": {"generate": round(t_gen, 2), "bcsr_build": round(t_build, 2),
-                    "pack_tiles": round(t_pack, 4)},
+                    "pack_tiles": round(t_pack, 4),
+                    "group_tiles": round(t_group, 4) if t_group is not None else None},
     }
     if not args.no_cpu_baseline:
         cb = cpu_baseline(g, G, X, Y, 1e-2 if dname != "f32" else 1e-5)

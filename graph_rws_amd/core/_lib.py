@@ -36,6 +36,13 @@ class PackedTilesView(ctypes.Structure):
     _fields_ = [("header", _vp), ("values", _vp), ("num_values", ctypes.c_int64)]
 
 
+class GroupedTilesView(ctypes.Structure):
+    """grws_grouped_tiles (include/grws.h)."""
+    _fields_ = [("group_offset", _vp), ("col_indices", _vp), ("header", _vp), ("values", _vp),
+                ("num_groups", ctypes.c_int64), ("num_slabs", ctypes.c_int64), ("num_values", ctypes.c_int64),
+                ("max_group_slabs", ctypes.c_int64), ("num_cols", ctypes.c_int64), ("group_size", ctypes.c_int32)]
+
+
 class SpmmPlanView(ctypes.Structure):
     """grws_spmm_plan (include/grws.h)."""
     _fields_ = [("items", _vp), ("split", _vp), ("num_items", ctypes.c_int64),
@@ -86,6 +93,17 @@ _PROTOS = {
                                              ctypes.POINTER(ctypes.c_int64), _vp]),
     "grws_pack_tiles_fill": (ctypes.c_int, [ctypes.POINTER(BcsrView), _vp, _vp, ctypes.c_int64, _vp,
                                             ctypes.c_size_t, _vp]),
+    "grws_group_tiles_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(BcsrView), ctypes.c_int64,
+                                                           ctypes.c_int32]),
+    "grws_group_tiles_count": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.c_int64, ctypes.c_int32, _vp,
+                                              ctypes.c_size_t, _c_i64p, _c_i64p, _c_i64p, _vp]),
+    "grws_group_tiles_fill": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.c_int64, ctypes.c_int32,
+                                             ctypes.c_int64, _vp, _vp, _vp, _vp, ctypes.c_int64, _vp,
+                                             ctypes.c_size_t, _vp]),
+    "grws_spmm_grouped": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.POINTER(GroupedTilesView), _vp,
+                                         ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _vp,
+                                         ctypes.c_int64, ctypes.c_int64, _vp, ctypes.c_int32, ctypes.c_int64,
+                                         _vp]),
     "grws_csr_to_bcsr_host_count": (ctypes.c_int, [ctypes.c_int64, _vp, _vp, ctypes.c_int32,
                                                    ctypes.c_int32, _vp, _c_i64p, ctypes.c_int32]),
     "grws_csr_to_bcsr_host_fill": (ctypes.c_int, [ctypes.c_int64, _vp, _vp, _vp, ctypes.c_int32,

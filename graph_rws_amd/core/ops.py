@@ -20,6 +20,8 @@ from . import _lib as L
 # sync per call, timer.h:22-52).  Off by default: ms is reported as 0.0 and
 # no synchronisation happens.  Set to True to time each call with events.
 TIMING = False
+# SpMM over grouped tiles where a graph has them (False: packed or dense tiles)
+GROUPED = True
 
 # Graphs multiplied more than once read their values from packed tiles
 # (BCSRGraph.packed_tiles); False keeps every SpMM on the dense tiles.
@@ -252,6 +254,99 @@ def pack_tiles(window_offset: torch.Tensor, col_indices: torch.Tensor, values: t
     return PackedTiles(header, pvals, nv.value)
 
 
+class GroupedTiles:
+    """A's tiles re-cut so that `group_size` consecutive windows share one
+    sorted list of their columns, 16 per slab, with one packed 16x16
+    sub-tile per window and slab (grws_grouped_tiles in include/grws.h).
+    grws_spmm_grouped gathers every union column's X row once per group."""
+
+    def __init__(self, group_offset, col_indices, header, values, num_groups, num_slabs, num_values,
+                 max_group_slabs, num_cols, group_size, slot_ratio):
+        self.group_offset = group_offset
+        self.col_indices = col_indices
+        self.header = header
+        self.values = values
+        self.num_groups = int(num_groups)
+        self.num_slabs = int(num_slabs)
+        self.num_values = int(num_values)
+        self.max_group_slabs = int(max_group_slabs)
+        self.num_cols = int(num_cols)
+        self.group_size = int(group_size)
+        # union column slots / the windows' own column slots
+        self.slot_ratio = float(slot_ratio)
+
+    def view(self) -> L.GroupedTilesView:
+        return L.GroupedTilesView(L.ptr(self.group_offset), L.ptr(self.col_indices), L.ptr(self.header),
+                                  L.ptr(self.values), self.num_groups, self.num_slabs, self.num_values,
+                                  self.max_group_slabs, self.num_cols, self.group_size)
+
+    def nbytes(self) -> int:
+        return (self.group_offset.numel() * 8 + self.col_indices.numel() * 4 + self.header.numel() * 4
+                + self.values.numel() * self.values.element_size())
+
+
+# Build grouped tiles when the union of a group's columns is at most this
+# share of its windows' own column slots (below it the saved gathers pay
+# for the extra sub-tiles), and every group at most this many times the
+# mean group's slabs (groups are not split across work-groups).
+GROUP_MAX_RATIO = 0.8
+GROUP_MAX_SKEW = 4.0
+GROUP_SIZE = 2
+# narrower products stay on the window-by-window kernel: a grouped chunk is
+# at least 128 columns wide (measured on c3: N = 48 took twice as long)
+GROUP_MIN_N = 192
+
+
+def group_tiles(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.Tensor, tile_cols: int,
+                num_cols: int, group_size: int = GROUP_SIZE, max_ratio: Optional[float] = None,
+                max_skew: Optional[float] = None) -> Optional[GroupedTiles]:
+    """Builds grouped tiles on the device (one stream sync), or returns None
+    when they do not apply (dtype, shape) or would not pay: the union of the
+    groups' columns above max_ratio of the windows' own column slots, or a
+    group longer than max_skew times the mean."""
+    if values.dtype not in (torch.float16, torch.bfloat16) or tile_cols not in (8, 16) or not values.is_cuda:
+        return None
+    _check_graph(window_offset, col_indices, values, tile_cols)
+    max_ratio = GROUP_MAX_RATIO if max_ratio is None else max_ratio
+    max_skew = GROUP_MAX_SKEW if max_skew is None else max_skew
+    lib = L.load()
+    dev = values.device
+    W = window_offset.numel() - 1
+    T = col_indices.numel() // tile_cols
+    if W == 0 or T == 0:
+        return None
+    view = L.BcsrView(L.ptr(window_offset), L.ptr(col_indices), L.ptr(values), W, T, 16, tile_cols,
+                      L.dtype_code(values.dtype), 0)
+    wsb = int(lib.grws_group_tiles_workspace_bytes(ctypes.byref(view), int(num_cols), int(group_size)))
+    ws = torch.empty(max(1, wsb), dtype=torch.uint8, device=dev)
+    ns, nv, mx = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    st = lib.grws_group_tiles_count(ctypes.byref(view), int(num_cols), int(group_size), L.ptr(ws), wsb,
+                                    ctypes.byref(ns), ctypes.byref(nv), ctypes.byref(mx), L.stream_of(dev))
+    if st == L.GRWS_E_CAPACITY:
+        return None
+    L.check("grws_group_tiles_count", st)
+    S, NV, MX = ns.value, nv.value, mx.value
+    Q = (W + group_size - 1) // group_size
+    ratio = (16 * S) / max(1, T * tile_cols)
+    if S == 0 or ratio > max_ratio or MX > max_skew * S / Q or NV > (1 << 30) - 16:
+        return None
+    goff = torch.empty(Q + 1, dtype=torch.int64, device=dev)
+    gcols = torch.empty(S * 16, dtype=torch.int32, device=dev)
+    header = torch.empty(S * group_size * 12, dtype=torch.int32, device=dev)
+    gvals = torch.zeros(NV + 8, dtype=values.dtype, device=dev)  # 8 readable elements past the last
+    L.call("grws_group_tiles_fill", ctypes.byref(view), int(num_cols), int(group_size), S, L.ptr(goff),
+           L.ptr(gcols), L.ptr(header), L.ptr(gvals), NV, L.ptr(ws), wsb, L.stream_of(dev))
+    return GroupedTiles(goff, gcols, header, gvals, Q, S, NV, MX, num_cols, group_size, ratio)
+
+
+def grouped_supported(x: torch.Tensor, values: torch.Tensor) -> bool:
+    """Whether grws_spmm_grouped takes x: 16-bit with the values' dtype,
+    16-byte rows and a 16-byte aligned start."""
+    return (x.dtype == values.dtype and x.dtype in (torch.float16, torch.bfloat16) and x.dim() == 2
+            and x.stride(1) == 1 and x.shape[1] % 8 == 0 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
+            and x.shape[0] > 0)
+
+
 # ---------------------------------------------------------------------------
 # SpMM forward
 # ---------------------------------------------------------------------------
@@ -273,10 +368,13 @@ def _check_graph(window_offset, col_indices, values, tile_cols):
 def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.Tensor,
          x: torch.Tensor, tile_cols: int, plan: Optional[SpmmPlan] = None,
          out: Optional[torch.Tensor] = None, packed: Optional[PackedTiles] = None,
-         max_window_slabs: int = 0, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+         max_window_slabs: int = 0, residual: Optional[torch.Tensor] = None,
+         grouped: Optional[GroupedTiles] = None) -> torch.Tensor:
     """Y[16W, N] = A X on the device (H1 kernel).  x: [x_rows, N] (row stride
     may exceed N); out dtype = x dtype.  packed: the graph's packed tiles
     (read instead of the dense values when x has the values' dtype).
+    grouped: the graph's grouped tiles, used when x is a 16-bit matrix of
+    the values' dtype with at most grouped.num_cols rows.
     max_window_slabs: an upper bound of every window's slabs when known
     (0 = unknown); lets a call without a plan use the buffer-load kernel.
     residual: R [r_rows, N] in x's dtype, added to the first r_rows rows of
@@ -304,7 +402,7 @@ def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.T
         x = _widen(x, vec)
         full = spmm(window_offset, col_indices, values, x, tile_cols, plan=plan, packed=packed,
                     max_window_slabs=max_window_slabs,
-                    residual=None if residual is None else _widen(residual, vec))
+                    residual=None if residual is None else _widen(residual, vec), grouped=grouped)
         return full[:, :N]
     if out is None:
         out = torch.empty((W * 16, N), dtype=x.dtype, device=x.device)
@@ -315,6 +413,15 @@ def spmm(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.T
     view = L.BcsrView(L.ptr(window_offset), L.ptr(col_indices), L.ptr(values), W,
                       col_indices.numel() // tile_cols, 16, tile_cols, L.dtype_code(values.dtype),
                       int(min(max(0, max_window_slabs), 2**31 - 1)))
+    if (grouped is not None and GROUPED and grouped_supported(x, values) and x.shape[0] <= grouped.num_cols
+            and N >= GROUP_MIN_N):
+        gv = grouped.view()
+        L.call("grws_spmm_grouped", ctypes.byref(view), ctypes.byref(gv), L.ptr(x), L.dtype_code(x.dtype),
+               x.shape[0], x.stride(0), N, L.ptr(residual) if residual is not None else None,
+               residual.stride(0) if residual is not None else 0,
+               residual.shape[0] if residual is not None else 0, L.ptr(out), L.dtype_code(out.dtype),
+               out.stride(0), L.stream_of(x.device))
+        return out
     pv = None
     ws = None
     wsb = 0

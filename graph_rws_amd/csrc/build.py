@@ -29,6 +29,7 @@ SOURCES = [
     "scan.hip",
     "sort.hip",
     "spmm.hip",
+    "group.hip",
     "bcsr_build.hip",
     "reindex.hip",
     "sample.hip",

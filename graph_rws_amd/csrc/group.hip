@@ -1,0 +1,449 @@
+// Grouped tiles: the BCSR of A re-tiled so that G consecutive row windows
+// share their column slabs (gfx950).
+//
+// A 16-row window multiplies its own distinct columns, 16 per tile.  On a
+// graph with community structure neighbouring windows reference mostly the
+// same columns, so the SpMM gathers the same X rows once per window.  Here
+// the G windows of a group get one sorted list of the union of their
+// columns, cut into slabs of 16; for every slab each window keeps a 16x16
+// sub-tile holding its values in those columns (zeros elsewhere), packed as
+// the SpMM's packed tiles are (per 4-row group a 64-bit mask of the nonzero
+// slots and the index of the group's first value).  The grouped SpMM kernel
+// then gathers each slab's 16 X rows once and multiplies them by the G
+// sub-tiles.
+//
+// Build, two calls (one host sync, in the first):
+//   count: key (group, column) of every tile slot with a valid column,
+//          stable radix sort, distinct keys ranked -> columns per group ->
+//          slabs per group -> group_offset (kept in the workspace); the
+//          nonzero value count; the longest group.
+//   fill:  union columns, every slot's (slab, position), masks by atomic OR,
+//          value counts -> scan -> group starts, then every value placed by
+//          the popcount of the mask bits below it (deterministic).
+#include "grws_internal.h"
+
+namespace grws {
+namespace {
+
+constexpr int kBlk = 256;
+
+inline int bits_for(int64_t x) {
+    int b = 0;
+    while (b < 63 && ((int64_t)1 << b) < x) ++b;
+    return b;
+}
+
+inline unsigned grid_for(int64_t n, int64_t per_block = kBlk) {
+    int64_t g = (n + per_block - 1) / per_block;
+    return (unsigned)(g < 1 ? 1 : g);
+}
+
+struct GroupShape {
+    int64_t n;      // tile slots (T * tc)
+    int64_t Q;      // groups
+    int G;          // windows per group
+    int cbits;      // column bits
+    int bits;       // sort key bits: group, column, then the invalid flag
+    int64_t scan_n; // longest scan
+};
+
+GroupShape group_shape(const grws_bcsr* A, int64_t num_cols, int G) {
+    GroupShape s;
+    s.n = A->num_tiles * A->tile_cols;
+    s.G = G;
+    s.Q = (A->num_windows + G - 1) / G;
+    s.cbits = bits_for(num_cols > 1 ? num_cols : 2);
+    s.bits = bits_for(s.Q > 1 ? s.Q : 2) + s.cbits + 1;
+    // sub-tile count scan: slabs <= tiles + groups
+    const int64_t subs = (A->num_tiles + s.Q) * G;
+    s.scan_n = s.n > subs ? s.n : subs;
+    if (s.scan_n < s.Q + 1) s.scan_n = s.Q + 1;
+    return s;
+}
+
+struct GroupWs {
+    uint64_t *ka, *kb;
+    uint32_t *va, *vb;
+    int32_t* uflag;
+    int64_t* uidx;     // exclusive scan of uflag, n + 1
+    uint32_t* pos;     // per slot: slab * 16 + position in the slab
+    int64_t* gfirst;   // per group: rank of its first distinct column
+    int64_t* glast;    // per group: one past its last
+    int32_t* gslabs;   // per group: slabs
+    int64_t* goff;     // group_offset, Q + 1
+    int32_t* scnt;     // per sub-tile: values
+    int64_t* soff;     // their exclusive scan
+    int64_t* stats;    // [0] nonzero values, [1] longest group (slabs)
+    char* sort_ws;
+    size_t sort_bytes;
+    char* scan_ws;
+    size_t scan_bytes;
+    bool alt;          // sorted keys in kb/vb
+};
+
+template <typename C>
+void carve_group(C& cv, const GroupShape& s, GroupWs* w) {
+    const int64_t n = s.n > 0 ? s.n : 1;
+    w->ka = cv.template take<uint64_t>(n);
+    w->kb = cv.template take<uint64_t>(n);
+    w->va = cv.template take<uint32_t>(n);
+    w->vb = cv.template take<uint32_t>(n);
+    w->uflag = cv.template take<int32_t>(n);
+    w->uidx = cv.template take<int64_t>(n + 1);
+    w->pos = cv.template take<uint32_t>(n);
+    w->gfirst = cv.template take<int64_t>(s.Q + 1);
+    w->glast = cv.template take<int64_t>(s.Q + 1);
+    w->gslabs = cv.template take<int32_t>(s.Q + 1);
+    w->goff = cv.template take<int64_t>(s.Q + 1);
+    w->stats = cv.template take<int64_t>(4);
+    w->sort_bytes = radix_sort_workspace_bytes(n);
+    w->sort_ws = cv.template take<char>(w->sort_bytes);
+    w->scan_bytes = scan_workspace_bytes(s.scan_n);
+    w->scan_ws = cv.template take<char>(w->scan_bytes);
+    w->scnt = nullptr;
+    w->soff = nullptr;
+}
+
+struct NullCarver {
+    Sizer s;
+    template <typename T>
+    T* take(size_t k) {
+        s.take<T>(k);
+        return nullptr;
+    }
+};
+
+// Window of tile t: the largest w with win_off[w] <= t.
+__device__ __forceinline__ int64_t tile_window(const int64_t* __restrict__ win_off, int64_t W, int64_t t) {
+    int64_t lo = 0, hi = W - 1;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (win_off[mid] <= t) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// 16-bit value bits of slot (t, r, c): nonzero bits are kept (as the packed
+// tiles keep them).
+__device__ __forceinline__ uint32_t value_bits(const uint16_t* __restrict__ vals, int64_t t, int r, int c, int tc) {
+    return vals[(t * 16 + r) * tc + c];
+}
+
+// Key of every slot: (group << cbits | column), or the invalid flag for a
+// padding slot or a column outside [0, num_cols).
+__global__ void grp_keys_kernel(const int64_t* __restrict__ win_off, int64_t W, const int32_t* __restrict__ cols,
+                                int64_t n, int tc, int64_t num_cols, int G, int cbits, int vbit,
+                                uint64_t* __restrict__ keys, uint32_t* __restrict__ pay) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int32_t c = cols[i];
+    uint64_t k = 1ull << vbit;
+    if (c >= 0 && (int64_t)c < num_cols) {
+        const int64_t w = tile_window(win_off, W, i / tc);
+        k = ((uint64_t)(w / G) << cbits) | (uint64_t)c;
+    }
+    keys[i] = k;
+    pay[i] = (uint32_t)i;
+}
+
+__global__ void grp_unique_kernel(const uint64_t* __restrict__ keys, int64_t n, int vbit, int32_t* __restrict__ uflag) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t k = keys[i];
+    uflag[i] = ((k >> vbit) == 0 && (i == 0 || keys[i - 1] != k)) ? 1 : 0;
+}
+
+// First and one-past-last distinct rank of every group present.
+__global__ void grp_bounds_kernel(const uint64_t* __restrict__ keys, int64_t n, int vbit, int cbits,
+                                  const int32_t* __restrict__ uflag, const int64_t* __restrict__ uidx,
+                                  int64_t* __restrict__ gfirst, int64_t* __restrict__ glast) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t k = keys[i];
+    if ((k >> vbit) != 0) return;
+    const uint64_t q = k >> cbits;
+    if (i == 0 || (keys[i - 1] >> cbits) != q) gfirst[q] = uidx[i];
+    if (i == n - 1 || (keys[i + 1] >> cbits) != q) glast[q] = uidx[i] + uflag[i];
+}
+
+__global__ void grp_slabs_kernel(const int64_t* __restrict__ gfirst, const int64_t* __restrict__ glast, int64_t Q,
+                                 int32_t* __restrict__ gslabs, int64_t* __restrict__ stats) {
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    const int64_t u = glast[q] - gfirst[q];
+    const int32_t s = (int32_t)((u + 15) / 16);
+    gslabs[q] = s;
+    if (s > 0) atomicMax((unsigned long long*)&stats[1], (unsigned long long)s);
+}
+
+// Nonzero values at valid columns (one wave per tile; lane l: row l / 4,
+// columns 4 (l % 4) .. +3 at tc 16, or rows (l / 2), columns 4 (l % 2) at tc 8).
+__global__ __launch_bounds__(256) void grp_count_values_kernel(const int32_t* __restrict__ cols,
+                                                               const uint16_t* __restrict__ vals, int64_t T, int tc,
+                                                               int64_t num_cols, int64_t* __restrict__ stats) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;  // uniform per wave
+    const int lane = threadIdx.x & 63;
+    const int per = 16 * tc / 64;  // slots per lane: 4 (tc 16) or 2 (tc 8)
+    int cnt = 0;
+    for (int j = 0; j < per; ++j) {
+        const int slot = lane * per + j;
+        const int r = slot / tc, c = slot % tc;
+        const int32_t col = cols[t * tc + c];
+        if (col >= 0 && (int64_t)col < num_cols && value_bits(vals, t, r, c, tc) != 0) ++cnt;
+    }
+    for (int d = 32; d > 0; d >>= 1) cnt += __shfl_xor(cnt, d, 64);
+    if (lane == 0 && cnt) atomicAdd((unsigned long long*)&stats[0], (unsigned long long)cnt);
+}
+
+// Every valid sorted slot: its (slab, position); the group's union column.
+__global__ void grp_place_kernel(const uint64_t* __restrict__ keys, const uint32_t* __restrict__ pay, int64_t n,
+                                 int vbit, int cbits, const int32_t* __restrict__ uflag,
+                                 const int64_t* __restrict__ uidx, const int64_t* __restrict__ gfirst,
+                                 const int64_t* __restrict__ goff, uint32_t* __restrict__ pos,
+                                 int32_t* __restrict__ gcols) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t k = keys[i];
+    if ((k >> vbit) != 0) return;
+    const uint64_t q = k >> cbits;
+    const int64_t u = uidx[i] + uflag[i] - 1;  // rank of this distinct (group, column)
+    const int64_t p = u - gfirst[q];
+    const int64_t slab = goff[q] + p / 16;
+    const int cc = (int)(p % 16);
+    pos[pay[i]] = (uint32_t)(slab * 16 + cc);
+    if (uflag[i]) gcols[slab * 16 + cc] = (int32_t)(k & ((1ull << cbits) - 1ull));
+}
+
+// Sub-tile slot of a nonzero at (tile t, row r, column slot c): header word
+// and bit.  Row group g = r / 4 holds mask bits (r % 4) * 16 + position.
+struct SubSlot {
+    int64_t sub;  // slab * G + window in group
+    int g, bit;
+};
+
+__device__ __forceinline__ SubSlot sub_slot(const uint32_t* __restrict__ pos, int64_t w, int G, int64_t t, int r,
+                                            int c, int tc) {
+    const uint32_t p = pos[t * tc + c];
+    SubSlot s;
+    s.sub = (int64_t)(p >> 4) * G + (w % G);
+    s.g = r >> 2;
+    s.bit = (r & 3) * 16 + (int)(p & 15u);
+    return s;
+}
+
+// Masks (atomic OR; the header starts zeroed).  One wave per tile.
+__global__ __launch_bounds__(256) void grp_mask_kernel(const int64_t* __restrict__ win_off, int64_t W,
+                                                       const int32_t* __restrict__ cols,
+                                                       const uint16_t* __restrict__ vals, int64_t T, int tc,
+                                                       int64_t num_cols, int G, const uint32_t* __restrict__ pos,
+                                                       uint32_t* __restrict__ hdr) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;  // uniform per wave
+    const int lane = threadIdx.x & 63;
+    const int64_t w = tile_window(win_off, W, t);
+    const int per = 16 * tc / 64;
+    for (int j = 0; j < per; ++j) {
+        const int slot = lane * per + j;
+        const int r = slot / tc, c = slot % tc;
+        const int32_t col = cols[t * tc + c];
+        if (col < 0 || (int64_t)col >= num_cols || value_bits(vals, t, r, c, tc) == 0) continue;
+        const SubSlot s = sub_slot(pos, w, G, t, r, c, tc);
+        atomicOr(&hdr[s.sub * 12 + s.g * 3 + (s.bit >> 5)], 1u << (s.bit & 31));
+    }
+}
+
+__global__ void grp_sub_count_kernel(const uint32_t* __restrict__ hdr, int64_t nsub, int32_t* __restrict__ scnt) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nsub) return;
+    int c = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) c += __popc(hdr[i * 12 + g * 3]) + __popc(hdr[i * 12 + g * 3 + 1]);
+    scnt[i] = c;
+}
+
+__global__ void grp_sub_start_kernel(uint32_t* __restrict__ hdr, int64_t nsub, const int64_t* __restrict__ soff) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nsub) return;
+    uint32_t run = (uint32_t)soff[i];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        hdr[i * 12 + g * 3 + 2] = run;
+        run += __popc(hdr[i * 12 + g * 3]) + __popc(hdr[i * 12 + g * 3 + 1]);
+    }
+}
+
+// Every nonzero to its place: the group start plus the mask bits below it.
+__global__ __launch_bounds__(256) void grp_values_kernel(const int64_t* __restrict__ win_off, int64_t W,
+                                                         const int32_t* __restrict__ cols,
+                                                         const uint16_t* __restrict__ vals, int64_t T, int tc,
+                                                         int64_t num_cols, int G, const uint32_t* __restrict__ pos,
+                                                         const uint32_t* __restrict__ hdr, uint16_t* __restrict__ out,
+                                                         int64_t num_values) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;  // uniform per wave
+    const int lane = threadIdx.x & 63;
+    const int64_t w = tile_window(win_off, W, t);
+    const int per = 16 * tc / 64;
+    for (int j = 0; j < per; ++j) {
+        const int slot = lane * per + j;
+        const int r = slot / tc, c = slot % tc;
+        const int32_t col = cols[t * tc + c];
+        if (col < 0 || (int64_t)col >= num_cols) continue;
+        const uint32_t v = value_bits(vals, t, r, c, tc);
+        if (v == 0) continue;
+        const SubSlot s = sub_slot(pos, w, G, t, r, c, tc);
+        const uint32_t* h = hdr + s.sub * 12 + s.g * 3;
+        const uint64_t m = ((uint64_t)h[1] << 32) | h[0];
+        const uint64_t below = s.bit ? (m & ((1ull << s.bit) - 1ull)) : 0ull;
+        const int64_t at = (int64_t)h[2] + __popcll(below);
+        if (at < num_values) out[at] = (uint16_t)v;
+    }
+}
+
+__global__ void copy_i64_dev_kernel(const int64_t* __restrict__ a, int64_t n, int64_t* __restrict__ b) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) b[i] = a[i];
+}
+
+int check_group_args(const grws_bcsr* A, int64_t num_cols, int32_t G) {
+    GRWS_CHECK_ARG(A != nullptr, "group_tiles: null graph");
+    GRWS_CHECK_ARG(A->tile_rows == 16 && (A->tile_cols == 16 || A->tile_cols == 8),
+                   "group_tiles: tiles must be 16x16 or 16x8");
+    if (A->values_dtype != GRWS_F16 && A->values_dtype != GRWS_BF16)
+        return set_error(GRWS_E_DTYPE, "group_tiles: values must be F16 or BF16");
+    GRWS_CHECK_ARG(G == 2 || G == 4 || G == 8, "group_tiles: group_size must be 2, 4 or 8 (got %d)", G);
+    GRWS_CHECK_ARG(A->num_windows >= 0 && A->num_tiles >= 0 && num_cols >= 0, "group_tiles: negative size");
+    GRWS_CHECK_ARG(A->num_tiles * A->tile_cols < ((int64_t)1 << 32), "group_tiles: more than 2^32 tile slots");
+    GRWS_CHECK_ARG(num_cols <= INT32_MAX, "group_tiles: num_cols exceeds int32 column ids");
+    if (A->num_tiles > 0)
+        GRWS_CHECK_ARG(A->window_offset && A->col_indices && A->values, "group_tiles: null arrays");
+    return GRWS_OK;
+}
+
+}  // namespace
+}  // namespace grws
+
+using namespace grws;
+
+extern "C" size_t grws_group_tiles_workspace_bytes(const grws_bcsr* A, int64_t num_cols, int32_t group_size) {
+    if (!A || A->num_windows < 0 || A->num_tiles < 0 || num_cols < 0) return 0;
+    if (group_size != 2 && group_size != 4 && group_size != 8) return 0;
+    const GroupShape s = group_shape(A, num_cols, group_size);
+    NullCarver nc;
+    GroupWs w;
+    carve_group(nc, s, &w);
+    // sub-tile counts and offsets (at most (tiles + groups) * G sub-tiles)
+    const int64_t subs = (A->num_tiles + s.Q) * group_size;
+    nc.s.take<int32_t>(subs + 1);
+    nc.s.take<int64_t>(subs + 2);
+    return nc.s.used + 256;
+}
+
+extern "C" int grws_group_tiles_count(const grws_bcsr* A, int64_t num_cols, int32_t group_size, void* workspace,
+                                      size_t workspace_bytes, int64_t* num_slabs, int64_t* num_values,
+                                      int64_t* max_group_slabs, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_TRY(check_group_args(A, num_cols, group_size));
+    GRWS_CHECK_ARG(num_slabs && num_values && max_group_slabs, "group_tiles_count: null output");
+    const GroupShape s = group_shape(A, num_cols, group_size);
+    Carver cv(workspace, workspace_bytes);
+    GroupWs w;
+    carve_group(cv, s, &w);
+    if (!cv.ok)
+        return set_error(GRWS_E_CAPACITY, "group_tiles: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+    const int vbit = s.bits - 1;
+    const int tc = A->tile_cols;
+    GRWS_TRY(fill_i64(w.gfirst, s.Q + 1, 0, stream));
+    GRWS_TRY(fill_i64(w.glast, s.Q + 1, 0, stream));
+    GRWS_TRY(fill_i64(w.stats, 4, 0, stream));
+    w.alt = false;
+    if (s.n > 0) {
+        hipLaunchKernelGGL(grp_keys_kernel, dim3(grid_for(s.n)), dim3(kBlk), 0, stream, A->window_offset,
+                           A->num_windows, A->col_indices, s.n, tc, num_cols, group_size, s.cbits, vbit, w.ka, w.va);
+        GRWS_LAUNCH_CHECK();
+        GRWS_TRY(radix_sort_pairs(w.ka, w.va, w.kb, w.vb, s.n, s.bits, w.sort_ws, w.sort_bytes, stream, &w.alt));
+        const uint64_t* k = w.alt ? w.kb : w.ka;
+        hipLaunchKernelGGL(grp_unique_kernel, dim3(grid_for(s.n)), dim3(kBlk), 0, stream, k, s.n, vbit, w.uflag);
+        GRWS_LAUNCH_CHECK();
+        GRWS_TRY(scan_i32_to_i64(w.uflag, w.uidx, s.n, false, w.scan_ws, w.scan_bytes, stream));
+        hipLaunchKernelGGL(grp_bounds_kernel, dim3(grid_for(s.n)), dim3(kBlk), 0, stream, k, s.n, vbit, s.cbits,
+                           w.uflag, w.uidx, w.gfirst, w.glast);
+        GRWS_LAUNCH_CHECK();
+        hipLaunchKernelGGL(grp_count_values_kernel, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream,
+                           A->col_indices, static_cast<const uint16_t*>(A->values), A->num_tiles, tc, num_cols,
+                           w.stats);
+        GRWS_LAUNCH_CHECK();
+    }
+    hipLaunchKernelGGL(grp_slabs_kernel, dim3(grid_for(s.Q)), dim3(kBlk), 0, stream, w.gfirst, w.glast, s.Q,
+                       w.gslabs, w.stats);
+    GRWS_LAUNCH_CHECK();
+    GRWS_TRY(scan_i32_to_i64(w.gslabs, w.goff, s.Q, false, w.scan_ws, w.scan_bytes, stream));
+    int64_t h[3] = {0, 0, 0};
+    GRWS_HIP(hipMemcpyAsync(&h[0], w.goff + s.Q, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipMemcpyAsync(&h[1], w.stats, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipStreamSynchronize(stream));
+    *num_slabs = h[0];
+    *num_values = h[1];
+    *max_group_slabs = h[2];
+    if (h[0] * 16 >= ((int64_t)1 << 32))
+        return set_error(GRWS_E_CAPACITY, "group_tiles: %lld slabs exceed 32-bit slot positions", (long long)h[0]);
+    return GRWS_OK;
+}
+
+extern "C" int grws_group_tiles_fill(const grws_bcsr* A, int64_t num_cols, int32_t group_size, int64_t num_slabs,
+                                     int64_t* group_offset, int32_t* col_indices, uint32_t* header, void* values,
+                                     int64_t num_values, void* workspace, size_t workspace_bytes, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_TRY(check_group_args(A, num_cols, group_size));
+    const GroupShape s = group_shape(A, num_cols, group_size);
+    GRWS_CHECK_ARG(num_slabs >= 0 && num_slabs <= A->num_tiles + s.Q, "group_tiles_fill: bad num_slabs %lld",
+                   (long long)num_slabs);
+    GRWS_CHECK_ARG(num_values >= 0, "group_tiles_fill: negative num_values");
+    GRWS_CHECK_ARG(group_offset != nullptr, "group_tiles_fill: null group_offset");
+    if (num_slabs > 0) GRWS_CHECK_ARG(col_indices && header, "group_tiles_fill: null outputs");
+    if (num_values > 0) GRWS_CHECK_ARG(values != nullptr, "group_tiles_fill: null values");
+    Carver cv(workspace, workspace_bytes);
+    GroupWs w;
+    carve_group(cv, s, &w);
+    const int64_t nsub = num_slabs * group_size;
+    w.scnt = cv.take<int32_t>((A->num_tiles + s.Q) * group_size + 1);
+    w.soff = cv.take<int64_t>((A->num_tiles + s.Q) * group_size + 2);
+    if (!cv.ok)
+        return set_error(GRWS_E_CAPACITY, "group_tiles: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+    const int vbit = s.bits - 1;
+    const int tc = A->tile_cols;
+    // the count pass's sort result: the pass count decides the buffer
+    const int passes = (s.bits + 7) / 8;
+    const bool alt = s.n > 1 && (passes & 1);
+    const uint64_t* k = alt ? w.kb : w.ka;
+    const uint32_t* v = alt ? w.vb : w.va;
+    hipLaunchKernelGGL(copy_i64_dev_kernel, dim3(grid_for(s.Q + 1)), dim3(kBlk), 0, stream, w.goff, s.Q + 1,
+                       group_offset);
+    GRWS_LAUNCH_CHECK();
+    if (num_slabs == 0) return GRWS_OK;
+    GRWS_TRY(fill_i32(col_indices, num_slabs * 16, -1, stream));
+    GRWS_TRY(fill_bytes_zero(header, (size_t)nsub * 12 * sizeof(uint32_t), stream));
+    if (s.n == 0) return GRWS_OK;
+    hipLaunchKernelGGL(grp_place_kernel, dim3(grid_for(s.n)), dim3(kBlk), 0, stream, k, v, s.n, vbit, s.cbits,
+                       w.uflag, w.uidx, w.gfirst, w.goff, w.pos, col_indices);
+    GRWS_LAUNCH_CHECK();
+    const uint16_t* vals = static_cast<const uint16_t*>(A->values);
+    hipLaunchKernelGGL(grp_mask_kernel, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, A->window_offset,
+                       A->num_windows, A->col_indices, vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos,
+                       header);
+    GRWS_LAUNCH_CHECK();
+    hipLaunchKernelGGL(grp_sub_count_kernel, dim3(grid_for(nsub)), dim3(kBlk), 0, stream, header, nsub, w.scnt);
+    GRWS_LAUNCH_CHECK();
+    GRWS_TRY(scan_i32_to_i64(w.scnt, w.soff, nsub, false, w.scan_ws, w.scan_bytes, stream));
+    hipLaunchKernelGGL(grp_sub_start_kernel, dim3(grid_for(nsub)), dim3(kBlk), 0, stream, header, nsub, w.soff);
+    GRWS_LAUNCH_CHECK();
+    hipLaunchKernelGGL(grp_values_kernel, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, A->window_offset,
+                       A->num_windows, A->col_indices, vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos,
+                       header, static_cast<uint16_t*>(values), num_values);
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}

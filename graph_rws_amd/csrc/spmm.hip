@@ -119,6 +119,10 @@ struct SpmmArgs {
     // buffer path, 16-bit X and values, chunks of 64+ columns: gather
     // 128-byte segments of 8 rows per instruction
     int32_t narrow;
+    // grouped tiles: union slabs of group q are [goff[q], goff[q+1]); the
+    // group's windows are q G .. q G + G - 1 (those below num_windows)
+    const int64_t* goff;
+    int64_t num_windows;
 };
 
 // Output conversion for the three element types.
@@ -781,6 +785,231 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(NBLK =
     spmm_epilogue<XT, NBLK, WPB>(a, acc, stage_all, wave, lane, w, slot, chunk, n0);
 }
 
+// Grouped tiles (group.hip builds them): G consecutive windows share one
+// sorted list of their columns in slabs of 16 and keep one packed 16x16
+// sub-tile each per slab (same packing as PK above).  A work-group of GW
+// waves takes one group and one N-chunk; each wave owns WPW of the group's
+// windows (G = WPW GW).  Per slab the waves gather the slab's 16 X rows
+// once, wave h the rows [h 16/GW, (h+1) 16/GW) in 128-byte segments of 8
+// rows per instruction, into LDS; then every wave multiplies each staged
+// 16-column block by its windows' sub-tiles, one transposing LDS read
+// serving WPW MFMAs.  With GW > 1 the stage is double buffered and one
+// barrier per slab orders its writes before its reads (a buffer is written
+// again two slabs later, after every wave passed the barrier in between).
+template <int XT, int NBLK, int WPW, int GW, int PF>
+__global__ __launch_bounds__(64 * GW) void spmm_grp_kernel(SpmmArgs a) {
+    static_assert(XT == GRWS_F16 || XT == GRWS_BF16, "grouped tiles: 16-bit X and values");
+    static_assert(GW == 1 || GW == 2 || GW == 4, "waves per group");
+    static_assert(PF >= 1 && PF <= 2, "prefetch depth 1..2");
+    constexpr int G = WPW * GW;
+    constexpr int NC = NBLK * 16;
+    constexpr int SEGS = NC / 64;       // 128-byte segments per staged row
+    constexpr int RPW = 16 / GW;        // staged rows each wave gathers
+    constexpr int NLD = RPW * SEGS / 8; // gather instructions per wave and slab
+    static_assert(NC % 64 == 0 && (RPW * SEGS) % 8 == 0, "whole 8-segment instructions per wave");
+    constexpr int PITCH = NC + 16;
+    constexpr int NST = GW > 1 ? 2 : 1;
+    constexpr int R = PF + 1;
+    using S = typename XTraits<XT>::S;
+    using ColV = typename std::conditional<GW == 1, i32x2_t, int32_t>::type;
+    __shared__ __attribute__((aligned(16))) S stage_all[NST * 16 * PITCH];
+
+    const int wave = GW > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;
+    const int lane = threadIdx.x & 63;
+    // chunk-major: every XCD walks chunk 0's groups (its own range), then chunk 1's
+    const int64_t ipc = (a.num_items + 7) & ~(int64_t)7;
+    const int chunk = (int)(blockIdx.x / ipc);
+    const int64_t rr = (int64_t)blockIdx.x - (int64_t)chunk * ipc;
+    const int64_t q = (rr & 7) * (ipc >> 3) + (rr >> 3);
+    if (chunk >= a.nchunks || q >= a.num_items) return;  // uniform over the work-group
+    const int64_t g0 = a.goff[q];
+    const int64_t nslabs = a.goff[q + 1] - g0;
+    const int64_t n0 = a.col_base + (int64_t)chunk * NC;
+
+    const __amdgpu_buffer_rsrc_t rsC = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.cols + g0 * 16), (short)0, (int)(nslabs * 64), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsH = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.hdr + g0 * G * 12), (short)0, (int)(nslabs * G * 48), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsV =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.pvals), (short)0, (int)a.pv_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsX =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.x), (short)0, (int)a.x_bytes, 0x00020000);
+
+    // gather instruction i of this wave covers its row segments 8 i .. 8 i + 7;
+    // lane l takes segment 8 i + l / 8: staged row and first element
+    auto row_of = [&](int i) { return wave * RPW + (8 * i + (lane >> 3)) % RPW; };
+    auto elem_of = [&](int i) { return 64 * ((8 * i + (lane >> 3)) / RPW) + 8 * (lane & 7); };
+    bool lcol[NLD];
+    uint32_t colb[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        lcol[i] = n0 + elem_of(i) < a.n_cols;
+        colb[i] = lcol[i] ? (uint32_t)((n0 + elem_of(i)) * 2) : 0u;
+    }
+    const uint32_t ldxb = (uint32_t)(a.ldx * 2);
+    const uint32_t xr = (uint32_t)a.x_rows;
+    const int ag = lane >> 4;
+    const int ar = lane & 15;
+    const int tr_off = (4 * ag + ((lane & 15) >> 2)) * PITCH + 4 * (lane & 3);
+    const uint32_t h_lane = (uint32_t)(ar >> 2) * 12;
+    const uint32_t bitoff = (uint32_t)((ar & 3) * 16 + 4 * ag);
+
+    // the lane's column indices of slab s: rows lane/8 and 8 + lane/8 (GW 1),
+    // else its one staged row; past the group the range check returns 0
+    auto load_cols = [&](int64_t s) -> ColV {
+        if constexpr (GW == 1) {
+            const uint32_t off = (uint32_t)(s * 64) + (uint32_t)(lane >> 3) * 4;
+            return ColV{(int32_t)__builtin_amdgcn_raw_buffer_load_b32(rsC, (int)off, 0, 2),
+                        (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rsC, (int)(off + 32), 0, 2)};
+        } else {
+            const uint32_t off = (uint32_t)(s * 64) + (uint32_t)(wave * RPW + (lane >> 3) % RPW) * 4;
+            return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rsC, (int)off, 0, 2);
+        }
+    };
+    auto load_x = [&](const ColV cv, u32x4_t* regs) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            int32_t c;
+            if constexpr (GW == 1) c = cv[i & 1]; else c = cv;
+            const bool ok = lcol[i] && (uint32_t)c < xr;
+            const uint32_t row = ok ? (uint32_t)c : xr;  // row x_rows lies past the resource
+            regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rsX, (int)(__umul24(row, ldxb) + colb[i]), 0, 0);
+        }
+    };
+    // window wi's 48-byte sub-tile header in slab s: in every quad of lanes
+    // (one row group: lanes 4g..4g+3 of each row of 16) the first three
+    // load the group's {mask_lo, mask_hi, start}, one word each, and
+    // broadcast them over the quad (DPP quad permutes: no LDS, no SMEM)
+    const uint32_t hword = (uint32_t)(3 * ((lane & 15) >> 2) + ((lane & 3) < 2 ? (lane & 3) : 2)) * 4;
+    auto load_hdr = [&](int64_t s, int wi) -> uint32_t {
+        return __builtin_amdgcn_raw_buffer_load_b32(rsH, (int)((uint32_t)((s * G + wave * WPW + wi) * 48) + hword), 0, 2);
+    };
+    auto lane_hdr = [&](const uint32_t raw) -> u32x3_t {
+        return u32x3_t{(uint32_t)__builtin_amdgcn_mov_dpp((int)raw, 0x00, 0xf, 0xf, false),
+                       (uint32_t)__builtin_amdgcn_mov_dpp((int)raw, 0x55, 0xf, 0xf, false),
+                       (uint32_t)__builtin_amdgcn_mov_dpp((int)raw, 0xaa, 0xf, 0xf, false)};
+    };
+    auto load_a = [&](const u32x3_t h) -> u32x4_t {
+        const uint64_t m = ((uint64_t)h[1] << 32) | h[0];
+        const uint32_t below = (uint32_t)__builtin_popcountll(m & ((1ull << bitoff) - 1));
+        const uint32_t nib = (uint32_t)(m >> bitoff) & 15u;
+        const uint32_t hidx = h[2] + below;
+        const uint32_t off = nib ? (hidx & ~1u) * 2u : 0x80000000u;  // empty: no read
+        const u32x3_t d = __builtin_amdgcn_raw_buffer_load_b96(rsV, (int)off, 0, 2);
+        return u32x4_t{d[0], d[1], d[2], nib | ((hidx & 1u) << 4)};
+    };
+    auto decode = [&](const u32x4_t v) -> short4_t {
+        const uint32_t info = v[3];
+        const uint32_t sh = (info >> 4) * 16u;
+        const uint32_t r0 = __builtin_amdgcn_alignbit(v[1], v[0], sh);
+        const uint32_t r1 = __builtin_amdgcn_alignbit(v[2], v[1], sh);
+        const uint32_t b0 = info & 1u, b1 = (info >> 1) & 1u, b2 = (info >> 2) & 1u, b3 = (info >> 3) & 1u;
+        const uint32_t k2 = b0 + b1, k3 = k2 + b2;
+        const uint32_t s0 = b0 ? 0x0100u : 0x0c0cu;
+        const uint32_t s1 = b1 ? 0x0100u + 0x0202u * b0 : 0x0c0cu;
+        const uint32_t s2 = b2 ? 0x0100u + 0x0202u * k2 : 0x0c0cu;
+        const uint32_t s3 = b3 ? 0x0100u + 0x0202u * k3 : 0x0c0cu;
+        return __builtin_bit_cast(short4_t, u32x2_t{__builtin_amdgcn_perm(r1, r0, s0 | (s1 << 16)),
+                                                    __builtin_amdgcn_perm(r1, r0, s2 | (s3 << 16))});
+    };
+
+    float4_t acc[WPW][NBLK];
+#pragma unroll
+    for (int w = 0; w < WPW; ++w)
+#pragma unroll
+        for (int b = 0; b < NBLK; ++b) acc[w][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto consume = [&](int buf, const u32x4_t* xb, const u32x4_t* av) {
+        S* st = stage_all + buf * (16 * PITCH);
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) *reinterpret_cast<u32x4_t*>(&st[row_of(i) * PITCH + elem_of(i)]) = xb[i];
+        if constexpr (GW > 1) {
+            __syncthreads();
+        } else {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        short4_t af[WPW];
+#pragma unroll
+        for (int w = 0; w < WPW; ++w) af[w] = decode(av[w]);
+#pragma unroll
+        for (int b = 0; b < NBLK; ++b) {
+            lds_ptr_t p = (lds_ptr_t)(st + tr_off + 16 * b);
+            if constexpr (XT == GRWS_F16) {
+                const half4_t bf =
+                    __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4f16_t*)p));
+#pragma unroll
+                for (int w = 0; w < WPW; ++w)
+                    acc[w][b] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, af[w]), bf,
+                                                                      acc[w][b], 0, 0, 0);
+            } else {
+                const short4_t bf =
+                    __builtin_bit_cast(short4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf16_t*)p));
+#pragma unroll
+                for (int w = 0; w < WPW; ++w)
+                    acc[w][b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(af[w], bf, acc[w][b], 0, 0, 0);
+            }
+        }
+        if constexpr (GW == 1) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    };
+
+    if (nslabs > 0 && xr > 0) {  // uniform over the work-group
+        // ring of R slots: column indices and headers R slabs ahead, X rows
+        // and A values PF slabs ahead of the slab multiplied
+        u32x4_t xbuf[R][NLD];
+        u32x4_t abuf[R][WPW];
+        ColV cring[R];
+        uint32_t hring[R][WPW];
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            cring[k] = load_cols(k);
+#pragma unroll
+            for (int w = 0; w < WPW; ++w) hring[k][w] = load_hdr(k, w);
+        }
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+            load_x(cring[k], xbuf[k]);
+#pragma unroll
+            for (int w = 0; w < WPW; ++w) abuf[k][w] = load_a(lane_hdr(hring[k][w]));
+        }
+        auto step = [&](const int u, const int64_t s) {
+            const int ps = (u + PF) % R;
+            cring[u] = load_cols(s + R);
+#pragma unroll
+            for (int w = 0; w < WPW; ++w) hring[u][w] = load_hdr(s + R, w);
+            load_x(cring[ps], xbuf[ps]);
+#pragma unroll
+            for (int w = 0; w < WPW; ++w) abuf[ps][w] = load_a(lane_hdr(hring[ps][w]));
+            consume(NST > 1 ? (int)(s & 1) : 0, xbuf[u], abuf[u]);
+        };
+        const int64_t nturns = nslabs / R;
+        int64_t s = 0;
+        for (int64_t t = 0; t < nturns; ++t) {
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                step(u, s);
+                ++s;
+            }
+        }
+        const int rest = (int)(nslabs - nturns * R);
+#pragma unroll
+        for (int u = 0; u < R - 1; ++u) {
+            if (u < rest) step(u, s);
+            ++s;
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < WPW; ++w) {
+        const int64_t win = q * G + wave * WPW + w;
+        if (win < a.num_windows) spmm_epilogue<XT, NBLK, 1>(a, acc[w], stage_all, 0, lane, win, -1, chunk, n0);
+    }
+}
+
 // Sums the partial slots of each split window in slot order (deterministic).
 // One wave per 256 floats of a (split window, chunk) block: NBLK waves per
 // block, lane l owns 4 consecutive floats (one row, 4 columns).  A hub
@@ -1407,6 +1636,136 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
     return GRWS_OK;
 }
 }  // namespace
+
+namespace {
+template <int XT, int NBLK, int WPW, int GW>
+int launch_grp(const SpmmArgs& a, hipStream_t stream) {
+    const int64_t ipc = (a.num_items + 7) & ~(int64_t)7;
+    const int64_t grid = ipc * a.nchunks;
+    if (grid <= 0) return GRWS_OK;
+    if (grid > INT32_MAX) return set_error(GRWS_E_INVALID, "spmm_grouped: grid too large");
+    // two waves per group: X rows two slabs ahead (more bytes in flight per
+    // CU; measured 5.54 against 5.73 ms on c3 at N = 608)
+    constexpr int PF = GW == 2 ? 2 : 1;
+    hipLaunchKernelGGL((spmm_grp_kernel<XT, NBLK, WPW, GW, PF>), dim3((unsigned)grid), dim3(64 * GW), 0, stream, a);
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
+// Kernel shapes per group size: (windows per wave, waves per group) and the
+// column blocks per chunk.  NBLK 20 needs whole 8-segment instructions per
+// wave (GW 1 or 2); WPW 4 keeps to NBLK 8 (128 accumulator registers).
+template <int XT>
+int dispatch_grp(const SpmmArgs& a, int G, int wpw, int nblk, hipStream_t stream) {
+    const int gw = G / wpw;
+#define GRWS_GRP(W_, GW_, NB_) \
+    if (wpw == W_ && gw == GW_ && nblk == NB_) return launch_grp<XT, NB_, W_, GW_>(a, stream)
+    GRWS_GRP(1, 2, 8); GRWS_GRP(1, 2, 16); GRWS_GRP(1, 2, 20);
+    GRWS_GRP(2, 1, 8); GRWS_GRP(2, 1, 16); GRWS_GRP(2, 1, 20);
+    GRWS_GRP(1, 4, 8); GRWS_GRP(1, 4, 16);
+    GRWS_GRP(2, 2, 8); GRWS_GRP(2, 2, 16); GRWS_GRP(2, 2, 20);
+    GRWS_GRP(4, 1, 8);
+    GRWS_GRP(2, 4, 8); GRWS_GRP(2, 4, 16);
+    GRWS_GRP(4, 2, 8);
+#undef GRWS_GRP
+    return set_error(GRWS_E_INVALID, "spmm_grouped: no kernel for group %d, %d windows per wave, %d blocks", G, wpw,
+                     nblk);
+}
+}  // namespace
+
+extern "C" int grws_spmm_grouped(const grws_bcsr* A, const grws_grouped_tiles* Gt, const void* x, int32_t x_dtype,
+                                 int64_t x_rows, int64_t ldx, int64_t n_cols, const void* r, int64_t ldr,
+                                 int64_t r_rows, void* y, int32_t y_dtype, int64_t ldy, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(A != nullptr && Gt != nullptr, "spmm_grouped: null graph or grouped tiles");
+    GRWS_CHECK_ARG(A->tile_rows == 16, "spmm_grouped: tile_rows must be 16");
+    if (x_dtype != GRWS_F16 && x_dtype != GRWS_BF16)
+        return set_error(GRWS_E_DTYPE, "spmm_grouped: x must be F16 or BF16 (got %d)", x_dtype);
+    if (y_dtype != x_dtype || A->values_dtype != x_dtype)
+        return set_error(GRWS_E_DTYPE, "spmm_grouped: y and the values must have the x dtype");
+    const int G = Gt->group_size;
+    GRWS_CHECK_ARG(G == 2 || G == 4 || G == 8, "spmm_grouped: group_size must be 2, 4 or 8 (got %d)", G);
+    GRWS_CHECK_ARG(Gt->num_groups == (A->num_windows + G - 1) / G, "spmm_grouped: %lld groups for %lld windows",
+                   (long long)Gt->num_groups, (long long)A->num_windows);
+    GRWS_CHECK_ARG(n_cols >= 0 && x_rows >= 0 && Gt->num_slabs >= 0 && Gt->num_values >= 0,
+                   "spmm_grouped: negative size");
+    GRWS_CHECK_ARG(x_rows <= Gt->num_cols, "spmm_grouped: x has %lld rows, the tiles were grouped for %lld columns",
+                   (long long)x_rows, (long long)Gt->num_cols);
+    GRWS_CHECK_ARG(Gt->num_values <= kPackMaxValues, "spmm_grouped: too many values (%lld)",
+                   (long long)Gt->num_values);
+    GRWS_CHECK_ARG(Gt->max_group_slabs >= 0 && Gt->max_group_slabs * G * 48 < ((int64_t)1 << 31),
+                   "spmm_grouped: a group's headers exceed 2^31 bytes");
+    if (A->num_windows == 0 || n_cols == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(Gt->group_offset && y, "spmm_grouped: null pointer");
+    if (Gt->num_slabs > 0) GRWS_CHECK_ARG(Gt->col_indices && Gt->header, "spmm_grouped: null tile arrays");
+    if (Gt->num_values > 0) GRWS_CHECK_ARG(Gt->values != nullptr, "spmm_grouped: null values");
+    GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(Gt->header) % 4 == 0, "spmm_grouped: header not 4-byte aligned");
+    GRWS_CHECK_ARG(ldy >= n_cols, "spmm_grouped: ldy < n_cols");
+    GRWS_CHECK_ARG(x_rows > 0 && x != nullptr && ldx >= n_cols, "spmm_grouped: bad x (empty, null or ldx < n_cols)");
+    GRWS_CHECK_ARG(n_cols % 8 == 0 && ldx % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0,
+                   "spmm_grouped: x needs 16-byte rows (n_cols and ldx multiples of 8, 16-byte aligned)");
+    GRWS_CHECK_ARG(x_rows < (1 << 24) && ldx * 2 < (1 << 24), "spmm_grouped: x exceeds 2^24 rows or row bytes");
+    GRWS_CHECK_ARG((x_rows + 1) * ldx * 2 + 320 * 2 < ((int64_t)1 << 32), "spmm_grouped: x exceeds 32-bit offsets");
+
+    if (r) {
+        GRWS_CHECK_ARG(ldr >= n_cols && r_rows >= 0, "spmm_grouped: ldr < n_cols or negative r_rows");
+        GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(r) % 2 == 0, "spmm_grouped: residual not 2-byte aligned");
+    }
+
+    SpmmArgs a{};
+    a.res = r;
+    a.ldr = ldr;
+    a.res_rows = r ? r_rows : 0;
+    a.cols = Gt->col_indices;
+    a.hdr = Gt->header;
+    a.pvals = Gt->values;
+    a.pv_bytes = (uint32_t)((Gt->num_values + kPackPad) * 2);
+    a.goff = Gt->group_offset;
+    a.num_items = Gt->num_groups;
+    a.num_windows = A->num_windows;
+    a.x = x;
+    a.x_rows = x_rows;
+    a.ldx = ldx;
+    a.n_cols = n_cols;
+    a.y = y;
+    a.ldy = ldy;
+    a.x_bytes = (uint32_t)((x_rows - 1) * ldx * 2 + n_cols * 2);
+    a.chunk_major = 1;
+    // shape: windows per wave and column blocks; N above 256 not a multiple
+    // of 256 runs 320-column chunks when they stream the tiles fewer times,
+    // else 256-column chunks plus one narrower launch for the rest
+    int wpw = G == 8 ? 2 : 1;
+    int head_nblk = n_cols > 128 ? 16 : 8, tail_nblk = 8;
+    if (const char* e = getenv("GRWS_GRP_WPW")) wpw = atoi(e);  // tuning overrides
+    if (const char* e = getenv("GRWS_GRP_NBLK")) head_nblk = atoi(e);
+    if (wpw == 4) head_nblk = 8;
+    if (wpw == 4 || G / wpw == 4) tail_nblk = 8;
+    const int64_t hnc = head_nblk * 16;
+    const bool c320 = head_nblk == 16 && n_cols > 256 && n_cols % 256 != 0 && (n_cols + 319) / 320 < (n_cols + 255) / 256 &&
+                      G / wpw <= 2 && !(getenv("GRWS_GRP_C320") && atoi(getenv("GRWS_GRP_C320")) == 0);
+    int st;
+    if (c320) {
+        a.col_base = 0;
+        a.nchunks = (int32_t)((n_cols + 319) / 320);
+        st = x_dtype == GRWS_F16 ? dispatch_grp<GRWS_F16>(a, G, wpw, 20, stream)
+                                 : dispatch_grp<GRWS_BF16>(a, G, wpw, 20, stream);
+        return st;
+    }
+    const int64_t head = n_cols > hnc && n_cols % hnc != 0 ? n_cols / hnc * hnc : n_cols;
+    const int64_t parts[2][2] = {{0, head}, {head, n_cols}};
+    for (int pi = 0; pi < (head < n_cols ? 2 : 1); ++pi) {
+        const int64_t c0 = parts[pi][0], c1 = parts[pi][1];
+        int nb = pi == 0 ? head_nblk : tail_nblk;
+        if (pi == 1 && c1 - c0 > tail_nblk * 16) nb = head_nblk;
+        a.col_base = c0;
+        a.nchunks = (int32_t)((c1 - c0 + nb * 16 - 1) / (nb * 16));
+        st = x_dtype == GRWS_F16 ? dispatch_grp<GRWS_F16>(a, G, wpw, nb, stream)
+                                 : dispatch_grp<GRWS_BF16>(a, G, wpw, nb, stream);
+        if (st != GRWS_OK) return st;
+    }
+    return GRWS_OK;
+}
 
 extern "C" int grws_spmm(const grws_bcsr* A, const grws_spmm_plan* plan, const void* x, int32_t x_dtype,
                          int64_t x_rows, int64_t ldx, int64_t n_cols, void* y, int32_t y_dtype, int64_t ldy,

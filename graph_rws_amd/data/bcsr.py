@@ -278,6 +278,29 @@ class BCSRGraph:
             self._cache["packed"] = (key, 2, p)
         return p or None
 
+    def grouped_tiles(self, num_cols: int):
+        """Grouped tiles (windows sharing their union columns, see
+        core.ops.group_tiles) for products over num_cols X rows, built on
+        this graph's second such product and kept while the arrays are
+        unchanged; None when grouping is off, does not apply, or would not
+        pay on this graph (decided once per graph state)."""
+        from ..core import ops as _ops
+        if (not _ops.GROUPED or not _ops.PACK_TILES or getattr(self, "refilled", False)
+                or self.values_condensed.dtype not in (torch.float16, torch.bfloat16)):
+            return None
+        from ..core.ops import TensorKey
+        arrays = (self.window_offset, self.original_col_indices, self.values_condensed)
+        ent = self._cache.get("grouped")
+        if ent is None or not ent[0].matches(arrays, (int(num_cols),)):
+            self._cache["grouped"] = (TensorKey(arrays, (int(num_cols),)), 1, None)
+            return None
+        key, calls, g = ent
+        if g is None and calls == 1:
+            g = _ops.group_tiles(self.window_offset, self.original_col_indices, self.values_condensed,
+                                 self.tile_cols, int(num_cols)) or False
+            self._cache["grouped"] = (key, 2, g)
+        return g or None
+
     def _gather_input(self, x: torch.Tensor) -> torch.Tensor:
         """x, or a copy whose rows start on 128-byte lines when x's row pitch
         is not a multiple of 128 bytes and this graph gathers every row many
@@ -330,10 +353,15 @@ class BCSRGraph:
         nothing); plus residual on its rows when given (Y = A x + R there)."""
         from ..core import spmm as _spmm
         x = self._gather_input(x)
+        same = x.dtype == self.values_condensed.dtype
+        from ..core import ops as _ops
+        grouped = (self.grouped_tiles(x.shape[0])
+                   if _ops.grouped_supported(x, self.values_condensed) and x.shape[1] >= _ops.GROUP_MIN_N else None)
         return _spmm(self.window_offset, self.original_col_indices, self.values_condensed, x,
-                     self.tile_cols, plan=self.spmm_plan(x.shape[1]), out=out,
-                     packed=self.packed_tiles() if x.dtype == self.values_condensed.dtype else None,
-                     max_window_slabs=getattr(self, "max_window_slabs", None) or 0, residual=residual)
+                     self.tile_cols, plan=None if grouped is not None else self.spmm_plan(x.shape[1]), out=out,
+                     packed=self.packed_tiles() if same and grouped is None else None,
+                     max_window_slabs=getattr(self, "max_window_slabs", None) or 0, residual=residual,
+                     grouped=grouped)
 
     def transpose(self) -> "BCSRGraph":
         """Cached BCSR of A^T (num_cols x 16W), built on the device.  Rebuilt

@@ -180,6 +180,61 @@ int grws_spmm_packed(const grws_bcsr* A, const grws_packed_tiles* P, const grws_
                      void* y, int32_t y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Grouped tiles: A's tiles re-cut so that group_size consecutive windows    */
+/* share one sorted list of the union of their columns (16 per slab), each   */
+/* window keeping one 16x16 sub-tile per slab, packed as above.  The SpMM    */
+/* (spmm_tc.cuh:113-193 computes Y = A X window by window, gathering each    */
+/* window's columns) then gathers every union column's X row once per group  */
+/* instead of once per window: on graphs with community structure the       */
+/* windows of a group share most columns (c3, 4 windows: 74.5M column slots  */
+/* become 40.0M).  No counterpart in the reference; the dense arrays stay    */
+/* the graph of record.  Sums run over each row's columns in ascending order */
+/* as in grws_spmm, 16 union columns per MFMA step instead of 16 of the      */
+/* window's own, so fp32 rounding of the sums may differ in the last bits.   */
+/*                                                                          */
+/* Layout: group_offset int64 [num_groups+1] (slabs of group q are          */
+/* [group_offset[q], group_offset[q+1])), col_indices int32 [num_slabs*16]   */
+/* (the group's columns ascending, -1 after its last), header uint32         */
+/* [num_slabs][group_size][12] (the packed header of window q*G + i's       */
+/* sub-tile of each slab), values [num_values + 8] (A's dtype).  Built for   */
+/* columns < num_cols (others dropped); x_rows must not exceed it.           */
+/* ------------------------------------------------------------------------ */
+typedef struct grws_grouped_tiles {
+    const int64_t* group_offset;
+    const int32_t* col_indices;
+    const uint32_t* header;
+    const void* values;
+    int64_t num_groups;
+    int64_t num_slabs;
+    int64_t num_values;
+    int64_t max_group_slabs;
+    int64_t num_cols;
+    int32_t group_size; /* 2, 4 or 8 */
+} grws_grouped_tiles;
+
+/* Workspace for both build calls (tile slots: sort keys, ranks, positions). */
+size_t grws_group_tiles_workspace_bytes(const grws_bcsr* A, int64_t num_cols, int32_t group_size);
+
+/* Pass 1 (synchronises `stream`): the union columns per group; writes the
+ * host *num_slabs, *num_values and the longest group *max_group_slabs. */
+int grws_group_tiles_count(const grws_bcsr* A, int64_t num_cols, int32_t group_size, void* workspace,
+                           size_t workspace_bytes, int64_t* num_slabs, int64_t* num_values,
+                           int64_t* max_group_slabs, void* stream);
+
+/* Pass 2: writes the four arrays, reading what pass 1 left in the same,
+ * unchanged, workspace. */
+int grws_group_tiles_fill(const grws_bcsr* A, int64_t num_cols, int32_t group_size, int64_t num_slabs,
+                          int64_t* group_offset, int32_t* col_indices, uint32_t* header, void* values,
+                          int64_t num_values, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Y[16W x n_cols] = A X (+ R on rows < r_rows when r is not NULL, as in
+ * grws_spmm_residual) over grouped tiles (16-bit X, values, R and Y of one
+ * dtype; n_cols and ldx multiples of 8, X 16-byte aligned). */
+int grws_spmm_grouped(const grws_bcsr* A, const grws_grouped_tiles* Gt, const void* x, int32_t x_dtype,
+                      int64_t x_rows, int64_t ldx, int64_t n_cols, const void* r, int64_t ldr, int64_t r_rows,
+                      void* y, int32_t y_dtype, int64_t ldy, void* stream);
+
 /* Y = A X + R: as grws_spmm_packed (P may be NULL for the dense tiles),
  * with R [r_rows x ldr] in the y dtype added to rows < r_rows of the
  * product in fp32 before Y is rounded; rows >= r_rows get A X alone.  R may

@@ -55,9 +55,14 @@ def c4(cuda_device):
     return g, G, HostGraph(G)
 
 
-def test_c3_headline_n608_bench_path(c3, cuda_device):
+def test_c3_headline_n608_bench_path(c3, cuda_device, monkeypatch):
     """bench.py's timed call: X [n, 608] f16 at a 640 pitch, Y preallocated,
-    G.spmm(X, out=Y); the second product reads the packed tiles."""
+    G.spmm(X, out=Y).  The first product runs window by window on the dense
+    tiles; the second builds and reads the grouped tiles (c3 has community
+    structure: 2 windows share 74% of their column slots), the product
+    bench.py times; with grouping off the packed tiles give the first
+    product's bits."""
+    from graph_rws_amd.core import ops
     print("case c3 N=608 f16 bench path", flush=True)
     g, G, hg = c3
     X = aligned_rows(synth.features(g.num_nodes, 602, pad_to=608, seed=7, device=cuda_device).half())
@@ -68,9 +73,16 @@ def test_c3_headline_n608_bench_path(c3, cuda_device):
     G.spmm(X, out=Y1)
     G.spmm(X, out=Y2)
     torch.cuda.synchronize()
-    assert G.packed_tiles() is not None, "the second product must have packed the tiles"
-    assert torch.equal(Y1.view(torch.int16), Y2.view(torch.int16)), "packed and dense tiles differ"
+    gt = G.grouped_tiles(X.shape[0])
+    assert gt is not None and gt.slot_ratio < ops.GROUP_MAX_RATIO, "c3 must take the grouped tiles"
     print(check_forward(hg, X, Y2, RTOL, plan=plan, seed=3), flush=True)
+    print(check_forward(hg, X, Y1, RTOL, plan=plan, seed=4), flush=True)
+    monkeypatch.setattr(ops, "GROUPED", False)
+    Y3 = torch.empty_like(Y1)
+    G.spmm(X, out=Y3)
+    torch.cuda.synchronize()
+    assert G.packed_tiles() is not None, "the packed tiles are built on the next product"
+    assert torch.equal(Y1.view(torch.int16), Y3.view(torch.int16)), "packed and dense tiles differ"
 
 
 @pytest.mark.parametrize("N", [256, 41])
