@@ -177,21 +177,24 @@ __global__ void grp_slabs_kernel(const int64_t* __restrict__ gfirst, const int64
     if (s > 0) atomicMax((unsigned long long*)&stats[1], (unsigned long long)s);
 }
 
-// Nonzero values at valid columns (one wave per tile; lane l: row l / 4,
-// columns 4 (l % 4) .. +3 at tc 16, or rows (l / 2), columns 4 (l % 2) at tc 8).
+// Nonzero values at valid columns.  Each wave walks tiles t = its global
+// wave index + k * (all waves) (lane l: row l / 4, columns 4 (l % 4) .. +3
+// at tc 16, or row l / 4, columns 2 (l % 4) .. +1 at tc 8) and adds its
+// count once at the end: one atomic per wave, not per tile.
 __global__ __launch_bounds__(256) void grp_count_values_kernel(const int32_t* __restrict__ cols,
                                                                const uint16_t* __restrict__ vals, int64_t T, int tc,
                                                                int64_t num_cols, int64_t* __restrict__ stats) {
-    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= T) return;  // uniform per wave
     const int lane = threadIdx.x & 63;
+    const int64_t nw = (int64_t)gridDim.x * 4;
     const int per = 16 * tc / 64;  // slots per lane: 4 (tc 16) or 2 (tc 8)
-    int cnt = 0;
-    for (int j = 0; j < per; ++j) {
-        const int slot = lane * per + j;
-        const int r = slot / tc, c = slot % tc;
-        const int32_t col = cols[t * tc + c];
-        if (col >= 0 && (int64_t)col < num_cols && value_bits(vals, t, r, c, tc) != 0) ++cnt;
+    int64_t cnt = 0;
+    for (int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); t < T; t += nw) {  // uniform per wave
+        for (int j = 0; j < per; ++j) {
+            const int slot = lane * per + j;
+            const int r = slot / tc, c = slot % tc;
+            const int32_t col = cols[t * tc + c];
+            if (col >= 0 && (int64_t)col < num_cols && value_bits(vals, t, r, c, tc) != 0) ++cnt;
+        }
     }
     for (int d = 32; d > 0; d >>= 1) cnt += __shfl_xor(cnt, d, 64);
     if (lane == 0 && cnt) atomicAdd((unsigned long long*)&stats[0], (unsigned long long)cnt);
@@ -372,9 +375,9 @@ extern "C" int grws_group_tiles_count(const grws_bcsr* A, int64_t num_cols, int3
         hipLaunchKernelGGL(grp_bounds_kernel, dim3(grid_for(s.n)), dim3(kBlk), 0, stream, k, s.n, vbit, s.cbits,
                            w.uflag, w.uidx, w.gfirst, w.glast);
         GRWS_LAUNCH_CHECK();
-        hipLaunchKernelGGL(grp_count_values_kernel, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream,
-                           A->col_indices, static_cast<const uint16_t*>(A->values), A->num_tiles, tc, num_cols,
-                           w.stats);
+        const unsigned cgrid = grid_for(A->num_tiles, 4) < 8192u ? grid_for(A->num_tiles, 4) : 8192u;
+        hipLaunchKernelGGL(grp_count_values_kernel, dim3(cgrid), dim3(256), 0, stream, A->col_indices,
+                           static_cast<const uint16_t*>(A->values), A->num_tiles, tc, num_cols, w.stats);
         GRWS_LAUNCH_CHECK();
     }
     hipLaunchKernelGGL(grp_slabs_kernel, dim3(grid_for(s.Q)), dim3(kBlk), 0, stream, w.gfirst, w.glast, s.Q,

@@ -959,14 +959,26 @@ __global__ __launch_bounds__(64 * GW) void spmm_grp_kernel(SpmmArgs a) {
     };
 
     if (nslabs > 0 && xr > 0) {  // uniform over the work-group
-        // ring of R slots: column indices and headers R slabs ahead, X rows
-        // and A values PF slabs ahead of the slab multiplied
+        // X rows and A values PF slabs ahead of the slab multiplied (ring of
+        // R); the column indices and headers they depend on DC slabs ahead
+        // (ring of RC, a multiple of R): both stream from memory once, and
+        // one slab's work is too short to cover their latency (two waves
+        // per group, up to 16 column blocks: c3 N = 256 2.31 against 2.39 ms).
+        // With 20 blocks a slab's work covers it, and with four waves the
+        // deeper ring's registers cost a wave per SIMD (both measured slower)
+        constexpr int DC = (GW == 2 && NBLK < 20) ? PF + 2 : PF + 1;
+        // a slot is rewritten DC slabs on: RC must exceed DC - PF so that no
+        // slot of a pending slab (PF .. DC - 1 ahead) is overwritten
+        constexpr int RC = (DC - PF + R) / R * R;
+        static_assert(RC > DC - PF && RC >= PF && RC % R == 0, "column ring");
         u32x4_t xbuf[R][NLD];
         u32x4_t abuf[R][WPW];
-        ColV cring[R];
-        uint32_t hring[R][WPW];
+        ColV cring[RC];
+        uint32_t hring[RC][WPW];
+        // slab k's indices live in slot k mod RC: the first PF slabs' are
+        // used here, before slabs PF .. DC - 1 take their slots
 #pragma unroll
-        for (int k = 0; k < R; ++k) {
+        for (int k = 0; k < PF; ++k) {
             cring[k] = load_cols(k);
 #pragma unroll
             for (int w = 0; w < WPW; ++w) hring[k][w] = load_hdr(k, w);
@@ -977,28 +989,34 @@ __global__ __launch_bounds__(64 * GW) void spmm_grp_kernel(SpmmArgs a) {
 #pragma unroll
             for (int w = 0; w < WPW; ++w) abuf[k][w] = load_a(lane_hdr(hring[k][w]));
         }
-        auto step = [&](const int u, const int64_t s) {
-            const int ps = (u + PF) % R;
-            cring[u] = load_cols(s + R);
 #pragma unroll
-            for (int w = 0; w < WPW; ++w) hring[u][w] = load_hdr(s + R, w);
-            load_x(cring[ps], xbuf[ps]);
+        for (int k = PF; k < DC; ++k) {
+            cring[k % RC] = load_cols(k);
 #pragma unroll
-            for (int w = 0; w < WPW; ++w) abuf[ps][w] = load_a(lane_hdr(hring[ps][w]));
-            consume(NST > 1 ? (int)(s & 1) : 0, xbuf[u], abuf[u]);
+            for (int w = 0; w < WPW; ++w) hring[k % RC][w] = load_hdr(k, w);
+        }
+        auto step = [&](const int u, const int64_t s) {  // u = s mod RC
+            const int cd = (u + DC) % RC, cp = (u + PF) % RC, xp = (u + PF) % R;
+            cring[cd] = load_cols(s + DC);
+#pragma unroll
+            for (int w = 0; w < WPW; ++w) hring[cd][w] = load_hdr(s + DC, w);
+            load_x(cring[cp], xbuf[xp]);
+#pragma unroll
+            for (int w = 0; w < WPW; ++w) abuf[xp][w] = load_a(lane_hdr(hring[cp][w]));
+            consume(NST > 1 ? (int)(s & 1) : 0, xbuf[u % R], abuf[u % R]);
         };
-        const int64_t nturns = nslabs / R;
+        const int64_t nturns = nslabs / RC;
         int64_t s = 0;
         for (int64_t t = 0; t < nturns; ++t) {
 #pragma unroll
-            for (int u = 0; u < R; ++u) {
+            for (int u = 0; u < RC; ++u) {
                 step(u, s);
                 ++s;
             }
         }
-        const int rest = (int)(nslabs - nturns * R);
+        const int rest = (int)(nslabs - nturns * RC);
 #pragma unroll
-        for (int u = 0; u < R - 1; ++u) {
+        for (int u = 0; u < RC - 1; ++u) {
             if (u < rest) step(u, s);
             ++s;
         }
