@@ -192,8 +192,20 @@ __global__ __launch_bounds__(1024) void gemm_tn_reduce_kernel(const float* __res
     }
 }
 
-int64_t chunks_for(int64_t K) {
+// K-chunks: of kMinChunkRows rows, or, when that leaves fewer than
+// kMinBlocks work-groups (a mini-batch's few thousand rows), of as few as
+// kSmallChunkRows rows until there are kMinBlocks; at most kMaxChunks.
+constexpr int64_t kSmallChunkRows = 256;
+constexpr int64_t kMinBlocks = 256;
+
+int64_t chunks_for(int64_t K, int64_t M, int64_t N) {
+    const int64_t tiles = ((M + kT - 1) / kT) * ((N + kT - 1) / kT);
     int64_t n = (K + kMinChunkRows - 1) / kMinChunkRows;
+    if (tiles > 0 && n * tiles < kMinBlocks) {
+        const int64_t small = (K + kSmallChunkRows - 1) / kSmallChunkRows;
+        const int64_t want = (kMinBlocks + tiles - 1) / tiles;
+        n = small < want ? small : want;
+    }
     if (n > kMaxChunks) n = kMaxChunks;
     return n < 1 ? 1 : n;
 }
@@ -205,7 +217,7 @@ using namespace grws;
 
 extern "C" size_t grws_gemm_tn_workspace_bytes(int64_t K, int64_t M, int64_t N) {
     if (K < 0 || M < 0 || N < 0) return 0;
-    return (size_t)chunks_for(K) * (size_t)M * (size_t)N * sizeof(float);
+    return (size_t)chunks_for(K, M, N) * (size_t)M * (size_t)N * sizeof(float);
 }
 
 extern "C" int grws_gemm_tn(const void* a, int64_t lda, const void* b, int64_t ldb, int32_t in_dtype, int64_t K,
@@ -229,7 +241,7 @@ extern "C" int grws_gemm_tn(const void* a, int64_t lda, const void* b, int64_t l
         GRWS_CHECK_ARG((reinterpret_cast<uintptr_t>(a) % 16) == 0 && (reinterpret_cast<uintptr_t>(b) % 16) == 0,
                        "gemm_tn: inputs must be 16-byte aligned");
     }
-    const int64_t nch = K > 0 ? chunks_for(K) : 0;
+    const int64_t nch = K > 0 ? chunks_for(K, M, N) : 0;
     const size_t need = (size_t)nch * (size_t)M * (size_t)N * sizeof(float);
     if (nch > 0 && (!workspace || workspace_bytes < need))
         return set_error(GRWS_E_CAPACITY, "gemm_tn: workspace too small (%zu < %zu)", workspace_bytes, need);
