@@ -189,3 +189,28 @@ def test_graph_groups_its_tiles_when_it_pays(cuda_device):
     B.spmm(Xb)
     B.spmm(Xb)
     assert B._cache["grouped"][2] is False
+
+
+@pytest.mark.parametrize("G", [2, 4])
+def test_grouped_layout_special_values_and_empty_windows(cuda_device, G):
+    """Windows with 0..40 tiles (a whole group may be empty), explicit zeros
+    (dropped), -0.0, NaN and infinities (kept: nonzero bit patterns), -1
+    padding: the grouped layout still decodes to the dense matrix bit for
+    bit, and on the finite values the product meets the oracle."""
+    from test_packed_gpu import _special_graph
+    print(f"case grouped special G={G}", flush=True)
+    A = _special_graph(cuda_device, torch.float16, seed=7)
+    gt = ops.group_tiles(A.window_offset, A.original_col_indices, A.values_condensed, 16, A.num_cols,
+                         group_size=G, max_ratio=10.0, max_skew=1e9)
+    assert gt is not None
+    np.testing.assert_array_equal(_dense_from_grouped(gt, A.num_windows, A.num_cols), _dense_from_bcsr(A))
+    v = A.values_condensed.clone()
+    v[~torch.isfinite(v)] = 0
+    F = BCSRGraph(A.num_cols, 0, 16, 16, A.window_offset, A.original_col_indices, v, device=cuda_device,
+                  num_cols=A.num_cols, values_dtype=torch.float16)
+    gf = ops.group_tiles(F.window_offset, F.original_col_indices, F.values_condensed, 16, F.num_cols,
+                         group_size=G, max_ratio=10.0, max_skew=1e9)
+    torch.manual_seed(11)
+    X = torch.randn(F.num_cols, 256, device=cuda_device).half()
+    Y = ops.spmm(F.window_offset, F.original_col_indices, F.values_condensed, X, 16, grouped=gf)
+    _oracle_check(F, X, Y)
