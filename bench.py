@@ -274,6 +274,25 @@ def bench_sampling(dev, batches: int, warmup: int, cpu: bool) -> dict:
                               "index, the source's degree, three relabel passes of 8 B) plus the block "
                               "written"},
     }
+    # the mini-batch engine's call: the same batches with the transposes of
+    # the blocks whose backward multiplies by A^T (layers 1 and 2 of the
+    # 3-layer model) built in the same device call
+    want = [False, True, True]
+    for b in range(warmup):
+        s.sample_layers(g.row_ptr, g.col_idx, seed_sets[b], transposes=want)
+    torch.cuda.synchronize(dev)
+    tt = []
+    for b in range(warmup, warmup + batches):
+        t1 = time.perf_counter()
+        s.sample_layers(g.row_ptr, g.col_idx, seed_sets[b], transposes=want)
+        torch.cuda.synchronize(dev)
+        tt.append(time.perf_counter() - t1)
+    out["with_transposes"] = {
+        "transposes": "layers 1 and 2 (grws_sample_blocks_transposed)",
+        "batch_ms": round(1e3 * sum(tt) / batches, 4),
+        "host_syncs_per_batch": 1,
+        "note": "per transposed hop: slot keys, a 2-pass radix sort by source window, tiles per "
+                "window, a scan and the fill"}
     if cpu:
         import numpy as np
         import oracle
