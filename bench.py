@@ -33,13 +33,12 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16
 # that exact workload.  Sources: the profile file named with each figure
 MEASURED_TRAFFIC = {
     # (config, N, x dtype, tile cols, A format): (bytes per SpMM, profile file)
-    ("c3", 608, "f16", 16, "dense tiles"): (38.764e9, "profiles/spmm_buf_c3_n608_f16.md"),
-    ("c3", 608, "f16", 16, "packed tiles"): (38.437e9, "profiles/spmm_buf_c3_n608_f16.md"),
-    # grouped tiles, 2 windows per group: FETCH 18.02M KiB x2, WRITE 0.277M KiB
-    ("c3", 608, "f16", 16, "grouped tiles (2 windows)"): (37.18e9, "profiles/spmm_grp_c3_n608_f16.md"),
-    # SpMM kernel (373.1 MB read, 54.7 MB written) plus the split-window fixup (14.6 MB)
-    ("c2", 128, "f16", 16, "packed tiles"): (442.4e6, "profiles/spmm_buf_c2_n128_f16.md"),
-    ("c4", 112, "bf16", 16, "packed tiles"): (26.571e9, "profiles/spmm_buf_c4_n112_bf16.md"),
+    # grouped tiles, 2 windows per group: FETCH 17.47M KiB x2, WRITE 0.277M KiB
+    ("c3", 608, "f16", 16, "grouped tiles (2 windows)"): (36.05e9, "profiles/spmm_grp_c3_n608_f16.md"),
+    # SpMM kernel (351.0 MB read, 55.1 MB written) plus the split-window fixup (14.6 MB)
+    ("c2", 128, "f16", 16, "packed tiles"): (420.7e6, "profiles/spmm_buf_c2_n128_f16.md"),
+    # SpMM kernel (24.96 GB read, 0.56 GB written) plus the fixup (13 MB)
+    ("c4", 112, "bf16", 16, "packed tiles"): (25.534e9, "profiles/spmm_buf_c4_n112_bf16.md"),
 }
 
 
