@@ -863,6 +863,41 @@ def sample_block(indptr: torch.Tensor, indices: torch.Tensor, frontier: torch.Te
     return win, cols[:T * tile_cols], vals[:T * 16 * tile_cols], nxt[:S], E
 
 
+def gather_rows(src: torch.Tensor, index: torch.Tensor, out: Optional[torch.Tensor] = None,
+                err: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``src.index_select(0, index)`` for a 2-D device tensor whose rows are
+    contiguous (any row pitch), in one launch of grws_gather_rows: the
+    mini-batch producer's input features (engine.py:132-141 gathers
+    ``features[input_nodes]``).  ``index`` is int64 or int32 on the same
+    device.  An index outside [0, src.shape[0]) yields a zero row and, when
+    ``err`` (an int32 device tensor the caller cleared) is given, sets
+    ``err[0]`` to 1; no host sync either way."""
+    if src.dim() != 2 or not src.is_cuda:
+        raise ValueError("gather_rows: src must be a 2-D device tensor")
+    if src.shape[1] > 1 and src.stride(1) != 1:
+        raise ValueError("gather_rows: the rows of src must be contiguous")
+    idx = index
+    if idx.device != src.device:
+        raise ValueError("gather_rows: index must be on src's device")
+    if idx.dtype not in (torch.int64, torch.int32):
+        idx = idx.to(torch.int64)
+    idx = idx.contiguous().view(-1)
+    n = idx.numel()
+    D = src.shape[1]
+    if out is None:
+        out = torch.empty(n, D, dtype=src.dtype, device=src.device)
+    elif out.shape != (n, D) or out.dtype != src.dtype or out.device != src.device or \
+            (D > 1 and out.stride(1) != 1):
+        raise ValueError("gather_rows: out must be a [n, D] tensor of src's dtype with contiguous rows")
+    esz = src.element_size()
+    if n == 0 or D == 0:
+        return out
+    L.call("grws_gather_rows", L.ptr(src), src.shape[0], src.stride(0) * esz, L.ptr(idx),
+           int(idx.dtype == torch.int64), n, D * esz, L.ptr(out), out.stride(0) * esz,
+           L.ptr(err) if err is not None else None, L.stream_of(src.device))
+    return out
+
+
 _BLOCKS_SIZES: dict = {}
 
 

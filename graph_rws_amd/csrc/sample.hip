@@ -1635,3 +1635,108 @@ extern "C" int grws_sample_blocks_transposed(const int64_t* indptr, const int32_
                               transpose_hops, t_window_offset, t_col_indices, t_values, workspace, workspace_bytes,
                               counts_out, 5, as_stream(stream_));
 }
+
+// ---------------------------------------------------------------------------
+// Row gather (the mini-batch producer's input features)
+// ---------------------------------------------------------------------------
+// dst[i, :] = src[idx[i], :].  Each work item moves one unit of UB bytes
+// (the widest of 16/8/4/2/1 that divides the row length, both pitches and
+// both base addresses); the units of a row are consecutive items, so a wave
+// reads whole rows (a 256-byte row: 16 lanes of 16 bytes).  Every thread
+// handles kGatherUnroll items a grid stride apart and issues all of their
+// loads before its stores, to keep many random rows in flight.
+namespace grws {
+namespace {
+
+constexpr int kGatherBlock = 256;
+constexpr int kGatherUnroll = 4;
+
+template <int UB> struct GatherUnit;
+template <> struct GatherUnit<16> { typedef u32x4_t T; };
+template <> struct GatherUnit<8> { typedef uint64_t T; };
+template <> struct GatherUnit<4> { typedef uint32_t T; };
+template <> struct GatherUnit<2> { typedef uint16_t T; };
+template <> struct GatherUnit<1> { typedef uint8_t T; };
+
+template <int UB, bool IDX64>
+__global__ __launch_bounds__(kGatherBlock) void gather_rows_kernel(const char* __restrict__ src, int64_t src_rows,
+                                                                   int64_t ld_src, const void* __restrict__ idx,
+                                                                   int64_t total, uint32_t upr,
+                                                                   char* __restrict__ dst, int64_t ld_dst,
+                                                                   int32_t* __restrict__ err) {
+    using T = typename GatherUnit<UB>::T;
+    const int64_t stride = (int64_t)gridDim.x * kGatherBlock;
+    for (int64_t base = (int64_t)blockIdx.x * kGatherBlock + threadIdx.x; base < total;
+         base += stride * kGatherUnroll) {
+        T v[kGatherUnroll];
+        int64_t row[kGatherUnroll];
+        uint32_t unit[kGatherUnroll];
+        bool in[kGatherUnroll];
+        bool bad = false;
+#pragma unroll
+        for (int j = 0; j < kGatherUnroll; ++j) {
+            const int64_t u = base + j * stride;
+            in[j] = u < total;
+            row[j] = in[j] ? u / upr : 0;
+            unit[j] = in[j] ? (uint32_t)(u - row[j] * upr) : 0u;
+            const int64_t s = !in[j]   ? 0
+                              : IDX64 ? static_cast<const int64_t*>(idx)[row[j]]
+                                      : (int64_t) static_cast<const int32_t*>(idx)[row[j]];
+            const bool ok = in[j] && s >= 0 && s < src_rows;
+            bad |= in[j] && !ok;
+            v[j] = ok ? *reinterpret_cast<const T*>(src + s * ld_src + (int64_t)unit[j] * UB) : T{};
+        }
+#pragma unroll
+        for (int j = 0; j < kGatherUnroll; ++j)
+            if (in[j]) *reinterpret_cast<T*>(dst + row[j] * ld_dst + (int64_t)unit[j] * UB) = v[j];
+        if (bad && err) *err = 1;
+    }
+}
+
+template <int UB>
+void launch_gather_rows(const void* src, int64_t src_rows, int64_t ld_src, const void* idx, bool idx64, int64_t n,
+                        int64_t row_bytes, void* dst, int64_t ld_dst, int32_t* err, hipStream_t stream) {
+    const int64_t upr = row_bytes / UB;
+    const int64_t total = n * upr;
+    const int64_t want = (total + (int64_t)kGatherBlock * kGatherUnroll - 1) / ((int64_t)kGatherBlock * kGatherUnroll);
+    const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, 65536));
+    if (idx64)
+        hipLaunchKernelGGL((gather_rows_kernel<UB, true>), dim3(grid), dim3(kGatherBlock), 0, stream,
+                           static_cast<const char*>(src), src_rows, ld_src, idx, total, (uint32_t)upr,
+                           static_cast<char*>(dst), ld_dst, err);
+    else
+        hipLaunchKernelGGL((gather_rows_kernel<UB, false>), dim3(grid), dim3(kGatherBlock), 0, stream,
+                           static_cast<const char*>(src), src_rows, ld_src, idx, total, (uint32_t)upr,
+                           static_cast<char*>(dst), ld_dst, err);
+}
+
+}  // namespace
+}  // namespace grws
+
+extern "C" int grws_gather_rows(const void* src, int64_t src_rows, int64_t ld_src, const void* idx,
+                                int32_t idx_is_i64, int64_t n, int64_t row_bytes, void* dst, int64_t ld_dst,
+                                int32_t* err, void* stream_) {
+    clear_error();
+    GRWS_CHECK_ARG(n >= 0 && src_rows >= 0 && row_bytes >= 0, "gather_rows: negative size");
+    if (n == 0 || row_bytes == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(src != nullptr && idx != nullptr && dst != nullptr, "gather_rows: null pointer");
+    GRWS_CHECK_ARG(ld_src >= row_bytes && ld_dst >= row_bytes, "gather_rows: row pitch below the row length");
+    GRWS_CHECK_ARG(row_bytes <= ((int64_t)1 << 31), "gather_rows: rows above 2 GiB");
+    const uint64_t align = (uint64_t)row_bytes | (uint64_t)ld_src | (uint64_t)ld_dst | (uint64_t)(uintptr_t)src |
+                           (uint64_t)(uintptr_t)dst;
+    const hipStream_t stream = as_stream(stream_);
+    const bool i64 = idx_is_i64 != 0;
+    if ((align & 15) == 0)
+        launch_gather_rows<16>(src, src_rows, ld_src, idx, i64, n, row_bytes, dst, ld_dst, err, stream);
+    else if ((align & 7) == 0)
+        launch_gather_rows<8>(src, src_rows, ld_src, idx, i64, n, row_bytes, dst, ld_dst, err, stream);
+    else if ((align & 3) == 0)
+        launch_gather_rows<4>(src, src_rows, ld_src, idx, i64, n, row_bytes, dst, ld_dst, err, stream);
+    else if ((align & 1) == 0)
+        launch_gather_rows<2>(src, src_rows, ld_src, idx, i64, n, row_bytes, dst, ld_dst, err, stream);
+    else
+        launch_gather_rows<1>(src, src_rows, ld_src, idx, i64, n, row_bytes, dst, ld_dst, err, stream);
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+

@@ -20,11 +20,21 @@ class WindowWiseDataLoader:
         self.sorted_train_idx = idx[order]
         _, counts = torch.unique_consecutive(wids[order], return_counts=True)
         starts = torch.cumsum(counts, 0) - counts
-        self.window_info = list(zip(starts.tolist(), counts.tolist()))
-        self.num_windows = len(self.window_info)
+        self.num_windows = int(counts.numel())
         self._starts = starts.numpy().astype(np.int64)
         self._counts = counts.numpy().astype(np.int64)
         self._sorted_np = self.sorted_train_idx.numpy()
+        self._window_info = None
+
+    @property
+    def window_info(self):
+        """[(start, count)] per window in sorted_train_idx (data_loader.py:74-80),
+        built on first use: the batches come from the arrays above, and a
+        list of one tuple per window (~40k for a c5 epoch) cost milliseconds
+        and garbage-collector passes at every epoch's start."""
+        if self._window_info is None:
+            self._window_info = list(zip(self._starts.tolist(), self._counts.tolist()))
+        return self._window_info
 
     def __iter__(self):
         """Same batches as walking the shuffled windows one by one

@@ -473,6 +473,17 @@ int grws_sample_blocks_transposed(const int64_t* indptr, const int32_t* indices,
                                   int32_t* const* t_col_indices, void* const* t_values, void* workspace,
                                   size_t workspace_bytes, int64_t* counts_out, void* stream);
 
+/* Input features of a sampled batch: dst row i = src row idx[i] for        */
+/* i < n, row_bytes bytes per row, rows ld_src / ld_dst bytes apart; idx is  */
+/* int64 (idx_is_i64 != 0) or int32.  An index outside [0, src_rows) gives a */
+/* zero row and, when err is not NULL, sets *err to 1 (nothing else writes   */
+/* *err: the caller clears it).  Replaces the producer's feature gather      */
+/* (helper/engine.py:132-141 gathers features[input_nodes] per batch) with   */
+/* one launch that moves 16-byte units whenever the row length, pitches and  */
+/* base addresses allow.  Asynchronous on `stream`.                          */
+int grws_gather_rows(const void* src, int64_t src_rows, int64_t ld_src, const void* idx, int32_t idx_is_i64,
+                     int64_t n, int64_t row_bytes, void* dst, int64_t ld_dst, int32_t* err, void* stream);
+
 int grws_sample_state_init(int32_t* node_map, uint32_t* bitmap, int64_t num_nodes, void* stream);
 size_t grws_sample_block_workspace_bytes(int64_t num_frontier, int32_t fanout, int64_t num_nodes);
 int grws_sample_block_capacity(int64_t num_frontier, int32_t fanout, int32_t tile_cols,
