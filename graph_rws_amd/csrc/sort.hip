@@ -3,8 +3,10 @@
 // Used by the device BCSR builder (key = window, column, row-in-window) and
 // by the sampler's unique-and-relabel (key = global node id).  Each pass over
 // one 8-bit digit is three launches:
-//   1. digit histogram per 4096-key tile (wave64 match by ballot, one LDS
-//      atomic per distinct digit per wave),
+//   1. digit histogram per tile of 256 x iters keys (wave64 match by ballot,
+//      one LDS atomic per distinct digit per wave); iters is 16 for large
+//      inputs and as small as 1 below 16k keys, so that a small sort still
+//      spreads over up to 64 work-groups instead of a few long ones,
 //   2. exclusive scan of the digit-major [256][tiles] histogram, which gives
 //      every (digit, tile) its output base in stable order,
 //   3. stable scatter: each tile re-reads its keys in index order and ranks
@@ -18,8 +20,15 @@ namespace {
 
 constexpr int kRsBlock = 256;
 constexpr int kRsWaves = kRsBlock / kWave;
-constexpr int kRsIters = 16;
-constexpr int64_t kRsTile = (int64_t)kRsBlock * kRsIters;
+constexpr int kRsMaxIters = 16;
+
+// Keys per tile: 256 x iters, iters = ceil(n / 16k) clamped to [1, 16]: up
+// to 256k keys a sort has at most 64 tiles, so its 256 x tiles digit counts
+// take the one-launch scan (16k elements).
+inline int radix_iters(int64_t n) {
+    const int64_t it = (n + 16383) / 16384;
+    return (int)(it < 1 ? 1 : (it > kRsMaxIters ? kRsMaxIters : it));
+}
 
 // Lanes of the wave whose 8-bit digit equals this lane's (valid lanes only).
 __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
@@ -34,12 +43,12 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
 }
 
 __global__ __launch_bounds__(kRsBlock) void radix_hist_kernel(const uint64_t* __restrict__ keys, int64_t n, int shift,
-                                                              int64_t ntiles, int32_t* __restrict__ counts) {
+                                                              int64_t ntiles, int iters, int32_t* __restrict__ counts) {
     __shared__ int32_t h[256];
     h[threadIdx.x] = 0;
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kRsTile;
-    for (int it = 0; it < kRsIters; ++it) {
+    const int64_t base = (int64_t)blockIdx.x * kRsBlock * iters;
+    for (int it = 0; it < iters; ++it) {
         const int64_t i = base + (int64_t)it * kRsBlock + threadIdx.x;
         const bool valid = i < n;
         const uint32_t d = valid ? (uint32_t)(keys[i] >> shift) & 255u : 0u;
@@ -52,7 +61,7 @@ __global__ __launch_bounds__(kRsBlock) void radix_hist_kernel(const uint64_t* __
 
 __global__ __launch_bounds__(kRsBlock) void radix_scatter_kernel(const uint64_t* __restrict__ kin,
                                                                  const uint32_t* __restrict__ vin, int64_t n,
-                                                                 int shift, int64_t ntiles,
+                                                                 int shift, int64_t ntiles, int iters,
                                                                  const int64_t* __restrict__ offsets,
                                                                  uint64_t* __restrict__ kout,
                                                                  uint32_t* __restrict__ vout) {
@@ -61,8 +70,8 @@ __global__ __launch_bounds__(kRsBlock) void radix_scatter_kernel(const uint64_t*
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
     base_off[tid] = offsets[(int64_t)tid * ntiles + blockIdx.x];
-    const int64_t tile0 = (int64_t)blockIdx.x * kRsTile;
-    for (int it = 0; it < kRsIters; ++it) {
+    const int64_t tile0 = (int64_t)blockIdx.x * kRsBlock * iters;
+    for (int it = 0; it < iters; ++it) {
         const int64_t i = tile0 + (int64_t)it * kRsBlock + tid;
         const bool valid = i < n;
         uint64_t k = 0;
@@ -99,8 +108,13 @@ __global__ __launch_bounds__(kRsBlock) void radix_scatter_kernel(const uint64_t*
 
 }  // namespace
 
+// Sized for any sort of at most n keys (callers size by a capacity and sort
+// what a batch holds): up to 256k keys a sort uses at most 64 tiles (at most
+// ceil(n / 256) of them), above it ceil(n / 4096).
 size_t radix_sort_workspace_bytes(int64_t n) {
-    const int64_t ntiles = (n + kRsTile - 1) / kRsTile;
+    const int64_t small = (n + kRsBlock - 1) / kRsBlock;
+    const int64_t big = (n + (int64_t)kRsBlock * kRsMaxIters - 1) / ((int64_t)kRsBlock * kRsMaxIters);
+    const int64_t ntiles = std::max(std::min<int64_t>(small, 64), big);
     Sizer s;
     s.take<int32_t>((size_t)(256 * ntiles + 1));
     s.take<int64_t>((size_t)(256 * ntiles + 2));
@@ -113,7 +127,9 @@ int radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_
     *result_in_alt = false;
     if (n <= 1 || bits <= 0) return GRWS_OK;
     if (bits > 64) bits = 64;
-    const int64_t ntiles = (n + kRsTile - 1) / kRsTile;
+    const int iters = radix_iters(n);
+    const int64_t tile = (int64_t)kRsBlock * iters;
+    const int64_t ntiles = (n + tile - 1) / tile;
     if (ntiles > INT32_MAX / 2) return set_error(GRWS_E_INVALID, "radix sort: %lld keys is too many", (long long)n);
     Carver cv(ws, ws_bytes);
     int32_t* counts = cv.take<int32_t>(256 * ntiles + 1);
@@ -128,11 +144,11 @@ int radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_
     bool alt = false;
     for (int shift = 0; shift < bits; shift += 8) {
         hipLaunchKernelGGL(radix_hist_kernel, dim3((unsigned)ntiles), dim3(kRsBlock), 0, stream, ka, n, shift, ntiles,
-                           counts);
+                           iters, counts);
         GRWS_LAUNCH_CHECK();
         GRWS_TRY(scan_i32_to_i64(counts, offsets, 256 * ntiles, false, scan_ws, scan_bytes, stream));
         hipLaunchKernelGGL(radix_scatter_kernel, dim3((unsigned)ntiles), dim3(kRsBlock), 0, stream, ka, va, n, shift,
-                           ntiles, offsets, kb, vb);
+                           ntiles, iters, offsets, kb, vb);
         GRWS_LAUNCH_CHECK();
         std::swap(ka, kb);
         std::swap(va, vb);
