@@ -1032,6 +1032,168 @@ def sample_blocks(indptr: torch.Tensor, indices: torch.Tensor, seeds: torch.Tens
     return out
 
 
+class CapturedSampleBlocks:
+    """sample_blocks replayed from a HIP graph: the batch's ~50 kernels
+    (every hop's sampling, relabel, block and transpose builds) launched as
+    one graph instead of one host launch each, which on a c5 batch cost more
+    than the kernels themselves.
+
+    One instance serves one batch shape: the CSR graph, the hop fanouts and
+    transposes, the tile and dtype, the Philox seed, the SampleState and a
+    seed-count capacity ``max_seeds``; any batch of at most max_seeds seeds
+    replays it (grws_sample_blocks_enqueue reads the count on the device).
+    The first call runs the enqueue eagerly and captures it; later calls copy
+    the seeds into the static input, replay, read the counters back (the one
+    sync of the batch, as in sample_blocks) and copy the outputs out of the
+    static buffers into fresh compact tensors in one launch
+    (grws_copy_ranges), so a returned batch stays valid after the next one.
+    Returns what sample_blocks returns, bit for bit."""
+
+    def __init__(self, indptr: torch.Tensor, indices: torch.Tensor, fanouts, state: "SampleState",
+                 seed: int, tile_cols: int, values_dtype: torch.dtype, transposes, max_seeds: int):
+        self.indptr, self.indices = indptr, indices
+        n, nnz = _csr_arrays(indptr, indices)
+        dev = indptr.device
+        self.dev, self.n, self.nnz = dev, n, nnz
+        self.H = H = len(fanouts)
+        self.fanouts = [int(k) for k in fanouts]
+        self.state = state
+        self.seed = int(seed)
+        self.tc = tc = int(tile_cols)
+        self.values_dtype = values_dtype
+        self.max_seeds = int(max_seeds)
+        if self.max_seeds < 1:
+            raise ValueError("CapturedSampleBlocks: max_seeds must be at least 1")
+        fo, ms, mt, fcap, wsb = _sample_blocks_sizes(self.max_seeds, fanouts, tc, n)
+        self.fo = fo
+        thops = [bool(t) for t in transposes] if transposes is not None else [False] * H
+        if len(thops) != H:
+            raise ValueError("CapturedSampleBlocks: one transposes flag per hop")
+        self.thops = thops
+        tw, tt = [0] * H, [0] * H
+        self.th = None
+        if any(thops):
+            self.th, tw, tt, wsb = _sample_blocks_t_sizes(self.max_seeds, fanouts, tc, n, thops)
+            tw = [tw[h] if thops[h] else 0 for h in range(H)]
+            tt = [tt[h] if thops[h] else 0 for h in range(H)]
+        self.wsb = wsb
+        self.esz = torch.empty(0, dtype=values_dtype).element_size()
+        i64 = torch.int64
+        self.sin = torch.empty(1 + self.max_seeds, dtype=i64, device=dev)  # [count, seeds...]
+        self.pin = torch.empty(1 + self.max_seeds, dtype=i64, pin_memory=True)
+        self.nxt = [torch.empty(max(1, ms[h]), dtype=i64, device=dev) for h in range(H)]
+        self.win = [torch.empty((fcap[h] + 15) // 16 + 1, dtype=i64, device=dev) for h in range(H)]
+        self.cols = [torch.empty(max(1, mt[h] * tc), dtype=torch.int32, device=dev) for h in range(H)]
+        self.vals = [torch.empty(max(1, mt[h] * 16 * tc), dtype=values_dtype, device=dev) for h in range(H)]
+        self.twin = [torch.empty(tw[h] + 1, dtype=i64, device=dev) for h in range(H)]
+        self.tcols = [torch.empty(max(1, tt[h] * tc), dtype=torch.int32, device=dev) for h in range(H)]
+        self.tvals = [torch.empty(max(1, tt[h] * 16 * tc), dtype=values_dtype, device=dev) for h in range(H)]
+        self.ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        self.cnt_dev = torch.zeros(5 * H + 2, dtype=i64, device=dev)
+        self.cnt_host = torch.empty(5 * H + 2, dtype=i64, pin_memory=True)
+        self.graph = None
+        self.replays = 0
+
+    def _parr(self, ts):
+        return (ctypes.c_void_p * self.H)(*[t.data_ptr() for t in ts])
+
+    def _enqueue(self, stream) -> None:
+        L.call("grws_sample_blocks_enqueue", L.ptr(self.indptr), L.ptr(self.indices), self.n, self.nnz,
+               ctypes.c_void_p(self.sin.data_ptr() + 8), self.max_seeds, L.ptr(self.sin), self.fo, self.H,
+               ctypes.c_uint64(self.seed & 0xFFFFFFFFFFFFFFFF), L.ptr(self.state.node_map),
+               L.ptr(self.state.bitmap), self.tc, L.dtype_code(self.values_dtype), self._parr(self.nxt),
+               self._parr(self.win), self._parr(self.cols), self._parr(self.vals), self.th,
+               self._parr(self.twin), self._parr(self.tcols), self._parr(self.tvals), L.ptr(self.ws), self.wsb,
+               L.ptr(self.cnt_dev), ctypes.c_void_p(stream.cuda_stream))
+
+    def run(self, seeds: torch.Tensor):
+        F0 = int(seeds.numel())
+        if F0 > self.max_seeds:
+            raise ValueError(f"CapturedSampleBlocks: {F0} seeds above the capacity {self.max_seeds}")
+        stream = torch.cuda.current_stream(self.dev)
+        # stage the count and the seeds (the pinned buffer is free again: the
+        # previous call synchronised after its copy)
+        self.pin[0] = F0
+        if seeds.is_cuda:
+            self.sin[1:1 + F0].copy_(seeds.view(-1).to(torch.int64))
+            self.sin[:1].copy_(self.pin[:1], non_blocking=True)
+        else:
+            self.pin[1:1 + F0].copy_(seeds.view(-1).to(torch.int64))
+            self.sin[:1 + F0].copy_(self.pin[:1 + F0], non_blocking=True)
+        if self.graph is None:
+            self._enqueue(stream)  # this batch, and every kernel loaded before the capture
+            cs = torch.cuda.Stream(self.dev)
+            cs.wait_stream(stream)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(cs):
+                g.capture_begin(capture_error_mode="thread_local")
+                try:
+                    self._enqueue(cs)
+                finally:
+                    g.capture_end()
+            stream.wait_stream(cs)
+            self.graph = g
+        else:
+            self.graph.replay()
+            self.replays += 1
+        self.cnt_host.copy_(self.cnt_dev, non_blocking=True)
+        stream.synchronize()
+        c = self.cnt_host.tolist()
+        H = self.H
+        if c[5 * H + 1]:
+            L.call("grws_sample_blocks_error", int(c[5 * H + 1]))
+        F = c[:H + 1]
+        E = c[H + 1:2 * H + 1]
+        T = c[2 * H + 1:3 * H + 1]
+        TT = c[3 * H + 1:4 * H + 1]
+        TM = c[4 * H + 1:5 * H + 1]
+        tc, esz = self.tc, self.esz
+        # compact outputs: one buffer per element type, segments on 16 bytes
+        seg64, seg32, segv = [], [], []
+        for h in range(H):
+            seg64 += [(self.nxt[h], F[h + 1]), (self.win[h], (F[h] + 15) // 16 + 1)]
+            seg32.append((self.cols[h], T[h] * tc))
+            segv.append((self.vals[h], T[h] * 16 * tc))
+            if self.thops[h]:
+                seg64.append((self.twin[h], (F[h + 1] + 15) // 16 + 1))
+                seg32.append((self.tcols[h], TT[h] * tc))
+                segv.append((self.tvals[h], TT[h] * 16 * tc))
+
+        def place(segs, dtype, esize):
+            per = 16 // esize
+            offs, o = [], 0
+            for _, k in segs:
+                offs.append(o)
+                o += -(-k // per) * per
+            buf = torch.empty(max(o, per), dtype=dtype, device=self.dev)
+            return buf, offs
+        b64, o64 = place(seg64, torch.int64, 8)
+        b32, o32 = place(seg32, torch.int32, 4)
+        bv, ov = place(segv, self.values_dtype, esz)
+        src, dst, nbytes, views = [], [], [], []
+        for segs, buf, offs, es in ((seg64, b64, o64, 8), (seg32, b32, o32, 4), (segv, bv, ov, esz)):
+            vs = []
+            for (t, k), o in zip(segs, offs):
+                src.append(t.data_ptr())
+                dst.append(buf.data_ptr() + o * es)
+                nbytes.append(k * es)
+                vs.append(buf[o:o + k])
+            views.append(vs)
+        m = len(src)
+        L.call("grws_copy_ranges", (ctypes.c_void_p * m)(*src), (ctypes.c_void_p * m)(*dst),
+               (ctypes.c_int64 * m)(*nbytes), m, ctypes.c_void_p(stream.cuda_stream))
+        v64, v32, vv = (iter(v) for v in views)
+        out = []
+        for h in range(H):
+            nxt, win = next(v64), next(v64)
+            hop = (win, next(v32), next(vv), nxt, int(E[h]))
+            t = None
+            if self.thops[h]:
+                t = (next(v64), next(v32), next(vv), int(TM[h]))
+            out.append(hop + (t,) if any(self.thops) else hop)
+        return out
+
+
 # ---------------------------------------------------------------------------
 # weight gradient A^T B (csrc/gemm_tn.hip)
 # ---------------------------------------------------------------------------

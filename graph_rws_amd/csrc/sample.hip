@@ -37,7 +37,7 @@ constexpr int kWavesPerBlock = kBlk / kWave;
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-enum : int32_t { kErrNode = 1, kErrIndptr = 2, kErrIndex = 4, kErrDup = 8, kErrDegree = 16 };
+enum : int32_t { kErrNode = 1, kErrIndptr = 2, kErrIndex = 4, kErrDup = 8, kErrDegree = 16, kErrCount = 32 };
 
 inline int bits_for(int64_t x) {
     int b = 0;
@@ -258,6 +258,7 @@ int report(int32_t e, const char* who) {
     if (e & kErrIndex) return set_error(GRWS_E_RANGE, "%s: a neighbour index is outside [0, num_nodes)", who);
     if (e & kErrDegree) return set_error(GRWS_E_RANGE, "%s: a node has 2^32 or more neighbours", who);
     if (e & kErrDup) return set_error(GRWS_E_INVALID, "%s: the frontier holds a node id twice", who);
+    if (e & kErrCount) return set_error(GRWS_E_RANGE, "%s: the seed count in device memory is outside [0, max_seeds]", who);
     return GRWS_OK;
 }
 
@@ -563,7 +564,21 @@ constexpr int64_t kCtrWords = (sizeof(BatchCtr) + 3) / 4;
 inline int64_t bitmap_words(int64_t n) { return (n + 31) / 32; }
 inline int64_t group_count(int64_t n) { return (n + (1 << kGroupShift) - 1) >> kGroupShift; }
 
-__device__ __forceinline__ int64_t hop_frontier(const BatchCtr* c, int h, int64_t F0) { return h == 0 ? F0 : c->F[h]; }
+// Frontier size of hop h: the seeds' count is F0, or with F0 < 0 (an
+// enqueued batch, whose count lives in device memory) c->F[0].
+__device__ __forceinline__ int64_t hop_frontier(const BatchCtr* c, int h, int64_t F0) {
+    return h == 0 ? (F0 >= 0 ? F0 : c->F[0]) : c->F[h];
+}
+
+// An enqueued batch's seed count, read from device memory before hop 0.
+__global__ void mh_start_kernel(const int64_t* __restrict__ num_seeds_dev, int64_t max_seeds,
+                                BatchCtr* __restrict__ ctr) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const int64_t n = *num_seeds_dev;
+    const bool ok = n >= 0 && n <= max_seeds;
+    ctr->F[0] = ok ? n : 0;
+    if (!ok) atomicOr(&ctr->err, kErrCount);
+}
 
 // Per frontier node: min(deg, k) and the node map entry; edge total per hop.
 __global__ __launch_bounds__(kBlk) void mh_count_kernel(const int64_t* __restrict__ indptr, int64_t nnz,
@@ -572,7 +587,7 @@ __global__ __launch_bounds__(kBlk) void mh_count_kernel(const int64_t* __restric
                                                         BatchCtr* __restrict__ ctr) {
     const int64_t F = hop_frontier(ctr, h, F0);
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (h == 0 && i == 0) ctr->F[0] = F0;
+    if (h == 0 && i == 0 && F0 >= 0) ctr->F[0] = F0;
     int64_t c = 0;
     if (i < F) {
         const int64_t v = frontier[i];
@@ -1529,12 +1544,12 @@ static int sample_blocks_impl(const int64_t* indptr, const int32_t* indices, int
                               int32_t* const* col_indices, void* const* values, const int32_t* thops,
                               int64_t* const* t_window_offset, int32_t* const* t_col_indices, void* const* t_values,
                               void* workspace, size_t workspace_bytes, int64_t* counts_out, int per_hop,
-                              hipStream_t stream) {
+                              const int64_t* num_seeds_dev, int64_t* counts_dev, hipStream_t stream) {
     const int H = num_hops;
     GRWS_CHECK_ARG(num_nodes >= 0 && nnz >= 0 && num_seeds >= 0, "sample_blocks: negative size");
     GRWS_CHECK_ARG(num_nodes <= INT32_MAX, "sample_blocks: ids exceed int32 local ids");
     GRWS_CHECK_ARG(H >= 1 && H <= kMaxHops, "sample_blocks: num_hops must be in [1, %d]", kMaxHops);
-    GRWS_CHECK_ARG(fanouts && counts_out, "sample_blocks: null pointer");
+    GRWS_CHECK_ARG(fanouts && (counts_out || counts_dev), "sample_blocks: null pointer");
     GRWS_CHECK_ARG(tile_cols == 8 || tile_cols == 16, "sample_blocks: tile_cols must be 8 or 16");
     if (values_dtype != GRWS_F32 && values_dtype != GRWS_F16 && values_dtype != GRWS_BF16)
         return set_error(GRWS_E_DTYPE, "sample_blocks: unsupported values dtype %d", values_dtype);
@@ -1542,7 +1557,8 @@ static int sample_blocks_impl(const int64_t* indptr, const int32_t* indices, int
         GRWS_CHECK_ARG(fanouts[h] >= 1 && fanouts[h] <= kWave, "sample_blocks: fanout %d outside [1, 64]", fanouts[h]);
     const HopCaps c = hop_caps(num_seeds, fanouts, H, tile_cols, num_nodes);
     GRWS_CHECK_ARG(c.F[H] <= INT32_MAX, "sample_blocks: a hop could exceed int32 local ids");
-    for (int h = 0; h < per_hop * H; ++h) counts_out[h] = 0;
+    if (counts_out)
+        for (int h = 0; h < per_hop * H; ++h) counts_out[h] = 0;
     bool any_t = false;
     for (int h = 0; h < H; ++h) any_t = any_t || (thops && thops[h]);
     if (any_t) {
@@ -1554,7 +1570,7 @@ static int sample_blocks_impl(const int64_t* indptr, const int32_t* indices, int
                 GRWS_CHECK_ARG(c.E[h] <= (int64_t)UINT32_MAX, "sample_blocks: hop %d has too many edge slots", h);
             }
     }
-    if (num_seeds == 0) {
+    if (num_seeds == 0 && !num_seeds_dev) {
         for (int h = 0; h < H; ++h) GRWS_TRY(fill_i64(window_offset[h], 1, 0, stream));
         for (int h = 0; h < H; ++h)
             if (any_t && thops[h]) GRWS_TRY(fill_i64(t_window_offset[h], 1, 0, stream));
@@ -1577,27 +1593,34 @@ static int sample_blocks_impl(const int64_t* indptr, const int32_t* indices, int
     int32_t* grpcnt = reinterpret_cast<int32_t*>(state + l.grp_off);
     BatchCtr* ctr = reinterpret_cast<BatchCtr*>(state + l.ctr_off);
     const int tc = tile_cols;
+    // kernels take the seed count as an argument, or read it from the
+    // counters (-1) when it lives in device memory
+    const int64_t F0 = num_seeds_dev ? -1 : num_seeds;
+    if (num_seeds_dev) {
+        hipLaunchKernelGGL(mh_start_kernel, dim3(1), dim3(64), 0, stream, num_seeds_dev, num_seeds, ctr);
+        GRWS_LAUNCH_CHECK();
+    }
     for (int h = 0; h < H; ++h) {
         const int k = fanouts[h];
         const int64_t Fc = c.F[h], Wc = c.W[h];
         const int64_t* fr = h == 0 ? seeds : next_frontier[h - 1];
         hipLaunchKernelGGL(mh_count_kernel, dim3(grid_for(Fc)), dim3(kBlk), 0, stream, indptr, nnz, num_nodes, fr,
-                           num_seeds, h, k, node_map, ctr);
+                           F0, h, k, node_map, ctr);
         GRWS_LAUNCH_CHECK();
         hipLaunchKernelGGL(mh_sample_kernel, dim3(grid_for(Fc, kWavesPerBlock)), dim3(kBlk), 0, stream, indptr,
-                           indices, nnz, num_nodes, fr, num_seeds, h, k, seed, node_map, bitmap, grpcnt, w.edge_src,
+                           indices, nnz, num_nodes, fr, F0, h, k, seed, node_map, bitmap, grpcnt, w.edge_src,
                            w.edge_val, ctr);
         GRWS_LAUNCH_CHECK();
         const int64_t nslices = (l.groups + kSliceGroups - 1) / kSliceGroups;
         hipLaunchKernelGGL(mh_group_scan_kernel, dim3((unsigned)nslices), dim3(kBlk), 0, stream, grpcnt, l.groups,
-                           w.grpoff, w.slicesum, w.sliceoff, nslices, num_seeds, h, ctr);
+                           w.grpoff, w.slicesum, w.sliceoff, nslices, F0, h, ctr);
         GRWS_LAUNCH_CHECK();
-        hipLaunchKernelGGL(mh_assign_kernel, dim3(grid_for(c.E[h])), dim3(kBlk), 0, stream, fr, num_seeds, h, k,
+        hipLaunchKernelGGL(mh_assign_kernel, dim3(grid_for(c.E[h])), dim3(kBlk), 0, stream, fr, F0, h, k,
                            num_nodes, w.edge_src, node_map, bitmap, w.grpoff, w.sliceoff, w.src_local,
                            next_frontier[h], ctr);
         GRWS_LAUNCH_CHECK();
 #define GRWS_MH_WINDOWS(FILL, VT)                                                                                  \
-    hipLaunchKernelGGL(mh_window_kernel<VT>, dim3((unsigned)Wc), dim3(kBlk), 0, stream, FILL, fr, num_seeds, h, k,    \
+    hipLaunchKernelGGL(mh_window_kernel<VT>, dim3((unsigned)Wc), dim3(kBlk), 0, stream, FILL, fr, F0, h, k,           \
                        w.src_local, w.edge_src, w.edge_val, tc, w.wtiles, Wc, window_offset[h], col_indices[h],       \
                        static_cast<VT*>(values[h]), num_nodes, node_map, bitmap, grpcnt, ctr)
         if (values_dtype == GRWS_F32) GRWS_MH_WINDOWS(0, float);
@@ -1618,7 +1641,7 @@ static int sample_blocks_impl(const int64_t* indptr, const int32_t* indices, int
     if (values_dtype == GRWS_F32) GRWS_MH_T(KERNEL, float, __VA_ARGS__);                \
     else if (values_dtype == GRWS_F16) GRWS_MH_T(KERNEL, _Float16, __VA_ARGS__);        \
     else GRWS_MH_T(KERNEL, __hip_bfloat16, __VA_ARGS__)
-            GRWS_MH_TDISPATCH(mh_tkeys_kernel, dim3(grid_for(ecap)), dim3(kBlk), 0, stream, num_seeds, h, k,
+            GRWS_MH_TDISPATCH(mh_tkeys_kernel, dim3(grid_for(ecap)), dim3(kBlk), 0, stream, F0, h, k,
                               w.src_local, w.edge_val, ecap, wcap, w.tka, w.tpa, ctr);
             GRWS_LAUNCH_CHECK();
             bool alt = false;
@@ -1642,8 +1665,9 @@ static int sample_blocks_impl(const int64_t* indptr, const int32_t* indices, int
             GRWS_LAUNCH_CHECK();
         }
     }
-    hipLaunchKernelGGL(mh_finish_kernel, dim3(1), dim3(64), 0, stream, ctr, w.out, H);
+    hipLaunchKernelGGL(mh_finish_kernel, dim3(1), dim3(64), 0, stream, ctr, counts_dev ? counts_dev : w.out, H);
     GRWS_LAUNCH_CHECK();
+    if (counts_dev) return GRWS_OK;  // enqueued: the caller reads the counts after the stream's work
     int64_t h_out[5 * kMaxHops + 4];
     GRWS_HIP(hipMemcpyAsync(h_out, w.out, sizeof(int64_t) * (5 * H + 2), hipMemcpyDeviceToHost, stream));
     GRWS_HIP(hipStreamSynchronize(stream));
@@ -1671,7 +1695,7 @@ extern "C" int grws_sample_blocks(const int64_t* indptr, const int32_t* indices,
     return sample_blocks_impl(indptr, indices, num_nodes, nnz, seeds, num_seeds, fanouts, num_hops, seed, node_map,
                               state, tile_cols, values_dtype, next_frontier, window_offset, col_indices, values,
                               nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes, counts_out, 3,
-                              as_stream(stream_));
+                              nullptr, nullptr, as_stream(stream_));
 }
 
 extern "C" int grws_sample_blocks_transposed(const int64_t* indptr, const int32_t* indices, int64_t num_nodes,
@@ -1689,7 +1713,102 @@ extern "C" int grws_sample_blocks_transposed(const int64_t* indptr, const int32_
     return sample_blocks_impl(indptr, indices, num_nodes, nnz, seeds, num_seeds, fanouts, num_hops, seed, node_map,
                               state, tile_cols, values_dtype, next_frontier, window_offset, col_indices, values,
                               transpose_hops, t_window_offset, t_col_indices, t_values, workspace, workspace_bytes,
-                              counts_out, 5, as_stream(stream_));
+                              counts_out, 5, nullptr, nullptr, as_stream(stream_));
+}
+
+extern "C" int grws_sample_blocks_enqueue(const int64_t* indptr, const int32_t* indices, int64_t num_nodes,
+                                          int64_t nnz, const int64_t* seeds, int64_t max_seeds,
+                                          const int64_t* num_seeds_dev, const int32_t* fanouts, int32_t num_hops,
+                                          uint64_t seed, int32_t* node_map, uint32_t* state, int32_t tile_cols,
+                                          int32_t values_dtype, int64_t* const* next_frontier,
+                                          int64_t* const* window_offset, int32_t* const* col_indices,
+                                          void* const* values, const int32_t* transpose_hops,
+                                          int64_t* const* t_window_offset, int32_t* const* t_col_indices,
+                                          void* const* t_values, void* workspace, size_t workspace_bytes,
+                                          int64_t* counts_dev, void* stream_) {
+    clear_error();
+    GRWS_CHECK_ARG(max_seeds >= 1, "sample_blocks_enqueue: max_seeds must be at least 1");
+    GRWS_CHECK_ARG(num_seeds_dev != nullptr && counts_dev != nullptr, "sample_blocks_enqueue: null pointer");
+    bool any_t = false;
+    for (int h = 0; transpose_hops && h < num_hops && h < kMaxHops; ++h) any_t = any_t || transpose_hops[h];
+    return sample_blocks_impl(indptr, indices, num_nodes, nnz, seeds, max_seeds, fanouts, num_hops, seed, node_map,
+                              state, tile_cols, values_dtype, next_frontier, window_offset, col_indices, values,
+                              any_t ? transpose_hops : nullptr, t_window_offset, t_col_indices, t_values, workspace,
+                              workspace_bytes, nullptr, any_t ? 5 : 3, num_seeds_dev, counts_dev,
+                              as_stream(stream_));
+}
+
+extern "C" int grws_sample_blocks_error(int64_t err) {
+    clear_error();
+    return report((int32_t)err, "sample_blocks");
+}
+
+// ---------------------------------------------------------------------------
+// Batched device copies (one launch for many ranges)
+// ---------------------------------------------------------------------------
+namespace grws {
+namespace {
+
+constexpr int kMaxCopyRanges = 32;
+
+struct CopyArgs {
+    const char* src[kMaxCopyRanges];
+    char* dst[kMaxCopyRanges];
+    int64_t first[kMaxCopyRanges + 1];  // first 16-byte unit of each range (prefix over ranges)
+    int64_t bytes[kMaxCopyRanges];
+    int n;
+};
+
+// Unit u of the launch belongs to the range r with first[r] <= u < first[r+1];
+// a unit is 16 bytes of its range, the last one possibly shorter (copied
+// byte by byte).  Ranges are 16-byte aligned at both ends' bases.
+__global__ __launch_bounds__(256) void copy_ranges_kernel(CopyArgs a) {
+    const int64_t total = a.first[a.n];
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < total; u += (int64_t)gridDim.x * 256) {
+        int r = 0;
+        while (u >= a.first[r + 1]) ++r;
+        const int64_t off = (u - a.first[r]) * 16;
+        const int64_t left = a.bytes[r] - off;
+        if (left >= 16) {
+            *reinterpret_cast<u32x4_t*>(a.dst[r] + off) = *reinterpret_cast<const u32x4_t*>(a.src[r] + off);
+        } else {
+            for (int64_t b = 0; b < left; ++b) a.dst[r][off + b] = a.src[r][off + b];
+        }
+    }
+}
+
+}  // namespace
+}  // namespace grws
+
+extern "C" int grws_copy_ranges(const void* const* src, void* const* dst, const int64_t* bytes, int32_t n,
+                                void* stream_) {
+    clear_error();
+    GRWS_CHECK_ARG(n >= 0, "copy_ranges: negative count");
+    if (n == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(src && dst && bytes, "copy_ranges: null pointer");
+    const hipStream_t stream = as_stream(stream_);
+    for (int32_t base = 0; base < n; base += kMaxCopyRanges) {
+        CopyArgs a{};
+        a.n = 0;
+        a.first[0] = 0;
+        for (int32_t i = base; i < n && i < base + kMaxCopyRanges; ++i) {
+            GRWS_CHECK_ARG(bytes[i] >= 0, "copy_ranges: negative length");
+            GRWS_CHECK_ARG(bytes[i] == 0 || (src[i] && dst[i]), "copy_ranges: null range");
+            GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(src[i]) % 16 == 0 && reinterpret_cast<uintptr_t>(dst[i]) % 16 == 0,
+                           "copy_ranges: range %d not 16-byte aligned", i);
+            a.src[a.n] = static_cast<const char*>(src[i]);
+            a.dst[a.n] = static_cast<char*>(dst[i]);
+            a.bytes[a.n] = bytes[i];
+            a.first[a.n + 1] = a.first[a.n] + (bytes[i] + 15) / 16;
+            ++a.n;
+        }
+        const int64_t total = a.first[a.n];
+        if (total == 0) continue;
+        const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 4096);
+        hipLaunchKernelGGL(copy_ranges_kernel, dim3(grid), dim3(256), 0, stream, a);
+        GRWS_LAUNCH_CHECK();
+    }
+    return GRWS_OK;
 }
 
 // ---------------------------------------------------------------------------

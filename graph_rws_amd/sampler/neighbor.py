@@ -21,7 +21,10 @@ Per hop, on the device (csrc/sample.hip, csrc/bcsr_build.hip):
                   out-degrees.
 The fused path runs every hop of the batch in one grws_sample_blocks call
 with one stream sync; fused=False runs grws_sample_hop, grws_relabel and the
-COO build per hop.
+COO build per hop.  capture=True replays the fused call from a HIP graph
+captured once per batch shape (seed counts bucketed by 64), which removes
+the host's ~50 kernel launches per batch; the blocks are the same, bit for
+bit.
 """
 from __future__ import annotations
 
@@ -31,7 +34,7 @@ from typing import List, Sequence
 import torch
 
 from ..core import relabel, sample_hop
-from ..core.ops import SampleState, sample_blocks
+from ..core.ops import CapturedSampleBlocks, SampleState, sample_blocks
 from ..data import BCSRGraph
 
 
@@ -44,11 +47,16 @@ class NeighborSampler:
         seed: Philox key (the stream is counter = (node, draw)).
         tile_cols: 16 (MFMA-native) or 8 (the reference's tile).
         values_dtype: dtype of the blocks' values_condensed.
+        capture: replay each batch from a HIP graph (fused path; one capture
+            per CSR graph, transposes flags and bucket of 64 seed counts).
     """
+
+    # captured batch shapes kept per sampler (least recently used dropped)
+    MAX_CAPTURES = 8
 
     def __init__(self, fanouts: Sequence[int], seed: int = 42, tile_rows: int = 16,
                  tile_cols: int = 16, values_dtype: torch.dtype = torch.float32,
-                 verbose: bool = False, fused: bool = True):
+                 verbose: bool = False, fused: bool = True, capture: bool = False):
         if tile_rows != 16:
             raise ValueError("tile_rows must be 16")
         if tile_cols not in (8, 16):
@@ -69,7 +77,9 @@ class NeighborSampler:
         # state kept per graph, one sync); otherwise sample_hop + relabel +
         # COO build per hop
         self.fused = bool(fused)
+        self.capture = bool(capture) and self.fused
         self._state = None
+        self._captures: dict = {}
 
     def sample_layers(self, indptr: torch.Tensor, indices: torch.Tensor,
                       seed_nodes: torch.Tensor, transposes=None) -> List[BCSRGraph]:
@@ -101,9 +111,12 @@ class NeighborSampler:
             hop_t = [bool(t) for t in reversed(list(transposes))]
             if not any(hop_t):
                 hop_t = None
-        batch = (sample_blocks(indptr, indices, frontier, hop_fanouts, self._state, seed=self.seed,
-                               tile_cols=self.tile_cols, values_dtype=self.values_dtype, transposes=hop_t)
-                 if self.fused else None)
+        batch = None
+        if self.capture and frontier.numel() > 0:
+            batch = self._captured(indptr, indices, hop_fanouts, hop_t, frontier.numel()).run(frontier)
+        elif self.fused:
+            batch = sample_blocks(indptr, indices, frontier, hop_fanouts, self._state, seed=self.seed,
+                                  tile_cols=self.tile_cols, values_dtype=self.values_dtype, transposes=hop_t)
         for h, k in enumerate(hop_fanouts):
             tr = None
             if self.fused:
@@ -152,6 +165,20 @@ class NeighborSampler:
             print(f"[NeighborSampler] {len(self.fanouts)} hops, {s['edges']} edges, "
                   f"{s['input_nodes']} input nodes, {1e3 * s['seconds']:.3f} ms")
         return blocks
+
+    def _captured(self, indptr, indices, hop_fanouts, hop_t, num_seeds: int) -> CapturedSampleBlocks:
+        """The captured batch of this shape (created on first use)."""
+        cap = -(-int(num_seeds) // 64) * 64
+        key = (indptr.data_ptr(), indices.data_ptr(), indptr.numel(), indices.numel(), tuple(hop_fanouts),
+               tuple(hop_t) if hop_t is not None else None, cap, self._state.node_map.data_ptr())
+        c = self._captures.pop(key, None)
+        if c is None:
+            if len(self._captures) >= self.MAX_CAPTURES:
+                self._captures.pop(next(iter(self._captures)))
+            c = CapturedSampleBlocks(indptr, indices, hop_fanouts, self._state, self.seed, self.tile_cols,
+                                     self.values_dtype, hop_t, cap)
+        self._captures[key] = c  # most recently used last
+        return c
 
     def __repr__(self) -> str:
         return (f"NeighborSampler(fanouts={self.fanouts}, seed={self.seed}, "

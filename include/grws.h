@@ -473,6 +473,37 @@ int grws_sample_blocks_transposed(const int64_t* indptr, const int32_t* indices,
                                   int32_t* const* t_col_indices, void* const* t_values, void* workspace,
                                   size_t workspace_bytes, int64_t* counts_out, void* stream);
 
+/* grws_sample_blocks(_transposed) for replay from a captured HIP graph: the */
+/* same work, enqueued on `stream` with no host sync.  Capacities, grids and */
+/* the workspace are those of max_seeds seeds (>= 1); the batch's seed      */
+/* count is read on the device from *num_seeds_dev (0 .. max_seeds; outside */
+/* that range the batch is empty and the error flag is set), and the seeds  */
+/* from seeds[0 .. count).  transpose_hops may be NULL (no transposes).      */
+/* Instead of counts_out, the counters are left in device memory:          */
+/* counts_dev[0 .. 5 num_hops + 1] = {F[0..H], E[H], T[H], TT[H], TM[H],    */
+/* err}: F[h] frontier sizes (F[h+1] = sources of hop h), E edges, T tiles, */
+/* TT / TM tiles of the transposed block and most tiles in one of its       */
+/* windows, err a flag word for grws_sample_blocks_error.  The reference    */
+/* syncs once per hop (sampling_wrapper.cu:340-344); this call syncs never, */
+/* so a caller can capture it once and replay it per batch.                 */
+int grws_sample_blocks_enqueue(const int64_t* indptr, const int32_t* indices, int64_t num_nodes, int64_t nnz,
+                               const int64_t* seeds, int64_t max_seeds, const int64_t* num_seeds_dev,
+                               const int32_t* fanouts, int32_t num_hops, uint64_t seed, int32_t* node_map,
+                               uint32_t* state, int32_t tile_cols, int32_t values_dtype,
+                               int64_t* const* next_frontier, int64_t* const* window_offset,
+                               int32_t* const* col_indices, void* const* values, const int32_t* transpose_hops,
+                               int64_t* const* t_window_offset, int32_t* const* t_col_indices,
+                               void* const* t_values, void* workspace, size_t workspace_bytes, int64_t* counts_dev,
+                               void* stream);
+/* The status (and grws_last_error message) of an enqueued batch's error    */
+/* flag, counts_dev[5 num_hops + 1] read back by the caller: GRWS_OK for 0. */
+int grws_sample_blocks_error(int64_t err);
+
+/* n device-to-device copies in one launch (32 ranges per launch): bytes[i] */
+/* bytes from src[i] to dst[i], both 16-byte aligned.  Used to hand out a   */
+/* replayed batch's outputs as compact tensors.  Asynchronous on `stream`.  */
+int grws_copy_ranges(const void* const* src, void* const* dst, const int64_t* bytes, int32_t n, void* stream);
+
 /* Input features of a sampled batch: dst row i = src row idx[i] for        */
 /* i < n, row_bytes bytes per row, rows ld_src / ld_dst bytes apart; idx is  */
 /* int64 (idx_is_i64 != 0) or int32.  An index outside [0, src_rows) gives a */
