@@ -609,9 +609,10 @@ def bench_minibatch(dev, batches: int, warmup: int) -> dict:
 def bench_dps(dev, cpu: bool, reps: int = 10) -> dict:
     """The next-row extensions: the halo repack of BCSRSampler.repack_subgraph
     (sampler.py:420-690) on c3 (a batch of 256 random windows = 4,096 seed
-    rows, external budget 5x, the reference's default), and loading a BCSR
-    cache in the reference's on-disk layout (data_loader.py:282-406) into
-    HBM, on c2 (page cache warm: host-memory-to-HBM rate, not the disk)."""
+    rows, external budget 5x, the reference's default), the reference's
+    window top-K sampler on c2, and loading a BCSR cache in the reference's
+    on-disk layout (data_loader.py:282-406) into HBM, on c2 (page cache warm:
+    host-memory-to-HBM rate, not the disk)."""
     import tempfile
 
     import numpy as np
@@ -672,6 +673,46 @@ def bench_dps(dev, cpu: bool, reps: int = 10) -> dict:
         t_load = time.perf_counter() - t0
         nbytes = 8 * H.window_offset.numel() + 4 * H.original_col_indices.numel() + 4 * H.values_condensed.numel()
         same = bool(torch.equal(H.values_condensed, G2.values_condensed.half()))
+    # the reference's own sampler (window top-K, BCSRSampler.sample_layers,
+    # sampler.py:186-279) on c2 with its defaults: 16x8 tiles, f32 values,
+    # 1,024 seeds, fanouts [15, 10, 5] (5 drawn first)
+    G8 = BCSRGraph.from_csr(g.row_ptr, g.col_idx, g.values, g.num_nodes, g.num_nodes, tile_cols=8, device=dev)
+    ws = BCSRSampler([15, 10, 5], tile_cols=8, verbose=False)
+    seed_sets = [synth.distinct_seeds(g.num_nodes, 1024, seed=500 + b, device=dev) for b in range(23)]
+    for b in range(3):
+        ws.sample_layers(G8, seed_sets[b])
+    torch.cuda.synchronize(dev)
+    tw = []
+    for b in range(3, 23):
+        t0 = time.perf_counter()
+        layers = ws.sample_layers(G8, seed_sets[b])
+        torch.cuda.synchronize(dev)
+        tw.append(time.perf_counter() - t0)
+    tiles = [int(x.window_offset[-1]) for x in layers]
+    wr = {"workload": "c2 window top-K sampling (BCSRSampler, 16x8 tiles, f32 values, 1,024 seeds, fanouts "
+                      "[15,10,5]): prepare windows, top-K per window, recompress, per layer",
+          "batch_ms": round(1e3 * sum(tw) / len(tw), 4), "batches": len(tw),
+          "tiles_last_batch": tiles, "active_windows_last_batch": [int(x.active_windows.numel()) for x in layers],
+          "host_syncs_per_batch": 3}
+    if cpu:
+        import oracle
+        seeds = seed_sets[-1].cpu().numpy()
+        win8 = G8.window_offset.cpu().numpy()
+        cols8 = G8.original_col_indices.cpu().numpy()
+        vals8 = G8.values_condensed.cpu().numpy()
+        t0 = time.perf_counter()
+        ref = oracle.window_sample_all_layers(win8, cols8, vals8, seeds, [5, 10, 15], g.num_nodes)
+        t_cpu = time.perf_counter() - t0
+        same = all(np.array_equal(x.window_offset.cpu().numpy(), r[0])
+                   and np.array_equal(x.original_col_indices.cpu().numpy(), r[1])
+                   and np.array_equal(x.values_condensed.cpu().numpy(), r[2])
+                   for x, r in zip(reversed(layers), ref))
+        wr["bit_exact_vs_oracle_last_batch"] = same
+        wr["cpu_baseline"] = {"value": round(1e3 * t_cpu, 2), "unit": "ms per batch", "cores": oracle.num_threads(),
+                              "kind": "port", "sample": "the last batch through oracle.window_sample_all_layers "
+                                                        "(C restatement; graph arrays in host memory)"}
+    out["window_sampling"] = wr
+    del G8
     out["bcsr_load"] = {"workload": "c2 BCSR cache (reference layout, f32 values) -> HBM, values to f16 on "
                                     "the device", "file_bytes": nbytes, "ms": round(1e3 * t_load, 2),
                         "gb_per_s": round(nbytes / t_load / 1e9, 2), "round_trip_equal": same}

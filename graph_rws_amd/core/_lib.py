@@ -137,6 +137,7 @@ _PROTOS = {
                                          ctypes.c_int32, _vp, _vp, _vp, ctypes.c_size_t, _c_i64p,
                                          _vp]),
     "grws_window_topk_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "grws_window_topk_key_scratch_bytes": (ctypes.c_size_t, [ctypes.POINTER(BcsrView)]),
     "grws_window_topk": (ctypes.c_int, [ctypes.POINTER(BcsrView), _vp, ctypes.c_int64,
                                         ctypes.c_int32, ctypes.POINTER(HacsView), _vp, _vp, _vp,
                                         _vp, ctypes.c_size_t, _c_i64p, _vp]),

@@ -739,6 +739,12 @@ def _hacs_view(dev, static_scores, window_part_ids, part_starts, part_ends, alph
                       1, 1 if locality_enabled else 0)
 
 
+# Key scratch lent to grws_window_topk for windows of more than 4,096 slots
+# (their keys computed once instead of once per selection pass); results do
+# not depend on it
+WINDOW_KEY_SCRATCH = 64 << 20
+
+
 def sample_all_layers(window_offset: torch.Tensor, original_col_indices: torch.Tensor,
                       values_condensed: torch.Tensor, initial_seeds: torch.Tensor, fanouts,
                       num_global_nodes: int, static_scores: Optional[torch.Tensor] = None,
@@ -786,7 +792,10 @@ def sample_all_layers(window_offset: torch.Tensor, original_col_indices: torch.T
         scols = torch.empty(max(A * S, 1), dtype=torch.int32, device=dev)
         sslot = torch.empty(max(A * S, 1), dtype=torch.int32, device=dev)
         out_off = torch.empty(A + 1, dtype=torch.int64, device=dev)
-        wsb = int(L.load().grws_window_topk_workspace_bytes(A))
+        # plus key scratch for the hub windows (more than 4,096 slots): at
+        # most the graph's slots, at most WINDOW_KEY_SCRATCH bytes
+        wsb = int(L.load().grws_window_topk_workspace_bytes(A)) + min(
+            int(L.load().grws_window_topk_key_scratch_bytes(ctypes.byref(view))), WINDOW_KEY_SCRATCH)
         ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
         T = ctypes.c_int64()
         L.call("grws_window_topk", ctypes.byref(view), L.ptr(active), A, f,

@@ -29,12 +29,13 @@
 //     column j (or -1) and its tile_rows values are that column's values in
 //     the input window (or 0), :520-578.
 //
-// Design: one 256-thread work-group per active window.  The 64-bit key
+// Design: one 1,024-thread work-group per active window.  The 64-bit key
 // (~total << 32 | column) orders candidates exactly as the reference's
 // comparator; an MSB-first 8-bit radix select over the window's slots (keys
-// recomputed from the values on every pass; the window stays in L2) finds the
-// CAP-th key, the selected (column, slot) pairs are compacted into LDS and
-// bitonic-sorted by column.  The slot index replaces the reference's linear
+// kept in LDS for windows of up to 4,096 slots, recomputed from the values on
+// every pass for larger ones; passes start at the first byte where the
+// candidates' keys differ) finds the CAP-th key, the selected (column, slot)
+// pairs are compacted into LDS and bitonic-sorted by column.  The slot index replaces the reference's linear
 // column search when the tiles are rebuilt.
 #include "grws_internal.h"
 
@@ -133,16 +134,48 @@ __device__ __forceinline__ bool slot_key(const int32_t* __restrict__ cols, const
     return true;
 }
 
+// One 1,024-thread work-group per active window.  The candidates' keys are
+// computed once (16 values each) and kept in LDS when the window has at most
+// kKeyCache slots, or for a larger (hub) window in the caller's key scratch
+// (a region claimed with one atomic on a cursor); a hub window that finds the
+// scratch full recomputes them on every pass, spread over the work-group's
+// 1,024 threads.  The count pass also finds the least
+// and greatest key, so the MSB-first radix select starts at the first byte
+// where they differ (the bytes above are common to every candidate).
+constexpr int kTopkBlk = 1024;
+constexpr int kKeyCache = 4096;
+
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const uint64_t o = __shfl_xor(v, d, kWave);
+        v = o < v ? o : v;
+    }
+    return v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const uint64_t o = __shfl_xor(v, d, kWave);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
 template <typename VT>
-__global__ __launch_bounds__(kBlk) void window_topk_kernel(const int64_t* __restrict__ win_off, int64_t num_windows,
-                                                           const int32_t* __restrict__ cols,
-                                                           const void* __restrict__ vals, int tc,
-                                                           const int32_t* __restrict__ active, int64_t num_active,
-                                                           ScoreParams p, int cap, int S,
-                                                           int32_t* __restrict__ out_cols,
-                                                           int32_t* __restrict__ out_slots,
-                                                           int32_t* __restrict__ out_tiles,
-                                                           int32_t* __restrict__ err) {
+__global__ __launch_bounds__(kTopkBlk) void window_topk_kernel(const int64_t* __restrict__ win_off, int64_t num_windows,
+                                                               const int32_t* __restrict__ cols,
+                                                               const void* __restrict__ vals, int tc,
+                                                               const int32_t* __restrict__ active, int64_t num_active,
+                                                               ScoreParams p, int cap, int S,
+                                                               int32_t* __restrict__ out_cols,
+                                                               int32_t* __restrict__ out_slots,
+                                                               int32_t* __restrict__ out_tiles,
+                                                               int32_t* __restrict__ err,
+                                                               uint64_t* __restrict__ gkeys, int64_t gcap,
+                                                               unsigned long long* __restrict__ gcursor) {
+    constexpr int NW = kTopkBlk / kWave;
+    __shared__ int64_t s_goff;
     __shared__ int32_t hist[256];
     __shared__ int32_t s_cnt;
     __shared__ uint64_t s_prefix;
@@ -150,6 +183,8 @@ __global__ __launch_bounds__(kBlk) void window_topk_kernel(const int64_t* __rest
     __shared__ int32_t s_k;
     __shared__ int32_t s_col[kMaxCap];
     __shared__ int32_t s_slot[kMaxCap];
+    __shared__ uint64_t s_key[kKeyCache];
+    __shared__ uint64_t s_min[NW], s_max[NW];
 
     const int64_t b = blockIdx.x;
     if (b >= num_active) return;
@@ -162,7 +197,7 @@ __global__ __launch_bounds__(kBlk) void window_topk_kernel(const int64_t* __rest
             atomicOr(err, kErrWindow);
             out_tiles[b] = 0;
         }
-        for (int i = tid; i < S; i += kBlk) {
+        for (int i = tid; i < S; i += kTopkBlk) {
             oc[i] = -1;
             os[i] = -1;
         }
@@ -170,6 +205,17 @@ __global__ __launch_bounds__(kBlk) void window_topk_kernel(const int64_t* __rest
     }
     const int64_t t0 = win_off[w];
     const int64_t nslots = (win_off[w + 1] - t0) * tc;
+    const bool cached = nslots <= kKeyCache;
+    if (tid == 0) {
+        int64_t off = -1;
+        if (!cached && gkeys) {
+            const int64_t o = (int64_t)atomicAdd(gcursor, (unsigned long long)nslots);
+            if (o + nslots <= gcap) off = o;
+        }
+        s_goff = off;
+    }
+    __syncthreads();
+    uint64_t* const gk = s_goff >= 0 ? gkeys + s_goff : nullptr;  // uniform over the work-group
     int32_t part_lo = 0, part_hi = 0;
     bool in_part_known = false;
     if (p.use_hacs && p.locality && p.window_part_ids && p.part_starts && p.part_ends) {
@@ -182,40 +228,112 @@ __global__ __launch_bounds__(kBlk) void window_topk_kernel(const int64_t* __rest
             in_part_known = true;
         }
     }
+    // a slot's key: from the LDS cache (~0: not a candidate), or recomputed
+    auto key_of = [&](int64_t s, uint64_t* k) -> bool {
+        if (cached) {
+            *k = s_key[s];
+            return *k != ~0ull;
+        }
+        if (gk) {
+            *k = gk[s];
+            return *k != ~0ull;
+        }
+        return slot_key<VT>(cols, vals, t0, tc, s, w, part_lo, part_hi, in_part_known, p, k);
+    };
 
-    // candidates
+    // candidates: count, least and greatest key (and the cache)
     if (tid == 0) s_cnt = 0;
     __syncthreads();
     {
         int local = 0;
-        for (int64_t s = tid; s < nslots; s += kBlk) {
+        uint64_t kmin = ~0ull, kmax = 0;
+        for (int64_t s = tid; s < nslots; s += kTopkBlk) {
             uint64_t k;
-            local += slot_key<VT>(cols, vals, t0, tc, s, w, part_lo, part_hi, in_part_known, p, &k) ? 1 : 0;
+            const bool c = slot_key<VT>(cols, vals, t0, tc, s, w, part_lo, part_hi, in_part_known, p, &k);
+            if (cached) s_key[s] = c ? k : ~0ull;
+            else if (gk) gk[s] = c ? k : ~0ull;
+            if (c) {
+                ++local;
+                kmin = k < kmin ? k : kmin;
+                kmax = k > kmax ? k : kmax;
+            }
             if (p.use_hacs) {
                 const int32_t col = cols[(t0 + s / tc) * tc + s % tc];
                 if (col != -1 && (col < 0 || (int64_t)col >= p.num_static_scores)) atomicOr(err, kErrHacs);
             }
         }
         if (local) atomicAdd(&s_cnt, local);
+        kmin = wave_min_u64(kmin);
+        kmax = wave_max_u64(kmax);
+        if ((tid & (kWave - 1)) == 0) {
+            s_min[tid / kWave] = kmin;
+            s_max[tid / kWave] = kmax;
+        }
     }
     __syncthreads();
     const int32_t count = s_cnt;
+
+    if (cached && count <= kTopkBlk) {
+        // a window of at most 1,024 candidates (most of them): a candidate's
+        // rank is the number of smaller keys (keys are distinct; ~0 marks a
+        // non-candidate and is above them all), the cap first are kept, and
+        // each kept one's output place is the number of kept columns below
+        // its own: two passes over LDS, two barriers, no select or sort
+        for (int64_t s = tid; s < nslots; s += kTopkBlk) {
+            const uint64_t k = s_key[s];
+            if (k == ~0ull) continue;
+            int r = 0;
+            for (int64_t q = 0; q < nslots; ++q) r += s_key[q] < k ? 1 : 0;
+            if (r < cap) {
+                s_col[r] = (int32_t)(uint32_t)k;
+                s_slot[r] = (int32_t)s;
+            }
+        }
+        __syncthreads();
+        const int nsel = count < cap ? count : cap;
+        for (int i = tid; i < nsel; i += kTopkBlk) {
+            const int32_t c = s_col[i];
+            int pos = 0;
+            for (int j = 0; j < nsel; ++j) pos += s_col[j] < c ? 1 : 0;
+            if (pos < S) {
+                oc[pos] = c;
+                os[pos] = s_slot[i];
+            }
+        }
+        for (int i = nsel + tid; i < S; i += kTopkBlk) {
+            oc[i] = -1;
+            os[i] = -1;
+        }
+        const int nout = nsel < S ? nsel : S;
+        if (tid == 0) out_tiles[b] = (nout + tc - 1) / tc;
+        return;
+    }
 
     // radix select of the cap-th smallest key (keys are distinct)
     uint64_t prefix = 0;
     int shift = 64;  // selected: key >> shift <= prefix >> shift (shift 64: all)
     if (count > cap) {
+        uint64_t kmin = s_min[0], kmax = s_max[0];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) {
+            kmin = s_min[i] < kmin ? s_min[i] : kmin;
+            kmax = s_max[i] > kmax ? s_max[i] : kmax;
+        }
+        // the bytes above the first one where the least and greatest key
+        // differ are the same in every candidate
+        const int hb = 63 - __clzll((long long)(kmin ^ kmax));  // count > cap >= 32: kmin != kmax
+        const int sh0 = (hb / 8) * 8;
         if (tid == 0) {
             s_k = cap;
-            s_prefix = 0;
+            s_prefix = sh0 >= 56 ? 0ull : (kmax >> (sh0 + 8)) << (sh0 + 8);
         }
-        for (int sh = 56; sh >= 0; sh -= 8) {
-            hist[tid] = 0;
+        for (int sh = sh0; sh >= 0; sh -= 8) {
+            if (tid < 256) hist[tid] = 0;
             __syncthreads();
             const uint64_t pre = s_prefix;
-            for (int64_t s = tid; s < nslots; s += kBlk) {
+            for (int64_t s = tid; s < nslots; s += kTopkBlk) {
                 uint64_t k;
-                if (!slot_key<VT>(cols, vals, t0, tc, s, w, part_lo, part_hi, in_part_known, p, &k)) continue;
+                if (!key_of(s, &k)) continue;
                 if (sh < 56 && (k >> (sh + 8)) != (pre >> (sh + 8))) continue;
                 atomicAdd(&hist[(k >> sh) & 255u], 1);
             }
@@ -240,14 +358,14 @@ __global__ __launch_bounds__(kBlk) void window_topk_kernel(const int64_t* __rest
 
     // compact the selected (column, slot) pairs
     if (tid == 0) s_cnt = 0;
-    for (int i = tid; i < kMaxCap; i += kBlk) {
+    for (int i = tid; i < kMaxCap; i += kTopkBlk) {
         s_col[i] = INT32_MAX;
         s_slot[i] = -1;
     }
     __syncthreads();
-    for (int64_t s = tid; s < nslots; s += kBlk) {
+    for (int64_t s = tid; s < nslots; s += kTopkBlk) {
         uint64_t k;
-        if (!slot_key<VT>(cols, vals, t0, tc, s, w, part_lo, part_hi, in_part_known, p, &k)) continue;
+        if (!key_of(s, &k)) continue;
         if (shift < 64 && (k >> shift) > (prefix >> shift)) continue;
         const int i = atomicAdd(&s_cnt, 1);
         if (i < kMaxCap) {
@@ -262,7 +380,7 @@ __global__ __launch_bounds__(kBlk) void window_topk_kernel(const int64_t* __rest
     for (int size = 2; size <= kMaxCap; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             const int j = tid ^ stride;
-            if (j > tid) {
+            if (tid < kMaxCap && j > tid) {
                 const bool up = (tid & size) == 0;
                 const int32_t a = s_col[tid], c = s_col[j];
                 if ((a > c) == up) {
@@ -278,14 +396,13 @@ __global__ __launch_bounds__(kBlk) void window_topk_kernel(const int64_t* __rest
     }
 
     const int nout = nsel < S ? nsel : S;
-    for (int i = tid; i < S; i += kBlk) {
+    for (int i = tid; i < S; i += kTopkBlk) {
         oc[i] = i < nout ? s_col[i] : -1;
         os[i] = i < nout ? s_slot[i] : -1;
     }
     if (tid == 0) out_tiles[b] = (nout + tc - 1) / tc;
 }
 
-// Output tile t of window b holds sample columns t*tc .. t*tc+tc-1.
 template <typename VT>
 __global__ __launch_bounds__(kBlk) void window_recompress_kernel(const int64_t* __restrict__ win_off,
                                                                  int64_t num_windows,
@@ -484,6 +601,14 @@ extern "C" size_t grws_window_topk_workspace_bytes(int64_t num_active) {
     return s.used;
 }
 
+// Workspace beyond grws_window_topk_workspace_bytes(num_active) is key
+// scratch for windows of more than 4,096 slots (8 bytes per slot of each
+// such active window; a window that does not fit recomputes its keys).
+extern "C" size_t grws_window_topk_key_scratch_bytes(const grws_bcsr* A) {
+    if (!A || A->num_tiles < 0) return 0;
+    return (size_t)(A->num_tiles * A->tile_cols) * 8 + 256;
+}
+
 extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
                                 int32_t fanout, const grws_hacs* hacs, int32_t* sampled_cols,
                                 int32_t* sampled_slots, int64_t* out_window_offset, void* workspace,
@@ -532,23 +657,41 @@ extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_window
     const size_t scan_bytes = scan_workspace_bytes(num_active);
     char* scan_ws = cv.take<char>(scan_bytes);
     if (!cv.ok) return set_error(GRWS_E_CAPACITY, "window_topk: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+    // the rest: a cursor and the hub windows' key scratch
+    unsigned long long* gcursor = nullptr;
+    uint64_t* gkeys = nullptr;
+    int64_t gcap = 0;
+    {
+        Carver rest = cv;
+        unsigned long long* cur = rest.take<unsigned long long>(1);
+        if (rest.ok && rest.used + 256 <= rest.cap) {
+            const size_t left = rest.cap - rest.used - 256;
+            uint64_t* keys = rest.take<uint64_t>(left / 8);
+            if (rest.ok && left / 8 > 0) {
+                gcursor = cur;
+                gkeys = keys;
+                gcap = (int64_t)(left / 8);
+            }
+        }
+    }
     GRWS_TRY(fill_i32(err, 1, 0, stream));
+    if (gcursor) GRWS_TRY(fill_i32(reinterpret_cast<int32_t*>(gcursor), 2, 0, stream));
     switch (A->values_dtype) {
         case GRWS_F32:
-            hipLaunchKernelGGL(window_topk_kernel<float>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
+            hipLaunchKernelGGL(window_topk_kernel<float>, dim3((unsigned)num_active), dim3(kTopkBlk), 0, stream,
                                A->window_offset, A->num_windows, A->col_indices, A->values, (int)A->tile_cols,
-                               active_windows, num_active, p, cap, S, sampled_cols, sampled_slots, tiles, err);
+                               active_windows, num_active, p, cap, S, sampled_cols, sampled_slots, tiles, err, gkeys, gcap, gcursor);
             break;
         case GRWS_F16:
-            hipLaunchKernelGGL(window_topk_kernel<_Float16>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
+            hipLaunchKernelGGL(window_topk_kernel<_Float16>, dim3((unsigned)num_active), dim3(kTopkBlk), 0, stream,
                                A->window_offset, A->num_windows, A->col_indices, A->values, (int)A->tile_cols,
-                               active_windows, num_active, p, cap, S, sampled_cols, sampled_slots, tiles, err);
+                               active_windows, num_active, p, cap, S, sampled_cols, sampled_slots, tiles, err, gkeys, gcap, gcursor);
             break;
         default:
-            hipLaunchKernelGGL(window_topk_kernel<__hip_bfloat16>, dim3((unsigned)num_active), dim3(kBlk), 0,
+            hipLaunchKernelGGL(window_topk_kernel<__hip_bfloat16>, dim3((unsigned)num_active), dim3(kTopkBlk), 0,
                                stream, A->window_offset, A->num_windows, A->col_indices, A->values,
                                (int)A->tile_cols, active_windows, num_active, p, cap, S, sampled_cols, sampled_slots,
-                               tiles, err);
+                               tiles, err, gkeys, gcap, gcursor);
             break;
     }
     GRWS_LAUNCH_CHECK();

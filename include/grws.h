@@ -570,8 +570,14 @@ int grws_window_seeds(const int32_t* ids, int64_t num_ids, int64_t num_nodes, in
 /* ascending, first min(kept, S) kept.  Writes sampled_cols [num_active * S] */
 /* (-1 padded), sampled_slots [num_active * S] (the column's slot index in   */
 /* its input window), out_window_offset [num_active+1] int64; synchronises   */
-/* and returns the output tile count.  fanout in [1, 256].                   */
+/* and returns the output tile count.  fanout in [1, 256].  A workspace     */
+/* larger than grws_window_topk_workspace_bytes(num_active) lends the rest   */
+/* to windows of more than 4,096 slots as key scratch (8 bytes per slot;   */
+/* grws_window_topk_key_scratch_bytes(A) covers every window of A): their   */
+/* keys are then computed once instead of once per selection pass.  The     */
+/* results do not depend on it.                                              */
 size_t grws_window_topk_workspace_bytes(int64_t num_active);
+size_t grws_window_topk_key_scratch_bytes(const grws_bcsr* A);
 int grws_window_topk(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
                      int32_t fanout, const grws_hacs* hacs, int32_t* sampled_cols,
                      int32_t* sampled_slots, int64_t* out_window_offset, void* workspace,

@@ -154,3 +154,21 @@ def test_bcsr_sampler_layers(cuda_device):
         assert L.num_tiles == L.window_offset[-1].item()
     assert set(s.time_tracker) == {0, 1}
     assert "BCSRSampler" in repr(s)
+
+
+@pytest.mark.parametrize("scratch", [0, 300_000])
+def test_window_topk_hub_windows_without_key_scratch(cuda_device, monkeypatch, scratch):
+    """Windows of more than 4,096 slots keep their keys in the caller's
+    scratch when it has room and recompute them on every pass when it has
+    none (0 bytes) or runs out part-way (300 kB: some hub windows fit): the
+    same layers either way, bit for bit against the oracle."""
+    from graph_rws_amd.core import ops
+    print(f"case window top-K key scratch {scratch}", flush=True)
+    monkeypatch.setattr(ops, "WINDOW_KEY_SCRATCH", scratch)
+    g, G = _graph("c2", cuda_device)
+    seeds = synth.distinct_seeds(g.num_nodes, 1024, seed=9).numpy()
+    layers, _ = sample_all_layers(G.window_offset, G.original_col_indices, G.values_condensed,
+                                  torch.from_numpy(seeds).to(cuda_device), [5, 10, 15], g.num_nodes)
+    ref = oracle.window_sample_all_layers(G.window_offset.cpu().numpy(), G.original_col_indices.cpu().numpy(),
+                                          G.values_condensed.cpu().numpy(), seeds, [5, 10, 15], g.num_nodes)
+    _compare(layers, ref)
