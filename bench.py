@@ -66,6 +66,73 @@ def build_graph(cfg: str, tc: int, vdt: torch.dtype, dev: torch.device):
     return g, G, t1 - t0, t2 - t1
 
 
+def bench_build(g, dev, cpu: bool, reps: int = 5) -> dict:
+    """The device BCSR build (csr_to_bcsr, H3) of the headline graph: CSR
+    (int64 row pointer, int32 columns, f32 values) -> 16x16 BCSR with f16
+    values, and the build of its transpose (the backward's operand).  Wall
+    time per build (each build synchronises once to size its outputs),
+    median of `reps`.  Bytes the algorithm moves: the CSR read, per radix
+    pass the keys read by the histogram (8 B) and keys + payload read and
+    written by the scatter (24 B) per edge, the flags/scans over the sorted
+    edges (~16 B per edge) and the BCSR written."""
+    from graph_rws_amd import builder
+    n, nnz = g.num_nodes, g.nnz
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize(dev)
+        ts, out = [], None
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            out = fn()
+            torch.cuda.synchronize(dev)
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        return ts[len(ts) // 2], out
+
+    t_fwd, (win, cols, vals) = timed(lambda: builder.csr_to_bcsr_device(
+        n, n, g.row_ptr, g.col_idx, g.values, tile_cols=16, values_dtype=torch.float16))
+    W, T = win.numel() - 1, cols.numel() // 16
+    bits = max(1, (W - 1).bit_length()) + max(1, (n - 1).bit_length()) + 4
+    passes = -(-bits // 8)
+    b_alg = 8 * (n + 1) + 8 * nnz + passes * 32 * nnz + 16 * nnz + 8 * (W + 1) + 4 * T * 16 + 2 * T * 256
+    t_tr, _ = timed(lambda: builder.transpose_arrays(win, cols, vals, 16, n))
+    gbs = b_alg / t_fwd / 1e9
+    r = {"workload": f"device BCSR build of the {nnz:,}-edge headline graph: CSR -> 16x16 BCSR, f16 values",
+         "ms": round(1e3 * t_fwd, 3), "edges_per_s": round(nnz / t_fwd, 1), "radix_passes": passes,
+         "transpose_ms": round(1e3 * t_tr, 3),
+         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": int(b_alg),
+                      "note": "algorithmic bytes of this build (sort passes included), wall time with "
+                              "its one sync"}}
+    if cpu:
+        import oracle
+        rows = n
+        e = int(g.row_ptr[rows])
+        rp = g.row_ptr[:rows + 1].cpu().numpy()
+        ci = g.col_idx[:e].cpu().numpy()
+        va = g.values[:e].float().cpu().numpy()
+        kind, fn = "reference", lambda: oracle.ref_csr_to_bcsr(rows, rp, ci, va, 16, 16)
+        if oracle.ref_csr_to_bcsr(16, rp[:17], ci[:int(rp[16])], va[:int(rp[16])], 16, 16) is None:
+            from graph_rws_amd import core
+            kind = "port"
+            fn = lambda: core.csr_to_bcsr_cpu(rows, torch.from_numpy(rp), torch.from_numpy(ci),
+                                              torch.from_numpy(va), 16, 16)
+        t0 = time.perf_counter()
+        fn()
+        t_cpu = time.perf_counter() - t0
+        r["cpu_baseline"] = {"value": round(e / t_cpu, 1), "unit": "edges/s", "cores": os.cpu_count(),
+                             "kind": kind,
+                             "sample": f"rows 0..{rows} ({e:,} edges) through "
+                                       + ("the reference's csr_to_bcsr_cpu (convert_wrapper.cpp, compiled "
+                                          "into oracle/_ref, OpenMP)" if kind == "reference"
+                                          else "the host converter (csrc/abi.cpp, OpenMP)")
+                                       + f", {t_cpu:.2f} s"}
+    del win, cols, vals
+    torch.cuda.empty_cache()
+    return r
+
+
 def alg_bytes(G, N: int, s_x: int, s_y: int, packed=None, plan=None, grouped=None) -> dict:
     """Bytes one SpMM must move, two ways.
 
@@ -814,6 +881,7 @@ def main():
     ap.add_argument("--tile-cols", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sampling", action="store_true")
+    ap.add_argument("--no-build", action="store_true", help="skip the device BCSR build record")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 5 device-to-device copies of BYTES (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -987,6 +1055,8 @@ def main():
         out["cpu_baseline"] = cb
     else:
         out["parity"] = {"pass": None, "note": "not checked (--no-cpu-baseline)"}
+    if not args.no_build:
+        out["bcsr_build"] = bench_build(g, dev, not args.no_cpu_baseline)
     if not args.no_sampling:
         del G, X, Y, g, plan
         torch.cuda.empty_cache()
