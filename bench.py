@@ -949,7 +949,7 @@ def main():
     for _ in range(max(2, args.warmup)):
         G.spmm(X, out=Y)
     torch.cuda.synchronize(dev)
-    grouped = G.grouped_tiles(X.shape[0]) if N >= _ops.GROUP_MIN_N else None
+    grouped = G.grouped_tiles(X.shape[0], N) if N >= _ops.GROUP_MIN_N else None
     if grouped is not None:
         a_format = f"grouped tiles ({grouped.group_size} windows)"
     else:

@@ -291,14 +291,26 @@ class GroupedTiles:
 # mean group's slabs (groups are not split across work-groups).
 GROUP_MAX_RATIO = 0.8
 GROUP_MAX_SKEW = 4.0
-GROUP_SIZE = 2
+# windows per group: None picks by the product's width (group_size_for);
+# an int fixes it
+GROUP_SIZE = None
+def group_size_for(n_cols: int) -> int:
+    """Windows per group for products n_cols wide (measured on c3, f16):
+    four up to 256 columns (N = 256: 2.16 against 2.25 ms with two; more
+    gathers saved than sub-tile headers added), two above (N = 608: 5.37
+    against 5.62 ms with four)."""
+    if GROUP_SIZE:
+        return int(GROUP_SIZE)
+    return 4 if n_cols <= 256 else 2
+
+
 # narrower products stay on the window-by-window kernel: a grouped chunk is
 # at least 128 columns wide (measured on c3: N = 48 took twice as long)
 GROUP_MIN_N = 192
 
 
 def group_tiles(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch.Tensor, tile_cols: int,
-                num_cols: int, group_size: int = GROUP_SIZE, max_ratio: Optional[float] = None,
+                num_cols: int, group_size: Optional[int] = None, max_ratio: Optional[float] = None,
                 max_skew: Optional[float] = None) -> Optional[GroupedTiles]:
     """Builds grouped tiles on the device (one stream sync), or returns None
     when they do not apply (dtype, shape) or would not pay: the union of the
@@ -307,6 +319,7 @@ def group_tiles(window_offset: torch.Tensor, col_indices: torch.Tensor, values: 
     if values.dtype not in (torch.float16, torch.bfloat16) or tile_cols not in (8, 16) or not values.is_cuda:
         return None
     _check_graph(window_offset, col_indices, values, tile_cols)
+    group_size = (GROUP_SIZE or 2) if group_size is None else group_size
     max_ratio = GROUP_MAX_RATIO if max_ratio is None else max_ratio
     max_skew = GROUP_MAX_SKEW if max_skew is None else max_skew
     lib = L.load()

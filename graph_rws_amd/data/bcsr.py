@@ -278,12 +278,13 @@ class BCSRGraph:
             self._cache["packed"] = (key, 2, p)
         return p or None
 
-    def grouped_tiles(self, num_cols: int):
+    def grouped_tiles(self, num_cols: int, n_cols: int = 0):
         """Grouped tiles (windows sharing their union columns, see
         core.ops.group_tiles) for products over num_cols X rows, built on
-        this graph's second such product and kept while the arrays are
-        unchanged; None when grouping is off, does not apply, or would not
-        pay on this graph (decided once per graph state)."""
+        this graph's second such product (with the group size that suits
+        that product's width n_cols, core.ops.group_size_for) and kept while
+        the arrays are unchanged; None when grouping is off, does not apply,
+        or would not pay on this graph (decided once per graph state)."""
         from ..core import ops as _ops
         if (not _ops.GROUPED or not _ops.PACK_TILES or getattr(self, "refilled", False)
                 or self.values_condensed.dtype not in (torch.float16, torch.bfloat16)):
@@ -297,7 +298,7 @@ class BCSRGraph:
         key, calls, g = ent
         if g is None and calls == 1:
             g = _ops.group_tiles(self.window_offset, self.original_col_indices, self.values_condensed,
-                                 self.tile_cols, int(num_cols)) or False
+                                 self.tile_cols, int(num_cols), group_size=_ops.group_size_for(n_cols)) or False
             self._cache["grouped"] = (key, 2, g)
         return g or None
 
@@ -355,7 +356,7 @@ class BCSRGraph:
         x = self._gather_input(x)
         same = x.dtype == self.values_condensed.dtype
         from ..core import ops as _ops
-        grouped = (self.grouped_tiles(x.shape[0])
+        grouped = (self.grouped_tiles(x.shape[0], x.shape[1])
                    if _ops.grouped_supported(x, self.values_condensed) and x.shape[1] >= _ops.GROUP_MIN_N else None)
         return _spmm(self.window_offset, self.original_col_indices, self.values_condensed, x,
                      self.tile_cols, plan=None if grouped is not None else self.spmm_plan(x.shape[1]), out=out,

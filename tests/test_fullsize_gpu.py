@@ -73,7 +73,7 @@ def test_c3_headline_n608_bench_path(c3, cuda_device, monkeypatch):
     G.spmm(X, out=Y1)
     G.spmm(X, out=Y2)
     torch.cuda.synchronize()
-    gt = G.grouped_tiles(X.shape[0])
+    gt = G.grouped_tiles(X.shape[0], 608)
     assert gt is not None and gt.slot_ratio < ops.GROUP_MAX_RATIO, "c3 must take the grouped tiles"
     print(check_forward(hg, X, Y2, RTOL, plan=plan, seed=3), flush=True)
     print(check_forward(hg, X, Y1, RTOL, plan=plan, seed=4), flush=True)

@@ -182,8 +182,15 @@ def test_graph_groups_its_tiles_when_it_pays(cuda_device):
     gt = A._cache["grouped"][2]
     assert gt, "c3-like graph not grouped"
     assert gt.slot_ratio <= ops.GROUP_MAX_RATIO
+    assert gt.group_size == ops.group_size_for(256) == 4  # the group size suits the product's width
     torch.testing.assert_close(y1.float(), y2.float(), rtol=2 ** -10, atol=2 ** -14)
     _oracle_check(A, X, y2)
+    _, A2 = _graph(cuda_device, torch.float16, 16, scale=0.01)
+    X6 = torch.randn(A2.num_cols, 608, device=cuda_device).half()
+    A2.spmm(X6)
+    y6 = A2.spmm(X6)
+    assert A2._cache["grouped"][2].group_size == ops.group_size_for(608) == 2
+    _oracle_check(A2, X6, y6)
     _, B = _graph(cuda_device, torch.float16, 16, scale=0.01, cfg="c4")
     Xb = torch.randn(B.num_cols, 256, device=cuda_device).half()
     B.spmm(Xb)
