@@ -144,6 +144,47 @@ __global__ void build_keys_kernel(const int64_t* __restrict__ row_ptr, const int
     pay[i] = vals ? __float_as_uint(vals[i]) : 0x3f800000u;  // 1.0f when no values are given
 }
 
+// The same keys from a CSR, one wave per row: the row is known, its edges
+// [row_ptr[r], row_ptr[r+1]) are read in order (a per-edge binary search for
+// the row took 2.3 ms on 115M edges).  A valid row pointer covers [0, nnz)
+// exactly, so every edge gets its key.  check_row_ptr_kernel runs first: when
+// it flagged the row pointer, every key is written as 0 instead (in range for
+// the kernels after the sort; the call then reports the error).
+__global__ __launch_bounds__(256) void build_keys_rows_kernel(const int64_t* __restrict__ row_ptr,
+                                                              const int32_t* __restrict__ cols,
+                                                              const float* __restrict__ vals, int64_t n,
+                                                              int64_t num_rows, int64_t num_cols, int transpose,
+                                                              int cbits, uint64_t* __restrict__ keys,
+                                                              uint32_t* __restrict__ pay, int32_t* __restrict__ err) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x / kWave);
+    if (*err & kErrRowPtr) {  // uniform: set by the check before this launch
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+            keys[i] = 0;
+            pay[i] = 0;
+        }
+        return;
+    }
+    for (int64_t r = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave; r < num_rows; r += nwaves) {
+        int64_t lo = row_ptr[r], hi = row_ptr[r + 1];
+        lo = lo < 0 ? 0 : (lo > n ? n : lo);
+        hi = hi < lo ? lo : (hi > n ? n : hi);
+        bool bad = false;
+        for (int64_t i = lo + lane; i < hi; i += kWave) {
+            int64_t c = cols[i];
+            if (c < 0 || c >= num_cols) {
+                bad = true;
+                c = 0;
+            }
+            const int64_t wr = transpose ? c : r;
+            const int64_t cc = transpose ? r : c;
+            keys[i] = ((uint64_t)(wr >> 4) << (cbits + 4)) | ((uint64_t)cc << 4) | (uint64_t)(wr & 15);
+            pay[i] = vals ? __float_as_uint(vals[i]) : 0x3f800000u;  // 1.0f when no values are given
+        }
+        if (bad) atomicOr(err, kErrCol);
+    }
+}
+
 __global__ void unique_flag_kernel(const uint64_t* __restrict__ keys, int64_t n, int32_t* __restrict__ uflag) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -187,9 +228,10 @@ template <typename VT>
 __global__ void build_scatter_kernel(const uint64_t* __restrict__ keys, const uint32_t* __restrict__ pay, int64_t n,
                                      int cbits, const int32_t* __restrict__ uflag, const int64_t* __restrict__ uidx,
                                      const int64_t* __restrict__ wstart, const int64_t* __restrict__ win_off,
-                                     int tc, int32_t* __restrict__ out_cols, void* __restrict__ out_vals) {
+                                     int tc, int32_t* __restrict__ out_cols, void* __restrict__ out_vals,
+                                     const int32_t* __restrict__ err) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
+    if (i >= n || err[2] == 1) return;  // err[2] == 1: the per-window build ran
     const uint64_t k = keys[i];
     const int wshift = cbits + 4;
     const int64_t w = (int64_t)(k >> wshift);
@@ -201,6 +243,154 @@ __global__ void build_scatter_kernel(const uint64_t* __restrict__ keys, const ui
     const int c = (int)(p % tc);
     if (f) out_cols[tile * tc + c] = (int32_t)col;
     if (i == n - 1 || keys[i + 1] != k) store_value<VT>(out_vals, (tile * 16 + r) * tc + c, __uint_as_float(pay[i]));
+}
+
+// --- per-window CSR build ---------------------------------------------------
+// A CSR's edges come grouped by window already (16 consecutive rows), so when
+// every window has at most kWinCap edges (c3: at most 8,246) each window is
+// built by one work-group from LDS, with no global sort: the window's keys
+// (column << 18 | row-in-window << 14 | edge offset in the window) are
+// bitonic-sorted in LDS, the distinct columns counted, and the sorted keys
+// with their values kept in the workspace for the fill.  Keys are distinct
+// (the offset), so of duplicate (row, column) edges the one last in CSR order
+// sorts last and is the one stored, as with the global sort.
+constexpr int kWinCap = 16384;  // windows of up to 8,192 edges use a half-size LDS twin
+constexpr int kWinBlk = 512;
+
+// Windows with more than kWinCap edges (err[1]), from a valid row pointer.
+__global__ void win_big_kernel(const int64_t* __restrict__ row_ptr, int64_t R, int64_t W, int64_t n,
+                               int32_t* __restrict__ err) {
+    const int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (w >= W) return;
+    const int64_t r1 = 16 * w + 16 < R ? 16 * w + 16 : R;
+    if (row_ptr[r1] - row_ptr[16 * w] > kWinCap) atomicAdd(&err[1], 1);
+}
+
+template <int CAP>
+__global__ __launch_bounds__(kWinBlk) void win_sort_kernel(const int64_t* __restrict__ row_ptr,
+                                                            const int32_t* __restrict__ cols,
+                                                            const float* __restrict__ vals, int64_t n, int64_t R,
+                                                            int64_t W, int64_t num_cols, int tc,
+                                                            uint64_t* __restrict__ skeys, uint32_t* __restrict__ svals,
+                                                            int64_t* __restrict__ wstart, int64_t* __restrict__ wend,
+                                                            int32_t* __restrict__ wtiles, int32_t* __restrict__ err) {
+    // CAP 8192: the windows of at most 8,192 edges; CAP 16384: the larger
+    // ones (at most kWinCap edges: checked before the launch)
+    __shared__ uint64_t key[CAP];
+    __shared__ int64_t rp[17];
+    __shared__ int32_t cnt[kWinBlk / kWave];
+    const int tid = threadIdx.x;
+    for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {  // uniform over the work-group
+        const int64_t r0 = 16 * w;
+        const int nr = (int)(R - r0 < 16 ? R - r0 : 16);
+        if (tid <= nr) {
+            int64_t v = row_ptr[r0 + tid];
+            rp[tid] = v < 0 ? 0 : (v > n ? n : v);
+        }
+        __syncthreads();
+        const int64_t e0 = rp[0];
+        const int m = (int)(rp[nr] - e0);
+        if ((CAP == 8192) != (m <= 8192)) {  // the other launch's window (uniform)
+            __syncthreads();
+            continue;
+        }
+        int P = 1;
+        while (P < m) P <<= 1;  // <= CAP
+        bool bad = false;
+        for (int j = tid; j < P; j += kWinBlk) {
+            uint64_t k = ~0ull;
+            if (j < m) {
+                const int64_t e = e0 + j;
+                int q = 0;
+                while (q + 1 < nr && rp[q + 1] <= e) ++q;
+                int64_t c = cols[e];
+                if (c < 0 || c >= num_cols) {
+                    bad = true;
+                    c = 0;
+                }
+                k = ((uint64_t)c << 18) | ((uint64_t)q << 14) | (uint64_t)j;
+            }
+            key[j] = k;
+        }
+        if (bad) atomicOr(err, kErrCol);
+        __syncthreads();
+        for (int size = 2; size <= P; size <<= 1) {
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                for (int i = tid; i < P; i += kWinBlk) {
+                    const int j = i ^ stride;
+                    if (j > i) {
+                        const bool up = (i & size) == 0;
+                        const uint64_t a = key[i], b = key[j];
+                        if ((a > b) == up) {
+                            key[i] = b;
+                            key[j] = a;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        int u = 0;
+        for (int i = tid; i < m; i += kWinBlk) {
+            const uint64_t k = key[i];
+            u += (i == 0 || (key[i - 1] >> 18) != (k >> 18)) ? 1 : 0;
+            skeys[e0 + i] = k;
+            svals[e0 + i] = vals ? __float_as_uint(vals[e0 + (int64_t)(k & 16383u)]) : 0x3f800000u;
+        }
+        for (int d = kWave / 2; d >= 1; d >>= 1) u += __shfl_xor(u, d, kWave);
+        if ((tid & (kWave - 1)) == 0) cnt[tid / kWave] = u;
+        __syncthreads();
+        if (tid == 0) {
+            int t = 0;
+            for (int i = 0; i < kWinBlk / kWave; ++i) t += cnt[i];
+            wtiles[w] = (t + tc - 1) / tc;
+            wstart[w] = e0;
+            wend[w] = e0 + m;
+        }
+        __syncthreads();  // key[], rp[] and cnt[] are rewritten for the next window
+    }
+}
+
+// The fill of the per-window build (err[2] = 1; the global path's scatter
+// exits then, and this kernel exits otherwise).
+template <typename VT>
+__global__ __launch_bounds__(kWinBlk) void win_fill_kernel(const uint64_t* __restrict__ skeys,
+                                                            const uint32_t* __restrict__ svals,
+                                                            const int64_t* __restrict__ wstart,
+                                                            const int64_t* __restrict__ wend,
+                                                            const int64_t* __restrict__ win_off, int64_t W, int tc,
+                                                            int32_t* __restrict__ out_cols, void* __restrict__ out_vals,
+                                                            const int32_t* __restrict__ err) {
+    __shared__ int64_t tmp[kWinBlk / kWave + 1];
+    if (err[2] != 1) return;  // uniform
+    const int tid = threadIdx.x;
+    for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {  // uniform over the work-group
+        const int64_t e0 = wstart[w], m = wend[w] - e0, wo = win_off[w];
+        int64_t run = 0;
+        for (int64_t b = 0; b < m; b += kWinBlk) {  // uniform over the work-group
+            const int64_t i = b + tid;
+            const bool v = i < m;
+            uint64_t k = 0;
+            int f = 0;
+            if (v) {
+                k = skeys[e0 + i];
+                f = (i == 0 || (skeys[e0 + i - 1] >> 18) != (k >> 18)) ? 1 : 0;
+            }
+            int64_t tot;
+            const int64_t inc = block_incl_scan<kWinBlk>(f, tmp, &tot);
+            if (v) {
+                const int64_t p = run + inc - 1;  // the column's place among the window's distinct columns
+                const int64_t tile = wo + p / tc;
+                const int c = (int)(p % tc);
+                if (f) out_cols[tile * tc + c] = (int32_t)(k >> 18);
+                if (i == m - 1 || (skeys[e0 + i + 1] >> 14) != (k >> 14)) {
+                    const int r = (int)((k >> 14) & 15u);
+                    store_value<VT>(out_vals, (tile * 16 + r) * tc + c, __uint_as_float(svals[e0 + i]));
+                }
+            }
+            run += tot;
+        }
+    }
 }
 
 // --- BCSR -> COO ---------------------------------------------------------
@@ -366,7 +556,7 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
     carve_build(cv, s, &w);
     if (!cv.ok) return set_error(GRWS_E_CAPACITY, "bcsr_build: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
 
-    GRWS_TRY(fill_i32(w.err, 1, 0, stream));
+    GRWS_TRY(fill_i32(w.err, 3, 0, stream));  // error flags, big windows, path of the fill
     if (s.W == 0) {
         GRWS_TRY(fill_i64(window_offset, 1, 0, stream));
         GRWS_HIP(hipStreamSynchronize(stream));
@@ -380,10 +570,41 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
                            num_rows, nnz, w.err);
         GRWS_LAUNCH_CHECK();
     }
+    // a CSR whose windows all hold at most kWinCap edges is built window by
+    // window from LDS (one sync decides); anything else by the global sort
+    bool per_window = false;
+    if (row_ptr && !transpose && nnz > 0) {
+        hipLaunchKernelGGL(win_big_kernel, dim3(grid_for(s.W)), dim3(kBlk), 0, stream, row_ptr, s.R, s.W, nnz, w.err);
+        GRWS_LAUNCH_CHECK();
+        int32_t h[2] = {0, 0};
+        GRWS_HIP(hipMemcpyAsync(h, w.err, 2 * sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+        GRWS_HIP(hipStreamSynchronize(stream));
+        per_window = (h[0] & kErrRowPtr) == 0 && h[1] == 0;
+    }
+    if (per_window) {
+        GRWS_TRY(fill_i32(w.err + 2, 1, 1, stream));
+        const unsigned wg = (unsigned)std::min<int64_t>(s.W, 4096);
+        hipLaunchKernelGGL(win_sort_kernel<8192>, dim3(wg), dim3(kWinBlk), 0, stream, row_ptr, cols, values, nnz, s.R,
+                           s.W, num_cols, (int)tile_cols, w.ka, w.va, w.wstart, w.wend, w.wtiles, w.err);
+        GRWS_LAUNCH_CHECK();
+        hipLaunchKernelGGL(win_sort_kernel<16384>, dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0, stream, row_ptr,
+                           cols, values, nnz, s.R, s.W, num_cols, (int)tile_cols, w.ka, w.va, w.wstart, w.wend,
+                           w.wtiles, w.err);
+        GRWS_LAUNCH_CHECK();
+    }
     bool alt = false;
-    if (nnz > 0) {
-        hipLaunchKernelGGL(build_keys_kernel, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, row_ptr, rows, cols, values,
-                           nnz, num_rows, num_cols, (int)transpose, s.cbits, w.ka, w.va, w.err);
+    if (nnz > 0 && !per_window) {
+        if (rows) {
+            hipLaunchKernelGGL(build_keys_kernel, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, row_ptr, rows, cols,
+                               values, nnz, num_rows, num_cols, (int)transpose, s.cbits, w.ka, w.va, w.err);
+        } else {
+            // every edge lies in some row's range (check_row_ptr_kernel flags
+            // a row pointer that does not cover [0, nnz) exactly)
+            const int64_t wg = std::min<int64_t>((num_rows + 3) / 4, 65536);
+            hipLaunchKernelGGL(build_keys_rows_kernel, dim3((unsigned)std::max<int64_t>(wg, 1)), dim3(256), 0, stream,
+                               row_ptr, cols, values, nnz, num_rows, num_cols, (int)transpose, s.cbits, w.ka, w.va,
+                               w.err);
+        }
         GRWS_LAUNCH_CHECK();
         GRWS_TRY(radix_sort_pairs(w.ka, w.va, w.kb, w.vb, nnz, s.bits, w.sort_ws, w.sort_bytes, stream, &alt));
         const uint64_t* k = alt ? w.kb : w.ka;
@@ -394,9 +615,11 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
                            w.uflag, w.uidx, w.wstart, w.wend);
         GRWS_LAUNCH_CHECK();
     }
-    hipLaunchKernelGGL(window_tiles_kernel, dim3(grid_for(s.W)), dim3(kBlk), 0, stream, w.wstart, w.wend, s.W,
-                       (int)tile_cols, w.wtiles);
-    GRWS_LAUNCH_CHECK();
+    if (!per_window) {
+        hipLaunchKernelGGL(window_tiles_kernel, dim3(grid_for(s.W)), dim3(kBlk), 0, stream, w.wstart, w.wend, s.W,
+                           (int)tile_cols, w.wtiles);
+        GRWS_LAUNCH_CHECK();
+    }
     GRWS_TRY(scan_i32_to_i64(w.wtiles, window_offset, s.W, false, w.scan_ws, w.scan_bytes, stream));
     int64_t T = 0;
     int32_t e = 0;
@@ -432,21 +655,25 @@ extern "C" int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_c
     GRWS_TRY(fill_i32(col_indices, num_tiles * tile_cols, -1, stream));
     GRWS_TRY(fill_bytes_zero(values, (size_t)num_tiles * 16 * tile_cols * dtype_size(values_dtype), stream));
     if (nnz == 0) return GRWS_OK;
+    // the path the count phase took (err[2] = 1: per window; its sorted keys
+    // and values are in ka / va)
+    int32_t path = 0;
+    GRWS_HIP(hipMemcpyAsync(&path, w.err + 2, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipStreamSynchronize(stream));
+    const unsigned wg = (unsigned)std::min<int64_t>(s.W, 4096);
+#define GRWS_BUILD_FILL(VT)                                                                                        \
+    if (path == 1)                                                                                                 \
+        hipLaunchKernelGGL(win_fill_kernel<VT>, dim3(wg), dim3(kWinBlk), 0, stream, w.ka, w.va, w.wstart, w.wend,  \
+                           window_offset, s.W, (int)tile_cols, col_indices, values, w.err);                        \
+    else                                                                                                           \
+        hipLaunchKernelGGL(build_scatter_kernel<VT>, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, v, nnz, s.cbits, \
+                           w.uflag, w.uidx, w.wstart, window_offset, (int)tile_cols, col_indices, values, w.err)
     switch (values_dtype) {
-        case GRWS_F32:
-            hipLaunchKernelGGL(build_scatter_kernel<float>, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, v, nnz,
-                               s.cbits, w.uflag, w.uidx, w.wstart, window_offset, (int)tile_cols, col_indices, values);
-            break;
-        case GRWS_F16:
-            hipLaunchKernelGGL(build_scatter_kernel<_Float16>, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, v, nnz,
-                               s.cbits, w.uflag, w.uidx, w.wstart, window_offset, (int)tile_cols, col_indices, values);
-            break;
-        default:
-            hipLaunchKernelGGL(build_scatter_kernel<__hip_bfloat16>, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, v,
-                               nnz, s.cbits, w.uflag, w.uidx, w.wstart, window_offset, (int)tile_cols, col_indices,
-                               values);
-            break;
+        case GRWS_F32: GRWS_BUILD_FILL(float); break;
+        case GRWS_F16: GRWS_BUILD_FILL(_Float16); break;
+        default: GRWS_BUILD_FILL(__hip_bfloat16); break;
     }
+#undef GRWS_BUILD_FILL
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }
