@@ -248,14 +248,30 @@ __global__ void build_scatter_kernel(const uint64_t* __restrict__ keys, const ui
 // --- per-window CSR build ---------------------------------------------------
 // A CSR's edges come grouped by window already (16 consecutive rows), so when
 // every window has at most kWinCap edges (c3: at most 8,246) each window is
-// built by one work-group from LDS, with no global sort: the window's keys
-// (column << 18 | row-in-window << 14 | edge offset in the window) are
-// bitonic-sorted in LDS, the distinct columns counted, and the sorted keys
-// with their values kept in the workspace for the fill.  Keys are distinct
-// (the offset), so of duplicate (row, column) edges the one last in CSR order
-// sorts last and is the one stored, as with the global sort.
+// built by one work-group from LDS, with no global sort: the window's edge
+// offsets are radix-sorted in LDS by column (stable, 9-bit digits over the
+// window's column span: two passes for spans up to 2^18), each distinct
+// column given its place among the window's distinct columns, and one record
+// per edge written in (column, row, offset) order with the distinct columns
+// at their places.  Edges enter in CSR order, (row, offset), and the sort is
+// stable, so of duplicate (row, column) edges the one last in CSR order is
+// the last of its run and is the one stored, as with the global sort.
+//
+// record: value bits (f32) | place << 32 (14 bits) | row << 46 (4 bits) |
+// last of its (column, row) run << 50; the window's last record holds its
+// last place, so the fill knows the count of distinct columns.
+__device__ __forceinline__ uint64_t win_record(uint32_t vbits, int place, int row, bool last) {
+    return (uint64_t)vbits | ((uint64_t)place << 32) | ((uint64_t)row << 46) | ((uint64_t)last << 50);
+}
+__device__ __forceinline__ int rec_place(uint64_t r) { return (int)((r >> 32) & 16383u); }
+__device__ __forceinline__ int rec_row(uint64_t r) { return (int)((r >> 46) & 15u); }
+__device__ __forceinline__ bool rec_last(uint64_t r) { return (r >> 50) & 1u; }
+
 constexpr int kWinCap = 16384;  // windows of up to 8,192 edges use a half-size LDS twin
 constexpr int kWinBlk = 512;
+constexpr int kWinDig = 9;                 // radix digit bits
+constexpr int kWinBkt = 1 << kWinDig;      // digit values: one per thread in the offset scan
+static_assert(kWinBkt == kWinBlk, "the offset scan gives each thread one digit");
 
 // Windows with more than kWinCap edges (err[1]), from a valid row pointer.
 __global__ void win_big_kernel(const int64_t* __restrict__ row_ptr, int64_t R, int64_t W, int64_t n,
@@ -267,19 +283,27 @@ __global__ void win_big_kernel(const int64_t* __restrict__ row_ptr, int64_t R, i
 }
 
 template <int CAP>
-__global__ __launch_bounds__(kWinBlk) void win_sort_kernel(const int64_t* __restrict__ row_ptr,
+__global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 8192 ? 4 : 2))) void win_sort_kernel(const int64_t* __restrict__ row_ptr,
                                                             const int32_t* __restrict__ cols,
                                                             const float* __restrict__ vals, int64_t n, int64_t R,
                                                             int64_t W, int64_t num_cols, int tc,
-                                                            uint64_t* __restrict__ skeys, uint32_t* __restrict__ svals,
+                                                            uint64_t* __restrict__ skeys, int32_t* __restrict__ ucol,
                                                             int64_t* __restrict__ wstart, int64_t* __restrict__ wend,
                                                             int32_t* __restrict__ wtiles, int32_t* __restrict__ err) {
-    // CAP 8192: the windows of at most 8,192 edges; CAP 16384: the larger
-    // ones (at most kWinCap edges: checked before the launch)
-    __shared__ uint64_t key[CAP];
+    // CAP 8192: the windows of at most 8,192 edges (73 KB of LDS: two
+    // work-groups per CU); CAP 16384: the larger ones (at most kWinCap
+    // edges: checked before the launch)
+    constexpr int NW = kWinBlk / kWave;
+    constexpr int PER = CAP / kWinBlk;        // edges per thread
+    __shared__ int32_t colv[CAP];             // the window's columns, by edge offset
+    __shared__ uint16_t ia[CAP], ib[CAP];     // edge offsets: sort source and destination
+    // [wave][digit] counts, then scatter positions, 16 bits each (at most
+    // CAP), two digits a word
+    __shared__ uint32_t cnt[NW * kWinBkt / 2];
     __shared__ int64_t rp[17];
-    __shared__ int32_t cnt[kWinBlk / kWave];
-    const int tid = threadIdx.x;
+    __shared__ int64_t tmp[NW + 1];
+    __shared__ int32_t mm[2 * NW];            // per-wave column range
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
     for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {  // uniform over the work-group
         const int64_t r0 = 16 * w;
         const int nr = (int)(R - r0 < 16 ? R - r0 : 16);
@@ -294,101 +318,258 @@ __global__ __launch_bounds__(kWinBlk) void win_sort_kernel(const int64_t* __rest
             __syncthreads();
             continue;
         }
-        int P = 1;
-        while (P < m) P <<= 1;  // <= CAP
+        // columns into LDS (checked), offsets in CSR order, the column span;
+        // every load issued before the first is used
+        int32_t cv[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int j = tid + k * kWinBlk;
+            cv[k] = j < m ? cols[e0 + j] : 0;
+        }
+        int cmin = 0x7fffffff, cmax = 0;
         bool bad = false;
-        for (int j = tid; j < P; j += kWinBlk) {
-            uint64_t k = ~0ull;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int j = tid + k * kWinBlk;
             if (j < m) {
-                const int64_t e = e0 + j;
-                int q = 0;
-                while (q + 1 < nr && rp[q + 1] <= e) ++q;
-                int64_t c = cols[e];
-                if (c < 0 || c >= num_cols) {
+                int32_t c = cv[k];
+                if (c < 0 || (int64_t)c >= num_cols) {
                     bad = true;
                     c = 0;
                 }
-                k = ((uint64_t)c << 18) | ((uint64_t)q << 14) | (uint64_t)j;
+                colv[j] = c;
+                ia[j] = (uint16_t)j;
+                cmin = min(cmin, c);
+                cmax = max(cmax, c);
             }
-            key[j] = k;
         }
         if (bad) atomicOr(err, kErrCol);
+        for (int d = kWave / 2; d >= 1; d >>= 1) {
+            cmin = min(cmin, __shfl_xor(cmin, d, kWave));
+            cmax = max(cmax, __shfl_xor(cmax, d, kWave));
+        }
+        if (lane == 0) {
+            mm[wv] = cmin;
+            mm[NW + wv] = cmax;
+        }
         __syncthreads();
-        for (int size = 2; size <= P; size <<= 1) {
-            for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                for (int i = tid; i < P; i += kWinBlk) {
-                    const int j = i ^ stride;
-                    if (j > i) {
-                        const bool up = (i & size) == 0;
-                        const uint64_t a = key[i], b = key[j];
-                        if ((a > b) == up) {
-                            key[i] = b;
-                            key[j] = a;
-                        }
-                    }
+        for (int v = 0; v < NW; ++v) {
+            cmin = min(cmin, mm[v]);
+            cmax = max(cmax, mm[NW + v]);
+        }
+        const uint32_t span = m > 0 ? (uint32_t)(cmax - cmin) : 0u;
+        const int bits = span ? 32 - __clz(span) : 0;
+        // wave v sorts positions [lo, hi): whole rounds of 64, in wave order
+        const int chunk = ((m + NW * kWave - 1) / (NW * kWave)) * kWave;
+        const int lo = min(wv * chunk, m), hi = min(lo + chunk, m);
+        uint16_t* src = ia;
+        uint16_t* dst = ib;
+        for (int sh = 0; sh < bits; sh += kWinDig) {  // uniform
+            for (int i = tid; i < NW * kWinBkt / 2; i += kWinBlk) cnt[i] = 0;
+            __syncthreads();
+            for (int i = lo + lane; i < hi; i += kWave) {
+                const uint32_t d = ((uint32_t)(colv[src[i]] - cmin) >> sh) & (kWinBkt - 1);
+                atomicAdd(&cnt[wv * (kWinBkt / 2) + (d >> 1)], 1u << (16 * (d & 1)));
+            }
+            __syncthreads();
+            {  // exclusive offsets in (digit, wave) order; this thread's digit is tid
+                const int hw = 16 * (tid & 1);
+                int pos[NW];
+                int t = 0;
+#pragma unroll
+                for (int v = 0; v < NW; ++v) {
+                    pos[v] = (int)((cnt[v * (kWinBkt / 2) + (tid >> 1)] >> hw) & 0xffffu);
+                    t += pos[v];
                 }
-                __syncthreads();
+                int64_t tot;
+                int run = (int)(block_incl_scan<kWinBlk>(t, tmp, &tot) - t);  // every count read first
+#pragma unroll
+                for (int v = 0; v < NW; ++v) {
+                    const int c = pos[v];
+                    pos[v] = run;
+                    run += c;
+                }
+                // the even digit's thread writes the pair's word
+#pragma unroll
+                for (int v = 0; v < NW; ++v) {
+                    const int odd = __shfl_down(pos[v], 1, kWave);
+                    if (!(tid & 1)) cnt[v * (kWinBkt / 2) + (tid >> 1)] = (uint32_t)pos[v] | ((uint32_t)odd << 16);
+                }
+            }
+            __syncthreads();
+            // stable scatter: each wave walks its positions in order, 64 at a
+            // time; lanes with equal digits take consecutive places in lane
+            // order, and the group's highest lane advances the wave's count
+            for (int b = lo; b < hi; b += kWave) {  // uniform over the wave
+                const int i = b + lane;
+                const bool v = i < hi;
+                uint16_t x = 0;
+                int d = 0;
+                if (v) {
+                    x = src[i];
+                    d = (int)(((uint32_t)(colv[x] - cmin) >> sh) & (kWinBkt - 1));
+                }
+                uint64_t peers = __ballot(v);
+#pragma unroll
+                for (int k = 0; k < kWinDig; ++k) {
+                    const bool bit = (d >> k) & 1;
+                    const uint64_t bb = __ballot(bit);
+                    peers &= bit ? bb : ~bb;
+                }
+                if (v) {
+                    const int word = wv * (kWinBkt / 2) + (d >> 1), hw = 16 * (d & 1);
+                    const int base = (int)((cnt[word] >> hw) & 0xffffu);
+                    dst[base + __popcll(peers & ((1ull << lane) - 1))] = x;
+                    if ((peers >> lane) == 1ull) atomicAdd(&cnt[word], (uint32_t)__popcll(peers) << hw);
+                }
+            }
+            __syncthreads();
+            uint16_t* t = src;
+            src = dst;
+            dst = t;
+        }
+        // each distinct column's place among the window's distinct columns:
+        // first-of-column flags counted over contiguous runs of sorted
+        // positions, one block scan, places into the free offset buffer
+        auto first_of_col = [&](int i) { return i == 0 || colv[src[i - 1]] != colv[src[i]]; };
+        auto row_of = [&](int j) {  // the edge's row in the window: the last q with rp[q] <= e0 + j
+            const int64_t e = e0 + j;
+            int q = 0;
+#pragma unroll
+            for (int st = 8; st >= 1; st >>= 1)
+                if (q + st < nr && rp[q + st] <= e) q += st;
+            return q;
+        };
+        {
+            const int run = (m + kWinBlk - 1) / kWinBlk;
+            const int a0 = min(tid * run, m), a1 = min(a0 + run, m);
+            int f = 0;
+            for (int i = a0; i < a1; ++i) f += first_of_col(i) ? 1 : 0;
+            int64_t tot;
+            int pl = (int)block_incl_scan<kWinBlk>(f, tmp, &tot) - f;
+            for (int i = a0; i < a1; ++i) {
+                pl += first_of_col(i) ? 1 : 0;
+                dst[i] = (uint16_t)(pl - 1);
+            }
+            if (tid == 0) {
+                wtiles[w] = ((int)tot + tc - 1) / tc;
+                wstart[w] = e0;
+                wend[w] = e0 + m;
             }
         }
-        int u = 0;
-        for (int i = tid; i < m; i += kWinBlk) {
-            const uint64_t k = key[i];
-            u += (i == 0 || (key[i - 1] >> 18) != (k >> 18)) ? 1 : 0;
-            skeys[e0 + i] = k;
-            svals[e0 + i] = vals ? __float_as_uint(vals[e0 + (int64_t)(k & 16383u)]) : 0x3f800000u;
-        }
-        for (int d = kWave / 2; d >= 1; d >>= 1) u += __shfl_xor(u, d, kWave);
-        if ((tid & (kWave - 1)) == 0) cnt[tid / kWave] = u;
         __syncthreads();
-        if (tid == 0) {
-            int t = 0;
-            for (int i = 0; i < kWinBlk / kWave; ++i) t += cnt[i];
-            wtiles[w] = (t + tc - 1) / tc;
-            wstart[w] = e0;
-            wend[w] = e0 + m;
+        // one record per edge in sorted order (value bits, place, row, last of
+        // its (column, row) run), the distinct columns at their places; the
+        // value gathers issued first
+        int jj[PER];
+        uint32_t vv[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = tid + k * kWinBlk;
+            jj[k] = i < m ? src[i] : 0;
         }
-        __syncthreads();  // key[], rp[] and cnt[] are rewritten for the next window
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = tid + k * kWinBlk;
+            vv[k] = (vals && i < m) ? __float_as_uint(vals[e0 + jj[k]]) : 0x3f800000u;
+        }
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = tid + k * kWinBlk;
+            if (i < m) {
+                const int j = jj[k];
+                const int c = colv[j], q = row_of(j), pl = dst[i];
+                bool last = true;
+                if (i + 1 < m) {
+                    const int jn = src[i + 1];
+                    last = colv[jn] != c || row_of(jn) != q;
+                }
+                if (i == 0 || dst[i - 1] != pl) ucol[e0 + pl] = c;
+                skeys[e0 + i] = win_record(vv[k], pl, q, last);
+            }
+        }
+        __syncthreads();  // LDS is rewritten for the next window
     }
 }
 
-// The fill of the per-window build (err[2] = 1; the global path's scatter
-// exits then, and this kernel exits otherwise).
 template <typename VT>
-__global__ __launch_bounds__(kWinBlk) void win_fill_kernel(const uint64_t* __restrict__ skeys,
-                                                            const uint32_t* __restrict__ svals,
+__device__ __forceinline__ VT to_value(float v);
+template <>
+__device__ __forceinline__ float to_value<float>(float v) {
+    return v;
+}
+template <>
+__device__ __forceinline__ _Float16 to_value<_Float16>(float v) {
+    return (_Float16)v;
+}
+template <>
+__device__ __forceinline__ __hip_bfloat16 to_value<__hip_bfloat16>(float v) {
+    return __float2bfloat16(v);
+}
+
+// The fill of the per-window build (err[2] = 1; the global path's scatter
+// exits then, and this kernel exits otherwise).  One work-group per window
+// writes the window's whole tile range, padding included, so the outputs
+// need no clearing first: the columns straight from the distinct-column list
+// (then -1 to the tile boundary), the values kFillVals at a time (32 tiles of
+// 16 x 16, 64 of 16 x 8) assembled in LDS from the records, which every
+// thread loads once, and written out with 16-byte stores.
+constexpr int kFillVals = 8192;
+template <int CAP, typename VT>
+__global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 8192 ? 4 : 2))) void win_fill_kernel(const uint64_t* __restrict__ rec,
+                                                            const int32_t* __restrict__ ucol,
                                                             const int64_t* __restrict__ wstart,
                                                             const int64_t* __restrict__ wend,
                                                             const int64_t* __restrict__ win_off, int64_t W, int tc,
                                                             int32_t* __restrict__ out_cols, void* __restrict__ out_vals,
-                                                            const int32_t* __restrict__ err) {
-    __shared__ int64_t tmp[kWinBlk / kWave + 1];
+                                                            int aligned, const int32_t* __restrict__ err) {
+    // CAP 8192: the windows of at most 8,192 edges; CAP 16384: the larger ones
+    constexpr int PER = CAP / kWinBlk;  // records per thread
+    constexpr int VPU = 16 / (int)sizeof(VT);  // values per 16 bytes
+    __shared__ __align__(16) VT sval[kFillVals];
     if (err[2] != 1) return;  // uniform
     const int tid = threadIdx.x;
+    const int ltc = tc == 16 ? 4 : 3;
+    const int gt = kFillVals / (16 * tc);  // tiles per step
     for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {  // uniform over the work-group
-        const int64_t e0 = wstart[w], m = wend[w] - e0, wo = win_off[w];
-        int64_t run = 0;
-        for (int64_t b = 0; b < m; b += kWinBlk) {  // uniform over the work-group
-            const int64_t i = b + tid;
-            const bool v = i < m;
-            uint64_t k = 0;
-            int f = 0;
-            if (v) {
-                k = skeys[e0 + i];
-                f = (i == 0 || (skeys[e0 + i - 1] >> 18) != (k >> 18)) ? 1 : 0;
-            }
-            int64_t tot;
-            const int64_t inc = block_incl_scan<kWinBlk>(f, tmp, &tot);
-            if (v) {
-                const int64_t p = run + inc - 1;  // the column's place among the window's distinct columns
-                const int64_t tile = wo + p / tc;
-                const int c = (int)(p % tc);
-                if (f) out_cols[tile * tc + c] = (int32_t)(k >> 18);
-                if (i == m - 1 || (skeys[e0 + i + 1] >> 14) != (k >> 14)) {
-                    const int r = (int)((k >> 14) & 15u);
-                    store_value<VT>(out_vals, (tile * 16 + r) * tc + c, __uint_as_float(svals[e0 + i]));
+        const int64_t e0 = wstart[w], wo = win_off[w];
+        const int m = (int)(wend[w] - e0);
+        if ((CAP == 8192) != (m <= 8192)) continue;  // the other launch's window (uniform)
+        const int64_t nt64 = win_off[w + 1] - wo;
+        const int nt = (int)(nt64 < 0 ? 0 : nt64);
+        uint64_t r[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = tid + k * kWinBlk;
+            r[k] = i < m ? rec[e0 + i] : 0;
+        }
+        const int u = m > 0 ? rec_place(rec[e0 + m - 1]) + 1 : 0;
+        int32_t* oc = out_cols + wo * tc;
+        for (int x = tid; x < nt * tc; x += kWinBlk) oc[x] = x < u ? ucol[e0 + x] : -1;
+        for (int g0 = 0; g0 < nt; g0 += gt) {  // uniform over the work-group
+            const int g1 = g0 + gt < nt ? g0 + gt : nt;
+            const int nv = (g1 - g0) * 16 * tc;
+            for (int x = tid; x < nv / VPU; x += kWinBlk) reinterpret_cast<uint4*>(sval)[x] = make_uint4(0, 0, 0, 0);
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                if (tid + k * kWinBlk < m && rec_last(r[k])) {
+                    const int pl = rec_place(r[k]);
+                    const int t = (pl >> ltc) - g0;
+                    if (t >= 0 && t < g1 - g0)
+                        sval[((t * 16 + rec_row(r[k])) << ltc) + (pl & (tc - 1))] =
+                            to_value<VT>(__uint_as_float((uint32_t)r[k]));
                 }
             }
-            run += tot;
+            __syncthreads();
+            VT* ov = static_cast<VT*>(out_vals) + (wo + g0) * 16 * tc;
+            if (aligned) {  // the values 16-byte aligned (uniform)
+                for (int x = tid; x < nv / VPU; x += kWinBlk)
+                    reinterpret_cast<uint4*>(ov)[x] = reinterpret_cast<const uint4*>(sval)[x];
+            } else {
+                for (int x = tid; x < nv; x += kWinBlk) ov[x] = sval[x];
+            }
+            __syncthreads();
         }
     }
 }
@@ -584,11 +765,12 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
     if (per_window) {
         GRWS_TRY(fill_i32(w.err + 2, 1, 1, stream));
         const unsigned wg = (unsigned)std::min<int64_t>(s.W, 4096);
+        int32_t* ucol = reinterpret_cast<int32_t*>(w.va);
         hipLaunchKernelGGL(win_sort_kernel<8192>, dim3(wg), dim3(kWinBlk), 0, stream, row_ptr, cols, values, nnz, s.R,
-                           s.W, num_cols, (int)tile_cols, w.ka, w.va, w.wstart, w.wend, w.wtiles, w.err);
+                           s.W, num_cols, (int)tile_cols, w.ka, ucol, w.wstart, w.wend, w.wtiles, w.err);
         GRWS_LAUNCH_CHECK();
         hipLaunchKernelGGL(win_sort_kernel<16384>, dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0, stream, row_ptr,
-                           cols, values, nnz, s.R, s.W, num_cols, (int)tile_cols, w.ka, w.va, w.wstart, w.wend,
+                           cols, values, nnz, s.R, s.W, num_cols, (int)tile_cols, w.ka, ucol, w.wstart, w.wend,
                            w.wtiles, w.err);
         GRWS_LAUNCH_CHECK();
     }
@@ -652,20 +834,31 @@ extern "C" int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_c
     const bool alt = nnz > 1 && (passes & 1);
     const uint64_t* k = alt ? w.kb : w.ka;
     const uint32_t* v = alt ? w.vb : w.va;
-    GRWS_TRY(fill_i32(col_indices, num_tiles * tile_cols, -1, stream));
-    GRWS_TRY(fill_bytes_zero(values, (size_t)num_tiles * 16 * tile_cols * dtype_size(values_dtype), stream));
-    if (nnz == 0) return GRWS_OK;
     // the path the count phase took (err[2] = 1: per window; its sorted keys
-    // and values are in ka / va)
+    // and values are in ka / va, and its fill writes every tile, padding
+    // included)
     int32_t path = 0;
-    GRWS_HIP(hipMemcpyAsync(&path, w.err + 2, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
-    GRWS_HIP(hipStreamSynchronize(stream));
+    if (nnz > 0) {
+        GRWS_HIP(hipMemcpyAsync(&path, w.err + 2, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+        GRWS_HIP(hipStreamSynchronize(stream));
+    }
+    if (path != 1) {
+        GRWS_TRY(fill_i32(col_indices, num_tiles * tile_cols, -1, stream));
+        GRWS_TRY(fill_bytes_zero(values, (size_t)num_tiles * 16 * tile_cols * dtype_size(values_dtype), stream));
+    }
+    if (nnz == 0) return GRWS_OK;
     const unsigned wg = (unsigned)std::min<int64_t>(s.W, 4096);
+    const int aligned = (reinterpret_cast<uintptr_t>(values) & 15) == 0;
 #define GRWS_BUILD_FILL(VT)                                                                                        \
     if (path == 1)                                                                                                 \
-        hipLaunchKernelGGL(win_fill_kernel<VT>, dim3(wg), dim3(kWinBlk), 0, stream, w.ka, w.va, w.wstart, w.wend,  \
-                           window_offset, s.W, (int)tile_cols, col_indices, values, w.err);                        \
-    else                                                                                                           \
+    {                                                                                                              \
+        hipLaunchKernelGGL((win_fill_kernel<8192, VT>), dim3(wg), dim3(kWinBlk), 0, stream, w.ka,                  \
+                           reinterpret_cast<const int32_t*>(w.va), w.wstart, w.wend, window_offset, s.W,           \
+                           (int)tile_cols, col_indices, values, aligned, w.err);                                   \
+        hipLaunchKernelGGL((win_fill_kernel<16384, VT>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0,      \
+                           stream, w.ka, reinterpret_cast<const int32_t*>(w.va), w.wstart, w.wend, window_offset,  \
+                           s.W, (int)tile_cols, col_indices, values, aligned, w.err);                              \
+    } else                                                                                                         \
         hipLaunchKernelGGL(build_scatter_kernel<VT>, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, v, nnz, s.cbits, \
                            w.uflag, w.uidx, w.wstart, window_offset, (int)tile_cols, col_indices, values, w.err)
     switch (values_dtype) {

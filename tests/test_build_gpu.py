@@ -83,6 +83,85 @@ def test_coo_build_duplicates_last_wins(cuda_device):
     np.testing.assert_array_equal(dv.cpu().numpy(), ov.astype(np.float32))
 
 
+def _window_case_csr(hub: bool, seed: int):
+    """A 75-row CSR (five 16-row windows, the last ragged) over 2^20 + 5
+    columns: window 0 holds 8,000 edges over 3,000 columns (many duplicate
+    (row, column) edges), window 1 holds 11,200 edges over all the columns
+    (span above 2^18), window 2 one column only, window 3 none, window 4 a
+    few short rows; rows are unsorted.  hub adds 20,000 edges to row 40
+    (a window above 16,384 edges)."""
+    rng = np.random.default_rng(seed)
+    n_r, n_c = 75, (1 << 20) + 5
+    per_row = []
+    for r in range(n_r):
+        if r < 16:
+            c = rng.integers(0, 3000, 500)
+        elif r < 32:
+            c = rng.integers(0, n_c, 700)
+        elif r < 48:
+            c = np.full(10, 7)
+        elif r < 64:
+            c = np.zeros(0, np.int64)
+        else:
+            c = rng.integers(0, n_c, int(rng.integers(0, 40)))
+        if hub and r == 40:
+            c = rng.integers(0, n_c, 20000)
+        per_row.append(c.astype(np.int32))
+    rp = np.zeros(n_r + 1, np.int64)
+    rp[1:] = np.cumsum([len(c) for c in per_row])
+    cols = np.concatenate(per_row)
+    vals = rng.standard_normal(cols.size).astype(np.float32)
+    return n_r, n_c, rp, cols, vals
+
+
+@pytest.mark.parametrize("hub", [False, True])
+@pytest.mark.parametrize("tc", [8, 16])
+def test_csr_build_window_paths(cuda_device, hub, tc):
+    """CSR input through each case of the window-by-window build (and, with
+    a window above 16,384 edges, the global sort): equal to the oracle's
+    converter, duplicates last-wins, bit-exact f32 values."""
+    print(f"case window paths hub={hub} tc={tc}", flush=True)
+    n_r, n_c, rp, cols, vals = _window_case_csr(hub, seed=21 + tc)
+    ow, oc, ov = oracle.csr_to_bcsr(n_r, rp, cols, vals, 16, tc)
+    dw, dc, dv = builder.csr_to_bcsr_device(n_r, n_c, torch.from_numpy(rp).to(cuda_device),
+                                            torch.from_numpy(cols).to(cuda_device),
+                                            torch.from_numpy(vals).to(cuda_device), tile_cols=tc)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dw.cpu().numpy(), ow)
+    np.testing.assert_array_equal(dc.cpu().numpy(), oc)
+    np.testing.assert_array_equal(dv.cpu().numpy(), ov.astype(np.float32))
+
+
+@pytest.mark.parametrize("vdt", [torch.float32, torch.float16])
+def test_csr_build_unaligned_outputs(cuda_device, vdt):
+    """Outputs that start one element past a 16-byte boundary (a C-ABI
+    caller's buffers): the window-by-window fill stores element by element
+    and gives the same BCSR."""
+    import ctypes
+    from graph_rws_amd.core import _lib as L
+    print(f"case unaligned outputs {vdt}", flush=True)
+    n_r, n_c, rp, cols, vals = _window_case_csr(False, seed=5)
+    ow, oc, ov = oracle.csr_to_bcsr(n_r, rp, cols, vals, 16, 16)
+    d_rp, d_c, d_v = (torch.from_numpy(a).to(cuda_device) for a in (rp, cols, vals))
+    W = (n_r + 15) // 16
+    win = torch.empty(W + 1, dtype=torch.int64, device=cuda_device)
+    wsb = int(L.load().grws_bcsr_build_workspace_bytes(cols.size, n_r, n_c, 0))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=cuda_device)
+    T = ctypes.c_int64()
+    stream = L.stream_of(cuda_device)
+    L.call("grws_bcsr_build_count", L.ptr(d_rp), None, L.ptr(d_c), L.ptr(d_v), cols.size, n_r, n_c, 16, 0,
+           L.ptr(win), L.ptr(ws), wsb, ctypes.byref(T), stream)
+    T = T.value
+    cbuf = torch.empty(T * 16 + 1, dtype=torch.int32, device=cuda_device)
+    vbuf = torch.empty(T * 256 + 1, dtype=vdt, device=cuda_device)
+    L.call("grws_bcsr_build_fill", cols.size, n_r, n_c, 16, 0, L.ptr(win), T, L.ptr(cbuf[1:]), L.ptr(vbuf[1:]),
+           L.dtype_code(vdt), L.ptr(ws), wsb, stream)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(win.cpu().numpy(), ow)
+    np.testing.assert_array_equal(cbuf[1:].cpu().numpy(), oc)
+    _eq(vbuf[1:], torch.from_numpy(ov.astype(np.float32)).to(vdt))
+
+
 def test_rectangular_and_empty(cuda_device):
     print("case rectangular", flush=True)
     # 37 rows x 1000 cols, rows 0..15 empty
