@@ -126,9 +126,20 @@ __device__ __forceinline__ int64_t csr_row_of(const int64_t* __restrict__ row_pt
     return lo;
 }
 
+// An edge's sort key from its window-row wr (the BCSR row) and column cc.
+// wbits == 0: (window, column, row-in-window), the global sort's key.
+// wbits > 0 (a multiple of 8): window | row-in-window << wbits | column <<
+// (wbits + 4), for the window-major sort (only the low wbits bits sorted);
+// equal edges have equal keys, so a stable sort keeps duplicates in input
+// order.
+__device__ __forceinline__ uint64_t edge_key(int64_t wr, int64_t cc, int cbits, int wbits) {
+    if (wbits) return (uint64_t)(wr >> 4) | ((uint64_t)(wr & 15) << wbits) | ((uint64_t)cc << (wbits + 4));
+    return ((uint64_t)(wr >> 4) << (cbits + 4)) | ((uint64_t)cc << 4) | (uint64_t)(wr & 15);
+}
+
 __global__ void build_keys_kernel(const int64_t* __restrict__ row_ptr, const int32_t* __restrict__ rows,
                                   const int32_t* __restrict__ cols, const float* __restrict__ vals, int64_t n,
-                                  int64_t num_rows, int64_t num_cols, int transpose, int cbits,
+                                  int64_t num_rows, int64_t num_cols, int transpose, int cbits, int wbits,
                                   uint64_t* __restrict__ keys, uint32_t* __restrict__ pay, int32_t* __restrict__ err) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -138,9 +149,7 @@ __global__ void build_keys_kernel(const int64_t* __restrict__ row_ptr, const int
     if (r < 0 || r >= num_rows) { e |= kErrRow; r = 0; }
     if (c < 0 || c >= num_cols) { e |= kErrCol; c = 0; }
     if (e) atomicOr(err, e);
-    const int64_t wr = transpose ? c : r;
-    const int64_t cc = transpose ? r : c;
-    keys[i] = ((uint64_t)(wr >> 4) << (cbits + 4)) | ((uint64_t)cc << 4) | (uint64_t)(wr & 15);
+    keys[i] = transpose ? edge_key(c, r, cbits, wbits) : edge_key(r, c, cbits, wbits);
     pay[i] = vals ? __float_as_uint(vals[i]) : 0x3f800000u;  // 1.0f when no values are given
 }
 
@@ -154,7 +163,7 @@ __global__ __launch_bounds__(256) void build_keys_rows_kernel(const int64_t* __r
                                                               const int32_t* __restrict__ cols,
                                                               const float* __restrict__ vals, int64_t n,
                                                               int64_t num_rows, int64_t num_cols, int transpose,
-                                                              int cbits, uint64_t* __restrict__ keys,
+                                                              int cbits, int wbits, uint64_t* __restrict__ keys,
                                                               uint32_t* __restrict__ pay, int32_t* __restrict__ err) {
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x / kWave);
@@ -176,9 +185,7 @@ __global__ __launch_bounds__(256) void build_keys_rows_kernel(const int64_t* __r
                 bad = true;
                 c = 0;
             }
-            const int64_t wr = transpose ? c : r;
-            const int64_t cc = transpose ? r : c;
-            keys[i] = ((uint64_t)(wr >> 4) << (cbits + 4)) | ((uint64_t)cc << 4) | (uint64_t)(wr & 15);
+            keys[i] = transpose ? edge_key(c, r, cbits, wbits) : edge_key(r, c, cbits, wbits);
             pay[i] = vals ? __float_as_uint(vals[i]) : 0x3f800000u;  // 1.0f when no values are given
         }
         if (bad) atomicOr(err, kErrCol);
@@ -207,6 +214,16 @@ __global__ void window_tiles_kernel(const int64_t* __restrict__ wstart, const in
     if (w >= W) return;
     const int64_t u = wend[w] - wstart[w];
     wtiles[w] = (int32_t)((u + tc - 1) / tc);
+}
+
+// Window bounds of window-major sorted keys (edge_key with wbits > 0).
+__global__ void keyed_bounds_kernel(const uint64_t* __restrict__ keys, int64_t n, uint64_t wmask,
+                                    int64_t* __restrict__ wstart, int64_t* __restrict__ wend) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t w = keys[i] & wmask;
+    if (i == 0 || (keys[i - 1] & wmask) != w) wstart[w] = i;
+    if (i == n - 1 || (keys[i + 1] & wmask) != w) wend[w] = i + 1;
 }
 
 template <typename VT>
@@ -282,20 +299,32 @@ __global__ void win_big_kernel(const int64_t* __restrict__ row_ptr, int64_t R, i
     if (row_ptr[r1] - row_ptr[16 * w] > kWinCap) atomicAdd(&err[1], 1);
 }
 
-template <int CAP>
-__global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 8192 ? 4 : 2))) void win_sort_kernel(const int64_t* __restrict__ row_ptr,
-                                                            const int32_t* __restrict__ cols,
-                                                            const float* __restrict__ vals, int64_t n, int64_t R,
-                                                            int64_t W, int64_t num_cols, int tc,
-                                                            uint64_t* __restrict__ skeys, int32_t* __restrict__ ucol,
-                                                            int64_t* __restrict__ wstart, int64_t* __restrict__ wend,
-                                                            int32_t* __restrict__ wtiles, int32_t* __restrict__ err) {
+// The same from window bounds (the window-major sorted keys').
+__global__ void keyed_big_kernel(const int64_t* __restrict__ wstart, const int64_t* __restrict__ wend, int64_t W,
+                                 int32_t* __restrict__ err) {
+    const int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (w >= W) return;
+    if (wend[w] - wstart[w] > kWinCap) atomicAdd(&err[1], 1);
+}
+
+// KEYED false: the window's edges straight from a CSR (row_ptr, cols, vals),
+// sorted by column (they arrive in row order).  KEYED true: from
+// window-major sorted keys (edge_key with wbits > 0) and their value bits
+// (tkeys, tvals, bounds in wstart / wend), which arrive in input order and
+// are sorted by (column, row): the LDS key is (column - min) << 4 | row,
+// which needs column spans under 2^27 (the host checks).
+template <int CAP, bool KEYED>
+__global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 8192 ? 4 : 2))) void win_sort_kernel(
+    const int64_t* __restrict__ row_ptr, const int32_t* __restrict__ cols, const float* __restrict__ vals,
+    const uint64_t* __restrict__ tkeys, const uint32_t* __restrict__ tvals, int wbits, int64_t n, int64_t R, int64_t W,
+    int64_t num_cols, int tc, uint64_t* __restrict__ skeys, int32_t* __restrict__ ucol, int64_t* __restrict__ wstart,
+    int64_t* __restrict__ wend, int32_t* __restrict__ wtiles, int32_t* __restrict__ err) {
     // CAP 8192: the windows of at most 8,192 edges (73 KB of LDS: two
     // work-groups per CU); CAP 16384: the larger ones (at most kWinCap
     // edges: checked before the launch)
     constexpr int NW = kWinBlk / kWave;
     constexpr int PER = CAP / kWinBlk;        // edges per thread
-    __shared__ int32_t colv[CAP];             // the window's columns, by edge offset
+    __shared__ int32_t colv[CAP];             // the window's sort keys, by edge offset
     __shared__ uint16_t ia[CAP], ib[CAP];     // edge offsets: sort source and destination
     // [wave][digit] counts, then scatter positions, 16 bits each (at most
     // CAP), two digits a word
@@ -305,59 +334,112 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
     __shared__ int32_t mm[2 * NW];            // per-wave column range
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
     for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {  // uniform over the work-group
-        const int64_t r0 = 16 * w;
-        const int nr = (int)(R - r0 < 16 ? R - r0 : 16);
-        if (tid <= nr) {
-            int64_t v = row_ptr[r0 + tid];
-            rp[tid] = v < 0 ? 0 : (v > n ? n : v);
-        }
-        __syncthreads();
-        const int64_t e0 = rp[0];
-        const int m = (int)(rp[nr] - e0);
-        if ((CAP == 8192) != (m <= 8192)) {  // the other launch's window (uniform)
+        int nr = 16;
+        int64_t e0;
+        int m;
+        if (KEYED) {
+            e0 = wstart[w];
+            const int64_t mm64 = wend[w] - e0;
+            m = (int)(mm64 < 0 ? 0 : (mm64 > CAP ? CAP : mm64));
+            if ((CAP == 8192) != (mm64 <= 8192)) continue;  // the other launch's window (uniform; no LDS yet)
+        } else {
+            const int64_t r0 = 16 * w;
+            nr = (int)(R - r0 < 16 ? R - r0 : 16);
+            if (tid <= nr) {
+                int64_t v = row_ptr[r0 + tid];
+                rp[tid] = v < 0 ? 0 : (v > n ? n : v);
+            }
             __syncthreads();
-            continue;
-        }
-        // columns into LDS (checked), offsets in CSR order, the column span;
-        // every load issued before the first is used
-        int32_t cv[PER];
-#pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int j = tid + k * kWinBlk;
-            cv[k] = j < m ? cols[e0 + j] : 0;
-        }
-        int cmin = 0x7fffffff, cmax = 0;
-        bool bad = false;
-#pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int j = tid + k * kWinBlk;
-            if (j < m) {
-                int32_t c = cv[k];
-                if (c < 0 || (int64_t)c >= num_cols) {
-                    bad = true;
-                    c = 0;
-                }
-                colv[j] = c;
-                ia[j] = (uint16_t)j;
-                cmin = min(cmin, c);
-                cmax = max(cmax, c);
+            e0 = rp[0];
+            m = (int)(rp[nr] - e0);
+            if ((CAP == 8192) != (m <= 8192)) {  // the other launch's window (uniform)
+                __syncthreads();
+                continue;
             }
         }
-        if (bad) atomicOr(err, kErrCol);
-        for (int d = kWave / 2; d >= 1; d >>= 1) {
-            cmin = min(cmin, __shfl_xor(cmin, d, kWave));
-            cmax = max(cmax, __shfl_xor(cmax, d, kWave));
+        // columns into LDS (checked), offsets in input order, the column
+        // span; every load issued before the first is used
+        int cmin = 0x7fffffff, cmax = 0;
+        int cbase;  // subtracted from colv[] for the digits
+        if (KEYED) {
+            uint64_t kk[PER];
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const int j = tid + k * kWinBlk;
+                kk[k] = j < m ? tkeys[e0 + j] : 0;
+            }
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                if (tid + k * kWinBlk < m) {
+                    const int c = (int)(kk[k] >> (wbits + 4));
+                    cmin = min(cmin, c);
+                    cmax = max(cmax, c);
+                }
+            }
+            for (int d = kWave / 2; d >= 1; d >>= 1) {
+                cmin = min(cmin, __shfl_xor(cmin, d, kWave));
+                cmax = max(cmax, __shfl_xor(cmax, d, kWave));
+            }
+            if (lane == 0) {
+                mm[wv] = cmin;
+                mm[NW + wv] = cmax;
+            }
+            __syncthreads();
+            for (int v = 0; v < NW; ++v) {
+                cmin = min(cmin, mm[v]);
+                cmax = max(cmax, mm[NW + v]);
+            }
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const int j = tid + k * kWinBlk;
+                if (j < m) {
+                    const int c = (int)(kk[k] >> (wbits + 4)), q = (int)((kk[k] >> wbits) & 15u);
+                    colv[j] = ((c - cmin) << 4) | q;
+                    ia[j] = (uint16_t)j;
+                }
+            }
+            __syncthreads();
+            cbase = 0;
+        } else {
+            int32_t cv[PER];
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const int j = tid + k * kWinBlk;
+                cv[k] = j < m ? cols[e0 + j] : 0;
+            }
+            bool bad = false;
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const int j = tid + k * kWinBlk;
+                if (j < m) {
+                    int32_t c = cv[k];
+                    if (c < 0 || (int64_t)c >= num_cols) {
+                        bad = true;
+                        c = 0;
+                    }
+                    colv[j] = c;
+                    ia[j] = (uint16_t)j;
+                    cmin = min(cmin, c);
+                    cmax = max(cmax, c);
+                }
+            }
+            if (bad) atomicOr(err, kErrCol);
+            for (int d = kWave / 2; d >= 1; d >>= 1) {
+                cmin = min(cmin, __shfl_xor(cmin, d, kWave));
+                cmax = max(cmax, __shfl_xor(cmax, d, kWave));
+            }
+            if (lane == 0) {
+                mm[wv] = cmin;
+                mm[NW + wv] = cmax;
+            }
+            __syncthreads();
+            for (int v = 0; v < NW; ++v) {
+                cmin = min(cmin, mm[v]);
+                cmax = max(cmax, mm[NW + v]);
+            }
+            cbase = cmin;
         }
-        if (lane == 0) {
-            mm[wv] = cmin;
-            mm[NW + wv] = cmax;
-        }
-        __syncthreads();
-        for (int v = 0; v < NW; ++v) {
-            cmin = min(cmin, mm[v]);
-            cmax = max(cmax, mm[NW + v]);
-        }
-        const uint32_t span = m > 0 ? (uint32_t)(cmax - cmin) : 0u;
+        const uint32_t span = m > 0 ? (KEYED ? ((uint32_t)(cmax - cmin) << 4) | 15u : (uint32_t)(cmax - cmin)) : 0u;
         const int bits = span ? 32 - __clz(span) : 0;
         // wave v sorts positions [lo, hi): whole rounds of 64, in wave order
         const int chunk = ((m + NW * kWave - 1) / (NW * kWave)) * kWave;
@@ -368,7 +450,7 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
             for (int i = tid; i < NW * kWinBkt / 2; i += kWinBlk) cnt[i] = 0;
             __syncthreads();
             for (int i = lo + lane; i < hi; i += kWave) {
-                const uint32_t d = ((uint32_t)(colv[src[i]] - cmin) >> sh) & (kWinBkt - 1);
+                const uint32_t d = ((uint32_t)(colv[src[i]] - cbase) >> sh) & (kWinBkt - 1);
                 atomicAdd(&cnt[wv * (kWinBkt / 2) + (d >> 1)], 1u << (16 * (d & 1)));
             }
             __syncthreads();
@@ -407,7 +489,7 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
                 int d = 0;
                 if (v) {
                     x = src[i];
-                    d = (int)(((uint32_t)(colv[x] - cmin) >> sh) & (kWinBkt - 1));
+                    d = (int)(((uint32_t)(colv[x] - cbase) >> sh) & (kWinBkt - 1));
                 }
                 uint64_t peers = __ballot(v);
 #pragma unroll
@@ -431,8 +513,11 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
         // each distinct column's place among the window's distinct columns:
         // first-of-column flags counted over contiguous runs of sorted
         // positions, one block scan, places into the free offset buffer
-        auto first_of_col = [&](int i) { return i == 0 || colv[src[i - 1]] != colv[src[i]]; };
-        auto row_of = [&](int j) {  // the edge's row in the window: the last q with rp[q] <= e0 + j
+        // (KEYED: the column is colv >> 4, the row colv & 15)
+        auto first_of_col = [&](int i) {
+            return i == 0 || (KEYED ? (colv[src[i - 1]] >> 4) != (colv[src[i]] >> 4) : colv[src[i - 1]] != colv[src[i]]);
+        };
+        auto row_of = [&](int j) {  // CSR: the edge's row in the window, the last q with rp[q] <= e0 + j
             const int64_t e = e0 + j;
             int q = 0;
 #pragma unroll
@@ -453,8 +538,10 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
             }
             if (tid == 0) {
                 wtiles[w] = ((int)tot + tc - 1) / tc;
-                wstart[w] = e0;
-                wend[w] = e0 + m;
+                if (!KEYED) {
+                    wstart[w] = e0;
+                    wend[w] = e0 + m;
+                }
             }
         }
         __syncthreads();
@@ -471,19 +558,32 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             const int i = tid + k * kWinBlk;
-            vv[k] = (vals && i < m) ? __float_as_uint(vals[e0 + jj[k]]) : 0x3f800000u;
+            if (KEYED) vv[k] = i < m ? tvals[e0 + jj[k]] : 0u;
+            else vv[k] = (vals && i < m) ? __float_as_uint(vals[e0 + jj[k]]) : 0x3f800000u;
         }
+        // KEYED: the records and columns may overwrite tkeys / tvals of this
+        // window (the same workspace): every value read first
+        if (KEYED) __syncthreads();
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             const int i = tid + k * kWinBlk;
             if (i < m) {
                 const int j = jj[k];
-                const int c = colv[j], q = row_of(j), pl = dst[i];
+                int c, q;
                 bool last = true;
-                if (i + 1 < m) {
-                    const int jn = src[i + 1];
-                    last = colv[jn] != c || row_of(jn) != q;
+                if (KEYED) {
+                    c = (colv[j] >> 4) + cmin;
+                    q = colv[j] & 15;
+                    if (i + 1 < m) last = colv[src[i + 1]] != colv[j];
+                } else {
+                    c = colv[j];
+                    q = row_of(j);
+                    if (i + 1 < m) {
+                        const int jn = src[i + 1];
+                        last = colv[jn] != c || row_of(jn) != q;
+                    }
                 }
+                const int pl = dst[i];
                 if (i == 0 || dst[i - 1] != pl) ucol[e0 + pl] = c;
                 skeys[e0 + i] = win_record(vv[k], pl, q, last);
             }
@@ -751,9 +851,15 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
                            num_rows, nnz, w.err);
         GRWS_LAUNCH_CHECK();
     }
-    // a CSR whose windows all hold at most kWinCap edges is built window by
-    // window from LDS (one sync decides); anything else by the global sort
-    bool per_window = false;
+    // A build goes window by window from LDS when every window holds at most
+    // kWinCap edges (one sync decides); anything else by the global sort.  A
+    // CSR is already grouped by window; a transposed build or COO input is
+    // grouped first by a stable sort over the window bits of its keys
+    // (keyed), given BCSR column spans under 2^27.
+    bool per_window = false, keyed = false, kalt = false;
+    // the window field of the keyed layout: whole bytes, since the radix
+    // passes sort bytes and the field must hold the window and nothing else
+    const int kwbits = 8 * (((s.wbits > 0 ? s.wbits : 1) + 7) / 8);
     if (row_ptr && !transpose && nnz > 0) {
         hipLaunchKernelGGL(win_big_kernel, dim3(grid_for(s.W)), dim3(kBlk), 0, stream, row_ptr, s.R, s.W, nnz, w.err);
         GRWS_LAUNCH_CHECK();
@@ -761,31 +867,74 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
         GRWS_HIP(hipMemcpyAsync(h, w.err, 2 * sizeof(int32_t), hipMemcpyDeviceToHost, stream));
         GRWS_HIP(hipStreamSynchronize(stream));
         per_window = (h[0] & kErrRowPtr) == 0 && h[1] == 0;
+    } else if (nnz > 0 && s.C <= ((int64_t)1 << 27)) {
+        if (rows) {
+            hipLaunchKernelGGL(build_keys_kernel, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, row_ptr, rows, cols,
+                               values, nnz, num_rows, num_cols, (int)transpose, s.cbits, kwbits, w.ka, w.va, w.err);
+        } else {
+            const int64_t wg = std::min<int64_t>((num_rows + 3) / 4, 65536);
+            hipLaunchKernelGGL(build_keys_rows_kernel, dim3((unsigned)std::max<int64_t>(wg, 1)), dim3(256), 0, stream,
+                               row_ptr, cols, values, nnz, num_rows, num_cols, (int)transpose, s.cbits, kwbits, w.ka,
+                               w.va, w.err);
+        }
+        GRWS_LAUNCH_CHECK();
+        GRWS_TRY(radix_sort_pairs(w.ka, w.va, w.kb, w.vb, nnz, kwbits, w.sort_ws, w.sort_bytes, stream, &kalt));
+        hipLaunchKernelGGL(keyed_bounds_kernel, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, kalt ? w.kb : w.ka, nnz,
+                           ((uint64_t)1 << kwbits) - 1, w.wstart, w.wend);
+        GRWS_LAUNCH_CHECK();
+        hipLaunchKernelGGL(keyed_big_kernel, dim3(grid_for(s.W)), dim3(kBlk), 0, stream, w.wstart, w.wend, s.W, w.err);
+        GRWS_LAUNCH_CHECK();
+        int32_t h[2] = {0, 0};
+        GRWS_HIP(hipMemcpyAsync(h, w.err, 2 * sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+        GRWS_HIP(hipStreamSynchronize(stream));
+        GRWS_TRY(report_input_error(h[0], "bcsr_build"));
+        if (h[1] == 0) {
+            per_window = keyed = true;
+        } else {  // the global sort rebuilds its keys and bounds
+            GRWS_TRY(fill_i64(w.wstart, s.W, 0, stream));
+            GRWS_TRY(fill_i64(w.wend, s.W, 0, stream));
+        }
     }
     if (per_window) {
         GRWS_TRY(fill_i32(w.err + 2, 1, 1, stream));
         const unsigned wg = (unsigned)std::min<int64_t>(s.W, 4096);
         int32_t* ucol = reinterpret_cast<int32_t*>(w.va);
-        hipLaunchKernelGGL(win_sort_kernel<8192>, dim3(wg), dim3(kWinBlk), 0, stream, row_ptr, cols, values, nnz, s.R,
-                           s.W, num_cols, (int)tile_cols, w.ka, ucol, w.wstart, w.wend, w.wtiles, w.err);
-        GRWS_LAUNCH_CHECK();
-        hipLaunchKernelGGL(win_sort_kernel<16384>, dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0, stream, row_ptr,
-                           cols, values, nnz, s.R, s.W, num_cols, (int)tile_cols, w.ka, ucol, w.wstart, w.wend,
-                           w.wtiles, w.err);
-        GRWS_LAUNCH_CHECK();
+        if (keyed) {
+            // sorted keys and values in ka / va (then the records overwrite
+            // them window by window) or kb / vb
+            const uint64_t* tk = kalt ? w.kb : w.ka;
+            const uint32_t* tv = kalt ? w.vb : w.va;
+            hipLaunchKernelGGL((win_sort_kernel<8192, true>), dim3(wg), dim3(kWinBlk), 0, stream, nullptr, nullptr,
+                               nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols, w.ka, ucol, w.wstart, w.wend,
+                               w.wtiles, w.err);
+            GRWS_LAUNCH_CHECK();
+            hipLaunchKernelGGL((win_sort_kernel<16384, true>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0,
+                               stream, nullptr, nullptr, nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols,
+                               w.ka, ucol, w.wstart, w.wend, w.wtiles, w.err);
+            GRWS_LAUNCH_CHECK();
+        } else {
+            hipLaunchKernelGGL((win_sort_kernel<8192, false>), dim3(wg), dim3(kWinBlk), 0, stream, row_ptr, cols, values,
+                               nullptr, nullptr, 0, nnz, s.R, s.W, num_cols, (int)tile_cols, w.ka, ucol, w.wstart,
+                               w.wend, w.wtiles, w.err);
+            GRWS_LAUNCH_CHECK();
+            hipLaunchKernelGGL((win_sort_kernel<16384, false>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0,
+                               stream, row_ptr, cols, values, nullptr, nullptr, 0, nnz, s.R, s.W, num_cols,
+                               (int)tile_cols, w.ka, ucol, w.wstart, w.wend, w.wtiles, w.err);
+            GRWS_LAUNCH_CHECK();
+        }
     }
     bool alt = false;
     if (nnz > 0 && !per_window) {
         if (rows) {
             hipLaunchKernelGGL(build_keys_kernel, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, row_ptr, rows, cols,
-                               values, nnz, num_rows, num_cols, (int)transpose, s.cbits, w.ka, w.va, w.err);
+                               values, nnz, num_rows, num_cols, (int)transpose, s.cbits, 0, w.ka, w.va, w.err);
         } else {
             // every edge lies in some row's range (check_row_ptr_kernel flags
             // a row pointer that does not cover [0, nnz) exactly)
             const int64_t wg = std::min<int64_t>((num_rows + 3) / 4, 65536);
             hipLaunchKernelGGL(build_keys_rows_kernel, dim3((unsigned)std::max<int64_t>(wg, 1)), dim3(256), 0, stream,
-                               row_ptr, cols, values, nnz, num_rows, num_cols, (int)transpose, s.cbits, w.ka, w.va,
-                               w.err);
+                               row_ptr, cols, values, nnz, num_rows, num_cols, (int)transpose, s.cbits, 0, w.ka,
+                               w.va, w.err);
         }
         GRWS_LAUNCH_CHECK();
         GRWS_TRY(radix_sort_pairs(w.ka, w.va, w.kb, w.vb, nnz, s.bits, w.sort_ws, w.sort_bytes, stream, &alt));

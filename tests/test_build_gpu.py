@@ -132,6 +132,66 @@ def test_csr_build_window_paths(cuda_device, hub, tc):
     np.testing.assert_array_equal(dv.cpu().numpy(), ov.astype(np.float32))
 
 
+def _oracle_transposed(n_r, n_c, rp, cols, vals, tc):
+    """BCSR of A^T by the oracle's converter over A^T's CSR, whose rows list
+    their edges in input order (a stable sort by column), so duplicate
+    edges keep their input order."""
+    rows = np.repeat(np.arange(n_r, dtype=np.int32), np.diff(rp))
+    order = np.argsort(cols, kind="stable")
+    trp = np.zeros(n_c + 1, np.int64)
+    np.add.at(trp, cols.astype(np.int64) + 1, 1)
+    return oracle.csr_to_bcsr(n_c, np.cumsum(trp), rows[order], vals[order], 16, tc)
+
+
+@pytest.mark.parametrize("hub", [False, True])
+@pytest.mark.parametrize("tc", [8, 16])
+def test_transposed_csr_build_window_paths(cuda_device, hub, tc):
+    """Transposed builds from a CSR: windows of A^T grouped by a sort over
+    the window bits, then built window by window; with a column of 17,000
+    in-edges (a window above 16,384 edges) the global sort instead.  Equal
+    to the oracle's converter over A^T, duplicates in input order."""
+    print(f"case transposed window paths hub={hub} tc={tc}", flush=True)
+    n_r, n_c, rp, cols, vals = _window_case_csr(False, seed=40 + tc)
+    if hub:  # 17,000 more rows, each with an edge to column 3 and one random edge
+        rng = np.random.default_rng(3)
+        extra = np.stack([np.full(17000, 3), rng.integers(0, n_c, 17000)], 1).reshape(-1).astype(np.int32)
+        cols = np.concatenate([cols, extra])
+        vals = np.concatenate([vals, rng.standard_normal(extra.size).astype(np.float32)])
+        rp = np.concatenate([rp, rp[-1] + 2 * np.arange(1, 17001, dtype=np.int64)])
+        n_r += 17000
+    ow, oc, ov = _oracle_transposed(n_r, n_c, rp, cols, vals, tc)
+    dw, dc, dv = builder.csr_to_bcsr_device(n_r, n_c, torch.from_numpy(rp).to(cuda_device),
+                                            torch.from_numpy(cols).to(cuda_device),
+                                            torch.from_numpy(vals).to(cuda_device), tile_cols=tc, transpose=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dw.cpu().numpy(), ow)
+    np.testing.assert_array_equal(dc.cpu().numpy(), oc)
+    np.testing.assert_array_equal(dv.cpu().numpy(), ov.astype(np.float32))
+
+
+def test_coo_build_wide_columns_global_sort(cuda_device):
+    """COO input over more than 2^27 columns (beyond the window-by-window
+    path's column span): the global sort, equal to the oracle."""
+    print("case coo wide columns", flush=True)
+    rng = np.random.default_rng(17)
+    n, n_c, m = 300, (1 << 27) + 100, 6000
+    rows = rng.integers(0, n, m).astype(np.int32)
+    cols = rng.integers(0, n_c, m).astype(np.int32)
+    cols[:50] = n_c - 1
+    vals = rng.standard_normal(m).astype(np.float32)
+    order = np.argsort(rows, kind="stable")
+    rp = np.zeros(n + 1, np.int64)
+    np.add.at(rp, rows + 1, 1)
+    ow, oc, ov = oracle.csr_to_bcsr(n, np.cumsum(rp), cols[order], vals[order], 16, 16)
+    dw, dc, dv = builder.coo_to_bcsr_device(n, n_c, torch.from_numpy(rows).to(cuda_device),
+                                            torch.from_numpy(cols).to(cuda_device),
+                                            torch.from_numpy(vals).to(cuda_device), tile_cols=16)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dw.cpu().numpy(), ow)
+    np.testing.assert_array_equal(dc.cpu().numpy(), oc)
+    np.testing.assert_array_equal(dv.cpu().numpy(), ov.astype(np.float32))
+
+
 @pytest.mark.parametrize("vdt", [torch.float32, torch.float16])
 def test_csr_build_unaligned_outputs(cuda_device, vdt):
     """Outputs that start one element past a 16-byte boundary (a C-ABI
