@@ -65,6 +65,7 @@ struct BuildWs {
     int64_t* uidx;
     int64_t *wstart, *wend;
     int32_t* wtiles;
+    int32_t* blist;  // windows of more than kWinCap edges (per-window path)
     int32_t* err;
     char* sort_ws;
     size_t sort_bytes;
@@ -84,6 +85,7 @@ void carve_build(C& cv, const BuildShape& s, BuildWs* w) {
     w->wstart = cv.template take<int64_t>(s.W + 1);
     w->wend = cv.template take<int64_t>(s.W + 1);
     w->wtiles = cv.template take<int32_t>(s.W + 1);
+    w->blist = cv.template take<int32_t>(s.W + 1);
     w->err = cv.template take<int32_t>(64);
     w->sort_bytes = radix_sort_workspace_bytes(n);
     w->sort_ws = cv.template take<char>(w->sort_bytes);
@@ -274,15 +276,16 @@ __global__ void build_scatter_kernel(const uint64_t* __restrict__ keys, const ui
 // stable, so of duplicate (row, column) edges the one last in CSR order is
 // the last of its run and is the one stored, as with the global sort.
 //
-// record: value bits (f32) | place << 32 (14 bits) | row << 46 (4 bits) |
-// last of its (column, row) run << 50; the window's last record holds its
+// record: value bits (f32) | place << 32 (27 bits) | row << 59 (4 bits) |
+// last of its (column, row) run << 63; the window's last record holds its
 // last place, so the fill knows the count of distinct columns.
+constexpr int64_t kWinHuge = (int64_t)1 << 27;  // windows of more edges take the global sort
 __device__ __forceinline__ uint64_t win_record(uint32_t vbits, int place, int row, bool last) {
-    return (uint64_t)vbits | ((uint64_t)place << 32) | ((uint64_t)row << 46) | ((uint64_t)last << 50);
+    return (uint64_t)vbits | ((uint64_t)place << 32) | ((uint64_t)row << 59) | ((uint64_t)last << 63);
 }
-__device__ __forceinline__ int rec_place(uint64_t r) { return (int)((r >> 32) & 16383u); }
-__device__ __forceinline__ int rec_row(uint64_t r) { return (int)((r >> 46) & 15u); }
-__device__ __forceinline__ bool rec_last(uint64_t r) { return (r >> 50) & 1u; }
+__device__ __forceinline__ int rec_place(uint64_t r) { return (int)((r >> 32) & (uint64_t)(kWinHuge - 1)); }
+__device__ __forceinline__ int rec_row(uint64_t r) { return (int)((r >> 59) & 15u); }
+__device__ __forceinline__ bool rec_last(uint64_t r) { return (r >> 63) & 1u; }
 
 constexpr int kWinCap = 16384;  // windows of up to 8,192 edges use a half-size LDS twin
 constexpr int kWinBlk = 512;
@@ -290,21 +293,29 @@ constexpr int kWinDig = 9;                 // radix digit bits
 constexpr int kWinBkt = 1 << kWinDig;      // digit values: one per thread in the offset scan
 static_assert(kWinBkt == kWinBlk, "the offset scan gives each thread one digit");
 
-// Windows with more than kWinCap edges (err[1]), from a valid row pointer.
+// Windows of more than kWinCap edges: counted in err[1] and listed in blist
+// (in no particular order; each is built by itself); windows of more than
+// kWinHuge edges counted in err[3].  From a valid row pointer.
+__device__ __forceinline__ void note_window_size(int64_t w, int64_t m, int32_t* __restrict__ blist,
+                                                 int32_t* __restrict__ err) {
+    if (m > kWinCap) blist[atomicAdd(&err[1], 1)] = (int32_t)w;
+    if (m > kWinHuge) atomicAdd(&err[3], 1);
+}
+
 __global__ void win_big_kernel(const int64_t* __restrict__ row_ptr, int64_t R, int64_t W, int64_t n,
-                               int32_t* __restrict__ err) {
+                               int32_t* __restrict__ blist, int32_t* __restrict__ err) {
     const int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (w >= W) return;
     const int64_t r1 = 16 * w + 16 < R ? 16 * w + 16 : R;
-    if (row_ptr[r1] - row_ptr[16 * w] > kWinCap) atomicAdd(&err[1], 1);
+    note_window_size(w, row_ptr[r1] - row_ptr[16 * w], blist, err);
 }
 
 // The same from window bounds (the window-major sorted keys').
 __global__ void keyed_big_kernel(const int64_t* __restrict__ wstart, const int64_t* __restrict__ wend, int64_t W,
-                                 int32_t* __restrict__ err) {
+                                 int32_t* __restrict__ blist, int32_t* __restrict__ err) {
     const int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (w >= W) return;
-    if (wend[w] - wstart[w] > kWinCap) atomicAdd(&err[1], 1);
+    note_window_size(w, wend[w] - wstart[w], blist, err);
 }
 
 // KEYED false: the window's edges straight from a CSR (row_ptr, cols, vals),
@@ -313,22 +324,26 @@ __global__ void keyed_big_kernel(const int64_t* __restrict__ wstart, const int64
 // (tkeys, tvals, bounds in wstart / wend), which arrive in input order and
 // are sorted by (column, row): the LDS key is (column - min) << 4 | row,
 // which needs column spans under 2^27 (the host checks).
-template <int CAP, bool KEYED>
-__global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 8192 ? 4 : 2))) void win_sort_kernel(
+template <int CAP, int BLK, bool KEYED>
+__global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192 ? 4 : (CAP == 16384 ? 2 : 1)))) void win_sort_kernel(
     const int64_t* __restrict__ row_ptr, const int32_t* __restrict__ cols, const float* __restrict__ vals,
     const uint64_t* __restrict__ tkeys, const uint32_t* __restrict__ tvals, int wbits, int64_t n, int64_t R, int64_t W,
     int64_t num_cols, int tc, uint64_t* __restrict__ skeys, int32_t* __restrict__ ucol, int64_t* __restrict__ wstart,
     int64_t* __restrict__ wend, int32_t* __restrict__ wtiles, int32_t* __restrict__ err) {
-    // CAP 8192: the windows of at most 8,192 edges (73 KB of LDS: two
-    // work-groups per CU); CAP 16384: the larger ones (at most kWinCap
-    // edges: checked before the launch)
-    constexpr int NW = kWinBlk / kWave;
-    constexpr int PER = CAP / kWinBlk;        // edges per thread
+    // CAP 2048 (256 threads, 8-bit digits, 18 KB of LDS): the windows of at
+    // most 2,048 edges; CAP 8192 (512 threads, 9-bit digits, 73 KB: two
+    // work-groups per CU): up to 8,192; CAP 16384: the larger ones (at most
+    // kWinCap edges: checked before the launch)
+    static_assert((CAP == 2048 && BLK == 256) || (CAP != 2048 && BLK == BLK), "launch shapes");
+    constexpr int NW = BLK / kWave;
+    constexpr int PER = CAP / BLK;            // edges per thread
+    constexpr int DIG = BLK == 256 ? 8 : 9;   // digit bits: one digit per thread in the offset scan
+    constexpr int MLO = CAP == 2048 ? -1 : (CAP == 8192 ? 2048 : 8192);  // this launch: MLO < edges <= CAP
     __shared__ int32_t colv[CAP];             // the window's sort keys, by edge offset
     __shared__ uint16_t ia[CAP], ib[CAP];     // edge offsets: sort source and destination
     // [wave][digit] counts, then scatter positions, 16 bits each (at most
     // CAP), two digits a word
-    __shared__ uint32_t cnt[NW * kWinBkt / 2];
+    __shared__ uint32_t cnt[NW * BLK / 2];
     __shared__ int64_t rp[17];
     __shared__ int64_t tmp[NW + 1];
     __shared__ int32_t mm[2 * NW];            // per-wave column range
@@ -341,7 +356,8 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
             e0 = wstart[w];
             const int64_t mm64 = wend[w] - e0;
             m = (int)(mm64 < 0 ? 0 : (mm64 > CAP ? CAP : mm64));
-            if ((CAP == 8192) != (mm64 <= 8192)) continue;  // the other launch's window (uniform; no LDS yet)
+            // another launch's window (uniform; no LDS yet)
+            if (mm64 <= MLO || mm64 > CAP) continue;
         } else {
             const int64_t r0 = 16 * w;
             nr = (int)(R - r0 < 16 ? R - r0 : 16);
@@ -351,8 +367,9 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
             }
             __syncthreads();
             e0 = rp[0];
-            m = (int)(rp[nr] - e0);
-            if ((CAP == 8192) != (m <= 8192)) {  // the other launch's window (uniform)
+            const int64_t mm64 = rp[nr] - e0;
+            m = (int)(mm64 > CAP ? CAP : mm64);
+            if (mm64 <= MLO || mm64 > CAP) {  // another launch's window (uniform)
                 __syncthreads();
                 continue;
             }
@@ -365,12 +382,12 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
             uint64_t kk[PER];
 #pragma unroll
             for (int k = 0; k < PER; ++k) {
-                const int j = tid + k * kWinBlk;
+                const int j = tid + k * BLK;
                 kk[k] = j < m ? tkeys[e0 + j] : 0;
             }
 #pragma unroll
             for (int k = 0; k < PER; ++k) {
-                if (tid + k * kWinBlk < m) {
+                if (tid + k * BLK < m) {
                     const int c = (int)(kk[k] >> (wbits + 4));
                     cmin = min(cmin, c);
                     cmax = max(cmax, c);
@@ -391,7 +408,7 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
             }
 #pragma unroll
             for (int k = 0; k < PER; ++k) {
-                const int j = tid + k * kWinBlk;
+                const int j = tid + k * BLK;
                 if (j < m) {
                     const int c = (int)(kk[k] >> (wbits + 4)), q = (int)((kk[k] >> wbits) & 15u);
                     colv[j] = ((c - cmin) << 4) | q;
@@ -404,13 +421,13 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
             int32_t cv[PER];
 #pragma unroll
             for (int k = 0; k < PER; ++k) {
-                const int j = tid + k * kWinBlk;
+                const int j = tid + k * BLK;
                 cv[k] = j < m ? cols[e0 + j] : 0;
             }
             bool bad = false;
 #pragma unroll
             for (int k = 0; k < PER; ++k) {
-                const int j = tid + k * kWinBlk;
+                const int j = tid + k * BLK;
                 if (j < m) {
                     int32_t c = cv[k];
                     if (c < 0 || (int64_t)c >= num_cols) {
@@ -446,12 +463,12 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
         const int lo = min(wv * chunk, m), hi = min(lo + chunk, m);
         uint16_t* src = ia;
         uint16_t* dst = ib;
-        for (int sh = 0; sh < bits; sh += kWinDig) {  // uniform
-            for (int i = tid; i < NW * kWinBkt / 2; i += kWinBlk) cnt[i] = 0;
+        for (int sh = 0; sh < bits; sh += DIG) {  // uniform
+            for (int i = tid; i < NW * BLK / 2; i += BLK) cnt[i] = 0;
             __syncthreads();
             for (int i = lo + lane; i < hi; i += kWave) {
-                const uint32_t d = ((uint32_t)(colv[src[i]] - cbase) >> sh) & (kWinBkt - 1);
-                atomicAdd(&cnt[wv * (kWinBkt / 2) + (d >> 1)], 1u << (16 * (d & 1)));
+                const uint32_t d = ((uint32_t)(colv[src[i]] - cbase) >> sh) & (BLK - 1);
+                atomicAdd(&cnt[wv * (BLK / 2) + (d >> 1)], 1u << (16 * (d & 1)));
             }
             __syncthreads();
             {  // exclusive offsets in (digit, wave) order; this thread's digit is tid
@@ -460,11 +477,11 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
                 int t = 0;
 #pragma unroll
                 for (int v = 0; v < NW; ++v) {
-                    pos[v] = (int)((cnt[v * (kWinBkt / 2) + (tid >> 1)] >> hw) & 0xffffu);
+                    pos[v] = (int)((cnt[v * (BLK / 2) + (tid >> 1)] >> hw) & 0xffffu);
                     t += pos[v];
                 }
                 int64_t tot;
-                int run = (int)(block_incl_scan<kWinBlk>(t, tmp, &tot) - t);  // every count read first
+                int run = (int)(block_incl_scan<BLK>(t, tmp, &tot) - t);  // every count read first
 #pragma unroll
                 for (int v = 0; v < NW; ++v) {
                     const int c = pos[v];
@@ -475,7 +492,7 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
 #pragma unroll
                 for (int v = 0; v < NW; ++v) {
                     const int odd = __shfl_down(pos[v], 1, kWave);
-                    if (!(tid & 1)) cnt[v * (kWinBkt / 2) + (tid >> 1)] = (uint32_t)pos[v] | ((uint32_t)odd << 16);
+                    if (!(tid & 1)) cnt[v * (BLK / 2) + (tid >> 1)] = (uint32_t)pos[v] | ((uint32_t)odd << 16);
                 }
             }
             __syncthreads();
@@ -489,17 +506,17 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
                 int d = 0;
                 if (v) {
                     x = src[i];
-                    d = (int)(((uint32_t)(colv[x] - cbase) >> sh) & (kWinBkt - 1));
+                    d = (int)(((uint32_t)(colv[x] - cbase) >> sh) & (BLK - 1));
                 }
                 uint64_t peers = __ballot(v);
 #pragma unroll
-                for (int k = 0; k < kWinDig; ++k) {
+                for (int k = 0; k < DIG; ++k) {
                     const bool bit = (d >> k) & 1;
                     const uint64_t bb = __ballot(bit);
                     peers &= bit ? bb : ~bb;
                 }
                 if (v) {
-                    const int word = wv * (kWinBkt / 2) + (d >> 1), hw = 16 * (d & 1);
+                    const int word = wv * (BLK / 2) + (d >> 1), hw = 16 * (d & 1);
                     const int base = (int)((cnt[word] >> hw) & 0xffffu);
                     dst[base + __popcll(peers & ((1ull << lane) - 1))] = x;
                     if ((peers >> lane) == 1ull) atomicAdd(&cnt[word], (uint32_t)__popcll(peers) << hw);
@@ -526,12 +543,12 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
             return q;
         };
         {
-            const int run = (m + kWinBlk - 1) / kWinBlk;
+            const int run = (m + BLK - 1) / BLK;
             const int a0 = min(tid * run, m), a1 = min(a0 + run, m);
             int f = 0;
             for (int i = a0; i < a1; ++i) f += first_of_col(i) ? 1 : 0;
             int64_t tot;
-            int pl = (int)block_incl_scan<kWinBlk>(f, tmp, &tot) - f;
+            int pl = (int)block_incl_scan<BLK>(f, tmp, &tot) - f;
             for (int i = a0; i < a1; ++i) {
                 pl += first_of_col(i) ? 1 : 0;
                 dst[i] = (uint16_t)(pl - 1);
@@ -552,12 +569,12 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
         uint32_t vv[PER];
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int i = tid + k * kWinBlk;
+            const int i = tid + k * BLK;
             jj[k] = i < m ? src[i] : 0;
         }
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int i = tid + k * kWinBlk;
+            const int i = tid + k * BLK;
             if (KEYED) vv[k] = i < m ? tvals[e0 + jj[k]] : 0u;
             else vv[k] = (vals && i < m) ? __float_as_uint(vals[e0 + jj[k]]) : 0x3f800000u;
         }
@@ -566,7 +583,7 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
         if (KEYED) __syncthreads();
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int i = tid + k * kWinBlk;
+            const int i = tid + k * BLK;
             if (i < m) {
                 const int j = jj[k];
                 int c, q;
@@ -589,6 +606,219 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
             }
         }
         __syncthreads();  // LDS is rewritten for the next window
+    }
+}
+
+// Windows of more than kWinCap edges (listed in blist; at most kWinHuge
+// edges, checked before the launch), one work-group each: the same stable
+// radix sort and records, with the edge offsets double-buffered in global
+// scratch (jbuf, 2 m entries at 2 e0), the places in pbuf, and every sort key
+// read from the input where it is used.  KEYED with kcopy: the sorted keys and
+// values are where the records and distinct columns go (ka / va), so the
+// window's share is copied to kcopy / vcopy first.
+template <bool KEYED>
+__global__ __launch_bounds__(kWinBlk) void win_sort_big_kernel(
+    const int64_t* __restrict__ row_ptr, const int32_t* __restrict__ cols, const float* __restrict__ vals,
+    const uint64_t* tkeys, const uint32_t* tvals, uint64_t* kcopy, uint32_t* vcopy, int wbits, int64_t n, int64_t R,
+    const int32_t* __restrict__ blist, int nbig, int64_t num_cols, int tc, uint32_t* __restrict__ jbuf,
+    uint32_t* __restrict__ pbuf, uint64_t* skeys, int32_t* ucol, int64_t* __restrict__ wstart,
+    int64_t* __restrict__ wend, int32_t* __restrict__ wtiles, int32_t* __restrict__ err) {
+    constexpr int NW = kWinBlk / kWave;
+    __shared__ uint32_t cnt[NW * kWinBkt];  // [wave][digit] counts, then scatter positions
+    __shared__ int64_t rp[17];
+    __shared__ int64_t tmp[NW + 1];
+    __shared__ int32_t mm[2 * NW];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+    for (int bi = blockIdx.x; bi < nbig; bi += gridDim.x) {  // uniform over the work-group
+        const int64_t w = blist[bi];
+        int nr = 16;
+        int64_t e0;
+        int m;
+        if (KEYED) {
+            e0 = wstart[w];
+            m = (int)(wend[w] - e0);
+        } else {
+            const int64_t r0 = 16 * w;
+            nr = (int)(R - r0 < 16 ? R - r0 : 16);
+            if (tid <= nr) {
+                int64_t v = row_ptr[r0 + tid];
+                rp[tid] = v < 0 ? 0 : (v > n ? n : v);
+            }
+            __syncthreads();
+            e0 = rp[0];
+            m = (int)(rp[nr] - e0);
+        }
+        const uint64_t* tk = tkeys;
+        const uint32_t* tv = tvals;
+        if (KEYED && kcopy) {
+            for (int j = tid; j < m; j += kWinBlk) {
+                kcopy[e0 + j] = tkeys[e0 + j];
+                vcopy[e0 + j] = tvals[e0 + j];
+            }
+            __syncthreads();
+            tk = kcopy;
+            tv = vcopy;
+        }
+        int cmin = 0x7fffffff, cmax = 0;
+        bool bad = false;
+        for (int j = tid; j < m; j += kWinBlk) {
+            int c;
+            if (KEYED) {
+                c = (int)(tk[e0 + j] >> (wbits + 4));
+            } else {
+                int64_t cc = cols[e0 + j];
+                if (cc < 0 || cc >= num_cols) {
+                    bad = true;
+                    cc = 0;
+                }
+                c = (int)cc;
+            }
+            cmin = min(cmin, c);
+            cmax = max(cmax, c);
+        }
+        if (bad) atomicOr(err, kErrCol);
+        for (int d = kWave / 2; d >= 1; d >>= 1) {
+            cmin = min(cmin, __shfl_xor(cmin, d, kWave));
+            cmax = max(cmax, __shfl_xor(cmax, d, kWave));
+        }
+        if (lane == 0) {
+            mm[wv] = cmin;
+            mm[NW + wv] = cmax;
+        }
+        __syncthreads();
+        for (int v = 0; v < NW; ++v) {
+            cmin = min(cmin, mm[v]);
+            cmax = max(cmax, mm[NW + v]);
+        }
+        // the sort key of edge offset j: (column - min) << 4 | row (KEYED),
+        // column - min (CSR; the rows are in input order already)
+        auto skey = [&](uint32_t j) -> uint32_t {
+            if (KEYED) {
+                const uint64_t k = tk[e0 + j];
+                return ((uint32_t)((int)(k >> (wbits + 4)) - cmin) << 4) | (uint32_t)((k >> wbits) & 15u);
+            }
+            int64_t cc = cols[e0 + j];
+            if (cc < 0 || cc >= num_cols) cc = 0;
+            return (uint32_t)((int)cc - cmin);
+        };
+        auto colkey = [&](uint32_t j) -> uint32_t { return KEYED ? skey(j) >> 4 : skey(j); };
+        auto row_of = [&](uint32_t j) {  // CSR: the last q with rp[q] <= e0 + j
+            const int64_t e = e0 + j;
+            int q = 0;
+#pragma unroll
+            for (int st = 8; st >= 1; st >>= 1)
+                if (q + st < nr && rp[q + st] <= e) q += st;
+            return q;
+        };
+        const uint32_t span = m > 0 ? (KEYED ? ((uint32_t)(cmax - cmin) << 4) | 15u : (uint32_t)(cmax - cmin)) : 0u;
+        const int bits = span ? 32 - __clz(span) : 0;
+        uint32_t* src = jbuf + 2 * e0;
+        uint32_t* dst = src + m;
+        for (int j = tid; j < m; j += kWinBlk) src[j] = (uint32_t)j;
+        __syncthreads();
+        const int chunk = ((m + NW * kWave - 1) / (NW * kWave)) * kWave;
+        const int lo = min(wv * chunk, m), hi = min(lo + chunk, m);
+        for (int sh = 0; sh < bits; sh += kWinDig) {  // uniform
+            for (int i = tid; i < NW * kWinBkt; i += kWinBlk) cnt[i] = 0;
+            __syncthreads();
+            for (int i = lo + lane; i < hi; i += kWave)
+                atomicAdd(&cnt[wv * kWinBkt + ((skey(src[i]) >> sh) & (kWinBkt - 1))], 1u);
+            __syncthreads();
+            {  // exclusive offsets in (digit, wave) order; this thread's digit is tid
+                int pos[NW];
+                int t = 0;
+#pragma unroll
+                for (int v = 0; v < NW; ++v) {
+                    pos[v] = (int)cnt[v * kWinBkt + tid];
+                    t += pos[v];
+                }
+                int64_t tot;
+                int run = (int)(block_incl_scan<kWinBlk>(t, tmp, &tot) - t);  // every count read first
+#pragma unroll
+                for (int v = 0; v < NW; ++v) {
+                    cnt[v * kWinBkt + tid] = (uint32_t)run;
+                    run += pos[v];
+                }
+            }
+            __syncthreads();
+            for (int b = lo; b < hi; b += kWave) {  // uniform over the wave
+                const int i = b + lane;
+                const bool v = i < hi;
+                uint32_t x = 0;
+                int d = 0;
+                if (v) {
+                    x = src[i];
+                    d = (int)((skey(x) >> sh) & (kWinBkt - 1));
+                }
+                uint64_t peers = __ballot(v);
+#pragma unroll
+                for (int k = 0; k < kWinDig; ++k) {
+                    const bool bit = (d >> k) & 1;
+                    const uint64_t bb = __ballot(bit);
+                    peers &= bit ? bb : ~bb;
+                }
+                if (v) {
+                    const uint32_t base = cnt[wv * kWinBkt + d];
+                    dst[base + __popcll(peers & ((1ull << lane) - 1))] = x;
+                    if ((peers >> lane) == 1ull) cnt[wv * kWinBkt + d] = base + (uint32_t)__popcll(peers);
+                }
+            }
+            __syncthreads();
+            uint32_t* t = src;
+            src = dst;
+            dst = t;
+        }
+        {  // places: contiguous runs of sorted positions, one block scan
+            const int run = (m + kWinBlk - 1) / kWinBlk;
+            const int a0 = min(tid * run, m), a1 = min(a0 + run, m);
+            int f = 0;
+            uint32_t prev = a0 > 0 ? colkey(src[a0 - 1]) : 0u;
+            for (int i = a0; i < a1; ++i) {
+                const uint32_t ck = colkey(src[i]);
+                f += (i == 0 || ck != prev) ? 1 : 0;
+                prev = ck;
+            }
+            int64_t tot;
+            int pl = (int)block_incl_scan<kWinBlk>(f, tmp, &tot) - f;
+            prev = a0 > 0 ? colkey(src[a0 - 1]) : 0u;
+            for (int i = a0; i < a1; ++i) {
+                const uint32_t ck = colkey(src[i]);
+                pl += (i == 0 || ck != prev) ? 1 : 0;
+                prev = ck;
+                pbuf[e0 + i] = (uint32_t)(pl - 1);
+            }
+            if (tid == 0) {
+                wtiles[w] = (int32_t)((tot + tc - 1) / tc);
+                if (!KEYED) {
+                    wstart[w] = e0;
+                    wend[w] = e0 + m;
+                }
+            }
+        }
+        __syncthreads();
+        for (int i = tid; i < m; i += kWinBlk) {
+            const uint32_t j = src[i];
+            const uint32_t kj = skey(j);
+            int c, q;
+            bool last = true;
+            if (KEYED) {
+                c = (int)(kj >> 4) + cmin;
+                q = (int)(kj & 15u);
+                if (i + 1 < m) last = skey(src[i + 1]) != kj;
+            } else {
+                c = (int)kj + cmin;
+                q = row_of(j);
+                if (i + 1 < m) {
+                    const uint32_t jn = src[i + 1];
+                    last = skey(jn) != kj || row_of(jn) != q;
+                }
+            }
+            const int pl = (int)pbuf[e0 + i];
+            if (i == 0 || (int)pbuf[e0 + i - 1] != pl) ucol[e0 + pl] = c;
+            const uint32_t vb = KEYED ? tv[e0 + j] : (vals ? __float_as_uint(vals[e0 + j]) : 0x3f800000u);
+            skeys[e0 + i] = win_record(vb, pl, q, last);
+        }
+        __syncthreads();  // LDS and scratch are rewritten for the next window
     }
 }
 
@@ -615,16 +845,18 @@ __device__ __forceinline__ __hip_bfloat16 to_value<__hip_bfloat16>(float v) {
 // 16 x 16, 64 of 16 x 8) assembled in LDS from the records, which every
 // thread loads once, and written out with 16-byte stores.
 constexpr int kFillVals = 8192;
-template <int CAP, typename VT>
-__global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 8192 ? 4 : 2))) void win_fill_kernel(const uint64_t* __restrict__ rec,
+template <int CAP, int BLK, typename VT>
+__global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192 ? 4 : (CAP == 16384 ? 2 : 1)))) void win_fill_kernel(const uint64_t* __restrict__ rec,
                                                             const int32_t* __restrict__ ucol,
                                                             const int64_t* __restrict__ wstart,
                                                             const int64_t* __restrict__ wend,
                                                             const int64_t* __restrict__ win_off, int64_t W, int tc,
                                                             int32_t* __restrict__ out_cols, void* __restrict__ out_vals,
                                                             int aligned, const int32_t* __restrict__ err) {
-    // CAP 8192: the windows of at most 8,192 edges; CAP 16384: the larger ones
-    constexpr int PER = CAP / kWinBlk;  // records per thread
+    // CAP 2048 (256 threads): the windows of at most 2,048 edges; CAP 8192:
+    // up to 8,192; CAP 16384: the larger ones (at most kWinCap)
+    constexpr int PER = CAP / BLK;  // records per thread
+    constexpr int MLO = CAP == 2048 ? -1 : (CAP == 8192 ? 2048 : 8192);  // this launch: MLO < edges <= CAP
     constexpr int VPU = 16 / (int)sizeof(VT);  // values per 16 bytes
     __shared__ __align__(16) VT sval[kFillVals];
     if (err[2] != 1) return;  // uniform
@@ -633,27 +865,28 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
     const int gt = kFillVals / (16 * tc);  // tiles per step
     for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {  // uniform over the work-group
         const int64_t e0 = wstart[w], wo = win_off[w];
-        const int m = (int)(wend[w] - e0);
-        if ((CAP == 8192) != (m <= 8192)) continue;  // the other launch's window (uniform)
+        const int64_t mm64 = wend[w] - e0;
+        if (mm64 <= MLO || mm64 > CAP) continue;  // another launch's window (uniform)
+        const int m = (int)mm64;
         const int64_t nt64 = win_off[w + 1] - wo;
         const int nt = (int)(nt64 < 0 ? 0 : nt64);
         uint64_t r[PER];
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int i = tid + k * kWinBlk;
+            const int i = tid + k * BLK;
             r[k] = i < m ? rec[e0 + i] : 0;
         }
         const int u = m > 0 ? rec_place(rec[e0 + m - 1]) + 1 : 0;
         int32_t* oc = out_cols + wo * tc;
-        for (int x = tid; x < nt * tc; x += kWinBlk) oc[x] = x < u ? ucol[e0 + x] : -1;
+        for (int x = tid; x < nt * tc; x += BLK) oc[x] = x < u ? ucol[e0 + x] : -1;
         for (int g0 = 0; g0 < nt; g0 += gt) {  // uniform over the work-group
             const int g1 = g0 + gt < nt ? g0 + gt : nt;
             const int nv = (g1 - g0) * 16 * tc;
-            for (int x = tid; x < nv / VPU; x += kWinBlk) reinterpret_cast<uint4*>(sval)[x] = make_uint4(0, 0, 0, 0);
+            for (int x = tid; x < nv / VPU; x += BLK) reinterpret_cast<uint4*>(sval)[x] = make_uint4(0, 0, 0, 0);
             __syncthreads();
 #pragma unroll
             for (int k = 0; k < PER; ++k) {
-                if (tid + k * kWinBlk < m && rec_last(r[k])) {
+                if (tid + k * BLK < m && rec_last(r[k])) {
                     const int pl = rec_place(r[k]);
                     const int t = (pl >> ltc) - g0;
                     if (t >= 0 && t < g1 - g0)
@@ -664,11 +897,90 @@ __global__ __launch_bounds__(kWinBlk) __attribute__((amdgpu_waves_per_eu(CAP == 
             __syncthreads();
             VT* ov = static_cast<VT*>(out_vals) + (wo + g0) * 16 * tc;
             if (aligned) {  // the values 16-byte aligned (uniform)
+                for (int x = tid; x < nv / VPU; x += BLK)
+                    reinterpret_cast<uint4*>(ov)[x] = reinterpret_cast<const uint4*>(sval)[x];
+            } else {
+                for (int x = tid; x < nv; x += BLK) ov[x] = sval[x];
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// The fill of the windows of more than kWinCap edges (listed in blist), one
+// work-group each: the columns as in win_fill_kernel; the records are read
+// in order, 512 at a time, and their places only grow, so the values are
+// assembled kFillVals at a time in LDS and each step written out once no
+// later record can fall in it.
+template <typename VT>
+__global__ __launch_bounds__(kWinBlk) void win_fill_big_kernel(const uint64_t* __restrict__ rec,
+                                                               const int32_t* __restrict__ ucol,
+                                                               const int64_t* __restrict__ wstart,
+                                                               const int64_t* __restrict__ wend,
+                                                               const int64_t* __restrict__ win_off,
+                                                               const int32_t* __restrict__ blist, int nbig, int tc,
+                                                               int32_t* __restrict__ out_cols, void* __restrict__ out_vals,
+                                                               int aligned, const int32_t* __restrict__ err) {
+    constexpr int VPU = 16 / (int)sizeof(VT);  // values per 16 bytes
+    __shared__ __align__(16) VT sval[kFillVals];
+    if (err[2] != 1) return;  // uniform
+    const int tid = threadIdx.x;
+    const int ltc = tc == 16 ? 4 : 3;
+    const int gt = kFillVals / (16 * tc);  // tiles per step
+    for (int bi = blockIdx.x; bi < nbig; bi += gridDim.x) {  // uniform over the work-group
+        const int64_t w = blist[bi];
+        const int64_t e0 = wstart[w], wo = win_off[w];
+        const int m = (int)(wend[w] - e0);
+        const int64_t nt64 = win_off[w + 1] - wo;
+        const int nt = (int)(nt64 < 0 ? 0 : nt64);
+        const int u = m > 0 ? rec_place(rec[e0 + m - 1]) + 1 : 0;
+        int32_t* oc = out_cols + wo * tc;
+        for (int64_t x = tid; x < (int64_t)nt * tc; x += kWinBlk) oc[x] = x < u ? ucol[e0 + x] : -1;
+        // write out the step at tile g0 (its first min(gt, nt - g0) tiles)
+        auto flush = [&](int g0) {
+            const int g1 = g0 + gt < nt ? g0 + gt : nt;
+            if (g1 <= g0) return;
+            const int nv = (g1 - g0) * 16 * tc;
+            VT* ov = static_cast<VT*>(out_vals) + (wo + g0) * 16 * tc;
+            if (aligned) {
                 for (int x = tid; x < nv / VPU; x += kWinBlk)
                     reinterpret_cast<uint4*>(ov)[x] = reinterpret_cast<const uint4*>(sval)[x];
             } else {
                 for (int x = tid; x < nv; x += kWinBlk) ov[x] = sval[x];
             }
+        };
+        auto clear = [&]() {
+            for (int x = tid; x < kFillVals / VPU; x += kWinBlk) reinterpret_cast<uint4*>(sval)[x] = make_uint4(0, 0, 0, 0);
+        };
+        int g0 = 0;
+        clear();
+        __syncthreads();
+        for (int b = 0; b < m; b += kWinBlk) {  // uniform over the work-group
+            const int i = b + tid;
+            const uint64_t r = i < m ? rec[e0 + i] : 0;
+            // the chunk's last place (places do not decrease): one address for all
+            const int last_tile = rec_place(rec[e0 + (b + kWinBlk < m ? b + kWinBlk : m) - 1]) >> ltc;
+            for (;;) {  // uniform
+                if (i < m && rec_last(r)) {
+                    const int pl = rec_place(r);
+                    const int t = (pl >> ltc) - g0;
+                    if (t >= 0 && t < gt)
+                        sval[((t * 16 + rec_row(r)) << ltc) + (pl & (tc - 1))] = to_value<VT>(__uint_as_float((uint32_t)r));
+                }
+                if (last_tile < g0 + gt) break;  // every record of the chunk placed
+                __syncthreads();
+                flush(g0);
+                __syncthreads();
+                clear();
+                __syncthreads();
+                g0 += gt;
+            }
+        }
+        __syncthreads();
+        for (; g0 < nt; g0 += gt) {  // the last step, and any steps after it (zeros)
+            flush(g0);
+            __syncthreads();
+            clear();
             __syncthreads();
         }
     }
@@ -690,61 +1002,110 @@ __device__ __forceinline__ float load_value<__hip_bfloat16>(const void* v, int64
     return __bfloat162float(static_cast<const __hip_bfloat16*>(v)[idx]);
 }
 
-// One wave per tile; slot s = lane + 64 j is (row s / tc, column s % tc).
-template <typename VT>
-__global__ __launch_bounds__(256) void tile_nnz_kernel(const int32_t* __restrict__ cols, const void* __restrict__ vals,
-                                                       int64_t T, int tc, int64_t num_cols,
-                                                       int32_t* __restrict__ cnt) {
-    const int64_t t = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
-    if (t >= T) return;
-    const int lane = lane_id();
-    const int per = 16 * tc / kWave;
-    int total = 0;
-    for (int j = 0; j < per; ++j) {
-        const int s = lane + kWave * j;
-        const int c = s % tc;
-        const int64_t col = cols[t * tc + c];
-        const bool v = col >= 0 && col < num_cols && load_value<VT>(vals, t * 16 * tc + s) != 0.0f;
-        total += __popcll(__ballot(v));
+// Tiles' values read 16 bytes a lane: chunk x holds values [x V, x V + V) (V
+// = 16 / sizeof(VT)), i.e. slots s0 .. s0 + V - 1 of tile x / tpb (tpb =
+// chunks per tile, 16 to 64: a tile's chunks sit on consecutive lanes of one
+// wave); slot s is (row s / tc, column s % tc).  A slot counts when its
+// column is in [0, num_cols) and its value is nonzero.  ALIGNED: the values
+// 16-byte aligned (else read value by value).
+template <typename VT, bool ALIGNED>
+__device__ __forceinline__ void load_chunk(const void* __restrict__ vals, int64_t chunk, float* out) {
+    constexpr int V = 16 / (int)sizeof(VT);
+    if (ALIGNED) {
+        const uint4 raw = static_cast<const uint4*>(vals)[chunk];
+        const VT* v = reinterpret_cast<const VT*>(&raw);
+#pragma unroll
+        for (int k = 0; k < V; ++k) out[k] = (float)v[k];
+    } else {
+#pragma unroll
+        for (int k = 0; k < V; ++k) out[k] = load_value<VT>(vals, chunk * V + k);
     }
-    if (lane == 0) cnt[t] = total;
 }
 
-template <typename VT>
-__global__ __launch_bounds__(256) void tile_to_coo_kernel(const int64_t* __restrict__ win_off, int64_t W,
+template <typename VT, bool ALIGNED>
+__global__ __launch_bounds__(256) void tile_nnz_kernel(const int32_t* __restrict__ cols, const void* __restrict__ vals,
+                                                       int64_t T, int tc, int64_t num_cols, int32_t* __restrict__ cnt) {
+    constexpr int V = 16 / (int)sizeof(VT);
+    const int tpb = 16 * tc / V;
+    const int64_t nch = T * tpb;
+    for (int64_t xb = (int64_t)blockIdx.x * 256; xb < nch; xb += (int64_t)gridDim.x * 256) {  // uniform
+        const int64_t x = xb + threadIdx.x;
+        int c = 0;
+        if (x < nch) {
+            const int64_t t = x / tpb;
+            const int s0 = (int)(x % tpb) * V;
+            float v[V];
+            load_chunk<VT, ALIGNED>(vals, x, v);
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const int64_t col = cols[t * tc + (s0 + k) % tc];
+                c += (col >= 0 && col < num_cols && v[k] != 0.0f) ? 1 : 0;
+            }
+        }
+        for (int d = tpb / 2; d >= 1; d >>= 1) c += __shfl_xor(c, d, tpb);
+        if (x < nch && x % tpb == 0) cnt[x / tpb] = c;
+    }
+}
+
+// The window of every tile (twin), one work-group per window; tiles outside
+// every window (only from a malformed window_offset) keep window 0.
+__global__ __launch_bounds__(256) void tile_window_kernel(const int64_t* __restrict__ win_off, int64_t W, int64_t T,
+                                                          int32_t* __restrict__ twin) {
+    for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {
+        const int64_t a = win_off[w], e = win_off[w + 1];
+        const int64_t t0 = a < 0 ? 0 : (a > T ? T : a);
+        const int64_t t1 = e < t0 ? t0 : (e > T ? T : e);
+        for (int64_t t = t0 + threadIdx.x; t < t1; t += 256) twin[t] = (int32_t)w;
+    }
+}
+
+template <typename VT, bool ALIGNED>
+__global__ __launch_bounds__(256) void tile_to_coo_kernel(const int32_t* __restrict__ twin,
                                                           const int32_t* __restrict__ cols,
                                                           const void* __restrict__ vals, int64_t T, int tc,
                                                           int64_t num_cols, const int64_t* __restrict__ toff,
                                                           int32_t* __restrict__ out_rows,
                                                           int32_t* __restrict__ out_cols,
                                                           float* __restrict__ out_vals) {
-    const int64_t t = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
-    if (t >= T) return;
-    const int lane = lane_id();
-    // window of tile t: largest w with win_off[w] <= t
-    int64_t lo = 0, hi = W - 1;
-    while (lo < hi) {
-        const int64_t mid = (lo + hi + 1) >> 1;
-        if (win_off[mid] <= t) lo = mid;
-        else hi = mid - 1;
-    }
-    const int64_t row0 = lo * 16;
-    const int per = 16 * tc / kWave;
-    int64_t pos = toff[t];
-    for (int j = 0; j < per; ++j) {
-        const int s = lane + kWave * j;
-        const int c = s % tc;
-        const int64_t col = cols[t * tc + c];
-        const float x = load_value<VT>(vals, t * 16 * tc + s);
-        const bool v = col >= 0 && col < num_cols && x != 0.0f;
-        const uint64_t m = __ballot(v);
-        if (v) {
-            const int64_t o = pos + __popcll(m & lanemask_lt());
-            out_rows[o] = (int32_t)(row0 + s / tc);
-            out_cols[o] = (int32_t)col;
-            out_vals[o] = x;
+    constexpr int V = 16 / (int)sizeof(VT);
+    const int tpb = 16 * tc / V;
+    const int64_t nch = T * tpb;
+    for (int64_t xb = (int64_t)blockIdx.x * 256; xb < nch; xb += (int64_t)gridDim.x * 256) {  // uniform
+        const int64_t x = xb + threadIdx.x;
+        const bool in = x < nch;
+        const int64_t t = in ? x / tpb : 0;
+        const int s0 = in ? (int)(x % tpb) * V : 0;
+        float v[V];
+        int32_t cc[V];
+        int c = 0;
+        if (in) {
+            load_chunk<VT, ALIGNED>(vals, x, v);
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                cc[k] = cols[t * tc + (s0 + k) % tc];
+                c += (cc[k] >= 0 && cc[k] < num_cols && v[k] != 0.0f) ? 1 : 0;
+            }
         }
-        pos += __popcll(m);
+        // exclusive prefix over the tile's chunks (consecutive lanes)
+        int inc = c;
+        const int gl = (int)(threadIdx.x % tpb);
+        for (int d = 1; d < tpb; d <<= 1) {
+            const int y = __shfl_up(inc, d, tpb);
+            if (gl >= d) inc += y;
+        }
+        if (in && c) {
+            int64_t pos = toff[t] + inc - c;
+            const int64_t row0 = 16 * (int64_t)twin[t];
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                if (cc[k] >= 0 && cc[k] < num_cols && v[k] != 0.0f) {
+                    out_rows[pos] = (int32_t)(row0 + (s0 + k) / tc);
+                    out_cols[pos] = cc[k];
+                    out_vals[pos] = v[k];
+                    ++pos;
+                }
+            }
+        }
     }
 }
 
@@ -837,7 +1198,7 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
     carve_build(cv, s, &w);
     if (!cv.ok) return set_error(GRWS_E_CAPACITY, "bcsr_build: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
 
-    GRWS_TRY(fill_i32(w.err, 3, 0, stream));  // error flags, big windows, path of the fill
+    GRWS_TRY(fill_i32(w.err, 4, 0, stream));  // error flags, big windows, path of the fill, huge windows
     if (s.W == 0) {
         GRWS_TRY(fill_i64(window_offset, 1, 0, stream));
         GRWS_HIP(hipStreamSynchronize(stream));
@@ -857,16 +1218,19 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
     // grouped first by a stable sort over the window bits of its keys
     // (keyed), given BCSR column spans under 2^27.
     bool per_window = false, keyed = false, kalt = false;
+    int nbig = 0;
     // the window field of the keyed layout: whole bytes, since the radix
     // passes sort bytes and the field must hold the window and nothing else
     const int kwbits = 8 * (((s.wbits > 0 ? s.wbits : 1) + 7) / 8);
     if (row_ptr && !transpose && nnz > 0) {
-        hipLaunchKernelGGL(win_big_kernel, dim3(grid_for(s.W)), dim3(kBlk), 0, stream, row_ptr, s.R, s.W, nnz, w.err);
+        hipLaunchKernelGGL(win_big_kernel, dim3(grid_for(s.W)), dim3(kBlk), 0, stream, row_ptr, s.R, s.W, nnz,
+                           w.blist, w.err);
         GRWS_LAUNCH_CHECK();
-        int32_t h[2] = {0, 0};
-        GRWS_HIP(hipMemcpyAsync(h, w.err, 2 * sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+        int32_t h[4] = {0, 0, 0, 0};
+        GRWS_HIP(hipMemcpyAsync(h, w.err, 4 * sizeof(int32_t), hipMemcpyDeviceToHost, stream));
         GRWS_HIP(hipStreamSynchronize(stream));
-        per_window = (h[0] & kErrRowPtr) == 0 && h[1] == 0;
+        per_window = (h[0] & kErrRowPtr) == 0 && h[3] == 0;
+        nbig = h[1];
     } else if (nnz > 0 && s.C <= ((int64_t)1 << 27)) {
         if (rows) {
             hipLaunchKernelGGL(build_keys_kernel, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, row_ptr, rows, cols,
@@ -882,14 +1246,16 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
         hipLaunchKernelGGL(keyed_bounds_kernel, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, kalt ? w.kb : w.ka, nnz,
                            ((uint64_t)1 << kwbits) - 1, w.wstart, w.wend);
         GRWS_LAUNCH_CHECK();
-        hipLaunchKernelGGL(keyed_big_kernel, dim3(grid_for(s.W)), dim3(kBlk), 0, stream, w.wstart, w.wend, s.W, w.err);
+        hipLaunchKernelGGL(keyed_big_kernel, dim3(grid_for(s.W)), dim3(kBlk), 0, stream, w.wstart, w.wend, s.W,
+                           w.blist, w.err);
         GRWS_LAUNCH_CHECK();
-        int32_t h[2] = {0, 0};
-        GRWS_HIP(hipMemcpyAsync(h, w.err, 2 * sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+        int32_t h[4] = {0, 0, 0, 0};
+        GRWS_HIP(hipMemcpyAsync(h, w.err, 4 * sizeof(int32_t), hipMemcpyDeviceToHost, stream));
         GRWS_HIP(hipStreamSynchronize(stream));
         GRWS_TRY(report_input_error(h[0], "bcsr_build"));
-        if (h[1] == 0) {
+        if (h[3] == 0) {
             per_window = keyed = true;
+            nbig = h[1];
         } else {  // the global sort rebuilds its keys and bounds
             GRWS_TRY(fill_i64(w.wstart, s.W, 0, stream));
             GRWS_TRY(fill_i64(w.wend, s.W, 0, stream));
@@ -898,29 +1264,54 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
     if (per_window) {
         GRWS_TRY(fill_i32(w.err + 2, 1, 1, stream));
         const unsigned wg = (unsigned)std::min<int64_t>(s.W, 4096);
+        const unsigned wgs = (unsigned)std::min<int64_t>(s.W, 16384);  // the 2,048-edge class, 256 threads
         int32_t* ucol = reinterpret_cast<int32_t*>(w.va);
         if (keyed) {
             // sorted keys and values in ka / va (then the records overwrite
             // them window by window) or kb / vb
             const uint64_t* tk = kalt ? w.kb : w.ka;
             const uint32_t* tv = kalt ? w.vb : w.va;
-            hipLaunchKernelGGL((win_sort_kernel<8192, true>), dim3(wg), dim3(kWinBlk), 0, stream, nullptr, nullptr,
+            hipLaunchKernelGGL((win_sort_kernel<2048, 256, true>), dim3(wgs), dim3(256), 0, stream, nullptr, nullptr,
                                nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols, w.ka, ucol, w.wstart, w.wend,
                                w.wtiles, w.err);
             GRWS_LAUNCH_CHECK();
-            hipLaunchKernelGGL((win_sort_kernel<16384, true>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0,
+            hipLaunchKernelGGL((win_sort_kernel<8192, kWinBlk, true>), dim3(wg), dim3(kWinBlk), 0, stream, nullptr,
+                               nullptr, nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols, w.ka, ucol, w.wstart,
+                               w.wend, w.wtiles, w.err);
+            GRWS_LAUNCH_CHECK();
+            hipLaunchKernelGGL((win_sort_kernel<16384, kWinBlk, true>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0,
                                stream, nullptr, nullptr, nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols,
                                w.ka, ucol, w.wstart, w.wend, w.wtiles, w.err);
             GRWS_LAUNCH_CHECK();
+            if (nbig > 0) {
+                hipLaunchKernelGGL((win_sort_big_kernel<true>), dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, stream,
+                                   nullptr, nullptr, nullptr, tk, tv, kalt ? nullptr : w.kb, kalt ? nullptr : w.vb,
+                                   kwbits, nnz, s.R, w.blist, nbig, s.C, (int)tile_cols,
+                                   reinterpret_cast<uint32_t*>(w.uidx), reinterpret_cast<uint32_t*>(w.uflag), w.ka,
+                                   ucol, w.wstart, w.wend, w.wtiles, w.err);
+                GRWS_LAUNCH_CHECK();
+            }
         } else {
-            hipLaunchKernelGGL((win_sort_kernel<8192, false>), dim3(wg), dim3(kWinBlk), 0, stream, row_ptr, cols, values,
-                               nullptr, nullptr, 0, nnz, s.R, s.W, num_cols, (int)tile_cols, w.ka, ucol, w.wstart,
-                               w.wend, w.wtiles, w.err);
+            hipLaunchKernelGGL((win_sort_kernel<2048, 256, false>), dim3(wgs), dim3(256), 0, stream, row_ptr, cols,
+                               values, nullptr, nullptr, 0, nnz, s.R, s.W, num_cols, (int)tile_cols, w.ka, ucol,
+                               w.wstart, w.wend, w.wtiles, w.err);
             GRWS_LAUNCH_CHECK();
-            hipLaunchKernelGGL((win_sort_kernel<16384, false>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0,
+            hipLaunchKernelGGL((win_sort_kernel<8192, kWinBlk, false>), dim3(wg), dim3(kWinBlk), 0, stream, row_ptr,
+                               cols, values, nullptr, nullptr, 0, nnz, s.R, s.W, num_cols, (int)tile_cols, w.ka, ucol,
+                               w.wstart, w.wend, w.wtiles, w.err);
+            GRWS_LAUNCH_CHECK();
+            hipLaunchKernelGGL((win_sort_kernel<16384, kWinBlk, false>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0,
                                stream, row_ptr, cols, values, nullptr, nullptr, 0, nnz, s.R, s.W, num_cols,
                                (int)tile_cols, w.ka, ucol, w.wstart, w.wend, w.wtiles, w.err);
             GRWS_LAUNCH_CHECK();
+            if (nbig > 0) {
+                hipLaunchKernelGGL((win_sort_big_kernel<false>), dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, stream,
+                                   row_ptr, cols, values, nullptr, nullptr, nullptr, nullptr, 0, nnz, s.R, w.blist,
+                                   nbig, num_cols, (int)tile_cols, reinterpret_cast<uint32_t*>(w.uidx),
+                                   reinterpret_cast<uint32_t*>(w.uflag), w.ka, ucol, w.wstart, w.wend, w.wtiles,
+                                   w.err);
+                GRWS_LAUNCH_CHECK();
+            }
         }
     }
     bool alt = false;
@@ -986,11 +1377,13 @@ extern "C" int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_c
     // the path the count phase took (err[2] = 1: per window; its sorted keys
     // and values are in ka / va, and its fill writes every tile, padding
     // included)
-    int32_t path = 0;
+    int32_t hf[3] = {0, 0, 0};  // err[0..2]: flags, windows over kWinCap edges, path
     if (nnz > 0) {
-        GRWS_HIP(hipMemcpyAsync(&path, w.err + 2, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+        GRWS_HIP(hipMemcpyAsync(hf, w.err, 3 * sizeof(int32_t), hipMemcpyDeviceToHost, stream));
         GRWS_HIP(hipStreamSynchronize(stream));
     }
+    const int32_t path = hf[2];
+    const int nbig = path == 1 ? hf[1] : 0;
     if (path != 1) {
         GRWS_TRY(fill_i32(col_indices, num_tiles * tile_cols, -1, stream));
         GRWS_TRY(fill_bytes_zero(values, (size_t)num_tiles * 16 * tile_cols * dtype_size(values_dtype), stream));
@@ -1001,12 +1394,19 @@ extern "C" int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_c
 #define GRWS_BUILD_FILL(VT)                                                                                        \
     if (path == 1)                                                                                                 \
     {                                                                                                              \
-        hipLaunchKernelGGL((win_fill_kernel<8192, VT>), dim3(wg), dim3(kWinBlk), 0, stream, w.ka,                  \
+        hipLaunchKernelGGL((win_fill_kernel<2048, 256, VT>), dim3((unsigned)std::min<int64_t>(s.W, 16384)),     \
+                           dim3(256), 0, stream, w.ka, reinterpret_cast<const int32_t*>(w.va), w.wstart, w.wend,   \
+                           window_offset, s.W, (int)tile_cols, col_indices, values, aligned, w.err);               \
+        hipLaunchKernelGGL((win_fill_kernel<8192, kWinBlk, VT>), dim3(wg), dim3(kWinBlk), 0, stream, w.ka,         \
                            reinterpret_cast<const int32_t*>(w.va), w.wstart, w.wend, window_offset, s.W,           \
                            (int)tile_cols, col_indices, values, aligned, w.err);                                   \
-        hipLaunchKernelGGL((win_fill_kernel<16384, VT>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0,      \
+        hipLaunchKernelGGL((win_fill_kernel<16384, kWinBlk, VT>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0,      \
                            stream, w.ka, reinterpret_cast<const int32_t*>(w.va), w.wstart, w.wend, window_offset,  \
                            s.W, (int)tile_cols, col_indices, values, aligned, w.err);                              \
+        if (nbig > 0)                                                                                              \
+            hipLaunchKernelGGL(win_fill_big_kernel<VT>, dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, stream,      \
+                               w.ka, reinterpret_cast<const int32_t*>(w.va), w.wstart, w.wend, window_offset,      \
+                               w.blist, nbig, (int)tile_cols, col_indices, values, aligned, w.err);               \
     } else                                                                                                         \
         hipLaunchKernelGGL(build_scatter_kernel<VT>, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, v, nnz, s.cbits, \
                            w.uflag, w.uidx, w.wstart, window_offset, (int)tile_cols, col_indices, values, w.err)
@@ -1071,21 +1471,22 @@ extern "C" int grws_bcsr_to_coo_count(const grws_bcsr* A, int64_t num_cols, void
     char* sws;
     size_t sb;
     GRWS_TRY(coo_ws(workspace, workspace_bytes, T, &cnt, &toff, &sws, &sb));
-    const unsigned grid = (unsigned)((T + 3) / 4);
+    const int64_t nch = T * 16 * A->tile_cols / (16 / dtype_size(A->values_dtype));
+    const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((nch + 255) / 256, 65536));
+    const bool al = (reinterpret_cast<uintptr_t>(A->values) & 15) == 0;
+#define GRWS_TILE_NNZ(VT)                                                                                          \
+    if (al)                                                                                                        \
+        hipLaunchKernelGGL((tile_nnz_kernel<VT, true>), dim3(grid), dim3(256), 0, stream, A->col_indices,          \
+                           A->values, T, A->tile_cols, num_cols, cnt);                                             \
+    else                                                                                                           \
+        hipLaunchKernelGGL((tile_nnz_kernel<VT, false>), dim3(grid), dim3(256), 0, stream, A->col_indices,         \
+                           A->values, T, A->tile_cols, num_cols, cnt)
     switch (A->values_dtype) {
-        case GRWS_F32:
-            hipLaunchKernelGGL(tile_nnz_kernel<float>, dim3(grid), dim3(256), 0, stream, A->col_indices, A->values, T,
-                               A->tile_cols, num_cols, cnt);
-            break;
-        case GRWS_F16:
-            hipLaunchKernelGGL(tile_nnz_kernel<_Float16>, dim3(grid), dim3(256), 0, stream, A->col_indices, A->values,
-                               T, A->tile_cols, num_cols, cnt);
-            break;
-        default:
-            hipLaunchKernelGGL(tile_nnz_kernel<__hip_bfloat16>, dim3(grid), dim3(256), 0, stream, A->col_indices,
-                               A->values, T, A->tile_cols, num_cols, cnt);
-            break;
+        case GRWS_F32: GRWS_TILE_NNZ(float); break;
+        case GRWS_F16: GRWS_TILE_NNZ(_Float16); break;
+        default: GRWS_TILE_NNZ(__hip_bfloat16); break;
     }
+#undef GRWS_TILE_NNZ
     GRWS_LAUNCH_CHECK();
     GRWS_TRY(scan_i32_to_i64(cnt, toff, T, false, sws, sb, stream));
     int64_t nnz = 0;
@@ -1109,24 +1510,28 @@ extern "C" int grws_bcsr_to_coo_fill(const grws_bcsr* A, int64_t num_cols, int32
     char* sws;
     size_t sb;
     GRWS_TRY(coo_ws(workspace, workspace_bytes, T, &cnt, &toff, &sws, &sb));
-    const unsigned grid = (unsigned)((T + 3) / 4);
+    // the count's per-tile counts are spent (toff holds their scan): the
+    // array takes each tile's window
+    GRWS_TRY(fill_i32(cnt, T, 0, stream));
+    hipLaunchKernelGGL(tile_window_kernel, dim3((unsigned)std::max<int64_t>(1, std::min<int64_t>(A->num_windows, 8192))),
+                       dim3(256), 0, stream, A->window_offset, A->num_windows, T, cnt);
+    GRWS_LAUNCH_CHECK();
+    const int64_t nch = T * 16 * A->tile_cols / (16 / dtype_size(A->values_dtype));
+    const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((nch + 255) / 256, 65536));
+    const bool al = (reinterpret_cast<uintptr_t>(A->values) & 15) == 0;
+#define GRWS_TILE_COO(VT)                                                                                          \
+    if (al)                                                                                                        \
+        hipLaunchKernelGGL((tile_to_coo_kernel<VT, true>), dim3(grid), dim3(256), 0, stream, cnt, A->col_indices,  \
+                           A->values, T, A->tile_cols, num_cols, toff, rows, cols, values);                        \
+    else                                                                                                           \
+        hipLaunchKernelGGL((tile_to_coo_kernel<VT, false>), dim3(grid), dim3(256), 0, stream, cnt, A->col_indices, \
+                           A->values, T, A->tile_cols, num_cols, toff, rows, cols, values)
     switch (A->values_dtype) {
-        case GRWS_F32:
-            hipLaunchKernelGGL(tile_to_coo_kernel<float>, dim3(grid), dim3(256), 0, stream, A->window_offset,
-                               A->num_windows, A->col_indices, A->values, T, A->tile_cols, num_cols, toff, rows, cols,
-                               values);
-            break;
-        case GRWS_F16:
-            hipLaunchKernelGGL(tile_to_coo_kernel<_Float16>, dim3(grid), dim3(256), 0, stream, A->window_offset,
-                               A->num_windows, A->col_indices, A->values, T, A->tile_cols, num_cols, toff, rows, cols,
-                               values);
-            break;
-        default:
-            hipLaunchKernelGGL(tile_to_coo_kernel<__hip_bfloat16>, dim3(grid), dim3(256), 0, stream, A->window_offset,
-                               A->num_windows, A->col_indices, A->values, T, A->tile_cols, num_cols, toff, rows, cols,
-                               values);
-            break;
+        case GRWS_F32: GRWS_TILE_COO(float); break;
+        case GRWS_F16: GRWS_TILE_COO(_Float16); break;
+        default: GRWS_TILE_COO(__hip_bfloat16); break;
     }
+#undef GRWS_TILE_COO
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }

@@ -88,8 +88,9 @@ def _window_case_csr(hub: bool, seed: int):
     columns: window 0 holds 8,000 edges over 3,000 columns (many duplicate
     (row, column) edges), window 1 holds 11,200 edges over all the columns
     (span above 2^18), window 2 one column only, window 3 none, window 4 a
-    few short rows; rows are unsorted.  hub adds 20,000 edges to row 40
-    (a window above 16,384 edges)."""
+    few short rows; rows are unsorted.  hub adds 20,000 edges to row 40 and
+    3,000 over 100 columns to row 41 (a window above 16,384 edges, with
+    duplicates)."""
     rng = np.random.default_rng(seed)
     n_r, n_c = 75, (1 << 20) + 5
     per_row = []
@@ -106,6 +107,8 @@ def _window_case_csr(hub: bool, seed: int):
             c = rng.integers(0, n_c, int(rng.integers(0, 40)))
         if hub and r == 40:
             c = rng.integers(0, n_c, 20000)
+        if hub and r == 41:  # many duplicate (row, column) edges in the same large window
+            c = rng.integers(0, 100, 3000)
         per_row.append(c.astype(np.int32))
     rp = np.zeros(n_r + 1, np.int64)
     rp[1:] = np.cumsum([len(c) for c in per_row])
@@ -117,9 +120,10 @@ def _window_case_csr(hub: bool, seed: int):
 @pytest.mark.parametrize("hub", [False, True])
 @pytest.mark.parametrize("tc", [8, 16])
 def test_csr_build_window_paths(cuda_device, hub, tc):
-    """CSR input through each case of the window-by-window build (and, with
-    a window above 16,384 edges, the global sort): equal to the oracle's
-    converter, duplicates last-wins, bit-exact f32 values."""
+    """CSR input through each case of the window-by-window build (hub: a
+    window above 16,384 edges, sorted in global scratch by one work-group):
+    equal to the oracle's converter, duplicates last-wins, bit-exact f32
+    values."""
     print(f"case window paths hub={hub} tc={tc}", flush=True)
     n_r, n_c, rp, cols, vals = _window_case_csr(hub, seed=21 + tc)
     ow, oc, ov = oracle.csr_to_bcsr(n_r, rp, cols, vals, 16, tc)
@@ -147,14 +151,15 @@ def _oracle_transposed(n_r, n_c, rp, cols, vals, tc):
 @pytest.mark.parametrize("tc", [8, 16])
 def test_transposed_csr_build_window_paths(cuda_device, hub, tc):
     """Transposed builds from a CSR: windows of A^T grouped by a sort over
-    the window bits, then built window by window; with a column of 17,000
-    in-edges (a window above 16,384 edges) the global sort instead.  Equal
-    to the oracle's converter over A^T, duplicates in input order."""
+    the window bits, then built window by window; hub: a column of 17,000
+    in-edges (a window above 16,384 edges), a tenth of them duplicated.
+    Equal to the oracle's converter over A^T, duplicates in input order."""
     print(f"case transposed window paths hub={hub} tc={tc}", flush=True)
     n_r, n_c, rp, cols, vals = _window_case_csr(False, seed=40 + tc)
-    if hub:  # 17,000 more rows, each with an edge to column 3 and one random edge
+    if hub:  # 17,000 more rows, each with an edge to column 3 and one random edge (a tenth: column 3 again)
         rng = np.random.default_rng(3)
-        extra = np.stack([np.full(17000, 3), rng.integers(0, n_c, 17000)], 1).reshape(-1).astype(np.int32)
+        other = np.where(rng.random(17000) < 0.1, 3, rng.integers(0, n_c, 17000))
+        extra = np.stack([np.full(17000, 3), other], 1).reshape(-1).astype(np.int32)
         cols = np.concatenate([cols, extra])
         vals = np.concatenate([vals, rng.standard_normal(extra.size).astype(np.float32)])
         rp = np.concatenate([rp, rp[-1] + 2 * np.arange(1, 17001, dtype=np.int64)])
@@ -281,6 +286,43 @@ def test_coo_to_csr_matches_stable_sort(cuda_device, n_r, n_c, m):
     np.testing.assert_array_equal(va.cpu().numpy(), w[order])
 
 
+def _coo_of_bcsr(win, cols, vals, tc, num_cols):
+    """COO of BCSR arrays in the order grws_bcsr_to_coo emits: tile by tile,
+    each tile's slots in (row, column) order, keeping slots whose column is
+    in [0, num_cols) and whose value is nonzero."""
+    T = cols.size // tc
+    tile_win = np.repeat(np.arange(win.size - 1), np.diff(win))
+    s = np.arange(16 * tc)
+    row = (16 * tile_win[:, None] + s[None, :] // tc).reshape(-1)
+    col = cols.reshape(T, tc)[:, s % tc].reshape(-1)
+    val = vals.reshape(-1).astype(np.float32)
+    keep = (col >= 0) & (col < num_cols) & (val != 0)
+    return row[keep], col[keep], val[keep]
+
+
+@pytest.mark.parametrize("tc", [8, 16])
+@pytest.mark.parametrize("vdt", [torch.float32, torch.float16])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_bcsr_to_coo_matches_slot_order(cuda_device, tc, vdt, offset):
+    """BCSR -> COO on the device: every valid nonzero slot, in tile and slot
+    order; values one element past a 16-byte boundary (offset 1) take the
+    value-by-value loads."""
+    print(f"case bcsr_to_coo tc={tc} {vdt} offset={offset}", flush=True)
+    g = synth.chung_lu(3000, 50000, 2.1, seed=12)
+    hw, hc, hv = _host(g, tc)
+    hv = hv.to(vdt)
+    hv.view(-1)[::7] = 0  # explicit zeros are dropped
+    buf = torch.empty(hv.numel() + offset, dtype=vdt, device=cuda_device)
+    dv = buf[offset:]
+    dv.copy_(hv.view(-1).to(cuda_device))
+    r, c, v = builder.bcsr_to_coo(hw.to(cuda_device), hc.to(cuda_device), dv, tc, g.num_nodes - 5)
+    torch.cuda.synchronize()
+    er, ec, ev = _coo_of_bcsr(hw.numpy(), hc.numpy(), hv.float().numpy(), tc, g.num_nodes - 5)
+    np.testing.assert_array_equal(r.cpu().numpy(), er)
+    np.testing.assert_array_equal(c.cpu().numpy(), ec)
+    np.testing.assert_array_equal(v.cpu().numpy(), ev)
+
+
 @pytest.mark.parametrize("tc", [8, 16])
 def test_transpose_matches_host_build_of_transpose(cuda_device, tc):
     """BCSR(A^T) built from BCSR(A) on the device equals the host converter
@@ -350,6 +392,34 @@ def test_reindex_matches_oracle(cuda_device, vdt):
         assert dv._version > v0, "the in-place prune must bump the version caches key on"
         np.testing.assert_array_equal(out.cpu().numpy(), oc)
         np.testing.assert_array_equal(dv.float().cpu().numpy(), ov)
+
+
+@pytest.mark.parametrize("cfg", ["c3", "c4"])
+def test_build_full_size_forward_and_transposed(cuda_device, cfg):
+    """BASELINE configs c3 (windows of up to 8,246 edges) and c4 (667
+    windows above 16,384 edges, built each by one work-group from global
+    scratch) at full size: the device build equals the host converter, and
+    the transposed build equals the device build of A^T's CSR (made by a
+    stable sort of the edges by column)."""
+    print(f"case {cfg} full-size build", flush=True)
+    g = synth.config_graph(cfg, device=cuda_device)
+    n = g.num_nodes
+    hw, hc, hv = core.csr_to_bcsr_cpu(n, g.row_ptr.cpu(), g.col_idx.cpu(), g.values.cpu(), 16, 16)
+    dw, dc, dv = builder.csr_to_bcsr_device(n, n, g.row_ptr, g.col_idx, g.values, tile_cols=16)
+    _eq(dw, hw)
+    _eq(dc, hc)
+    _eq(dv, hv)
+    del hw, hc, hv, dw, dc, dv
+    tw, tc_, tv = builder.csr_to_bcsr_device(n, n, g.row_ptr, g.col_idx, g.values, tile_cols=16, transpose=True)
+    rows = torch.repeat_interleave(torch.arange(n, device=cuda_device, dtype=torch.int32),
+                                   torch.diff(g.row_ptr))
+    _, order = torch.sort(g.col_idx, stable=True)
+    trp = torch.zeros(n + 1, dtype=torch.int64, device=cuda_device)
+    trp[1:] = torch.cumsum(torch.bincount(g.col_idx, minlength=n), 0)
+    ew, ec, ev = builder.csr_to_bcsr_device(n, n, trp, rows[order], g.values[order], tile_cols=16)
+    _eq(tw, ew)
+    _eq(tc_, ec)
+    _eq(tv, ev)
 
 
 def test_build_c2_full_size(cuda_device):
