@@ -72,11 +72,11 @@ def bench_build(g, dev, cpu: bool, reps: int = 5) -> dict:
     values, and the build of its transpose (the backward's operand).  Wall
     time per build (each build synchronises to size its outputs), median of
     `reps`.  Bytes the algorithm moves: the CSR read; window by window, the
-    sorted keys and values written and read back (24 B per edge); with the
-    global sort, per radix pass the keys read by the histogram (8 B) and keys
-    + payload read and written by the scatter (24 B) per edge and the
-    flags/scans over the sorted edges (~16 B per edge); the BCSR written
-    once."""
+    per-edge records and distinct columns written and read back (24 B per
+    edge); with the global sort, per radix pass the keys read by the
+    histogram (8 B) and keys + payload read and written by the scatter (24 B)
+    per edge and the flags/scans over the sorted edges (~16 B per edge); the
+    BCSR written once."""
     from graph_rws_amd import builder
     n, nnz = g.num_nodes, g.nnz
 
@@ -95,15 +95,16 @@ def bench_build(g, dev, cpu: bool, reps: int = 5) -> dict:
     t_fwd, (win, cols, vals) = timed(lambda: builder.csr_to_bcsr_device(
         n, n, g.row_ptr, g.col_idx, g.values, tile_cols=16, values_dtype=torch.float16))
     W, T = win.numel() - 1, cols.numel() // 16
-    # the path the library takes (csrc/bcsr_build.hip): window by window from
-    # LDS when every 16-row window holds at most 16,384 edges, else one global
-    # radix sort over (window, column, row) keys
+    # the path the library takes (csrc/bcsr_build.hip): window by window (in
+    # LDS up to 16,384 edges a window, larger windows by one work-group from
+    # global scratch) unless a window holds more than 2^27 edges, then one
+    # global radix sort over (window, column, row) keys
     idx = torch.clamp(torch.arange(0, n + 16, 16, device=g.row_ptr.device), max=n)
-    per_window = int(torch.diff(g.row_ptr[idx]).max()) <= 16384
+    per_window = int(torch.diff(g.row_ptr[idx]).max()) <= (1 << 27)
     out_bytes = 8 * (W + 1) + 4 * T * 16 + 2 * T * 256
     if per_window:
-        # row pointers, columns and values read; sorted keys (8 B) and values
-        # (4 B) written and read back by the fill
+        # row pointers, columns and values read; one 8-byte record per edge
+        # and the distinct columns (4 B) written and read back by the fill
         passes = 0
         b_alg = 8 * (n + 1) + 8 * nnz + 24 * nnz + out_bytes
     else:
@@ -114,12 +115,15 @@ def bench_build(g, dev, cpu: bool, reps: int = 5) -> dict:
     gbs = b_alg / t_fwd / 1e9
     r = {"workload": f"device BCSR build of the {nnz:,}-edge headline graph: CSR -> 16x16 BCSR, f16 values",
          "ms": round(1e3 * t_fwd, 3), "edges_per_s": round(nnz / t_fwd, 1),
-         "path": "window by window in LDS" if per_window else "global radix sort", "radix_passes": passes,
+         "path": "window by window" if per_window else "global radix sort", "radix_passes": passes,
          "transpose_ms": round(1e3 * t_tr, 3),
+         "transpose_how": "BCSR(A) -> COO -> BCSR(A^T): the COO grouped by window (radix sort over the window "
+                          "bits), then built window by window",
          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                       "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": int(b_alg),
-                      "note": "algorithmic bytes of this build (sort passes included), wall time with "
-                              "its one sync"}}
+                      "note": "algorithmic bytes of the path taken: the CSR read, the BCSR written once, and "
+                              "the workspace round trip (window by window: 24 B per edge; global sort: "
+                              "32 B per edge per radix pass + 16); wall time including the build's syncs"}}
     if cpu:
         import oracle
         rows = n

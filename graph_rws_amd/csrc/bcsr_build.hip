@@ -595,9 +595,11 @@ __global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192
                 } else {
                     c = colv[j];
                     q = row_of(j);
+                    // the next edge of the same column comes later in CSR
+                    // order (stable sort): the same row while before its end
                     if (i + 1 < m) {
                         const int jn = src[i + 1];
-                        last = colv[jn] != c || row_of(jn) != q;
+                        last = colv[jn] != c || e0 + jn >= rp[q + 1];
                     }
                 }
                 const int pl = dst[i];
@@ -808,9 +810,9 @@ __global__ __launch_bounds__(kWinBlk) void win_sort_big_kernel(
             } else {
                 c = (int)kj + cmin;
                 q = row_of(j);
-                if (i + 1 < m) {
+                if (i + 1 < m) {  // as in win_sort_kernel
                     const uint32_t jn = src[i + 1];
-                    last = skey(jn) != kj || row_of(jn) != q;
+                    last = skey(jn) != kj || e0 + jn >= rp[q + 1];
                 }
             }
             const int pl = (int)pbuf[e0 + i];

@@ -321,7 +321,8 @@ int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_cols, int32_
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* BCSR -> COO: every slot with a column in [0, num_cols) and a non-zero
- * value becomes one edge (row = 16*window + row in tile).  Feeds the
+ * value becomes one edge (row = 16*window + row in tile), tile by tile and
+ * each tile's slots in (row, column) order.  Feeds the
  * transposed build of a graph that exists only as BCSR (sampled subgraphs,
  * from_components).  count synchronises `stream`. */
 size_t grws_bcsr_to_coo_workspace_bytes(int64_t num_tiles);
