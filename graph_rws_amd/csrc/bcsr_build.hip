@@ -618,6 +618,7 @@ __global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192
 // read from the input where it is used.  KEYED with kcopy: the sorted keys and
 // values are where the records and distinct columns go (ka / va), so the
 // window's share is copied to kcopy / vcopy first.
+constexpr int kBig = 8;  // rounds of 64 edges whose loads are issued together
 template <bool KEYED>
 __global__ __launch_bounds__(kWinBlk) void win_sort_big_kernel(
     const int64_t* __restrict__ row_ptr, const int32_t* __restrict__ cols, const float* __restrict__ vals,
@@ -723,8 +724,20 @@ __global__ __launch_bounds__(kWinBlk) void win_sort_big_kernel(
         for (int sh = 0; sh < bits; sh += kWinDig) {  // uniform
             for (int i = tid; i < NW * kWinBkt; i += kWinBlk) cnt[i] = 0;
             __syncthreads();
-            for (int i = lo + lane; i < hi; i += kWave)
-                atomicAdd(&cnt[wv * kWinBkt + ((skey(src[i]) >> sh) & (kWinBkt - 1))], 1u);
+            // kBig rounds of 64 at a time: their loads in flight together
+            for (int b = lo; b < hi; b += kBig * kWave) {  // uniform over the wave
+                uint32_t x[kBig];
+#pragma unroll
+                for (int r = 0; r < kBig; ++r) {
+                    const int i = b + r * kWave + lane;
+                    x[r] = i < hi ? src[i] : 0u;
+                }
+#pragma unroll
+                for (int r = 0; r < kBig; ++r) {
+                    const int i = b + r * kWave + lane;
+                    if (i < hi) atomicAdd(&cnt[wv * kWinBkt + ((skey(x[r]) >> sh) & (kWinBkt - 1))], 1u);
+                }
+            }
             __syncthreads();
             {  // exclusive offsets in (digit, wave) order; this thread's digit is tid
                 int pos[NW];
@@ -743,26 +756,35 @@ __global__ __launch_bounds__(kWinBlk) void win_sort_big_kernel(
                 }
             }
             __syncthreads();
-            for (int b = lo; b < hi; b += kWave) {  // uniform over the wave
-                const int i = b + lane;
-                const bool v = i < hi;
-                uint32_t x = 0;
-                int d = 0;
-                if (v) {
-                    x = src[i];
-                    d = (int)((skey(x) >> sh) & (kWinBkt - 1));
-                }
-                uint64_t peers = __ballot(v);
+            for (int b0 = lo; b0 < hi; b0 += kBig * kWave) {  // uniform over the wave
+                uint32_t x[kBig];
+                int d[kBig];
 #pragma unroll
-                for (int k = 0; k < kWinDig; ++k) {
-                    const bool bit = (d >> k) & 1;
-                    const uint64_t bb = __ballot(bit);
-                    peers &= bit ? bb : ~bb;
+                for (int r = 0; r < kBig; ++r) {
+                    const int i = b0 + r * kWave + lane;
+                    x[r] = i < hi ? src[i] : 0u;
                 }
-                if (v) {
-                    const uint32_t base = cnt[wv * kWinBkt + d];
-                    dst[base + __popcll(peers & ((1ull << lane) - 1))] = x;
-                    if ((peers >> lane) == 1ull) cnt[wv * kWinBkt + d] = base + (uint32_t)__popcll(peers);
+#pragma unroll
+                for (int r = 0; r < kBig; ++r) {
+                    const int i = b0 + r * kWave + lane;
+                    d[r] = i < hi ? (int)((skey(x[r]) >> sh) & (kWinBkt - 1)) : 0;
+                }
+#pragma unroll
+                for (int r = 0; r < kBig; ++r) {  // the rounds in order
+                    const int i = b0 + r * kWave + lane;
+                    const bool v = i < hi;
+                    uint64_t peers = __ballot(v);
+#pragma unroll
+                    for (int k = 0; k < kWinDig; ++k) {
+                        const bool bit = (d[r] >> k) & 1;
+                        const uint64_t bb = __ballot(bit);
+                        peers &= bit ? bb : ~bb;
+                    }
+                    if (v) {
+                        const uint32_t base = cnt[wv * kWinBkt + d[r]];
+                        dst[base + __popcll(peers & ((1ull << lane) - 1))] = x[r];
+                        if ((peers >> lane) == 1ull) cnt[wv * kWinBkt + d[r]] = base + (uint32_t)__popcll(peers);
+                    }
                 }
             }
             __syncthreads();
@@ -775,6 +797,7 @@ __global__ __launch_bounds__(kWinBlk) void win_sort_big_kernel(
             const int a0 = min(tid * run, m), a1 = min(a0 + run, m);
             int f = 0;
             uint32_t prev = a0 > 0 ? colkey(src[a0 - 1]) : 0u;
+#pragma unroll 8
             for (int i = a0; i < a1; ++i) {
                 const uint32_t ck = colkey(src[i]);
                 f += (i == 0 || ck != prev) ? 1 : 0;
@@ -783,6 +806,7 @@ __global__ __launch_bounds__(kWinBlk) void win_sort_big_kernel(
             int64_t tot;
             int pl = (int)block_incl_scan<kWinBlk>(f, tmp, &tot) - f;
             prev = a0 > 0 ? colkey(src[a0 - 1]) : 0u;
+#pragma unroll 8
             for (int i = a0; i < a1; ++i) {
                 const uint32_t ck = colkey(src[i]);
                 pl += (i == 0 || ck != prev) ? 1 : 0;
@@ -798,6 +822,7 @@ __global__ __launch_bounds__(kWinBlk) void win_sort_big_kernel(
             }
         }
         __syncthreads();
+#pragma unroll 4
         for (int i = tid; i < m; i += kWinBlk) {
             const uint32_t j = src[i];
             const uint32_t kj = skey(j);

@@ -119,21 +119,23 @@ def _window_case_csr(hub: bool, seed: int):
 
 @pytest.mark.parametrize("hub", [False, True])
 @pytest.mark.parametrize("tc", [8, 16])
-def test_csr_build_window_paths(cuda_device, hub, tc):
+@pytest.mark.parametrize("vdt", [torch.float32, torch.float16, torch.bfloat16])
+def test_csr_build_window_paths(cuda_device, hub, tc, vdt):
     """CSR input through each case of the window-by-window build (hub: a
     window above 16,384 edges, sorted in global scratch by one work-group):
-    equal to the oracle's converter, duplicates last-wins, bit-exact f32
-    values."""
-    print(f"case window paths hub={hub} tc={tc}", flush=True)
+    equal to the oracle's converter, duplicates last-wins, values bit-exact
+    (f32) or its round-to-nearest-even cast (f16, bf16)."""
+    print(f"case window paths hub={hub} tc={tc} {vdt}", flush=True)
     n_r, n_c, rp, cols, vals = _window_case_csr(hub, seed=21 + tc)
     ow, oc, ov = oracle.csr_to_bcsr(n_r, rp, cols, vals, 16, tc)
     dw, dc, dv = builder.csr_to_bcsr_device(n_r, n_c, torch.from_numpy(rp).to(cuda_device),
                                             torch.from_numpy(cols).to(cuda_device),
-                                            torch.from_numpy(vals).to(cuda_device), tile_cols=tc)
+                                            torch.from_numpy(vals).to(cuda_device), tile_cols=tc,
+                                            values_dtype=vdt)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(dw.cpu().numpy(), ow)
     np.testing.assert_array_equal(dc.cpu().numpy(), oc)
-    np.testing.assert_array_equal(dv.cpu().numpy(), ov.astype(np.float32))
+    _eq(dv, torch.from_numpy(ov.astype(np.float32)).to(vdt))
 
 
 def _oracle_transposed(n_r, n_c, rp, cols, vals, tc):
@@ -149,12 +151,13 @@ def _oracle_transposed(n_r, n_c, rp, cols, vals, tc):
 
 @pytest.mark.parametrize("hub", [False, True])
 @pytest.mark.parametrize("tc", [8, 16])
-def test_transposed_csr_build_window_paths(cuda_device, hub, tc):
+@pytest.mark.parametrize("vdt", [torch.float32, torch.bfloat16])
+def test_transposed_csr_build_window_paths(cuda_device, hub, tc, vdt):
     """Transposed builds from a CSR: windows of A^T grouped by a sort over
     the window bits, then built window by window; hub: a column of 17,000
     in-edges (a window above 16,384 edges), a tenth of them duplicated.
     Equal to the oracle's converter over A^T, duplicates in input order."""
-    print(f"case transposed window paths hub={hub} tc={tc}", flush=True)
+    print(f"case transposed window paths hub={hub} tc={tc} {vdt}", flush=True)
     n_r, n_c, rp, cols, vals = _window_case_csr(False, seed=40 + tc)
     if hub:  # 17,000 more rows, each with an edge to column 3 and one random edge (a tenth: column 3 again)
         rng = np.random.default_rng(3)
@@ -167,11 +170,12 @@ def test_transposed_csr_build_window_paths(cuda_device, hub, tc):
     ow, oc, ov = _oracle_transposed(n_r, n_c, rp, cols, vals, tc)
     dw, dc, dv = builder.csr_to_bcsr_device(n_r, n_c, torch.from_numpy(rp).to(cuda_device),
                                             torch.from_numpy(cols).to(cuda_device),
-                                            torch.from_numpy(vals).to(cuda_device), tile_cols=tc, transpose=True)
+                                            torch.from_numpy(vals).to(cuda_device), tile_cols=tc, transpose=True,
+                                            values_dtype=vdt)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(dw.cpu().numpy(), ow)
     np.testing.assert_array_equal(dc.cpu().numpy(), oc)
-    np.testing.assert_array_equal(dv.cpu().numpy(), ov.astype(np.float32))
+    _eq(dv, torch.from_numpy(ov.astype(np.float32)).to(vdt))
 
 
 def test_coo_build_wide_columns_global_sort(cuda_device):
