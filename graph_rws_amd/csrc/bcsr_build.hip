@@ -347,6 +347,7 @@ __global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192
     __shared__ int64_t rp[17];
     __shared__ int64_t tmp[NW + 1];
     __shared__ int32_t mm[2 * NW];            // per-wave column range
+    __shared__ int32_t wcnt[NW];              // per-wave distinct columns
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
     for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {  // uniform over the work-group
         int nr = 16;
@@ -527,9 +528,6 @@ __global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192
             src = dst;
             dst = t;
         }
-        // each distinct column's place among the window's distinct columns:
-        // first-of-column flags counted over contiguous runs of sorted
-        // positions, one block scan, places into the free offset buffer
         // (KEYED: the column is colv >> 4, the row colv & 15)
         auto first_of_col = [&](int i) {
             return i == 0 || (KEYED ? (colv[src[i - 1]] >> 4) != (colv[src[i]] >> 4) : colv[src[i - 1]] != colv[src[i]]);
@@ -542,26 +540,33 @@ __global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192
                 if (q + st < nr && rp[q + st] <= e) q += st;
             return q;
         };
+        // each distinct column's place among the window's distinct columns:
+        // every wave walks its sorted positions [lo, hi) in rounds of 64
+        // consecutive ones (the sort's ownership), counts first-of-column
+        // flags by ballot, and one barrier gives the waves' offsets
+        int wbase = 0;
         {
-            const int run = (m + BLK - 1) / BLK;
-            const int a0 = min(tid * run, m), a1 = min(a0 + run, m);
-            int f = 0;
-            for (int i = a0; i < a1; ++i) f += first_of_col(i) ? 1 : 0;
-            int64_t tot;
-            int pl = (int)block_incl_scan<BLK>(f, tmp, &tot) - f;
-            for (int i = a0; i < a1; ++i) {
-                pl += first_of_col(i) ? 1 : 0;
-                dst[i] = (uint16_t)(pl - 1);
+            int wcount = 0;
+            for (int b = lo; b < hi; b += kWave) {  // uniform over the wave
+                const int i = b + lane;
+                wcount += __popcll(__ballot(i < hi && first_of_col(i)));
+            }
+            if (lane == 0) wcnt[wv] = wcount;
+            __syncthreads();
+            int tot = 0;
+            for (int v = 0; v < NW; ++v) {
+                const int c = wcnt[v];
+                wbase += v < wv ? c : 0;
+                tot += c;
             }
             if (tid == 0) {
-                wtiles[w] = ((int)tot + tc - 1) / tc;
+                wtiles[w] = (tot + tc - 1) / tc;
                 if (!KEYED) {
                     wstart[w] = e0;
                     wend[w] = e0 + m;
                 }
             }
         }
-        __syncthreads();
         // one record per edge in sorted order (value bits, place, row, last of
         // its (column, row) run), the distinct columns at their places; the
         // value gathers issued first
@@ -569,42 +574,48 @@ __global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192
         uint32_t vv[PER];
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int i = tid + k * BLK;
-            jj[k] = i < m ? src[i] : 0;
+            const int i = lo + k * kWave + lane;
+            jj[k] = i < hi ? src[i] : 0;
         }
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int i = tid + k * BLK;
-            if (KEYED) vv[k] = i < m ? tvals[e0 + jj[k]] : 0u;
-            else vv[k] = (vals && i < m) ? __float_as_uint(vals[e0 + jj[k]]) : 0x3f800000u;
+            const int i = lo + k * kWave + lane;
+            if (KEYED) vv[k] = i < hi ? tvals[e0 + jj[k]] : 0u;
+            else vv[k] = (vals && i < hi) ? __float_as_uint(vals[e0 + jj[k]]) : 0x3f800000u;
         }
         // KEYED: the records and columns may overwrite tkeys / tvals of this
         // window (the same workspace): every value read first
         if (KEYED) __syncthreads();
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int i = tid + k * BLK;
-            if (i < m) {
-                const int j = jj[k];
-                int c, q;
-                bool last = true;
-                if (KEYED) {
-                    c = (colv[j] >> 4) + cmin;
-                    q = colv[j] & 15;
-                    if (i + 1 < m) last = colv[src[i + 1]] != colv[j];
-                } else {
-                    c = colv[j];
-                    q = row_of(j);
-                    // the next edge of the same column comes later in CSR
-                    // order (stable sort): the same row while before its end
-                    if (i + 1 < m) {
-                        const int jn = src[i + 1];
-                        last = colv[jn] != c || e0 + jn >= rp[q + 1];
+            const int i = lo + k * kWave + lane;
+            if (lo + k * kWave < hi) {  // uniform over the wave
+                const bool in = i < hi;
+                const bool f = in && first_of_col(i);
+                const uint64_t fm = __ballot(f);
+                const int pl = wbase + __popcll(fm & ((2ull << lane) - 1)) - 1;  // flags up to this lane
+                wbase += __popcll(fm);
+                if (in) {
+                    const int j = jj[k];
+                    int c, q;
+                    bool last = true;
+                    if (KEYED) {
+                        c = (colv[j] >> 4) + cmin;
+                        q = colv[j] & 15;
+                        if (i + 1 < m) last = colv[src[i + 1]] != colv[j];
+                    } else {
+                        c = colv[j];
+                        q = row_of(j);
+                        // the next edge of the same column comes later in CSR
+                        // order (stable sort): the same row while before its end
+                        if (i + 1 < m) {
+                            const int jn = src[i + 1];
+                            last = colv[jn] != c || e0 + jn >= rp[q + 1];
+                        }
                     }
+                    if (f) ucol[e0 + pl] = c;
+                    skeys[e0 + i] = win_record(vv[k], pl, q, last);
                 }
-                const int pl = dst[i];
-                if (i == 0 || dst[i - 1] != pl) ucol[e0 + pl] = c;
-                skeys[e0 + i] = win_record(vv[k], pl, q, last);
             }
         }
         __syncthreads();  // LDS is rewritten for the next window
