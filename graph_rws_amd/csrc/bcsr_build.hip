@@ -250,7 +250,7 @@ __global__ void build_scatter_kernel(const uint64_t* __restrict__ keys, const ui
                                      int tc, int32_t* __restrict__ out_cols, void* __restrict__ out_vals,
                                      const int32_t* __restrict__ err) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n || err[2] == 1) return;  // err[2] == 1: the per-window build ran
+    if (i >= n || err[2] != 0) return;  // err[2] != 0: the per-window build ran
     const uint64_t k = keys[i];
     const int wshift = cbits + 4;
     const int64_t w = (int64_t)(k >> wshift);
@@ -287,6 +287,17 @@ __device__ __forceinline__ int rec_place(uint64_t r) { return (int)((r >> 32) & 
 __device__ __forceinline__ int rec_row(uint64_t r) { return (int)((r >> 59) & 15u); }
 __device__ __forceinline__ bool rec_last(uint64_t r) { return (r >> 63) & 1u; }
 
+// record of a window of at most kWinCap edges (in any order): value bits |
+// place << 32 (14 bits) | row << 46 (4 bits) | edge offset in the window <<
+// 50 (14 bits); of duplicate (row, column) edges the fill keeps the largest
+// offset, the last in input order.
+__device__ __forceinline__ uint64_t srec(uint32_t vbits, int place, int row, int j) {
+    return (uint64_t)vbits | ((uint64_t)place << 32) | ((uint64_t)row << 46) | ((uint64_t)j << 50);
+}
+__device__ __forceinline__ int srec_place(uint64_t r) { return (int)((r >> 32) & 16383u); }
+__device__ __forceinline__ int srec_row(uint64_t r) { return (int)((r >> 46) & 15u); }
+__device__ __forceinline__ int srec_j(uint64_t r) { return (int)(r >> 50); }
+
 constexpr int kWinCap = 16384;  // windows of up to 8,192 edges use a half-size LDS twin
 constexpr int kWinBlk = 512;
 constexpr int kWinDig = 9;                 // radix digit bits
@@ -318,12 +329,20 @@ __global__ void keyed_big_kernel(const int64_t* __restrict__ wstart, const int64
     note_window_size(w, wend[w] - wstart[w], blist, err);
 }
 
-// KEYED false: the window's edges straight from a CSR (row_ptr, cols, vals),
-// sorted by column (they arrive in row order).  KEYED true: from
-// window-major sorted keys (edge_key with wbits > 0) and their value bits
-// (tkeys, tvals, bounds in wstart / wend), which arrive in input order and
-// are sorted by (column, row): the LDS key is (column - min) << 4 | row,
-// which needs column spans under 2^27 (the host checks).
+// KEYED false: the window's edges straight from a CSR (row_ptr, cols, vals).
+// KEYED true: from window-major sorted keys (edge_key with wbits > 0) and
+// their value bits (tkeys, tvals, bounds in wstart / wend); the LDS key is
+// (column - min) << 4 | row, which needs column spans under 2^27 (the host
+// checks).  The records (skeys) and distinct columns (ucol) never share
+// memory with the input.
+//
+// Places: a bitmap of the window's columns over its span when the span fits
+// the offsets' LDS (2 bits an edge slot; c3: every window), its popcounts
+// giving each column's place, the records in input order; else a stable LSD
+// radix sort of the edge offsets by the LDS key (9-bit digits, 8 with 256
+// threads) and first-of-column flags counted per wave, the records in sorted
+// order.  Either way the fill keeps, of duplicate (row, column) edges, the
+// largest offset, i.e. the last in input order.
 template <int CAP, int BLK, bool KEYED>
 __global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192 ? 4 : (CAP == 16384 ? 2 : 1)))) void win_sort_kernel(
     const int64_t* __restrict__ row_ptr, const int32_t* __restrict__ cols, const float* __restrict__ vals,
@@ -340,9 +359,12 @@ __global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192
     constexpr int DIG = BLK == 256 ? 8 : 9;   // digit bits: one digit per thread in the offset scan
     constexpr int MLO = CAP == 2048 ? -1 : (CAP == 8192 ? 2048 : 8192);  // this launch: MLO < edges <= CAP
     __shared__ int32_t colv[CAP];             // the window's sort keys, by edge offset
-    __shared__ uint16_t ia[CAP], ib[CAP];     // edge offsets: sort source and destination
+    // edge offsets: sort source and destination (radix); or the column bitmap
+    __shared__ __align__(16) uint16_t iab[2 * CAP];
+    uint16_t* const ia = iab;
+    uint16_t* const ib = iab + CAP;
     // [wave][digit] counts, then scatter positions, 16 bits each (at most
-    // CAP), two digits a word
+    // CAP), two digits a word; or the bitmap's popcount bases
     __shared__ uint32_t cnt[NW * BLK / 2];
     __shared__ int64_t rp[17];
     __shared__ int64_t tmp[NW + 1];
@@ -457,81 +479,6 @@ __global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192
             }
             cbase = cmin;
         }
-        const uint32_t span = m > 0 ? (KEYED ? ((uint32_t)(cmax - cmin) << 4) | 15u : (uint32_t)(cmax - cmin)) : 0u;
-        const int bits = span ? 32 - __clz(span) : 0;
-        // wave v sorts positions [lo, hi): whole rounds of 64, in wave order
-        const int chunk = ((m + NW * kWave - 1) / (NW * kWave)) * kWave;
-        const int lo = min(wv * chunk, m), hi = min(lo + chunk, m);
-        uint16_t* src = ia;
-        uint16_t* dst = ib;
-        for (int sh = 0; sh < bits; sh += DIG) {  // uniform
-            for (int i = tid; i < NW * BLK / 2; i += BLK) cnt[i] = 0;
-            __syncthreads();
-            for (int i = lo + lane; i < hi; i += kWave) {
-                const uint32_t d = ((uint32_t)(colv[src[i]] - cbase) >> sh) & (BLK - 1);
-                atomicAdd(&cnt[wv * (BLK / 2) + (d >> 1)], 1u << (16 * (d & 1)));
-            }
-            __syncthreads();
-            {  // exclusive offsets in (digit, wave) order; this thread's digit is tid
-                const int hw = 16 * (tid & 1);
-                int pos[NW];
-                int t = 0;
-#pragma unroll
-                for (int v = 0; v < NW; ++v) {
-                    pos[v] = (int)((cnt[v * (BLK / 2) + (tid >> 1)] >> hw) & 0xffffu);
-                    t += pos[v];
-                }
-                int64_t tot;
-                int run = (int)(block_incl_scan<BLK>(t, tmp, &tot) - t);  // every count read first
-#pragma unroll
-                for (int v = 0; v < NW; ++v) {
-                    const int c = pos[v];
-                    pos[v] = run;
-                    run += c;
-                }
-                // the even digit's thread writes the pair's word
-#pragma unroll
-                for (int v = 0; v < NW; ++v) {
-                    const int odd = __shfl_down(pos[v], 1, kWave);
-                    if (!(tid & 1)) cnt[v * (BLK / 2) + (tid >> 1)] = (uint32_t)pos[v] | ((uint32_t)odd << 16);
-                }
-            }
-            __syncthreads();
-            // stable scatter: each wave walks its positions in order, 64 at a
-            // time; lanes with equal digits take consecutive places in lane
-            // order, and the group's highest lane advances the wave's count
-            for (int b = lo; b < hi; b += kWave) {  // uniform over the wave
-                const int i = b + lane;
-                const bool v = i < hi;
-                uint16_t x = 0;
-                int d = 0;
-                if (v) {
-                    x = src[i];
-                    d = (int)(((uint32_t)(colv[x] - cbase) >> sh) & (BLK - 1));
-                }
-                uint64_t peers = __ballot(v);
-#pragma unroll
-                for (int k = 0; k < DIG; ++k) {
-                    const bool bit = (d >> k) & 1;
-                    const uint64_t bb = __ballot(bit);
-                    peers &= bit ? bb : ~bb;
-                }
-                if (v) {
-                    const int word = wv * (BLK / 2) + (d >> 1), hw = 16 * (d & 1);
-                    const int base = (int)((cnt[word] >> hw) & 0xffffu);
-                    dst[base + __popcll(peers & ((1ull << lane) - 1))] = x;
-                    if ((peers >> lane) == 1ull) atomicAdd(&cnt[word], (uint32_t)__popcll(peers) << hw);
-                }
-            }
-            __syncthreads();
-            uint16_t* t = src;
-            src = dst;
-            dst = t;
-        }
-        // (KEYED: the column is colv >> 4, the row colv & 15)
-        auto first_of_col = [&](int i) {
-            return i == 0 || (KEYED ? (colv[src[i - 1]] >> 4) != (colv[src[i]] >> 4) : colv[src[i - 1]] != colv[src[i]]);
-        };
         auto row_of = [&](int j) {  // CSR: the edge's row in the window, the last q with rp[q] <= e0 + j
             const int64_t e = e0 + j;
             int q = 0;
@@ -540,82 +487,192 @@ __global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192
                 if (q + st < nr && rp[q + st] <= e) q += st;
             return q;
         };
-        // each distinct column's place among the window's distinct columns:
-        // every wave walks its sorted positions [lo, hi) in rounds of 64
-        // consecutive ones (the sort's ownership), counts first-of-column
-        // flags by ballot, and one barrier gives the waves' offsets
-        int wbase = 0;
-        {
-            int wcount = 0;
-            for (int b = lo; b < hi; b += kWave) {  // uniform over the wave
-                const int i = b + lane;
-                wcount += __popcll(__ballot(i < hi && first_of_col(i)));
+        // the edge's column relative to cmin (KEYED: colv >> 4; the row colv & 15)
+        auto rel_col = [&](int j) { return KEYED ? colv[j] >> 4 : colv[j] - cmin; };
+        int u;  // distinct columns
+        // a column bitmap over the span when it fits the offsets' LDS (2 bits
+        // an edge slot): places straight from popcounts, no sort
+        constexpr int kBmWords = CAP;                 // 32-bit words in iab
+        constexpr int G = CAP / (NW * BLK);           // words per popcount base (16-bit bases in cnt)
+        const bool bm = m > 0 && (int64_t)cmax - cmin < (int64_t)kBmWords * 32;  // uniform
+        if (bm) {
+            // value bits of edge offsets tid + k BLK, every load issued first
+            uint32_t vv[PER];
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const int j = tid + k * BLK;
+                if (KEYED) vv[k] = j < m ? tvals[e0 + j] : 0u;
+                else vv[k] = (vals && j < m) ? __float_as_uint(vals[e0 + j]) : 0x3f800000u;
             }
-            if (lane == 0) wcnt[wv] = wcount;
+            uint32_t* bmp = reinterpret_cast<uint32_t*>(iab);
+            uint16_t* wb = reinterpret_cast<uint16_t*>(cnt);
+            const int nwords = (cmax - cmin) / 32 + 1;
+            const int nent = (nwords + G - 1) / G;
+            for (int x = tid; x < nwords; x += BLK) bmp[x] = 0;
             __syncthreads();
-            int tot = 0;
-            for (int v = 0; v < NW; ++v) {
-                const int c = wcnt[v];
-                wbase += v < wv ? c : 0;
-                tot += c;
-            }
-            if (tid == 0) {
-                wtiles[w] = (tot + tc - 1) / tc;
-                if (!KEYED) {
-                    wstart[w] = e0;
-                    wend[w] = e0 + m;
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const int j = tid + k * BLK;
+                if (j < m) {
+                    const int rc = rel_col(j);
+                    atomicOr(&bmp[rc >> 5], 1u << (rc & 31));
                 }
             }
-        }
-        // one record per edge in sorted order (value bits, place, row, last of
-        // its (column, row) run), the distinct columns at their places; the
-        // value gathers issued first
-        int jj[PER];
-        uint32_t vv[PER];
+            __syncthreads();
+            {  // bases: each thread a contiguous run of entries, one block scan
+                const int E = (nent + BLK - 1) / BLK;
+                const int a0 = min(tid * E, nent), a1 = min(a0 + E, nent);
+                int sum = 0;
+                for (int e = a0; e < a1; ++e)
 #pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int i = lo + k * kWave + lane;
-            jj[k] = i < hi ? src[i] : 0;
-        }
+                    for (int g = 0; g < G; ++g)
+                        if (e * G + g < nwords) sum += __popc(bmp[e * G + g]);
+                int64_t tot;
+                int run = (int)(block_incl_scan<BLK>(sum, tmp, &tot) - sum);
+                for (int e = a0; e < a1; ++e) {
+                    wb[e] = (uint16_t)run;
 #pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int i = lo + k * kWave + lane;
-            if (KEYED) vv[k] = i < hi ? tvals[e0 + jj[k]] : 0u;
-            else vv[k] = (vals && i < hi) ? __float_as_uint(vals[e0 + jj[k]]) : 0x3f800000u;
-        }
-        // KEYED: the records and columns may overwrite tkeys / tvals of this
-        // window (the same workspace): every value read first
-        if (KEYED) __syncthreads();
+                    for (int g = 0; g < G; ++g)
+                        if (e * G + g < nwords) run += __popc(bmp[e * G + g]);
+                }
+                u = (int)tot;
+            }
+            __syncthreads();
 #pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int i = lo + k * kWave + lane;
-            if (lo + k * kWave < hi) {  // uniform over the wave
+            for (int k = 0; k < PER; ++k) {
+                const int j = tid + k * BLK;
+                if (j < m) {
+                    const int rc = rel_col(j), wd = rc >> 5;
+                    int pl = wb[wd / G] + __popc(bmp[wd] & ((1u << (rc & 31)) - 1u));
+#pragma unroll
+                    for (int g = 1; g < G; ++g)
+                        if (g <= wd % G) pl += __popc(bmp[wd - g]);
+                    const int q = KEYED ? (colv[j] & 15) : row_of(j);
+                    ucol[e0 + pl] = rc + cmin;  // every edge of the column writes the same id
+                    skeys[e0 + j] = srec(vv[k], pl, q, j);
+                }
+            }
+        } else {
+            const uint32_t span = m > 0 ? (KEYED ? ((uint32_t)(cmax - cmin) << 4) | 15u : (uint32_t)(cmax - cmin)) : 0u;
+            const int bits = span ? 32 - __clz(span) : 0;
+            // wave v sorts positions [lo, hi): whole rounds of 64, in wave order
+            const int chunk = ((m + NW * kWave - 1) / (NW * kWave)) * kWave;
+            const int lo = min(wv * chunk, m), hi = min(lo + chunk, m);
+            uint16_t* src = ia;
+            uint16_t* dst = ib;
+            for (int sh = 0; sh < bits; sh += DIG) {  // uniform
+                for (int i = tid; i < NW * BLK / 2; i += BLK) cnt[i] = 0;
+                __syncthreads();
+                for (int i = lo + lane; i < hi; i += kWave) {
+                    const uint32_t d = ((uint32_t)(colv[src[i]] - cbase) >> sh) & (BLK - 1);
+                    atomicAdd(&cnt[wv * (BLK / 2) + (d >> 1)], 1u << (16 * (d & 1)));
+                }
+                __syncthreads();
+                {  // exclusive offsets in (digit, wave) order; this thread's digit is tid
+                    const int hw = 16 * (tid & 1);
+                    int pos[NW];
+                    int t = 0;
+#pragma unroll
+                    for (int v = 0; v < NW; ++v) {
+                        pos[v] = (int)((cnt[v * (BLK / 2) + (tid >> 1)] >> hw) & 0xffffu);
+                        t += pos[v];
+                    }
+                    int64_t tot;
+                    int run = (int)(block_incl_scan<BLK>(t, tmp, &tot) - t);  // every count read first
+#pragma unroll
+                    for (int v = 0; v < NW; ++v) {
+                        const int c = pos[v];
+                        pos[v] = run;
+                        run += c;
+                    }
+                    // the even digit's thread writes the pair's word
+#pragma unroll
+                    for (int v = 0; v < NW; ++v) {
+                        const int odd = __shfl_down(pos[v], 1, kWave);
+                        if (!(tid & 1)) cnt[v * (BLK / 2) + (tid >> 1)] = (uint32_t)pos[v] | ((uint32_t)odd << 16);
+                    }
+                }
+                __syncthreads();
+                // scatter: each wave walks its positions in order, 64 at a
+                // time; lanes with equal digits take consecutive places in
+                // lane order, and the group's highest lane advances the count
+                for (int b = lo; b < hi; b += kWave) {  // uniform over the wave
+                    const int i = b + lane;
+                    const bool v = i < hi;
+                    uint16_t x = 0;
+                    int d = 0;
+                    if (v) {
+                        x = src[i];
+                        d = (int)(((uint32_t)(colv[x] - cbase) >> sh) & (BLK - 1));
+                    }
+                    uint64_t peers = __ballot(v);
+#pragma unroll
+                    for (int k = 0; k < DIG; ++k) {
+                        const bool bit = (d >> k) & 1;
+                        const uint64_t bb = __ballot(bit);
+                        peers &= bit ? bb : ~bb;
+                    }
+                    if (v) {
+                        const int word = wv * (BLK / 2) + (d >> 1), hw = 16 * (d & 1);
+                        const int base = (int)((cnt[word] >> hw) & 0xffffu);
+                        dst[base + __popcll(peers & ((1ull << lane) - 1))] = x;
+                        if ((peers >> lane) == 1ull) atomicAdd(&cnt[word], (uint32_t)__popcll(peers) << hw);
+                    }
+                }
+                __syncthreads();
+                uint16_t* t = src;
+                src = dst;
+                dst = t;
+            }
+            auto first_of_col = [&](int i) { return i == 0 || rel_col(src[i - 1]) != rel_col(src[i]); };
+            // places: every wave walks its sorted positions in rounds of 64
+            // consecutive ones, counts first-of-column flags by ballot, and
+            // one barrier gives the waves' offsets
+            int wbase = 0;
+            {
+                int wcount = 0;
+                for (int b = lo; b < hi; b += kWave) {  // uniform over the wave
+                    const int i = b + lane;
+                    wcount += __popcll(__ballot(i < hi && first_of_col(i)));
+                }
+                if (lane == 0) wcnt[wv] = wcount;
+                __syncthreads();
+                u = 0;
+                for (int v = 0; v < NW; ++v) {
+                    const int c = wcnt[v];
+                    wbase += v < wv ? c : 0;
+                    u += c;
+                }
+            }
+            for (int b = lo; b < hi; b += kWave) {  // uniform over the wave
+                const int i = b + lane;
                 const bool in = i < hi;
                 const bool f = in && first_of_col(i);
                 const uint64_t fm = __ballot(f);
                 const int pl = wbase + __popcll(fm & ((2ull << lane) - 1)) - 1;  // flags up to this lane
                 wbase += __popcll(fm);
                 if (in) {
-                    const int j = jj[k];
-                    int c, q;
-                    bool last = true;
-                    if (KEYED) {
-                        c = (colv[j] >> 4) + cmin;
-                        q = colv[j] & 15;
-                        if (i + 1 < m) last = colv[src[i + 1]] != colv[j];
-                    } else {
-                        c = colv[j];
-                        q = row_of(j);
-                        // the next edge of the same column comes later in CSR
-                        // order (stable sort): the same row while before its end
-                        if (i + 1 < m) {
-                            const int jn = src[i + 1];
-                            last = colv[jn] != c || e0 + jn >= rp[q + 1];
-                        }
-                    }
-                    if (f) ucol[e0 + pl] = c;
-                    skeys[e0 + i] = win_record(vv[k], pl, q, last);
+                    const int j = src[i];
+                    const int q = KEYED ? (colv[j] & 15) : row_of(j);
+                    if (f) ucol[e0 + pl] = rel_col(j) + cmin;
+                    // the value of offset j sits in another thread's vv[]: read
+                    // it from the input again (cache-resident)
+                    const uint32_t vb = KEYED ? tvals[e0 + j] : (vals ? __float_as_uint(vals[e0 + j]) : 0x3f800000u);
+                    skeys[e0 + i] = srec(vb, pl, q, j);
                 }
+            }
+        }
+        // -1 after the distinct columns, up to the tile boundary (within the
+        // window's slots; the fill writes -1 beyond them itself)
+        {
+            const int upad = min((u + tc - 1) / tc * tc, m);
+            for (int x = u + tid; x < upad; x += BLK) ucol[e0 + x] = -1;
+        }
+        if (tid == 0) {
+            wtiles[w] = (u + tc - 1) / tc;
+            if (!KEYED) {
+                wstart[w] = e0;
+                wend[w] = e0 + m;
             }
         }
         __syncthreads();  // LDS is rewritten for the next window
@@ -626,16 +683,14 @@ __global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192
 // edges, checked before the launch), one work-group each: the same stable
 // radix sort and records, with the edge offsets double-buffered in global
 // scratch (jbuf, 2 m entries at 2 e0), the places in pbuf, and every sort key
-// read from the input where it is used.  KEYED with kcopy: the sorted keys and
-// values are where the records and distinct columns go (ka / va), so the
-// window's share is copied to kcopy / vcopy first.
+// read from the input where it is used.
 constexpr int kBig = 8;  // rounds of 64 edges whose loads are issued together
 template <bool KEYED>
 __global__ __launch_bounds__(kWinBlk) void win_sort_big_kernel(
     const int64_t* __restrict__ row_ptr, const int32_t* __restrict__ cols, const float* __restrict__ vals,
-    const uint64_t* tkeys, const uint32_t* tvals, uint64_t* kcopy, uint32_t* vcopy, int wbits, int64_t n, int64_t R,
+    const uint64_t* __restrict__ tkeys, const uint32_t* __restrict__ tvals, int wbits, int64_t n, int64_t R,
     const int32_t* __restrict__ blist, int nbig, int64_t num_cols, int tc, uint32_t* __restrict__ jbuf,
-    uint32_t* __restrict__ pbuf, uint64_t* skeys, int32_t* ucol, int64_t* __restrict__ wstart,
+    uint32_t* __restrict__ pbuf, uint64_t* __restrict__ skeys, int32_t* __restrict__ ucol, int64_t* __restrict__ wstart,
     int64_t* __restrict__ wend, int32_t* __restrict__ wtiles, int32_t* __restrict__ err) {
     constexpr int NW = kWinBlk / kWave;
     __shared__ uint32_t cnt[NW * kWinBkt];  // [wave][digit] counts, then scatter positions
@@ -664,15 +719,6 @@ __global__ __launch_bounds__(kWinBlk) void win_sort_big_kernel(
         }
         const uint64_t* tk = tkeys;
         const uint32_t* tv = tvals;
-        if (KEYED && kcopy) {
-            for (int j = tid; j < m; j += kWinBlk) {
-                kcopy[e0 + j] = tkeys[e0 + j];
-                vcopy[e0 + j] = tvals[e0 + j];
-            }
-            __syncthreads();
-            tk = kcopy;
-            tv = vcopy;
-        }
         int cmin = 0x7fffffff, cmax = 0;
         bool bad = false;
         for (int j = tid; j < m; j += kWinBlk) {
@@ -875,29 +921,47 @@ __device__ __forceinline__ __hip_bfloat16 to_value<__hip_bfloat16>(float v) {
     return __float2bfloat16(v);
 }
 
-// The fill of the per-window build (err[2] = 1; the global path's scatter
-// exits then, and this kernel exits otherwise).  One work-group per window
-// writes the window's whole tile range, padding included, so the outputs
-// need no clearing first: the columns straight from the distinct-column list
-// (then -1 to the tile boundary), the values kFillVals at a time (32 tiles of
-// 16 x 16, 64 of 16 x 8) assembled in LDS from the records, which every
-// thread loads once, and written out with 16-byte stores.
+// The fill of the per-window build (err[2] = 1 or 2; the global path's
+// scatter exits then, and this kernel exits otherwise).  One work-group per
+// window writes the window's whole tile range, padding included, so the
+// outputs need no clearing first: the columns straight from the
+// distinct-column list (which holds -1 after its last column), the values
+// kFillVals at a time (32 tiles of 16 x 16, 64 of 16 x 8) assembled in LDS
+// from the records, which every thread loads once, and written out with
+// 16-byte stores.  Of records with the same (tile, row, column) slot --
+// duplicate edges -- the one with the largest offset, the last in input
+// order, is stored.
 constexpr int kFillVals = 8192;
+template <typename VT>
+__device__ __forceinline__ uint32_t value_bits(VT v) {
+    static_assert(sizeof(VT) == 2 || sizeof(VT) == 4, "16- or 32-bit values");
+    if constexpr (sizeof(VT) == 2) {
+        uint16_t b;
+        __builtin_memcpy(&b, &v, 2);
+        return b;
+    } else {
+        uint32_t b;
+        __builtin_memcpy(&b, &v, 4);
+        return b;
+    }
+}
 template <int CAP, int BLK, typename VT>
-__global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192 ? 4 : (CAP == 16384 ? 2 : 1)))) void win_fill_kernel(const uint64_t* __restrict__ rec,
-                                                            const int32_t* __restrict__ ucol,
-                                                            const int64_t* __restrict__ wstart,
-                                                            const int64_t* __restrict__ wend,
-                                                            const int64_t* __restrict__ win_off, int64_t W, int tc,
-                                                            int32_t* __restrict__ out_cols, void* __restrict__ out_vals,
-                                                            int aligned, const int32_t* __restrict__ err) {
+__global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192 ? 4 : (CAP == 16384 ? 2 : 1)))) void win_fill_kernel(
+    const uint64_t* __restrict__ rec, const int32_t* __restrict__ ucol, const int64_t* __restrict__ wstart,
+    const int64_t* __restrict__ wend, const int64_t* __restrict__ win_off, int64_t W, int tc,
+    int32_t* __restrict__ out_cols, void* __restrict__ out_vals, int aligned, const int32_t* __restrict__ err) {
     // CAP 2048 (256 threads): the windows of at most 2,048 edges; CAP 8192:
     // up to 8,192; CAP 16384: the larger ones (at most kWinCap)
     constexpr int PER = CAP / BLK;  // records per thread
     constexpr int MLO = CAP == 2048 ? -1 : (CAP == 8192 ? 2048 : 8192);  // this launch: MLO < edges <= CAP
     constexpr int VPU = 16 / (int)sizeof(VT);  // values per 16 bytes
-    __shared__ __align__(16) VT sval[kFillVals];
-    if (err[2] != 1) return;  // uniform
+    // a slot holds (1 + offset) << value bits | the value's bits: one atomicMax
+    // keeps the last duplicate with its value; 0 is an empty slot (value 0)
+    using PT = std::conditional_t<sizeof(VT) == 4, unsigned long long, uint32_t>;
+    constexpr int VB = 8 * (int)sizeof(VT);
+    constexpr int SPU = 16 / (int)sizeof(PT);  // slots per 16 bytes
+    __shared__ __align__(16) PT stage[kFillVals];
+    if (err[2] == 0) return;  // uniform
     const int tid = threadIdx.x;
     const int ltc = tc == 16 ? 4 : 3;
     const int gt = kFillVals / (16 * tc);  // tiles per step
@@ -914,31 +978,51 @@ __global__ __launch_bounds__(BLK) __attribute__((amdgpu_waves_per_eu(CAP == 8192
             const int i = tid + k * BLK;
             r[k] = i < m ? rec[e0 + i] : 0;
         }
-        const int u = m > 0 ? rec_place(rec[e0 + m - 1]) + 1 : 0;
         int32_t* oc = out_cols + wo * tc;
-        for (int x = tid; x < nt * tc; x += BLK) oc[x] = x < u ? ucol[e0 + x] : -1;
+        for (int x = tid; x < nt * tc; x += BLK) oc[x] = x < m ? ucol[e0 + x] : -1;
         for (int g0 = 0; g0 < nt; g0 += gt) {  // uniform over the work-group
             const int g1 = g0 + gt < nt ? g0 + gt : nt;
             const int nv = (g1 - g0) * 16 * tc;
-            for (int x = tid; x < nv / VPU; x += BLK) reinterpret_cast<uint4*>(sval)[x] = make_uint4(0, 0, 0, 0);
+            for (int x = tid; x < nv / SPU; x += BLK) reinterpret_cast<uint4*>(stage)[x] = make_uint4(0, 0, 0, 0);
             __syncthreads();
 #pragma unroll
             for (int k = 0; k < PER; ++k) {
-                if (tid + k * BLK < m && rec_last(r[k])) {
-                    const int pl = rec_place(r[k]);
+                if (tid + k * BLK < m) {
+                    const int pl = srec_place(r[k]);
                     const int t = (pl >> ltc) - g0;
-                    if (t >= 0 && t < g1 - g0)
-                        sval[((t * 16 + rec_row(r[k])) << ltc) + (pl & (tc - 1))] =
-                            to_value<VT>(__uint_as_float((uint32_t)r[k]));
+                    if (t >= 0 && t < g1 - g0) {
+                        const PT pk = ((PT)(srec_j(r[k]) + 1) << VB) |
+                                      (PT)value_bits(to_value<VT>(__uint_as_float((uint32_t)r[k])));
+                        atomicMax(&stage[((t * 16 + srec_row(r[k])) << ltc) + (pl & (tc - 1))], pk);
+                    }
                 }
             }
             __syncthreads();
             VT* ov = static_cast<VT*>(out_vals) + (wo + g0) * 16 * tc;
             if (aligned) {  // the values 16-byte aligned (uniform)
-                for (int x = tid; x < nv / VPU; x += BLK)
-                    reinterpret_cast<uint4*>(ov)[x] = reinterpret_cast<const uint4*>(sval)[x];
+                for (int x = tid; x < nv / VPU; x += BLK) {
+                    uint32_t o[4];
+                    if constexpr (sizeof(VT) == 2) {
+#pragma unroll
+                        for (int h = 0; h < 4; ++h)
+                            o[h] = ((uint32_t)stage[x * 8 + 2 * h] & 0xffffu) |
+                                   (((uint32_t)stage[x * 8 + 2 * h + 1] & 0xffffu) << 16);
+                    } else {
+#pragma unroll
+                        for (int h = 0; h < 4; ++h) o[h] = (uint32_t)stage[x * 4 + h];
+                    }
+                    reinterpret_cast<uint4*>(ov)[x] = make_uint4(o[0], o[1], o[2], o[3]);
+                }
             } else {
-                for (int x = tid; x < nv; x += BLK) ov[x] = sval[x];
+                for (int x = tid; x < nv; x += BLK) {
+                    const uint32_t bits = (uint32_t)stage[x] & (VB == 16 ? 0xffffu : 0xffffffffu);
+                    if constexpr (sizeof(VT) == 2) {
+                        const uint16_t h = (uint16_t)bits;
+                        __builtin_memcpy(&ov[x], &h, 2);
+                    } else {
+                        __builtin_memcpy(&ov[x], &bits, 4);
+                    }
+                }
             }
             __syncthreads();
         }
@@ -961,7 +1045,7 @@ __global__ __launch_bounds__(kWinBlk) void win_fill_big_kernel(const uint64_t* _
                                                                int aligned, const int32_t* __restrict__ err) {
     constexpr int VPU = 16 / (int)sizeof(VT);  // values per 16 bytes
     __shared__ __align__(16) VT sval[kFillVals];
-    if (err[2] != 1) return;  // uniform
+    if (err[2] == 0) return;  // uniform
     const int tid = threadIdx.x;
     const int ltc = tc == 16 ? 4 : 3;
     const int gt = kFillVals / (16 * tc);  // tiles per step
@@ -1305,28 +1389,30 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
         const unsigned wgs = (unsigned)std::min<int64_t>(s.W, 16384);  // the 2,048-edge class, 256 threads
         int32_t* ucol = reinterpret_cast<int32_t*>(w.va);
         if (keyed) {
-            // sorted keys and values in ka / va (then the records overwrite
-            // them window by window) or kb / vb
+            // sorted keys and values in ka / va or kb / vb; the records and
+            // distinct columns go to the other pair (path 2: kb / vb)
             const uint64_t* tk = kalt ? w.kb : w.ka;
             const uint32_t* tv = kalt ? w.vb : w.va;
+            uint64_t* rk = kalt ? w.ka : w.kb;
+            ucol = reinterpret_cast<int32_t*>(kalt ? w.va : w.vb);
+            if (!kalt) GRWS_TRY(fill_i32(w.err + 2, 1, 2, stream));
             hipLaunchKernelGGL((win_sort_kernel<2048, 256, true>), dim3(wgs), dim3(256), 0, stream, nullptr, nullptr,
-                               nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols, w.ka, ucol, w.wstart, w.wend,
+                               nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols, rk, ucol, w.wstart, w.wend,
                                w.wtiles, w.err);
             GRWS_LAUNCH_CHECK();
             hipLaunchKernelGGL((win_sort_kernel<8192, kWinBlk, true>), dim3(wg), dim3(kWinBlk), 0, stream, nullptr,
-                               nullptr, nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols, w.ka, ucol, w.wstart,
+                               nullptr, nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols, rk, ucol, w.wstart,
                                w.wend, w.wtiles, w.err);
             GRWS_LAUNCH_CHECK();
             hipLaunchKernelGGL((win_sort_kernel<16384, kWinBlk, true>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0,
                                stream, nullptr, nullptr, nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols,
-                               w.ka, ucol, w.wstart, w.wend, w.wtiles, w.err);
+                               rk, ucol, w.wstart, w.wend, w.wtiles, w.err);
             GRWS_LAUNCH_CHECK();
             if (nbig > 0) {
                 hipLaunchKernelGGL((win_sort_big_kernel<true>), dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, stream,
-                                   nullptr, nullptr, nullptr, tk, tv, kalt ? nullptr : w.kb, kalt ? nullptr : w.vb,
-                                   kwbits, nnz, s.R, w.blist, nbig, s.C, (int)tile_cols,
-                                   reinterpret_cast<uint32_t*>(w.uidx), reinterpret_cast<uint32_t*>(w.uflag), w.ka,
-                                   ucol, w.wstart, w.wend, w.wtiles, w.err);
+                                   nullptr, nullptr, nullptr, tk, tv, kwbits, nnz, s.R, w.blist, nbig,
+                                   s.C, (int)tile_cols, reinterpret_cast<uint32_t*>(w.uidx),
+                                   reinterpret_cast<uint32_t*>(w.uflag), rk, ucol, w.wstart, w.wend, w.wtiles, w.err);
                 GRWS_LAUNCH_CHECK();
             }
         } else {
@@ -1344,7 +1430,7 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
             GRWS_LAUNCH_CHECK();
             if (nbig > 0) {
                 hipLaunchKernelGGL((win_sort_big_kernel<false>), dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, stream,
-                                   row_ptr, cols, values, nullptr, nullptr, nullptr, nullptr, 0, nnz, s.R, w.blist,
+                                   row_ptr, cols, values, nullptr, nullptr, 0, nnz, s.R, w.blist,
                                    nbig, num_cols, (int)tile_cols, reinterpret_cast<uint32_t*>(w.uidx),
                                    reinterpret_cast<uint32_t*>(w.uflag), w.ka, ucol, w.wstart, w.wend, w.wtiles,
                                    w.err);
@@ -1412,39 +1498,41 @@ extern "C" int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_c
     const bool alt = nnz > 1 && (passes & 1);
     const uint64_t* k = alt ? w.kb : w.ka;
     const uint32_t* v = alt ? w.vb : w.va;
-    // the path the count phase took (err[2] = 1: per window; its sorted keys
-    // and values are in ka / va, and its fill writes every tile, padding
-    // included)
+    // the path the count phase took: err[2] = 0 the global sort; 1 window by
+    // window with the records and distinct columns in ka / va, 2 in kb / vb
+    // (its fill writes every tile, padding included)
     int32_t hf[3] = {0, 0, 0};  // err[0..2]: flags, windows over kWinCap edges, path
     if (nnz > 0) {
         GRWS_HIP(hipMemcpyAsync(hf, w.err, 3 * sizeof(int32_t), hipMemcpyDeviceToHost, stream));
         GRWS_HIP(hipStreamSynchronize(stream));
     }
     const int32_t path = hf[2];
-    const int nbig = path == 1 ? hf[1] : 0;
-    if (path != 1) {
+    const int nbig = path != 0 ? hf[1] : 0;
+    if (path == 0) {
         GRWS_TRY(fill_i32(col_indices, num_tiles * tile_cols, -1, stream));
         GRWS_TRY(fill_bytes_zero(values, (size_t)num_tiles * 16 * tile_cols * dtype_size(values_dtype), stream));
     }
     if (nnz == 0) return GRWS_OK;
     const unsigned wg = (unsigned)std::min<int64_t>(s.W, 4096);
     const int aligned = (reinterpret_cast<uintptr_t>(values) & 15) == 0;
+    const uint64_t* wrec = path == 2 ? w.kb : w.ka;
+    const int32_t* wcol = reinterpret_cast<const int32_t*>(path == 2 ? w.vb : w.va);
 #define GRWS_BUILD_FILL(VT)                                                                                        \
-    if (path == 1)                                                                                                 \
+    if (path != 0)                                                                                                 \
     {                                                                                                              \
         hipLaunchKernelGGL((win_fill_kernel<2048, 256, VT>), dim3((unsigned)std::min<int64_t>(s.W, 16384)),     \
-                           dim3(256), 0, stream, w.ka, reinterpret_cast<const int32_t*>(w.va), w.wstart, w.wend,   \
-                           window_offset, s.W, (int)tile_cols, col_indices, values, aligned, w.err);               \
-        hipLaunchKernelGGL((win_fill_kernel<8192, kWinBlk, VT>), dim3(wg), dim3(kWinBlk), 0, stream, w.ka,         \
-                           reinterpret_cast<const int32_t*>(w.va), w.wstart, w.wend, window_offset, s.W,           \
-                           (int)tile_cols, col_indices, values, aligned, w.err);                                   \
-        hipLaunchKernelGGL((win_fill_kernel<16384, kWinBlk, VT>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), 0,      \
-                           stream, w.ka, reinterpret_cast<const int32_t*>(w.va), w.wstart, w.wend, window_offset,  \
-                           s.W, (int)tile_cols, col_indices, values, aligned, w.err);                              \
+                           dim3(256), 0, stream, wrec, wcol, w.wstart, w.wend, window_offset, s.W, (int)tile_cols, \
+                           col_indices, values, aligned, w.err);                                                   \
+        hipLaunchKernelGGL((win_fill_kernel<8192, kWinBlk, VT>), dim3(wg), dim3(kWinBlk), 0, stream, wrec, wcol,   \
+                           w.wstart, w.wend, window_offset, s.W, (int)tile_cols, col_indices, values, aligned,     \
+                           w.err);                                                                                 \
+        hipLaunchKernelGGL((win_fill_kernel<16384, kWinBlk, VT>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), \
+                           0, stream, wrec, wcol, w.wstart, w.wend, window_offset, s.W, (int)tile_cols,            \
+                           col_indices, values, aligned, w.err);                                                   \
         if (nbig > 0)                                                                                              \
             hipLaunchKernelGGL(win_fill_big_kernel<VT>, dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, stream,      \
-                               w.ka, reinterpret_cast<const int32_t*>(w.va), w.wstart, w.wend, window_offset,      \
-                               w.blist, nbig, (int)tile_cols, col_indices, values, aligned, w.err);               \
+                               wrec, wcol, w.wstart, w.wend, window_offset, w.blist, nbig, (int)tile_cols,        \
+                               col_indices, values, aligned, w.err);                                               \
     } else                                                                                                         \
         hipLaunchKernelGGL(build_scatter_kernel<VT>, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, v, nnz, s.cbits, \
                            w.uflag, w.uidx, w.wstart, window_offset, (int)tile_cols, col_indices, values, w.err)
