@@ -42,6 +42,15 @@ MEASURED_TRAFFIC = {
 }
 
 
+# HBM bytes of one device BCSR build (the window sort and the fill), measured
+# the same way (FETCH_SIZE x2.0 + WRITE_SIZE x1.0 per dispatch), for the
+# profiled workload only
+BUILD_TRAFFIC = {
+    # (config, path): (bytes per build, profile file)
+    ("c3", "window by window"): (6.19e9, "profiles/bcsr_build_c3_f16.md"),
+}
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -66,7 +75,7 @@ def build_graph(cfg: str, tc: int, vdt: torch.dtype, dev: torch.device):
     return g, G, t1 - t0, t2 - t1
 
 
-def bench_build(g, dev, cpu: bool, reps: int = 5) -> dict:
+def bench_build(g, dev, cpu: bool, reps: int = 5, cfg: str = "c3") -> dict:
     """The device BCSR build (csr_to_bcsr, H3) of the headline graph: CSR
     (int64 row pointer, int32 columns, f32 values) -> 16x16 BCSR with f16
     values, and the build of its transpose (the backward's operand).  Wall
@@ -124,6 +133,10 @@ def bench_build(g, dev, cpu: bool, reps: int = 5) -> dict:
                       "note": "algorithmic bytes of the path taken: the CSR read, the BCSR written once, and "
                               "the workspace round trip (window by window: 24 B per edge; global sort: "
                               "32 B per edge per radix pass + 16); wall time including the build's syncs"}}
+    traffic = BUILD_TRAFFIC.get((cfg, r["path"]))
+    if traffic is not None:
+        r["roofline"]["traffic"] = traffic[0]
+        r["roofline"]["traffic_source"] = traffic[1]
     if cpu:
         import oracle
         rows = n
@@ -1075,7 +1088,7 @@ def main():
     else:
         out["parity"] = {"pass": None, "note": "not checked (--no-cpu-baseline)"}
     if not args.no_build:
-        out["bcsr_build"] = bench_build(g, dev, not args.no_cpu_baseline)
+        out["bcsr_build"] = bench_build(g, dev, not args.no_cpu_baseline, cfg=cfg)
     if not args.no_sampling:
         del G, X, Y, g, plan
         torch.cuda.empty_cache()
