@@ -264,19 +264,18 @@ __global__ void build_scatter_kernel(const uint64_t* __restrict__ keys, const ui
     if (i == n - 1 || keys[i + 1] != k) store_value<VT>(out_vals, (tile * 16 + r) * tc + c, __uint_as_float(pay[i]));
 }
 
-// --- per-window CSR build ---------------------------------------------------
-// A CSR's edges come grouped by window already (16 consecutive rows), so when
-// every window has at most kWinCap edges (c3: at most 8,246) each window is
-// built by one work-group from LDS, with no global sort: the window's edge
-// offsets are radix-sorted in LDS by column (stable, 9-bit digits over the
-// window's column span: two passes for spans up to 2^18), each distinct
-// column given its place among the window's distinct columns, and one record
-// per edge written in (column, row, offset) order with the distinct columns
-// at their places.  Edges enter in CSR order, (row, offset), and the sort is
-// stable, so of duplicate (row, column) edges the one last in CSR order is
-// the last of its run and is the one stored, as with the global sort.
+// --- window-by-window build ---------------------------------------------------
+// A CSR's edges come grouped by window already (16 consecutive rows); COO
+// input and transposed builds are grouped by a sort over the window bits of
+// their keys.  Each window of at most kWinCap edges is then built by one
+// work-group from LDS (win_sort_kernel: each distinct column's place among the
+// window's distinct columns, from a column bitmap or an LDS radix sort, and one
+// record per edge; win_fill_kernel: the tiles assembled in LDS), larger ones
+// by one work-group each from global scratch (win_sort_big_kernel,
+// win_fill_big_kernel).
 //
-// record: value bits (f32) | place << 32 (27 bits) | row << 59 (4 bits) |
+// record of a window of more than kWinCap edges (in (column, row, offset)
+// order): value bits (f32) | place << 32 (27 bits) | row << 59 (4 bits) |
 // last of its (column, row) run << 63; the window's last record holds its
 // last place, so the fill knows the count of distinct columns.
 constexpr int64_t kWinHuge = (int64_t)1 << 27;  // windows of more edges take the global sort
