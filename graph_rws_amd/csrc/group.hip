@@ -113,26 +113,28 @@ struct NullCarver {
     }
 };
 
-// Window of tile t: the largest w with win_off[w] <= t.
-__device__ __forceinline__ int64_t tile_window(const int64_t* __restrict__ win_off, int64_t W, int64_t t) {
-    int64_t lo = 0, hi = W - 1;
-    while (lo < hi) {
-        const int64_t mid = (lo + hi + 1) >> 1;
-        if (win_off[mid] <= t) lo = mid;
-        else hi = mid - 1;
-    }
-    return lo;
-}
-
 // 16-bit value bits of slot (t, r, c): nonzero bits are kept (as the packed
 // tiles keep them).
 __device__ __forceinline__ uint32_t value_bits(const uint16_t* __restrict__ vals, int64_t t, int r, int c, int tc) {
     return vals[(t * 16 + r) * tc + c];
 }
 
+// The window of every tile (twin), one work-group per window; the map starts
+// zeroed, so tiles outside every window (only from a malformed
+// window_offset) belong to window 0.
+__global__ __launch_bounds__(256) void grp_tile_window_kernel(const int64_t* __restrict__ win_off, int64_t W,
+                                                              int64_t T, int32_t* __restrict__ twin) {
+    for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {
+        const int64_t a = win_off[w], e = win_off[w + 1];
+        const int64_t t0 = a < 0 ? 0 : (a > T ? T : a);
+        const int64_t t1 = e < t0 ? t0 : (e > T ? T : e);
+        for (int64_t t = t0 + threadIdx.x; t < t1; t += blockDim.x) twin[t] = (int32_t)w;
+    }
+}
+
 // Key of every slot: (group << cbits | column), or the invalid flag for a
 // padding slot or a column outside [0, num_cols).
-__global__ void grp_keys_kernel(const int64_t* __restrict__ win_off, int64_t W, const int32_t* __restrict__ cols,
+__global__ void grp_keys_kernel(const int32_t* __restrict__ twin, const int32_t* __restrict__ cols,
                                 int64_t n, int tc, int64_t num_cols, int G, int cbits, int vbit,
                                 uint64_t* __restrict__ keys, uint32_t* __restrict__ pay) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -140,7 +142,7 @@ __global__ void grp_keys_kernel(const int64_t* __restrict__ win_off, int64_t W, 
     const int32_t c = cols[i];
     uint64_t k = 1ull << vbit;
     if (c >= 0 && (int64_t)c < num_cols) {
-        const int64_t w = tile_window(win_off, W, i / tc);
+        const int64_t w = twin[i / tc];
         k = ((uint64_t)(w / G) << cbits) | (uint64_t)c;
     }
     keys[i] = k;
@@ -200,6 +202,31 @@ __global__ __launch_bounds__(256) void grp_count_values_kernel(const int32_t* __
     if (lane == 0 && cnt) atomicAdd((unsigned long long*)&stats[0], (unsigned long long)cnt);
 }
 
+// The same count from 16 bytes of values a lane (values 16-byte aligned):
+// chunk x holds slots 8 (x % tpb) .. + 7 of tile x / tpb (tpb = 2 tc chunks
+// a tile); one atomic per wave.
+__global__ __launch_bounds__(256) void grp_count_values16_kernel(const int32_t* __restrict__ cols,
+                                                                 const uint16_t* __restrict__ vals, int64_t T, int tc,
+                                                                 int64_t num_cols, int64_t* __restrict__ stats) {
+    const int tpb = 2 * tc;
+    const int64_t nch = T * tpb;
+    int64_t cnt = 0;
+    for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < nch; x += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = x / tpb;
+        const int s0 = (int)(x % tpb) * 8;
+        const uint4 raw = reinterpret_cast<const uint4*>(vals)[x];
+        const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t v = (w4[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+            const int32_t col = cols[t * tc + (s0 + k) % tc];
+            cnt += (v != 0 && col >= 0 && (int64_t)col < num_cols) ? 1 : 0;
+        }
+    }
+    for (int d = 32; d > 0; d >>= 1) cnt += __shfl_xor(cnt, d, 64);
+    if ((threadIdx.x & 63) == 0 && cnt) atomicAdd((unsigned long long*)&stats[0], (unsigned long long)cnt);
+}
+
 // Every valid sorted slot: its (slab, position); the group's union column.
 __global__ void grp_place_kernel(const uint64_t* __restrict__ keys, const uint32_t* __restrict__ pay, int64_t n,
                                  int vbit, int cbits, const int32_t* __restrict__ uflag,
@@ -237,7 +264,7 @@ __device__ __forceinline__ SubSlot sub_slot(const uint32_t* __restrict__ pos, in
 }
 
 // Masks (atomic OR; the header starts zeroed).  One wave per tile.
-__global__ __launch_bounds__(256) void grp_mask_kernel(const int64_t* __restrict__ win_off, int64_t W,
+__global__ __launch_bounds__(256) void grp_mask_kernel(const int32_t* __restrict__ twin,
                                                        const int32_t* __restrict__ cols,
                                                        const uint16_t* __restrict__ vals, int64_t T, int tc,
                                                        int64_t num_cols, int G, const uint32_t* __restrict__ pos,
@@ -245,7 +272,7 @@ __global__ __launch_bounds__(256) void grp_mask_kernel(const int64_t* __restrict
     const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;  // uniform per wave
     const int lane = threadIdx.x & 63;
-    const int64_t w = tile_window(win_off, W, t);
+    const int64_t w = twin[t];
     const int per = 16 * tc / 64;
     for (int j = 0; j < per; ++j) {
         const int slot = lane * per + j;
@@ -278,7 +305,7 @@ __global__ void grp_sub_start_kernel(uint32_t* __restrict__ hdr, int64_t nsub, c
 }
 
 // Every nonzero to its place: the group start plus the mask bits below it.
-__global__ __launch_bounds__(256) void grp_values_kernel(const int64_t* __restrict__ win_off, int64_t W,
+__global__ __launch_bounds__(256) void grp_values_kernel(const int32_t* __restrict__ twin,
                                                          const int32_t* __restrict__ cols,
                                                          const uint16_t* __restrict__ vals, int64_t T, int tc,
                                                          int64_t num_cols, int G, const uint32_t* __restrict__ pos,
@@ -287,7 +314,7 @@ __global__ __launch_bounds__(256) void grp_values_kernel(const int64_t* __restri
     const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;  // uniform per wave
     const int lane = threadIdx.x & 63;
-    const int64_t w = tile_window(win_off, W, t);
+    const int64_t w = twin[t];
     const int per = 16 * tc / 64;
     for (int j = 0; j < per; ++j) {
         const int slot = lane * per + j;
@@ -364,8 +391,14 @@ extern "C" int grws_group_tiles_count(const grws_bcsr* A, int64_t num_cols, int3
     GRWS_TRY(fill_i64(w.stats, 4, 0, stream));
     w.alt = false;
     if (s.n > 0) {
-        hipLaunchKernelGGL(grp_keys_kernel, dim3(grid_for(s.n)), dim3(kBlk), 0, stream, A->window_offset,
-                           A->num_windows, A->col_indices, s.n, tc, num_cols, group_size, s.cbits, vbit, w.ka, w.va);
+        // each tile's window, in pos (the fill's array, unused until then)
+        int32_t* twin = reinterpret_cast<int32_t*>(w.pos);
+        GRWS_TRY(fill_i32(twin, A->num_tiles, 0, stream));
+        hipLaunchKernelGGL(grp_tile_window_kernel, dim3(grid_for(A->num_windows, 1) < 8192u ? grid_for(A->num_windows, 1) : 8192u),
+                           dim3(256), 0, stream, A->window_offset, A->num_windows, A->num_tiles, twin);
+        GRWS_LAUNCH_CHECK();
+        hipLaunchKernelGGL(grp_keys_kernel, dim3(grid_for(s.n)), dim3(kBlk), 0, stream, twin, A->col_indices, s.n,
+                           tc, num_cols, group_size, s.cbits, vbit, w.ka, w.va);
         GRWS_LAUNCH_CHECK();
         GRWS_TRY(radix_sort_pairs(w.ka, w.va, w.kb, w.vb, s.n, s.bits, w.sort_ws, w.sort_bytes, stream, &w.alt));
         const uint64_t* k = w.alt ? w.kb : w.ka;
@@ -375,9 +408,16 @@ extern "C" int grws_group_tiles_count(const grws_bcsr* A, int64_t num_cols, int3
         hipLaunchKernelGGL(grp_bounds_kernel, dim3(grid_for(s.n)), dim3(kBlk), 0, stream, k, s.n, vbit, s.cbits,
                            w.uflag, w.uidx, w.gfirst, w.glast);
         GRWS_LAUNCH_CHECK();
-        const unsigned cgrid = grid_for(A->num_tiles, 4) < 8192u ? grid_for(A->num_tiles, 4) : 8192u;
-        hipLaunchKernelGGL(grp_count_values_kernel, dim3(cgrid), dim3(256), 0, stream, A->col_indices,
-                           static_cast<const uint16_t*>(A->values), A->num_tiles, tc, num_cols, w.stats);
+        if ((reinterpret_cast<uintptr_t>(A->values) & 15) == 0) {
+            const int64_t nch = A->num_tiles * 2 * tc;
+            const unsigned cgrid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((nch + 255) / 256, 16384));
+            hipLaunchKernelGGL(grp_count_values16_kernel, dim3(cgrid), dim3(256), 0, stream, A->col_indices,
+                               static_cast<const uint16_t*>(A->values), A->num_tiles, tc, num_cols, w.stats);
+        } else {
+            const unsigned cgrid = grid_for(A->num_tiles, 4) < 8192u ? grid_for(A->num_tiles, 4) : 8192u;
+            hipLaunchKernelGGL(grp_count_values_kernel, dim3(cgrid), dim3(256), 0, stream, A->col_indices,
+                               static_cast<const uint16_t*>(A->values), A->num_tiles, tc, num_cols, w.stats);
+        }
         GRWS_LAUNCH_CHECK();
     }
     hipLaunchKernelGGL(grp_slabs_kernel, dim3(grid_for(s.Q)), dim3(kBlk), 0, stream, w.gfirst, w.glast, s.Q,
@@ -435,18 +475,23 @@ extern "C" int grws_group_tiles_fill(const grws_bcsr* A, int64_t num_cols, int32
                        w.uflag, w.uidx, w.gfirst, w.goff, w.pos, col_indices);
     GRWS_LAUNCH_CHECK();
     const uint16_t* vals = static_cast<const uint16_t*>(A->values);
-    hipLaunchKernelGGL(grp_mask_kernel, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, A->window_offset,
-                       A->num_windows, A->col_indices, vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos,
-                       header);
+    // each tile's window, in uflag (spent once the slots are placed)
+    int32_t* twin = w.uflag;
+    GRWS_TRY(fill_i32(twin, A->num_tiles, 0, stream));
+    hipLaunchKernelGGL(grp_tile_window_kernel, dim3(grid_for(A->num_windows, 1) < 8192u ? grid_for(A->num_windows, 1) : 8192u),
+                       dim3(256), 0, stream, A->window_offset, A->num_windows, A->num_tiles, twin);
+    GRWS_LAUNCH_CHECK();
+    hipLaunchKernelGGL(grp_mask_kernel, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, twin, A->col_indices,
+                       vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos, header);
     GRWS_LAUNCH_CHECK();
     hipLaunchKernelGGL(grp_sub_count_kernel, dim3(grid_for(nsub)), dim3(kBlk), 0, stream, header, nsub, w.scnt);
     GRWS_LAUNCH_CHECK();
     GRWS_TRY(scan_i32_to_i64(w.scnt, w.soff, nsub, false, w.scan_ws, w.scan_bytes, stream));
     hipLaunchKernelGGL(grp_sub_start_kernel, dim3(grid_for(nsub)), dim3(kBlk), 0, stream, header, nsub, w.soff);
     GRWS_LAUNCH_CHECK();
-    hipLaunchKernelGGL(grp_values_kernel, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, A->window_offset,
-                       A->num_windows, A->col_indices, vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos,
-                       header, static_cast<uint16_t*>(values), num_values);
+    hipLaunchKernelGGL(grp_values_kernel, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, twin, A->col_indices,
+                       vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos, header, static_cast<uint16_t*>(values),
+                       num_values);
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }
