@@ -284,6 +284,110 @@ __global__ __launch_bounds__(256) void grp_mask_kernel(const int32_t* __restrict
     }
 }
 
+// Graphs of at most kUnionCols columns (c2, c3) skip the sort: one
+// work-group per group sets a bit per valid tile slot in an LDS bitmap of
+// [0, num_cols); its popcount is the union's size (count), and popcount
+// bases give every column its place in the union (fill).  The group's tiles
+// are contiguous: those of windows [qG, qG + G).
+constexpr int64_t kUnionCols = 1 << 18;   // bitmap bits: 32 KB
+constexpr int kUnionWords = (int)(kUnionCols / 32);
+constexpr int kUnionBase = 4;             // words per popcount base
+
+__device__ __forceinline__ void union_bitmap(const int64_t* __restrict__ win_off, int64_t W, int64_t T,
+                                             const int32_t* __restrict__ cols, int tc, int64_t num_cols, int G,
+                                             int64_t q, uint32_t* bm, int nwords, int64_t* x0, int64_t* x1) {
+    const int64_t wa = q * G, wb = (q + 1) * G < W ? (q + 1) * G : W;
+    const int64_t a = win_off[wa], e = win_off[wb];
+    const int64_t t0 = a < 0 ? 0 : (a > T ? T : a);
+    const int64_t t1 = e < t0 ? t0 : (e > T ? T : e);
+    for (int x = threadIdx.x; x < nwords; x += blockDim.x) bm[x] = 0;
+    __syncthreads();
+    for (int64_t x = t0 * tc + threadIdx.x; x < t1 * tc; x += blockDim.x) {
+        const int32_t c = cols[x];
+        if (c >= 0 && (int64_t)c < num_cols) atomicOr(&bm[c >> 5], 1u << (c & 31));
+    }
+    __syncthreads();
+    *x0 = t0 * tc;
+    *x1 = t1 * tc;
+}
+
+__global__ __launch_bounds__(512) void grp_union_count_kernel(const int64_t* __restrict__ win_off, int64_t W, int64_t T,
+                                                              const int32_t* __restrict__ cols, int tc,
+                                                              int64_t num_cols, int G, int64_t Q,
+                                                              int32_t* __restrict__ gslabs, int64_t* __restrict__ stats) {
+    __shared__ uint32_t bm[kUnionWords];
+    __shared__ int64_t tmp[512 / 64 + 1];
+    const int nwords = (int)((num_cols + 31) / 32);
+    for (int64_t q = blockIdx.x; q < Q; q += gridDim.x) {  // uniform over the work-group
+        int64_t x0, x1;
+        union_bitmap(win_off, W, T, cols, tc, num_cols, G, q, bm, nwords, &x0, &x1);
+        int c = 0;
+        for (int x = threadIdx.x; x < nwords; x += 512) c += __popc(bm[x]);
+        int64_t tot;
+        block_incl_scan<512>(c, tmp, &tot);
+        if (threadIdx.x == 0) {
+            const int32_t sl = (int32_t)((tot + 15) / 16);
+            gslabs[q] = sl;
+            if (sl > 0) atomicMax((unsigned long long*)&stats[1], (unsigned long long)sl);
+        }
+        __syncthreads();  // the bitmap is rewritten for the next group
+    }
+}
+
+__global__ __launch_bounds__(512) void grp_union_fill_kernel(const int64_t* __restrict__ win_off, int64_t W, int64_t T,
+                                                             const int32_t* __restrict__ cols, int tc, int64_t num_cols,
+                                                             int G, int64_t Q, const int64_t* __restrict__ goff,
+                                                             uint32_t* __restrict__ pos, int32_t* __restrict__ gcols) {
+    __shared__ uint32_t bm[kUnionWords];
+    __shared__ uint32_t base[kUnionWords / kUnionBase];
+    __shared__ int64_t tmp[512 / 64 + 1];
+    const int nwords = (int)((num_cols + 31) / 32);
+    const int nbase = (nwords + kUnionBase - 1) / kUnionBase;
+    for (int64_t q = blockIdx.x; q < Q; q += gridDim.x) {  // uniform over the work-group
+        int64_t x0, x1;
+        union_bitmap(win_off, W, T, cols, tc, num_cols, G, q, bm, nwords, &x0, &x1);
+        {  // bases: each thread a contiguous run of entries, one block scan
+            const int E = (nbase + 511) / 512;
+            const int a0 = min((int)threadIdx.x * E, nbase), a1 = min(a0 + E, nbase);
+            int sum = 0;
+            for (int b = a0; b < a1; ++b)
+                for (int k = 0; k < kUnionBase; ++k)
+                    if (b * kUnionBase + k < nwords) sum += __popc(bm[b * kUnionBase + k]);
+            int64_t tot;
+            int run = (int)(block_incl_scan<512>(sum, tmp, &tot) - sum);
+            for (int b = a0; b < a1; ++b) {
+                base[b] = (uint32_t)run;
+                for (int k = 0; k < kUnionBase; ++k)
+                    if (b * kUnionBase + k < nwords) run += __popc(bm[b * kUnionBase + k]);
+            }
+        }
+        __syncthreads();
+        const int64_t s16 = goff[q] * 16;  // the group's first slot position
+        auto place = [&](int32_t c) -> uint32_t {
+            const int wd = c >> 5;
+            uint32_t p = base[wd / kUnionBase] + __popc(bm[wd] & ((1u << (c & 31)) - 1u));
+            for (int k = wd - wd % kUnionBase; k < wd; ++k) p += __popc(bm[k]);
+            return p;
+        };
+        // the union's columns at their places
+        for (int x = threadIdx.x; x < nwords; x += 512) {
+            uint32_t v = bm[x];
+            while (v) {
+                const int b = __ffs(v) - 1;
+                v &= v - 1;
+                const int32_t c = x * 32 + b;
+                gcols[s16 + place(c)] = c;
+            }
+        }
+        // every valid slot's (slab, position)
+        for (int64_t x = x0 + threadIdx.x; x < x1; x += 512) {
+            const int32_t c = cols[x];
+            if (c >= 0 && (int64_t)c < num_cols) pos[x] = (uint32_t)(s16 + place(c));
+        }
+        __syncthreads();  // the bitmap is rewritten for the next group
+    }
+}
+
 __global__ void grp_sub_count_kernel(const uint32_t* __restrict__ hdr, int64_t nsub, int32_t* __restrict__ scnt) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nsub) return;
@@ -390,7 +494,14 @@ extern "C" int grws_group_tiles_count(const grws_bcsr* A, int64_t num_cols, int3
     GRWS_TRY(fill_i64(w.glast, s.Q + 1, 0, stream));
     GRWS_TRY(fill_i64(w.stats, 4, 0, stream));
     w.alt = false;
-    if (s.n > 0) {
+    const bool uni = num_cols <= kUnionCols;  // union bitmaps instead of the sort (the fill decides alike)
+    if (s.n > 0 && uni) {
+        hipLaunchKernelGGL(grp_union_count_kernel, dim3((unsigned)std::min<int64_t>(s.Q, 4096)), dim3(512), 0, stream,
+                           A->window_offset, A->num_windows, A->num_tiles, A->col_indices, tc, num_cols, group_size,
+                           s.Q, w.gslabs, w.stats);
+        GRWS_LAUNCH_CHECK();
+    }
+    if (s.n > 0 && !uni) {
         // each tile's window, in pos (the fill's array, unused until then)
         int32_t* twin = reinterpret_cast<int32_t*>(w.pos);
         GRWS_TRY(fill_i32(twin, A->num_tiles, 0, stream));
@@ -408,6 +519,8 @@ extern "C" int grws_group_tiles_count(const grws_bcsr* A, int64_t num_cols, int3
         hipLaunchKernelGGL(grp_bounds_kernel, dim3(grid_for(s.n)), dim3(kBlk), 0, stream, k, s.n, vbit, s.cbits,
                            w.uflag, w.uidx, w.gfirst, w.glast);
         GRWS_LAUNCH_CHECK();
+    }
+    if (s.n > 0) {
         if ((reinterpret_cast<uintptr_t>(A->values) & 15) == 0) {
             const int64_t nch = A->num_tiles * 2 * tc;
             const unsigned cgrid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((nch + 255) / 256, 16384));
@@ -420,9 +533,11 @@ extern "C" int grws_group_tiles_count(const grws_bcsr* A, int64_t num_cols, int3
         }
         GRWS_LAUNCH_CHECK();
     }
-    hipLaunchKernelGGL(grp_slabs_kernel, dim3(grid_for(s.Q)), dim3(kBlk), 0, stream, w.gfirst, w.glast, s.Q,
-                       w.gslabs, w.stats);
-    GRWS_LAUNCH_CHECK();
+    if (!uni || s.n == 0) {
+        hipLaunchKernelGGL(grp_slabs_kernel, dim3(grid_for(s.Q)), dim3(kBlk), 0, stream, w.gfirst, w.glast, s.Q,
+                           w.gslabs, w.stats);
+        GRWS_LAUNCH_CHECK();
+    }
     GRWS_TRY(scan_i32_to_i64(w.gslabs, w.goff, s.Q, false, w.scan_ws, w.scan_bytes, stream));
     int64_t h[3] = {0, 0, 0};
     GRWS_HIP(hipMemcpyAsync(&h[0], w.goff + s.Q, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
@@ -471,8 +586,14 @@ extern "C" int grws_group_tiles_fill(const grws_bcsr* A, int64_t num_cols, int32
     GRWS_TRY(fill_i32(col_indices, num_slabs * 16, -1, stream));
     GRWS_TRY(fill_bytes_zero(header, (size_t)nsub * 12 * sizeof(uint32_t), stream));
     if (s.n == 0) return GRWS_OK;
-    hipLaunchKernelGGL(grp_place_kernel, dim3(grid_for(s.n)), dim3(kBlk), 0, stream, k, v, s.n, vbit, s.cbits,
-                       w.uflag, w.uidx, w.gfirst, w.goff, w.pos, col_indices);
+    if (num_cols <= kUnionCols) {  // as the count decided
+        hipLaunchKernelGGL(grp_union_fill_kernel, dim3((unsigned)std::min<int64_t>(s.Q, 4096)), dim3(512), 0, stream,
+                           A->window_offset, A->num_windows, A->num_tiles, A->col_indices, tc, num_cols, group_size,
+                           s.Q, w.goff, w.pos, col_indices);
+    } else {
+        hipLaunchKernelGGL(grp_place_kernel, dim3(grid_for(s.n)), dim3(kBlk), 0, stream, k, v, s.n, vbit, s.cbits,
+                           w.uflag, w.uidx, w.gfirst, w.goff, w.pos, col_indices);
+    }
     GRWS_LAUNCH_CHECK();
     const uint16_t* vals = static_cast<const uint16_t*>(A->values);
     // each tile's window, in uflag (spent once the slots are placed)

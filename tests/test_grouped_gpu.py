@@ -95,6 +95,29 @@ def test_grouped_layout_restates_a(cuda_device, G, tc, vdt):
     assert gt.slot_ratio < 0.9
 
 
+@pytest.mark.parametrize("G", [2, 4])
+def test_grouped_union_bitmap_matches_sort(cuda_device, G):
+    """Graphs of at most 2^18 columns build their groups' unions from LDS
+    bitmaps, wider ones by a sort: the same layout bit for bit.  The columns
+    are shifted to end at 2^18 - 1 (the bitmap's last bit), then the same
+    arrays are declared 2^18 + 1 columns wide (the sort)."""
+    print(f"case grouped union bitmap vs sort G={G}", flush=True)
+    g, A = _graph(cuda_device, torch.float16, 16, scale=0.002)
+    shift = (1 << 18) - A.num_cols
+    cols = A.original_col_indices.clone()
+    cols[cols >= 0] += shift
+    a = ops.group_tiles(A.window_offset, cols, A.values_condensed, 16, 1 << 18, group_size=G,
+                        max_ratio=1.0, max_skew=1e9)
+    b = ops.group_tiles(A.window_offset, cols, A.values_condensed, 16, (1 << 18) + 1, group_size=G,
+                        max_ratio=1.0, max_skew=1e9)
+    assert a is not None and b is not None
+    for name in ("group_offset", "col_indices", "header", "values"):
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+    Da = _dense_from_grouped(a, A.num_windows, 1 << 18)
+    np.testing.assert_array_equal(Da[:, shift:], _dense_from_bcsr(A))
+    assert not Da[:, :shift].any()
+
+
 def _oracle_check(A, X, Y, R=None):
     vq = A.values_condensed.double().cpu().numpy()
     Yr, Ya = oracle.bcsr_spmm(A.window_offset.cpu().numpy(), A.original_col_indices.cpu().numpy(), vq, 16,
