@@ -388,6 +388,96 @@ __global__ __launch_bounds__(512) void grp_union_fill_kernel(const int64_t* __re
     }
 }
 
+// The masks and the values with each lane's PER slots (PER = 16 tc / 64: one
+// row, PER consecutive columns) read by one vector load each of values,
+// columns and positions (values 8-byte aligned at PER 4, 4-byte at PER 2;
+// the host checks), then every slot's header words loaded together.
+template <int PER>
+struct SlotVecs {
+    uint32_t v[PER];
+    int32_t c[PER];
+    uint32_t p[PER];
+};
+template <int PER>
+__device__ __forceinline__ SlotVecs<PER> load_slots(const int32_t* __restrict__ cols, const uint16_t* __restrict__ vals,
+                                                    const uint32_t* __restrict__ pos, int64_t t, int tc, int lane) {
+    const int slot0 = lane * PER, r = slot0 / tc, c0 = slot0 % tc;
+    SlotVecs<PER> o;
+    if constexpr (PER == 4) {
+        const uint2 vv = *reinterpret_cast<const uint2*>(vals + (t * 16 + r) * tc + c0);
+        const int4 cc = *reinterpret_cast<const int4*>(cols + t * tc + c0);
+        const uint4 pp = *reinterpret_cast<const uint4*>(pos + t * tc + c0);
+        o.v[0] = vv.x & 0xffffu; o.v[1] = vv.x >> 16; o.v[2] = vv.y & 0xffffu; o.v[3] = vv.y >> 16;
+        o.c[0] = cc.x; o.c[1] = cc.y; o.c[2] = cc.z; o.c[3] = cc.w;
+        o.p[0] = pp.x; o.p[1] = pp.y; o.p[2] = pp.z; o.p[3] = pp.w;
+    } else {
+        const uint32_t vv = *reinterpret_cast<const uint32_t*>(vals + (t * 16 + r) * tc + c0);
+        const int2 cc = *reinterpret_cast<const int2*>(cols + t * tc + c0);
+        const uint2 pp = *reinterpret_cast<const uint2*>(pos + t * tc + c0);
+        o.v[0] = vv & 0xffffu; o.v[1] = vv >> 16;
+        o.c[0] = cc.x; o.c[1] = cc.y;
+        o.p[0] = pp.x; o.p[1] = pp.y;
+    }
+    return o;
+}
+
+template <int PER>
+__global__ __launch_bounds__(256) void grp_mask_vec_kernel(const int32_t* __restrict__ twin,
+                                                           const int32_t* __restrict__ cols,
+                                                           const uint16_t* __restrict__ vals, int64_t T, int tc,
+                                                           int64_t num_cols, int G, const uint32_t* __restrict__ pos,
+                                                           uint32_t* __restrict__ hdr) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;  // uniform per wave
+    const int lane = threadIdx.x & 63;
+    const int64_t w = twin[t];
+    const SlotVecs<PER> sv = load_slots<PER>(cols, vals, pos, t, tc, lane);
+    const int r = (lane * PER) / tc;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        if (sv.c[k] < 0 || (int64_t)sv.c[k] >= num_cols || sv.v[k] == 0) continue;
+        const int64_t sub = (int64_t)(sv.p[k] >> 4) * G + (w % G);
+        const int bit = (r & 3) * 16 + (int)(sv.p[k] & 15u);
+        atomicOr(&hdr[sub * 12 + (r >> 2) * 3 + (bit >> 5)], 1u << (bit & 31));
+    }
+}
+
+template <int PER>
+__global__ __launch_bounds__(256) void grp_values_vec_kernel(const int32_t* __restrict__ twin,
+                                                             const int32_t* __restrict__ cols,
+                                                             const uint16_t* __restrict__ vals, int64_t T, int tc,
+                                                             int64_t num_cols, int G, const uint32_t* __restrict__ pos,
+                                                             const uint32_t* __restrict__ hdr,
+                                                             uint16_t* __restrict__ out, int64_t num_values) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;  // uniform per wave
+    const int lane = threadIdx.x & 63;
+    const int64_t w = twin[t];
+    const SlotVecs<PER> sv = load_slots<PER>(cols, vals, pos, t, tc, lane);
+    const int r = (lane * PER) / tc;
+    bool ok[PER];
+    uint32_t h0[PER], h1[PER], h2[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        ok[k] = sv.c[k] >= 0 && (int64_t)sv.c[k] < num_cols && sv.v[k] != 0;
+        // an invalid slot's position was never written: no address from it
+        const int64_t sub = ok[k] ? (int64_t)(sv.p[k] >> 4) * G + (w % G) : 0;
+        const uint32_t* h = hdr + sub * 12 + (r >> 2) * 3;
+        h0[k] = ok[k] ? h[0] : 0u;
+        h1[k] = ok[k] ? h[1] : 0u;
+        h2[k] = ok[k] ? h[2] : 0u;
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        if (!ok[k]) continue;
+        const int bit = (r & 3) * 16 + (int)(sv.p[k] & 15u);
+        const uint64_t m = ((uint64_t)h1[k] << 32) | h0[k];
+        const uint64_t below = bit ? (m & ((1ull << bit) - 1ull)) : 0ull;
+        const int64_t at = (int64_t)h2[k] + __popcll(below);
+        if (at < num_values) out[at] = (uint16_t)sv.v[k];
+    }
+}
+
 __global__ void grp_sub_count_kernel(const uint32_t* __restrict__ hdr, int64_t nsub, int32_t* __restrict__ scnt) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nsub) return;
@@ -602,17 +692,37 @@ extern "C" int grws_group_tiles_fill(const grws_bcsr* A, int64_t num_cols, int32
     hipLaunchKernelGGL(grp_tile_window_kernel, dim3(grid_for(A->num_windows, 1) < 8192u ? grid_for(A->num_windows, 1) : 8192u),
                        dim3(256), 0, stream, A->window_offset, A->num_windows, A->num_tiles, twin);
     GRWS_LAUNCH_CHECK();
-    hipLaunchKernelGGL(grp_mask_kernel, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, twin, A->col_indices,
-                       vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos, header);
+    // vector loads when the values are 8-byte aligned (tc 16) or 4-byte (tc 8)
+    // and the columns 16-byte aligned
+    const bool vec = (reinterpret_cast<uintptr_t>(vals) & (tc == 16 ? 7 : 3)) == 0 &&
+                     (reinterpret_cast<uintptr_t>(A->col_indices) & 15) == 0;
+    if (vec && tc == 16)
+        hipLaunchKernelGGL(grp_mask_vec_kernel<4>, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, twin,
+                           A->col_indices, vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos, header);
+    else if (vec)
+        hipLaunchKernelGGL(grp_mask_vec_kernel<2>, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, twin,
+                           A->col_indices, vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos, header);
+    else
+        hipLaunchKernelGGL(grp_mask_kernel, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, twin,
+                           A->col_indices, vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos, header);
     GRWS_LAUNCH_CHECK();
     hipLaunchKernelGGL(grp_sub_count_kernel, dim3(grid_for(nsub)), dim3(kBlk), 0, stream, header, nsub, w.scnt);
     GRWS_LAUNCH_CHECK();
     GRWS_TRY(scan_i32_to_i64(w.scnt, w.soff, nsub, false, w.scan_ws, w.scan_bytes, stream));
     hipLaunchKernelGGL(grp_sub_start_kernel, dim3(grid_for(nsub)), dim3(kBlk), 0, stream, header, nsub, w.soff);
     GRWS_LAUNCH_CHECK();
-    hipLaunchKernelGGL(grp_values_kernel, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, twin, A->col_indices,
-                       vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos, header, static_cast<uint16_t*>(values),
-                       num_values);
+    if (vec && tc == 16)
+        hipLaunchKernelGGL(grp_values_vec_kernel<4>, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, twin,
+                           A->col_indices, vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos, header,
+                           static_cast<uint16_t*>(values), num_values);
+    else if (vec)
+        hipLaunchKernelGGL(grp_values_vec_kernel<2>, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, twin,
+                           A->col_indices, vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos, header,
+                           static_cast<uint16_t*>(values), num_values);
+    else
+        hipLaunchKernelGGL(grp_values_kernel, dim3(grid_for(A->num_tiles, 4)), dim3(256), 0, stream, twin,
+                           A->col_indices, vals, A->num_tiles, tc, num_cols, (int)group_size, w.pos, header,
+                           static_cast<uint16_t*>(values), num_values);
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }
