@@ -138,6 +138,52 @@ def test_csr_build_window_paths(cuda_device, hub, tc, vdt):
     _eq(dv, torch.from_numpy(ov.astype(np.float32)).to(vdt))
 
 
+def _boundary_csr(seed: int):
+    """One 16-row window per size class edge -- 2,048 / 2,049, 8,192 / 8,193,
+    16,384 / 16,385 edges -- each with a column span exactly filling or just
+    past its class's bitmap (2^16, 2^18, 2^19 columns), duplicates included."""
+    rng = np.random.default_rng(seed)
+    # (edges, columns spanned): a span of 2^k columns fills a 2^k-bit bitmap
+    # exactly, 2^k + 1 takes the class's radix sort instead
+    sizes = [(2048, 1 << 16), (2048, (1 << 16) + 1), (2049, 1 << 18), (8192, (1 << 18) + 1),
+             (8193, 1 << 19), (16384, (1 << 19) + 1), (16385, 1 << 19), (8192, 1 << 18)]
+    n_c = (1 << 19) + 8
+    per_row = []
+    for m, span in sizes:
+        base = int(rng.integers(0, n_c - span))
+        c = base + rng.integers(0, span, m)
+        c[0], c[1] = base, base + span - 1  # the span's two ends
+        c[2:40] = c[40:78]  # duplicates
+        split = np.sort(rng.integers(0, m, 15))
+        per_row += [p.astype(np.int32) for p in np.split(c, split)]
+    rp = np.zeros(len(per_row) + 1, np.int64)
+    rp[1:] = np.cumsum([len(c) for c in per_row])
+    cols = np.concatenate(per_row)
+    vals = rng.standard_normal(cols.size).astype(np.float32)
+    return len(per_row), n_c, rp, cols, vals
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_build_size_and_span_boundaries(cuda_device, transpose):
+    """Windows at every size-class edge of the window-by-window build, with
+    column spans at the edges of each class's bitmap: equal to the oracle's
+    converter (transposed: over A^T)."""
+    print(f"case size/span boundaries transpose={transpose}", flush=True)
+    n_r, n_c, rp, cols, vals = _boundary_csr(seed=77)
+    if transpose:
+        ow, oc, ov = _oracle_transposed(n_r, n_c, rp, cols, vals, 16)
+    else:
+        ow, oc, ov = oracle.csr_to_bcsr(n_r, rp, cols, vals, 16, 16)
+    dw, dc, dv = builder.csr_to_bcsr_device(n_r, n_c, torch.from_numpy(rp).to(cuda_device),
+                                            torch.from_numpy(cols).to(cuda_device),
+                                            torch.from_numpy(vals).to(cuda_device), tile_cols=16,
+                                            transpose=transpose)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dw.cpu().numpy(), ow)
+    np.testing.assert_array_equal(dc.cpu().numpy(), oc)
+    np.testing.assert_array_equal(dv.cpu().numpy(), ov.astype(np.float32))
+
+
 def _oracle_transposed(n_r, n_c, rp, cols, vals, tc):
     """BCSR of A^T by the oracle's converter over A^T's CSR, whose rows list
     their edges in input order (a stable sort by column), so duplicate
