@@ -13,13 +13,16 @@
 // sub-tiles.
 //
 // Build, two calls (one host sync, in the first):
-//   count: key (group, column) of every tile slot with a valid column,
-//          stable radix sort, distinct keys ranked -> columns per group ->
-//          slabs per group -> group_offset (kept in the workspace); the
-//          nonzero value count; the longest group.
-//   fill:  union columns, every slot's (slab, position), masks by atomic OR,
-//          value counts -> scan -> group starts, then every value placed by
-//          the popcount of the mask bits below it (deterministic).
+//   count: the union's size per group -> slabs per group -> group_offset
+//          (kept in the workspace); the nonzero value count; the longest
+//          group.  Graphs of at most 2^18 columns: one work-group per group
+//          sets a bit per valid slot in an LDS bitmap of all the columns and
+//          counts them; wider graphs: the (group, column) key of every valid
+//          slot, a stable radix sort, distinct keys ranked.
+//   fill:  union columns and every slot's (slab, position) (the bitmap again,
+//          its popcount bases giving places; or the sorted ranks), masks by
+//          atomic OR, value counts -> scan -> group starts, then every value
+//          placed by the popcount of the mask bits below it (deterministic).
 #include "grws_internal.h"
 
 namespace grws {
