@@ -18,6 +18,8 @@
 //   column) edges keep input order through the stable sort; the last one
 //   wins, as in the reference's plain store (convert_wrapper.cpp:174).
 // The transposed build swaps the roles of rows and columns in the key.
+#include <mutex>
+
 #include "grws_internal.h"
 
 namespace grws {
@@ -1280,6 +1282,49 @@ int report_input_error(int32_t e, const char* who) {
     return GRWS_OK;
 }
 
+// Windows over kWinCap edges take one work-group each, a long serial chain
+// that leaves most of the GPU idle; on a second stream they run beside the
+// size classes' kernels instead of after them.  One such stream per device,
+// created on first use with the default priority; each call forks from the
+// caller's stream and joins back into it through events of its own, so
+// concurrent calls stay ordered.  Without a device index in range the side
+// work stays on the caller's stream.
+constexpr int kSideDevices = 64;
+
+int side_fork(hipStream_t main, hipStream_t* side) {
+    *side = main;
+    int dev = 0;
+    GRWS_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kSideDevices) return GRWS_OK;
+    static std::mutex mu;
+    static hipStream_t streams[kSideDevices] = {};
+    hipStream_t s = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!streams[dev]) GRWS_HIP(hipStreamCreateWithFlags(&streams[dev], hipStreamNonBlocking));
+        s = streams[dev];
+    }
+    hipEvent_t ev;
+    GRWS_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    hipError_t e = hipEventRecord(ev, main);
+    if (e == hipSuccess) e = hipStreamWaitEvent(s, ev, 0);
+    (void)hipEventDestroy(ev);
+    GRWS_HIP(e);
+    *side = s;
+    return GRWS_OK;
+}
+
+int side_join(hipStream_t main, hipStream_t side) {
+    if (side == main) return GRWS_OK;
+    hipEvent_t ev;
+    GRWS_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    hipError_t e = hipEventRecord(ev, side);
+    if (e == hipSuccess) e = hipStreamWaitEvent(main, ev, 0);
+    (void)hipEventDestroy(ev);
+    GRWS_HIP(e);
+    return GRWS_OK;
+}
+
 }  // namespace
 }  // namespace grws
 
@@ -1395,6 +1440,15 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
             uint64_t* rk = kalt ? w.ka : w.kb;
             ucol = reinterpret_cast<int32_t*>(kalt ? w.va : w.vb);
             if (!kalt) GRWS_TRY(fill_i32(w.err + 2, 1, 2, stream));
+            hipStream_t side = stream;
+            if (nbig > 0) {
+                GRWS_TRY(side_fork(stream, &side));
+                hipLaunchKernelGGL((win_sort_big_kernel<true>), dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, side,
+                                   nullptr, nullptr, nullptr, tk, tv, kwbits, nnz, s.R, w.blist, nbig,
+                                   s.C, (int)tile_cols, reinterpret_cast<uint32_t*>(w.uidx),
+                                   reinterpret_cast<uint32_t*>(w.uflag), rk, ucol, w.wstart, w.wend, w.wtiles, w.err);
+                GRWS_LAUNCH_CHECK();
+            }
             hipLaunchKernelGGL((win_sort_kernel<2048, 256, true>), dim3(wgs), dim3(256), 0, stream, nullptr, nullptr,
                                nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols, rk, ucol, w.wstart, w.wend,
                                w.wtiles, w.err);
@@ -1407,14 +1461,18 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
                                stream, nullptr, nullptr, nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols,
                                rk, ucol, w.wstart, w.wend, w.wtiles, w.err);
             GRWS_LAUNCH_CHECK();
+            GRWS_TRY(side_join(stream, side));
+        } else {
+            hipStream_t side = stream;
             if (nbig > 0) {
-                hipLaunchKernelGGL((win_sort_big_kernel<true>), dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, stream,
-                                   nullptr, nullptr, nullptr, tk, tv, kwbits, nnz, s.R, w.blist, nbig,
-                                   s.C, (int)tile_cols, reinterpret_cast<uint32_t*>(w.uidx),
-                                   reinterpret_cast<uint32_t*>(w.uflag), rk, ucol, w.wstart, w.wend, w.wtiles, w.err);
+                GRWS_TRY(side_fork(stream, &side));
+                hipLaunchKernelGGL((win_sort_big_kernel<false>), dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, side,
+                                   row_ptr, cols, values, nullptr, nullptr, 0, nnz, s.R, w.blist,
+                                   nbig, num_cols, (int)tile_cols, reinterpret_cast<uint32_t*>(w.uidx),
+                                   reinterpret_cast<uint32_t*>(w.uflag), w.ka, ucol, w.wstart, w.wend, w.wtiles,
+                                   w.err);
                 GRWS_LAUNCH_CHECK();
             }
-        } else {
             hipLaunchKernelGGL((win_sort_kernel<2048, 256, false>), dim3(wgs), dim3(256), 0, stream, row_ptr, cols,
                                values, nullptr, nullptr, 0, nnz, s.R, s.W, num_cols, (int)tile_cols, w.ka, ucol,
                                w.wstart, w.wend, w.wtiles, w.err);
@@ -1427,14 +1485,7 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
                                stream, row_ptr, cols, values, nullptr, nullptr, 0, nnz, s.R, s.W, num_cols,
                                (int)tile_cols, w.ka, ucol, w.wstart, w.wend, w.wtiles, w.err);
             GRWS_LAUNCH_CHECK();
-            if (nbig > 0) {
-                hipLaunchKernelGGL((win_sort_big_kernel<false>), dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, stream,
-                                   row_ptr, cols, values, nullptr, nullptr, 0, nnz, s.R, w.blist,
-                                   nbig, num_cols, (int)tile_cols, reinterpret_cast<uint32_t*>(w.uidx),
-                                   reinterpret_cast<uint32_t*>(w.uflag), w.ka, ucol, w.wstart, w.wend, w.wtiles,
-                                   w.err);
-                GRWS_LAUNCH_CHECK();
-            }
+            GRWS_TRY(side_join(stream, side));
         }
     }
     bool alt = false;
@@ -1516,9 +1567,15 @@ extern "C" int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_c
     const int aligned = (reinterpret_cast<uintptr_t>(values) & 15) == 0;
     const uint64_t* wrec = path == 2 ? w.kb : w.ka;
     const int32_t* wcol = reinterpret_cast<const int32_t*>(path == 2 ? w.vb : w.va);
+    hipStream_t side = stream;
+    if (nbig > 0) GRWS_TRY(side_fork(stream, &side));
 #define GRWS_BUILD_FILL(VT)                                                                                        \
     if (path != 0)                                                                                                 \
     {                                                                                                              \
+        if (nbig > 0)                                                                                              \
+            hipLaunchKernelGGL(win_fill_big_kernel<VT>, dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, side,        \
+                               wrec, wcol, w.wstart, w.wend, window_offset, w.blist, nbig, (int)tile_cols,        \
+                               col_indices, values, aligned, w.err);                                               \
         hipLaunchKernelGGL((win_fill_kernel<2048, 256, VT>), dim3((unsigned)std::min<int64_t>(s.W, 16384)),     \
                            dim3(256), 0, stream, wrec, wcol, w.wstart, w.wend, window_offset, s.W, (int)tile_cols, \
                            col_indices, values, aligned, w.err);                                                   \
@@ -1528,10 +1585,6 @@ extern "C" int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_c
         hipLaunchKernelGGL((win_fill_kernel<16384, kWinBlk, VT>), dim3(std::min<unsigned>(wg, 512)), dim3(kWinBlk), \
                            0, stream, wrec, wcol, w.wstart, w.wend, window_offset, s.W, (int)tile_cols,            \
                            col_indices, values, aligned, w.err);                                                   \
-        if (nbig > 0)                                                                                              \
-            hipLaunchKernelGGL(win_fill_big_kernel<VT>, dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, stream,      \
-                               wrec, wcol, w.wstart, w.wend, window_offset, w.blist, nbig, (int)tile_cols,        \
-                               col_indices, values, aligned, w.err);                                               \
     } else                                                                                                         \
         hipLaunchKernelGGL(build_scatter_kernel<VT>, dim3(grid_for(nnz)), dim3(kBlk), 0, stream, k, v, nnz, s.cbits, \
                            w.uflag, w.uidx, w.wstart, window_offset, (int)tile_cols, col_indices, values, w.err)
@@ -1542,6 +1595,7 @@ extern "C" int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_c
     }
 #undef GRWS_BUILD_FILL
     GRWS_LAUNCH_CHECK();
+    GRWS_TRY(side_join(stream, side));
     return GRWS_OK;
 }
 

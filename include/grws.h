@@ -11,10 +11,14 @@
  *     last failure on the calling thread is returned by grws_last_error();
  *   - never allocates device memory: outputs and workspaces are provided by
  *     the caller, sized by the matching *_bytes / *_capacity query;
- *   - all device work is enqueued on `stream`; entry points that must return
- *     a data-dependent size to the host say so and synchronise that stream;
- *   - no global mutable state: calls on different streams and threads are
- *     independent (re-entrant).
+ *   - all device work is ordered on `stream`; entry points that must return
+ *     a data-dependent size to the host say so and synchronise that stream.
+ *     The BCSR build runs its windows of over 16,384 edges on a second
+ *     stream of the device (one per device, made on first use), forked from
+ *     `stream` and joined back into it by events before the call returns;
+ *   - calls on different streams and threads are independent (re-entrant):
+ *     the only global state is that per-device stream and the no-alloc
+ *     entry point's device array.
  *
  * Tile geometry: tile_rows is 16 (one row window); tile_cols is 8 (the
  * reference default, config.h:16-18) or 16 (MFMA-native).
