@@ -138,6 +138,55 @@ def test_csr_build_window_paths(cuda_device, hub, tc, vdt):
     _eq(dv, torch.from_numpy(ov.astype(np.float32)).to(vdt))
 
 
+def test_big_window_builds_on_concurrent_streams(cuda_device):
+    """Windows above 16,384 edges run on one extra stream per device, forked
+    from and joined back into the caller's stream.  Two threads, each on a
+    stream of its own, build graphs with such windows at the same time (a
+    CSR build and a transposed one, three times each): every result equals
+    the oracle's converter."""
+    import threading
+    print("case big windows on concurrent streams", flush=True)
+    n_r, n_c, rp, cols, vals = _window_case_csr(True, seed=51)
+    want_csr = oracle.csr_to_bcsr(n_r, rp, cols, vals, 16, 16)
+    # transposed: 17,000 rows, each with an edge to column 3 (a window of A^T above 16,384 edges) and a random one
+    rng = np.random.default_rng(5)
+    t_rows = 17000
+    t_cols = np.stack([np.full(t_rows, 3), rng.integers(0, n_c, t_rows)], 1).reshape(-1).astype(np.int32)
+    t_vals = rng.standard_normal(t_cols.size).astype(np.float32)
+    t_rp = 2 * np.arange(t_rows + 1, dtype=np.int64)
+    want_t = _oracle_transposed(t_rows, n_c, t_rp, t_cols, t_vals, 16)
+    got, failures = {}, []
+
+    def run(name, nr, rp_, cols_, vals_, transpose):
+        try:
+            s = torch.cuda.Stream(device=cuda_device)
+            with torch.cuda.stream(s):
+                args = [torch.from_numpy(a).to(cuda_device, non_blocking=False) for a in (rp_, cols_, vals_)]
+                out = []
+                for _ in range(3):
+                    w, c, v = builder.csr_to_bcsr_device(nr, n_c, *args, tile_cols=16,
+                                                         values_dtype=torch.float32, transpose=transpose)
+                    out.append((w, c, v))
+                s.synchronize()
+                got[name] = [(w.cpu().numpy(), c.cpu().numpy(), v.cpu().numpy()) for w, c, v in out]
+        except BaseException as e:  # reported by the main thread
+            failures.append(e)
+
+    threads = [threading.Thread(target=run, args=("csr", n_r, rp, cols, vals, False)),
+               threading.Thread(target=run, args=("t", t_rows, t_rp, t_cols, t_vals, True))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=90)
+        assert not t.is_alive(), "a build thread did not finish"
+    assert not failures, failures
+    for name, want in (("csr", want_csr), ("t", want_t)):
+        for w, c, v in got[name]:
+            np.testing.assert_array_equal(w, want[0])
+            np.testing.assert_array_equal(c, want[1])
+            np.testing.assert_array_equal(v, want[2].astype(np.float32))
+
+
 def _boundary_csr(seed: int):
     """One 16-row window per size class edge -- 2,048 / 2,049, 8,192 / 8,193,
     16,384 / 16,385 edges -- each with a column span exactly filling or just
