@@ -1287,7 +1287,8 @@ int report_input_error(int32_t e, const char* who) {
 // size classes' kernels instead of after them.  One such stream per device,
 // created on first use with the default priority; each call forks from the
 // caller's stream and joins back into it through events of its own, so
-// concurrent calls stay ordered.  Without a device index in range the side
+// concurrent calls stay ordered.  When the caller's stream belongs to another
+// device than the current one, or the device index is out of range, the side
 // work stays on the caller's stream.
 constexpr int kSideDevices = 64;
 
@@ -1295,7 +1296,12 @@ int side_fork(hipStream_t main, hipStream_t* side) {
     *side = main;
     int dev = 0;
     GRWS_HIP(hipGetDevice(&dev));
-    if (dev < 0 || dev >= kSideDevices) return GRWS_OK;
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(main, &sdev) != hipSuccess) {
+        (void)hipGetLastError();  // clears the failed query's error
+        return GRWS_OK;
+    }
+    if (sdev != dev || dev < 0 || dev >= kSideDevices) return GRWS_OK;
     static std::mutex mu;
     static hipStream_t streams[kSideDevices] = {};
     hipStream_t s = nullptr;
