@@ -284,22 +284,29 @@ class BCSRGraph:
         this graph's second such product (with the group size that suits
         that product's width n_cols, core.ops.group_size_for) and kept while
         the arrays are unchanged; None when grouping is off, does not apply,
-        or would not pay on this graph (decided once per graph state)."""
+        or would not pay on this graph (decided once per graph state).
+
+        One layout is cached per group size: products of different widths
+        that want different group sizes (the 608-column features and the
+        256-column hidden layers) each get their own, built on the second
+        product of that group size."""
         from ..core import ops as _ops
         if (not _ops.GROUPED or not _ops.PACK_TILES or getattr(self, "refilled", False)
                 or self.values_condensed.dtype not in (torch.float16, torch.bfloat16)):
             return None
         from ..core.ops import TensorKey
+        gs = int(_ops.group_size_for(n_cols))
         arrays = (self.window_offset, self.original_col_indices, self.values_condensed)
-        ent = self._cache.get("grouped")
+        slot = ("grouped", gs)
+        ent = self._cache.get(slot)
         if ent is None or not ent[0].matches(arrays, (int(num_cols),)):
-            self._cache["grouped"] = (TensorKey(arrays, (int(num_cols),)), 1, None)
+            self._cache[slot] = (TensorKey(arrays, (int(num_cols),)), 1, None)
             return None
         key, calls, g = ent
         if g is None and calls == 1:
             g = _ops.group_tiles(self.window_offset, self.original_col_indices, self.values_condensed,
-                                 self.tile_cols, int(num_cols), group_size=_ops.group_size_for(n_cols)) or False
-            self._cache["grouped"] = (key, 2, g)
+                                 self.tile_cols, int(num_cols), group_size=gs) or False
+            self._cache[slot] = (key, 2, g)
         return g or None
 
     def _gather_input(self, x: torch.Tensor) -> torch.Tensor:

@@ -497,28 +497,44 @@ def test_reindex_matches_oracle(cuda_device, vdt):
 def test_build_full_size_forward_and_transposed(cuda_device, cfg):
     """BASELINE configs c3 (windows of up to 8,246 edges) and c4 (667
     windows above 16,384 edges, built each by one work-group from global
-    scratch) at full size: the device build equals the host converter, and
-    the transposed build equals the device build of A^T's CSR (made by a
-    stable sort of the edges by column)."""
+    scratch) at full size: the device build equals the oracle's converter
+    (oracle.csr_to_bcsr, pinned to the reference's compiled
+    convert_wrapper.cpp in tests/test_oracle.py), and the transposed build
+    equals the oracle's converter on A^T's CSR (the edges put in column
+    order by a stable host sort)."""
     print(f"case {cfg} full-size build", flush=True)
     g = synth.config_graph(cfg, device=cuda_device)
     n = g.num_nodes
-    hw, hc, hv = core.csr_to_bcsr_cpu(n, g.row_ptr.cpu(), g.col_idx.cpu(), g.values.cpu(), 16, 16)
+    rp, ci, va = g.row_ptr.cpu().numpy(), g.col_idx.cpu().numpy(), g.values.cpu().numpy()
     dw, dc, dv = builder.csr_to_bcsr_device(n, n, g.row_ptr, g.col_idx, g.values, tile_cols=16)
-    _eq(dw, hw)
-    _eq(dc, hc)
-    _eq(dv, hv)
-    del hw, hc, hv, dw, dc, dv
+    ow, oc, ov = oracle.csr_to_bcsr(n, rp, ci, va, 16, 16)
+    _eq_np(dw, ow)
+    _eq_np(dc, oc)
+    _eq_np(dv, ov)
+    del dw, dc, dv, ow, oc, ov
+    print(f"case {cfg} full-size transposed build", flush=True)
     tw, tc_, tv = builder.csr_to_bcsr_device(n, n, g.row_ptr, g.col_idx, g.values, tile_cols=16, transpose=True)
-    rows = torch.repeat_interleave(torch.arange(n, device=cuda_device, dtype=torch.int32),
-                                   torch.diff(g.row_ptr))
-    _, order = torch.sort(g.col_idx, stable=True)
-    trp = torch.zeros(n + 1, dtype=torch.int64, device=cuda_device)
-    trp[1:] = torch.cumsum(torch.bincount(g.col_idx, minlength=n), 0)
-    ew, ec, ev = builder.csr_to_bcsr_device(n, n, trp, rows[order], g.values[order], tile_cols=16)
-    _eq(tw, ew)
-    _eq(tc_, ec)
-    _eq(tv, ev)
+    order = np.argsort(ci, kind="stable")
+    rows = np.repeat(np.arange(n, dtype=np.int32), np.diff(rp))[order]
+    trp = np.zeros(n + 1, np.int64)
+    trp[1:] = np.cumsum(np.bincount(ci, minlength=n))
+    ew, ec, ev = oracle.csr_to_bcsr(n, trp, rows, va[order], 16, 16)
+    del order
+    _eq_np(tw, ew)
+    _eq_np(tc_, ec)
+    _eq_np(tv, ev)
+
+
+def _eq_np(d, o, step=1 << 26):
+    """A device array equal to an oracle array (values compared as float32:
+    the oracle carries them in float64, exactly), in chunks."""
+    assert d.numel() == o.size, (d.numel(), o.size)
+    for i in range(0, o.size, step):
+        a = d[i:i + step].cpu().numpy()
+        b = o[i:i + step].astype(a.dtype) if o.dtype != a.dtype else o[i:i + step]
+        if not np.array_equal(a, b):
+            j = i + int(np.flatnonzero(a != b)[0])
+            raise AssertionError(f"first difference at {j}: device {a[j - i]!r}, oracle {b[j - i]!r}")
 
 
 def test_build_c2_full_size(cuda_device):

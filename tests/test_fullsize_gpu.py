@@ -4,8 +4,12 @@ over every row), through the same calls bench.py times.
 
 * c3 (232,965 nodes, 114.6M nnz, f16): the headline N=608 product on X at a
   640-element pitch, default plan, chunk-major order, the dense-tile first
-  product and the packed-tile second product (bit-identical); the epoch
-  widths N=256 and N=41 (ragged); A^T G at N=256.
+  product, the 2-window grouped second product and the packed-tile product
+  (bit-identical to the dense one); the epoch widths N=256 (window by
+  window, then 4-window groups) and N=41 (ragged); A^T G at N=256 (first
+  product window by window, second on 4-window groups).  Every grouped
+  product is also compared with the window-by-window one over the whole
+  output.
 * c4 (2,449,029 nodes, 123.7M nnz, bf16): N=112 at a 128-element pitch,
   N=256 (two 128-column chunks), N=47 (ragged); A^T G at N=256.
 * c2 (169,343 nodes, 2.33M nnz): A^T G at N=128 in f16 and bf16 through the
@@ -13,7 +17,8 @@ over every row), through the same calls bench.py times.
 * c5 (111M nodes, 1.6B edges): one full-size sampling batch bit-exact
   against the host sampler driven by the same Philox draws.
 
-Tolerance (north_star): rtol 1e-2 for f16/bf16 inputs against |A| |X|.
+Tolerance (north_star): rtol 1e-2 for f16/bf16 inputs against |A| |X|,
+and the tight tier of tests/_fullsize.py (the arithmetic's own bound).
 The forward semantics follow /root/reference/core/include/spmm_tc.cuh:113-193
 (every output column computed, -1 slots skipped), the transpose :238-269
 without its atomics and 1e-9 skip, the sampling hop order
@@ -75,6 +80,7 @@ def test_c3_headline_n608_bench_path(c3, cuda_device, monkeypatch):
     torch.cuda.synchronize()
     gt = G.grouped_tiles(X.shape[0], 608)
     assert gt is not None and gt.slot_ratio < ops.GROUP_MAX_RATIO, "c3 must take the grouped tiles"
+    assert gt.group_size == 2
     print(check_forward(hg, X, Y2, RTOL, plan=plan, seed=3), flush=True)
     print(check_forward(hg, X, Y1, RTOL, plan=plan, seed=4), flush=True)
     monkeypatch.setattr(ops, "GROUPED", False)
@@ -83,27 +89,107 @@ def test_c3_headline_n608_bench_path(c3, cuda_device, monkeypatch):
     torch.cuda.synchronize()
     assert G.packed_tiles() is not None, "the packed tiles are built on the next product"
     assert torch.equal(Y1.view(torch.int16), Y3.view(torch.int16)), "packed and dense tiles differ"
+    Ya = G.spmm(X.abs())
+    torch.cuda.synchronize()
+    print("grouped vs window by window, worst of bound:", _compare_orders(G, hg, X, Ya, Y2, Y1), flush=True)
 
 
-@pytest.mark.parametrize("N", [256, 41])
-def test_c3_epoch_widths(c3, cuda_device, N):
-    print(f"case c3 N={N} f16", flush=True)
+def _record_grouped(monkeypatch):
+    """Records, for every SpMM entry point the shim calls, its name and the
+    group size of the grouped tiles it was handed (None otherwise)."""
+    from graph_rws_amd.core import ops
+    calls = []
+    real = ops.L.call
+
+    def spy(fn, *args):
+        gs = None
+        if fn == "grws_spmm_grouped":
+            gs = args[1]._obj.group_size
+        if fn.startswith("grws_spmm"):
+            calls.append((fn, gs))
+        return real(fn, *args)
+
+    monkeypatch.setattr(ops.L, "call", spy)
+    return calls
+
+
+def _compare_orders(G, hg, X, Ya_x, Yg, Yw):
+    """The grouped product Yg against the window-by-window product Yw over
+    every output element: both round the same exact sum once to f16 after
+    fp32 accumulations in different orders, so they differ by at most
+    u_out (|Yg| + |Yw|) + 2 C k 2^-24 (|A||X|) (+ subnormal and flush
+    terms), with |A||X| from the device product of A and |X| (A >= 0 on
+    these graphs)."""
+    from _fullsize import C_SUM_16, FTZ, S_OUT, U32, U_OUT, all_row_nnz
+    k = torch.from_numpy(all_row_nnz(hg)).to(Yg.device, torch.float32)[:, None]
+    ya = Ya_x.float() * (1 + 2 ** -9)
+    d = (Yg.float() - Yw.float()).abs()
+    bound = (U_OUT["f16"] * (Yg.float().abs() + Yw.float().abs()) + 2 * C_SUM_16 * U32 * k * ya
+             + 2 * (k * FTZ + S_OUT["f16"]))
+    bad = d > bound
+    assert not bool(bad.any()), f"grouped vs window by window: {int(bad.sum())} of {bad.numel()} apart"
+    return float((d / bound).max())
+
+
+def test_c3_epoch_n256_grouped_4_windows(c3, cuda_device, monkeypatch):
+    """The c3 epoch's 256-column products: the first runs window by window,
+    the second builds and reads 4-window grouped tiles (the layout the
+    epoch's hidden layers use, spmm_grp_kernel with 4 waves), both checked
+    against the oracle in both tiers, and the two compared over the whole
+    output (semantics: /root/reference/core/include/spmm_tc.cuh:113-193)."""
+    from graph_rws_amd.core import ops
+    print("case c3 N=256 f16 window by window, then 4-window groups", flush=True)
     g, G, hg = c3
-    X = synth.features(g.num_nodes, N, seed=N, device=cuda_device).half()
+    X = synth.features(g.num_nodes, 256, seed=256, device=cuda_device).half()
+    calls = _record_grouped(monkeypatch)
+    Y1 = G.spmm(X)
+    Y2 = G.spmm(X)
+    torch.cuda.synchronize()
+    gt = G.grouped_tiles(X.shape[0], 256)
+    assert gt is not None and gt.group_size == 4, "c3 at N=256 must take 4-window grouped tiles"
+    assert ("grws_spmm_grouped", 4) in calls, calls
+    print(check_forward(hg, X, Y2, RTOL, plan=G.spmm_plan(256), seed=256), flush=True)
+    Yw = Y1 if calls[0][0] != "grws_spmm_grouped" else None
+    if Yw is None:  # an earlier product made this the grouped one: force window by window
+        monkeypatch.setattr(ops, "GROUPED", False)
+        Yw = G.spmm(X)
+        monkeypatch.setattr(ops, "GROUPED", True)
+    print(check_forward(hg, X, Yw, RTOL, plan=G.spmm_plan(256), seed=257), flush=True)
+    monkeypatch.setattr(ops, "GROUPED", False)
+    Ya = G.spmm(X.abs())
+    torch.cuda.synchronize()
+    print("grouped vs window by window, worst of bound:", _compare_orders(G, hg, X, Ya, Y2, Yw), flush=True)
+
+
+def test_c3_epoch_n41(c3, cuda_device):
+    print("case c3 N=41 f16", flush=True)
+    g, G, hg = c3
+    X = synth.features(g.num_nodes, 41, seed=41, device=cuda_device).half()
     Y = G.spmm(X)
     torch.cuda.synchronize()
-    assert Y.shape == (16 * G.num_windows, N)
-    print(check_forward(hg, X, Y, RTOL, plan=G.spmm_plan(N), seed=N), flush=True)
+    assert Y.shape == (16 * G.num_windows, 41)
+    print(check_forward(hg, X, Y, RTOL, plan=G.spmm_plan(41), seed=41), flush=True)
 
 
-def test_c3_transpose_n256(c3, cuda_device):
-    print("case c3 A^T G N=256 f16", flush=True)
+def test_c3_transpose_n256(c3, cuda_device, monkeypatch):
+    """A^T G through the cached transpose, as the epoch's backward makes it:
+    the first product window by window, the second (and every later one)
+    on the transpose's own 4-window grouped tiles; both against the oracle
+    on A (/root/reference/core/include/spmm_tc.cuh:238-269 semantics,
+    without its atomics and 1e-9 skip)."""
+    print("case c3 A^T G N=256 f16, first and second product", flush=True)
     g, G, hg = c3
     Gout = synth.features(16 * G.num_windows, 256, seed=31, device=cuda_device).half()
-    out = G.spmm_transpose(Gout)
+    calls = _record_grouped(monkeypatch)
+    out1 = G.spmm_transpose(Gout)
+    out2 = G.spmm_transpose(Gout)
     torch.cuda.synchronize()
     AT = G.transpose()
-    print(check_transpose(hg, HostGraph(AT), Gout, out, RTOL, planT=AT.spmm_plan(256), seed=5), flush=True)
+    assert ("grws_spmm_grouped", 4) in calls, calls
+    assert AT.grouped_tiles(Gout.shape[0], 256).group_size == 4
+    hgT = HostGraph(AT)
+    print(check_transpose(hg, hgT, Gout, out2, RTOL, planT=AT.spmm_plan(256), seed=5), flush=True)
+    print(check_transpose(hg, hgT, Gout, out1, RTOL, planT=AT.spmm_plan(256), seed=6), flush=True)
 
 
 def test_c4_bench_path_n112(c4, cuda_device):

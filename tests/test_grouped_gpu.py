@@ -202,7 +202,7 @@ def test_graph_groups_its_tiles_when_it_pays(cuda_device):
     X = torch.randn(A.num_cols, 256, device=cuda_device).half()
     y1 = A.spmm(X)
     y2 = A.spmm(X)
-    gt = A._cache["grouped"][2]
+    gt = A._cache[("grouped", 4)][2]
     assert gt, "c3-like graph not grouped"
     assert gt.slot_ratio <= ops.GROUP_MAX_RATIO
     assert gt.group_size == ops.group_size_for(256) == 4  # the group size suits the product's width
@@ -212,13 +212,21 @@ def test_graph_groups_its_tiles_when_it_pays(cuda_device):
     X6 = torch.randn(A2.num_cols, 608, device=cuda_device).half()
     A2.spmm(X6)
     y6 = A2.spmm(X6)
-    assert A2._cache["grouped"][2].group_size == ops.group_size_for(608) == 2
+    assert A2._cache[("grouped", 2)][2].group_size == ops.group_size_for(608) == 2
     _oracle_check(A2, X6, y6)
+    # the same graph's 256-column products then get their own 4-window
+    # layout (one cached layout per group size, not the first width's)
+    X2 = torch.randn(A2.num_cols, 256, device=cuda_device).half()
+    A2.spmm(X2)
+    y2b = A2.spmm(X2)
+    assert A2._cache[("grouped", 4)][2].group_size == 4
+    assert A2._cache[("grouped", 2)][2].group_size == 2
+    _oracle_check(A2, X2, y2b)
     _, B = _graph(cuda_device, torch.float16, 16, scale=0.01, cfg="c4")
     Xb = torch.randn(B.num_cols, 256, device=cuda_device).half()
     B.spmm(Xb)
     B.spmm(Xb)
-    assert B._cache["grouped"][2] is False
+    assert B._cache[("grouped", 4)][2] is False
 
 
 @pytest.mark.parametrize("G", [2, 4])

@@ -189,6 +189,33 @@ def test_element_decoders_cover_every_bit_pattern(dt):
     assert np.all(Y[1:] == 0)
 
 
+def test_round_to_bf16_matches_torch_cast():
+    """oracle.round_to_bf16 against torch's own float32 -> bfloat16 cast (an
+    independent implementation): every upper 16-bit pattern with the low
+    halves 0x0000 (exact), 0x7FFF (just below the tie), 0x8000 (the tie:
+    even upper half kept, odd rounded up), 0x8001 (just above) and 0xFFFF
+    covers ties, carries into the exponent, overflow to inf, subnormals,
+    +-0 and NaN.  Non-NaN results agree bit for bit; NaN stays NaN (torch
+    and the oracle pick different NaN payloads)."""
+    import torch
+    hi = np.arange(65536, dtype=np.uint32) << 16
+    lows = np.array([0x0000, 0x7FFF, 0x8000, 0x8001, 0xFFFF], np.uint32)
+    x = (hi[:, None] | lows[None, :]).reshape(-1).view(np.float32)
+    got = oracle.round_to_bf16(x).view(np.uint32)
+    ref = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    ref = ref.astype(np.uint32) << 16
+    nan = np.isnan(x)
+    assert nan.sum() == 5 * 2 * 127 + 2 * 4  # exponent 0xFF with a non-zero mantissa, both signs
+    assert np.all(got & 0xFFFF == 0)
+    np.testing.assert_array_equal(got[~nan], ref[~nan])
+    assert np.all(np.isnan(got[nan].view(np.float32)))
+    # spot values: ties to even, carry, overflow
+    f = lambda u: np.array([u], np.uint32).view(np.float32)
+    assert oracle.round_to_bf16(f(0x3F808000)).view(np.uint32)[0] == 0x3F800000  # tie, even kept
+    assert oracle.round_to_bf16(f(0x3F818000)).view(np.uint32)[0] == 0x3F820000  # tie, odd up
+    assert oracle.round_to_bf16(f(0x7F7FFFFF)).view(np.uint32)[0] == 0x7F800000  # max -> inf
+
+
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("tc", [8, 16])
 def test_fullsize_checkers_match_scipy(dt, tc):
