@@ -88,6 +88,8 @@ _PROTOS = {
                                          ctypes.POINTER(SpmmPlanView), _vp, ctypes.c_int32, ctypes.c_int64,
                                          ctypes.c_int64, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int64,
                                          _vp, ctypes.c_int32, ctypes.c_int64, _vp]),
+    "grws_spmm_set_tuning": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int32]),
+    "grws_spmm_get_tuning": (ctypes.c_int32, [ctypes.c_char_p]),
     "grws_pack_tiles_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
     "grws_pack_tiles_count": (ctypes.c_int, [ctypes.POINTER(BcsrView), _vp, ctypes.c_size_t,
                                              ctypes.POINTER(ctypes.c_int64), _vp]),

@@ -46,6 +46,29 @@ class SpmmPlan:
                               self.num_split, self.num_slots, self.slabs_per_item, 0)
 
 
+class spmm_tuning:
+    """Context manager that sets SpMM dispatch overrides (grws_spmm_set_tuning;
+    benchmarks and tests only) and restores the previous values on exit:
+    ``with spmm_tuning(GRWS_SPMM_WAVES=2): ...``.  Process-wide: no other
+    thread may be in an SpMM call meanwhile."""
+
+    def __init__(self, **overrides: int):
+        self.overrides = {k: int(v) for k, v in overrides.items()}
+        self.saved = {}
+
+    def __enter__(self):
+        lib = L.load()
+        for k, v in self.overrides.items():
+            self.saved[k] = int(lib.grws_spmm_get_tuning(k.encode()))
+            L.call("grws_spmm_set_tuning", k.encode(), v)
+        return self
+
+    def __exit__(self, *exc):
+        for k, v in self.saved.items():
+            L.call("grws_spmm_set_tuning", k.encode(), v)
+        return False
+
+
 def default_slabs(num_windows: int, num_tiles: int, tile_cols: int, n_cols: int) -> int:
     return int(L.load().grws_spmm_default_slabs(num_windows, num_tiles, tile_cols, n_cols))
 

@@ -1289,11 +1289,20 @@ int report_input_error(int32_t e, const char* who) {
 // caller's stream and joins back into it through events of its own, so
 // concurrent calls stay ordered.  When the caller's stream belongs to another
 // device than the current one, or the device index is out of range, the side
-// work stays on the caller's stream.
+// work stays on the caller's stream.  So it does when the caller's stream is
+// being captured (or its capture state cannot be read): a fork there would
+// pull the shared stream into the caller's graph, and a build on another
+// thread would then land in that graph.
 constexpr int kSideDevices = 64;
 
 int side_fork(hipStream_t main, hipStream_t* side) {
     *side = main;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(main, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return GRWS_OK;
+    }
+    if (cs != hipStreamCaptureStatusNone) return GRWS_OK;
     int dev = 0;
     GRWS_HIP(hipGetDevice(&dev));
     hipDevice_t sdev = -1;
@@ -1331,6 +1340,55 @@ int side_join(hipStream_t main, hipStream_t side) {
     return GRWS_OK;
 }
 
+// A forked side stream that is joined back on every exit: an error return
+// between the fork and the join must not leave side work running on a
+// workspace the caller may free (and its allocator hand out again on the
+// caller's stream).  join() reports the join's status; the destructor joins
+// quietly (the first error's message stays), and when even the events fail
+// it waits for the side stream.
+struct SideStream {
+    hipStream_t main, side;
+    explicit SideStream(hipStream_t m) : main(m), side(m) {}
+    SideStream(const SideStream&) = delete;
+    SideStream& operator=(const SideStream&) = delete;
+    int fork() { return side_fork(main, &side); }
+    int join() {
+        const hipStream_t s = side;
+        side = main;
+        return side_join(main, s);
+    }
+    ~SideStream() {
+        if (side == main) return;
+        hipEvent_t ev;
+        hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e == hipSuccess) {
+            e = hipEventRecord(ev, side);
+            if (e == hipSuccess) e = hipStreamWaitEvent(main, ev, 0);
+            (void)hipEventDestroy(ev);
+        }
+        if (e != hipSuccess) (void)hipStreamSynchronize(side);
+        (void)hipGetLastError();
+    }
+};
+
+// The build synchronises on data-dependent sizes, which a stream under
+// capture does not allow.  Refused before the stream is touched, so the
+// caller's capture stays valid.
+int refuse_capture(hipStream_t stream, const char* who) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(GRWS_E_INVALID, "%s: cannot read the stream's capture state (%s)", who,
+                         hipGetErrorString(e));
+    }
+    if (cs != hipStreamCaptureStatusNone)
+        return set_error(GRWS_E_INVALID,
+                         "%s: the stream is being captured; the build waits for its data-dependent sizes, "
+                         "so build before the capture", who);
+    return GRWS_OK;
+}
+
 }  // namespace
 }  // namespace grws
 
@@ -1355,6 +1413,7 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
                                      size_t workspace_bytes, int64_t* num_tiles_out, void* stream_) {
     clear_error();
     hipStream_t stream = as_stream(stream_);
+    GRWS_TRY(refuse_capture(stream, "bcsr_build_count"));
     GRWS_CHECK_ARG(nnz >= 0 && num_rows >= 0 && num_cols >= 0, "bcsr_build: negative size");
     GRWS_CHECK_ARG(num_rows <= INT32_MAX && num_cols <= INT32_MAX, "bcsr_build: dimensions exceed int32 ids");
     GRWS_CHECK_ARG(nnz <= (int64_t)UINT32_MAX, "bcsr_build: more than 2^32-1 edges");
@@ -1446,9 +1505,10 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
             uint64_t* rk = kalt ? w.ka : w.kb;
             ucol = reinterpret_cast<int32_t*>(kalt ? w.va : w.vb);
             if (!kalt) GRWS_TRY(fill_i32(w.err + 2, 1, 2, stream));
-            hipStream_t side = stream;
+            SideStream ss(stream);
             if (nbig > 0) {
-                GRWS_TRY(side_fork(stream, &side));
+                GRWS_TRY(ss.fork());
+                const hipStream_t side = ss.side;
                 hipLaunchKernelGGL((win_sort_big_kernel<true>), dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, side,
                                    nullptr, nullptr, nullptr, tk, tv, kwbits, nnz, s.R, w.blist, nbig,
                                    s.C, (int)tile_cols, reinterpret_cast<uint32_t*>(w.uidx),
@@ -1467,11 +1527,12 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
                                stream, nullptr, nullptr, nullptr, tk, tv, kwbits, nnz, s.R, s.W, s.C, (int)tile_cols,
                                rk, ucol, w.wstart, w.wend, w.wtiles, w.err);
             GRWS_LAUNCH_CHECK();
-            GRWS_TRY(side_join(stream, side));
+            GRWS_TRY(ss.join());
         } else {
-            hipStream_t side = stream;
+            SideStream ss(stream);
             if (nbig > 0) {
-                GRWS_TRY(side_fork(stream, &side));
+                GRWS_TRY(ss.fork());
+                const hipStream_t side = ss.side;
                 hipLaunchKernelGGL((win_sort_big_kernel<false>), dim3(std::min(nbig, 1024)), dim3(kWinBlk), 0, side,
                                    row_ptr, cols, values, nullptr, nullptr, 0, nnz, s.R, w.blist,
                                    nbig, num_cols, (int)tile_cols, reinterpret_cast<uint32_t*>(w.uidx),
@@ -1491,7 +1552,7 @@ extern "C" int grws_bcsr_build_count(const int64_t* row_ptr, const int32_t* rows
                                stream, row_ptr, cols, values, nullptr, nullptr, 0, nnz, s.R, s.W, num_cols,
                                (int)tile_cols, w.ka, ucol, w.wstart, w.wend, w.wtiles, w.err);
             GRWS_LAUNCH_CHECK();
-            GRWS_TRY(side_join(stream, side));
+            GRWS_TRY(ss.join());
         }
     }
     bool alt = false;
@@ -1539,6 +1600,7 @@ extern "C" int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_c
                                     size_t workspace_bytes, void* stream_) {
     clear_error();
     hipStream_t stream = as_stream(stream_);
+    GRWS_TRY(refuse_capture(stream, "bcsr_build_fill"));
     GRWS_CHECK_ARG(nnz >= 0 && num_rows >= 0 && num_cols >= 0 && num_tiles >= 0, "bcsr_build: negative size");
     GRWS_CHECK_ARG(tile_cols == 8 || tile_cols == 16, "bcsr_build: tile_cols must be 8 or 16 (got %d)", tile_cols);
     if (values_dtype != GRWS_F32 && values_dtype != GRWS_F16 && values_dtype != GRWS_BF16)
@@ -1573,8 +1635,9 @@ extern "C" int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_c
     const int aligned = (reinterpret_cast<uintptr_t>(values) & 15) == 0;
     const uint64_t* wrec = path == 2 ? w.kb : w.ka;
     const int32_t* wcol = reinterpret_cast<const int32_t*>(path == 2 ? w.vb : w.va);
-    hipStream_t side = stream;
-    if (nbig > 0) GRWS_TRY(side_fork(stream, &side));
+    SideStream ss(stream);
+    if (nbig > 0) GRWS_TRY(ss.fork());
+    const hipStream_t side = ss.side;
 #define GRWS_BUILD_FILL(VT)                                                                                        \
     if (path != 0)                                                                                                 \
     {                                                                                                              \
@@ -1601,7 +1664,7 @@ extern "C" int grws_bcsr_build_fill(int64_t nnz, int64_t num_rows, int64_t num_c
     }
 #undef GRWS_BUILD_FILL
     GRWS_LAUNCH_CHECK();
-    GRWS_TRY(side_join(stream, side));
+    GRWS_TRY(ss.join());
     return GRWS_OK;
 }
 

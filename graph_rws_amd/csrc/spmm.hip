@@ -23,12 +23,13 @@
 //   * work-group ids are remapped so each XCD (work-groups are dealt to the 8
 //     XCDs round-robin) walks a contiguous range of windows of one chunk,
 //     keeping a community's X rows (one chunk wide) in that XCD's L2.
-// Tuning overrides for benchmarking: GRWS_SPMM_WAVES (1|2), GRWS_SPMM_NBLK (1|2|4|8|16),
-// GRWS_SPMM_ORDER (1: chunk-major work order, the default; 0: XCD shares of
-// the (chunk, window) pairs).
+// Tuning overrides for benchmarking and tests (TuneKey below): read once
+// from the environment at load, set through grws_spmm_set_tuning.
 #include "grws_internal.h"
 
+#include <atomic>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 namespace grws {
@@ -37,6 +38,37 @@ namespace {
 // cache policy of the A-side buffer loads (column indices, tile headers and
 // values): 0, the default (no streaming hint)
 constexpr int kAPolicy = 0;
+
+// Tuning overrides, for benchmarks and tests only (production calls leave
+// them unset and get the measured defaults).  Each is read once from its
+// environment variable when the library is loaded, and can be changed
+// through grws_spmm_set_tuning; -1 means "no override".  No product call
+// reads the environment.
+enum TuneKey {
+    kTuneNblk,     // GRWS_SPMM_NBLK: column blocks per chunk (1, 2, 4, 8, 16)
+    kTuneWaves,    // GRWS_SPMM_WAVES: waves per work-group (1, 2)
+    kTuneKernel,   // GRWS_SPMM_KERNEL: 1 = the element-masked kernel
+    kTuneOrder,    // GRWS_SPMM_ORDER: 1 = chunk-major work order, 0 = XCD shares
+    kTuneNarrow,   // GRWS_SPMM_NARROW: 1 = 128-byte gathers of 8 rows
+    kTuneC320,     // GRWS_SPMM_C320: 0 = no 320-column chunks
+    kTuneGrpWpw,   // GRWS_GRP_WPW: windows per wave of the grouped kernel
+    kTuneGrpNblk,  // GRWS_GRP_NBLK: column blocks of the grouped kernel's first launch
+    kTuneGrpC320,  // GRWS_GRP_C320: 0 = no 320-column grouped chunks
+    kTuneCount
+};
+const char* const kTuneNames[kTuneCount] = {"GRWS_SPMM_NBLK",   "GRWS_SPMM_WAVES",  "GRWS_SPMM_KERNEL",
+                                            "GRWS_SPMM_ORDER",  "GRWS_SPMM_NARROW", "GRWS_SPMM_C320",
+                                            "GRWS_GRP_WPW",     "GRWS_GRP_NBLK",    "GRWS_GRP_C320"};
+std::atomic<int> g_tune[kTuneCount];
+struct TuneInit {
+    TuneInit() {
+        for (int i = 0; i < kTuneCount; ++i) {
+            const char* e = getenv(kTuneNames[i]);
+            g_tune[i].store(e ? atoi(e) : -1, std::memory_order_relaxed);
+        }
+    }
+} g_tune_init;
+inline int tune(TuneKey k) { return g_tune[k].load(std::memory_order_relaxed); }
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -1138,8 +1170,7 @@ bool wide_chunks(int64_t x_rows, int32_t x_dtype) {
 // wide_chunks holds.  fp32 X stays at 128 (its loads carry half as many
 // elements per lane).
 int nblk_for(int64_t N, int32_t x_dtype, bool buffer_path, int64_t x_rows) {
-    if (const char* e = getenv("GRWS_SPMM_NBLK")) {  // tuning override
-        const int v = atoi(e);
+    if (const int v = tune(kTuneNblk); v >= 0) {  // tuning override
         if (v == 1 || v == 2 || v == 4 || v == 8 || (v == 16 && x_dtype != GRWS_F32)) return v;
     }
     if (buffer_path && wide_chunks(x_rows, x_dtype) && N >= 256 && N % 256 == 0) return 16;
@@ -1162,10 +1193,7 @@ int launch_fwd(const SpmmArgs& a, hipStream_t stream) {
 // small launches keep one wave per work-group so the chip still fills.
 int waves_for(const SpmmArgs& a, int nblk) {
     (void)nblk;
-    if (const char* e = getenv("GRWS_SPMM_WAVES")) {  // tuning override
-        const int v = atoi(e);
-        if (v == 1 || v == 2) return v;
-    }
+    if (const int v = tune(kTuneWaves); v == 1 || v == 2) return v;  // tuning override
     return a.num_items * a.nchunks >= 65536 ? 2 : 1;
 }
 
@@ -1265,8 +1293,7 @@ int dispatch_buf_tc(const SpmmArgs& a, int tc, int nblk, hipStream_t stream) {
 // A->max_window_slabs when the caller knows it, else the whole graph).
 bool buffer_path_fits(const grws_bcsr* A, const grws_spmm_plan* plan, int64_t x_rows, int64_t ldx, int64_t nc,
                       size_t esz) {
-    if (const char* e = getenv("GRWS_SPMM_KERNEL"))  // tuning override: 1 = element-masked kernel
-        if (atoi(e) == 1) return false;
+    if (tune(kTuneKernel) == 1) return false;  // tuning override: the element-masked kernel
     const int64_t ldxb = ldx * (int64_t)esz;
     if (x_rows <= 0 || x_rows >= (1 << 24) || ldxb >= (1 << 24)) return false;
     if ((x_rows + 1) * ldxb + nc * (int64_t)esz >= ((int64_t)1 << 32)) return false;
@@ -1582,9 +1609,9 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
     if (use_buf) {
         a.x_bytes = (uint32_t)((x_rows - 1) * ldx * (int64_t)esz + n_cols * (int64_t)esz);
         a.chunk_major = 1;
-        if (const char* e = getenv("GRWS_SPMM_ORDER")) a.chunk_major = atoi(e) == 1;  // tuning override
+        if (const int v = tune(kTuneOrder); v >= 0) a.chunk_major = v == 1;  // tuning override
         a.narrow = 1;  // 128-byte segments of 8 rows per gather where the kernel has them
-        if (const char* e = getenv("GRWS_SPMM_NARROW")) a.narrow = atoi(e) == 1;      // tuning override
+        if (const int v = tune(kTuneNarrow); v >= 0) a.narrow = v == 1;      // tuning override
         if (P && A->num_tiles > 0) {  // the element-masked kernel below reads the dense values
             a.hdr = P->header;
             a.pvals = P->values;
@@ -1595,13 +1622,13 @@ int spmm_impl(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_pl
         // N above 256 and not a multiple of it: 256-column chunks over the
         // whole multiples, then one narrower launch for the rest, so A is
         // streamed once per 256 columns and no chunk is mostly empty
-        const bool forced = getenv("GRWS_SPMM_NBLK") != nullptr;
+        const bool forced = tune(kTuneNblk) >= 0;
         // 320-column chunks (narrow path) when they stream A fewer times than
         // 256-column chunks plus a narrower rest (N = 608: 2 passes, not 3)
         if (!forced && !af32 && x_dtype != GRWS_F32 && n_cols > 256 && n_cols % 256 != 0 &&
             x_rows * 320 * (int64_t)esz <= ((int64_t)256 << 20) && (n_cols + 319) / 320 < (n_cols + 255) / 256 &&
             (x_rows + 1) * ldx * (int64_t)esz + 320 * (int64_t)esz < ((int64_t)1 << 32) &&
-            !(getenv("GRWS_SPMM_C320") && atoi(getenv("GRWS_SPMM_C320")) == 0)) {
+            tune(kTuneC320) != 0) {
             a.col_base = 0;
             a.nchunks = (int32_t)((n_cols + 319) / 320);
             st = x_dtype == GRWS_F16 ? dispatch_buf_tc<GRWS_F16, false>(a, tc, 20, stream)
@@ -1760,13 +1787,13 @@ extern "C" int grws_spmm_grouped(const grws_bcsr* A, const grws_grouped_tiles* G
     // else 256-column chunks plus one narrower launch for the rest
     int wpw = G == 8 ? 2 : 1;
     int head_nblk = n_cols > 128 ? 16 : 8, tail_nblk = 8;
-    if (const char* e = getenv("GRWS_GRP_WPW")) wpw = atoi(e);  // tuning overrides
-    if (const char* e = getenv("GRWS_GRP_NBLK")) head_nblk = atoi(e);
+    if (const int v = tune(kTuneGrpWpw); v >= 0) wpw = v;  // tuning overrides
+    if (const int v = tune(kTuneGrpNblk); v >= 0) head_nblk = v;
     if (wpw == 4) head_nblk = 8;
     if (wpw == 4 || G / wpw == 4) tail_nblk = 8;
     const int64_t hnc = head_nblk * 16;
     const bool c320 = head_nblk == 16 && n_cols > 256 && n_cols % 256 != 0 && (n_cols + 319) / 320 < (n_cols + 255) / 256 &&
-                      G / wpw <= 2 && !(getenv("GRWS_GRP_C320") && atoi(getenv("GRWS_GRP_C320")) == 0);
+                      G / wpw <= 2 && tune(kTuneGrpC320) != 0;
     int st;
     if (c320) {
         a.col_base = 0;
@@ -1845,6 +1872,24 @@ int scratch_for_current_device(void** out) {
 }
 }  // namespace
 
+extern "C" int grws_spmm_set_tuning(const char* name, int32_t value) {
+    clear_error();
+    GRWS_CHECK_ARG(name != nullptr, "spmm_set_tuning: null name");
+    for (int i = 0; i < kTuneCount; ++i)
+        if (strcmp(name, kTuneNames[i]) == 0) {
+            g_tune[i].store(value < 0 ? -1 : value, std::memory_order_relaxed);
+            return GRWS_OK;
+        }
+    return set_error(GRWS_E_INVALID, "spmm_set_tuning: unknown override '%s'", name);
+}
+
+extern "C" int32_t grws_spmm_get_tuning(const char* name) {
+    if (!name) return -1;
+    for (int i = 0; i < kTuneCount; ++i)
+        if (strcmp(name, kTuneNames[i]) == 0) return g_tune[i].load(std::memory_order_relaxed);
+    return -1;
+}
+
 extern "C" int grws_spmm_noalloc(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_plan* plan,
                                  const void* x, int32_t x_dtype, int64_t x_rows, int64_t ldx, int64_t n_cols,
                                  const void* r, int64_t ldr, int64_t r_rows, void* y, int32_t y_dtype, int64_t ldy,
@@ -1857,7 +1902,24 @@ extern "C" int grws_spmm_noalloc(const grws_bcsr* A, const grws_packed_tiles* P,
                          "(use grws_spmm_residual with a workspace, or a plan with more slabs per item)",
                          need, (size_t)GRWS_SPMM_NOALLOC_SCRATCH_BYTES);
     void* ws = nullptr;
-    if (need > 0) GRWS_TRY(scratch_for_current_device(&ws));
+    if (need > 0) {
+        // the scratch array read below is the current device's: a stream of
+        // another device would reach it across devices
+        int dev = 0;
+        GRWS_HIP(hipGetDevice(&dev));
+        hipDevice_t sdev = -1;
+        const hipError_t e = hipStreamGetDevice(as_stream(stream), &sdev);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return set_error(GRWS_E_INVALID, "spmm_noalloc: cannot tell the stream's device (%s)",
+                             hipGetErrorString(e));
+        }
+        if (sdev != dev)
+            return set_error(GRWS_E_INVALID,
+                             "spmm_noalloc: the stream belongs to device %d, not the current device %d "
+                             "(make the stream's device current first)", (int)sdev, dev);
+        GRWS_TRY(scratch_for_current_device(&ws));
+    }
     // every partial a launch reads was written by the same launch's items
     // first, so the scratch needs no clearing between calls
     return spmm_impl(A, P, plan, x, x_dtype, x_rows, ldx, n_cols, r, ldr, r_rows, y, y_dtype,

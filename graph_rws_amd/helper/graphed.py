@@ -56,7 +56,7 @@ class GraphedFullStep:
                 self._step()
         cur.wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        with torch.cuda.graph(self.graph, capture_error_mode="thread_local"):
             self.loss, self.acc = self._step()
         self._idx_version = train_idx._version
 
@@ -249,7 +249,7 @@ class GraphedBlockStep:
                 self._eager(bk)
         cur.wait_stream(side)
         bk.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(bk.graph):
+        with torch.cuda.graph(bk.graph, capture_error_mode="thread_local"):
             bk.loss, bk.correct = self._eager(bk)
         # the capture recorded the step without running it; undo the warm-up
         with torch.no_grad():

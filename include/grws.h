@@ -251,6 +251,17 @@ int grws_spmm_residual(const grws_bcsr* A, const grws_packed_tiles* P, const grw
                        const void* r, int64_t ldr, int64_t r_rows, void* y, int32_t y_dtype, int64_t ldy,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* Tuning overrides of the SpMM dispatch, for benchmarks and tests only.
+ * No counterpart in the reference.  Names: GRWS_SPMM_NBLK, GRWS_SPMM_WAVES,
+ * GRWS_SPMM_KERNEL, GRWS_SPMM_ORDER, GRWS_SPMM_NARROW, GRWS_SPMM_C320,
+ * GRWS_GRP_WPW, GRWS_GRP_NBLK, GRWS_GRP_C320.  Each starts from the
+ * environment variable of that name, read once when the library is loaded;
+ * value -1 clears the override (the measured default then applies).  The
+ * overrides are process-wide: set them only where no other thread is in
+ * an SpMM call.  get returns -1 when unset or for an unknown name. */
+int grws_spmm_set_tuning(const char* name, int32_t value);
+int32_t grws_spmm_get_tuning(const char* name);
+
 /*
  * grws_spmm_residual without a workspace argument; it allocates nothing.
  * No counterpart in the reference: it is for callers that cannot allocate
@@ -261,7 +272,8 @@ int grws_spmm_residual(const grws_bcsr* A, const grws_packed_tiles* P, const grw
  * (grws_spmm_workspace_bytes(plan, n_cols)) returns GRWS_E_CAPACITY.  All
  * calls on one GPU share that array: calls that overlap in time on one GPU
  * (different streams or threads) race and give wrong results.  The stream
- * must belong to the current device.  r may be NULL (Y = A X).
+ * must belong to the current device (a stream of another device returns
+ * GRWS_E_INVALID).  r may be NULL (Y = A X).
  */
 #define GRWS_SPMM_NOALLOC_SCRATCH_BYTES (16u << 20)
 int grws_spmm_noalloc(const grws_bcsr* A, const grws_packed_tiles* P, const grws_spmm_plan* plan,

@@ -138,6 +138,34 @@ def test_csr_build_window_paths(cuda_device, hub, tc, vdt):
     _eq(dv, torch.from_numpy(ov.astype(np.float32)).to(vdt))
 
 
+def test_build_under_capture_is_refused_cleanly(cuda_device):
+    """The build waits for its data-dependent sizes, which a stream under
+    capture does not allow.  Inside a capture it returns a clean error
+    before it touches the stream, so the capture stays valid (it ends, and
+    its replays run the work captured around the call), and the same build
+    then runs eagerly and equals the oracle's converter."""
+    print("case build under capture", flush=True)
+    g = GRAPHS["random"]()
+    args = [t.to(cuda_device) for t in (g.row_ptr, g.col_idx, g.values)]
+    x = torch.zeros(64, device=cuda_device)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, capture_error_mode="thread_local"):
+        x.add_(1.0)
+        with pytest.raises(GrwsError, match="being captured"):
+            builder.csr_to_bcsr_device(g.num_nodes, g.num_nodes, *args, tile_cols=16)
+        x.mul_(3.0)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+    assert float(x[0]) == 39.0 and bool((x == x[0]).all())  # ((0 + 1) 3 + 1) 3 + 1) 3
+    dw, dc, dv = builder.csr_to_bcsr_device(g.num_nodes, g.num_nodes, *args, tile_cols=16)
+    ow, oc, ov = _oracle_bcsr(g, 16)
+    _eq(dw, ow)
+    _eq(dc, oc)
+    _eq(dv, ov)
+
+
 def test_big_window_builds_on_concurrent_streams(cuda_device):
     """Windows above 16,384 edges run on one extra stream per device, forked
     from and joined back into the caller's stream.  Two threads, each on a

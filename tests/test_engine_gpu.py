@@ -55,6 +55,56 @@ def test_block_step_matches_dense_reference(cuda_device):
         assert float((a - b).abs().max()) <= 1e-4 * max(float(b.abs().max()), 1e-30), n
 
 
+def test_block_step_c5_widths_f16(cuda_device):
+    """One mini-batch step at c5's configured shape: 1,024 seeds, fanouts
+    [15, 10, 5] (Philox seed 42), 128 -> 256 -> 256 -> 172 in float16
+    autocast with float16 block values, on a c5 graph at 1e-3 scale (111k
+    nodes, 1.6M edges), against float64 autograd over dense copies of the
+    same (float16) blocks and features (/root/reference/helper/engine.py:
+    86-256 through models/model.py:212-266).
+
+    Tolerance: autocast rounds every GEMM and SpMM output to float16
+    (u = 2^-11) through three layers, LayerNorm and the backward pass; the
+    loss within 1e-2 relative and every gradient within 3e-2 of its
+    largest magnitude (about 60 units of the float16 rounding)."""
+    print("case block step c5 widths f16", flush=True)
+    torch.manual_seed(0)
+    dev = cuda_device
+    g = synth.c5_graph(device=dev, scale=1e-3)
+    seeds = synth.distinct_seeds(g.num_nodes, 1024, seed=3, device=dev)
+    blocks = NeighborSampler([15, 10, 5], seed=42, values_dtype=torch.float16).sample_layers(
+        g.row_ptr, g.col_idx, seeds)
+    assert [b.num_rows for b in blocks][-1] == 1024
+    X = synth.features(g.num_nodes, 128, seed=4, device=dev).half()
+    labels = torch.randint(0, 172, (g.num_nodes,), device=dev)
+    model = GCN_BCSR(128, 256, 172, 3, dropout=0.0, use_checkpoint=False).to(dev)
+    ref = copy.deepcopy(model).cpu().double()
+    dense = [torch.from_numpy(oracle.bcsr_to_dense(b.window_offset.cpu().numpy(),
+                                                   b.original_col_indices.cpu().numpy(),
+                                                   b.values_condensed.float().cpu().numpy(), 16,
+                                                   b.tile_cols, b.num_cols)[:b.num_rows]).double()
+             for b in blocks]
+    feats = X.index_select(0, blocks[0].src_nodes)
+    with torch.autocast("cuda", dtype=torch.float16):
+        logits = model(blocks, feats)
+    assert logits.shape == (1024, 172)
+    loss = torch.nn.functional.cross_entropy(logits.float(), labels[seeds])
+    loss.backward()
+
+    h = feats.double().cpu()
+    for l, (layer, A) in enumerate(zip(ref.layers, dense)):
+        h = A @ (h @ layer.weight_neigh) + h[: A.shape[0]] @ layer.weight_self
+        if l < 2:
+            h = ref.norms[l](torch.relu(h))
+    rl = torch.nn.functional.cross_entropy(h, labels[seeds].cpu())
+    rl.backward()
+    assert abs(float(loss) - float(rl)) <= 1e-2 * abs(float(rl)), (float(loss), float(rl))
+    for (n, p), (_, q) in zip(model.named_parameters(), ref.named_parameters()):
+        a, b = p.grad.double().cpu(), q.grad
+        err = float((a - b).abs().max())
+        assert err <= 3e-2 * max(float(b.abs().max()), 1e-30), (n, err, float(b.abs().max()))
+
+
 @pytest.mark.parametrize("pipeline", [True, False])
 def test_neighbor_sampler_epoch(cuda_device, pipeline):
     print(f"case neighbor epoch pipeline={pipeline}", flush=True)

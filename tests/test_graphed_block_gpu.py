@@ -82,6 +82,104 @@ def test_graphed_block_step_tracks_eager(cuda_device, dt, tc):
     assert len(step.buckets) == step.captures
 
 
+def test_graphed_block_step_c5_widths(cuda_device):
+    """The captured step at c5's configured widths (128 -> 256 -> 256 ->
+    172, float16 autocast, fanouts [15, 10, 5], about 1,024 seeds per
+    batch, c5 graph at 1e-3 scale) tracks the eager step batch by batch."""
+    print("case graphed block step c5 widths", flush=True)
+    dev = cuda_device
+    g = synth.c5_graph(device=dev, scale=1e-3)
+    X = synth.features(g.num_nodes, 128, seed=4, device=dev).half()
+    labels = X.float().argmax(1)  # 128 of the 172 classes occur
+    torch.manual_seed(7)
+    m_e = GCN_BCSR(128, 256, 172, 3, dropout=0.0, use_checkpoint=False).to(dev)
+    m_g = copy.deepcopy(m_e)
+    o_e = torch.optim.Adam(m_e.parameters(), lr=0.01, eps=1.0, capturable=True)
+    o_g = torch.optim.Adam(m_g.parameters(), lr=0.01, eps=1.0, capturable=True)
+    step = GraphedBlockStep(m_g, o_g, dev, autocast_dtype=torch.float16, warmup=2)
+    sampler = NeighborSampler([15, 10, 5], seed=42, values_dtype=torch.float16)
+    rtol, atol = TOL[torch.float16]
+    for b, n in enumerate([1024, 1024, 1000, 1024]):
+        seeds = torch.sort(synth.distinct_seeds(g.num_nodes, n, seed=20 + b, device=dev)).values
+        blocks = sampler.sample_layers(g.row_ptr, g.col_idx, seeds)
+        feats = X.index_select(0, blocks[0].src_nodes)
+        lab = labels[seeds]
+        loss_g, corr_g = step(blocks, feats, lab)
+        loss_g, corr_g = loss_g.clone(), corr_g.clone()
+        loss_e, corr_e = _eager_step(m_e, o_e, blocks, feats, lab, torch.float16)
+        torch.cuda.synchronize()
+        assert torch.isfinite(loss_g).all()
+        torch.testing.assert_close(loss_g.float(), loss_e.float(), rtol=rtol, atol=rtol, msg=f"batch {b}: loss")
+        assert abs(int(corr_g) - int(corr_e)) <= max(1, n // 100), (b, int(corr_g), int(corr_e))
+        for (name, p), (_, q) in zip(m_g.named_parameters(), m_e.named_parameters()):
+            torch.testing.assert_close(p, q, rtol=0, atol=atol, msg=f"batch {b}: {name}")
+    assert step.captures >= 1
+
+
+def test_capture_while_another_thread_samples(cuda_device):
+    """A bucket is captured while another thread samples on its own stream
+    (stream syncs, device-to-host copies, allocations), as the pipelined
+    epoch's producer does when a new batch shape appears mid-epoch: the
+    capture is thread-local, so neither thread's work fails, and the
+    replayed step still tracks the eager one."""
+    import threading
+    print("case capture while another thread samples", flush=True)
+    dev = cuda_device
+    g = synth.c5_graph(device=dev, scale=2e-4)
+    D = 48
+    X = synth.features(g.num_nodes, D, seed=4, device=dev).half()
+    labels = X[:, :5].float().argmax(1)
+    torch.manual_seed(3)
+    m_e = GCN_BCSR(D, 32, 5, 3, dropout=0.0, use_checkpoint=False).to(dev)
+    m_g = copy.deepcopy(m_e)
+    o_e = torch.optim.Adam(m_e.parameters(), lr=0.01, eps=1.0, capturable=True)
+    o_g = torch.optim.Adam(m_g.parameters(), lr=0.01, eps=1.0, capturable=True)
+    step = GraphedBlockStep(m_g, o_g, dev, autocast_dtype=torch.float16, warmup=2)
+    main_sampler = NeighborSampler([6, 4, 3], values_dtype=torch.float16)
+    stop, started, failures, done = threading.Event(), threading.Event(), [], [0]
+
+    def producer():
+        try:
+            s = torch.cuda.Stream(device=dev)
+            smp = NeighborSampler([6, 4, 3], values_dtype=torch.float16)
+            with torch.cuda.stream(s):
+                i = 0
+                while not stop.is_set() and i < 2000:
+                    sd = synth.distinct_seeds(g.num_nodes, 150 + (i % 7), seed=500 + i, device=dev)
+                    bl = smp.sample_layers(g.row_ptr, g.col_idx, sd)
+                    int(bl[0].src_nodes.numel())
+                    bl[-1].window_offset.cpu()
+                    s.synchronize()
+                    i += 1
+                    done[0] = i
+                    started.set()
+        except BaseException as e:  # reported by the main thread
+            failures.append(e)
+            started.set()
+
+    th = threading.Thread(target=producer)
+    th.start()
+    try:
+        assert started.wait(120), "the producer thread did not start"
+        rtol, atol = TOL[torch.float16]
+        for b, n in enumerate([200, 64, 200, 64]):
+            seeds = torch.sort(synth.distinct_seeds(g.num_nodes, n, seed=30 + b, device=dev)).values
+            blocks = main_sampler.sample_layers(g.row_ptr, g.col_idx, seeds)
+            feats = X.index_select(0, blocks[0].src_nodes)
+            lab = labels[seeds]
+            loss_g, _ = step(blocks, feats, lab)
+            loss_g = loss_g.clone()
+            loss_e, _ = _eager_step(m_e, o_e, blocks, feats, lab, torch.float16)
+            torch.cuda.synchronize()
+            torch.testing.assert_close(loss_g.float(), loss_e.float(), rtol=rtol, atol=rtol, msg=f"batch {b}")
+    finally:
+        stop.set()
+        th.join(timeout=120)
+    assert not th.is_alive(), "the producer thread did not finish"
+    assert not failures, failures
+    assert step.captures == 2 and done[0] > 0
+
+
 def test_graphed_block_epoch(cuda_device):
     """train_epoch_node_sampling with graphed=: the pipelined epoch replays
     captured steps and trains like the eager epoch (dropout off)."""

@@ -13,7 +13,6 @@ Checks:
     on a partial last group; it stays within one rounding of the output
     dtype of the window-by-window kernel.
 """
-import os
 
 import numpy as np
 import pytest
@@ -147,18 +146,9 @@ def test_grouped_spmm_meets_oracle(cuda_device, monkeypatch, G, wpw, nblk, N):
     assert gt is not None
     torch.manual_seed(N + G)
     X = torch.randn(A.num_cols, N, device=cuda_device).half()
-    old = {k: os.environ.get(k) for k in ("GRWS_GRP_WPW", "GRWS_GRP_NBLK")}
-    os.environ["GRWS_GRP_WPW"] = str(wpw)
-    os.environ["GRWS_GRP_NBLK"] = str(nblk)
-    try:
+    with ops.spmm_tuning(GRWS_GRP_WPW=wpw, GRWS_GRP_NBLK=nblk):
         Y = ops.spmm(A.window_offset, A.original_col_indices, A.values_condensed, X, 16, grouped=gt)
         torch.cuda.synchronize()
-    finally:
-        for k, v in old.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
     _oracle_check(A, X, Y)
     Yw = ops.spmm(A.window_offset, A.original_col_indices, A.values_condensed, X, 16)
     # one rounding of fp16 apart at most: the sums differ only in fp32 order

@@ -15,7 +15,6 @@ Two checks:
     path.
 """
 import ctypes
-import os
 
 import numpy as np
 import pytest
@@ -135,17 +134,11 @@ def test_packed_spmm_waves_and_c2(cuda_device, waves):
     P = core.pack_tiles(G.window_offset, G.original_col_indices, G.values_condensed, 16)
     X = synth.features(g.num_nodes, 128, seed=3, device=cuda_device).to(torch.float16)
     args = (G.window_offset, G.original_col_indices, G.values_condensed, X, 16)
-    old = os.environ.get("GRWS_SPMM_WAVES")
-    os.environ["GRWS_SPMM_WAVES"] = waves
-    try:
+    from graph_rws_amd.core.ops import spmm_tuning
+    with spmm_tuning(GRWS_SPMM_WAVES=int(waves)):
         Yd = core.spmm(*args)
         Yp = core.spmm(*args, packed=P)
         torch.cuda.synchronize()
-    finally:
-        if old is None:
-            del os.environ["GRWS_SPMM_WAVES"]
-        else:
-            os.environ["GRWS_SPMM_WAVES"] = old
     assert torch.equal(_bits(Yd), _bits(Yp))
     if waves == "1":
         Yr, Ya = oracle.bcsr_spmm(G.window_offset.cpu().numpy(), G.original_col_indices.cpu().numpy(),

@@ -265,8 +265,7 @@ def test_ragged_width_copy_is_line_aligned(cuda_device):
 def test_fp32_buffer_kernel_equals_element_masked(cuda_device, tc, N, slabs):
     """fp32 X runs the buffer-load kernel (v_mfma_f32_16x16x4f32, the same
     MFMA sequence as the element-masked kernel): the same bits as the
-    element-masked kernel, forced with GRWS_SPMM_KERNEL=1."""
-    import os
+    element-masked kernel, forced with the GRWS_SPMM_KERNEL=1 override."""
     print(f"case fp32 buf tc={tc} N={N} slabs={slabs}", flush=True)
     g = synth.chung_lu(2500, 30000, 2.1, seed=N + tc)
     G = _bcsr(g, tc, cuda_device)
@@ -274,32 +273,19 @@ def test_fp32_buffer_kernel_equals_element_masked(cuda_device, tc, N, slabs):
     X = synth.features(g.num_nodes, N, seed=N, device=cuda_device)
     args = (G.window_offset, G.original_col_indices, G.values_condensed, X, tc)
     Yb = core.spmm(*args, plan=plan)
-    old = os.environ.get("GRWS_SPMM_KERNEL")
-    os.environ["GRWS_SPMM_KERNEL"] = "1"
-    try:
+    from graph_rws_amd.core.ops import spmm_tuning
+    with spmm_tuning(GRWS_SPMM_KERNEL=1):
         Ye = core.spmm(*args, plan=plan)
         torch.cuda.synchronize()
-    finally:
-        if old is None:
-            del os.environ["GRWS_SPMM_KERNEL"]
-        else:
-            os.environ["GRWS_SPMM_KERNEL"] = old
     assert torch.equal(Yb.view(torch.int32), Ye.view(torch.int32))
     _check(G, X, Yb, torch.float32)
 
 
 def _with_env(env, fn):
-    import os
-    old = {k: os.environ.get(k) for k in env}
-    os.environ.update(env)
-    try:
+    """fn() under the SpMM tuning overrides env (name -> value)."""
+    from graph_rws_amd.core.ops import spmm_tuning
+    with spmm_tuning(**{k: int(v) for k, v in env.items()}):
         return fn()
-    finally:
-        for k, v in old.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
 
 
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
@@ -355,18 +341,11 @@ def test_spmm_residual_parity(cuda_device, xdt, variant, N):
     packed = core.pack_tiles(G.window_offset, G.original_col_indices, G.values_condensed, 16) \
         if variant == "packed" else None
     env = {"two_waves": {"GRWS_SPMM_WAVES": "2"}, "element_masked": {"GRWS_SPMM_KERNEL": "1"}}.get(variant, {})
-    old = {k: os.environ.get(k) for k in env}
-    os.environ.update(env)
-    try:
+    from graph_rws_amd.core.ops import spmm_tuning
+    with spmm_tuning(**{k: int(v) for k, v in env.items()}):
         Y = core.spmm(*args, plan=plan, packed=packed, residual=R)
         Y0 = core.spmm(*args, plan=plan, packed=packed)
         torch.cuda.synchronize()
-    finally:
-        for k, v in old.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
     vq = G.values_condensed.double().cpu().numpy()
     Yr, Ya = oracle.bcsr_spmm(G.window_offset.cpu().numpy(), G.original_col_indices.cpu().numpy(), vq, 16, 16,
                               X.double().cpu().numpy())

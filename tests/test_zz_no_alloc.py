@@ -98,3 +98,24 @@ def test_noalloc_rejects_plans_past_the_scratch(cuda_device):
                                None, 0, 0, L.ptr(Y), L.GRWS_F16, N, L.stream_of(cuda_device))
     assert st == L.GRWS_E_CAPACITY
     assert b"scratch" in lib.grws_last_error()
+
+
+def test_noalloc_refuses_a_stream_of_another_device(cuda_device):
+    """The scratch array belongs to the current device: a stream of another
+    device is refused with GRWS_E_INVALID before any kernel is launched.
+    Needs two GPUs (a one-GPU box has no stream of another device)."""
+    if torch.cuda.device_count() < 2:
+        pytest.skip("needs a second GPU for a stream of another device")
+    print("case noalloc stream of another device", flush=True)
+    G = _graph(3000, 60000, 5, cuda_device)
+    plan = core.build_spmm_plan(G.window_offset, G.num_tiles, 16, 2)
+    X = torch.randn(G.num_cols, 64, device=cuda_device).half()
+    R = torch.zeros(0, 64, device=cuda_device).half()
+    Y = torch.empty(16 * G.num_windows, 64, device=cuda_device).half()
+    view, pv = _views(G, plan)
+    other = torch.cuda.Stream(device=torch.device("cuda", 1))
+    st = L.load().grws_spmm_noalloc(ctypes.byref(view), None, ctypes.byref(pv), L.ptr(X), L.GRWS_F16,
+                                    X.shape[0], X.stride(0), 64, L.ptr(R), R.stride(0), 0, L.ptr(Y),
+                                    L.GRWS_F16, Y.stride(0), ctypes.c_void_p(other.cuda_stream))
+    assert st == L.GRWS_E_INVALID
+    assert b"belongs to device" in L.load().grws_last_error()
