@@ -55,27 +55,37 @@ def test_block_step_matches_dense_reference(cuda_device):
         assert float((a - b).abs().max()) <= 1e-4 * max(float(b.abs().max()), 1e-30), n
 
 
-def test_block_step_c5_widths_f16(cuda_device):
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_block_step_c5_widths(cuda_device, dt):
     """One mini-batch step at c5's configured shape: 1,024 seeds, fanouts
-    [15, 10, 5] (Philox seed 42), 128 -> 256 -> 256 -> 172 in float16
-    autocast with float16 block values, on a c5 graph at 1e-3 scale (111k
-    nodes, 1.6M edges), against float64 autograd over dense copies of the
-    same (float16) blocks and features (/root/reference/helper/engine.py:
-    86-256 through models/model.py:212-266).
+    [15, 10, 5] (Philox seed 42), 128 -> 256 -> 256 -> 172, on a c5 graph
+    at 1e-3 scale (111k nodes, 1.6M edges), against float64 autograd over
+    dense copies of the same blocks and features (/root/reference/helper/
+    engine.py:86-256 through models/model.py:212-266).
 
-    Tolerance: autocast rounds every GEMM and SpMM output to float16
-    (u = 2^-11) through three layers, LayerNorm and the backward pass; the
-    loss within 1e-2 relative and every gradient within 3e-2 of its
-    largest magnitude (about 60 units of the float16 rounding)."""
-    print("case block step c5 widths f16", flush=True)
+    The reference applies the device's ReLU masks (a unit within rounding
+    of zero may take the other sign in float64 and pass or drop its whole
+    gradient: with its own masks the float32 gradients of layers 0-1 were
+    3e-4 off, the float16 ones 2%).
+
+    float32 (block values and features float32, no autocast): the loss
+    within 1e-4 relative, every gradient within 2e-5 relative in the
+    Frobenius norm and within 5e-5 of its largest magnitude elementwise
+    (measured: 4e-6 at worst).  float16 (float16 block values and
+    features, float16 autocast, as c5 runs): autocast rounds every GEMM
+    and SpMM output to float16 (u = 2^-11 = 4.9e-4) through three layers,
+    LayerNorm and the backward pass: the loss within 1e-2 relative, every
+    gradient within 1e-2 relative in the Frobenius norm and within 1e-2 of
+    its largest magnitude elementwise (measured: 2.8e-3 at worst, a few
+    float16 roundings)."""
+    print(f"case block step c5 widths {dt}", flush=True)
     torch.manual_seed(0)
     dev = cuda_device
     g = synth.c5_graph(device=dev, scale=1e-3)
     seeds = synth.distinct_seeds(g.num_nodes, 1024, seed=3, device=dev)
-    blocks = NeighborSampler([15, 10, 5], seed=42, values_dtype=torch.float16).sample_layers(
-        g.row_ptr, g.col_idx, seeds)
+    blocks = NeighborSampler([15, 10, 5], seed=42, values_dtype=dt).sample_layers(g.row_ptr, g.col_idx, seeds)
     assert [b.num_rows for b in blocks][-1] == 1024
-    X = synth.features(g.num_nodes, 128, seed=4, device=dev).half()
+    X = synth.features(g.num_nodes, 128, seed=4, device=dev).to(dt)
     labels = torch.randint(0, 172, (g.num_nodes,), device=dev)
     model = GCN_BCSR(128, 256, 172, 3, dropout=0.0, use_checkpoint=False).to(dev)
     ref = copy.deepcopy(model).cpu().double()
@@ -85,9 +95,23 @@ def test_block_step_c5_widths_f16(cuda_device):
                                                    b.tile_cols, b.num_cols)[:b.num_rows]).double()
              for b in blocks]
     feats = X.index_select(0, blocks[0].src_nodes)
-    with torch.autocast("cuda", dtype=torch.float16):
+    # the device's ReLU masks (each hidden layer's output > 0, taken where
+    # the fused ReLU + LayerNorm tail receives it): the reference applies
+    # them instead of its own, so that activations within rounding of zero,
+    # whose sign the two sides may see differently, do not move the
+    # comparison (a flipped unit passes or drops a whole gradient)
+    masks = []
+    tail = model._hidden_tail
+
+    def spy(l, h, training):
+        masks.append((h > 0).detach().cpu())
+        return tail(l, h, training)
+
+    model._hidden_tail = spy
+    with torch.autocast("cuda", dtype=torch.float16, enabled=dt == torch.float16):
         logits = model(blocks, feats)
-    assert logits.shape == (1024, 172)
+    del model._hidden_tail
+    assert logits.shape == (1024, 172) and len(masks) == 2
     loss = torch.nn.functional.cross_entropy(logits.float(), labels[seeds])
     loss.backward()
 
@@ -95,14 +119,23 @@ def test_block_step_c5_widths_f16(cuda_device):
     for l, (layer, A) in enumerate(zip(ref.layers, dense)):
         h = A @ (h @ layer.weight_neigh) + h[: A.shape[0]] @ layer.weight_self
         if l < 2:
-            h = ref.norms[l](torch.relu(h))
+            flips = int(((h > 0) != masks[l]).sum())
+            print(f"layer {l}: {flips} of {h.numel()} ReLU signs differ from the device's", flush=True)
+            h = ref.norms[l](h * masks[l])
     rl = torch.nn.functional.cross_entropy(h, labels[seeds].cpu())
     rl.backward()
-    assert abs(float(loss) - float(rl)) <= 1e-2 * abs(float(rl)), (float(loss), float(rl))
+    f16 = dt == torch.float16
+    assert abs(float(loss) - float(rl)) <= (1e-2 if f16 else 1e-4) * abs(float(rl)), (float(loss), float(rl))
+    fro_tol, max_tol = (1e-2, 1e-2) if f16 else (2e-5, 5e-5)
+    bad = []
     for (n, p), (_, q) in zip(model.named_parameters(), ref.named_parameters()):
         a, b = p.grad.double().cpu(), q.grad
-        err = float((a - b).abs().max())
-        assert err <= 3e-2 * max(float(b.abs().max()), 1e-30), (n, err, float(b.abs().max()))
+        fro = float((a - b).norm()) / max(float(b.norm()), 1e-30)
+        mx = float((a - b).abs().max()) / max(float(b.abs().max()), 1e-30)
+        print(f"{n}: error / largest {mx:.3e}, Frobenius {fro:.3e}", flush=True)
+        if fro > fro_tol or mx > max_tol:
+            bad.append((n, fro, mx))
+    assert not bad, bad
 
 
 @pytest.mark.parametrize("pipeline", [True, False])
