@@ -421,6 +421,32 @@ def bench_sampling(dev, batches: int, warmup: int, cpu: bool) -> dict:
                               "index, the source's degree, three relabel passes of 8 B) plus the block "
                               "written"},
     }
+    # the same plain call replayed from a HIP graph (NeighborSampler(capture=
+    # True): grws_sample_blocks_enqueue captured once per batch shape, the
+    # outputs copied out of the static buffers in one launch)
+    sp = NeighborSampler(c["fanouts"], seed=c["philox_seed"], tile_cols=16, capture=True)
+    for b in range(warmup):
+        sp.sample_layers(g.row_ptr, g.col_idx, seed_sets[b])
+    torch.cuda.synchronize(dev)
+    tp, pe, pb = [], 0, 0
+    for b in range(warmup, warmup + batches):
+        t1 = time.perf_counter()
+        bl = sp.sample_layers(g.row_ptr, g.col_idx, seed_sets[b])
+        torch.cuda.synchronize(dev)
+        tp.append(time.perf_counter() - t1)
+        pe += sum(x.num_sampled_edges for x in bl)
+        pb += sum(sampling_bytes(x) for x in bl)
+    tpt = sum(tp)
+    out["captured"] = {
+        "batch_ms": round(1e3 * tpt / batches, 4),
+        "sampled_edges_per_s": round(pe / tpt, 1),
+        "replays": sum(x.replays for x in sp._captures.values()),
+        "roofline": {"achieved": round(pb / tpt / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(pb / tpt / 1e9 / HBM_PEAK_GBS, 5), "bytes_per_batch": round(pb / batches)},
+        "note": "the plain call replayed from a HIP graph captured in the warm-up (the engine's mode); per "
+                "batch a seed copy, the replay, the counters read back (the batch's one sync) and one copy "
+                "launch for the outputs"}
+    del sp
     # the mini-batch engine's call: the same batches with the transposes of
     # the blocks whose backward multiplies by A^T (layers 1 and 2 of the
     # 3-layer model) built in the same device call

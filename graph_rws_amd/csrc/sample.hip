@@ -718,39 +718,22 @@ __global__ __launch_bounds__(kBlk) void mh_group_scan_kernel(const int32_t* __re
     }
 }
 
-// Local id of every filled slot's source (-1 for an empty slot, 0 for an
-// invalid id, which the sampler flagged), the next frontier's new ids, and
-// (threads below F) its first F entries.
-__global__ __launch_bounds__(kBlk) void mh_assign_kernel(const int64_t* __restrict__ frontier, int64_t F0, int h,
-                                                         int k, int64_t num_nodes,
-                                                         const int64_t* __restrict__ edge_src,
-                                                         const int32_t* __restrict__ node_map,
-                                                         const uint32_t* __restrict__ bitmap,
-                                                         const int32_t* __restrict__ grpoff,
-                                                         const int32_t* __restrict__ sliceoff,
-                                                         int32_t* __restrict__ src_local,
-                                                         int64_t* __restrict__ next_frontier,
-                                                         const BatchCtr* __restrict__ ctr) {
-    const int64_t F = hop_frontier(ctr, h, F0);
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < F) next_frontier[e] = frontier[e];
-    if (e >= F * (int64_t)k) return;
-    const int64_t s = edge_src[e];
-    if (s < 0) {
-        src_local[e] = -1;
-        return;
-    }
-    if (s >= num_nodes) {
-        src_local[e] = 0;
-        return;
-    }
+// Local id of a slot's source s (edge_src[e]): -1 for an empty slot, 0 for
+// an invalid id (the sampler flagged it), the frontier position of a
+// frontier node, else F + the new sources of earlier groups + the set bits
+// before it in its group (the group's 32 words are one 128-byte line); a new
+// source also writes its global id at its place in the next frontier (every
+// slot of that source writes the same value).
+__device__ __forceinline__ int32_t mh_local_id(int64_t s, int64_t F, int64_t num_nodes,
+                                               const int32_t* __restrict__ node_map,
+                                               const uint32_t* __restrict__ bitmap,
+                                               const int32_t* __restrict__ grpoff,
+                                               const int32_t* __restrict__ sliceoff,
+                                               int64_t* __restrict__ next_frontier) {
+    if (s < 0) return -1;
+    if (s >= num_nodes) return 0;
     const int32_t l = node_map[s];
-    if (l >= 0) {
-        src_local[e] = l;
-        return;
-    }
-    // new source: sources of earlier groups, then the set bits before it in
-    // its group (the group's 32 words are one 128-byte line)
+    if (l >= 0) return l;
     const int64_t g = s >> kGroupShift;
     const int wi = (int)((s >> 5) & 31);
     const u32x4_t* gw = reinterpret_cast<const u32x4_t*>(bitmap + (g << 5));
@@ -763,22 +746,82 @@ __global__ __launch_bounds__(kBlk) void mh_assign_kernel(const int64_t* __restri
     }
     below += __popc(bitmap[s >> 5] & ((1u << (s & 31)) - 1u));
     const int64_t local = F + sliceoff[g / kSliceGroups] + grpoff[g] + below;
-    src_local[e] = (int32_t)local;
-    next_frontier[local] = s;  // every slot of this source writes the same value
+    next_frontier[local] = s;
+    return (int32_t)local;
 }
 
-// One work-group per 16-row window of the hop's block, slots
+// Count pass of a hop's block, one work-group per 16-row window, slots
+// [16 w k, min(16 w + 16, F) k): the local id of every slot's source
+// (mh_local_id) into src_local, the window's rows into the next frontier's
+// first F entries, and the window's tiles: its distinct local ids, counted
+// by insertion into an LDS hash set (open addressing, at most half full;
+// no sort: the fill pass sorts), over tc per tile.  The relabel state stays
+// as it is here (other windows still read it); the fill pass restores it.
+__global__ __launch_bounds__(kBlk) void mh_wcount_kernel(const int64_t* __restrict__ frontier, int64_t F0, int h,
+                                                         int k, int64_t num_nodes,
+                                                         const int64_t* __restrict__ edge_src,
+                                                         const int32_t* __restrict__ node_map,
+                                                         const uint32_t* __restrict__ bitmap,
+                                                         const int32_t* __restrict__ grpoff,
+                                                         const int32_t* __restrict__ sliceoff,
+                                                         int32_t* __restrict__ src_local,
+                                                         int64_t* __restrict__ next_frontier, int tc,
+                                                         int32_t* __restrict__ wtiles,
+                                                         const BatchCtr* __restrict__ ctr) {
+    __shared__ uint32_t tab[2 * kWinEdges];
+    __shared__ int64_t scan_tmp[kBlk / kWave + 1];
+    const int tid = threadIdx.x;
+    const int64_t F = hop_frontier(ctr, h, F0);
+    const int64_t W = (F + 15) / 16;
+    const int64_t w = blockIdx.x;
+    if (w >= W) {
+        if (tid == 0) wtiles[w] = 0;
+        return;
+    }
+    const int64_t r0 = w * 16;
+    const int rows = (int)(F - r0 < 16 ? F - r0 : 16);
+    const int64_t s0 = r0 * k;
+    const int ns = rows * k;  // <= kWinEdges
+    int TS = 64;
+    while (TS < 2 * ns) TS <<= 1;
+    if (tid < rows) next_frontier[r0 + tid] = frontier[r0 + tid];
+    for (int i = tid; i < TS; i += kBlk) tab[i] = 0xffffffffu;
+    __syncthreads();
+    int cnt = 0;
+    for (int i = tid; i < ns; i += kBlk) {
+        const int32_t c = mh_local_id(edge_src[s0 + i], F, num_nodes, node_map, bitmap, grpoff, sliceoff,
+                                      next_frontier);
+        src_local[s0 + i] = c;
+        if (c < 0) continue;
+        uint32_t q = ((uint32_t)c * 0x9E3779B1u) >> 16;
+        for (;;) {  // at most TS probes: the set holds at most ns < TS ids
+            q &= (uint32_t)(TS - 1);
+            const uint32_t old = atomicCAS(&tab[q], 0xffffffffu, (uint32_t)c);
+            if (old == 0xffffffffu) {
+                ++cnt;
+                break;
+            }
+            if (old == (uint32_t)c) break;
+            ++q;
+        }
+    }
+    int64_t total;
+    block_incl_scan<kBlk>(cnt, scan_tmp, &total);
+    if (tid == 0) wtiles[w] = (int32_t)((total + tc - 1) / tc);
+}
+
+// Fill pass of a hop's block, one work-group per 16-row window, slots
 // [16 w k, min(16 w + 16, F) k): sorted in LDS by (column, row, slot), the
-// distinct columns numbered; count pass: tiles per window, and the window's
-// share of the state restored (its rows' node map entries, its sources' bitmap
-// words and group counts); fill pass: the tiles.  Same rules as
+// distinct columns numbered and the window's tiles written, at the offsets
+// the scan of the count pass's tiles gave; then the window's share of the
+// relabel state restored (its rows' node map entries, its sources' bitmap
+// words and group counts; every local id is known by now).  Same rules as
 // block_window_kernel (the last of duplicate (row, column) slots wins).
 template <typename VT>
-__global__ __launch_bounds__(256) void mh_window_kernel(int fill, const int64_t* __restrict__ frontier, int64_t F0,
+__global__ __launch_bounds__(256) void mh_window_kernel(const int64_t* __restrict__ frontier, int64_t F0,
                                                         int h, int k, const int32_t* __restrict__ src_local,
                                                         const int64_t* __restrict__ edge_src,
-                                                        const float* __restrict__ edge_val, int tc,
-                                                        int32_t* __restrict__ wtiles, int64_t wcap,
+                                                        const float* __restrict__ edge_val, int tc, int64_t wcap,
                                                         const int64_t* __restrict__ window_offset,
                                                         int32_t* __restrict__ out_cols, VT* __restrict__ out_vals,
                                                         int64_t num_nodes, int32_t* __restrict__ node_map,
@@ -791,11 +834,8 @@ __global__ __launch_bounds__(256) void mh_window_kernel(int fill, const int64_t*
     const int64_t F = hop_frontier(ctr, h, F0);
     const int64_t W = (F + 15) / 16;
     const int64_t w = blockIdx.x;
-    if (fill && w == 0 && tid == 0) ctr->T[h] = window_offset[wcap];
-    if (w >= W) {
-        if (!fill && tid == 0) wtiles[w] = 0;
-        return;
-    }
+    if (w == 0 && tid == 0) ctr->T[h] = window_offset[wcap];
+    if (w >= W) return;
     const int64_t r0 = w * 16;
     const int rows = (int)(F - r0 < 16 ? F - r0 : 16);
     const int64_t s0 = r0 * k;
@@ -810,19 +850,18 @@ __global__ __launch_bounds__(256) void mh_window_kernel(int fill, const int64_t*
         }
         key[i] = kk;
     }
-    if (!fill) {
-        // restore the state this hop changed: node map of the window's rows,
-        // bitmap words and group counts of its sources (the relabel is done)
-        if (tid < rows) {
-            const int64_t v = frontier[r0 + tid];
-            if (v >= 0 && v < num_nodes) node_map[v] = -1;
-        }
-        for (int i = tid; i < ns; i += kBlk) {
-            const int64_t s = edge_src[s0 + i];
-            if (s >= 0 && s < num_nodes) {
-                bitmap[s >> 5] = 0u;
-                grpcnt[s >> kGroupShift] = 0;
-            }
+    // restore the state this hop changed: node map of the window's rows,
+    // bitmap words and group counts of its sources (the count pass, which
+    // read them, has finished)
+    if (tid < rows) {
+        const int64_t v = frontier[r0 + tid];
+        if (v >= 0 && v < num_nodes) node_map[v] = -1;
+    }
+    for (int i = tid; i < ns; i += kBlk) {
+        const int64_t s = edge_src[s0 + i];
+        if (s >= 0 && s < num_nodes) {
+            bitmap[s >> 5] = 0u;
+            grpcnt[s >> kGroupShift] = 0;
         }
     }
     __syncthreads();
@@ -883,10 +922,6 @@ __global__ __launch_bounds__(256) void mh_window_kernel(int fill, const int64_t*
         }
     }
     const int64_t tiles = (total + tc - 1) / tc;
-    if (!fill) {
-        if (tid == 0) wtiles[w] = (int32_t)tiles;
-        return;
-    }
     __syncthreads();
     const int64_t wo = window_offset[w];
     for (int64_t i = tid; i < tiles * tc; i += kBlk) out_cols[wo * tc + i] = -1;
@@ -1615,22 +1650,18 @@ static int sample_blocks_impl(const int64_t* indptr, const int32_t* indices, int
         hipLaunchKernelGGL(mh_group_scan_kernel, dim3((unsigned)nslices), dim3(kBlk), 0, stream, grpcnt, l.groups,
                            w.grpoff, w.slicesum, w.sliceoff, nslices, F0, h, ctr);
         GRWS_LAUNCH_CHECK();
-        hipLaunchKernelGGL(mh_assign_kernel, dim3(grid_for(c.E[h])), dim3(kBlk), 0, stream, fr, F0, h, k,
-                           num_nodes, w.edge_src, node_map, bitmap, w.grpoff, w.sliceoff, w.src_local,
-                           next_frontier[h], ctr);
-        GRWS_LAUNCH_CHECK();
-#define GRWS_MH_WINDOWS(FILL, VT)                                                                                  \
-    hipLaunchKernelGGL(mh_window_kernel<VT>, dim3((unsigned)Wc), dim3(kBlk), 0, stream, FILL, fr, F0, h, k,           \
-                       w.src_local, w.edge_src, w.edge_val, tc, w.wtiles, Wc, window_offset[h], col_indices[h],       \
-                       static_cast<VT*>(values[h]), num_nodes, node_map, bitmap, grpcnt, ctr)
-        if (values_dtype == GRWS_F32) GRWS_MH_WINDOWS(0, float);
-        else if (values_dtype == GRWS_F16) GRWS_MH_WINDOWS(0, _Float16);
-        else GRWS_MH_WINDOWS(0, __hip_bfloat16);
+        hipLaunchKernelGGL(mh_wcount_kernel, dim3((unsigned)Wc), dim3(kBlk), 0, stream, fr, F0, h, k, num_nodes,
+                           w.edge_src, node_map, bitmap, w.grpoff, w.sliceoff, w.src_local, next_frontier[h], tc,
+                           w.wtiles, ctr);
         GRWS_LAUNCH_CHECK();
         GRWS_TRY(scan_i32_to_i64(w.wtiles, window_offset[h], Wc, false, w.scan_ws, w.scan_bytes, stream));
-        if (values_dtype == GRWS_F32) GRWS_MH_WINDOWS(1, float);
-        else if (values_dtype == GRWS_F16) GRWS_MH_WINDOWS(1, _Float16);
-        else GRWS_MH_WINDOWS(1, __hip_bfloat16);
+#define GRWS_MH_WINDOWS(VT)                                                                                        \
+    hipLaunchKernelGGL(mh_window_kernel<VT>, dim3((unsigned)Wc), dim3(kBlk), 0, stream, fr, F0, h, k, w.src_local,   \
+                       w.edge_src, w.edge_val, tc, Wc, window_offset[h], col_indices[h],                              \
+                       static_cast<VT*>(values[h]), num_nodes, node_map, bitmap, grpcnt, ctr)
+        if (values_dtype == GRWS_F32) GRWS_MH_WINDOWS(float);
+        else if (values_dtype == GRWS_F16) GRWS_MH_WINDOWS(_Float16);
+        else GRWS_MH_WINDOWS(__hip_bfloat16);
 #undef GRWS_MH_WINDOWS
         GRWS_LAUNCH_CHECK();
         if (any_t && thops[h]) {
