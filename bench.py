@@ -402,6 +402,8 @@ def bench_sampling(dev, batches: int, warmup: int, cpu: bool) -> dict:
     total = sum(times)
     sgbs = b_alg / total / 1e9
     out = {
+        "mode": "eager (grws_sample_blocks per batch); the captured mode below replays the same call "
+                "from a HIP graph and is the one the mini-batch engine runs",
         "workload": "c5 mini-batch sampling (Philox fanout [15,10,5], unique+relabel, per-hop BCSR)",
         "graph": {"nodes": g.num_nodes, "edges": g.nnz, "indptr": "int64", "indices": "int32"},
         "batches": batches, "seeds_per_batch": c["batch"],
@@ -411,9 +413,9 @@ def bench_sampling(dev, batches: int, warmup: int, cpu: bool) -> dict:
         "hop_edges_last_batch": [x.num_sampled_edges for x in blocks],
         "input_nodes_last_batch": int(blocks[0].num_cols),
         "generate_s": round(t_gen, 2),
-        "dispatches_per_batch": 7 * len(c["fanouts"]) + 2,
+        "dispatches_per_batch": 4 * len(c["fanouts"]) + 2,
         "host_syncs_per_batch": 1,
-        "roofline": {"bound": "hbm (random 8-64 B reads: latency bound in practice)",
+        "roofline_eager": {"bound": "hbm (random 8-64 B reads: latency bound in practice)",
                      "achieved": round(sgbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(sgbs / HBM_PEAK_GBS, 5),
                      "bytes_per_batch": round(b_alg / batches),
@@ -441,11 +443,17 @@ def bench_sampling(dev, batches: int, warmup: int, cpu: bool) -> dict:
         "batch_ms": round(1e3 * tpt / batches, 4),
         "sampled_edges_per_s": round(pe / tpt, 1),
         "replays": sum(x.replays for x in sp._captures.values()),
-        "roofline": {"achieved": round(pb / tpt / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(pb / tpt / 1e9 / HBM_PEAK_GBS, 5), "bytes_per_batch": round(pb / batches)},
         "note": "the plain call replayed from a HIP graph captured in the warm-up (the engine's mode); per "
-                "batch a seed copy, the replay, the counters read back (the batch's one sync) and one copy "
-                "launch for the outputs"}
+                "batch one launch staging the seeds and their count, the replay, the counters read back (the "
+                "batch's one sync) and one copy launch for the outputs"}
+    # the record's roofline: the captured call, the mode the engine runs
+    out["roofline"] = {"bound": "hbm (random 8-64 B reads: latency bound in practice)",
+                       "mode": "captured (replayed from a HIP graph)",
+                       "achieved": round(pb / tpt / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(pb / tpt / 1e9 / HBM_PEAK_GBS, 5), "bytes_per_batch": round(pb / batches),
+                       "bytes": "per hop 16 F + 36 E (indptr pair and frontier id per node; per edge the "
+                                "index, the source's degree, three relabel passes of 8 B) plus the block "
+                                "written"}
     del sp
     # the mini-batch engine's call: the same batches with the transposes of
     # the blocks whose backward multiplies by A^T (layers 1 and 2 of the

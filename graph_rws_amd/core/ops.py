@@ -1124,8 +1124,14 @@ class CapturedSampleBlocks:
         self.wsb = wsb
         self.esz = torch.empty(0, dtype=values_dtype).element_size()
         i64 = torch.int64
-        self.sin = torch.empty(1 + self.max_seeds, dtype=i64, device=dev)  # [count, seeds...]
-        self.pin = torch.empty(1 + self.max_seeds, dtype=i64, pin_memory=True)
+        # the seed count and the seeds the captured call reads; the count
+        # arrives by a device copy from a table of [i, 0] pairs, in the same
+        # launch as the seeds (16-byte aligned both)
+        self.cnt_in = torch.zeros(2, dtype=i64, device=dev)
+        self.seeds_buf = torch.empty(self.max_seeds, dtype=i64, device=dev)
+        self.cnt_table = torch.stack([torch.arange(self.max_seeds + 1, dtype=i64),
+                                      torch.zeros(self.max_seeds + 1, dtype=i64)], 1).contiguous().to(dev)
+        self.pin = torch.empty(self.max_seeds, dtype=i64, pin_memory=True)
         self.nxt = [torch.empty(max(1, ms[h]), dtype=i64, device=dev) for h in range(H)]
         self.win = [torch.empty((fcap[h] + 15) // 16 + 1, dtype=i64, device=dev) for h in range(H)]
         self.cols = [torch.empty(max(1, mt[h] * tc), dtype=torch.int32, device=dev) for h in range(H)]
@@ -1144,7 +1150,7 @@ class CapturedSampleBlocks:
 
     def _enqueue(self, stream) -> None:
         L.call("grws_sample_blocks_enqueue", L.ptr(self.indptr), L.ptr(self.indices), self.n, self.nnz,
-               ctypes.c_void_p(self.sin.data_ptr() + 8), self.max_seeds, L.ptr(self.sin), self.fo, self.H,
+               L.ptr(self.seeds_buf), self.max_seeds, L.ptr(self.cnt_in), self.fo, self.H,
                ctypes.c_uint64(self.seed & 0xFFFFFFFFFFFFFFFF), L.ptr(self.state.node_map),
                L.ptr(self.state.bitmap), self.tc, L.dtype_code(self.values_dtype), self._parr(self.nxt),
                self._parr(self.win), self._parr(self.cols), self._parr(self.vals), self.th,
@@ -1156,15 +1162,27 @@ class CapturedSampleBlocks:
         if F0 > self.max_seeds:
             raise ValueError(f"CapturedSampleBlocks: {F0} seeds above the capacity {self.max_seeds}")
         stream = torch.cuda.current_stream(self.dev)
-        # stage the count and the seeds (the pinned buffer is free again: the
-        # previous call synchronised after its copy)
-        self.pin[0] = F0
-        if seeds.is_cuda:
-            self.sin[1:1 + F0].copy_(seeds.view(-1).to(torch.int64))
-            self.sin[:1].copy_(self.pin[:1], non_blocking=True)
+        # stage the count and the seeds: device seeds (int64, 16-byte
+        # aligned) and the count in one copy launch; host seeds through the
+        # pinned buffer (free again: the previous call synchronised after
+        # its copy)
+        sd = seeds.view(-1)
+        if sd.is_cuda and sd.dtype == torch.int64 and sd.data_ptr() % 16 == 0:
+            srcs, dsts, nb = [self.cnt_table.data_ptr() + 16 * F0], [self.cnt_in.data_ptr()], [16]
+            if F0:
+                srcs.append(sd.data_ptr())
+                dsts.append(self.seeds_buf.data_ptr())
+                nb.append(8 * F0)
+            m = len(srcs)
+            L.call("grws_copy_ranges", (ctypes.c_void_p * m)(*srcs), (ctypes.c_void_p * m)(*dsts),
+                   (ctypes.c_int64 * m)(*nb), m, ctypes.c_void_p(stream.cuda_stream))
         else:
-            self.pin[1:1 + F0].copy_(seeds.view(-1).to(torch.int64))
-            self.sin[:1 + F0].copy_(self.pin[:1 + F0], non_blocking=True)
+            if sd.is_cuda:
+                self.seeds_buf[:F0].copy_(sd.to(torch.int64))
+            else:
+                self.pin[:F0].copy_(sd.to(torch.int64))
+                self.seeds_buf[:F0].copy_(self.pin[:F0], non_blocking=True)
+            self.cnt_in.copy_(self.cnt_table[F0])
         if self.graph is None:
             self._enqueue(stream)  # this batch, and every kernel loaded before the capture
             cs = torch.cuda.Stream(self.dev)

@@ -550,9 +550,12 @@ void carve_block(C& cv, int64_t F, int32_t k, int64_t num_nodes, BlockWs* w) {
 constexpr int kMaxHops = 8;
 constexpr int kGroupShift = 10;  // 1024 ids (32 bitmap words) per group
 
+constexpr int kESub = 16;   // sub-counters per hop's edge count (fewer atomics on one address)
+
 struct BatchCtr {
     int64_t F[kMaxHops + 1];  // frontier size of each hop (F[h+1] = sources of hop h)
     int64_t E[kMaxHops];      // sampled edges of each hop
+    int64_t Esub[kMaxHops][kESub];  // the count pass's per-window adds (window w into w % kESub)
     int64_t T[kMaxHops];      // tiles of each hop's block
     int64_t TT[kMaxHops];     // tiles of each hop's transposed block
     int32_t TM[kMaxHops];     // most tiles in one window of the transposed block
@@ -580,28 +583,26 @@ __global__ void mh_start_kernel(const int64_t* __restrict__ num_seeds_dev, int64
     if (!ok) atomicOr(&ctr->err, kErrCount);
 }
 
-// Per frontier node: min(deg, k) and the node map entry; edge total per hop.
-__global__ __launch_bounds__(kBlk) void mh_count_kernel(const int64_t* __restrict__ indptr, int64_t nnz,
-                                                        int64_t num_nodes, const int64_t* __restrict__ frontier,
-                                                        int64_t F0, int h, int k, int32_t* __restrict__ node_map,
-                                                        BatchCtr* __restrict__ ctr) {
-    const int64_t F = hop_frontier(ctr, h, F0);
+// The seeds' node map entries (hop 0's frontier positions), duplicates and
+// bad ids flagged.  Later hops need no such pass: the node map keeps every
+// entry through the batch (a hop's frontier is the previous frontier, at the
+// same positions, followed by its new sources, which the count pass maps),
+// and the last hop's fill pass clears it.
+__global__ __launch_bounds__(kBlk) void mh_seed_kernel(const int64_t* __restrict__ indptr, int64_t nnz,
+                                                       int64_t num_nodes, const int64_t* __restrict__ seeds,
+                                                       int64_t F0, int32_t* __restrict__ node_map,
+                                                       BatchCtr* __restrict__ ctr) {
+    const int64_t F = hop_frontier(ctr, 0, F0);
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (h == 0 && i == 0 && F0 >= 0) ctr->F[0] = F0;
-    int64_t c = 0;
-    if (i < F) {
-        const int64_t v = frontier[i];
-        const NodeRange r = node_range(indptr, nnz, num_nodes, v);
-        if (r.err) {
-            atomicOr(&ctr->err, r.err);
-        } else if (atomicExch(&node_map[v], (int32_t)i) != -1) {
-            atomicOr(&ctr->err, kErrDup);
-        }
-        c = r.deg < k ? r.deg : k;
+    if (i == 0 && F0 >= 0) ctr->F[0] = F0;
+    if (i >= F) return;
+    const int64_t v = seeds[i];
+    const NodeRange r = node_range(indptr, nnz, num_nodes, v);
+    if (r.err) {
+        atomicOr(&ctr->err, r.err);
+    } else if (atomicExch(&node_map[v], (int32_t)i) != -1) {
+        atomicOr(&ctr->err, kErrDup);
     }
-    // one atomic per wave
-    for (int d = 32; d > 0; d >>= 1) c += __shfl_xor(c, d, kWave);
-    if (lane_id() == 0 && c) atomicAdd((unsigned long long*)&ctr->E[h], (unsigned long long)c);
 }
 
 // One wave per frontier node: the hop_sample_kernel draw into fixed slots,
@@ -620,6 +621,7 @@ __global__ __launch_bounds__(kBlk) void mh_sample_kernel(const int64_t* __restri
     const int lane = lane_id();
     const int64_t v = frontier[i];
     const NodeRange r = node_range(indptr, nnz, num_nodes, v);
+    if (r.err && lane == 0) atomicOr(&ctr->err, r.err);
     const int64_t deg = r.err ? 0 : r.deg;
     int64_t x = lane;
     int rank = lane;
@@ -723,9 +725,10 @@ __global__ __launch_bounds__(kBlk) void mh_group_scan_kernel(const int32_t* __re
 // frontier node, else F + the new sources of earlier groups + the set bits
 // before it in its group (the group's 32 words are one 128-byte line); a new
 // source also writes its global id at its place in the next frontier (every
-// slot of that source writes the same value).
+// slot of that source writes the same value) and, with map_new (every hop but
+// the last), its local id into the node map.
 __device__ __forceinline__ int32_t mh_local_id(int64_t s, int64_t F, int64_t num_nodes,
-                                               const int32_t* __restrict__ node_map,
+                                               int32_t* __restrict__ node_map, bool map_new,
                                                const uint32_t* __restrict__ bitmap,
                                                const int32_t* __restrict__ grpoff,
                                                const int32_t* __restrict__ sliceoff,
@@ -747,27 +750,31 @@ __device__ __forceinline__ int32_t mh_local_id(int64_t s, int64_t F, int64_t num
     below += __popc(bitmap[s >> 5] & ((1u << (s & 31)) - 1u));
     const int64_t local = F + sliceoff[g / kSliceGroups] + grpoff[g] + below;
     next_frontier[local] = s;
+    // the next hop's frontier position of s; a slot of this hop that reads
+    // the entry early takes the frontier branch above and gets the same id
+    if (map_new) node_map[s] = (int32_t)local;
     return (int32_t)local;
 }
 
 // Count pass of a hop's block, one work-group per 16-row window, slots
 // [16 w k, min(16 w + 16, F) k): the local id of every slot's source
 // (mh_local_id) into src_local, the window's rows into the next frontier's
-// first F entries, and the window's tiles: its distinct local ids, counted
-// by insertion into an LDS hash set (open addressing, at most half full;
-// no sort: the fill pass sorts), over tc per tile.  The relabel state stays
-// as it is here (other windows still read it); the fill pass restores it.
+// first F entries, the window's tiles (its distinct local ids, counted by
+// insertion into an LDS hash set: open addressing, at most half full; no
+// sort, the fill pass sorts; over tc per tile) and its filled slots added to
+// one of the hop's edge sub-counters.  The relabel state stays as it is here
+// (other windows still read it); the fill pass restores it.
 __global__ __launch_bounds__(kBlk) void mh_wcount_kernel(const int64_t* __restrict__ frontier, int64_t F0, int h,
                                                          int k, int64_t num_nodes,
                                                          const int64_t* __restrict__ edge_src,
-                                                         const int32_t* __restrict__ node_map,
+                                                         int32_t* __restrict__ node_map, int map_new,
                                                          const uint32_t* __restrict__ bitmap,
                                                          const int32_t* __restrict__ grpoff,
                                                          const int32_t* __restrict__ sliceoff,
                                                          int32_t* __restrict__ src_local,
                                                          int64_t* __restrict__ next_frontier, int tc,
                                                          int32_t* __restrict__ wtiles,
-                                                         const BatchCtr* __restrict__ ctr) {
+                                                         BatchCtr* __restrict__ ctr) {
     __shared__ uint32_t tab[2 * kWinEdges];
     __shared__ int64_t scan_tmp[kBlk / kWave + 1];
     const int tid = threadIdx.x;
@@ -787,12 +794,14 @@ __global__ __launch_bounds__(kBlk) void mh_wcount_kernel(const int64_t* __restri
     if (tid < rows) next_frontier[r0 + tid] = frontier[r0 + tid];
     for (int i = tid; i < TS; i += kBlk) tab[i] = 0xffffffffu;
     __syncthreads();
-    int cnt = 0;
+    // distinct ids (low 32 bits) and filled slots (high 32 bits) in one sum
+    int64_t cnt = 0;
     for (int i = tid; i < ns; i += kBlk) {
-        const int32_t c = mh_local_id(edge_src[s0 + i], F, num_nodes, node_map, bitmap, grpoff, sliceoff,
-                                      next_frontier);
+        const int32_t c = mh_local_id(edge_src[s0 + i], F, num_nodes, node_map, map_new != 0, bitmap, grpoff,
+                                      sliceoff, next_frontier);
         src_local[s0 + i] = c;
         if (c < 0) continue;
+        cnt += (int64_t)1 << 32;
         uint32_t q = ((uint32_t)c * 0x9E3779B1u) >> 16;
         for (;;) {  // at most TS probes: the set holds at most ns < TS ids
             q &= (uint32_t)(TS - 1);
@@ -807,26 +816,32 @@ __global__ __launch_bounds__(kBlk) void mh_wcount_kernel(const int64_t* __restri
     }
     int64_t total;
     block_incl_scan<kBlk>(cnt, scan_tmp, &total);
-    if (tid == 0) wtiles[w] = (int32_t)((total + tc - 1) / tc);
+    if (tid == 0) {
+        const int64_t distinct = total & 0xffffffffll;
+        wtiles[w] = (int32_t)((distinct + tc - 1) / tc);
+        if (total >> 32)  // sampled edges, spread over the hop's sub-counters
+            atomicAdd((unsigned long long*)&ctr->Esub[h][w % kESub], (unsigned long long)(total >> 32));
+    }
 }
 
 // Fill pass of a hop's block, one work-group per 16-row window, slots
 // [16 w k, min(16 w + 16, F) k): sorted in LDS by (column, row, slot), the
-// distinct columns numbered and the window's tiles written, at the offsets
-// the scan of the count pass's tiles gave; then the window's share of the
-// relabel state restored (its rows' node map entries, its sources' bitmap
-// words and group counts; every local id is known by now).  Same rules as
+// distinct columns numbered and the window's tiles written, at the offset
+// the count pass's tiles of the earlier windows sum to; then the window's share of the
+// relabel state restored (its sources' bitmap words and group counts, and in
+// the last hop its rows' node map entries; every local id is known by now).  Same rules as
 // block_window_kernel (the last of duplicate (row, column) slots wins).
 template <typename VT>
 __global__ __launch_bounds__(256) void mh_window_kernel(const int64_t* __restrict__ frontier, int64_t F0,
                                                         int h, int k, const int32_t* __restrict__ src_local,
                                                         const int64_t* __restrict__ edge_src,
-                                                        const float* __restrict__ edge_val, int tc, int64_t wcap,
-                                                        const int64_t* __restrict__ window_offset,
+                                                        const float* __restrict__ edge_val, int tc,
+                                                        const int32_t* __restrict__ wtiles,
+                                                        int64_t* __restrict__ window_offset,
                                                         int32_t* __restrict__ out_cols, VT* __restrict__ out_vals,
                                                         int64_t num_nodes, int32_t* __restrict__ node_map,
-                                                        uint32_t* __restrict__ bitmap, int32_t* __restrict__ grpcnt,
-                                                        BatchCtr* __restrict__ ctr) {
+                                                        int last, uint32_t* __restrict__ bitmap,
+                                                        int32_t* __restrict__ grpcnt, BatchCtr* __restrict__ ctr) {
     __shared__ uint64_t key[kWinEdges];
     __shared__ int32_t pos[kWinEdges];
     __shared__ int64_t scan_tmp[kBlk / kWave + 1];
@@ -834,7 +849,7 @@ __global__ __launch_bounds__(256) void mh_window_kernel(const int64_t* __restric
     const int64_t F = hop_frontier(ctr, h, F0);
     const int64_t W = (F + 15) / 16;
     const int64_t w = blockIdx.x;
-    if (w == 0 && tid == 0) ctr->T[h] = window_offset[wcap];
+    if (w == 0 && tid == 0) window_offset[0] = 0;
     if (w >= W) return;
     const int64_t r0 = w * 16;
     const int rows = (int)(F - r0 < 16 ? F - r0 : 16);
@@ -850,10 +865,11 @@ __global__ __launch_bounds__(256) void mh_window_kernel(const int64_t* __restric
         }
         key[i] = kk;
     }
-    // restore the state this hop changed: node map of the window's rows,
-    // bitmap words and group counts of its sources (the count pass, which
-    // read them, has finished)
-    if (tid < rows) {
+    // restore the state this hop changed: bitmap words and group counts of
+    // its sources (the count pass, which read them, has finished); in the
+    // last hop also the node map of the window's rows, which by then are
+    // every node the batch mapped
+    if (last && tid < rows) {
         const int64_t v = frontier[r0 + tid];
         if (v >= 0 && v < num_nodes) node_map[v] = -1;
     }
@@ -922,8 +938,17 @@ __global__ __launch_bounds__(256) void mh_window_kernel(const int64_t* __restric
         }
     }
     const int64_t tiles = (total + tc - 1) / tc;
-    __syncthreads();
-    const int64_t wo = window_offset[w];
+    // the window's first tile: the count pass's tiles of the windows before
+    // it, summed by this work-group (no scan launch; at most a few thousand
+    // windows per hop); the last window writes the total
+    int64_t part = 0;
+    for (int64_t v = tid; v < w; v += kBlk) part += wtiles[v];
+    int64_t wo;
+    block_incl_scan<kBlk>(part, scan_tmp, &wo);
+    if (tid == 0) {
+        window_offset[w + 1] = wo + tiles;
+        if (w == W - 1) ctr->T[h] = wo + tiles;
+    }
     for (int64_t i = tid; i < tiles * tc; i += kBlk) out_cols[wo * tc + i] = -1;
     for (int64_t i = tid; i < tiles * 16 * tc; i += kBlk) out_vals[wo * 16 * tc + i] = cvt_value<VT>(0.0f);
     __syncthreads();
@@ -1097,7 +1122,10 @@ __global__ void mh_finish_kernel(BatchCtr* __restrict__ ctr, int64_t* __restrict
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     for (int h = 0; h <= H; ++h) out[h] = ctr->F[h];
     for (int h = 0; h < H; ++h) {
-        out[H + 1 + h] = ctr->E[h];
+        int64_t e = ctr->E[h];
+#pragma unroll
+        for (int j = 0; j < kESub; ++j) e += ctr->Esub[h][j];
+        out[H + 1 + h] = e;
         out[2 * H + 1 + h] = ctr->T[h];
         out[3 * H + 1 + h] = ctr->TT[h];
         out[4 * H + 1 + h] = ctr->TM[h];
@@ -1106,6 +1134,7 @@ __global__ void mh_finish_kernel(BatchCtr* __restrict__ ctr, int64_t* __restrict
     for (int h = 0; h <= kMaxHops; ++h) ctr->F[h] = 0;
     for (int h = 0; h < kMaxHops; ++h) {
         ctr->E[h] = ctr->T[h] = ctr->TT[h] = 0;
+        for (int j = 0; j < kESub; ++j) ctr->Esub[h][j] = 0;
         ctr->TM[h] = 0;
     }
     ctr->err = 0;
@@ -1639,9 +1668,11 @@ static int sample_blocks_impl(const int64_t* indptr, const int32_t* indices, int
         const int k = fanouts[h];
         const int64_t Fc = c.F[h], Wc = c.W[h];
         const int64_t* fr = h == 0 ? seeds : next_frontier[h - 1];
-        hipLaunchKernelGGL(mh_count_kernel, dim3(grid_for(Fc)), dim3(kBlk), 0, stream, indptr, nnz, num_nodes, fr,
-                           F0, h, k, node_map, ctr);
-        GRWS_LAUNCH_CHECK();
+        if (h == 0) {
+            hipLaunchKernelGGL(mh_seed_kernel, dim3(grid_for(Fc)), dim3(kBlk), 0, stream, indptr, nnz, num_nodes,
+                               fr, F0, node_map, ctr);
+            GRWS_LAUNCH_CHECK();
+        }
         hipLaunchKernelGGL(mh_sample_kernel, dim3(grid_for(Fc, kWavesPerBlock)), dim3(kBlk), 0, stream, indptr,
                            indices, nnz, num_nodes, fr, F0, h, k, seed, node_map, bitmap, grpcnt, w.edge_src,
                            w.edge_val, ctr);
@@ -1651,14 +1682,13 @@ static int sample_blocks_impl(const int64_t* indptr, const int32_t* indices, int
                            w.grpoff, w.slicesum, w.sliceoff, nslices, F0, h, ctr);
         GRWS_LAUNCH_CHECK();
         hipLaunchKernelGGL(mh_wcount_kernel, dim3((unsigned)Wc), dim3(kBlk), 0, stream, fr, F0, h, k, num_nodes,
-                           w.edge_src, node_map, bitmap, w.grpoff, w.sliceoff, w.src_local, next_frontier[h], tc,
-                           w.wtiles, ctr);
+                           w.edge_src, node_map, (int)(h + 1 < H), bitmap, w.grpoff, w.sliceoff, w.src_local,
+                           next_frontier[h], tc, w.wtiles, ctr);
         GRWS_LAUNCH_CHECK();
-        GRWS_TRY(scan_i32_to_i64(w.wtiles, window_offset[h], Wc, false, w.scan_ws, w.scan_bytes, stream));
 #define GRWS_MH_WINDOWS(VT)                                                                                        \
     hipLaunchKernelGGL(mh_window_kernel<VT>, dim3((unsigned)Wc), dim3(kBlk), 0, stream, fr, F0, h, k, w.src_local,   \
-                       w.edge_src, w.edge_val, tc, Wc, window_offset[h], col_indices[h],                              \
-                       static_cast<VT*>(values[h]), num_nodes, node_map, bitmap, grpcnt, ctr)
+                       w.edge_src, w.edge_val, tc, w.wtiles, window_offset[h], col_indices[h],                        \
+                       static_cast<VT*>(values[h]), num_nodes, node_map, (int)(h + 1 == H), bitmap, grpcnt, ctr)
         if (values_dtype == GRWS_F32) GRWS_MH_WINDOWS(float);
         else if (values_dtype == GRWS_F16) GRWS_MH_WINDOWS(_Float16);
         else GRWS_MH_WINDOWS(__hip_bfloat16);

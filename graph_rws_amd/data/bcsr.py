@@ -26,6 +26,14 @@ import torch
 from ..core import csr_to_bcsr_cpu, build_spmm_plan, default_slabs
 
 
+def _placed(t: torch.Tensor, device, dtype: torch.dtype) -> torch.Tensor:
+    """t on `device` with `dtype`: t itself when it already is (the common
+    case of arrays made on the device, e.g. sampled blocks), else a copy."""
+    if t.dtype == dtype and (device is None or t.device == device):
+        return t
+    return t.to(device, non_blocking=True).to(dtype)
+
+
 class BCSRGraph:
     """BCSR graph (data/bcsr.py:23-62)."""
 
@@ -43,9 +51,9 @@ class BCSRGraph:
                  values_dtype: Optional[torch.dtype] = None) -> None:
         self.device = device
         vdt = torch.float32 if values_dtype is None else values_dtype
-        self.window_offset = window_offset.to(device, non_blocking=True).to(torch.int64)
-        self.original_col_indices = original_col_indices.to(device, non_blocking=True).to(torch.int32)
-        self.values_condensed = values_condensed.to(device, non_blocking=True).to(vdt)
+        self.window_offset = _placed(window_offset, device, torch.int64)
+        self.original_col_indices = _placed(original_col_indices, device, torch.int32)
+        self.values_condensed = _placed(values_condensed, device, vdt)
         self.num_rows = int(num_rows) if num_rows is not None else int(num_nodes)
         self.num_cols = int(num_cols) if num_cols is not None else int(num_nodes)
         self.num_nodes = int(num_nodes)
