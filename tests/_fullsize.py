@@ -112,6 +112,25 @@ def col_nnz(hg: "HostGraph", n: int) -> np.ndarray:
     return np.bincount(hg.cols[valid], weights=cnt[valid], minlength=n)[:n]
 
 
+def rows_nnz_of(win: np.ndarray, vals: np.ndarray, tc: int, dt: str = "f32") -> np.ndarray:
+    """Non-zero values of every output row of a BCSR (window offsets and
+    values of any stored type), [16W]."""
+    class _H:
+        pass
+    h = _H()
+    h.win, h.vals, h.tc, h.vdt = win, vals, tc, dt
+    h.cols = np.zeros(vals.size // 16, np.int32)
+    return all_row_nnz(h)
+
+
+def assert_tight(Yd, Yr, Ya, k, vdt: str, xdt: str, ydt: str, what: str = "tight tier") -> float:
+    """The tight tier over a whole small product: Yd (device, as float64),
+    Yr / Ya the float64 oracle's A X and |A||X| (residual terms included),
+    k the non-zero terms of each row [rows]."""
+    err = np.abs(np.asarray(Yd, np.float64) - Yr)
+    return _assert_within(err, tight_bound(Yr, Ya, np.asarray(k)[:, None], vdt, xdt, ydt), what)
+
+
 def raw(t: torch.Tensor) -> np.ndarray:
     """Host copy of t in its stored element type (bf16 as uint16 bits)."""
     t = t.detach().contiguous().cpu()

@@ -19,6 +19,7 @@ import pytest
 import torch
 
 import oracle
+from _fullsize import DT, assert_tight, rows_nnz_of
 from graph_rws_amd import core, synth
 from graph_rws_amd.core import ops
 from graph_rws_amd.data import BCSRGraph
@@ -118,16 +119,24 @@ def test_grouped_union_bitmap_matches_sort(cuda_device, G):
 
 
 def _oracle_check(A, X, Y, R=None):
+    """The float64 oracle (residual R added to its rows), in the contract
+    tier (1e-2 |A||X|) and the tight tier of tests/_fullsize.py."""
     vq = A.values_condensed.double().cpu().numpy()
-    Yr, Ya = oracle.bcsr_spmm(A.window_offset.cpu().numpy(), A.original_col_indices.cpu().numpy(), vq, 16,
+    win = A.window_offset.cpu().numpy()
+    Yr, Ya = oracle.bcsr_spmm(win, A.original_col_indices.cpu().numpy(), vq, 16,
                               A.tile_cols, X.double().cpu().numpy())
+    k = rows_nnz_of(win, vq, A.tile_cols)
     if R is not None:
         Rn = R.double().cpu().numpy()
         Yr[:Rn.shape[0]] += Rn
         Ya[:Rn.shape[0]] += np.abs(Rn)
-    err = np.abs(Y.double().cpu().numpy() - Yr)
+        k[:Rn.shape[0]] += 1
+    Yd = Y.double().cpu().numpy()
+    err = np.abs(Yd - Yr)
     bad = err > 1e-2 * Ya
     assert not bad.any(), f"{bad.sum()} of {bad.size} out of tolerance; worst {float((err - 1e-2 * Ya).max()):.3e}"
+    dt = DT[X.dtype]
+    assert_tight(Yd, Yr, Ya, k, DT[A.values_condensed.dtype], dt, DT[Y.dtype])
 
 
 SHAPES = [  # (group size, windows per wave, column blocks of the first launch)

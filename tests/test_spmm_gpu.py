@@ -9,6 +9,7 @@ import pytest
 import torch
 
 import oracle
+from _fullsize import DT, assert_tight, rows_nnz_of
 from graph_rws_amd import core, synth
 from graph_rws_amd.data import BCSRGraph
 
@@ -24,10 +25,13 @@ def _bcsr(g, tc, dev, vdt=torch.float32):
 
 
 def _check(G, X, Y, xdt):
-    """Compare the device result with the oracle on the quantised inputs."""
+    """Compare the device result with the oracle on the quantised inputs, in
+    the contract tier (RTOL |A||X|) and the tight tier of tests/_fullsize.py
+    (the arithmetic's own bound: one output rounding plus C k 2^-24 |A||X|)."""
     vq = G.values_condensed.to(xdt).double().cpu().numpy() if G.values_condensed.dtype != xdt \
         else G.values_condensed.double().cpu().numpy()
-    Yr, Ya = oracle.bcsr_spmm(G.window_offset.cpu().numpy(), G.original_col_indices.cpu().numpy(),
+    win = G.window_offset.cpu().numpy()
+    Yr, Ya = oracle.bcsr_spmm(win, G.original_col_indices.cpu().numpy(),
                               vq, 16, G.tile_cols, X.double().cpu().numpy())
     Yd = Y.double().cpu().numpy()
     err = np.abs(Yd - Yr)
@@ -35,6 +39,8 @@ def _check(G, X, Y, xdt):
     bad = err > bound
     assert not bad.any(), (f"{bad.sum()} of {bad.size} elements out of tolerance; "
                            f"worst excess {float((err - bound).max()):.3e}")
+    dt = DT[xdt]
+    assert_tight(Yd, Yr, Ya, rows_nnz_of(win, vq, G.tile_cols), dt, dt, DT[Y.dtype])
     return Yr
 
 
@@ -354,6 +360,11 @@ def test_spmm_residual_parity(cuda_device, xdt, variant, N):
     Ya[:r_rows] += np.abs(Rn)
     err = np.abs(Y.double().cpu().numpy() - Yr)
     assert (err <= RTOL[xdt] * Ya).all()
+    # tight tier: the residual is one more term of its rows' sums
+    k = rows_nnz_of(G.window_offset.cpu().numpy(), vq, 16)
+    k[:r_rows] += 1
+    dt = DT[xdt]
+    assert_tight(Y.double().cpu().numpy(), Yr, Ya, k, DT[G.values_condensed.dtype], dt, dt)
     assert torch.equal(Y[r_rows:], Y0[r_rows:])
 
 
