@@ -908,6 +908,38 @@ def sample_block(indptr: torch.Tensor, indices: torch.Tensor, frontier: torch.Te
     return win, cols[:T * tile_cols], vals[:T * 16 * tile_cols], nxt[:S], E
 
 
+def copy_and_fill(copies, fills, stream: Optional[torch.cuda.Stream] = None) -> bool:
+    """Device copies and int64 fills in one launch each (grws_copy_ranges,
+    grws_fill_ranges_i64) on `stream` (the current stream by default).
+    copies: (dst, src) pairs of contiguous tensors of equal byte size, both
+    16-byte aligned; fills: (dst int64 contiguous tensor, value).  Returns
+    False, with nothing done, when an operand does not qualify (the caller
+    then copies with torch)."""
+    for d, s_ in copies:
+        if (not (d.is_cuda and s_.is_cuda and d.is_contiguous() and s_.is_contiguous())
+                or d.data_ptr() % 16 or s_.data_ptr() % 16
+                or d.numel() * d.element_size() != s_.numel() * s_.element_size()):
+            return False
+    for d, _ in fills:
+        if not (d.is_cuda and d.dtype == torch.int64 and d.is_contiguous()):
+            return False
+    dev = (copies[0][0] if copies else fills[0][0]).device
+    sp = ctypes.c_void_p((stream or torch.cuda.current_stream(dev)).cuda_stream)
+    cp = [(d, s_) for d, s_ in copies if d.numel()]
+    if cp:
+        m = len(cp)
+        L.call("grws_copy_ranges", (ctypes.c_void_p * m)(*[s_.data_ptr() for _, s_ in cp]),
+               (ctypes.c_void_p * m)(*[d.data_ptr() for d, _ in cp]),
+               (ctypes.c_int64 * m)(*[d.numel() * d.element_size() for d, _ in cp]), m, sp)
+    fl = [(d, v) for d, v in fills if d.numel()]
+    if fl:
+        m = len(fl)
+        L.call("grws_fill_ranges_i64", (ctypes.c_void_p * m)(*[d.data_ptr() for d, _ in fl]),
+               (ctypes.c_int64 * m)(*[d.numel() for d, _ in fl]), (ctypes.c_int64 * m)(*[int(v) for _, v in fl]),
+               m, sp)
+    return True
+
+
 def gather_rows(src: torch.Tensor, index: torch.Tensor, out: Optional[torch.Tensor] = None,
                 err: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``src.index_select(0, index)`` for a 2-D device tensor whose rows are

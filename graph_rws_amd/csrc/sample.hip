@@ -1838,8 +1838,54 @@ __global__ __launch_bounds__(256) void copy_ranges_kernel(CopyArgs a) {
     }
 }
 
+struct FillArgs {
+    int64_t* dst[kMaxCopyRanges];
+    int64_t first[kMaxCopyRanges + 1];  // first element of each range (prefix over ranges)
+    int64_t value[kMaxCopyRanges];
+    int n;
+};
+
+// Element u of the launch belongs to the range r with first[r] <= u < first[r+1].
+__global__ __launch_bounds__(256) void fill_ranges_kernel(FillArgs a) {
+    const int64_t total = a.first[a.n];
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < total; u += (int64_t)gridDim.x * 256) {
+        int r = 0;
+        while (u >= a.first[r + 1]) ++r;
+        a.dst[r][u - a.first[r]] = a.value[r];
+    }
+}
+
 }  // namespace
 }  // namespace grws
+
+extern "C" int grws_fill_ranges_i64(int64_t* const* dst, const int64_t* count, const int64_t* value, int32_t n,
+                                    void* stream_) {
+    clear_error();
+    GRWS_CHECK_ARG(n >= 0, "fill_ranges: negative count");
+    if (n == 0) return GRWS_OK;
+    GRWS_CHECK_ARG(dst && count && value, "fill_ranges: null pointer");
+    const hipStream_t stream = as_stream(stream_);
+    for (int32_t base = 0; base < n; base += kMaxCopyRanges) {
+        FillArgs a{};
+        a.n = 0;
+        a.first[0] = 0;
+        for (int32_t i = base; i < n && i < base + kMaxCopyRanges; ++i) {
+            GRWS_CHECK_ARG(count[i] >= 0, "fill_ranges: negative length");
+            GRWS_CHECK_ARG(count[i] == 0 || dst[i], "fill_ranges: null range");
+            GRWS_CHECK_ARG(reinterpret_cast<uintptr_t>(dst[i]) % 8 == 0, "fill_ranges: range %d not 8-byte aligned", i);
+            a.dst[a.n] = dst[i];
+            a.value[a.n] = value[i];
+            a.first[a.n + 1] = a.first[a.n] + count[i];
+            ++a.n;
+        }
+        const int64_t total = a.first[a.n];
+        if (total == 0) continue;
+        const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 4096);
+        hipLaunchKernelGGL(fill_ranges_kernel, dim3(grid), dim3(256), 0, stream, a);
+        GRWS_LAUNCH_CHECK();
+    }
+    return GRWS_OK;
+}
 
 extern "C" int grws_copy_ranges(const void* const* src, void* const* dst, const int64_t* bytes, int32_t n,
                                 void* stream_) {

@@ -80,10 +80,16 @@ def evaluate(model, bcsr_full, features: torch.Tensor, labels: torch.Tensor,
 # ---------------------------------------------------------------------------
 def _adopt(tensors, stream) -> None:
     """Tensors made on the sampling stream are used on `stream`: tell the
-    caching allocator, so their memory is not reused before that work ends."""
+    caching allocator, so their memory is not reused before that work ends.
+    The allocator tracks storages, so views of one storage (a sampled
+    batch's arrays are views of a few compact buffers) are recorded once."""
+    seen = set()
     for t in tensors:
         if isinstance(t, torch.Tensor) and t.is_cuda:
-            t.record_stream(stream)
+            key = t.untyped_storage().data_ptr()
+            if key not in seen:
+                seen.add(key)
+                t.record_stream(stream)
 
 
 def _graph_tensors(g):
@@ -290,9 +296,7 @@ def train_epoch_node_sampling(model, graphs_for_model, features: torch.Tensor,
                 break
             seeds, subgraphs, feats, ev = item
             main.wait_event(ev)
-            for g in subgraphs:
-                _adopt(_graph_tensors(g), main)
-            _adopt([seeds, feats], main)
+            _adopt([t for g in subgraphs for t in _graph_tensors(g)] + [seeds, feats], main)
             timer.record("Sample")
             step(seeds, subgraphs, feats)
         worker.join()

@@ -154,15 +154,32 @@ class _BlockBucket:
         dst.values_condensed[: T * 16 * tc].copy_(src.values_condensed)
 
     def fill(self, blocks, feats, labels) -> None:
-        """Copies one batch in, on the current stream."""
-        from ..core.ops import TensorKey
-        self.X[: feats.shape[0]].copy_(feats)
-        self.labels[: labels.numel()].copy_(labels)
-        self.labels[labels.numel():].fill_(-100)
-        for g, at, b in zip(self.graphs, self.AT, blocks):
-            self._copy_bcsr(g, b)
+        """Copies one batch in, on the current stream: every array in one
+        copy launch and every padding fill (labels past the batch's, window
+        offsets past its windows) in one fill launch when the operands allow
+        (core.ops.copy_and_fill), else one torch copy or fill per array."""
+        from ..core.ops import TensorKey, copy_and_fill
+        pairs = [(g, b) for g, b in zip(self.graphs, blocks)]
+        pairs += [(at, b.transpose()) for at, b in zip(self.AT, blocks) if at is not None]
+        copies = [(self.X[: feats.shape[0]], feats), (self.labels[: labels.numel()], labels)]
+        fills = [(self.labels[labels.numel():], -100)]
+        for dst, src in pairs:
+            W, T, tc = src.num_windows, src.num_tiles, src.tile_cols
+            if W > dst.num_windows or T > dst.num_tiles or src.tile_cols != dst.tile_cols:
+                raise ValueError(f"GraphedBlockStep: a block of {W} windows / {T} tiles exceeds its bucket "
+                                 f"({dst.num_windows} / {dst.num_tiles})")
+            copies += [(dst.window_offset[: W + 1], src.window_offset),
+                       (dst.original_col_indices[: T * tc], src.original_col_indices),
+                       (dst.values_condensed[: T * 16 * tc], src.values_condensed)]
+            fills.append((dst.window_offset[W + 1:], T))
+        if not copy_and_fill(copies, fills):
+            self.X[: feats.shape[0]].copy_(feats)
+            self.labels[: labels.numel()].copy_(labels)
+            self.labels[labels.numel():].fill_(-100)
+            for dst, src in pairs:
+                self._copy_bcsr(dst, src)
+        for g, at in zip(self.graphs, self.AT):
             if at is not None:
-                self._copy_bcsr(at, b.transpose())
                 # the layer's backward finds the static transpose through the
                 # graph's cache, keyed by the arrays' current versions
                 arrays = (g.window_offset, g.original_col_indices, g.values_condensed)

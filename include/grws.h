@@ -521,6 +521,14 @@ int grws_sample_blocks_error(int64_t err);
 /* replayed batch's outputs as compact tensors.  Asynchronous on `stream`.  */
 int grws_copy_ranges(const void* const* src, void* const* dst, const int64_t* bytes, int32_t n, void* stream);
 
+/* n int64 fills in one launch (32 ranges per launch): count[i] elements   */
+/* from dst[i] (8-byte aligned) set to value[i].  No counterpart in the     */
+/* reference: the captured mini-batch step uses it with grws_copy_ranges to */
+/* load a batch into its bucket's static buffers (the window offsets past   */
+/* the batch's windows, the padding labels) in two launches instead of one */
+/* per array.  Asynchronous on `stream`.                                    */
+int grws_fill_ranges_i64(int64_t* const* dst, const int64_t* count, const int64_t* value, int32_t n, void* stream);
+
 /* Input features of a sampled batch: dst row i = src row idx[i] for        */
 /* i < n, row_bytes bytes per row, rows ld_src / ld_dst bytes apart; idx is  */
 /* int64 (idx_is_i64 != 0) or int32.  An index outside [0, src_rows) gives a */
