@@ -33,8 +33,8 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16
 # that exact workload.  Sources: the profile file named with each figure
 MEASURED_TRAFFIC = {
     # (config, N, x dtype, tile cols, A format): (bytes per SpMM, profile file)
-    # grouped tiles, 2 windows per group: FETCH 17.47M KiB x2, WRITE 0.277M KiB
-    ("c3", 608, "f16", 16, "grouped tiles (2 windows)"): (36.05e9, "profiles/spmm_grp_c3_n608_f16.md"),
+    # grouped tiles, 4 windows per group: FETCH 15.83M KiB x2, WRITE 0.277M KiB
+    ("c3", 608, "f16", 16, "grouped tiles (4 windows)"): (32.70e9, "profiles/spmm_grp_c3_n608_f16.md"),
     # SpMM kernel (351.0 MB read, 55.1 MB written) plus the split-window fixup (14.6 MB)
     ("c2", 128, "f16", 16, "packed tiles"): (420.7e6, "profiles/spmm_buf_c2_n128_f16.md"),
     # SpMM kernel (24.96 GB read, 0.56 GB written) plus the fixup (13 MB)
@@ -207,6 +207,39 @@ def alg_bytes(G, N: int, s_x: int, s_y: int, packed=None, plan=None, grouped=Non
                                   "x_rows_referenced": rows_ref, "x_once": s_x * rows_ref * N,
                                   "plan_items": items}
     return parts
+
+
+def row_gather_ceiling(dev, rows: int, pitch_bytes: int, segments: int, n_idx: int, reps: int = 5) -> float:
+    """GB/s of grws_probe_row_gather: n_idx random rows (uniform over
+    `rows`, seeded) of segments * 128 bytes each from a table of rows x
+    pitch_bytes, the SpMM's X-read pattern with nothing else around it.
+    Median of reps after one warm-up, HIP events on the stream."""
+    from graph_rws_amd.core import _lib as L
+    n_idx = n_idx // 8 * 8
+    table = torch.zeros(rows * pitch_bytes // 4, dtype=torch.int32, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    idx = torch.randint(0, rows, (n_idx,), device=dev, dtype=torch.int32, generator=gen)
+    blocks = 4096
+    out = torch.empty(4 * blocks, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream(dev)
+
+    def run():
+        L.call("grws_probe_row_gather", L.ptr(table), rows, pitch_bytes, segments, L.ptr(idx), n_idx, L.ptr(out),
+               blocks, L.stream_of(dev))
+
+    run()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        run()
+        e1.record(s)
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    ts.sort()
+    del table, idx, out
+    return n_idx * segments * 128 / (ts[len(ts) // 2] / 1e3) / 1e9
 
 
 def copy_peak(dev, nbytes: int = 1 << 30, reps: int = 5) -> float:
@@ -1084,7 +1117,7 @@ def main():
         torch.cuda.synchronize(dev)
         tq = time.perf_counter()
         _gq = _ops.group_tiles(G.window_offset, G.original_col_indices, G.values_condensed, G.tile_cols,
-                               X.shape[0])
+                               X.shape[0], group_size=grouped.group_size)
         torch.cuda.synchronize(dev)
         t_group = time.perf_counter() - tq
         del _gq
@@ -1114,6 +1147,15 @@ def main():
               else 2.0 * G.num_tiles * 16 * G.tile_cols * N)
     tkey = (cfg, N, dname, G.tile_cols, a_format)
     traffic = MEASURED_TRAFFIC.get(tkey, (None, None))
+    # the rate at which random X row segments come from beyond the L2s (a
+    # table of X's rows and pitch) and from one XCD's L2 (1,600 rows), in
+    # the kernels' gather shape: 640-byte segments (a 320-column chunk of
+    # 16-bit X) where the pitch holds them, else 128-byte ones
+    pitch_b = X.stride(0) * X.element_size()
+    g_segs = 5 if pitch_b >= 640 else 1
+    ceil_miss = row_gather_ceiling(dev, X.shape[0], pitch_b, g_segs, 16_000_000)
+    ceil_l2 = row_gather_ceiling(dev, 1600, pitch_b, g_segs, 16_000_000)
+    traffic_gbs = traffic[0] / (ms_avg / 1e3) / 1e9 if traffic[0] else None
 
     out = {
         "metric": "BCSR SpMM GFLOP/s + HBM GB/s (% peak); GCN epoch ms; sampled edges/s",
@@ -1159,7 +1201,13 @@ def main():
             "traffic": traffic[0],
             "traffic_source": traffic[1],
             "traffic_over_compulsory": round(traffic[0] / B["compulsory"], 2) if traffic[0] else None,
-            "traffic_gbs": round(traffic[0] / (ms_avg / 1e3) / 1e9, 1) if traffic[0] else None,
+            "traffic_gbs": round(traffic_gbs, 1) if traffic_gbs else None,
+            # grws_probe_row_gather: the kernel's L2-miss traffic against the
+            # rate the chip serves random row segments from beyond the L2s
+            "row_gather_ceiling": {"l2_miss_gbs": round(ceil_miss, 1), "l2_resident_gbs": round(ceil_l2, 1),
+                                   "segment_bytes": 128 * g_segs, "table_rows": int(X.shape[0]),
+                                   "pitch_bytes": int(pitch_b)},
+            "traffic_frac_of_row_gather_ceiling": round(traffic_gbs / ceil_miss, 3) if traffic_gbs else None,
             "gather_model": {"bytes": B["total"], "gbs": round(gather_gbs, 1),
                              "note": "modelled L2-side bytes: each gathered X row counted once per "
                                      "window that references it; the caches serve re-references, so "

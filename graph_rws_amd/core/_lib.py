@@ -181,6 +181,8 @@ _PROTOS = {
     "grws_sample_blocks_error": (ctypes.c_int, [ctypes.c_int64]),
     "grws_copy_ranges": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int32, _vp]),
     "grws_fill_ranges_i64": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int32, _vp]),
+    "grws_probe_row_gather": (ctypes.c_int, [_vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp,
+                                             ctypes.c_int64, _vp, ctypes.c_int32, _vp]),
     "grws_gather_rows": (ctypes.c_int, [_vp, ctypes.c_int64, ctypes.c_int64, _vp, ctypes.c_int32,
                                         ctypes.c_int64, ctypes.c_int64, _vp, ctypes.c_int64, _vp, _vp]),
     "grws_gemm_tn_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64,

@@ -318,13 +318,14 @@ GROUP_MAX_SKEW = 4.0
 # an int fixes it
 GROUP_SIZE = None
 def group_size_for(n_cols: int) -> int:
-    """Windows per group for products n_cols wide (measured on c3, f16):
-    four up to 256 columns (N = 256: 2.16 against 2.25 ms with two; more
-    gathers saved than sub-tile headers added), two above (N = 608: 5.37
-    against 5.62 ms with four)."""
+    """Windows per group for products n_cols wide.  Four at every width
+    measured on c3 (f16): N = 256 2.16 against 2.25 ms with two windows,
+    N = 608 5.29 against 5.39 ms (320-column chunks, one window per wave);
+    the saved intra-community gathers outweigh the added sub-tile headers.
+    Eight ran slower at N = 608 (8.21 ms, two windows per wave)."""
     if GROUP_SIZE:
         return int(GROUP_SIZE)
-    return 4 if n_cols <= 256 else 2
+    return 4
 
 
 # narrower products stay on the window-by-window kernel: a grouped chunk is
@@ -342,7 +343,7 @@ def group_tiles(window_offset: torch.Tensor, col_indices: torch.Tensor, values: 
     if values.dtype not in (torch.float16, torch.bfloat16) or tile_cols not in (8, 16) or not values.is_cuda:
         return None
     _check_graph(window_offset, col_indices, values, tile_cols)
-    group_size = (GROUP_SIZE or 2) if group_size is None else group_size
+    group_size = (GROUP_SIZE or 4) if group_size is None else group_size
     max_ratio = GROUP_MAX_RATIO if max_ratio is None else max_ratio
     max_skew = GROUP_MAX_SKEW if max_skew is None else max_skew
     lib = L.load()

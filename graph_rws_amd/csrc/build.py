@@ -37,6 +37,7 @@ SOURCES = [
     "gemm_tn.hip",
     "repack.hip",
     "fused.hip",
+    "probe.hip",
 ]
 
 ARCH = os.environ.get("GRWS_OFFLOAD_ARCH", "gfx950")

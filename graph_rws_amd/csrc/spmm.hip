@@ -827,10 +827,11 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(NBLK =
 // sub-tile each per slab (same packing as PK above).  A work-group of GW
 // waves takes one group and one N-chunk; each wave owns WPW of the group's
 // windows (G = WPW GW).  Per slab the waves gather the slab's 16 X rows
-// once, wave h the rows [h 16/GW, (h+1) 16/GW) in 128-byte segments of 8
-// rows per instruction, into LDS; then every wave multiplies each staged
-// 16-column block by its windows' sub-tiles, one transposing LDS read
-// serving WPW MFMAs.  With GW > 1 the stage is double buffered and one
+// once, wave h the rows [h 16/GW, (h+1) 16/GW) in 128-byte segments, 8
+// per instruction (a last partial instruction repeats segments of the same
+// rows: its extra lanes write what other lanes write), into LDS; then every
+// wave multiplies each staged 16-column block by its windows' sub-tiles,
+// one transposing LDS read serving WPW MFMAs.  With GW > 1 the stage is double buffered and one
 // barrier per slab orders its writes before its reads (a buffer is written
 // again two slabs later, after every wave passed the barrier in between).
 template <int XT, int NBLK, int WPW, int GW, int PF>
@@ -842,8 +843,10 @@ __global__ __launch_bounds__(64 * GW) void spmm_grp_kernel(SpmmArgs a) {
     constexpr int NC = NBLK * 16;
     constexpr int SEGS = NC / 64;       // 128-byte segments per staged row
     constexpr int RPW = 16 / GW;        // staged rows each wave gathers
-    constexpr int NLD = RPW * SEGS / 8; // gather instructions per wave and slab
-    static_assert(NC % 64 == 0 && (RPW * SEGS) % 8 == 0, "whole 8-segment instructions per wave");
+    constexpr int NSEG = RPW * SEGS;
+    constexpr int NLD = (NSEG + 7) / 8; // gather instructions per wave and slab
+    constexpr int PAD = NLD * 8 - NSEG;
+    static_assert(NC % 64 == 0 && PAD % RPW == 0 && PAD < 8, "gather instructions per wave");
     constexpr int PITCH = NC + 16;
     constexpr int NST = GW > 1 ? 2 : 1;
     constexpr int R = PF + 1;
@@ -873,9 +876,11 @@ __global__ __launch_bounds__(64 * GW) void spmm_grp_kernel(SpmmArgs a) {
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.x), (short)0, (int)a.x_bytes, 0x00020000);
 
     // gather instruction i of this wave covers its row segments 8 i .. 8 i + 7;
-    // lane l takes segment 8 i + l / 8: staged row and first element
-    auto row_of = [&](int i) { return wave * RPW + (8 * i + (lane >> 3)) % RPW; };
-    auto elem_of = [&](int i) { return 64 * ((8 * i + (lane >> 3)) / RPW) + 8 * (lane & 7); };
+    // lane l takes segment 8 i + l / 8 (past the last, PAD earlier: the same
+    // row, since PAD is a multiple of RPW): staged row and first element
+    auto seg_of = [&](int i) { const int si = 8 * i + (lane >> 3); return si < NSEG ? si : si - PAD; };
+    auto row_of = [&](int i) { return wave * RPW + seg_of(i) % RPW; };
+    auto elem_of = [&](int i) { return 64 * (seg_of(i) / RPW) + 8 * (lane & 7); };
     bool lcol[NLD];
     uint32_t colb[NLD];
 #pragma unroll
@@ -1703,8 +1708,9 @@ int launch_grp(const SpmmArgs& a, hipStream_t stream) {
 }
 
 // Kernel shapes per group size: (windows per wave, waves per group) and the
-// column blocks per chunk.  NBLK 20 needs whole 8-segment instructions per
-// wave (GW 1 or 2); WPW 4 keeps to NBLK 8 (128 accumulator registers).
+// column blocks per chunk.  With four waves and NBLK 20 each wave's 20 row
+// segments take three gather instructions (the last repeats four); WPW 4
+// keeps to NBLK 8 (128 accumulator registers).
 template <int XT>
 int dispatch_grp(const SpmmArgs& a, int G, int wpw, int nblk, hipStream_t stream) {
     const int gw = G / wpw;
@@ -1712,7 +1718,7 @@ int dispatch_grp(const SpmmArgs& a, int G, int wpw, int nblk, hipStream_t stream
     if (wpw == W_ && gw == GW_ && nblk == NB_) return launch_grp<XT, NB_, W_, GW_>(a, stream)
     GRWS_GRP(1, 2, 8); GRWS_GRP(1, 2, 16); GRWS_GRP(1, 2, 20);
     GRWS_GRP(2, 1, 8); GRWS_GRP(2, 1, 16); GRWS_GRP(2, 1, 20);
-    GRWS_GRP(1, 4, 8); GRWS_GRP(1, 4, 16);
+    GRWS_GRP(1, 4, 8); GRWS_GRP(1, 4, 16); GRWS_GRP(1, 4, 20);
     GRWS_GRP(2, 2, 8); GRWS_GRP(2, 2, 16); GRWS_GRP(2, 2, 20);
     GRWS_GRP(4, 1, 8);
     GRWS_GRP(2, 4, 8); GRWS_GRP(2, 4, 16);
@@ -1793,7 +1799,7 @@ extern "C" int grws_spmm_grouped(const grws_bcsr* A, const grws_grouped_tiles* G
     if (wpw == 4 || G / wpw == 4) tail_nblk = 8;
     const int64_t hnc = head_nblk * 16;
     const bool c320 = head_nblk == 16 && n_cols > 256 && n_cols % 256 != 0 && (n_cols + 319) / 320 < (n_cols + 255) / 256 &&
-                      G / wpw <= 2 && tune(kTuneGrpC320) != 0;
+                      (G / wpw <= 2 || (wpw == 1 && G == 4)) && tune(kTuneGrpC320) != 0;
     int st;
     if (c320) {
         a.col_base = 0;

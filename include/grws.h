@@ -721,6 +721,21 @@ int grws_cross_entropy_bwd(const void* logits, int32_t dtype, int64_t ld, int64_
                            const float* lse, const float* dloss, const int64_t* counts, void* grad,
                            int32_t grad_dtype, int64_t ldg, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Measurement only: no counterpart in the reference.  The random row-      */
+/* gather ceiling that bounds the SpMM's X reads, for benchmark reports.    */
+/* n_idx row indices (int32, a multiple of 8; values outside [0, rows)      */
+/* read zeros) into a table of `rows` rows pitch_bytes apart (16-byte       */
+/* aligned, at most 2^31 bytes);                                            */
+/* every index loads the row's first segments * 128 bytes (1, 5 or 10, at   */
+/* most the pitch), 16 bytes per lane.  `blocks` work-groups of 256 lanes   */
+/* (1..65536) share the list; out[4 * blocks] receives one word per wave    */
+/* (a fold of what it read).  Asynchronous on `stream`; time it with events */
+/* on that stream.                                                          */
+/* ------------------------------------------------------------------------ */
+int grws_probe_row_gather(const void* table, int64_t rows, int64_t pitch_bytes, int32_t segments,
+                          const int32_t* idx, int64_t n_idx, uint32_t* out, int32_t blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

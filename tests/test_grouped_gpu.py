@@ -139,7 +139,8 @@ def _oracle_check(A, X, Y, R=None):
     assert_tight(Yd, Yr, Ya, k, DT[A.values_condensed.dtype], dt, DT[Y.dtype])
 
 
-SHAPES = [  # (group size, windows per wave, column blocks of the first launch)
+SHAPES = [  # (group size, windows per wave, column blocks of the first launch;
+    # 16 at N = 608 runs 320-column chunks, with padded gathers at 4 waves)
     (4, 2, 16), (4, 1, 16), (4, 4, 8), (4, 2, 8), (2, 2, 16), (2, 1, 16), (2, 2, 8), (8, 2, 16), (8, 4, 8),
     (8, 2, 8)]
 
@@ -192,7 +193,7 @@ def test_grouped_spmm_residual_and_partial_group(cuda_device, monkeypatch, vdt):
     _oracle_check(B, X, Yb)
 
 
-def test_graph_groups_its_tiles_when_it_pays(cuda_device):
+def test_graph_groups_its_tiles_when_it_pays(cuda_device, monkeypatch):
     """BCSRGraph.spmm builds grouped tiles on the second product of a graph
     with community structure and uses them; a Chung-Lu graph (no community
     structure) is left on the window-by-window path."""
@@ -207,14 +208,17 @@ def test_graph_groups_its_tiles_when_it_pays(cuda_device):
     assert gt.group_size == ops.group_size_for(256) == 4  # the group size suits the product's width
     torch.testing.assert_close(y1.float(), y2.float(), rtol=2 ** -10, atol=2 ** -14)
     _oracle_check(A, X, y2)
+    assert ops.group_size_for(608) == 4
+    # one cached layout per group size, not the first width's: under a
+    # policy that picks 2 windows above 256 columns, a graph first
+    # multiplied 608 columns wide still gets 4-window tiles at 256 columns
+    monkeypatch.setattr(ops, "group_size_for", lambda n: 2 if n > 256 else 4)
     _, A2 = _graph(cuda_device, torch.float16, 16, scale=0.01)
     X6 = torch.randn(A2.num_cols, 608, device=cuda_device).half()
     A2.spmm(X6)
     y6 = A2.spmm(X6)
-    assert A2._cache[("grouped", 2)][2].group_size == ops.group_size_for(608) == 2
+    assert A2._cache[("grouped", 2)][2].group_size == 2
     _oracle_check(A2, X6, y6)
-    # the same graph's 256-column products then get their own 4-window
-    # layout (one cached layout per group size, not the first width's)
     X2 = torch.randn(A2.num_cols, 256, device=cuda_device).half()
     A2.spmm(X2)
     y2b = A2.spmm(X2)
