@@ -4,7 +4,7 @@ over every row), through the same calls bench.py times.
 
 * c3 (232,965 nodes, 114.6M nnz, f16): the headline N=608 product on X at a
   640-element pitch, default plan, chunk-major order, the dense-tile first
-  product, the 2-window grouped second product and the packed-tile product
+  product, the 4-window grouped second product and the packed-tile product
   (bit-identical to the dense one); the epoch widths N=256 (window by
   window, then 4-window groups) and N=41 (ragged); A^T G at N=256 (first
   product window by window, second on 4-window groups).  Every grouped
