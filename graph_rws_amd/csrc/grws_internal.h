@@ -5,6 +5,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_bf16.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "grws_host.h"
@@ -58,6 +59,94 @@ struct Sizer {
     template <typename T>
     void take(size_t n) {
         used = align_up(used, 256) + align_up(n * sizeof(T), 256);
+    }
+};
+
+// A second stream for work that would leave most of the GPU idle if it ran
+// after the rest (a few long work-groups).  One such stream per device,
+// created on first use with the default priority; each call forks from the
+// caller's stream and joins back into it through events of its own, so
+// concurrent calls stay ordered.  When the caller's stream belongs to another
+// device than the current one, or the device index is out of range, the side
+// work stays on the caller's stream.  So it does when the caller's stream is
+// being captured (or its capture state cannot be read): a fork there would
+// pull the shared stream into the caller's graph, and a call on another
+// thread would then land in that graph.
+constexpr int kSideDevices = 64;
+
+inline int side_fork(hipStream_t main, hipStream_t* side) {
+    *side = main;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(main, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return GRWS_OK;
+    }
+    if (cs != hipStreamCaptureStatusNone) return GRWS_OK;
+    int dev = 0;
+    GRWS_HIP(hipGetDevice(&dev));
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(main, &sdev) != hipSuccess) {
+        (void)hipGetLastError();  // clears the failed query's error
+        return GRWS_OK;
+    }
+    if (sdev != dev || dev < 0 || dev >= kSideDevices) return GRWS_OK;
+    static std::mutex mu;
+    static hipStream_t streams[kSideDevices] = {};
+    hipStream_t s = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!streams[dev]) GRWS_HIP(hipStreamCreateWithFlags(&streams[dev], hipStreamNonBlocking));
+        s = streams[dev];
+    }
+    hipEvent_t ev;
+    GRWS_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    hipError_t e = hipEventRecord(ev, main);
+    if (e == hipSuccess) e = hipStreamWaitEvent(s, ev, 0);
+    (void)hipEventDestroy(ev);
+    GRWS_HIP(e);
+    *side = s;
+    return GRWS_OK;
+}
+
+inline int side_join(hipStream_t main, hipStream_t side) {
+    if (side == main) return GRWS_OK;
+    hipEvent_t ev;
+    GRWS_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    hipError_t e = hipEventRecord(ev, side);
+    if (e == hipSuccess) e = hipStreamWaitEvent(main, ev, 0);
+    (void)hipEventDestroy(ev);
+    GRWS_HIP(e);
+    return GRWS_OK;
+}
+
+// A forked side stream that is joined back on every exit: an error return
+// between the fork and the join must not leave side work running on a
+// workspace the caller may free (and its allocator hand out again on the
+// caller's stream).  join() reports the join's status; the destructor joins
+// quietly (the first error's message stays), and when even the events fail
+// it waits for the side stream.
+struct SideStream {
+    hipStream_t main, side;
+    explicit SideStream(hipStream_t m) : main(m), side(m) {}
+    SideStream(const SideStream&) = delete;
+    SideStream& operator=(const SideStream&) = delete;
+    int fork() { return side_fork(main, &side); }
+    int join() {
+        const hipStream_t s = side;
+        side = main;
+        return side_join(main, s);
+    }
+    ~SideStream() {
+        if (side == main) return;
+        hipEvent_t ev;
+        hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e == hipSuccess) {
+            e = hipEventRecord(ev, side);
+            if (e == hipSuccess) e = hipStreamWaitEvent(main, ev, 0);
+            (void)hipEventDestroy(ev);
+        }
+        if (e != hipSuccess) (void)hipStreamSynchronize(side);
+        (void)hipGetLastError();
     }
 };
 

@@ -86,19 +86,33 @@ __device__ __forceinline__ float ld_val(const void* v, int64_t i) {
 }
 
 // Key of one column slot of a window (sampling.cuh:222-345 restated per
-// column): ~(total as order-preserving u32) << 32 | column.  Returns false
+// column): ~(total as order-preserving u32) << 32 | column, in two steps:
+// slot_load reads the slot's column and its 16 values (no branch, so that
+// the loads of several slots can be in flight together; every slot of a
+// window's tiles has its values), slot_key_of scores them and returns false
 // when the slot is not a candidate.
+struct SlotRaw {
+    int32_t col;
+    float v[16];
+};
+
 template <typename VT>
-__device__ __forceinline__ bool slot_key(const int32_t* __restrict__ cols, const void* __restrict__ vals,
-                                         int64_t tile0, int tc, int64_t s, int32_t window, int32_t part_lo,
-                                         int32_t part_hi, bool in_part_known, const ScoreParams& p,
-                                         uint64_t* key) {
+__device__ __forceinline__ void slot_load(const int32_t* __restrict__ cols, const void* __restrict__ vals,
+                                          int64_t tile0, int tc, int64_t s, SlotRaw& r) {
+    const int64_t t = tile0 + s / tc;
+    const int c = (int)(s % tc);
+    r.col = cols[t * tc + c];
+    const int64_t vbase = t * 16 * tc + c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r.v[i] = ld_val<VT>(vals, vbase + (int64_t)i * tc);
+}
+
+__device__ __forceinline__ bool slot_key_of(const SlotRaw& raw, int32_t part_lo, int32_t part_hi, bool in_part_known,
+                                            const ScoreParams& p, uint64_t* key) {
     // separate roundings where the reference's source writes separate
     // operations (only its 1 + 10|v| and alpha + beta|v| are fused)
 #pragma clang fp contract(off)
-    const int64_t t = tile0 + s / tc;
-    const int c = (int)(s % tc);
-    const int32_t col = cols[t * tc + c];
+    const int32_t col = raw.col;
     if (col == -1) return false;
     float q = 1.0f;
     bool in_part = false;
@@ -109,10 +123,9 @@ __device__ __forceinline__ bool slot_key(const int32_t* __restrict__ cols, const
     }
     uint32_t total = 0;
     bool any = false;
-    const int64_t vbase = t * 16 * tc + c;
-#pragma unroll 4
+#pragma unroll
     for (int r = 0; r < 16; ++r) {
-        const float v = fabsf(ld_val<VT>(vals, vbase + (int64_t)r * tc));
+        const float v = fabsf(raw.v[r]);
         int32_t sc;
         if (p.use_hacs) {
             float f = __builtin_fmaf(p.beta, v, p.alpha) * q;
@@ -130,20 +143,39 @@ __device__ __forceinline__ bool slot_key(const int32_t* __restrict__ cols, const
     total += (uint32_t)p.gamma_int;
     const uint32_t ord = total ^ 0x80000000u;  // int32 order -> u32 order
     *key = ((uint64_t)(~ord) << 32) | (uint32_t)col;
-    (void)window;
     return true;
 }
 
-// One 1,024-thread work-group per active window.  The candidates' keys are
-// computed once (16 values each) and kept in LDS when the window has at most
-// kKeyCache slots, or for a larger (hub) window in the caller's key scratch
-// (a region claimed with one atomic on a cursor); a hub window that finds the
-// scratch full recomputes them on every pass, spread over the work-group's
-// 1,024 threads.  The count pass also finds the least
-// and greatest key, so the MSB-first radix select starts at the first byte
-// where they differ (the bytes above are common to every candidate).
+template <typename VT>
+__device__ __forceinline__ bool slot_key(const int32_t* __restrict__ cols, const void* __restrict__ vals,
+                                         int64_t tile0, int tc, int64_t s, int32_t part_lo, int32_t part_hi,
+                                         bool in_part_known, const ScoreParams& p, uint64_t* key) {
+    SlotRaw r;
+    slot_load<VT>(cols, vals, tile0, tc, s, r);
+    return slot_key_of(r, part_lo, part_hi, in_part_known, p, key);
+}
+
+// A classify kernel lists the active windows of more than kSmallCache slots;
+// two kernels share the per-window work (topk_window):
+//   * window_topk_small_kernel, one 256-thread work-group per active window,
+//     takes the others: a window's keys stay in LDS and are ranked directly;
+//   * window_topk_big_kernel, 1,024-thread work-groups walking the list, on a
+//     second stream beside it (a hub window is one long work-group): keys in
+//     LDS up to kKeyCache slots, beyond that in the caller's key scratch (a
+//     region claimed with one atomic on a cursor); a hub window that finds
+//     the scratch full recomputes them on every pass.
+// Most windows are small (c2: 10,434 of 10,584 have at most 1,024 slots),
+// and at 256 threads five of them share a CU instead of two.  The radix
+// passes count into one histogram per wave (a hub window's keys crowd a few
+// digits).  The count
+// pass also finds the least and greatest key, so the MSB-first radix select
+// starts at the first byte where they differ (the bytes above are common to
+// every candidate).  The count, select and compaction passes take several
+// slots per thread at a time, their loads issued together.
 constexpr int kTopkBlk = 1024;
 constexpr int kKeyCache = 4096;
+constexpr int kSmallBlk = 256;
+constexpr int kSmallCache = 1024;
 
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
 #pragma unroll
@@ -162,245 +194,387 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
-template <typename VT>
-__global__ __launch_bounds__(kTopkBlk) void window_topk_kernel(const int64_t* __restrict__ win_off, int64_t num_windows,
-                                                               const int32_t* __restrict__ cols,
-                                                               const void* __restrict__ vals, int tc,
-                                                               const int32_t* __restrict__ active, int64_t num_active,
-                                                               ScoreParams p, int cap, int S,
-                                                               int32_t* __restrict__ out_cols,
-                                                               int32_t* __restrict__ out_slots,
-                                                               int32_t* __restrict__ out_tiles,
-                                                               int32_t* __restrict__ err,
-                                                               uint64_t* __restrict__ gkeys, int64_t gcap,
-                                                               unsigned long long* __restrict__ gcursor) {
-    constexpr int NW = kTopkBlk / kWave;
-    __shared__ int64_t s_goff;
-    __shared__ int32_t hist[256];
-    __shared__ int32_t s_cnt;
-    __shared__ uint64_t s_prefix;
-    __shared__ int32_t s_shift;
-    __shared__ int32_t s_k;
-    __shared__ int32_t s_col[kMaxCap];
-    __shared__ int32_t s_slot[kMaxCap];
-    __shared__ uint64_t s_key[kKeyCache];
-    __shared__ uint64_t s_min[NW], s_max[NW];
+struct TopkArgs {
+    const int64_t* win_off;
+    int64_t num_windows;
+    const int32_t* cols;
+    const void* vals;
+    int tc;
+    const int32_t* active;
+    int64_t num_active;
+    ScoreParams p;
+    int cap;
+    int S;
+    int32_t* out_cols;
+    int32_t* out_slots;
+    int32_t* out_tiles;
+    int32_t* err;
+    uint64_t* gkeys;
+    int64_t gcap;
+    unsigned long long* gcursor;
+    int32_t* big_list;   // active indices of the windows left to the big kernel
+    int32_t* big_count;  // their number (zero before the small kernel)
+};
 
-    const int64_t b = blockIdx.x;
-    if (b >= num_active) return;
+template <int BLK, int KC, int HW>
+struct TopkShared {
+    int64_t goff;
+    int32_t whist[HW][256];  // the radix passes' per-wave histograms
+    int32_t hist[256];       // and their sum
+    int32_t cnt;
+    uint64_t prefix;
+    int32_t shift;
+    int32_t k;
+    int32_t col[kMaxCap];
+    int32_t slot[kMaxCap];
+    uint64_t kmin[BLK / kWave], kmax[BLK / kWave];
+    __attribute__((aligned(16))) uint64_t key[KC + 8];
+};
+
+// Selects active window b's sample (its columns in ascending order and their
+// slots, -1 past the sample) and its output tile count.  Every thread of the
+// work-group calls it with the same b; it leaves LDS to the caller's next
+// window only after a barrier.
+template <typename VT, int BLK, int KC, bool SMALL, int HW>
+__device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const int64_t b, const TopkArgs& a) {
+    constexpr int NW = BLK / kWave;
+    constexpr int FASTMAX = SMALL ? KC : BLK;  // rank directly up to this many candidates
+    // slots per thread whose loads are issued together: NB in the count pass
+    // (a slot's column and 16 values), NK in the select and compaction
+    // passes (one key each); more do not fit the 1,024-thread kernel's 128
+    // registers without spilling
+    constexpr int NB = SMALL ? 4 : 2;
+    constexpr int NK = SMALL ? NB : 4;
     const int tid = threadIdx.x;
-    const int32_t w = active[b];
-    int32_t* oc = out_cols + b * (int64_t)S;
-    int32_t* os = out_slots + b * (int64_t)S;
-    if (w < 0 || (int64_t)w >= num_windows) {
+    const ScoreParams& p = a.p;
+    const int tc = a.tc;
+    const int cap = a.cap, S = a.S;
+    const int32_t w = a.active[b];
+    int32_t* oc = a.out_cols + b * (int64_t)S;
+    int32_t* os = a.out_slots + b * (int64_t)S;
+    if (w < 0 || (int64_t)w >= a.num_windows) {
         if (tid == 0) {
-            atomicOr(err, kErrWindow);
-            out_tiles[b] = 0;
+            atomicOr(a.err, kErrWindow);
+            a.out_tiles[b] = 0;
         }
-        for (int i = tid; i < S; i += kTopkBlk) {
+        for (int i = tid; i < S; i += BLK) {
             oc[i] = -1;
             os[i] = -1;
         }
         return;
     }
-    const int64_t t0 = win_off[w];
-    const int64_t nslots = (win_off[w + 1] - t0) * tc;
-    const bool cached = nslots <= kKeyCache;
+    const int64_t t0 = a.win_off[w];
+    const int64_t nslots = (a.win_off[w + 1] - t0) * tc;
+    if constexpr (SMALL) {
+        if (nslots > KC) return;  // listed for the big kernel
+    }
+    const bool cached = nslots <= KC;
     if (tid == 0) {
         int64_t off = -1;
-        if (!cached && gkeys) {
-            const int64_t o = (int64_t)atomicAdd(gcursor, (unsigned long long)nslots);
-            if (o + nslots <= gcap) off = o;
+        if (!cached && a.gkeys) {
+            const int64_t o = (int64_t)atomicAdd(a.gcursor, (unsigned long long)nslots);
+            if (o + nslots <= a.gcap) off = o;
         }
-        s_goff = off;
+        sh.goff = off;
+        sh.cnt = 0;
     }
     __syncthreads();
-    uint64_t* const gk = s_goff >= 0 ? gkeys + s_goff : nullptr;  // uniform over the work-group
+    uint64_t* const gk = sh.goff >= 0 ? a.gkeys + sh.goff : nullptr;  // uniform over the work-group
     int32_t part_lo = 0, part_hi = 0;
     bool in_part_known = false;
     if (p.use_hacs && p.locality && p.window_part_ids && p.part_starts && p.part_ends) {
         const int32_t pid = p.window_part_ids[w];
         if ((int64_t)pid >= p.num_parts) {
-            if (tid == 0) atomicOr(err, kErrHacs);
+            if (tid == 0) atomicOr(a.err, kErrHacs);
         } else if (pid >= 0) {
             part_lo = p.part_starts[pid];
             part_hi = p.part_ends[pid];
             in_part_known = true;
         }
     }
-    // a slot's key: from the LDS cache (~0: not a candidate), or recomputed
-    auto key_of = [&](int64_t s, uint64_t* k) -> bool {
-        if (cached) {
-            *k = s_key[s];
-            return *k != ~0ull;
+    // the keys of slots s + u BLK (u < NK, s + u BLK < nslots): from the LDS
+    // cache or the scratch (~0: not a candidate), or recomputed
+    auto keysn = [&](int64_t s, uint64_t* k, bool* c) {
+        if (cached || gk) {
+            const uint64_t* src = cached ? sh.key : gk;
+#pragma unroll
+            for (int u = 0; u < NK; ++u) {
+                const int64_t su = s + (int64_t)u * BLK;
+                k[u] = su < nslots ? src[su] : ~0ull;
+            }
+#pragma unroll
+            for (int u = 0; u < NK; ++u) c[u] = k[u] != ~0ull;
+        } else {  // a hub window without scratch (rare): one slot at a time
+            for (int u = 0; u < NK; ++u) {
+                const int64_t su = s + (int64_t)u * BLK;
+                c[u] = su < nslots && slot_key<VT>(a.cols, a.vals, t0, tc, su, part_lo, part_hi, in_part_known, p, &k[u]);
+            }
         }
-        if (gk) {
-            *k = gk[s];
-            return *k != ~0ull;
-        }
-        return slot_key<VT>(cols, vals, t0, tc, s, w, part_lo, part_hi, in_part_known, p, k);
     };
 
     // candidates: count, least and greatest key (and the cache)
-    if (tid == 0) s_cnt = 0;
-    __syncthreads();
     {
         int local = 0;
         uint64_t kmin = ~0ull, kmax = 0;
-        for (int64_t s = tid; s < nslots; s += kTopkBlk) {
-            uint64_t k;
-            const bool c = slot_key<VT>(cols, vals, t0, tc, s, w, part_lo, part_hi, in_part_known, p, &k);
-            if (cached) s_key[s] = c ? k : ~0ull;
-            else if (gk) gk[s] = c ? k : ~0ull;
-            if (c) {
-                ++local;
-                kmin = k < kmin ? k : kmin;
-                kmax = k > kmax ? k : kmax;
-            }
-            if (p.use_hacs) {
-                const int32_t col = cols[(t0 + s / tc) * tc + s % tc];
-                if (col != -1 && (col < 0 || (int64_t)col >= p.num_static_scores)) atomicOr(err, kErrHacs);
+        for (int64_t s = tid; s < nslots; s += NB * BLK) {
+            SlotRaw r[NB];
+#pragma unroll
+            for (int u = 0; u < NB; ++u)
+                if (s + (int64_t)u * BLK < nslots) slot_load<VT>(a.cols, a.vals, t0, tc, s + (int64_t)u * BLK, r[u]);
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const int64_t su = s + (int64_t)u * BLK;
+                if (su >= nslots) continue;
+                uint64_t k = 0;
+                const bool c = slot_key_of(r[u], part_lo, part_hi, in_part_known, p, &k);
+                if (cached) sh.key[su] = c ? k : ~0ull;
+                else if (gk) gk[su] = c ? k : ~0ull;
+                if (c) {
+                    ++local;
+                    kmin = k < kmin ? k : kmin;
+                    kmax = k > kmax ? k : kmax;
+                }
+                if (p.use_hacs) {
+                    const int32_t col = r[u].col;
+                    if (col != -1 && (col < 0 || (int64_t)col >= p.num_static_scores)) atomicOr(a.err, kErrHacs);
+                }
             }
         }
-        if (local) atomicAdd(&s_cnt, local);
+        if (local) atomicAdd(&sh.cnt, local);
         kmin = wave_min_u64(kmin);
         kmax = wave_max_u64(kmax);
         if ((tid & (kWave - 1)) == 0) {
-            s_min[tid / kWave] = kmin;
-            s_max[tid / kWave] = kmax;
+            sh.kmin[tid / kWave] = kmin;
+            sh.kmax[tid / kWave] = kmax;
         }
     }
     __syncthreads();
-    const int32_t count = s_cnt;
+    const int32_t count = sh.cnt;
 
-    if (cached && count <= kTopkBlk) {
-        // a window of at most 1,024 candidates (most of them): a candidate's
-        // rank is the number of smaller keys (keys are distinct; ~0 marks a
-        // non-candidate and is above them all), the cap first are kept, and
-        // each kept one's output place is the number of kept columns below
-        // its own: two passes over LDS, two barriers, no select or sort
-        for (int64_t s = tid; s < nslots; s += kTopkBlk) {
-            const uint64_t k = s_key[s];
+    if (cached && count <= FASTMAX) {
+        // a candidate's rank is the number of smaller keys (keys are
+        // distinct; ~0 marks a non-candidate and is above them all), the cap
+        // first are kept, and each kept one's output place is the number of
+        // kept columns below its own: two passes over LDS, no select or sort.
+        // Keys past nslots read as ~0: the scan runs over whole 8-key groups
+        // in 16-byte LDS reads
+        const int ngrp = (int)((nslots + 7) / 8);
+        for (int64_t s = nslots + tid; s < 8 * (int64_t)ngrp; s += BLK) sh.key[s] = ~0ull;
+        __syncthreads();
+        for (int64_t s = tid; s < nslots; s += BLK) {
+            const uint64_t k = sh.key[s];
             if (k == ~0ull) continue;
             int r = 0;
-            for (int64_t q = 0; q < nslots; ++q) r += s_key[q] < k ? 1 : 0;
+            const ulonglong2* kq = reinterpret_cast<const ulonglong2*>(sh.key);
+            for (int g = 0; g < ngrp; ++g) {
+                const ulonglong2 k0 = kq[4 * g], k1 = kq[4 * g + 1], k2 = kq[4 * g + 2], k3 = kq[4 * g + 3];
+                r += (k0.x < k) + (k0.y < k) + (k1.x < k) + (k1.y < k) + (k2.x < k) + (k2.y < k) + (k3.x < k) +
+                     (k3.y < k);
+            }
             if (r < cap) {
-                s_col[r] = (int32_t)(uint32_t)k;
-                s_slot[r] = (int32_t)s;
+                sh.col[r] = (int32_t)(uint32_t)k;
+                sh.slot[r] = (int32_t)s;
             }
         }
         __syncthreads();
         const int nsel = count < cap ? count : cap;
-        for (int i = tid; i < nsel; i += kTopkBlk) {
-            const int32_t c = s_col[i];
+        for (int i = tid; i < nsel; i += BLK) {
+            const int32_t c = sh.col[i];
             int pos = 0;
-            for (int j = 0; j < nsel; ++j) pos += s_col[j] < c ? 1 : 0;
+            for (int j = 0; j < nsel; ++j) pos += sh.col[j] < c ? 1 : 0;
             if (pos < S) {
                 oc[pos] = c;
-                os[pos] = s_slot[i];
+                os[pos] = sh.slot[i];
             }
         }
-        for (int i = nsel + tid; i < S; i += kTopkBlk) {
+        for (int i = nsel + tid; i < S; i += BLK) {
             oc[i] = -1;
             os[i] = -1;
         }
         const int nout = nsel < S ? nsel : S;
-        if (tid == 0) out_tiles[b] = (nout + tc - 1) / tc;
+        if (tid == 0) a.out_tiles[b] = (nout + tc - 1) / tc;
         return;
     }
-
-    // radix select of the cap-th smallest key (keys are distinct)
-    uint64_t prefix = 0;
-    int shift = 64;  // selected: key >> shift <= prefix >> shift (shift 64: all)
-    if (count > cap) {
-        uint64_t kmin = s_min[0], kmax = s_max[0];
+    if constexpr (!SMALL) {  // a small window always takes the direct ranking above
+        static_assert(BLK >= kMaxCap, "the bitonic sort takes one thread per entry");
+        // radix select of the cap-th smallest key (keys are distinct)
+        uint64_t prefix = 0;
+        int shift = 64;  // selected: key >> shift <= prefix >> shift (shift 64: all)
+        if (count > cap) {
+            uint64_t kmin = sh.kmin[0], kmax = sh.kmax[0];
 #pragma unroll
-        for (int i = 1; i < NW; ++i) {
-            kmin = s_min[i] < kmin ? s_min[i] : kmin;
-            kmax = s_max[i] > kmax ? s_max[i] : kmax;
-        }
-        // the bytes above the first one where the least and greatest key
-        // differ are the same in every candidate
-        const int hb = 63 - __clzll((long long)(kmin ^ kmax));  // count > cap >= 32: kmin != kmax
-        const int sh0 = (hb / 8) * 8;
-        if (tid == 0) {
-            s_k = cap;
-            s_prefix = sh0 >= 56 ? 0ull : (kmax >> (sh0 + 8)) << (sh0 + 8);
-        }
-        for (int sh = sh0; sh >= 0; sh -= 8) {
-            if (tid < 256) hist[tid] = 0;
-            __syncthreads();
-            const uint64_t pre = s_prefix;
-            for (int64_t s = tid; s < nslots; s += kTopkBlk) {
-                uint64_t k;
-                if (!key_of(s, &k)) continue;
-                if (sh < 56 && (k >> (sh + 8)) != (pre >> (sh + 8))) continue;
-                atomicAdd(&hist[(k >> sh) & 255u], 1);
+            for (int i = 1; i < NW; ++i) {
+                kmin = sh.kmin[i] < kmin ? sh.kmin[i] : kmin;
+                kmax = sh.kmax[i] > kmax ? sh.kmax[i] : kmax;
             }
-            __syncthreads();
+            // the bytes above the first one where the least and greatest key
+            // differ are the same in every candidate
+            const int hb = 63 - __clzll((long long)(kmin ^ kmax));  // count > cap >= 32: kmin != kmax
+            const int sh0 = (hb / 8) * 8;
             if (tid == 0) {
-                int kk = s_k, below = 0, d = 0;
-                for (; d < 255; ++d) {
-                    if (below + hist[d] >= kk) break;
-                    below += hist[d];
-                }
-                s_prefix = pre | ((uint64_t)d << sh);
-                s_k = kk - below;
-                // the whole bucket is taken: no need to resolve lower digits
-                s_shift = (below + hist[d] == kk) ? sh : -1;
+                sh.k = cap;
+                sh.prefix = sh0 >= 56 ? 0ull : (kmax >> (sh0 + 8)) << (sh0 + 8);
             }
-            __syncthreads();
-            if (s_shift >= 0) break;
+            static_assert(HW == NW, "one histogram per wave");
+            int32_t* const myh = sh.whist[tid / kWave];
+            for (int shb = sh0; shb >= 0; shb -= 8) {
+                for (int i = tid; i < NW * 256; i += BLK) sh.whist[i / 256][i % 256] = 0;
+                __syncthreads();
+                const uint64_t pre = sh.prefix;
+                for (int64_t s = tid; s < nslots; s += NK * BLK) {
+                    uint64_t k[NK];
+                    bool c[NK];
+                    keysn(s, k, c);
+#pragma unroll
+                    for (int u = 0; u < NK; ++u) {
+                        if (!c[u]) continue;
+                        if (shb < 56 && (k[u] >> (shb + 8)) != (pre >> (shb + 8))) continue;
+                        atomicAdd(&myh[(k[u] >> shb) & 255u], 1);
+                    }
+                }
+                __syncthreads();
+                if (tid < 256) {
+                    int t = 0;
+#pragma unroll
+                    for (int i = 0; i < NW; ++i) t += sh.whist[i][tid];
+                    sh.hist[tid] = t;
+                }
+                __syncthreads();
+                if (tid < kWave) {
+                    // the first digit d whose running count reaches kk (the
+                    // prefix's candidates number at least kk): lane l holds
+                    // digits 4l .. 4l + 3, a wave scan finds the lane
+                    const int kk = sh.k;
+                    int h[4], sum = 0;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        h[j] = sh.hist[4 * tid + j];
+                        sum += h[j];
+                    }
+                    int incl = sum;
+#pragma unroll
+                    for (int dd = 1; dd < kWave; dd <<= 1) {
+                        const int t = __shfl_up(incl, dd, kWave);
+                        if (tid >= dd) incl += t;
+                    }
+                    const int excl = incl - sum;
+                    if (excl < kk && kk <= incl) {
+                        int below = excl, d = 4 * tid, hd = h[0];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            d = 4 * tid + j;
+                            hd = h[j];
+                            if (below + h[j] >= kk) break;
+                            below += h[j];
+                        }
+                        sh.prefix = pre | ((uint64_t)d << shb);
+                        sh.k = kk - below;
+                        // the whole bucket is taken: no need to resolve lower digits
+                        sh.shift = (below + hd == kk) ? shb : -1;
+                    }
+                }
+                __syncthreads();
+                if (sh.shift >= 0) break;
+            }
+            prefix = sh.prefix;
+            shift = sh.shift >= 0 ? sh.shift : 0;
         }
-        prefix = s_prefix;
-        shift = s_shift >= 0 ? s_shift : 0;
-    }
 
-    // compact the selected (column, slot) pairs
-    if (tid == 0) s_cnt = 0;
-    for (int i = tid; i < kMaxCap; i += kTopkBlk) {
-        s_col[i] = INT32_MAX;
-        s_slot[i] = -1;
-    }
-    __syncthreads();
-    for (int64_t s = tid; s < nslots; s += kTopkBlk) {
-        uint64_t k;
-        if (!key_of(s, &k)) continue;
-        if (shift < 64 && (k >> shift) > (prefix >> shift)) continue;
-        const int i = atomicAdd(&s_cnt, 1);
-        if (i < kMaxCap) {
-            s_col[i] = (int32_t)(uint32_t)k;
-            s_slot[i] = (int32_t)s;
+        // compact the selected (column, slot) pairs
+        if (tid == 0) sh.cnt = 0;
+        for (int i = tid; i < kMaxCap; i += BLK) {
+            sh.col[i] = INT32_MAX;
+            sh.slot[i] = -1;
         }
-    }
-    __syncthreads();
-    const int nsel = s_cnt < cap ? s_cnt : cap;
-
-    // bitonic sort of the 256 LDS entries by column (padding INT32_MAX last)
-    for (int size = 2; size <= kMaxCap; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            const int j = tid ^ stride;
-            if (tid < kMaxCap && j > tid) {
-                const bool up = (tid & size) == 0;
-                const int32_t a = s_col[tid], c = s_col[j];
-                if ((a > c) == up) {
-                    s_col[tid] = c;
-                    s_col[j] = a;
-                    const int32_t t = s_slot[tid];
-                    s_slot[tid] = s_slot[j];
-                    s_slot[j] = t;
+        __syncthreads();
+        for (int64_t s = tid; s < nslots; s += NK * BLK) {
+            uint64_t k[NK];
+            bool c[NK];
+            keysn(s, k, c);
+#pragma unroll
+            for (int u = 0; u < NK; ++u) {
+                if (!c[u]) continue;
+                if (shift < 64 && (k[u] >> shift) > (prefix >> shift)) continue;
+                const int i = atomicAdd(&sh.cnt, 1);
+                if (i < kMaxCap) {
+                    sh.col[i] = (int32_t)(uint32_t)k[u];
+                    sh.slot[i] = (int32_t)(s + (int64_t)u * BLK);
                 }
             }
-            __syncthreads();
         }
-    }
+        __syncthreads();
+        const int nsel = sh.cnt < cap ? sh.cnt : cap;
 
-    const int nout = nsel < S ? nsel : S;
-    for (int i = tid; i < S; i += kTopkBlk) {
-        oc[i] = i < nout ? s_col[i] : -1;
-        os[i] = i < nout ? s_slot[i] : -1;
+        // bitonic sort of the 256 LDS entries by column (padding INT32_MAX last)
+        for (int size = 2; size <= kMaxCap; size <<= 1) {
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                const int j = tid ^ stride;
+                if (tid < kMaxCap && j > tid) {
+                    const bool up = (tid & size) == 0;
+                    const int32_t x = sh.col[tid], y = sh.col[j];
+                    if ((x > y) == up) {
+                        sh.col[tid] = y;
+                        sh.col[j] = x;
+                        const int32_t t = sh.slot[tid];
+                        sh.slot[tid] = sh.slot[j];
+                        sh.slot[j] = t;
+                    }
+                }
+                __syncthreads();
+            }
+        }
+
+        const int nout = nsel < S ? nsel : S;
+        for (int i = tid; i < S; i += BLK) {
+            oc[i] = i < nout ? sh.col[i] : -1;
+            os[i] = i < nout ? sh.slot[i] : -1;
+        }
+        if (tid == 0) a.out_tiles[b] = (nout + tc - 1) / tc;
     }
-    if (tid == 0) out_tiles[b] = (nout + tc - 1) / tc;
+}
+
+// Lists the active windows of more than kSmallCache slots (in no particular
+// order) for the big kernel; an invalid window id stays with the small
+// kernel, which reports it.
+__global__ __launch_bounds__(kBlk) void window_topk_classify_kernel(const int64_t* __restrict__ win_off,
+                                                                    int64_t num_windows, int tc,
+                                                                    const int32_t* __restrict__ active,
+                                                                    int64_t num_active, int32_t* __restrict__ big_list,
+                                                                    int32_t* __restrict__ big_count) {
+    const int64_t b = (int64_t)blockIdx.x * kBlk + threadIdx.x;
+    bool big = false;
+    if (b < num_active) {
+        const int32_t w = active[b];
+        if (w >= 0 && (int64_t)w < num_windows) big = (win_off[w + 1] - win_off[w]) * tc > kSmallCache;
+    }
+    const uint64_t m = __ballot(big);
+    if (m == 0) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int leader = __ffsll((long long)m) - 1;
+    int32_t base = 0;
+    if (lane == leader) base = atomicAdd(big_count, __popcll(m));
+    base = __shfl(base, leader, kWave);
+    if (big) big_list[base + __popcll(m & lanemask_lt())] = (int32_t)b;
+}
+
+template <typename VT>
+__global__ __launch_bounds__(kSmallBlk) void window_topk_small_kernel(TopkArgs a) {
+    __shared__ TopkShared<kSmallBlk, kSmallCache, 1> sh;
+    const int64_t b = blockIdx.x;
+    if (b >= a.num_active) return;
+    topk_window<VT, kSmallBlk, kSmallCache, true, 1>(sh, b, a);
+}
+
+// Walks the classify kernel's list (launched after it, so the count is
+// final); every work-group leaves once the list is done.
+template <typename VT>
+__global__ __launch_bounds__(kTopkBlk) void window_topk_big_kernel(TopkArgs a) {
+    __shared__ TopkShared<kTopkBlk, kKeyCache, kTopkBlk / kWave> sh;
+    const int32_t n = *a.big_count;
+    for (int32_t i = (int32_t)blockIdx.x; i < n; i += (int32_t)gridDim.x) {
+        topk_window<VT, kTopkBlk, kKeyCache, false, kTopkBlk / kWave>(sh, a.big_list[i], a);
+        __syncthreads();
+    }
 }
 
 template <typename VT>
@@ -597,6 +771,8 @@ extern "C" size_t grws_window_topk_workspace_bytes(int64_t num_active) {
     Sizer s;
     s.take<int32_t>((size_t)num_active + 1);
     s.take<int32_t>(64);
+    s.take<int32_t>((size_t)num_active + 1);  // the big kernel's list
+    s.take<int32_t>(64);                      // and its count
     s.used += scan_workspace_bytes(num_active) + 256;
     return s.used;
 }
@@ -654,6 +830,8 @@ extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_window
     Carver cv(workspace, workspace_bytes);
     int32_t* tiles = cv.take<int32_t>(num_active + 1);
     int32_t* err = cv.take<int32_t>(64);
+    int32_t* big_list = cv.take<int32_t>(num_active + 1);
+    int32_t* big_count = cv.take<int32_t>(64);
     const size_t scan_bytes = scan_workspace_bytes(num_active);
     char* scan_ws = cv.take<char>(scan_bytes);
     if (!cv.ok) return set_error(GRWS_E_CAPACITY, "window_topk: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
@@ -675,26 +853,64 @@ extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_window
         }
     }
     GRWS_TRY(fill_i32(err, 1, 0, stream));
+    GRWS_TRY(fill_i32(big_count, 1, 0, stream));
     if (gcursor) GRWS_TRY(fill_i32(reinterpret_cast<int32_t*>(gcursor), 2, 0, stream));
-    switch (A->values_dtype) {
-        case GRWS_F32:
-            hipLaunchKernelGGL(window_topk_kernel<float>, dim3((unsigned)num_active), dim3(kTopkBlk), 0, stream,
-                               A->window_offset, A->num_windows, A->col_indices, A->values, (int)A->tile_cols,
-                               active_windows, num_active, p, cap, S, sampled_cols, sampled_slots, tiles, err, gkeys, gcap, gcursor);
-            break;
-        case GRWS_F16:
-            hipLaunchKernelGGL(window_topk_kernel<_Float16>, dim3((unsigned)num_active), dim3(kTopkBlk), 0, stream,
-                               A->window_offset, A->num_windows, A->col_indices, A->values, (int)A->tile_cols,
-                               active_windows, num_active, p, cap, S, sampled_cols, sampled_slots, tiles, err, gkeys, gcap, gcursor);
-            break;
-        default:
-            hipLaunchKernelGGL(window_topk_kernel<__hip_bfloat16>, dim3((unsigned)num_active), dim3(kTopkBlk), 0,
-                               stream, A->window_offset, A->num_windows, A->col_indices, A->values,
-                               (int)A->tile_cols, active_windows, num_active, p, cap, S, sampled_cols, sampled_slots,
-                               tiles, err, gkeys, gcap, gcursor);
-            break;
-    }
+    TopkArgs ta{};
+    ta.win_off = A->window_offset;
+    ta.num_windows = A->num_windows;
+    ta.cols = A->col_indices;
+    ta.vals = A->values;
+    ta.tc = (int)A->tile_cols;
+    ta.active = active_windows;
+    ta.num_active = num_active;
+    ta.p = p;
+    ta.cap = cap;
+    ta.S = S;
+    ta.out_cols = sampled_cols;
+    ta.out_slots = sampled_slots;
+    ta.out_tiles = tiles;
+    ta.err = err;
+    ta.gkeys = gkeys;
+    ta.gcap = gcap;
+    ta.gcursor = gcursor;
+    ta.big_list = big_list;
+    ta.big_count = big_count;
+    // the classify kernel lists the windows of more than 1,024 slots; the big
+    // kernel walks that list on the side stream (at most one work-group per
+    // listed window, 1,024 at most) while the small kernel takes every other
+    // window on the caller's stream
+    hipLaunchKernelGGL(window_topk_classify_kernel, dim3(grid_for(num_active)), dim3(kBlk), 0, stream,
+                       A->window_offset, A->num_windows, (int)A->tile_cols, active_windows, num_active, big_list,
+                       big_count);
     GRWS_LAUNCH_CHECK();
+    const unsigned big_grid = (unsigned)(num_active < 1024 ? num_active : 1024);
+    {
+        SideStream ss(stream);
+        GRWS_TRY(ss.fork());
+        switch (A->values_dtype) {
+            case GRWS_F32:
+                hipLaunchKernelGGL(window_topk_big_kernel<float>, dim3(big_grid), dim3(kTopkBlk), 0, ss.side, ta);
+                GRWS_LAUNCH_CHECK();
+                hipLaunchKernelGGL(window_topk_small_kernel<float>, dim3((unsigned)num_active), dim3(kSmallBlk), 0,
+                                   stream, ta);
+                break;
+            case GRWS_F16:
+                hipLaunchKernelGGL(window_topk_big_kernel<_Float16>, dim3(big_grid), dim3(kTopkBlk), 0, ss.side, ta);
+                GRWS_LAUNCH_CHECK();
+                hipLaunchKernelGGL(window_topk_small_kernel<_Float16>, dim3((unsigned)num_active), dim3(kSmallBlk), 0,
+                                   stream, ta);
+                break;
+            default:
+                hipLaunchKernelGGL(window_topk_big_kernel<__hip_bfloat16>, dim3(big_grid), dim3(kTopkBlk), 0, ss.side,
+                                   ta);
+                GRWS_LAUNCH_CHECK();
+                hipLaunchKernelGGL(window_topk_small_kernel<__hip_bfloat16>, dim3((unsigned)num_active),
+                                   dim3(kSmallBlk), 0, stream, ta);
+                break;
+        }
+        GRWS_LAUNCH_CHECK();
+        GRWS_TRY(ss.join());
+    }
     GRWS_TRY(scan_i32_to_i64(tiles, out_window_offset, num_active, false, scan_ws, scan_bytes, stream));
     int64_t T = 0;
     int32_t e = 0;

@@ -57,7 +57,7 @@ class BCSRGraph:
         self.num_rows = int(num_rows) if num_rows is not None else int(num_nodes)
         self.num_cols = int(num_cols) if num_cols is not None else int(num_nodes)
         self.num_nodes = int(num_nodes)
-        self.num_edges = int(num_edges)
+        self.num_edges = num_edges
         self.tile_rows = int(tile_rows)
         self.tile_cols = int(tile_cols)
         if self.tile_rows != 16:
@@ -70,6 +70,22 @@ class BCSRGraph:
         self._cache: Dict[Any, Any] = {}
 
     # ---------------- constructors (data/bcsr.py:65-159) ----------------
+
+    # num_edges is an int, or a 0-dim device tensor counted on the stream
+    # when the graph was made (from_components): it is read, and kept as an
+    # int, on first access, so that building a sampled layer costs no host
+    # sync unless its edge count is asked for
+    @property
+    def num_edges(self) -> int:
+        n = self._num_edges
+        if isinstance(n, torch.Tensor):
+            n = self._num_edges = int(n.item())
+        return n
+
+    @num_edges.setter
+    def num_edges(self, v) -> None:
+        self._num_edges = v if isinstance(v, torch.Tensor) else int(v)
+
     @classmethod
     def from_dgl(cls, g: Any, tile_rows: int = 16, tile_cols: int = 8,
                  values_dtype: Optional[torch.dtype] = None) -> "BCSRGraph":
@@ -118,10 +134,11 @@ class BCSRGraph:
                         tile_rows: int, tile_cols: int, device: Optional[torch.device] = None,
                         values_dtype: Optional[torch.dtype] = None) -> "BCSRGraph":
         """From kernel outputs (data/bcsr.py:134-159).  num_edges is the
-        count of non-zero values, as in the reference (:147)."""
+        count of non-zero values, as in the reference (:147), counted on the
+        values' stream now and read on first access."""
         if device is None:
             device = window_offset.device
-        nnz = int(torch.count_nonzero(values_condensed).item()) if values_condensed.numel() > 0 else 0
+        nnz = torch.count_nonzero(values_condensed) if values_condensed.numel() > 0 else 0
         return cls(num_nodes=int(num_rows), num_edges=nnz, tile_rows=tile_rows, tile_cols=tile_cols,
                    window_offset=window_offset, original_col_indices=original_col_indices,
                    values_condensed=values_condensed, device=device, num_rows=int(num_rows),
@@ -204,7 +221,7 @@ class BCSRGraph:
         """Move to a device, keeping the rectangular shape (data/bcsr.py:238-258)."""
         if device == self.device:
             return self
-        return BCSRGraph(num_nodes=self.num_rows, num_edges=self.num_edges,
+        return BCSRGraph(num_nodes=self.num_rows, num_edges=self._num_edges,
                          tile_rows=self.tile_rows, tile_cols=self.tile_cols,
                          window_offset=self.window_offset.to(device, non_blocking=non_blocking),
                          original_col_indices=self.original_col_indices.to(device, non_blocking=non_blocking),
@@ -214,7 +231,7 @@ class BCSRGraph:
 
     def with_values_dtype(self, dtype: torch.dtype) -> "BCSRGraph":
         """Same structure, values cast to `dtype` (round to nearest even)."""
-        return BCSRGraph(num_nodes=self.num_rows, num_edges=self.num_edges,
+        return BCSRGraph(num_nodes=self.num_rows, num_edges=self._num_edges,
                          tile_rows=self.tile_rows, tile_cols=self.tile_cols,
                          window_offset=self.window_offset,
                          original_col_indices=self.original_col_indices,
