@@ -176,6 +176,7 @@ constexpr int kTopkBlk = 1024;
 constexpr int kKeyCache = 4096;
 constexpr int kSmallBlk = 256;
 constexpr int kSmallCache = 1024;
+constexpr int kChunk = 1024;  // slots per work-group item of the keys kernel
 
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
 #pragma unroll
@@ -213,7 +214,18 @@ struct TopkArgs {
     int64_t gcap;
     unsigned long long* gcursor;
     int32_t* big_list;   // active indices of the windows left to the big kernel
-    int32_t* big_count;  // their number (zero before the small kernel)
+    int32_t* big_count;  // their number (zero before the classify kernel)
+    // per listed window i: the scratch offset of keys the keys kernel
+    // computes (-1: the big kernel computes them itself), their candidate
+    // count, least and greatest key, and its first chunk
+    int64_t* big_goff;
+    int32_t* big_cnt;
+    unsigned long long* big_kmin;
+    unsigned long long* big_kmax;
+    int32_t* big_cbase;
+    int32_t* chunk_owner;  // per chunk of kChunk slots: its window's list index, -1: none
+    int32_t* chunk_total;  // chunks claimed (zero before the classify kernel)
+    int64_t chunk_cap;     // chunk_owner's entries (0: no keys kernel)
 };
 
 template <int BLK, int KC, int HW>
@@ -236,14 +248,15 @@ struct TopkShared {
 // work-group calls it with the same b; it leaves LDS to the caller's next
 // window only after a barrier.
 template <typename VT, int BLK, int KC, bool SMALL, int HW>
-__device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const int64_t b, const TopkArgs& a) {
+__device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const int64_t b, const int32_t li,
+                                            const TopkArgs& a) {
     constexpr int NW = BLK / kWave;
     constexpr int FASTMAX = SMALL ? KC : BLK;  // rank directly up to this many candidates
     // slots per thread whose loads are issued together: NB in the count pass
     // (a slot's column and 16 values), NK in the select and compaction
     // passes (one key each); more do not fit the 1,024-thread kernel's 128
     // registers without spilling
-    constexpr int NB = SMALL ? 4 : 2;
+    constexpr int NB = SMALL ? 1 : 2;
     constexpr int NK = SMALL ? NB : 4;
     const int tid = threadIdx.x;
     const ScoreParams& p = a.p;
@@ -269,9 +282,13 @@ __device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const i
         if (nslots > KC) return;  // listed for the big kernel
     }
     const bool cached = nslots <= KC;
+    // keys the keys kernel computed (a listed window with scratch of its own)
+    const int64_t pre = !SMALL && li >= 0 ? a.big_goff[li] : -1;  // uniform over the work-group
     if (tid == 0) {
         int64_t off = -1;
-        if (!cached && a.gkeys) {
+        if (pre >= 0) {
+            off = cached ? -1 : pre;
+        } else if (!cached && a.gkeys) {
             const int64_t o = (int64_t)atomicAdd(a.gcursor, (unsigned long long)nslots);
             if (o + nslots <= a.gcap) off = o;
         }
@@ -312,8 +329,17 @@ __device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const i
         }
     };
 
-    // candidates: count, least and greatest key (and the cache)
-    {
+    if (pre >= 0) {
+        // the keys kernel's: into LDS when they fit, else read in place
+        if (cached)
+            for (int64_t s = tid; s < nslots; s += BLK) sh.key[s] = a.gkeys[pre + s];
+        if (tid < NW) {
+            sh.kmin[tid] = a.big_kmin[li];
+            sh.kmax[tid] = a.big_kmax[li];
+        }
+        if (tid == 0) sh.cnt = a.big_cnt[li];
+    } else {
+        // candidates: count, least and greatest key (and the cache)
         int local = 0;
         uint64_t kmin = ~0ull, kmax = 0;
         for (int64_t s = tid; s < nslots; s += NB * BLK) {
@@ -535,26 +561,106 @@ __device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const i
 
 // Lists the active windows of more than kSmallCache slots (in no particular
 // order) for the big kernel; an invalid window id stays with the small
-// kernel, which reports it.
-__global__ __launch_bounds__(kBlk) void window_topk_classify_kernel(const int64_t* __restrict__ win_off,
-                                                                    int64_t num_windows, int tc,
-                                                                    const int32_t* __restrict__ active,
-                                                                    int64_t num_active, int32_t* __restrict__ big_list,
-                                                                    int32_t* __restrict__ big_count) {
+// kernel, which reports it.  A listed window whose keys fit the scratch and
+// whose chunks fit chunk_owner gets both (its keys then come from the keys
+// kernel); any other keeps big_goff -1.
+__global__ __launch_bounds__(kBlk) void window_topk_classify_kernel(TopkArgs a) {
     const int64_t b = (int64_t)blockIdx.x * kBlk + threadIdx.x;
     bool big = false;
-    if (b < num_active) {
-        const int32_t w = active[b];
-        if (w >= 0 && (int64_t)w < num_windows) big = (win_off[w + 1] - win_off[w]) * tc > kSmallCache;
+    int64_t nslots = 0;
+    if (b < a.num_active) {
+        const int32_t w = a.active[b];
+        if (w >= 0 && (int64_t)w < a.num_windows) {
+            nslots = (a.win_off[w + 1] - a.win_off[w]) * a.tc;
+            big = nslots > kSmallCache;
+        }
     }
     const uint64_t m = __ballot(big);
     if (m == 0) return;
     const int lane = threadIdx.x & (kWave - 1);
     const int leader = __ffsll((long long)m) - 1;
     int32_t base = 0;
-    if (lane == leader) base = atomicAdd(big_count, __popcll(m));
+    if (lane == leader) base = atomicAdd(a.big_count, __popcll(m));
     base = __shfl(base, leader, kWave);
-    if (big) big_list[base + __popcll(m & lanemask_lt())] = (int32_t)b;
+    if (!big) return;
+    const int32_t li = base + __popcll(m & lanemask_lt());
+    a.big_list[li] = (int32_t)b;
+    int64_t goff = -1;
+    if (a.gkeys && a.chunk_cap > 0) {
+        const int64_t nch = (nslots + kChunk - 1) / kChunk;
+        const int64_t o = (int64_t)atomicAdd(a.gcursor, (unsigned long long)nslots);
+        const int64_t cb = atomicAdd(a.chunk_total, (int32_t)nch);
+        const bool ok = o + nslots <= a.gcap && cb + nch <= a.chunk_cap;
+        for (int64_t j = 0; j < nch && cb + j < a.chunk_cap; ++j) a.chunk_owner[cb + j] = ok ? li : -1;
+        if (ok) {
+            goff = o;
+            a.big_cbase[li] = (int32_t)cb;
+        }
+    }
+    a.big_goff[li] = goff;
+    a.big_cnt[li] = 0;
+    a.big_kmin[li] = ~0ull;
+    a.big_kmax[li] = 0ull;
+}
+
+// The listed windows' keys, kChunk slots per item, written to each window's
+// scratch; every item adds its candidates to the window's count and folds
+// its least and greatest key in (atomics), as the big kernel's own count
+// pass would.  Walks the chunks the classify kernel claimed; every
+// work-group leaves once they are done.
+template <typename VT>
+__global__ __launch_bounds__(kBlk) void window_topk_keys_kernel(TopkArgs a) {
+    const int tid = threadIdx.x;
+    const ScoreParams& p = a.p;
+    const int64_t claimed = *a.chunk_total;
+    const int64_t total = claimed < a.chunk_cap ? claimed : a.chunk_cap;
+    for (int64_t c = blockIdx.x; c < total; c += gridDim.x) {
+        const int32_t li = a.chunk_owner[c];
+        if (li < 0) continue;  // uniform over the work-group
+        const int32_t w = a.active[a.big_list[li]];
+        const int64_t t0 = a.win_off[w];
+        const int64_t nslots = (a.win_off[w + 1] - t0) * a.tc;
+        const int64_t s0 = (c - a.big_cbase[li]) * (int64_t)kChunk;
+        const int64_t s1 = s0 + kChunk < nslots ? s0 + kChunk : nslots;
+        uint64_t* const gk = a.gkeys + a.big_goff[li];
+        int32_t part_lo = 0, part_hi = 0;
+        bool in_part_known = false;
+        if (p.use_hacs && p.locality && p.window_part_ids && p.part_starts && p.part_ends) {
+            const int32_t pid = p.window_part_ids[w];
+            if ((int64_t)pid >= p.num_parts) {
+                if (tid == 0) atomicOr(a.err, kErrHacs);
+            } else if (pid >= 0) {
+                part_lo = p.part_starts[pid];
+                part_hi = p.part_ends[pid];
+                in_part_known = true;
+            }
+        }
+        int local = 0;
+        uint64_t kmin = ~0ull, kmax = 0;
+        for (int64_t s = s0 + tid; s < s1; s += kBlk) {
+            SlotRaw r;
+            slot_load<VT>(a.cols, a.vals, t0, a.tc, s, r);
+            uint64_t k = 0;
+            const bool cand = slot_key_of(r, part_lo, part_hi, in_part_known, p, &k);
+            gk[s] = cand ? k : ~0ull;
+            if (cand) {
+                ++local;
+                kmin = k < kmin ? k : kmin;
+                kmax = k > kmax ? k : kmax;
+            }
+            if (p.use_hacs && r.col != -1 && (r.col < 0 || (int64_t)r.col >= p.num_static_scores))
+                atomicOr(a.err, kErrHacs);
+        }
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) local += __shfl_xor(local, d, kWave);
+        kmin = wave_min_u64(kmin);
+        kmax = wave_max_u64(kmax);
+        if ((tid & (kWave - 1)) == 0 && local > 0) {
+            atomicAdd(&a.big_cnt[li], local);
+            atomicMin(&a.big_kmin[li], (unsigned long long)kmin);
+            atomicMax(&a.big_kmax[li], (unsigned long long)kmax);
+        }
+    }
 }
 
 template <typename VT>
@@ -562,17 +668,18 @@ __global__ __launch_bounds__(kSmallBlk) void window_topk_small_kernel(TopkArgs a
     __shared__ TopkShared<kSmallBlk, kSmallCache, 1> sh;
     const int64_t b = blockIdx.x;
     if (b >= a.num_active) return;
-    topk_window<VT, kSmallBlk, kSmallCache, true, 1>(sh, b, a);
+    topk_window<VT, kSmallBlk, kSmallCache, true, 1>(sh, b, -1, a);
 }
 
-// Walks the classify kernel's list (launched after it, so the count is
-// final); every work-group leaves once the list is done.
+// Walks the classify kernel's list (launched after it and after the keys
+// kernel, so the count and the keys are final); every work-group leaves
+// once the list is done.
 template <typename VT>
 __global__ __launch_bounds__(kTopkBlk) void window_topk_big_kernel(TopkArgs a) {
     __shared__ TopkShared<kTopkBlk, kKeyCache, kTopkBlk / kWave> sh;
     const int32_t n = *a.big_count;
     for (int32_t i = (int32_t)blockIdx.x; i < n; i += (int32_t)gridDim.x) {
-        topk_window<VT, kTopkBlk, kKeyCache, false, kTopkBlk / kWave>(sh, a.big_list[i], a);
+        topk_window<VT, kTopkBlk, kKeyCache, false, kTopkBlk / kWave>(sh, a.big_list[i], i, a);
         __syncthreads();
     }
 }
@@ -773,16 +880,31 @@ extern "C" size_t grws_window_topk_workspace_bytes(int64_t num_active) {
     s.take<int32_t>(64);
     s.take<int32_t>((size_t)num_active + 1);  // the big kernel's list
     s.take<int32_t>(64);                      // and its count
+    s.take<int64_t>((size_t)num_active + 1);  // per listed window: scratch offset,
+    s.take<int32_t>((size_t)num_active + 1);  // candidate count,
+    s.take<uint64_t>((size_t)num_active + 1); // least key,
+    s.take<uint64_t>((size_t)num_active + 1); // greatest key,
+    s.take<int32_t>((size_t)num_active + 1);  // first chunk
+    s.take<int32_t>(64);                      // chunks claimed
     s.used += scan_workspace_bytes(num_active) + 256;
     return s.used;
 }
 
-// Workspace beyond grws_window_topk_workspace_bytes(num_active) is key
-// scratch for windows of more than 4,096 slots (8 bytes per slot of each
-// such active window; a window that does not fit recomputes its keys).
+namespace {
+// chunk_owner entries that cover every chunk of distinct active windows
+int64_t topk_chunk_cap(const grws_bcsr* A) {
+    return A->num_tiles * A->tile_cols / kChunk + A->num_windows + 1;
+}
+}  // namespace
+
+// Workspace beyond grws_window_topk_workspace_bytes(num_active) is the keys
+// kernel's chunk table and key scratch for the windows of more than 1,024
+// slots (8 bytes per slot of each such active window).  A window whose keys
+// do not fit computes them in the big kernel (into LDS up to 4,096 slots,
+// recomputed on every pass beyond), with the same results.
 extern "C" size_t grws_window_topk_key_scratch_bytes(const grws_bcsr* A) {
-    if (!A || A->num_tiles < 0) return 0;
-    return (size_t)(A->num_tiles * A->tile_cols) * 8 + 256;
+    if (!A || A->num_tiles < 0 || A->num_windows < 0) return 0;
+    return align_up((size_t)topk_chunk_cap(A) * 4, 256) + (size_t)(A->num_tiles * A->tile_cols) * 8 + 512;
 }
 
 extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
@@ -832,15 +954,33 @@ extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_window
     int32_t* err = cv.take<int32_t>(64);
     int32_t* big_list = cv.take<int32_t>(num_active + 1);
     int32_t* big_count = cv.take<int32_t>(64);
+    int64_t* big_goff = cv.take<int64_t>(num_active + 1);
+    int32_t* big_cnt = cv.take<int32_t>(num_active + 1);
+    uint64_t* big_kmin = cv.take<uint64_t>(num_active + 1);
+    uint64_t* big_kmax = cv.take<uint64_t>(num_active + 1);
+    int32_t* big_cbase = cv.take<int32_t>(num_active + 1);
+    int32_t* chunk_total = cv.take<int32_t>(64);
     const size_t scan_bytes = scan_workspace_bytes(num_active);
     char* scan_ws = cv.take<char>(scan_bytes);
     if (!cv.ok) return set_error(GRWS_E_CAPACITY, "window_topk: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
-    // the rest: a cursor and the hub windows' key scratch
+    // the rest: the chunk table, a cursor and the big windows' key scratch
     unsigned long long* gcursor = nullptr;
     uint64_t* gkeys = nullptr;
     int64_t gcap = 0;
+    int32_t* chunk_owner = nullptr;
+    int64_t chunk_cap = 0;
     {
         Carver rest = cv;
+        const int64_t want = topk_chunk_cap(A);
+        {
+            Carver probe = rest;
+            int32_t* co = probe.take<int32_t>((size_t)want);
+            if (probe.ok && probe.used + 512 <= probe.cap) {
+                rest = probe;
+                chunk_owner = co;
+                chunk_cap = want;
+            }
+        }
         unsigned long long* cur = rest.take<unsigned long long>(1);
         if (rest.ok && rest.used + 256 <= rest.cap) {
             const size_t left = rest.cap - rest.used - 256;
@@ -854,6 +994,7 @@ extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_window
     }
     GRWS_TRY(fill_i32(err, 1, 0, stream));
     GRWS_TRY(fill_i32(big_count, 1, 0, stream));
+    GRWS_TRY(fill_i32(chunk_total, 1, 0, stream));
     if (gcursor) GRWS_TRY(fill_i32(reinterpret_cast<int32_t*>(gcursor), 2, 0, stream));
     TopkArgs ta{};
     ta.win_off = A->window_offset;
@@ -875,32 +1016,47 @@ extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_window
     ta.gcursor = gcursor;
     ta.big_list = big_list;
     ta.big_count = big_count;
-    // the classify kernel lists the windows of more than 1,024 slots; the big
-    // kernel walks that list on the side stream (at most one work-group per
-    // listed window, 1,024 at most) while the small kernel takes every other
-    // window on the caller's stream
-    hipLaunchKernelGGL(window_topk_classify_kernel, dim3(grid_for(num_active)), dim3(kBlk), 0, stream,
-                       A->window_offset, A->num_windows, (int)A->tile_cols, active_windows, num_active, big_list,
-                       big_count);
+    ta.big_goff = big_goff;
+    ta.big_cnt = big_cnt;
+    ta.big_kmin = reinterpret_cast<unsigned long long*>(big_kmin);
+    ta.big_kmax = reinterpret_cast<unsigned long long*>(big_kmax);
+    ta.big_cbase = big_cbase;
+    ta.chunk_owner = chunk_owner;
+    ta.chunk_total = chunk_total;
+    ta.chunk_cap = gcursor ? chunk_cap : 0;
+    // the classify kernel lists the windows of more than 1,024 slots; on the
+    // side stream the keys kernel computes their keys and the big kernel
+    // walks the list (at most one work-group per listed window, 1,024 at
+    // most) while the small kernel takes every other window on the caller's
+    // stream
+    hipLaunchKernelGGL(window_topk_classify_kernel, dim3(grid_for(num_active)), dim3(kBlk), 0, stream, ta);
     GRWS_LAUNCH_CHECK();
     const unsigned big_grid = (unsigned)(num_active < 1024 ? num_active : 1024);
+    constexpr unsigned kKeysGrid = 1024;  // the keys kernel's work-groups walk the chunks
     {
         SideStream ss(stream);
         GRWS_TRY(ss.fork());
         switch (A->values_dtype) {
             case GRWS_F32:
+                hipLaunchKernelGGL(window_topk_keys_kernel<float>, dim3(kKeysGrid), dim3(kBlk), 0, ss.side, ta);
+                GRWS_LAUNCH_CHECK();
                 hipLaunchKernelGGL(window_topk_big_kernel<float>, dim3(big_grid), dim3(kTopkBlk), 0, ss.side, ta);
                 GRWS_LAUNCH_CHECK();
                 hipLaunchKernelGGL(window_topk_small_kernel<float>, dim3((unsigned)num_active), dim3(kSmallBlk), 0,
                                    stream, ta);
                 break;
             case GRWS_F16:
+                hipLaunchKernelGGL(window_topk_keys_kernel<_Float16>, dim3(kKeysGrid), dim3(kBlk), 0, ss.side, ta);
+                GRWS_LAUNCH_CHECK();
                 hipLaunchKernelGGL(window_topk_big_kernel<_Float16>, dim3(big_grid), dim3(kTopkBlk), 0, ss.side, ta);
                 GRWS_LAUNCH_CHECK();
                 hipLaunchKernelGGL(window_topk_small_kernel<_Float16>, dim3((unsigned)num_active), dim3(kSmallBlk), 0,
                                    stream, ta);
                 break;
             default:
+                hipLaunchKernelGGL(window_topk_keys_kernel<__hip_bfloat16>, dim3(kKeysGrid), dim3(kBlk), 0, ss.side,
+                                   ta);
+                GRWS_LAUNCH_CHECK();
                 hipLaunchKernelGGL(window_topk_big_kernel<__hip_bfloat16>, dim3(big_grid), dim3(kTopkBlk), 0, ss.side,
                                    ta);
                 GRWS_LAUNCH_CHECK();
