@@ -904,11 +904,31 @@ def bench_dps(dev, cpu: bool, reps: int = 10) -> dict:
         torch.cuda.synchronize(dev)
         tw.append(time.perf_counter() - t0)
     tiles = [int(x.window_offset[-1]) for x in layers]
+    # algorithmic bytes of the last batch: per layer the active windows'
+    # input tiles read once (column ids and values), the sampled tiles
+    # written (column ids and values), the layer's seed ids read and its
+    # active windows and masks written
+    woff = G8.window_offset
+    s_v = G8.values_condensed.element_size()
+    tile_b = 8 * 4 + 16 * 8 * s_v
+    wb = 0
+    n_ids = 1024
+    for x in reversed(layers):  # the hop from the seeds first
+        act = x.active_windows.long()
+        wb += int((woff[act + 1] - woff[act]).sum()) * tile_b + int(x.window_offset[-1]) * tile_b
+        wb += 4 * n_ids + 8 * act.numel()
+        n_ids = 8 * int(x.window_offset[-1])
+    bms = 1e3 * sum(tw) / len(tw)
     wr = {"workload": "c2 window top-K sampling (BCSRSampler, 16x8 tiles, f32 values, 1,024 seeds, fanouts "
                       "[15,10,5]): prepare windows, top-K per window, recompress, per layer",
-          "batch_ms": round(1e3 * sum(tw) / len(tw), 4), "batches": len(tw),
+          "batch_ms": round(bms, 4), "batches": len(tw),
           "tiles_last_batch": tiles, "active_windows_last_batch": [int(x.active_windows.numel()) for x in layers],
-          "host_syncs_per_batch": 3}
+          "host_syncs_per_batch": 1,
+          "roofline": {"bound": "hbm (per-window selection: latency bound in practice)",
+                       "achieved": round(wb / (bms / 1e3) / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(wb / (bms / 1e3) / 1e9 / HBM_PEAK_GBS, 5), "bytes_per_batch": wb,
+                       "bytes": "per layer: the active windows' input tiles read once (column ids and values), "
+                                "the sampled tiles written, the seed ids read, the windows and masks written"}}
     if cpu:
         import oracle
         seeds = seed_sets[-1].cpu().numpy()

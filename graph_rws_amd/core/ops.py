@@ -795,9 +795,80 @@ def sample_all_layers(window_offset: torch.Tensor, original_col_indices: torch.T
     sampling_wrapper.cu:365-438).  Returns (layers, timings): per fanout, in
     the order given, [out_window_offset int64, out_col_indices int32 (global
     ids), out_values, active_windows int32, masks int32], and one
-    SamplingTimingResult.  Output arrays are sized exactly (no -1 tail);
-    values keep values_condensed's dtype.  warps_per_block is validated as
-    the reference does (4 or 8) and has no effect on the result."""
+    SamplingTimingResult.  Output arrays are sized exactly (no -1 tail;
+    views of buffers sized by the layers' bounds); values keep
+    values_condensed's dtype.  warps_per_block is validated as the reference
+    does (4 or 8) and has no effect on the result.  Every layer runs in one
+    grws_window_sample_layers call: one host sync for the batch."""
+    if tile_rows != 16 or tile_cols not in (8, 16):
+        raise RuntimeError("sample_all_layers supports 16x8 tiles (the reference's) and 16x16")
+    if warps_per_block not in (4, 8):
+        raise RuntimeError(f"Unsupported warps_per_block: {warps_per_block}. Only 4 and 8 allowed.")
+    _check_graph(window_offset, original_col_indices, values_condensed, tile_cols)
+    if not window_offset.is_cuda:
+        raise RuntimeError("window_offset must be a CUDA tensor")
+    fanouts = [int(f) for f in fanouts]
+    for f in fanouts:
+        if not 1 <= f <= 256:
+            raise RuntimeError("Fanout > 256 not supported (fanout must be in [1, 256])")
+    if not fanouts:
+        return [], []
+    dev = window_offset.device
+    W = window_offset.numel() - 1
+    n_nodes = int(num_global_nodes) if int(num_global_nodes) > 0 else 16 * W
+    keep: list = []
+    hv = _hacs_view(dev, static_scores, window_part_ids, part_starts, part_ends, alpha, beta,
+                    delta, gamma_bonus, score_scale, use_hacs, locality_enabled, keep)
+    view = L.BcsrView(L.ptr(window_offset), L.ptr(original_col_indices), L.ptr(values_condensed),
+                      W, original_col_indices.numel() // tile_cols, 16, tile_cols,
+                      L.dtype_code(values_condensed.dtype), 0)
+    seeds = initial_seeds.to(dev).to(torch.int32).contiguous()
+    nl = len(fanouts)
+    fan = (ctypes.c_int32 * nl)(*fanouts)
+    max_a = (ctypes.c_int64 * nl)()
+    max_t = (ctypes.c_int64 * nl)()
+    L.call("grws_window_sample_layers_bounds", ctypes.byref(view), n_nodes, seeds.numel(), fan, nl, max_a, max_t)
+    lib = L.load()
+    bufs = []
+    for i in range(nl):
+        a, t = int(max_a[i]), int(max_t[i])
+        bufs.append((torch.empty(a + 1, dtype=torch.int64, device=dev),
+                     torch.empty(max(t * tile_cols, 1), dtype=torch.int32, device=dev),
+                     torch.empty(max(t * 16 * tile_cols, 1), dtype=values_condensed.dtype, device=dev),
+                     torch.empty(max(a, 1), dtype=torch.int32, device=dev),
+                     torch.empty(max(a, 1), dtype=torch.int32, device=dev)))
+    ptrs = [(ctypes.c_void_p * nl)(*[b[k].data_ptr() for b in bufs]) for k in range(5)]
+    # plus key scratch for the big windows: at most the graph's slots, at
+    # most WINDOW_KEY_SCRATCH bytes
+    wsb = int(lib.grws_window_sample_layers_workspace_bytes(ctypes.byref(view), n_nodes, seeds.numel(), fan, nl))
+    wsb += min(int(lib.grws_window_topk_key_scratch_bytes(ctypes.byref(view))), WINDOW_KEY_SCRATCH)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    counts = (ctypes.c_int64 * (2 * nl))()
+    phase = (ctypes.c_float * (2 * nl))()
+    L.call("grws_window_sample_layers", ctypes.byref(view), n_nodes, L.ptr(seeds), seeds.numel(), fan, nl,
+           ctypes.byref(hv) if hv is not None else None, ptrs[0], ptrs[1], ptrs[2], ptrs[3], ptrs[4], counts,
+           phase, L.ptr(ws), wsb, L.stream_of(dev))
+    layers, timings = [], []
+    for i, (off, cols, vals, act, msk) in enumerate(bufs):
+        A, T = int(counts[2 * i]), int(counts[2 * i + 1])
+        layers.append([off[:A + 1], cols[:T * tile_cols], vals[:T * 16 * tile_cols], act[:A], msk[:A]])
+        p1, p3 = float(phase[2 * i]), float(phase[2 * i + 1])
+        timings.append(SamplingTimingResult(p1, 0.0, p3, p1 + p3))
+    return layers, timings
+
+
+def _sample_all_layers_per_layer(window_offset: torch.Tensor, original_col_indices: torch.Tensor,
+                      values_condensed: torch.Tensor, initial_seeds: torch.Tensor, fanouts,
+                      num_global_nodes: int, static_scores: Optional[torch.Tensor] = None,
+                      window_part_ids: Optional[torch.Tensor] = None,
+                      part_starts: Optional[torch.Tensor] = None,
+                      part_ends: Optional[torch.Tensor] = None, alpha: float = 1.0,
+                      beta: float = 10.0, delta: float = 0.0, gamma_bonus: float = 0.0,
+                      score_scale: float = 100.0, use_hacs: int = 0, locality_enabled: int = 0,
+                      tile_rows: int = 16, tile_cols: int = 8, warps_per_block: int = 8):
+    """sample_all_layers through the per-layer entry points (grws_window_seeds,
+    grws_window_topk, grws_window_recompress; two host syncs per layer):
+    the same results as the one-call path, kept to check it."""
     if tile_rows != 16 or tile_cols not in (8, 16):
         raise RuntimeError("sample_all_layers supports 16x8 tiles (the reference's) and 16x16")
     if warps_per_block not in (4, 8):

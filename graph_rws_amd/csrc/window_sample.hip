@@ -202,7 +202,8 @@ struct TopkArgs {
     const void* vals;
     int tc;
     const int32_t* active;
-    int64_t num_active;
+    int64_t num_active;             // the count, or its bound when num_active_dev is set
+    const int64_t* num_active_dev;  // the count on the device (NULL: num_active)
     ScoreParams p;
     int cap;
     int S;
@@ -566,9 +567,10 @@ __device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const i
 // kernel); any other keeps big_goff -1.
 __global__ __launch_bounds__(kBlk) void window_topk_classify_kernel(TopkArgs a) {
     const int64_t b = (int64_t)blockIdx.x * kBlk + threadIdx.x;
+    const int64_t na = a.num_active_dev ? *a.num_active_dev : a.num_active;
     bool big = false;
     int64_t nslots = 0;
-    if (b < a.num_active) {
+    if (b < na) {
         const int32_t w = a.active[b];
         if (w >= 0 && (int64_t)w < a.num_windows) {
             nslots = (a.win_off[w + 1] - a.win_off[w]) * a.tc;
@@ -667,7 +669,11 @@ template <typename VT>
 __global__ __launch_bounds__(kSmallBlk) void window_topk_small_kernel(TopkArgs a) {
     __shared__ TopkShared<kSmallBlk, kSmallCache, 1> sh;
     const int64_t b = blockIdx.x;
-    if (b >= a.num_active) return;
+    const int64_t na = a.num_active_dev ? *a.num_active_dev : a.num_active;
+    if (b >= na) {  // past the device count: no tiles (the scan runs over the bound)
+        if (b < a.num_active && threadIdx.x == 0) a.out_tiles[b] = 0;
+        return;
+    }
     topk_window<VT, kSmallBlk, kSmallCache, true, 1>(sh, b, -1, a);
 }
 
@@ -689,14 +695,15 @@ __global__ __launch_bounds__(kBlk) void window_recompress_kernel(const int64_t* 
                                                                  int64_t num_windows,
                                                                  const void* __restrict__ vals, int tc,
                                                                  const int32_t* __restrict__ active,
-                                                                 int64_t num_active, int S,
+                                                                 int64_t num_active,
+                                                                 const int64_t* __restrict__ num_active_dev, int S,
                                                                  const int32_t* __restrict__ samp_cols,
                                                                  const int32_t* __restrict__ samp_slots,
                                                                  const int64_t* __restrict__ out_off,
                                                                  int32_t* __restrict__ out_cols,
                                                                  VT* __restrict__ out_vals) {
     const int64_t b = blockIdx.x;
-    if (b >= num_active) return;
+    if (b >= (num_active_dev ? *num_active_dev : num_active)) return;
     const int64_t o0 = out_off[b];
     const int64_t ntile = out_off[b + 1] - o0;
     const int per_tile = 16 * tc;
@@ -761,6 +768,52 @@ __global__ void seed_emit_kernel(const uint64_t* __restrict__ keys, const uint32
     const int64_t idx = rank[i] + head[i] - 1;  // inclusive rank of this run
     if (head[i]) windows[idx] = (int32_t)keys[i];
     atomicOr(reinterpret_cast<uint32_t*>(masks) + idx, bits[i]);
+}
+
+// --- the same from a dense per-window mask (zero on entry, left zero) ----
+// ids -> OR of their row bits into dense[id / 16]; n ids, or n_dev[0] * mul
+// when n_dev is set (the previous layer's tiles times their columns)
+__global__ __launch_bounds__(kBlk) void seeds_scatter_kernel(const int32_t* __restrict__ ids, int64_t n,
+                                                             const int64_t* __restrict__ n_dev, int64_t mul,
+                                                             int64_t num_nodes, int drop_out_of_range,
+                                                             uint32_t* __restrict__ dense, int32_t* __restrict__ err) {
+    const int64_t m = n_dev ? *n_dev * mul : n;
+    for (int64_t i = (int64_t)blockIdx.x * kBlk + threadIdx.x; i < m; i += (int64_t)gridDim.x * kBlk) {
+        const int32_t v = ids[i];
+        if (v >= 0 && (int64_t)v < num_nodes) atomicOr(&dense[v >> 4], 1u << (v & 15));
+        else if (v != -1 && !drop_out_of_range) atomicOr(err, kErrSeed);
+    }
+}
+
+__global__ __launch_bounds__(kBlk) void seeds_flags_kernel(const uint32_t* __restrict__ dense, int64_t nw,
+                                                           int32_t* __restrict__ flags) {
+    const int64_t w = (int64_t)blockIdx.x * kBlk + threadIdx.x;
+    if (w < nw) flags[w] = dense[w] != 0u;
+}
+
+// windows in ascending order with their masks; the dense entries go back
+// to zero
+__global__ __launch_bounds__(kBlk) void seeds_dense_emit_kernel(uint32_t* __restrict__ dense, int64_t nw,
+                                                                const int64_t* __restrict__ rank,
+                                                                int32_t* __restrict__ windows,
+                                                                int32_t* __restrict__ masks) {
+    const int64_t w = (int64_t)blockIdx.x * kBlk + threadIdx.x;
+    if (w >= nw) return;
+    const uint32_t m = dense[w];
+    if (m == 0u) return;
+    const int64_t idx = rank[w];
+    windows[idx] = (int32_t)w;
+    masks[idx] = (int32_t)m;
+    dense[w] = 0u;
+}
+
+// a layer's active windows and tiles, kept for the one read-back at the end
+__global__ void layer_counts_kernel(const int64_t* __restrict__ num_active, const int64_t* __restrict__ num_tiles,
+                                    int64_t* __restrict__ out) {
+    if (threadIdx.x == 0) {
+        out[0] = *num_active;
+        out[1] = *num_tiles;
+    }
 }
 
 struct SeedWs {
@@ -873,21 +926,28 @@ extern "C" int grws_window_seeds(const int32_t* ids, int64_t num_ids, int64_t nu
     return GRWS_OK;
 }
 
-extern "C" size_t grws_window_topk_workspace_bytes(int64_t num_active) {
-    if (num_active < 0) return 0;
+namespace {
+// topk_enqueue's fixed part of its workspace
+size_t topk_fixed_bytes(int64_t num_active) {
     Sizer s;
-    s.take<int32_t>((size_t)num_active + 1);
-    s.take<int32_t>(64);
+    s.take<int32_t>((size_t)num_active + 1);  // tile counts
+    s.take<int32_t>(64);                      // counters
     s.take<int32_t>((size_t)num_active + 1);  // the big kernel's list
-    s.take<int32_t>(64);                      // and its count
     s.take<int64_t>((size_t)num_active + 1);  // per listed window: scratch offset,
     s.take<int32_t>((size_t)num_active + 1);  // candidate count,
     s.take<uint64_t>((size_t)num_active + 1); // least key,
     s.take<uint64_t>((size_t)num_active + 1); // greatest key,
     s.take<int32_t>((size_t)num_active + 1);  // first chunk
-    s.take<int32_t>(64);                      // chunks claimed
     s.used += scan_workspace_bytes(num_active) + 256;
     return s.used;
+}
+}  // namespace
+
+extern "C" size_t grws_window_topk_workspace_bytes(int64_t num_active) {
+    if (num_active < 0) return 0;
+    Sizer s;
+    s.take<int32_t>(64);  // the flag word
+    return s.used + topk_fixed_bytes(num_active);
 }
 
 namespace {
@@ -907,22 +967,10 @@ extern "C" size_t grws_window_topk_key_scratch_bytes(const grws_bcsr* A) {
     return align_up((size_t)topk_chunk_cap(A) * 4, 256) + (size_t)(A->num_tiles * A->tile_cols) * 8 + 512;
 }
 
-extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
-                                int32_t fanout, const grws_hacs* hacs, int32_t* sampled_cols,
-                                int32_t* sampled_slots, int64_t* out_window_offset, void* workspace,
-                                size_t workspace_bytes, int64_t* num_tiles_out, void* stream_) {
-    clear_error();
-    hipStream_t stream = as_stream(stream_);
-    GRWS_TRY(check_graph(A, "window_topk"));
-    GRWS_CHECK_ARG(num_active >= 0, "window_topk: negative num_active");
-    GRWS_CHECK_ARG(num_active <= INT32_MAX, "window_topk: too many active windows");
-    GRWS_CHECK_ARG(num_tiles_out && out_window_offset, "window_topk: null output");
-    const int S = grws_window_sample_num(fanout);
-    GRWS_CHECK_ARG(S >= 32 && S <= kMaxCap, "window_topk: fanout must be in [1, 256] (got %d)", fanout);
-    const int cap = S <= 32 ? 32 : (S <= 128 ? 128 : 256);
-    *num_tiles_out = 0;
-    if (num_active == 0) return fill_i64(out_window_offset, 1, 0, stream);
-    GRWS_CHECK_ARG(active_windows && sampled_cols && sampled_slots, "window_topk: null pointer");
+namespace grws {
+namespace {
+
+ScoreParams score_params(const grws_hacs* hacs) {
     ScoreParams p{};
     p.alpha = 1.0f;
     p.beta = 10.0f;
@@ -941,30 +989,47 @@ extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_window
         p.window_part_ids = hacs->window_part_ids;
         p.part_starts = hacs->part_starts;
         p.part_ends = hacs->part_ends;
-        GRWS_CHECK_ARG(p.static_scores != nullptr, "window_topk: HACS needs static_scores");
-        if (p.locality) {
-            GRWS_CHECK_ARG(p.window_part_ids && p.part_starts && p.part_ends,
-                           "window_topk: locality needs window_part_ids, part_starts and part_ends");
-            GRWS_CHECK_ARG(hacs->num_window_part_ids >= A->num_windows,
-                           "window_topk: window_part_ids has fewer entries than the graph has windows");
-        }
     }
+    return p;
+}
+
+int check_hacs(const grws_bcsr* A, const grws_hacs* hacs, const char* who) {
+    if (!hacs || !hacs->use_hacs) return GRWS_OK;
+    GRWS_CHECK_ARG(hacs->static_scores != nullptr, "%s: HACS needs static_scores", who);
+    if (hacs->locality_enabled) {
+        GRWS_CHECK_ARG(hacs->window_part_ids && hacs->part_starts && hacs->part_ends,
+                       "%s: locality needs window_part_ids, part_starts and part_ends", who);
+        GRWS_CHECK_ARG(hacs->num_window_part_ids >= A->num_windows,
+                       "%s: window_part_ids has fewer entries than the graph has windows", who);
+    }
+    return GRWS_OK;
+}
+
+// grws_window_topk's work without the read-back: the active windows' samples
+// and the scan of their tile counts into out_window_offset (num_active + 1
+// entries; with num_active_dev set, num_active is a bound, the windows past
+// the device count get no tiles and every entry from there on is the
+// total).  err is the caller's flag word.  workspace: at least
+// grws_window_topk_workspace_bytes(num_active); the rest is the chunk table
+// and key scratch.
+int topk_enqueue(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
+                 const int64_t* num_active_dev, int S, const ScoreParams& p, int32_t* sampled_cols,
+                 int32_t* sampled_slots, int64_t* out_window_offset, int32_t* err, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream) {
+    const int cap = S <= 32 ? 32 : (S <= 128 ? 128 : 256);
     Carver cv(workspace, workspace_bytes);
     int32_t* tiles = cv.take<int32_t>(num_active + 1);
-    int32_t* err = cv.take<int32_t>(64);
+    int32_t* ctr = cv.take<int32_t>(64);  // [0] listed windows, [1] chunks claimed, [2..3] the scratch cursor
     int32_t* big_list = cv.take<int32_t>(num_active + 1);
-    int32_t* big_count = cv.take<int32_t>(64);
     int64_t* big_goff = cv.take<int64_t>(num_active + 1);
     int32_t* big_cnt = cv.take<int32_t>(num_active + 1);
     uint64_t* big_kmin = cv.take<uint64_t>(num_active + 1);
     uint64_t* big_kmax = cv.take<uint64_t>(num_active + 1);
     int32_t* big_cbase = cv.take<int32_t>(num_active + 1);
-    int32_t* chunk_total = cv.take<int32_t>(64);
     const size_t scan_bytes = scan_workspace_bytes(num_active);
     char* scan_ws = cv.take<char>(scan_bytes);
     if (!cv.ok) return set_error(GRWS_E_CAPACITY, "window_topk: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
-    // the rest: the chunk table, a cursor and the big windows' key scratch
-    unsigned long long* gcursor = nullptr;
+    // the rest: the chunk table and the big windows' key scratch
     uint64_t* gkeys = nullptr;
     int64_t gcap = 0;
     int32_t* chunk_owner = nullptr;
@@ -975,27 +1040,22 @@ extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_window
         {
             Carver probe = rest;
             int32_t* co = probe.take<int32_t>((size_t)want);
-            if (probe.ok && probe.used + 512 <= probe.cap) {
+            if (probe.ok && probe.used + 256 <= probe.cap) {
                 rest = probe;
                 chunk_owner = co;
                 chunk_cap = want;
             }
         }
-        unsigned long long* cur = rest.take<unsigned long long>(1);
         if (rest.ok && rest.used + 256 <= rest.cap) {
             const size_t left = rest.cap - rest.used - 256;
             uint64_t* keys = rest.take<uint64_t>(left / 8);
             if (rest.ok && left / 8 > 0) {
-                gcursor = cur;
                 gkeys = keys;
                 gcap = (int64_t)(left / 8);
             }
         }
     }
-    GRWS_TRY(fill_i32(err, 1, 0, stream));
-    GRWS_TRY(fill_i32(big_count, 1, 0, stream));
-    GRWS_TRY(fill_i32(chunk_total, 1, 0, stream));
-    if (gcursor) GRWS_TRY(fill_i32(reinterpret_cast<int32_t*>(gcursor), 2, 0, stream));
+    GRWS_TRY(fill_i32(ctr, 4, 0, stream));
     TopkArgs ta{};
     ta.win_off = A->window_offset;
     ta.num_windows = A->num_windows;
@@ -1004,6 +1064,7 @@ extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_window
     ta.tc = (int)A->tile_cols;
     ta.active = active_windows;
     ta.num_active = num_active;
+    ta.num_active_dev = num_active_dev;
     ta.p = p;
     ta.cap = cap;
     ta.S = S;
@@ -1013,17 +1074,17 @@ extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_window
     ta.err = err;
     ta.gkeys = gkeys;
     ta.gcap = gcap;
-    ta.gcursor = gcursor;
+    ta.gcursor = reinterpret_cast<unsigned long long*>(ctr + 2);
     ta.big_list = big_list;
-    ta.big_count = big_count;
+    ta.big_count = ctr;
     ta.big_goff = big_goff;
     ta.big_cnt = big_cnt;
     ta.big_kmin = reinterpret_cast<unsigned long long*>(big_kmin);
     ta.big_kmax = reinterpret_cast<unsigned long long*>(big_kmax);
     ta.big_cbase = big_cbase;
     ta.chunk_owner = chunk_owner;
-    ta.chunk_total = chunk_total;
-    ta.chunk_cap = gcursor ? chunk_cap : 0;
+    ta.chunk_total = ctr + 1;
+    ta.chunk_cap = gkeys ? chunk_cap : 0;
     // the classify kernel lists the windows of more than 1,024 slots; on the
     // side stream the keys kernel computes their keys and the big kernel
     // walks the list (at most one work-group per listed window, 1,024 at
@@ -1067,15 +1128,77 @@ extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_window
         GRWS_LAUNCH_CHECK();
         GRWS_TRY(ss.join());
     }
-    GRWS_TRY(scan_i32_to_i64(tiles, out_window_offset, num_active, false, scan_ws, scan_bytes, stream));
+    return scan_i32_to_i64(tiles, out_window_offset, num_active, false, scan_ws, scan_bytes, stream);
+}
+
+int recompress_enqueue(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
+                       const int64_t* num_active_dev, int S, const int32_t* sampled_cols,
+                       const int32_t* sampled_slots, const int64_t* out_window_offset, int32_t* out_cols,
+                       void* out_values, hipStream_t stream) {
+    switch (A->values_dtype) {
+        case GRWS_F32:
+            hipLaunchKernelGGL(window_recompress_kernel<float>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
+                               A->window_offset, A->num_windows, A->values, (int)A->tile_cols, active_windows,
+                               num_active, num_active_dev, S, sampled_cols, sampled_slots, out_window_offset,
+                               out_cols, static_cast<float*>(out_values));
+            break;
+        case GRWS_F16:
+            hipLaunchKernelGGL(window_recompress_kernel<_Float16>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
+                               A->window_offset, A->num_windows, A->values, (int)A->tile_cols, active_windows,
+                               num_active, num_active_dev, S, sampled_cols, sampled_slots, out_window_offset,
+                               out_cols, static_cast<_Float16*>(out_values));
+            break;
+        default:
+            hipLaunchKernelGGL(window_recompress_kernel<uint16_t>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
+                               A->window_offset, A->num_windows, A->values, (int)A->tile_cols, active_windows,
+                               num_active, num_active_dev, S, sampled_cols, sampled_slots, out_window_offset,
+                               out_cols, static_cast<uint16_t*>(out_values));
+            break;
+    }
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
+int report_topk_errors(int32_t e, const char* who) {
+    if (e & kErrSeed) return set_error(GRWS_E_RANGE, "%s: a seed id is outside [0, num_nodes) and not -1", who);
+    if (e & kErrWindow) return set_error(GRWS_E_RANGE, "%s: an active window is outside the graph", who);
+    if (e & kErrHacs) return set_error(GRWS_E_RANGE, "%s: a column has no static score or a part id has no range", who);
+    return GRWS_OK;
+}
+
+}  // namespace
+}  // namespace grws
+
+extern "C" int grws_window_topk(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
+                                int32_t fanout, const grws_hacs* hacs, int32_t* sampled_cols,
+                                int32_t* sampled_slots, int64_t* out_window_offset, void* workspace,
+                                size_t workspace_bytes, int64_t* num_tiles_out, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_TRY(check_graph(A, "window_topk"));
+    GRWS_CHECK_ARG(num_active >= 0, "window_topk: negative num_active");
+    GRWS_CHECK_ARG(num_active <= INT32_MAX, "window_topk: too many active windows");
+    GRWS_CHECK_ARG(num_tiles_out && out_window_offset, "window_topk: null output");
+    const int S = grws_window_sample_num(fanout);
+    GRWS_CHECK_ARG(S >= 32 && S <= kMaxCap, "window_topk: fanout must be in [1, 256] (got %d)", fanout);
+    *num_tiles_out = 0;
+    if (num_active == 0) return fill_i64(out_window_offset, 1, 0, stream);
+    GRWS_CHECK_ARG(active_windows && sampled_cols && sampled_slots, "window_topk: null pointer");
+    GRWS_TRY(check_hacs(A, hacs, "window_topk"));
+    const ScoreParams p = score_params(hacs);
+    // the flag word first, the rest for topk_enqueue
+    Carver cv(workspace, workspace_bytes);
+    int32_t* err = cv.take<int32_t>(64);
+    if (!cv.ok) return set_error(GRWS_E_CAPACITY, "window_topk: workspace too small");
+    GRWS_TRY(fill_i32(err, 1, 0, stream));
+    GRWS_TRY(topk_enqueue(A, active_windows, num_active, nullptr, S, p, sampled_cols, sampled_slots,
+                          out_window_offset, err, cv.base + cv.used, cv.cap - cv.used, stream));
     int64_t T = 0;
     int32_t e = 0;
     GRWS_HIP(hipMemcpyAsync(&T, out_window_offset + num_active, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
     GRWS_HIP(hipMemcpyAsync(&e, err, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
     GRWS_HIP(hipStreamSynchronize(stream));
-    if (e & kErrWindow) return set_error(GRWS_E_RANGE, "window_topk: an active window is outside the graph");
-    if (e & kErrHacs)
-        return set_error(GRWS_E_RANGE, "window_topk: a column has no static score or a part id has no range");
+    GRWS_TRY(report_topk_errors(e, "window_topk"));
     *num_tiles_out = T;
     return GRWS_OK;
 }
@@ -1097,25 +1220,226 @@ extern "C" int grws_window_recompress(const grws_bcsr* A, const int32_t* active_
         case GRWS_F32:
             hipLaunchKernelGGL(window_recompress_kernel<float>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
                                A->window_offset, A->num_windows, A->values, (int)A->tile_cols, active_windows,
-                               num_active, S,
+                               num_active, nullptr, S,
                                sampled_cols, sampled_slots, out_window_offset, out_cols,
                                static_cast<float*>(out_values));
             break;
         case GRWS_F16:
             hipLaunchKernelGGL(window_recompress_kernel<_Float16>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
                                A->window_offset, A->num_windows, A->values, (int)A->tile_cols, active_windows,
-                               num_active, S,
+                               num_active, nullptr, S,
                                sampled_cols, sampled_slots, out_window_offset, out_cols,
                                static_cast<_Float16*>(out_values));
             break;
         default:
             hipLaunchKernelGGL(window_recompress_kernel<uint16_t>, dim3((unsigned)num_active), dim3(kBlk), 0, stream,
                                A->window_offset, A->num_windows, A->values, (int)A->tile_cols, active_windows,
-                               num_active, S,
+                               num_active, nullptr, S,
                                sampled_cols, sampled_slots, out_window_offset, out_cols,
                                static_cast<uint16_t*>(out_values));
             break;
     }
     GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
+// --- every layer in one call: sampling_wrapper.cu:365-438 with one sync ---
+namespace {
+struct LayerBound {
+    int64_t ids;     // seed ids in (bound)
+    int64_t active;  // active windows (bound)
+    int64_t tiles;   // output tiles (bound)
+    int S;
+};
+
+int layer_bounds(const grws_bcsr* A, int64_t num_nodes, int64_t num_seeds, const int32_t* fanouts,
+                 int32_t num_layers, LayerBound* lb) {
+    const int64_t nw = (num_nodes + 15) / 16;
+    int64_t ids = num_seeds;
+    for (int32_t l = 0; l < num_layers; ++l) {
+        const int S = grws_window_sample_num(fanouts[l]);
+        GRWS_CHECK_ARG(fanouts[l] >= 1 && S <= kMaxCap, "window_sample_layers: fanout must be in [1, 256] (got %d)",
+                       fanouts[l]);
+        lb[l].ids = ids;
+        lb[l].active = ids < nw ? ids : nw;
+        lb[l].tiles = lb[l].active * (S / A->tile_cols);
+        lb[l].S = S;
+        ids = lb[l].tiles * A->tile_cols;
+    }
+    return GRWS_OK;
+}
+
+constexpr int32_t kMaxLayers = 64;
+
+template <typename C>
+void carve_layers(C& cv, int64_t nw, int32_t num_layers, const LayerBound* lb, int32_t** err, int64_t** cnt,
+                  uint32_t** dense, int32_t** flags, int64_t** rank, char** scan_ws, size_t* scan_bytes,
+                  int32_t** scols, int32_t** sslot) {
+    int64_t samp = 1;
+    for (int32_t l = 0; l < num_layers; ++l) samp = lb[l].active * lb[l].S > samp ? lb[l].active * lb[l].S : samp;
+    *err = cv.template take<int32_t>(64);
+    *cnt = cv.template take<int64_t>(2 * (size_t)num_layers);
+    *dense = cv.template take<uint32_t>((size_t)(nw > 0 ? nw : 1));
+    *flags = cv.template take<int32_t>((size_t)(nw > 0 ? nw : 1));
+    *rank = cv.template take<int64_t>((size_t)nw + 1);
+    *scan_bytes = scan_workspace_bytes(nw > 0 ? nw : 1);
+    *scan_ws = cv.template take<char>(*scan_bytes);
+    *scols = cv.template take<int32_t>((size_t)samp);
+    *sslot = cv.template take<int32_t>((size_t)samp);
+}
+}  // namespace
+
+extern "C" int grws_window_sample_layers_bounds(const grws_bcsr* A, int64_t num_nodes, int64_t num_seeds,
+                                                const int32_t* fanouts, int32_t num_layers, int64_t* max_active,
+                                                int64_t* max_tiles) {
+    clear_error();
+    GRWS_TRY(check_graph(A, "window_sample_layers"));
+    GRWS_CHECK_ARG(num_layers >= 1 && num_layers <= kMaxLayers, "window_sample_layers: 1..64 layers (got %d)",
+                   num_layers);
+    GRWS_CHECK_ARG(num_nodes >= 0 && num_seeds >= 0, "window_sample_layers: negative size");
+    GRWS_CHECK_ARG(fanouts && max_active && max_tiles, "window_sample_layers: null pointer");
+    LayerBound lb[kMaxLayers];
+    GRWS_TRY(layer_bounds(A, num_nodes, num_seeds, fanouts, num_layers, lb));
+    for (int32_t l = 0; l < num_layers; ++l) {
+        max_active[l] = lb[l].active;
+        max_tiles[l] = lb[l].tiles;
+    }
+    return GRWS_OK;
+}
+
+extern "C" size_t grws_window_sample_layers_workspace_bytes(const grws_bcsr* A, int64_t num_nodes,
+                                                            int64_t num_seeds, const int32_t* fanouts,
+                                                            int32_t num_layers) {
+    if (!A || !fanouts || num_layers < 1 || num_layers > kMaxLayers || num_nodes < 0 || num_seeds < 0) return 0;
+    if (A->tile_cols != 8 && A->tile_cols != 16) return 0;
+    LayerBound lb[kMaxLayers];
+    for (int32_t l = 0; l < num_layers; ++l)
+        if (fanouts[l] < 1 || grws_window_sample_num(fanouts[l]) > kMaxCap) return 0;
+    if (layer_bounds(A, num_nodes, num_seeds, fanouts, num_layers, lb) != GRWS_OK) return 0;
+    NullCarver nc;
+    int32_t *err, *flags, *scols, *sslot;
+    int64_t *cnt, *rank;
+    uint32_t* dense;
+    char* scan_ws;
+    size_t scan_bytes;
+    carve_layers(nc, (num_nodes + 15) / 16, num_layers, lb, &err, &cnt, &dense, &flags, &rank, &scan_ws, &scan_bytes,
+                 &scols, &sslot);
+    size_t topk = 0;
+    for (int32_t l = 0; l < num_layers; ++l) {
+        const size_t t = topk_fixed_bytes(lb[l].active > 0 ? lb[l].active : 1);
+        topk = t > topk ? t : topk;
+    }
+    return align_up(nc.s.used, 256) + topk + 256;
+}
+
+extern "C" int grws_window_sample_layers(const grws_bcsr* A, int64_t num_nodes, const int32_t* seeds,
+                                         int64_t num_seeds, const int32_t* fanouts, int32_t num_layers,
+                                         const grws_hacs* hacs, int64_t* const* window_offset,
+                                         int32_t* const* col_indices, void* const* values,
+                                         int32_t* const* active_windows, int32_t* const* masks, int64_t* counts,
+                                         float* phase_ms, void* workspace, size_t workspace_bytes, void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_TRY(check_graph(A, "window_sample_layers"));
+    GRWS_CHECK_ARG(num_layers >= 1 && num_layers <= kMaxLayers, "window_sample_layers: 1..64 layers (got %d)",
+                   num_layers);
+    GRWS_CHECK_ARG(num_nodes >= 0 && num_seeds >= 0 && num_seeds <= INT32_MAX, "window_sample_layers: bad size");
+    GRWS_CHECK_ARG(fanouts && counts && window_offset && col_indices && values && active_windows && masks,
+                   "window_sample_layers: null pointer");
+    GRWS_CHECK_ARG(num_seeds == 0 || seeds, "window_sample_layers: null seeds");
+    GRWS_TRY(check_hacs(A, hacs, "window_sample_layers"));
+    LayerBound lb[kMaxLayers];
+    GRWS_TRY(layer_bounds(A, num_nodes, num_seeds, fanouts, num_layers, lb));
+    for (int32_t l = 0; l < num_layers; ++l) {
+        GRWS_CHECK_ARG(lb[l].active <= INT32_MAX, "window_sample_layers: too many active windows in layer %d", l);
+        GRWS_CHECK_ARG(window_offset[l], "window_sample_layers: null window_offset[%d]", l);
+        if (lb[l].active > 0)
+            GRWS_CHECK_ARG(active_windows[l] && masks[l], "window_sample_layers: null outputs in layer %d", l);
+        if (lb[l].tiles > 0)
+            GRWS_CHECK_ARG(col_indices[l] && values[l], "window_sample_layers: null outputs in layer %d", l);
+    }
+    const ScoreParams p = score_params(hacs);
+    const int64_t nw = (num_nodes + 15) / 16;
+    Carver cv(workspace, workspace_bytes);
+    int32_t *err, *flags, *scols, *sslot;
+    int64_t *cnt, *rank;
+    uint32_t* dense;
+    char* scan_ws;
+    size_t scan_bytes;
+    carve_layers(cv, nw, num_layers, lb, &err, &cnt, &dense, &flags, &rank, &scan_ws, &scan_bytes, &scols, &sslot);
+    if (!cv.ok)
+        return set_error(GRWS_E_CAPACITY, "window_sample_layers: workspace too small (%zu < %zu)", workspace_bytes,
+                         cv.used);
+    char* const topk_ws = cv.base + align_up(cv.used, 256);
+    const size_t topk_bytes = workspace_bytes > align_up(cv.used, 256) ? workspace_bytes - align_up(cv.used, 256) : 0;
+    GRWS_TRY(fill_i32(err, 1, 0, stream));
+    GRWS_TRY(fill_i32(reinterpret_cast<int32_t*>(cnt), 4 * num_layers, 0, stream));
+    if (nw > 0) GRWS_TRY(fill_i32(reinterpret_cast<int32_t*>(dense), nw, 0, stream));
+    // phase events: before the top-K, between it and the recompression, after
+    hipEvent_t ev[3 * kMaxLayers] = {};
+    int nev = 0;
+    struct EventGuard {
+        hipEvent_t* ev;
+        int* n;
+        ~EventGuard() {
+            for (int i = 0; i < *n; ++i) (void)hipEventDestroy(ev[i]);
+        }
+    } guard{ev, &nev};
+    if (phase_ms) {
+        for (int i = 0; i < 3 * num_layers; ++i) {
+            GRWS_HIP(hipEventCreate(&ev[i]));
+            nev = i + 1;
+        }
+    }
+    for (int32_t l = 0; l < num_layers; ++l) {
+        const LayerBound& b = lb[l];
+        if (b.active == 0) {  // no seeds: an empty layer (and every later one)
+            GRWS_TRY(fill_i64(window_offset[l], 1, 0, stream));
+            if (phase_ms)
+                for (int k = 0; k < 3; ++k) GRWS_HIP(hipEventRecord(ev[3 * l + k], stream));
+            continue;
+        }
+        // the layer's seeds: the batch's, else the previous layer's sampled
+        // columns (-1 and columns past num_nodes dropped)
+        const unsigned sgrid = (unsigned)(grid_for(b.ids) < 4096 ? grid_for(b.ids) : 4096);
+        if (l == 0) {
+            hipLaunchKernelGGL(seeds_scatter_kernel, dim3(sgrid), dim3(kBlk), 0, stream, seeds, num_seeds, nullptr,
+                               (int64_t)1, num_nodes, 0, dense, err);
+        } else {
+            hipLaunchKernelGGL(seeds_scatter_kernel, dim3(sgrid), dim3(kBlk), 0, stream, col_indices[l - 1],
+                               (int64_t)0, window_offset[l - 1] + lb[l - 1].active, (int64_t)A->tile_cols, num_nodes,
+                               1, dense, err);
+        }
+        GRWS_LAUNCH_CHECK();
+        hipLaunchKernelGGL(seeds_flags_kernel, dim3(grid_for(nw)), dim3(kBlk), 0, stream, dense, nw, flags);
+        GRWS_LAUNCH_CHECK();
+        GRWS_TRY(scan_i32_to_i64(flags, rank, nw, false, scan_ws, scan_bytes, stream));
+        hipLaunchKernelGGL(seeds_dense_emit_kernel, dim3(grid_for(nw)), dim3(kBlk), 0, stream, dense, nw, rank,
+                           active_windows[l], masks[l]);
+        GRWS_LAUNCH_CHECK();
+        const int64_t* na_dev = rank + nw;
+        if (phase_ms) GRWS_HIP(hipEventRecord(ev[3 * l], stream));
+        GRWS_TRY(topk_enqueue(A, active_windows[l], b.active, na_dev, b.S, p, scols, sslot, window_offset[l], err,
+                              topk_ws, topk_bytes, stream));
+        if (phase_ms) GRWS_HIP(hipEventRecord(ev[3 * l + 1], stream));
+        if (b.tiles > 0)
+            GRWS_TRY(recompress_enqueue(A, active_windows[l], b.active, na_dev, b.S, scols, sslot, window_offset[l],
+                                        col_indices[l], values[l], stream));
+        if (phase_ms) GRWS_HIP(hipEventRecord(ev[3 * l + 2], stream));
+        hipLaunchKernelGGL(layer_counts_kernel, dim3(1), dim3(64), 0, stream, na_dev, window_offset[l] + b.active,
+                           cnt + 2 * l);
+        GRWS_LAUNCH_CHECK();
+    }
+    int32_t e = 0;
+    GRWS_HIP(hipMemcpyAsync(counts, cnt, sizeof(int64_t) * 2 * num_layers, hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipMemcpyAsync(&e, err, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+    GRWS_HIP(hipStreamSynchronize(stream));
+    GRWS_TRY(report_topk_errors(e, "window_sample_layers"));
+    if (phase_ms) {
+        for (int32_t l = 0; l < num_layers; ++l) {
+            GRWS_HIP(hipEventElapsedTime(&phase_ms[2 * l], ev[3 * l], ev[3 * l + 1]));
+            GRWS_HIP(hipEventElapsedTime(&phase_ms[2 * l + 1], ev[3 * l + 1], ev[3 * l + 2]));
+        }
+    }
     return GRWS_OK;
 }

@@ -597,10 +597,11 @@ int grws_window_seeds(const int32_t* ids, int64_t num_ids, int64_t num_nodes, in
 /* its input window), out_window_offset [num_active+1] int64; synchronises   */
 /* and returns the output tile count.  fanout in [1, 256].  A workspace     */
 /* larger than grws_window_topk_workspace_bytes(num_active) lends the rest   */
-/* to windows of more than 4,096 slots as key scratch (8 bytes per slot;   */
-/* grws_window_topk_key_scratch_bytes(A) covers every window of A): their   */
-/* keys are then computed once instead of once per selection pass.  The     */
-/* results do not depend on it.                                              */
+/* to windows of more than 1,024 slots as a chunk table and key scratch     */
+/* (8 bytes per slot; grws_window_topk_key_scratch_bytes(A) covers every    */
+/* window of A): their keys are then computed once, spread over many        */
+/* work-groups, instead of within the window's own work-group or once per   */
+/* selection pass.  The results do not depend on it.                         */
 size_t grws_window_topk_workspace_bytes(int64_t num_active);
 size_t grws_window_topk_key_scratch_bytes(const grws_bcsr* A);
 int grws_window_topk(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
@@ -617,6 +618,34 @@ int grws_window_recompress(const grws_bcsr* A, const int32_t* active_windows, in
                            int32_t fanout, const int32_t* sampled_cols,
                            const int32_t* sampled_slots, const int64_t* out_window_offset,
                            int64_t num_tiles, int32_t* out_cols, void* out_values, void* stream);
+
+/* Every layer of sample_all_layers (sampling_wrapper.cu:365-438) in one     */
+/* call with one synchronisation: layer l's seeds are the batch's (l = 0,   */
+/* ids outside [0, num_nodes) other than -1 are GRWS_E_RANGE) or layer      */
+/* l-1's sampled columns (-1 and ids past num_nodes dropped), its windows   */
+/* those of grws_window_seeds (tile_rows 16), its sample those of           */
+/* grws_window_topk and grws_window_recompress with fanouts[l]: the same    */
+/* results.  The outputs are caller buffers sized by the bounds query       */
+/* (layer l: window_offset [max_active+1], active_windows and masks         */
+/* [max_active], col_indices [max_tiles*tile_cols], values                  */
+/* [max_tiles*16*tile_cols] in A's values dtype); counts [2*num_layers]     */
+/* (host) receives each layer's active windows A and tiles T: the layer's  */
+/* arrays are the first A+1, A, A, T*tile_cols and T*16*tile_cols entries.  */
+/* phase_ms [2*num_layers] (host, or NULL) receives each layer's            */
+/* top-K and recompression times.  Workspace beyond                         */
+/* grws_window_sample_layers_workspace_bytes is key scratch as for          */
+/* grws_window_topk.  Replaces the per-layer calls' host syncs (two per     */
+/* layer) with one.                                                         */
+int grws_window_sample_layers_bounds(const grws_bcsr* A, int64_t num_nodes, int64_t num_seeds,
+                                     const int32_t* fanouts, int32_t num_layers, int64_t* max_active,
+                                     int64_t* max_tiles);
+size_t grws_window_sample_layers_workspace_bytes(const grws_bcsr* A, int64_t num_nodes, int64_t num_seeds,
+                                                 const int32_t* fanouts, int32_t num_layers);
+int grws_window_sample_layers(const grws_bcsr* A, int64_t num_nodes, const int32_t* seeds, int64_t num_seeds,
+                              const int32_t* fanouts, int32_t num_layers, const grws_hacs* hacs,
+                              int64_t* const* window_offset, int32_t* const* col_indices, void* const* values,
+                              int32_t* const* active_windows, int32_t* const* masks, int64_t* counts,
+                              float* phase_ms, void* workspace, size_t workspace_bytes, void* stream);
 
 size_t grws_relabel_workspace_bytes(int64_t num_frontier, int64_t num_edges);
 int grws_relabel(const int64_t* frontier, int64_t num_frontier, const int64_t* edge_src,

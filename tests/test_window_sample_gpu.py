@@ -158,10 +158,11 @@ def test_bcsr_sampler_layers(cuda_device):
 
 @pytest.mark.parametrize("scratch", [0, 300_000])
 def test_window_topk_hub_windows_without_key_scratch(cuda_device, monkeypatch, scratch):
-    """Windows of more than 4,096 slots keep their keys in the caller's
-    scratch when it has room and recompute them on every pass when it has
-    none (0 bytes) or runs out part-way (300 kB: some hub windows fit): the
-    same layers either way, bit for bit against the oracle."""
+    """Windows of more than 1,024 slots keep their keys in the caller's
+    scratch (computed by the keys kernel) when it has room, and compute them
+    in their own work-group (into LDS, or on every pass beyond 4,096 slots)
+    when it has none (0 bytes) or runs out part-way (300 kB: some of them
+    fit): the same layers either way, bit for bit against the oracle."""
     from graph_rws_amd.core import ops
     print(f"case window top-K key scratch {scratch}", flush=True)
     monkeypatch.setattr(ops, "WINDOW_KEY_SCRATCH", scratch)
@@ -172,3 +173,60 @@ def test_window_topk_hub_windows_without_key_scratch(cuda_device, monkeypatch, s
     ref = oracle.window_sample_all_layers(G.window_offset.cpu().numpy(), G.original_col_indices.cpu().numpy(),
                                           G.values_condensed.cpu().numpy(), seeds, [5, 10, 15], g.num_nodes)
     _compare(layers, ref)
+
+
+def _layers_equal(a, b):
+    assert len(a) == len(b)
+    for x, y in zip(a, b):
+        for u, v in zip(x, y):
+            assert u.dtype == v.dtype and u.shape == v.shape
+            assert torch.equal(u.cpu(), v.cpu())
+
+
+@pytest.mark.parametrize("case", ["c2", "c1_hacs", "no_seeds", "minus_one_and_repeats", "bf16_tc16"])
+def test_one_call_matches_the_per_layer_calls(cuda_device, case):
+    """sample_all_layers runs every layer in one grws_window_sample_layers
+    call (seeds from a dense per-window mask, device counts, one sync); the
+    per-layer entry points (grws_window_seeds' sort, a sync per call) give
+    the same layers bit for bit: full-size c2, HACS with locality, no seeds,
+    seeds of -1 and repeated ids, bf16 values in 16x16 tiles."""
+    from graph_rws_amd.core import ops
+    print(f"case one call vs per layer {case}", flush=True)
+    kw = {}
+    if case == "c2":
+        g, G = _graph("c2", cuda_device)
+        seeds = synth.distinct_seeds(g.num_nodes, 1024, seed=21).numpy()
+        fan = [5, 10, 15]
+    elif case == "c1_hacs":
+        g, G = _graph("c1", cuda_device)
+        rng = np.random.default_rng(8)
+        q = torch.from_numpy(rng.random(g.num_nodes).astype(np.float32)).to(cuda_device)
+        wpart = torch.from_numpy(rng.integers(-1, 3, G.num_windows).astype(np.int32)).to(cuda_device)
+        kw = dict(static_scores=q, window_part_ids=wpart,
+                  part_starts=torch.tensor([0, 900, 1800], dtype=torch.int32, device=cuda_device),
+                  part_ends=torch.tensor([900, 1800, 2708], dtype=torch.int32, device=cuda_device),
+                  use_hacs=1, locality_enabled=1, alpha=0.5, beta=3.0, delta=0.25, gamma_bonus=0.37,
+                  score_scale=250.0)
+        seeds = np.arange(1, g.num_nodes, 7)
+        fan = [12, 40, 3]
+    elif case == "no_seeds":
+        g, G = _graph("c1", cuda_device)
+        seeds = np.zeros(0, np.int64)
+        fan = [5, 10]
+    elif case == "minus_one_and_repeats":
+        g, G = _graph("c1", cuda_device)
+        seeds = np.array([-1, 7, 7, 8, -1, 2700, 16, 16, 15, 0, -1])
+        fan = [3, 33, 129]
+    else:
+        g, G = _graph("c1", cuda_device, tc=16, vdt=torch.bfloat16)
+        seeds = np.arange(0, g.num_nodes, 13)
+        fan = [20, 7]
+    args = (G.window_offset, G.original_col_indices, G.values_condensed,
+            torch.from_numpy(seeds).to(cuda_device), fan, g.num_nodes)
+    tc = G.tile_cols
+    one, t1 = sample_all_layers(*args, tile_cols=tc, **kw)
+    per, t2 = ops._sample_all_layers_per_layer(*args, tile_cols=tc, **kw)
+    _layers_equal(one, per)
+    assert len(t1) == len(fan) and all(t.total_time >= 0 for t in t1)
+    if case == "no_seeds":
+        assert all(int(x[0][-1]) == 0 and x[3].numel() == 0 for x in one)
