@@ -776,9 +776,9 @@ def _hacs_view(dev, static_scores, window_part_ids, part_starts, part_ends, alph
                       1, 1 if locality_enabled else 0)
 
 
-# Key scratch lent to grws_window_topk for windows of more than 4,096 slots
-# (their keys computed once instead of once per selection pass); results do
-# not depend on it
+# Key scratch lent to grws_window_topk for windows of more than 1,024 slots
+# (their keys computed once, by many work-groups, instead of in the window's
+# own work-group or once per selection pass); results do not depend on it
 WINDOW_KEY_SCRATCH = 64 << 20
 
 
@@ -900,7 +900,7 @@ def _sample_all_layers_per_layer(window_offset: torch.Tensor, original_col_indic
         scols = torch.empty(max(A * S, 1), dtype=torch.int32, device=dev)
         sslot = torch.empty(max(A * S, 1), dtype=torch.int32, device=dev)
         out_off = torch.empty(A + 1, dtype=torch.int64, device=dev)
-        # plus key scratch for the hub windows (more than 4,096 slots): at
+        # plus key scratch for the big windows (more than 1,024 slots): at
         # most the graph's slots, at most WINDOW_KEY_SCRATCH bytes
         wsb = int(L.load().grws_window_topk_workspace_bytes(A)) + min(
             int(L.load().grws_window_topk_key_scratch_bytes(ctypes.byref(view))), WINDOW_KEY_SCRATCH)

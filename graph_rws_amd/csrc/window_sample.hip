@@ -29,14 +29,16 @@
 //     column j (or -1) and its tile_rows values are that column's values in
 //     the input window (or 0), :520-578.
 //
-// Design: one 1,024-thread work-group per active window.  The 64-bit key
-// (~total << 32 | column) orders candidates exactly as the reference's
-// comparator; an MSB-first 8-bit radix select over the window's slots (keys
-// kept in LDS for windows of up to 4,096 slots, recomputed from the values on
-// every pass for larger ones; passes start at the first byte where the
-// candidates' keys differ) finds the CAP-th key, the selected (column, slot)
-// pairs are compacted into LDS and bitonic-sorted by column.  The slot index replaces the reference's linear
-// column search when the tiles are rebuilt.
+// Design: one work-group per active window (256 threads up to 1,024 slots,
+// 1,024 threads beyond, those windows' keys computed beforehand by many
+// work-groups).  The 64-bit key (~total << 32 | column) orders candidates
+// exactly as the reference's comparator; up to 1,024 candidates are ranked
+// directly, more go through an MSB-first 8-bit radix select (passes start at
+// the first byte where the candidates' keys differ) that finds the CAP-th
+// key, and the selected (column, slot) pairs are compacted into LDS and
+// bitonic-sorted by column.  The slot index replaces the reference's linear
+// column search when the tiles are rebuilt.  Every layer of a batch can run
+// in one call (grws_window_sample_layers) on device counts, with one sync.
 #include "grws_internal.h"
 
 namespace grws {
