@@ -230,3 +230,27 @@ def test_one_call_matches_the_per_layer_calls(cuda_device, case):
     assert len(t1) == len(fan) and all(t.total_time >= 0 for t in t1)
     if case == "no_seeds":
         assert all(int(x[0][-1]) == 0 and x[3].numel() == 0 for x in one)
+
+
+@pytest.mark.parametrize("path", ["one_call", "per_layer"])
+def test_hacs_score_table_too_short_is_an_error(cuda_device, path):
+    """A candidate column without a static score is GRWS_E_RANGE, whether
+    its window is ranked by the small kernel or its keys come from the keys
+    kernel (c2's windows of more than 1,024 slots), on both paths; the
+    reference would read past the table."""
+    from graph_rws_amd.core import ops
+    print(f"case HACS short score table {path}", flush=True)
+    g, G = _graph("c2", cuda_device)
+    fn = sample_all_layers if path == "one_call" else ops._sample_all_layers_per_layer
+    seeds = torch.arange(0, g.num_nodes, 97, device=cuda_device)
+    short = torch.rand(g.num_nodes // 2, device=cuda_device)
+    with pytest.raises(GrwsError, match="static score"):
+        fn(G.window_offset, G.original_col_indices, G.values_condensed, seeds, [5, 10], g.num_nodes,
+           static_scores=short, use_hacs=1)
+    # a full table is fine, and both paths agree on it
+    full = torch.rand(g.num_nodes, device=cuda_device)
+    a, _ = sample_all_layers(G.window_offset, G.original_col_indices, G.values_condensed, seeds, [5, 10],
+                             g.num_nodes, static_scores=full, use_hacs=1)
+    b, _ = ops._sample_all_layers_per_layer(G.window_offset, G.original_col_indices, G.values_condensed, seeds,
+                                            [5, 10], g.num_nodes, static_scores=full, use_hacs=1)
+    _layers_equal(a, b)
