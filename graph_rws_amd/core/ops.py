@@ -790,7 +790,8 @@ def sample_all_layers(window_offset: torch.Tensor, original_col_indices: torch.T
                       part_ends: Optional[torch.Tensor] = None, alpha: float = 1.0,
                       beta: float = 10.0, delta: float = 0.0, gamma_bonus: float = 0.0,
                       score_scale: float = 100.0, use_hacs: int = 0, locality_enabled: int = 0,
-                      tile_rows: int = 16, tile_cols: int = 8, warps_per_block: int = 8):
+                      tile_rows: int = 16, tile_cols: int = 8, warps_per_block: int = 8,
+                      with_timings: bool = True):
     """Drop-in for core_lib.sample_all_layers (bind.cpp:99-121 ->
     sampling_wrapper.cu:365-438).  Returns (layers, timings): per fanout, in
     the order given, [out_window_offset int64, out_col_indices int32 (global
@@ -799,7 +800,9 @@ def sample_all_layers(window_offset: torch.Tensor, original_col_indices: torch.T
     views of buffers sized by the layers' bounds); values keep
     values_condensed's dtype.  warps_per_block is validated as the reference
     does (4 or 8) and has no effect on the result.  Every layer runs in one
-    grws_window_sample_layers call: one host sync for the batch."""
+    grws_window_sample_layers call: one host sync for the batch.
+    with_timings=False (not in the reference) skips the phase timing events,
+    which cost ~45 us of a c2 batch, and returns zero timings."""
     if tile_rows != 16 or tile_cols not in (8, 16):
         raise RuntimeError("sample_all_layers supports 16x8 tiles (the reference's) and 16x16")
     if warps_per_block not in (4, 8):
@@ -847,7 +850,7 @@ def sample_all_layers(window_offset: torch.Tensor, original_col_indices: torch.T
     phase = (ctypes.c_float * (2 * nl))()
     L.call("grws_window_sample_layers", ctypes.byref(view), n_nodes, L.ptr(seeds), seeds.numel(), fan, nl,
            ctypes.byref(hv) if hv is not None else None, ptrs[0], ptrs[1], ptrs[2], ptrs[3], ptrs[4], counts,
-           phase, L.ptr(ws), wsb, L.stream_of(dev))
+           phase if with_timings else None, L.ptr(ws), wsb, L.stream_of(dev))
     layers, timings = [], []
     for i, (off, cols, vals, act, msk) in enumerate(bufs):
         A, T = int(counts[2 * i]), int(counts[2 * i + 1])

@@ -73,7 +73,7 @@ class BCSRSampler:
             g.window_offset, g.original_col_indices, g.values_condensed, seeds,
             list(reversed(self.fanouts)), int(g.num_nodes), ss, wp, ps, pe, self.alpha, self.beta,
             self.delta, self.gamma_bonus, self.score_scale, use_hacs, loc, self.tile_rows,
-            self.tile_cols, self.warps_per_block)
+            self.tile_cols, self.warps_per_block, with_timings=self.verbose)
         if self.verbose:
             n = len(self.fanouts)
             for i, t in enumerate(timings):
