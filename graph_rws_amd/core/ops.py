@@ -69,6 +69,13 @@ class spmm_tuning:
         return False
 
 
+def grouped_slab_pairs() -> bool:
+    """Whether 4-window grouped products multiply slab pairs on the
+    16x16x32 MFMA (spmm_grp2_kernel, the default) rather than single slabs
+    (GRWS_GRP_K32=0)."""
+    return int(L.load().grws_spmm_get_tuning(b"GRWS_GRP_K32")) != 0
+
+
 def default_slabs(num_windows: int, num_tiles: int, tile_cols: int, n_cols: int) -> int:
     return int(L.load().grws_spmm_default_slabs(num_windows, num_tiles, tile_cols, n_cols))
 
@@ -322,7 +329,8 @@ def group_size_for(n_cols: int) -> int:
     measured on c3 (f16): N = 256 2.16 against 2.25 ms with two windows,
     N = 608 5.29 against 5.39 ms (320-column chunks, one window per wave);
     the saved intra-community gathers outweigh the added sub-tile headers.
-    Eight ran slower at N = 608 (8.21 ms, two windows per wave)."""
+    Eight ran slower at N = 608 (8.21 ms, two windows per wave).  Four-window
+    groups multiply slab pairs on the 16x16x32 MFMA (N = 608 5.14 ms)."""
     if GROUP_SIZE:
         return int(GROUP_SIZE)
     return 4

@@ -54,11 +54,13 @@ enum TuneKey {
     kTuneGrpWpw,   // GRWS_GRP_WPW: windows per wave of the grouped kernel
     kTuneGrpNblk,  // GRWS_GRP_NBLK: column blocks of the grouped kernel's first launch
     kTuneGrpC320,  // GRWS_GRP_C320: 0 = no 320-column grouped chunks
+    kTuneGrpK32,   // GRWS_GRP_K32: 0 = 4-window groups on the 16x16x16 kernel, not slab pairs
     kTuneCount
 };
 const char* const kTuneNames[kTuneCount] = {"GRWS_SPMM_NBLK",   "GRWS_SPMM_WAVES",  "GRWS_SPMM_KERNEL",
                                             "GRWS_SPMM_ORDER",  "GRWS_SPMM_NARROW", "GRWS_SPMM_C320",
-                                            "GRWS_GRP_WPW",     "GRWS_GRP_NBLK",    "GRWS_GRP_C320"};
+                                            "GRWS_GRP_WPW",     "GRWS_GRP_NBLK",    "GRWS_GRP_C320",
+                                            "GRWS_GRP_K32"};
 std::atomic<int> g_tune[kTuneCount];
 struct TuneInit {
     TuneInit() {
@@ -1070,6 +1072,220 @@ __global__ __launch_bounds__(64 * GW) void spmm_grp_kernel(SpmmArgs a) {
     }
 }
 
+// Grouped tiles of 4 windows, slabs taken in pairs: v_mfma_f32_16x16x32
+// issues at the rate of v_mfma_f32_16x16x16 on gfx950 (measured: 110G
+// instructions/s either way, 1.7-1.8 against 0.92 PFLOP/s f16), so one
+// instruction multiplies two consecutive slabs of the same layout.  Four
+// waves per group, one window each.  Per pair p the waves gather its 32 X
+// rows into LDS: slab 2p into stage rows 0..15, slab 2p + 1 into 16..31,
+// wave h the rows 4h..4h+3 of each slab (lane l the row of slab half
+// l / 32 at position 4h + (l / 8) % 4, 8 lanes per 128-byte segment, one
+// gather instruction per 64 columns); one barrier; then per 16-column
+// block two transposing LDS reads (stage rows 8g..8g+3 and 8g+4..8g+7 for
+// lane group g) make the B operand of one MFMA.  Lane (g, r) of the A
+// operand holds row r, columns 8 (g & 1) .. + 7 of slab 2p + g / 2: two
+// nibbles of that slab's row-group mask, each decoded as the 4-slot runs of
+// the packed tiles.  A group with an odd slab count ends with half a pair:
+// the missing slab's headers read as empty (range check) and its X rows
+// as the zero row.  Double-buffered stage, one barrier per pair (a buffer
+// is written again two pairs later, after every wave passed the barrier in
+// between).  The sums take each row's columns in ascending order, 32 per
+// MFMA step.
+template <int XT, int NBLK>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NBLK == 20 ? 3 : 1, 8))) void spmm_grp2_kernel(
+    SpmmArgs a) {
+    static_assert(XT == GRWS_F16 || XT == GRWS_BF16, "grouped tiles: 16-bit X and values");
+    static_assert(NBLK == 8 || NBLK == 16 || NBLK == 20, "column blocks per chunk");
+    constexpr int G = 4;
+    constexpr int NC = NBLK * 16;
+    constexpr int NLD = NC / 64;  // gather instructions per wave and pair
+    constexpr int PITCH = NC + 16;
+    using S = typename XTraits<XT>::S;
+    typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+    typedef short short8_t __attribute__((ext_vector_type(8)));
+    typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+    __shared__ __attribute__((aligned(16))) S stage_all[2 * 32 * PITCH];
+
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    // chunk-major: every XCD walks chunk 0's groups (its own range), then chunk 1's
+    const int64_t ipc = (a.num_items + 7) & ~(int64_t)7;
+    const int chunk = (int)(blockIdx.x / ipc);
+    const int64_t rr = (int64_t)blockIdx.x - (int64_t)chunk * ipc;
+    const int64_t q = (rr & 7) * (ipc >> 3) + (rr >> 3);
+    if (chunk >= a.nchunks || q >= a.num_items) return;  // uniform over the work-group
+    const int64_t g0 = a.goff[q];
+    const int64_t nslabs = a.goff[q + 1] - g0;
+    const int64_t npairs = (nslabs + 1) >> 1;
+    const int64_t n0 = a.col_base + (int64_t)chunk * NC;
+
+    const __amdgpu_buffer_rsrc_t rsC = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.cols + g0 * 16), (short)0, (int)(nslabs * 64), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsH = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.hdr + g0 * G * 12), (short)0, (int)(nslabs * G * 48), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsV =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.pvals), (short)0, (int)a.pv_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsX =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.x), (short)0, (int)a.x_bytes, 0x00020000);
+
+    // the lane's gathered row: slab half hx of the pair, position 4 wave + r4
+    // in that slab, staged row srow; gather instruction i reads its columns
+    // 64 i + 8 (lane % 8) .. + 7 of the chunk
+    const int hx = lane >> 5, r4 = (lane >> 3) & 3;
+    const int srow = 16 * hx + 4 * wave + r4;
+    const uint32_t col_off = (uint32_t)(4 * wave + r4) * 4;
+    bool lcol[NLD];
+    uint32_t colb[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        const int64_t e = n0 + 64 * i + 8 * (lane & 7);
+        lcol[i] = e < a.n_cols;
+        colb[i] = lcol[i] ? (uint32_t)(e * 2) : 0u;
+    }
+    const uint32_t ldxb = (uint32_t)(a.ldx * 2);
+    const uint32_t xr = (uint32_t)a.x_rows;
+    const int ag = lane >> 4;
+    const int ar = lane & 15;
+    const int tr0 = (8 * ag + (ar >> 2)) * PITCH + 4 * (ar & 3);
+    const int tr1 = tr0 + 4 * PITCH;
+    const int ha = ag >> 1;  // the slab of the pair the lane's A operand comes from
+    const uint32_t bitoff = (uint32_t)((ar & 3) * 16 + 8 * (ag & 1));
+    const uint32_t hword = (uint32_t)(3 * (ar >> 2) + ((lane & 3) < 2 ? (lane & 3) : 2)) * 4;
+
+    // column index of the lane's row in pair p; -1 (the zero row) for the
+    // missing slab of a group's last pair
+    auto load_col = [&](int64_t p) -> int32_t {
+        const int64_t sl = 2 * p + hx;
+        const int32_t c =
+            (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rsC, (int)((uint32_t)(sl * 64) + col_off), 0, kAPolicy);
+        return sl < nslabs ? c : -1;
+    };
+    auto load_x = [&](const int32_t c, u32x4_t* regs) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            const bool ok = lcol[i] && (uint32_t)c < xr;
+            const uint32_t row = ok ? (uint32_t)c : xr;  // row x_rows lies past the resource
+            regs[i] = __builtin_amdgcn_raw_buffer_load_b128(rsX, (int)(__umul24(row, ldxb) + colb[i]), 0, 0);
+        }
+    };
+    // the window's 48-byte sub-tile header in slab 2p + ha: the first three
+    // lanes of each quad load the row group's {mask_lo, mask_hi, start}, one
+    // word each, broadcast over the quad by DPP quad permutes (a quad shares
+    // its row group and its slab); past the group the range check reads 0
+    auto load_hdr = [&](int64_t p) -> uint32_t {
+        return __builtin_amdgcn_raw_buffer_load_b32(
+            rsH, (int)((uint32_t)(((2 * p + ha) * G + wave) * 48) + hword), 0, kAPolicy);
+    };
+    auto lane_hdr = [&](const uint32_t raw) -> u32x3_t {
+        return u32x3_t{(uint32_t)__builtin_amdgcn_mov_dpp((int)raw, 0x00, 0xf, 0xf, false),
+                       (uint32_t)__builtin_amdgcn_mov_dpp((int)raw, 0x55, 0xf, 0xf, false),
+                       (uint32_t)__builtin_amdgcn_mov_dpp((int)raw, 0xaa, 0xf, 0xf, false)};
+    };
+    // the lane's 8 slots as two 4-slot runs: 12-byte reads from the even
+    // value index at or below each run's first value, with the run's mask
+    // nibble and the odd-start flag beside them (an empty run reads nothing)
+    auto load_a = [&](const u32x3_t h, u32x4_t* out) {
+        const uint64_t m = ((uint64_t)h[1] << 32) | h[0];
+        const uint32_t below = (uint32_t)__builtin_popcountll(m & ((1ull << bitoff) - 1));
+        const uint32_t byte = (uint32_t)(m >> bitoff) & 255u;
+        const uint32_t nib0 = byte & 15u, nib1 = byte >> 4;
+        const uint32_t i0 = h[2] + below;
+        const uint32_t i1 = i0 + (uint32_t)__builtin_popcount(nib0);
+        const uint32_t off0 = nib0 ? (i0 & ~1u) * 2u : 0x80000000u;
+        const uint32_t off1 = nib1 ? (i1 & ~1u) * 2u : 0x80000000u;
+        const u32x3_t d0 = __builtin_amdgcn_raw_buffer_load_b96(rsV, (int)off0, 0, kAPolicy);
+        const u32x3_t d1 = __builtin_amdgcn_raw_buffer_load_b96(rsV, (int)off1, 0, kAPolicy);
+        out[0] = u32x4_t{d0[0], d0[1], d0[2], nib0 | ((i0 & 1u) << 4)};
+        out[1] = u32x4_t{d1[0], d1[1], d1[2], nib1 | ((i1 & 1u) << 4)};
+    };
+    auto decode = [&](const u32x4_t v) -> short4_t {
+        const uint32_t info = v[3];
+        const uint32_t sh = (info >> 4) * 16u;
+        const uint32_t r0 = __builtin_amdgcn_alignbit(v[1], v[0], sh);
+        const uint32_t r1 = __builtin_amdgcn_alignbit(v[2], v[1], sh);
+        const uint32_t b0 = info & 1u, b1 = (info >> 1) & 1u, b2 = (info >> 2) & 1u, b3 = (info >> 3) & 1u;
+        const uint32_t k2 = b0 + b1, k3 = k2 + b2;
+        const uint32_t s0 = b0 ? 0x0100u : 0x0c0cu;
+        const uint32_t s1 = b1 ? 0x0100u + 0x0202u * b0 : 0x0c0cu;
+        const uint32_t s2 = b2 ? 0x0100u + 0x0202u * k2 : 0x0c0cu;
+        const uint32_t s3 = b3 ? 0x0100u + 0x0202u * k3 : 0x0c0cu;
+        return __builtin_bit_cast(short4_t, u32x2_t{__builtin_amdgcn_perm(r1, r0, s0 | (s1 << 16)),
+                                                    __builtin_amdgcn_perm(r1, r0, s2 | (s3 << 16))});
+    };
+
+    float4_t acc[NBLK];
+#pragma unroll
+    for (int b = 0; b < NBLK; ++b) acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // pair p's X rows into stage buffer p & 1 (they were loaded one step
+    // before); the caller issues the next pair's gathers into the same
+    // registers before the barrier, so they fly during this pair's MFMAs
+    auto stage_x = [&](int buf, const u32x4_t* xb) {
+        S* st = stage_all + buf * (32 * PITCH);
+#pragma unroll
+        for (int i = 0; i < NLD; ++i)
+            *reinterpret_cast<u32x4_t*>(&st[srow * PITCH + 64 * i + 8 * (lane & 7)]) = xb[i];
+    };
+    auto multiply = [&](int buf, const u32x4_t* av) {
+        S* st = stage_all + buf * (32 * PITCH);
+        const short8_t af = __builtin_shufflevector(decode(av[0]), decode(av[1]), 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+        for (int b = 0; b < NBLK; ++b) {
+            lds_ptr_t p0 = (lds_ptr_t)(st + tr0 + 16 * b);
+            lds_ptr_t p1 = (lds_ptr_t)(st + tr1 + 16 * b);
+            if constexpr (XT == GRWS_F16) {
+                const half4_t lo =
+                    __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4f16_t*)p0));
+                const half4_t hi =
+                    __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4f16_t*)p1));
+                const half8_t bf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, af), bf, acc[b], 0, 0, 0);
+            } else {
+                const short4_t lo =
+                    __builtin_bit_cast(short4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf16_t*)p0));
+                const short4_t hi =
+                    __builtin_bit_cast(short4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf16_t*)p1));
+                const short8_t bf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, af),
+                                                                 __builtin_bit_cast(bf16x8_t, bf), acc[b], 0, 0, 0);
+            }
+        }
+    };
+
+    if (npairs > 0 && xr > 0) {  // uniform over the work-group
+        // X rows and A values one pair ahead of the pair multiplied (one X
+        // register set, two A sets), the column indices and headers they
+        // depend on two pairs ahead (ring of 2)
+        u32x4_t xbuf[NLD];
+        u32x4_t abuf[2][2];
+        int32_t cring[2];
+        uint32_t hring[2];
+        cring[0] = load_col(0);
+        hring[0] = load_hdr(0);
+        load_x(cring[0], xbuf);
+        load_a(lane_hdr(hring[0]), abuf[0]);
+        cring[1] = load_col(1);
+        hring[1] = load_hdr(1);
+        auto step = [&](const int u, const int64_t p) {  // u = p mod 2
+            stage_x(u, xbuf);
+            cring[u] = load_col(p + 2);
+            hring[u] = load_hdr(p + 2);
+            load_x(cring[u ^ 1], xbuf);
+            load_a(lane_hdr(hring[u ^ 1]), abuf[u ^ 1]);
+            __syncthreads();
+            multiply(u, abuf[u]);
+        };
+        int64_t p = 0;
+        for (; p + 1 < npairs; p += 2) {
+            step(0, p);
+            step(1, p + 1);
+        }
+        if (p < npairs) step(0, p);
+    }
+    const int64_t win = q * G + wave;
+    if (win < a.num_windows) spmm_epilogue<XT, NBLK, 1>(a, acc, stage_all, 0, lane, win, -1, chunk, n0);
+}
+
 // Sums the partial slots of each split window in slot order (deterministic).
 // One wave per 256 floats of a (split window, chunk) block: NBLK waves per
 // block, lane l owns 4 consecutive floats (one row, 4 columns).  A hub
@@ -1711,9 +1927,26 @@ int launch_grp(const SpmmArgs& a, hipStream_t stream) {
 // column blocks per chunk.  With four waves and NBLK 20 each wave's 20 row
 // segments take three gather instructions (the last repeats four); WPW 4
 // keeps to NBLK 8 (128 accumulator registers).
+template <int XT, int NBLK>
+int launch_grp2(const SpmmArgs& a, hipStream_t stream) {
+    const int64_t ipc = (a.num_items + 7) & ~(int64_t)7;
+    const int64_t grid = ipc * a.nchunks;
+    if (grid <= 0) return GRWS_OK;
+    if (grid > INT32_MAX) return set_error(GRWS_E_INVALID, "spmm_grouped: grid too large");
+    hipLaunchKernelGGL((spmm_grp2_kernel<XT, NBLK>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
 template <int XT>
 int dispatch_grp(const SpmmArgs& a, int G, int wpw, int nblk, hipStream_t stream) {
     const int gw = G / wpw;
+    // 4 windows, one per wave: slab pairs on the 16x16x32 MFMA
+    if (G == 4 && wpw == 1 && tune(kTuneGrpK32) != 0) {
+        if (nblk == 20) return launch_grp2<XT, 20>(a, stream);
+        if (nblk == 16) return launch_grp2<XT, 16>(a, stream);
+        if (nblk == 8) return launch_grp2<XT, 8>(a, stream);
+    }
 #define GRWS_GRP(W_, GW_, NB_) \
     if (wpw == W_ && gw == GW_ && nblk == NB_) return launch_grp<XT, NB_, W_, GW_>(a, stream)
     GRWS_GRP(1, 2, 8); GRWS_GRP(1, 2, 16); GRWS_GRP(1, 2, 20);

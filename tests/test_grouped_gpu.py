@@ -11,7 +11,10 @@ Checks:
     (windows per wave 1, 2, 4; waves per group 1, 2, 4; 128-, 256- and
     320-column chunks and the narrower last launch), with the residual, and
     on a partial last group; it stays within one rounding of the output
-    dtype of the window-by-window kernel.
+    dtype of the window-by-window kernel;
+  * 4-window groups multiply slab pairs on the 16x16x32 MFMA by default:
+    against the oracle and the 16x16x16 kernel, with groups of odd slab
+    counts (half a pair at the end).
 """
 
 import numpy as np
@@ -163,6 +166,39 @@ def test_grouped_spmm_meets_oracle(cuda_device, monkeypatch, G, wpw, nblk, N):
     Yw = ops.spmm(A.window_offset, A.original_col_indices, A.values_condensed, X, 16)
     # one rounding of fp16 apart at most: the sums differ only in fp32 order
     torch.testing.assert_close(Y.float(), Yw.float(), rtol=2 ** -10, atol=2 ** -14)
+
+
+@pytest.mark.parametrize("vdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N", [608, 256, 96, 48])
+@pytest.mark.parametrize("cfg,scale", [("c3", 0.004), ("c4", 0.002)])
+def test_grouped_slab_pairs_match_single_slabs(cuda_device, monkeypatch, vdt, N, cfg, scale):
+    """4-window groups run slab pairs on the 16x16x32 MFMA by default
+    (spmm_grp2_kernel; GRWS_GRP_K32=0 selects the 16x16x16 kernel): both
+    meet the oracle in both tiers and stay within one output rounding of
+    each other (the same exact sums in another fp32 order).  A group of an
+    odd slab count ends with half a pair: the small c3-shaped graph is
+    nearly dense (every group 59 slabs), the sparse c4-shaped one has
+    groups of both parities."""
+    print(f"case grouped slab pairs {cfg} {vdt} N={N}", flush=True)
+    monkeypatch.setattr(ops, "GROUP_MIN_N", 0)
+    _, A = _graph(cuda_device, vdt, 16, scale=scale, cfg=cfg)
+    gt = ops.group_tiles(A.window_offset, A.original_col_indices, A.values_condensed, 16, A.num_cols,
+                         group_size=4, max_ratio=10.0, max_skew=1e9)
+    slabs = (gt.group_offset[1:] - gt.group_offset[:-1]).cpu()
+    assert bool((slabs % 2 == 1).any())
+    if cfg == "c4":
+        assert bool((slabs % 2 == 0).any())
+    torch.manual_seed(N + 17)
+    X = torch.randn(A.num_cols, N, device=cuda_device).to(vdt)
+    assert int(ops.L.load().grws_spmm_get_tuning(b"GRWS_GRP_K32")) == -1  # the default: slab pairs
+    Y2 = ops.spmm(A.window_offset, A.original_col_indices, A.values_condensed, X, 16, grouped=gt)
+    with ops.spmm_tuning(GRWS_GRP_K32=0):
+        Y1 = ops.spmm(A.window_offset, A.original_col_indices, A.values_condensed, X, 16, grouped=gt)
+    torch.cuda.synchronize()
+    _oracle_check(A, X, Y2)
+    _oracle_check(A, X, Y1)
+    u = 2 ** -10 if vdt == torch.float16 else 2 ** -7
+    torch.testing.assert_close(Y2.float(), Y1.float(), rtol=u, atol=2 ** -14)
 
 
 @pytest.mark.parametrize("vdt", [torch.float16, torch.bfloat16])
