@@ -7,8 +7,9 @@
 //     (16 column slots); one or two wave64s share it, splitting its slabs;
 //   * the 16 X rows a slab references are gathered with 16-byte loads
 //     (coalesced row segments), staged in LDS, and fed to CDNA4 MFMA:
-//     v_mfma_f32_16x16x16_{f16,bf16} for 16-bit inputs, v_mfma_f32_16x16x4_f32
-//     for fp32; fp32 accumulation in registers;
+//     v_mfma_f32_16x16x16_{f16,bf16} for 16-bit inputs (16x16x32 over slab
+//     pairs for grouped tiles of 4 windows), v_mfma_f32_16x16x4_f32 for fp32;
+//     fp32 accumulation in registers;
 //   * a ring of register buffers keeps the next slab's gathers, A values and
 //     the column indices beyond them in flight while a slab is multiplied;
 //     loads are branch-free (clamped address, result masked when consumed)
