@@ -7,9 +7,9 @@ over every row), through the same calls bench.py times.
   product, the 4-window grouped second product and the packed-tile product
   (bit-identical to the dense one); the epoch widths N=256 (window by
   window, then 4-window groups) and N=41 (ragged); A^T G at N=256 (first
-  product window by window, second on 4-window groups).  Every grouped
-  product is also compared with the window-by-window one over the whole
-  output.
+  product window by window, second on 4-window groups); the same graph in
+  bf16 at N=256 (the bf16 slab-pair kernel).  Every grouped product is also
+  compared with the window-by-window one over the whole output.
 * c4 (2,449,029 nodes, 123.7M nnz, bf16): N=112 at a 128-element pitch,
   N=256 (two 128-column chunks), N=47 (ragged); A^T G at N=256.
 * c2 (169,343 nodes, 2.33M nnz): A^T G at N=128 in f16 and bf16 through the
@@ -116,17 +116,19 @@ def _record_grouped(monkeypatch):
 
 def _compare_orders(G, hg, X, Ya_x, Yg, Yw):
     """The grouped product Yg against the window-by-window product Yw over
-    every output element: both round the same exact sum once to f16 after
-    fp32 accumulations in different orders, so they differ by at most
-    u_out (|Yg| + |Yw|) + 2 C k 2^-24 (|A||X|) (+ subnormal and flush
-    terms), with |A||X| from the device product of A and |X| (A >= 0 on
-    these graphs)."""
-    from _fullsize import C_SUM_16, FTZ, S_OUT, U32, U_OUT, all_row_nnz
+    every output element: both round the same exact sum once to the output
+    type (f16 or bf16) after fp32 accumulations in different orders, so they
+    differ by at most u_out (|Yg| + |Yw|) + 2 C k 2^-24 (|A||X|) (+ subnormal
+    and flush terms), with |A||X| from the device product of A and |X|
+    (A >= 0 on these graphs; Ya_x is rounded to the output type, hence the
+    factor 1 + 4 u_out on it)."""
+    from _fullsize import C_SUM_16, DT, FTZ, S_OUT, U32, U_OUT, all_row_nnz
+    dt = DT[Yg.dtype]
     k = torch.from_numpy(all_row_nnz(hg)).to(Yg.device, torch.float32)[:, None]
-    ya = Ya_x.float() * (1 + 2 ** -9)
+    ya = Ya_x.float() * (1 + 4 * U_OUT[dt])
     d = (Yg.float() - Yw.float()).abs()
-    bound = (U_OUT["f16"] * (Yg.float().abs() + Yw.float().abs()) + 2 * C_SUM_16 * U32 * k * ya
-             + 2 * (k * FTZ + S_OUT["f16"]))
+    bound = (U_OUT[dt] * (Yg.float().abs() + Yw.float().abs()) + 2 * C_SUM_16 * U32 * k * ya
+             + 2 * (k * FTZ + S_OUT[dt]))
     bad = d > bound
     assert not bool(bad.any()), f"grouped vs window by window: {int(bad.sum())} of {bad.numel()} apart"
     return float((d / bound).max())
@@ -191,6 +193,32 @@ def test_c3_transpose_n256(c3, cuda_device, monkeypatch):
     hgT = HostGraph(AT)
     print(check_transpose(hg, hgT, Gout, out2, RTOL, planT=AT.spmm_plan(256), seed=5), flush=True)
     print(check_transpose(hg, hgT, Gout, out1, RTOL, planT=AT.spmm_plan(256), seed=6), flush=True)
+
+
+def test_c3_bf16_n256_slab_pairs(c3, cuda_device, monkeypatch):
+    """The c3 graph with bf16 values and X (the 16-bit type c4 is configured
+    in) at N=256: the second product runs the 4-window grouped tiles on the
+    bf16 slab-pair kernel (v_mfma_f32_16x16x32_bf16); against the oracle in
+    both tiers and against the window-by-window product over the whole
+    output (semantics: /root/reference/core/include/spmm_tc.cuh:113-193)."""
+    from graph_rws_amd.core import ops
+    print("case c3 N=256 bf16, 4-window groups on slab pairs", flush=True)
+    g, G16, _ = c3
+    G = G16.with_values_dtype(torch.bfloat16)
+    hg = HostGraph(G)
+    X = synth.features(g.num_nodes, 256, seed=612, device=cuda_device).to(torch.bfloat16)
+    calls = _record_grouped(monkeypatch)
+    G.spmm(X)
+    Y2 = G.spmm(X)
+    torch.cuda.synchronize()
+    assert ("grws_spmm_grouped", 4) in calls, calls
+    assert ops.grouped_slab_pairs(), "4-window groups run slab pairs by default"
+    print(check_forward(hg, X, Y2, RTOL, plan=G.spmm_plan(256), seed=612), flush=True)
+    monkeypatch.setattr(ops, "GROUPED", False)
+    Yw = G.spmm(X)
+    Ya = G.spmm(X.abs())
+    torch.cuda.synchronize()
+    print("grouped vs window by window, worst of bound:", _compare_orders(G, hg, X, Ya, Y2, Yw), flush=True)
 
 
 def test_c4_bench_path_n112(c4, cuda_device):
