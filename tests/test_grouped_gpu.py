@@ -170,19 +170,20 @@ def test_grouped_spmm_meets_oracle(cuda_device, monkeypatch, G, wpw, nblk, N):
 
 @pytest.mark.parametrize("vdt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("N", [608, 256, 96, 48])
-@pytest.mark.parametrize("cfg,scale", [("c3", 0.004), ("c4", 0.002)])
-def test_grouped_slab_pairs_match_single_slabs(cuda_device, monkeypatch, vdt, N, cfg, scale):
+@pytest.mark.parametrize("cfg,scale,tc", [("c3", 0.004, 16), ("c4", 0.002, 16), ("c3", 0.004, 8)])
+def test_grouped_slab_pairs_match_single_slabs(cuda_device, monkeypatch, vdt, N, cfg, scale, tc):
     """4-window groups run slab pairs on the 16x16x32 MFMA by default
     (spmm_grp2_kernel; GRWS_GRP_K32=0 selects the 16x16x16 kernel): both
     meet the oracle in both tiers and stay within one output rounding of
     each other (the same exact sums in another fp32 order).  A group of an
     odd slab count ends with half a pair: the small c3-shaped graph is
     nearly dense (every group 59 slabs), the sparse c4-shaped one has
-    groups of both parities."""
-    print(f"case grouped slab pairs {cfg} {vdt} N={N}", flush=True)
+    groups of both parities.  The grouped layout is the same whether the
+    graph's tiles are 16 or 8 columns wide (the reference's default)."""
+    print(f"case grouped slab pairs {cfg} tc={tc} {vdt} N={N}", flush=True)
     monkeypatch.setattr(ops, "GROUP_MIN_N", 0)
-    _, A = _graph(cuda_device, vdt, 16, scale=scale, cfg=cfg)
-    gt = ops.group_tiles(A.window_offset, A.original_col_indices, A.values_condensed, 16, A.num_cols,
+    _, A = _graph(cuda_device, vdt, tc, scale=scale, cfg=cfg)
+    gt = ops.group_tiles(A.window_offset, A.original_col_indices, A.values_condensed, tc, A.num_cols,
                          group_size=4, max_ratio=10.0, max_skew=1e9)
     slabs = (gt.group_offset[1:] - gt.group_offset[:-1]).cpu()
     assert bool((slabs % 2 == 1).any())
@@ -191,9 +192,9 @@ def test_grouped_slab_pairs_match_single_slabs(cuda_device, monkeypatch, vdt, N,
     torch.manual_seed(N + 17)
     X = torch.randn(A.num_cols, N, device=cuda_device).to(vdt)
     assert int(ops.L.load().grws_spmm_get_tuning(b"GRWS_GRP_K32")) == -1  # the default: slab pairs
-    Y2 = ops.spmm(A.window_offset, A.original_col_indices, A.values_condensed, X, 16, grouped=gt)
+    Y2 = ops.spmm(A.window_offset, A.original_col_indices, A.values_condensed, X, tc, grouped=gt)
     with ops.spmm_tuning(GRWS_GRP_K32=0):
-        Y1 = ops.spmm(A.window_offset, A.original_col_indices, A.values_condensed, X, 16, grouped=gt)
+        Y1 = ops.spmm(A.window_offset, A.original_col_indices, A.values_condensed, X, tc, grouped=gt)
     torch.cuda.synchronize()
     _oracle_check(A, X, Y2)
     _oracle_check(A, X, Y1)
