@@ -995,9 +995,14 @@ def copy_and_fill(copies, fills, stream: Optional[torch.cuda.Stream] = None) -> 
     """Device copies and int64 fills in one launch each (grws_copy_ranges,
     grws_fill_ranges_i64) on `stream` (the current stream by default).
     copies: (dst, src) pairs of contiguous tensors of equal byte size, both
-    16-byte aligned; fills: (dst int64 contiguous tensor, value).  Returns
-    False, with nothing done, when an operand does not qualify (the caller
-    then copies with torch)."""
+    16-byte aligned; fills: (dst int64 contiguous tensor, value); every
+    tensor on one device.  Returns False, with nothing done, when an operand
+    does not qualify (the caller then copies with torch)."""
+    if not copies and not fills:
+        return True
+    dev = (copies[0][0] if copies else fills[0][0]).device
+    if any(t.device != dev for pair in copies for t in pair) or any(d.device != dev for d, _ in fills):
+        return False
     for d, s_ in copies:
         if (not (d.is_cuda and s_.is_cuda and d.is_contiguous() and s_.is_contiguous())
                 or d.data_ptr() % 16 or s_.data_ptr() % 16
@@ -1006,7 +1011,6 @@ def copy_and_fill(copies, fills, stream: Optional[torch.cuda.Stream] = None) -> 
     for d, _ in fills:
         if not (d.is_cuda and d.dtype == torch.int64 and d.is_contiguous()):
             return False
-    dev = (copies[0][0] if copies else fills[0][0]).device
     sp = ctypes.c_void_p((stream or torch.cuda.current_stream(dev)).cuda_stream)
     cp = [(d, s_) for d, s_ in copies if d.numel()]
     if cp:

@@ -3,7 +3,8 @@ gather.  Bit-exact against torch's index_select for every unit width the
 kernel picks (16, 8, 4, 2 and 1 bytes: row length, pitches and base
 addresses decide), int64 and int32 indices, repeated indices, a strided
 source and an empty index; an index outside the source gives a zero row and
-raises the error flag, and nothing else writes the flag."""
+raises the error flag, and nothing else writes the flag.  Also the batch
+copy of the graphed mini-batch step (ops.copy_and_fill)."""
 import pytest
 import torch
 
@@ -68,3 +69,50 @@ def test_gather_rows_out_of_range_and_empty(cuda_device):
     assert int(err.item()) == 5
     empty = ops.gather_rows(src, torch.empty(0, dtype=torch.int64, device=cuda_device))
     assert empty.shape == (0, 64)
+
+
+def test_copy_and_fill_ranges(cuda_device):
+    """ops.copy_and_fill (grws_copy_ranges, grws_fill_ranges_i64), the
+    graphed mini-batch step's batch copy: 40 copies (more than one launch's
+    32 ranges) of byte sizes with and without a 16-byte tail, empty ranges,
+    and int64 fills, bit-exact against the sources and the fill values;
+    nothing outside the ranges is written."""
+    print("case copy_and_fill 40 ranges", flush=True)
+    g = torch.Generator(device=cuda_device)
+    g.manual_seed(40)
+    copies, expect = [], []
+    for i in range(40):
+        nbytes = [0, 1, 15, 16, 17, 4096, 12345][i % 7] + 16 * i
+        src = torch.randint(0, 256, (nbytes,), generator=g, device=cuda_device, dtype=torch.uint8)
+        buf = torch.full((nbytes + 64,), 0xA5, dtype=torch.uint8, device=cuda_device)
+        copies.append((buf[:nbytes], src))
+        expect.append((buf, src, nbytes))
+    fills, fbufs = [], []
+    for i, n in enumerate([0, 1, 7, 1000, 33]):
+        buf = torch.full((n + 8,), -7, dtype=torch.int64, device=cuda_device)
+        fills.append((buf[:n], i * 1000 - 3))
+        fbufs.append((buf, n, i * 1000 - 3))
+    assert ops.copy_and_fill(copies, fills)
+    torch.cuda.synchronize()
+    for buf, src, n in expect:
+        assert torch.equal(buf[:n], src)
+        assert bool((buf[n:] == 0xA5).all()), "a copy wrote past its range"
+    for buf, n, v in fbufs:
+        assert bool((buf[:n] == v).all())
+        assert bool((buf[n:] == -7).all()), "a fill wrote past its range"
+
+
+def test_copy_and_fill_refuses_unsuitable_operands(cuda_device):
+    """Host tensors, a misaligned start, unequal sizes, a non-int64 fill and
+    operands on two devices are refused (False, nothing done); empty lists
+    are a no-op."""
+    x = torch.zeros(64, dtype=torch.uint8, device=cuda_device)
+    y = torch.ones(64, dtype=torch.uint8, device=cuda_device)
+    assert ops.copy_and_fill([], [])
+    assert not ops.copy_and_fill([(x, torch.ones(64, dtype=torch.uint8))], [])
+    assert not ops.copy_and_fill([(x[1:33], y[:32])], [])
+    assert not ops.copy_and_fill([(x[:32], y[:16])], [])
+    assert not ops.copy_and_fill([], [(torch.zeros(4, dtype=torch.int32, device=cuda_device), 1)])
+    assert not ops.copy_and_fill([(x, y)], [(torch.zeros(4, dtype=torch.int64), 1)])
+    torch.cuda.synchronize()
+    assert bool((x == 0).all())
