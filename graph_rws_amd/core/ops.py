@@ -1281,12 +1281,14 @@ class CapturedSampleBlocks:
         if F0 > self.max_seeds:
             raise ValueError(f"CapturedSampleBlocks: {F0} seeds above the capacity {self.max_seeds}")
         stream = torch.cuda.current_stream(self.dev)
-        # stage the count and the seeds: device seeds (int64, 16-byte
-        # aligned) and the count in one copy launch; host seeds through the
-        # pinned buffer (free again: the previous call synchronised after
-        # its copy)
-        sd = seeds.view(-1)
-        if sd.is_cuda and sd.dtype == torch.int64 and sd.data_ptr() % 16 == 0:
+        # stage the count and the seeds: contiguous int64 seeds on this
+        # device, 16-byte aligned, and the count in one copy launch; other
+        # device seeds by torch's copy (strides, dtype, device); host seeds
+        # through the pinned buffer (free again: the previous call
+        # synchronised after its copy)
+        sd = seeds.reshape(-1)
+        if (sd.is_cuda and sd.device == self.dev and sd.dtype == torch.int64 and sd.is_contiguous()
+                and sd.data_ptr() % 16 == 0):
             srcs, dsts, nb = [self.cnt_table.data_ptr() + 16 * F0], [self.cnt_in.data_ptr()], [16]
             if F0:
                 srcs.append(sd.data_ptr())

@@ -55,6 +55,24 @@ def test_captured_batches_equal_the_direct_call(cuda_device, vdt, tc, thops):
         _same_batch(got, want)
 
 
+def test_captured_seeds_of_any_layout(cuda_device):
+    """The captured call stages contiguous int64 device seeds with one copy
+    launch and any other seeds through torch's copy: a strided view, int32
+    seeds, a 2-D seed tensor and host seeds all give the batch of the same
+    seeds passed contiguous."""
+    print("case captured sampling seed layouts", flush=True)
+    g = synth.c5_graph(device=cuda_device, scale=2e-4)
+    st = SampleState(g.num_nodes, cuda_device)
+    hops = [5, 10, 15]
+    cap = CapturedSampleBlocks(g.row_ptr, g.col_idx, hops, st, 42, 16, torch.float16, None, 256)
+    base = synth.distinct_seeds(g.num_nodes, 512, seed=7, device=cuda_device)
+    seeds = base[::2].clone()  # 256 seeds, contiguous
+    want = cap.run(seeds)
+    pad = torch.stack([seeds, base[1::2]], 1).contiguous()  # seeds at stride 2, 16-byte aligned
+    for variant in (pad[:, 0], seeds.to(torch.int32), seeds.view(16, 16), seeds.cpu()):
+        _same_batch(cap.run(variant), want)
+
+
 def test_neighbor_sampler_capture_matches_oracle(cuda_device):
     """The sampler with capture=True, batches of one bucket and of another,
     against the oracle; the captures are reused."""
