@@ -36,6 +36,7 @@ def coo_to_csr_device(num_rows: int, num_cols: int, src: torch.Tensor, dst: torc
     """COO -> CSR on the device (data/bcsr.py:162-187): stable sort by
     (src, dst); returns (num_edges, row_ptr int64, col_idx int32, values f32)."""
     dev = src.device
+    L.require_device("coo_to_csr_device", dev)  # the other inputs are moved to dev below
     s = _i32(src, dev)
     d = _i32(dst, dev)
     w = None if edge_weights is None else edge_weights.to(dev, torch.float32).contiguous()
@@ -77,6 +78,7 @@ def csr_to_bcsr_device(num_rows: int, num_cols: int, row_ptr: torch.Tensor, col_
     (convert_wrapper.cpp:27-180); values cast to `values_dtype` (round to
     nearest even).  transpose=True builds the BCSR of A^T."""
     dev = row_ptr.device
+    L.require_device("csr_to_bcsr_device", dev)  # the other inputs are moved to dev below
     rp = row_ptr.to(dev, torch.int64).contiguous()
     ci = _i32(col_idx, dev)
     va = None if values is None else values.to(dev, torch.float32).contiguous()
@@ -92,6 +94,7 @@ def coo_to_bcsr_device(num_rows: int, num_cols: int, rows: torch.Tensor, cols: t
     """COO (any order, duplicates allowed: the last in input order wins) ->
     BCSR on the device, in one sort."""
     dev = rows.device
+    L.require_device("coo_to_bcsr_device", dev)  # the other inputs are moved to dev below
     r = _i32(rows, dev)
     c = _i32(cols, dev)
     va = None if values is None else values.to(dev, torch.float32).contiguous()
@@ -106,6 +109,9 @@ def bcsr_to_coo(window_offset: torch.Tensor, col_indices: torch.Tensor, values: 
     """Edges of a BCSR graph: every slot with a column in [0, num_cols) and a
     non-zero value.  Returns (rows int32, cols int32, values f32)."""
     dev = window_offset.device
+    L.require_device("bcsr_to_coo", dev, window_offset, col_indices, values)
+    if not (window_offset.is_contiguous() and col_indices.is_contiguous() and values.is_contiguous()):
+        raise RuntimeError("bcsr_to_coo: the graph arrays must be contiguous")
     W = window_offset.numel() - 1
     T = col_indices.numel() // tile_cols
     view = L.BcsrView(L.ptr(window_offset), L.ptr(col_indices), L.ptr(values), W, T, 16, tile_cols,

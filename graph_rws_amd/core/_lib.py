@@ -291,5 +291,16 @@ def ptr(t: torch.Tensor | None):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def require_device(who: str, dev: torch.device, *tensors) -> None:
+    """Raises unless `dev` is a GPU and every tensor given (None skipped)
+    lives on it: the library reads them through raw device pointers, and a
+    host or other-device pointer would reach a kernel."""
+    if dev.type != "cuda":
+        raise RuntimeError(f"{who}: tensors must be CUDA tensors (got {dev})")
+    for t in tensors:
+        if t is not None and t.device != dev:
+            raise RuntimeError(f"{who}: every tensor must be on {dev} (got one on {t.device})")
+
+
 def stream_of(dev: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)

@@ -85,6 +85,9 @@ def build_spmm_plan(window_offset: torch.Tensor, num_tiles: int, tile_cols: int,
     """Builds the SpMM schedule on the device (one stream sync)."""
     lib = L.load()
     dev = window_offset.device
+    L.require_device("build_spmm_plan", dev, window_offset)
+    if not window_offset.is_contiguous() or window_offset.dtype != torch.int64:
+        raise RuntimeError("build_spmm_plan: window_offset must be a contiguous int64 tensor")
     W = window_offset.numel() - 1
     mi = ctypes.c_int64()
     ms = ctypes.c_int64()
@@ -265,6 +268,7 @@ def pack_tiles(window_offset: torch.Tensor, col_indices: torch.Tensor, values: t
     _check_graph(window_offset, col_indices, values, tile_cols)
     lib = L.load()
     dev = values.device
+    L.require_device("pack_tiles", dev, window_offset, col_indices)
     W = window_offset.numel() - 1
     T = col_indices.numel() // tile_cols
     view = L.BcsrView(L.ptr(window_offset), L.ptr(col_indices), L.ptr(values), W, T, 16, tile_cols,
@@ -356,6 +360,7 @@ def group_tiles(window_offset: torch.Tensor, col_indices: torch.Tensor, values: 
     max_skew = GROUP_MAX_SKEW if max_skew is None else max_skew
     lib = L.load()
     dev = values.device
+    L.require_device("group_tiles", dev, window_offset, col_indices)
     W = window_offset.numel() - 1
     T = col_indices.numel() // tile_cols
     if W == 0 or T == 0:
@@ -698,6 +703,7 @@ def relabel(frontier: torch.Tensor, edge_src: torch.Tensor, num_nodes: int):
     follow in ascending global id.  Returns (src_local int32 [E],
     next_frontier int64 [num_src]).  One stream sync."""
     dev = edge_src.device
+    L.require_device("relabel", dev, edge_src)
     fr = frontier.to(dev, torch.int64).contiguous()
     es = edge_src.to(torch.int64).contiguous()
     F, E = fr.numel(), es.numel()
@@ -740,6 +746,7 @@ class SamplingTimingResult:
 
 def _window_seeds(ids: torch.Tensor, num_nodes: int, drop: bool):
     dev = ids.device
+    L.require_device("window_seeds", dev, ids)
     ids = ids.to(torch.int32).contiguous()
     n = ids.numel()
     act = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
@@ -818,6 +825,7 @@ def sample_all_layers(window_offset: torch.Tensor, original_col_indices: torch.T
     _check_graph(window_offset, original_col_indices, values_condensed, tile_cols)
     if not window_offset.is_cuda:
         raise RuntimeError("window_offset must be a CUDA tensor")
+    L.require_device("sample_all_layers", window_offset.device, original_col_indices, values_condensed)
     fanouts = [int(f) for f in fanouts]
     for f in fanouts:
         if not 1 <= f <= 256:
@@ -887,6 +895,7 @@ def _sample_all_layers_per_layer(window_offset: torch.Tensor, original_col_indic
     _check_graph(window_offset, original_col_indices, values_condensed, tile_cols)
     if not window_offset.is_cuda:
         raise RuntimeError("window_offset must be a CUDA tensor")
+    L.require_device("sample_all_layers", window_offset.device, original_col_indices, values_condensed)
     dev = window_offset.device
     W = window_offset.numel() - 1
     n_nodes = int(num_global_nodes) if int(num_global_nodes) > 0 else 16 * W
@@ -968,6 +977,7 @@ def sample_block(indptr: torch.Tensor, indices: torch.Tensor, frontier: torch.Te
     int64 [num_src], num_edges).  One stream sync."""
     n, nnz = _csr_arrays(indptr, indices)
     dev = indptr.device
+    L.require_device("sample_block", dev, indices, state.node_map, state.bitmap)
     fr = frontier.to(dev, torch.int64).contiguous()
     F = fr.numel()
     lib = L.load()
@@ -1122,6 +1132,7 @@ def sample_blocks(indptr: torch.Tensor, indices: torch.Tensor, seeds: torch.Tens
     one window) for a transposed hop and None for another."""
     n, nnz = _csr_arrays(indptr, indices)
     dev = indptr.device
+    L.require_device("sample_blocks", dev, indices, state.node_map, state.bitmap)
     sd = seeds.to(dev, torch.int64).contiguous()
     F0 = sd.numel()
     H = len(fanouts)
@@ -1218,6 +1229,7 @@ class CapturedSampleBlocks:
         self.indptr, self.indices = indptr, indices
         n, nnz = _csr_arrays(indptr, indices)
         dev = indptr.device
+        L.require_device("CapturedSampleBlocks", dev, state.node_map, state.bitmap)
         self.dev, self.n, self.nnz = dev, n, nnz
         self.H = H = len(fanouts)
         self.fanouts = [int(k) for k in fanouts]
@@ -1397,6 +1409,7 @@ def gemm_tn(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype = torch.flo
     deterministic); returns [M, N] in out_dtype (float32 or the inputs')."""
     if not gemm_tn_supported(a, b):
         raise ValueError("gemm_tn: unsupported operands (see gemm_tn_supported)")
+    L.require_device("gemm_tn", a.device, b)
     K, M = a.shape
     N = b.shape[1]
     a2, b2 = _widen(a, 8), _widen(b, 8)
@@ -1446,9 +1459,7 @@ def repack(window_offset: torch.Tensor, col_indices: torch.Tensor, values: torch
     found, also when a call fails."""
     _check_graph(window_offset, col_indices, values, tile_cols)
     dev = window_offset.device
-    for t in (col_indices, values, window_ids, state.node_map):
-        if t.device != dev:
-            raise RuntimeError("repack: graph, window ids and state must be on one device")
+    L.require_device("repack", dev, col_indices, values, window_ids, state.node_map, state.bitmap)
     if state.num_nodes < int(num_nodes):
         raise ValueError("repack: state is smaller than the graph")
     ids = window_ids.to(torch.int64).contiguous()
