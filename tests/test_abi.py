@@ -207,3 +207,44 @@ def test_spmm_residual_rejects_bad_arguments_without_launching():
                                 L.GRWS_F16, 8, None, 0, None)
     assert st == L.GRWS_E_INVALID
 
+
+
+def test_spmm_grouped_rejects_bad_arguments_without_launching():
+    """grws_spmm_grouped validates the graph, the grouped tiles and X before
+    anything touches the device: dtypes, group size, group count, X wider
+    than the grouped columns, ldy, 16-byte rows, the value count."""
+    lib = L.load()
+    view = L.BcsrView(None, None, None, 8, 0, 16, 16, L.GRWS_F16, 0)  # 8 windows
+    x = ctypes.c_void_p(256)  # never dereferenced: every case fails a check first
+
+    def call(gt, x_dtype=L.GRWS_F16, x_rows=100, ldx=64, n=64, y_dtype=L.GRWS_F16, ldy=64, A=view):
+        return lib.grws_spmm_grouped(ctypes.byref(A) if A is not None else None,
+                                     ctypes.byref(gt) if gt is not None else None, x, x_dtype, x_rows, ldx, n,
+                                     None, 0, 0, x, y_dtype, ldy, None)
+
+    def gview(groups=2, slabs=0, values=0, mx=0, cols=100, G=4):
+        # a group_offset address that no case reaches (every one fails a check first)
+        return L.GroupedTilesView(ctypes.c_void_p(512), None, None, None, groups, slabs, values, mx, cols, G)
+
+    assert call(None) == L.GRWS_E_INVALID and b"null" in lib.grws_last_error()
+    assert call(gview(), x_dtype=L.GRWS_F32) == L.GRWS_E_DTYPE
+    assert call(gview(), y_dtype=L.GRWS_BF16) == L.GRWS_E_DTYPE
+    assert call(gview(G=3)) == L.GRWS_E_INVALID and b"group_size" in lib.grws_last_error()
+    assert call(gview(groups=3)) == L.GRWS_E_INVALID and b"groups" in lib.grws_last_error()
+    assert call(gview(cols=50)) == L.GRWS_E_INVALID and b"grouped for" in lib.grws_last_error()
+    assert call(gview(values=1 << 31)) == L.GRWS_E_INVALID and b"too many values" in lib.grws_last_error()
+    assert call(gview(), ldy=32) == L.GRWS_E_INVALID and b"ldy" in lib.grws_last_error()
+    assert call(gview(), n=60, ldx=64, ldy=64) == L.GRWS_E_INVALID and b"16-byte rows" in lib.grws_last_error()
+
+
+def test_grouped_slab_pair_switch_round_trips():
+    """GRWS_GRP_K32 (4-window groups on slab pairs, the default; 0 = single
+    slabs) is a tuning override like the others: unset reads -1, a set
+    value reads back, -1 clears it, an unknown name is refused."""
+    lib = L.load()
+    assert lib.grws_spmm_get_tuning(b"GRWS_GRP_K32") == -1
+    assert lib.grws_spmm_set_tuning(b"GRWS_GRP_K32", 0) == 0
+    assert lib.grws_spmm_get_tuning(b"GRWS_GRP_K32") == 0
+    assert lib.grws_spmm_set_tuning(b"GRWS_GRP_K32", -1) == 0
+    assert lib.grws_spmm_get_tuning(b"GRWS_GRP_K32") == -1
+    assert lib.grws_spmm_set_tuning(b"GRWS_NO_SUCH_SWITCH", 1) != 0
