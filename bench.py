@@ -929,6 +929,31 @@ def bench_dps(dev, cpu: bool, reps: int = 10) -> dict:
                        "frac": round(wb / (bms / 1e3) / 1e9 / HBM_PEAK_GBS, 5), "bytes_per_batch": wb,
                        "bytes": "per layer: the active windows' input tiles read once (column ids and values), "
                                 "the sampled tiles written, the seed ids read, the windows and masks written"}}
+    # the same batches with BCSRSampler(capture=True): the call captured once
+    # in a HIP graph (CapturedWindowSampler) and replayed per batch
+    wsc = BCSRSampler([15, 10, 5], tile_cols=8, verbose=False, capture=True)
+    for b in range(3):
+        wsc.sample_layers(G8, seed_sets[b])
+    torch.cuda.synchronize(dev)
+    tc_ = []
+    for b in range(3, 23):
+        t0 = time.perf_counter()
+        layers_c = wsc.sample_layers(G8, seed_sets[b])
+        torch.cuda.synchronize(dev)
+        tc_.append(time.perf_counter() - t0)
+    cms = 1e3 * sum(tc_) / len(tc_)
+    cap = next(iter(wsc._captures.values()))[1]
+    wr["captured"] = {
+        "batch_ms": round(cms, 4), "batches": len(tc_), "replays": cap.replays,
+        "equals_eager_last_batch": all(
+            torch.equal(x.window_offset, y.window_offset) and torch.equal(x.original_col_indices, y.original_col_indices)
+            and torch.equal(x.values_condensed, y.values_condensed) and torch.equal(x.active_windows, y.active_windows)
+            for x, y in zip(layers_c, layers)),
+        "roofline_frac": round(wb / (cms / 1e3) / 1e9 / HBM_PEAK_GBS, 5),
+        "note": "BCSRSampler(capture=True): grws_window_sample_layers_enqueue captured once and replayed per "
+                "batch; per batch one seed copy, the replay, the counts read back (the batch's one sync) and one "
+                "copy launch for the outputs"}
+    del wsc, cap
     if cpu:
         import oracle
         seeds = seed_sets[-1].cpu().numpy()

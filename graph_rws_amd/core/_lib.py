@@ -153,6 +153,11 @@ _PROTOS = {
     "grws_window_sample_layers": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.c_int64, _vp, ctypes.c_int64,
                                                  _vp, ctypes.c_int32, ctypes.POINTER(HacsView), _vp, _vp, _vp,
                                                  _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "grws_window_sample_layers_enqueue": (ctypes.c_int, [ctypes.POINTER(BcsrView), ctypes.c_int64, _vp,
+                                                         ctypes.c_int64, _vp, _vp, ctypes.c_int32,
+                                                         ctypes.POINTER(HacsView), _vp, _vp, _vp, _vp, _vp, _vp,
+                                                         ctypes.c_size_t, _vp, _vp, _vp]),
+    "grws_window_sample_layers_status": (ctypes.c_int, [ctypes.c_int64]),
     "grws_sample_state_init": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, _vp]),
     "grws_sample_block_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int32,
                                                             ctypes.c_int64]),

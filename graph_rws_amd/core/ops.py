@@ -876,6 +876,157 @@ def sample_all_layers(window_offset: torch.Tensor, original_col_indices: torch.T
     return layers, timings
 
 
+class CapturedWindowSampler:
+    """sample_all_layers replayed from a HIP graph: grws_window_sample_layers
+    _enqueue captured once for a graph, its fanouts, its HACS settings and a
+    seed-count capacity ``max_seeds``; any batch of at most max_seeds seeds
+    replays it (the count is read on the device).  Per batch: the seeds
+    staged by one copy, the replay, the layers' counts and error flags read
+    back (the batch's one sync), then one copy launch hands out compact
+    copies of the outputs, so a returned batch stays valid after later
+    replays.  The layers are those sample_all_layers returns, bit for bit
+    (no phase timings).  The graph arrays and score tables are held while
+    the capture lives (it reads them through their addresses) and must not
+    be modified meanwhile; one instance serves one stream at a time."""
+
+    def __init__(self, window_offset: torch.Tensor, original_col_indices: torch.Tensor,
+                 values_condensed: torch.Tensor, fanouts, num_global_nodes: int, max_seeds: int,
+                 static_scores: Optional[torch.Tensor] = None, window_part_ids: Optional[torch.Tensor] = None,
+                 part_starts: Optional[torch.Tensor] = None, part_ends: Optional[torch.Tensor] = None,
+                 alpha: float = 1.0, beta: float = 10.0, delta: float = 0.0, gamma_bonus: float = 0.0,
+                 score_scale: float = 100.0, use_hacs: int = 0, locality_enabled: int = 0, tile_cols: int = 8):
+        if tile_cols not in (8, 16):
+            raise RuntimeError("CapturedWindowSampler supports 16x8 tiles (the reference's) and 16x16")
+        _check_graph(window_offset, original_col_indices, values_condensed, tile_cols)
+        dev = window_offset.device
+        L.require_device("CapturedWindowSampler", dev, original_col_indices, values_condensed)
+        self.fanouts = [int(f) for f in fanouts]
+        if not self.fanouts or any(not 1 <= f <= 256 for f in self.fanouts):
+            raise RuntimeError("CapturedWindowSampler: one to 64 fanouts, each in [1, 256]")
+        self.max_seeds = int(max_seeds)
+        if self.max_seeds < 1:
+            raise ValueError("CapturedWindowSampler: max_seeds must be at least 1")
+        self.dev, self.tc = dev, int(tile_cols)
+        self.arrays = (window_offset, original_col_indices, values_condensed)
+        self.values_dtype = values_condensed.dtype
+        W = window_offset.numel() - 1
+        self.n_nodes = int(num_global_nodes) if int(num_global_nodes) > 0 else 16 * W
+        self.keep: list = []
+        self.hv = _hacs_view(dev, static_scores, window_part_ids, part_starts, part_ends, alpha, beta, delta,
+                             gamma_bonus, score_scale, use_hacs, locality_enabled, self.keep)
+        self.view = L.BcsrView(L.ptr(window_offset), L.ptr(original_col_indices), L.ptr(values_condensed), W,
+                               original_col_indices.numel() // tile_cols, 16, tile_cols,
+                               L.dtype_code(values_condensed.dtype), 0)
+        nl = self.nl = len(self.fanouts)
+        self.fan = (ctypes.c_int32 * nl)(*self.fanouts)
+        max_a = (ctypes.c_int64 * nl)()
+        max_t = (ctypes.c_int64 * nl)()
+        L.call("grws_window_sample_layers_bounds", ctypes.byref(self.view), self.n_nodes, self.max_seeds, self.fan,
+               nl, max_a, max_t)
+        tc, lib = self.tc, L.load()
+        self.bufs = []
+        for i in range(nl):
+            a, t = int(max_a[i]), int(max_t[i])
+            self.bufs.append((torch.empty(a + 1, dtype=torch.int64, device=dev),
+                              torch.empty(max(t * tc, 1), dtype=torch.int32, device=dev),
+                              torch.empty(max(t * 16 * tc, 1), dtype=self.values_dtype, device=dev),
+                              torch.empty(max(a, 1), dtype=torch.int32, device=dev),
+                              torch.empty(max(a, 1), dtype=torch.int32, device=dev)))
+        self.ptrs = [(ctypes.c_void_p * nl)(*[b[k].data_ptr() for b in self.bufs]) for k in range(5)]
+        wsb = int(lib.grws_window_sample_layers_workspace_bytes(ctypes.byref(self.view), self.n_nodes,
+                                                                self.max_seeds, self.fan, nl))
+        wsb += min(int(lib.grws_window_topk_key_scratch_bytes(ctypes.byref(self.view))), WINDOW_KEY_SCRATCH)
+        self.wsb = wsb
+        self.ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        self.seeds_buf = torch.empty(self.max_seeds, dtype=torch.int32, device=dev)
+        self.cnt_in = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.out_dev = torch.zeros(2 * nl + 1, dtype=torch.int64, device=dev)
+        self.out_host = torch.empty(2 * nl + 1, dtype=torch.int64, pin_memory=True)
+        # this capture's own second stream: the windows of over 1,024 slots
+        # run on it beside the others (forked and joined with events, which
+        # the capture records as two branches)
+        self.side = torch.cuda.Stream(dev)
+        self.graph = None
+        self.replays = 0
+
+    def _enqueue(self, stream) -> None:
+        L.call("grws_window_sample_layers_enqueue", ctypes.byref(self.view), self.n_nodes, L.ptr(self.seeds_buf),
+               self.max_seeds, L.ptr(self.cnt_in), self.fan, self.nl,
+               ctypes.byref(self.hv) if self.hv is not None else None, self.ptrs[0], self.ptrs[1], self.ptrs[2],
+               self.ptrs[3], self.ptrs[4], L.ptr(self.ws), self.wsb, L.ptr(self.out_dev),
+               ctypes.c_void_p(stream.cuda_stream), ctypes.c_void_p(self.side.cuda_stream))
+
+    def run(self, seeds: torch.Tensor):
+        """The layers of sample_all_layers for these seeds (global node ids,
+        any integer dtype, on any device): per fanout, in the order given,
+        [window_offset, col_indices, values, active_windows, masks]."""
+        sd = seeds.reshape(-1)
+        F0 = int(sd.numel())
+        if F0 > self.max_seeds:
+            raise ValueError(f"CapturedWindowSampler: {F0} seeds above the capacity {self.max_seeds}")
+        stream = torch.cuda.current_stream(self.dev)
+        if F0:
+            self.seeds_buf[:F0].copy_(sd.to(self.dev, torch.int32), non_blocking=True)
+        self.cnt_in.fill_(F0)
+        if self.graph is None:
+            self._enqueue(stream)  # this batch, and every kernel loaded before the capture
+            cs = torch.cuda.Stream(self.dev)
+            cs.wait_stream(stream)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(cs):
+                g.capture_begin(capture_error_mode="thread_local")
+                try:
+                    self._enqueue(cs)
+                finally:
+                    g.capture_end()
+            stream.wait_stream(cs)
+            self.graph = g
+        else:
+            self.graph.replay()
+            self.replays += 1
+        self.out_host.copy_(self.out_dev, non_blocking=True)
+        stream.synchronize()
+        c = self.out_host.tolist()
+        if c[2 * self.nl]:
+            L.call("grws_window_sample_layers_status", int(c[2 * self.nl]))
+        # compact copies, one buffer per element type, segments on 16 bytes
+        tc = self.tc
+        seg64, seg32, segv = [], [], []
+        for i, (off, cols, vals, act, msk) in enumerate(self.bufs):
+            A, T = int(c[2 * i]), int(c[2 * i + 1])
+            seg64.append((off, A + 1))
+            seg32 += [(cols, T * tc), (act, A), (msk, A)]
+            segv.append((vals, T * 16 * tc))
+        esz = torch.empty(0, dtype=self.values_dtype).element_size()
+        src, dst, nbytes, views = [], [], [], []
+        for segs, dtype, es in ((seg64, torch.int64, 8), (seg32, torch.int32, 4), (segv, self.values_dtype, esz)):
+            per = 16 // es
+            offs, o = [], 0
+            for _, k in segs:
+                offs.append(o)
+                o += -(-k // per) * per
+            buf = torch.empty(max(o, per), dtype=dtype, device=self.dev)
+            vs = []
+            for (t, k), o in zip(segs, offs):
+                if k:
+                    src.append(t.data_ptr())
+                    dst.append(buf.data_ptr() + o * es)
+                    nbytes.append(k * es)
+                vs.append(buf[o:o + k])
+            views.append(vs)
+        if src:
+            m = len(src)
+            L.call("grws_copy_ranges", (ctypes.c_void_p * m)(*src), (ctypes.c_void_p * m)(*dst),
+                   (ctypes.c_int64 * m)(*nbytes), m, ctypes.c_void_p(stream.cuda_stream))
+        v64, v32, vv = (iter(v) for v in views)
+        layers = []
+        for _ in range(self.nl):
+            off = next(v64)
+            cols, act, msk = next(v32), next(v32), next(v32)
+            layers.append([off, cols, next(vv), act, msk])
+        return layers
+
+
 def _sample_all_layers_per_layer(window_offset: torch.Tensor, original_col_indices: torch.Tensor,
                       values_condensed: torch.Tensor, initial_seeds: torch.Tensor, fanouts,
                       num_global_nodes: int, static_scores: Optional[torch.Tensor] = None,

@@ -131,6 +131,20 @@ struct SideStream {
     SideStream(const SideStream&) = delete;
     SideStream& operator=(const SideStream&) = delete;
     int fork() { return side_fork(main, &side); }
+    // fork onto a caller-owned stream `s` instead (a capture's own second
+    // stream: under capture the event wait joins `s` into the capture, and
+    // no other caller shares it); null keeps the work on `main`
+    int fork_to(hipStream_t s) {
+        if (s == nullptr || s == main) return GRWS_OK;
+        hipEvent_t ev;
+        GRWS_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+        hipError_t e = hipEventRecord(ev, main);
+        if (e == hipSuccess) e = hipStreamWaitEvent(s, ev, 0);
+        (void)hipEventDestroy(ev);
+        GRWS_HIP(e);
+        side = s;
+        return GRWS_OK;
+    }
     int join() {
         const hipStream_t s = side;
         side = main;

@@ -47,7 +47,7 @@ namespace {
 constexpr int kBlk = 256;
 constexpr int kMaxCap = 256;
 
-enum : int32_t { kErrWindow = 1, kErrSeed = 2, kErrHacs = 4 };
+enum : int32_t { kErrWindow = 1, kErrSeed = 2, kErrHacs = 4, kErrCount = 8 };
 
 inline int bits_for(int64_t x) {
     int b = 0;
@@ -774,12 +774,22 @@ __global__ void seed_emit_kernel(const uint64_t* __restrict__ keys, const uint32
 
 // --- the same from a dense per-window mask (zero on entry, left zero) ----
 // ids -> OR of their row bits into dense[id / 16]; n ids, or n_dev[0] * mul
-// when n_dev is set (the previous layer's tiles times their columns)
+// when n_dev is set (the previous layer's tiles times their columns, or an
+// enqueued batch's seed count), then at most n (the bound the buffers were
+// sized by; a larger device count is flagged and clamped)
 __global__ __launch_bounds__(kBlk) void seeds_scatter_kernel(const int32_t* __restrict__ ids, int64_t n,
                                                              const int64_t* __restrict__ n_dev, int64_t mul,
                                                              int64_t num_nodes, int drop_out_of_range,
                                                              uint32_t* __restrict__ dense, int32_t* __restrict__ err) {
-    const int64_t m = n_dev ? *n_dev * mul : n;
+    int64_t m = n;
+    if (n_dev) {
+        const int64_t want = *n_dev * mul;
+        if (want < 0 || want > n) {
+            if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, kErrCount);
+        } else {
+            m = want;
+        }
+    }
     for (int64_t i = (int64_t)blockIdx.x * kBlk + threadIdx.x; i < m; i += (int64_t)gridDim.x * kBlk) {
         const int32_t v = ids[i];
         if (v >= 0 && (int64_t)v < num_nodes) atomicOr(&dense[v >> 4], 1u << (v & 15));
@@ -807,6 +817,12 @@ __global__ __launch_bounds__(kBlk) void seeds_dense_emit_kernel(uint32_t* __rest
     windows[idx] = (int32_t)w;
     masks[idx] = (int32_t)m;
     dense[w] = 0u;
+}
+
+// the batch's error flags beside its counts (an enqueued call's one word
+// the caller reads back)
+__global__ void flags_out_kernel(const int32_t* __restrict__ err, int64_t* __restrict__ out) {
+    if (threadIdx.x == 0) out[0] = (int64_t)*err;
 }
 
 // a layer's active windows and tiles, kept for the one read-back at the end
@@ -1017,7 +1033,7 @@ int check_hacs(const grws_bcsr* A, const grws_hacs* hacs, const char* who) {
 int topk_enqueue(const grws_bcsr* A, const int32_t* active_windows, int64_t num_active,
                  const int64_t* num_active_dev, int S, const ScoreParams& p, int32_t* sampled_cols,
                  int32_t* sampled_slots, int64_t* out_window_offset, int32_t* err, void* workspace,
-                 size_t workspace_bytes, hipStream_t stream) {
+                 size_t workspace_bytes, hipStream_t stream, hipStream_t side_given = nullptr) {
     const int cap = S <= 32 ? 32 : (S <= 128 ? 128 : 256);
     Carver cv(workspace, workspace_bytes);
     int32_t* tiles = cv.take<int32_t>(num_active + 1);
@@ -1098,7 +1114,7 @@ int topk_enqueue(const grws_bcsr* A, const int32_t* active_windows, int64_t num_
     constexpr unsigned kKeysGrid = 1024;  // the keys kernel's work-groups walk the chunks
     {
         SideStream ss(stream);
-        GRWS_TRY(ss.fork());
+        GRWS_TRY(side_given ? ss.fork_to(side_given) : ss.fork());
         switch (A->values_dtype) {
             case GRWS_F32:
                 hipLaunchKernelGGL(window_topk_keys_kernel<float>, dim3(kKeysGrid), dim3(kBlk), 0, ss.side, ta);
@@ -1162,6 +1178,8 @@ int recompress_enqueue(const grws_bcsr* A, const int32_t* active_windows, int64_
 }
 
 int report_topk_errors(int32_t e, const char* who) {
+    if (e & kErrCount)
+        return set_error(GRWS_E_CAPACITY, "%s: the seed count is above the bound the call was sized for", who);
     if (e & kErrSeed) return set_error(GRWS_E_RANGE, "%s: a seed id is outside [0, num_nodes) and not -1", who);
     if (e & kErrWindow) return set_error(GRWS_E_RANGE, "%s: an active window is outside the graph", who);
     if (e & kErrHacs) return set_error(GRWS_E_RANGE, "%s: a column has no static score or a part id has no range", who);
@@ -1334,20 +1352,27 @@ extern "C" size_t grws_window_sample_layers_workspace_bytes(const grws_bcsr* A, 
     return align_up(nc.s.used, 256) + topk + 256;
 }
 
-extern "C" int grws_window_sample_layers(const grws_bcsr* A, int64_t num_nodes, const int32_t* seeds,
-                                         int64_t num_seeds, const int32_t* fanouts, int32_t num_layers,
-                                         const grws_hacs* hacs, int64_t* const* window_offset,
-                                         int32_t* const* col_indices, void* const* values,
-                                         int32_t* const* active_windows, int32_t* const* masks, int64_t* counts,
-                                         float* phase_ms, void* workspace, size_t workspace_bytes, void* stream_) {
-    clear_error();
-    hipStream_t stream = as_stream(stream_);
+namespace {
+// grws_window_sample_layers and its enqueue-only form.  Every layer's
+// kernels go on `stream`.  With out_dev set (the enqueued form) the seed
+// count is read on the device from num_seeds_dev[0] (num_seeds is its
+// bound, the size of every buffer and grid), each layer's counts go to
+// out_dev[2 l], out_dev[2 l + 1] and the error flags to out_dev[2 L], and
+// nothing is synchronised or read back; otherwise the counts and flags are
+// read back with one sync into counts and reported.
+int window_layers(const grws_bcsr* A, int64_t num_nodes, const int32_t* seeds, int64_t num_seeds,
+                  const int64_t* num_seeds_dev, const int32_t* fanouts, int32_t num_layers, const grws_hacs* hacs,
+                  int64_t* const* window_offset, int32_t* const* col_indices, void* const* values,
+                  int32_t* const* active_windows, int32_t* const* masks, int64_t* counts, int64_t* out_dev,
+                  float* phase_ms, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                  hipStream_t side_given) {
     GRWS_TRY(check_graph(A, "window_sample_layers"));
     GRWS_CHECK_ARG(num_layers >= 1 && num_layers <= kMaxLayers, "window_sample_layers: 1..64 layers (got %d)",
                    num_layers);
     GRWS_CHECK_ARG(num_nodes >= 0 && num_seeds >= 0 && num_seeds <= INT32_MAX, "window_sample_layers: bad size");
-    GRWS_CHECK_ARG(fanouts && counts && window_offset && col_indices && values && active_windows && masks,
+    GRWS_CHECK_ARG(fanouts && window_offset && col_indices && values && active_windows && masks,
                    "window_sample_layers: null pointer");
+    GRWS_CHECK_ARG(out_dev || counts, "window_sample_layers: null counts");
     GRWS_CHECK_ARG(num_seeds == 0 || seeds, "window_sample_layers: null seeds");
     GRWS_TRY(check_hacs(A, hacs, "window_sample_layers"));
     LayerBound lb[kMaxLayers];
@@ -1360,6 +1385,7 @@ extern "C" int grws_window_sample_layers(const grws_bcsr* A, int64_t num_nodes, 
         if (lb[l].tiles > 0)
             GRWS_CHECK_ARG(col_indices[l] && values[l], "window_sample_layers: null outputs in layer %d", l);
     }
+    const bool enq = out_dev != nullptr;
     const ScoreParams p = score_params(hacs);
     const int64_t nw = (num_nodes + 15) / 16;
     Carver cv(workspace, workspace_bytes);
@@ -1374,8 +1400,9 @@ extern "C" int grws_window_sample_layers(const grws_bcsr* A, int64_t num_nodes, 
                          cv.used);
     char* const topk_ws = cv.base + align_up(cv.used, 256);
     const size_t topk_bytes = workspace_bytes > align_up(cv.used, 256) ? workspace_bytes - align_up(cv.used, 256) : 0;
+    int64_t* const cnt_out = enq ? out_dev : cnt;  // per layer {active windows, tiles}
     GRWS_TRY(fill_i32(err, 1, 0, stream));
-    GRWS_TRY(fill_i32(reinterpret_cast<int32_t*>(cnt), 4 * num_layers, 0, stream));
+    GRWS_TRY(fill_i32(reinterpret_cast<int32_t*>(cnt_out), 4 * num_layers, 0, stream));
     if (nw > 0) GRWS_TRY(fill_i32(reinterpret_cast<int32_t*>(dense), nw, 0, stream));
     // phase events: before the top-K, between it and the recompression, after
     hipEvent_t ev[3 * kMaxLayers] = {};
@@ -1387,17 +1414,18 @@ extern "C" int grws_window_sample_layers(const grws_bcsr* A, int64_t num_nodes, 
             for (int i = 0; i < *n; ++i) (void)hipEventDestroy(ev[i]);
         }
     } guard{ev, &nev};
-    if (phase_ms) {
+    if (phase_ms && !enq) {
         for (int i = 0; i < 3 * num_layers; ++i) {
             GRWS_HIP(hipEventCreate(&ev[i]));
             nev = i + 1;
         }
     }
+    const bool timed = nev > 0;
     for (int32_t l = 0; l < num_layers; ++l) {
         const LayerBound& b = lb[l];
         if (b.active == 0) {  // no seeds: an empty layer (and every later one)
             GRWS_TRY(fill_i64(window_offset[l], 1, 0, stream));
-            if (phase_ms)
+            if (timed)
                 for (int k = 0; k < 3; ++k) GRWS_HIP(hipEventRecord(ev[3 * l + k], stream));
             continue;
         }
@@ -1405,12 +1433,12 @@ extern "C" int grws_window_sample_layers(const grws_bcsr* A, int64_t num_nodes, 
         // columns (-1 and columns past num_nodes dropped)
         const unsigned sgrid = (unsigned)(grid_for(b.ids) < 4096 ? grid_for(b.ids) : 4096);
         if (l == 0) {
-            hipLaunchKernelGGL(seeds_scatter_kernel, dim3(sgrid), dim3(kBlk), 0, stream, seeds, num_seeds, nullptr,
-                               (int64_t)1, num_nodes, 0, dense, err);
+            hipLaunchKernelGGL(seeds_scatter_kernel, dim3(sgrid), dim3(kBlk), 0, stream, seeds, num_seeds,
+                               num_seeds_dev, (int64_t)1, num_nodes, 0, dense, err);
         } else {
-            hipLaunchKernelGGL(seeds_scatter_kernel, dim3(sgrid), dim3(kBlk), 0, stream, col_indices[l - 1],
-                               (int64_t)0, window_offset[l - 1] + lb[l - 1].active, (int64_t)A->tile_cols, num_nodes,
-                               1, dense, err);
+            hipLaunchKernelGGL(seeds_scatter_kernel, dim3(sgrid), dim3(kBlk), 0, stream, col_indices[l - 1], b.ids,
+                               window_offset[l - 1] + lb[l - 1].active, (int64_t)A->tile_cols, num_nodes, 1, dense,
+                               err);
         }
         GRWS_LAUNCH_CHECK();
         hipLaunchKernelGGL(seeds_flags_kernel, dim3(grid_for(nw)), dim3(kBlk), 0, stream, dense, nw, flags);
@@ -1420,28 +1448,65 @@ extern "C" int grws_window_sample_layers(const grws_bcsr* A, int64_t num_nodes, 
                            active_windows[l], masks[l]);
         GRWS_LAUNCH_CHECK();
         const int64_t* na_dev = rank + nw;
-        if (phase_ms) GRWS_HIP(hipEventRecord(ev[3 * l], stream));
+        if (timed) GRWS_HIP(hipEventRecord(ev[3 * l], stream));
         GRWS_TRY(topk_enqueue(A, active_windows[l], b.active, na_dev, b.S, p, scols, sslot, window_offset[l], err,
-                              topk_ws, topk_bytes, stream));
-        if (phase_ms) GRWS_HIP(hipEventRecord(ev[3 * l + 1], stream));
+                              topk_ws, topk_bytes, stream, side_given));
+        if (timed) GRWS_HIP(hipEventRecord(ev[3 * l + 1], stream));
         if (b.tiles > 0)
             GRWS_TRY(recompress_enqueue(A, active_windows[l], b.active, na_dev, b.S, scols, sslot, window_offset[l],
                                         col_indices[l], values[l], stream));
-        if (phase_ms) GRWS_HIP(hipEventRecord(ev[3 * l + 2], stream));
+        if (timed) GRWS_HIP(hipEventRecord(ev[3 * l + 2], stream));
         hipLaunchKernelGGL(layer_counts_kernel, dim3(1), dim3(64), 0, stream, na_dev, window_offset[l] + b.active,
-                           cnt + 2 * l);
+                           cnt_out + 2 * l);
         GRWS_LAUNCH_CHECK();
+    }
+    if (enq) {
+        hipLaunchKernelGGL(flags_out_kernel, dim3(1), dim3(64), 0, stream, err, out_dev + 2 * num_layers);
+        GRWS_LAUNCH_CHECK();
+        return GRWS_OK;
     }
     int32_t e = 0;
     GRWS_HIP(hipMemcpyAsync(counts, cnt, sizeof(int64_t) * 2 * num_layers, hipMemcpyDeviceToHost, stream));
     GRWS_HIP(hipMemcpyAsync(&e, err, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
     GRWS_HIP(hipStreamSynchronize(stream));
     GRWS_TRY(report_topk_errors(e, "window_sample_layers"));
-    if (phase_ms) {
+    if (timed) {
         for (int32_t l = 0; l < num_layers; ++l) {
             GRWS_HIP(hipEventElapsedTime(&phase_ms[2 * l], ev[3 * l], ev[3 * l + 1]));
             GRWS_HIP(hipEventElapsedTime(&phase_ms[2 * l + 1], ev[3 * l + 1], ev[3 * l + 2]));
         }
     }
     return GRWS_OK;
+}
+}  // namespace
+
+extern "C" int grws_window_sample_layers(const grws_bcsr* A, int64_t num_nodes, const int32_t* seeds,
+                                         int64_t num_seeds, const int32_t* fanouts, int32_t num_layers,
+                                         const grws_hacs* hacs, int64_t* const* window_offset,
+                                         int32_t* const* col_indices, void* const* values,
+                                         int32_t* const* active_windows, int32_t* const* masks, int64_t* counts,
+                                         float* phase_ms, void* workspace, size_t workspace_bytes, void* stream_) {
+    clear_error();
+    return window_layers(A, num_nodes, seeds, num_seeds, nullptr, fanouts, num_layers, hacs, window_offset,
+                         col_indices, values, active_windows, masks, counts, nullptr, phase_ms, workspace,
+                         workspace_bytes, as_stream(stream_), nullptr);
+}
+
+extern "C" int grws_window_sample_layers_enqueue(const grws_bcsr* A, int64_t num_nodes, const int32_t* seeds,
+                                                 int64_t max_seeds, const int64_t* num_seeds_dev,
+                                                 const int32_t* fanouts, int32_t num_layers, const grws_hacs* hacs,
+                                                 int64_t* const* window_offset, int32_t* const* col_indices,
+                                                 void* const* values, int32_t* const* active_windows,
+                                                 int32_t* const* masks, void* workspace, size_t workspace_bytes,
+                                                 int64_t* out_dev, void* stream_, void* side_stream) {
+    clear_error();
+    GRWS_CHECK_ARG(num_seeds_dev && out_dev, "window_sample_layers_enqueue: null device count or output");
+    return window_layers(A, num_nodes, seeds, max_seeds, num_seeds_dev, fanouts, num_layers, hacs, window_offset,
+                         col_indices, values, active_windows, masks, nullptr, out_dev, nullptr, workspace,
+                         workspace_bytes, as_stream(stream_), static_cast<hipStream_t>(side_stream));
+}
+
+extern "C" int grws_window_sample_layers_status(int64_t err) {
+    clear_error();
+    return report_topk_errors((int32_t)err, "window_sample_layers");
 }

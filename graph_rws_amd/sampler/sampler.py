@@ -19,7 +19,7 @@ from typing import List
 import torch
 
 from ..core import sample_all_layers
-from ..core.ops import SampleState, repack
+from ..core.ops import CapturedWindowSampler, SampleState, TensorKey, repack
 from ..data import BCSRGraph
 
 
@@ -30,7 +30,7 @@ class BCSRSampler:
                  part_ranges: torch.Tensor = None, hacs_enabled: bool = False,
                  alpha: float = 1.0, beta: float = 10.0, delta: float = 0.0,
                  gamma_bonus: float = 0.0, score_scale: float = 100.0,
-                 locality_enabled: bool = False):
+                 locality_enabled: bool = False, capture: bool = False):
         self.fanouts = list(fanouts)
         self.tile_rows = tile_rows
         self.tile_cols = tile_cols
@@ -48,6 +48,11 @@ class BCSRSampler:
         self.delta = float(delta)
         self.gamma_bonus = float(gamma_bonus)
         self.score_scale = float(score_scale)
+        # not in the reference: replay every batch's call from a HIP graph
+        # (CapturedWindowSampler, one per seed-count bucket), the same layers
+        # bit for bit; phase timings are not recorded then
+        self.capture = bool(capture)
+        self._captures = {}
 
     def _hacs_args(self, device):
         """(static_scores, window_part_ids, part_starts, part_ends, use_hacs,
@@ -68,6 +73,12 @@ class BCSRSampler:
         """Samples len(fanouts) layers from `seed_nodes` (global node ids)."""
         device = g.window_offset.device if g.window_offset.is_cuda else torch.device("cuda")
         seeds = torch.as_tensor(seed_nodes).to(device, torch.int32).contiguous()
+        if self.capture:
+            if self.tile_rows != 16 or self.tile_cols not in (8, 16):
+                raise RuntimeError("sample_all_layers supports 16x8 tiles (the reference's) and 16x16")
+            if self.warps_per_block not in (4, 8):
+                raise RuntimeError(f"Unsupported warps_per_block: {self.warps_per_block}. Only 4 and 8 allowed.")
+            return self._build_layers(g, self._captured(g, seeds, device).run(seeds))
         ss, wp, ps, pe, use_hacs, loc = self._hacs_args(device)
         layers_data, timings = sample_all_layers(
             g.window_offset, g.original_col_indices, g.values_condensed, seeds,
@@ -85,6 +96,39 @@ class BCSRSampler:
                 st["p2_map"] += t.phase2_mapping_time
                 st["p3_recomp"] += t.phase3_recompression_time
                 st["total"] += t.total_time
+        return self._build_layers(g, layers_data)
+
+    # buckets of seed counts that share a capture, and at most this many
+    # captures kept (the least recently used is dropped)
+    CAPTURE_BUCKET = 256
+    MAX_CAPTURES = 4
+
+    def _captured(self, g: BCSRGraph, seeds: torch.Tensor, device) -> CapturedWindowSampler:
+        """The capture that serves this graph, these settings and this seed
+        count (made on first use, then kept while the graph arrays and the
+        score tensors are the same objects, unmodified)."""
+        cap = -(-max(1, int(seeds.numel())) // self.CAPTURE_BUCKET) * self.CAPTURE_BUCKET
+        tensors = [g.window_offset, g.original_col_indices, g.values_condensed]
+        tensors += [t for t in (self.static_scores, self.window_part_ids, self.part_ranges)
+                    if isinstance(t, torch.Tensor)]
+        extra = (tuple(self.fanouts), int(g.num_nodes), self.tile_cols, self.hacs_enabled, self.locality_enabled,
+                 self.alpha, self.beta, self.delta, self.gamma_bonus, self.score_scale,
+                 tuple(id(t) for t in (self.static_scores, self.window_part_ids, self.part_ranges)))
+        ent = self._captures.pop(cap, None)
+        if ent is None or not ent[0].matches(tensors, extra):
+            if len(self._captures) >= self.MAX_CAPTURES:
+                self._captures.pop(next(iter(self._captures)))
+            ss, wp, ps, pe, use_hacs, loc = self._hacs_args(device)
+            c = CapturedWindowSampler(g.window_offset, g.original_col_indices, g.values_condensed,
+                                      list(reversed(self.fanouts)), int(g.num_nodes), cap, ss, wp, ps, pe,
+                                      self.alpha, self.beta, self.delta, self.gamma_bonus, self.score_scale,
+                                      use_hacs, loc, self.tile_cols)
+            ent = (TensorKey(tensors, extra), c)
+        self._captures[cap] = ent  # most recently used last
+        return ent[1]
+
+    def _build_layers(self, g: BCSRGraph, layers_data) -> List[BCSRGraph]:
+        """One BCSRGraph per sampled layer, input side first."""
         layers: List[BCSRGraph] = []
         for win, cols, vals, act, msk in layers_data:
             sub = BCSRGraph.from_components(window_offset=win, original_col_indices=cols,

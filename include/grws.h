@@ -646,6 +646,30 @@ int grws_window_sample_layers(const grws_bcsr* A, int64_t num_nodes, const int32
                               int64_t* const* window_offset, int32_t* const* col_indices, void* const* values,
                               int32_t* const* active_windows, int32_t* const* masks, int64_t* counts,
                               float* phase_ms, void* workspace, size_t workspace_bytes, void* stream);
+/* grws_window_sample_layers without its read-back (sampling_wrapper.cu:    */
+/* 365-438 with no host sync at all), so that a caller can capture it once  */
+/* in a HIP graph and replay it per batch: the seed count is read on the   */
+/* device from num_seeds_dev[0]; every buffer, the workspace and the grids  */
+/* are sized by max_seeds (bounds and workspace queries with max_seeds); a  */
+/* larger device count is flagged (GRWS_E_CAPACITY) and clamped.  When the  */
+/* stream reaches the end of the call, out_dev [2*num_layers + 1] (device)  */
+/* holds each layer's active windows and tiles (as counts above) and then   */
+/* the batch's error flags, for grws_window_sample_layers_status.  No      */
+/* phase timings.  Same results as grws_window_sample_layers.  side_stream  */
+/* (or NULL): a second stream the caller owns on the same device; the      */
+/* windows of over 1,024 slots run on it, forked from and joined back to    */
+/* `stream` with events, also while `stream` is being captured (a capture   */
+/* then records the two branches side by side).  With NULL they run on the  */
+/* library's extra stream, or on `stream` itself under capture.            */
+int grws_window_sample_layers_enqueue(const grws_bcsr* A, int64_t num_nodes, const int32_t* seeds,
+                                      int64_t max_seeds, const int64_t* num_seeds_dev, const int32_t* fanouts,
+                                      int32_t num_layers, const grws_hacs* hacs, int64_t* const* window_offset,
+                                      int32_t* const* col_indices, void* const* values,
+                                      int32_t* const* active_windows, int32_t* const* masks, void* workspace,
+                                      size_t workspace_bytes, int64_t* out_dev, void* stream, void* side_stream);
+/* The status (and grws_last_error message) of an enqueued call's error     */
+/* flags, out_dev[2*num_layers] read back by the caller: GRWS_OK for 0.     */
+int grws_window_sample_layers_status(int64_t err);
 
 size_t grws_relabel_workspace_bytes(int64_t num_frontier, int64_t num_edges);
 int grws_relabel(const int64_t* frontier, int64_t num_frontier, const int64_t* edge_src,

@@ -254,3 +254,104 @@ def test_hacs_score_table_too_short_is_an_error(cuda_device, path):
     b, _ = ops._sample_all_layers_per_layer(G.window_offset, G.original_col_indices, G.values_condensed, seeds,
                                             [5, 10], g.num_nodes, static_scores=full, use_hacs=1)
     _layers_equal(a, b)
+
+
+def _c1_hacs(dev, G, g):
+    rng = np.random.default_rng(8)
+    q = torch.from_numpy(rng.random(g.num_nodes).astype(np.float32)).to(dev)
+    wpart = torch.from_numpy(rng.integers(-1, 3, G.num_windows).astype(np.int32)).to(dev)
+    return dict(static_scores=q, window_part_ids=wpart,
+                part_starts=torch.tensor([0, 900, 1800], dtype=torch.int32, device=dev),
+                part_ends=torch.tensor([900, 1800, 2708], dtype=torch.int32, device=dev),
+                use_hacs=1, locality_enabled=1, alpha=0.5, beta=3.0, delta=0.25, gamma_bonus=0.37,
+                score_scale=250.0)
+
+
+@pytest.mark.parametrize("case", ["c2", "c1_hacs", "bf16_tc16"])
+def test_captured_window_sampler_matches_the_direct_call(cuda_device, case):
+    """CapturedWindowSampler (grws_window_sample_layers_enqueue captured once,
+    replayed per batch, the seed count read on the device) gives the layers
+    of sample_all_layers bit for bit, for batches of several seed counts
+    under one capacity (the first batch runs eagerly and captures); a
+    returned batch stays valid after later replays; -1, repeated and empty
+    seed sets too."""
+    from graph_rws_amd.core.ops import CapturedWindowSampler
+    print(f"case captured window sampler {case}", flush=True)
+    kw = {}
+    if case == "c2":
+        g, G = _graph("c2", cuda_device)
+        fan, cap = [5, 10, 15], 1024
+        batches = [synth.distinct_seeds(g.num_nodes, n, seed=40 + i).to(cuda_device)
+                   for i, n in enumerate([1024, 1000, 1024, 513])]
+    elif case == "c1_hacs":
+        g, G = _graph("c1", cuda_device)
+        kw = _c1_hacs(cuda_device, G, g)
+        fan, cap = [12, 40, 3], 400
+        batches = [torch.arange(1, g.num_nodes, 7), torch.arange(0, g.num_nodes, 9),
+                   torch.tensor([-1, 7, 7, 8, -1, 16, 16, 15, 0, -1]), torch.zeros(0, dtype=torch.int64)]
+    else:
+        g, G = _graph("c1", cuda_device, tc=16, vdt=torch.bfloat16)
+        fan, cap = [20, 7], 256
+        batches = [torch.arange(0, g.num_nodes, 13), torch.arange(5, g.num_nodes, 11).to(torch.int32)]
+    c = CapturedWindowSampler(G.window_offset, G.original_col_indices, G.values_condensed, fan, g.num_nodes, cap,
+                              tile_cols=G.tile_cols, **kw)
+    kept = []
+    for i, seeds in enumerate(batches):
+        got = c.run(seeds if i % 2 == 0 else seeds.cpu())
+        want, _ = sample_all_layers(G.window_offset, G.original_col_indices, G.values_condensed,
+                                    seeds.to(cuda_device), fan, g.num_nodes, tile_cols=G.tile_cols, **kw)
+        _layers_equal(got, want)
+        kept.append((got, want))
+    assert c.replays == len(batches) - 1
+    for got, want in kept:  # earlier batches untouched by the later replays
+        _layers_equal(got, want)
+
+
+def test_captured_window_sampler_errors(cuda_device):
+    """An out-of-range seed is GRWS_E_RANGE after the replay and the next
+    batch is fine; more seeds than the capacity are refused on the host; a
+    device seed count above the capacity is clamped and flagged
+    (GRWS_E_CAPACITY) by the kernel that reads the seeds."""
+    from graph_rws_amd.core import ops
+    from graph_rws_amd.core.ops import CapturedWindowSampler
+    g, G = _graph("c1", cuda_device)
+    c = CapturedWindowSampler(G.window_offset, G.original_col_indices, G.values_condensed, [5, 10], g.num_nodes,
+                              64)
+    good = torch.arange(0, 640, 10)
+    first = c.run(good)
+    with pytest.raises(GrwsError, match="outside"):
+        c.run(torch.tensor([3, g.num_nodes + 5, 9]))
+    _layers_equal(c.run(good), first)
+    with pytest.raises(ValueError, match="capacity"):
+        c.run(torch.arange(65))
+    c.cnt_in.fill_(c.max_seeds + 7)
+    c.graph.replay()
+    torch.cuda.synchronize()
+    flags = int(c.out_dev[-1].item())
+    with pytest.raises(GrwsError, match="seed count"):
+        ops.L.call("grws_window_sample_layers_status", flags)
+    _layers_equal(c.run(good), first)
+
+
+def test_bcsr_sampler_capture_option(cuda_device):
+    """BCSRSampler(capture=True) samples the layers of the uncaptured
+    sampler; seed counts of one bucket share a capture; modifying the
+    graph's values in place makes a new one."""
+    g, G = _graph("c1", cuda_device)
+    a = BCSRSampler(fanouts=[10, 5], verbose=False, capture=True)
+    b = BCSRSampler(fanouts=[10, 5], verbose=False)
+    for n in (170, 150, 170):
+        seeds = torch.arange(0, g.num_nodes, g.num_nodes // n)[:n]
+        for x, y in zip(a.sample_layers(G, seeds), b.sample_layers(G, seeds)):
+            for name in ("window_offset", "original_col_indices", "values_condensed", "active_windows",
+                         "active_masks"):
+                assert torch.equal(getattr(x, name).cpu(), getattr(y, name).cpu()), name
+            assert (x.num_rows, x.num_cols) == (y.num_rows, y.num_cols)
+    assert len(a._captures) == 1
+    cap = next(iter(a._captures.values()))[1]
+    assert cap.replays == 2
+    G.values_condensed.mul_(0.5)
+    seeds = torch.arange(0, g.num_nodes, 17)
+    for x, y in zip(a.sample_layers(G, seeds), b.sample_layers(G, seeds)):
+        assert torch.equal(x.values_condensed.cpu(), y.values_condensed.cpu())
+    assert next(iter(a._captures.values()))[1] is not cap
