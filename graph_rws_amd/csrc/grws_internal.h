@@ -136,6 +136,19 @@ struct SideStream {
     // no other caller shares it); null keeps the work on `main`
     int fork_to(hipStream_t s) {
         if (s == nullptr || s == main) return GRWS_OK;
+        int md = -1;
+        hipDevice_t sd = -1;
+        if (main == nullptr) {
+            GRWS_HIP(hipGetDevice(&md));
+        } else {
+            hipDevice_t d = -1;
+            GRWS_HIP(hipStreamGetDevice(main, &d));
+            md = (int)d;
+        }
+        GRWS_HIP(hipStreamGetDevice(s, &sd));
+        if (md != sd)
+            return set_error(GRWS_E_INVALID, "side stream on device %d, the call's stream on device %d", (int)sd,
+                             (int)md);
         hipEvent_t ev;
         GRWS_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
         hipError_t e = hipEventRecord(ev, main);

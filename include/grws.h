@@ -656,11 +656,12 @@ int grws_window_sample_layers(const grws_bcsr* A, int64_t num_nodes, const int32
 /* holds each layer's active windows and tiles (as counts above) and then   */
 /* the batch's error flags, for grws_window_sample_layers_status.  No      */
 /* phase timings.  Same results as grws_window_sample_layers.  side_stream  */
-/* (or NULL): a second stream the caller owns on the same device; the      */
-/* windows of over 1,024 slots run on it, forked from and joined back to    */
-/* `stream` with events, also while `stream` is being captured (a capture   */
-/* then records the two branches side by side).  With NULL they run on the  */
-/* library's extra stream, or on `stream` itself under capture.            */
+/* (or NULL): a second stream the caller owns on the same device (one of   */
+/* another device: GRWS_E_INVALID); the windows of over 1,024 slots run on  */
+/* it, forked from and joined back to `stream` with events, also while      */
+/* `stream` is being captured (a capture then records the two branches side */
+/* by side).  With NULL they run on the library's extra stream, or on       */
+/* `stream` itself under capture.                                           */
 int grws_window_sample_layers_enqueue(const grws_bcsr* A, int64_t num_nodes, const int32_t* seeds,
                                       int64_t max_seeds, const int64_t* num_seeds_dev, const int32_t* fanouts,
                                       int32_t num_layers, const grws_hacs* hacs, int64_t* const* window_offset,
