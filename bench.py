@@ -33,8 +33,9 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16
 # that exact workload.  Sources: the profile file named with each figure
 MEASURED_TRAFFIC = {
     # (config, N, x dtype, tile cols, A format): (bytes per SpMM, profile file)
-    # grouped tiles, 4 windows per group, slab pairs: FETCH 15.95M KiB x2, WRITE 0.277M KiB
-    ("c3", 608, "f16", 16, "grouped tiles (4 windows)"): (32.95e9, "profiles/spmm_grp2_c3_n608_f16.md"),
+    # grouped tiles, 4 windows per group, slab pairs staged by direct loads
+    # into LDS: FETCH 16.88M KiB x2, WRITE 0.277M KiB
+    ("c3", 608, "f16", 16, "grouped tiles (4 windows)"): (34.86e9, "profiles/spmm_grp2d_c3_n608_f16.md"),
     # SpMM kernel (351.0 MB read, 55.1 MB written) plus the split-window fixup (14.6 MB)
     ("c2", 128, "f16", 16, "packed tiles"): (420.7e6, "profiles/spmm_buf_c2_n128_f16.md"),
     # SpMM kernel (24.96 GB read, 0.56 GB written) plus the fixup (13 MB)
@@ -1232,9 +1233,8 @@ def main():
         "roofline": {
             "bound": "hbm",
             # 16-bit X runs the buffer-load kernel, fp32 X the element-masked
-            # one; 4-window groups multiply slab pairs (spmm_grp2_kernel)
-            "kernel": (("spmm_grp2_kernel" if grouped.group_size == 4 and _ops.grouped_slab_pairs()
-                        else "spmm_grp_kernel") if grouped is not None else
+            # one; 4-window groups multiply slab pairs (spmm_grp2d_kernel)
+            "kernel": (_ops.grouped_kernel(grouped.group_size) if grouped is not None else
                        "spmm_buf_kernel" if dname in ("f16", "bf16") else "spmm_fwd_kernel"),
             # compulsory bytes (A in the format read, X and Y once) per product
             # over the product's kernel time (HIP events on the launch stream)

@@ -71,9 +71,18 @@ class spmm_tuning:
 
 def grouped_slab_pairs() -> bool:
     """Whether 4-window grouped products multiply slab pairs on the
-    16x16x32 MFMA (spmm_grp2_kernel, the default) rather than single slabs
-    (GRWS_GRP_K32=0)."""
+    16x16x32 MFMA (the default) rather than single slabs (GRWS_GRP_K32=0)."""
     return int(L.load().grws_spmm_get_tuning(b"GRWS_GRP_K32")) != 0
+
+
+def grouped_kernel(group_size: int) -> str:
+    """The kernel a grouped product of `group_size` windows runs: slab pairs
+    staged by direct loads into LDS (spmm_grp2d_kernel, the default), the
+    same through registers (spmm_grp2_kernel, GRWS_GRP_DMA=0), or single
+    slabs (spmm_grp_kernel: GRWS_GRP_K32=0, or groups of 2 or 8)."""
+    if group_size != 4 or not grouped_slab_pairs():
+        return "spmm_grp_kernel"
+    return "spmm_grp2_kernel" if int(L.load().grws_spmm_get_tuning(b"GRWS_GRP_DMA")) == 0 else "spmm_grp2d_kernel"
 
 
 def default_slabs(num_windows: int, num_tiles: int, tile_cols: int, n_cols: int) -> int:

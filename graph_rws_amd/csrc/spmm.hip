@@ -56,12 +56,13 @@ enum TuneKey {
     kTuneGrpNblk,  // GRWS_GRP_NBLK: column blocks of the grouped kernel's first launch
     kTuneGrpC320,  // GRWS_GRP_C320: 0 = no 320-column grouped chunks
     kTuneGrpK32,   // GRWS_GRP_K32: 0 = 4-window groups on the 16x16x16 kernel, not slab pairs
+    kTuneGrpDma,   // GRWS_GRP_DMA: 0 = slab pairs staged through registers, not direct loads into LDS
     kTuneCount
 };
 const char* const kTuneNames[kTuneCount] = {"GRWS_SPMM_NBLK",   "GRWS_SPMM_WAVES",  "GRWS_SPMM_KERNEL",
                                             "GRWS_SPMM_ORDER",  "GRWS_SPMM_NARROW", "GRWS_SPMM_C320",
                                             "GRWS_GRP_WPW",     "GRWS_GRP_NBLK",    "GRWS_GRP_C320",
-                                            "GRWS_GRP_K32"};
+                                            "GRWS_GRP_K32",     "GRWS_GRP_DMA"};
 std::atomic<int> g_tune[kTuneCount];
 struct TuneInit {
     TuneInit() {
@@ -1287,6 +1288,231 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NBLK == 20 
     if (win < a.num_windows) spmm_epilogue<XT, NBLK, 1>(a, acc, stage_all, 0, lane, win, -1, chunk, n0);
 }
 
+// The slab-pair kernel with X staged by direct loads into LDS
+// (buffer_load_dwordx4 ... lds): the gathered rows go from the L2 straight
+// into the stage, not through registers and LDS writes, which frees the
+// 20 staging registers and 5 LDS writes per pair.  Lane l of such a load
+// writes its 16 bytes at the instruction's LDS base + 16 l (a lane past the
+// buffer resource writes zeros: the zero row), so the stage is blocked:
+// wave h's load i fills a 1 KiB block of 8 rows (rows 4h..4h+3 of each slab
+// of the pair) x 64 columns, row k of the block at 128 k, its 16-byte
+// segment s at position (s + 2 (k mod 4)) mod 8: the four rows a
+// transposing read takes then cover all 128 bytes of the banks once.  The
+// two stage buffers are separate arrays, so the compiler can tell that a
+// load into one does not feed the reads of the other.  One barrier per
+// pair: each wave waits for its own loads (s_waitcnt), then the barrier
+// makes every wave's rows visible and tells that the other buffer is no
+// longer read; the next pair's loads go into it after the barrier.  Same
+// sums, same order as spmm_grp2_kernel.
+template <int XT, int NBLK>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NBLK == 20 ? 3 : 1, NBLK == 20 ? 3 : 8))) void spmm_grp2d_kernel(
+    SpmmArgs a) {
+    static_assert(XT == GRWS_F16 || XT == GRWS_BF16, "grouped tiles: 16-bit X and values");
+    static_assert(NBLK == 8 || NBLK == 16 || NBLK == 20, "column blocks per chunk");
+    constexpr int G = 4;
+    constexpr int NC = NBLK * 16;
+    constexpr int NLD = NC / 64;  // direct loads per wave and pair
+    using S = typename XTraits<XT>::S;
+    typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+    typedef short short8_t __attribute__((ext_vector_type(8)));
+    typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+    typedef __attribute__((address_space(3))) char lds_char_t;
+    __shared__ __attribute__((aligned(1024))) S st0[32 * NC];
+    __shared__ __attribute__((aligned(1024))) S st1[32 * NC];
+
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int64_t ipc = (a.num_items + 7) & ~(int64_t)7;
+    const int chunk = (int)(blockIdx.x / ipc);
+    const int64_t rr = (int64_t)blockIdx.x - (int64_t)chunk * ipc;
+    const int64_t q = (rr & 7) * (ipc >> 3) + (rr >> 3);
+    if (chunk >= a.nchunks || q >= a.num_items) return;  // uniform over the work-group
+    const int64_t g0 = a.goff[q];
+    const int64_t nslabs = a.goff[q + 1] - g0;
+    const int64_t npairs = (nslabs + 1) >> 1;
+    const int64_t n0 = a.col_base + (int64_t)chunk * NC;
+
+    const __amdgpu_buffer_rsrc_t rsC = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.cols + g0 * 16), (short)0, (int)(nslabs * 64), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsH = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.hdr + g0 * G * 12), (short)0, (int)(nslabs * G * 48), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsV =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.pvals), (short)0, (int)a.pv_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsX =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.x), (short)0, (int)a.x_bytes, 0x00020000);
+
+    // the lane's gathered row: slab half hx of the pair, position 4 wave + r4
+    // in that slab (block row k = 4 hx + r4 = lane / 8); block position
+    // lane % 8 holds column segment (lane % 8 - 2 r4) mod 8 of each 64
+    const int hx = lane >> 5, r4 = (lane >> 3) & 3;
+    const uint32_t col_off = (uint32_t)(4 * wave + r4) * 4;
+    const int seg = ((lane & 7) - 2 * r4) & 7;
+    // load i reads columns e0 + 64 i .. + 7 (bytes 2 e0 + 128 i), if below n_cols
+    const int64_t e0 = n0 + 8 * seg;
+    const uint32_t colb0 = (uint32_t)(e0 * 2);
+    const int32_t nvalid = (int32_t)(a.n_cols - e0 > 64 * NLD ? 64 * NLD : a.n_cols - e0);  // < 64 i: past n_cols
+    const uint32_t ldxb = (uint32_t)(a.ldx * 2);
+    const uint32_t xr = (uint32_t)a.x_rows;
+    const int ag = lane >> 4;
+    const int ar = lane & 15;
+    // transposing reads: lane (ag, ar) reads row ar / 4 of block rows
+    // 4 (ag / 2) .. + 3 in wave block 2 (ag % 2) (rows 8 ag .. 8 ag + 3 of
+    // the 32-row stage; + NLD blocks for rows 8 ag + 4 ..), 8 bytes at
+    // column 16 b + 4 (ar % 4); per b % 4 the byte offset in the block
+    uint32_t troff[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int k = 4 * (ag >> 1) + (ar >> 2);
+        const int s = 2 * m + ((ar & 3) >> 1);
+        troff[m] = (uint32_t)((2 * (ag & 1) * NLD) * 1024 + 128 * k + 16 * ((s + 2 * (ar >> 2)) & 7) + 8 * (ar & 1));
+    }
+    const int ha = ag >> 1;
+    const uint32_t bitoff = (uint32_t)((ar & 3) * 16 + 8 * (ag & 1));
+    const uint32_t hword = (uint32_t)(3 * (ar >> 2) + ((lane & 3) < 2 ? (lane & 3) : 2)) * 4;
+
+    auto load_col = [&](int64_t p) -> int32_t {
+        const int64_t sl = 2 * p + hx;
+        const int32_t c =
+            (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rsC, (int)((uint32_t)(sl * 64) + col_off), 0, kAPolicy);
+        return sl < nslabs ? c : -1;
+    };
+    // pair's X rows into stage buffer `st` (a lane past the resource writes
+    // the zero row)
+    auto load_x = [&](S* st, const int32_t c) {
+        const uint32_t rowb = __umul24((uint32_t)c < xr ? (uint32_t)c : xr, ldxb) + colb0;
+        const uint32_t zrow = __umul24(xr, ldxb);  // past the resource: the zero row
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            const uint32_t off = 64 * i < nvalid ? rowb + 128u * i : zrow;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsX, (lds_ptr_t)((lds_char_t*)st + (wave * NLD + i) * 1024), 16, (int)off, 0, 0, 0);
+        }
+    };
+    auto load_hdr = [&](int64_t p) -> uint32_t {
+        return __builtin_amdgcn_raw_buffer_load_b32(
+            rsH, (int)((uint32_t)(((2 * p + ha) * G + wave) * 48) + hword), 0, kAPolicy);
+    };
+    auto lane_hdr = [&](const uint32_t raw) -> u32x3_t {
+        return u32x3_t{(uint32_t)__builtin_amdgcn_mov_dpp((int)raw, 0x00, 0xf, 0xf, false),
+                       (uint32_t)__builtin_amdgcn_mov_dpp((int)raw, 0x55, 0xf, 0xf, false),
+                       (uint32_t)__builtin_amdgcn_mov_dpp((int)raw, 0xaa, 0xf, 0xf, false)};
+    };
+    auto load_a = [&](const u32x3_t h, u32x4_t* out) {
+        const uint64_t m = ((uint64_t)h[1] << 32) | h[0];
+        const uint32_t below = (uint32_t)__builtin_popcountll(m & ((1ull << bitoff) - 1));
+        const uint32_t byte = (uint32_t)(m >> bitoff) & 255u;
+        const uint32_t nib0 = byte & 15u, nib1 = byte >> 4;
+        const uint32_t i0 = h[2] + below;
+        const uint32_t i1 = i0 + (uint32_t)__builtin_popcount(nib0);
+        const uint32_t off0 = nib0 ? (i0 & ~1u) * 2u : 0x80000000u;
+        const uint32_t off1 = nib1 ? (i1 & ~1u) * 2u : 0x80000000u;
+        const u32x3_t d0 = __builtin_amdgcn_raw_buffer_load_b96(rsV, (int)off0, 0, kAPolicy);
+        const u32x3_t d1 = __builtin_amdgcn_raw_buffer_load_b96(rsV, (int)off1, 0, kAPolicy);
+        out[0] = u32x4_t{d0[0], d0[1], d0[2], nib0 | ((i0 & 1u) << 4)};
+        out[1] = u32x4_t{d1[0], d1[1], d1[2], nib1 | ((i1 & 1u) << 4)};
+    };
+    auto decode = [&](const u32x4_t v) -> short4_t {
+        const uint32_t info = v[3];
+        const uint32_t sh = (info >> 4) * 16u;
+        const uint32_t r0 = __builtin_amdgcn_alignbit(v[1], v[0], sh);
+        const uint32_t r1 = __builtin_amdgcn_alignbit(v[2], v[1], sh);
+        const uint32_t b0 = info & 1u, b1 = (info >> 1) & 1u, b2 = (info >> 2) & 1u, b3 = (info >> 3) & 1u;
+        const uint32_t k2 = b0 + b1, k3 = k2 + b2;
+        const uint32_t s0 = b0 ? 0x0100u : 0x0c0cu;
+        const uint32_t s1 = b1 ? 0x0100u + 0x0202u * b0 : 0x0c0cu;
+        const uint32_t s2 = b2 ? 0x0100u + 0x0202u * k2 : 0x0c0cu;
+        const uint32_t s3 = b3 ? 0x0100u + 0x0202u * k3 : 0x0c0cu;
+        return __builtin_bit_cast(short4_t, u32x2_t{__builtin_amdgcn_perm(r1, r0, s0 | (s1 << 16)),
+                                                    __builtin_amdgcn_perm(r1, r0, s2 | (s3 << 16))});
+    };
+
+    float4_t acc[NBLK];
+#pragma unroll
+    for (int b = 0; b < NBLK; ++b) acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto multiply = [&](S* st, const u32x4_t* av) {
+        const short8_t af = __builtin_shufflevector(decode(av[0]), decode(av[1]), 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+        for (int b = 0; b < NBLK; ++b) {
+            lds_ptr_t p0 = (lds_ptr_t)((lds_char_t*)st + troff[b & 3] + (b >> 2) * 1024);
+            lds_ptr_t p1 = (lds_ptr_t)((lds_char_t*)st + troff[b & 3] + (b >> 2) * 1024 + NLD * 1024);
+            if constexpr (XT == GRWS_F16) {
+                const half4_t lo =
+                    __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4f16_t*)p0));
+                const half4_t hi =
+                    __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4f16_t*)p1));
+                const half8_t bf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, af), bf, acc[b], 0, 0, 0);
+            } else {
+                const short4_t lo =
+                    __builtin_bit_cast(short4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf16_t*)p0));
+                const short4_t hi =
+                    __builtin_bit_cast(short4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf16_t*)p1));
+                const short8_t bf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, af),
+                                                                 __builtin_bit_cast(bf16x8_t, bf), acc[b], 0, 0, 0);
+            }
+        }
+        // the scheduler's order: the reads of block b + 4 go out before the
+        // MFMA of block b (0x100: LDS reads, 0x008: MFMA)
+        constexpr int AHEAD = 4;
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * AHEAD, 0);
+#pragma unroll
+        for (int b = 0; b < NBLK - AHEAD; ++b) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, AHEAD, 0);
+    };
+
+    if (npairs > 0 && xr > 0) {  // uniform over the work-group
+        // pair p + 1's X rows are loaded into the other buffer while pair p
+        // is multiplied; A values one pair ahead, column indices and
+        // headers two pairs ahead (ring of 2)
+        u32x4_t abuf[2][2];
+        int32_t cring[2];
+        uint32_t hring[2];
+        cring[0] = load_col(0);
+        hring[0] = load_hdr(0);
+        load_x(st0, cring[0]);
+        load_a(lane_hdr(hring[0]), abuf[0]);
+        cring[1] = load_col(1);
+        hring[1] = load_hdr(1);
+        // the buffers are named, not selected at run time, so that each
+        // read's wait covers only the loads into its own buffer
+        // (unconditional loads: past the last pair they fetch nothing and
+        // write zeros into the buffer no longer read; a branch around them
+        // would make the compiler wait for them before the next reads)
+        auto step = [&](S* cur, S* nxt, const int u, const int64_t p) {  // u = p mod 2
+            // this wave's loads into `cur` have landed before the barrier:
+            // the barrier itself does not wait for loads into LDS, and the
+            // compiler's own wait before a read covers only the reading
+            // wave's loads, not the other waves' rows of the same buffer
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();  // pair p in `cur`; every wave is done reading `nxt`
+            __builtin_amdgcn_sched_barrier(0);
+            cring[u] = load_col(p + 2);
+            hring[u] = load_hdr(p + 2);
+            load_x(nxt, cring[u ^ 1]);
+            load_a(lane_hdr(hring[u ^ 1]), abuf[u ^ 1]);
+            // keep the loads ahead of the multiply (the scheduler would
+            // otherwise sink them to its end, leaving them no time)
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(cur, abuf[u]);
+        };
+        int64_t p = 0;
+        for (; p + 1 < npairs; p += 2) {
+            step(st0, st1, 0, p);
+            step(st1, st0, 1, p + 1);
+        }
+        if (p < npairs) step(st0, st1, 0, p);
+        // the loads past the last pair land before the work-group ends
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+    const int64_t win = q * G + wave;
+    if (win < a.num_windows) spmm_epilogue<XT, NBLK, 1>(a, acc, st0, 0, lane, win, -1, chunk, n0);
+}
+
 // Sums the partial slots of each split window in slot order (deterministic).
 // One wave per 256 floats of a (split window, chunk) block: NBLK waves per
 // block, lane l owns 4 consecutive floats (one row, 4 columns).  A hub
@@ -1934,7 +2160,10 @@ int launch_grp2(const SpmmArgs& a, hipStream_t stream) {
     const int64_t grid = ipc * a.nchunks;
     if (grid <= 0) return GRWS_OK;
     if (grid > INT32_MAX) return set_error(GRWS_E_INVALID, "spmm_grouped: grid too large");
-    hipLaunchKernelGGL((spmm_grp2_kernel<XT, NBLK>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    if (tune(kTuneGrpDma) != 0)
+        hipLaunchKernelGGL((spmm_grp2d_kernel<XT, NBLK>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((spmm_grp2_kernel<XT, NBLK>), dim3((unsigned)grid), dim3(256), 0, stream, a);
     GRWS_LAUNCH_CHECK();
     return GRWS_OK;
 }

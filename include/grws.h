@@ -254,7 +254,7 @@ int grws_spmm_residual(const grws_bcsr* A, const grws_packed_tiles* P, const grw
 /* Tuning overrides of the SpMM dispatch, for benchmarks and tests only.
  * No counterpart in the reference.  Names: GRWS_SPMM_NBLK, GRWS_SPMM_WAVES,
  * GRWS_SPMM_KERNEL, GRWS_SPMM_ORDER, GRWS_SPMM_NARROW, GRWS_SPMM_C320,
- * GRWS_GRP_WPW, GRWS_GRP_NBLK, GRWS_GRP_C320, GRWS_GRP_K32.  Each starts from the
+ * GRWS_GRP_WPW, GRWS_GRP_NBLK, GRWS_GRP_C320, GRWS_GRP_K32, GRWS_GRP_DMA.  Each starts from the
  * environment variable of that name, read once when the library is loaded;
  * value -1 clears the override (the measured default then applies).  The
  * overrides are process-wide: set them only where no other thread is in

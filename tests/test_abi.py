@@ -237,14 +237,17 @@ def test_spmm_grouped_rejects_bad_arguments_without_launching():
     assert call(gview(), n=60, ldx=64, ldy=64) == L.GRWS_E_INVALID and b"16-byte rows" in lib.grws_last_error()
 
 
-def test_grouped_slab_pair_switch_round_trips():
+@pytest.mark.parametrize("name", [b"GRWS_GRP_K32", b"GRWS_GRP_DMA"])
+def test_grouped_slab_pair_switches_round_trip(name):
     """GRWS_GRP_K32 (4-window groups on slab pairs, the default; 0 = single
-    slabs) is a tuning override like the others: unset reads -1, a set
-    value reads back, -1 clears it, an unknown name is refused."""
+    slabs) and GRWS_GRP_DMA (slab pairs staged by direct loads into LDS, the
+    default; 0 = through registers) are tuning overrides like the others:
+    unset reads -1, a set value reads back, -1 clears it, an unknown name is
+    refused."""
     lib = L.load()
-    assert lib.grws_spmm_get_tuning(b"GRWS_GRP_K32") == -1
-    assert lib.grws_spmm_set_tuning(b"GRWS_GRP_K32", 0) == 0
-    assert lib.grws_spmm_get_tuning(b"GRWS_GRP_K32") == 0
-    assert lib.grws_spmm_set_tuning(b"GRWS_GRP_K32", -1) == 0
-    assert lib.grws_spmm_get_tuning(b"GRWS_GRP_K32") == -1
+    assert lib.grws_spmm_get_tuning(name) == -1
+    assert lib.grws_spmm_set_tuning(name, 0) == 0
+    assert lib.grws_spmm_get_tuning(name) == 0
+    assert lib.grws_spmm_set_tuning(name, -1) == 0
+    assert lib.grws_spmm_get_tuning(name) == -1
     assert lib.grws_spmm_set_tuning(b"GRWS_NO_SUCH_SWITCH", 1) != 0

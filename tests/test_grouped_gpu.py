@@ -203,6 +203,37 @@ def test_grouped_slab_pairs_match_single_slabs(cuda_device, monkeypatch, vdt, N,
 
 
 @pytest.mark.parametrize("vdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N,pad", [(608, 640), (576, 576), (320, 320), (384, 384), (256, 256), (200, 200),
+                                   (96, 104)])
+@pytest.mark.parametrize("cfg,scale", [("c3", 0.004), ("c4", 0.002)])
+def test_slab_pairs_direct_loads_equal_register_staging(cuda_device, monkeypatch, vdt, N, pad, cfg, scale):
+    """The slab-pair kernel stages X by direct loads into LDS by default
+    (spmm_grp2d_kernel; GRWS_GRP_DMA=0 selects spmm_grp2_kernel, which stages
+    through registers): the same sums in the same order, so the outputs are
+    equal bit for bit, on every chunk width (320-column chunks, 256 plus a
+    narrower tail, 128), with a row pitch wider than N, and twice in a row
+    (the direct loads of one pair must land before any wave reads them)."""
+    print(f"case slab pairs direct loads {cfg} {vdt} N={N} pitch={pad}", flush=True)
+    monkeypatch.setattr(ops, "GROUP_MIN_N", 0)
+    _, A = _graph(cuda_device, vdt, 16, scale=scale, cfg=cfg)
+    gt = ops.group_tiles(A.window_offset, A.original_col_indices, A.values_condensed, 16, A.num_cols,
+                         group_size=4, max_ratio=10.0, max_skew=1e9)
+    torch.manual_seed(N + 29)
+    X = torch.zeros(A.num_cols, pad, device=cuda_device, dtype=vdt)
+    X[:, :N] = torch.randn(A.num_cols, N, device=cuda_device).to(vdt)
+    X = X[:, :N]
+    assert int(ops.L.load().grws_spmm_get_tuning(b"GRWS_GRP_DMA")) == -1  # the default: direct loads
+    Yd = [ops.spmm(A.window_offset, A.original_col_indices, A.values_condensed, X, 16, grouped=gt)
+          for _ in range(2)]
+    with ops.spmm_tuning(GRWS_GRP_DMA=0):
+        Yr = ops.spmm(A.window_offset, A.original_col_indices, A.values_condensed, X, 16, grouped=gt)
+    torch.cuda.synchronize()
+    for Y in Yd:
+        assert torch.equal(Y.view(torch.int16), Yr.view(torch.int16))
+    _oracle_check(A, X, Yd[0])
+
+
+@pytest.mark.parametrize("vdt", [torch.float16, torch.bfloat16])
 def test_grouped_spmm_residual_and_partial_group(cuda_device, monkeypatch, vdt):
     """Y = A X + R with R on a prefix of the rows; a window count that leaves
     the last group partial (its missing windows write nothing)."""
