@@ -351,7 +351,8 @@ def cpu_baseline(g, G, X: torch.Tensor, Y: torch.Tensor, rtol: float, budget_s: 
               "tight_elementwise_worst_err_over_bound": round(worst_t, 5),
               "tight_projection_worst_err_over_bound": round(proj_t, 5)}
     del vals, vabs, Xabs, Yd
-    # torch.sparse CSR fp32 over the whole graph (the CPU SpMM BASELINE.md names)
+    # torch.sparse CSR fp32 over the whole graph: the CPU SpMM this product is
+    # measured against (the same A @ X on the host cores)
     torch.set_num_threads(host_threads())
     A = torch.sparse_csr_tensor(g.row_ptr.cpu(), g.col_idx.cpu().long(), g.values.cpu().float(),
                                 size=(g.num_nodes, g.num_nodes))
