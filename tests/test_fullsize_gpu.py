@@ -221,6 +221,36 @@ def test_c3_bf16_n256_slab_pairs(c3, cuda_device, monkeypatch):
     print("grouped vs window by window, worst of bound:", _compare_orders(G, hg, X, Ya, Y2, Yw), flush=True)
 
 
+@pytest.mark.parametrize("N,d", [(608, 602), (256, 256)])
+def test_c3_grouped_product_repeats_bit_identically(c3, cuda_device, N, d):
+    """The grouped product's direct loads into LDS against a race: at full
+    size (3,641 groups, 320-column chunks at N=608, 3 work-groups per CU),
+    twenty products in a row equal the first bit for bit, and equal the
+    register-staged kernel's (GRWS_GRP_DMA=0): the same sums in the same
+    order.  A pair's rows read before every wave's loads had landed gave
+    results that changed from run to run."""
+    from graph_rws_amd.core import ops
+    print(f"case c3 N={N} grouped product repeated", flush=True)
+    g, G, _ = c3
+    X = aligned_rows(synth.features(g.num_nodes, d, pad_to=N, seed=N + 3, device=cuda_device).half())
+    gt = G.grouped_tiles(X.shape[0], N)
+    if gt is None:  # built on the graph's second product of this width
+        G.spmm(X)
+        gt = G.grouped_tiles(X.shape[0], N)
+    assert gt is not None and gt.group_size == 4
+    assert ops.grouped_kernel(4) == "spmm_grp2d_kernel"
+    Y0 = ops.spmm(G.window_offset, G.original_col_indices, G.values_condensed, X, 16, grouped=gt)
+    same = 0
+    for _ in range(20):
+        Y = ops.spmm(G.window_offset, G.original_col_indices, G.values_condensed, X, 16, grouped=gt)
+        same += bool(torch.equal(Y.view(torch.int16), Y0.view(torch.int16)))
+    with ops.spmm_tuning(GRWS_GRP_DMA=0):
+        Yr = ops.spmm(G.window_offset, G.original_col_indices, G.values_condensed, X, 16, grouped=gt)
+    torch.cuda.synchronize()
+    assert same == 20, f"{20 - same} of 20 repeats differ"
+    assert torch.equal(Yr.view(torch.int16), Y0.view(torch.int16))
+
+
 def test_c4_bench_path_n112(c4, cuda_device):
     """X [n, 112] bf16 at a 128-element (256-byte) pitch, as bench.py
     --config c4 and the aggregate-first layer 0 gather it."""
