@@ -69,6 +69,8 @@ _PROTOS = {
     "grws_spmm_default_slabs": (ctypes.c_int32, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
                                                  ctypes.c_int64]),
     "grws_spmm_plan_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "grws_spmm_plan_order_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "grws_spmm_plan_order": (ctypes.c_int, [_vp, ctypes.c_int64, _vp, ctypes.c_size_t, _vp]),
     "grws_spmm_plan_build": (ctypes.c_int, [_vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
                                             ctypes.c_int32, _vp, ctypes.c_int64, _vp,
                                             ctypes.c_int64, _vp, ctypes.c_size_t, _c_i64p, _vp]),

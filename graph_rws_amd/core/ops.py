@@ -89,9 +89,19 @@ def default_slabs(num_windows: int, num_tiles: int, tile_cols: int, n_cols: int)
     return int(L.load().grws_spmm_default_slabs(num_windows, num_tiles, tile_cols, n_cols))
 
 
+# Longest items first within each XCD's eighth of the plan
+# (grws_spmm_plan_order) when the plan splits windows: None = that rule,
+# False = never, True = always.  Measured: c2 N=128 -5%, c4 N=112 -6.6%,
+# N=256 -4.6%; c3 (community order, no split windows) +1% when forced
+ORDER_ITEMS: Optional[bool] = None
+
+
 def build_spmm_plan(window_offset: torch.Tensor, num_tiles: int, tile_cols: int,
-                    slabs_per_item: int) -> SpmmPlan:
-    """Builds the SpMM schedule on the device (one stream sync)."""
+                    slabs_per_item: int, order: Optional[bool] = None) -> SpmmPlan:
+    """Builds the SpMM schedule on the device (one stream sync).  order:
+    reorder the items longest first within each XCD's share
+    (grws_spmm_plan_order); None follows ORDER_ITEMS (by default: when the
+    plan splits windows, a power-law graph's hub windows)."""
     lib = L.load()
     dev = window_offset.device
     L.require_device("build_spmm_plan", dev, window_offset)
@@ -110,6 +120,12 @@ def build_spmm_plan(window_offset: torch.Tensor, num_tiles: int, tile_cols: int,
     L.call("grws_spmm_plan_build", L.ptr(window_offset), W, num_tiles, tile_cols, slabs_per_item,
            L.ptr(items), mi.value, L.ptr(split), ms.value, L.ptr(ws), wsb,
            ctypes.cast(counts, ctypes.POINTER(ctypes.c_int64)), L.stream_of(dev))
+    if order is None:
+        order = ORDER_ITEMS if ORDER_ITEMS is not None else counts[1] > 0
+    if order and counts[0] > 1:
+        owsb = int(lib.grws_spmm_plan_order_workspace_bytes(counts[0]))
+        ows = torch.empty(max(1, owsb), dtype=torch.uint8, device=dev)
+        L.call("grws_spmm_plan_order", L.ptr(items), counts[0], L.ptr(ows), owsb, L.stream_of(dev))
     return SpmmPlan(items, split, list(counts), slabs_per_item)
 
 

@@ -1960,6 +1960,95 @@ extern "C" int grws_spmm_plan_build(const int64_t* window_offset, int64_t num_wi
     return GRWS_OK;
 }
 
+namespace {
+// Plan order: the item list is walked in eighths, one per XCD (work-group r
+// takes item (r % 8) * per + r / 8, per = n rounded up to 8, over 8); within
+// each eighth the items go longest first, so that the long items (a
+// power-law graph's hub windows) do not start last and end the launch late.
+// Key = eighth (bits 32..34) and 2^31 - 1 - slabs (low 32 bits): an
+// ascending stable sort keeps equal lengths in window order.
+__global__ void plan_order_keys_kernel(const int32_t* __restrict__ items, int64_t n, int64_t per,
+                                       uint64_t* __restrict__ keys, uint32_t* __restrict__ idx,
+                                       int32_t* __restrict__ copy) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int32_t w = items[4 * i], b = items[4 * i + 1], e = items[4 * i + 2], sl = items[4 * i + 3];
+    const int64_t len = (int64_t)e - b;
+    const uint32_t k = (uint32_t)(0x7fffffff - (len < 0 ? 0 : (len > 0x7fffffff ? 0x7fffffff : len)));
+    keys[i] = ((uint64_t)(i / per) << 32) | k;
+    idx[i] = (uint32_t)i;
+    copy[4 * i] = w;
+    copy[4 * i + 1] = b;
+    copy[4 * i + 2] = e;
+    copy[4 * i + 3] = sl;
+}
+
+__global__ void plan_order_gather_kernel(const int32_t* __restrict__ copy, const uint32_t* __restrict__ idx, int64_t n,
+                                         int32_t* __restrict__ items) {
+    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    const int64_t i = idx[j];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) items[4 * j + c] = copy[4 * i + c];
+}
+
+struct PlanOrderWs {
+    uint64_t *k, *k2;
+    uint32_t *v, *v2;
+    int32_t* copy;
+    char* sort_ws;
+    size_t sort_bytes;
+};
+
+void carve_plan_order(Carver& c, int64_t n, PlanOrderWs* w) {
+    w->k = c.take<uint64_t>((size_t)n);
+    w->k2 = c.take<uint64_t>((size_t)n);
+    w->v = c.take<uint32_t>((size_t)n);
+    w->v2 = c.take<uint32_t>((size_t)n);
+    w->copy = c.take<int32_t>((size_t)n * 4);
+    w->sort_bytes = radix_sort_workspace_bytes(n);
+    w->sort_ws = c.take<char>(w->sort_bytes);
+}
+}  // namespace
+
+extern "C" size_t grws_spmm_plan_order_workspace_bytes(int64_t num_items) {
+    if (num_items <= 0) return 0;
+    Sizer s;  // the takes of carve_plan_order
+    s.take<uint64_t>((size_t)num_items);
+    s.take<uint64_t>((size_t)num_items);
+    s.take<uint32_t>((size_t)num_items);
+    s.take<uint32_t>((size_t)num_items);
+    s.take<int32_t>((size_t)num_items * 4);
+    s.take<char>(radix_sort_workspace_bytes(num_items));
+    return s.used + 256;
+}
+
+extern "C" int grws_spmm_plan_order(int32_t* items, int64_t num_items, void* workspace, size_t workspace_bytes,
+                                    void* stream_) {
+    clear_error();
+    hipStream_t stream = as_stream(stream_);
+    GRWS_CHECK_ARG(num_items >= 0 && num_items < ((int64_t)1 << 31), "plan_order: bad item count %lld",
+                   (long long)num_items);
+    if (num_items <= 1) return GRWS_OK;
+    GRWS_CHECK_ARG(items != nullptr, "plan_order: null items");
+    Carver cv(workspace, workspace_bytes);
+    PlanOrderWs w{};
+    carve_plan_order(cv, num_items, &w);
+    if (!cv.ok)
+        return set_error(GRWS_E_CAPACITY, "plan_order: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
+    const int64_t per = ((num_items + 7) / 8 * 8) / 8;
+    const unsigned blocks = (unsigned)((num_items + 255) / 256);
+    hipLaunchKernelGGL(plan_order_keys_kernel, dim3(blocks), dim3(256), 0, stream, items, num_items, per, w.k, w.v,
+                       w.copy);
+    GRWS_LAUNCH_CHECK();
+    bool alt = false;
+    GRWS_TRY(radix_sort_pairs(w.k, w.v, w.k2, w.v2, num_items, 35, w.sort_ws, w.sort_bytes, stream, &alt));
+    hipLaunchKernelGGL(plan_order_gather_kernel, dim3(blocks), dim3(256), 0, stream, w.copy, alt ? w.v2 : w.v,
+                       num_items, items);
+    GRWS_LAUNCH_CHECK();
+    return GRWS_OK;
+}
+
 extern "C" size_t grws_spmm_workspace_bytes(const grws_spmm_plan* plan, int64_t n_cols) {
     if (!plan || plan->num_slots <= 0 || n_cols <= 0) return 0;
     // chunk widths divide 256 or are 320: this covers whichever runs

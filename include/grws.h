@@ -122,6 +122,19 @@ int grws_spmm_plan_build(const int64_t* window_offset, int64_t num_windows, int6
                          int64_t max_items, int32_t* split, int64_t max_split, void* workspace,
                          size_t workspace_bytes, int64_t* counts_out, void* stream);
 
+/* Reorders a built plan's items (int32 [num_items][4], device) for a
+ * shorter launch: the kernels walk the item list in eighths, one per XCD,
+ * and within each eighth the items go longest first (stable), so that long
+ * items (a power-law graph's hub windows) do not start last.  No
+ * counterpart in the reference (its kernel launches one block per window,
+ * spmm_wrapper.cu:33-95).  Results are identical in either order; the
+ * window order lets neighbouring windows share X rows in the L2, so this
+ * pays on graphs without such locality (bindings apply it when the plan
+ * splits windows).  Workspace from grws_spmm_plan_order_workspace_bytes;
+ * stream-ordered, no sync. */
+size_t grws_spmm_plan_order_workspace_bytes(int64_t num_items);
+int grws_spmm_plan_order(int32_t* items, int64_t num_items, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes grws_spmm needs (0 when the plan has no split windows or
  * plan is NULL). */
 size_t grws_spmm_workspace_bytes(const grws_spmm_plan* plan, int64_t n_cols);

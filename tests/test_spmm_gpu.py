@@ -88,6 +88,57 @@ def test_spmm_split_windows(cuda_device, xdt, slabs):
     _check(G, X, Y0, xdt)
 
 
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("slabs,N", [(2, 80), (3, 128), (16, 300)])
+def test_plan_order_longest_first_same_results(cuda_device, xdt, slabs, N):
+    """grws_spmm_plan_order (what build_spmm_plan applies when the plan
+    splits windows): the items are a permutation of the window-order plan's,
+    each eighth of the list (one XCD's share) keeps its own items, longest
+    first, equal lengths in window order; the product (forward and over A^T)
+    equals the window-order plan's bit for bit."""
+    print(f"case plan order xdt={xdt} slabs={slabs} N={N}", flush=True)
+    g = synth.chung_lu(3000, 40000, 2.1, seed=11)
+    G = _bcsr(g, 16, cuda_device, vdt=xdt)
+    p0 = core.build_spmm_plan(G.window_offset, G.num_tiles, 16, slabs, order=False)
+    p1 = core.build_spmm_plan(G.window_offset, G.num_tiles, 16, slabs)
+    assert p0.num_split > 0 and p1.num_items == p0.num_items and p1.num_slots == p0.num_slots
+    n = p0.num_items
+    i0 = p0.items.view(-1, 4)[:n].cpu().numpy()
+    i1 = p1.items.view(-1, 4)[:n].cpu().numpy()
+    per = (n + 7) // 8
+    for k in range(8):
+        a, b = i0[k * per:(k + 1) * per], i1[k * per:(k + 1) * per]
+        la, lb = a[:, 2] - a[:, 1], b[:, 2] - b[:, 1]
+        want = a[np.argsort(-la, kind="stable")]
+        np.testing.assert_array_equal(b, want)
+        assert (np.diff(lb) <= 0).all()
+    ns = 3 * p0.num_split
+    assert torch.equal(p1.split[:ns], p0.split[:ns])
+    X = synth.features(g.num_nodes, N, seed=5, device=cuda_device).to(xdt)
+    Y0 = core.spmm(G.window_offset, G.original_col_indices, G.values_condensed, X, 16, plan=p0)
+    Y1 = core.spmm(G.window_offset, G.original_col_indices, G.values_condensed, X, 16, plan=p1)
+    torch.cuda.synchronize()
+    assert torch.equal(Y1.view(torch.uint8), Y0.view(torch.uint8))
+    _check(G, X, Y1, xdt)
+
+
+def test_plan_order_applies_to_split_plans_only(cuda_device):
+    """build_spmm_plan orders the items when the plan splits windows (the
+    hub windows of a power-law graph) and keeps window order otherwise (a
+    graph whose windows all fit one item keeps its neighbours together)."""
+    print("case plan order rule", flush=True)
+    g = synth.chung_lu(3000, 40000, 2.1, seed=11)
+    G = _bcsr(g, 16, cuda_device)
+    big = core.build_spmm_plan(G.window_offset, G.num_tiles, 16, 1 << 20)
+    assert big.num_split == 0
+    n = big.num_items
+    assert (np.diff(big.items.view(-1, 4)[:n, 0].cpu().numpy()) >= 0).all()  # window order kept
+    split = core.build_spmm_plan(G.window_offset, G.num_tiles, 16, 2)
+    ref = core.build_spmm_plan(G.window_offset, G.num_tiles, 16, 2, order=False)
+    m = 4 * ref.num_items
+    assert split.num_split > 0 and not torch.equal(split.items[:m], ref.items[:m])
+
+
 def test_spmm_deterministic(cuda_device):
     print("case determinism", flush=True)
     g = synth.chung_lu(4000, 60000, 2.1, seed=12)
