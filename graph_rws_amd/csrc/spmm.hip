@@ -1303,7 +1303,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NBLK == 20 
 // pair: each wave waits for its own loads (s_waitcnt), then the barrier
 // makes every wave's rows visible and tells that the other buffer is no
 // longer read; the next pair's loads go into it after the barrier.  Same
-// sums, same order as spmm_grp2_kernel.
+// sums, same order as spmm_grp2_kernel.  320-column chunks are held to
+// three waves per SIMD (40 KiB of LDS would allow four, and the scheduler
+// then serialised every MFMA behind its own LDS reads to fit 128 VGPRs);
+// scheduling-group barriers keep the reads four blocks ahead of the MFMAs.
+// The kernel must not spill: a build that did (scratch reloads beside the
+// accumulators) summed wrongly, and a test checks the code objects for it.
 template <int XT, int NBLK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NBLK == 20 ? 3 : 1, NBLK == 20 ? 3 : 8))) void spmm_grp2d_kernel(
     SpmmArgs a) {
