@@ -214,6 +214,7 @@ struct TopkArgs {
     int32_t* out_tiles;
     int32_t* err;
     uint64_t* gkeys;
+    uint32_t* gslot;  // beside gkeys: a packed key's slot (windows of more than kKeyCache slots)
     int64_t gcap;
     unsigned long long* gcursor;
     int32_t* big_list;   // active indices of the windows left to the big kernel
@@ -312,7 +313,13 @@ __device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const i
             in_part_known = true;
         }
     }
-    // the keys of slots s + u BLK (u < NK, s + u BLK < nslots): from the LDS
+    // a listed window of more than KC slots whose keys the keys kernel
+    // computed holds only its items' cap smallest keys, packed, with their
+    // slots beside them: the passes below scan those (nscan, set once the
+    // count is known), not the window's slots
+    const bool packed = !SMALL && pre >= 0 && !cached;  // uniform over the work-group
+    int64_t nscan = nslots;
+    // the keys of slots s + u BLK (u < NK, s + u BLK < nscan): from the LDS
     // cache or the scratch (~0: not a candidate), or recomputed
     auto keysn = [&](int64_t s, uint64_t* k, bool* c) {
         if (cached || gk) {
@@ -320,7 +327,7 @@ __device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const i
 #pragma unroll
             for (int u = 0; u < NK; ++u) {
                 const int64_t su = s + (int64_t)u * BLK;
-                k[u] = su < nslots ? src[su] : ~0ull;
+                k[u] = su < nscan ? src[su] : ~0ull;
             }
 #pragma unroll
             for (int u = 0; u < NK; ++u) c[u] = k[u] != ~0ull;
@@ -379,6 +386,7 @@ __device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const i
     }
     __syncthreads();
     const int32_t count = sh.cnt;
+    if (packed) nscan = count;
 
     if (cached && count <= FASTMAX) {
         // a candidate's rank is the number of smaller keys (keys are
@@ -450,7 +458,7 @@ __device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const i
                 for (int i = tid; i < NW * 256; i += BLK) sh.whist[i / 256][i % 256] = 0;
                 __syncthreads();
                 const uint64_t pre = sh.prefix;
-                for (int64_t s = tid; s < nslots; s += NK * BLK) {
+                for (int64_t s = tid; s < nscan; s += NK * BLK) {
                     uint64_t k[NK];
                     bool c[NK];
                     keysn(s, k, c);
@@ -516,7 +524,7 @@ __device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const i
             sh.slot[i] = -1;
         }
         __syncthreads();
-        for (int64_t s = tid; s < nslots; s += NK * BLK) {
+        for (int64_t s = tid; s < nscan; s += NK * BLK) {
             uint64_t k[NK];
             bool c[NK];
             keysn(s, k, c);
@@ -526,8 +534,9 @@ __device__ __forceinline__ void topk_window(TopkShared<BLK, KC, HW>& sh, const i
                 if (shift < 64 && (k[u] >> shift) > (prefix >> shift)) continue;
                 const int i = atomicAdd(&sh.cnt, 1);
                 if (i < kMaxCap) {
+                    const int64_t su = s + (int64_t)u * BLK;
                     sh.col[i] = (int32_t)(uint32_t)k[u];
-                    sh.slot[i] = (int32_t)(s + (int64_t)u * BLK);
+                    sh.slot[i] = packed ? (int32_t)a.gslot[sh.goff + su] : (int32_t)su;
                 }
             }
         }
@@ -610,11 +619,20 @@ __global__ __launch_bounds__(kBlk) void window_topk_classify_kernel(TopkArgs a) 
 // The listed windows' keys, kChunk slots per item, written to each window's
 // scratch; every item adds its candidates to the window's count and folds
 // its least and greatest key in (atomics), as the big kernel's own count
-// pass would.  Walks the chunks the classify kernel claimed; every
-// work-group leaves once they are done.
+// pass would.  For a window of more than kKeyCache slots (which the big
+// kernel reads in place, pass after pass) an item keeps only its cap
+// smallest keys (the others cannot be among the window's cap smallest:
+// keys are distinct) and packs them, with their slots, at the window's
+// cursor.  Walks the chunks the classify kernel claimed; every work-group
+// leaves once they are done.
+static_assert(kChunk % kBlk == 0 && kChunk % 2 == 0, "whole slots per thread, key pairs in LDS");
 template <typename VT>
 __global__ __launch_bounds__(kBlk) void window_topk_keys_kernel(TopkArgs a) {
+    constexpr int PER = kChunk / kBlk;  // slots per thread and item
+    __shared__ __attribute__((aligned(16))) uint64_t skey[kChunk];
+    __shared__ int scnt;
     const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
     const ScoreParams& p = a.p;
     const int64_t claimed = *a.chunk_total;
     const int64_t total = claimed < a.chunk_cap ? claimed : a.chunk_cap;
@@ -627,6 +645,9 @@ __global__ __launch_bounds__(kBlk) void window_topk_keys_kernel(TopkArgs a) {
         const int64_t s0 = (c - a.big_cbase[li]) * (int64_t)kChunk;
         const int64_t s1 = s0 + kChunk < nslots ? s0 + kChunk : nslots;
         uint64_t* const gk = a.gkeys + a.big_goff[li];
+        uint32_t* const gs = a.gslot + a.big_goff[li];
+        // windows the big kernel cannot hold in LDS get packed candidates
+        const bool pack = nslots > kKeyCache;  // uniform over the work-group
         int32_t part_lo = 0, part_hi = 0;
         bool in_part_known = false;
         if (p.use_hacs && p.locality && p.window_part_ids && p.part_starts && p.part_ends) {
@@ -639,31 +660,81 @@ __global__ __launch_bounds__(kBlk) void window_topk_keys_kernel(TopkArgs a) {
                 in_part_known = true;
             }
         }
+        if (tid == 0) scnt = 0;
+        uint64_t kk[PER];
         int local = 0;
-        uint64_t kmin = ~0ull, kmax = 0;
-        for (int64_t s = s0 + tid; s < s1; s += kBlk) {
-            SlotRaw r;
-            slot_load<VT>(a.cols, a.vals, t0, a.tc, s, r);
-            uint64_t k = 0;
-            const bool cand = slot_key_of(r, part_lo, part_hi, in_part_known, p, &k);
-            gk[s] = cand ? k : ~0ull;
-            if (cand) {
-                ++local;
-                kmin = k < kmin ? k : kmin;
-                kmax = k > kmax ? k : kmax;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int64_t s = s0 + tid + u * kBlk;
+            kk[u] = ~0ull;
+            if (s < s1) {
+                SlotRaw r;
+                slot_load<VT>(a.cols, a.vals, t0, a.tc, s, r);
+                uint64_t k = 0;
+                if (slot_key_of(r, part_lo, part_hi, in_part_known, p, &k)) {
+                    kk[u] = k;
+                    ++local;
+                }
+                if (p.use_hacs && r.col != -1 && (r.col < 0 || (int64_t)r.col >= p.num_static_scores))
+                    atomicOr(a.err, kErrHacs);
             }
-            if (p.use_hacs && r.col != -1 && (r.col < 0 || (int64_t)r.col >= p.num_static_scores))
-                atomicOr(a.err, kErrHacs);
+            if (pack) skey[tid + u * kBlk] = kk[u];
+        }
+        if (pack) {
+            __syncthreads();  // scnt cleared, the item's keys in LDS
+            if (local) atomicAdd(&scnt, local);
+            __syncthreads();
+            // only the item's cap smallest keys can be among the window's cap
+            // smallest (keys are distinct): the rest are dropped
+            if (scnt > a.cap) {
+                int rank[PER] = {};
+                const ulonglong2* kq = reinterpret_cast<const ulonglong2*>(skey);
+                for (int g = 0; g < kChunk / 2; ++g) {
+                    const ulonglong2 q = kq[g];
+#pragma unroll
+                    for (int u = 0; u < PER; ++u) rank[u] += (q.x < kk[u]) + (q.y < kk[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < PER; ++u)
+                    if (rank[u] >= a.cap) kk[u] = ~0ull;
+            }
+        }
+        uint64_t kmin = ~0ull, kmax = 0;
+        int kept = 0;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int64_t s = s0 + tid + u * kBlk;
+            const bool keep = kk[u] != ~0ull;
+            if (pack) {
+                // packed at the window's cursor (its count), one atomic per wave
+                const uint64_t m = __ballot(keep);
+                int base = 0;
+                if (lane == 0 && m) base = atomicAdd(&a.big_cnt[li], __popcll(m));
+                base = __shfl(base, 0, kWave);
+                if (keep) {
+                    const int pos = base + __popcll(m & lanemask_lt());
+                    gk[pos] = kk[u];
+                    gs[pos] = (uint32_t)s;
+                }
+            } else if (s < s1) {
+                gk[s] = kk[u];
+            }
+            if (keep) {
+                ++kept;
+                kmin = kk[u] < kmin ? kk[u] : kmin;
+                kmax = kk[u] > kmax ? kk[u] : kmax;
+            }
         }
 #pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) local += __shfl_xor(local, d, kWave);
+        for (int d = 32; d >= 1; d >>= 1) kept += __shfl_xor(kept, d, kWave);
         kmin = wave_min_u64(kmin);
         kmax = wave_max_u64(kmax);
-        if ((tid & (kWave - 1)) == 0 && local > 0) {
-            atomicAdd(&a.big_cnt[li], local);
+        if (lane == 0 && kept > 0) {
+            if (!pack) atomicAdd(&a.big_cnt[li], kept);
             atomicMin(&a.big_kmin[li], (unsigned long long)kmin);
             atomicMax(&a.big_kmax[li], (unsigned long long)kmax);
         }
+        if (pack) __syncthreads();  // the LDS keys are read before the next item overwrites them
     }
 }
 
@@ -1049,6 +1120,7 @@ int topk_enqueue(const grws_bcsr* A, const int32_t* active_windows, int64_t num_
     if (!cv.ok) return set_error(GRWS_E_CAPACITY, "window_topk: workspace too small (%zu < %zu)", workspace_bytes, cv.used);
     // the rest: the chunk table and the big windows' key scratch
     uint64_t* gkeys = nullptr;
+    uint32_t* gslot = nullptr;
     int64_t gcap = 0;
     int32_t* chunk_owner = nullptr;
     int64_t chunk_cap = 0;
@@ -1066,10 +1138,13 @@ int topk_enqueue(const grws_bcsr* A, const int32_t* active_windows, int64_t num_
         }
         if (rest.ok && rest.used + 256 <= rest.cap) {
             const size_t left = rest.cap - rest.used - 256;
-            uint64_t* keys = rest.take<uint64_t>(left / 8);
-            if (rest.ok && left / 8 > 0) {
+            const size_t n = left > 512 ? (left - 512) / 12 : 0;  // a key and a slot per entry
+            uint64_t* keys = rest.take<uint64_t>(n);
+            uint32_t* slots = rest.take<uint32_t>(n);
+            if (rest.ok && n > 0) {
                 gkeys = keys;
-                gcap = (int64_t)(left / 8);
+                gslot = slots;
+                gcap = (int64_t)n;
             }
         }
     }
@@ -1091,6 +1166,7 @@ int topk_enqueue(const grws_bcsr* A, const int32_t* active_windows, int64_t num_
     ta.out_tiles = tiles;
     ta.err = err;
     ta.gkeys = gkeys;
+    ta.gslot = gslot;
     ta.gcap = gcap;
     ta.gcursor = reinterpret_cast<unsigned long long*>(ctr + 2);
     ta.big_list = big_list;
